@@ -1,0 +1,286 @@
+"""Benchmark of the streaming edge-arena step (forward + backward + update).
+
+Default workload: configuration C2 -- 8 layers x 131,072 tanh units, 2^26
+edges with Zipf(1.1) source popularity, MSE to a signed-permutation target,
+Adam(1e-3), batch 1 streaming -- on one MI355X. Inputs and targets for every
+step are generated up front and resident in HBM before the timed region.
+
+Prints one JSON line: edges/s over the timed steps (live edges / step time),
+the roofline of the dominant kernel (algorithmic bytes per launch / mean launch
+time from HIP events recorded on the launching stream inside the timed
+region), and the CPU oracle timed on the host on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "edges/sec per streaming step (fwd+bwd+update) at 64M edges; % of HBM peak"
+
+
+class EventTimer:
+    """HIP events around each kernel launch, on torch's current stream."""
+
+    def __init__(self) -> None:
+        import torch
+
+        self.torch = torch
+        self.on = False
+        self.pairs: dict[str, list] = collections.defaultdict(list)
+        self._open: tuple | None = None
+
+    def begin(self, kind: str) -> None:
+        if self.on:
+            e = self.torch.cuda.Event(enable_timing=True)
+            e.record()
+            self._open = (kind, e)
+
+    def end(self, kind: str) -> None:
+        if self.on and self._open is not None:
+            e = self.torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.pairs[kind].append((self._open[1], e))
+            self._open = None
+
+    def summary(self) -> dict[str, dict[str, float]]:
+        self.torch.cuda.synchronize()
+        out = {}
+        for kind, pairs in self.pairs.items():
+            ms = [a.elapsed_time(b) for a, b in pairs]
+            out[kind] = {"launches": len(ms), "total_ms": float(sum(ms)), "mean_ms": float(np.mean(ms))}
+        return out
+
+
+
+
+def build_c2(px, seed: int, scale: int):
+    import plastax_amd.numpy as jnp
+    from plastax_amd import synth
+
+    grad = px.FieldSpec.float32("grad_pre_act")
+    lossg = px.FieldSpec.float32("loss_grad")
+
+    class TanhForward(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(acc)))
+
+    class TanhBackward(px.BackwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, src, dst, c, cid, g):
+            return c[px.WEIGHT, cid] * u[grad, dst]
+
+        def apply(self, u, i, g, acc):
+            a = u[px.ACTIVATION, i]
+            return px.UnitWrite.of((grad, (acc + u[lossg, i]) * (jnp.float32(1.0) - a * a)))
+
+    class MSELoss(px.Loss):
+        seed_field = lossg
+
+        def calculate_loss(self, u, outputs, targets, g):
+            d = u.gather(px.ACTIVATION, outputs) - targets
+            return jnp.sum(jnp.float32(0.5) * d * d), d
+
+    opt = px.optim.adam(1e-3, grad)
+
+    class C2Net(px.Network):
+        forward_pass = TanhForward()
+        backward_pass = TanhBackward()
+        loss = MSELoss()
+        update_conn = opt.update_conn()
+        extra_unit_fields = (grad, lossg)
+        extra_conn_fields = opt.state_fields
+        propagation = px.Propagation.TOPOLOGICAL
+
+    e = synth.c2_topological(seed=seed, scale=scale)
+    return C2Net, e
+
+
+def cpu_baseline(px, net, static, e, host_units, host_conns, inputs, targets, steps: int) -> dict:
+    """The oracle (a scalar C port, one thread) on the same workload."""
+    from oracle import oracle as ox
+    from plastax_amd._plan import compile_plan
+
+    o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static))
+    o.step(inputs[0], targets[0])  # warm-up
+    times = []
+    for k in range(steps):
+        t0 = time.perf_counter()
+        o.step(inputs[(k + 1) % len(inputs)], targets[(k + 1) % len(targets)])
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": float(e.src.size / med),
+        "unit": "edges/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{steps} full C2 steps (2^26 edges) after 1 warm-up, median step {med * 1e3:.1f} ms, "
+        "single-threaded C oracle (oracle/plastax_oracle.c)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--scale", type=int, default=1, help="shrink C2's layer width (tests only)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: this build measures the step on one "
+            "GPU (the single-GPU kernel runs on the full arena); multi-GPU sharding is out of scope",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    import plastax_amd as px
+    from plastax_amd.state import column_to_numpy
+
+    t_setup = time.perf_counter()
+    net, e = build_c2(px, args.seed, args.scale)
+    from plastax_amd import synth
+
+    width = e.input_ids.size
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, capacity_align=256, device="cpu")
+    specs = {s.name: s for s in static.conn_fields}
+    host_units = {s.name: column_to_numpy(state.units[s.name], s).copy() for s in static.unit_fields}
+    host_conns = [{n: column_to_numpy(b[n], specs[n]).copy() for n in specs} for b in state.conns]
+    dev = torch.device("cuda", 0)
+    gstate = px.NetworkState(
+        {k: v.to(dev) for k, v in state.units.items()},
+        tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
+        None,
+    )
+    del state
+    step = px.make_step(net, static)
+    sign, perm = synth.c2_target(args.seed, width)
+    nsteps = args.warmup + args.steps
+    rng = np.random.default_rng(args.seed + 2)
+    xs = rng.standard_normal((nsteps, width)).astype(np.float32)
+    ts = (sign[None, :] * xs[:, perm]).astype(np.float32)
+    xs_d = torch.from_numpy(xs).to(dev)
+    ts_d = torch.from_numpy(ts).to(dev)
+    step.arena(gstate)  # physical layout build (host, once)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    for k in range(args.warmup):
+        gstate = step(gstate, px.StepInputs(xs_d[k], ts_d[k])).state
+    torch.cuda.synchronize()
+
+    timer = EventTimer()
+    step.timer = timer
+    timer.on = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    last = None
+    for k in range(args.warmup, nsteps):
+        last = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+        gstate = last.state
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.on = False
+    kernels = timer.summary()
+    loss = float(last.loss)
+
+    edges = int(e.src.size)
+    n_units = int(e.num_units)
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = edges / (elapsed / args.steps)
+    step_bytes = 54 * edges + 16 * n_units
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Algorithmic bytes per launch of each kernel kind (per live edge).
+    arena = gstate._arena
+    live_per_bucket = arena.lives
+    bytes_per_launch = {
+        # forward reads FROM_ID, TO_ID, DEAD, WEIGHT: 13 B/edge
+        "forward": 13 * edges / len(live_per_bucket),
+        # update reads FROM_ID, TO_ID, DEAD, WEIGHT, m, v, t and writes WEIGHT, m, v, t
+        "update_conn": 41 * edges,
+    }
+    dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    dom_bytes = bytes_per_launch.get(dominant)
+    roofline = None
+    if dom_bytes is not None:
+        ach = dom_bytes / (kernels[dominant]["mean_ms"] * 1e-3) / 1e9
+        roofline = {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": round(ach, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        }
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if roofline is not None and traffic_file.exists():
+        roofline["traffic"] = json.loads(traffic_file.read_text()).get(dominant)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(px, net, static, e, host_units, host_conns, xs, ts, args.cpu_steps)
+
+    for k in kernels.values():
+        k["total_ms"] = round(k["total_ms"], 3)
+        k["mean_ms"] = round(k["mean_ms"], 4)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: 8x131072 tanh units, 2^26 Zipf(1.1) edges, MSE, Adam, batch 1 streaming",
+            "edges": edges,
+            "units": n_units,
+            "layers": 8,
+            "optimizer": "adam(1e-3)",
+            "scale": args.scale,
+        },
+        "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "step_algorithmic_gbs": round(step_gbs, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "loss_last": loss,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

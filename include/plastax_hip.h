@@ -1,0 +1,211 @@
+/*
+ * plastax_hip.h -- C ABI of the MI355X-native edge-arena step.
+ *
+ * The reference (Sir-NoChill/plastax) runs its streaming step as one jitted
+ * JAX function whose edge work goes through XLA scatters or jax_triton custom
+ * calls. This library is the drop-in for that edge work: each entry point
+ * below replaces one reference seam (cited file:line), takes plain device
+ * pointers and sizes, owns no memory, launches stream-ordered HIP kernels for
+ * gfx950 and never synchronises the host. A return value of 0 means success;
+ * any other value is a PLX_ERR_* code and plx_last_error() gives the text
+ * (thread-local). No C++ exception crosses this boundary.
+ *
+ * Callers: plastax_amd/_lib.py (ctypes over torch-allocated device memory);
+ * INTEGRATION.md shows the jax.ffi / XLA custom-call binding.
+ */
+#ifndef PLASTAX_HIP_H_
+#define PLASTAX_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define PLX_EXPORT __attribute__((visibility("default")))
+#else
+#define PLX_EXPORT
+#endif
+
+#define PLX_OK 0
+#define PLX_ERR_INVALID 1     /* bad argument (shape, null pointer, range)   */
+#define PLX_ERR_HIP 2         /* a HIP runtime call failed                   */
+#define PLX_ERR_UNSUPPORTED 3 /* a policy or size this library cannot run    */
+
+/* Named monoids (monoid.py:22-39). */
+#define PLX_MONOID_SUM 0
+#define PLX_MONOID_PROD 1
+#define PLX_MONOID_MAX 2
+#define PLX_MONOID_MIN 3
+
+/* Per-edge update rules (optim/_sgd.py, _momentum.py, _adam.py, _rmsprop.py). */
+#define PLX_RULE_SGD 0
+#define PLX_RULE_MOMENTUM 1
+#define PLX_RULE_ADAM 2
+#define PLX_RULE_RMSPROP 3
+
+#define PLX_MAX_INSTR 48
+#define PLX_MAX_CONST 32
+#define PLX_MAX_FIELDS 8
+#define PLX_MAX_OUTS 4
+
+/* A traced per-unit program: a user Apply (sweep.py:183-230) or the per-output
+ * term of an elementwise Loss (phases.py:1107-1131). Opcodes are listed in
+ * plastax_amd/_expr.py; each instruction is {op, dst, a, b}. LDU operand a
+ * indexes `fields`; OUT slot d writes `outs[d]` at the unit. Passed by value
+ * (it travels in the kernel argument segment). */
+typedef struct plx_program {
+  int32_t ninstr;
+  int32_t nout;
+  int32_t nfields;
+  int32_t reserved;
+  int32_t code[4 * PLX_MAX_INSTR];
+  float consts[PLX_MAX_CONST];
+  const float* fields[PLX_MAX_FIELDS];
+  float* outs[PLX_MAX_OUTS];
+} plx_program;
+
+/* Which units a pass finalizes (phases.py:1011, :1096-1101, sweep.py:205-207):
+ * unit u finalizes iff (fin_level < 0 || level[u] == fin_level)
+ * && !(skip_inputs && is_input[u]) && !(pruned && pruned[u]). */
+typedef struct plx_finalize {
+  const int32_t* level;
+  const uint8_t* is_input;
+  const uint8_t* pruned; /* null: the net has no unit capacity */
+  int32_t fin_level;
+  int32_t skip_inputs;
+} plx_finalize;
+
+/* One bucket of the forward pass: _accumulate_into + _apply_masked
+ * (sweep.py:113-230, phases.py:972-1015) for a linear map
+ * weight * x[from] (phases.py:535-556). Rows are destination units in a CSR
+ * over the physical (destination-sorted) positions; each row is folded in slot
+ * order, combined into acc, and finalized rows apply `apply` and reset acc. */
+typedef struct plx_forward_desc {
+  int32_t nrows;
+  int32_t monoid;
+  const int32_t* row_unit; /* [nrows] destination unit ids, ascending      */
+  const int32_t* row_ptr;  /* [nrows+1] physical positions                 */
+  const int32_t* src;      /* [positions] FROM_ID                          */
+  const float* weight;     /* [positions] WEIGHT                           */
+  const uint8_t* dead;     /* [positions] DEAD                             */
+  const float* x;          /* [num_units] the map's linear_input field     */
+  float* acc;              /* [num_units] carried accumulator, or null     */
+  plx_finalize fin;
+  plx_program apply;
+} plx_forward_desc;
+
+PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
+
+/* Backward fold over the source-sorted mirror of one bucket
+ * (sweep.py:343-399 with target FROM_ID; phases.py:1049-1104): item k folds
+ * weight[sperm[j]] * g[sdst[j]] for j in [item_ptr[k], item_ptr[k+1]) in
+ * order, skipping sdst < 0 (dead), into item_sum[k]. */
+typedef struct plx_backward_fold_desc {
+  int32_t nitems;
+  int32_t monoid;
+  const int32_t* item_ptr; /* [nitems+1] mirror positions                 */
+  const int32_t* sperm;    /* [mirror] physical position of the edge       */
+  const int32_t* sdst;     /* [mirror] destination unit, -1 when dead      */
+  const float* weight;     /* [positions] WEIGHT (pre-update)              */
+  const float* g;          /* [num_units] the map's linear_input field     */
+  float* item_sum;         /* [nitems] out                                 */
+} plx_backward_fold_desc;
+
+PLX_EXPORT int plx_backward_fold(const plx_backward_fold_desc* d, void* stream);
+
+/* Backward finalize of one level: row r folds item_sum over
+ * [row_item[r], row_item[r+1]) in order, combines into acc (null: fresh
+ * identity) and, where finalized, applies `apply` and resets acc. */
+typedef struct plx_backward_finalize_desc {
+  int32_t nrows;
+  int32_t monoid;
+  const int32_t* row_unit; /* [nrows]                                      */
+  const int32_t* row_item; /* [nrows+1] item ranges (null: no items)       */
+  const float* item_sum;   /* [nitems]                                     */
+  float* acc;              /* [num_units] or null                          */
+  plx_finalize fin;
+  plx_program apply;
+} plx_backward_finalize_desc;
+
+PLX_EXPORT int plx_backward_finalize(const plx_backward_finalize_desc* d, void* stream);
+
+/* Connection update over physical positions [0, n): build_update_conn_phase
+ * (phases.py:1196-1242, sweep.py:488-532) for the optim bundles. grad =
+ * gfield[dst] * act[src]; dead rows keep their values.
+ *   SGD:      p0=lr                          (_sgd.py:121-126)
+ *   MOMENTUM: p0=lr p1=mu           s0=opt/v (_momentum.py:136-139)
+ *   ADAM:     p0=lr p1=b1 p2=b2 p3=eps p4=wd p5=1-b1 p6=1-b2;
+ *             s0=opt/m s1=opt/v s2=opt/t     (_adam.py:154-172)
+ *   RMSPROP:  p0=lr p1=decay p2=1-decay p3=eps  s0=opt/v (_rmsprop.py:135-140)
+ * pow_table (optional, Adam) holds float32(b1^t), float32(b2^t) at [2t], [2t+1]
+ * for t < pow_table_len; other t are computed on the device the same way. */
+typedef struct plx_update_desc {
+  int64_t n;
+  int32_t rule;
+  int32_t pow_table_len;
+  const int32_t* src;
+  const int32_t* dst;
+  const uint8_t* dead;
+  float* weight;
+  float* s0;
+  float* s1;
+  float* s2;
+  const float* gfield;
+  const float* act;
+  const float* pow_table;
+  float p[8];
+} plx_update_desc;
+
+PLX_EXPORT int plx_update_conn(const plx_update_desc* d, void* stream);
+
+/* Step input scatter (step.py:598): dst[ids[k]] = values[k]. */
+PLX_EXPORT int plx_scatter_f32(int32_t n, const int32_t* ids, const float* values,
+                    float* dst, void* stream);
+
+/* Elementwise loss (phases.py:1107-1131 with a policy whose seed and loss
+ * term are elementwise in (prediction, target), e.g. MSE): `term` writes out
+ * slot 0 (the seed) to seed_field[output_ids[k]]; slot 1 is the loss term.
+ * *loss_out = the fold of the terms in 256-output pieces (each piece folded
+ * in order, then the piece sums in order). partials: n_out + ceil(n_out/256)
+ * floats of scratch. */
+PLX_EXPORT int plx_loss_elementwise(int32_t n_out, const int32_t* output_ids,
+                         const float* targets, const plx_program* term,
+                         float* seed_field, float* partials, float* loss_out,
+                         void* stream);
+
+/* SoftmaxCrossEntropyLoss (traits.py:204-250): max, sum of exp(a - max) in
+ * 256-output pieces, seed = exp(z)/s - t, loss = piecewise fold of
+ * t*(log s - z). Runs in one workgroup. */
+PLX_EXPORT int plx_loss_softmax_ce(int32_t n_out, const int32_t* output_ids,
+                        const float* act, const float* targets,
+                        float* seed_field, float* loss_out, void* stream);
+
+/* Fill n floats with a value (identity accumulators). */
+PLX_EXPORT int plx_fill_f32(int64_t n, float value, float* dst, void* stream);
+
+/* Device-side Philox-4x32-10 in the plastax mapping (rng.py:109-141):
+ * out[i] = philox32(seeds[i], ctrs[i]). Used to pin the device generator. */
+PLX_EXPORT int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ctrs,
+                 uint32_t* out, void* stream);
+
+/* Elementary functions exactly as the kernels evaluate them (op 0 exp,
+ * 1 log, 2 tanh, 3 sigmoid, 4 sqrt, 5 Adam power b^t with b=x[i], t=y[i]). */
+PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float* y,
+                  float* out, void* stream);
+
+/* sizeof of the descriptor structs, in the order plx_program, plx_finalize,
+ * plx_forward_desc, plx_backward_fold_desc, plx_backward_finalize_desc,
+ * plx_update_desc (for binding layers to check their mirrors). Writes
+ * min(n, 6) values and returns 6. */
+PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
+
+PLX_EXPORT const char* plx_last_error(void);
+PLX_EXPORT int32_t plx_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLASTAX_HIP_H_ */

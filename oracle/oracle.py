@@ -1,0 +1,327 @@
+"""CPU oracle of the streaming step -- TEST INFRASTRUCTURE ONLY.
+
+Restates the reference's step (src/plastax/step.py:578-618 and the phase
+builders of src/plastax/phases.py) over the *logical* arena, i.e. the
+reference's own layout: per-bucket dicts of columns in slot order. The O(E)
+loops run in plastax_oracle.c (built by the Makefile beside this file); the
+level walks below follow phases.py line by line:
+
+- forward, TOPOLOGICAL: phases.py:972-1015 (accumulate bucket l, finalize
+  level l+1, non-input, live); PIPELINE: sweep.py:287-340 (one sweep,
+  every non-input unit);
+- loss: phases.py:1107-1131 (seed written at the output ids);
+- backward, TOPOLOGICAL: phases.py:1049-1104 (prime the deepest level from
+  the identity, then buckets L-1..1; bucket 0 is never reduced); PIPELINE:
+  sweep.py:402-449 (every unit, inputs included);
+- update_conn: phases.py:1196-1242 with the optim rules.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
+this module, as the checker. The policies' apply / loss programs are the
+ones the framework traced (plastax_amd._expr); this file evaluates them with
+its own interpreter.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import subprocess
+from typing import Any
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libplastax_oracle.so"
+PIECE = 256
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_lib: ctypes.CDLL | None = None
+
+
+def build() -> pathlib.Path:
+    """Compile the C restatement (make)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf"):
+            getattr(lib, name).restype = ctypes.c_float
+            getattr(lib, name).argtypes = [ctypes.c_float]
+        lib.ox_pow_step.restype = ctypes.c_float
+        lib.ox_pow_step.argtypes = [ctypes.c_float, ctypes.c_float]
+        lib.ox_philox32.restype = ctypes.c_uint32
+        lib.ox_philox32.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        lib.ox_philox4x32_10.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 3
+        lib.ox_site_seed.restype = ctypes.c_uint64
+        lib.ox_site_seed.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        lib.ox_conn_key.restype = ctypes.c_uint32
+        lib.ox_conn_key.argtypes = [ctypes.c_uint32] * 3
+        lib.ox_site_draw.restype = ctypes.c_uint32
+        lib.ox_site_draw.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32]
+        lib.ox_uniform_int.restype = ctypes.c_uint32
+        lib.ox_uniform_int.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+        lib.ox_unit_float.restype = ctypes.c_float
+        lib.ox_unit_float.argtypes = [ctypes.c_uint32]
+        lib.ox_loss_elementwise.restype = ctypes.c_float
+        lib.ox_loss_softmax_ce.restype = ctypes.c_float
+        lib.ox_identity.restype = ctypes.c_float
+        lib.ox_identity.argtypes = [ctypes.c_int32]
+        lib.ox_bucket_reduce_fwd.argtypes = [
+            ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32, _f32p
+        ]
+        lib.ox_bucket_reduce_bwd.argtypes = [
+            ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32,
+            ctypes.c_int32, ctypes.c_int32, _f32p, _f32p, _i32p,
+        ]
+        lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
+        lib.ox_apply.argtypes = [
+            _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
+            ctypes.c_int64, _f32p, _u8p, ctypes.c_int32, _f32p,
+        ]
+        lib.ox_loss_elementwise.argtypes = [
+            _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
+            _f32p, _f32p, _f32p, ctypes.c_int32,
+        ]
+        lib.ox_loss_softmax_ce.argtypes = [
+            _f32p, _i32p, ctypes.c_int32, _f32p, _f32p, _f32p, ctypes.c_int32
+        ]
+        upd = [ctypes.c_int64, _i32p, _i32p, _u8p, _f32p]
+        lib.ox_update_sgd.argtypes = upd + [_f32p, _f32p, ctypes.c_float]
+        lib.ox_update_momentum.argtypes = upd + [_f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_float]
+        lib.ox_update_adam.argtypes = upd + [_f32p, _f32p, _f32p, _f32p, _f32p] + [ctypes.c_float] * 7
+        lib.ox_update_rmsprop.argtypes = upd + [_f32p, _f32p, _f32p] + [ctypes.c_float] * 4
+        lib.ox_free_block_counts.argtypes = [ctypes.c_int64, _u8p, ctypes.c_int32, _i32p]
+        lib.ox_nth_free_slots.restype = ctypes.c_int64
+        lib.ox_nth_free_slots.argtypes = [
+            ctypes.c_int64, _u8p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)
+        ]
+        _lib = lib
+    return _lib
+
+
+def ptr(a: np.ndarray, ctype: Any) -> Any:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def fptr(a: np.ndarray) -> Any:
+    assert a.dtype == np.float32
+    return ptr(a, ctypes.c_float)
+
+
+def iptr(a: np.ndarray) -> Any:
+    assert a.dtype == np.int32
+    return ptr(a, ctypes.c_int32)
+
+
+def bptr(a: np.ndarray) -> Any:
+    assert a.dtype in (np.uint8, np.bool_)
+    return ptr(a.view(np.uint8), ctypes.c_uint8)
+
+
+class _ProgramArgs:
+    """A traced program's code/consts and its field-pointer table."""
+
+    def __init__(self, prog: Any, units: dict[str, np.ndarray], globals_: Any) -> None:
+        self.code = np.ascontiguousarray(prog.flat_code(), dtype=np.int32)
+        self.consts = np.ascontiguousarray(prog.const_values(globals_), dtype=np.float32)
+        if self.consts.size == 0:
+            self.consts = np.zeros(1, np.float32)
+        names = list(prog.fields)
+        out_idx = []
+        for name in prog.out_fields:
+            if name is None:
+                out_idx.append(-1)
+                continue
+            if name not in names:
+                names.append(name)
+            out_idx.append(names.index(name))
+        self.names = names
+        self.table = (_f32p * max(len(names), 1))(*[fptr(units[n]) for n in names])
+        self.out_idx = np.asarray(out_idx, dtype=np.int32)
+        self.ninstr = prog.ninstr
+
+
+class OracleNet:
+    """The reference step over host copies of a logical arena."""
+
+    def __init__(
+        self,
+        static: Any,
+        units: dict[str, np.ndarray],
+        conns: list[dict[str, np.ndarray]],
+        plan: Any,
+        globals_: Any = None,
+        *,
+        piece: int = PIECE,
+    ) -> None:
+        self.static = static
+        self.units = {k: np.ascontiguousarray(v) for k, v in units.items()}
+        self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in conns]
+        self.plan = plan
+        self.globals_ = globals_
+        self.piece = piece
+        self.step_count = 0
+        n = static.num_units
+        self.is_input = np.zeros(n, dtype=bool)
+        if static.input_ids:
+            self.is_input[np.asarray(static.input_ids)] = True
+        self.pipeline = static.propagation.value == "pipeline"
+        self.lib = load()
+
+    # -- helpers ------------------------------------------------------------
+    def _live(self) -> np.ndarray:
+        pruned = self.units.get("pruned")
+        n = self.static.num_units
+        return np.ones(n, dtype=bool) if pruned is None else ~pruned.astype(bool)
+
+    def _apply(self, pp: Any, acc: np.ndarray, mask: np.ndarray) -> None:
+        lib = self.lib
+        n = self.static.num_units
+        args = _ProgramArgs(pp.program, self.units, self.globals_)
+        nout = len(pp.program.out_fields)
+        scratch = np.zeros(max(nout, 1) * n, dtype=np.float32)
+        m = np.ascontiguousarray(mask.astype(np.uint8))
+        lib.ox_apply(
+            iptr(args.code), args.ninstr, fptr(args.consts), args.table, iptr(args.out_idx),
+            nout, n, fptr(acc), bptr(m), pp.monoid, fptr(scratch),
+        )
+
+    def _reduce_fwd(self, b: int, field: str, monoid: int) -> np.ndarray:
+        c = self.conns[b]
+        n = self.static.num_units
+        out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
+        self.lib.ox_bucket_reduce_fwd(
+            c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
+            fptr(c["weight"]), fptr(self.units[field]), monoid, fptr(out),
+        )
+        return out
+
+    def _reduce_bwd(self, b: int, field: str, monoid: int) -> np.ndarray:
+        c = self.conns[b]
+        n = self.static.num_units
+        out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
+        pc = np.zeros(n, dtype=np.float32)
+        pn = np.zeros(n, dtype=np.int32)
+        self.lib.ox_bucket_reduce_bwd(
+            c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
+            fptr(c["weight"]), fptr(self.units[field]), n, monoid, self.piece,
+            fptr(out), fptr(pc), iptr(pn),
+        )
+        return out
+
+    # -- phases ---------------------------------------------------------------
+    def forward(self) -> None:
+        fp = self.plan.forward
+        n = self.static.num_units
+        levels = self.units["level"]
+        live = self._live()
+        acc = np.full(n, fp.identity, dtype=np.float32)
+        nb = len(self.conns)
+        if self.pipeline:
+            self.lib.ox_combine(n, fp.monoid, fptr(acc), fptr(self._reduce_fwd(0, fp.field, fp.monoid)))
+            self._apply(fp, acc, ~self.is_input & live)
+            return
+        for lv in range(nb):
+            out = self._reduce_fwd(lv, fp.field, fp.monoid)
+            self.lib.ox_combine(n, fp.monoid, fptr(acc), fptr(out))
+            self._apply(fp, acc, (levels == lv + 1) & ~self.is_input & live)
+
+    def loss(self, targets: np.ndarray) -> np.float32:
+        lp = self.plan.loss
+        out_ids = np.asarray(self.static.output_ids, dtype=np.int32)
+        t = np.ascontiguousarray(np.asarray(targets, dtype=np.float32).reshape(-1))
+        seed = np.zeros(out_ids.size, dtype=np.float32)
+        terms = np.zeros(max(out_ids.size, 1), dtype=np.float32)
+        if lp.kind == "softmax":
+            val = self.lib.ox_loss_softmax_ce(
+                fptr(self.units["activation"]), iptr(out_ids), out_ids.size, fptr(t),
+                fptr(seed), fptr(terms), self.piece,
+            )
+        else:
+            args = _ProgramArgs(lp.program, self.units, self.globals_)
+            val = self.lib.ox_loss_elementwise(
+                iptr(args.code), args.ninstr, fptr(args.consts), args.table, iptr(out_ids),
+                out_ids.size, fptr(t), fptr(seed), fptr(terms), self.piece,
+            )
+        self.units[lp.seed_field][out_ids] = seed
+        return np.float32(val)
+
+    def backward(self) -> None:
+        bp = self.plan.backward
+        n = self.static.num_units
+        levels = self.units["level"]
+        live = self._live()
+        acc = np.full(n, bp.identity, dtype=np.float32)
+        nb = len(self.conns)
+        if self.pipeline:
+            self.lib.ox_combine(n, bp.monoid, fptr(acc), fptr(self._reduce_bwd(0, bp.field, bp.monoid)))
+            self._apply(bp, acc, live)
+            return
+        self._apply(bp, acc, (levels == nb) & ~self.is_input & live)
+        for lv in range(nb - 1, 0, -1):
+            out = self._reduce_bwd(lv, bp.field, bp.monoid)
+            self.lib.ox_combine(n, bp.monoid, fptr(acc), fptr(out))
+            self._apply(bp, acc, (levels == lv) & ~self.is_input & live)
+
+    def update(self) -> None:
+        up = self.plan.update
+        p = [float(v) for v in up.params()]
+        g = self.units[up.grad_field.name]
+        act = self.units["activation"]
+        for c in self.conns:
+            cap = c["dead"].size
+            base = (cap, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]), fptr(c["weight"]))
+            cols = [fptr(c[name]) for name in up.state_columns()]
+            if up.rule_code == 0:
+                self.lib.ox_update_sgd(*base, fptr(g), fptr(act), p[0])
+            elif up.rule_code == 1:
+                self.lib.ox_update_momentum(*base, *cols, fptr(g), fptr(act), p[0], p[1])
+            elif up.rule_code == 2:
+                self.lib.ox_update_adam(*base, *cols, fptr(g), fptr(act), *p[:7])
+            else:
+                self.lib.ox_update_rmsprop(*base, *cols, fptr(g), fptr(act), p[0], p[1], p[2], p[3])
+
+    def step(self, inputs: Any, targets: Any = None) -> np.float32:
+        """One streaming step (step.py:578-618); returns the loss."""
+        ids = np.asarray(self.static.input_ids, dtype=np.int64)
+        if ids.size:
+            self.units["activation"][ids] = np.asarray(inputs, dtype=np.float32).reshape(-1)
+        self.forward()
+        loss = np.float32(0.0)
+        if self.plan.loss is not None:
+            loss = np.float32(np.float32(0.0) + self.loss(targets))
+        if self.plan.backward is not None:
+            self.backward()
+        if self.plan.update is not None:
+            self.update()
+        self.step_count += 1
+        return loss
+
+
+def free_block_counts(dead: np.ndarray, block: int) -> np.ndarray:
+    """Per-block dead counts (phases.py:2595-2618)."""
+    lib = load()
+    d = np.ascontiguousarray(dead.astype(np.uint8))
+    nb = -(-d.size // block)
+    out = np.zeros(nb, dtype=np.int32)
+    lib.ox_free_block_counts(d.size, bptr(d), block, iptr(out))
+    return out
+
+
+def nth_free_slots(dead: np.ndarray, n: int) -> np.ndarray:
+    """The first n free slots in ascending slot order, -1 past the end
+    (phases.py:2670-2754)."""
+    lib = load()
+    d = np.ascontiguousarray(dead.astype(np.uint8))
+    out = np.zeros(n, dtype=np.int64)
+    lib.ox_nth_free_slots(d.size, bptr(d), n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)))
+    return out

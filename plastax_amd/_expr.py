@@ -1,0 +1,465 @@
+"""Symbolic tracing of user policies into device unit programs.
+
+The reference traces every policy callback with JAX and lowers the jaxpr
+(phases.py:535-556 reads ``linear_input``; phases.py:1910-2147 translates
+prune predicates to Triton source). This module plays the same role for the
+device library: a policy's ``map`` / ``apply`` / ``calculate_loss`` is called
+once with symbolic views, the returned expression tree is checked against what
+the kernels run, and an ``apply`` or an elementwise loss is compiled to a
+register program that the kernels interpret per unit (``plx_program`` in
+include/plastax_hip.h). The program keeps the user's float32 operation order,
+so a traced apply rounds exactly as the reference's jnp expression does.
+
+User policies write jnp-style code against :mod:`plastax_amd.numpy` (``jnp``)
+and :mod:`plastax_amd.nn`; anything the tracer cannot represent raises
+:class:`UnsupportedPolicyError` when the step is built.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any, Iterable, Sequence
+
+import numpy as np
+
+from plastax_amd._types import FieldSpec
+
+
+class UnsupportedPolicyError(NotImplementedError):
+    """A policy the device path cannot run (raised when a step is built)."""
+
+
+class TracerBoolError(UnsupportedPolicyError):
+    """Python control flow on a traced value (use jnp.where instead)."""
+
+
+# Opcodes: keep in sync with plastax_amd/csrc/plastax_hip.hip (and the
+# oracle's evaluator).
+OPCODES = {
+    "acc": 1,
+    "ldu": 2,
+    "const": 3,
+    "add": 4,
+    "sub": 5,
+    "mul": 6,
+    "div": 7,
+    "neg": 8,
+    "abs": 9,
+    "max": 10,
+    "min": 11,
+    "tanh": 12,
+    "exp": 13,
+    "log": 14,
+    "sqrt": 15,
+    "sigmoid": 16,
+    "gt": 17,
+    "ge": 18,
+    "lt": 19,
+    "le": 20,
+    "eq": 21,
+    "ne": 22,
+    "sel": 23,
+    "out": 24,
+    "target": 25,
+    "mov": 26,
+    "square": 27,
+    "relu": 28,
+    "sign": 29,
+}
+_UNARY = {"neg", "abs", "tanh", "exp", "log", "sqrt", "sigmoid", "square", "relu", "sign"}
+_BINARY = {"add", "sub", "mul", "div", "max", "min", "gt", "ge", "lt", "le", "eq", "ne"}
+MAX_REGS = 16
+MAX_INSTR = 48
+MAX_CONST = 32
+MAX_FIELDS = 8
+MAX_OUTS = 4
+
+
+def _f32(x: Any) -> np.float32:
+    return np.float32(x)
+
+
+class Expr:
+    """A node of a traced float32 expression."""
+
+    __slots__ = ("op", "args", "value", "field", "role")
+    __array_ufunc__ = None  # numpy scalars defer to the reflected operators
+
+    def __init__(
+        self,
+        op: str,
+        args: Sequence["Expr"] = (),
+        *,
+        value: Any = None,
+        field: str | None = None,
+        role: str | None = None,
+    ) -> None:
+        self.op = op
+        self.args = tuple(args)
+        self.value = value
+        self.field = field
+        self.role = role
+
+    # -- construction helpers -------------------------------------------------
+    def __repr__(self) -> str:
+        if self.op == "const":
+            return repr(float(self.value))
+        if self.op in ("ldu", "ldc"):
+            return f"{self.field}[{self.role}]"
+        if self.op in ("acc", "target", "global"):
+            return self.op if self.field is None else f"g.{self.field}"
+        return f"{self.op}({', '.join(map(repr, self.args))})"
+
+    def __bool__(self) -> bool:
+        raise TracerBoolError(
+            "a traced policy value was used in Python control flow; use jnp.where"
+        )
+
+    __hash__ = object.__hash__
+
+    # -- arithmetic -----------------------------------------------------------
+    def __add__(self, o: Any) -> "Expr":
+        return Expr("add", (self, lift(o)))
+
+    def __radd__(self, o: Any) -> "Expr":
+        return Expr("add", (lift(o), self))
+
+    def __sub__(self, o: Any) -> "Expr":
+        return Expr("sub", (self, lift(o)))
+
+    def __rsub__(self, o: Any) -> "Expr":
+        return Expr("sub", (lift(o), self))
+
+    def __mul__(self, o: Any) -> "Expr":
+        return Expr("mul", (self, lift(o)))
+
+    def __rmul__(self, o: Any) -> "Expr":
+        return Expr("mul", (lift(o), self))
+
+    def __truediv__(self, o: Any) -> "Expr":
+        return Expr("div", (self, lift(o)))
+
+    def __rtruediv__(self, o: Any) -> "Expr":
+        return Expr("div", (lift(o), self))
+
+    def __neg__(self) -> "Expr":
+        return Expr("neg", (self,))
+
+    def __pos__(self) -> "Expr":
+        return self
+
+    def __abs__(self) -> "Expr":
+        return Expr("abs", (self,))
+
+    def __pow__(self, o: Any) -> "Expr":
+        # jnp's x ** 2 lowers to integer_pow, i.e. one multiply x * x.
+        if isinstance(o, (int, np.integer)) and int(o) == 2:
+            return Expr("square", (self,))
+        if isinstance(o, (int, np.integer)) and int(o) == 1:
+            return self
+        raise UnsupportedPolicyError(f"only x ** 2 is supported in a traced policy, got ** {o!r}")
+
+    def __gt__(self, o: Any) -> "Expr":
+        return Expr("gt", (self, lift(o)))
+
+    def __ge__(self, o: Any) -> "Expr":
+        return Expr("ge", (self, lift(o)))
+
+    def __lt__(self, o: Any) -> "Expr":
+        return Expr("lt", (self, lift(o)))
+
+    def __le__(self, o: Any) -> "Expr":
+        return Expr("le", (self, lift(o)))
+
+    def __eq__(self, o: Any) -> "Expr":  # type: ignore[override]
+        return Expr("eq", (self, lift(o)))
+
+    def __ne__(self, o: Any) -> "Expr":  # type: ignore[override]
+        return Expr("ne", (self, lift(o)))
+
+    def astype(self, dtype: Any) -> "Expr":
+        if np.dtype(dtype) not in (np.dtype(np.float32), np.dtype(np.bool_)):
+            raise UnsupportedPolicyError(f"cast to {dtype} in a traced policy")
+        return self
+
+
+def lift(x: Any) -> Expr:
+    """A traced value, or a float32 constant for a Python/numpy scalar."""
+    if isinstance(x, Expr):
+        return x
+    if isinstance(x, (bool, np.bool_)):
+        return Expr("const", value=_f32(1.0 if x else 0.0))
+    if isinstance(x, (int, float, np.integer, np.floating)):
+        return Expr("const", value=_f32(x))
+    if isinstance(x, np.ndarray) and x.shape == ():
+        return Expr("const", value=_f32(x))
+    raise UnsupportedPolicyError(f"cannot trace a {type(x).__name__} value in a policy")
+
+
+# ---------------------------------------------------------------------------
+# Symbolic views handed to policies while tracing.
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass(frozen=True)
+class Index:
+    """A symbolic unit/connection index (the role it plays for the edge)."""
+
+    role: str  # "self", "src", "dst", "out", "cid"
+
+
+class TraceUnitView:
+    """Symbolic stand-in for views.UnitView: ``u[FIELD, idx]``."""
+
+    def __init__(self, dtypes: dict[str, np.dtype]) -> None:
+        self._dtypes = dtypes
+
+    def _load(self, spec: FieldSpec, role: str) -> Expr:
+        name = spec.name
+        if name not in self._dtypes:
+            raise UnsupportedPolicyError(f"unit field {name!r} is not a column of this net")
+        return Expr("ldu", field=name, role=role)
+
+    def __getitem__(self, key: tuple[FieldSpec, Any]) -> Expr:
+        spec, idx = key
+        if isinstance(idx, Index):
+            return self._load(spec, idx.role)
+        if isinstance(idx, Expr) and idx.op == "ldc" and idx.field in ("from_id", "to_id"):
+            return self._load(spec, "src" if idx.field == "from_id" else "dst")
+        raise UnsupportedPolicyError(f"unit field read at an untraceable index {idx!r}")
+
+    def gather(self, spec: FieldSpec, ids: Any) -> Expr:
+        if isinstance(ids, Index):
+            return self._load(spec, ids.role)
+        raise UnsupportedPolicyError("UnitView.gather is traced only over the output ids")
+
+
+class TraceConnView:
+    """Symbolic stand-in for views.ConnView: ``c[FIELD, cid]``."""
+
+    def __init__(self, dtypes: dict[str, np.dtype]) -> None:
+        self._dtypes = dtypes
+
+    def __getitem__(self, key: tuple[FieldSpec, Any]) -> Expr:
+        spec, idx = key
+        if not (isinstance(idx, Index) and idx.role == "cid"):
+            raise UnsupportedPolicyError("connection fields are read at the edge's own cid")
+        if spec.name not in self._dtypes:
+            raise UnsupportedPolicyError(f"conn field {spec.name!r} is not a column of this net")
+        return Expr("ldc", field=spec.name, role="cid")
+
+
+class TraceGlobals:
+    """Symbolic globals: ``g["name"]`` / ``g.name`` read a scalar global."""
+
+    def __init__(self, concrete: Any) -> None:
+        self._concrete = concrete
+
+    def __getitem__(self, key: str) -> Expr:
+        return Expr("global", field=str(key))
+
+    def __getattr__(self, key: str) -> Expr:
+        if key.startswith("_"):
+            raise AttributeError(key)
+        return Expr("global", field=key)
+
+
+# ---------------------------------------------------------------------------
+# Pattern checks for the per-edge map.
+# ---------------------------------------------------------------------------
+
+
+def linear_map_field(expr: Any, other_role: str) -> str:
+    """The unit field a map multiplies the edge weight by.
+
+    The device runs maps of the form ``c[WEIGHT, cid] * u[F, other]`` (either
+    operand order; float multiplication commutes bit for bit), the reference's
+    ``linear_input`` contract (phases.py:535-556).
+    """
+    if isinstance(expr, Expr) and expr.op == "mul":
+        a, b = expr.args
+        for w, x in ((a, b), (b, a)):
+            if (
+                w.op == "ldc"
+                and w.field == "weight"
+                and x.op == "ldu"
+                and x.role == other_role
+            ):
+                return str(x.field)
+    raise UnsupportedPolicyError(
+        f"map must be c[WEIGHT, cid] * u[FIELD, {other_role}] to run on the device, got {expr!r}"
+    )
+
+
+# ---------------------------------------------------------------------------
+# Program compilation.
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass
+class Program:
+    """A compiled unit program (plx_program)."""
+
+    code: list[tuple[int, int, int, int]]
+    consts: list[np.float32]
+    fields: list[str]  # LDU operand table (unit field names)
+    out_fields: list[str | None]  # OUT slot -> unit field written (None: returned)
+    globals_at: dict[int, str]  # const slot -> global name, refreshed per call
+
+    @property
+    def ninstr(self) -> int:
+        return len(self.code)
+
+    def flat_code(self) -> np.ndarray:
+        return np.asarray(self.code, dtype=np.int32).reshape(-1)
+
+    def const_values(self, globals_: Any = None) -> np.ndarray:
+        vals = np.asarray(self.consts, dtype=np.float32).copy()
+        for slot, name in self.globals_at.items():
+            vals[slot] = np.float32(_read_global(globals_, name))
+        return vals
+
+
+def _read_global(g: Any, name: str) -> Any:
+    if isinstance(g, dict):
+        v = g[name]
+    else:
+        v = getattr(g, name)
+    arr = np.asarray(v)
+    if arr.shape != ():
+        raise UnsupportedPolicyError(f"global {name!r} must be a scalar to be traced")
+    return arr
+
+
+def compile_program(
+    outputs: Sequence[Any], out_fields: Sequence[str | None], *, allow: Iterable[str]
+) -> Program:
+    """Compile expression outputs to a register program.
+
+    ``allow`` names the leaf kinds the context permits: "acc" (apply),
+    "target" (loss), and the unit-field roles ("self" or "out").
+    """
+    allowed = set(allow)
+    outs = [lift(o) for o in outputs]
+    if len(outs) > MAX_OUTS:
+        raise UnsupportedPolicyError(f"a policy writes {len(outs)} fields; at most {MAX_OUTS}")
+
+    order: list[Expr] = []
+    seen: set[int] = set()
+
+    def visit(e: Expr) -> None:
+        stack = [(e, False)]
+        while stack:
+            node, done = stack.pop()
+            if id(node) in seen:
+                continue
+            if done:
+                seen.add(id(node))
+                order.append(node)
+                continue
+            stack.append((node, True))
+            for a in reversed(node.args):
+                if id(a) not in seen:
+                    stack.append((a, False))
+
+    for o in outs:
+        visit(o)
+
+    # Last use of each node, for register reuse.
+    last_use: dict[int, int] = {}
+    for pos, node in enumerate(order):
+        for a in node.args:
+            last_use[id(a)] = pos
+    for o in outs:
+        last_use[id(o)] = len(order)
+
+    consts: list[np.float32] = []
+    const_slot: dict[Any, int] = {}
+    globals_at: dict[int, str] = {}
+    fields: list[str] = []
+    reg: dict[int, int] = {}
+    free = list(range(MAX_REGS - 1, -1, -1))
+    code: list[tuple[int, int, int, int]] = []
+
+    def const_index(key: Any, value: np.float32) -> int:
+        if key not in const_slot:
+            if len(consts) >= MAX_CONST:
+                raise UnsupportedPolicyError("a policy uses too many constants")
+            const_slot[key] = len(consts)
+            consts.append(value)
+        return const_slot[key]
+
+    for pos, node in enumerate(order):
+        if not free:
+            raise UnsupportedPolicyError("a policy expression needs too many registers")
+        op = node.op
+        if op == "const":
+            k = const_index(("c", np.float32(node.value).tobytes()), np.float32(node.value))
+            instr = ("const", k, 0)
+        elif op == "global":
+            k = const_index(("g", node.field), np.float32(0.0))
+            globals_at[k] = str(node.field)
+            instr = ("const", k, 0)
+        elif op == "acc":
+            if "acc" not in allowed:
+                raise UnsupportedPolicyError("the accumulator is only visible to apply")
+            instr = ("acc", 0, 0)
+        elif op == "target":
+            if "target" not in allowed:
+                raise UnsupportedPolicyError("targets are only visible to the loss")
+            instr = ("target", 0, 0)
+        elif op == "ldu":
+            if node.role not in allowed:
+                raise UnsupportedPolicyError(
+                    f"unit field {node.field!r} read at {node.role!r}: only the unit's own "
+                    "fields are visible here"
+                )
+            if node.field not in fields:
+                if len(fields) >= MAX_FIELDS:
+                    raise UnsupportedPolicyError("a policy reads too many unit fields")
+                fields.append(str(node.field))
+            instr = ("ldu", fields.index(str(node.field)), 0)
+        elif op in _UNARY:
+            instr = (op, reg[id(node.args[0])], 0)
+        elif op in _BINARY:
+            instr = (op, reg[id(node.args[0])], reg[id(node.args[1])])
+        elif op == "sel":
+            # r[d] = r[a] != 0 ? r[b] : r[b+1]: the two branches go to a
+            # consecutive register pair.
+            c, t, f = (reg[id(a)] for a in node.args)
+            if not free or len(free) < 2:
+                raise UnsupportedPolicyError("a policy expression needs too many registers")
+            pair = _take_pair(free)
+            code.append((OPCODES["mov"], pair, t, 0))
+            code.append((OPCODES["mov"], pair + 1, f, 0))
+            instr = ("sel", c, pair)
+        elif op == "ldc":
+            raise UnsupportedPolicyError("connection fields are not visible to a unit program")
+        else:
+            raise UnsupportedPolicyError(f"operation {op!r} cannot run on the device")
+        # Release operands whose last use is here before picking a register.
+        for a in node.args:
+            if last_use.get(id(a)) == pos and reg[id(a)] not in free:
+                free.append(reg[id(a)])
+        d = free.pop()
+        reg[id(node)] = d
+        name, a0, b0 = instr
+        code.append((OPCODES[name], d, a0, b0))
+        if op == "sel":
+            free.append(b0)
+            free.append(b0 + 1)
+    for slot, o in enumerate(outs):
+        code.append((OPCODES["out"], slot, reg[id(o)], 0))
+    if len(code) > MAX_INSTR:
+        raise UnsupportedPolicyError(f"a policy compiles to {len(code)} instructions; at most {MAX_INSTR}")
+    return Program(code, consts, fields, list(out_fields), globals_at)
+
+
+def _take_pair(free: list[int]) -> int:
+    s = set(free)
+    for r in range(0, MAX_REGS - 1):
+        if r in s and r + 1 in s:
+            free.remove(r)
+            free.remove(r + 1)
+            return r
+    raise UnsupportedPolicyError("a policy expression needs too many registers")

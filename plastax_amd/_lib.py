@@ -1,0 +1,177 @@
+"""ctypes binding of the C ABI in include/plastax_hip.h.
+
+The library is loaded from the package directory (built in-tree by
+plastax_amd.build). There is no fallback: if the library is missing or a call
+fails, the error is raised here, so a step either runs the HIP kernels or
+fails loudly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+from typing import Any
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
+
+PLX_MAX_INSTR = 48
+PLX_MAX_CONST = 32
+PLX_MAX_FIELDS = 8
+PLX_MAX_OUTS = 4
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+c_vp = ctypes.c_void_p
+
+
+class PlxError(RuntimeError):
+    """A C-ABI call returned an error code."""
+
+
+class plx_program(ctypes.Structure):
+    _fields_ = [
+        ("ninstr", c_i32),
+        ("nout", c_i32),
+        ("nfields", c_i32),
+        ("reserved", c_i32),
+        ("code", c_i32 * (4 * PLX_MAX_INSTR)),
+        ("consts", c_f32 * PLX_MAX_CONST),
+        ("fields", c_vp * PLX_MAX_FIELDS),
+        ("outs", c_vp * PLX_MAX_OUTS),
+    ]
+
+
+class plx_finalize(ctypes.Structure):
+    _fields_ = [
+        ("level", c_vp),
+        ("is_input", c_vp),
+        ("pruned", c_vp),
+        ("fin_level", c_i32),
+        ("skip_inputs", c_i32),
+    ]
+
+
+class plx_forward_desc(ctypes.Structure):
+    _fields_ = [
+        ("nrows", c_i32),
+        ("monoid", c_i32),
+        ("row_unit", c_vp),
+        ("row_ptr", c_vp),
+        ("src", c_vp),
+        ("weight", c_vp),
+        ("dead", c_vp),
+        ("x", c_vp),
+        ("acc", c_vp),
+        ("fin", plx_finalize),
+        ("apply", plx_program),
+    ]
+
+
+class plx_backward_fold_desc(ctypes.Structure):
+    _fields_ = [
+        ("nitems", c_i32),
+        ("monoid", c_i32),
+        ("item_ptr", c_vp),
+        ("sperm", c_vp),
+        ("sdst", c_vp),
+        ("weight", c_vp),
+        ("g", c_vp),
+        ("item_sum", c_vp),
+    ]
+
+
+class plx_backward_finalize_desc(ctypes.Structure):
+    _fields_ = [
+        ("nrows", c_i32),
+        ("monoid", c_i32),
+        ("row_unit", c_vp),
+        ("row_item", c_vp),
+        ("item_sum", c_vp),
+        ("acc", c_vp),
+        ("fin", plx_finalize),
+        ("apply", plx_program),
+    ]
+
+
+class plx_update_desc(ctypes.Structure):
+    _fields_ = [
+        ("n", c_i64),
+        ("rule", c_i32),
+        ("pow_table_len", c_i32),
+        ("src", c_vp),
+        ("dst", c_vp),
+        ("dead", c_vp),
+        ("weight", c_vp),
+        ("s0", c_vp),
+        ("s1", c_vp),
+        ("s2", c_vp),
+        ("gfield", c_vp),
+        ("act", c_vp),
+        ("pow_table", c_vp),
+        ("p", c_f32 * 8),
+    ]
+
+
+_SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
+    "plx_forward_bucket": (c_i32, [ctypes.POINTER(plx_forward_desc), c_vp]),
+    "plx_backward_fold": (c_i32, [ctypes.POINTER(plx_backward_fold_desc), c_vp]),
+    "plx_backward_finalize": (c_i32, [ctypes.POINTER(plx_backward_finalize_desc), c_vp]),
+    "plx_update_conn": (c_i32, [ctypes.POINTER(plx_update_desc), c_vp]),
+    "plx_scatter_f32": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "plx_loss_elementwise": (
+        c_i32,
+        [c_i32, c_vp, c_vp, ctypes.POINTER(plx_program), c_vp, c_vp, c_vp, c_vp],
+    ),
+    "plx_loss_softmax_ce": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_fill_f32": (c_i32, [c_i64, c_f32, c_vp, c_vp]),
+    "plx_philox32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "plx_eval_math": (c_i32, [c_i32, c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "plx_last_error": (ctypes.c_char_p, []),
+    "plx_abi_version": (c_i32, []),
+    "plx_struct_sizes": (c_i32, [ctypes.POINTER(c_i64), c_i32]),
+}
+
+# Entry points the header declares (checked by the CPU test suite).
+EXPORTED = tuple(_SIGNATURES)
+
+STRUCTS = (
+    plx_program,
+    plx_finalize,
+    plx_forward_desc,
+    plx_backward_fold_desc,
+    plx_backward_finalize_desc,
+    plx_update_desc,
+)
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build the HIP library with `python -m plastax_amd.build`"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise PlxError for a non-zero return code."""
+    if rc != 0:
+        msg = load().plx_last_error()
+        raise PlxError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+def call(name: str, *args: Any) -> None:
+    """Call an entry point and raise on error."""
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,207 @@
+"""Trace a Network's policies into the device plan of its step.
+
+``build_phases`` (phases.py:87-182) decides the reference's phase tuple at
+trace time; ``compile_plan`` makes the same decisions for the device and
+checks that every present policy has a device lowering:
+
+- forward / backward: the map must be linear (``WEIGHT * field[other]``,
+  the ``linear_input`` contract of phases.py:535-556), the combine a named
+  monoid, and ``apply`` is compiled to a unit program;
+- loss: ``SoftmaxCrossEntropyLoss`` runs its own kernel; any other loss must
+  return ``(jnp.sum(term), seed)`` with ``term`` and ``seed`` elementwise in
+  the output's prediction and target, and is compiled to a program;
+- update_conn: one of the optim bundles (fused update kernel).
+
+Policies outside these forms raise UnsupportedPolicyError.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any
+
+import numpy as np
+
+from plastax_amd import _lib
+from plastax_amd._expr import (
+    Expr,
+    Index,
+    Program,
+    TraceConnView,
+    TraceGlobals,
+    TraceUnitView,
+    UnsupportedPolicyError,
+    compile_program,
+    linear_map_field,
+)
+from plastax_amd.monoid import Monoid
+from plastax_amd.optim._rules import _RuleBase
+from plastax_amd.state import NetworkStatic
+from plastax_amd.traits import SoftmaxCrossEntropyLoss
+from plastax_amd.views import UnitWrite
+
+POW_TABLE_LEN = 1 << 16
+
+
+@dataclasses.dataclass
+class PassPlan:
+    """A traced forward or backward pass."""
+
+    field: str  # the linear_input unit field the map gathers
+    monoid: int
+    identity: float
+    program: Program  # the apply
+
+
+@dataclasses.dataclass
+class LossPlan:
+    kind: str  # "softmax" or "elementwise"
+    seed_field: str
+    program: Program | None = None
+
+
+@dataclasses.dataclass
+class Plan:
+    forward: PassPlan
+    loss: LossPlan | None
+    backward: PassPlan | None
+    update: Any  # an optim _RuleBase or None
+
+    def pow_table(self) -> np.ndarray:
+        """float32(b1^t), float32(b2^t) for t < POW_TABLE_LEN, by binary
+        exponentiation in float64 (the device's pow_step, bit for bit)."""
+        p = self.update.params()
+        b1, b2 = float(p[1]), float(p[2])
+        t = np.arange(POW_TABLE_LEN, dtype=np.int64)
+        out = np.empty((POW_TABLE_LEN, 2), dtype=np.float32)
+        for col, b in enumerate((b1, b2)):
+            acc = np.ones(POW_TABLE_LEN, dtype=np.float64)
+            base = np.float64(b)
+            n = t.copy()
+            while bool(n.any()):
+                odd = (n & 1).astype(bool)
+                acc = np.where(odd, acc * base, acc)
+                base = base * base
+                n >>= 1
+            out[:, col] = acc.astype(np.float32)
+        return out.reshape(-1)
+
+
+def _float_unit_fields(static: NetworkStatic) -> dict[str, np.dtype]:
+    return {s.name: np.dtype(s.dtype) for s in static.unit_fields}
+
+
+def _check_float_fields(names: list[str | None], dtypes: dict[str, np.dtype], what: str) -> None:
+    for name in names:
+        if name is None:
+            continue
+        if name not in dtypes:
+            raise UnsupportedPolicyError(f"{what} writes {name!r}, which is not a unit column")
+        if dtypes[name] != np.float32:
+            raise UnsupportedPolicyError(f"{what} touches {name!r}, which is not float32")
+
+
+def _trace_pass(policy: Any, static: NetworkStatic, *, backward: bool) -> PassPlan:
+    dtypes = _float_unit_fields(static)
+    conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
+    u = TraceUnitView(dtypes)
+    c = TraceConnView(conn_dtypes)
+    g = TraceGlobals(None)
+    name = type(policy).__name__
+    combine = policy.combine
+    if not isinstance(combine, Monoid):
+        raise UnsupportedPolicyError(f"{name}.combine must be a single named monoid")
+    if backward:
+        expr = policy.map(u, Index("src"), Index("dst"), c, Index("cid"), g)
+        field = linear_map_field(expr, "dst")
+    else:
+        expr = policy.map(u, Index("dst"), Index("src"), c, Index("cid"), g)
+        field = linear_map_field(expr, "src")
+    write = policy.apply(u, Index("self"), g, Expr("acc"))
+    if not isinstance(write, UnitWrite):
+        raise UnsupportedPolicyError(f"{name}.apply must return a UnitWrite")
+    outs = list(write.fields.keys())
+    prog = compile_program(list(write.fields.values()), outs, allow={"acc", "self"})
+    _check_float_fields(outs + prog.fields + [field], dtypes, f"{name}")
+    return PassPlan(field=field, monoid=combine.code, identity=combine.identity_for(), program=prog)
+
+
+def _trace_loss(loss: Any, static: NetworkStatic) -> LossPlan:
+    dtypes = _float_unit_fields(static)
+    seed_field = loss.seed_field.name
+    _check_float_fields([seed_field], dtypes, type(loss).__name__)
+    if isinstance(loss, SoftmaxCrossEntropyLoss):
+        return LossPlan("softmax", seed_field)
+    u = TraceUnitView(dtypes)
+    out = loss.calculate_loss(u, Index("out"), Expr("target"), TraceGlobals(None))
+    if not (isinstance(out, tuple) and len(out) == 2):
+        raise UnsupportedPolicyError("calculate_loss must return (loss, seed)")
+    value, seed = out
+    if not (isinstance(value, Expr) and value.op == "sum"):
+        raise UnsupportedPolicyError(
+            "an elementwise loss must return jnp.sum(term) over the outputs as its value"
+        )
+    term = value.args[0]
+    prog = compile_program([seed, term], [seed_field, None], allow={"target", "out"})
+    _check_float_fields(prog.fields, dtypes, type(loss).__name__)
+    return LossPlan("elementwise", seed_field, prog)
+
+
+def compile_plan(net: type, static: NetworkStatic) -> Plan:
+    """The device plan of ``net``'s streaming step."""
+    for slot in ("update_unit", "prune_unit", "prune_conn", "add_unit", "add_conn", "reset_global"):
+        if getattr(net, slot, None) is not None:
+            raise UnsupportedPolicyError(f"{net.__name__}.{slot}: not in this build yet")
+    forward = _trace_pass(net.forward_pass, static, backward=False)
+    loss = _trace_loss(net.loss, static) if net.loss is not None else None
+    backward = (
+        _trace_pass(net.backward_pass, static, backward=True)
+        if net.backward_pass is not None
+        else None
+    )
+    update = None
+    if net.update_conn is not None:
+        uc = net.update_conn
+        if not isinstance(uc, _RuleBase):
+            raise UnsupportedPolicyError(
+                f"{net.__name__}.update_conn must be an optim bundle's update_conn() to run "
+                "on the device"
+            )
+        dtypes = _float_unit_fields(static)
+        _check_float_fields([uc.grad_field.name], dtypes, "update_conn")
+        conn_names = {s.name for s in static.conn_fields}
+        for col in uc.state_columns():
+            if col not in conn_names:
+                raise ValueError(
+                    f"{net.__name__}: optimizer column {col!r} missing from extra_conn_fields"
+                )
+        update = uc
+    return Plan(forward, loss, backward, update)
+
+
+def program_struct(
+    prog: Program,
+    units: dict,
+    globals_: Any,
+    *,
+    out_override: dict | None = None,
+) -> "_lib.plx_program":
+    """The plx_program of ``prog`` over the given unit tensors."""
+    p = _lib.plx_program()
+    p.ninstr = prog.ninstr
+    p.nout = len(prog.out_fields)
+    p.nfields = len(prog.fields)
+    code = prog.flat_code()
+    for k, v in enumerate(code):
+        p.code[k] = int(v)
+    for k, v in enumerate(prog.const_values(globals_)):
+        p.consts[k] = float(v)
+    for k, name in enumerate(prog.fields):
+        p.fields[k] = units[name].data_ptr()
+    over = out_override or {}
+    for k, name in enumerate(prog.out_fields):
+        if name is None:
+            p.outs[k] = None
+        else:
+            p.outs[k] = (over[name] if name in over else units[name]).data_ptr()
+    return p

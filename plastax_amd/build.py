@@ -1,0 +1,70 @@
+"""Compile the gfx950 HIP library in-tree: plastax_amd/libplastax_hip.so.
+
+Run as ``python -m plastax_amd.build`` (``__graft_entry__.build()`` calls
+:func:`build`). The library has no Python dependency: ctypes loads it.
+
+Flags that carry meaning:
+
+- ``-ffp-contract=off``: no fused multiply-add contraction. Every product and
+  sum of the step rounds to float32 on its own, exactly as the reference's
+  jnp operations do, so the device trajectory can be compared bit for bit.
+- ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed float32
+  instructions (their results have been unreliable on this pool).
+"""
+
+from __future__ import annotations
+
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+PKG = pathlib.Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libplastax_hip.so"
+SOURCES = ("plastax_hip.hip", "structural.hip")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-fvisibility=hidden",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    """Path of hipcc (ROCm's, or the one on PATH)."""
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and pathlib.Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the HIP library cannot be built")
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    """Compile every HIP source into the in-tree shared library."""
+    sources = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), *sources, "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

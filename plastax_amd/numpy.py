@@ -1,0 +1,98 @@
+"""jnp-style functions for writing device-traceable policies.
+
+Import as ``import plastax_amd.numpy as jnp``. On traced values these build
+expression nodes (see plastax_amd._expr); on plain numbers they compute in
+float32 with numpy, so a policy also runs eagerly on host scalars.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import numpy as np
+
+from plastax_amd._expr import Expr, UnsupportedPolicyError, lift
+
+float32 = np.float32
+int32 = np.int32
+uint32 = np.uint32
+bool_ = np.bool_
+inf = np.inf
+nan = np.nan
+pi = np.pi
+
+
+def _traced(*xs: Any) -> bool:
+    return any(isinstance(x, Expr) for x in xs)
+
+
+def _unary(name: str, fn: Any) -> Any:
+    def op(x: Any) -> Any:
+        if _traced(x):
+            return Expr(name, (lift(x),))
+        return fn(np.float32(x))
+
+    op.__name__ = name
+    return op
+
+
+tanh = _unary("tanh", np.tanh)
+exp = _unary("exp", np.exp)
+log = _unary("log", np.log)
+sqrt = _unary("sqrt", np.sqrt)
+abs = _unary("abs", np.abs)  # noqa: A001 -- mirrors jnp.abs
+absolute = abs
+negative = _unary("neg", np.negative)
+sign = _unary("sign", np.sign)
+
+
+def square(x: Any) -> Any:
+    if _traced(x):
+        return Expr("square", (lift(x),))
+    x = np.float32(x)
+    return np.float32(x * x)
+
+
+def _binary(name: str, fn: Any) -> Any:
+    def op(a: Any, b: Any) -> Any:
+        if _traced(a, b):
+            return Expr(name, (lift(a), lift(b)))
+        return fn(np.float32(a), np.float32(b))
+
+    op.__name__ = name
+    return op
+
+
+maximum = _binary("max", np.maximum)
+minimum = _binary("min", np.minimum)
+add = _binary("add", np.add)
+subtract = _binary("sub", np.subtract)
+multiply = _binary("mul", np.multiply)
+divide = _binary("div", np.divide)
+greater = _binary("gt", np.greater)
+less = _binary("lt", np.less)
+
+
+def where(cond: Any, a: Any, b: Any) -> Any:
+    if _traced(cond, a, b):
+        return Expr("sel", (lift(cond), lift(a), lift(b)))
+    return np.where(cond, np.float32(a), np.float32(b))
+
+
+def sum(x: Any, axis: Any = None) -> Any:  # noqa: A001 -- mirrors jnp.sum
+    """Sum over the traced output axis (a loss's reduction)."""
+    if _traced(x):
+        if axis not in (None, 0, -1):
+            raise UnsupportedPolicyError("traced sums reduce over the output axis only")
+        return Expr("sum", (lift(x),))
+    return np.sum(np.asarray(x, dtype=np.float32), axis=axis, dtype=np.float32)
+
+
+def asarray(x: Any, dtype: Any = None) -> Any:
+    if _traced(x):
+        return x
+    return np.asarray(x, dtype=dtype)
+
+
+def clip(x: Any, lo: Any, hi: Any) -> Any:
+    return minimum(maximum(x, lo), hi)

@@ -1,0 +1,219 @@
+"""Network state: the static jit key and the mutable struct of arrays.
+
+Mirrors src/plastax/state.py:22-313. ``NetworkStatic`` is the hashable
+configuration; ``NetworkState`` holds the unit columns, the connection
+buckets and the scalar signals. Columns are torch tensors on the GPU
+(``cuda:0``), or on the CPU for host-only construction.
+
+Connection buckets are presented in the reference's *logical* slot order
+(``state.conns[b][name]``). The step itself runs on a physical,
+destination-sorted copy (plastax_amd._layout.Arena); after a step the logical
+columns are refreshed from it the first time they are read.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any
+
+import numpy as np
+import torch
+
+from plastax_amd._types import PRUNED, FieldSpec, Propagation, ShardSpec
+
+Columns = dict[str, torch.Tensor]
+
+
+@dataclasses.dataclass(frozen=True)
+class NetworkStatic:
+    """Static network configuration (state.py:22-75)."""
+
+    num_units: int
+    propagation: Propagation
+    unit_fields: tuple[FieldSpec, ...]
+    conn_fields: tuple[FieldSpec, ...]
+    level_capacities: tuple[int, ...]
+    kahn_max_depth: int | None
+    input_ids: tuple[int, ...]
+    output_ids: tuple[int, ...]
+    sharding: ShardSpec | None = None
+    capacity_headroom: float = 0.0
+    capacity_align: int | None = None
+    seed: int = 0
+    deepest_grows: bool = False
+
+
+def torch_dtype(dtype: np.dtype) -> torch.dtype:
+    """The torch dtype storing a column of numpy dtype ``dtype``."""
+    dt = np.dtype(dtype)
+    if dt == np.bool_:
+        return torch.uint8
+    return {
+        np.dtype(np.float32): torch.float32,
+        np.dtype(np.int32): torch.int32,
+        np.dtype(np.uint32): torch.int32,
+        np.dtype(np.float64): torch.float64,
+        np.dtype(np.int64): torch.int64,
+        np.dtype(np.uint8): torch.uint8,
+    }[dt]
+
+
+def default_device() -> torch.device:
+    """``cuda:0`` when a GPU is visible, else the CPU."""
+    return torch.device("cuda", 0) if torch.cuda.is_available() else torch.device("cpu")
+
+
+def to_column(host: np.ndarray, spec: FieldSpec, device: torch.device) -> torch.Tensor:
+    """Upload one host column with the storage dtype of ``spec``."""
+    arr = np.ascontiguousarray(np.asarray(host).astype(spec.dtype, copy=False))
+    if arr.dtype == np.bool_:
+        arr = arr.view(np.uint8)
+    elif arr.dtype == np.uint32:
+        arr = arr.view(np.int32)
+    return torch.from_numpy(arr.copy()).to(device)
+
+
+def column_to_numpy(col: torch.Tensor, spec: FieldSpec) -> np.ndarray:
+    """Download one column as a numpy array of the spec's dtype."""
+    arr = col.detach().cpu().numpy()
+    if np.dtype(spec.dtype) == np.bool_:
+        return arr.astype(np.bool_)
+    if np.dtype(spec.dtype) == np.uint32:
+        return arr.view(np.uint32)
+    return arr
+
+
+class NetworkState:
+    """Mutable arena state (state.py:83-135).
+
+    Attributes mirror the reference: ``units`` (name -> (num_units,) tensor),
+    ``conns`` (one dict per bucket, logical slot order), ``globals_``,
+    ``needs_resort``, ``step``, ``grown``, ``overflow``, ``units_added``,
+    ``unit_overflow``, ``tail_start``. A state passed to a step is donated:
+    the step reuses its buffers and the old object raises on access.
+    """
+
+    def __init__(
+        self,
+        units: Columns,
+        conns: tuple[Columns, ...],
+        globals_: Any,
+        needs_resort: bool = False,
+        step: int = 0,
+        grown: int = 0,
+        overflow: bool = False,
+        units_added: int = 0,
+        unit_overflow: bool = False,
+        tail_start: int = 0,
+    ) -> None:
+        self._units = dict(units)
+        self._conns: tuple[Columns, ...] = tuple(dict(b) for b in conns)
+        self.globals_ = globals_
+        self.needs_resort = needs_resort
+        self.step = step
+        self.grown = grown
+        self.overflow = overflow
+        self.units_added = units_added
+        self.unit_overflow = unit_overflow
+        self.tail_start = tail_start
+        self._arena: Any = None  # plastax_amd._layout.Arena once a step ran
+        self._arena_ahead = False  # the arena holds newer conn values
+        self._donated = False
+
+    # -- donation -------------------------------------------------------------
+    def _check(self) -> None:
+        if self._donated:
+            raise RuntimeError(
+                "this NetworkState was donated to a step; use the state in its StepResult"
+            )
+
+    def _donate(self) -> "NetworkState":
+        """Hand every buffer to a fresh state object and retire this one."""
+        self._check()
+        new = NetworkState(
+            self._units,
+            self._conns,
+            self.globals_,
+            self.needs_resort,
+            self.step,
+            self.grown,
+            self.overflow,
+            self.units_added,
+            self.unit_overflow,
+            self.tail_start,
+        )
+        new._arena = self._arena
+        new._arena_ahead = self._arena_ahead
+        self._donated = True
+        return new
+
+    # -- columns --------------------------------------------------------------
+    @property
+    def units(self) -> Columns:
+        self._check()
+        return self._units
+
+    @units.setter
+    def units(self, value: Columns) -> None:
+        self._check()
+        self._units = dict(value)
+
+    @property
+    def conns(self) -> tuple[Columns, ...]:
+        """Connection buckets in logical slot order (synchronised from the
+        device arena on first access after a step)."""
+        self._check()
+        if self._arena is not None and self._arena_ahead:
+            self._arena.write_logical(self._conns)
+            self._arena_ahead = False
+        return self._conns
+
+    @conns.setter
+    def conns(self, value: tuple[Columns, ...]) -> None:
+        self._check()
+        self._conns = tuple(dict(b) for b in value)
+        self._arena = None  # structure or values changed on the host side
+        self._arena_ahead = False
+
+    @property
+    def device(self) -> torch.device:
+        return next(iter(self._units.values())).device
+
+    def __repr__(self) -> str:
+        if self._donated:
+            return "NetworkState(<donated>)"
+        caps = tuple(int(next(iter(b.values())).shape[0]) for b in self._conns)
+        return f"NetworkState(units={len(self._units)} cols, buckets={caps}, step={self.step})"
+
+
+def _filled(specs: tuple[FieldSpec, ...], n: int, device: torch.device) -> Columns:
+    return {s.name: to_column(np.full((n,), s.default, dtype=s.dtype), s, device) for s in specs}
+
+
+def make_empty_state(static: NetworkStatic, globals_: Any, device: Any = None) -> NetworkState:
+    """Arenas at capacity with every connection slot dead (state.py:148-177)."""
+    dev = torch.device(device) if device is not None else default_device()
+    units = _filled(static.unit_fields, static.num_units, dev)
+    conns = tuple(_filled(static.conn_fields, c, dev) for c in static.level_capacities)
+    return NetworkState(units, conns, globals_)
+
+
+def live_conn_count(state: NetworkState, level: int | None = None) -> int:
+    """Live connections in one bucket or all (state.py:180-198)."""
+    buckets = state.conns if level is None else (state.conns[level],)
+    return int(sum(int((b["dead"] == 0).sum()) for b in buckets))
+
+
+def live_unit_mask(units: Columns) -> torch.Tensor | None:
+    """Unit slots holding a live unit, or None without a unit capacity
+    (state.py:201-219)."""
+    pruned = units.get(PRUNED.name)
+    return None if pruned is None else pruned == 0
+
+
+def live_unit_count(state: NetworkState) -> int:
+    """Live units (state.py:222-235)."""
+    live = live_unit_mask(state.units)
+    if live is None:
+        return int(next(iter(state.units.values())).shape[0])
+    return int(live.sum())

@@ -1,0 +1,347 @@
+"""``make_step``: assemble a network's phases into one device step.
+
+Mirrors src/plastax/step.py:76-237 and :545-626. ``make_step(net, static)``
+traces the net's policies once (plastax_amd._plan) and returns a callable
+``step(state, inputs) -> StepResult``. A call runs, on torch's current HIP
+stream and without a host synchronisation: the input scatter (step.py:598),
+the forward level walk, the loss, the backward level walk and the fused
+connection update (phases.py:150-157), then bumps ``state.step``. The state
+is donated (step.py:624): its buffers are updated in place and the returned
+``StepResult.state`` owns them.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any, Literal
+
+import numpy as np
+import torch
+
+from plastax_amd import _lib
+from plastax_amd._expr import UnsupportedPolicyError
+from plastax_amd._layout import Arena
+from plastax_amd._plan import Plan, compile_plan, program_struct
+from plastax_amd._types import ACTIVATION, Propagation
+from plastax_amd.state import NetworkState, NetworkStatic
+
+
+@dataclasses.dataclass(frozen=True)
+class StepInputs:
+    """Clamped inputs and loss targets of one step (phases.py:72-84)."""
+
+    inputs: Any
+    targets: Any = None
+
+
+@dataclasses.dataclass(frozen=True)
+class StepResult:
+    """A step's output (step.py:45-67): the new state, the growth overflow
+    flag, the loss (a 0-d float32 device tensor) and the dropped growth
+    candidates (None without growth)."""
+
+    state: NetworkState
+    overflow: Any
+    loss: Any
+    growth_remainder: Any = None
+
+
+def make_step(
+    net: type,
+    static: NetworkStatic,
+    *,
+    batch_size: int | None = None,
+    layout: Literal["auto", "edge_list", "csr", "triton"] = "auto",
+    fuse_prune: Literal["auto", "triton", "xla", "off"] = "auto",
+    growth: Literal["auto", "xla", "triton"] = "auto",
+) -> "StepFn":
+    """Build the device step of ``net`` (step.py:76-237).
+
+    Raises ValueError on the reference's argument errors and
+    UnsupportedPolicyError for a policy the device path cannot run.
+    """
+    if batch_size is not None:
+        if batch_size < 1:
+            raise ValueError(f"make_step: batch_size must be >= 1, got {batch_size}")
+        if net.propagation is Propagation.PIPELINE:
+            raise ValueError(
+                "make_step: batch_size is for TOPOLOGICAL (feed-forward) nets; a "
+                "PIPELINE net carries per-sample recurrent state between steps"
+            )
+        if net.batch_reduction is None:
+            raise ValueError(
+                f"make_step: a batched step needs {net.__name__}.batch_reduction"
+            )
+    if layout not in ("auto", "edge_list", "csr", "triton"):
+        raise ValueError(f"make_step: unknown layout {layout!r}")
+    if fuse_prune not in ("auto", "triton", "xla", "off"):
+        raise ValueError(f"make_step: unknown fuse_prune {fuse_prune!r}")
+    if growth not in ("auto", "xla", "triton"):
+        raise ValueError(f"make_step: unknown growth engine {growth!r}")
+    if batch_size is not None:
+        raise UnsupportedPolicyError("batched steps (batch_size) are not in this build yet")
+    return StepFn(compile_plan(net, static), static)
+
+
+def _stream(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+class StepFn:
+    """The callable ``make_step`` returns."""
+
+    def __init__(self, plan: Plan, static: NetworkStatic) -> None:
+        self.plan = plan
+        self.static = static
+        self._dev_consts: dict[Any, Any] = {}
+        # Optional hook with begin(kind) / end(kind), called around every
+        # kernel launch on the launching stream (the benchmark records HIP
+        # events there).
+        self.timer: Any = None
+
+    def _launch(self, kind: str, fn: Any, *args: Any) -> None:
+        timer = self.timer
+        if timer is not None:
+            timer.begin(kind)
+        _lib.check(fn(*args), kind)
+        if timer is not None:
+            timer.end(kind)
+
+    # -- per-device constants ------------------------------------------------
+    def _consts(self, device: torch.device) -> dict[str, Any]:
+        key = (device.type, device.index)
+        if key not in self._dev_consts:
+            st = self.static
+            is_input = np.zeros(st.num_units, dtype=np.uint8)
+            if st.input_ids:
+                is_input[np.asarray(st.input_ids)] = 1
+            c = {
+                "input_ids": torch.tensor(st.input_ids, dtype=torch.int32, device=device),
+                "output_ids": torch.tensor(st.output_ids, dtype=torch.int32, device=device),
+                "is_input": torch.from_numpy(is_input).to(device),
+            }
+            if self.plan.update is not None and self.plan.update.rule_code == 2:
+                c["pow_table"] = torch.from_numpy(self.plan.pow_table()).to(device)
+            self._dev_consts[key] = c
+        return self._dev_consts[key]
+
+    def arena(self, state: NetworkState) -> Arena:
+        """The state's physical arena (built on first use)."""
+        if state._arena is None:
+            state._arena = Arena(self.static, state.units, state._conns, state.device)
+            state._arena_ahead = False
+        return state._arena
+
+    # -- the step ------------------------------------------------------------
+    def __call__(self, state: NetworkState, inputs: StepInputs) -> StepResult:
+        plan = self.plan
+        dev = state.device
+        if dev.type != "cuda":
+            raise RuntimeError("the plastax_amd step runs on a GPU; the state lives on the CPU")
+        lib = _lib.load()
+        state = state._donate()
+        arena = self.arena(state)
+        consts = self._consts(dev)
+        stream = _stream(dev)
+        units = state.units
+        n_units = self.static.num_units
+
+        # Input scatter (step.py:598).
+        n_in = len(self.static.input_ids)
+        if n_in:
+            x_in = torch.as_tensor(inputs.inputs, dtype=torch.float32, device=dev).reshape(-1)
+            if x_in.numel() != n_in:
+                raise ValueError(f"step: expected {n_in} inputs, got {x_in.numel()}")
+            _lib.check(
+                lib.plx_scatter_f32(
+                    n_in,
+                    consts["input_ids"].data_ptr(),
+                    x_in.data_ptr(),
+                    units[ACTIVATION.name].data_ptr(),
+                    stream,
+                ),
+                "plx_scatter_f32",
+            )
+
+        fin_common = dict(
+            level=units["level"].data_ptr(),
+            is_input=consts["is_input"].data_ptr(),
+            pruned=units["pruned"].data_ptr() if "pruned" in units else None,
+        )
+        g = state.globals_
+
+        # Forward (phases.py:942-1015).
+        fp = plan.forward
+        swaps = self._shadow(units, fp.program.out_fields) if arena.pipeline else {}
+        acc = None
+        if arena.fwd_carry:
+            acc = torch.empty(n_units, dtype=torch.float32, device=dev)
+            _lib.call("plx_fill_f32", n_units, fp.identity, acc.data_ptr(), stream)
+        prog = program_struct(fp.program, units, g, out_override=swaps)
+        for b in range(arena.num_buckets):
+            rows = arena.fwd[b]
+            d = _lib.plx_forward_desc()
+            d.nrows = rows.nrows
+            d.monoid = fp.monoid
+            d.row_unit = rows.rows.data_ptr()
+            d.row_ptr = rows.ptr.data_ptr()
+            d.src = arena.cols["from_id"].data_ptr()
+            d.weight = arena.cols["weight"].data_ptr()
+            d.dead = arena.cols["dead"].data_ptr()
+            d.x = units[fp.field].data_ptr()
+            d.acc = acc.data_ptr() if acc is not None else None
+            d.fin.level = fin_common["level"]
+            d.fin.is_input = fin_common["is_input"]
+            d.fin.pruned = fin_common["pruned"]
+            d.fin.fin_level = -1 if arena.pipeline else b + 1
+            d.fin.skip_inputs = 1
+            d.apply = prog
+            self._launch("forward", lib.plx_forward_bucket, d, stream)
+        self._unshadow(units, swaps)
+
+        # Loss (phases.py:1107-1131).
+        loss = torch.zeros((), dtype=torch.float32, device=dev)
+        if plan.loss is not None:
+            self._loss(plan, units, inputs, consts, loss, stream, g)
+
+        # Backward (phases.py:1018-1104).
+        if plan.backward is not None:
+            self._backward(plan, arena, units, fin_common, stream, g)
+
+        # Connection update (phases.py:1196-1242), fused over every bucket.
+        if plan.update is not None:
+            self._update(plan, arena, units, consts, stream)
+            state._arena_ahead = True
+
+        state.step = state.step + 1
+        return StepResult(state=state, overflow=False, loss=loss, growth_remainder=None)
+
+    # -- phases -----------------------------------------------------------------
+    @staticmethod
+    def _shadow(units: dict[str, torch.Tensor], out_fields: list[str | None]) -> dict[str, torch.Tensor]:
+        """PIPELINE applies write every unit at once against the pre-phase
+        columns (sweep.py:205-228): write into copies, swapped in after."""
+        return {f: units[f].clone() for f in out_fields if f is not None}
+
+    @staticmethod
+    def _unshadow(units: dict[str, torch.Tensor], swaps: dict[str, torch.Tensor]) -> None:
+        for name, buf in swaps.items():
+            units[name] = buf
+
+    def _loss(self, plan: Plan, units: dict, inputs: StepInputs, consts: dict,
+              loss: torch.Tensor, stream: int, g: Any) -> None:
+        lib = _lib.load()
+        dev = loss.device
+        n_out = len(self.static.output_ids)
+        if inputs.targets is None:
+            raise ValueError("step: this net has a loss, so StepInputs.targets is required")
+        t = torch.as_tensor(inputs.targets, dtype=torch.float32, device=dev).reshape(-1)
+        if t.numel() != n_out:
+            raise ValueError(f"step: expected {n_out} targets, got {t.numel()}")
+        lp = plan.loss
+        seed = units[lp.seed_field]
+        if lp.kind == "softmax":
+            _lib.check(
+                lib.plx_loss_softmax_ce(
+                    n_out,
+                    consts["output_ids"].data_ptr(),
+                    units[ACTIVATION.name].data_ptr(),
+                    t.data_ptr(),
+                    seed.data_ptr(),
+                    loss.data_ptr(),
+                    stream,
+                ),
+                "plx_loss_softmax_ce",
+            )
+            return
+        scratch = torch.empty(n_out + n_out // 256 + 2, dtype=torch.float32, device=dev)
+        prog = program_struct(lp.program, units, g)
+        _lib.check(
+            lib.plx_loss_elementwise(
+                n_out,
+                consts["output_ids"].data_ptr(),
+                t.data_ptr(),
+                prog,
+                seed.data_ptr(),
+                scratch.data_ptr(),
+                loss.data_ptr(),
+                stream,
+            ),
+            "plx_loss_elementwise",
+        )
+
+    def _backward(self, plan: Plan, arena: Arena, units: dict, fin_common: dict,
+                  stream: int, g: Any) -> None:
+        lib = _lib.load()
+        bp = plan.backward
+        dev = arena.device
+        n_units = self.static.num_units
+        swaps = self._shadow(units, bp.program.out_fields) if arena.pipeline else {}
+        acc = None
+        if arena.bwd_carry:
+            acc = torch.empty(n_units, dtype=torch.float32, device=dev)
+            _lib.call("plx_fill_f32", n_units, bp.identity, acc.data_ptr(), stream)
+        prog = program_struct(bp.program, units, g, out_override=swaps)
+
+        def finalize(rows: Any, fin_level: int, skip_inputs: int) -> None:
+            d = _lib.plx_backward_finalize_desc()
+            d.nrows = rows.nrows
+            d.monoid = bp.monoid
+            d.row_unit = rows.rows.data_ptr()
+            d.row_item = rows.ptr.data_ptr() if rows.ptr is not None else None
+            d.item_sum = arena.item_sum.data_ptr()
+            d.acc = acc.data_ptr() if acc is not None else None
+            d.fin.level = fin_common["level"]
+            d.fin.is_input = fin_common["is_input"]
+            d.fin.pruned = fin_common["pruned"]
+            d.fin.fin_level = fin_level
+            d.fin.skip_inputs = skip_inputs
+            d.apply = prog
+            self._launch("backward_finalize", lib.plx_backward_finalize, d, stream)
+
+        def fold(b: int) -> None:
+            rows = arena.bwd[b]
+            d = _lib.plx_backward_fold_desc()
+            d.nitems = rows.nitems
+            d.monoid = bp.monoid
+            d.item_ptr = rows.item_ptr.data_ptr()
+            d.sperm = arena.sperm.data_ptr()
+            d.sdst = arena.sdst.data_ptr()
+            d.weight = arena.cols["weight"].data_ptr()
+            d.g = units[bp.field].data_ptr()
+            d.item_sum = arena.item_sum.data_ptr() + 4 * rows.item_base
+            self._launch("backward_fold", lib.plx_backward_fold, d, stream)
+
+        if arena.pipeline:
+            # One sweep; every unit, inputs included, is applied (sweep.py:442-447).
+            fold(0)
+            finalize(arena.bwd[0], -1, 0)
+        else:
+            nb = arena.num_buckets
+            finalize(arena.top, nb, 1)
+            for b in range(nb - 1, 0, -1):
+                fold(b)
+                finalize(arena.bwd[b], b, 1)
+        self._unshadow(units, swaps)
+
+    def _update(self, plan: Plan, arena: Arena, units: dict, consts: dict, stream: int) -> None:
+        lib = _lib.load()
+        up = plan.update
+        d = _lib.plx_update_desc()
+        d.n = arena.n_positions
+        d.rule = up.rule_code
+        d.src = arena.cols["from_id"].data_ptr()
+        d.dst = arena.cols["to_id"].data_ptr()
+        d.dead = arena.cols["dead"].data_ptr()
+        d.weight = arena.cols["weight"].data_ptr()
+        state_cols = up.state_columns()
+        for k, name in enumerate(state_cols):
+            setattr(d, f"s{k}", arena.cols[name].data_ptr())
+        d.gfield = units[up.grad_field.name].data_ptr()
+        d.act = units[ACTIVATION.name].data_ptr()
+        if "pow_table" in consts:
+            d.pow_table = consts["pow_table"].data_ptr()
+            d.pow_table_len = consts["pow_table"].numel() // 2
+        for k, v in enumerate(up.params()):
+            d.p[k] = float(v)
+        self._launch("update_conn", lib.plx_update_conn, d, stream)

@@ -1,0 +1,133 @@
+"""Synthetic workloads of the benchmark configurations.
+
+``c1_pipeline`` and ``c2_topological`` build the edge lists of the first two
+configurations with numpy's PCG64 (seed 0 by default), so the same arrays are
+reproducible on any host:
+
+- C1: 1,024 units; 16,384 edges with uniform src/dst and no self-loops;
+  PIPELINE tanh; 32 inputs, 8 outputs; weights N(0, 1/fan_in).
+- C2: 8 layers x 131,072 units (layer 0 = inputs, layer 7 = outputs);
+  2^26 edges between consecutive layers, fan-in 73 plus one more for every
+  7th destination; each destination's sources are drawn without replacement
+  by Zipf(s=1.1) popularity over a seeded permutation of the source layer;
+  weights N(0, 1/fan_in).
+
+``scale`` shrinks the layer width (and with it the edge count) for tests.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+
+@dataclasses.dataclass
+class EdgeList:
+    num_units: int
+    src: np.ndarray  # int32
+    dst: np.ndarray  # int32
+    weight: np.ndarray  # float32
+    input_ids: np.ndarray
+    output_ids: np.ndarray
+
+
+def c1_pipeline(seed: int = 0, num_units: int = 1024, num_edges: int = 16384,
+                n_in: int = 32, n_out: int = 8) -> EdgeList:
+    """C1's recurrent pipeline net."""
+    rng = np.random.default_rng(seed)
+    src = rng.integers(0, num_units, size=num_edges, dtype=np.int64)
+    dst = rng.integers(0, num_units - 1, size=num_edges, dtype=np.int64)
+    dst = dst + (dst >= src)  # uniform over the other units: no self-loops
+    fan_in = np.bincount(dst, minlength=num_units)
+    std = 1.0 / np.sqrt(np.maximum(fan_in[dst], 1))
+    weight = (rng.standard_normal(num_edges) * std).astype(np.float32)
+    return EdgeList(
+        num_units,
+        src.astype(np.int32),
+        dst.astype(np.int32),
+        weight,
+        np.arange(n_in, dtype=np.int32),
+        np.arange(num_units - n_out, num_units, dtype=np.int32),
+    )
+
+
+def zipf_sources(rng: np.random.Generator, width: int, counts: np.ndarray,
+                 s: float = 1.1, oversample: int = 160) -> tuple[np.ndarray, np.ndarray]:
+    """For destination row r, ``counts[r]`` distinct source ranks drawn
+    sequentially by Zipf(s) popularity (rank k has weight k^-s), mapped
+    through a random permutation of the layer. Returns (row, source) pairs."""
+    cdf = np.cumsum(np.arange(1, width + 1, dtype=np.float64) ** -s)
+    cdf /= cdf[-1]
+    perm = rng.permutation(width).astype(np.int32)
+    rows_out, src_out = [], []
+    n = counts.size
+    need = counts.astype(np.int64)
+    pending = np.arange(n)
+    chunk = 4096
+    while pending.size:
+        next_pending = []
+        for c0 in range(0, pending.size, chunk):
+            rows = pending[c0 : c0 + chunk]
+            k = int(max(oversample, 2 * need[rows].max()))
+            u = rng.random((rows.size, k))
+            draws = np.searchsorted(cdf, u, side="right").astype(np.int32)
+            np.minimum(draws, width - 1, out=draws)
+            order = np.argsort(draws, axis=1, kind="stable")
+            srt = np.take_along_axis(draws, order, axis=1)
+            dup_sorted = np.zeros_like(srt, dtype=bool)
+            dup_sorted[:, 1:] = srt[:, 1:] == srt[:, :-1]
+            dup = np.zeros_like(dup_sorted)
+            np.put_along_axis(dup, order, dup_sorted, axis=1)
+            keep = ~dup
+            rank = np.cumsum(keep, axis=1)
+            take = keep & (rank <= need[rows][:, None])
+            ok = take.sum(axis=1) == need[rows]
+            r_idx, c_idx = np.nonzero(take & ok[:, None])
+            rows_out.append(rows[r_idx])
+            src_out.append(perm[draws[r_idx, c_idx]])
+            next_pending.append(rows[~ok])
+        pending = np.concatenate(next_pending) if next_pending else np.zeros(0, np.int64)
+    return np.concatenate(rows_out), np.concatenate(src_out)
+
+
+def c2_topological(seed: int = 0, scale: int = 1, layers: int = 8) -> EdgeList:
+    """C2's 8-layer Zipf net (2^26 edges at scale 1)."""
+    rng = np.random.default_rng(seed)
+    width = 131072 // scale
+    num_units = layers * width
+    src_all, dst_all, w_all = [], [], []
+    for layer in range(layers - 1):
+        counts = np.full(width, 73, dtype=np.int64)
+        # every 7th of the (layers-1)*width destinations gets one more source
+        counts[((layer * width + np.arange(width)) % 7) == 0] += 1
+        rows, srcs = zipf_sources(rng, width, counts)
+        dst = (layer + 1) * width + rows.astype(np.int64)
+        src = layer * width + srcs.astype(np.int64)
+        std = 1.0 / np.sqrt(counts[rows].astype(np.float64))
+        w = (rng.standard_normal(rows.size) * std).astype(np.float32)
+        src_all.append(src.astype(np.int32))
+        dst_all.append(dst.astype(np.int32))
+        w_all.append(w)
+    return EdgeList(
+        num_units,
+        np.concatenate(src_all),
+        np.concatenate(dst_all),
+        np.concatenate(w_all),
+        np.arange(width, dtype=np.int32),
+        np.arange((layers - 1) * width, layers * width, dtype=np.int32),
+    )
+
+
+def c2_target(seed: int, width: int):
+    """The fixed linear target of C2: y_k = s_k * x_{pi(k)}."""
+    rng = np.random.default_rng(seed + 1)
+    sign = np.where(rng.random(width) < 0.5, -1.0, 1.0).astype(np.float32)
+    perm = rng.permutation(width)
+    return sign, perm
+
+
+def c1_target(seed: int, n_in: int = 32, n_out: int = 8) -> np.ndarray:
+    """C1's fixed random linear target matrix A (n_out x n_in), N(0, 1/n_in)."""
+    rng = np.random.default_rng(seed + 1)
+    return (rng.standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float32)

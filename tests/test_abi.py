@@ -1,0 +1,58 @@
+"""The C-ABI library loads and exports what include/plastax_hip.h declares
+(CPU only: no kernel is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from plastax_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "plastax_hip.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"PLX_EXPORT\s+[\w\s\*]+?\b(plx_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from plastax_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_entry_points() -> None:
+    assert declared_symbols() == set(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib) -> None:
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_descriptor_layouts_match_the_header(lib) -> None:
+    out = (ctypes.c_int64 * 6)()
+    assert lib.plx_struct_sizes(out, 6) == 6
+    assert list(out) == [ctypes.sizeof(s) for s in _lib.STRUCTS]
+    assert lib.plx_abi_version() == 1
+
+
+def test_argument_errors_are_reported_not_raised(lib) -> None:
+    """Validation runs before any HIP call, so it is testable without a GPU."""
+    rc = lib.plx_forward_bucket(None, None)
+    assert rc == 1
+    assert b"null descriptor" in lib.plx_last_error()
+    d = _lib.plx_update_desc()
+    d.n = 6
+    assert lib.plx_update_conn(d, None) == 1
+    assert b"multiple of 4" in lib.plx_last_error()
+    assert lib.plx_fill_f32(-1, 0.0, None, None) == 1
+    # zero-sized work is a no-op success
+    assert lib.plx_fill_f32(0, 0.0, None, None) == 0
