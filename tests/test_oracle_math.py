@@ -1,0 +1,153 @@
+"""Pins of the oracle's primitives that do not depend on the device.
+
+- Philox-4x32-10 against the Random123 known-answer vectors (Salmon et al.,
+  SC'11; the plastax mapping of rng.py:109-141 makes the all-zero and
+  all-ones blocks diagonal, so those two KATs apply to philox32 directly).
+- exp / log / tanh / sigmoid within 2 ulp of the double-precision functions
+  over the float32 range, and their special values.
+- The Adam power b^t (integer t) equal to the correctly rounded power, from
+  exact rational arithmetic.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import plastax_amd as px
+
+KATS = [
+    # (ctr[4], key[2]) -> out[4]   (Random123 kat_vectors, philox4x32_10)
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    (
+        (0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344),
+        (0xA4093822, 0x299F31D0),
+        (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1),
+    ),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", KATS)
+def test_philox_core_matches_random123_kats(oracle, ctr, key, want) -> None:
+    lib = oracle.load()
+    c = (ctypes.c_uint32 * 4)(*ctr)
+    k = (ctypes.c_uint32 * 2)(*key)
+    out = (ctypes.c_uint32 * 4)()
+    lib.ox_philox4x32_10(c, k, out)
+    assert tuple(out) == want
+
+
+def test_plastax_philox_mapping_on_diagonal_kats(oracle) -> None:
+    lib = oracle.load()
+    assert lib.ox_philox32(0, 0) == 0x6627E8D5
+    assert lib.ox_philox32(2**64 - 1, 2**64 - 1) == 0x408F276D
+    assert int(px.rng.philox32(0, 0)) == 0x6627E8D5
+    assert int(px.rng.philox32(np.uint64(2**64 - 1), np.uint64(2**64 - 1))) == 0x408F276D
+
+
+def test_host_rng_matches_oracle_words(oracle) -> None:
+    lib = oracle.load()
+    rng = np.random.default_rng(0)
+    seeds = rng.integers(0, 2**63, 500, dtype=np.int64).astype(np.uint64)
+    ctrs = rng.integers(0, 2**63, 500, dtype=np.int64).astype(np.uint64)
+    words = px.rng.philox32(seeds, ctrs)
+    assert [int(w) for w in words] == [lib.ox_philox32(int(s), int(c)) for s, c in zip(seeds, ctrs)]
+    # site contract (rng.py:10-56): draw = philox(site_seed, (j<<16)|sub)
+    site = px.rng.site_seed(7, np.uint32(3), 1, np.uint64(42))
+    assert int(site) == lib.ox_site_seed(7, 3, 1, 42)
+    assert int(px.rng.draw(site, np.uint64(5), 2)) == lib.ox_site_draw(int(site), 5, 2)
+    w = px.rng.philox32(seeds[:50], ctrs[:50])
+    for n in (1, 2, 3, 10, 1000):
+        got = px.rng.uniform_int(w, n)
+        assert [int(v) for v in got] == [lib.ox_uniform_int(int(x), n) for x in w]
+        assert int(got.max()) < n
+
+
+def _ulps(got: float, exact: float) -> float:
+    if math.isnan(exact):
+        return 0.0 if math.isnan(got) else math.inf
+    if math.isinf(exact):
+        return 0.0 if got == exact else math.inf
+    spacing = float(np.spacing(np.float32(abs(exact))))
+    return abs(got - exact) / spacing
+
+
+@pytest.mark.parametrize(
+    "name,ref,lo,hi",
+    [
+        ("ox_expf", math.exp, -87.0, 88.5),
+        ("ox_tanhf", math.tanh, -12.0, 12.0),
+        ("ox_sigmoidf", lambda x: 1.0 / (1.0 + math.exp(-x)), -30.0, 30.0),
+    ],
+)
+def test_elementary_functions_within_two_ulp(oracle, name, ref, lo, hi) -> None:
+    fn = getattr(oracle.load(), name)
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([rng.uniform(lo, hi, 20000), rng.uniform(-1, 1, 20000)]).astype(np.float32)
+    worst = max(_ulps(fn(float(x)), ref(float(x))) for x in xs)
+    assert worst <= 2.0, worst
+
+
+def test_log_within_two_ulp(oracle) -> None:
+    fn = oracle.load().ox_logf
+    rng = np.random.default_rng(2)
+    xs = np.concatenate(
+        [np.exp(rng.uniform(-87, 88, 20000)), rng.uniform(0.5, 2.0, 20000), [1e-40, 3e-45]]
+    ).astype(np.float32)
+    worst = max(_ulps(fn(float(x)), math.log(float(x))) for x in xs)
+    assert worst <= 2.0, worst
+
+
+def test_special_values(oracle) -> None:
+    lib = oracle.load()
+    assert lib.ox_expf(0.0) == 1.0
+    assert lib.ox_expf(-200.0) == 0.0
+    assert lib.ox_expf(100.0) == math.inf
+    assert lib.ox_expf(-math.inf) == 0.0
+    assert math.isnan(lib.ox_expf(math.nan))
+    assert lib.ox_logf(1.0) == 0.0
+    assert lib.ox_logf(0.0) == -math.inf
+    assert math.isnan(lib.ox_logf(-1.0))
+    assert lib.ox_logf(math.inf) == math.inf
+    assert lib.ox_tanhf(0.0) == 0.0 and math.copysign(1, lib.ox_tanhf(-0.0)) < 0
+    assert lib.ox_tanhf(50.0) == 1.0 and lib.ox_tanhf(-50.0) == -1.0
+    assert lib.ox_tanhf(math.inf) == 1.0
+    assert lib.ox_sigmoidf(0.0) == 0.5
+
+
+def test_adam_power_is_the_correctly_rounded_power(oracle) -> None:
+    lib = oracle.load()
+    for b in (np.float32(0.9), np.float32(0.999)):
+        fb = Fraction(float(b))
+        for t in list(range(0, 300)) + [1000, 4096, 65535, 100000]:
+            exact = fb**t
+            want = np.float32(float(exact))  # float() rounds the rational correctly
+            got = np.float32(lib.ox_pow_step(float(b), float(t)))
+            assert got == want, (float(b), t)
+
+
+def test_capacity_policy_matches_reference_rules() -> None:
+    """topo.py:455-506: next power of two (min 64), or a multiple of align."""
+    cp = px.topo.capacity_policy
+    assert cp(0) == 64 and cp(1) == 64 and cp(64) == 64 and cp(65) == 128
+    assert cp(1000) == 1024 and cp(1024) == 1024 and cp(1025) == 2048
+    assert cp(100, headroom=1.0) == 256
+    assert cp(1000, align=256) == 1024 and cp(1, align=256) == 256 and cp(513, align=256) == 768
+    with pytest.raises(ValueError):
+        cp(10, headroom=-1.0)
+
+
+def test_initial_levels_longest_path() -> None:
+    edges = np.asarray([[0, 2], [1, 2], [2, 3], [0, 3], [3, 4], [1, 4]])
+    lv = px.topo.initial_levels(5, edges)
+    assert lv.tolist() == [0, 0, 1, 2, 3]
+    with pytest.raises(ValueError):
+        px.topo.initial_levels(3, np.asarray([[0, 1], [1, 2], [2, 0]]))
+    # inputs stay at level 0 even with an edge into them
+    lv = px.topo.initial_levels(3, np.asarray([[1, 0], [0, 2]]), input_ids=(0,))
+    assert lv[0] == 0 and lv[2] == 1
