@@ -98,38 +98,85 @@ typedef struct plx_forward_desc {
 
 PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
 
-/* Backward fold over the source-sorted mirror of one bucket
- * (sweep.py:343-399 with target FROM_ID; phases.py:1049-1104): item k folds
- * weight[sperm[j]] * g[sdst[j]] for j in [item_ptr[k], item_ptr[k+1]) in
- * order, skipping sdst < 0 (dead), into item_sum[k]. */
-typedef struct plx_backward_fold_desc {
-  int32_t nitems;
+/* Backward pass over one bucket, fused with the connection update
+ * (phases.py:1049-1104 accumulating into FROM_ID; phases.py:1196-1242).
+ * The bucket's physical positions [base, end) are split into tiles of
+ * tile_size positions, one workgroup each. With `fold`, every live edge's
+ * backward term weight * g[dst] (pre-update weight) is folded per (tile,
+ * source) group, in physical order, into a tile partial: hot sources write
+ * their slot of the tile's dense row hot_partial[tile * nhot + h], the others
+ * their slot of the source-major cold_partial array (group target -1-h or the
+ * cold slot). With `update`, the same pass applies the update rule (see
+ * plx_update_desc for p[] and the state columns) with grad = gfield[dst] *
+ * act[src] and stores the new weight and state; dead edges keep theirs.
+ * Tile metadata: grp_off[tile..tile+1] ranges the tile's groups; grp_se packs
+ * a group's start (low 16 bits) and length (high 16 bits) in the tile's
+ * source-sorted list sorted_local[tile * tile_size + j] of local edge indices. */
+typedef struct plx_tile_desc {
+  int64_t base;
+  int64_t end;
+  int32_t tile_size;
+  int32_t ntiles;
   int32_t monoid;
-  const int32_t* item_ptr; /* [nitems+1] mirror positions                 */
-  const int32_t* sperm;    /* [mirror] physical position of the edge       */
-  const int32_t* sdst;     /* [mirror] destination unit, -1 when dead      */
-  const float* weight;     /* [positions] WEIGHT (pre-update)              */
-  const float* g;          /* [num_units] the map's linear_input field     */
-  float* item_sum;         /* [nitems] out                                 */
-} plx_backward_fold_desc;
+  int32_t fold;
+  int32_t update;
+  int32_t nhot;
+  int32_t rule;
+  int32_t pow_table_len;
+  const int32_t* grp_off;
+  const uint32_t* grp_se;
+  const int32_t* grp_tgt;
+  const uint16_t* sorted_local;
+  float* hot_partial;
+  float* cold_partial;
+  const int32_t* src;
+  const int32_t* dst;
+  const uint8_t* dead;
+  float* weight;
+  float* s0;
+  float* s1;
+  float* s2;
+  const float* g;       /* the backward map's linear_input field         */
+  const float* gfield;  /* the update rule's grad field                  */
+  const float* act;     /* ACTIVATION                                    */
+  const float* pow_table;
+  float p[8];
+} plx_tile_desc;
 
-PLX_EXPORT int plx_backward_fold(const plx_backward_fold_desc* d, void* stream);
+PLX_EXPORT int plx_backward_tiles(const plx_tile_desc* d, void* stream);
 
-/* Backward finalize of one level: row r folds item_sum over
- * [row_item[r], row_item[r+1]) in order, combines into acc (null: fresh
- * identity) and, where finalized, applies `apply` and resets acc. */
-typedef struct plx_backward_finalize_desc {
+/* Backward finalize of one level from the tile partials. The tiles are
+ * grouped in superblocks of `superblock` consecutive tiles. A source's sum is
+ * the fold, in superblock order, of its superblock sums, each the fold in
+ * tile order of its tile partials (an absent tile holds the identity). Row r
+ * (unit row_unit[r]) is hot (row_hot[r] >= 0: its column of the dense
+ * hot_partial[tile * nhot + h], first reduced per superblock into hot_sb
+ * scratch of ceil(ntiles / superblock) * nhot floats) or cold (its run
+ * cold_partial[row_cold[r] .. row_cold[r+1]) in tile order, with each
+ * partial's superblock in cold_sb). The sum is combined into acc (null: a
+ * fresh identity) and, where finalized, `apply` runs and acc resets
+ * (sweep.py:183-230). Null row_hot / row_cold: rows fold nothing (the deepest
+ * level, primed from the identity: phases.py:1089-1094). */
+typedef struct plx_partials_desc {
   int32_t nrows;
   int32_t monoid;
-  const int32_t* row_unit; /* [nrows]                                      */
-  const int32_t* row_item; /* [nrows+1] item ranges (null: no items)       */
-  const float* item_sum;   /* [nitems]                                     */
-  float* acc;              /* [num_units] or null                          */
+  int32_t ntiles;
+  int32_t nhot;
+  int32_t superblock;
+  int32_t reserved;
+  const int32_t* row_unit;
+  const int32_t* row_hot;
+  const int32_t* row_cold;
+  const float* hot_partial;
+  float* hot_sb;
+  const float* cold_partial;
+  const uint16_t* cold_sb;
+  float* acc;
   plx_finalize fin;
   plx_program apply;
-} plx_backward_finalize_desc;
+} plx_partials_desc;
 
-PLX_EXPORT int plx_backward_finalize(const plx_backward_finalize_desc* d, void* stream);
+PLX_EXPORT int plx_backward_partials(const plx_partials_desc* d, void* stream);
 
 /* Connection update over physical positions [0, n): build_update_conn_phase
  * (phases.py:1196-1242, sweep.py:488-532) for the optim bundles. grad =
@@ -168,8 +215,8 @@ PLX_EXPORT int plx_scatter_f32(int32_t n, const int32_t* ids, const float* value
  * term are elementwise in (prediction, target), e.g. MSE): `term` writes out
  * slot 0 (the seed) to seed_field[output_ids[k]]; slot 1 is the loss term.
  * *loss_out = the fold of the terms in 256-output pieces (each piece folded
- * in order, then the piece sums in order). partials: n_out + ceil(n_out/256)
- * floats of scratch. */
+ * in order, then the piece sums in order). partials: ceil(n_out/256) floats
+ * of scratch. */
 PLX_EXPORT int plx_loss_elementwise(int32_t n_out, const int32_t* output_ids,
                          const float* targets, const plx_program* term,
                          float* seed_field, float* partials, float* loss_out,
@@ -196,8 +243,7 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
                   float* out, void* stream);
 
 /* sizeof of the descriptor structs, in the order plx_program, plx_finalize,
- * plx_forward_desc, plx_backward_fold_desc, plx_backward_finalize_desc,
- * plx_update_desc (for binding layers to check their mirrors). Writes
+ * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc (for binding layers to check their mirrors). Writes
  * min(n, 6) values and returns 6. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
 

@@ -32,7 +32,9 @@ import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libplastax_oracle.so"
-PIECE = 256
+PIECE = 256  # loss folds: pieces of 256 outputs
+TILE = 8192  # backward folds: the device's destination-sorted tile size
+SUPERBLOCK = 32  # backward folds: tiles per superblock
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -80,6 +82,10 @@ def load() -> ctypes.CDLL:
         lib.ox_bucket_reduce_bwd.argtypes = [
             ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32,
             ctypes.c_int32, ctypes.c_int32, _f32p, _f32p, _i32p,
+        ]
+        lib.ox_bucket_reduce_bwd_tiled.argtypes = [
+            ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _i32p, _i32p, _f32p, _f32p,
+            _i32p, ctypes.c_int32, ctypes.c_int32, _f32p,
         ]
         lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
         lib.ox_apply.argtypes = [
@@ -162,6 +168,8 @@ class OracleNet:
         globals_: Any = None,
         *,
         piece: int = PIECE,
+        tile: int | None = TILE,
+        superblock: int = SUPERBLOCK,
     ) -> None:
         self.static = static
         self.units = {k: np.ascontiguousarray(v) for k, v in units.items()}
@@ -169,6 +177,9 @@ class OracleNet:
         self.plan = plan
         self.globals_ = globals_
         self.piece = piece
+        self.tile = tile
+        self.superblock = superblock
+        self._bwd_order: dict[int, tuple[np.ndarray, np.ndarray]] = {}
         self.step_count = 0
         n = static.num_units
         self.is_input = np.zeros(n, dtype=bool)
@@ -205,16 +216,42 @@ class OracleNet:
         )
         return out
 
+    def _tiles(self, b: int) -> tuple[np.ndarray, np.ndarray]:
+        """(order, tile) of bucket b's live slots: order sorts them by
+        (src, dst, slot); tile is each slot's rank in (dst, slot) order
+        divided by the tile size. Cached (the structure is static)."""
+        if b not in self._bwd_order:
+            c = self.conns[b]
+            live = np.flatnonzero(~c["dead"].astype(bool))
+            dst = c["to_id"][live]
+            src = c["from_id"][live]
+            rank = np.empty(live.size, dtype=np.int64)
+            rank[np.lexsort((live, dst))] = np.arange(live.size)
+            tile = np.zeros(c["dead"].size, dtype=np.int32)
+            tile[live] = (rank // self.tile) if self.tile else 0
+            order = np.ascontiguousarray(live[np.lexsort((live, dst, src))].astype(np.int64))
+            self._bwd_order[b] = (order, tile)
+        return self._bwd_order[b]
+
     def _reduce_bwd(self, b: int, field: str, monoid: int) -> np.ndarray:
         c = self.conns[b]
         n = self.static.num_units
         out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
-        pc = np.zeros(n, dtype=np.float32)
-        pn = np.zeros(n, dtype=np.int32)
-        self.lib.ox_bucket_reduce_bwd(
-            c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
-            fptr(c["weight"]), fptr(self.units[field]), n, monoid, self.piece,
-            fptr(out), fptr(pc), iptr(pn),
+        if self.tile is None:
+            # the reference's literal slot-order fold
+            pc = np.zeros(n, dtype=np.float32)
+            pn = np.zeros(n, dtype=np.int32)
+            self.lib.ox_bucket_reduce_bwd(
+                c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
+                fptr(c["weight"]), fptr(self.units[field]), n, monoid, 1 << 30,
+                fptr(out), fptr(pc), iptr(pn),
+            )
+            return out
+        order, tile = self._tiles(b)
+        self.lib.ox_bucket_reduce_bwd_tiled(
+            order.size, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+            iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
+            fptr(self.units[field]), iptr(tile), self.superblock, monoid, fptr(out),
         )
         return out
 

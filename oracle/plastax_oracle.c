@@ -13,11 +13,12 @@
  * Summation order. The reference's per-bucket reduction is XLA's scatter
  * (jax.ops.segment_sum, monoid.py:84-122), which on the CPU folds updates in
  * slot order into a zero-filled output. The forward fold here is exactly
- * that. The backward fold follows the same slot order but splits a source's
- * terms into consecutive pieces of at most `piece` terms: each piece is
- * folded from +0.0 and the piece sums are folded in order (the deterministic
- * tree the device uses for hub sources); with piece >= out-degree it is the
- * plain slot-order fold.
+ * that. The backward fold (ox_bucket_reduce_bwd_tiled) follows each source's
+ * terms in destination-sorted order, grouped by the device's fixed tiles of
+ * that order: each tile's terms are folded from the identity and the tile sums
+ * are folded in order (the deterministic tree of the device's transpose
+ * reduce). ox_bucket_reduce_bwd keeps the plain slot-order fold (optionally in
+ * pieces) for comparisons against the reference's literal order.
  *
  * Build: see Makefile (gcc -O2 -ffp-contract=off: no contraction, so every
  * product and sum rounds to float32 exactly as the reference's jnp ops do).
@@ -313,6 +314,46 @@ OX_API void ox_bucket_reduce_bwd(int64_t cap, const int32_t* from,
   }
   for (int32_t s = 0; s < num_units; ++s)
     if (pn[s]) out[s] = ox_combine1(monoid, out[s], pc[s]);
+}
+
+/* Backward accumulate of one bucket in the device's tiled order. `order`
+ * lists the bucket's n live slots sorted by (src, dst, slot) -- for each
+ * source, its terms in the physical (destination-sorted) order -- and
+ * tile[e] is the tile of slot e: its rank in (dst, slot) order divided by the
+ * tile size. Per source, the terms of each tile are folded from the identity
+ * in order; the tile sums of each superblock (`superblock` consecutive tiles)
+ * are folded in tile order; the superblock sums are folded in order into
+ * out[s] (pre-filled with the identity). With one tile this is the plain fold
+ * of each source's terms in (dst, slot) order, which is the slot order of a
+ * source-major bucket (builder.py:566-579). */
+OX_API void ox_bucket_reduce_bwd_tiled(int64_t n, const int64_t* order,
+                                       const int32_t* from, const int32_t* to,
+                                       const float* weight, const float* g,
+                                       const int32_t* tile, int32_t superblock,
+                                       int32_t monoid, float* out) {
+  float id = ox_identity(monoid);
+  int64_t k = 0;
+  while (k < n) {
+    int32_t s = from[order[k]];
+    float total = out[s];
+    while (k < n && from[order[k]] == s) {
+      /* superblock: `superblock` consecutive tiles, folded first */
+      int32_t sb = tile[order[k]] / superblock;
+      float sbsum = id;
+      while (k < n && from[order[k]] == s && tile[order[k]] / superblock == sb) {
+        int32_t t = tile[order[k]];
+        float part = id;
+        while (k < n && from[order[k]] == s && tile[order[k]] == t) {
+          int64_t e = order[k];
+          part = ox_combine1(monoid, part, weight[e] * g[to[e]]);
+          ++k;
+        }
+        sbsum = ox_combine1(monoid, sbsum, part);
+      }
+      total = ox_combine1(monoid, total, sbsum);
+    }
+    out[s] = total;
+  }
 }
 
 /* combine_pairwise (monoid.py:124-152): acc = acc op b, elementwise. */

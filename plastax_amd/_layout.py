@@ -8,18 +8,24 @@ edges are laid out once more, per bucket, in one slab:
   (destination, logical slot) -- each destination's in-edges are one
   contiguous run, in slot order, which is the order the reference's
   ``segment_sum`` folds them (sweep.py:113-180);
-- positions ``[base_b + live_b, base_b + cap_b)``: the bucket's dead slots in
-  slot order;
+- positions ``[base_b + live_b, end_b)``: the bucket's dead slots in slot
+  order, then padding to a multiple of 4 positions (bucket bases are
+  multiples of 4, so every tile and vector load is 16-byte aligned);
 - ``slot``: the logical slot of every position, so the reference's logical
-  view (and slot-ordered free lists) can be recovered exactly.
+  view (and slot-ordered free lists) is recovered exactly.
 
 Forward rows are the destination units of a bucket plus the units the
 bucket finalizes (phases.py:1011); each row is a CSR range of positions.
-The backward reads a source-sorted mirror of each bucket: for every live
-edge in (source, slot) order its physical position (``sperm``) and its
-destination (``sdst``). A source with more than ``PIECE`` out-edges is split
-into pieces of at most ``PIECE`` consecutive terms (the items a lane folds);
-the piece sums are folded in order by the finalize kernel.
+
+The backward is a transpose reduce (sum into FROM_ID, sweep.py:343-399). The
+bucket's positions are cut into tiles of ``tile`` positions; within a tile,
+the live edges of each source form one group (listed in a per-tile
+source-sorted index, ``sorted_local``), folded on the device in physical
+order into one partial per (tile, source). Sources present in more than
+``HOT_FRAC`` of the tiles (the Zipf head) get a dense per-tile row of
+partials (``nhot`` wide); the others get source-major runs of cold partials.
+A source's sum is therefore the fold of its tile partials in tile order, each
+tile partial the fold of its terms in (dst, slot) order.
 
 Units are not permuted: unit columns are the state's own tensors.
 """
@@ -34,20 +40,43 @@ import torch
 from plastax_amd._types import DEAD, FROM_ID, TO_ID, Propagation
 from plastax_amd.state import Columns, NetworkStatic, column_to_numpy, torch_dtype
 
-PIECE = 256  # terms per backward item
+TILE = 8192  # positions per backward tile (multiple of 4, <= 32768)
+SUPERBLOCK = 32  # tiles per superblock of the cross-tile fold
+HOT_FRAC = 0.125  # a source present in more than this fraction of tiles is hot
+MAX_HOT = 8192  # dense hot partials per tile (LDS: 4 B each)
 PAD = 256  # slack positions after each slab (vector loads may run past the end)
 
 
 @dataclasses.dataclass
-class BucketRows:
-    """Device CSR of one bucket's forward or backward rows."""
+class ForwardRows:
+    """Device CSR of one bucket's forward rows."""
 
     nrows: int
     rows: torch.Tensor  # int32 [nrows] unit ids
-    ptr: torch.Tensor | None  # int32 [nrows+1] (forward: positions; backward: items)
-    nitems: int = 0
-    item_ptr: torch.Tensor | None = None  # int32 [nitems+1] mirror positions
-    item_base: int = 0  # offset of this bucket's items in the item_sum scratch
+    ptr: torch.Tensor  # int32 [nrows+1] physical positions
+
+
+@dataclasses.dataclass
+class BackwardTiles:
+    """Device metadata of one bucket's tiled transpose reduce."""
+
+    base: int
+    end: int
+    ntiles: int
+    fold: bool
+    nhot: int = 0
+    grp_off: torch.Tensor | None = None  # int32 [ntiles+1]
+    grp_se: torch.Tensor | None = None  # int32 (uint32 bits) [groups]
+    grp_tgt: torch.Tensor | None = None  # int32 [groups]
+    sorted_local: torch.Tensor | None = None  # int16 (uint16 bits) [ntiles*tile]
+    hot_partial: torch.Tensor | None = None  # f32 [ntiles*nhot]
+    hot_sb: torch.Tensor | None = None  # f32 [nsuperblocks*nhot]
+    cold_partial: torch.Tensor | None = None  # f32 [ncold]
+    cold_sb: torch.Tensor | None = None  # int16 (uint16 bits) [ncold] superblock ids
+    nrows: int = 0
+    rows: torch.Tensor | None = None  # int32 [nrows] units finalized here
+    row_hot: torch.Tensor | None = None  # int32 [nrows]
+    row_cold: torch.Tensor | None = None  # int32 [nrows+1]
 
 
 def _round_up(n: int, k: int) -> int:
@@ -55,7 +84,7 @@ def _round_up(n: int, k: int) -> int:
 
 
 class Arena:
-    """Physical slab + forward CSR + backward mirror, on the device."""
+    """Physical slab, forward CSR and backward tiles, on the device."""
 
     def __init__(
         self,
@@ -63,9 +92,14 @@ class Arena:
         units: Columns,
         conns: tuple[Columns, ...],
         device: torch.device,
+        *,
+        tile: int = TILE,
     ) -> None:
+        if tile <= 0 or tile % 4 or tile > 32768:
+            raise ValueError("tile must be a positive multiple of 4, at most 32768")
         self.static = static
         self.device = device
+        self.tile = tile
         n = static.num_units
         nb = len(conns)
         self.num_buckets = nb
@@ -77,26 +111,25 @@ class Arena:
         pruned = units.get("pruned")
         live_unit = np.ones(n, dtype=bool) if pruned is None else pruned.cpu().numpy() == 0
         specs = {s.name: s for s in static.conn_fields}
-        host = {
-            name: [column_to_numpy(b[name], specs[name]) for b in conns] for name in specs
-        }
+        host = {name: [column_to_numpy(b[name], specs[name]) for b in conns] for name in specs}
         caps = [int(h.shape[0]) for h in host[DEAD.name]]
-        bases = np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
+        spans = [_round_up(c, 4) for c in caps]
+        bases = np.concatenate([[0], np.cumsum(spans)]).astype(np.int64)
         total = int(bases[-1])
-        self.total = total
-        self.n_positions = _round_up(total, 4)  # the update kernel's range
-        size = self.n_positions + PAD
+        self.n_positions = total
+        size = total + PAD
         if size >= 2**31:
             raise ValueError("the edge arena exceeds 2^31 positions")
         self.caps = caps
         self.bases = [int(b) for b in bases[:-1]]
+        self.ends = [int(b) for b in bases[1:]]
 
         phys_slot = np.full(size, -1, dtype=np.int32)
         phys = {name: np.full(size, specs[name].default, dtype=specs[name].dtype) for name in specs}
         phys[DEAD.name][:] = True
         self.lives: list[int] = []
-        fwd_rows_h: list[tuple[np.ndarray, np.ndarray]] = []
-        mirrors: list[tuple[np.ndarray, np.ndarray, np.ndarray]] = []
+        self.fwd: list[ForwardRows] = []
+        self.bwd: list[BackwardTiles] = []
         self.fwd_carry = False
         self.bwd_carry = False
         for b in range(nb):
@@ -114,8 +147,6 @@ class Arena:
                 phys[name][base : base + cap] = host[name][b][slots]
             live = int(order.size)
             self.lives.append(live)
-            pos_of_slot = np.empty(cap, dtype=np.int64)
-            pos_of_slot[slots] = base + np.arange(cap)
 
             # Forward rows: destinations of this bucket and the units it
             # finalizes (phases.py:1011; sweep.py:328-338 for PIPELINE).
@@ -130,73 +161,20 @@ class Arena:
             rows = np.union1d(np.unique(dsts), fin).astype(np.int64)
             lo = np.searchsorted(dsts, rows, side="left")
             ptr = np.concatenate([lo, [live]]).astype(np.int64) + base
-            fwd_rows_h.append((rows.astype(np.int32), ptr.astype(np.int32)))
+            self.fwd.append(ForwardRows(int(rows.size), self._i32(rows), self._i32(ptr)))
 
-            # Backward mirror (sweep.py:343-399): live edges in (src, slot) order.
-            # A TOPOLOGICAL walk never reduces bucket 0 (phases.py:1071-1074).
-            mirrored = live_idx if (self.pipeline or b > 0) else live_idx[:0]
-            by_src = mirrored[np.argsort(src[mirrored], kind="stable")]
-            srcs = src[by_src].astype(np.int64)
-            sperm = pos_of_slot[by_src].astype(np.int32)
-            sdst = dst[by_src].astype(np.int32)
-            if self.pipeline:
-                brows = np.arange(n, dtype=np.int64)
-            else:
-                brows = np.union1d(np.flatnonzero(levels == b), np.unique(srcs)).astype(np.int64)
-                if live and not bool((levels[srcs] == b).all()):
-                    self.bwd_carry = True
-            mirrors.append((brows, srcs, np.stack([sperm, sdst])))
+            # Backward tiles. A TOPOLOGICAL walk never reduces bucket 0
+            # (phases.py:1071-1074): it is only updated.
+            fold = self.pipeline or b > 0
+            srcs = src[order].astype(np.int64)
+            if not self.pipeline and fold and live and not bool((levels[srcs] == b).all()):
+                self.bwd_carry = True
+            self.bwd.append(self._tiles(b, srcs, fold, levels, n))
 
-        # Assemble the mirror slab and the backward items.
-        mtotal = sum(int(m[1].size) for m in mirrors)
-        msize = _round_up(mtotal, 4) + PAD
-        sperm_all = np.zeros(msize, dtype=np.int32)
-        sdst_all = np.full(msize, -1, dtype=np.int32)
-        mbase = 0
-        item_base = 0
-        self.bwd: list[BucketRows] = []
-        self.fwd: list[BucketRows] = []
-        for b in range(nb):
-            brows, srcs, sp_sd = mirrors[b]
-            m = int(srcs.size)
-            sperm_all[mbase : mbase + m] = sp_sd[0]
-            sdst_all[mbase : mbase + m] = sp_sd[1]
-            lo = np.searchsorted(srcs, brows, side="left")
-            hi = np.searchsorted(srcs, brows, side="right")
-            counts = hi - lo
-            npieces = -(-counts // PIECE)
-            row_item = np.concatenate([[0], np.cumsum(npieces)]).astype(np.int64)
-            nitems = int(row_item[-1])
-            # item k of row r starts at lo[r] + j * PIECE
-            item_start = np.empty(nitems + 1, dtype=np.int64)
-            if nitems:
-                owner = np.repeat(np.arange(brows.size), npieces)
-                j = np.arange(nitems) - row_item[owner]
-                item_start[:nitems] = lo[owner] + j * PIECE
-            item_start[nitems] = m
-            item_start += mbase
-            self.bwd.append(
-                BucketRows(
-                    nrows=int(brows.size),
-                    rows=self._i32(brows),
-                    ptr=self._i32(row_item + item_base),
-                    nitems=nitems,
-                    item_ptr=self._i32(item_start),
-                    item_base=item_base,
-                )
-            )
-            item_base += nitems
-            mbase += m
-            rows, ptr = fwd_rows_h[b]
-            self.fwd.append(BucketRows(nrows=int(rows.size), rows=self._i32(rows), ptr=self._i32(ptr)))
-        self.total_items = item_base
         # Rows finalized from the identity before the backward bucket walk:
         # the deepest level (phases.py:1089-1094).
-        if self.pipeline:
-            top = np.zeros(0, dtype=np.int64)
-        else:
-            top = np.flatnonzero(levels == nb)
-        self.top = BucketRows(nrows=int(top.size), rows=self._i32(top), ptr=None)
+        top = np.zeros(0, dtype=np.int64) if self.pipeline else np.flatnonzero(levels == nb)
+        self.top = BackwardTiles(0, 0, 0, False, nrows=int(top.size), rows=self._i32(top))
 
         self.slot = torch.from_numpy(phys_slot).to(device)
         self.cols: Columns = {}
@@ -208,12 +186,103 @@ class Arena:
                 arr = arr.view(np.int32)
             self.cols[name] = torch.from_numpy(np.ascontiguousarray(arr)).to(device)
             assert self.cols[name].dtype == torch_dtype(spec.dtype)
-        self.sperm = torch.from_numpy(sperm_all).to(device)
-        self.sdst = torch.from_numpy(sdst_all).to(device)
-        self.item_sum = torch.zeros(max(self.total_items, 1), dtype=torch.float32, device=device)
 
     def _i32(self, a: np.ndarray) -> torch.Tensor:
-        return torch.from_numpy(np.ascontiguousarray(a.astype(np.int32))).to(self.device)
+        return torch.from_numpy(np.ascontiguousarray(np.asarray(a).astype(np.int32))).to(self.device)
+
+    def _tiles(self, b: int, srcs: np.ndarray, fold: bool, levels: np.ndarray, n: int) -> BackwardTiles:
+        """Tile metadata of bucket b; ``srcs`` are the live edges' sources in
+        physical order."""
+        T = self.tile
+        base, end = self.bases[b], self.ends[b]
+        ntiles = -(-(end - base) // T)
+        if not fold:
+            return BackwardTiles(base, end, ntiles, False)
+        live = int(srcs.size)
+        rank = np.arange(live, dtype=np.int64)
+        tile_of = rank // T
+        # The tile's live edges sorted by (source, physical position).
+        o2 = np.lexsort((rank, srcs, tile_of))
+        t_sorted = tile_of[o2]
+        s_sorted = srcs[o2]
+        tile_first = np.searchsorted(t_sorted, np.arange(ntiles + 1), side="left")
+        sorted_local = np.zeros(ntiles * T + 4, dtype=np.uint16)
+        j_in_tile = np.arange(live, dtype=np.int64) - tile_first[t_sorted]
+        sorted_local[t_sorted * T + j_in_tile] = (rank[o2] - t_sorted * T).astype(np.uint16)
+        # Groups: runs of one source inside one tile.
+        if live:
+            brk = np.flatnonzero((np.diff(t_sorted) != 0) | (np.diff(s_sorted) != 0)) + 1
+            g_start = np.concatenate([[0], brk])
+        else:
+            g_start = np.zeros(0, dtype=np.int64)
+        g_end = np.concatenate([g_start[1:], [live]]).astype(np.int64)
+        g_tile = t_sorted[g_start] if live else g_start
+        g_src = s_sorted[g_start] if live else g_start
+        g_len = g_end - g_start
+        g_st = g_start - tile_first[g_tile] if live else g_start
+        # Hot sources: present in more than HOT_FRAC of the tiles.
+        presence = np.bincount(g_src, minlength=n) if live else np.zeros(n, np.int64)
+        cand = np.flatnonzero(presence > HOT_FRAC * ntiles)
+        if cand.size > MAX_HOT:
+            keep = np.argsort(-presence[cand], kind="stable")[:MAX_HOT]
+            cand = np.sort(cand[keep])
+        hot_src = cand
+        hot_idx = np.full(n, -1, dtype=np.int64)
+        hot_idx[hot_src] = np.arange(hot_src.size)
+        nhot = int(hot_src.size)
+        is_hot = hot_idx[g_src] >= 0 if live else np.zeros(0, bool)
+        # Cold groups: source-major, tile order within a source.
+        cold = np.flatnonzero(~is_hot)
+        cold_order = cold[np.lexsort((g_tile[cold], g_src[cold]))]
+        tgt = np.empty(g_start.size, dtype=np.int64)
+        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
+        tgt[cold_order] = np.arange(cold_order.size)
+        cold_count = np.bincount(g_src[cold], minlength=n) if cold.size else np.zeros(n, np.int64)
+        # Within a tile, longest groups first (lanes take them round robin).
+        g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
+        grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
+        se = (g_st[g_perm].astype(np.uint64) | (g_len[g_perm].astype(np.uint64) << np.uint64(16)))
+        # Rows finalized at this bucket: hot sources first (by hot slot, so a
+        # wave reads consecutive columns), then every other unit of the level.
+        if self.pipeline:
+            level_units = np.arange(n, dtype=np.int64)
+        else:
+            level_units = np.union1d(np.flatnonzero(levels == b), np.unique(srcs)).astype(np.int64)
+        others = level_units[hot_idx[level_units] < 0]
+        rows = np.concatenate([hot_src, others])
+        row_hot = np.concatenate([np.arange(nhot), np.full(others.size, -1)])
+        # Cold slots were numbered in (source, tile) order and `others` is in
+        # source order (hot sources have no cold groups), so each cold row's
+        # run is contiguous and the runs follow the row order.
+        counts = np.concatenate([np.zeros(nhot, np.int64), cold_count[others]])
+        row_cold = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+        assert int(row_cold[-1]) == cold_order.size
+        tgt_final = tgt
+        ncold = int(cold_order.size)
+        cold_sb = (g_tile[cold_order] // SUPERBLOCK).astype(np.uint16)
+        nsb = -(-ntiles // SUPERBLOCK)
+        dev = self.device
+        return BackwardTiles(
+            base,
+            end,
+            ntiles,
+            True,
+            nhot=nhot,
+            grp_off=self._i32(grp_off),
+            grp_se=torch.from_numpy(se.astype(np.uint32).view(np.int32)).to(dev),
+            grp_tgt=self._i32(tgt_final[g_perm] if live else tgt),
+            sorted_local=torch.from_numpy(sorted_local.view(np.int16)).to(dev),
+            hot_partial=torch.zeros(max(ntiles * nhot, 1), dtype=torch.float32, device=dev),
+            hot_sb=torch.zeros(max(nsb * nhot, 1), dtype=torch.float32, device=dev),
+            cold_partial=torch.zeros(max(ncold, 1), dtype=torch.float32, device=dev),
+            cold_sb=torch.from_numpy(
+                np.concatenate([cold_sb, np.zeros(1, np.uint16)]).view(np.int16)
+            ).to(dev),
+            nrows=int(rows.size),
+            rows=self._i32(rows),
+            row_hot=self._i32(row_hot),
+            row_cold=self._i32(row_cold),
+        )
 
     def write_logical(self, conns: tuple[Columns, ...]) -> None:
         """Scatter the physical columns back into the logical buckets."""

@@ -9,10 +9,14 @@ fails loudly.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 from typing import Any
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
+LIB_PATH = pathlib.Path(
+    os.environ.get("PLASTAX_HIP_LIB")
+    or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
+)
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -68,26 +72,54 @@ class plx_forward_desc(ctypes.Structure):
     ]
 
 
-class plx_backward_fold_desc(ctypes.Structure):
+class plx_tile_desc(ctypes.Structure):
     _fields_ = [
-        ("nitems", c_i32),
+        ("base", c_i64),
+        ("end", c_i64),
+        ("tile_size", c_i32),
+        ("ntiles", c_i32),
         ("monoid", c_i32),
-        ("item_ptr", c_vp),
-        ("sperm", c_vp),
-        ("sdst", c_vp),
+        ("fold", c_i32),
+        ("update", c_i32),
+        ("nhot", c_i32),
+        ("rule", c_i32),
+        ("pow_table_len", c_i32),
+        ("grp_off", c_vp),
+        ("grp_se", c_vp),
+        ("grp_tgt", c_vp),
+        ("sorted_local", c_vp),
+        ("hot_partial", c_vp),
+        ("cold_partial", c_vp),
+        ("src", c_vp),
+        ("dst", c_vp),
+        ("dead", c_vp),
         ("weight", c_vp),
+        ("s0", c_vp),
+        ("s1", c_vp),
+        ("s2", c_vp),
         ("g", c_vp),
-        ("item_sum", c_vp),
+        ("gfield", c_vp),
+        ("act", c_vp),
+        ("pow_table", c_vp),
+        ("p", c_f32 * 8),
     ]
 
 
-class plx_backward_finalize_desc(ctypes.Structure):
+class plx_partials_desc(ctypes.Structure):
     _fields_ = [
         ("nrows", c_i32),
         ("monoid", c_i32),
+        ("ntiles", c_i32),
+        ("nhot", c_i32),
+        ("superblock", c_i32),
+        ("reserved", c_i32),
         ("row_unit", c_vp),
-        ("row_item", c_vp),
-        ("item_sum", c_vp),
+        ("row_hot", c_vp),
+        ("row_cold", c_vp),
+        ("hot_partial", c_vp),
+        ("hot_sb", c_vp),
+        ("cold_partial", c_vp),
+        ("cold_sb", c_vp),
         ("acc", c_vp),
         ("fin", plx_finalize),
         ("apply", plx_program),
@@ -115,8 +147,8 @@ class plx_update_desc(ctypes.Structure):
 
 _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_bucket": (c_i32, [ctypes.POINTER(plx_forward_desc), c_vp]),
-    "plx_backward_fold": (c_i32, [ctypes.POINTER(plx_backward_fold_desc), c_vp]),
-    "plx_backward_finalize": (c_i32, [ctypes.POINTER(plx_backward_finalize_desc), c_vp]),
+    "plx_backward_tiles": (c_i32, [ctypes.POINTER(plx_tile_desc), c_vp]),
+    "plx_backward_partials": (c_i32, [ctypes.POINTER(plx_partials_desc), c_vp]),
     "plx_update_conn": (c_i32, [ctypes.POINTER(plx_update_desc), c_vp]),
     "plx_scatter_f32": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_loss_elementwise": (
@@ -139,8 +171,8 @@ STRUCTS = (
     plx_program,
     plx_finalize,
     plx_forward_desc,
-    plx_backward_fold_desc,
-    plx_backward_finalize_desc,
+    plx_tile_desc,
+    plx_partials_desc,
     plx_update_desc,
 )
 

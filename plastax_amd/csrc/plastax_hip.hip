@@ -3,10 +3,11 @@
 //
 // Data layout (built by plastax_amd/_layout.py): every bucket's edge columns
 // live in one physical slab, destination-sorted inside each bucket (live edges
-// ordered by (dst, logical slot), then the bucket's dead slots). A source-sorted
-// mirror (physical position + destination per edge, ordered by (src, slot))
-// serves the backward transpose reduce. All folds are deterministic: no float
-// atomics anywhere, so a step is bitwise repeatable.
+// ordered by (dst, logical slot), then the bucket's dead slots). The backward
+// transpose reduce works on fixed tiles of that order: per-(tile, source)
+// partials, folded per superblock of tiles, then across superblocks. All folds
+// are deterministic: no float atomics anywhere, so a step is bitwise
+// repeatable.
 //
 // The path is a memory-bound gather / segment reduce (about 2 flops per edge
 // per pass), so nothing here uses MFMA; the kernels stream the edge columns
@@ -156,7 +157,11 @@ __device__ __forceinline__ bool finalizes(const plx_finalize& f, int u) {
 // any row length.
 // ---------------------------------------------------------------------------
 constexpr int kFwdBlock = 256;
-constexpr int kWin = 4096;
+#ifndef PLX_FWD_QUADS
+#define PLX_FWD_QUADS 8
+#endif
+constexpr int kWinQuads = PLX_FWD_QUADS;  // 16-byte quads per thread per window
+constexpr int kWin = 4 * kWinQuads * kFwdBlock;
 
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
@@ -173,17 +178,31 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   float s = ident;
   for (int w0 = e_begin & ~3; w0 < e_end; w0 += kWin) {
     const int wn = min(kWin, e_end - w0);
-    for (int q = threadIdx.x; 4 * q < wn; q += kFwdBlock) {
-      const int e = w0 + 4 * q;
-      const int4 sv = *reinterpret_cast<const int4*>(d.src + e);
-      const float4 wv = *reinterpret_cast<const float4*>(d.weight + e);
-      const uint32_t dv = *reinterpret_cast<const uint32_t*>(d.dead + e);
-      float4 o;
-      o.x = (dv & 0x000000FFu) ? ident : wv.x * d.x[sv.x];
-      o.y = (dv & 0x0000FF00u) ? ident : wv.y * d.x[sv.y];
-      o.z = (dv & 0x00FF0000u) ? ident : wv.z * d.x[sv.z];
-      o.w = (dv & 0xFF000000u) ? ident : wv.w * d.x[sv.w];
-      *reinterpret_cast<float4*>(buf + 4 * q) = o;
+    // Issue every load of the window before using any of them.
+    int4 sv[kWinQuads];
+    float4 wv[kWinQuads];
+    uint32_t dv[kWinQuads];
+#pragma unroll
+    for (int i = 0; i < kWinQuads; ++i) {
+      const int q = threadIdx.x + i * kFwdBlock;
+      if (4 * q < wn) {
+        const int e = w0 + 4 * q;
+        sv[i] = *reinterpret_cast<const int4*>(d.src + e);
+        wv[i] = *reinterpret_cast<const float4*>(d.weight + e);
+        dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kWinQuads; ++i) {
+      const int q = threadIdx.x + i * kFwdBlock;
+      if (4 * q < wn) {
+        float4 o;
+        o.x = (dv[i] & 0x000000FFu) ? ident : wv[i].x * d.x[sv[i].x];
+        o.y = (dv[i] & 0x0000FF00u) ? ident : wv[i].y * d.x[sv[i].y];
+        o.z = (dv[i] & 0x00FF0000u) ? ident : wv[i].z * d.x[sv[i].z];
+        o.w = (dv[i] & 0xFF000000u) ? ident : wv[i].w * d.x[sv[i].w];
+        *reinterpret_cast<float4*>(buf + 4 * q) = o;
+      }
     }
     __syncthreads();
     const int lo = max(my_b, w0), hi = min(my_e, w0 + wn);
@@ -202,79 +221,21 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward fold: one item (a piece of at most 256 consecutive terms of one
-// source) per lane, same LDS windowing over the source-sorted mirror. Terms
-// gather the pre-update weight at the mirror's physical position.
-// ---------------------------------------------------------------------------
-template <int M>
-__global__ __launch_bounds__(kFwdBlock) void k_backward_fold(plx_backward_fold_desc d) {
-  __shared__ float buf[kWin];
-  const int it0 = blockIdx.x * kFwdBlock;
-  const int it = it0 + threadIdx.x;
-  const int iend = min(it0 + kFwdBlock, d.nitems);
-  const int e_begin = d.item_ptr[it0];
-  const int e_end = d.item_ptr[iend];
-  const bool has = it < d.nitems;
-  const int my_b = has ? d.item_ptr[it] : 0;
-  const int my_e = has ? d.item_ptr[it + 1] : 0;
-  const float ident = Mono<M>::id();
-  float s = ident;
-  for (int w0 = e_begin & ~3; w0 < e_end; w0 += kWin) {
-    const int wn = min(kWin, e_end - w0);
-    for (int q = threadIdx.x; 4 * q < wn; q += kFwdBlock) {
-      const int e = w0 + 4 * q;
-      const int4 pv = *reinterpret_cast<const int4*>(d.sperm + e);
-      const int4 dv = *reinterpret_cast<const int4*>(d.sdst + e);
-      float4 o;
-      o.x = dv.x < 0 ? ident : d.weight[pv.x] * d.g[dv.x];
-      o.y = dv.y < 0 ? ident : d.weight[pv.y] * d.g[dv.y];
-      o.z = dv.z < 0 ? ident : d.weight[pv.z] * d.g[dv.z];
-      o.w = dv.w < 0 ? ident : d.weight[pv.w] * d.g[dv.w];
-      *reinterpret_cast<float4*>(buf + 4 * q) = o;
-    }
-    __syncthreads();
-    const int lo = max(my_b, w0), hi = min(my_e, w0 + wn);
-    for (int e = lo; e < hi; ++e) s = Mono<M>::op(s, buf[e - w0]);
-    __syncthreads();
-  }
-  if (has) d.item_sum[it] = s;
-}
-
-template <int M>
-__global__ __launch_bounds__(kFwdBlock) void k_backward_finalize(plx_backward_finalize_desc d) {
-  const int r = blockIdx.x * kFwdBlock + threadIdx.x;
-  if (r >= d.nrows) return;
-  const int u = d.row_unit[r];
-  const float ident = Mono<M>::id();
-  float s = ident;
-  if (d.row_item) {
-    const int k1 = d.row_item[r + 1];
-    for (int k = d.row_item[r]; k < k1; ++k) s = Mono<M>::op(s, d.item_sum[k]);
-  }
-  const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
-  if (finalizes(d.fin, u)) {
-    run_program(d.apply, u, a, 0.0f, true);
-    if (d.acc) d.acc[u] = ident;
-  } else if (d.acc) {
-    d.acc[u] = a;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Connection update: four physical positions per lane, 16-byte loads and
 // stores of every column; dead positions store their old values back.
 // ---------------------------------------------------------------------------
 constexpr int kUpdBlock = 256;
 
-__device__ __forceinline__ float adam_pow(const plx_update_desc& d, float b, float t, int which) {
+template <class D>
+__device__ __forceinline__ float adam_pow(const D& d, float b, float t, int which) {
   if (d.pow_table && t >= 0.0f && t < static_cast<float>(d.pow_table_len) && floorf(t) == t)
     return d.pow_table[2 * static_cast<int>(t) + which];
   return px::pow_step(b, t);
 }
 
-template <int RULE>
-__device__ __forceinline__ void update_one(const plx_update_desc& d, float grad, float& w,
-                                           float& s0, float& s1, float& s2) {
+template <int RULE, class D>
+__device__ __forceinline__ void update_one(const D& d, float grad, float& w, float& s0, float& s1,
+                                           float& s2) {
   if (RULE == PLX_RULE_SGD) {
     w = w - d.p[0] * grad;
   } else if (RULE == PLX_RULE_MOMENTUM) {
@@ -330,6 +291,173 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
 }
 
 // ---------------------------------------------------------------------------
+// Backward + update, one destination-sorted tile per workgroup.
+//
+// The workgroup streams its tile's edge columns once (16-byte loads): for
+// each live edge it forms the backward term c = weight * g[dst] with the
+// pre-update weight into LDS and, when fused, applies the update rule and
+// stores the new weight and optimizer state. Then the tile's (source) groups
+// are folded from LDS in physical order -- the group lists are precomputed
+// per tile -- and each group sum lands either in the tile's dense row of hot
+// partials (sources present in many tiles) or in its slot of the source-major
+// cold partial array. No float atomics: every partial has exactly one writer.
+// ---------------------------------------------------------------------------
+constexpr int kTileBlock = 512;
+#ifndef PLX_TILE_QUADS
+#define PLX_TILE_QUADS 2
+#endif
+constexpr int kTileQuads = PLX_TILE_QUADS;  // 16-byte quads per thread per streaming pass
+
+template <int RULE, int M, bool FOLD>
+__global__ __launch_bounds__(kTileBlock) void k_tile(plx_tile_desc d) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int T = d.tile_size;
+  float* buf = reinterpret_cast<float*>(smem);  // [T]
+  float* hot = buf + T;                          // [nhot], padded to 16 bytes
+  uint16_t* sl = reinterpret_cast<uint16_t*>(hot + ((d.nhot + 3) & ~3));  // [T]
+  const int blk = blockIdx.x;
+  const int64_t t0 = d.base + static_cast<int64_t>(blk) * T;
+  const int64_t t1 = min(t0 + T, d.end);
+  const int n = static_cast<int>(t1 - t0);
+  const float ident = Mono<M>::id();
+  if (FOLD) {
+    for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hot[j] = ident;
+    const uint16_t* slg = d.sorted_local + static_cast<int64_t>(blk) * T;
+    for (int j = threadIdx.x; 4 * j < n; j += kTileBlock)
+      *reinterpret_cast<uint2*>(sl + 4 * j) = *reinterpret_cast<const uint2*>(slg + 4 * j);
+  }
+  constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? 3 : 1);
+  constexpr int U = kTileQuads;
+  // Each pass covers U quads per thread; every load of a pass is issued
+  // before any of it is used.
+  for (int q0 = threadIdx.x; 4 * q0 < n; q0 += U * kTileBlock) {
+    int4 sv[U], tv[U];
+    uint32_t dv[U];
+    float4 w[U], s0[U], s1[U], s2[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = q0 + i * kTileBlock;
+      if (4 * q < n) {
+        const int64_t e = t0 + 4 * q;
+        tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
+        dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+        w[i] = *reinterpret_cast<const float4*>(d.weight + e);
+        if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
+        if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
+        if (nstate >= 3) {
+          s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
+          s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = q0 + i * kTileBlock;
+      if (4 * q >= n) continue;
+      const int64_t e = t0 + 4 * q;
+      const bool l0 = !(dv[i] & 0x000000FFu), l1 = !(dv[i] & 0x0000FF00u);
+      const bool l2 = !(dv[i] & 0x00FF0000u), l3 = !(dv[i] & 0xFF000000u);
+      if (FOLD) {
+        float4 c;
+        c.x = l0 ? w[i].x * d.g[tv[i].x] : ident;
+        c.y = l1 ? w[i].y * d.g[tv[i].y] : ident;
+        c.z = l2 ? w[i].z * d.g[tv[i].z] : ident;
+        c.w = l3 ? w[i].w * d.g[tv[i].w] : ident;
+        *reinterpret_cast<float4*>(buf + 4 * q) = c;
+      }
+      if (RULE >= 0) {
+        float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
+        if (l0) update_one<RULE>(d, d.gfield[tv[i].x] * d.act[sv[i].x], a.x, m.x, v.x, t.x);
+        if (l1) update_one<RULE>(d, d.gfield[tv[i].y] * d.act[sv[i].y], a.y, m.y, v.y, t.y);
+        if (l2) update_one<RULE>(d, d.gfield[tv[i].z] * d.act[sv[i].z], a.z, m.z, v.z, t.z);
+        if (l3) update_one<RULE>(d, d.gfield[tv[i].w] * d.act[sv[i].w], a.w, m.w, v.w, t.w);
+        *reinterpret_cast<float4*>(d.weight + e) = a;
+        if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
+        if (nstate >= 3) {
+          *reinterpret_cast<float4*>(d.s1 + e) = v;
+          *reinterpret_cast<float4*>(d.s2 + e) = t;
+        }
+      }
+    }
+  }
+  if (!FOLD) return;
+  __syncthreads();
+  const int g1 = d.grp_off[blk + 1];
+  for (int gi = d.grp_off[blk] + threadIdx.x; gi < g1; gi += kTileBlock) {
+    const uint32_t se = d.grp_se[gi];
+    const int st = static_cast<int>(se & 0xFFFFu);
+    const int len = static_cast<int>(se >> 16);
+    float v = ident;
+    for (int j = st; j < st + len; ++j) v = Mono<M>::op(v, buf[sl[j]]);
+    const int tgt = d.grp_tgt[gi];
+    if (tgt >= 0)
+      d.cold_partial[tgt] = v;
+    else
+      hot[-1 - tgt] = v;
+  }
+  __syncthreads();
+  float* hp = d.hot_partial + static_cast<int64_t>(blk) * d.nhot;
+  for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hp[j] = hot[j];
+}
+
+// Hot superblock sums: thread (h, superblock) folds the hot partials of the
+// superblock's tiles in tile order. Consecutive threads read consecutive
+// columns, so every load is coalesced.
+template <int M>
+__global__ __launch_bounds__(kFwdBlock) void k_hot_sb(plx_partials_desc d) {
+  const int h = blockIdx.x * kFwdBlock + threadIdx.x;
+  if (h >= d.nhot) return;
+  const int sb = blockIdx.y;
+  const int k0 = sb * d.superblock;
+  const int k1 = min(k0 + d.superblock, d.ntiles);
+  const float* hp = d.hot_partial + h;
+  float s = Mono<M>::id();
+  for (int k = k0; k < k1; ++k) s = Mono<M>::op(s, hp[static_cast<int64_t>(k) * d.nhot]);
+  d.hot_sb[static_cast<int64_t>(sb) * d.nhot + h] = s;
+}
+
+// Backward finalize from tile partials: one row (source unit) per lane. A hot
+// row folds its superblock sums in order; a cold row folds its run of cold
+// partials (tile order), closing a superblock sum whenever the superblock id
+// changes. Then combine into acc and apply.
+template <int M>
+__global__ __launch_bounds__(kFwdBlock) void k_partials(plx_partials_desc d) {
+  const int r = blockIdx.x * kFwdBlock + threadIdx.x;
+  if (r >= d.nrows) return;
+  const int u = d.row_unit[r];
+  const float ident = Mono<M>::id();
+  float s = ident;
+  const int h = d.row_hot ? d.row_hot[r] : -1;
+  if (h >= 0) {
+    const int nsb = (d.ntiles + d.superblock - 1) / d.superblock;
+    for (int j = 0; j < nsb; ++j) s = Mono<M>::op(s, d.hot_sb[static_cast<int64_t>(j) * d.nhot + h]);
+  } else if (d.row_cold) {
+    const int j0 = d.row_cold[r], j1 = d.row_cold[r + 1];
+    if (j0 < j1) {
+      int cur = d.cold_sb[j0];
+      float q = ident;
+      for (int j = j0; j < j1; ++j) {
+        const int sb = d.cold_sb[j];
+        if (sb != cur) {
+          s = Mono<M>::op(s, q);
+          q = ident;
+          cur = sb;
+        }
+        q = Mono<M>::op(q, d.cold_partial[j]);
+      }
+      s = Mono<M>::op(s, q);
+    }
+  }
+  const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
+  if (finalizes(d.fin, u)) {
+    run_program(d.apply, u, a, 0.0f, true);
+    if (d.acc) d.acc[u] = ident;
+  } else if (d.acc) {
+    d.acc[u] = a;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small kernels: scatter, fill, losses, Philox, math probes.
 // ---------------------------------------------------------------------------
 __global__ void k_scatter(int32_t n, const int32_t* ids, const float* values, float* dst) {
@@ -344,32 +472,37 @@ __global__ void k_fill(int64_t n, float value, float* dst) {
 
 constexpr int kPiece = 256;
 
-__global__ void k_loss_terms(int32_t n_out, const int32_t* ids, const float* targets,
-                             plx_program P, float* terms) {
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= n_out) return;
-  // out slot 0 (the seed) lands at the output's unit id; slot 1 is the term.
-  terms[k] = run_program(P, ids[k], 0.0f, targets[k], true);
+// One 256-output piece per workgroup: each thread runs the loss program for
+// one output (out slot 0, the seed, lands at the output's unit id; slot 1 is
+// the loss term), then one lane folds the piece's terms in order from +0.0.
+__global__ __launch_bounds__(kPiece) void k_loss_pieces(int32_t n_out, const int32_t* ids,
+                                                       const float* targets, plx_program P,
+                                                       float* piece_sums) {
+  __shared__ float terms[kPiece];
+  const int k = blockIdx.x * kPiece + threadIdx.x;
+  if (k < n_out) terms[threadIdx.x] = run_program(P, ids[k], 0.0f, targets[k], true);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int len = min(kPiece, n_out - static_cast<int>(blockIdx.x) * kPiece);
+    float s = 0.0f;
+    for (int j = 0; j < len; ++j) s = s + terms[j];
+    piece_sums[blockIdx.x] = s;
+  }
 }
 
-// Piecewise fold of n terms: each 256-term piece folded in order from +0.0,
-// then the piece sums folded in order. One workgroup.
-__global__ __launch_bounds__(1024) void k_fold_pieces(int32_t n, const float* terms,
-                                                      float* partials, float* out) {
-  const int npieces = (n + kPiece - 1) / kPiece;
-  for (int p = threadIdx.x; p < npieces; p += blockDim.x) {
-    float s = 0.0f;
-    const int end = min(n, (p + 1) * kPiece);
-    for (int k = p * kPiece; k < end; ++k) s = s + terms[k];
-    partials[p] = s;
+// Folds n piece sums in order from +0.0 into *out, staging them through LDS.
+__global__ __launch_bounds__(1024) void k_fold_sums(int32_t n, const float* sums, float* out) {
+  __shared__ float buf[1024];
+  float s = 0.0f;
+  for (int base = 0; base < n; base += 1024) {
+    const int len = min(1024, n - base);
+    if (static_cast<int>(threadIdx.x) < len) buf[threadIdx.x] = sums[base + threadIdx.x];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int j = 0; j < len; ++j) s = s + buf[j];
+    __syncthreads();
   }
-  __syncthreads();
-  __threadfence_block();
-  if (threadIdx.x == 0) {
-    float s = 0.0f;
-    for (int p = 0; p < npieces; ++p) s = s + partials[p];
-    *out = 0.0f + s;
-  }
+  if (threadIdx.x == 0) *out = 0.0f + s;
 }
 
 constexpr int kSoftmaxMaxPieces = 1024;
@@ -479,6 +612,29 @@ bool program_ok(const plx_program& p) {
   return p.ninstr >= 0 && p.ninstr <= PLX_MAX_INSTR && p.nout >= 0 && p.nout <= PLX_MAX_OUTS;
 }
 
+template <int RULE, int M, bool FOLD>
+void launch_tile(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+  // LDS beyond 64 KiB needs an explicit per-kernel opt-in.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  (void)attr;
+  k_tile<RULE, M, FOLD><<<d.ntiles, kTileBlock, lds, s>>>(d);
+}
+
+template <int M, bool FOLD>
+int dispatch_rule(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+  switch (d.update ? d.rule : -1) {
+    case -1: launch_tile<-1, M, FOLD>(d, lds, s); break;
+    case PLX_RULE_SGD: launch_tile<PLX_RULE_SGD, M, FOLD>(d, lds, s); break;
+    case PLX_RULE_MOMENTUM: launch_tile<PLX_RULE_MOMENTUM, M, FOLD>(d, lds, s); break;
+    case PLX_RULE_ADAM: launch_tile<PLX_RULE_ADAM, M, FOLD>(d, lds, s); break;
+    case PLX_RULE_RMSPROP: launch_tile<PLX_RULE_RMSPROP, M, FOLD>(d, lds, s); break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: unknown rule");
+  }
+  return PLX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -490,8 +646,8 @@ int32_t plx_abi_version(void) { return 1; }
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[6] = {
       sizeof(plx_program),          sizeof(plx_finalize),
-      sizeof(plx_forward_desc),     sizeof(plx_backward_fold_desc),
-      sizeof(plx_backward_finalize_desc), sizeof(plx_update_desc)};
+      sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
+      sizeof(plx_partials_desc),    sizeof(plx_update_desc)};
   for (int32_t k = 0; k < n && k < 6; ++k) out[k] = sizes[k];
   return 6;
 }
@@ -519,45 +675,86 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
   return check_launch("plx_forward_bucket");
 }
 
-int plx_backward_fold(const plx_backward_fold_desc* d, void* stream) {
-  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_fold: null descriptor");
-  if (d->nitems < 0) return fail(PLX_ERR_INVALID, "plx_backward_fold: negative nitems");
-  if (d->nitems == 0) return PLX_OK;
-  if (!d->item_ptr || !d->sperm || !d->sdst || !d->weight || !d->g || !d->item_sum)
-    return fail(PLX_ERR_INVALID, "plx_backward_fold: null column");
+int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_tiles: null descriptor");
+  if (d->ntiles < 0 || d->tile_size <= 0 || d->tile_size % 4 || d->tile_size > 32768)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile_size must be a positive multiple of 4 <= 32768");
+  if (d->base % 4 || d->end % 4 || d->end < d->base)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: base/end must be multiples of 4");
+  if ((d->end - d->base + d->tile_size - 1) / d->tile_size != d->ntiles)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: ntiles does not cover [base, end)");
+  if (d->ntiles == 0) return PLX_OK;
+  if (!d->src || !d->dst || !d->dead || !d->weight)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
+  if (d->fold && (!d->grp_off || !d->grp_se || !d->grp_tgt || !d->sorted_local || !d->g ||
+                  (d->nhot > 0 && !d->hot_partial)))
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: fold metadata missing");
+  if (d->update && (!d->gfield || !d->act))
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: update fields missing");
+  if (d->update && (d->rule == PLX_RULE_MOMENTUM || d->rule == PLX_RULE_RMSPROP) && !d->s0)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: state column missing");
+  if (d->update && d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || !d->s2))
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: Adam state columns missing");
+  if (!d->fold && !d->update) return PLX_OK;
+  if (d->fold && d->nhot < 0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: negative nhot");
+  const size_t lds = d->fold ? static_cast<size_t>(d->tile_size) * 6 +
+                                   static_cast<size_t>((d->nhot + 3) & ~3) * 4
+                             : 0;
+  if (lds > 160 * 1024) return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: tile does not fit in LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned grid = grid_for(d->nitems, kFwdBlock);
-  switch (d->monoid) {
-    case PLX_MONOID_SUM: k_backward_fold<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_PROD: k_backward_fold<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MAX: k_backward_fold<PLX_MONOID_MAX><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MIN: k_backward_fold<PLX_MONOID_MIN><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_fold: unknown monoid");
+  int rc = PLX_OK;
+  if (!d->fold) {
+    rc = dispatch_rule<PLX_MONOID_SUM, false>(*d, 0, s);
+  } else {
+    switch (d->monoid) {
+      case PLX_MONOID_SUM: rc = dispatch_rule<PLX_MONOID_SUM, true>(*d, lds, s); break;
+      case PLX_MONOID_PROD: rc = dispatch_rule<PLX_MONOID_PROD, true>(*d, lds, s); break;
+      case PLX_MONOID_MAX: rc = dispatch_rule<PLX_MONOID_MAX, true>(*d, lds, s); break;
+      case PLX_MONOID_MIN: rc = dispatch_rule<PLX_MONOID_MIN, true>(*d, lds, s); break;
+      default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: unknown monoid");
+    }
   }
-  return check_launch("plx_backward_fold");
+  if (rc) return rc;
+  return check_launch("plx_backward_tiles");
 }
 
-int plx_backward_finalize(const plx_backward_finalize_desc* d, void* stream) {
-  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_finalize: null descriptor");
-  if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_finalize: negative nrows");
+int plx_backward_partials(const plx_partials_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_partials: null descriptor");
+  if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_partials: negative nrows");
   if (d->nrows == 0) return PLX_OK;
-  if (!d->row_unit || (d->row_item && !d->item_sum))
-    return fail(PLX_ERR_INVALID, "plx_backward_finalize: null column");
-  if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_finalize: bad program");
+  if (!d->row_unit) return fail(PLX_ERR_INVALID, "plx_backward_partials: null row_unit");
+  if (d->row_hot && (d->nhot < 0 || d->superblock <= 0 || d->ntiles < 0 ||
+                     (d->nhot > 0 && (!d->hot_partial || !d->hot_sb))))
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: hot partials missing");
+  if (d->row_cold && (!d->cold_partial || !d->cold_sb))
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: cold partials missing");
+  if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_partials: bad program");
   if (d->fin.fin_level >= 0 && !d->fin.level)
-    return fail(PLX_ERR_INVALID, "plx_backward_finalize: level needed");
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: level needed");
   if (d->fin.skip_inputs && !d->fin.is_input)
-    return fail(PLX_ERR_INVALID, "plx_backward_finalize: is_input needed");
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: is_input needed");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->row_hot && d->nhot > 0 && d->ntiles > 0) {
+    const dim3 g(grid_for(d->nhot, kFwdBlock), (d->ntiles + d->superblock - 1) / d->superblock);
+    switch (d->monoid) {
+      case PLX_MONOID_SUM: k_hot_sb<PLX_MONOID_SUM><<<g, kFwdBlock, 0, s>>>(*d); break;
+      case PLX_MONOID_PROD: k_hot_sb<PLX_MONOID_PROD><<<g, kFwdBlock, 0, s>>>(*d); break;
+      case PLX_MONOID_MAX: k_hot_sb<PLX_MONOID_MAX><<<g, kFwdBlock, 0, s>>>(*d); break;
+      case PLX_MONOID_MIN: k_hot_sb<PLX_MONOID_MIN><<<g, kFwdBlock, 0, s>>>(*d); break;
+      default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
+    }
+    const int rc = check_launch("plx_backward_partials");
+    if (rc) return rc;
+  }
   const unsigned grid = grid_for(d->nrows, kFwdBlock);
   switch (d->monoid) {
-    case PLX_MONOID_SUM: k_backward_finalize<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_PROD: k_backward_finalize<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MAX: k_backward_finalize<PLX_MONOID_MAX><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MIN: k_backward_finalize<PLX_MONOID_MIN><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_finalize: unknown monoid");
+    case PLX_MONOID_SUM: k_partials<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_PROD: k_partials<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MAX: k_partials<PLX_MONOID_MAX><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MIN: k_partials<PLX_MONOID_MIN><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
   }
-  return check_launch("plx_backward_finalize");
+  return check_launch("plx_backward_partials");
 }
 
 int plx_update_conn(const plx_update_desc* d, void* stream) {
@@ -614,14 +811,13 @@ int plx_loss_elementwise(int32_t n_out, const int32_t* output_ids, const float* 
   p.outs[0] = seed_field;  // slot 0: the seed, stored at the output unit
   p.outs[1] = nullptr;     // slot 1: the term, returned to the kernel
   if (p.nout < 2) p.nout = 2;
-  float* terms = partials;
-  float* piece = partials + n_out;
-  if (n_out > 0) {
-    k_loss_terms<<<grid_for(n_out, 256), 256, 0, s>>>(n_out, output_ids, targets, p, terms);
+  const int npieces = (n_out + kPiece - 1) / kPiece;
+  if (npieces > 0) {
+    k_loss_pieces<<<npieces, kPiece, 0, s>>>(n_out, output_ids, targets, p, partials);
     int rc = check_launch("plx_loss_elementwise");
     if (rc) return rc;
   }
-  k_fold_pieces<<<1, 1024, 0, s>>>(n_out, terms, piece, loss_out);
+  k_fold_sums<<<1, 1024, 0, s>>>(npieces, partials, loss_out);
   return check_launch("plx_loss_elementwise");
 }
 

@@ -20,7 +20,7 @@ import torch
 
 from plastax_amd import _lib
 from plastax_amd._expr import UnsupportedPolicyError
-from plastax_amd._layout import Arena
+from plastax_amd._layout import SUPERBLOCK, TILE, Arena
 from plastax_amd._plan import Plan, compile_plan, program_struct
 from plastax_amd._types import ACTIVATION, Propagation
 from plastax_amd.state import NetworkState, NetworkStatic
@@ -98,6 +98,8 @@ class StepFn:
         # kernel launch on the launching stream (the benchmark records HIP
         # events there).
         self.timer: Any = None
+        # Positions per backward tile of the arenas this step builds.
+        self.tile: int = TILE
 
     def _launch(self, kind: str, fn: Any, *args: Any) -> None:
         timer = self.timer
@@ -128,7 +130,9 @@ class StepFn:
     def arena(self, state: NetworkState) -> Arena:
         """The state's physical arena (built on first use)."""
         if state._arena is None:
-            state._arena = Arena(self.static, state.units, state._conns, state.device)
+            state._arena = Arena(
+                self.static, state.units, state._conns, state.device, tile=self.tile
+            )
             state._arena_ahead = False
         return state._arena
 
@@ -200,17 +204,19 @@ class StepFn:
         self._unshadow(units, swaps)
 
         # Loss (phases.py:1107-1131).
-        loss = torch.zeros((), dtype=torch.float32, device=dev)
         if plan.loss is not None:
+            loss = torch.empty((), dtype=torch.float32, device=dev)
             self._loss(plan, units, inputs, consts, loss, stream, g)
+        else:
+            loss = torch.zeros((), dtype=torch.float32, device=dev)
 
-        # Backward (phases.py:1018-1104).
-        if plan.backward is not None:
-            self._backward(plan, arena, units, fin_common, stream, g)
-
-        # Connection update (phases.py:1196-1242), fused over every bucket.
+        # Backward (phases.py:1018-1104) and connection update
+        # (phases.py:1196-1242). In a TOPOLOGICAL step they share one pass per
+        # bucket: no update_unit runs between them (the plan refuses one),
+        # bucket b's backward terms use its pre-update weights, and bucket b's
+        # update needs only finalized grads (levels > b) and activations.
+        self._backward_update(plan, arena, units, consts, fin_common, stream, g)
         if plan.update is not None:
-            self._update(plan, arena, units, consts, stream)
             state._arena_ahead = True
 
         state.step = state.step + 1
@@ -254,7 +260,7 @@ class StepFn:
                 "plx_loss_softmax_ce",
             )
             return
-        scratch = torch.empty(n_out + n_out // 256 + 2, dtype=torch.float32, device=dev)
+        scratch = torch.empty(n_out // 256 + 2, dtype=torch.float32, device=dev)
         prog = program_struct(lp.program, units, g)
         _lib.check(
             lib.plx_loss_elementwise(
@@ -270,78 +276,103 @@ class StepFn:
             "plx_loss_elementwise",
         )
 
-    def _backward(self, plan: Plan, arena: Arena, units: dict, fin_common: dict,
-                  stream: int, g: Any) -> None:
+    def _tiles(self, plan: Plan, arena: Arena, units: dict, consts: dict, b: int,
+               fold: bool, update: bool, stream: int) -> None:
         lib = _lib.load()
-        bp = plan.backward
-        dev = arena.device
-        n_units = self.static.num_units
-        swaps = self._shadow(units, bp.program.out_fields) if arena.pipeline else {}
-        acc = None
-        if arena.bwd_carry:
-            acc = torch.empty(n_units, dtype=torch.float32, device=dev)
-            _lib.call("plx_fill_f32", n_units, bp.identity, acc.data_ptr(), stream)
-        prog = program_struct(bp.program, units, g, out_override=swaps)
-
-        def finalize(rows: Any, fin_level: int, skip_inputs: int) -> None:
-            d = _lib.plx_backward_finalize_desc()
-            d.nrows = rows.nrows
-            d.monoid = bp.monoid
-            d.row_unit = rows.rows.data_ptr()
-            d.row_item = rows.ptr.data_ptr() if rows.ptr is not None else None
-            d.item_sum = arena.item_sum.data_ptr()
-            d.acc = acc.data_ptr() if acc is not None else None
-            d.fin.level = fin_common["level"]
-            d.fin.is_input = fin_common["is_input"]
-            d.fin.pruned = fin_common["pruned"]
-            d.fin.fin_level = fin_level
-            d.fin.skip_inputs = skip_inputs
-            d.apply = prog
-            self._launch("backward_finalize", lib.plx_backward_finalize, d, stream)
-
-        def fold(b: int) -> None:
-            rows = arena.bwd[b]
-            d = _lib.plx_backward_fold_desc()
-            d.nitems = rows.nitems
-            d.monoid = bp.monoid
-            d.item_ptr = rows.item_ptr.data_ptr()
-            d.sperm = arena.sperm.data_ptr()
-            d.sdst = arena.sdst.data_ptr()
-            d.weight = arena.cols["weight"].data_ptr()
-            d.g = units[bp.field].data_ptr()
-            d.item_sum = arena.item_sum.data_ptr() + 4 * rows.item_base
-            self._launch("backward_fold", lib.plx_backward_fold, d, stream)
-
-        if arena.pipeline:
-            # One sweep; every unit, inputs included, is applied (sweep.py:442-447).
-            fold(0)
-            finalize(arena.bwd[0], -1, 0)
-        else:
-            nb = arena.num_buckets
-            finalize(arena.top, nb, 1)
-            for b in range(nb - 1, 0, -1):
-                fold(b)
-                finalize(arena.bwd[b], b, 1)
-        self._unshadow(units, swaps)
-
-    def _update(self, plan: Plan, arena: Arena, units: dict, consts: dict, stream: int) -> None:
-        lib = _lib.load()
-        up = plan.update
-        d = _lib.plx_update_desc()
-        d.n = arena.n_positions
-        d.rule = up.rule_code
+        bt = arena.bwd[b]
+        d = _lib.plx_tile_desc()
+        d.base = bt.base
+        d.end = bt.end
+        d.tile_size = arena.tile
+        d.ntiles = bt.ntiles
+        d.fold = int(fold)
+        d.update = int(update)
         d.src = arena.cols["from_id"].data_ptr()
         d.dst = arena.cols["to_id"].data_ptr()
         d.dead = arena.cols["dead"].data_ptr()
         d.weight = arena.cols["weight"].data_ptr()
-        state_cols = up.state_columns()
-        for k, name in enumerate(state_cols):
-            setattr(d, f"s{k}", arena.cols[name].data_ptr())
-        d.gfield = units[up.grad_field.name].data_ptr()
-        d.act = units[ACTIVATION.name].data_ptr()
-        if "pow_table" in consts:
-            d.pow_table = consts["pow_table"].data_ptr()
-            d.pow_table_len = consts["pow_table"].numel() // 2
-        for k, v in enumerate(up.params()):
-            d.p[k] = float(v)
-        self._launch("update_conn", lib.plx_update_conn, d, stream)
+        if fold:
+            bp = plan.backward
+            d.monoid = bp.monoid
+            d.nhot = bt.nhot
+            d.grp_off = bt.grp_off.data_ptr()
+            d.grp_se = bt.grp_se.data_ptr()
+            d.grp_tgt = bt.grp_tgt.data_ptr()
+            d.sorted_local = bt.sorted_local.data_ptr()
+            d.hot_partial = bt.hot_partial.data_ptr()
+            d.cold_partial = bt.cold_partial.data_ptr()
+            d.g = units[bp.field].data_ptr()
+        if update:
+            up = plan.update
+            d.rule = up.rule_code
+            for k, name in enumerate(up.state_columns()):
+                setattr(d, f"s{k}", arena.cols[name].data_ptr())
+            d.gfield = units[up.grad_field.name].data_ptr()
+            d.act = units[ACTIVATION.name].data_ptr()
+            if "pow_table" in consts:
+                d.pow_table = consts["pow_table"].data_ptr()
+                d.pow_table_len = consts["pow_table"].numel() // 2
+            for k, v in enumerate(up.params()):
+                d.p[k] = float(v)
+        kind = "backward_update" if fold and update else ("backward" if fold else "update_conn")
+        self._launch(kind, lib.plx_backward_tiles, d, stream)
+
+    def _partials(self, plan: Plan, bt: Any, acc: Any, prog: Any, fin_common: dict,
+                  fin_level: int, skip_inputs: int, stream: int) -> None:
+        lib = _lib.load()
+        d = _lib.plx_partials_desc()
+        d.nrows = bt.nrows
+        d.monoid = plan.backward.monoid
+        d.ntiles = bt.ntiles
+        d.nhot = bt.nhot
+        d.superblock = SUPERBLOCK
+        d.row_unit = bt.rows.data_ptr()
+        if bt.row_hot is not None:
+            d.row_hot = bt.row_hot.data_ptr()
+            d.row_cold = bt.row_cold.data_ptr()
+            d.hot_partial = bt.hot_partial.data_ptr()
+            d.hot_sb = bt.hot_sb.data_ptr()
+            d.cold_partial = bt.cold_partial.data_ptr()
+            d.cold_sb = bt.cold_sb.data_ptr()
+        d.acc = acc.data_ptr() if acc is not None else None
+        d.fin.level = fin_common["level"]
+        d.fin.is_input = fin_common["is_input"]
+        d.fin.pruned = fin_common["pruned"]
+        d.fin.fin_level = fin_level
+        d.fin.skip_inputs = skip_inputs
+        d.apply = prog
+        self._launch("backward_finalize", lib.plx_backward_partials, d, stream)
+
+    def _backward_update(self, plan: Plan, arena: Arena, units: dict, consts: dict,
+                         fin_common: dict, stream: int, g: Any) -> None:
+        bp, up = plan.backward, plan.update
+        nb = arena.num_buckets
+        if bp is not None:
+            dev = arena.device
+            n_units = self.static.num_units
+            swaps = self._shadow(units, bp.program.out_fields) if arena.pipeline else {}
+            acc = None
+            if arena.bwd_carry:
+                acc = torch.empty(n_units, dtype=torch.float32, device=dev)
+                _lib.call("plx_fill_f32", n_units, bp.identity, acc.data_ptr(), stream)
+            prog = program_struct(bp.program, units, g, out_override=swaps)
+            if arena.pipeline:
+                # One sweep reading the pre-phase grads; every unit, inputs
+                # included, is applied (sweep.py:442-447). The update then
+                # reads the new grads, so it is its own pass.
+                self._tiles(plan, arena, units, consts, 0, True, False, stream)
+                self._partials(plan, arena.bwd[0], acc, prog, fin_common, -1, 0, stream)
+            else:
+                fused = up is not None
+                self._partials(plan, arena.top, acc, prog, fin_common, nb, 1, stream)
+                for b in range(nb - 1, 0, -1):
+                    self._tiles(plan, arena, units, consts, b, True, fused, stream)
+                    self._partials(plan, arena.bwd[b], acc, prog, fin_common, b, 1, stream)
+            self._unshadow(units, swaps)
+        if up is not None:
+            if bp is None or arena.pipeline:
+                todo = range(nb)
+            else:
+                todo = range(1)  # bucket 0 is never reduced, only updated
+            for b in todo:
+                self._tiles(plan, arena, units, consts, b, False, True, stream)

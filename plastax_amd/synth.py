@@ -63,13 +63,19 @@ def zipf_sources(rng: np.random.Generator, width: int, counts: np.ndarray,
     rows_out, src_out = [], []
     n = counts.size
     need = counts.astype(np.int64)
+    if int(need.max(initial=0)) > width:
+        raise ValueError("more distinct sources requested than the layer holds")
     pending = np.arange(n)
     chunk = 4096
+    rounds = 0
     while pending.size:
         next_pending = []
-        for c0 in range(0, pending.size, chunk):
-            rows = pending[c0 : c0 + chunk]
-            k = int(max(oversample, 2 * need[rows].max()))
+        # rows that found too few distinct sources retry with twice the draws
+        k_round = int(max(oversample, 2 * need.max(initial=0))) << rounds
+        rounds += 1
+        for c0 in range(0, pending.size, max(1, chunk >> (rounds - 1))):
+            rows = pending[c0 : c0 + max(1, chunk >> (rounds - 1))]
+            k = k_round
             u = rng.random((rows.size, k))
             draws = np.searchsorted(cdf, u, side="right").astype(np.int32)
             np.minimum(draws, width - 1, out=draws)

@@ -164,9 +164,11 @@ def test_softmax_ce_golden_on_device(name: str) -> None:
 # ---------------------------------------------------------------------------
 
 
-def _run_both(net, static, state, oracle, inputs_fn, steps, check_at):
-    o = nets.oracle_for(oracle, net, static, state)
+def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None):
+    o = nets.oracle_for(oracle, net, static, state, **({} if tile is None else {"tile": tile}))
     step = px.make_step(net, static)
+    if tile is not None:
+        step.tile = tile
     for k in range(1, steps + 1):
         x, t = inputs_fn(k)
         res = step(state, px.StepInputs(x, t))
@@ -223,6 +225,50 @@ def test_topological_zipf_net_bit_exact(oracle, opt_name: str) -> None:
         return x, (sign * x[perm]).astype(np.float32)
 
     _run_both(net, static, state, oracle, inputs, 12, {1, 12})
+
+
+@pytest.mark.parametrize("tile", [64, 1024])
+def test_many_tiles_and_hot_sources_bit_exact(oracle, tile: int) -> None:
+    """Small tiles: many tiles per bucket, the Zipf head lands in the dense
+    hot partials and the tail in the cold runs."""
+    e = synth.c2_topological(seed=8, scale=128)
+    net = nets.make_trained_net(f"T{tile}", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, device="cuda")
+    width = e.input_ids.size
+    rng = np.random.default_rng(12)
+
+    def inputs(k):
+        x = rng.standard_normal(width).astype(np.float32)
+        return x, np.tanh(x[::-1]).astype(np.float32)
+
+    _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile)
+
+
+def test_dead_slots_and_headroom_bit_exact(oracle) -> None:
+    """Tombstoned slots inside rows and a capacity tail are skipped by every
+    pass and never written."""
+    e = synth.c2_topological(seed=10, scale=256)
+    net = nets.make_trained_net("DS", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.momentum(1e-2, 0.9, nets.GRAD_PRE_ACT),
+                                px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, device="cuda", capacity_headroom=0.3,
+        capacity_align=12)
+    for bucket in state.conns:
+        live = torch.nonzero(bucket["dead"] == 0).flatten()
+        bucket["dead"][live[::5]] = 1
+    width = e.input_ids.size
+    rng = np.random.default_rng(13)
+
+    def inputs(k):
+        x = rng.standard_normal(width).astype(np.float32)
+        return x, x[::-1].copy()
+
+    _run_both(net, static, state, oracle, inputs, 4, {1, 4}, tile=512)
 
 
 @pytest.mark.parametrize("fwd,bwd", [
