@@ -27,6 +27,13 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+
+
+def progress(msg: str) -> None:
+    """A setup/progress line on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 METRIC = "edges/sec per streaming step (fwd+bwd+update) at 64M edges; % of HBM peak"
 
 
@@ -61,8 +68,6 @@ class EventTimer:
             ms = [a.elapsed_time(b) for a, b in pairs]
             out[kind] = {"launches": len(ms), "total_ms": float(sum(ms)), "mean_ms": float(np.mean(ms))}
         return out
-
-
 
 
 def build_c2(px, seed: int, scale: int):
@@ -131,7 +136,7 @@ def cpu_baseline(px, net, static, e, host_units, host_conns, inputs, targets, st
         "unit": "edges/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{steps} full C2 steps (2^26 edges) after 1 warm-up, median step {med * 1e3:.1f} ms, "
+        "sample": f"{steps} full C2 steps ({e.src.size} edges) after 1 warm-up, median step {med * 1e3:.1f} ms, "
         "single-threaded C oracle (oracle/plastax_oracle.c)",
     }
 
@@ -143,8 +148,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--scale", type=int, default=1, help="shrink C2's layer width (tests only)")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain elementwise copy of MIB MiB (read MIB, write MIB) "
+                    "five times: the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -156,17 +164,29 @@ def main() -> int:
 
     import torch
 
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        progress(f"copy calibration: 5 x {args.copy_calibration} MiB read + write")
+        return 0
+
     import plastax_amd as px
     from plastax_amd.state import column_to_numpy
 
     t_setup = time.perf_counter()
     net, e = build_c2(px, args.seed, args.scale)
+    progress(f"synthetic C2 edges: {e.src.size} ({time.perf_counter() - t_setup:.1f} s)")
     from plastax_amd import synth
 
     width = e.input_ids.size
     static, state = px.NetworkBuilder.from_edges(
         net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
         output_ids=e.output_ids, globals_=None, capacity_align=256, device="cpu")
+    progress(f"logical arena built ({time.perf_counter() - t_setup:.1f} s)")
     specs = {s.name: s for s in static.conn_fields}
     host_units = {s.name: column_to_numpy(state.units[s.name], s).copy() for s in static.unit_fields}
     host_conns = [{n: column_to_numpy(b[n], specs[n]).copy() for n in specs} for b in state.conns]
@@ -186,6 +206,7 @@ def main() -> int:
     xs_d = torch.from_numpy(xs).to(dev)
     ts_d = torch.from_numpy(ts).to(dev)
     step.arena(gstate)  # physical layout build (host, once)
+    progress(f"physical arena on the device ({time.perf_counter() - t_setup:.1f} s)")
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
 
@@ -217,18 +238,22 @@ def main() -> int:
 
     # Algorithmic bytes per launch of each kernel kind (per live edge).
     arena = gstate._arena
-    live_per_bucket = arena.lives
-    bytes_per_launch = {
-        # forward reads FROM_ID, TO_ID, DEAD, WEIGHT: 13 B/edge
-        "forward": 13 * edges / len(live_per_bucket),
-        # update reads FROM_ID, TO_ID, DEAD, WEIGHT, m, v, t and writes WEIGHT, m, v, t
-        "update_conn": 41 * edges,
+    # Algorithmic bytes per step of each launch kind (the reference column
+    # model): the forward reads FROM_ID, TO_ID, DEAD, WEIGHT (13 B/edge) of
+    # every bucket; the fused backward+update and the update-only pass read
+    # FROM_ID, TO_ID, DEAD, WEIGHT, m, v, t and write WEIGHT, m, v, t
+    # (41 B/edge), the former over buckets 1.., the latter over bucket 0.
+    lives = [int(v) for v in arena.lives]
+    bytes_per_step = {
+        "forward": 13 * sum(lives),
+        "backward_update": 41 * sum(lives[1:]),
+        "update_conn": 41 * lives[0],
     }
     dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
-    dom_bytes = bytes_per_launch.get(dominant)
     roofline = None
-    if dom_bytes is not None:
-        ach = dom_bytes / (kernels[dominant]["mean_ms"] * 1e-3) / 1e9
+    if dominant in bytes_per_step:
+        per_launch = bytes_per_step[dominant] * args.steps / kernels[dominant]["launches"]
+        ach = per_launch / (kernels[dominant]["mean_ms"] * 1e-3) / 1e9
         roofline = {
             "kernel": dominant,
             "bound": "hbm",
@@ -237,12 +262,14 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": None,
+            "algorithmic_bytes_per_launch": int(per_launch),
         }
     traffic_file = ROOT / "profiles" / "traffic.json"
     if roofline is not None and traffic_file.exists():
         roofline["traffic"] = json.loads(traffic_file.read_text()).get(dominant)
 
     cpu = None
+    progress(f"timed {args.steps} steps: {elapsed * 1e3 / args.steps:.3f} ms/step")
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(px, net, static, e, host_units, host_conns, xs, ts, args.cpu_steps)
 
