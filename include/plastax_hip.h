@@ -68,7 +68,8 @@ typedef struct plx_program {
 
 /* Which units a pass finalizes (phases.py:1011, :1096-1101, sweep.py:205-207):
  * unit u finalizes iff (fin_level < 0 || level[u] == fin_level)
- * && !(skip_inputs && is_input[u]) && !(pruned && pruned[u]). */
+ * && !(skip_inputs && is_input[u]) && !(pruned && pruned[u]). level and
+ * is_input are required; pruned may be null. */
 typedef struct plx_finalize {
   const int32_t* level;
   const uint8_t* is_input;
@@ -81,7 +82,8 @@ typedef struct plx_finalize {
  * (sweep.py:113-230, phases.py:972-1015) for a linear map
  * weight * x[from] (phases.py:535-556). Rows are destination units in a CSR
  * over the physical (destination-sorted) positions; each row is folded in slot
- * order, combined into acc, and finalized rows apply `apply` and reset acc. */
+ * order, combined into acc, and finalized rows apply `apply` and reset acc.
+ * `dead` may be null when no row range holds a tombstone. */
 typedef struct plx_forward_desc {
   int32_t nrows;
   int32_t monoid;
@@ -100,34 +102,44 @@ PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
 
 /* Backward pass over one bucket, fused with the connection update
  * (phases.py:1049-1104 accumulating into FROM_ID; phases.py:1196-1242).
- * The bucket's physical positions [base, end) are split into tiles of
- * tile_size positions, one workgroup each. With `fold`, every live edge's
- * backward term weight * g[dst] (pre-update weight) is folded per (tile,
- * source) group, in physical order, into a tile partial: hot sources write
- * their slot of the tile's dense row hot_partial[tile * nhot + h], the others
- * their slot of the source-major cold_partial array (group target -1-h or the
- * cold slot). With `update`, the same pass applies the update rule (see
- * plx_update_desc for p[] and the state columns) with grad = gfield[dst] *
- * act[src] and stores the new weight and state; dead edges keep theirs.
- * Tile metadata: grp_off[tile..tile+1] ranges the tile's groups; grp_se packs
- * a group's start (low 16 bits) and length (high 16 bits) in the tile's
- * source-sorted list sorted_local[tile * tile_size + j] of local edge indices. */
+ * The bucket's physical positions [base, end) are split into nsuper
+ * superblocks of consecutive tiles (super_tile[k] .. super_tile[k+1]); tile t
+ * covers positions base + tile_pos[t] .. base + tile_pos[t+1] (at most
+ * tile_size, multiples of 4). One workgroup walks each superblock in tile
+ * order. With `fold`, every live edge's backward
+ * term weight * g[dst] (pre-update weight) is folded per (tile, source)
+ * group, in physical order, into a tile partial: a hot source's tile partial
+ * is folded, in tile order, into its superblock sum, stored at
+ * hot_sb[superblock * nhot + h] (the identity where the source is absent);
+ * the other sources' tile partials are stored in their slot of the
+ * source-major cold_partial array (group target -1-h or the cold slot). With
+ * `update`, the same pass applies the update rule (see plx_update_desc for
+ * p[] and the state columns) with grad = gfield[dst] * act[src] and stores
+ * the new weight and state; dead edges keep theirs. Tile metadata:
+ * sorted_rank[p - base] is the rank of live position p in its tile's
+ * (source, position) order; grp_off[tile..tile+1] ranges the tile's groups;
+ * grp_se packs a group's first rank (low 16 bits) and length (high 16
+ * bits); tile_size is at most 65536. */
 typedef struct plx_tile_desc {
   int64_t base;
   int64_t end;
   int32_t tile_size;
   int32_t ntiles;
+  int32_t nsuper;
   int32_t monoid;
   int32_t fold;
   int32_t update;
   int32_t nhot;
   int32_t rule;
   int32_t pow_table_len;
+  int32_t reserved;
+  const int32_t* tile_pos;   /* [ntiles+1] tile starts relative to base   */
+  const int32_t* super_tile; /* [nsuper+1] first tile of each superblock  */
   const int32_t* grp_off;
   const uint32_t* grp_se;
   const int32_t* grp_tgt;
-  const uint16_t* sorted_local;
-  float* hot_partial;
+  const uint16_t* sorted_rank;
+  float* hot_sb;
   float* cold_partial;
   const int32_t* src;
   const int32_t* dst;
@@ -145,30 +157,29 @@ typedef struct plx_tile_desc {
 
 PLX_EXPORT int plx_backward_tiles(const plx_tile_desc* d, void* stream);
 
-/* Backward finalize of one level from the tile partials. The tiles are
- * grouped in superblocks of `superblock` consecutive tiles. A source's sum is
- * the fold, in superblock order, of its superblock sums, each the fold in
- * tile order of its tile partials (an absent tile holds the identity). Row r
- * (unit row_unit[r]) is hot (row_hot[r] >= 0: its column of the dense
- * hot_partial[tile * nhot + h], first reduced per superblock into hot_sb
- * scratch of ceil(ntiles / superblock) * nhot floats) or cold (its run
- * cold_partial[row_cold[r] .. row_cold[r+1]) in tile order, with each
- * partial's superblock in cold_sb). The sum is combined into acc (null: a
- * fresh identity) and, where finalized, `apply` runs and acc resets
- * (sweep.py:183-230). Null row_hot / row_cold: rows fold nothing (the deepest
- * level, primed from the identity: phases.py:1089-1094). */
+/* Backward finalize of one level from the partials of plx_backward_tiles.
+ * A source's sum is the fold, in superblock order, of its superblock sums,
+ * each the fold in tile order of its tile partials. Rows [0, nhot) are the hot
+ * sources in hot-column order (row_hot[r] == r: column r of hot_sb, nsuper
+ * rows of nhot); the others are cold (row_hot[r] == -1), finalized by
+ * nparts workgroups, the k-th taking rows [part_rows[k], part_rows[k+1])
+ * (at most 256; part_rows[0] == nhot when row_hot is given, else 0) (its run cold_partial[row_cold[r] .. row_cold[r+1])
+ * in tile order, with each partial's superblock in cold_sb). The sum is
+ * combined into acc (null: a fresh identity) and, where finalized, `apply`
+ * runs and acc resets (sweep.py:183-230). Null row_hot / row_cold: rows fold
+ * nothing (the deepest level, primed from the identity: phases.py:1089-1094). */
 typedef struct plx_partials_desc {
   int32_t nrows;
   int32_t monoid;
-  int32_t ntiles;
+  int32_t nsuper;
   int32_t nhot;
-  int32_t superblock;
+  int32_t nparts;
   int32_t reserved;
+  const int32_t* part_rows;
   const int32_t* row_unit;
   const int32_t* row_hot;
   const int32_t* row_cold;
-  const float* hot_partial;
-  float* hot_sb;
+  const float* hot_sb;
   const float* cold_partial;
   const uint16_t* cold_sb;
   float* acc;

@@ -33,13 +33,48 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libplastax_oracle.so"
 PIECE = 256  # loss folds: pieces of 256 outputs
-TILE = 8192  # backward folds: the device's destination-sorted tile size
-SUPERBLOCK = 32  # backward folds: tiles per superblock
+TILE = 4096  # backward folds: tiles of at most this many positions
+NSUPER = 512  # backward folds: superblocks per bucket at most
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _lib: ctypes.CDLL | None = None
+
+
+def tiles_of_positions(span: int, tile: int, nsuper_max: int) -> tuple[np.ndarray, np.ndarray]:
+    """Tile and superblock of every position of a bucket span (the device's
+    fold structure): min(nsuper_max, ceil(span/tile)) superblocks, the k-th
+    starting at floor(k*span/nsuper) rounded down to a multiple of 4, each
+    cut into tiles of `tile` positions from its start. Returns per-position
+    (global tile index, superblock index)."""
+    if span == 0:
+        return np.zeros(0, np.int32), np.zeros(0, np.int32)
+    nsuper = min(nsuper_max, -(-span // tile))
+    k = np.arange(nsuper + 1, dtype=np.int64)
+    starts = (k * span // nsuper) & ~3
+    starts[-1] = span
+    pos = np.arange(span, dtype=np.int64)
+    sb = np.searchsorted(starts, pos, side="right") - 1
+    tiles_per_sb = -(-(starts[1:] - starts[:-1]) // tile)
+    first_tile = np.concatenate([[0], np.cumsum(tiles_per_sb)])
+    tile_ix = first_tile[sb] + (pos - starts[sb]) // tile
+    return tile_ix.astype(np.int32), sb.astype(np.int32)
+
+
+def physical_unit_index(levels: np.ndarray, conns: list[dict[str, np.ndarray]]) -> np.ndarray:
+    """The device's unit numbering, restated: units ordered by level, then by
+    live out-degree descending, then by id. Returns, for every unit id, its
+    physical index (the device's destination-sorted order sorts by it)."""
+    n = levels.size
+    outdeg = np.zeros(n, dtype=np.int64)
+    for c in conns:
+        live = ~c["dead"].astype(bool)
+        outdeg += np.bincount(c["from_id"][live].astype(np.int64), minlength=n)
+    order = sorted(range(n), key=lambda u: (int(levels[u]), -int(outdeg[u]), u))
+    index = np.empty(n, dtype=np.int64)
+    index[np.asarray(order, dtype=np.int64)] = np.arange(n)
+    return index
 
 
 def build() -> pathlib.Path:
@@ -85,7 +120,7 @@ def load() -> ctypes.CDLL:
         ]
         lib.ox_bucket_reduce_bwd_tiled.argtypes = [
             ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _i32p, _i32p, _f32p, _f32p,
-            _i32p, ctypes.c_int32, ctypes.c_int32, _f32p,
+            _i32p, _i32p, ctypes.c_int32, _f32p,
         ]
         lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
         lib.ox_apply.argtypes = [
@@ -169,7 +204,7 @@ class OracleNet:
         *,
         piece: int = PIECE,
         tile: int | None = TILE,
-        superblock: int = SUPERBLOCK,
+        nsuper: int = NSUPER,
     ) -> None:
         self.static = static
         self.units = {k: np.ascontiguousarray(v) for k, v in units.items()}
@@ -178,8 +213,9 @@ class OracleNet:
         self.globals_ = globals_
         self.piece = piece
         self.tile = tile
-        self.superblock = superblock
-        self._bwd_order: dict[int, tuple[np.ndarray, np.ndarray]] = {}
+        self.nsuper = nsuper
+        self._bwd_order: dict[int, tuple[np.ndarray, np.ndarray, np.ndarray]] = {}
+        self._phys_index: np.ndarray | None = None
         self.step_count = 0
         n = static.num_units
         self.is_input = np.zeros(n, dtype=bool)
@@ -216,21 +252,30 @@ class OracleNet:
         )
         return out
 
-    def _tiles(self, b: int) -> tuple[np.ndarray, np.ndarray]:
-        """(order, tile) of bucket b's live slots: order sorts them by
-        (src, dst, slot); tile is each slot's rank in (dst, slot) order
-        divided by the tile size. Cached (the structure is static)."""
+    def _tiles(self, b: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """(order, tile, sb) of bucket b's live slots: order sorts them by
+        (src, physical dst, slot); a slot's physical position is its rank in
+        (physical dst, slot) order, and tile / sb are that position's tile
+        and superblock over the bucket's span (capacity rounded up to 4).
+        Cached (the structure is static)."""
+        if self._phys_index is None:
+            self._phys_index = physical_unit_index(self.units["level"], self.conns)
         if b not in self._bwd_order:
             c = self.conns[b]
+            cap = c["dead"].size
             live = np.flatnonzero(~c["dead"].astype(bool))
-            dst = c["to_id"][live]
+            dst = self._phys_index[c["to_id"][live]]
             src = c["from_id"][live]
             rank = np.empty(live.size, dtype=np.int64)
             rank[np.lexsort((live, dst))] = np.arange(live.size)
-            tile = np.zeros(c["dead"].size, dtype=np.int32)
-            tile[live] = (rank // self.tile) if self.tile else 0
+            tile = np.zeros(cap, dtype=np.int32)
+            sb = np.zeros(cap, dtype=np.int32)
+            if self.tile:
+                t_pos, s_pos = tiles_of_positions(-(-cap // 4) * 4, self.tile, self.nsuper)
+                tile[live] = t_pos[rank]
+                sb[live] = s_pos[rank]
             order = np.ascontiguousarray(live[np.lexsort((live, dst, src))].astype(np.int64))
-            self._bwd_order[b] = (order, tile)
+            self._bwd_order[b] = (order, tile, sb)
         return self._bwd_order[b]
 
     def _reduce_bwd(self, b: int, field: str, monoid: int) -> np.ndarray:
@@ -247,11 +292,11 @@ class OracleNet:
                 fptr(out), fptr(pc), iptr(pn),
             )
             return out
-        order, tile = self._tiles(b)
+        order, tile, sb = self._tiles(b)
         self.lib.ox_bucket_reduce_bwd_tiled(
             order.size, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
             iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
-            fptr(self.units[field]), iptr(tile), self.superblock, monoid, fptr(out),
+            fptr(self.units[field]), iptr(tile), iptr(sb), monoid, fptr(out),
         )
         return out
 

@@ -319,17 +319,17 @@ OX_API void ox_bucket_reduce_bwd(int64_t cap, const int32_t* from,
 /* Backward accumulate of one bucket in the device's tiled order. `order`
  * lists the bucket's n live slots sorted by (src, dst, slot) -- for each
  * source, its terms in the physical (destination-sorted) order -- and
- * tile[e] is the tile of slot e: its rank in (dst, slot) order divided by the
- * tile size. Per source, the terms of each tile are folded from the identity
- * in order; the tile sums of each superblock (`superblock` consecutive tiles)
- * are folded in tile order; the superblock sums are folded in order into
- * out[s] (pre-filled with the identity). With one tile this is the plain fold
- * of each source's terms in (dst, slot) order, which is the slot order of a
- * source-major bucket (builder.py:566-579). */
+ * tile[e] / sb[e] are slot e's tile and superblock (both non-decreasing in
+ * that physical order). Per source, the terms of each tile are folded from
+ * the identity in order; the tile sums of each superblock are folded in tile
+ * order; the superblock sums are folded in order into out[s] (pre-filled
+ * with the identity). With one tile this is the plain fold of each source's
+ * terms in (dst, slot) order, which is the slot order of a source-major
+ * bucket (builder.py:566-579). */
 OX_API void ox_bucket_reduce_bwd_tiled(int64_t n, const int64_t* order,
                                        const int32_t* from, const int32_t* to,
                                        const float* weight, const float* g,
-                                       const int32_t* tile, int32_t superblock,
+                                       const int32_t* tile, const int32_t* sb,
                                        int32_t monoid, float* out) {
   float id = ox_identity(monoid);
   int64_t k = 0;
@@ -337,10 +337,9 @@ OX_API void ox_bucket_reduce_bwd_tiled(int64_t n, const int64_t* order,
     int32_t s = from[order[k]];
     float total = out[s];
     while (k < n && from[order[k]] == s) {
-      /* superblock: `superblock` consecutive tiles, folded first */
-      int32_t sb = tile[order[k]] / superblock;
+      int32_t b = sb[order[k]];
       float sbsum = id;
-      while (k < n && from[order[k]] == s && tile[order[k]] / superblock == sb) {
+      while (k < n && from[order[k]] == s && sb[order[k]] == b) {
         int32_t t = tile[order[k]];
         float part = id;
         while (k < n && from[order[k]] == s && tile[order[k]] == t) {

@@ -18,16 +18,25 @@ Forward rows are the destination units of a bucket plus the units the
 bucket finalizes (phases.py:1011); each row is a CSR range of positions.
 
 The backward is a transpose reduce (sum into FROM_ID, sweep.py:343-399). The
-bucket's positions are cut into tiles of ``tile`` positions; within a tile,
-the live edges of each source form one group (listed in a per-tile
-source-sorted index, ``sorted_local``), folded on the device in physical
-order into one partial per (tile, source). Sources present in more than
-``HOT_FRAC`` of the tiles (the Zipf head) get a dense per-tile row of
-partials (``nhot`` wide); the others get source-major runs of cold partials.
-A source's sum is therefore the fold of its tile partials in tile order, each
-tile partial the fold of its terms in (dst, slot) order.
+bucket's positions are cut into at most ``NSUPER`` superblocks of near-equal
+length (one device workgroup each) and each superblock into tiles of at most
+``tile`` positions (``tile_partition``). Within a tile, the live edges of each
+source form one group (``sorted_rank`` gives every live position its rank in
+the tile's (source, position) order, so a group is a run of ranks), folded on
+the device in physical order into one partial per (tile, source). Sources present in many tiles (the Zipf head) are hot:
+the workgroup keeps their running sums in LDS and writes one dense row per
+superblock (``nhot`` wide); the others get source-major runs of cold
+partials. A source's sum is therefore the fold, in superblock order, of its
+superblock sums, each the fold in tile order of its tile partials, each tile
+partial the fold of its terms in (dst, slot) order.
 
-Units are not permuted: unit columns are the state's own tensors.
+Units are renumbered: the arena fixes a physical unit order (``unit_order``:
+by level, then out-degree descending, then unit id), the edge columns and
+every kernel work in physical ids, and the device unit columns are kept in
+that order (``units_to_physical`` / ``units_to_logical`` convert). So each
+bucket's most used sources occupy the first ids of their level: the gathers
+of their values hit a few cache lines, and a workgroup can copy them into LDS
+as one contiguous slice.
 """
 
 from __future__ import annotations
@@ -40,11 +49,30 @@ import torch
 from plastax_amd._types import DEAD, FROM_ID, TO_ID, Propagation
 from plastax_amd.state import Columns, NetworkStatic, column_to_numpy, torch_dtype
 
-TILE = 8192  # positions per backward tile (multiple of 4, <= 32768)
-SUPERBLOCK = 32  # tiles per superblock of the cross-tile fold
-HOT_FRAC = 0.125  # a source present in more than this fraction of tiles is hot
-MAX_HOT = 8192  # dense hot partials per tile (LDS: 4 B each)
+TILE = 4096  # positions per backward tile (multiple of 4, <= 32768)
+NSUPER = 512  # superblocks per bucket at most (device workgroups: 2 per CU)
+HOT_PER_SUPER = 0.25  # hot iff present in more than this many tiles per superblock
+MAX_HOT = 8192  # hot running sums per workgroup (LDS: 4 B each)
 PAD = 256  # slack positions after each slab (vector loads may run past the end)
+PART_ROWS = 256  # cold finalize: rows per workgroup at most (one per lane)
+PART_WIN = 2048  # cold finalize: cold partials staged per window
+
+
+def cold_row_parts(row_cold: np.ndarray, first: int) -> np.ndarray:
+    """Split rows [first, nrows) into workgroups of at most PART_ROWS rows
+    and, where rows allow, at most PART_WIN cold partials (one LDS window),
+    so no workgroup of the finalize waits on far more windows than another.
+    Returns the boundaries [first, ..., nrows]."""
+    nrows = row_cold.size - 1
+    bounds = [first]
+    r = first
+    while r < nrows:
+        hi = min(r + PART_ROWS, nrows)
+        # the most rows from r whose cold runs fit one window (at least one)
+        fit = int(np.searchsorted(row_cold, row_cold[r] + PART_WIN, side="right")) - 1
+        r = max(r + 1, min(hi, fit))
+        bounds.append(r)
+    return np.asarray(bounds, dtype=np.int64)
 
 
 @dataclasses.dataclass
@@ -64,23 +92,63 @@ class BackwardTiles:
     end: int
     ntiles: int
     fold: bool
+    nsuper: int = 0
+    tile_pos: torch.Tensor | None = None  # int32 [ntiles+1] tile starts (relative to base)
+    super_tile: torch.Tensor | None = None  # int32 [nsuper+1] first tile of each superblock
     nhot: int = 0
     grp_off: torch.Tensor | None = None  # int32 [ntiles+1]
     grp_se: torch.Tensor | None = None  # int32 (uint32 bits) [groups]
     grp_tgt: torch.Tensor | None = None  # int32 [groups]
-    sorted_local: torch.Tensor | None = None  # int16 (uint16 bits) [ntiles*tile]
-    hot_partial: torch.Tensor | None = None  # f32 [ntiles*nhot]
-    hot_sb: torch.Tensor | None = None  # f32 [nsuperblocks*nhot]
+    sorted_rank: torch.Tensor | None = None  # int16 (uint16 bits) [span] by position
+    hot_sb: torch.Tensor | None = None  # f32 [nsuper*nhot]
     cold_partial: torch.Tensor | None = None  # f32 [ncold]
     cold_sb: torch.Tensor | None = None  # int16 (uint16 bits) [ncold] superblock ids
     nrows: int = 0
     rows: torch.Tensor | None = None  # int32 [nrows] units finalized here
     row_hot: torch.Tensor | None = None  # int32 [nrows]
     row_cold: torch.Tensor | None = None  # int32 [nrows+1]
+    nparts: int = 0
+    part_rows: torch.Tensor | None = None  # int32 [nparts+1] cold rows per workgroup
 
 
 def _round_up(n: int, k: int) -> int:
     return -(-n // k) * k
+
+
+def unit_order(levels: np.ndarray, live_src: np.ndarray) -> np.ndarray:
+    """The physical unit order: units sorted by level, then by out-degree
+    (live edges leaving the unit) descending, then by id. Returns ``uperm``:
+    physical index -> unit id."""
+    n = levels.size
+    outdeg = np.bincount(live_src.astype(np.int64), minlength=n)
+    return np.lexsort((np.arange(n), -outdeg, levels.astype(np.int64)))
+
+
+def tile_partition(span: int, tile: int, nsuper_max: int = NSUPER) -> tuple[np.ndarray, np.ndarray]:
+    """Cut positions [0, span) (span a multiple of 4) into superblocks and
+    tiles: ``nsuper = min(nsuper_max, ceil(span / tile))`` superblocks, the
+    k-th starting at ``(k * span // nsuper)`` rounded down to a multiple of 4,
+    each cut into tiles of ``tile`` positions (the last one shorter). Returns
+    (tile_pos [ntiles+1], super_tile [nsuper+1]): tile t covers
+    [tile_pos[t], tile_pos[t+1]); superblock k owns tiles
+    [super_tile[k], super_tile[k+1])."""
+    if span % 4 or tile % 4 or tile <= 0:
+        raise ValueError("tile_partition: span and tile must be multiples of 4")
+    if span == 0:
+        return np.zeros(1, np.int64), np.zeros(1, np.int64)
+    nsuper = min(nsuper_max, -(-span // tile))
+    starts = [(k * span // nsuper) & ~3 for k in range(nsuper)] + [span]
+    tile_pos: list[int] = []
+    super_tile: list[int] = []
+    for k in range(nsuper):
+        lo, hi = starts[k], starts[k + 1]
+        if hi <= lo:
+            raise AssertionError("tile_partition: empty superblock")
+        super_tile.append(len(tile_pos))
+        tile_pos.extend(range(lo, hi, tile))
+    super_tile.append(len(tile_pos))
+    tile_pos.append(span)
+    return np.asarray(tile_pos, np.int64), np.asarray(super_tile, np.int64)
 
 
 class Arena:
@@ -94,24 +162,46 @@ class Arena:
         device: torch.device,
         *,
         tile: int = TILE,
+        nsuper: int = NSUPER,
     ) -> None:
         if tile <= 0 or tile % 4 or tile > 32768:
             raise ValueError("tile must be a positive multiple of 4, at most 32768")
+        if not 1 <= nsuper <= 65535:
+            raise ValueError("nsuper must be in [1, 65535]")
         self.static = static
         self.device = device
         self.tile = tile
+        self.nsuper = nsuper
         n = static.num_units
         nb = len(conns)
         self.num_buckets = nb
         self.pipeline = static.propagation is Propagation.PIPELINE
-        levels = units["level"].cpu().numpy().astype(np.int64)
-        is_input = np.zeros(n, dtype=bool)
-        if static.input_ids:
-            is_input[np.asarray(static.input_ids)] = True
-        pruned = units.get("pruned")
-        live_unit = np.ones(n, dtype=bool) if pruned is None else pruned.cpu().numpy() == 0
         specs = {s.name: s for s in static.conn_fields}
         host = {name: [column_to_numpy(b[name], specs[name]) for b in conns] for name in specs}
+        # Physical unit order; from here on every unit id is physical.
+        levels_l = units["level"].cpu().numpy().astype(np.int64)
+        live_src = np.concatenate(
+            [h[~d] for h, d in zip(host[FROM_ID.name], host[DEAD.name])] or [np.zeros(0, np.int32)]
+        )
+        self.uperm = unit_order(levels_l, live_src)
+        self.uinv = np.empty(n, dtype=np.int64)
+        self.uinv[self.uperm] = np.arange(n)
+        self.uperm_t = torch.from_numpy(self.uperm).to(device)
+        self.uinv_t = torch.from_numpy(self.uinv).to(device)
+        for name in (FROM_ID.name, TO_ID.name):
+            host[name] = [self.uinv[np.clip(h, 0, n - 1)].astype(np.int32) for h in host[name]]
+        levels = levels_l[self.uperm]
+        is_input = np.zeros(n, dtype=bool)
+        if static.input_ids:
+            is_input[self.uinv[np.asarray(static.input_ids)]] = True
+        pruned = units.get("pruned")
+        live_unit = np.ones(n, dtype=bool) if pruned is None else pruned.cpu().numpy()[self.uperm] == 0
+        # First physical id of every level (level l is [lvl_start[l], lvl_start[l+1])).
+        self.lvl_start = np.searchsorted(levels, np.arange(int(levels.max(initial=0)) + 2))
+        # Per-arena device constants in physical ids.
+        self.input_ids = self._i32(self.uinv[np.asarray(static.input_ids, dtype=np.int64)])
+        self.output_ids = self._i32(self.uinv[np.asarray(static.output_ids, dtype=np.int64)])
+        self.is_input = torch.from_numpy(is_input.astype(np.uint8)).to(device)
         caps = [int(h.shape[0]) for h in host[DEAD.name]]
         spans = [_round_up(c, 4) for c in caps]
         bases = np.concatenate([[0], np.cumsum(spans)]).astype(np.int64)
@@ -132,6 +222,9 @@ class Arena:
         self.bwd: list[BackwardTiles] = []
         self.fwd_carry = False
         self.bwd_carry = False
+        # Live positions come first in every bucket, so no forward row range
+        # holds a tombstone until one is set in place after this build.
+        self.dead_in_rows = False
         for b in range(nb):
             base, cap = self.bases[b], caps[b]
             dead = host[DEAD.name][b]
@@ -174,7 +267,10 @@ class Arena:
         # Rows finalized from the identity before the backward bucket walk:
         # the deepest level (phases.py:1089-1094).
         top = np.zeros(0, dtype=np.int64) if self.pipeline else np.flatnonzero(levels == nb)
-        self.top = BackwardTiles(0, 0, 0, False, nrows=int(top.size), rows=self._i32(top))
+        top_parts = np.minimum(np.arange(0, top.size + PART_ROWS, PART_ROWS), top.size)
+        top_parts = np.unique(top_parts) if top.size else np.zeros(1, np.int64)
+        self.top = BackwardTiles(0, 0, 0, False, nrows=int(top.size), rows=self._i32(top),
+                                 nparts=top_parts.size - 1, part_rows=self._i32(top_parts))
 
         self.slot = torch.from_numpy(phys_slot).to(device)
         self.cols: Columns = {}
@@ -195,20 +291,24 @@ class Arena:
         physical order."""
         T = self.tile
         base, end = self.bases[b], self.ends[b]
-        ntiles = -(-(end - base) // T)
+        tile_pos, super_tile = tile_partition(end - base, T, self.nsuper)
+        ntiles = tile_pos.size - 1
+        nsuper = super_tile.size - 1
+        tables = dict(nsuper=nsuper, tile_pos=self._i32(tile_pos), super_tile=self._i32(super_tile))
         if not fold:
-            return BackwardTiles(base, end, ntiles, False)
+            return BackwardTiles(base, end, ntiles, False, **tables)
         live = int(srcs.size)
         rank = np.arange(live, dtype=np.int64)
-        tile_of = rank // T
+        tile_of = np.searchsorted(tile_pos, rank, side="right") - 1
+        sb_of_tile = np.searchsorted(super_tile, np.arange(ntiles), side="right") - 1
         # The tile's live edges sorted by (source, physical position).
         o2 = np.lexsort((rank, srcs, tile_of))
         t_sorted = tile_of[o2]
         s_sorted = srcs[o2]
         tile_first = np.searchsorted(t_sorted, np.arange(ntiles + 1), side="left")
-        sorted_local = np.zeros(ntiles * T + 4, dtype=np.uint16)
+        sorted_rank = np.zeros(int(tile_pos[-1]) + 4, dtype=np.uint16)
         j_in_tile = np.arange(live, dtype=np.int64) - tile_first[t_sorted]
-        sorted_local[t_sorted * T + j_in_tile] = (rank[o2] - t_sorted * T).astype(np.uint16)
+        sorted_rank[rank[o2]] = j_in_tile.astype(np.uint16)
         # Groups: runs of one source inside one tile.
         if live:
             brk = np.flatnonzero((np.diff(t_sorted) != 0) | (np.diff(s_sorted) != 0)) + 1
@@ -220,9 +320,12 @@ class Arena:
         g_src = s_sorted[g_start] if live else g_start
         g_len = g_end - g_start
         g_st = g_start - tile_first[g_tile] if live else g_start
-        # Hot sources: present in more than HOT_FRAC of the tiles.
+        # Hot sources: a dense superblock row costs 8 B per superblock (write
+        # and read), a cold partial about as much as a scattered 4-byte store
+        # plus its read per tile present: hot iff present in more than
+        # HOT_PER_SUPER tiles per superblock, the most present first.
         presence = np.bincount(g_src, minlength=n) if live else np.zeros(n, np.int64)
-        cand = np.flatnonzero(presence > HOT_FRAC * ntiles)
+        cand = np.flatnonzero(presence > max(1.0, HOT_PER_SUPER * nsuper))
         if cand.size > MAX_HOT:
             keep = np.argsort(-presence[cand], kind="stable")[:MAX_HOT]
             cand = np.sort(cand[keep])
@@ -257,10 +360,9 @@ class Arena:
         counts = np.concatenate([np.zeros(nhot, np.int64), cold_count[others]])
         row_cold = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
         assert int(row_cold[-1]) == cold_order.size
-        tgt_final = tgt
         ncold = int(cold_order.size)
-        cold_sb = (g_tile[cold_order] // SUPERBLOCK).astype(np.uint16)
-        nsb = -(-ntiles // SUPERBLOCK)
+        cold_sb = sb_of_tile[g_tile[cold_order]].astype(np.uint16)
+        parts = cold_row_parts(row_cold, nhot)
         dev = self.device
         return BackwardTiles(
             base,
@@ -270,10 +372,9 @@ class Arena:
             nhot=nhot,
             grp_off=self._i32(grp_off),
             grp_se=torch.from_numpy(se.astype(np.uint32).view(np.int32)).to(dev),
-            grp_tgt=self._i32(tgt_final[g_perm] if live else tgt),
-            sorted_local=torch.from_numpy(sorted_local.view(np.int16)).to(dev),
-            hot_partial=torch.zeros(max(ntiles * nhot, 1), dtype=torch.float32, device=dev),
-            hot_sb=torch.zeros(max(nsb * nhot, 1), dtype=torch.float32, device=dev),
+            grp_tgt=self._i32(tgt[g_perm] if live else tgt),
+            sorted_rank=torch.from_numpy(sorted_rank.view(np.int16)).to(dev),
+            hot_sb=torch.zeros(max(nsuper * nhot, 1), dtype=torch.float32, device=dev),
             cold_partial=torch.zeros(max(ncold, 1), dtype=torch.float32, device=dev),
             cold_sb=torch.from_numpy(
                 np.concatenate([cold_sb, np.zeros(1, np.uint16)]).view(np.int16)
@@ -282,12 +383,27 @@ class Arena:
             rows=self._i32(rows),
             row_hot=self._i32(row_hot),
             row_cold=self._i32(row_cold),
+            nparts=parts.size - 1,
+            part_rows=self._i32(parts),
+            **tables,
         )
 
     def write_logical(self, conns: tuple[Columns, ...]) -> None:
-        """Scatter the physical columns back into the logical buckets."""
+        """Scatter the physical columns back into the logical buckets (unit
+        ids mapped back to the caller's numbering)."""
         for b, bucket in enumerate(conns):
             base, cap = self.bases[b], self.caps[b]
             idx = self.slot[base : base + cap].long()
             for name, col in bucket.items():
-                col[idx] = self.cols[name][base : base + cap]
+                vals = self.cols[name][base : base + cap]
+                if name in (FROM_ID.name, TO_ID.name):
+                    vals = self.uperm_t[vals.long()].to(col.dtype)
+                col[idx] = vals
+
+    def units_to_physical(self, units: Columns) -> Columns:
+        """Unit columns in the caller's numbering -> physical order."""
+        return {k: v.index_select(0, self.uperm_t) for k, v in units.items()}
+
+    def units_to_logical(self, units: Columns) -> Columns:
+        """Physical unit columns -> the caller's numbering."""
+        return {k: v.index_select(0, self.uinv_t) for k, v in units.items()}

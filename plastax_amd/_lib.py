@@ -18,6 +18,8 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
+ABI_VERSION = 2  # plx_abi_version() of the library these mirrors describe
+
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
 PLX_MAX_FIELDS = 8
@@ -78,17 +80,21 @@ class plx_tile_desc(ctypes.Structure):
         ("end", c_i64),
         ("tile_size", c_i32),
         ("ntiles", c_i32),
+        ("nsuper", c_i32),
         ("monoid", c_i32),
         ("fold", c_i32),
         ("update", c_i32),
         ("nhot", c_i32),
         ("rule", c_i32),
         ("pow_table_len", c_i32),
+        ("reserved", c_i32),
+        ("tile_pos", c_vp),
+        ("super_tile", c_vp),
         ("grp_off", c_vp),
         ("grp_se", c_vp),
         ("grp_tgt", c_vp),
-        ("sorted_local", c_vp),
-        ("hot_partial", c_vp),
+        ("sorted_rank", c_vp),
+        ("hot_sb", c_vp),
         ("cold_partial", c_vp),
         ("src", c_vp),
         ("dst", c_vp),
@@ -109,14 +115,14 @@ class plx_partials_desc(ctypes.Structure):
     _fields_ = [
         ("nrows", c_i32),
         ("monoid", c_i32),
-        ("ntiles", c_i32),
+        ("nsuper", c_i32),
         ("nhot", c_i32),
-        ("superblock", c_i32),
+        ("nparts", c_i32),
         ("reserved", c_i32),
+        ("part_rows", c_vp),
         ("row_unit", c_vp),
         ("row_hot", c_vp),
         ("row_cold", c_vp),
-        ("hot_partial", c_vp),
         ("hot_sb", c_vp),
         ("cold_partial", c_vp),
         ("cold_sb", c_vp),
@@ -193,6 +199,10 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
+    if lib.plx_abi_version() != ABI_VERSION:
+        raise ImportError(
+            f"{LIB_PATH} has ABI version {lib.plx_abi_version()}, expected {ABI_VERSION}: rebuild it"
+        )
     _lib = lib
     return lib
 

@@ -4,8 +4,8 @@
 // Data layout (built by plastax_amd/_layout.py): every bucket's edge columns
 // live in one physical slab, destination-sorted inside each bucket (live edges
 // ordered by (dst, logical slot), then the bucket's dead slots). The backward
-// transpose reduce works on fixed tiles of that order: per-(tile, source)
-// partials, folded per superblock of tiles, then across superblocks. All folds
+// transpose reduce works on tiles of that order: per-(tile, source) partials,
+// folded per superblock of tiles, then across superblocks. All folds
 // are deterministic: no float atomics anywhere, so a step is bitwise
 // repeatable.
 //
@@ -81,10 +81,53 @@ enum : int32_t {
 
 constexpr int kRegs = 16;
 
-// Runs `P` for unit `u`; out slot k is stored to P.outs[k][u] when `store`.
-// Returns out slot 1 (the loss term of a loss program).
-__device__ float run_program(const plx_program& P, int64_t u, float acc, float aux,
-                             bool store) {
+// The unit fields a program reads (LDU), loaded for one unit ahead of time:
+// a program reads its fields only at its own unit, so every load can be
+// issued before the work that produces `acc`.
+struct UnitFields {
+  float v[PLX_MAX_FIELDS];
+};
+
+// Field k of `f`; k is uniform across the wave, so this is a scalar branch
+// and the values stay in registers.
+__device__ __forceinline__ float pick_field(const UnitFields& f, int k) {
+  switch (k & (PLX_MAX_FIELDS - 1)) {
+    case 0: return f.v[0];
+    case 1: return f.v[1];
+    case 2: return f.v[2];
+    case 3: return f.v[3];
+    case 4: return f.v[4];
+    case 5: return f.v[5];
+    case 6: return f.v[6];
+    default: return f.v[7];
+  }
+}
+
+// Loads the program's fields at unit u: a uniform switch on the field count
+// leaves straight-line code with every load issued before any is used.
+__device__ __forceinline__ UnitFields load_fields(const plx_program& P, int64_t u) {
+  UnitFields f;
+#pragma unroll
+  for (int k = 0; k < PLX_MAX_FIELDS; ++k) f.v[k] = 0.0f;
+  switch (P.nfields) {
+    case 8: f.v[7] = P.fields[7][u]; [[fallthrough]];
+    case 7: f.v[6] = P.fields[6][u]; [[fallthrough]];
+    case 6: f.v[5] = P.fields[5][u]; [[fallthrough]];
+    case 5: f.v[4] = P.fields[4][u]; [[fallthrough]];
+    case 4: f.v[3] = P.fields[3][u]; [[fallthrough]];
+    case 3: f.v[2] = P.fields[2][u]; [[fallthrough]];
+    case 2: f.v[1] = P.fields[1][u]; [[fallthrough]];
+    case 1: f.v[0] = P.fields[0][u]; [[fallthrough]];
+    default: break;
+  }
+  return f;
+}
+
+// Runs `P` for unit `u`, reading its fields from `f`; out slot k is stored to
+// P.outs[k][u] when `store`. Returns out slot 1 (the loss term of a loss
+// program).
+__device__ float run_program(const plx_program& P, int64_t u, const UnitFields& f, float acc,
+                             float aux, bool store) {
   float r[kRegs];
   float outs[PLX_MAX_OUTS];
 #pragma unroll
@@ -102,7 +145,7 @@ __device__ float run_program(const plx_program& P, int64_t u, float acc, float a
     float v = 0.0f;
     switch (op) {
       case OP_ACC: v = acc; break;
-      case OP_LDU: v = P.fields[a & (PLX_MAX_FIELDS - 1)][u]; break;
+      case OP_LDU: v = pick_field(f, a); break;
       case OP_CONST: v = P.consts[a & (PLX_MAX_CONST - 1)]; break;
       case OP_LDX: v = aux; break;
       case OP_MOV: v = ra; break;
@@ -141,66 +184,112 @@ __device__ float run_program(const plx_program& P, int64_t u, float acc, float a
   return outs[1];
 }
 
+// Whether unit u finalizes. level and is_input are never null (the entry
+// points check); a null `pruned` reads is_input and is masked off, so the
+// three loads are unconditional and issued before any is tested.
 __device__ __forceinline__ bool finalizes(const plx_finalize& f, int u) {
-  if (f.fin_level >= 0 && f.level[u] != f.fin_level) return false;
-  if (f.skip_inputs && f.is_input[u]) return false;
-  if (f.pruned && f.pruned[u]) return false;
-  return true;
+  const int lv = f.level[u];
+  const int inp = f.is_input[u];
+  const int prn = (f.pruned ? f.pruned : f.is_input)[u];
+  return (f.fin_level < 0 || lv == f.fin_level) && !(f.skip_inputs && inp) &&
+         !(f.pruned && prn);
+}
+
+// A row's unit, whether it finalizes and the fields its program reads,
+// loaded together before the row's reduction.
+struct RowPre {
+  int u;
+  bool fin;
+  UnitFields f;
+};
+
+__device__ __forceinline__ RowPre prefetch_row(const int32_t* row_unit, int r,
+                                               const plx_finalize& fin,
+                                               const plx_program& P) {
+  RowPre p;
+  p.u = row_unit[r];
+  p.fin = finalizes(fin, p.u);
+  p.f = load_fields(P, p.u);
+  return p;
 }
 
 // ---------------------------------------------------------------------------
-// Forward: one row (destination unit) per lane. The workgroup's rows own a
-// contiguous physical range; it is streamed through LDS in windows of kWin
-// terms with 16-byte loads (map = weight * x[src], dead slots contribute the
-// identity), and each lane folds its own row from LDS in slot order, carrying
-// the running value across windows, so the fold order is the slot order for
-// any row length.
+// Forward: kFwdRows rows (destination units) per workgroup, one row per lane
+// of the first kFwdRows lanes. The rows own a contiguous physical range; the
+// whole workgroup streams it through LDS in windows of kFwdWin terms with
+// 16-byte loads of FROM_ID and WEIGHT (map = weight * x[src]), and each row's
+// lane folds its terms from LDS in slot order, carrying the running value
+// across windows, so the fold order is the slot order for any row length.
+// Row ranges cover live positions only; DEAD is read only when the caller
+// passes it (a bucket with tombstones inside its rows).
 // ---------------------------------------------------------------------------
 constexpr int kFwdBlock = 256;
-#ifndef PLX_FWD_QUADS
-#define PLX_FWD_QUADS 8
+#ifndef PLX_FWD_ROWS
+#define PLX_FWD_ROWS 32
 #endif
-constexpr int kWinQuads = PLX_FWD_QUADS;  // 16-byte quads per thread per window
-constexpr int kWin = 4 * kWinQuads * kFwdBlock;
+constexpr int kFwdRows = PLX_FWD_ROWS;
+#ifndef PLX_FWD_QUADS
+#define PLX_FWD_QUADS 4
+#endif
+constexpr int kFwdQuads = PLX_FWD_QUADS;  // 16-byte quads per thread per window
+constexpr int kFwdWin = 4 * kFwdQuads * kFwdBlock;
 
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
-  __shared__ float buf[kWin];
-  const int row0 = blockIdx.x * kFwdBlock;
-  const int r = row0 + threadIdx.x;
-  const int rend = min(row0 + kFwdBlock, d.nrows);
+  __shared__ __align__(16) float buf[kFwdWin];
+  const int row0 = blockIdx.x * kFwdRows;
+  const int rend = min(row0 + kFwdRows, d.nrows);
   const int e_begin = d.row_ptr[row0];
   const int e_end = d.row_ptr[rend];
-  const bool has = r < d.nrows;
+  const int r = row0 + static_cast<int>(threadIdx.x);
+  const bool has = threadIdx.x < kFwdRows && r < rend;
   const int my_b = has ? d.row_ptr[r] : 0;
   const int my_e = has ? d.row_ptr[r + 1] : 0;
+  RowPre pre;
+  if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
   const float ident = Mono<M>::id();
   float s = ident;
-  for (int w0 = e_begin & ~3; w0 < e_end; w0 += kWin) {
-    const int wn = min(kWin, e_end - w0);
+  for (int w0 = e_begin & ~3; w0 < e_end; w0 += kFwdWin) {
+    const int wn = min(kFwdWin, e_end - w0);
     // Issue every load of the window before using any of them.
-    int4 sv[kWinQuads];
-    float4 wv[kWinQuads];
-    uint32_t dv[kWinQuads];
+    int4 sv[kFwdQuads];
+    float4 wv[kFwdQuads];
+    uint32_t dv[kFwdQuads];
 #pragma unroll
-    for (int i = 0; i < kWinQuads; ++i) {
+    for (int i = 0; i < kFwdQuads; ++i) {
       const int q = threadIdx.x + i * kFwdBlock;
+      dv[i] = 0;
       if (4 * q < wn) {
         const int e = w0 + 4 * q;
         sv[i] = *reinterpret_cast<const int4*>(d.src + e);
         wv[i] = *reinterpret_cast<const float4*>(d.weight + e);
-        dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+        if (d.dead) dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+      }
+    }
+    // Only positions of this workgroup's rows contribute; the others gather
+    // unit 0, so every gather is unconditional and issued before any use.
+    bool ok[kFwdQuads][4];
+    float xv[kFwdQuads][4];
+#pragma unroll
+    for (int i = 0; i < kFwdQuads; ++i) {
+      const int e = w0 + 4 * (threadIdx.x + i * kFwdBlock);
+      const bool in = 4 * (threadIdx.x + i * kFwdBlock) < wn;
+      const int idx[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        ok[i][k] = in && e + k >= e_begin && e + k < e_end && !((dv[i] >> (8 * k)) & 0xFFu);
+        xv[i][k] = d.x[ok[i][k] ? idx[k] : 0];
       }
     }
 #pragma unroll
-    for (int i = 0; i < kWinQuads; ++i) {
+    for (int i = 0; i < kFwdQuads; ++i) {
       const int q = threadIdx.x + i * kFwdBlock;
       if (4 * q < wn) {
         float4 o;
-        o.x = (dv[i] & 0x000000FFu) ? ident : wv[i].x * d.x[sv[i].x];
-        o.y = (dv[i] & 0x0000FF00u) ? ident : wv[i].y * d.x[sv[i].y];
-        o.z = (dv[i] & 0x00FF0000u) ? ident : wv[i].z * d.x[sv[i].z];
-        o.w = (dv[i] & 0xFF000000u) ? ident : wv[i].w * d.x[sv[i].w];
+        o.x = ok[i][0] ? wv[i].x * xv[i][0] : ident;
+        o.y = ok[i][1] ? wv[i].y * xv[i][1] : ident;
+        o.z = ok[i][2] ? wv[i].z * xv[i][2] : ident;
+        o.w = ok[i][3] ? wv[i].w * xv[i][3] : ident;
         *reinterpret_cast<float4*>(buf + 4 * q) = o;
       }
     }
@@ -210,10 +299,10 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
     __syncthreads();
   }
   if (!has) return;
-  const int u = d.row_unit[r];
+  const int u = pre.u;
   const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
-  if (finalizes(d.fin, u)) {
-    run_program(d.apply, u, a, 0.0f, true);
+  if (pre.fin) {
+    run_program(d.apply, u, pre.f, a, 0.0f, true);
     if (d.acc) d.acc[u] = ident;
   } else if (d.acc) {
     d.acc[u] = a;
@@ -278,10 +367,27 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
     s1 = *reinterpret_cast<const float4*>(d.s1 + e);
     s2 = *reinterpret_cast<const float4*>(d.s2 + e);
   }
-  if (!(dv & 0x000000FFu)) update_one<RULE>(d, d.gfield[tv.x] * d.act[sv.x], w.x, s0.x, s1.x, s2.x);
-  if (!(dv & 0x0000FF00u)) update_one<RULE>(d, d.gfield[tv.y] * d.act[sv.y], w.y, s0.y, s1.y, s2.y);
-  if (!(dv & 0x00FF0000u)) update_one<RULE>(d, d.gfield[tv.z] * d.act[sv.z], w.z, s0.z, s1.z, s2.z);
-  if (!(dv & 0xFF000000u)) update_one<RULE>(d, d.gfield[tv.w] * d.act[sv.w], w.w, s0.w, s1.w, s2.w);
+  // Every gather is unconditional (dead lanes gather unit 0) and issued
+  // before any result is used.
+  bool lv[4];
+  float gr[4];
+  {
+    const int di[4] = {tv.x, tv.y, tv.z, tv.w};
+    const int si[4] = {sv.x, sv.y, sv.z, sv.w};
+    float gu[4], ac[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lv[k] = !((dv >> (8 * k)) & 0xFFu);
+      gu[k] = d.gfield[lv[k] ? di[k] : 0];
+      ac[k] = d.act[lv[k] ? si[k] : 0];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gr[k] = gu[k] * ac[k];
+  }
+  if (lv[0]) update_one<RULE>(d, gr[0], w.x, s0.x, s1.x, s2.x);
+  if (lv[1]) update_one<RULE>(d, gr[1], w.y, s0.y, s1.y, s2.y);
+  if (lv[2]) update_one<RULE>(d, gr[2], w.z, s0.z, s1.z, s2.z);
+  if (lv[3]) update_one<RULE>(d, gr[3], w.w, s0.w, s1.w, s2.w);
   *reinterpret_cast<float4*>(d.weight + e) = w;
   if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = s0;
   if (nstate >= 3) {
@@ -291,16 +397,20 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward + update, one destination-sorted tile per workgroup.
+// Backward + update over destination-sorted tiles; one workgroup per
+// superblock (a run of consecutive tiles of near-equal total length, so every
+// workgroup streams the same number of positions), walked in tile order.
 //
-// The workgroup streams its tile's edge columns once (16-byte loads): for
-// each live edge it forms the backward term c = weight * g[dst] with the
-// pre-update weight into LDS and, when fused, applies the update rule and
+// For each tile the workgroup streams the edge columns once (16-byte loads):
+// for each live edge it forms the backward term c = weight * g[dst] with the
+// pre-update weight into LDS and, when updating, applies the update rule and
 // stores the new weight and optimizer state. Then the tile's (source) groups
 // are folded from LDS in physical order -- the group lists are precomputed
-// per tile -- and each group sum lands either in the tile's dense row of hot
-// partials (sources present in many tiles) or in its slot of the source-major
-// cold partial array. No float atomics: every partial has exactly one writer.
+// per tile -- and each group sum lands either in the workgroup's LDS running
+// sum of a hot source (sources present in many tiles), folded in tile order,
+// or in its slot of the source-major cold partial array. At the end the
+// running hot sums are the superblock's dense row of hot_sb. No float atomics:
+// every value has exactly one writer and a fixed fold order.
 // ---------------------------------------------------------------------------
 constexpr int kTileBlock = 512;
 #ifndef PLX_TILE_QUADS
@@ -308,153 +418,276 @@ constexpr int kTileBlock = 512;
 #endif
 constexpr int kTileQuads = PLX_TILE_QUADS;  // 16-byte quads per thread per streaming pass
 
-template <int RULE, int M, bool FOLD>
+constexpr int kGrpPer = 6;  // group descriptors prefetched per thread per tile
+
+// Folds one (tile, source) group: the contiguous run buf[st, st+len) in
+// order, into its cold partial slot or its hot running sum. A source has one
+// group per tile, so no other lane touches a hot slot within the tile.
+template <int M>
+__device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* buf, float* hot,
+                                           uint32_t se, int32_t tgt) {
+  const float* run = buf + (se & 0xFFFFu);
+  const int len = static_cast<int>(se >> 16);
+  float v = Mono<M>::id();
+  int j = 0;
+  for (; j + 4 <= len; j += 4) {
+    const float a0 = run[j], a1 = run[j + 1], a2 = run[j + 2], a3 = run[j + 3];
+    v = Mono<M>::op(v, a0);
+    v = Mono<M>::op(v, a1);
+    v = Mono<M>::op(v, a2);
+    v = Mono<M>::op(v, a3);
+  }
+  for (; j < len; ++j) v = Mono<M>::op(v, run[j]);
+  if (tgt >= 0) {
+    d.cold_partial[tgt] = v;
+  } else {
+    const int h = -1 - tgt;
+    hot[h] = Mono<M>::op(hot[h], v);
+  }
+}
+
+// SAME_G: the backward field and the update's grad field are one column, so
+// one gather serves both.
+template <int RULE, int M, bool FOLD, bool SAME_G>
 __global__ __launch_bounds__(kTileBlock) void k_tile(plx_tile_desc d) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int T = d.tile_size;
-  float* buf = reinterpret_cast<float*>(smem);  // [T]
-  float* hot = buf + T;                          // [nhot], padded to 16 bytes
-  uint16_t* sl = reinterpret_cast<uint16_t*>(hot + ((d.nhot + 3) & ~3));  // [T]
-  const int blk = blockIdx.x;
-  const int64_t t0 = d.base + static_cast<int64_t>(blk) * T;
-  const int64_t t1 = min(t0 + T, d.end);
-  const int n = static_cast<int>(t1 - t0);
+  float* buf = reinterpret_cast<float*>(smem);  // [T] terms in source-sorted order
+  float* hot = buf + T;                          // [nhot]
+  const int k0 = d.super_tile[blockIdx.x];
+  const int k1 = d.super_tile[blockIdx.x + 1];
   const float ident = Mono<M>::id();
-  if (FOLD) {
+  if (FOLD)
     for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hot[j] = ident;
-    const uint16_t* slg = d.sorted_local + static_cast<int64_t>(blk) * T;
-    for (int j = threadIdx.x; 4 * j < n; j += kTileBlock)
-      *reinterpret_cast<uint2*>(sl + 4 * j) = *reinterpret_cast<const uint2*>(slg + 4 * j);
-  }
   constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? 3 : 1);
   constexpr int U = kTileQuads;
-  // Each pass covers U quads per thread; every load of a pass is issued
-  // before any of it is used.
-  for (int q0 = threadIdx.x; 4 * q0 < n; q0 += U * kTileBlock) {
-    int4 sv[U], tv[U];
-    uint32_t dv[U];
-    float4 w[U], s0[U], s1[U], s2[U];
+  for (int blk = k0; blk < k1; ++blk) {
+    const int64_t t0 = d.base + d.tile_pos[blk];
+    const int n = d.tile_pos[blk + 1] - d.tile_pos[blk];
+    // The tile's group descriptors, kGrpPer per thread, are loaded with the
+    // edge columns so the fold below waits on no global load.
+    uint32_t gse[kGrpPer];
+    int32_t gtg[kGrpPer];
+    int ga = 0, gb = 0;
+    if (FOLD) {
+      ga = d.grp_off[blk];
+      gb = d.grp_off[blk + 1];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int q = q0 + i * kTileBlock;
-      if (4 * q < n) {
+      for (int i = 0; i < kGrpPer; ++i) {
+        const int gi = ga + threadIdx.x + i * kTileBlock;
+        gse[i] = gi < gb ? d.grp_se[gi] : 0u;
+        gtg[i] = gi < gb ? d.grp_tgt[gi] : 0;
+      }
+    }
+    // Each pass covers U quads per thread; every load of a pass is issued
+    // before any of it is used.
+    for (int q0 = threadIdx.x; 4 * q0 < n; q0 += U * kTileBlock) {
+      int4 sv[U], tv[U];
+      uint32_t dv[U];
+      uint2 rk[U];
+      float4 w[U], s0[U], s1[U], s2[U];
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int q = q0 + i * kTileBlock;
+        if (4 * q < n) {
+          const int64_t e = t0 + 4 * q;
+          tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
+          dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+          w[i] = *reinterpret_cast<const float4*>(d.weight + e);
+          if (FOLD) rk[i] = *reinterpret_cast<const uint2*>(d.sorted_rank + (e - d.base));
+          if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
+          if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
+          if (nstate >= 3) {
+            s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
+            s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
+          }
+        }
+      }
+      // Every gather is unconditional (dead or out-of-tile lanes gather
+      // unit 0) and issued before any result is used.
+      bool lv[U][4];
+      float gd[U][4], gu[U][4], ac[U][4];
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const bool in = 4 * (q0 + i * kTileBlock) < n;
+        const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
+        const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
+          const int dk = lv[i][k] ? di[k] : 0;
+          if (FOLD) gd[i][k] = d.g[dk];
+          if (RULE >= 0) {
+            gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
+            ac[i][k] = d.act[lv[i][k] ? si[k] : 0];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int q = q0 + i * kTileBlock;
+        if (4 * q >= n) continue;
         const int64_t e = t0 + 4 * q;
-        tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
-        dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
-        w[i] = *reinterpret_cast<const float4*>(d.weight + e);
-        if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
-        if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
-        if (nstate >= 3) {
-          s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
-          s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
+        if (FOLD) {
+          // Each live edge's term goes to its slot in the tile's
+          // source-sorted order, so every (tile, source) group is a
+          // contiguous run of buf.
+          if (lv[i][0]) buf[rk[i].x & 0xFFFFu] = w[i].x * gd[i][0];
+          if (lv[i][1]) buf[rk[i].x >> 16] = w[i].y * gd[i][1];
+          if (lv[i][2]) buf[rk[i].y & 0xFFFFu] = w[i].z * gd[i][2];
+          if (lv[i][3]) buf[rk[i].y >> 16] = w[i].w * gd[i][3];
         }
-      }
-    }
+        if (RULE >= 0) {
+          float gr[4];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int q = q0 + i * kTileBlock;
-      if (4 * q >= n) continue;
-      const int64_t e = t0 + 4 * q;
-      const bool l0 = !(dv[i] & 0x000000FFu), l1 = !(dv[i] & 0x0000FF00u);
-      const bool l2 = !(dv[i] & 0x00FF0000u), l3 = !(dv[i] & 0xFF000000u);
-      if (FOLD) {
-        float4 c;
-        c.x = l0 ? w[i].x * d.g[tv[i].x] : ident;
-        c.y = l1 ? w[i].y * d.g[tv[i].y] : ident;
-        c.z = l2 ? w[i].z * d.g[tv[i].z] : ident;
-        c.w = l3 ? w[i].w * d.g[tv[i].w] : ident;
-        *reinterpret_cast<float4*>(buf + 4 * q) = c;
-      }
-      if (RULE >= 0) {
-        float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
-        if (l0) update_one<RULE>(d, d.gfield[tv[i].x] * d.act[sv[i].x], a.x, m.x, v.x, t.x);
-        if (l1) update_one<RULE>(d, d.gfield[tv[i].y] * d.act[sv[i].y], a.y, m.y, v.y, t.y);
-        if (l2) update_one<RULE>(d, d.gfield[tv[i].z] * d.act[sv[i].z], a.z, m.z, v.z, t.z);
-        if (l3) update_one<RULE>(d, d.gfield[tv[i].w] * d.act[sv[i].w], a.w, m.w, v.w, t.w);
-        *reinterpret_cast<float4*>(d.weight + e) = a;
-        if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
-        if (nstate >= 3) {
-          *reinterpret_cast<float4*>(d.s1 + e) = v;
-          *reinterpret_cast<float4*>(d.s2 + e) = t;
+          for (int k = 0; k < 4; ++k) gr[k] = (SAME_G && FOLD ? gd[i][k] : gu[i][k]) * ac[i][k];
+          float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
+          if (lv[i][0]) update_one<RULE>(d, gr[0], a.x, m.x, v.x, t.x);
+          if (lv[i][1]) update_one<RULE>(d, gr[1], a.y, m.y, v.y, t.y);
+          if (lv[i][2]) update_one<RULE>(d, gr[2], a.z, m.z, v.z, t.z);
+          if (lv[i][3]) update_one<RULE>(d, gr[3], a.w, m.w, v.w, t.w);
+          *reinterpret_cast<float4*>(d.weight + e) = a;
+          if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
+          if (nstate >= 3) {
+            *reinterpret_cast<float4*>(d.s1 + e) = v;
+            *reinterpret_cast<float4*>(d.s2 + e) = t;
+          }
         }
       }
     }
+    if (!FOLD) continue;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kGrpPer; ++i) {
+      const int gi = ga + threadIdx.x + i * kTileBlock;
+      if (gi < gb) fold_group<M>(d, buf, hot, gse[i], gtg[i]);
+    }
+    // Tiles with more groups than the prefetch covers fold the rest here.
+    for (int gi = ga + kGrpPer * kTileBlock + threadIdx.x; gi < gb; gi += kTileBlock)
+      fold_group<M>(d, buf, hot, d.grp_se[gi], d.grp_tgt[gi]);
+    __syncthreads();
   }
   if (!FOLD) return;
-  __syncthreads();
-  const int g1 = d.grp_off[blk + 1];
-  for (int gi = d.grp_off[blk] + threadIdx.x; gi < g1; gi += kTileBlock) {
-    const uint32_t se = d.grp_se[gi];
-    const int st = static_cast<int>(se & 0xFFFFu);
-    const int len = static_cast<int>(se >> 16);
-    float v = ident;
-    for (int j = st; j < st + len; ++j) v = Mono<M>::op(v, buf[sl[j]]);
-    const int tgt = d.grp_tgt[gi];
-    if (tgt >= 0)
-      d.cold_partial[tgt] = v;
-    else
-      hot[-1 - tgt] = v;
-  }
-  __syncthreads();
-  float* hp = d.hot_partial + static_cast<int64_t>(blk) * d.nhot;
+  float* hp = d.hot_sb + static_cast<int64_t>(blockIdx.x) * d.nhot;
   for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hp[j] = hot[j];
 }
 
-// Hot superblock sums: thread (h, superblock) folds the hot partials of the
-// superblock's tiles in tile order. Consecutive threads read consecutive
-// columns, so every load is coalesced.
+// Backward finalize of one row: combine its sum into acc and, where the row
+// finalizes, run the apply program and reset acc.
 template <int M>
-__global__ __launch_bounds__(kFwdBlock) void k_hot_sb(plx_partials_desc d) {
-  const int h = blockIdx.x * kFwdBlock + threadIdx.x;
-  if (h >= d.nhot) return;
-  const int sb = blockIdx.y;
-  const int k0 = sb * d.superblock;
-  const int k1 = min(k0 + d.superblock, d.ntiles);
-  const float* hp = d.hot_partial + h;
-  float s = Mono<M>::id();
-  for (int k = k0; k < k1; ++k) s = Mono<M>::op(s, hp[static_cast<int64_t>(k) * d.nhot]);
-  d.hot_sb[static_cast<int64_t>(sb) * d.nhot + h] = s;
-}
-
-// Backward finalize from tile partials: one row (source unit) per lane. A hot
-// row folds its superblock sums in order; a cold row folds its run of cold
-// partials (tile order), closing a superblock sum whenever the superblock id
-// changes. Then combine into acc and apply.
-template <int M>
-__global__ __launch_bounds__(kFwdBlock) void k_partials(plx_partials_desc d) {
-  const int r = blockIdx.x * kFwdBlock + threadIdx.x;
-  if (r >= d.nrows) return;
-  const int u = d.row_unit[r];
-  const float ident = Mono<M>::id();
-  float s = ident;
-  const int h = d.row_hot ? d.row_hot[r] : -1;
-  if (h >= 0) {
-    const int nsb = (d.ntiles + d.superblock - 1) / d.superblock;
-    for (int j = 0; j < nsb; ++j) s = Mono<M>::op(s, d.hot_sb[static_cast<int64_t>(j) * d.nhot + h]);
-  } else if (d.row_cold) {
-    const int j0 = d.row_cold[r], j1 = d.row_cold[r + 1];
-    if (j0 < j1) {
-      int cur = d.cold_sb[j0];
-      float q = ident;
-      for (int j = j0; j < j1; ++j) {
-        const int sb = d.cold_sb[j];
-        if (sb != cur) {
-          s = Mono<M>::op(s, q);
-          q = ident;
-          cur = sb;
-        }
-        q = Mono<M>::op(q, d.cold_partial[j]);
-      }
-      s = Mono<M>::op(s, q);
-    }
-  }
-  const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
-  if (finalizes(d.fin, u)) {
-    run_program(d.apply, u, a, 0.0f, true);
-    if (d.acc) d.acc[u] = ident;
+__device__ __forceinline__ void finish_row(const plx_partials_desc& d, const RowPre& pre, float s) {
+  const int u = pre.u;
+  const float a = Mono<M>::op(d.acc ? d.acc[u] : Mono<M>::id(), s);
+  if (pre.fin) {
+    run_program(d.apply, u, pre.f, a, 0.0f, true);
+    if (d.acc) d.acc[u] = Mono<M>::id();
   } else if (d.acc) {
     d.acc[u] = a;
   }
+}
+
+// Backward finalize of the hot rows (rows [0, nhot) are hot columns 0..nhot-1
+// in order): kHotCols columns per workgroup. The workgroup stages its columns
+// of hot_sb through LDS, kHotSbChunk superblocks at a time, with coalesced
+// loads, and each column's lane folds its superblock sums in order.
+constexpr int kHotCols = 64;
+constexpr int kHotSbChunk = 128;
+
+template <int M>
+__global__ __launch_bounds__(256) void k_hot_final(plx_partials_desc d) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* stage = reinterpret_cast<float*>(smem);  // [kHotSbChunk][kHotCols]
+  const int c0 = blockIdx.x * kHotCols;
+  const int ncol = min(kHotCols, d.nhot - c0);
+  const bool has = static_cast<int>(threadIdx.x) < ncol;
+  RowPre pre;
+  if (has) pre = prefetch_row(d.row_unit, c0 + threadIdx.x, d.fin, d.apply);
+  float s = Mono<M>::id();
+  constexpr int kPer = kHotSbChunk * kHotCols / 256;  // staged values per thread
+  for (int sb0 = 0; sb0 < d.nsuper; sb0 += kHotSbChunk) {
+    const int nsb = min(kHotSbChunk, d.nsuper - sb0);
+    // Issue every load of the chunk before storing any of it.
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int j = threadIdx.x + i * 256;
+      // Clamped into range: every load is unconditional (values past the
+      // chunk are staged but never folded).
+      const int sb = min(j / kHotCols, nsb - 1), c = min(j % kHotCols, ncol - 1);
+      v[i] = d.hot_sb[static_cast<int64_t>(sb0 + sb) * d.nhot + c0 + c];
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) stage[threadIdx.x + i * 256] = v[i];
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < ncol)
+      for (int sb = 0; sb < nsb; ++sb) s = Mono<M>::op(s, stage[sb * kHotCols + threadIdx.x]);
+    __syncthreads();
+  }
+  if (has) finish_row<M>(d, pre, s);
+}
+
+// Backward finalize of the other rows: workgroup k takes rows
+// [part_rows[k], part_rows[k+1]) (at most kPartBlock, one per lane, cut so
+// that their cold runs mostly fit one window). A workgroup's rows own one
+// contiguous range of the source-major cold arrays, which is staged through
+// LDS with coalesced loads; each row folds its run in tile order, closing a
+// superblock sum whenever the superblock id changes.
+constexpr int kPartBlock = 256;
+constexpr int kPartWin = 2048;
+
+template <int M>
+__global__ __launch_bounds__(kPartBlock) void k_partials(plx_partials_desc d) {
+  __shared__ float cval[kPartWin];
+  __shared__ uint16_t csb[kPartWin];
+  const int row0 = d.part_rows[blockIdx.x];
+  const int rend = d.part_rows[blockIdx.x + 1];
+  const int r = row0 + static_cast<int>(threadIdx.x);
+  const bool has = r < rend;
+  RowPre pre;
+  if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+  const float ident = Mono<M>::id();
+  float s = ident;
+  if (d.row_cold) {
+    const int c_begin = d.row_cold[row0], c_end = d.row_cold[rend];
+    const int j0 = has ? d.row_cold[r] : 0;
+    const int j1 = has ? d.row_cold[r + 1] : 0;
+    float q = ident;
+    int cur = -1;
+    for (int w0 = c_begin; w0 < c_end; w0 += kPartWin) {
+      const int wn = min(kPartWin, c_end - w0);
+      // Issue every load of the window before storing any of it.
+      constexpr int kPer = kPartWin / kPartBlock;
+      float pv[kPer];
+      uint16_t ps[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        // Clamped into range: every load is unconditional (entries past the
+        // window are staged but never folded).
+        const int j = min(static_cast<int>(threadIdx.x) + i * kPartBlock, wn - 1);
+        pv[i] = d.cold_partial[w0 + j];
+        ps[i] = d.cold_sb[w0 + j];
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        cval[threadIdx.x + i * kPartBlock] = pv[i];
+        csb[threadIdx.x + i * kPartBlock] = ps[i];
+      }
+      __syncthreads();
+      const int lo = max(j0, w0), hi = min(j1, w0 + wn);
+      for (int j = lo; j < hi; ++j) {
+        const int sb = csb[j - w0];
+        if (sb != cur) {
+          if (cur >= 0) s = Mono<M>::op(s, q);
+          q = ident;
+          cur = sb;
+        }
+        q = Mono<M>::op(q, cval[j - w0]);
+      }
+      __syncthreads();
+    }
+    if (cur >= 0) s = Mono<M>::op(s, q);
+  }
+  if (has) finish_row<M>(d, pre, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -480,7 +713,10 @@ __global__ __launch_bounds__(kPiece) void k_loss_pieces(int32_t n_out, const int
                                                        float* piece_sums) {
   __shared__ float terms[kPiece];
   const int k = blockIdx.x * kPiece + threadIdx.x;
-  if (k < n_out) terms[threadIdx.x] = run_program(P, ids[k], 0.0f, targets[k], true);
+  if (k < n_out) {
+    const int u = ids[k];
+    terms[threadIdx.x] = run_program(P, u, load_fields(P, u), 0.0f, targets[k], true);
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
     const int len = min(kPiece, n_out - static_cast<int>(blockIdx.x) * kPiece);
@@ -612,14 +848,23 @@ bool program_ok(const plx_program& p) {
   return p.ninstr >= 0 && p.ninstr <= PLX_MAX_INSTR && p.nout >= 0 && p.nout <= PLX_MAX_OUTS;
 }
 
-template <int RULE, int M, bool FOLD>
-void launch_tile(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+template <int RULE, int M, bool FOLD, bool SAME_G>
+void launch_tile_g(const plx_tile_desc& d, size_t lds, hipStream_t s) {
   // LDS beyond 64 KiB needs an explicit per-kernel opt-in.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD>),
+      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD, SAME_G>),
       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   (void)attr;
-  k_tile<RULE, M, FOLD><<<d.ntiles, kTileBlock, lds, s>>>(d);
+  // One workgroup per superblock of tiles.
+  k_tile<RULE, M, FOLD, SAME_G><<<static_cast<unsigned>(d.nsuper), kTileBlock, lds, s>>>(d);
+}
+
+template <int RULE, int M, bool FOLD>
+void launch_tile(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+  if (FOLD && RULE >= 0 && d.g == d.gfield)
+    launch_tile_g<RULE, M, FOLD, true>(d, lds, s);
+  else
+    launch_tile_g<RULE, M, FOLD, false>(d, lds, s);
 }
 
 template <int M, bool FOLD>
@@ -641,7 +886,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 1; }
+int32_t plx_abi_version(void) { return 2; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[6] = {
@@ -656,15 +901,13 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
   if (!d) return fail(PLX_ERR_INVALID, "plx_forward_bucket: null descriptor");
   if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_forward_bucket: negative nrows");
   if (d->nrows == 0) return PLX_OK;
-  if (!d->row_unit || !d->row_ptr || !d->src || !d->weight || !d->dead || !d->x)
+  if (!d->row_unit || !d->row_ptr || !d->src || !d->weight || !d->x)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: null column");
   if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_forward_bucket: bad program");
-  if (d->fin.fin_level >= 0 && !d->fin.level)
-    return fail(PLX_ERR_INVALID, "plx_forward_bucket: level needed");
-  if (d->fin.skip_inputs && !d->fin.is_input)
-    return fail(PLX_ERR_INVALID, "plx_forward_bucket: is_input needed");
+  if (!d->fin.level || !d->fin.is_input)
+    return fail(PLX_ERR_INVALID, "plx_forward_bucket: fin.level and fin.is_input are required");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned grid = grid_for(d->nrows, kFwdBlock);
+  const unsigned grid = grid_for(d->nrows, kFwdRows);
   switch (d->monoid) {
     case PLX_MONOID_SUM: k_forward<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
     case PLX_MONOID_PROD: k_forward<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
@@ -681,13 +924,13 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile_size must be a positive multiple of 4 <= 32768");
   if (d->base % 4 || d->end % 4 || d->end < d->base)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: base/end must be multiples of 4");
-  if ((d->end - d->base + d->tile_size - 1) / d->tile_size != d->ntiles)
-    return fail(PLX_ERR_INVALID, "plx_backward_tiles: ntiles does not cover [base, end)");
-  if (d->ntiles == 0) return PLX_OK;
+  if (d->ntiles == 0 || d->end == d->base) return PLX_OK;
+  if (d->nsuper <= 0 || d->nsuper > d->ntiles || !d->tile_pos || !d->super_tile)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile / superblock tables missing");
   if (!d->src || !d->dst || !d->dead || !d->weight)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
-  if (d->fold && (!d->grp_off || !d->grp_se || !d->grp_tgt || !d->sorted_local || !d->g ||
-                  (d->nhot > 0 && !d->hot_partial)))
+  if (d->fold && (!d->grp_off || !d->grp_se || !d->grp_tgt || !d->sorted_rank || !d->g ||
+                  (d->nhot > 0 && !d->hot_sb)))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: fold metadata missing");
   if (d->update && (!d->gfield || !d->act))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: update fields missing");
@@ -697,8 +940,8 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: Adam state columns missing");
   if (!d->fold && !d->update) return PLX_OK;
   if (d->fold && d->nhot < 0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: negative nhot");
-  const size_t lds = d->fold ? static_cast<size_t>(d->tile_size) * 6 +
-                                   static_cast<size_t>((d->nhot + 3) & ~3) * 4
+  const size_t lds = d->fold ? static_cast<size_t>(d->tile_size) * 4 +
+                                   static_cast<size_t>(d->nhot) * 4
                              : 0;
   if (lds > 160 * 1024) return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: tile does not fit in LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -723,35 +966,38 @@ int plx_backward_partials(const plx_partials_desc* d, void* stream) {
   if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_partials: negative nrows");
   if (d->nrows == 0) return PLX_OK;
   if (!d->row_unit) return fail(PLX_ERR_INVALID, "plx_backward_partials: null row_unit");
-  if (d->row_hot && (d->nhot < 0 || d->superblock <= 0 || d->ntiles < 0 ||
-                     (d->nhot > 0 && (!d->hot_partial || !d->hot_sb))))
+  if (d->nparts < 0 || (d->nparts > 0 && !d->part_rows))
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: part_rows missing");
+  if (d->row_hot && (d->nhot < 0 || d->nsuper < 0 || (d->nhot > 0 && !d->hot_sb)))
     return fail(PLX_ERR_INVALID, "plx_backward_partials: hot partials missing");
   if (d->row_cold && (!d->cold_partial || !d->cold_sb))
     return fail(PLX_ERR_INVALID, "plx_backward_partials: cold partials missing");
   if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_partials: bad program");
-  if (d->fin.fin_level >= 0 && !d->fin.level)
-    return fail(PLX_ERR_INVALID, "plx_backward_partials: level needed");
-  if (d->fin.skip_inputs && !d->fin.is_input)
-    return fail(PLX_ERR_INVALID, "plx_backward_partials: is_input needed");
+  if (!d->fin.level || !d->fin.is_input)
+    return fail(PLX_ERR_INVALID, "plx_backward_partials: fin.level and fin.is_input are required");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (d->row_hot && d->nhot > 0 && d->ntiles > 0) {
-    const dim3 g(grid_for(d->nhot, kFwdBlock), (d->ntiles + d->superblock - 1) / d->superblock);
+  const int nhot_rows = d->row_hot ? d->nhot : 0;
+  if (nhot_rows > d->nrows) return fail(PLX_ERR_INVALID, "plx_backward_partials: nhot > nrows");
+  if (nhot_rows > 0 && d->nsuper > 0) {
+    const unsigned hgrid = grid_for(nhot_rows, kHotCols);
+    const size_t lds = static_cast<size_t>(min(d->nsuper, kHotSbChunk)) * kHotCols * 4;
     switch (d->monoid) {
-      case PLX_MONOID_SUM: k_hot_sb<PLX_MONOID_SUM><<<g, kFwdBlock, 0, s>>>(*d); break;
-      case PLX_MONOID_PROD: k_hot_sb<PLX_MONOID_PROD><<<g, kFwdBlock, 0, s>>>(*d); break;
-      case PLX_MONOID_MAX: k_hot_sb<PLX_MONOID_MAX><<<g, kFwdBlock, 0, s>>>(*d); break;
-      case PLX_MONOID_MIN: k_hot_sb<PLX_MONOID_MIN><<<g, kFwdBlock, 0, s>>>(*d); break;
+      case PLX_MONOID_SUM: k_hot_final<PLX_MONOID_SUM><<<hgrid, 256, lds, s>>>(*d); break;
+      case PLX_MONOID_PROD: k_hot_final<PLX_MONOID_PROD><<<hgrid, 256, lds, s>>>(*d); break;
+      case PLX_MONOID_MAX: k_hot_final<PLX_MONOID_MAX><<<hgrid, 256, lds, s>>>(*d); break;
+      case PLX_MONOID_MIN: k_hot_final<PLX_MONOID_MIN><<<hgrid, 256, lds, s>>>(*d); break;
       default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
     }
     const int rc = check_launch("plx_backward_partials");
     if (rc) return rc;
   }
-  const unsigned grid = grid_for(d->nrows, kFwdBlock);
+  if (d->nparts <= 0) return PLX_OK;
+  const unsigned grid = static_cast<unsigned>(d->nparts);
   switch (d->monoid) {
-    case PLX_MONOID_SUM: k_partials<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_PROD: k_partials<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MAX: k_partials<PLX_MONOID_MAX><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MIN: k_partials<PLX_MONOID_MIN><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_SUM: k_partials<PLX_MONOID_SUM><<<grid, kPartBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_PROD: k_partials<PLX_MONOID_PROD><<<grid, kPartBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MAX: k_partials<PLX_MONOID_MAX><<<grid, kPartBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MIN: k_partials<PLX_MONOID_MIN><<<grid, kPartBlock, 0, s>>>(*d); break;
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
   }
   return check_launch("plx_backward_partials");

@@ -6,9 +6,12 @@ buckets and the scalar signals. Columns are torch tensors on the GPU
 (``cuda:0``), or on the CPU for host-only construction.
 
 Connection buckets are presented in the reference's *logical* slot order
-(``state.conns[b][name]``). The step itself runs on a physical,
-destination-sorted copy (plastax_amd._layout.Arena); after a step the logical
-columns are refreshed from it the first time they are read.
+(``state.conns[b][name]``) and unit columns in the caller's unit numbering.
+The step itself runs on a physical, destination-sorted copy of the edges with
+renumbered units (plastax_amd._layout.Arena): once a step has run, the unit
+columns live in the arena's unit order and ``state.units`` is a read view in
+the caller's numbering, rebuilt on first access after each step; the logical
+connection columns are refreshed from the arena the same way.
 """
 
 from __future__ import annotations
@@ -118,6 +121,8 @@ class NetworkState:
         self.tail_start = tail_start
         self._arena: Any = None  # plastax_amd._layout.Arena once a step ran
         self._arena_ahead = False  # the arena holds newer conn values
+        self._units_phys = False  # _units are in the arena's unit order
+        self._units_view: Columns | None = None  # cached caller-order view
         self._donated = False
 
     # -- donation -------------------------------------------------------------
@@ -144,19 +149,38 @@ class NetworkState:
         )
         new._arena = self._arena
         new._arena_ahead = self._arena_ahead
+        new._units_phys = self._units_phys
         self._donated = True
         return new
+
+    def _physical_units(self, arena: Any) -> Columns:
+        """The unit columns in ``arena``'s unit order (converted once); the
+        step updates them in place, so the caller-order view is dropped."""
+        if not self._units_phys:
+            self._units = arena.units_to_physical(self._units)
+            self._units_phys = True
+        self._units_view = None
+        return self._units
 
     # -- columns --------------------------------------------------------------
     @property
     def units(self) -> Columns:
+        """Unit columns in the caller's unit numbering. After a step this is
+        a read view of the device columns (rebuilt on first access after
+        each step): assign ``state.units = {...}`` to change values."""
         self._check()
-        return self._units
+        if not self._units_phys:
+            return self._units
+        if self._units_view is None:
+            self._units_view = self._arena.units_to_logical(self._units)
+        return self._units_view
 
     @units.setter
     def units(self, value: Columns) -> None:
         self._check()
         self._units = dict(value)
+        self._units_phys = False
+        self._units_view = None
 
     @property
     def conns(self) -> tuple[Columns, ...]:
@@ -171,6 +195,10 @@ class NetworkState:
     @conns.setter
     def conns(self, value: tuple[Columns, ...]) -> None:
         self._check()
+        if self._units_phys:  # the next arena may number units differently
+            self._units = self.units
+            self._units_phys = False
+            self._units_view = None
         self._conns = tuple(dict(b) for b in value)
         self._arena = None  # structure or values changed on the host side
         self._arena_ahead = False

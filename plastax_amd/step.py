@@ -20,7 +20,7 @@ import torch
 
 from plastax_amd import _lib
 from plastax_amd._expr import UnsupportedPolicyError
-from plastax_amd._layout import SUPERBLOCK, TILE, Arena
+from plastax_amd._layout import NSUPER, TILE, Arena
 from plastax_amd._plan import Plan, compile_plan, program_struct
 from plastax_amd._types import ACTIVATION, Propagation
 from plastax_amd.state import NetworkState, NetworkStatic
@@ -98,8 +98,10 @@ class StepFn:
         # kernel launch on the launching stream (the benchmark records HIP
         # events there).
         self.timer: Any = None
-        # Positions per backward tile of the arenas this step builds.
+        # Positions per backward tile, and superblocks per bucket at most, of
+        # the arenas this step builds.
         self.tile: int = TILE
+        self.nsuper: int = NSUPER
 
     def _launch(self, kind: str, fn: Any, *args: Any) -> None:
         timer = self.timer
@@ -110,28 +112,27 @@ class StepFn:
             timer.end(kind)
 
     # -- per-device constants ------------------------------------------------
-    def _consts(self, device: torch.device) -> dict[str, Any]:
+    def _consts(self, device: torch.device, arena: Arena) -> dict[str, Any]:
+        """Device constants of a step on ``arena``: input / output ids and the
+        input mask in the arena's unit order, and Adam's power table."""
         key = (device.type, device.index)
         if key not in self._dev_consts:
-            st = self.static
-            is_input = np.zeros(st.num_units, dtype=np.uint8)
-            if st.input_ids:
-                is_input[np.asarray(st.input_ids)] = 1
-            c = {
-                "input_ids": torch.tensor(st.input_ids, dtype=torch.int32, device=device),
-                "output_ids": torch.tensor(st.output_ids, dtype=torch.int32, device=device),
-                "is_input": torch.from_numpy(is_input).to(device),
-            }
+            c = {}
             if self.plan.update is not None and self.plan.update.rule_code == 2:
                 c["pow_table"] = torch.from_numpy(self.plan.pow_table()).to(device)
             self._dev_consts[key] = c
-        return self._dev_consts[key]
+        c = dict(self._dev_consts[key])
+        c["input_ids"] = arena.input_ids
+        c["output_ids"] = arena.output_ids
+        c["is_input"] = arena.is_input
+        return c
 
     def arena(self, state: NetworkState) -> Arena:
         """The state's physical arena (built on first use)."""
         if state._arena is None:
             state._arena = Arena(
-                self.static, state.units, state._conns, state.device, tile=self.tile
+                self.static, state.units, state._conns, state.device, tile=self.tile,
+                nsuper=self.nsuper,
             )
             state._arena_ahead = False
         return state._arena
@@ -145,9 +146,9 @@ class StepFn:
         lib = _lib.load()
         state = state._donate()
         arena = self.arena(state)
-        consts = self._consts(dev)
+        consts = self._consts(dev, arena)
         stream = _stream(dev)
-        units = state.units
+        units = state._physical_units(arena)
         n_units = self.static.num_units
 
         # Input scatter (step.py:598).
@@ -191,7 +192,9 @@ class StepFn:
             d.row_ptr = rows.ptr.data_ptr()
             d.src = arena.cols["from_id"].data_ptr()
             d.weight = arena.cols["weight"].data_ptr()
-            d.dead = arena.cols["dead"].data_ptr()
+            # Row ranges hold live positions only unless tombstones were set
+            # inside them after the layout was built.
+            d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
             d.x = units[fp.field].data_ptr()
             d.acc = acc.data_ptr() if acc is not None else None
             d.fin.level = fin_common["level"]
@@ -285,6 +288,9 @@ class StepFn:
         d.end = bt.end
         d.tile_size = arena.tile
         d.ntiles = bt.ntiles
+        d.nsuper = bt.nsuper
+        d.tile_pos = bt.tile_pos.data_ptr()
+        d.super_tile = bt.super_tile.data_ptr()
         d.fold = int(fold)
         d.update = int(update)
         d.src = arena.cols["from_id"].data_ptr()
@@ -298,8 +304,8 @@ class StepFn:
             d.grp_off = bt.grp_off.data_ptr()
             d.grp_se = bt.grp_se.data_ptr()
             d.grp_tgt = bt.grp_tgt.data_ptr()
-            d.sorted_local = bt.sorted_local.data_ptr()
-            d.hot_partial = bt.hot_partial.data_ptr()
+            d.sorted_rank = bt.sorted_rank.data_ptr()
+            d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
             d.g = units[bp.field].data_ptr()
         if update:
@@ -323,14 +329,14 @@ class StepFn:
         d = _lib.plx_partials_desc()
         d.nrows = bt.nrows
         d.monoid = plan.backward.monoid
-        d.ntiles = bt.ntiles
+        d.nsuper = bt.nsuper
         d.nhot = bt.nhot
-        d.superblock = SUPERBLOCK
+        d.nparts = bt.nparts
+        d.part_rows = bt.part_rows.data_ptr() if bt.part_rows is not None else None
         d.row_unit = bt.rows.data_ptr()
         if bt.row_hot is not None:
             d.row_hot = bt.row_hot.data_ptr()
             d.row_cold = bt.row_cold.data_ptr()
-            d.hot_partial = bt.hot_partial.data_ptr()
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
             d.cold_sb = bt.cold_sb.data_ptr()
@@ -375,4 +381,34 @@ class StepFn:
             else:
                 todo = range(1)  # bucket 0 is never reduced, only updated
             for b in todo:
-                self._tiles(plan, arena, units, consts, b, False, True, stream)
+                self._update_only(plan, arena, units, consts, b, stream)
+
+    def _update_only(self, plan: Plan, arena: Arena, units: dict, consts: dict, b: int,
+                     stream: int) -> None:
+        """A bucket the walk never reduces: the update rule alone, one 16-byte
+        quad of positions per lane (phases.py:1196-1242)."""
+        lib = _lib.load()
+        up = plan.update
+        bt = arena.bwd[b]
+        d = _lib.plx_update_desc()
+        d.n = bt.end - bt.base
+        d.rule = up.rule_code
+
+        def col(name: str) -> int:
+            t = arena.cols[name]
+            return t.data_ptr() + bt.base * t.element_size()
+
+        d.src = col("from_id")
+        d.dst = col("to_id")
+        d.dead = col("dead")
+        d.weight = col("weight")
+        for k, name in enumerate(up.state_columns()):
+            setattr(d, f"s{k}", col(name))
+        d.gfield = units[up.grad_field.name].data_ptr()
+        d.act = units[ACTIVATION.name].data_ptr()
+        if "pow_table" in consts:
+            d.pow_table = consts["pow_table"].data_ptr()
+            d.pow_table_len = consts["pow_table"].numel() // 2
+        for k, v in enumerate(up.params()):
+            d.p[k] = float(v)
+        self._launch("update_conn", lib.plx_update_conn, d, stream)

@@ -41,7 +41,7 @@ def test_descriptor_layouts_match_the_header(lib) -> None:
     out = (ctypes.c_int64 * 6)()
     assert lib.plx_struct_sizes(out, 6) == 6
     assert list(out) == [ctypes.sizeof(s) for s in _lib.STRUCTS]
-    assert lib.plx_abi_version() == 1
+    assert lib.plx_abi_version() == _lib.ABI_VERSION
 
 
 def test_argument_errors_are_reported_not_raised(lib) -> None:

@@ -164,11 +164,16 @@ def test_softmax_ce_golden_on_device(name: str) -> None:
 # ---------------------------------------------------------------------------
 
 
-def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None):
-    o = nets.oracle_for(oracle, net, static, state, **({} if tile is None else {"tile": tile}))
+def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None, nsuper=None):
+    kw = {} if tile is None else {"tile": tile}
+    if nsuper is not None:
+        kw["nsuper"] = nsuper
+    o = nets.oracle_for(oracle, net, static, state, **kw)
     step = px.make_step(net, static)
     if tile is not None:
         step.tile = tile
+    if nsuper is not None:
+        step.nsuper = nsuper
     for k in range(1, steps + 1):
         x, t = inputs_fn(k)
         res = step(state, px.StepInputs(x, t))
@@ -227,10 +232,10 @@ def test_topological_zipf_net_bit_exact(oracle, opt_name: str) -> None:
     _run_both(net, static, state, oracle, inputs, 12, {1, 12})
 
 
-@pytest.mark.parametrize("tile", [64, 1024])
-def test_many_tiles_and_hot_sources_bit_exact(oracle, tile: int) -> None:
-    """Small tiles: many tiles per bucket, the Zipf head lands in the dense
-    hot partials and the tail in the cold runs."""
+@pytest.mark.parametrize("tile,nsuper", [(64, 512), (1024, 512), (64, 5), (256, 37)])
+def test_many_tiles_and_hot_sources_bit_exact(oracle, tile: int, nsuper: int) -> None:
+    """Small tiles: many tiles per superblock, the Zipf head lands in the
+    workgroups' hot running sums and the tail in the cold runs."""
     e = synth.c2_topological(seed=8, scale=128)
     net = nets.make_trained_net(f"T{tile}", nets.TanhForward(), nets.TanhBackward(),
                                 px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
@@ -244,7 +249,7 @@ def test_many_tiles_and_hot_sources_bit_exact(oracle, tile: int) -> None:
         x = rng.standard_normal(width).astype(np.float32)
         return x, np.tanh(x[::-1]).astype(np.float32)
 
-    _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile)
+    _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile, nsuper=nsuper)
 
 
 def test_dead_slots_and_headroom_bit_exact(oracle) -> None:

@@ -17,11 +17,12 @@ import plastax_amd as px
 from plastax_amd import _layout, synth
 
 
-def _arena(net, e, tile, **kw):
+def _arena(net, e, tile, nsuper=_layout.NSUPER, **kw):
     static, state = px.NetworkBuilder.from_edges(
         net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
         output_ids=e.output_ids, globals_=None, device="cpu", **kw)
-    arena = _layout.Arena(static, state.units, state.conns, torch.device("cpu"), tile=tile)
+    arena = _layout.Arena(static, state.units, state.conns, torch.device("cpu"), tile=tile,
+                          nsuper=nsuper)
     return static, state, arena
 
 
@@ -58,42 +59,62 @@ def _check_arena(static, state, arena) -> None:
         assert (np.diff(key) > 0).all()
 
 
-def _emulate_fold(arena, b, g_field: np.ndarray):
-    """The device's tile fold + partials fold, in numpy float32."""
+def _emulate_fold(arena, b, g_logical: np.ndarray):
+    """The device's superblock/tile fold + partials fold, in numpy float32.
+    Takes the grad field in the caller's unit numbering; returns sums keyed by
+    the caller's unit ids."""
+    g_field = g_logical[arena.uperm]  # the device's unit order
     bt = arena.bwd[b]
     T = arena.tile
     w = _np(arena.cols["weight"])
     dst = _np(arena.cols["to_id"])
     dead = _np(arena.cols["dead"]).astype(bool)
-    sl = _np(bt.sorted_local).view(np.uint16)
+    rank = _np(bt.sorted_rank).view(np.uint16)
     off = _np(bt.grp_off)
     se = _np(bt.grp_se).view(np.uint32)
     tgt = _np(bt.grp_tgt)
-    nhot = bt.nhot
-    hot = np.zeros(bt.ntiles * nhot, np.float32)
+    tile_pos = _np(bt.tile_pos)
+    super_tile = _np(bt.super_tile)
+    nhot, nsuper = bt.nhot, bt.nsuper
+    assert tile_pos[0] == 0 and tile_pos[-1] == bt.end - bt.base and (np.diff(tile_pos) > 0).all()
+    assert (np.diff(tile_pos) <= T).all() and (tile_pos % 4 == 0).all()
+    assert super_tile[0] == 0 and super_tile[-1] == bt.ntiles and (np.diff(super_tile) > 0).all()
+    hot_sb = np.zeros(nsuper * nhot, np.float32)
     cold = np.zeros(_np(bt.cold_partial).size, np.float32)
     seen = np.zeros(bt.end - bt.base, np.int64)
-    for k in range(bt.ntiles):
-        t0 = bt.base + k * T
-        n = min(T, bt.end - t0)
-        assert off[k] <= off[k + 1]
-        for gi in range(off[k], off[k + 1]):
-            st, ln = int(se[gi] & 0xFFFF), int(se[gi] >> 16)
-            assert ln >= 1 and st + ln <= n
-            v = np.float32(0.0)
-            for j in range(st, st + ln):
-                loc = int(sl[k * T + j])
-                assert loc < n
-                e = t0 + loc
-                assert not dead[e]
-                seen[e - bt.base] += 1
-                v = np.float32(v + np.float32(w[e] * g_field[dst[e]]))
-            if tgt[gi] >= 0:
-                cold[tgt[gi]] = v
-            else:
-                h = -1 - tgt[gi]
-                assert 0 <= h < nhot
-                hot[k * nhot + h] = v
+    for sb in range(nsuper):
+        run = np.zeros(nhot, np.float32)
+        for k in range(super_tile[sb], super_tile[sb + 1]):
+            t0 = bt.base + tile_pos[k]
+            n = tile_pos[k + 1] - tile_pos[k]
+            assert off[k] <= off[k + 1]
+            # the tile's live positions, placed at their source-sorted rank
+            order = np.full(n, -1, np.int64)
+            for p in range(n):
+                if not dead[t0 + p]:
+                    r = int(rank[tile_pos[k] + p])
+                    assert r < n and order[r] == -1
+                    order[r] = p
+            touched = set()
+            for gi in range(off[k], off[k + 1]):
+                st, ln = int(se[gi] & 0xFFFF), int(se[gi] >> 16)
+                assert ln >= 1 and st + ln <= n
+                v = np.float32(0.0)
+                for j in range(st, st + ln):
+                    loc = int(order[j])
+                    assert 0 <= loc < n
+                    e = t0 + loc
+                    assert not dead[e]
+                    seen[e - bt.base] += 1
+                    v = np.float32(v + np.float32(w[e] * g_field[dst[e]]))
+                if tgt[gi] >= 0:
+                    cold[tgt[gi]] = v
+                else:
+                    h = -1 - tgt[gi]
+                    assert 0 <= h < nhot and h not in touched  # one writer per tile
+                    touched.add(h)
+                    run[h] = np.float32(run[h] + v)
+        hot_sb[sb * nhot : (sb + 1) * nhot] = run
     live = arena.lives[b]
     assert (seen[:live] == 1).all() and (seen[live:] == 0).all()
     rows = _np(bt.rows)
@@ -101,16 +122,20 @@ def _emulate_fold(arena, b, g_field: np.ndarray):
     row_cold = _np(bt.row_cold)
     assert row_cold[0] == 0 and (np.diff(row_cold) >= 0).all() and row_cold[-1] == cold.size or (cold.size == 1 and row_cold[-1] == 0)
     cold_sb = _np(bt.cold_sb).view(np.uint16)
-    SB = _layout.SUPERBLOCK
+    # the finalize kernel relies on hot rows coming first, in column order,
+    # and on the cold workgroups covering the other rows, 256 at most each
+    assert (row_hot[:nhot] == np.arange(nhot)).all() and (row_hot[nhot:] == -1).all()
+    parts = _np(bt.part_rows)
+    assert bt.nparts == parts.size - 1 and parts[0] == nhot and parts[-1] == rows.size
+    assert (np.diff(parts) > 0).all() and (np.diff(parts) <= _layout.PART_ROWS).all()
+    one_row = np.diff(parts) == 1
+    assert (np.diff(row_cold[parts])[~one_row] <= _layout.PART_WIN).all()
     out = {}
     for r in range(rows.size):
         s = np.float32(0.0)
         if row_hot[r] >= 0:
-            for k0 in range(0, bt.ntiles, SB):
-                q = np.float32(0.0)
-                for k in range(k0, min(k0 + SB, bt.ntiles)):
-                    q = np.float32(q + hot[k * nhot + row_hot[r]])
-                s = np.float32(s + q)
+            for sb in range(nsuper):
+                s = np.float32(s + hot_sb[sb * nhot + row_hot[r]])
         else:
             j0, j1 = row_cold[r], row_cold[r + 1]
             if j0 < j1:
@@ -120,18 +145,20 @@ def _emulate_fold(arena, b, g_field: np.ndarray):
                         s, q, cur = np.float32(s + q), np.float32(0.0), cold_sb[j]
                     q = np.float32(q + cold[j])
                 s = np.float32(s + q)
-        out[int(rows[r])] = s
+        out[int(arena.uperm[rows[r]])] = s
     return out
 
 
-@pytest.mark.parametrize("tile", [64, 256])
-def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int) -> None:
+@pytest.mark.parametrize("tile,nsuper", [(64, 512), (256, 512), (64, 7), (96, 3)])
+def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int, nsuper: int) -> None:
     e = synth.c2_topological(seed=2, scale=512, layers=4)
     net = nets.make_trained_net("L", nets.TanhForward(), nets.TanhBackward(),
                                 px.optim.sgd(0.1, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
-    static, state, arena = _arena(net, e, tile)
+    static, state, arena = _arena(net, e, tile, nsuper=nsuper)
     _check_arena(static, state, arena)
-    o = nets.oracle_for(oracle, net, static, state, tile=tile)
+    if nsuper < 512:
+        assert any(np.diff(_np(arena.bwd[b].super_tile)).max() > 1 for b in range(1, arena.num_buckets))
+    o = nets.oracle_for(oracle, net, static, state, tile=tile, nsuper=nsuper)
     rng = np.random.default_rng(0)
     g = rng.standard_normal(static.num_units).astype(np.float32)
     o.units["grad_pre_act"][:] = g
@@ -194,5 +221,61 @@ def test_write_logical_round_trips() -> None:
             assert torch.equal(b0[k], b1[k]), k
 
 
+def test_unit_order_agrees_with_the_oracle_restatement(oracle) -> None:
+    """The arena's unit renumbering (level, out-degree descending, id) and the
+    oracle's independent restatement agree, and hot sources come first in
+    their level."""
+    e = synth.c2_topological(seed=3, scale=256, layers=5)
+    net = nets.make_trained_net("UO", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.sgd(0.1, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state, arena = _arena(net, e, 256)
+    conns = [{k: v.numpy().astype(bool) if k == "dead" else v.numpy() for k, v in b.items()}
+             for b in state.conns]
+    index = oracle.physical_unit_index(state.units["level"].numpy(), conns)
+    assert np.array_equal(index, arena.uinv)
+    assert np.array_equal(arena.uperm[arena.uinv], np.arange(static.num_units))
+    levels = state.units["level"].numpy()[arena.uperm]
+    assert (np.diff(levels) >= 0).all()
+    deg = np.bincount(e.src, minlength=static.num_units)[arena.uperm]
+    for lv in range(levels.max() + 1):
+        d = deg[levels == lv]
+        assert (np.diff(d) <= 0).all()
+
+
+def test_units_round_trip_through_the_physical_order() -> None:
+    e = synth.c2_topological(seed=7, scale=1024, layers=3)
+    net = nets.make_trained_net("UR", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.sgd(0.1, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state, arena = _arena(net, e, 64)
+    units = {k: v.clone() for k, v in state.units.items()}
+    phys = arena.units_to_physical(units)
+    back = arena.units_to_logical(phys)
+    for k in units:
+        assert torch.equal(units[k], back[k])
+    lv = phys["level"].numpy()
+    assert (np.diff(lv) >= 0).all()
+
+
 def test_oracle_and_device_agree_on_the_default_tile(oracle) -> None:
-    assert oracle.TILE == _layout.TILE
+    assert oracle.TILE == _layout.TILE and oracle.NSUPER == _layout.NSUPER
+
+
+@pytest.mark.parametrize("span,tile,nsuper", [
+    (4, 4, 512), (8, 4, 512), (12, 8, 2), (100, 64, 512), (1000, 64, 16), (4096, 4096, 512),
+    (4100, 4096, 512), (9590016, 4096, 512), (9590016 + 4, 8192, 512), (123456, 96, 7),
+])
+def test_tile_partition_agrees_with_the_oracle_restatement(oracle, span, tile, nsuper) -> None:
+    """Two independent restatements of the tiling (the layout's tables and
+    the oracle's per-position ids) describe the same partition, whose
+    superblocks have near-equal length and whose tiles fit the tile size."""
+    tile_pos, super_tile = _layout.tile_partition(span, tile, nsuper)
+    t_ix, s_ix = oracle.tiles_of_positions(span, tile, nsuper)
+    pos = np.arange(span)
+    t_of = np.searchsorted(tile_pos, pos, side="right") - 1
+    s_of = np.searchsorted(super_tile, t_of, side="right") - 1
+    assert np.array_equal(t_of, t_ix) and np.array_equal(s_of, s_ix)
+    lens = np.diff(tile_pos)
+    assert (lens > 0).all() and (lens <= tile).all() and (tile_pos % 4 == 0).all()
+    sb_len = tile_pos[super_tile[1:]] - tile_pos[super_tile[:-1]]
+    assert super_tile.size - 1 == min(nsuper, -(-span // tile))
+    assert sb_len.max() - sb_len.min() <= 8
