@@ -87,6 +87,8 @@ typedef struct plx_finalize {
 typedef struct plx_forward_desc {
   int32_t nrows;
   int32_t monoid;
+  int32_t tbl_base; /* x[tbl_base, tbl_base + tbl_len) is staged in LDS    */
+  int32_t tbl_len;  /* (at most 8192; 0: none)                             */
   const int32_t* row_unit; /* [nrows] destination unit ids, ascending      */
   const int32_t* row_ptr;  /* [nrows+1] physical positions                 */
   const int32_t* src;      /* [positions] FROM_ID                          */
@@ -119,7 +121,7 @@ PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
  * sorted_rank[p - base] is the rank of live position p in its tile's
  * (source, position) order; grp_off[tile..tile+1] ranges the tile's groups;
  * grp_se packs a group's first rank (low 16 bits) and length (high 16
- * bits); tile_size is at most 65536. */
+ * bits); tile_size is at most 4096. */
 typedef struct plx_tile_desc {
   int64_t base;
   int64_t end;
@@ -132,7 +134,12 @@ typedef struct plx_tile_desc {
   int32_t nhot;
   int32_t rule;
   int32_t pow_table_len;
-  int32_t reserved;
+  int32_t tbl_base; /* act[tbl_base, tbl_base + tbl_len) is staged in LDS  */
+  int32_t tbl_len;  /* (at most 8192; 0: none)                             */
+  int64_t live_end; /* with dead == null: positions >= live_end are dead   */
+  int32_t step_mode; /* Adam: 0 per-edge step count s2; 1 every live edge  */
+  float step_t;      /* has the step count step_t (s2 neither read nor      */
+                     /* written; the caller advances step_t after the call) */
   const int32_t* tile_pos;   /* [ntiles+1] tile starts relative to base   */
   const int32_t* super_tile; /* [nsuper+1] first tile of each superblock  */
   const int32_t* grp_off;
@@ -189,6 +196,12 @@ typedef struct plx_partials_desc {
 
 PLX_EXPORT int plx_backward_partials(const plx_partials_desc* d, void* stream);
 
+/* Source-value tables: a bucket's sources are renumbered most-used first,
+ * so the values of its busiest sources are one contiguous slice of the
+ * gathered column; kernels copy that slice into LDS once per workgroup and
+ * gather those sources from it (bit-identical values, fewer cache requests). */
+#define PLX_MAX_TBL 8192
+
 /* Connection update over physical positions [0, n): build_update_conn_phase
  * (phases.py:1196-1242, sweep.py:488-532) for the optim bundles. grad =
  * gfield[dst] * act[src]; dead rows keep their values.
@@ -198,11 +211,17 @@ PLX_EXPORT int plx_backward_partials(const plx_partials_desc* d, void* stream);
  *             s0=opt/m s1=opt/v s2=opt/t     (_adam.py:154-172)
  *   RMSPROP:  p0=lr p1=decay p2=1-decay p3=eps  s0=opt/v (_rmsprop.py:135-140)
  * pow_table (optional, Adam) holds float32(b1^t), float32(b2^t) at [2t], [2t+1]
- * for t < pow_table_len; other t are computed on the device the same way. */
+ * for t < pow_table_len; other t are computed on the device the same way.
+ * `dead` may be null: positions >= live_end are then the dead ones. */
 typedef struct plx_update_desc {
   int64_t n;
   int32_t rule;
   int32_t pow_table_len;
+  int32_t tbl_base; /* act[tbl_base, tbl_base + tbl_len) is staged in LDS  */
+  int32_t tbl_len;  /* (at most 8192; 0: none)                             */
+  int64_t live_end; /* with dead == null: positions >= live_end are dead   */
+  int32_t step_mode; /* as plx_tile_desc                                   */
+  float step_t;
   const int32_t* src;
   const int32_t* dst;
   const uint8_t* dead;

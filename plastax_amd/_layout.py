@@ -49,10 +49,11 @@ import torch
 from plastax_amd._types import DEAD, FROM_ID, TO_ID, Propagation
 from plastax_amd.state import Columns, NetworkStatic, column_to_numpy, torch_dtype
 
-TILE = 4096  # positions per backward tile (multiple of 4, <= 32768)
+TILE = 4096  # positions per backward tile (multiple of 4, <= 4096: one device pass)
 NSUPER = 512  # superblocks per bucket at most (device workgroups: 2 per CU)
 HOT_PER_SUPER = 0.25  # hot iff present in more than this many tiles per superblock
 MAX_HOT = 8192  # hot running sums per workgroup (LDS: 4 B each)
+MAX_TBL = 8192  # source values staged in LDS per workgroup (PLX_MAX_TBL)
 PAD = 256  # slack positions after each slab (vector loads may run past the end)
 PART_ROWS = 256  # cold finalize: rows per workgroup at most (one per lane)
 PART_WIN = 2048  # cold finalize: cold partials staged per window
@@ -164,8 +165,8 @@ class Arena:
         tile: int = TILE,
         nsuper: int = NSUPER,
     ) -> None:
-        if tile <= 0 or tile % 4 or tile > 32768:
-            raise ValueError("tile must be a positive multiple of 4, at most 32768")
+        if tile <= 0 or tile % 4 or tile > 4096:
+            raise ValueError("tile must be a positive multiple of 4, at most 4096")
         if not 1 <= nsuper <= 65535:
             raise ValueError("nsuper must be in [1, 65535]")
         self.static = static
@@ -225,6 +226,10 @@ class Arena:
         # Live positions come first in every bucket, so no forward row range
         # holds a tombstone until one is set in place after this build.
         self.dead_in_rows = False
+        # Adam's step count when every live edge of a bucket holds the same
+        # one (per bucket; None: the per-edge column is authoritative).
+        self.t_name: str | None = None
+        self.t_now: list[float | None] = []
         for b in range(nb):
             base, cap = self.bases[b], caps[b]
             dead = host[DEAD.name][b]
@@ -399,6 +404,40 @@ class Arena:
                 if name in (FROM_ID.name, TO_ID.name):
                     vals = self.uperm_t[vals.long()].to(col.dtype)
                 col[idx] = vals
+                if name == self.t_name and self.t_now and self.t_now[b] is not None:
+                    col[idx[: self.lives[b]]] = self.t_now[b]
+
+    def init_uniform_t(self, t_name: str) -> None:
+        """Adam's per-edge step count: where every live edge of a bucket holds
+        the same integer count below 2^23 (each step adds exactly 1.0 to
+        every live edge, so they stay equal), keep it as one number per
+        bucket; the kernels then neither read nor write that column."""
+        self.t_name = t_name
+        col = self.cols[t_name]
+        self.t_now = []
+        for b in range(self.num_buckets):
+            live = col[self.bases[b] : self.bases[b] + self.lives[b]]
+            t = None
+            if live.numel():
+                lo, hi = float(live.min()), float(live.max())
+                if lo == hi and lo == int(lo) and 0.0 <= lo < 2.0**23:
+                    t = lo
+            self.t_now.append(t)
+
+    def live_end(self, b: int) -> int:
+        """End of bucket b's live positions (live edges come first)."""
+        return self.bases[b] + self.lives[b]
+
+    def src_table(self, b: int) -> tuple[int, int]:
+        """(base, len) of bucket b's source-value table: its busiest sources,
+        the first physical ids of the sources' level (all units for a
+        PIPELINE bucket), at most PLX_MAX_TBL of them."""
+        if self.pipeline:
+            return 0, min(MAX_TBL, self.static.num_units)
+        if b + 1 >= self.lvl_start.size:
+            return 0, 0
+        lo, hi = int(self.lvl_start[b]), int(self.lvl_start[b + 1])
+        return lo, min(MAX_TBL, hi - lo)
 
     def units_to_physical(self, units: Columns) -> Columns:
         """Unit columns in the caller's numbering -> physical order."""

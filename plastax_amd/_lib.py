@@ -18,12 +18,13 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 2  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 4  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
 PLX_MAX_FIELDS = 8
 PLX_MAX_OUTS = 4
+PLX_MAX_TBL = 8192
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -62,6 +63,8 @@ class plx_forward_desc(ctypes.Structure):
     _fields_ = [
         ("nrows", c_i32),
         ("monoid", c_i32),
+        ("tbl_base", c_i32),
+        ("tbl_len", c_i32),
         ("row_unit", c_vp),
         ("row_ptr", c_vp),
         ("src", c_vp),
@@ -87,7 +90,11 @@ class plx_tile_desc(ctypes.Structure):
         ("nhot", c_i32),
         ("rule", c_i32),
         ("pow_table_len", c_i32),
-        ("reserved", c_i32),
+        ("tbl_base", c_i32),
+        ("tbl_len", c_i32),
+        ("live_end", c_i64),
+        ("step_mode", c_i32),
+        ("step_t", c_f32),
         ("tile_pos", c_vp),
         ("super_tile", c_vp),
         ("grp_off", c_vp),
@@ -137,6 +144,11 @@ class plx_update_desc(ctypes.Structure):
         ("n", c_i64),
         ("rule", c_i32),
         ("pow_table_len", c_i32),
+        ("tbl_base", c_i32),
+        ("tbl_len", c_i32),
+        ("live_end", c_i64),
+        ("step_mode", c_i32),
+        ("step_t", c_f32),
         ("src", c_vp),
         ("dst", c_vp),
         ("dead", c_vp),

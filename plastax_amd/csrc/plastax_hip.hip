@@ -214,6 +214,50 @@ __device__ __forceinline__ RowPre prefetch_row(const int32_t* row_unit, int r,
 }
 
 // ---------------------------------------------------------------------------
+// Source-value tables. Units are numbered most-used source first within each
+// level, so the values a bucket gathers most are one contiguous slice
+// x[base, base + len); a workgroup copies it into LDS once and gathers those
+// sources from there (the same bits, without an L1/L2 request per lane).
+// ---------------------------------------------------------------------------
+constexpr int kTbl = PLX_MAX_TBL;
+
+// Copies x[base, base + len) into tbl with every load issued before any LDS
+// store (len <= CAP; the caller synchronises before use).
+template <int BLOCK, int CAP = kTbl>
+__device__ __forceinline__ void stage_table(float* tbl, const float* x, int base, int len) {
+  if (len <= 0) return;
+  constexpr int kPer = (CAP + BLOCK - 1) / BLOCK;
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) v[i] = x[base + min(static_cast<int>(threadIdx.x) + i * BLOCK, len - 1)];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = threadIdx.x + i * BLOCK;
+    if (j < len) tbl[j] = v[i];
+  }
+}
+
+// Gathers K values x[idx[k]] (lanes with use[k] false read the table's first
+// entry, or x[0] without a table, and their value is ignored): table hits
+// read LDS, the rest issue one global load each, all before any is used.
+template <int K>
+__device__ __forceinline__ void gather_k(const float* tbl, const float* x, int base, int len,
+                                         const int* idx, const bool* use, float* out) {
+  int o[K];
+  bool in[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = use[k] ? idx[k] : (len > 0 ? base : 0);
+    o[k] = i - base;
+    in[k] = static_cast<unsigned>(o[k]) < static_cast<unsigned>(len);
+    if (!in[k]) out[k] = x[i];
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (in[k]) out[k] = tbl[o[k]];
+}
+
+// ---------------------------------------------------------------------------
 // Forward: kFwdRows rows (destination units) per workgroup, one row per lane
 // of the first kFwdRows lanes. The rows own a contiguous physical range; the
 // whole workgroup streams it through LDS in windows of kFwdWin terms with
@@ -227,6 +271,10 @@ constexpr int kFwdBlock = 256;
 #ifndef PLX_FWD_ROWS
 #define PLX_FWD_ROWS 32
 #endif
+#ifndef PLX_FWD_TBL
+#define PLX_FWD_TBL 1024
+#endif
+constexpr int kFwdTbl = PLX_FWD_TBL;  // the forward's workgroups are small: a short table
 constexpr int kFwdRows = PLX_FWD_ROWS;
 #ifndef PLX_FWD_QUADS
 #define PLX_FWD_QUADS 4
@@ -237,6 +285,10 @@ constexpr int kFwdWin = 4 * kFwdQuads * kFwdBlock;
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   __shared__ __align__(16) float buf[kFwdWin];
+  __shared__ float tbl[kFwdTbl];
+  const int tlen = min(d.tbl_len, kFwdTbl);
+  stage_table<kFwdBlock, kFwdTbl>(tbl, d.x, d.tbl_base, tlen);
+  __syncthreads();
   const int row0 = blockIdx.x * kFwdRows;
   const int rend = min(row0 + kFwdRows, d.nrows);
   const int e_begin = d.row_ptr[row0];
@@ -266,8 +318,8 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
         if (d.dead) dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
       }
     }
-    // Only positions of this workgroup's rows contribute; the others gather
-    // unit 0, so every gather is unconditional and issued before any use.
+    // Only positions of this workgroup's rows contribute; every gather is
+    // issued before any is used.
     bool ok[kFwdQuads][4];
     float xv[kFwdQuads][4];
 #pragma unroll
@@ -276,10 +328,9 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
       const bool in = 4 * (threadIdx.x + i * kFwdBlock) < wn;
       const int idx[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 4; ++k)
         ok[i][k] = in && e + k >= e_begin && e + k < e_end && !((dv[i] >> (8 * k)) & 0xFFu);
-        xv[i][k] = d.x[ok[i][k] ? idx[k] : 0];
-      }
+      gather_k<4>(tbl, d.x, d.tbl_base, tlen, idx, ok[i], xv[i]);
     }
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
@@ -295,7 +346,19 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
     }
     __syncthreads();
     const int lo = max(my_b, w0), hi = min(my_e, w0 + wn);
-    for (int e = lo; e < hi; ++e) s = Mono<M>::op(s, buf[e - w0]);
+    {
+      const float* run = buf + (lo - w0);
+      const int len = hi - lo;
+      int j = 0;
+      for (; j + 4 <= len; j += 4) {
+        const float a0 = run[j], a1 = run[j + 1], a2 = run[j + 2], a3 = run[j + 3];
+        s = Mono<M>::op(s, a0);
+        s = Mono<M>::op(s, a1);
+        s = Mono<M>::op(s, a2);
+        s = Mono<M>::op(s, a3);
+      }
+      for (; j < len; ++j) s = Mono<M>::op(s, run[j]);
+    }
     __syncthreads();
   }
   if (!has) return;
@@ -352,47 +415,93 @@ __device__ __forceinline__ void update_one(const D& d, float grad, float& w, flo
   }
 }
 
-template <int RULE>
+// Adam with the step count shared by every live edge of the launch: the
+// same float32 operations as update_one<ADAM>, with the bias-correction
+// denominators 1 - b^step computed once.
+template <class D>
+__device__ __forceinline__ void adam_uniform(const D& d, float grad, float den1, float den2,
+                                             float& w, float& m, float& v) {
+  const float weight = w;
+  const float mm = d.p[1] * m + d.p[5] * grad;
+  const float vv = d.p[2] * v + d.p[6] * (grad * grad);
+  const float m_hat = mm / den1;
+  const float v_hat = vv / den2;
+  const float dir = m_hat / (sqrtf(v_hat) + d.p[3]);
+  const float upd = d.p[0] * (dir + d.p[4] * weight);
+  w = weight - upd;
+  m = mm;
+  v = vv;
+}
+
+// Applies the rule to one edge: per-edge step count (state s2) or, with
+// UNI_T, the launch's shared one (den1/den2 precomputed; s2 untouched).
+template <int RULE, bool UNI_T, class D>
+__device__ __forceinline__ void update_edge(const D& d, float grad, float den1, float den2,
+                                            float& w, float& s0, float& s1, float& s2) {
+  if (RULE == PLX_RULE_ADAM && UNI_T)
+    adam_uniform(d, grad, den1, den2, w, s0, s1);
+  else
+    update_one<RULE>(d, grad, w, s0, s1, s2);
+}
+
+// Dead-byte mask of the quad at position e when the caller passes no DEAD
+// column: positions at or past live_end are dead.
+__device__ __forceinline__ uint32_t dead_from_end(int64_t e, int64_t live_end) {
+  return (e + 0 >= live_end ? 0x000000FFu : 0u) | (e + 1 >= live_end ? 0x0000FF00u : 0u) |
+         (e + 2 >= live_end ? 0x00FF0000u : 0u) | (e + 3 >= live_end ? 0xFF000000u : 0u);
+}
+
+// One 16-byte quad of positions per lane per iteration, the workgroups
+// striding over the bucket (each stages its act table once).
+template <int RULE, bool UNI_T>
 __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
-  const int64_t e = 4 * (static_cast<int64_t>(blockIdx.x) * kUpdBlock + threadIdx.x);
-  if (e >= d.n) return;
-  const int4 sv = *reinterpret_cast<const int4*>(d.src + e);
-  const int4 tv = *reinterpret_cast<const int4*>(d.dst + e);
-  const uint32_t dv = *reinterpret_cast<const uint32_t*>(d.dead + e);
-  float4 w = *reinterpret_cast<const float4*>(d.weight + e);
-  constexpr int nstate = RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? 3 : 1);
-  float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0, s2 = s0;
-  if (nstate >= 1) s0 = *reinterpret_cast<const float4*>(d.s0 + e);
-  if (nstate >= 3) {
-    s1 = *reinterpret_cast<const float4*>(d.s1 + e);
-    s2 = *reinterpret_cast<const float4*>(d.s2 + e);
+  __shared__ float tbl[kTbl];
+  stage_table<kUpdBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
+  __syncthreads();
+  constexpr int nstate =
+      RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
+  float den1 = 1.0f, den2 = 1.0f;
+  if (RULE == PLX_RULE_ADAM && UNI_T) {
+    const float step = d.step_t + 1.0f;
+    den1 = 1.0f - adam_pow(d, d.p[1], step, 0);
+    den2 = 1.0f - adam_pow(d, d.p[2], step, 1);
   }
-  // Every gather is unconditional (dead lanes gather unit 0) and issued
-  // before any result is used.
-  bool lv[4];
-  float gr[4];
-  {
-    const int di[4] = {tv.x, tv.y, tv.z, tv.w};
-    const int si[4] = {sv.x, sv.y, sv.z, sv.w};
-    float gu[4], ac[4];
+  const int64_t stride = 4 * static_cast<int64_t>(gridDim.x) * kUpdBlock;
+  for (int64_t e = 4 * (static_cast<int64_t>(blockIdx.x) * kUpdBlock + threadIdx.x); e < d.n;
+       e += stride) {
+    const int4 sv = *reinterpret_cast<const int4*>(d.src + e);
+    const int4 tv = *reinterpret_cast<const int4*>(d.dst + e);
+    const uint32_t dv = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
+                               : dead_from_end(e, d.live_end);
+    float4 w = *reinterpret_cast<const float4*>(d.weight + e);
+    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0, s2 = s0;
+    if (nstate >= 1) s0 = *reinterpret_cast<const float4*>(d.s0 + e);
+    if (nstate >= 2) s1 = *reinterpret_cast<const float4*>(d.s1 + e);
+    if (nstate >= 3) s2 = *reinterpret_cast<const float4*>(d.s2 + e);
+    // Every gather is issued before any result is used.
+    bool lv[4];
+    float gr[4];
+    {
+      const int di[4] = {tv.x, tv.y, tv.z, tv.w};
+      const int si[4] = {sv.x, sv.y, sv.z, sv.w};
+      float gu[4], ac[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      lv[k] = !((dv >> (8 * k)) & 0xFFu);
-      gu[k] = d.gfield[lv[k] ? di[k] : 0];
-      ac[k] = d.act[lv[k] ? si[k] : 0];
+      for (int k = 0; k < 4; ++k) {
+        lv[k] = !((dv >> (8 * k)) & 0xFFu);
+        gu[k] = d.gfield[lv[k] ? di[k] : 0];
+      }
+      gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv, ac);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) gr[k] = gu[k] * ac[k];
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) gr[k] = gu[k] * ac[k];
-  }
-  if (lv[0]) update_one<RULE>(d, gr[0], w.x, s0.x, s1.x, s2.x);
-  if (lv[1]) update_one<RULE>(d, gr[1], w.y, s0.y, s1.y, s2.y);
-  if (lv[2]) update_one<RULE>(d, gr[2], w.z, s0.z, s1.z, s2.z);
-  if (lv[3]) update_one<RULE>(d, gr[3], w.w, s0.w, s1.w, s2.w);
-  *reinterpret_cast<float4*>(d.weight + e) = w;
-  if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = s0;
-  if (nstate >= 3) {
-    *reinterpret_cast<float4*>(d.s1 + e) = s1;
-    *reinterpret_cast<float4*>(d.s2 + e) = s2;
+    if (lv[0]) update_edge<RULE, UNI_T>(d, gr[0], den1, den2, w.x, s0.x, s1.x, s2.x);
+    if (lv[1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, w.y, s0.y, s1.y, s2.y);
+    if (lv[2]) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, w.z, s0.z, s1.z, s2.z);
+    if (lv[3]) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, w.w, s0.w, s1.w, s2.w);
+    *reinterpret_cast<float4*>(d.weight + e) = w;
+    if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = s0;
+    if (nstate >= 2) *reinterpret_cast<float4*>(d.s1 + e) = s1;
+    if (nstate >= 3) *reinterpret_cast<float4*>(d.s2 + e) = s2;
   }
 }
 
@@ -418,7 +527,7 @@ constexpr int kTileBlock = 512;
 #endif
 constexpr int kTileQuads = PLX_TILE_QUADS;  // 16-byte quads per thread per streaming pass
 
-constexpr int kGrpPer = 6;  // group descriptors prefetched per thread per tile
+constexpr int kGrpPer = 4;  // group descriptors prefetched per thread per tile
 
 // Folds one (tile, source) group: the contiguous run buf[st, st+len) in
 // order, into its cold partial slot or its hot running sum. A source has one
@@ -448,122 +557,143 @@ __device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* 
 
 // SAME_G: the backward field and the update's grad field are one column, so
 // one gather serves both.
-template <int RULE, int M, bool FOLD, bool SAME_G>
-__global__ __launch_bounds__(kTileBlock) void k_tile(plx_tile_desc d) {
+template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
+__global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int T = d.tile_size;
   float* buf = reinterpret_cast<float*>(smem);  // [T] terms in source-sorted order
   float* hot = buf + T;                          // [nhot]
+  // [tbl_len] act of the busiest sources (the whole allocation without fold)
+  float* tbl = FOLD ? hot + ((d.nhot + 3) & ~3) : reinterpret_cast<float*>(smem);
+  if (RULE >= 0) stage_table<kTileBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
   const int k0 = d.super_tile[blockIdx.x];
   const int k1 = d.super_tile[blockIdx.x + 1];
   const float ident = Mono<M>::id();
   if (FOLD)
     for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hot[j] = ident;
-  constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? 3 : 1);
-  constexpr int U = kTileQuads;
-  for (int blk = k0; blk < k1; ++blk) {
-    const int64_t t0 = d.base + d.tile_pos[blk];
-    const int n = d.tile_pos[blk + 1] - d.tile_pos[blk];
-    // The tile's group descriptors, kGrpPer per thread, are loaded with the
-    // edge columns so the fold below waits on no global load.
-    uint32_t gse[kGrpPer];
-    int32_t gtg[kGrpPer];
-    int ga = 0, gb = 0;
+  __syncthreads();
+  constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD
+                             ? 0
+                             : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
+  float den1 = 1.0f, den2 = 1.0f;
+  if (RULE == PLX_RULE_ADAM && UNI_T) {
+    const float step = d.step_t + 1.0f;
+    den1 = 1.0f - adam_pow(d, d.p[1], step, 0);
+    den2 = 1.0f - adam_pow(d, d.p[2], step, 1);
+  }
+  constexpr int U = kTileQuads;  // a tile is one pass: at most 4 * U * kTileBlock positions
+
+  // Registers of the tile in flight. A tile's loads (edge columns and its
+  // group descriptors) are issued while the previous tile is folded, so the
+  // fold never leaves the memory system idle.
+  int4 sv[U], tv[U];
+  uint32_t dv[U];
+  uint2 rk[U];
+  float4 w[U], s0[U], s1[U], s2[U];
+  uint32_t gse[kGrpPer];
+  int32_t gtg[kGrpPer];
+  int ga = 0, gb = 0, n = 0;
+  int64_t t0 = 0;
+  auto load = [&](int blk) {
+    t0 = d.base + d.tile_pos[blk];
+    n = d.tile_pos[blk + 1] - d.tile_pos[blk];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = threadIdx.x + i * kTileBlock;
+      if (4 * q < n) {
+        const int64_t e = t0 + 4 * q;
+        tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
+        dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
+                       : dead_from_end(e, d.live_end);
+        w[i] = *reinterpret_cast<const float4*>(d.weight + e);
+        if (FOLD) rk[i] = *reinterpret_cast<const uint2*>(d.sorted_rank + (e - d.base));
+        if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
+        if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
+        if (nstate >= 2) s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
+        if (nstate >= 3) s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
+      }
+    }
     if (FOLD) {
       ga = d.grp_off[blk];
       gb = d.grp_off[blk + 1];
 #pragma unroll
       for (int i = 0; i < kGrpPer; ++i) {
         const int gi = ga + threadIdx.x + i * kTileBlock;
-        gse[i] = gi < gb ? d.grp_se[gi] : 0u;
-        gtg[i] = gi < gb ? d.grp_tgt[gi] : 0;
-      }
-    }
-    // Each pass covers U quads per thread; every load of a pass is issued
-    // before any of it is used.
-    for (int q0 = threadIdx.x; 4 * q0 < n; q0 += U * kTileBlock) {
-      int4 sv[U], tv[U];
-      uint32_t dv[U];
-      uint2 rk[U];
-      float4 w[U], s0[U], s1[U], s2[U];
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int q = q0 + i * kTileBlock;
-        if (4 * q < n) {
-          const int64_t e = t0 + 4 * q;
-          tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
-          dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
-          w[i] = *reinterpret_cast<const float4*>(d.weight + e);
-          if (FOLD) rk[i] = *reinterpret_cast<const uint2*>(d.sorted_rank + (e - d.base));
-          if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
-          if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
-          if (nstate >= 3) {
-            s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
-            s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
-          }
-        }
-      }
-      // Every gather is unconditional (dead or out-of-tile lanes gather
-      // unit 0) and issued before any result is used.
-      bool lv[U][4];
-      float gd[U][4], gu[U][4], ac[U][4];
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const bool in = 4 * (q0 + i * kTileBlock) < n;
-        const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
-        const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
-          const int dk = lv[i][k] ? di[k] : 0;
-          if (FOLD) gd[i][k] = d.g[dk];
-          if (RULE >= 0) {
-            gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
-            ac[i][k] = d.act[lv[i][k] ? si[k] : 0];
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int q = q0 + i * kTileBlock;
-        if (4 * q >= n) continue;
-        const int64_t e = t0 + 4 * q;
-        if (FOLD) {
-          // Each live edge's term goes to its slot in the tile's
-          // source-sorted order, so every (tile, source) group is a
-          // contiguous run of buf.
-          if (lv[i][0]) buf[rk[i].x & 0xFFFFu] = w[i].x * gd[i][0];
-          if (lv[i][1]) buf[rk[i].x >> 16] = w[i].y * gd[i][1];
-          if (lv[i][2]) buf[rk[i].y & 0xFFFFu] = w[i].z * gd[i][2];
-          if (lv[i][3]) buf[rk[i].y >> 16] = w[i].w * gd[i][3];
-        }
-        if (RULE >= 0) {
-          float gr[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) gr[k] = (SAME_G && FOLD ? gd[i][k] : gu[i][k]) * ac[i][k];
-          float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
-          if (lv[i][0]) update_one<RULE>(d, gr[0], a.x, m.x, v.x, t.x);
-          if (lv[i][1]) update_one<RULE>(d, gr[1], a.y, m.y, v.y, t.y);
-          if (lv[i][2]) update_one<RULE>(d, gr[2], a.z, m.z, v.z, t.z);
-          if (lv[i][3]) update_one<RULE>(d, gr[3], a.w, m.w, v.w, t.w);
-          *reinterpret_cast<float4*>(d.weight + e) = a;
-          if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
-          if (nstate >= 3) {
-            *reinterpret_cast<float4*>(d.s1 + e) = v;
-            *reinterpret_cast<float4*>(d.s2 + e) = t;
-          }
+        if (gi < gb) {
+          gse[i] = d.grp_se[gi];
+          gtg[i] = d.grp_tgt[gi];
         }
       }
     }
+  };
+
+  load(k0);
+  for (int blk = k0; blk < k1; ++blk) {
+    // Gathers: every one is issued before any result is used (dead or
+    // out-of-tile lanes gather a harmless unit).
+    bool lv[U][4];
+    float gd[U][4], gu[U][4], ac[U][4];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const bool in = 4 * (threadIdx.x + i * kTileBlock) < n;
+      const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
+      const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
+        const int dk = lv[i][k] ? di[k] : 0;
+        if (FOLD) gd[i][k] = d.g[dk];
+        if (RULE >= 0) gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
+      }
+      if (RULE >= 0) gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ac[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = threadIdx.x + i * kTileBlock;
+      if (4 * q >= n) continue;
+      const int64_t e = t0 + 4 * q;
+      if (FOLD) {
+        // Each live edge's term goes to its slot in the tile's source-sorted
+        // order, so every (tile, source) group is a contiguous run of buf.
+        if (lv[i][0]) buf[rk[i].x & 0xFFFFu] = w[i].x * gd[i][0];
+        if (lv[i][1]) buf[rk[i].x >> 16] = w[i].y * gd[i][1];
+        if (lv[i][2]) buf[rk[i].y & 0xFFFFu] = w[i].z * gd[i][2];
+        if (lv[i][3]) buf[rk[i].y >> 16] = w[i].w * gd[i][3];
+      }
+      if (RULE >= 0) {
+        float gr[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) gr[k] = (SAME_G && FOLD ? gd[i][k] : gu[i][k]) * ac[i][k];
+        float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
+        if (lv[i][0]) update_edge<RULE, UNI_T>(d, gr[0], den1, den2, a.x, m.x, v.x, t.x);
+        if (lv[i][1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, a.y, m.y, v.y, t.y);
+        if (lv[i][2]) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, a.z, m.z, v.z, t.z);
+        if (lv[i][3]) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, a.w, m.w, v.w, t.w);
+        *reinterpret_cast<float4*>(d.weight + e) = a;
+        if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
+        if (nstate >= 2) *reinterpret_cast<float4*>(d.s1 + e) = v;
+        if (nstate >= 3) *reinterpret_cast<float4*>(d.s2 + e) = t;
+      }
+    }
+    // This tile's group descriptors, kept while the next tile loads.
+    uint32_t cse[kGrpPer];
+    int32_t ctg[kGrpPer];
+    const int cga = ga, cgb = gb;
+#pragma unroll
+    for (int i = 0; i < kGrpPer; ++i) {
+      cse[i] = gse[i];
+      ctg[i] = gtg[i];
+    }
+    if (blk + 1 < k1) load(blk + 1);
     if (!FOLD) continue;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kGrpPer; ++i) {
-      const int gi = ga + threadIdx.x + i * kTileBlock;
-      if (gi < gb) fold_group<M>(d, buf, hot, gse[i], gtg[i]);
+      const int gi = cga + threadIdx.x + i * kTileBlock;
+      if (gi < cgb) fold_group<M>(d, buf, hot, cse[i], ctg[i]);
     }
     // Tiles with more groups than the prefetch covers fold the rest here.
-    for (int gi = ga + kGrpPer * kTileBlock + threadIdx.x; gi < gb; gi += kTileBlock)
+    for (int gi = cga + kGrpPer * kTileBlock + threadIdx.x; gi < cgb; gi += kTileBlock)
       fold_group<M>(d, buf, hot, d.grp_se[gi], d.grp_tgt[gi]);
     __syncthreads();
   }
@@ -591,7 +721,7 @@ __device__ __forceinline__ void finish_row(const plx_partials_desc& d, const Row
 // of hot_sb through LDS, kHotSbChunk superblocks at a time, with coalesced
 // loads, and each column's lane folds its superblock sums in order.
 constexpr int kHotCols = 64;
-constexpr int kHotSbChunk = 128;
+constexpr int kHotSbChunk = 512;
 
 template <int M>
 __global__ __launch_bounds__(256) void k_hot_final(plx_partials_desc d) {
@@ -848,23 +978,32 @@ bool program_ok(const plx_program& p) {
   return p.ninstr >= 0 && p.ninstr <= PLX_MAX_INSTR && p.nout >= 0 && p.nout <= PLX_MAX_OUTS;
 }
 
-template <int RULE, int M, bool FOLD, bool SAME_G>
+template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
 void launch_tile_g(const plx_tile_desc& d, size_t lds, hipStream_t s) {
   // LDS beyond 64 KiB needs an explicit per-kernel opt-in.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD, SAME_G>),
+      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD, SAME_G, UNI_T>),
       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   (void)attr;
   // One workgroup per superblock of tiles.
-  k_tile<RULE, M, FOLD, SAME_G><<<static_cast<unsigned>(d.nsuper), kTileBlock, lds, s>>>(d);
+  k_tile<RULE, M, FOLD, SAME_G, UNI_T>
+      <<<static_cast<unsigned>(d.nsuper), kTileBlock, lds, s>>>(d);
 }
 
 template <int RULE, int M, bool FOLD>
 void launch_tile(const plx_tile_desc& d, size_t lds, hipStream_t s) {
-  if (FOLD && RULE >= 0 && d.g == d.gfield)
-    launch_tile_g<RULE, M, FOLD, true>(d, lds, s);
-  else
-    launch_tile_g<RULE, M, FOLD, false>(d, lds, s);
+  const bool same = FOLD && RULE >= 0 && d.g == d.gfield;
+  if (RULE == PLX_RULE_ADAM && d.step_mode == 1) {
+    if (same)
+      launch_tile_g<RULE, M, FOLD, true, true>(d, lds, s);
+    else
+      launch_tile_g<RULE, M, FOLD, false, true>(d, lds, s);
+  } else {
+    if (same)
+      launch_tile_g<RULE, M, FOLD, true, false>(d, lds, s);
+    else
+      launch_tile_g<RULE, M, FOLD, false, false>(d, lds, s);
+  }
 }
 
 template <int M, bool FOLD>
@@ -886,7 +1025,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 2; }
+int32_t plx_abi_version(void) { return 4; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[6] = {
@@ -904,6 +1043,8 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
   if (!d->row_unit || !d->row_ptr || !d->src || !d->weight || !d->x)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: null column");
   if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_forward_bucket: bad program");
+  if (d->tbl_len < 0 || d->tbl_len > PLX_MAX_TBL)
+    return fail(PLX_ERR_INVALID, "plx_forward_bucket: tbl_len must be in [0, PLX_MAX_TBL]");
   if (!d->fin.level || !d->fin.is_input)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: fin.level and fin.is_input are required");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -920,15 +1061,18 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
 
 int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
   if (!d) return fail(PLX_ERR_INVALID, "plx_backward_tiles: null descriptor");
-  if (d->ntiles < 0 || d->tile_size <= 0 || d->tile_size % 4 || d->tile_size > 32768)
-    return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile_size must be a positive multiple of 4 <= 32768");
+  if (d->ntiles < 0 || d->tile_size <= 0 || d->tile_size % 4 ||
+      d->tile_size > 4 * kTileQuads * kTileBlock)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile_size must be a positive multiple of 4 <= 4096");
   if (d->base % 4 || d->end % 4 || d->end < d->base)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: base/end must be multiples of 4");
   if (d->ntiles == 0 || d->end == d->base) return PLX_OK;
   if (d->nsuper <= 0 || d->nsuper > d->ntiles || !d->tile_pos || !d->super_tile)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile / superblock tables missing");
-  if (!d->src || !d->dst || !d->dead || !d->weight)
+  if (!d->src || !d->dst || !d->weight)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
+  if (d->step_mode != 0 && d->step_mode != 1)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: step_mode must be 0 or 1");
   if (d->fold && (!d->grp_off || !d->grp_se || !d->grp_tgt || !d->sorted_rank || !d->g ||
                   (d->nhot > 0 && !d->hot_sb)))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: fold metadata missing");
@@ -936,18 +1080,22 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: update fields missing");
   if (d->update && (d->rule == PLX_RULE_MOMENTUM || d->rule == PLX_RULE_RMSPROP) && !d->s0)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: state column missing");
-  if (d->update && d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || !d->s2))
+  if (d->update && d->rule == PLX_RULE_ADAM &&
+      (!d->s0 || !d->s1 || (d->step_mode == 0 && !d->s2)))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: Adam state columns missing");
   if (!d->fold && !d->update) return PLX_OK;
   if (d->fold && d->nhot < 0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: negative nhot");
-  const size_t lds = d->fold ? static_cast<size_t>(d->tile_size) * 4 +
-                                   static_cast<size_t>(d->nhot) * 4
-                             : 0;
+  if (d->tbl_len < 0 || d->tbl_len > PLX_MAX_TBL)
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: tbl_len must be in [0, PLX_MAX_TBL]");
+  const size_t tbl = d->update ? static_cast<size_t>(d->tbl_len) * 4 : 0;
+  const size_t lds = (d->fold ? static_cast<size_t>(d->tile_size) * 4 +
+                                    static_cast<size_t>((d->nhot + 3) & ~3) * 4
+                              : 0) + tbl;
   if (lds > 160 * 1024) return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: tile does not fit in LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = PLX_OK;
   if (!d->fold) {
-    rc = dispatch_rule<PLX_MONOID_SUM, false>(*d, 0, s);
+    rc = dispatch_rule<PLX_MONOID_SUM, false>(*d, lds, s);
   } else {
     switch (d->monoid) {
       case PLX_MONOID_SUM: rc = dispatch_rule<PLX_MONOID_SUM, true>(*d, lds, s); break;
@@ -981,6 +1129,19 @@ int plx_backward_partials(const plx_partials_desc* d, void* stream) {
   if (nhot_rows > 0 && d->nsuper > 0) {
     const unsigned hgrid = grid_for(nhot_rows, kHotCols);
     const size_t lds = static_cast<size_t>(min(d->nsuper, kHotSbChunk)) * kHotCols * 4;
+    static const hipError_t attr_hot = [] {
+      hipError_t e = hipSuccess;
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_SUM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_PROD>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_MAX>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_MIN>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      return e;
+    }();
+    (void)attr_hot;
     switch (d->monoid) {
       case PLX_MONOID_SUM: k_hot_final<PLX_MONOID_SUM><<<hgrid, 256, lds, s>>>(*d); break;
       case PLX_MONOID_PROD: k_hot_final<PLX_MONOID_PROD><<<hgrid, 256, lds, s>>>(*d); break;
@@ -1008,19 +1169,30 @@ int plx_update_conn(const plx_update_desc* d, void* stream) {
   if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_update_conn: negative n");
   if (d->n == 0) return PLX_OK;
   if (d->n % 4 != 0) return fail(PLX_ERR_INVALID, "plx_update_conn: n must be a multiple of 4");
-  if (!d->src || !d->dst || !d->dead || !d->weight || !d->gfield || !d->act)
+  if (!d->src || !d->dst || !d->weight || !d->gfield || !d->act)
     return fail(PLX_ERR_INVALID, "plx_update_conn: null column");
+  if (d->step_mode != 0 && d->step_mode != 1)
+    return fail(PLX_ERR_INVALID, "plx_update_conn: step_mode must be 0 or 1");
   if ((d->rule == PLX_RULE_MOMENTUM || d->rule == PLX_RULE_RMSPROP) && !d->s0)
     return fail(PLX_ERR_INVALID, "plx_update_conn: state column missing");
-  if (d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || !d->s2))
+  if (d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || (d->step_mode == 0 && !d->s2)))
     return fail(PLX_ERR_INVALID, "plx_update_conn: Adam state columns missing");
+  if (d->tbl_len < 0 || d->tbl_len > PLX_MAX_TBL)
+    return fail(PLX_ERR_INVALID, "plx_update_conn: tbl_len must be in [0, PLX_MAX_TBL]");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned grid = grid_for(d->n / 4, kUpdBlock);
+  // Four workgroups per CU stride over the positions.
+  const unsigned quads_grid = grid_for(d->n / 4, kUpdBlock);
+  const unsigned grid = quads_grid < 1024u ? quads_grid : 1024u;
   switch (d->rule) {
-    case PLX_RULE_SGD: k_update<PLX_RULE_SGD><<<grid, kUpdBlock, 0, s>>>(*d); break;
-    case PLX_RULE_MOMENTUM: k_update<PLX_RULE_MOMENTUM><<<grid, kUpdBlock, 0, s>>>(*d); break;
-    case PLX_RULE_ADAM: k_update<PLX_RULE_ADAM><<<grid, kUpdBlock, 0, s>>>(*d); break;
-    case PLX_RULE_RMSPROP: k_update<PLX_RULE_RMSPROP><<<grid, kUpdBlock, 0, s>>>(*d); break;
+    case PLX_RULE_SGD: k_update<PLX_RULE_SGD, false><<<grid, kUpdBlock, 0, s>>>(*d); break;
+    case PLX_RULE_MOMENTUM: k_update<PLX_RULE_MOMENTUM, false><<<grid, kUpdBlock, 0, s>>>(*d); break;
+    case PLX_RULE_ADAM:
+      if (d->step_mode == 1)
+        k_update<PLX_RULE_ADAM, true><<<grid, kUpdBlock, 0, s>>>(*d);
+      else
+        k_update<PLX_RULE_ADAM, false><<<grid, kUpdBlock, 0, s>>>(*d);
+      break;
+    case PLX_RULE_RMSPROP: k_update<PLX_RULE_RMSPROP, false><<<grid, kUpdBlock, 0, s>>>(*d); break;
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_update_conn: unknown rule");
   }
   return check_launch("plx_update_conn");

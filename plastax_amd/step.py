@@ -134,8 +134,25 @@ class StepFn:
                 self.static, state.units, state._conns, state.device, tile=self.tile,
                 nsuper=self.nsuper,
             )
+            up = self.plan.update
+            if up is not None and up.rule_code == 2:
+                state._arena.init_uniform_t(up.state_columns()[2])
             state._arena_ahead = False
         return state._arena
+
+    @staticmethod
+    def _edge_state(d: Any, arena: Arena, b: int, update: bool) -> None:
+        """Liveness and Adam step-count fields of a tile / update descriptor."""
+        d.live_end = arena.live_end(b)
+        d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
+        if update and arena.t_now and arena.t_now[b] is not None:
+            d.step_mode = 1
+            d.step_t = arena.t_now[b]
+
+    @staticmethod
+    def _advance_t(arena: Arena, b: int) -> None:
+        if arena.t_now and arena.t_now[b] is not None:
+            arena.t_now[b] += 1.0
 
     # -- the step ------------------------------------------------------------
     def __call__(self, state: NetworkState, inputs: StepInputs) -> StepResult:
@@ -188,6 +205,7 @@ class StepFn:
             d = _lib.plx_forward_desc()
             d.nrows = rows.nrows
             d.monoid = fp.monoid
+            d.tbl_base, d.tbl_len = arena.src_table(b)
             d.row_unit = rows.rows.data_ptr()
             d.row_ptr = rows.ptr.data_ptr()
             d.src = arena.cols["from_id"].data_ptr()
@@ -311,6 +329,7 @@ class StepFn:
         if update:
             up = plan.update
             d.rule = up.rule_code
+            d.tbl_base, d.tbl_len = arena.src_table(b)
             for k, name in enumerate(up.state_columns()):
                 setattr(d, f"s{k}", arena.cols[name].data_ptr())
             d.gfield = units[up.grad_field.name].data_ptr()
@@ -320,8 +339,11 @@ class StepFn:
                 d.pow_table_len = consts["pow_table"].numel() // 2
             for k, v in enumerate(up.params()):
                 d.p[k] = float(v)
+        self._edge_state(d, arena, b, update)
         kind = "backward_update" if fold and update else ("backward" if fold else "update_conn")
         self._launch(kind, lib.plx_backward_tiles, d, stream)
+        if update:
+            self._advance_t(arena, b)
 
     def _partials(self, plan: Plan, bt: Any, acc: Any, prog: Any, fin_common: dict,
                   fin_level: int, skip_inputs: int, stream: int) -> None:
@@ -393,6 +415,7 @@ class StepFn:
         d = _lib.plx_update_desc()
         d.n = bt.end - bt.base
         d.rule = up.rule_code
+        d.tbl_base, d.tbl_len = arena.src_table(b)
 
         def col(name: str) -> int:
             t = arena.cols[name]
@@ -411,4 +434,9 @@ class StepFn:
             d.pow_table_len = consts["pow_table"].numel() // 2
         for k, v in enumerate(up.params()):
             d.p[k] = float(v)
+        self._edge_state(d, arena, b, True)
+        # positions of this descriptor start at the bucket base
+        d.live_end -= bt.base
+        d.dead = col("dead") if arena.dead_in_rows else None
         self._launch("update_conn", lib.plx_update_conn, d, stream)
+        self._advance_t(arena, b)
