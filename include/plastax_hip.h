@@ -114,7 +114,8 @@ PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
  * is folded, in tile order, into its superblock sum, stored at
  * hot_sb[superblock * nhot + h] (the identity where the source is absent);
  * the other sources' tile partials are stored in their slot of the
- * source-major cold_partial array (group target -1-h or the cold slot). With
+ * cold_partial array (group target -1-h or the cold slot; a tile's cold slots
+ * are consecutive, in its group order). With
  * `update`, the same pass applies the update rule (see plx_update_desc for
  * p[] and the state columns) with grad = gfield[dst] * act[src] and stores
  * the new weight and state; dead edges keep theirs. Tile metadata:
@@ -189,6 +190,7 @@ typedef struct plx_partials_desc {
   const float* hot_sb;
   const float* cold_partial;
   const uint16_t* cold_sb;
+  const int32_t* cold_idx;
   float* acc;
   plx_finalize fin;
   plx_program apply;

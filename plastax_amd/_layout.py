@@ -28,7 +28,9 @@ the workgroup keeps their running sums in LDS and writes one dense row per
 superblock (``nhot`` wide); the others get source-major runs of cold
 partials. A source's sum is therefore the fold, in superblock order, of its
 superblock sums, each the fold in tile order of its tile partials, each tile
-partial the fold of its terms in (dst, slot) order.
+partial the fold of its terms in (dst, slot) order. Cold partials are stored
+tile-major (each tile's in consecutive slots) and listed source-major by
+``cold_idx``.
 
 Units are renumbered: the arena fixes a physical unit order (``unit_order``:
 by level, then out-degree descending, then unit id), the edge columns and
@@ -104,6 +106,7 @@ class BackwardTiles:
     hot_sb: torch.Tensor | None = None  # f32 [nsuper*nhot]
     cold_partial: torch.Tensor | None = None  # f32 [ncold]
     cold_sb: torch.Tensor | None = None  # int16 (uint16 bits) [ncold] superblock ids
+    cold_idx: torch.Tensor | None = None  # int32 [ncold] tile-major slot, source-major order
     nrows: int = 0
     rows: torch.Tensor | None = None  # int32 [nrows] units finalized here
     row_hot: torch.Tensor | None = None  # int32 [nrows]
@@ -339,17 +342,23 @@ class Arena:
         hot_idx[hot_src] = np.arange(hot_src.size)
         nhot = int(hot_src.size)
         is_hot = hot_idx[g_src] >= 0 if live else np.zeros(0, bool)
-        # Cold groups: source-major, tile order within a source.
+        # Cold groups: each tile writes its cold partials to consecutive
+        # slots (tile-major, in the tile's group order below, so the stores
+        # of a wave are coalesced); cold_idx lists every source's slots in
+        # tile order, source-major, for the finalize.
         cold = np.flatnonzero(~is_hot)
         cold_order = cold[np.lexsort((g_tile[cold], g_src[cold]))]
-        tgt = np.empty(g_start.size, dtype=np.int64)
-        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
-        tgt[cold_order] = np.arange(cold_order.size)
         cold_count = np.bincount(g_src[cold], minlength=n) if cold.size else np.zeros(n, np.int64)
         # Within a tile, longest groups first (lanes take them round robin).
         g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
         grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
         se = (g_st[g_perm].astype(np.uint64) | (g_len[g_perm].astype(np.uint64) << np.uint64(16)))
+        # Tile-major cold slots: the cold groups in descriptor order.
+        tgt = np.empty(g_start.size, dtype=np.int64)
+        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
+        cold_in_perm = g_perm[~is_hot[g_perm]] if live else g_start
+        tgt[cold_in_perm] = np.arange(cold_in_perm.size)
+        cold_idx = tgt[cold_order]
         # Rows finalized at this bucket: hot sources first (by hot slot, so a
         # wave reads consecutive columns), then every other unit of the level.
         if self.pipeline:
@@ -378,6 +387,7 @@ class Arena:
             grp_off=self._i32(grp_off),
             grp_se=torch.from_numpy(se.astype(np.uint32).view(np.int32)).to(dev),
             grp_tgt=self._i32(tgt[g_perm] if live else tgt),
+            cold_idx=self._i32(np.concatenate([cold_idx, np.zeros(1, np.int64)])),
             sorted_rank=torch.from_numpy(sorted_rank.view(np.int16)).to(dev),
             hot_sb=torch.zeros(max(nsuper * nhot, 1), dtype=torch.float32, device=dev),
             cold_partial=torch.zeros(max(ncold, 1), dtype=torch.float32, device=dev),

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 4  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 5  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -133,6 +133,7 @@ class plx_partials_desc(ctypes.Structure):
         ("hot_sb", c_vp),
         ("cold_partial", c_vp),
         ("cold_sb", c_vp),
+        ("cold_idx", c_vp),
         ("acc", c_vp),
         ("fin", plx_finalize),
         ("apply", plx_program),

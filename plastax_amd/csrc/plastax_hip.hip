@@ -24,6 +24,29 @@
 
 namespace {
 
+// Streaming (non-temporal) 16-byte accesses for the edge columns: each
+// position is read and written once per pass, so these lines should not
+// displace the gathered unit vectors and partials in the caches.
+typedef float nt_v4f __attribute__((ext_vector_type(4)));
+typedef int nt_v4i __attribute__((ext_vector_type(4)));
+typedef unsigned nt_v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_stream(const float* p) {
+  const nt_v4f v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4f*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ int4 ld_stream(const int32_t* p) {
+  const nt_v4i v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4i*>(p));
+  return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream(const uint16_t* p) {
+  const nt_v2u v = __builtin_nontemporal_load(reinterpret_cast<const nt_v2u*>(p));
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ void st_stream(float* p, float4 a) {
+  const nt_v4f v = {a.x, a.y, a.z, a.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<nt_v4f*>(p));
+}
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* what) {
@@ -313,8 +336,8 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
       dv[i] = 0;
       if (4 * q < wn) {
         const int e = w0 + 4 * q;
-        sv[i] = *reinterpret_cast<const int4*>(d.src + e);
-        wv[i] = *reinterpret_cast<const float4*>(d.weight + e);
+        sv[i] = ld_stream(d.src + e);
+        wv[i] = ld_stream(d.weight + e);
         if (d.dead) dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
       }
     }
@@ -469,15 +492,15 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
   const int64_t stride = 4 * static_cast<int64_t>(gridDim.x) * kUpdBlock;
   for (int64_t e = 4 * (static_cast<int64_t>(blockIdx.x) * kUpdBlock + threadIdx.x); e < d.n;
        e += stride) {
-    const int4 sv = *reinterpret_cast<const int4*>(d.src + e);
-    const int4 tv = *reinterpret_cast<const int4*>(d.dst + e);
+    const int4 sv = ld_stream(d.src + e);
+    const int4 tv = ld_stream(d.dst + e);
     const uint32_t dv = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
                                : dead_from_end(e, d.live_end);
-    float4 w = *reinterpret_cast<const float4*>(d.weight + e);
+    float4 w = ld_stream(d.weight + e);
     float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0, s2 = s0;
-    if (nstate >= 1) s0 = *reinterpret_cast<const float4*>(d.s0 + e);
-    if (nstate >= 2) s1 = *reinterpret_cast<const float4*>(d.s1 + e);
-    if (nstate >= 3) s2 = *reinterpret_cast<const float4*>(d.s2 + e);
+    if (nstate >= 1) s0 = ld_stream(d.s0 + e);
+    if (nstate >= 2) s1 = ld_stream(d.s1 + e);
+    if (nstate >= 3) s2 = ld_stream(d.s2 + e);
     // Every gather is issued before any result is used.
     bool lv[4];
     float gr[4];
@@ -498,10 +521,10 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
     if (lv[1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, w.y, s0.y, s1.y, s2.y);
     if (lv[2]) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, w.z, s0.z, s1.z, s2.z);
     if (lv[3]) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, w.w, s0.w, s1.w, s2.w);
-    *reinterpret_cast<float4*>(d.weight + e) = w;
-    if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = s0;
-    if (nstate >= 2) *reinterpret_cast<float4*>(d.s1 + e) = s1;
-    if (nstate >= 3) *reinterpret_cast<float4*>(d.s2 + e) = s2;
+    st_stream(d.weight + e, w);
+    if (nstate >= 1) st_stream(d.s0 + e, s0);
+    if (nstate >= 2) st_stream(d.s1 + e, s1);
+    if (nstate >= 3) st_stream(d.s2 + e, s2);
   }
 }
 
@@ -602,15 +625,15 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       const int q = threadIdx.x + i * kTileBlock;
       if (4 * q < n) {
         const int64_t e = t0 + 4 * q;
-        tv[i] = *reinterpret_cast<const int4*>(d.dst + e);
+        tv[i] = ld_stream(d.dst + e);
         dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
                        : dead_from_end(e, d.live_end);
-        w[i] = *reinterpret_cast<const float4*>(d.weight + e);
-        if (FOLD) rk[i] = *reinterpret_cast<const uint2*>(d.sorted_rank + (e - d.base));
-        if (RULE >= 0) sv[i] = *reinterpret_cast<const int4*>(d.src + e);
-        if (nstate >= 1) s0[i] = *reinterpret_cast<const float4*>(d.s0 + e);
-        if (nstate >= 2) s1[i] = *reinterpret_cast<const float4*>(d.s1 + e);
-        if (nstate >= 3) s2[i] = *reinterpret_cast<const float4*>(d.s2 + e);
+        w[i] = ld_stream(d.weight + e);
+        if (FOLD) rk[i] = ld_stream(d.sorted_rank + (e - d.base));
+        if (RULE >= 0) sv[i] = ld_stream(d.src + e);
+        if (nstate >= 1) s0[i] = ld_stream(d.s0 + e);
+        if (nstate >= 2) s1[i] = ld_stream(d.s1 + e);
+        if (nstate >= 3) s2[i] = ld_stream(d.s2 + e);
       }
     }
     if (FOLD) {
@@ -669,10 +692,10 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         if (lv[i][1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, a.y, m.y, v.y, t.y);
         if (lv[i][2]) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, a.z, m.z, v.z, t.z);
         if (lv[i][3]) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, a.w, m.w, v.w, t.w);
-        *reinterpret_cast<float4*>(d.weight + e) = a;
-        if (nstate >= 1) *reinterpret_cast<float4*>(d.s0 + e) = m;
-        if (nstate >= 2) *reinterpret_cast<float4*>(d.s1 + e) = v;
-        if (nstate >= 3) *reinterpret_cast<float4*>(d.s2 + e) = t;
+        st_stream(d.weight + e, a);
+        if (nstate >= 1) st_stream(d.s0 + e, m);
+        if (nstate >= 2) st_stream(d.s1 + e, v);
+        if (nstate >= 3) st_stream(d.s2 + e, t);
       }
     }
     // This tile's group descriptors, kept while the next tile loads.
@@ -785,8 +808,10 @@ __global__ __launch_bounds__(kPartBlock) void k_partials(plx_partials_desc d) {
     int cur = -1;
     for (int w0 = c_begin; w0 < c_end; w0 += kPartWin) {
       const int wn = min(kPartWin, c_end - w0);
-      // Issue every load of the window before storing any of it.
+      // Issue every load of the window before storing any of it: the
+      // window's slots and superblock ids, then the partials they name.
       constexpr int kPer = kPartWin / kPartBlock;
+      int pi[kPer];
       float pv[kPer];
       uint16_t ps[kPer];
 #pragma unroll
@@ -794,9 +819,11 @@ __global__ __launch_bounds__(kPartBlock) void k_partials(plx_partials_desc d) {
         // Clamped into range: every load is unconditional (entries past the
         // window are staged but never folded).
         const int j = min(static_cast<int>(threadIdx.x) + i * kPartBlock, wn - 1);
-        pv[i] = d.cold_partial[w0 + j];
+        pi[i] = d.cold_idx[w0 + j];
         ps[i] = d.cold_sb[w0 + j];
       }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) pv[i] = d.cold_partial[pi[i]];
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         cval[threadIdx.x + i * kPartBlock] = pv[i];
@@ -1025,7 +1052,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 4; }
+int32_t plx_abi_version(void) { return 5; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[6] = {
@@ -1118,7 +1145,7 @@ int plx_backward_partials(const plx_partials_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_partials: part_rows missing");
   if (d->row_hot && (d->nhot < 0 || d->nsuper < 0 || (d->nhot > 0 && !d->hot_sb)))
     return fail(PLX_ERR_INVALID, "plx_backward_partials: hot partials missing");
-  if (d->row_cold && (!d->cold_partial || !d->cold_sb))
+  if (d->row_cold && (!d->cold_partial || !d->cold_sb || !d->cold_idx))
     return fail(PLX_ERR_INVALID, "plx_backward_partials: cold partials missing");
   if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_partials: bad program");
   if (!d->fin.level || !d->fin.is_input)

@@ -362,6 +362,7 @@ class StepFn:
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
             d.cold_sb = bt.cold_sb.data_ptr()
+            d.cold_idx = bt.cold_idx.data_ptr()
         d.acc = acc.data_ptr() if acc is not None else None
         d.fin.level = fin_common["level"]
         d.fin.is_input = fin_common["is_input"]

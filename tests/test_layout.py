@@ -122,6 +122,9 @@ def _emulate_fold(arena, b, g_logical: np.ndarray):
     row_cold = _np(bt.row_cold)
     assert row_cold[0] == 0 and (np.diff(row_cold) >= 0).all() and row_cold[-1] == cold.size or (cold.size == 1 and row_cold[-1] == 0)
     cold_sb = _np(bt.cold_sb).view(np.uint16)
+    cold_idx = _np(bt.cold_idx)
+    ncold = row_cold[-1]
+    assert sorted(cold_idx[:ncold].tolist()) == list(range(ncold))  # a permutation of the slots
     # the finalize kernel relies on hot rows coming first, in column order,
     # and on the cold workgroups covering the other rows, 256 at most each
     assert (row_hot[:nhot] == np.arange(nhot)).all() and (row_hot[nhot:] == -1).all()
@@ -143,7 +146,7 @@ def _emulate_fold(arena, b, g_logical: np.ndarray):
                 for j in range(j0, j1):
                     if cold_sb[j] != cur:
                         s, q, cur = np.float32(s + q), np.float32(0.0), cold_sb[j]
-                    q = np.float32(q + cold[j])
+                    q = np.float32(q + cold[cold_idx[j]])
                 s = np.float32(s + q)
         out[int(arena.uperm[rows[r]])] = s
     return out
