@@ -249,7 +249,7 @@ constexpr int kTbl = PLX_MAX_TBL;
 template <int BLOCK, int CAP = kTbl>
 __device__ __forceinline__ void stage_table(float* tbl, const float* x, int base, int len) {
   if (len <= 0) return;
-  constexpr int kPer = (CAP + BLOCK - 1) / BLOCK;
+  constexpr int kPer = CAP > 0 ? (CAP + BLOCK - 1) / BLOCK : 1;
   float v[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) v[i] = x[base + min(static_cast<int>(threadIdx.x) + i * BLOCK, len - 1)];
@@ -292,7 +292,7 @@ __device__ __forceinline__ void gather_k(const float* tbl, const float* x, int b
 // ---------------------------------------------------------------------------
 constexpr int kFwdBlock = 256;
 #ifndef PLX_FWD_ROWS
-#define PLX_FWD_ROWS 32
+#define PLX_FWD_ROWS 128
 #endif
 #ifndef PLX_FWD_TBL
 #define PLX_FWD_TBL 1024
@@ -308,9 +308,9 @@ constexpr int kFwdWin = 4 * kFwdQuads * kFwdBlock;
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   __shared__ __align__(16) float buf[kFwdWin];
-  __shared__ float tbl[kFwdTbl];
-  const int tlen = min(d.tbl_len, kFwdTbl);
-  stage_table<kFwdBlock, kFwdTbl>(tbl, d.x, d.tbl_base, tlen);
+  __shared__ float tbl[kFwdTbl > 0 ? kFwdTbl : 1];
+  const int tlen = kFwdTbl > 0 ? min(d.tbl_len, kFwdTbl) : 0;
+  stage_table<kFwdBlock, (kFwdTbl > 0 ? kFwdTbl : 1)>(tbl, d.x, d.tbl_base, tlen);
   __syncthreads();
   const int row0 = blockIdx.x * kFwdRows;
   const int rend = min(row0 + kFwdRows, d.nrows);
