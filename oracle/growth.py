@@ -1,0 +1,586 @@
+"""CPU restatement of the reference's structural phases: PruneConn and the
+add_conn growth pipeline. TEST INFRASTRUCTURE ONLY -- tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may use it, always as
+the checker; the product (plastax_amd) never imports it.
+
+Every stage restates src/plastax/phases.py (the reference's JAX path) with
+numpy on logical arenas (a list of per-bucket column dicts in slot order,
+unit ids in the caller's numbering):
+
+- ``prune_conn``: phases.py:1444-1498;
+- candidate producers: phases.py:3640-4058 (per-unit / per-connection /
+  global proposals, exhaustive grid, shortlist, per-level shortlist);
+- validity and dedupe: phases.py:4061-4183, :2481-2570;
+- total order and selection: phases.py:4200-4487 (the comparison sort on
+  ``(-score, src, dst, index)``, NaN last, -0 == +0);
+- the claims: phases.py:2853-2982 (TOPOLOGICAL: the i-th growable winner
+  of a bucket takes its i-th free slot), :2985-3106 (PIPELINE: own dead
+  slots, then the tail);
+- the phase body and its flags: phases.py:4700-5187.
+
+The policies' callbacks are evaluated by this file's own interpreter of the
+traced site programs (``ox_site_eval`` in plastax_oracle.c), with its own
+Philox. Parity of the whole (policy -> commits) is pinned by the reference's
+``grow_*`` golden fixtures (tests/golden/), which are independent of both.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from typing import Any
+
+import numpy as np
+
+from oracle import oracle as _ox
+from plastax_amd import _site
+from plastax_amd.growth_config import GrowthConfig
+
+U32 = np.uint32
+NEG_INF = np.float32(-np.inf)
+
+_ROLE_ORDER = ("i", "j", "src", "dst", "cid")
+
+
+def _lib() -> ctypes.CDLL:
+    lib = _ox.load()
+    if not getattr(lib, "_site_ready", False):
+        lib.ox_site_eval.restype = None
+        lib.ox_site_eval.argtypes = [
+            ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p,
+        ]
+        lib.ox_philox32_batch.restype = None
+        lib.ox_philox32_batch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib._site_ready = True
+    return lib
+
+
+def philox32(seed: Any, counter: Any) -> np.ndarray:
+    """Philox-4x32-10 first word, by the C oracle (rng.py:109-141)."""
+    s = np.ascontiguousarray(np.asarray(seed, dtype=np.uint64).ravel())
+    c = np.ascontiguousarray(np.asarray(counter, dtype=np.uint64).ravel())
+    s, c = np.broadcast_arrays(s, c)
+    s, c = np.ascontiguousarray(s), np.ascontiguousarray(c)
+    out = np.empty(s.shape, dtype=np.uint32)
+    _lib().ox_philox32_batch(s.ctypes.data, c.ctypes.data, out.ctypes.data, s.size)
+    return out
+
+
+def keyed_word(network_seed: int, step: int, stream: int = 1) -> int:
+    """philox32(net_seed, (u32(step) << 8) | stream) (rng.py:222-245)."""
+    ctr = (np.uint64(np.uint32(step & 0xFFFFFFFF)) << np.uint64(8)) | np.uint64(stream & 0xFF)
+    return int(philox32(np.uint64(network_seed & 0xFFFFFFFFFFFFFFFF), ctr)[0])
+
+
+def conn_key(src: np.ndarray, dst: np.ndarray, occ: np.ndarray) -> np.ndarray:
+    """philox32((src << 32) | dst, occurrence) (rng.py:156-180)."""
+    s = np.asarray(src).astype(np.uint32).astype(np.uint64)
+    d = np.asarray(dst).astype(np.uint32).astype(np.uint64)
+    return philox32((s << np.uint64(32)) | d, np.asarray(occ).astype(np.uint32).astype(np.uint64))
+
+
+def _col32(a: np.ndarray) -> tuple[np.ndarray, int]:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.bool_ or a.dtype == np.uint8:
+        return np.ascontiguousarray(a.astype(np.uint8)), 1
+    if a.dtype.itemsize != 4:
+        raise TypeError(f"column of dtype {a.dtype} is not 32-bit")
+    return a, 4
+
+
+def site_eval(
+    prog: _site.SiteProgram,
+    n: int,
+    roles: dict[str, np.ndarray],
+    units: dict[str, np.ndarray],
+    globals_: Any,
+    *,
+    key: np.ndarray | None = None,
+    keyed: int = 0,
+    conns: dict[str, np.ndarray] | None = None,
+) -> list[np.ndarray]:
+    """Evaluate ``prog`` at n sites; returns one array per output, typed by
+    the program's output kinds."""
+    lib = _lib()
+    keep: list[Any] = []
+    role_ptrs = (ctypes.c_void_p * 5)()
+    for q, name in enumerate(_ROLE_ORDER):
+        if name in roles:
+            arr = np.ascontiguousarray(np.asarray(roles[name], dtype=np.int32))
+            assert arr.shape == (n,)
+            keep.append(arr)
+            role_ptrs[q] = arr.ctypes.data
+    num_units = int(next(iter(units.values())).shape[0])
+    uptr = (ctypes.c_void_p * max(1, len(prog.unit_fields)))()
+    ubytes = np.zeros(max(1, len(prog.unit_fields)), dtype=np.int32)
+    for f, name in enumerate(prog.unit_fields):
+        arr, nb = _col32(units[name])
+        keep.append(arr)
+        uptr[f] = arr.ctypes.data
+        ubytes[f] = nb
+    cptr = (ctypes.c_void_p * max(1, len(prog.conn_fields)))()
+    cbytes = np.zeros(max(1, len(prog.conn_fields)), dtype=np.int32)
+    for f, name in enumerate(prog.conn_fields):
+        assert conns is not None
+        arr, nb = _col32(conns[name])
+        keep.append(arr)
+        cptr[f] = arr.ctypes.data
+        cbytes[f] = nb
+    outs = [np.zeros(n, dtype=np.uint32) for _ in prog.out_kinds]
+    out_ptrs = (ctypes.c_void_p * max(1, len(outs)))()
+    for k, o in enumerate(outs):
+        out_ptrs[k] = o.ctypes.data
+    code = np.ascontiguousarray(prog.flat_code())
+    consts = np.ascontiguousarray(prog.const_bits(globals_))
+    key_arr = None
+    if key is not None:
+        key_arr = np.ascontiguousarray(np.asarray(key, dtype=np.uint32))
+        assert key_arr.shape == (n,)
+    lib.ox_site_eval(
+        code.ctypes.data, prog.ninstr, consts.ctypes.data, n, ctypes.addressof(role_ptrs),
+        None if key_arr is None else key_arr.ctypes.data, keyed & 0xFFFFFFFF,
+        ctypes.addressof(uptr), ubytes.ctypes.data, num_units, ctypes.addressof(cptr),
+        cbytes.ctypes.data, ctypes.addressof(out_ptrs),
+    )
+    typed = []
+    for o, kind in zip(outs, prog.out_kinds):
+        typed.append({"f": o.view(np.float32), "i": o.view(np.int32), "u": o, "b": o.astype(bool)}[kind])
+    return typed
+
+
+# ---------------------------------------------------------------------------
+# PruneConn (phases.py:1444-1498).
+# ---------------------------------------------------------------------------
+
+
+def prune_conn(prog: _site.SiteProgram, units: dict, conns: list[dict], globals_: Any) -> list[dict]:
+    """dead |= predicate(u, c, cid, g) for every slot of every bucket (cid is
+    the bucket-local slot)."""
+    out = []
+    for bucket in conns:
+        cap = bucket["dead"].shape[0]
+        (die,) = site_eval(prog, cap, {"cid": np.arange(cap, dtype=np.int32)}, units, globals_, conns=bucket)
+        nb = dict(bucket)
+        nb["dead"] = bucket["dead"].astype(bool) | die
+        out.append(nb)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Candidates, validity, dedupe, order, selection.
+# ---------------------------------------------------------------------------
+
+
+def clamp_proposals(src: np.ndarray, dst: np.ndarray, n: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """_clamp_proposals (phases.py:4041-4058)."""
+    ok = (src >= 0) & (src < n) & (dst >= 0) & (dst < n)
+    return np.where(ok, src, 0).astype(np.int32), np.where(ok, dst, 0).astype(np.int32), ok
+
+
+def top_k_ids(values: np.ndarray, m: int) -> np.ndarray:
+    """lax.top_k's indices: descending, equal values by lower index."""
+    order = np.lexsort((np.arange(values.size), -values.astype(np.float64)))
+    return order[:m].astype(np.int32)
+
+
+def apply_validity(src, dst, level, b, gap, pipeline, direction, self_loops) -> np.ndarray:
+    """apply_validity (phases.py:4061-4108)."""
+    ls, ld = level[src], level[dst]
+    ok = np.abs(ld - ls) <= gap
+    if not self_loops:
+        ok &= src != dst
+    if direction == "deeper":
+        ok &= ld > ls
+    elif direction == "same_or_deeper":
+        ok &= ld >= ls
+    if not pipeline:
+        ok &= ls == b
+    return ok
+
+
+def live_pair_member(bucket: dict, src: np.ndarray, dst: np.ndarray, n: int) -> np.ndarray:
+    """live_pair_member (phases.py:2481-2537): is (src, dst) a live edge."""
+    dead = bucket["dead"].astype(bool)
+    live = set(
+        zip(bucket["from_id"][~dead].astype(np.int64).tolist(), bucket["to_id"][~dead].astype(np.int64).tolist())
+    )
+    return np.fromiter(((int(s), int(d)) in live for s, d in zip(src, dst)), dtype=bool, count=src.size)
+
+
+def sort_key(scores: np.ndarray) -> np.ndarray:
+    """_sort_key (phases.py:4200-4205) with -0 folded to +0: NaN -> +inf."""
+    k = np.where(np.isnan(scores), np.float32(np.inf), -scores).astype(np.float32)
+    return np.where(k == 0, np.float32(0.0), k)
+
+
+def total_order(scores: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
+    """Ascending (-score, src, dst, index) (phases.py:4208-4321)."""
+    idx = np.arange(scores.size)
+    return np.lexsort((idx, dst.astype(np.int64), src.astype(np.int64), sort_key(scores).astype(np.float64)))
+
+
+def dedupe_step(scores: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
+    """dedupe_step / repeats_earlier (phases.py:4156-4183, :2540-2570): in the
+    stable score-descending order, every later copy of a pair goes to -inf."""
+    neg = -scores.astype(np.float64)
+    neg = np.where(np.isnan(neg), np.inf, neg)  # jnp sorts NaN last
+    by_score = np.argsort(neg, kind="stable")
+    seen: set[tuple[int, int]] = set()
+    repeat = np.zeros(scores.size, dtype=bool)
+    for pos in by_score:
+        key = (int(src[pos]), int(dst[pos]))
+        if key in seen:
+            repeat[pos] = True
+        else:
+            seen.add(key)
+    return np.where(repeat, NEG_INF, scores).astype(np.float32)
+
+
+def select_per_segment(scores, src, dst, segment, nseg, k) -> list[tuple[np.ndarray, np.ndarray]]:
+    """select_per_segment (phases.py:4356-4423): each segment's first k in
+    the total order, and which of the k hold a member."""
+    perm = total_order(scores, src, dst)
+    seg = segment[perm]
+    out = []
+    for s in range(nseg):
+        members = perm[seg == s][:k]
+        top = np.zeros(k, dtype=np.int64)
+        top[: members.size] = members
+        filled = np.arange(k) < members.size
+        out.append((top, filled))
+    return out
+
+
+def select_level_major(scores, src, dst, level, k, num_levels) -> tuple[np.ndarray, np.ndarray]:
+    """select_level_major (phases.py:4426-4469)."""
+    n = scores.size
+    width = min(n, k * num_levels)
+    perm = total_order(scores, src, dst)
+    by_level = np.argsort(level[perm], kind="stable")
+    sorted_level = level[perm][by_level]
+    first = np.searchsorted(sorted_level, sorted_level, side="left")
+    wins = np.arange(n) - first < k
+    keep = np.argsort(~wins, kind="stable")[:width]
+    return perm[by_level][keep], wins[keep]
+
+
+def level_major(top, filled, level) -> tuple[np.ndarray, np.ndarray]:
+    """level_major (phases.py:4472-4487)."""
+    key = np.where(filled, level.astype(np.int64), np.iinfo(np.int32).max)
+    order = np.argsort(key, kind="stable")
+    return top[order], filled[order]
+
+
+# ---------------------------------------------------------------------------
+# Claims.
+# ---------------------------------------------------------------------------
+
+
+def nth_free_slots(dead: np.ndarray, rank: np.ndarray) -> np.ndarray:
+    """The rank-th (0-based) dead slot of a bucket (phases.py:2670-2754)."""
+    free = np.flatnonzero(dead.astype(bool))
+    return free[rank]
+
+
+def claim_topological(conns, claims, values_of):
+    """xla_claim_buckets (phases.py:2853-2982) on one device."""
+    out, overflowed, resort = [], [], []
+    for b, (bucket, claim) in enumerate(zip(conns, claims)):
+        growable = claim["growable"]
+        dead = bucket["dead"].astype(bool)
+        total_free = int(dead.sum())
+        rank = np.cumsum(growable.astype(np.int64)) - 1
+        committed = growable & (rank < total_free)
+        over = growable & (rank >= total_free)
+        nb = {k: v.copy() for k, v in bucket.items()}
+        where = np.flatnonzero(committed)
+        slots = nth_free_slots(dead, rank[where])
+        vals = values_of(b, where)
+        for name in nb:
+            if name == "dead":
+                nb[name][slots] = False
+            else:
+                nb[name][slots] = vals[name]
+        out.append(nb)
+        overflowed.append(over)
+        resort.append(committed & claim["violating"])
+    return out, overflowed, resort
+
+
+def claim_pipeline(bucket, claim, cand_level, unit_level, tail_start, values_of):
+    """pipeline_claim (phases.py:2985-3106) on one device."""
+    growable = claim["growable"]
+    k = growable.size
+    dead = bucket["dead"].astype(bool)
+    cap = dead.size
+    num_levels = unit_level.size
+    pos = np.arange(cap)
+    owner = np.clip(bucket["from_id"].astype(np.int64), 0, num_levels - 1)
+    domain = np.where(dead & (pos < tail_start), unit_level[owner].astype(np.int64), num_levels)
+    count = np.bincount(domain, minlength=num_levels + 1)[:num_levels]
+    level = np.clip(cand_level.astype(np.int64), 0, num_levels - 1)
+    key = np.where(growable, level, num_levels)
+    order = np.argsort(key, kind="stable")
+    sorted_key = key[order]
+    first = np.searchsorted(sorted_key, sorted_key, side="left")
+    own_rank = np.zeros(k, dtype=np.int64)
+    own_rank[order] = np.arange(k) - first
+    own = growable & (own_rank < count[level])
+    spill = growable & ~own
+    spill_rank = np.zeros(k, dtype=np.int64)
+    spill_rank[order] = np.cumsum(spill[order].astype(np.int64)) - 1
+    tail_free = cap - tail_start
+    to_tail = spill & (spill_rank < tail_free)
+    over = spill & ~to_tail
+    committed = own | to_tail
+    slot_order = np.argsort(domain, kind="stable")
+    start = np.cumsum(count) - count
+    own_slot = slot_order[np.clip(start[level] + own_rank, 0, cap - 1)]
+    target = np.where(own, own_slot, np.where(to_tail, tail_start + spill_rank, cap))
+    nb = {k2: v.copy() for k2, v in bucket.items()}
+    where = np.flatnonzero(committed)
+    vals = values_of(0, where)
+    for name in nb:
+        if name == "dead":
+            nb[name][target[where]] = False
+        else:
+            nb[name][target[where]] = vals[name]
+    new_tail = tail_start + int(to_tail.sum())
+    return nb, over, committed & claim["violating"], new_tail
+
+
+# ---------------------------------------------------------------------------
+# The add_conn phase.
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass
+class GrowthResult:
+    conns: list[dict]
+    grown: int
+    overflow: bool
+    needs_resort: bool
+    tail_start: int
+    fired: bool
+    winners: list[tuple[int, int]]  # (src, dst) of every committed edge, in claim order
+
+
+def add_conn(
+    net: Any,
+    static: Any,
+    units: dict[str, np.ndarray],
+    conns: list[dict[str, np.ndarray]],
+    *,
+    step: int,
+    globals_: Any,
+    tail_start: int = 0,
+    units_added: int = 0,
+    needs_resort: bool = False,
+) -> GrowthResult:
+    """One add_conn phase (phases.py:4490-5203) on host arrays."""
+    ac = net.add_conn
+    cfg = GrowthConfig.of(net, static)
+    n = cfg.num_units
+    nb = cfg.num_buckets
+    interval = int(getattr(net, "structural_interval", 1))
+    if not cfg.fires(ac, step=step, interval=interval, units_added=units_added, globals_=globals_):
+        return GrowthResult(conns, 0, False, needs_resort, tail_start, False, [])
+    level = units["level"].astype(np.int64)
+    live = None if "pruned" not in units else ~units["pruned"].astype(bool)
+    unit_dtypes = {s.name: np.dtype(s.dtype) for s in static.unit_fields}
+    conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
+    keyed = keyed_word(static.seed, step)
+
+    in_range = None
+    p_score = None
+    if cfg.propose:
+        prog = _site.trace_propose(ac, cfg.proposer, unit_dtypes, conn_dtypes, globals_)
+        P = cfg.proposals
+        if cfg.proposer == "per_unit":
+            s = np.arange(n * P)
+            i, j = (s // P).astype(np.int32), (s % P).astype(np.int32)
+            ps, pd, p_score = site_eval(prog, n * P, {"i": i, "j": j}, units, globals_, key=i.astype(np.uint32), keyed=keyed)
+            src, dst, in_range = clamp_proposals(ps, pd, n)
+            if live is not None:
+                in_range &= np.repeat(live, P)
+        elif cfg.proposer == "global":
+            j = np.arange(P, dtype=np.int32)
+            ps, pd, p_score = site_eval(prog, P, {"j": j}, units, globals_, key=np.zeros(P, np.uint32), keyed=keyed)
+            src, dst, in_range = clamp_proposals(ps, pd, n)
+        else:
+            flat = {name: np.concatenate([b[name] for b in conns]) for name in conns[0]}
+            c_src = flat["from_id"].astype(np.int64)
+            c_dst = flat["to_id"].astype(np.int64)
+            dead = flat["dead"].astype(bool)
+            total = c_src.size
+            k_src = np.where(dead, n, c_src)
+            k_dst = np.where(dead, n, c_dst)
+            perm = np.lexsort((np.arange(total), k_dst, k_src))
+            r_src, r_dst = c_src[perm], c_dst[perm]
+            new_run = np.ones(total, dtype=bool)
+            new_run[1:] = (r_src[1:] != r_src[:-1]) | (r_dst[1:] != r_dst[:-1])
+            run_start = np.maximum.accumulate(np.where(new_run, np.arange(total), 0))
+            occ = np.zeros(total, dtype=np.int64)
+            occ[perm] = np.arange(total) - run_start
+            cid = np.repeat(np.arange(total, dtype=np.int32), P)
+            j = np.tile(np.arange(P, dtype=np.int32), total)
+            key = conn_key(c_src[cid], c_dst[cid], occ[cid])
+            ps, pd, sc = site_eval(prog, total * P, {"cid": cid, "j": j}, units, globals_, key=key,
+                                   keyed=keyed, conns=flat)
+            by_rank = (perm[:, None] * P + np.arange(P)[None, :]).ravel()
+            src, dst, in_range = clamp_proposals(ps[by_rank], pd[by_rank], n)
+            p_score = sc[by_rank]
+            in_range &= np.repeat(~dead[perm], P)
+    elif cfg.shortlist:
+        iprog = _site.trace_importance(ac, unit_dtypes, globals_)
+        (imp,) = site_eval(iprog, n, {"i": np.arange(n, dtype=np.int32)}, units, globals_)
+        if live is not None:
+            imp = np.where(live, imp, NEG_INF)
+        M = cfg.pool_side
+        if not cfg.per_level:
+            top = top_k_ids(imp, M)
+            src = np.repeat(top, M).astype(np.int32)
+            dst = np.tile(top, M).astype(np.int32)
+    else:
+        src = np.repeat(np.arange(n, dtype=np.int32), n)
+        dst = np.tile(np.arange(n, dtype=np.int32), n)
+
+    def bucket_valid(b: int, s: np.ndarray, d: np.ndarray) -> np.ndarray:
+        v = apply_validity(s, d, level, b, cfg.max_level_gap, cfg.pipeline, cfg.direction, cfg.allow_self_loops)
+        if cfg.propose:
+            v &= in_range
+        if live is not None:
+            v &= live[s] & live[d]
+        if cfg.dedupe_live:
+            v &= ~live_pair_member(conns[b], s, d, n)
+        return v
+
+    sprog = None if cfg.propose else _site.trace_score(ac, unit_dtypes, globals_)
+
+    def scores_of(s: np.ndarray, d: np.ndarray, v: np.ndarray) -> np.ndarray:
+        if cfg.propose:
+            out = np.where(v, p_score, NEG_INF).astype(np.float32)
+        else:
+            (raw,) = site_eval(sprog, s.size, {"src": s, "dst": d}, units, globals_)
+            out = np.where(v, raw, NEG_INF).astype(np.float32)
+        if cfg.dedupe_step:
+            out = dedupe_step(out, s, d)
+        return out
+
+    k = cfg.k
+    selections = []  # (src, dst, valid, scores, top_idx, filled) per bucket
+    if cfg.per_level:
+        M = cfg.pool_side
+        grids = []
+        for b in range(nb):
+            s_imp = np.where(level == b, imp, NEG_INF)
+            s_top = top_k_ids(s_imp, M)
+            win = np.abs(level - b) <= cfg.max_level_gap
+            if cfg.direction == "deeper":
+                win &= level > b
+            elif cfg.direction == "same_or_deeper":
+                win &= level >= b
+            d_top = top_k_ids(np.where(win, imp, NEG_INF), M)
+            s = np.repeat(s_top, M).astype(np.int32)
+            d = np.tile(d_top, M).astype(np.int32)
+            v = bucket_valid(b, s, d)
+            grids.append((s, d, v, scores_of(s, d, v)))
+        if cfg.step_scope:
+            cs, cd, cv, csc = (np.concatenate(cols) for cols in zip(*grids))
+            k_step = min(k, cs.size)
+            perm = total_order(csc, cs, cd)[:k_step]
+            top_level = level[cs[perm]]
+            for b in range(nb):
+                selections.append((cs, cd, cv, csc, perm, top_level == b))
+        else:
+            for s, d, v, sc in grids:
+                perm = total_order(sc, s, d)[:k]
+                selections.append((s, d, v, sc, perm, np.ones(perm.size, dtype=bool)))
+    else:
+        valid = bucket_valid(0, src, dst)
+        for b in range(1, nb):
+            valid |= bucket_valid(b, src, dst)
+        scores = scores_of(src, dst, valid)
+        src_level = level[src]
+        if cfg.pipeline:
+            if cfg.step_scope:
+                top, filled = select_per_segment(scores, src, dst, np.zeros(src.size, np.int64), 1, k)[0]
+                top, filled = level_major(top, filled, src_level[top])
+            else:
+                top, filled = select_level_major(scores, src, dst, src_level, k, n)
+            selections.append((src, dst, valid, scores, top, filled))
+        elif cfg.step_scope:
+            top, filled = select_per_segment(scores, src, dst, np.zeros(src.size, np.int64), 1, k)[0]
+            top_level = src_level[top]
+            for b in range(nb):
+                selections.append((src, dst, valid, scores, top, filled & (top_level == b)))
+        else:
+            for top, filled in select_per_segment(scores, src, dst, src_level, nb, k):
+                selections.append((src, dst, valid, scores, top, filled))
+
+    thresh = None
+    if cfg.selection == "threshold":
+        thresh = np.float32(np.asarray(ac.threshold(globals_)))
+    iprog_init, init_names = _site.trace_init(ac, unit_dtypes, static.conn_fields, globals_)
+    claims, levels_of = [], []
+    for s, d, v, sc, top, filled in selections:
+        ts, td = s[top], d[top]
+        growable = filled & v[top] & np.isfinite(sc[top])
+        if thresh is not None:
+            growable &= sc[top] >= thresh
+        claims.append({"growable": growable, "violating": ~(level[td] > level[ts]), "src": ts, "dst": td})
+        levels_of.append(level[ts])
+    if cfg.max_new_per_step is not None:
+        prior = 0
+        for c in claims:
+            g32 = c["growable"].astype(np.int64)
+            rank = np.cumsum(g32) - 1 + prior
+            prior += int(g32.sum())
+            c["growable"] = c["growable"] & (rank < cfg.max_new_per_step)
+
+    specs = {sp.name: sp for sp in static.conn_fields}
+
+    def values_of(b: int, where: np.ndarray) -> dict[str, np.ndarray]:
+        ts = claims[b]["src"][where].astype(np.int32)
+        td = claims[b]["dst"][where].astype(np.int32)
+        outs = site_eval(iprog_init, ts.size, {"src": ts, "dst": td}, units, globals_) if ts.size else [
+            np.zeros(0) for _ in init_names
+        ]
+        vals = {}
+        for name, spec in specs.items():
+            if name == "from_id":
+                vals[name] = ts.astype(spec.dtype)
+            elif name == "to_id":
+                vals[name] = td.astype(spec.dtype)
+            elif name == "dead":
+                continue
+            elif name in init_names:
+                vals[name] = outs[init_names.index(name)].astype(spec.dtype)
+            else:
+                vals[name] = np.full(ts.size, spec.default, dtype=spec.dtype)
+        return vals
+
+    winners: list[tuple[int, int]] = []
+    if cfg.pipeline:
+        bucket, over, resort, new_tail = claim_pipeline(conns[0], claims[0], levels_of[0], level, tail_start, values_of)
+        new_conns = [bucket]
+        overflow = bool(over.any())
+        reassigning = bool(resort.any())
+        committed = [claims[0]["growable"] & ~over]
+        tail_start = new_tail
+    else:
+        new_conns, overs, resorts = claim_topological(conns, claims, values_of)
+        overflow = any(bool(o.any()) for o in overs)
+        reassigning = any(bool(r.any()) for r in resorts)
+        committed = [c["growable"] & ~o for c, o in zip(claims, overs)]
+    for c, m in zip(claims, committed):
+        winners.extend((int(a), int(b2)) for a, b2 in zip(c["src"][m], c["dst"][m]))
+    if overflow and cfg.on_overflow == "error":
+        raise RuntimeError(
+            "add_conn overflow: selected candidates exceeded the free connection capacity"
+        )
+    grown = int(sum(int(m.sum()) for m in committed))
+    return GrowthResult(new_conns, grown, overflow, needs_resort or reassigning, tail_start, True, winners)

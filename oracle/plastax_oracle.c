@@ -625,3 +625,175 @@ OX_API int64_t ox_nth_free_slots(int64_t cap, const uint8_t* dead, int64_t n,
   for (; r < n; ++r) slots[r] = -1;
   return found;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Site programs: the growth and pruning callbacks (propose, score,          */
+/* importance, init, PruneConn predicate) that the reference evaluates under */
+/* jax.vmap once per site (phases.py:3640-4058, :1444-1498). Registers hold  */
+/* 32-bit patterns of float32 / int32 / uint32 / bool values; the opcodes    */
+/* are listed in plastax_amd/_site.py (SOP). Integer semantics are jnp's     */
+/* with 64-bit types off (wrapping int32/uint32, floor division and modulo,  */
+/* saturating float->int casts with NaN -> 0). The rng draw of a site is     */
+/* philox32(((keyed << 32) | key), (j << 16) | sub) (rng.py:206-259).         */
+/* ------------------------------------------------------------------------ */
+
+enum {
+  S_CONST = 1, S_IDX = 2, S_LDU = 3, S_LDC = 4, S_RNG = 5, S_MOV = 6, S_SEL = 7,
+  S_OUT = 8,
+  S_FADD = 10, S_FSUB, S_FMUL, S_FDIV, S_FNEG, S_FABS, S_FMAX, S_FMIN, S_FTANH,
+  S_FEXP, S_FLOG, S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR,
+  S_FGT = 30, S_FGE, S_FLT, S_FLE, S_FEQ, S_FNE,
+  S_IADD = 40, S_ISUB, S_IMUL, S_INEG, S_IABS, S_IMAX, S_IMIN, S_IFLOORDIV,
+  S_IMOD, S_ISIGN,
+  S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
+  S_UMAX = 60, S_UMIN, S_UFLOORDIV, S_UMOD, S_UGT, S_UGE, S_ULT, S_ULE,
+  S_AND = 70, S_OR, S_XOR, S_NOT, S_SHL, S_SHRU, S_SHRI, S_BNOT,
+  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B
+};
+
+#define OX_SREGS 32
+
+static inline float ox_f(uint32_t b) { return ox_bits_to_float(b); }
+static inline uint32_t ox_u(float f) { return ox_float_to_bits(f); }
+
+static int32_t ox_floordiv_i32(int32_t a, int32_t b) {
+  if (b == 0) return a == 0 ? -1 : -2; /* XLA's x/0 = -1, then jnp's floor fix */
+  if (a == INT32_MIN && b == -1) return INT32_MIN;
+  int32_t q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) q -= 1;
+  return q;
+}
+static int32_t ox_mod_i32(int32_t a, int32_t b) {
+  if (b == 0) return a;
+  if (b == -1) return 0;
+  int32_t r = a % b;
+  if (r != 0 && ((r < 0) != (b < 0))) r += b;
+  return r;
+}
+static int32_t ox_f2i(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return INT32_MAX;
+  if (x <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)x;
+}
+static uint32_t ox_f2u(float x) {
+  if (x != x || x <= 0.0f) return 0u;
+  if (x >= 4294967296.0f) return UINT32_MAX;
+  return (uint32_t)x;
+}
+static uint32_t ox_load32(const void* base, int32_t bytes, int64_t at) {
+  if (bytes == 1) return ((const uint8_t*)base)[at] != 0;
+  return ((const uint32_t*)base)[at];
+}
+
+/* Runs the program once for each of n sites. roles[r] (r = i, j, src, dst,
+ * cid) is the role's per-site int32 array or NULL; key the per-site rng key
+ * word or NULL; ufields/ubytes the unit columns (num_units long) and their
+ * element sizes; cfields/cbytes the conn columns read at cid. Out slot k of
+ * site s goes to outs[k][s]. */
+OX_API void ox_site_eval(const int32_t* prog, int32_t ninstr, const uint32_t* consts,
+                         int64_t n, const int32_t* const* roles, const uint32_t* key,
+                         uint32_t keyed, const void* const* ufields,
+                         const int32_t* ubytes, int64_t num_units,
+                         const void* const* cfields, const int32_t* cbytes,
+                         uint32_t* const* outs) {
+  for (int64_t s = 0; s < n; ++s) {
+    uint32_t r[OX_SREGS];
+    memset(r, 0, sizeof r);
+    int32_t ctx[5];
+    for (int q = 0; q < 5; ++q) ctx[q] = roles[q] ? roles[q][s] : 0;
+    uint64_t site_seed = ((uint64_t)keyed << 32) | (key ? key[s] : 0u);
+    for (int32_t k = 0; k < ninstr; ++k) {
+      const int32_t* q = prog + 4 * k;
+      int32_t d = q[1], a = q[2], b = q[3];
+      uint32_t x = r[a], y = r[b];
+      int32_t xi = (int32_t)x, yi = (int32_t)y;
+      switch (q[0]) {
+        case S_CONST: r[d] = consts[a]; break;
+        case S_IDX: r[d] = (uint32_t)ctx[a]; break;
+        case S_LDU: {
+          int64_t at = (int32_t)y;
+          if (at < 0) at = 0;
+          if (at > num_units - 1) at = num_units - 1;
+          r[d] = ox_load32(ufields[a], ubytes[a], at);
+          break;
+        }
+        case S_LDC: r[d] = ox_load32(cfields[a], cbytes[a], ctx[4]); break;
+        case S_RNG:
+          r[d] = ox_philox32(site_seed, ((uint64_t)(uint32_t)ctx[1] << 16) | (uint32_t)a);
+          break;
+        case S_MOV: r[d] = x; break;
+        case S_SEL: r[d] = x ? r[b] : r[b + 1]; break;
+        case S_OUT: outs[d][s] = x; break;
+        case S_FADD: r[d] = ox_u(ox_f(x) + ox_f(y)); break;
+        case S_FSUB: r[d] = ox_u(ox_f(x) - ox_f(y)); break;
+        case S_FMUL: r[d] = ox_u(ox_f(x) * ox_f(y)); break;
+        case S_FDIV: r[d] = ox_u(ox_f(x) / ox_f(y)); break;
+        case S_FNEG: r[d] = x ^ 0x80000000u; break;
+        case S_FABS: r[d] = x & 0x7FFFFFFFu; break;
+        case S_FMAX: r[d] = ox_u(ox_fmax_nan(ox_f(x), ox_f(y))); break;
+        case S_FMIN: r[d] = ox_u(ox_fmin_nan(ox_f(x), ox_f(y))); break;
+        case S_FTANH: r[d] = ox_u(ox_tanhf(ox_f(x))); break;
+        case S_FEXP: r[d] = ox_u(ox_expf(ox_f(x))); break;
+        case S_FLOG: r[d] = ox_u(ox_logf(ox_f(x))); break;
+        case S_FSQRT: r[d] = ox_u(sqrtf(ox_f(x))); break;
+        case S_FSIGMOID: r[d] = ox_u(ox_sigmoidf(ox_f(x))); break;
+        case S_FSQUARE: r[d] = ox_u(ox_f(x) * ox_f(x)); break;
+        case S_FRELU: r[d] = ox_u(ox_fmax_nan(ox_f(x), 0.0f)); break;
+        case S_FSIGN: {
+          float v = ox_f(x);
+          r[d] = v > 0.0f ? ox_u(1.0f) : (v < 0.0f ? ox_u(-1.0f) : x);
+          break;
+        }
+        case S_FFLOOR: r[d] = ox_u(floorf(ox_f(x))); break;
+        case S_FGT: r[d] = ox_f(x) > ox_f(y); break;
+        case S_FGE: r[d] = ox_f(x) >= ox_f(y); break;
+        case S_FLT: r[d] = ox_f(x) < ox_f(y); break;
+        case S_FLE: r[d] = ox_f(x) <= ox_f(y); break;
+        case S_FEQ: r[d] = ox_f(x) == ox_f(y); break;
+        case S_FNE: r[d] = ox_f(x) != ox_f(y); break;
+        case S_IADD: r[d] = x + y; break;
+        case S_ISUB: r[d] = x - y; break;
+        case S_IMUL: r[d] = x * y; break;
+        case S_INEG: r[d] = 0u - x; break;
+        case S_IABS: r[d] = xi < 0 ? 0u - x : x; break;
+        case S_IMAX: r[d] = xi > yi ? x : y; break;
+        case S_IMIN: r[d] = xi < yi ? x : y; break;
+        case S_IFLOORDIV: r[d] = (uint32_t)ox_floordiv_i32(xi, yi); break;
+        case S_IMOD: r[d] = (uint32_t)ox_mod_i32(xi, yi); break;
+        case S_ISIGN: r[d] = (uint32_t)(xi > 0 ? 1 : (xi < 0 ? -1 : 0)); break;
+        case S_IGT: r[d] = xi > yi; break;
+        case S_IGE: r[d] = xi >= yi; break;
+        case S_ILT: r[d] = xi < yi; break;
+        case S_ILE: r[d] = xi <= yi; break;
+        case S_IEQ: r[d] = x == y; break;
+        case S_INE: r[d] = x != y; break;
+        case S_UMAX: r[d] = x > y ? x : y; break;
+        case S_UMIN: r[d] = x < y ? x : y; break;
+        case S_UFLOORDIV: r[d] = y ? x / y : UINT32_MAX; break;
+        case S_UMOD: r[d] = y ? x % y : x; break;
+        case S_UGT: r[d] = x > y; break;
+        case S_UGE: r[d] = x >= y; break;
+        case S_ULT: r[d] = x < y; break;
+        case S_ULE: r[d] = x <= y; break;
+        case S_AND: r[d] = x & y; break;
+        case S_OR: r[d] = x | y; break;
+        case S_XOR: r[d] = x ^ y; break;
+        case S_NOT: r[d] = ~x; break;
+        case S_BNOT: r[d] = x == 0u; break;
+        case S_SHL: r[d] = y >= 32u ? 0u : x << y; break;
+        case S_SHRU: r[d] = y >= 32u ? 0u : x >> y; break;
+        case S_SHRI:
+          r[d] = y >= 32u ? (xi < 0 ? UINT32_MAX : 0u) : (uint32_t)(xi >> y);
+          break;
+        case S_I2F: r[d] = ox_u((float)xi); break;
+        case S_U2F: r[d] = ox_u((float)x); break;
+        case S_F2I: r[d] = (uint32_t)ox_f2i(ox_f(x)); break;
+        case S_F2U: r[d] = ox_f2u(ox_f(x)); break;
+        case S_F2B: r[d] = ox_f(x) != 0.0f; break;
+        case S_I2B: r[d] = x != 0u; break;
+        default: break;
+      }
+    }
+  }
+}

@@ -79,10 +79,118 @@ def _f32(x: Any) -> np.float32:
     return np.float32(x)
 
 
-class Expr:
-    """A node of a traced float32 expression."""
+# Value kinds of a traced expression: float32 ("f"), int32 ("i"), uint32
+# ("u"), bool ("b"), and the weakly typed Python scalars ("wi", "wf") that
+# take the other operand's type, as jnp's weak typing does.
+_WEAK = {"wi", "wf"}
+_FLOAT_ONLY = {"tanh", "exp", "log", "sqrt", "sigmoid", "floor"}
+_INT_ONLY = {"mod", "floordiv", "shl", "shr"}
+_LOGIC = {"and", "or", "xor"}
 
-    __slots__ = ("op", "args", "value", "field", "role")
+
+def kind_of_dtype(dtype: Any) -> str:
+    """The value kind of a numpy dtype (x64 off: 64-bit types narrow to 32)."""
+    dt = np.dtype(dtype)
+    if dt == np.bool_:
+        return "b"
+    if dt.kind == "f":
+        return "f"
+    if dt.kind == "u":
+        return "u"
+    if dt.kind == "i":
+        return "i"
+    raise UnsupportedPolicyError(f"dtype {dt} cannot be traced")
+
+
+def _promote(a: "Expr", b: "Expr", op: str) -> str:
+    """The result kind of a binary arithmetic op (jnp promotion, x64 off)."""
+    ka, kb = a.dtype, b.dtype
+    strong = {k for k in (ka, kb) if k not in _WEAK}
+    weak = {k for k in (ka, kb) if k in _WEAK}
+    if not strong:
+        return "wf" if "wf" in weak else "wi"
+    if "f" in strong:
+        return "f"
+    if "i" in strong and "u" in strong:
+        raise UnsupportedPolicyError("int32 mixed with uint32 promotes to 64 bits in jnp")
+    if "wf" in weak:
+        return "f"
+    if "i" in strong:
+        return "i"
+    if "u" in strong:
+        return "u"
+    # only bools
+    if weak:
+        return "i"
+    if op in _LOGIC or op in ("eq", "ne", "max", "min"):
+        return "b"
+    raise UnsupportedPolicyError(f"arithmetic {op!r} on two booleans")
+
+
+def _as_kind(x: "Expr", kind: str) -> "Expr":
+    """``x`` as a value of ``kind`` (constants are retyped, others cast)."""
+    if x.dtype == kind:
+        return x
+    if x.op == "const":
+        return Expr("const", value=x.value, dtype=kind)
+    return Expr("cvt", (x,), dtype=kind)
+
+
+def binary(op: str, a: Any, b: Any) -> "Expr":
+    """A typed binary node: arithmetic, comparison or logical."""
+    a, b = lift(a), lift(b)
+    if op == "div":
+        t = "f"  # true division: ints go to float32, as jnp's / does
+    else:
+        t = _promote(a, b, op)
+    if t in _WEAK:
+        t = "f" if t == "wf" else "i"
+    if op in _INT_ONLY and t not in ("i", "u"):
+        raise UnsupportedPolicyError(f"{op!r} is traced on integers only")
+    if op in _LOGIC and t not in ("b", "i", "u"):
+        raise UnsupportedPolicyError(f"{op!r} is traced on booleans and integers only")
+    a2, b2 = _as_kind(a, t), _as_kind(b, t)
+    out = "b" if op in ("gt", "ge", "lt", "le", "eq", "ne") else t
+    return Expr(op, (a2, b2), dtype=out)
+
+
+def unary(op: str, x: Any) -> "Expr":
+    """A typed unary node."""
+    x = lift(x)
+    k = x.dtype
+    if k in _WEAK:
+        k = "f" if k == "wf" else "i"
+    if op in _FLOAT_ONLY or k == "b" and op not in ("not",):
+        k = "f"
+    if op == "not":
+        if k not in ("b", "i", "u"):
+            raise UnsupportedPolicyError("~ is traced on booleans and integers only")
+    return Expr(op, (_as_kind(x, k),), dtype=k)
+
+
+def select(cond: Any, a: Any, b: Any) -> "Expr":
+    """where(cond, a, b): the branches promoted to one kind."""
+    c = lift(cond)
+    if c.dtype != "b":
+        c = binary("ne", c, Expr("const", value=0, dtype="wi"))
+    a, b = lift(a), lift(b)
+    t = _promote(a, b, "sel")
+    if t in _WEAK:
+        t = "f" if t == "wf" else "i"
+    return Expr("sel", (c, _as_kind(a, t), _as_kind(b, t)), dtype=t)
+
+
+def cast(x: Any, dtype: Any) -> "Expr":
+    """x.astype(dtype)."""
+    x = lift(x)
+    k = kind_of_dtype(dtype)
+    return _as_kind(x, k)
+
+
+class Expr:
+    """A node of a traced expression; ``dtype`` is its value kind."""
+
+    __slots__ = ("op", "args", "value", "field", "role", "dtype")
     __array_ufunc__ = None  # numpy scalars defer to the reflected operators
 
     def __init__(
@@ -93,21 +201,25 @@ class Expr:
         value: Any = None,
         field: str | None = None,
         role: str | None = None,
+        dtype: str = "f",
     ) -> None:
         self.op = op
         self.args = tuple(args)
         self.value = value
         self.field = field
         self.role = role
+        self.dtype = dtype
 
     # -- construction helpers -------------------------------------------------
     def __repr__(self) -> str:
         if self.op == "const":
-            return repr(float(self.value))
+            return repr(self.value)
         if self.op in ("ldu", "ldc"):
             return f"{self.field}[{self.role}]"
         if self.op in ("acc", "target", "global"):
             return self.op if self.field is None else f"g.{self.field}"
+        if self.op == "idx":
+            return str(self.role)
         return f"{self.op}({', '.join(map(repr, self.args))})"
 
     def __bool__(self) -> bool:
@@ -119,80 +231,122 @@ class Expr:
 
     # -- arithmetic -----------------------------------------------------------
     def __add__(self, o: Any) -> "Expr":
-        return Expr("add", (self, lift(o)))
+        return binary("add", self, o)
 
     def __radd__(self, o: Any) -> "Expr":
-        return Expr("add", (lift(o), self))
+        return binary("add", o, self)
 
     def __sub__(self, o: Any) -> "Expr":
-        return Expr("sub", (self, lift(o)))
+        return binary("sub", self, o)
 
     def __rsub__(self, o: Any) -> "Expr":
-        return Expr("sub", (lift(o), self))
+        return binary("sub", o, self)
 
     def __mul__(self, o: Any) -> "Expr":
-        return Expr("mul", (self, lift(o)))
+        return binary("mul", self, o)
 
     def __rmul__(self, o: Any) -> "Expr":
-        return Expr("mul", (lift(o), self))
+        return binary("mul", o, self)
 
     def __truediv__(self, o: Any) -> "Expr":
-        return Expr("div", (self, lift(o)))
+        return binary("div", self, o)
 
     def __rtruediv__(self, o: Any) -> "Expr":
-        return Expr("div", (lift(o), self))
+        return binary("div", o, self)
+
+    def __floordiv__(self, o: Any) -> "Expr":
+        return binary("floordiv", self, o)
+
+    def __rfloordiv__(self, o: Any) -> "Expr":
+        return binary("floordiv", o, self)
+
+    def __mod__(self, o: Any) -> "Expr":
+        return binary("mod", self, o)
+
+    def __rmod__(self, o: Any) -> "Expr":
+        return binary("mod", o, self)
+
+    def __lshift__(self, o: Any) -> "Expr":
+        return binary("shl", self, o)
+
+    def __rshift__(self, o: Any) -> "Expr":
+        return binary("shr", self, o)
+
+    def __and__(self, o: Any) -> "Expr":
+        return binary("and", self, o)
+
+    def __rand__(self, o: Any) -> "Expr":
+        return binary("and", o, self)
+
+    def __or__(self, o: Any) -> "Expr":
+        return binary("or", self, o)
+
+    def __ror__(self, o: Any) -> "Expr":
+        return binary("or", o, self)
+
+    def __xor__(self, o: Any) -> "Expr":
+        return binary("xor", self, o)
+
+    def __rxor__(self, o: Any) -> "Expr":
+        return binary("xor", o, self)
+
+    def __invert__(self) -> "Expr":
+        return unary("not", self)
 
     def __neg__(self) -> "Expr":
-        return Expr("neg", (self,))
+        return unary("neg", self)
 
     def __pos__(self) -> "Expr":
         return self
 
     def __abs__(self) -> "Expr":
-        return Expr("abs", (self,))
+        return unary("abs", self)
 
     def __pow__(self, o: Any) -> "Expr":
         # jnp's x ** 2 lowers to integer_pow, i.e. one multiply x * x.
         if isinstance(o, (int, np.integer)) and int(o) == 2:
-            return Expr("square", (self,))
+            return unary("square", self)
         if isinstance(o, (int, np.integer)) and int(o) == 1:
             return self
         raise UnsupportedPolicyError(f"only x ** 2 is supported in a traced policy, got ** {o!r}")
 
     def __gt__(self, o: Any) -> "Expr":
-        return Expr("gt", (self, lift(o)))
+        return binary("gt", self, o)
 
     def __ge__(self, o: Any) -> "Expr":
-        return Expr("ge", (self, lift(o)))
+        return binary("ge", self, o)
 
     def __lt__(self, o: Any) -> "Expr":
-        return Expr("lt", (self, lift(o)))
+        return binary("lt", self, o)
 
     def __le__(self, o: Any) -> "Expr":
-        return Expr("le", (self, lift(o)))
+        return binary("le", self, o)
 
     def __eq__(self, o: Any) -> "Expr":  # type: ignore[override]
-        return Expr("eq", (self, lift(o)))
+        return binary("eq", self, o)
 
     def __ne__(self, o: Any) -> "Expr":  # type: ignore[override]
-        return Expr("ne", (self, lift(o)))
+        return binary("ne", self, o)
 
     def astype(self, dtype: Any) -> "Expr":
-        if np.dtype(dtype) not in (np.dtype(np.float32), np.dtype(np.bool_)):
-            raise UnsupportedPolicyError(f"cast to {dtype} in a traced policy")
-        return self
+        return cast(self, dtype)
 
 
 def lift(x: Any) -> Expr:
-    """A traced value, or a float32 constant for a Python/numpy scalar."""
+    """A traced value, or a constant node for a Python/numpy scalar (Python
+    scalars are weakly typed; numpy scalars carry their dtype)."""
     if isinstance(x, Expr):
         return x
     if isinstance(x, (bool, np.bool_)):
-        return Expr("const", value=_f32(1.0 if x else 0.0))
-    if isinstance(x, (int, float, np.integer, np.floating)):
-        return Expr("const", value=_f32(x))
+        return Expr("const", value=bool(x), dtype="b")
+    if isinstance(x, int):
+        return Expr("const", value=int(x), dtype="wi")
+    if isinstance(x, float):
+        return Expr("const", value=float(x), dtype="wf")
+    if isinstance(x, (np.integer, np.floating)):
+        return Expr("const", value=x.item(), dtype=kind_of_dtype(x.dtype))
     if isinstance(x, np.ndarray) and x.shape == ():
-        return Expr("const", value=_f32(x))
+        return Expr("const", value=x.item(), dtype=kind_of_dtype(x.dtype))
     raise UnsupportedPolicyError(f"cannot trace a {type(x).__name__} value in a policy")
 
 
@@ -393,9 +547,17 @@ def compile_program(
         if not free:
             raise UnsupportedPolicyError("a policy expression needs too many registers")
         op = node.op
+        if node.dtype in ("i", "u") and op != "const":
+            raise UnsupportedPolicyError(
+                f"integer arithmetic ({op!r}) cannot run in a unit program"
+            )
         if op == "const":
             k = const_index(("c", np.float32(node.value).tobytes()), np.float32(node.value))
             instr = ("const", k, 0)
+        elif op == "cvt":
+            if node.args[0].dtype not in ("f", "b", "wf", "wi"):
+                raise UnsupportedPolicyError("integer casts cannot run in a unit program")
+            instr = ("mov", reg[id(node.args[0])], 0)
         elif op == "global":
             k = const_index(("g", node.field), np.float32(0.0))
             globals_at[k] = str(node.field)

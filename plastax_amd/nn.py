@@ -6,13 +6,13 @@ from typing import Any
 
 import numpy as np
 
-from plastax_amd._expr import Expr, lift
+from plastax_amd._expr import Expr, unary
 
 
 def sigmoid(x: Any) -> Any:
     """1 / (1 + exp(-x)), as jax.nn.sigmoid (lax.logistic)."""
     if isinstance(x, Expr):
-        return Expr("sigmoid", (lift(x),))
+        return unary("sigmoid", x)
     x = np.float32(x)
     return np.float32(1.0) / (np.float32(1.0) + np.exp(-x))
 
@@ -20,11 +20,11 @@ def sigmoid(x: Any) -> Any:
 def relu(x: Any) -> Any:
     """max(x, 0), as jax.nn.relu."""
     if isinstance(x, Expr):
-        return Expr("relu", (lift(x),))
+        return unary("relu", x)
     return np.maximum(np.float32(x), np.float32(0.0))
 
 
 def tanh(x: Any) -> Any:
     if isinstance(x, Expr):
-        return Expr("tanh", (lift(x),))
+        return unary("tanh", x)
     return np.tanh(np.float32(x))

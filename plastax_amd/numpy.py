@@ -11,7 +11,7 @@ from typing import Any
 
 import numpy as np
 
-from plastax_amd._expr import Expr, UnsupportedPolicyError, lift
+from plastax_amd._expr import Expr, UnsupportedPolicyError, binary, cast, lift, select, unary
 
 float32 = np.float32
 int32 = np.int32
@@ -29,7 +29,7 @@ def _traced(*xs: Any) -> bool:
 def _unary(name: str, fn: Any) -> Any:
     def op(x: Any) -> Any:
         if _traced(x):
-            return Expr(name, (lift(x),))
+            return unary(name, x)
         return fn(np.float32(x))
 
     op.__name__ = name
@@ -48,7 +48,7 @@ sign = _unary("sign", np.sign)
 
 def square(x: Any) -> Any:
     if _traced(x):
-        return Expr("square", (lift(x),))
+        return unary("square", x)
     x = np.float32(x)
     return np.float32(x * x)
 
@@ -56,7 +56,7 @@ def square(x: Any) -> Any:
 def _binary(name: str, fn: Any) -> Any:
     def op(a: Any, b: Any) -> Any:
         if _traced(a, b):
-            return Expr(name, (lift(a), lift(b)))
+            return binary(name, a, b)
         return fn(np.float32(a), np.float32(b))
 
     op.__name__ = name
@@ -70,12 +70,59 @@ subtract = _binary("sub", np.subtract)
 multiply = _binary("mul", np.multiply)
 divide = _binary("div", np.divide)
 greater = _binary("gt", np.greater)
+greater_equal = _binary("ge", np.greater_equal)
 less = _binary("lt", np.less)
+less_equal = _binary("le", np.less_equal)
+equal = _binary("eq", np.equal)
+not_equal = _binary("ne", np.not_equal)
+floor = _unary("floor", np.floor)
+
+
+def _int_binary(name: str, fn: Any) -> Any:
+    def op(a: Any, b: Any) -> Any:
+        if _traced(a, b):
+            return binary(name, a, b)
+        return fn(a, b)
+
+    op.__name__ = name
+    return op
+
+
+floor_divide = _int_binary("floordiv", np.floor_divide)
+remainder = _int_binary("mod", np.remainder)
+mod = remainder
+logical_and = _int_binary("and", np.logical_and)
+logical_or = _int_binary("or", np.logical_or)
+logical_xor = _int_binary("xor", np.logical_xor)
+bitwise_and = _int_binary("and", np.bitwise_and)
+bitwise_or = _int_binary("or", np.bitwise_or)
+bitwise_xor = _int_binary("xor", np.bitwise_xor)
+right_shift = _int_binary("shr", np.right_shift)
+left_shift = _int_binary("shl", np.left_shift)
+
+
+def logical_not(x: Any) -> Any:
+    if _traced(x):
+        return unary("not", cast(x, np.bool_))
+    return np.logical_not(x)
+
+
+def isfinite(x: Any) -> Any:
+    """|x| < inf (false for NaN and the infinities)."""
+    if _traced(x):
+        return binary("lt", unary("abs", cast(x, np.float32)), np.float32(np.inf))
+    return np.isfinite(x)
+
+
+def astype(x: Any, dtype: Any) -> Any:
+    if _traced(x):
+        return cast(x, dtype)
+    return np.asarray(x).astype(dtype)
 
 
 def where(cond: Any, a: Any, b: Any) -> Any:
     if _traced(cond, a, b):
-        return Expr("sel", (lift(cond), lift(a), lift(b)))
+        return select(cond, a, b)
     return np.where(cond, np.float32(a), np.float32(b))
 
 
@@ -90,7 +137,7 @@ def sum(x: Any, axis: Any = None) -> Any:  # noqa: A001 -- mirrors jnp.sum
 
 def asarray(x: Any, dtype: Any = None) -> Any:
     if _traced(x):
-        return x
+        return x if dtype is None else cast(x, dtype)
     return np.asarray(x, dtype=dtype)
 
 
