@@ -66,8 +66,12 @@ def test_softmax_ce_matches_golden_exactly(oracle, name: str) -> None:
 
 def test_golden_fixtures_are_all_consumed() -> None:
     """Every golden fixture copied into tests/golden has a consumer here."""
+    import growth_cases
+
     names = {p.stem for p in nets.GOLDEN.glob("*.json")}
-    consumed = {"passes_relu_topological", "passes_relu_pipeline", *LOSS_GOLDENS}
+    growth = {p.stem for p in nets.GOLDEN.glob("grow_*.json")}
+    assert growth == set(growth_cases.names(lambda d: True))  # test_growth_oracle.py
+    consumed = {"passes_relu_topological", "passes_relu_pipeline", *LOSS_GOLDENS, *growth}
     assert names == consumed
 
 
