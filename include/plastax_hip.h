@@ -275,9 +275,284 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
                   float* out, void* stream);
 
 /* sizeof of the descriptor structs, in the order plx_program, plx_finalize,
- * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc (for binding layers to check their mirrors). Writes
- * min(n, 6) values and returns 6. */
+ * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc,
+ * plx_site_prog, plx_site_desc, plx_sort_key, plx_sort_desc,
+ * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc (for binding
+ * layers to check their mirrors). Writes min(n, 13) values and returns 13. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
+
+/* ========================================================================
+ * Structural phases: PruneConn and add_conn growth (plastax_amd/csrc/
+ * structural.hip). They work on the *logical* arena: every bucket's columns
+ * in slot order, concatenated bucket after bucket into flat columns (bucket
+ * b at [off_b, off_b + cap_b)), unit ids in the caller's numbering.
+ * ======================================================================== */
+
+#define PLX_MAX_SINSTR 96
+#define PLX_MAX_SCONST 32
+#define PLX_MAX_SFIELDS 8
+#define PLX_MAX_SOUTS 8
+
+/* A traced growth / pruning callback (propose, score, importance, init,
+ * PruneConn predicate: phases.py:3640-4058, :1444-1498). 32-bit registers
+ * hold float32 / int32 / uint32 / bool values; opcodes are listed in
+ * plastax_amd/_site.py (SOP). Unit field f is read at an int index clamped
+ * to [0, num_units); conn field f at the site's cid. ubytes/cbytes: 4, or 1
+ * for byte (bool) columns. */
+typedef struct plx_site_prog {
+  int32_t ninstr;
+  int32_t nout;
+  int32_t reserved[2];
+  int32_t code[4 * PLX_MAX_SINSTR];
+  uint32_t consts[PLX_MAX_SCONST];
+  const void* ufields[PLX_MAX_SFIELDS];
+  const void* cfields[PLX_MAX_SFIELDS];
+  int32_t ubytes[PLX_MAX_SFIELDS];
+  int32_t cbytes[PLX_MAX_SFIELDS];
+} plx_site_prog;
+
+/* How site s maps to the roles (i, j, src, dst, cid) and the rng key. */
+#define PLX_SITES_UNIT 0   /* i = s / per, j = s % per; key i (per-unit proposals, importance) */
+#define PLX_SITES_GLOBAL 1 /* j = s; key 0 (phases.py:3766-3810) */
+#define PLX_SITES_CONN 2   /* r = s / per, j = s % per, cid = list_a[r];
+                              key conn_key(from_id[cid], to_id[cid], occ[cid]) */
+#define PLX_SITES_GRID 3   /* g = s / per^2: src = list_a[g per + a], dst = list_b[g per + b],
+                              with s % per^2 = a per + b (candidate grids) */
+#define PLX_SITES_PAIRS 4  /* src = list_a[s], dst = list_b[s] (init of the winners) */
+#define PLX_SITES_EDGE 5   /* cid = s (PruneConn) */
+
+/* One evaluation of a site program over n sites (replaces the jax.vmap of a
+ * growth / pruning callback). The rng of a site is philox32(((keyed << 32)
+ * | key), (j << 16) | sub) with keyed = philox32(net_seed, (step << 8) | 1)
+ * (rng.py:206-259). Out slot k of site s is written to outs[k][s] (32-bit
+ * patterns); with or_into set, slot 0 is instead OR-ed into that byte column
+ * (dead |= predicate). n_dev, when set, holds the site count (<= n). */
+typedef struct plx_site_desc {
+  plx_site_prog prog;
+  int64_t n;
+  int32_t kind;
+  int32_t per;
+  int32_t num_units;
+  int32_t step;
+  uint64_t net_seed;
+  const int32_t* list_a;
+  const int32_t* list_b;
+  const int32_t* from_id;
+  const int32_t* to_id;
+  const int32_t* occ;
+  const int32_t* n_dev;
+  void* outs[PLX_MAX_SOUTS];
+  uint8_t* or_into;
+} plx_site_desc;
+
+PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
+
+/* Ordered stream compaction (the free-slot accounting of phases.py:2573-2754
+ * and every "which candidates survive" list): out[k] = the k-th position p
+ * in [0, n) whose flag is set, ascending; *count = their number. Flag of p:
+ * mode 0 u8[p] != 0, 1 u8[p] == 0, 2 f32[p] finite, 3 i32[p] != 0. n_dev
+ * optional. scratch: plx_scratch_ints(n) ints. */
+#define PLX_FLAG_U8 0
+#define PLX_FLAG_U8_ZERO 1
+#define PLX_FLAG_FINITE 2
+#define PLX_FLAG_I32 3
+PLX_EXPORT int plx_compact(int64_t n, const int32_t* n_dev, int32_t mode, const void* flags,
+                           int32_t* out, int32_t* count, int32_t* scratch, void* stream);
+
+/* Exclusive prefix sum of n int32 (n_dev optional); *total (optional) gets
+ * the sum. scratch: plx_scratch_ints(n) ints. */
+PLX_EXPORT int plx_scan_i32(int64_t n, const int32_t* n_dev, const int32_t* in, int32_t* out,
+                            int32_t* total, int32_t* scratch, void* stream);
+
+/* Scratch ints plx_compact / plx_scan_i32 / plx_sort need for n elements. */
+PLX_EXPORT int64_t plx_scratch_ints(int64_t n);
+
+/* Sort keys, least significant first; each is derived from the index being
+ * sorted (idx) and ordered ascending over its low `bits` bits:
+ *   I32      a[idx] (int32 read as unsigned; callers keep it >= 0)
+ *   SCORE    the total order's leading key of the float a[idx]: -score, NaN
+ *            as +inf, -0 as +0 (phases.py:4200-4281), as an ordered uint32
+ *   LEVEL_OF b[a[idx]] (a unit's level through an id column)
+ *   PAIR16   (a[idx] << 16) | b[idx] (ids below 2^16)
+ *   DEADMAX  dead-masked id: b (u8) [idx] ? bits-max : a[idx]  */
+#define PLX_KEY_I32 0
+#define PLX_KEY_SCORE 1
+#define PLX_KEY_LEVEL_OF 2
+#define PLX_KEY_PAIR16 3
+#define PLX_KEY_DEADMAX 4
+typedef struct plx_sort_key {
+  int32_t kind;
+  int32_t bits;
+  const void* a;
+  const void* b;
+} plx_sort_key;
+
+/* Stable LSD radix sort of an index list by up to 6 keys (8-bit digits,
+ * 4096-element LDS-ranked tiles): the total order of phases.py:4237-4321
+ * and the other sorts of the growth pipeline. vals (n_max, count in n_dev
+ * or n_max) is sorted in place; keys/keys_alt/vals_alt are n_max uint32 of
+ * scratch, hist plx_scratch_ints(n_max) ints. */
+typedef struct plx_sort_desc {
+  int64_t n_max;
+  const int32_t* n_dev;
+  int32_t nkeys;
+  int32_t reserved;
+  plx_sort_key keys[6];
+  uint32_t* vals;
+  uint32_t* keys_buf;
+  uint32_t* keys_alt;
+  uint32_t* vals_alt;
+  int32_t* hist;
+} plx_sort_desc;
+
+PLX_EXPORT int plx_sort(const plx_sort_desc* d, void* stream);
+
+/* Candidate validity (phases.py:4061-4153, :4776-4800): score[s] becomes
+ * -inf unless the candidate (src[s], dst[s]) is in range (check_range:
+ * proposals; out-of-range ids are clamped to 0, phases.py:4041-4058), its
+ * proposer is live (proposer_dead[proposer_idx ? proposer_idx[s/per] :
+ * s/per] == 0, when proposer_dead is set), both endpoints are live (pruned
+ * optional), |level[dst] - level[src]| <= max_level_gap, the direction holds
+ * (0 any, 1 deeper, 2 same_or_deeper), it is no self-loop unless allowed,
+ * TOPOLOGICAL: level[src] is a bucket (and equals s / grid_sq when grid_sq >
+ * 0, the per-level grids), and with nlive > 0 the pair is not a live edge of
+ * its bucket: live_idx (count in nlive_dev, or nlive) lists the live flat
+ * slots sorted by (bucket, src, dst) over live_bucket/live_src/live_dst. */
+typedef struct plx_grow_filter_desc {
+  int64_t n;
+  int64_t grid_sq;
+  int32_t num_units;
+  int32_t num_buckets;
+  int32_t pipeline;
+  int32_t max_level_gap;
+  int32_t direction;
+  int32_t allow_self_loops;
+  int32_t check_range;
+  int32_t per;
+  int32_t* src;
+  int32_t* dst;
+  float* score;
+  const int32_t* level;
+  const uint8_t* pruned;
+  const int32_t* proposer_idx;
+  const uint8_t* proposer_dead;
+  int64_t nlive;            /* capacity of live_idx */
+  const int32_t* nlive_dev; /* optional: the live count in device memory */
+  const int32_t* live_idx;
+  const int32_t* live_bucket;
+  const int32_t* live_src;
+  const int32_t* live_dst;
+} plx_grow_filter_desc;
+
+PLX_EXPORT int plx_grow_filter(const plx_grow_filter_desc* d, void* stream);
+
+/* dedupe_step (phases.py:4156-4183): order lists candidate indices sorted by
+ * (src, dst), stably over the score-descending order; every copy of a pair
+ * after its first gets score -inf. */
+PLX_EXPORT int plx_grow_mark_repeats(int64_t n_max, const int32_t* n_dev, const int32_t* order,
+                                     const int32_t* src, const int32_t* dst, float* score,
+                                     void* stream);
+
+/* Selection (phases.py:4324-4469): sorted (n_max, count n_dev) lists
+ * candidate indices in the total order, level-major when per_segment. A
+ * candidate's segment is level[src[idx]]; with per_segment, the first k of
+ * every segment win (first: num_segments ints of scratch), else the first k
+ * overall. win[p] = 1 for winning positions. */
+PLX_EXPORT int plx_grow_select(int64_t n_max, const int32_t* n_dev, const int32_t* sorted,
+                               const int32_t* src, const int32_t* level, int32_t per_segment,
+                               int64_t k, int32_t num_segments, int32_t* first, uint8_t* win,
+                               void* stream);
+
+/* The claim and write of the winners (phases.py:2853-3106, :4944-5110).
+ * winners (n_max, count n_dev) lists candidate indices levels ascending, the
+ * total order within a level. A winner is growable if its score is finite and
+ * at least `threshold` (has_threshold); max_new_per_step (>0) caps the
+ * growable ones in list order. Its rank among its own level's growable
+ * winners picks its slot:
+ *   TOPOLOGICAL (pipeline = 0): its source level's bucket's rank-th free
+ *     slot: free_slots lists every dead flat slot ascending and bucket b's
+ *     run of it is free_info[2b] (start), free_info[2b + 1] (length), as
+ *     plx_bucket_free computes them;
+ *   PIPELINE: the rank-th of its level's own dead slots (own_slots grouped
+ *     by level, own_start / own_count per level), the rest spill to the tail
+ *     at tail_start, levels ascending, up to capacity.
+ * Committed winners write from_id, to_id, dead = 0 and every column in
+ * cols: from init output slot (init_out[q] for winner q) or the column's
+ * default bits. flags[0] += committed, flags[1] |= overflow, flags[2] |=
+ * committed with level[dst] <= level[src], flags[3] += tail slots used.
+ * scratch: 8 n_max + plx_scratch_ints(n_max) ints. */
+#define PLX_MAX_GROW_COLS 16
+typedef struct plx_grow_col {
+  void* ptr;
+  int32_t bytes;
+  int32_t init_slot; /* -1: write default_bits */
+  uint32_t default_bits;
+  int32_t reserved;
+} plx_grow_col;
+
+typedef struct plx_grow_claim_desc {
+  int64_t n_max;
+  const int32_t* n_dev;
+  const int32_t* winners;
+  const int32_t* src;
+  const int32_t* dst;
+  const float* score;
+  const int32_t* level;
+  int32_t pipeline;
+  int32_t num_buckets;
+  int32_t num_levels;
+  int32_t has_threshold;
+  float threshold;
+  int32_t max_new_per_step;
+  int64_t capacity;
+  int64_t tail_start;
+  const int32_t* free_slots;
+  const int32_t* free_info;
+  const int32_t* own_slots;
+  const int32_t* own_start;
+  const int32_t* own_count;
+  int32_t* from_id;
+  int32_t* to_id;
+  uint8_t* dead;
+  int32_t ncols;
+  int32_t reserved;
+  plx_grow_col cols[PLX_MAX_GROW_COLS];
+  const uint32_t* init_out[PLX_MAX_SOUTS];
+  int32_t* flags;
+  int32_t* scratch;
+} plx_grow_claim_desc;
+
+PLX_EXPORT int plx_grow_claim(const plx_grow_claim_desc* d, void* stream);
+
+/* PIPELINE claim domains (phases.py:3040-3049): domain[p] = level of the
+ * former source of dead slot p below tail_start, else num_levels. */
+PLX_EXPORT int plx_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id,
+                                   const int32_t* level, int32_t num_levels, int64_t tail_start,
+                                   int32_t* domain, void* stream);
+
+/* Occurrence of each live edge among its parallel edges (phases.py:
+ * 3990-4007): sorted lists the flat slots by (src, dst, slot), dead last;
+ * occ[sorted[p]] = p - (first position of that pair). */
+PLX_EXPORT int plx_occurrence(int64_t n, const int32_t* sorted, const int32_t* from_id,
+                              const int32_t* to_id, int32_t* occ, void* stream);
+
+/* Small helpers of the growth pipeline: out[p] = a[idx[p]] (gather); per
+ * level counts and first positions of a level-sorted list (count, start:
+ * nlevels each); each bucket's run of the ascending free list (bucket_off:
+ * num_buckets + 1 flat offsets; free_info: start, length per bucket). */
+PLX_EXPORT int plx_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t* idx,
+                              const int32_t* a, int32_t* out, void* stream);
+PLX_EXPORT int plx_level_counts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* count,
+                                int32_t* start, void* stream);
+PLX_EXPORT int plx_bucket_free(int32_t num_buckets, const int64_t* bucket_off,
+                               const int32_t* free_slots, const int32_t* nfree_total,
+                               int32_t* free_info, void* stream);
+/* importance masks for the shortlists (phases.py:3683-3746): out[u] = imp[u]
+ * where (mode 0: level[u] == b; mode 1: |level[u] - b| <= gap with the
+ * direction; mode 2: always) and the unit is live, else -inf. */
+PLX_EXPORT int plx_mask_importance(int32_t n, const float* imp, const int32_t* level,
+                                   const uint8_t* pruned, int32_t mode, int32_t b,
+                                   int32_t gap, int32_t direction, float* out, void* stream);
 
 PLX_EXPORT const char* plx_last_error(void);
 PLX_EXPORT int32_t plx_abi_version(void);

@@ -18,13 +18,18 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 5  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 6  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
 PLX_MAX_FIELDS = 8
 PLX_MAX_OUTS = 4
 PLX_MAX_TBL = 8192
+PLX_MAX_SINSTR = 96
+PLX_MAX_SCONST = 32
+PLX_MAX_SFIELDS = 8
+PLX_MAX_SOUTS = 8
+PLX_MAX_GROW_COLS = 16
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -164,6 +169,131 @@ class plx_update_desc(ctypes.Structure):
     ]
 
 
+class plx_site_prog(ctypes.Structure):
+    _fields_ = [
+        ("ninstr", c_i32),
+        ("nout", c_i32),
+        ("reserved", c_i32 * 2),
+        ("code", c_i32 * (4 * PLX_MAX_SINSTR)),
+        ("consts", ctypes.c_uint32 * PLX_MAX_SCONST),
+        ("ufields", c_vp * PLX_MAX_SFIELDS),
+        ("cfields", c_vp * PLX_MAX_SFIELDS),
+        ("ubytes", c_i32 * PLX_MAX_SFIELDS),
+        ("cbytes", c_i32 * PLX_MAX_SFIELDS),
+    ]
+
+
+class plx_site_desc(ctypes.Structure):
+    _fields_ = [
+        ("prog", plx_site_prog),
+        ("n", c_i64),
+        ("kind", c_i32),
+        ("per", c_i32),
+        ("num_units", c_i32),
+        ("step", c_i32),
+        ("net_seed", ctypes.c_uint64),
+        ("list_a", c_vp),
+        ("list_b", c_vp),
+        ("from_id", c_vp),
+        ("to_id", c_vp),
+        ("occ", c_vp),
+        ("n_dev", c_vp),
+        ("outs", c_vp * PLX_MAX_SOUTS),
+        ("or_into", c_vp),
+    ]
+
+
+class plx_sort_key(ctypes.Structure):
+    _fields_ = [("kind", c_i32), ("bits", c_i32), ("a", c_vp), ("b", c_vp)]
+
+
+class plx_sort_desc(ctypes.Structure):
+    _fields_ = [
+        ("n_max", c_i64),
+        ("n_dev", c_vp),
+        ("nkeys", c_i32),
+        ("reserved", c_i32),
+        ("keys", plx_sort_key * 6),
+        ("vals", c_vp),
+        ("keys_buf", c_vp),
+        ("keys_alt", c_vp),
+        ("vals_alt", c_vp),
+        ("hist", c_vp),
+    ]
+
+
+class plx_grow_filter_desc(ctypes.Structure):
+    _fields_ = [
+        ("n", c_i64),
+        ("grid_sq", c_i64),
+        ("num_units", c_i32),
+        ("num_buckets", c_i32),
+        ("pipeline", c_i32),
+        ("max_level_gap", c_i32),
+        ("direction", c_i32),
+        ("allow_self_loops", c_i32),
+        ("check_range", c_i32),
+        ("per", c_i32),
+        ("src", c_vp),
+        ("dst", c_vp),
+        ("score", c_vp),
+        ("level", c_vp),
+        ("pruned", c_vp),
+        ("proposer_idx", c_vp),
+        ("proposer_dead", c_vp),
+        ("nlive", c_i64),
+        ("nlive_dev", c_vp),
+        ("live_idx", c_vp),
+        ("live_bucket", c_vp),
+        ("live_src", c_vp),
+        ("live_dst", c_vp),
+    ]
+
+
+class plx_grow_col(ctypes.Structure):
+    _fields_ = [
+        ("ptr", c_vp),
+        ("bytes", c_i32),
+        ("init_slot", c_i32),
+        ("default_bits", ctypes.c_uint32),
+        ("reserved", c_i32),
+    ]
+
+
+class plx_grow_claim_desc(ctypes.Structure):
+    _fields_ = [
+        ("n_max", c_i64),
+        ("n_dev", c_vp),
+        ("winners", c_vp),
+        ("src", c_vp),
+        ("dst", c_vp),
+        ("score", c_vp),
+        ("level", c_vp),
+        ("pipeline", c_i32),
+        ("num_buckets", c_i32),
+        ("num_levels", c_i32),
+        ("has_threshold", c_i32),
+        ("threshold", c_f32),
+        ("max_new_per_step", c_i32),
+        ("capacity", c_i64),
+        ("tail_start", c_i64),
+        ("free_slots", c_vp),
+        ("free_info", c_vp),
+        ("own_slots", c_vp),
+        ("own_start", c_vp),
+        ("own_count", c_vp),
+        ("from_id", c_vp),
+        ("to_id", c_vp),
+        ("dead", c_vp),
+        ("ncols", c_i32),
+        ("reserved", c_i32),
+        ("cols", plx_grow_col * PLX_MAX_GROW_COLS),
+        ("init_out", c_vp * PLX_MAX_SOUTS),
+        ("flags", c_vp),
+        ("scratch", c_vp),
+    ]
+
+
 _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_bucket": (c_i32, [ctypes.POINTER(plx_forward_desc), c_vp]),
     "plx_backward_tiles": (c_i32, [ctypes.POINTER(plx_tile_desc), c_vp]),
@@ -181,6 +311,21 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_last_error": (ctypes.c_char_p, []),
     "plx_abi_version": (c_i32, []),
     "plx_struct_sizes": (c_i32, [ctypes.POINTER(c_i64), c_i32]),
+    "plx_site_eval": (c_i32, [ctypes.POINTER(plx_site_desc), c_vp]),
+    "plx_compact": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_scan_i32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_scratch_ints": (c_i64, [c_i64]),
+    "plx_sort": (c_i32, [ctypes.POINTER(plx_sort_desc), c_vp]),
+    "plx_grow_filter": (c_i32, [ctypes.POINTER(plx_grow_filter_desc), c_vp]),
+    "plx_grow_mark_repeats": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_grow_select": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_vp, c_vp, c_vp]),
+    "plx_grow_claim": (c_i32, [ctypes.POINTER(plx_grow_claim_desc), c_vp]),
+    "plx_pipeline_domain": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp]),
+    "plx_occurrence": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_gather_i32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_level_counts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "plx_bucket_free": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_mask_importance": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
 }
 
 # Entry points the header declares (checked by the CPU test suite).
@@ -193,6 +338,13 @@ STRUCTS = (
     plx_tile_desc,
     plx_partials_desc,
     plx_update_desc,
+    plx_site_prog,
+    plx_site_desc,
+    plx_sort_key,
+    plx_sort_desc,
+    plx_grow_filter_desc,
+    plx_grow_col,
+    plx_grow_claim_desc,
 )
 
 _lib: ctypes.CDLL | None = None

@@ -20,7 +20,31 @@
 #include <string>
 
 #include "../../include/plastax_hip.h"
+#include "px_common.h"
 #include "px_math.h"
+
+namespace plx_detail {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* what) {
+  g_last_error = what;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(err);
+    return PLX_ERR_HIP;
+  }
+  return PLX_OK;
+}
+
+}  // namespace plx_detail
+
+using plx_detail::check_launch;
+using plx_detail::fail;
 
 namespace {
 
@@ -47,21 +71,6 @@ __device__ __forceinline__ void st_stream(float* p, float4 a) {
   __builtin_nontemporal_store(v, reinterpret_cast<nt_v4f*>(p));
 }
 
-thread_local std::string g_last_error;
-
-int fail(int code, const char* what) {
-  g_last_error = what;
-  return code;
-}
-
-int check_launch(const char* what) {
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) {
-    g_last_error = std::string(what) + ": " + hipGetErrorString(err);
-    return PLX_ERR_HIP;
-  }
-  return PLX_OK;
-}
 
 // ---------------------------------------------------------------------------
 // Monoids (monoid.py:22-39): identity and pairwise combine.
@@ -957,28 +966,10 @@ __global__ __launch_bounds__(1024) void k_softmax_ce(int32_t n, const int32_t* i
   }
 }
 
-__device__ __forceinline__ uint32_t philox32_dev(uint64_t seed, uint64_t counter) {
-  uint32_t x0 = static_cast<uint32_t>(counter), x1 = static_cast<uint32_t>(counter >> 32);
-  uint32_t x2 = static_cast<uint32_t>(seed), x3 = static_cast<uint32_t>(seed >> 32);
-  uint32_t k0 = x2, k1 = x3;
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint32_t lo0 = 0xD2511F53u * x0, hi0 = __umulhi(0xD2511F53u, x0);
-    const uint32_t lo1 = 0xCD9E8D57u * x2, hi1 = __umulhi(0xCD9E8D57u, x2);
-    const uint32_t n0 = hi1 ^ x1 ^ k0, n2 = hi0 ^ x3 ^ k1;
-    x0 = n0;
-    x1 = lo1;
-    x2 = n2;
-    x3 = lo0;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return x0;
-}
 
 __global__ void k_philox(int64_t n, const uint64_t* seeds, const uint64_t* ctrs, uint32_t* out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = philox32_dev(seeds[i], ctrs[i]);
+  if (i < n) out[i] = px::philox32(seeds[i], ctrs[i]);
 }
 
 __global__ void k_math(int32_t op, int64_t n, const float* x, const float* y, float* out) {
@@ -1050,17 +1041,21 @@ int dispatch_rule(const plx_tile_desc& d, size_t lds, hipStream_t s) {
 
 extern "C" {
 
-const char* plx_last_error(void) { return g_last_error.c_str(); }
+const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 5; }
+int32_t plx_abi_version(void) { return 6; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[6] = {
+  const int64_t sizes[13] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
-      sizeof(plx_partials_desc),    sizeof(plx_update_desc)};
-  for (int32_t k = 0; k < n && k < 6; ++k) out[k] = sizes[k];
-  return 6;
+      sizeof(plx_partials_desc),    sizeof(plx_update_desc),
+      sizeof(plx_site_prog),        sizeof(plx_site_desc),
+      sizeof(plx_sort_key),         sizeof(plx_sort_desc),
+      sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
+      sizeof(plx_grow_claim_desc)};
+  for (int32_t k = 0; k < n && k < 13; ++k) out[k] = sizes[k];
+  return 13;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {

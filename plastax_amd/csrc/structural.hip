@@ -1,0 +1,1053 @@
+// structural.hip -- gfx950 kernels of the structural phases (PruneConn and
+// add_conn growth) and the C ABI declared in include/plastax_hip.h.
+//
+// These phases are integer / ordering work over candidate lists and the
+// logical arena: evaluate a traced callback once per site, compact the
+// survivors in order, sort them into the library's total order, select the
+// first k per source level and claim free slots in order. Every result is an
+// exact function of its inputs (integer atomics only count; no float
+// atomics), so the device reproduces the CPU restatement bit for bit.
+//
+// Building blocks:
+//  - site programs: a register interpreter over 32-bit float/int/uint/bool
+//    values, one thread per site, with the counter-based Philox stream of
+//    rng.py (no device state);
+//  - ordered compaction and exclusive scans: per-chunk counts (2048
+//    elements per 256-lane workgroup), one workgroup scanning the chunk
+//    totals, then a chunk pass that ranks with wave ballots and LDS;
+//  - stable LSD radix sort: 8-bit digits over 4096-element tiles, a
+//    digit-major histogram per tile, its scan, and a scatter that ranks each
+//    round of 256 keys with 8 wave ballots (peers with the same digit) plus
+//    per-wave LDS counts.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/plastax_hip.h"
+#include "px_common.h"
+#include "px_math.h"
+
+using plx_detail::check_launch;
+using plx_detail::fail;
+
+namespace {
+
+constexpr int kBlock = 256;          // lanes per workgroup (4 waves of 64)
+constexpr int kWaves = kBlock / 64;
+constexpr int kChunk = kBlock * 8;   // elements per scan / compaction chunk
+constexpr int kTile = kBlock * 16;   // elements per radix tile
+constexpr int kScanLanes = 1024;     // the single-workgroup scan
+
+__device__ __forceinline__ int64_t live_count(int64_t n_max, const int32_t* n_dev) {
+  if (!n_dev) return n_max;
+  const int64_t c = *n_dev;
+  return c < n_max ? (c < 0 ? 0 : c) : n_max;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = threadIdx.x & 63;
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+// Exclusive scan across a workgroup of BLOCK lanes; *total gets the sum.
+// lds: BLOCK / 64 + 1 ints. Every lane must call it.
+template <int BLOCK>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) lds[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < BLOCK / 64; ++w) {
+      const int t = lds[w];
+      lds[w] = run;
+      run += t;
+    }
+    lds[BLOCK / 64] = run;
+  }
+  __syncthreads();
+  const int out = x - v + lds[wave];
+  *total = lds[BLOCK / 64];
+  __syncthreads();
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Flags, chunk sums and the scans.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int flag_of(int32_t mode, const void* flags, int64_t p) {
+  switch (mode) {
+    case PLX_FLAG_U8: return static_cast<const uint8_t*>(flags)[p] != 0;
+    case PLX_FLAG_U8_ZERO: return static_cast<const uint8_t*>(flags)[p] == 0;
+    case PLX_FLAG_FINITE: {
+      const float f = static_cast<const float*>(flags)[p];
+      return (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u;
+    }
+    default: return static_cast<const int32_t*>(flags)[p] != 0;
+  }
+}
+
+// mode < 0: the values of `in` (a scan); else the flags (a compaction).
+__global__ void k_chunk_sums(int64_t n_max, const int32_t* n_dev, int32_t mode, const void* in,
+                             int32_t* sums) {
+  __shared__ int lds[kWaves + 1];
+  const int64_t n = live_count(n_max, n_dev);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  int acc = 0;
+  for (int r = 0; r < kChunk / kBlock; ++r) {
+    const int64_t p = base + r * kBlock + threadIdx.x;
+    if (p < n) acc += mode < 0 ? static_cast<const int32_t*>(in)[p] : flag_of(mode, in, p);
+  }
+  int total;
+  block_exclusive_scan<kBlock>(acc, lds, &total);
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// One workgroup: exclusive scan of sums[0, m) in place; total (optional).
+__global__ void k_scan_single(int64_t m, int32_t* sums, int32_t* total) {
+  __shared__ int lds[kScanLanes / 64 + 1];
+  const int64_t per = (m + kScanLanes - 1) / kScanLanes;
+  const int64_t lo = threadIdx.x * per;
+  const int64_t hi = lo + per < m ? lo + per : m;
+  int acc = 0;
+  for (int64_t i = lo; i < hi; ++i) acc += sums[i];
+  int all;
+  int run = block_exclusive_scan<kScanLanes>(acc, lds, &all);
+  for (int64_t i = lo; i < hi; ++i) {
+    const int v = sums[i];
+    sums[i] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0 && total) *total = all;
+}
+
+__global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t* in, int32_t* out,
+                             const int32_t* sums) {
+  __shared__ int lds[kWaves + 1];
+  const int64_t n = live_count(n_max, n_dev);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  int run = sums[blockIdx.x];
+  for (int r = 0; r < kChunk / kBlock; ++r) {
+    const int64_t p = base + r * kBlock + threadIdx.x;
+    const int v = p < n ? in[p] : 0;
+    int total;
+    const int ex = block_exclusive_scan<kBlock>(v, lds, &total);
+    if (p < n) out[p] = run + ex;
+    run += total;
+  }
+}
+
+__global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mode, const void* flags,
+                                int32_t* out, const int32_t* sums) {
+  const int64_t n = live_count(n_max, n_dev);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  __shared__ int wcnt[kWaves];
+  int run = sums[blockIdx.x];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int r = 0; r < kChunk / kBlock; ++r) {
+    const int64_t p = base + r * kBlock + threadIdx.x;
+    const int f = p < n ? flag_of(mode, flags, p) : 0;
+    const uint64_t m = __ballot(f);
+    if (lane == 0) wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int before = run;
+    int total = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      if (w < wave) before += wcnt[w];
+      total += wcnt[w];
+    }
+    if (f) out[before + __popcll(m & lanemask_lt())] = static_cast<int32_t>(p);
+    run += total;
+    __syncthreads();
+  }
+}
+
+int64_t chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
+
+// A fill kernel rather than hipMemsetAsync, so every node stays a kernel if a
+// caller captures these launches in a graph.
+__global__ void k_fill_i32(int64_t n, int32_t v, int32_t* out) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[p] = v;
+}
+
+int scan_or_compact(int64_t n_max, const int32_t* n_dev, int32_t mode, const void* in, int32_t* out,
+                    int32_t* total, int32_t* scratch, hipStream_t s, const char* what) {
+  const int64_t nc = chunks_of(n_max);
+  if (nc == 0) {
+    if (total) hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(64), 0, s, int64_t(1), 0, total);
+    return check_launch(what);
+  }
+  hipLaunchKernelGGL(k_chunk_sums, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev, mode, in, scratch);
+  hipLaunchKernelGGL(k_scan_single, dim3(1), dim3(kScanLanes), 0, s, nc, scratch, total);
+  if (mode < 0)
+    hipLaunchKernelGGL(k_chunk_scan, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev,
+                       static_cast<const int32_t*>(in), out, scratch);
+  else
+    hipLaunchKernelGGL(k_chunk_compact, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev, mode, in, out,
+                       scratch);
+  return check_launch(what);
+}
+
+// ---------------------------------------------------------------------------
+// Stable LSD radix sort.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t score_key(float f) {
+  float k = (f != f) ? __builtin_huge_valf() : -f;
+  if (k == 0.0f) k = 0.0f;  // -0 ties +0
+  const uint32_t u = __float_as_uint(k);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ void k_gather_key(int64_t n_max, const int32_t* n_dev, plx_sort_key key,
+                             const uint32_t* vals, uint32_t* keys) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint32_t idx = vals[p];
+    uint32_t k;
+    switch (key.kind) {
+      case PLX_KEY_SCORE: k = score_key(static_cast<const float*>(key.a)[idx]); break;
+      case PLX_KEY_LEVEL_OF: {
+        const int32_t id = static_cast<const int32_t*>(key.a)[idx];
+        k = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id]);
+        break;
+      }
+      case PLX_KEY_PAIR16:
+        k = (static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]) << 16) |
+            (static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[idx]) & 0xFFFFu);
+        break;
+      case PLX_KEY_DEADMAX:
+        k = static_cast<const uint8_t*>(key.b)[idx]
+                ? (key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u))
+                : static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]);
+        break;
+      default: k = static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]); break;
+    }
+    keys[p] = k;
+  }
+}
+
+__global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, const uint32_t* keys, int shift,
+                             int64_t ntiles, int32_t* hist) {
+  __shared__ int h[256];
+  const int64_t n = live_count(n_max, n_dev);
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  for (int r = 0; r < kTile / kBlock; ++r) {
+    const int64_t p = base + r * kBlock + threadIdx.x;
+    if (p < n) atomicAdd(&h[(keys[p] >> shift) & 255u], 1);
+  }
+  __syncthreads();
+  hist[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x] = h[threadIdx.x];
+}
+
+__global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint32_t* keys_in,
+                                const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
+                                int shift, int64_t ntiles, const int32_t* hist) {
+  __shared__ int s_off[256];
+  __shared__ int s_wcnt[kWaves][256];
+  const int64_t n = live_count(n_max, n_dev);
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  s_off[t] = hist[static_cast<int64_t>(t) * ntiles + blockIdx.x];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  for (int r = 0; r < kTile / kBlock; ++r) {
+    for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
+    __syncthreads();
+    const int64_t p = base + r * kBlock + t;
+    const bool valid = p < n;
+    const uint32_t key = valid ? keys_in[p] : 0u;
+    const uint32_t val = valid ? vals_in[p] : 0u;
+    const uint32_t d = (key >> shift) & 255u;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool on = (d >> bit) & 1u;
+      const uint64_t b = __ballot(on);
+      peers &= on ? b : ~b;
+    }
+    const int lrank = __popcll(peers & lanemask_lt());
+    if (valid && lane == __ffsll(static_cast<long long>(peers)) - 1) s_wcnt[wave][d] = __popcll(peers);
+    __syncthreads();
+    {
+      int run = s_off[t];
+      for (int w = 0; w < kWaves; ++w) {
+        const int c = s_wcnt[w][t];
+        s_wcnt[w][t] = run;
+        run += c;
+      }
+      s_off[t] = run;
+    }
+    __syncthreads();
+    if (valid) {
+      const int pos = s_wcnt[wave][d] + lrank;
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void k_copy_u32(int64_t n_max, const int32_t* n_dev, const uint32_t* in, uint32_t* out) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[p] = in[p];
+}
+
+int grid_for(int64_t n) {
+  const int64_t g = (n + kBlock - 1) / kBlock;
+  return static_cast<int>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+// ---------------------------------------------------------------------------
+// Site programs.
+// ---------------------------------------------------------------------------
+
+enum : int32_t {
+  S_CONST = 1, S_IDX = 2, S_LDU = 3, S_LDC = 4, S_RNG = 5, S_MOV = 6, S_SEL = 7, S_OUT = 8,
+  S_FADD = 10, S_FSUB, S_FMUL, S_FDIV, S_FNEG, S_FABS, S_FMAX, S_FMIN, S_FTANH, S_FEXP, S_FLOG,
+  S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR,
+  S_FGT = 30, S_FGE, S_FLT, S_FLE, S_FEQ, S_FNE,
+  S_IADD = 40, S_ISUB, S_IMUL, S_INEG, S_IABS, S_IMAX, S_IMIN, S_IFLOORDIV, S_IMOD, S_ISIGN,
+  S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
+  S_UMAX = 60, S_UMIN, S_UFLOORDIV, S_UMOD, S_UGT, S_UGE, S_ULT, S_ULE,
+  S_AND = 70, S_OR, S_XOR, S_NOT, S_SHL, S_SHRU, S_SHRI, S_BNOT,
+  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B
+};
+
+__device__ __forceinline__ float fmax_nan(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ float fmin_nan(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ int32_t floordiv_i32(int32_t a, int32_t b) {
+  if (b == 0) return a == 0 ? -1 : -2;
+  if (a == INT32_MIN && b == -1) return INT32_MIN;
+  int32_t q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) q -= 1;
+  return q;
+}
+__device__ __forceinline__ int32_t mod_i32(int32_t a, int32_t b) {
+  if (b == 0) return a;
+  if (b == -1) return 0;
+  int32_t r = a % b;
+  if (r != 0 && ((r < 0) != (b < 0))) r += b;
+  return r;
+}
+__device__ __forceinline__ int32_t f2i(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return INT32_MAX;
+  if (x <= -2147483648.0f) return INT32_MIN;
+  return static_cast<int32_t>(x);
+}
+__device__ __forceinline__ uint32_t f2u(float x) {
+  if (x != x || x <= 0.0f) return 0u;
+  if (x >= 4294967296.0f) return UINT32_MAX;
+  return static_cast<uint32_t>(x);
+}
+__device__ __forceinline__ uint32_t load32(const void* base, int32_t bytes, int64_t at) {
+  if (bytes == 1) return static_cast<const uint8_t*>(base)[at] != 0;
+  return static_cast<const uint32_t*>(base)[at];
+}
+
+struct Site {
+  int32_t role[5];  // i, j, src, dst, cid
+  uint64_t seed;    // (keyed << 32) | key
+};
+
+__device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units, uint32_t* outv) {
+  uint32_t r[32];
+  for (int k = 0; k < p.ninstr; ++k) {
+    const int op = p.code[4 * k], d = p.code[4 * k + 1], a = p.code[4 * k + 2], b = p.code[4 * k + 3];
+    const uint32_t x = r[a & 31], y = r[b & 31];
+    const int32_t xi = static_cast<int32_t>(x), yi = static_cast<int32_t>(y);
+    const float xf = __uint_as_float(x), yf = __uint_as_float(y);
+    uint32_t v = 0;
+    switch (op) {
+      case S_CONST: v = p.consts[a]; break;
+      case S_IDX: v = static_cast<uint32_t>(c.role[a]); break;
+      case S_LDU: {
+        int64_t at = yi;
+        at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
+        v = load32(p.ufields[a], p.ubytes[a], at);
+        break;
+      }
+      case S_LDC: v = load32(p.cfields[a], p.cbytes[a], c.role[4]); break;
+      case S_RNG:
+        v = px::philox32(c.seed, (static_cast<uint64_t>(static_cast<uint32_t>(c.role[1])) << 16) |
+                                     static_cast<uint32_t>(a));
+        break;
+      case S_MOV: v = x; break;
+      case S_SEL: v = x ? r[b & 31] : r[(b + 1) & 31]; break;
+      case S_OUT: outv[d] = x; continue;
+      case S_FADD: v = __float_as_uint(xf + yf); break;
+      case S_FSUB: v = __float_as_uint(xf - yf); break;
+      case S_FMUL: v = __float_as_uint(xf * yf); break;
+      case S_FDIV: v = __float_as_uint(xf / yf); break;
+      case S_FNEG: v = x ^ 0x80000000u; break;
+      case S_FABS: v = x & 0x7FFFFFFFu; break;
+      case S_FMAX: v = __float_as_uint(fmax_nan(xf, yf)); break;
+      case S_FMIN: v = __float_as_uint(fmin_nan(xf, yf)); break;
+      case S_FTANH: v = __float_as_uint(px::tanhf_(xf)); break;
+      case S_FEXP: v = __float_as_uint(px::expf_(xf)); break;
+      case S_FLOG: v = __float_as_uint(px::logf_(xf)); break;
+      case S_FSQRT: v = __float_as_uint(__builtin_sqrtf(xf)); break;
+      case S_FSIGMOID: v = __float_as_uint(px::sigmoidf_(xf)); break;
+      case S_FSQUARE: v = __float_as_uint(xf * xf); break;
+      case S_FRELU: v = __float_as_uint(fmax_nan(xf, 0.0f)); break;
+      case S_FSIGN: v = xf > 0.0f ? 0x3F800000u : (xf < 0.0f ? 0xBF800000u : x); break;
+      case S_FFLOOR: v = __float_as_uint(floorf(xf)); break;
+      case S_FGT: v = xf > yf; break;
+      case S_FGE: v = xf >= yf; break;
+      case S_FLT: v = xf < yf; break;
+      case S_FLE: v = xf <= yf; break;
+      case S_FEQ: v = xf == yf; break;
+      case S_FNE: v = xf != yf; break;
+      case S_IADD: v = x + y; break;
+      case S_ISUB: v = x - y; break;
+      case S_IMUL: v = x * y; break;
+      case S_INEG: v = 0u - x; break;
+      case S_IABS: v = xi < 0 ? 0u - x : x; break;
+      case S_IMAX: v = xi > yi ? x : y; break;
+      case S_IMIN: v = xi < yi ? x : y; break;
+      case S_IFLOORDIV: v = static_cast<uint32_t>(floordiv_i32(xi, yi)); break;
+      case S_IMOD: v = static_cast<uint32_t>(mod_i32(xi, yi)); break;
+      case S_ISIGN: v = static_cast<uint32_t>(xi > 0 ? 1 : (xi < 0 ? -1 : 0)); break;
+      case S_IGT: v = xi > yi; break;
+      case S_IGE: v = xi >= yi; break;
+      case S_ILT: v = xi < yi; break;
+      case S_ILE: v = xi <= yi; break;
+      case S_IEQ: v = x == y; break;
+      case S_INE: v = x != y; break;
+      case S_UMAX: v = x > y ? x : y; break;
+      case S_UMIN: v = x < y ? x : y; break;
+      case S_UFLOORDIV: v = y ? x / y : UINT32_MAX; break;
+      case S_UMOD: v = y ? x % y : x; break;
+      case S_UGT: v = x > y; break;
+      case S_UGE: v = x >= y; break;
+      case S_ULT: v = x < y; break;
+      case S_ULE: v = x <= y; break;
+      case S_AND: v = x & y; break;
+      case S_OR: v = x | y; break;
+      case S_XOR: v = x ^ y; break;
+      case S_NOT: v = ~x; break;
+      case S_BNOT: v = x == 0u; break;
+      case S_SHL: v = y >= 32u ? 0u : x << y; break;
+      case S_SHRU: v = y >= 32u ? 0u : x >> y; break;
+      case S_SHRI: v = y >= 32u ? (xi < 0 ? UINT32_MAX : 0u) : static_cast<uint32_t>(xi >> y); break;
+      case S_I2F: v = __float_as_uint(static_cast<float>(xi)); break;
+      case S_U2F: v = __float_as_uint(static_cast<float>(x)); break;
+      case S_F2I: v = static_cast<uint32_t>(f2i(xf)); break;
+      case S_F2U: v = f2u(xf); break;
+      case S_F2B: v = xf != 0.0f; break;
+      case S_I2B: v = x != 0u; break;
+      default: break;
+    }
+    r[d & 31] = v;
+  }
+}
+
+__global__ void k_site_eval(plx_site_desc d) {
+  const int64_t n = live_count(d.n, d.n_dev);
+  const uint32_t keyed =
+      px::philox32(d.net_seed, (static_cast<uint64_t>(static_cast<uint32_t>(d.step)) << 8) | 1u);
+  const int64_t per = d.per > 0 ? d.per : 1;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < n;
+       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    Site c;
+    c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
+    uint32_t key = 0;
+    switch (d.kind) {
+      case PLX_SITES_UNIT:
+        c.role[0] = static_cast<int32_t>(s / per);
+        c.role[1] = static_cast<int32_t>(s % per);
+        key = static_cast<uint32_t>(c.role[0]);
+        break;
+      case PLX_SITES_GLOBAL: c.role[1] = static_cast<int32_t>(s); break;
+      case PLX_SITES_CONN: {
+        const int32_t cid = d.list_a[s / per];
+        c.role[1] = static_cast<int32_t>(s % per);
+        c.role[2] = d.from_id[cid];
+        c.role[3] = d.to_id[cid];
+        c.role[4] = cid;
+        const uint64_t pair = (static_cast<uint64_t>(static_cast<uint32_t>(c.role[2])) << 32) |
+                              static_cast<uint32_t>(c.role[3]);
+        key = px::philox32(pair, static_cast<uint32_t>(d.occ[cid]));
+        break;
+      }
+      case PLX_SITES_GRID: {
+        const int64_t m2 = per * per;
+        const int64_t g = s / m2, rem = s - g * m2;
+        c.role[2] = d.list_a[g * per + rem / per];
+        c.role[3] = d.list_b[g * per + rem % per];
+        break;
+      }
+      case PLX_SITES_PAIRS:
+        c.role[2] = d.list_a[s];
+        c.role[3] = d.list_b[s];
+        break;
+      default: c.role[4] = static_cast<int32_t>(s); break;  // EDGE
+    }
+    c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
+    uint32_t out[PLX_MAX_SOUTS];
+    site_run(d.prog, c, d.num_units, out);
+    if (d.or_into) {
+      if (out[0]) d.or_into[s] = 1;
+    } else {
+      for (int k = 0; k < d.prog.nout; ++k) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Growth: validity, dedupe, selection, claim.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ bool live_pair(const plx_grow_filter_desc& d, int64_t nlive, int32_t b, int32_t s,
+                                          int32_t t) {
+  int64_t lo = 0, hi = nlive;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    const int32_t j = d.live_idx[mid];
+    const int32_t jb = d.live_bucket[j], js = d.live_src[j], jd = d.live_dst[j];
+    const bool less = jb < b || (jb == b && (js < s || (js == s && jd < t)));
+    if (less)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  if (lo >= nlive) return false;
+  const int32_t j = d.live_idx[lo];
+  return d.live_bucket[j] == b && d.live_src[j] == s && d.live_dst[j] == t;
+}
+
+__global__ void k_grow_filter(plx_grow_filter_desc d) {
+  const int32_t nu = d.num_units;
+  const int64_t nlive = live_count(d.nlive, d.nlive_dev);
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < d.n;
+       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int32_t a = d.src[s], b = d.dst[s];
+    bool ok = true;
+    if (d.check_range) {
+      if (!(a >= 0 && a < nu && b >= 0 && b < nu)) {
+        ok = false;
+        a = 0;
+        b = 0;
+      }
+      d.src[s] = a;
+      d.dst[s] = b;
+    }
+    a = a < 0 ? 0 : (a >= nu ? nu - 1 : a);
+    b = b < 0 ? 0 : (b >= nu ? nu - 1 : b);
+    if (d.proposer_dead) {
+      const int64_t r = s / (d.per > 0 ? d.per : 1);
+      const int64_t who = d.proposer_idx ? d.proposer_idx[r] : r;
+      ok = ok && d.proposer_dead[who] == 0;
+    }
+    if (d.pruned) ok = ok && d.pruned[a] == 0 && d.pruned[b] == 0;
+    const int32_t la = d.level[a], lb = d.level[b];
+    const int32_t gap = lb - la;
+    ok = ok && (gap < 0 ? -gap : gap) <= d.max_level_gap;
+    if (!d.allow_self_loops) ok = ok && a != b;
+    if (d.direction == 1) ok = ok && lb > la;
+    if (d.direction == 2) ok = ok && lb >= la;
+    int32_t bucket = 0;
+    if (!d.pipeline) {
+      bucket = la;
+      ok = ok && la >= 0 && la < d.num_buckets;
+      if (d.grid_sq > 0) ok = ok && static_cast<int64_t>(la) == s / d.grid_sq;
+    }
+    if (ok && nlive > 0) ok = !live_pair(d, nlive, bucket, a, b);
+    if (!ok) d.score[s] = -__builtin_huge_valf();
+  }
+}
+
+__global__ void k_mark_repeats(int64_t n_max, const int32_t* n_dev, const int32_t* order,
+                               const int32_t* src, const int32_t* dst, float* score) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x + 1; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t i = order[p], h = order[p - 1];
+    if (src[i] == src[h] && dst[i] == dst[h]) score[i] = -__builtin_huge_valf();
+  }
+}
+
+__global__ void k_seg_first(int64_t n_max, const int32_t* n_dev, const int32_t* sorted,
+                            const int32_t* src, const int32_t* level, int32_t* first) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t seg = level[src[sorted[p]]];
+    if (p == 0 || level[src[sorted[p - 1]]] != seg) first[seg] = static_cast<int32_t>(p);
+  }
+}
+
+__global__ void k_select(int64_t n_max, const int32_t* n_dev, const int32_t* sorted, const int32_t* src,
+                         const int32_t* level, int32_t per_segment, int64_t k, const int32_t* first,
+                         uint8_t* win) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t rank = p;
+    if (per_segment) rank = p - first[level[src[sorted[p]]]];
+    win[p] = rank < k;
+  }
+}
+
+__device__ __forceinline__ int32_t level_of_winner(const plx_grow_claim_desc& d, int64_t q) {
+  return d.level[d.src[d.winners[q]]];
+}
+
+__global__ void k_claim_growable(plx_grow_claim_desc d, int32_t* g) {
+  const int64_t n = live_count(d.n_max, d.n_dev);
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float f = d.score[d.winners[q]];
+    bool ok = (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u;
+    if (d.has_threshold) ok = ok && f >= d.threshold;
+    g[q] = ok;
+  }
+}
+
+__global__ void k_claim_cap(plx_grow_claim_desc d, const int32_t* g, const int32_t* scan, int32_t* g2) {
+  const int64_t n = live_count(d.n_max, d.n_dev);
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    g2[q] = g[q] && scan[q] < d.max_new_per_step;
+}
+
+// rank[q]: q's rank among its level's growable winners; spill[q] (PIPELINE):
+// growable and past its level's own dead slots.
+__global__ void k_claim_rank(plx_grow_claim_desc d, const int32_t* g, const int32_t* scan, int32_t* rank,
+                             int32_t* spill) {
+  const int64_t n = live_count(d.n_max, d.n_dev);
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t lvl = level_of_winner(d, q);
+    int64_t lo = 0, hi = q;  // first position of this level's run
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (level_of_winner(d, mid) < lvl)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    const int32_t rk = scan[q] - scan[lo];
+    rank[q] = rk;
+    if (d.pipeline) {
+      const int32_t own = d.own_count[lvl < d.num_levels ? lvl : d.num_levels - 1];
+      spill[q] = g[q] && rk >= own;
+    } else {
+      spill[q] = 0;
+    }
+  }
+}
+
+__global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int32_t* rank,
+                              const int32_t* spill, const int32_t* spill_rank) {
+  const int64_t n = live_count(d.n_max, d.n_dev);
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (!g[q]) continue;
+    const int32_t w = d.winners[q];
+    const int32_t a = d.src[w], b = d.dst[w];
+    const int32_t lvl = d.level[a];
+    int64_t slot = -1;
+    if (!d.pipeline) {
+      const int32_t start = d.free_info[2 * lvl], len = d.free_info[2 * lvl + 1];
+      if (rank[q] < len) slot = d.free_slots[start + rank[q]];
+    } else if (!spill[q]) {
+      const int32_t l = lvl < d.num_levels ? lvl : d.num_levels - 1;
+      slot = d.own_slots[d.own_start[l] + rank[q]];
+    } else {
+      const int64_t t = d.tail_start + spill_rank[q];
+      if (t < d.capacity) {
+        slot = t;
+        atomicAdd(&d.flags[3], 1);
+      }
+    }
+    if (slot < 0) {
+      atomicOr(&d.flags[1], 1);
+      continue;
+    }
+    atomicAdd(&d.flags[0], 1);
+    if (d.level[b] <= lvl) atomicOr(&d.flags[2], 1);
+    d.from_id[slot] = a;
+    d.to_id[slot] = b;
+    d.dead[slot] = 0;
+    for (int c = 0; c < d.ncols; ++c) {
+      const plx_grow_col& col = d.cols[c];
+      const uint32_t v = col.init_slot >= 0 ? d.init_out[col.init_slot][q] : col.default_bits;
+      if (col.bytes == 1)
+        static_cast<uint8_t*>(col.ptr)[slot] = v != 0u;
+      else
+        static_cast<uint32_t*>(col.ptr)[slot] = v;
+    }
+  }
+}
+
+__global__ void k_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id,
+                                  const int32_t* level, int32_t nl, int64_t tail, int32_t* domain) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < cap;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int32_t o = from_id[p];
+    o = o < 0 ? 0 : (o > nl - 1 ? nl - 1 : o);
+    domain[p] = (dead[p] && p < tail) ? level[o] : nl;
+  }
+}
+
+__global__ void k_occurrence(int64_t n, const int32_t* sorted, const int32_t* from_id,
+                             const int32_t* to_id, int32_t* occ) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t i = sorted[p];
+    const int32_t s = from_id[i], t = to_id[i];
+    int64_t lo = 0, hi = p;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      const int32_t j = sorted[mid];
+      const bool less = from_id[j] < s || (from_id[j] == s && to_id[j] < t);
+      if (less)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    occ[i] = static_cast<int32_t>(p - lo);
+  }
+}
+
+__global__ void k_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const int32_t* a,
+                             int32_t* out) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[p] = a[idx[p]];
+}
+
+__global__ void k_level_count(int64_t n, const int32_t* keys, int32_t nl, int32_t* count) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t k = keys[p];
+    if (k >= 0 && k < nl) atomicAdd(&count[k], 1);
+  }
+}
+
+__global__ void k_copy_i32(int64_t n, const int32_t* in, int32_t* out) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[p] = in[p];
+}
+
+__global__ void k_bucket_free(int32_t nb, const int64_t* off, const int32_t* free_slots,
+                              const int32_t* ntotal, int32_t* info) {
+  const int32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nb) return;
+  const int64_t total = *ntotal;
+  auto lower = [&](int64_t v) {
+    int64_t lo = 0, hi = total;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (free_slots[mid] < v)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    return lo;
+  };
+  const int64_t s = lower(off[b]), e = lower(off[b + 1]);
+  info[2 * b] = static_cast<int32_t>(s);
+  info[2 * b + 1] = static_cast<int32_t>(e - s);
+}
+
+__global__ void k_mask_importance(int32_t n, const float* imp, const int32_t* level, const uint8_t* pruned,
+                                  int32_t mode, int32_t b, int32_t gap, int32_t direction, float* out) {
+  const int32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= n) return;
+  const int32_t l = level[u];
+  bool ok = true;
+  if (mode == 0) {
+    ok = l == b;
+  } else if (mode == 1) {
+    const int32_t dl = l - b;
+    ok = (dl < 0 ? -dl : dl) <= gap;
+    if (direction == 1) ok = ok && l > b;
+    if (direction == 2) ok = ok && l >= b;
+  }
+  if (pruned && pruned[u]) ok = false;
+  out[u] = ok ? imp[u] : -__builtin_huge_valf();
+}
+
+bool prog_ok(const plx_site_prog& p) {
+  if (p.ninstr < 0 || p.ninstr > PLX_MAX_SINSTR || p.nout < 0 || p.nout > PLX_MAX_SOUTS) return false;
+  for (int k = 0; k < p.ninstr; ++k) {
+    const int op = p.code[4 * k], d = p.code[4 * k + 1], a = p.code[4 * k + 2], b = p.code[4 * k + 3];
+    if (op == S_OUT) {
+      if (d < 0 || d >= p.nout || a < 0 || a >= 32) return false;
+      continue;
+    }
+    if (d < 0 || d >= 32) return false;
+    if (op == S_CONST && (a < 0 || a >= PLX_MAX_SCONST)) return false;
+    if (op == S_IDX && (a < 0 || a >= 5)) return false;
+    if (op == S_LDU && (a < 0 || a >= PLX_MAX_SFIELDS || !p.ufields[a] || b < 0 || b >= 32)) return false;
+    if (op == S_LDC && (a < 0 || a >= PLX_MAX_SFIELDS || !p.cfields[a])) return false;
+    if (op == S_SEL && (b < 0 || b + 1 >= 32)) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI.
+// ---------------------------------------------------------------------------
+
+int64_t plx_scratch_ints(int64_t n) {
+  const int64_t tiles = (n + kTile - 1) / kTile;
+  const int64_t h = 256 * tiles;
+  return h + chunks_of(h) + chunks_of(n) + 64;
+}
+
+int plx_site_eval(const plx_site_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_site_eval: null descriptor");
+  if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_site_eval: negative n");
+  if (d->n == 0) return PLX_OK;
+  if (!prog_ok(d->prog)) return fail(PLX_ERR_INVALID, "plx_site_eval: bad program");
+  if (d->num_units < 1) return fail(PLX_ERR_INVALID, "plx_site_eval: num_units must be positive");
+  if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE)
+    return fail(PLX_ERR_INVALID, "plx_site_eval: unknown site kind");
+  if ((d->kind == PLX_SITES_CONN && (!d->list_a || !d->from_id || !d->to_id || !d->occ)) ||
+      ((d->kind == PLX_SITES_GRID || d->kind == PLX_SITES_PAIRS) && (!d->list_a || !d->list_b)))
+    return fail(PLX_ERR_INVALID, "plx_site_eval: site lists missing");
+  if (!d->or_into)
+    for (int k = 0; k < d->prog.nout; ++k)
+      if (!d->outs[k]) return fail(PLX_ERR_INVALID, "plx_site_eval: null output");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_site_eval, dim3(grid_for(d->n)), dim3(kBlock), 0, s, *d);
+  return check_launch("plx_site_eval");
+}
+
+int plx_compact(int64_t n, const int32_t* n_dev, int32_t mode, const void* flags, int32_t* out,
+                int32_t* count, int32_t* scratch, void* stream) {
+  if (n < 0 || mode < 0 || mode > PLX_FLAG_I32) return fail(PLX_ERR_INVALID, "plx_compact: bad n or mode");
+  if ((n > 0 && (!flags || !out || !scratch)) || !count) return fail(PLX_ERR_INVALID, "plx_compact: null pointer");
+  return scan_or_compact(n, n_dev, mode, flags, out, count, scratch, static_cast<hipStream_t>(stream),
+                         "plx_compact");
+}
+
+int plx_scan_i32(int64_t n, const int32_t* n_dev, const int32_t* in, int32_t* out, int32_t* total,
+                 int32_t* scratch, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_scan_i32: negative n");
+  if (n > 0 && (!in || !out || !scratch)) return fail(PLX_ERR_INVALID, "plx_scan_i32: null pointer");
+  return scan_or_compact(n, n_dev, -1, in, out, total, scratch, static_cast<hipStream_t>(stream),
+                         "plx_scan_i32");
+}
+
+int plx_sort(const plx_sort_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_sort: null descriptor");
+  if (d->n_max < 0 || d->nkeys < 0 || d->nkeys > 6) return fail(PLX_ERR_INVALID, "plx_sort: bad sizes");
+  if (d->n_max == 0) return PLX_OK;
+  if (!d->vals || !d->keys_buf || !d->keys_alt || !d->vals_alt || !d->hist)
+    return fail(PLX_ERR_INVALID, "plx_sort: null buffer");
+  if (d->n_max > (int64_t(1) << 31) - 1) return fail(PLX_ERR_UNSUPPORTED, "plx_sort: more than 2^31 - 1 elements");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t ntiles = (d->n_max + kTile - 1) / kTile;
+  int32_t* hist = d->hist;
+  int32_t* scan_scratch = d->hist + 256 * ntiles;
+  for (int k = 0; k < d->nkeys; ++k) {
+    const plx_sort_key& key = d->keys[k];
+    if (key.bits < 1 || key.bits > 32 || !key.a) return fail(PLX_ERR_INVALID, "plx_sort: bad key");
+    if ((key.kind == PLX_KEY_LEVEL_OF || key.kind == PLX_KEY_PAIR16 || key.kind == PLX_KEY_DEADMAX) && !key.b)
+      return fail(PLX_ERR_INVALID, "plx_sort: key needs its second column");
+    hipLaunchKernelGGL(k_gather_key, dim3(grid_for(d->n_max)), dim3(kBlock), 0, s, d->n_max, d->n_dev, key,
+                       d->vals, d->keys_buf);
+    uint32_t* kin = d->keys_buf;
+    uint32_t* vin = d->vals;
+    uint32_t* kout = d->keys_alt;
+    uint32_t* vout = d->vals_alt;
+    const int passes = (key.bits + 7) / 8;
+    for (int pass = 0; pass < passes; ++pass) {
+      const int shift = 8 * pass;
+      hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, kin, shift,
+                         ntiles, hist);
+      const int rc = scan_or_compact(256 * ntiles, nullptr, -1, hist, hist, nullptr, scan_scratch, s, "plx_sort");
+      if (rc != PLX_OK) return rc;
+      hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, kin, vin, kout,
+                         vout, shift, ntiles, hist);
+      uint32_t* t = kin;
+      kin = kout;
+      kout = t;
+      t = vin;
+      vin = vout;
+      vout = t;
+    }
+    if (vin != d->vals)
+      hipLaunchKernelGGL(k_copy_u32, dim3(grid_for(d->n_max)), dim3(kBlock), 0, s, d->n_max, d->n_dev, vin,
+                         d->vals);
+  }
+  return check_launch("plx_sort");
+}
+
+int plx_grow_filter(const plx_grow_filter_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_grow_filter: null descriptor");
+  if (d->n < 0 || d->num_units < 1) return fail(PLX_ERR_INVALID, "plx_grow_filter: bad sizes");
+  if (d->n == 0) return PLX_OK;
+  if (!d->src || !d->dst || !d->score || !d->level) return fail(PLX_ERR_INVALID, "plx_grow_filter: null column");
+  if (d->nlive > 0 && (!d->live_idx || !d->live_bucket || !d->live_src || !d->live_dst))
+    return fail(PLX_ERR_INVALID, "plx_grow_filter: live pair list missing");
+  hipLaunchKernelGGL(k_grow_filter, dim3(grid_for(d->n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), *d);
+  return check_launch("plx_grow_filter");
+}
+
+int plx_grow_mark_repeats(int64_t n_max, const int32_t* n_dev, const int32_t* order, const int32_t* src,
+                          const int32_t* dst, float* score, void* stream) {
+  if (n_max < 0) return fail(PLX_ERR_INVALID, "plx_grow_mark_repeats: negative n");
+  if (n_max < 2) return PLX_OK;
+  if (!order || !src || !dst || !score) return fail(PLX_ERR_INVALID, "plx_grow_mark_repeats: null pointer");
+  hipLaunchKernelGGL(k_mark_repeats, dim3(grid_for(n_max)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     n_max, n_dev, order, src, dst, score);
+  return check_launch("plx_grow_mark_repeats");
+}
+
+int plx_grow_select(int64_t n_max, const int32_t* n_dev, const int32_t* sorted, const int32_t* src,
+                    const int32_t* level, int32_t per_segment, int64_t k, int32_t num_segments, int32_t* first,
+                    uint8_t* win, void* stream) {
+  if (n_max < 0 || k < 0) return fail(PLX_ERR_INVALID, "plx_grow_select: negative size");
+  if (n_max == 0) return PLX_OK;
+  if (!sorted || !src || !level || !win || (per_segment && (!first || num_segments < 1)))
+    return fail(PLX_ERR_INVALID, "plx_grow_select: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (per_segment)
+    hipLaunchKernelGGL(k_seg_first, dim3(grid_for(n_max)), dim3(kBlock), 0, s, n_max, n_dev, sorted, src, level,
+                       first);
+  hipLaunchKernelGGL(k_select, dim3(grid_for(n_max)), dim3(kBlock), 0, s, n_max, n_dev, sorted, src, level,
+                     per_segment, k, first, win);
+  return check_launch("plx_grow_select");
+}
+
+int plx_grow_claim(const plx_grow_claim_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_grow_claim: null descriptor");
+  if (d->n_max < 0 || d->ncols < 0 || d->ncols > PLX_MAX_GROW_COLS)
+    return fail(PLX_ERR_INVALID, "plx_grow_claim: bad sizes");
+  if (d->n_max == 0) return PLX_OK;
+  if (!d->winners || !d->src || !d->dst || !d->score || !d->level || !d->from_id || !d->to_id || !d->dead ||
+      !d->flags || !d->scratch)
+    return fail(PLX_ERR_INVALID, "plx_grow_claim: null pointer");
+  if (!d->pipeline && (!d->free_slots || !d->free_info))
+    return fail(PLX_ERR_INVALID, "plx_grow_claim: free lists missing");
+  if (d->pipeline && (!d->own_slots || !d->own_start || !d->own_count || d->num_levels < 1))
+    return fail(PLX_ERR_INVALID, "plx_grow_claim: own-slot lists missing");
+  for (int c = 0; c < d->ncols; ++c) {
+    const plx_grow_col& col = d->cols[c];
+    if (!col.ptr || (col.bytes != 1 && col.bytes != 4) || col.init_slot >= PLX_MAX_SOUTS ||
+        (col.init_slot >= 0 && !d->init_out[col.init_slot]))
+      return fail(PLX_ERR_INVALID, "plx_grow_claim: bad column");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = d->n_max;
+  int32_t* g = d->scratch;
+  int32_t* g2 = g + n;
+  int32_t* scan = g2 + n;
+  int32_t* rank = scan + n;
+  int32_t* spill = rank + n;
+  int32_t* spill_rank = spill + n;
+  int32_t* ss = spill_rank + 2 * n;
+  const int grid = grid_for(n);
+  hipLaunchKernelGGL(k_claim_growable, dim3(grid), dim3(kBlock), 0, s, *d, g);
+  int32_t* grow = g;
+  if (d->max_new_per_step > 0) {
+    int rc = scan_or_compact(n, d->n_dev, -1, g, scan, nullptr, ss, s, "plx_grow_claim");
+    if (rc != PLX_OK) return rc;
+    hipLaunchKernelGGL(k_claim_cap, dim3(grid), dim3(kBlock), 0, s, *d, g, scan, g2);
+    grow = g2;
+  }
+  int rc = scan_or_compact(n, d->n_dev, -1, grow, scan, nullptr, ss, s, "plx_grow_claim");
+  if (rc != PLX_OK) return rc;
+  hipLaunchKernelGGL(k_claim_rank, dim3(grid), dim3(kBlock), 0, s, *d, grow, scan, rank, spill);
+  if (d->pipeline) {
+    rc = scan_or_compact(n, d->n_dev, -1, spill, spill_rank, nullptr, ss, s, "plx_grow_claim");
+    if (rc != PLX_OK) return rc;
+  }
+  hipLaunchKernelGGL(k_claim_write, dim3(grid), dim3(kBlock), 0, s, *d, grow, rank, spill, spill_rank);
+  return check_launch("plx_grow_claim");
+}
+
+int plx_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id, const int32_t* level,
+                        int32_t num_levels, int64_t tail_start, int32_t* domain, void* stream) {
+  if (cap < 0 || num_levels < 1) return fail(PLX_ERR_INVALID, "plx_pipeline_domain: bad sizes");
+  if (cap == 0) return PLX_OK;
+  if (!dead || !from_id || !level || !domain) return fail(PLX_ERR_INVALID, "plx_pipeline_domain: null pointer");
+  hipLaunchKernelGGL(k_pipeline_domain, dim3(grid_for(cap)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     cap, dead, from_id, level, num_levels, tail_start, domain);
+  return check_launch("plx_pipeline_domain");
+}
+
+int plx_occurrence(int64_t n, const int32_t* sorted, const int32_t* from_id, const int32_t* to_id, int32_t* occ,
+                   void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_occurrence: negative n");
+  if (n == 0) return PLX_OK;
+  if (!sorted || !from_id || !to_id || !occ) return fail(PLX_ERR_INVALID, "plx_occurrence: null pointer");
+  hipLaunchKernelGGL(k_occurrence, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, sorted,
+                     from_id, to_id, occ);
+  return check_launch("plx_occurrence");
+}
+
+int plx_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const int32_t* a, int32_t* out,
+                   void* stream) {
+  if (n_max < 0) return fail(PLX_ERR_INVALID, "plx_gather_i32: negative n");
+  if (n_max == 0) return PLX_OK;
+  if (!idx || !a || !out) return fail(PLX_ERR_INVALID, "plx_gather_i32: null pointer");
+  hipLaunchKernelGGL(k_gather_i32, dim3(grid_for(n_max)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n_max,
+                     n_dev, idx, a, out);
+  return check_launch("plx_gather_i32");
+}
+
+int plx_level_counts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* count, int32_t* start,
+                     void* stream) {
+  if (n < 0 || nlevels < 1) return fail(PLX_ERR_INVALID, "plx_level_counts: bad sizes");
+  if (!count || !start || (n > 0 && !keys)) return fail(PLX_ERR_INVALID, "plx_level_counts: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(nlevels)), dim3(kBlock), 0, s, static_cast<int64_t>(nlevels), 0,
+                     count);
+  if (n > 0) hipLaunchKernelGGL(k_level_count, dim3(grid_for(n)), dim3(kBlock), 0, s, n, keys, nlevels, count);
+  hipLaunchKernelGGL(k_copy_i32, dim3(grid_for(nlevels)), dim3(kBlock), 0, s, static_cast<int64_t>(nlevels), count,
+                     start);
+  hipLaunchKernelGGL(k_scan_single, dim3(1), dim3(kScanLanes), 0, s, static_cast<int64_t>(nlevels), start,
+                     static_cast<int32_t*>(nullptr));
+  return check_launch("plx_level_counts");
+}
+
+int plx_bucket_free(int32_t num_buckets, const int64_t* bucket_off, const int32_t* free_slots,
+                    const int32_t* nfree_total, int32_t* free_info, void* stream) {
+  if (num_buckets < 1) return fail(PLX_ERR_INVALID, "plx_bucket_free: no buckets");
+  if (!bucket_off || !free_slots || !nfree_total || !free_info)
+    return fail(PLX_ERR_INVALID, "plx_bucket_free: null pointer");
+  hipLaunchKernelGGL(k_bucket_free, dim3((num_buckets + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), num_buckets, bucket_off, free_slots, nfree_total, free_info);
+  return check_launch("plx_bucket_free");
+}
+
+int plx_mask_importance(int32_t n, const float* imp, const int32_t* level, const uint8_t* pruned, int32_t mode,
+                        int32_t b, int32_t gap, int32_t direction, float* out, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_mask_importance: negative n");
+  if (n == 0) return PLX_OK;
+  if (!imp || !level || !out) return fail(PLX_ERR_INVALID, "plx_mask_importance: null pointer");
+  hipLaunchKernelGGL(k_mask_importance, dim3((n + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), n, imp, level, pruned, mode, b, gap, direction, out);
+  return check_launch("plx_mask_importance");
+}

@@ -1,0 +1,466 @@
+"""The structural phases on the device: PruneConn and add_conn growth.
+
+Host orchestration of the kernels in csrc/structural.hip, mirroring the
+reference's phases (phases.py:1444-1498 for PruneConn, :4490-5203 for
+add_conn). Everything between the phase's inputs and its flags runs on the
+GPU, stream-ordered, with device-side counts (no host round trip) until the
+phase's four flags are read at its end:
+
+1. candidates: the traced ``propose`` / ``score`` callback evaluated per
+   site (``plx_site_eval``); shortlists rank units by importance with the
+   radix sort;
+2. validity (``plx_grow_filter``): window, direction, self-loops, source
+   bucket, live endpoints, dedupe against the live edges (a sorted live-pair
+   list and binary search); invalid candidates get score -inf;
+3. dedupe within the step (``plx_grow_mark_repeats`` over a pair sort that
+   is stable in score order);
+4. the finite candidates, compacted in index order (``plx_compact``), sorted
+   into the total order ``(-score, src, dst, index)``, level-major where the
+   budget is per source level (``plx_sort``);
+5. selection (``plx_grow_select``), init of the winners (site eval), claim
+   and write (``plx_grow_claim``): TOPOLOGICAL winners take their bucket's
+   free slots in order, PIPELINE winners their level's own dead slots and
+   then the tail.
+
+The arena is handled in its logical form: each bucket's columns in slot
+order, concatenated into flat device columns (bucket ``b`` at
+``[off_b, off_b + cap_b)``); the buckets handed back are views of them.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any
+
+import numpy as np
+import torch
+
+from plastax_amd import _lib, _site
+from plastax_amd._types import Propagation
+from plastax_amd.growth_config import GrowthConfig
+
+Columns = dict[str, torch.Tensor]
+_DIRECTION = {"any": 0, "deeper": 1, "same_or_deeper": 2}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _bits_for(n: int) -> int:
+    """Key bits that hold every value in [0, n]."""
+    return max(1, int(n).bit_length())
+
+
+def fill_prog(sp: _site.SiteProgram, units: Columns, conns: Columns | None, globals_: Any) -> _lib.plx_site_prog:
+    """The plx_site_prog of a traced site program over device columns."""
+    p = _lib.plx_site_prog()
+    p.ninstr = sp.ninstr
+    p.nout = len(sp.out_kinds)
+    code = sp.flat_code()
+    for k, v in enumerate(code):
+        p.code[k] = int(v)
+    for k, v in enumerate(sp.const_bits(globals_)):
+        p.consts[k] = int(v)
+    for f, name in enumerate(sp.unit_fields):
+        col = units[name]
+        assert col.is_contiguous()
+        p.ufields[f] = col.data_ptr()
+        p.ubytes[f] = 1 if col.element_size() == 1 else 4
+    for f, name in enumerate(sp.conn_fields):
+        assert conns is not None
+        col = conns[name]
+        p.cfields[f] = col.data_ptr()
+        p.cbytes[f] = 1 if col.element_size() == 1 else 4
+    return p
+
+
+class Scratch:
+    """Device scratch of the growth pipeline, allocated per call through
+    torch's caching allocator."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+
+    def i32(self, n: int) -> torch.Tensor:
+        return torch.empty(max(int(n), 1), dtype=torch.int32, device=self.device)
+
+    def f32(self, n: int) -> torch.Tensor:
+        return torch.empty(max(int(n), 1), dtype=torch.float32, device=self.device)
+
+    def u8(self, n: int) -> torch.Tensor:
+        return torch.empty(max(int(n), 1), dtype=torch.uint8, device=self.device)
+
+    def ints_for(self, n: int) -> torch.Tensor:
+        return self.i32(int(_lib.load().plx_scratch_ints(int(n))))
+
+
+class Kernels:
+    """Thin wrappers of the structural entry points on one stream."""
+
+    def __init__(self, device: torch.device, stream: int) -> None:
+        self.lib = _lib.load()
+        self.s = stream
+        self.mem = Scratch(device)
+
+    def site_eval(self, sp: _site.SiteProgram, units: Columns, globals_: Any, *, n: int, kind: int,
+                  per: int = 1, num_units: int, step: int = 0, net_seed: int = 0,
+                  list_a: torch.Tensor | None = None, list_b: torch.Tensor | None = None,
+                  from_id: torch.Tensor | None = None, to_id: torch.Tensor | None = None,
+                  occ: torch.Tensor | None = None, n_dev: torch.Tensor | None = None,
+                  outs: list[torch.Tensor] | None = None, conns: Columns | None = None,
+                  or_into: torch.Tensor | None = None) -> None:
+        d = _lib.plx_site_desc()
+        d.prog = fill_prog(sp, units, conns, globals_)
+        d.n, d.kind, d.per, d.num_units = int(n), int(kind), int(per), int(num_units)
+        d.step = int(np.array(int(step) & 0xFFFFFFFF, dtype=np.uint32).view(np.int32))
+        d.net_seed = int(net_seed) & 0xFFFFFFFFFFFFFFFF
+        d.list_a, d.list_b = _ptr(list_a), _ptr(list_b)
+        d.from_id, d.to_id, d.occ, d.n_dev = _ptr(from_id), _ptr(to_id), _ptr(occ), _ptr(n_dev)
+        for k, o in enumerate(outs or []):
+            d.outs[k] = o.data_ptr()
+        d.or_into = _ptr(or_into)
+        _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
+
+    def compact(self, n: int, mode: int, flags: torch.Tensor, n_dev: torch.Tensor | None = None
+                ) -> tuple[torch.Tensor, torch.Tensor]:
+        out = self.mem.i32(n)
+        count = self.mem.i32(1)
+        scratch = self.mem.ints_for(n)
+        _lib.check(self.lib.plx_compact(int(n), _ptr(n_dev), int(mode), flags.data_ptr(), out.data_ptr(),
+                                        count.data_ptr(), scratch.data_ptr(), self.s), "plx_compact")
+        return out, count
+
+    def sort(self, vals: torch.Tensor, n_max: int, keys: list[tuple[int, int, torch.Tensor, torch.Tensor | None]],
+             n_dev: torch.Tensor | None = None) -> None:
+        """Stable sort of ``vals`` (in place) by ``keys`` (least significant first)."""
+        if n_max == 0 or not keys:
+            return
+        d = _lib.plx_sort_desc()
+        d.n_max, d.n_dev, d.nkeys = int(n_max), _ptr(n_dev), len(keys)
+        for k, (kind, bits, a, b) in enumerate(keys):
+            d.keys[k].kind, d.keys[k].bits = int(kind), int(bits)
+            d.keys[k].a, d.keys[k].b = a.data_ptr(), _ptr(b)
+        kb, ka, va = self.mem.i32(n_max), self.mem.i32(n_max), self.mem.i32(n_max)
+        hist = self.mem.ints_for(n_max)
+        d.vals, d.keys_buf, d.keys_alt, d.vals_alt, d.hist = (
+            vals.data_ptr(), kb.data_ptr(), ka.data_ptr(), va.data_ptr(), hist.data_ptr())
+        _lib.check(self.lib.plx_sort(d, self.s), "plx_sort")
+
+    def gather(self, idx: torch.Tensor, a: torch.Tensor, n_max: int, n_dev: torch.Tensor | None) -> torch.Tensor:
+        out = self.mem.i32(n_max)
+        _lib.check(self.lib.plx_gather_i32(int(n_max), _ptr(n_dev), idx.data_ptr(), a.data_ptr(), out.data_ptr(),
+                                           self.s), "plx_gather_i32")
+        return out
+
+    def iota(self, n: int) -> torch.Tensor:
+        return torch.arange(max(int(n), 1), dtype=torch.int32, device=self.mem.device)
+
+
+@dataclasses.dataclass
+class GrowthOutcome:
+    conns: tuple[Columns, ...]
+    grown: int
+    overflow: bool
+    needs_resort: bool
+    tail_start: int
+    fired: bool
+
+
+def flatten(conns: tuple[Columns, ...]) -> tuple[Columns, list[int]]:
+    """One flat column per field, the buckets end to end; offsets."""
+    caps = [int(next(iter(b.values())).shape[0]) for b in conns]
+    offs = [0]
+    for c in caps:
+        offs.append(offs[-1] + c)
+    flat = {name: torch.cat([b[name] for b in conns]).contiguous() for name in conns[0]}
+    return flat, offs
+
+
+def unflatten(flat: Columns, offs: list[int]) -> tuple[Columns, ...]:
+    return tuple({name: col[offs[b] : offs[b + 1]] for name, col in flat.items()} for b in range(len(offs) - 1))
+
+
+class PruneConnPhase:
+    """``dead |= predicate(u, c, cid, g)`` over every slot of every bucket
+    (phases.py:1444-1498), one site-program launch per bucket."""
+
+    def __init__(self, net: Any, static: Any, globals_: Any) -> None:
+        self.static = static
+        unit_dtypes = {s.name: np.dtype(s.dtype) for s in static.unit_fields}
+        conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
+        self.prog = _site.trace_predicate(net.prune_conn, unit_dtypes, conn_dtypes, globals_)
+
+    def run(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], globals_: Any) -> None:
+        n_units = int(next(iter(units.values())).shape[0])
+        for bucket in conns:
+            cap = int(bucket["dead"].shape[0])
+            if cap == 0:
+                continue
+            k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
+                        conns=bucket, or_into=bucket["dead"])
+
+
+def _lib_sites(name: str) -> int:
+    return {"UNIT": 0, "GLOBAL": 1, "CONN": 2, "GRID": 3, "PAIRS": 4, "EDGE": 5}[name]
+
+
+class AddConnPhase:
+    """One add_conn phase on the device (phases.py:4490-5203)."""
+
+    def __init__(self, net: Any, static: Any, globals_: Any) -> None:
+        self.net = net
+        self.ac = net.add_conn
+        self.static = static
+        self.cfg = GrowthConfig.of(net, static)
+        self.interval = int(getattr(net, "structural_interval", 1))
+        unit_dtypes = {s.name: np.dtype(s.dtype) for s in static.unit_fields}
+        conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
+        cfg = self.cfg
+        if cfg.propose:
+            self.cand_prog = _site.trace_propose(self.ac, cfg.proposer, unit_dtypes, conn_dtypes, globals_)
+        else:
+            self.cand_prog = _site.trace_score(self.ac, unit_dtypes, globals_)
+        self.imp_prog = _site.trace_importance(self.ac, unit_dtypes, globals_) if cfg.shortlist else None
+        self.init_prog, self.init_names = _site.trace_init(self.ac, unit_dtypes, static.conn_fields, globals_)
+
+    # -- helpers ---------------------------------------------------------------
+    def _top_units(self, k: Kernels, masked: torch.Tensor, m: int, n: int) -> torch.Tensor:
+        """lax.top_k's ids: descending value, ties to the lower id."""
+        order = k.iota(n)
+        k.sort(order, n, [(1, 32, masked, None)])  # PLX_KEY_SCORE
+        return order[:m]
+
+    def _importance(self, k: Kernels, units: Columns, globals_: Any, n: int) -> torch.Tensor:
+        imp = k.mem.f32(n)
+        k.site_eval(self.imp_prog, units, globals_, n=n, kind=_lib_sites("UNIT"), per=1, num_units=n, outs=[imp])
+        return imp
+
+    def _mask(self, k: Kernels, imp: torch.Tensor, units: Columns, mode: int, b: int) -> torch.Tensor:
+        n = int(imp.shape[0])
+        out = k.mem.f32(n)
+        pruned = units.get("pruned")
+        gap = self.cfg.max_level_gap if mode == 1 else 0
+        direction = _DIRECTION[self.cfg.direction] if mode == 1 else 0
+        _lib.check(k.lib.plx_mask_importance(n, imp.data_ptr(), units["level"].data_ptr(), _ptr(pruned), mode, b,
+                                             gap, direction, out.data_ptr(), k.s), "plx_mask_importance")
+        return out
+
+    # -- the phase --------------------------------------------------------------
+    def run(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], *, step: int, globals_: Any,
+            tail_start: int = 0, units_added: int = 0) -> GrowthOutcome:
+        cfg = self.cfg
+        if not cfg.fires(self.ac, step=step, interval=self.interval, units_added=units_added, globals_=globals_):
+            return GrowthOutcome(conns, 0, False, False, tail_start, False)
+        n = cfg.num_units
+        nb = cfg.num_buckets
+        flat, offs = flatten(conns)
+        total_slots = offs[-1]
+        level = units["level"]
+        pruned = units.get("pruned")
+        seed, dev = int(self.static.seed), level.device
+        INT_MAX = 0x7FFFFFFF
+
+        # 1. candidates
+        grid_sq = 0
+        proposer_idx = proposer_dead = None
+        per = 1
+        if cfg.propose:
+            P = cfg.proposals
+            per = P
+            if cfg.proposer == "per_unit":
+                nc, kind = n * P, _lib_sites("UNIT")
+                extra = {}
+                proposer_dead = pruned
+            elif cfg.proposer == "global":
+                nc, kind, extra = P, _lib_sites("GLOBAL"), {}
+            else:
+                nc, kind = total_slots * P, _lib_sites("CONN")
+                perm = k.iota(total_slots)
+                bits = _bits_for(n)
+                k.sort(perm, total_slots, [(4, bits, flat["to_id"], flat["dead"]),
+                                           (4, bits, flat["from_id"], flat["dead"])])
+                occ = k.mem.i32(total_slots)
+                _lib.check(k.lib.plx_occurrence(total_slots, perm.data_ptr(), flat["from_id"].data_ptr(),
+                                                flat["to_id"].data_ptr(), occ.data_ptr(), k.s), "plx_occurrence")
+                extra = dict(list_a=perm, from_id=flat["from_id"], to_id=flat["to_id"], occ=occ, conns=flat)
+                proposer_idx, proposer_dead = perm, flat["dead"]
+            src, dst, score = k.mem.i32(nc), k.mem.i32(nc), k.mem.f32(nc)
+            k.site_eval(self.cand_prog, units, globals_, n=nc, kind=kind, per=P, num_units=n, step=step,
+                        net_seed=seed, outs=[src, dst, score], **extra)
+        else:
+            if cfg.per_level:
+                M = cfg.pool_side
+                imp = self._importance(k, units, globals_, n)
+                src_lists = torch.cat([self._top_units(k, self._mask(k, imp, units, 0, b), M, n) for b in range(nb)])
+                dst_lists = torch.cat([self._top_units(k, self._mask(k, imp, units, 1, b), M, n) for b in range(nb)])
+                side, ngrids = M, nb
+                grid_sq = M * M
+            elif cfg.shortlist:
+                M = cfg.pool_side
+                imp = self._importance(k, units, globals_, n)
+                top = self._top_units(k, self._mask(k, imp, units, 2, 0), M, n)
+                src_lists = dst_lists = top
+                side, ngrids = M, 1
+            else:
+                src_lists = dst_lists = k.iota(n)
+                side, ngrids = n, 1
+            nc = ngrids * side * side
+            if nc > INT_MAX:
+                raise ValueError(f"add_conn: {nc} candidates exceed 2^31 - 1; use a shortlist")
+            src, dst, score = k.mem.i32(nc), k.mem.i32(nc), k.mem.f32(nc)
+            pairs = [src, dst]
+            k.site_eval(_pairs_prog(), units, globals_, n=nc, kind=_lib_sites("GRID"), per=side, num_units=n,
+                        list_a=src_lists, list_b=dst_lists, outs=pairs)
+            k.site_eval(self.cand_prog, units, globals_, n=nc, kind=_lib_sites("GRID"), per=side, num_units=n,
+                        list_a=src_lists, list_b=dst_lists, outs=[score])
+
+        # 2. validity
+        f = _lib.plx_grow_filter_desc()
+        f.n, f.grid_sq, f.num_units, f.num_buckets = nc, grid_sq, n, nb
+        f.pipeline = int(cfg.pipeline)
+        f.max_level_gap = min(cfg.max_level_gap, INT_MAX)
+        f.direction = _DIRECTION[cfg.direction]
+        f.allow_self_loops = int(cfg.allow_self_loops)
+        f.check_range = int(cfg.propose)
+        f.per = per
+        f.src, f.dst, f.score, f.level, f.pruned = src.data_ptr(), dst.data_ptr(), score.data_ptr(), \
+            level.data_ptr(), _ptr(pruned)
+        f.proposer_idx, f.proposer_dead = _ptr(proposer_idx), _ptr(proposer_dead)
+        if cfg.dedupe_live and total_slots:
+            live_idx, nlive = k.compact(total_slots, 1, flat["dead"])  # PLX_FLAG_U8_ZERO
+            if cfg.pipeline:
+                bucket_id = torch.zeros(total_slots, dtype=torch.int32, device=dev)
+            else:
+                caps = torch.tensor([offs[b + 1] - offs[b] for b in range(nb)], device=dev)
+                bucket_id = torch.repeat_interleave(torch.arange(nb, dtype=torch.int32, device=dev), caps)
+            bits = _bits_for(n)
+            k.sort(live_idx, total_slots, [(0, bits, flat["to_id"], None), (0, bits, flat["from_id"], None),
+                                           (0, _bits_for(nb), bucket_id, None)], n_dev=nlive)
+            f.nlive, f.nlive_dev, f.live_idx = total_slots, nlive.data_ptr(), live_idx.data_ptr()
+            f.live_bucket, f.live_src, f.live_dst = bucket_id.data_ptr(), flat["from_id"].data_ptr(), \
+                flat["to_id"].data_ptr()
+        _lib.check(k.lib.plx_grow_filter(f, k.s), "plx_grow_filter")
+
+        pair_keys = self._pair_keys(src, dst, n)
+        # 3. dedupe within the step
+        if cfg.dedupe_step:
+            fin, nfin = k.compact(nc, 2, score)  # PLX_FLAG_FINITE
+            k.sort(fin, nc, [(1, 32, score, None), *pair_keys], n_dev=nfin)
+            _lib.check(k.lib.plx_grow_mark_repeats(nc, nfin.data_ptr(), fin.data_ptr(), src.data_ptr(),
+                                                   dst.data_ptr(), score.data_ptr(), k.s), "plx_grow_mark_repeats")
+
+        # 4. total order of the finite candidates
+        order, nord = k.compact(nc, 2, score)
+        per_segment = not cfg.step_scope
+        nseg = n if cfg.pipeline else nb
+        keys = [*pair_keys, (1, 32, score, None)]
+        if per_segment:
+            keys.append((2, _bits_for(nseg), src, level))  # PLX_KEY_LEVEL_OF
+        k.sort(order, nc, keys, n_dev=nord)
+
+        # 5. selection
+        win = k.mem.u8(nc)
+        first = k.mem.i32(nseg)
+        _lib.check(k.lib.plx_grow_select(nc, nord.data_ptr(), order.data_ptr(), src.data_ptr(), level.data_ptr(),
+                                         int(per_segment), int(cfg.k), nseg, first.data_ptr(), win.data_ptr(), k.s),
+                   "plx_grow_select")
+        wpos, nwin = k.compact(nc, 0, win, n_dev=nord)  # PLX_FLAG_U8
+        winners = k.gather(wpos, order, nc, nwin)
+        if not per_segment:
+            k.sort(winners, nc, [(2, _bits_for(nseg), src, level)], n_dev=nwin)
+
+        # init of the winners
+        wsrc = k.gather(winners, src, nc, nwin)
+        wdst = k.gather(winners, dst, nc, nwin)
+        init_outs = [k.mem.i32(nc) for _ in self.init_names]
+        if self.init_names:
+            k.site_eval(self.init_prog, units, globals_, n=nc, kind=_lib_sites("PAIRS"), num_units=n,
+                        list_a=wsrc, list_b=wdst, n_dev=nwin, outs=init_outs)
+
+        # 6. claim and write
+        c = _lib.plx_grow_claim_desc()
+        c.n_max, c.n_dev, c.winners = nc, nwin.data_ptr(), winners.data_ptr()
+        c.src, c.dst, c.score, c.level = src.data_ptr(), dst.data_ptr(), score.data_ptr(), level.data_ptr()
+        c.pipeline, c.num_buckets, c.num_levels = int(cfg.pipeline), nb, n
+        if cfg.selection == "threshold":
+            c.has_threshold = 1
+            c.threshold = float(np.float32(np.asarray(self.ac.threshold(globals_))))
+        c.max_new_per_step = int(cfg.max_new_per_step or 0)
+        c.capacity, c.tail_start = total_slots, int(tail_start)
+        keep: list[torch.Tensor] = []
+        if cfg.pipeline:
+            domain = k.mem.i32(total_slots)
+            _lib.check(k.lib.plx_pipeline_domain(total_slots, flat["dead"].data_ptr(), flat["from_id"].data_ptr(),
+                                                 level.data_ptr(), n, int(tail_start), domain.data_ptr(), k.s),
+                       "plx_pipeline_domain")
+            own = k.iota(total_slots)
+            k.sort(own, total_slots, [(0, _bits_for(n), domain, None)])
+            count, start = k.mem.i32(n), k.mem.i32(n)
+            _lib.check(k.lib.plx_level_counts(total_slots, domain.data_ptr(), n, count.data_ptr(), start.data_ptr(),
+                                              k.s), "plx_level_counts")
+            c.own_slots, c.own_start, c.own_count = own.data_ptr(), start.data_ptr(), count.data_ptr()
+            keep += [domain, own, count, start]
+        else:
+            free, nfree = k.compact(total_slots, 0, flat["dead"])
+            off = torch.tensor(offs, dtype=torch.int64, device=dev)
+            info = k.mem.i32(2 * nb)
+            _lib.check(k.lib.plx_bucket_free(nb, off.data_ptr(), free.data_ptr(), nfree.data_ptr(), info.data_ptr(),
+                                             k.s), "plx_bucket_free")
+            c.free_slots, c.free_info = free.data_ptr(), info.data_ptr()
+            keep += [free, nfree, off, info]
+        c.from_id, c.to_id, c.dead = flat["from_id"].data_ptr(), flat["to_id"].data_ptr(), flat["dead"].data_ptr()
+        ncols = 0
+        for spec in self.static.conn_fields:
+            if spec.name in ("from_id", "to_id", "dead"):
+                continue
+            col = flat[spec.name]
+            gc = c.cols[ncols]
+            gc.ptr = col.data_ptr()
+            gc.bytes = 1 if col.element_size() == 1 else 4
+            if spec.name in self.init_names:
+                gc.init_slot = self.init_names.index(spec.name)
+            else:
+                gc.init_slot = -1
+                gc.default_bits = _default_bits(spec)
+            ncols += 1
+        c.ncols = ncols
+        for j, o in enumerate(init_outs):
+            c.init_out[j] = o.data_ptr()
+        flags = torch.zeros(4, dtype=torch.int32, device=dev)
+        scratch = k.mem.i32(8 * nc + int(k.lib.plx_scratch_ints(nc)))
+        c.flags, c.scratch = flags.data_ptr(), scratch.data_ptr()
+        _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
+        got = flags.cpu().tolist()  # the phase's one host read (synchronises the stream)
+        if bool(got[1]) and cfg.on_overflow == "error":
+            raise RuntimeError("add_conn overflow: selected candidates exceeded the free connection capacity")
+        return GrowthOutcome(unflatten(flat, offs), int(got[0]), bool(got[1]), bool(got[2]),
+                             int(tail_start) + int(got[3]), True)
+
+    @staticmethod
+    def _pair_keys(src: torch.Tensor, dst: torch.Tensor, n: int) -> list[tuple[int, int, torch.Tensor, Any]]:
+        """Sort keys ordering by (src, dst), least significant first."""
+        if n <= 1 << 16:
+            return [(3, 32, src, dst)]  # PLX_KEY_PAIR16
+        bits = _bits_for(n)
+        return [(0, bits, dst, None), (0, bits, src, None)]
+
+
+def _default_bits(spec: Any) -> int:
+    v = np.asarray(spec.default).astype(spec.dtype)
+    if v.dtype == np.bool_:
+        return int(bool(v))
+    if v.dtype.itemsize != 4:
+        raise TypeError(f"conn column {spec.name!r}: only 32-bit and bool columns can grow")
+    return int(v.view(np.uint32))
+
+
+_PAIRS: _site.SiteProgram | None = None
+
+
+def _pairs_prog() -> _site.SiteProgram:
+    """The site program writing a grid site's (src, dst)."""
+    global _PAIRS
+    if _PAIRS is None:
+        _PAIRS = _site.compile_site_program([(_site.idx("src"), "i"), (_site.idx("dst"), "i")], roles=("src", "dst"))
+    return _PAIRS

@@ -38,8 +38,9 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 
 
 def test_descriptor_layouts_match_the_header(lib) -> None:
-    out = (ctypes.c_int64 * 6)()
-    assert lib.plx_struct_sizes(out, 6) == 6
+    n = len(_lib.STRUCTS)
+    out = (ctypes.c_int64 * n)()
+    assert lib.plx_struct_sizes(out, n) == n == 13
     assert list(out) == [ctypes.sizeof(s) for s in _lib.STRUCTS]
     assert lib.plx_abi_version() == _lib.ABI_VERSION
 
@@ -56,3 +57,23 @@ def test_argument_errors_are_reported_not_raised(lib) -> None:
     assert lib.plx_fill_f32(-1, 0.0, None, None) == 1
     # zero-sized work is a no-op success
     assert lib.plx_fill_f32(0, 0.0, None, None) == 0
+    # the structural entry points validate before launching too
+    assert lib.plx_site_eval(None, None) == 1
+    sd = _lib.plx_site_desc()
+    sd.n, sd.num_units, sd.kind = 4, 8, 9
+    sd.prog.ninstr = 0
+    assert lib.plx_site_eval(sd, None) == 1
+    assert b"unknown site kind" in lib.plx_last_error()
+    sd.kind, sd.prog.ninstr = 0, 1
+    sd.prog.code[0], sd.prog.code[1], sd.prog.code[2] = 3, 0, 0  # LDU of an unset field
+    assert lib.plx_site_eval(sd, None) == 1
+    assert b"bad program" in lib.plx_last_error()
+    assert lib.plx_compact(-1, None, 0, None, None, None, None, None) == 1
+    assert lib.plx_compact(0, None, 0, None, None, None, None, None) == 1  # count is required
+    srt = _lib.plx_sort_desc()
+    srt.n_max, srt.nkeys = 10, 7
+    assert lib.plx_sort(srt, None) == 1
+    assert lib.plx_scratch_ints(4096) >= 256 + 2
+    cd = _lib.plx_grow_claim_desc()
+    cd.n_max = 0
+    assert lib.plx_grow_claim(cd, None) == 0
