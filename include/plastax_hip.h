@@ -326,7 +326,16 @@ typedef struct plx_site_prog {
  * | key), (j << 16) | sub) with keyed = philox32(net_seed, (step << 8) | 1)
  * (rng.py:206-259). Out slot k of site s is written to outs[k][s] (32-bit
  * patterns); with or_into set, slot 0 is instead OR-ed into that byte column
- * (dead |= predicate). n_dev, when set, holds the site count (<= n). */
+ * (dead |= predicate) and kill_count (optional) counts the bytes it turned
+ * from 0 to 1. n_dev, when set, holds the site count (<= n).
+ *
+ * Renumbered storage: the program always sees the caller's unit ids and
+ * logical slots. With ids_physical set, a unit field read at id u reads
+ * position ids_physical[u]; a conn field whose cbytes has PLX_SITE_ID_COLUMN
+ * holds physical unit ids and reads back ids_logical[value]; with cid_map
+ * set (EDGE sites), the cid the program sees is cid_map[s] while conn fields
+ * are read at s. */
+#define PLX_SITE_ID_COLUMN 0x100
 typedef struct plx_site_desc {
   plx_site_prog prog;
   int64_t n;
@@ -343,6 +352,10 @@ typedef struct plx_site_desc {
   const int32_t* n_dev;
   void* outs[PLX_MAX_SOUTS];
   uint8_t* or_into;
+  int32_t* kill_count;
+  const int32_t* cid_map;
+  const int32_t* ids_logical;
+  const int32_t* ids_physical;
 } plx_site_desc;
 
 PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);

@@ -217,6 +217,13 @@ class OracleNet:
         self._bwd_order: dict[int, tuple[np.ndarray, np.ndarray, np.ndarray]] = {}
         self._phys_index: np.ndarray | None = None
         self.step_count = 0
+        # Structural state (phases.py:4490-5203) and the traced predicate.
+        self.tail_start = 0
+        self.needs_resort = False
+        self.grown = 0
+        self.overflow = False
+        self.units_added = 0
+        self._prune_prog: Any = None
         n = static.num_units
         self.is_input = np.zeros(n, dtype=bool)
         if static.input_ids:
@@ -293,6 +300,11 @@ class OracleNet:
             )
             return out
         order, tile, sb = self._tiles(b)
+        # Edges tombstoned since the layout was fixed contribute the identity,
+        # i.e. nothing: every fold starts from the identity.
+        dead_now = c["dead"].astype(bool)[order]
+        if dead_now.any():
+            order = np.ascontiguousarray(order[~dead_now])
         self.lib.ox_bucket_reduce_bwd_tiled(
             order.size, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
             iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
@@ -385,8 +397,40 @@ class OracleNet:
             self.backward()
         if self.plan.update is not None:
             self.update()
+        if getattr(self.plan, "prune_conn", False) or getattr(self.plan, "add_conn", None) is not None:
+            self.structural()
         self.step_count += 1
         return loss
+
+    def structural(self) -> None:
+        """prune_conn then add_conn (phases.py:87-182 order) on the logical
+        arena. The backward's fold structure (tiles over the destination-
+        sorted positions, unit renumbering) is the layout's: it is fixed when
+        the arena is laid out and laid out again exactly when a growth phase
+        fires, as the device does; tombstones set in between contribute the
+        identity."""
+        from oracle import growth as og
+        from plastax_amd import _site
+
+        net = self.plan.net
+        unit_dtypes = {s.name: np.dtype(s.dtype) for s in self.static.unit_fields}
+        conn_dtypes = {s.name: np.dtype(s.dtype) for s in self.static.conn_fields}
+        if self.plan.prune_conn:
+            if self._prune_prog is None:
+                self._prune_prog = _site.trace_predicate(net.prune_conn, unit_dtypes, conn_dtypes, self.globals_)
+            self.conns = og.prune_conn(self._prune_prog, self.units, self.conns, self.globals_)
+        if self.plan.add_conn is not None:
+            res = og.add_conn(
+                net, self.static, self.units, self.conns, step=self.step_count, globals_=self.globals_,
+                tail_start=self.tail_start, units_added=self.units_added, needs_resort=self.needs_resort,
+            )
+            self.grown, self.overflow = res.grown, res.overflow
+            if res.fired:
+                self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in res.conns]
+                self.needs_resort = res.needs_resort
+                self.tail_start = res.tail_start
+                self._bwd_order = {}
+                self._phys_index = None
 
 
 def free_block_counts(dead: np.ndarray, block: int) -> np.ndarray:

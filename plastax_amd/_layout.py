@@ -192,6 +192,9 @@ class Arena:
         self.uinv[self.uperm] = np.arange(n)
         self.uperm_t = torch.from_numpy(self.uperm).to(device)
         self.uinv_t = torch.from_numpy(self.uinv).to(device)
+        # int32 copies for the kernels that translate ids (physical <-> caller's).
+        self.uperm32 = self.uperm_t.to(torch.int32)
+        self.uinv32 = self.uinv_t.to(torch.int32)
         for name in (FROM_ID.name, TO_ID.name):
             host[name] = [self.uinv[np.clip(h, 0, n - 1)].astype(np.int32) for h in host[name]]
         levels = levels_l[self.uperm]
@@ -433,6 +436,18 @@ class Arena:
                 if lo == hi and lo == int(lo) and 0.0 <= lo < 2.0**23:
                     t = lo
             self.t_now.append(t)
+
+    def materialize_t(self) -> None:
+        """Write every uniform Adam step count back into the per-edge column
+        (live positions) and return to per-edge counts: once tombstones are
+        set in place, dead edges keep the count they died with."""
+        if not self.t_name:
+            return
+        col = self.cols[self.t_name]
+        for b, t in enumerate(self.t_now):
+            if t is not None:
+                col[self.bases[b] : self.bases[b] + self.lives[b]] = t
+                self.t_now[b] = None
 
     def live_end(self, b: int) -> int:
         """End of bucket b's live positions (live edges come first)."""

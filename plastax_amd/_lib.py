@@ -30,6 +30,7 @@ PLX_MAX_SCONST = 32
 PLX_MAX_SFIELDS = 8
 PLX_MAX_SOUTS = 8
 PLX_MAX_GROW_COLS = 16
+PLX_SITE_ID_COLUMN = 0x100
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -200,6 +201,10 @@ class plx_site_desc(ctypes.Structure):
         ("n_dev", c_vp),
         ("outs", c_vp * PLX_MAX_SOUTS),
         ("or_into", c_vp),
+        ("kill_count", c_vp),
+        ("cid_map", c_vp),
+        ("ids_logical", c_vp),
+        ("ids_physical", c_vp),
     ]
 
 

@@ -34,6 +34,7 @@ from plastax_amd._expr import (
     compile_program,
     linear_map_field,
 )
+from plastax_amd.growth_config import GrowthConfig
 from plastax_amd.monoid import Monoid
 from plastax_amd.optim._rules import _RuleBase
 from plastax_amd.state import NetworkStatic
@@ -66,6 +67,9 @@ class Plan:
     loss: LossPlan | None
     backward: PassPlan | None
     update: Any  # an optim _RuleBase or None
+    net: Any = None  # the Network class (its structural policies are traced lazily)
+    prune_conn: bool = False
+    add_conn: Any = None  # the validated GrowthConfig, or None
 
     def pow_table(self) -> np.ndarray:
         """float32(b1^t), float32(b2^t) for t < POW_TABLE_LEN, by binary
@@ -149,9 +153,10 @@ def _trace_loss(loss: Any, static: NetworkStatic) -> LossPlan:
 
 def compile_plan(net: type, static: NetworkStatic) -> Plan:
     """The device plan of ``net``'s streaming step."""
-    for slot in ("update_unit", "prune_unit", "prune_conn", "add_unit", "add_conn", "reset_global"):
+    for slot in ("update_unit", "prune_unit", "add_unit", "reset_global"):
         if getattr(net, slot, None) is not None:
             raise UnsupportedPolicyError(f"{net.__name__}.{slot}: not in this build yet")
+    growth = GrowthConfig.of(net, static) if net.add_conn is not None else None
     forward = _trace_pass(net.forward_pass, static, backward=False)
     loss = _trace_loss(net.loss, static) if net.loss is not None else None
     backward = (
@@ -176,7 +181,8 @@ def compile_plan(net: type, static: NetworkStatic) -> Plan:
                     f"{net.__name__}: optimizer column {col!r} missing from extra_conn_fields"
                 )
         update = uc
-    return Plan(forward, loss, backward, update)
+    return Plan(forward, loss, backward, update, net=net, prune_conn=net.prune_conn is not None,
+                add_conn=growth)
 
 
 def program_struct(

@@ -686,11 +686,21 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       const int64_t e = t0 + 4 * q;
       if (FOLD) {
         // Each live edge's term goes to its slot in the tile's source-sorted
-        // order, so every (tile, source) group is a contiguous run of buf.
-        if (lv[i][0]) buf[rk[i].x & 0xFFFFu] = w[i].x * gd[i][0];
-        if (lv[i][1]) buf[rk[i].x >> 16] = w[i].y * gd[i][1];
-        if (lv[i][2]) buf[rk[i].y & 0xFFFFu] = w[i].z * gd[i][2];
-        if (lv[i][3]) buf[rk[i].y >> 16] = w[i].w * gd[i][3];
+        // order, so every (tile, source) group is a contiguous run of buf. A
+        // position tombstoned after the layout was built (below live_end)
+        // keeps its slot and contributes the identity; every group folds from
+        // the identity, so that leaves the fold's bits unchanged.
+        const float idv = Mono<M>::id();
+        const int32_t rs[4] = {static_cast<int32_t>(rk[i].x & 0xFFFFu), static_cast<int32_t>(rk[i].x >> 16),
+                               static_cast<int32_t>(rk[i].y & 0xFFFFu), static_cast<int32_t>(rk[i].y >> 16)};
+        const float wk[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (lv[i][k])
+            buf[rs[k]] = wk[k] * gd[i][k];
+          else if (e + k < d.live_end)
+            buf[rs[k]] = idv;
+        }
       }
       if (RULE >= 0) {
         float gr[4];

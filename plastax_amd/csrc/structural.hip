@@ -367,8 +367,11 @@ __device__ __forceinline__ uint32_t load32(const void* base, int32_t bytes, int6
 }
 
 struct Site {
-  int32_t role[5];  // i, j, src, dst, cid
-  uint64_t seed;    // (keyed << 32) | key
+  int32_t role[5];    // i, j, src, dst, cid (the position conn fields are read at)
+  int32_t cid_value;  // the cid the program sees
+  uint64_t seed;      // (keyed << 32) | key
+  const int32_t* ids_logical;
+  const int32_t* ids_physical;
 };
 
 __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units, uint32_t* outv) {
@@ -381,14 +384,21 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
     uint32_t v = 0;
     switch (op) {
       case S_CONST: v = p.consts[a]; break;
-      case S_IDX: v = static_cast<uint32_t>(c.role[a]); break;
+      case S_IDX: v = static_cast<uint32_t>(a == 4 ? c.cid_value : c.role[a]); break;
       case S_LDU: {
         int64_t at = yi;
         at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
+        if (c.ids_physical) at = c.ids_physical[at];
         v = load32(p.ufields[a], p.ubytes[a], at);
         break;
       }
-      case S_LDC: v = load32(p.cfields[a], p.cbytes[a], c.role[4]); break;
+      case S_LDC:
+        v = load32(p.cfields[a], p.cbytes[a] & 0xFF, c.role[4]);
+        if ((p.cbytes[a] & PLX_SITE_ID_COLUMN) && c.ids_logical) {
+          const int32_t id = static_cast<int32_t>(v);
+          v = static_cast<uint32_t>(c.ids_logical[id < 0 ? 0 : (id > num_units - 1 ? num_units - 1 : id)]);
+        }
+        break;
       case S_RNG:
         v = px::philox32(c.seed, (static_cast<uint64_t>(static_cast<uint32_t>(c.role[1])) << 16) |
                                      static_cast<uint32_t>(a));
@@ -504,11 +514,17 @@ __global__ void k_site_eval(plx_site_desc d) {
         break;
       default: c.role[4] = static_cast<int32_t>(s); break;  // EDGE
     }
+    c.cid_value = (d.kind == PLX_SITES_EDGE && d.cid_map) ? d.cid_map[s] : c.role[4];
+    c.ids_logical = d.ids_logical;
+    c.ids_physical = d.ids_physical;
     c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
     uint32_t out[PLX_MAX_SOUTS];
     site_run(d.prog, c, d.num_units, out);
     if (d.or_into) {
-      if (out[0]) d.or_into[s] = 1;
+      if (out[0] && !d.or_into[s]) {
+        d.or_into[s] = 1;
+        if (d.kill_count) atomicAdd(d.kill_count, 1);
+      }
     } else {
       for (int k = 0; k < d.prog.nout; ++k) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
     }

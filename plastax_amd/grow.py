@@ -52,8 +52,10 @@ def _bits_for(n: int) -> int:
     return max(1, int(n).bit_length())
 
 
-def fill_prog(sp: _site.SiteProgram, units: Columns, conns: Columns | None, globals_: Any) -> _lib.plx_site_prog:
-    """The plx_site_prog of a traced site program over device columns."""
+def fill_prog(sp: _site.SiteProgram, units: Columns, conns: Columns | None, globals_: Any,
+              physical_ids: bool = False) -> _lib.plx_site_prog:
+    """The plx_site_prog of a traced site program over device columns
+    (``physical_ids``: the conn id columns hold renumbered unit ids)."""
     p = _lib.plx_site_prog()
     p.ninstr = sp.ninstr
     p.nout = len(sp.out_kinds)
@@ -72,6 +74,8 @@ def fill_prog(sp: _site.SiteProgram, units: Columns, conns: Columns | None, glob
         col = conns[name]
         p.cfields[f] = col.data_ptr()
         p.cbytes[f] = 1 if col.element_size() == 1 else 4
+        if physical_ids and name in ("from_id", "to_id"):
+            p.cbytes[f] |= _lib.PLX_SITE_ID_COLUMN
     return p
 
 
@@ -109,9 +113,11 @@ class Kernels:
                   from_id: torch.Tensor | None = None, to_id: torch.Tensor | None = None,
                   occ: torch.Tensor | None = None, n_dev: torch.Tensor | None = None,
                   outs: list[torch.Tensor] | None = None, conns: Columns | None = None,
-                  or_into: torch.Tensor | None = None) -> None:
+                  or_into: torch.Tensor | None = None, kill_count: torch.Tensor | None = None,
+                  cid_map: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
+                  ids_physical: torch.Tensor | None = None) -> None:
         d = _lib.plx_site_desc()
-        d.prog = fill_prog(sp, units, conns, globals_)
+        d.prog = fill_prog(sp, units, conns, globals_, physical_ids=ids_logical is not None)
         d.n, d.kind, d.per, d.num_units = int(n), int(kind), int(per), int(num_units)
         d.step = int(np.array(int(step) & 0xFFFFFFFF, dtype=np.uint32).view(np.int32))
         d.net_seed = int(net_seed) & 0xFFFFFFFFFFFFFFFF
@@ -120,6 +126,8 @@ class Kernels:
         for k, o in enumerate(outs or []):
             d.outs[k] = o.data_ptr()
         d.or_into = _ptr(or_into)
+        d.kill_count, d.cid_map = _ptr(kill_count), _ptr(cid_map)
+        d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
         _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
 
     def compact(self, n: int, mode: int, flags: torch.Tensor, n_dev: torch.Tensor | None = None
@@ -191,14 +199,33 @@ class PruneConnPhase:
         conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
         self.prog = _site.trace_predicate(net.prune_conn, unit_dtypes, conn_dtypes, globals_)
 
-    def run(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], globals_: Any) -> None:
+    def run(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], globals_: Any,
+            kill_count: torch.Tensor | None = None) -> None:
+        """On the logical arena (caller's unit ids, slot order)."""
         n_units = int(next(iter(units.values())).shape[0])
         for bucket in conns:
             cap = int(bucket["dead"].shape[0])
             if cap == 0:
                 continue
             k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
-                        conns=bucket, or_into=bucket["dead"])
+                        conns=bucket, or_into=bucket["dead"], kill_count=kill_count)
+
+    def run_physical(self, k: Kernels, arena: Any, units: Columns, globals_: Any,
+                     kill_count: torch.Tensor) -> None:
+        """On the step's physical arena: positions of bucket b are
+        [base_b, base_b + cap_b), unit columns and the id columns are in the
+        arena's unit order; the program still sees the caller's ids and each
+        edge's logical slot (arena.slot)."""
+        n_units = int(next(iter(units.values())).shape[0])
+        for b in range(arena.num_buckets):
+            base, cap = arena.bases[b], arena.caps[b]
+            if cap == 0:
+                continue
+            view = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
+                        conns=view, or_into=view["dead"], kill_count=kill_count,
+                        cid_map=arena.slot[base : base + cap], ids_logical=arena.uperm32,
+                        ids_physical=arena.uinv32)
 
 
 def _lib_sites(name: str) -> int:

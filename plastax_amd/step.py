@@ -102,6 +102,10 @@ class StepFn:
         # the arenas this step builds.
         self.tile: int = TILE
         self.nsuper: int = NSUPER
+        # Structural phases, traced on the first step (their programs read
+        # the globals' structure).
+        self._prune: Any = None
+        self._grow: Any = None
 
     def _launch(self, kind: str, fn: Any, *args: Any) -> None:
         timer = self.timer
@@ -240,8 +244,50 @@ class StepFn:
         if plan.update is not None:
             state._arena_ahead = True
 
+        # Structural phases (phases.py:1444-1498, :4490-5203).
+        if plan.prune_conn or plan.add_conn is not None:
+            self._structural(state, arena, units, stream, g)
+
         state.step = state.step + 1
-        return StepResult(state=state, overflow=False, loss=loss, growth_remainder=None)
+        return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
+
+    def _structural(self, state: NetworkState, arena: Arena, units: dict, stream: int, g: Any) -> None:
+        """PruneConn on the physical arena (tombstones set in place), then
+        add_conn on the logical arena; a growth that fired replaces the
+        logical buckets, and the next step lays the arena out again."""
+        from plastax_amd import grow
+
+        plan = self.plan
+        k = grow.Kernels(state.device, stream)
+        if plan.prune_conn:
+            if self._prune is None:
+                self._prune = grow.PruneConnPhase(plan.net, self.static, g)
+            kills = torch.zeros(1, dtype=torch.int32, device=state.device)
+            timer = self.timer
+            if timer is not None:
+                timer.begin("prune_conn")
+            self._prune.run_physical(k, arena, units, g, kills)
+            if timer is not None:
+                timer.end("prune_conn")
+            if int(kills.item()):
+                arena.materialize_t()
+                arena.dead_in_rows = True
+                state._arena_ahead = True
+        if plan.add_conn is not None:
+            if self._grow is None:
+                self._grow = grow.AddConnPhase(plan.net, self.static, g)
+            phase = self._grow
+            fires = phase.cfg.fires(phase.ac, step=int(state.step), interval=phase.interval,
+                                    units_added=int(state.units_added), globals_=g)
+            if not fires:
+                state.grown, state.overflow = 0, False
+                return
+            out = phase.run(k, state.units, state.conns, step=int(state.step), globals_=g,
+                            tail_start=int(state.tail_start), units_added=int(state.units_added))
+            state.conns = out.conns
+            state.grown, state.overflow = out.grown, out.overflow
+            state.needs_resort = bool(state.needs_resort) or out.needs_resort
+            state.tail_start = out.tail_start
 
     # -- phases -----------------------------------------------------------------
     @staticmethod
