@@ -388,8 +388,10 @@ class Arena:
             True,
             nhot=nhot,
             grp_off=self._i32(grp_off),
-            grp_se=torch.from_numpy(se.astype(np.uint32).view(np.int32)).to(dev),
-            grp_tgt=self._i32(tgt[g_perm] if live else tgt),
+            # (one spare entry each: a bucket without live edges still gets
+            # real, if unused, tables)
+            grp_se=torch.from_numpy(np.concatenate([se.astype(np.uint32), np.zeros(1, np.uint32)]).view(np.int32)).to(dev),
+            grp_tgt=self._i32(np.concatenate([tgt[g_perm] if live else tgt, np.zeros(1, np.int64)])),
             cold_idx=self._i32(np.concatenate([cold_idx, np.zeros(1, np.int64)])),
             sorted_rank=torch.from_numpy(sorted_rank.view(np.int16)).to(dev),
             hot_sb=torch.zeros(max(nsuper * nhot, 1), dtype=torch.float32, device=dev),

@@ -347,6 +347,8 @@ class StepFn:
                fold: bool, update: bool, stream: int) -> None:
         lib = _lib.load()
         bt = arena.bwd[b]
+        if arena.lives[b] == 0:
+            return  # no edge was live when the arena was laid out: nothing to fold or update
         d = _lib.plx_tile_desc()
         d.base = bt.base
         d.end = bt.end
