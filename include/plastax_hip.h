@@ -396,6 +396,8 @@ PLX_EXPORT int64_t plx_scratch_ints(int64_t n);
 typedef struct plx_sort_key {
   int32_t kind;
   int32_t bits;
+  int32_t bound; /* LEVEL_OF: ids clamped to [0, bound) when > 0 */
+  int32_t reserved;
   const void* a;
   const void* b;
 } plx_sort_key;
@@ -537,11 +539,12 @@ typedef struct plx_grow_claim_desc {
 
 PLX_EXPORT int plx_grow_claim(const plx_grow_claim_desc* d, void* stream);
 
-/* PIPELINE claim domains (phases.py:3040-3049): domain[p] = level of the
- * former source of dead slot p below tail_start, else num_levels. */
-PLX_EXPORT int plx_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id,
-                                   const int32_t* level, int32_t num_levels, int64_t tail_start,
-                                   int32_t* domain, void* stream);
+/* PIPELINE claim domains (phases.py:3040-3049): for the listed slots,
+ * out[p] = level[clamp(ids[idx[p]], 0, bound - 1)], the level of each dead
+ * slot's former source (n_max, count n_dev). */
+PLX_EXPORT int plx_gather_level(int64_t n_max, const int32_t* n_dev, const int32_t* idx,
+                                const int32_t* ids, const int32_t* level, int32_t bound, int32_t* out,
+                                void* stream);
 
 /* Occurrence of each live edge among its parallel edges (phases.py:
  * 3990-4007): sorted lists the flat slots by (src, dst, slot), dead last;
@@ -550,13 +553,14 @@ PLX_EXPORT int plx_occurrence(int64_t n, const int32_t* sorted, const int32_t* f
                               const int32_t* to_id, int32_t* occ, void* stream);
 
 /* Small helpers of the growth pipeline: out[p] = a[idx[p]] (gather); per
- * level counts and first positions of a level-sorted list (count, start:
- * nlevels each); each bucket's run of the ascending free list (bucket_off:
+ * level counts of n keys (count in n_dev, optional) and the exclusive scan
+ * of those counts (count, start: nlevels each; scratch plx_scratch_ints(
+ * nlevels) ints); each bucket's run of the ascending free list (bucket_off:
  * num_buckets + 1 flat offsets; free_info: start, length per bucket). */
 PLX_EXPORT int plx_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t* idx,
                               const int32_t* a, int32_t* out, void* stream);
-PLX_EXPORT int plx_level_counts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* count,
-                                int32_t* start, void* stream);
+PLX_EXPORT int plx_level_counts(int64_t n, const int32_t* n_dev, const int32_t* keys, int32_t nlevels,
+                                int32_t* count, int32_t* start, int32_t* scratch, void* stream);
 PLX_EXPORT int plx_bucket_free(int32_t num_buckets, const int64_t* bucket_off,
                                const int32_t* free_slots, const int32_t* nfree_total,
                                int32_t* free_info, void* stream);

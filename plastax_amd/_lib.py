@@ -209,7 +209,7 @@ class plx_site_desc(ctypes.Structure):
 
 
 class plx_sort_key(ctypes.Structure):
-    _fields_ = [("kind", c_i32), ("bits", c_i32), ("a", c_vp), ("b", c_vp)]
+    _fields_ = [("kind", c_i32), ("bits", c_i32), ("bound", c_i32), ("reserved", c_i32), ("a", c_vp), ("b", c_vp)]
 
 
 class plx_sort_desc(ctypes.Structure):
@@ -325,10 +325,10 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_grow_mark_repeats": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_grow_select": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_vp, c_vp, c_vp]),
     "plx_grow_claim": (c_i32, [ctypes.POINTER(plx_grow_claim_desc), c_vp]),
-    "plx_pipeline_domain": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp]),
+    "plx_gather_level": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_occurrence": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_gather_i32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
-    "plx_level_counts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "plx_level_counts": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_bucket_free": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_mask_importance": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
 }

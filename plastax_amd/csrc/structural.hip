@@ -110,22 +110,21 @@ __global__ void k_chunk_sums(int64_t n_max, const int32_t* n_dev, int32_t mode, 
   if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-// One workgroup: exclusive scan of sums[0, m) in place; total (optional).
+// One workgroup: exclusive scan of sums[0, m) in place, 1024 consecutive
+// entries per round (coalesced); total (optional). Used for the chunk totals
+// of the multi-workgroup scans, so m stays small.
 __global__ void k_scan_single(int64_t m, int32_t* sums, int32_t* total) {
   __shared__ int lds[kScanLanes / 64 + 1];
-  const int64_t per = (m + kScanLanes - 1) / kScanLanes;
-  const int64_t lo = threadIdx.x * per;
-  const int64_t hi = lo + per < m ? lo + per : m;
-  int acc = 0;
-  for (int64_t i = lo; i < hi; ++i) acc += sums[i];
-  int all;
-  int run = block_exclusive_scan<kScanLanes>(acc, lds, &all);
-  for (int64_t i = lo; i < hi; ++i) {
-    const int v = sums[i];
-    sums[i] = run;
-    run += v;
+  int run = 0;
+  for (int64_t base = 0; base < m; base += kScanLanes) {
+    const int64_t i = base + threadIdx.x;
+    const int v = i < m ? sums[i] : 0;
+    int all;
+    const int ex = block_exclusive_scan<kScanLanes>(v, lds, &all);
+    if (i < m) sums[i] = run + ex;
+    run += all;
   }
-  if (threadIdx.x == 0 && total) *total = all;
+  if (threadIdx.x == 0 && total) *total = run;
 }
 
 __global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t* in, int32_t* out,
@@ -218,7 +217,8 @@ __global__ void k_gather_key(int64_t n_max, const int32_t* n_dev, plx_sort_key k
     switch (key.kind) {
       case PLX_KEY_SCORE: k = score_key(static_cast<const float*>(key.a)[idx]); break;
       case PLX_KEY_LEVEL_OF: {
-        const int32_t id = static_cast<const int32_t*>(key.a)[idx];
+        int32_t id = static_cast<const int32_t*>(key.a)[idx];
+        if (key.bound > 0) id = id < 0 ? 0 : (id >= key.bound ? key.bound - 1 : id);
         k = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id]);
         break;
       }
@@ -718,13 +718,14 @@ __global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int
   }
 }
 
-__global__ void k_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id,
-                                  const int32_t* level, int32_t nl, int64_t tail, int32_t* domain) {
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < cap;
+__global__ void k_gather_level(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const int32_t* ids,
+                               const int32_t* level, int32_t bound, int32_t* out) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
        p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    int32_t o = from_id[p];
-    o = o < 0 ? 0 : (o > nl - 1 ? nl - 1 : o);
-    domain[p] = (dead[p] && p < tail) ? level[o] : nl;
+    int32_t o = ids[idx[p]];
+    o = o < 0 ? 0 : (o > bound - 1 ? bound - 1 : o);
+    out[p] = level[o];
   }
 }
 
@@ -756,7 +757,9 @@ __global__ void k_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t*
     out[p] = a[idx[p]];
 }
 
-__global__ void k_level_count(int64_t n, const int32_t* keys, int32_t nl, int32_t* count) {
+__global__ void k_level_count(int64_t n_max, const int32_t* n_dev, const int32_t* keys, int32_t nl,
+                              int32_t* count) {
+  const int64_t n = live_count(n_max, n_dev);
   for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
        p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int32_t k = keys[p];
@@ -1003,14 +1006,14 @@ int plx_grow_claim(const plx_grow_claim_desc* d, void* stream) {
   return check_launch("plx_grow_claim");
 }
 
-int plx_pipeline_domain(int64_t cap, const uint8_t* dead, const int32_t* from_id, const int32_t* level,
-                        int32_t num_levels, int64_t tail_start, int32_t* domain, void* stream) {
-  if (cap < 0 || num_levels < 1) return fail(PLX_ERR_INVALID, "plx_pipeline_domain: bad sizes");
-  if (cap == 0) return PLX_OK;
-  if (!dead || !from_id || !level || !domain) return fail(PLX_ERR_INVALID, "plx_pipeline_domain: null pointer");
-  hipLaunchKernelGGL(k_pipeline_domain, dim3(grid_for(cap)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
-                     cap, dead, from_id, level, num_levels, tail_start, domain);
-  return check_launch("plx_pipeline_domain");
+int plx_gather_level(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const int32_t* ids,
+                     const int32_t* level, int32_t bound, int32_t* out, void* stream) {
+  if (n_max < 0 || bound < 1) return fail(PLX_ERR_INVALID, "plx_gather_level: bad sizes");
+  if (n_max == 0) return PLX_OK;
+  if (!idx || !ids || !level || !out) return fail(PLX_ERR_INVALID, "plx_gather_level: null pointer");
+  hipLaunchKernelGGL(k_gather_level, dim3(grid_for(n_max)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     n_max, n_dev, idx, ids, level, bound, out);
+  return check_launch("plx_gather_level");
 }
 
 int plx_occurrence(int64_t n, const int32_t* sorted, const int32_t* from_id, const int32_t* to_id, int32_t* occ,
@@ -1033,19 +1036,17 @@ int plx_gather_i32(int64_t n_max, const int32_t* n_dev, const int32_t* idx, cons
   return check_launch("plx_gather_i32");
 }
 
-int plx_level_counts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* count, int32_t* start,
-                     void* stream) {
+int plx_level_counts(int64_t n, const int32_t* n_dev, const int32_t* keys, int32_t nlevels, int32_t* count,
+                     int32_t* start, int32_t* scratch, void* stream) {
   if (n < 0 || nlevels < 1) return fail(PLX_ERR_INVALID, "plx_level_counts: bad sizes");
-  if (!count || !start || (n > 0 && !keys)) return fail(PLX_ERR_INVALID, "plx_level_counts: null pointer");
+  if (!count || !start || !scratch || (n > 0 && !keys))
+    return fail(PLX_ERR_INVALID, "plx_level_counts: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(nlevels)), dim3(kBlock), 0, s, static_cast<int64_t>(nlevels), 0,
                      count);
-  if (n > 0) hipLaunchKernelGGL(k_level_count, dim3(grid_for(n)), dim3(kBlock), 0, s, n, keys, nlevels, count);
-  hipLaunchKernelGGL(k_copy_i32, dim3(grid_for(nlevels)), dim3(kBlock), 0, s, static_cast<int64_t>(nlevels), count,
-                     start);
-  hipLaunchKernelGGL(k_scan_single, dim3(1), dim3(kScanLanes), 0, s, static_cast<int64_t>(nlevels), start,
-                     static_cast<int32_t*>(nullptr));
-  return check_launch("plx_level_counts");
+  if (n > 0)
+    hipLaunchKernelGGL(k_level_count, dim3(grid_for(n)), dim3(kBlock), 0, s, n, n_dev, keys, nlevels, count);
+  return scan_or_compact(nlevels, nullptr, -1, count, start, nullptr, scratch, s, "plx_level_counts");
 }
 
 int plx_bucket_free(int32_t num_buckets, const int64_t* bucket_off, const int32_t* free_slots,

@@ -139,15 +139,17 @@ class Kernels:
                                         count.data_ptr(), scratch.data_ptr(), self.s), "plx_compact")
         return out, count
 
-    def sort(self, vals: torch.Tensor, n_max: int, keys: list[tuple[int, int, torch.Tensor, torch.Tensor | None]],
-             n_dev: torch.Tensor | None = None) -> None:
-        """Stable sort of ``vals`` (in place) by ``keys`` (least significant first)."""
+    def sort(self, vals: torch.Tensor, n_max: int, keys: list[tuple], n_dev: torch.Tensor | None = None) -> None:
+        """Stable sort of ``vals`` (in place) by ``keys`` (least significant
+        first): (kind, bits, a, b[, bound]) per key."""
         if n_max == 0 or not keys:
             return
         d = _lib.plx_sort_desc()
         d.n_max, d.n_dev, d.nkeys = int(n_max), _ptr(n_dev), len(keys)
-        for k, (kind, bits, a, b) in enumerate(keys):
+        for k, key in enumerate(keys):
+            kind, bits, a, b = key[:4]
             d.keys[k].kind, d.keys[k].bits = int(kind), int(bits)
+            d.keys[k].bound = int(key[4]) if len(key) > 4 else 0
             d.keys[k].a, d.keys[k].b = a.data_ptr(), _ptr(b)
         kb, ka, va = self.mem.i32(n_max), self.mem.i32(n_max), self.mem.i32(n_max)
         hist = self.mem.ints_for(n_max)
@@ -181,7 +183,10 @@ def flatten(conns: tuple[Columns, ...]) -> tuple[Columns, list[int]]:
     offs = [0]
     for c in caps:
         offs.append(offs[-1] + c)
-    flat = {name: torch.cat([b[name] for b in conns]).contiguous() for name in conns[0]}
+    if len(conns) == 1:
+        flat = {name: col.contiguous() for name, col in conns[0].items()}
+    else:
+        flat = {name: torch.cat([b[name] for b in conns]).contiguous() for name in conns[0]}
     return flat, offs
 
 
@@ -287,6 +292,9 @@ class AddConnPhase:
         pruned = units.get("pruned")
         seed, dev = int(self.static.seed), level.device
         INT_MAX = 0x7FFFFFFF
+        # Levels bound the per-level segments (PIPELINE levels run up to the
+        # unit count): one read of the deepest level sizes them.
+        max_level = int(level.max().item()) if level.numel() else 0
 
         # 1. candidates
         grid_sq = 0
@@ -380,10 +388,11 @@ class AddConnPhase:
         # 4. total order of the finite candidates
         order, nord = k.compact(nc, 2, score)
         per_segment = not cfg.step_scope
-        nseg = n if cfg.pipeline else nb
+        nseg = max_level + 1 if cfg.pipeline else nb
+        level_key = (2, _bits_for(nseg - 1), src, level, n)  # PLX_KEY_LEVEL_OF, ids clamped to [0, n)
         keys = [*pair_keys, (1, 32, score, None)]
         if per_segment:
-            keys.append((2, _bits_for(nseg), src, level))  # PLX_KEY_LEVEL_OF
+            keys.append(level_key)
         k.sort(order, nc, keys, n_dev=nord)
 
         # 5. selection
@@ -395,7 +404,7 @@ class AddConnPhase:
         wpos, nwin = k.compact(nc, 0, win, n_dev=nord)  # PLX_FLAG_U8
         winners = k.gather(wpos, order, nc, nwin)
         if not per_segment:
-            k.sort(winners, nc, [(2, _bits_for(nseg), src, level)], n_dev=nwin)
+            k.sort(winners, nc, [level_key], n_dev=nwin)
 
         # init of the winners
         wsrc = k.gather(winners, src, nc, nwin)
@@ -409,7 +418,7 @@ class AddConnPhase:
         c = _lib.plx_grow_claim_desc()
         c.n_max, c.n_dev, c.winners = nc, nwin.data_ptr(), winners.data_ptr()
         c.src, c.dst, c.score, c.level = src.data_ptr(), dst.data_ptr(), score.data_ptr(), level.data_ptr()
-        c.pipeline, c.num_buckets, c.num_levels = int(cfg.pipeline), nb, n
+        c.pipeline, c.num_buckets, c.num_levels = int(cfg.pipeline), nb, nseg
         if cfg.selection == "threshold":
             c.has_threshold = 1
             c.threshold = float(np.float32(np.asarray(self.ac.threshold(globals_))))
@@ -417,17 +426,20 @@ class AddConnPhase:
         c.capacity, c.tail_start = total_slots, int(tail_start)
         keep: list[torch.Tensor] = []
         if cfg.pipeline:
-            domain = k.mem.i32(total_slots)
-            _lib.check(k.lib.plx_pipeline_domain(total_slots, flat["dead"].data_ptr(), flat["from_id"].data_ptr(),
-                                                 level.data_ptr(), n, int(tail_start), domain.data_ptr(), k.s),
-                       "plx_pipeline_domain")
-            own = k.iota(total_slots)
-            k.sort(own, total_slots, [(0, _bits_for(n), domain, None)])
-            count, start = k.mem.i32(n), k.mem.i32(n)
-            _lib.check(k.lib.plx_level_counts(total_slots, domain.data_ptr(), n, count.data_ptr(), start.data_ptr(),
-                                              k.s), "plx_level_counts")
+            # Each level's own dead slots (below the tail, by the level of
+            # their former source), in slot order, level after level.
+            tail = int(tail_start)
+            own, nown = k.compact(tail, 0, flat["dead"])  # PLX_FLAG_U8 over [0, tail)
+            k.sort(own, tail, [(2, _bits_for(nseg - 1), flat["from_id"], level, n)], n_dev=nown)
+            domain = k.mem.i32(tail)
+            _lib.check(k.lib.plx_gather_level(tail, nown.data_ptr(), own.data_ptr(), flat["from_id"].data_ptr(),
+                                              level.data_ptr(), n, domain.data_ptr(), k.s), "plx_gather_level")
+            count, start = k.mem.i32(nseg), k.mem.i32(nseg)
+            lscratch = k.mem.ints_for(nseg)
+            _lib.check(k.lib.plx_level_counts(tail, nown.data_ptr(), domain.data_ptr(), nseg, count.data_ptr(),
+                                              start.data_ptr(), lscratch.data_ptr(), k.s), "plx_level_counts")
             c.own_slots, c.own_start, c.own_count = own.data_ptr(), start.data_ptr(), count.data_ptr()
-            keep += [domain, own, count, start]
+            keep += [domain, own, nown, count, start, lscratch]
         else:
             free, nfree = k.compact(total_slots, 0, flat["dead"])
             off = torch.tensor(offs, dtype=torch.int64, device=dev)

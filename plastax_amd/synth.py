@@ -137,3 +137,26 @@ def c1_target(seed: int, n_in: int = 32, n_out: int = 8) -> np.ndarray:
     """C1's fixed random linear target matrix A (n_out x n_in), N(0, 1/n_in)."""
     rng = np.random.default_rng(seed + 1)
     return (rng.standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float32)
+
+
+def c5_reservoir(seed: int = 0, num_units: int = 65536, num_edges: int = 4 * 1024 * 1024,
+                 n_in: int = 256) -> EdgeList:
+    """C5's growing reservoir at its starting shape: 65,536 live units, 4M
+    uniform random recurrent edges without self-loops (PIPELINE), weights
+    N(0, 1) scaled by 1/sqrt(mean fan-in) so the spectral radius is about 1;
+    256 inputs. The unit and edge capacities (262,144 and 16M) are the
+    builder's (unit_capacity, capacity_headroom=3)."""
+    rng = np.random.default_rng(seed)
+    src = rng.integers(0, num_units, size=num_edges, dtype=np.int64)
+    dst = rng.integers(0, num_units - 1, size=num_edges, dtype=np.int64)
+    dst = dst + (dst >= src)
+    scale = 1.0 / np.sqrt(num_edges / num_units)
+    weight = (rng.standard_normal(num_edges) * scale).astype(np.float32)
+    return EdgeList(
+        num_units,
+        src.astype(np.int32),
+        dst.astype(np.int32),
+        weight,
+        np.arange(n_in, dtype=np.int32),
+        np.arange(num_units - 16, num_units, dtype=np.int32),
+    )
