@@ -144,8 +144,164 @@ def cpu_baseline(px, net, static, e, host_units, host_conns, inputs, targets, st
     }
 
 
+GROWTH_METRIC = "add_conn proposals/sec per growth phase (C5 reservoir, per-unit ProposeAddConn, P=4)"
+
+
+def build_c5(px):
+    """C5's growing reservoir at its starting shape, with the per-unit
+    proposal rule of the configuration (P = 4 via the counter-based rng)."""
+    import plastax_amd.numpy as jnp
+
+    class Tanh(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(acc)))
+
+    class Propose(px.ProposeAddConn):
+        proposer = "per_unit"
+        proposals_per_proposer = 4
+        max_new_per_level = 16
+        max_level_gap = 1 << 20
+
+        def propose(self, u, i, j, g, rng):
+            dst = rng.uniform_int(65536).astype(jnp.int32)
+            return jnp.asarray(i, jnp.int32), dst, rng.uniform()
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of((px.WEIGHT, jnp.float32(0.01)))
+
+    class C5(px.Network):
+        forward_pass = Tanh()
+        add_conn = Propose()
+        propagation = px.Propagation.PIPELINE
+        unit_capacity = 262144
+
+    return C5
+
+
+def run_c5_growth(args) -> int:
+    """The add_conn phase of C5 on the device: 262,144 unit slots x 4
+    proposals per phase, over the 16M-slot logical arena; each timed phase
+    commits its winners, so the arena evolves like C5's every-step growth."""
+    import torch
+
+    import plastax_amd as px
+    from plastax_amd import grow, synth
+    from plastax_amd.state import column_to_numpy
+
+    t_setup = time.perf_counter()
+    net = build_c5(px)
+    e = synth.c5_reservoir(args.seed)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, capacity_headroom=3.0, device="cpu")
+    progress(f"C5 arena: {e.src.size} live edges of {static.level_capacities[0]} slots "
+             f"({time.perf_counter() - t_setup:.1f} s)")
+    uspecs = {s.name: s for s in static.unit_fields}
+    cspecs = {s.name: s for s in static.conn_fields}
+    host_units = {k: column_to_numpy(v, uspecs[k]).copy() for k, v in state.units.items()}
+    host_conns = [{k: column_to_numpy(v, cspecs[k]).copy() for k, v in b.items()} for b in state.conns]
+    tail0 = int(state.tail_start)
+    dev = torch.device("cuda", 0)
+    units = {k: v.to(dev) for k, v in state.units.items()}
+    conns = tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns)
+    phase = grow.AddConnPhase(net, static, None)
+    timer = EventTimer({"total_order"})
+    k = grow.Kernels(dev, torch.cuda.current_stream(dev).cuda_stream, timer=timer)
+    tail = tail0
+    for it in range(args.warmup):
+        out = phase.run(k, units, conns, step=it, globals_=None, tail_start=tail)
+        conns, tail = out.conns, out.tail_start
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    timer.on = True
+    grown = 0
+    t0 = time.perf_counter()
+    for it in range(args.warmup, args.warmup + args.steps):
+        out = phase.run(k, units, conns, step=it, globals_=None, tail_start=tail)
+        conns, tail = out.conns, out.tail_start
+        grown += out.grown
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.on = False
+    dom = timer.summary()["total_order"]
+    n_sorted = int(phase.last_sort[0].item())
+    passes = int(phase.last_sort[1])
+    sites = int(static.num_units) * 4
+    ms = elapsed * 1e3 / args.steps
+    # The total order's radix passes read and write each key and index once
+    # (16 B per sorted candidate per 8-bit pass).
+    per_launch = 16 * passes * n_sorted
+    ach = per_launch / (dom["mean_ms"] * 1e-3) / 1e9
+    roofline = {
+        "kernel": "total_order (plx_sort)",
+        "bound": "hbm",
+        "achieved": round(ach, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "algorithmic_bytes_per_launch": per_launch,
+        "mean_launch_ms": round(dom["mean_ms"], 4),
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import growth as og
+
+        times = []
+        tail_c = tail0
+        conns_c = host_conns
+        for it in range(1):
+            t1 = time.perf_counter()
+            res = og.add_conn(net, static, host_units, conns_c, step=it, globals_=None, tail_start=tail_c)
+            times.append(time.perf_counter() - t1)
+            conns_c, tail_c = res.conns, res.tail_start
+        med = float(np.median(times))
+        cpu = {
+            "value": float(sites / med),
+            "unit": "proposals/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"1 add_conn phase of the same workload, {med * 1e3:.0f} ms "
+            "(numpy + the C site interpreter of oracle/, one thread)",
+        }
+    line = {
+        "metric": GROWTH_METRIC,
+        "value": round(sites / (ms * 1e-3), 1),
+        "unit": "proposals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C5 growth phase: 65,536 live of 262,144 unit slots, 4M live of 16M edge slots, "
+            "PIPELINE, per-unit proposals P=4, max_new_per_level 16",
+            "sites": sites,
+            "sorted_candidates": n_sorted,
+            "radix_passes": passes,
+        },
+        "grown_per_phase": grown / args.steps,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", choices=("c2", "c5_growth"), default="c2",
+                    help="c2: the streaming step (the headline metric); c5_growth: the add_conn phase")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
@@ -166,6 +322,9 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.workload == "c5_growth":
+        return run_c5_growth(args)
 
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4

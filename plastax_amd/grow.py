@@ -102,10 +102,21 @@ class Scratch:
 class Kernels:
     """Thin wrappers of the structural entry points on one stream."""
 
-    def __init__(self, device: torch.device, stream: int) -> None:
+    def __init__(self, device: torch.device, stream: int, timer: Any = None) -> None:
         self.lib = _lib.load()
         self.s = stream
         self.mem = Scratch(device)
+        # Optional hook with begin(kind) / end(kind) around each entry-point
+        # call (the benchmark records HIP events there).
+        self.timer = timer
+
+    def _begin(self, kind: str) -> None:
+        if self.timer is not None:
+            self.timer.begin(kind)
+
+    def _end(self, kind: str) -> None:
+        if self.timer is not None:
+            self.timer.end(kind)
 
     def site_eval(self, sp: _site.SiteProgram, units: Columns, globals_: Any, *, n: int, kind: int,
                   per: int = 1, num_units: int, step: int = 0, net_seed: int = 0,
@@ -128,7 +139,9 @@ class Kernels:
         d.or_into = _ptr(or_into)
         d.kill_count, d.cid_map = _ptr(kill_count), _ptr(cid_map)
         d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
+        self._begin("site_eval")
         _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
+        self._end("site_eval")
 
     def compact(self, n: int, mode: int, flags: torch.Tensor, n_dev: torch.Tensor | None = None
                 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -139,7 +152,8 @@ class Kernels:
                                         count.data_ptr(), scratch.data_ptr(), self.s), "plx_compact")
         return out, count
 
-    def sort(self, vals: torch.Tensor, n_max: int, keys: list[tuple], n_dev: torch.Tensor | None = None) -> None:
+    def sort(self, vals: torch.Tensor, n_max: int, keys: list[tuple], n_dev: torch.Tensor | None = None,
+             tag: str = "sort") -> None:
         """Stable sort of ``vals`` (in place) by ``keys`` (least significant
         first): (kind, bits, a, b[, bound]) per key."""
         if n_max == 0 or not keys:
@@ -155,7 +169,9 @@ class Kernels:
         hist = self.mem.ints_for(n_max)
         d.vals, d.keys_buf, d.keys_alt, d.vals_alt, d.hist = (
             vals.data_ptr(), kb.data_ptr(), ka.data_ptr(), va.data_ptr(), hist.data_ptr())
+        self._begin(tag)
         _lib.check(self.lib.plx_sort(d, self.s), "plx_sort")
+        self._end(tag)
 
     def gather(self, idx: torch.Tensor, a: torch.Tensor, n_max: int, n_dev: torch.Tensor | None) -> torch.Tensor:
         out = self.mem.i32(n_max)
@@ -393,7 +409,9 @@ class AddConnPhase:
         keys = [*pair_keys, (1, 32, score, None)]
         if per_segment:
             keys.append(level_key)
-        k.sort(order, nc, keys, n_dev=nord)
+        k.sort(order, nc, keys, n_dev=nord, tag="total_order")
+        # (for measurement: the sorted count and the 8-bit digit passes)
+        self.last_sort = (nord, sum((int(key[1]) + 7) // 8 for key in keys))
 
         # 5. selection
         win = k.mem.u8(nc)
