@@ -277,8 +277,9 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
 /* sizeof of the descriptor structs, in the order plx_program, plx_finalize,
  * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc,
  * plx_site_prog, plx_site_desc, plx_sort_key, plx_sort_desc,
- * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc (for binding
- * layers to check their mirrors). Writes min(n, 13) values and returns 13. */
+ * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc, plx_unit_col (for
+ * binding layers to check their mirrors). Writes min(n, 14) values and
+ * returns 14. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
 
 /* ========================================================================
@@ -332,9 +333,10 @@ typedef struct plx_site_prog {
  * Renumbered storage: the program always sees the caller's unit ids and
  * logical slots. With ids_physical set, a unit field read at id u reads
  * position ids_physical[u]; a conn field whose cbytes has PLX_SITE_ID_COLUMN
- * holds physical unit ids and reads back ids_logical[value]; with cid_map
- * set (EDGE sites), the cid the program sees is cid_map[s] while conn fields
- * are read at s. */
+ * holds physical unit ids and reads back ids_logical[value]; with site_ids
+ * set, the cid (EDGE sites) or unit i (UNIT sites) the program sees is
+ * site_ids[s] (site_ids[s / per]) while fields are read at the site's own
+ * position. */
 #define PLX_SITE_ID_COLUMN 0x100
 typedef struct plx_site_desc {
   plx_site_prog prog;
@@ -353,7 +355,7 @@ typedef struct plx_site_desc {
   void* outs[PLX_MAX_SOUTS];
   uint8_t* or_into;
   int32_t* kill_count;
-  const int32_t* cid_map;
+  const int32_t* site_ids;
   const int32_t* ids_logical;
   const int32_t* ids_physical;
 } plx_site_desc;
@@ -564,6 +566,49 @@ PLX_EXPORT int plx_level_counts(int64_t n, const int32_t* n_dev, const int32_t* 
 PLX_EXPORT int plx_bucket_free(int32_t num_buckets, const int64_t* bucket_off,
                                const int32_t* free_slots, const int32_t* nfree_total,
                                int32_t* free_info, void* stream);
+/* Unit lifecycle (phases.py:1148-1193, :1245-1441). A unit column list:
+ * pointer, element size (4, or 1 for bool columns), default bits. */
+#define PLX_MAX_UNIT_COLS 16
+typedef struct plx_unit_col {
+  void* ptr;
+  int32_t bytes;
+  uint32_t default_bits;
+} plx_unit_col;
+
+/* Masked unit writes: for r < n (count n_dev, optional), unit u = idx ? idx[r]
+ * : r gets cols[k][u] = outs[k][r] (32-bit patterns; byte columns take
+ * value != 0), unless skip[u] != 0 (skip optional: the PRUNED column for
+ * update_unit's live mask, phases.py:1184-1190). */
+PLX_EXPORT int plx_unit_write(int64_t n, const int32_t* n_dev, const int32_t* idx, const uint8_t* skip,
+                              int32_t ncols, const plx_unit_col* cols, const uint32_t* const* outs,
+                              void* stream);
+
+/* prune_unit (phases.py:1245-1307): doomed[u] = selected[u] && !pruned[u] &&
+ * !exempt[u]; a doomed unit's columns in cols take their defaults, PRUNED
+ * is set, and doomed_count counts them. */
+PLX_EXPORT int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const uint8_t* exempt,
+                              int32_t ncols, const plx_unit_col* cols, uint8_t* doomed, int32_t* doomed_count,
+                              void* stream);
+
+/* The incident-edge kill of prune_unit: dead[p] |= doomed[from[p]] |
+ * doomed[to[p]] over n positions (ids mapped through id_map when set);
+ * kill_count (optional) counts the bytes turned to 1. */
+PLX_EXPORT int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
+                                 const uint8_t* doomed, const int32_t* id_map, int32_t* kill_count,
+                                 void* stream);
+
+/* add_unit's placement (phases.py:1376-1405): the r-th parent (parents:
+ * ascending live spawning ids, *nparents) takes the r-th free slot (free:
+ * ascending PRUNED ids, *nfree): its columns take their defaults, its level
+ * clamp(level[parent] + offset[parent], 1, max_level), PRUNED is cleared;
+ * child[r], parent[r] list the placements. flags[0] = placed count, flags[1]
+ * = 1 when some parent found no slot. */
+PLX_EXPORT int plx_unit_place(int64_t n_max, const int32_t* parents, const int32_t* nparents,
+                              const int32_t* free_ids, const int32_t* nfree, const int32_t* offset,
+                              int32_t* level, uint8_t* pruned, int32_t max_level, int32_t ncols,
+                              const plx_unit_col* cols, int32_t* child, int32_t* parent, int32_t* flags,
+                              void* stream);
+
 /* importance masks for the shortlists (phases.py:3683-3746): out[u] = imp[u]
  * where (mode 0: level[u] == b; mode 1: |level[u] - b| <= gap with the
  * direction; mode 2: always) and the unit is live, else -inf. */

@@ -584,3 +584,74 @@ def add_conn(
         )
     grown = int(sum(int(m.sum()) for m in committed))
     return GrowthResult(new_conns, grown, overflow, needs_resort or reassigning, tail_start, True, winners)
+
+
+# ---------------------------------------------------------------------------
+# Unit lifecycle (phases.py:1148-1193, :1245-1441).
+# ---------------------------------------------------------------------------
+
+
+def _unit_defaults(static: Any) -> dict[str, Any]:
+    return {s.name: np.asarray(s.default, dtype=s.dtype) for s in static.unit_fields
+            if s.name not in ("level", "pruned")}
+
+
+def update_unit(prog: _site.SiteProgram, names: list[str], units: dict, globals_: Any) -> dict:
+    """Every live unit's update against the pre-phase columns."""
+    n = int(units["level"].shape[0])
+    outs = site_eval(prog, n, {"i": np.arange(n, dtype=np.int32)}, units, globals_)
+    new = {k: v.copy() for k, v in units.items()}
+    live = ~units["pruned"].astype(bool) if "pruned" in units else np.ones(n, bool)
+    for name, val in zip(names, outs):
+        new[name] = np.where(live, val.astype(units[name].dtype), units[name])
+    return new
+
+
+def prune_unit(prog: _site.SiteProgram, static: Any, units: dict, conns: list[dict], globals_: Any
+               ) -> tuple[dict, list[dict], np.ndarray]:
+    """Prune the selected live non-I/O units, reset their columns (LEVEL kept)
+    and tombstone every incident edge."""
+    n = int(units["level"].shape[0])
+    (selected,) = site_eval(prog, n, {"i": np.arange(n, dtype=np.int32)}, units, globals_)
+    exempt = np.zeros(n, bool)
+    ids = np.asarray(tuple(static.input_ids) + tuple(static.output_ids), dtype=np.int64)
+    exempt[ids] = True
+    pruned = units["pruned"].astype(bool)
+    doomed = selected & ~pruned & ~exempt
+    new = {k: v.copy() for k, v in units.items()}
+    for name, default in _unit_defaults(static).items():
+        new[name] = np.where(doomed, default, units[name]).astype(units[name].dtype)
+    new["pruned"] = (pruned | doomed).astype(units["pruned"].dtype)
+    out = []
+    for b in conns:
+        nb = dict(b)
+        nb["dead"] = b["dead"].astype(bool) | doomed[b["from_id"]] | doomed[b["to_id"]]
+        out.append(nb)
+    return new, out, doomed
+
+
+def add_unit(spawn: _site.SiteProgram, init: _site.SiteProgram, init_names: list[str], static: Any,
+             max_levels: int, units: dict, globals_: Any) -> tuple[dict, int, bool, np.ndarray]:
+    """The k-th spawning live parent (ascending id) takes the k-th lowest
+    PRUNED slot; returns (units, units_added, unit_overflow, children)."""
+    n = int(units["level"].shape[0])
+    wants, offset = site_eval(spawn, n, {"i": np.arange(n, dtype=np.int32)}, units, globals_)
+    free = units["pruned"].astype(bool)
+    parent = wants & ~free
+    parents = np.flatnonzero(parent)
+    free_ids = np.flatnonzero(free)
+    placed = min(parents.size, free_ids.size)
+    children = free_ids[:placed]
+    pars = parents[:placed]
+    new = {k: v.copy() for k, v in units.items()}
+    for name, default in _unit_defaults(static).items():
+        new[name][children] = default
+    lvl = units["level"].astype(np.int64)[pars] + offset.astype(np.int64)[pars]
+    new["level"][children] = np.clip(lvl, 1, max_levels - 1).astype(new["level"].dtype)
+    new["pruned"][children] = False
+    if placed and init_names:
+        outs = site_eval(init, placed, {"src": children.astype(np.int32), "dst": pars.astype(np.int32)},
+                         new, globals_)
+        for name, val in zip(init_names, outs):
+            new[name][children] = val.astype(new[name].dtype)
+    return new, int(placed), bool(parents.size > free_ids.size), children

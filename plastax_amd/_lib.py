@@ -31,6 +31,7 @@ PLX_MAX_SFIELDS = 8
 PLX_MAX_SOUTS = 8
 PLX_MAX_GROW_COLS = 16
 PLX_SITE_ID_COLUMN = 0x100
+PLX_MAX_UNIT_COLS = 16
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -202,7 +203,7 @@ class plx_site_desc(ctypes.Structure):
         ("outs", c_vp * PLX_MAX_SOUTS),
         ("or_into", c_vp),
         ("kill_count", c_vp),
-        ("cid_map", c_vp),
+        ("site_ids", c_vp),
         ("ids_logical", c_vp),
         ("ids_physical", c_vp),
     ]
@@ -299,6 +300,11 @@ class plx_grow_claim_desc(ctypes.Structure):
     ]
 
 
+
+class plx_unit_col(ctypes.Structure):
+    _fields_ = [("ptr", c_vp), ("bytes", c_i32), ("default_bits", ctypes.c_uint32)]
+
+
 _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_bucket": (c_i32, [ctypes.POINTER(plx_forward_desc), c_vp]),
     "plx_backward_tiles": (c_i32, [ctypes.POINTER(plx_tile_desc), c_vp]),
@@ -331,6 +337,11 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_level_counts": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_bucket_free": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_mask_importance": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
+                               c_vp]),
 }
 
 # Entry points the header declares (checked by the CPU test suite).
@@ -350,6 +361,7 @@ STRUCTS = (
     plx_grow_filter_desc,
     plx_grow_col,
     plx_grow_claim_desc,
+    plx_unit_col,
 )
 
 _lib: ctypes.CDLL | None = None

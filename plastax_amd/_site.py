@@ -485,3 +485,52 @@ def trace_predicate(rule: Any, unit_dtypes: dict, conn_dtypes: dict, g: Any) -> 
     out = rule.predicate(SiteUnitView(unit_dtypes), SiteConnView(conn_dtypes), idx("cid"), SiteGlobals(g))
     return compile_site_program([(out, "b")], roles=("cid", "src", "dst"))
 
+
+
+def _unit_outputs(write: Any, unit_dtypes: dict) -> tuple[list[tuple[Any, str]], list[str]]:
+    fields = dict(getattr(write, "fields", write))
+    outs, names = [], []
+    for name, value in fields.items():
+        if name not in unit_dtypes:
+            raise UnsupportedPolicyError(f"a unit policy writes {name!r}, which is not a unit column")
+        outs.append((value, kind_of_dtype(unit_dtypes[name])))
+        names.append(name)
+    return outs, names
+
+
+def trace_update_unit(rule: Any, unit_dtypes: dict, g: Any) -> tuple[SiteProgram, list[str]]:
+    """UpdateUnit.update(u, i, g) -> UnitWrite (phases.py:1148-1193)."""
+    write = rule.update(SiteUnitView(unit_dtypes), idx("i"), SiteGlobals(g))
+    outs, names = _unit_outputs(write, unit_dtypes)
+    return compile_site_program(outs, roles=("i",)), names
+
+
+def trace_prune_unit(rule: Any, unit_dtypes: dict, g: Any) -> SiteProgram:
+    """PruneUnit.predicate(u, i, g) -> bool (phases.py:1245-1307)."""
+    out = rule.predicate(SiteUnitView(unit_dtypes), idx("i"), SiteGlobals(g))
+    return compile_site_program([(out, "b")], roles=("i",))
+
+
+class _Pruned:
+    name = "pruned"
+
+
+def trace_spawn(rule: Any, unit_dtypes: dict, g: Any) -> SiteProgram:
+    """AddUnit.spawn(u, parent, g) -> (spawns bool, level offset int32)
+    (phases.py:1362-1367); the first output is already "a live unit that
+    spawns"."""
+    u = SiteUnitView(unit_dtypes)
+    wants, offset = rule.spawn(u, idx("i"), SiteGlobals(g))
+    wants = cast(lift(wants), np.bool_)
+    if "pruned" in unit_dtypes:
+        # a parent is a live unit that spawns (phases.py:1374)
+        wants = binary("and", wants, binary("eq", cast(u[_Pruned, idx("i")], np.int32), 0))
+    return compile_site_program([(wants, "b"), (offset, "i")], roles=("i",))
+
+
+def trace_unit_init(rule: Any, unit_dtypes: dict, g: Any) -> tuple[SiteProgram, list[str]]:
+    """AddUnit.init(u, child, parent, g) -> UnitWrite (phases.py:1398-1405);
+    the child is the site's src role and the parent its dst role."""
+    write = rule.init(SiteUnitView(unit_dtypes), idx("src"), idx("dst"), SiteGlobals(g))
+    outs, names = _unit_outputs(write, unit_dtypes)
+    return compile_site_program(outs, roles=("src", "dst")), names

@@ -1056,16 +1056,16 @@ const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 int32_t plx_abi_version(void) { return 6; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[13] = {
+  const int64_t sizes[14] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
       sizeof(plx_partials_desc),    sizeof(plx_update_desc),
       sizeof(plx_site_prog),        sizeof(plx_site_desc),
       sizeof(plx_sort_key),         sizeof(plx_sort_desc),
       sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
-      sizeof(plx_grow_claim_desc)};
-  for (int32_t k = 0; k < n && k < 13; ++k) out[k] = sizes[k];
-  return 13;
+      sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col)};
+  for (int32_t k = 0; k < n && k < 14; ++k) out[k] = sizes[k];
+  return 14;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {

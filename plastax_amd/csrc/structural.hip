@@ -514,7 +514,11 @@ __global__ void k_site_eval(plx_site_desc d) {
         break;
       default: c.role[4] = static_cast<int32_t>(s); break;  // EDGE
     }
-    c.cid_value = (d.kind == PLX_SITES_EDGE && d.cid_map) ? d.cid_map[s] : c.role[4];
+    c.cid_value = c.role[4];
+    if (d.site_ids) {
+      if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
+      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[s / per];
+    }
     c.ids_logical = d.ids_logical;
     c.ids_physical = d.ids_physical;
     c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
@@ -812,6 +816,102 @@ __global__ void k_mask_importance(int32_t n, const float* imp, const int32_t* le
   out[u] = ok ? imp[u] : -__builtin_huge_valf();
 }
 
+// ---------------------------------------------------------------------------
+// Unit lifecycle.
+// ---------------------------------------------------------------------------
+
+struct UnitCols {
+  plx_unit_col c[PLX_MAX_UNIT_COLS];
+  int32_t n;
+};
+
+__device__ __forceinline__ void unit_store(const plx_unit_col& col, int64_t u, uint32_t v) {
+  if (col.bytes == 1)
+    static_cast<uint8_t*>(col.ptr)[u] = v != 0u;
+  else
+    static_cast<uint32_t*>(col.ptr)[u] = v;
+}
+
+struct UnitOuts {
+  const uint32_t* o[PLX_MAX_UNIT_COLS];
+};
+
+__global__ void k_unit_write(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const uint8_t* skip,
+                             UnitCols cols, UnitOuts outs) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < n;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t u = idx ? idx[r] : r;
+    if (skip && skip[u]) continue;
+    for (int k = 0; k < cols.n; ++k) unit_store(cols.c[k], u, outs.o[k][r]);
+  }
+}
+
+__global__ void k_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const uint8_t* exempt,
+                             UnitCols cols, uint8_t* doomed, int32_t* count) {
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < n;
+       u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const bool d = selected[u] != 0u && !pruned[u] && !(exempt && exempt[u]);
+    doomed[u] = d;
+    if (!d) continue;
+    for (int k = 0; k < cols.n; ++k) unit_store(cols.c[k], u, cols.c[k].default_bits);
+    pruned[u] = 1;
+    if (count) atomicAdd(count, 1);
+  }
+}
+
+__global__ void k_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
+                                const uint8_t* doomed, const int32_t* id_map, int32_t* count) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int32_t a = from_id[p], b = to_id[p];
+    if (id_map) {
+      a = id_map[a];
+      b = id_map[b];
+    }
+    if ((doomed[a] || doomed[b]) && !dead[p]) {
+      dead[p] = 1;
+      if (count) atomicAdd(count, 1);
+    }
+  }
+}
+
+__global__ void k_unit_place(int64_t n_max, const int32_t* parents, const int32_t* nparents, const int32_t* free_ids,
+                             const int32_t* nfree, const int32_t* offset, int32_t* level, uint8_t* pruned,
+                             int32_t max_level, UnitCols cols, int32_t* child, int32_t* parent, int32_t* flags) {
+  const int64_t np = *nparents, nf = *nfree;
+  const int64_t placed = np < nf ? np : nf;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    flags[0] = static_cast<int32_t>(placed);
+    flags[1] = np > nf;
+  }
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < placed && r < n_max;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t p = parents[r], c = free_ids[r];
+    for (int k = 0; k < cols.n; ++k) unit_store(cols.c[k], c, cols.c[k].default_bits);
+    int32_t l = level[p] + offset[p];
+    l = l < 1 ? 1 : (l > max_level ? max_level : l);
+    level[c] = l;
+    pruned[c] = 0;
+    child[r] = c;
+    parent[r] = p;
+  }
+}
+
+bool unit_cols_ok(int32_t ncols, const plx_unit_col* cols) {
+  if (ncols < 0 || ncols > PLX_MAX_UNIT_COLS || (ncols > 0 && !cols)) return false;
+  for (int k = 0; k < ncols; ++k)
+    if (!cols[k].ptr || (cols[k].bytes != 1 && cols[k].bytes != 4)) return false;
+  return true;
+}
+
+UnitCols pack_cols(int32_t ncols, const plx_unit_col* cols) {
+  UnitCols u{};
+  u.n = ncols;
+  for (int k = 0; k < ncols; ++k) u.c[k] = cols[k];
+  return u;
+}
+
 bool prog_ok(const plx_site_prog& p) {
   if (p.ninstr < 0 || p.ninstr > PLX_MAX_SINSTR || p.nout < 0 || p.nout > PLX_MAX_SOUTS) return false;
   for (int k = 0; k < p.ninstr; ++k) {
@@ -1067,4 +1167,53 @@ int plx_mask_importance(int32_t n, const float* imp, const int32_t* level, const
   hipLaunchKernelGGL(k_mask_importance, dim3((n + kBlock - 1) / kBlock), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), n, imp, level, pruned, mode, b, gap, direction, out);
   return check_launch("plx_mask_importance");
+}
+
+int plx_unit_write(int64_t n, const int32_t* n_dev, const int32_t* idx, const uint8_t* skip, int32_t ncols,
+                   const plx_unit_col* cols, const uint32_t* const* outs, void* stream) {
+  if (n < 0 || !unit_cols_ok(ncols, cols)) return fail(PLX_ERR_INVALID, "plx_unit_write: bad columns");
+  if (n == 0 || ncols == 0) return PLX_OK;
+  if (!outs) return fail(PLX_ERR_INVALID, "plx_unit_write: null outputs");
+  UnitOuts o{};
+  for (int k = 0; k < ncols; ++k) {
+    if (!outs[k]) return fail(PLX_ERR_INVALID, "plx_unit_write: null output");
+    o.o[k] = outs[k];
+  }
+  hipLaunchKernelGGL(k_unit_write, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, n_dev,
+                     idx, skip, pack_cols(ncols, cols), o);
+  return check_launch("plx_unit_write");
+}
+
+int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const uint8_t* exempt, int32_t ncols,
+                   const plx_unit_col* cols, uint8_t* doomed, int32_t* doomed_count, void* stream) {
+  if (n < 0 || !unit_cols_ok(ncols, cols)) return fail(PLX_ERR_INVALID, "plx_unit_prune: bad columns");
+  if (n == 0) return PLX_OK;
+  if (!selected || !pruned || !doomed) return fail(PLX_ERR_INVALID, "plx_unit_prune: null pointer");
+  hipLaunchKernelGGL(k_unit_prune, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, selected,
+                     pruned, exempt, pack_cols(ncols, cols), doomed, doomed_count);
+  return check_launch("plx_unit_prune");
+}
+
+int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead, const uint8_t* doomed,
+                      const int32_t* id_map, int32_t* kill_count, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_kill_incident: negative n");
+  if (n == 0) return PLX_OK;
+  if (!from_id || !to_id || !dead || !doomed) return fail(PLX_ERR_INVALID, "plx_kill_incident: null pointer");
+  hipLaunchKernelGGL(k_kill_incident, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n,
+                     from_id, to_id, dead, doomed, id_map, kill_count);
+  return check_launch("plx_kill_incident");
+}
+
+int plx_unit_place(int64_t n_max, const int32_t* parents, const int32_t* nparents, const int32_t* free_ids,
+                   const int32_t* nfree, const int32_t* offset, int32_t* level, uint8_t* pruned, int32_t max_level,
+                   int32_t ncols, const plx_unit_col* cols, int32_t* child, int32_t* parent, int32_t* flags,
+                   void* stream) {
+  if (n_max < 0 || max_level < 1 || !unit_cols_ok(ncols, cols))
+    return fail(PLX_ERR_INVALID, "plx_unit_place: bad sizes or columns");
+  if (!parents || !nparents || !free_ids || !nfree || !offset || !level || !pruned || !child || !parent || !flags)
+    return fail(PLX_ERR_INVALID, "plx_unit_place: null pointer");
+  hipLaunchKernelGGL(k_unit_place, dim3(grid_for(n_max > 0 ? n_max : 1)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), n_max, parents, nparents, free_ids, nfree, offset, level, pruned,
+                     max_level, pack_cols(ncols, cols), child, parent, flags);
+  return check_launch("plx_unit_place");
 }

@@ -125,7 +125,7 @@ class Kernels:
                   occ: torch.Tensor | None = None, n_dev: torch.Tensor | None = None,
                   outs: list[torch.Tensor] | None = None, conns: Columns | None = None,
                   or_into: torch.Tensor | None = None, kill_count: torch.Tensor | None = None,
-                  cid_map: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
+                  site_ids: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
                   ids_physical: torch.Tensor | None = None) -> None:
         d = _lib.plx_site_desc()
         d.prog = fill_prog(sp, units, conns, globals_, physical_ids=ids_logical is not None)
@@ -137,7 +137,7 @@ class Kernels:
         for k, o in enumerate(outs or []):
             d.outs[k] = o.data_ptr()
         d.or_into = _ptr(or_into)
-        d.kill_count, d.cid_map = _ptr(kill_count), _ptr(cid_map)
+        d.kill_count, d.site_ids = _ptr(kill_count), _ptr(site_ids)
         d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
         self._begin("site_eval")
         _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
@@ -245,7 +245,7 @@ class PruneConnPhase:
             view = {name: col[base : base + cap] for name, col in arena.cols.items()}
             k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
                         conns=view, or_into=view["dead"], kill_count=kill_count,
-                        cid_map=arena.slot[base : base + cap], ids_logical=arena.uperm32,
+                        site_ids=arena.slot[base : base + cap], ids_logical=arena.uperm32,
                         ids_physical=arena.uinv32)
 
 

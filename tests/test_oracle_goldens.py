@@ -71,7 +71,8 @@ def test_golden_fixtures_are_all_consumed() -> None:
     names = {p.stem for p in nets.GOLDEN.glob("*.json")}
     growth = {p.stem for p in nets.GOLDEN.glob("grow_*.json")}
     assert growth == set(growth_cases.names(lambda d: True))  # test_growth_oracle.py
-    consumed = {"passes_relu_topological", "passes_relu_pipeline", *LOSS_GOLDENS, *growth}
+    units = {p.stem for p in nets.GOLDEN.glob("unit_*.json")}  # test_unit_oracle.py
+    consumed = {"passes_relu_topological", "passes_relu_pipeline", *LOSS_GOLDENS, *growth, *units}
     assert names == consumed
 
 
