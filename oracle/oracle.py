@@ -223,6 +223,7 @@ class OracleNet:
         self.grown = 0
         self.overflow = False
         self.units_added = 0
+        self.unit_overflow = False
         self._prune_prog: Any = None
         n = static.num_units
         self.is_input = np.zeros(n, dtype=bool)
@@ -395,12 +396,29 @@ class OracleNet:
             loss = np.float32(np.float32(0.0) + self.loss(targets))
         if self.plan.backward is not None:
             self.backward()
+        if getattr(self.plan, "update_unit", False):
+            self.update_unit()
         if self.plan.update is not None:
             self.update()
-        if getattr(self.plan, "prune_conn", False) or getattr(self.plan, "add_conn", None) is not None:
+        if (getattr(self.plan, "prune_unit", False) or getattr(self.plan, "prune_conn", False)
+                or getattr(self.plan, "add_unit", False) or getattr(self.plan, "add_conn", None) is not None):
             self.structural()
+        if getattr(self.plan, "reset_global", False):
+            self.globals_ = self.plan.net.reset_global.reset(self.globals_)
         self.step_count += 1
         return loss
+
+    def _unit_dtypes(self) -> dict[str, np.dtype]:
+        return {s.name: np.dtype(s.dtype) for s in self.static.unit_fields}
+
+    def update_unit(self) -> None:
+        """phases.py:1148-1193."""
+        from oracle import growth as og
+        from plastax_amd import _site
+
+        if not hasattr(self, "_uu"):
+            self._uu = _site.trace_update_unit(self.plan.net.update_unit, self._unit_dtypes(), self.globals_)
+        self.units = og.update_unit(self._uu[0], self._uu[1], self.units, self.globals_)
 
     def structural(self) -> None:
         """prune_conn then add_conn (phases.py:87-182 order) on the logical
@@ -415,10 +433,31 @@ class OracleNet:
         net = self.plan.net
         unit_dtypes = {s.name: np.dtype(s.dtype) for s in self.static.unit_fields}
         conn_dtypes = {s.name: np.dtype(s.dtype) for s in self.static.conn_fields}
+        if getattr(self.plan, "prune_unit", False):
+            if not hasattr(self, "_pu"):
+                self._pu = _site.trace_prune_unit(net.prune_unit, unit_dtypes, self.globals_)
+            self.units, self.conns, _ = og.prune_unit(self._pu, self.static, self.units, self.conns, self.globals_)
+            self.units = {k: np.ascontiguousarray(v) for k, v in self.units.items()}
+            self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in self.conns]
         if self.plan.prune_conn:
             if self._prune_prog is None:
                 self._prune_prog = _site.trace_predicate(net.prune_conn, unit_dtypes, conn_dtypes, self.globals_)
             self.conns = og.prune_conn(self._prune_prog, self.units, self.conns, self.globals_)
+        if getattr(self.plan, "add_unit", False):
+            interval = int(getattr(net, "structural_interval", 1))
+            if interval <= 1 or self.step_count % interval == 0:
+                if not hasattr(self, "_au"):
+                    spawn = _site.trace_spawn(net.add_unit, unit_dtypes, self.globals_)
+                    init, names = _site.trace_unit_init(net.add_unit, unit_dtypes, self.globals_)
+                    self._au = (spawn, init, names)
+                self.units, self.units_added, self.unit_overflow, _ = og.add_unit(
+                    *self._au, self.static, int(getattr(net, "max_levels", 1024)), self.units, self.globals_)
+                if self.units_added:
+                    # new units get rows when the arena is laid out again
+                    self._bwd_order = {}
+                    self._phys_index = None
+            else:
+                self.units_added, self.unit_overflow = 0, False
         if self.plan.add_conn is not None:
             res = og.add_conn(
                 net, self.static, self.units, self.conns, step=self.step_count, globals_=self.globals_,

@@ -67,9 +67,13 @@ class Plan:
     loss: LossPlan | None
     backward: PassPlan | None
     update: Any  # an optim _RuleBase or None
-    net: Any = None  # the Network class (its structural policies are traced lazily)
+    net: Any = None  # the Network class (its unit / structural policies are traced lazily)
+    update_unit: bool = False
+    prune_unit: bool = False
     prune_conn: bool = False
+    add_unit: bool = False
     add_conn: Any = None  # the validated GrowthConfig, or None
+    reset_global: bool = False
 
     def pow_table(self) -> np.ndarray:
         """float32(b1^t), float32(b2^t) for t < POW_TABLE_LEN, by binary
@@ -153,10 +157,17 @@ def _trace_loss(loss: Any, static: NetworkStatic) -> LossPlan:
 
 def compile_plan(net: type, static: NetworkStatic) -> Plan:
     """The device plan of ``net``'s streaming step."""
-    for slot in ("update_unit", "prune_unit", "add_unit", "reset_global"):
-        if getattr(net, slot, None) is not None:
-            raise UnsupportedPolicyError(f"{net.__name__}.{slot}: not in this build yet")
+    for slot, method in (("update_unit", "update"), ("prune_unit", "predicate"), ("prune_conn", "predicate")):
+        policy = getattr(net, slot, None)
+        if policy is not None and not callable(getattr(policy, method, None)):
+            raise TypeError(f"{net.__name__}.{slot} needs a {method} method")
     growth = GrowthConfig.of(net, static) if net.add_conn is not None else None
+    if net.add_unit is not None:
+        for name in ("spawn", "init"):
+            if not callable(getattr(net.add_unit, name, None)):
+                raise TypeError(f"{net.__name__}.add_unit needs a {name} method")
+    if net.reset_global is not None and not callable(getattr(net.reset_global, "reset", None)):
+        raise TypeError(f"{net.__name__}.reset_global needs a reset(g) method")
     forward = _trace_pass(net.forward_pass, static, backward=False)
     loss = _trace_loss(net.loss, static) if net.loss is not None else None
     backward = (
@@ -181,8 +192,10 @@ def compile_plan(net: type, static: NetworkStatic) -> Plan:
                     f"{net.__name__}: optimizer column {col!r} missing from extra_conn_fields"
                 )
         update = uc
-    return Plan(forward, loss, backward, update, net=net, prune_conn=net.prune_conn is not None,
-                add_conn=growth)
+    return Plan(forward, loss, backward, update, net=net, update_unit=net.update_unit is not None,
+                prune_unit=net.prune_unit is not None, prune_conn=net.prune_conn is not None,
+                add_unit=net.add_unit is not None, add_conn=growth,
+                reset_global=net.reset_global is not None)
 
 
 def program_struct(

@@ -102,9 +102,12 @@ class StepFn:
         # the arenas this step builds.
         self.tile: int = TILE
         self.nsuper: int = NSUPER
-        # Structural phases, traced on the first step (their programs read
-        # the globals' structure).
+        # Unit and structural phases, traced on the first step (their
+        # programs read the globals' structure).
+        self._update_unit: Any = None
+        self._prune_unit: Any = None
         self._prune: Any = None
+        self._add_unit: Any = None
         self._grow: Any = None
 
     def _launch(self, kind: str, fn: Any, *args: Any) -> None:
@@ -244,21 +247,37 @@ class StepFn:
         if plan.update is not None:
             state._arena_ahead = True
 
-        # Structural phases (phases.py:1444-1498, :4490-5203).
-        if plan.prune_conn or plan.add_conn is not None:
+        # Structural phases (phases.py:1245-1498, :4490-5203).
+        if plan.prune_unit or plan.prune_conn or plan.add_unit or plan.add_conn is not None:
             self._structural(state, arena, units, stream, g)
+        # reset_global (phases.py:87-182, last): the globals live on the host.
+        if plan.reset_global:
+            state.globals_ = plan.net.reset_global.reset(state.globals_)
 
         state.step = state.step + 1
         return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
 
     def _structural(self, state: NetworkState, arena: Arena, units: dict, stream: int, g: Any) -> None:
-        """PruneConn on the physical arena (tombstones set in place), then
-        add_conn on the logical arena; a growth that fired replaces the
-        logical buckets, and the next step lays the arena out again."""
-        from plastax_amd import grow
+        """prune_unit and PruneConn on the physical arena (tombstones set in
+        place), then add_unit and add_conn on the logical arena (the
+        caller's unit ids; slot order). New units or a growth that fired
+        replace the logical columns, and the next step lays the arena out
+        again."""
+        from plastax_amd import grow, units as unit_phases
 
         plan = self.plan
         k = grow.Kernels(state.device, stream)
+        if plan.prune_unit:
+            if self._prune_unit is None:
+                self._prune_unit = unit_phases.PruneUnitPhase(plan.net, self.static, g)
+            doomed, _ = self._prune_unit.run(k, units, g, site_ids=arena.uperm32, ids_physical=arena.uinv32)
+            kills = torch.zeros(1, dtype=torch.int32, device=state.device)
+            self._prune_unit.kill(k, arena.n_positions, arena.cols["from_id"], arena.cols["to_id"],
+                                  arena.cols["dead"], doomed, kills)
+            if int(kills.item()):
+                arena.materialize_t()
+                arena.dead_in_rows = True
+                state._arena_ahead = True
         if plan.prune_conn:
             if self._prune is None:
                 self._prune = grow.PruneConnPhase(plan.net, self.static, g)
@@ -273,6 +292,20 @@ class StepFn:
                 arena.materialize_t()
                 arena.dead_in_rows = True
                 state._arena_ahead = True
+        if plan.add_unit:
+            if self._add_unit is None:
+                self._add_unit = unit_phases.AddUnitPhase(plan.net, self.static, g)
+            phase_u = self._add_unit
+            if phase_u.fires(int(state.step)):
+                ulog = {name: col.clone() for name, col in state.units.items()}
+                added, unit_overflow = phase_u.run(k, ulog, g)
+                state.units_added, state.unit_overflow = added, unit_overflow
+                if added:
+                    # New units need rows in the layout: the arena is laid out again.
+                    state.conns = state.conns
+                state.units = ulog
+            else:
+                state.units_added, state.unit_overflow = 0, False
         if plan.add_conn is not None:
             if self._grow is None:
                 self._grow = grow.AddConnPhase(plan.net, self.static, g)
@@ -440,19 +473,33 @@ class StepFn:
                 self._tiles(plan, arena, units, consts, 0, True, False, stream)
                 self._partials(plan, arena.bwd[0], acc, prog, fin_common, -1, 0, stream)
             else:
-                fused = up is not None
+                # update_unit runs between the backward and update_conn
+                # (phases.py:87-182), so with one the passes are not fused.
+                fused = up is not None and not plan.update_unit
                 self._partials(plan, arena.top, acc, prog, fin_common, nb, 1, stream)
                 for b in range(nb - 1, 0, -1):
                     self._tiles(plan, arena, units, consts, b, True, fused, stream)
                     self._partials(plan, arena.bwd[b], acc, prog, fin_common, b, 1, stream)
             self._unshadow(units, swaps)
+        if plan.update_unit:
+            self._run_update_unit(arena, units, stream, g)
         if up is not None:
-            if bp is None or arena.pipeline:
+            if bp is None or arena.pipeline or plan.update_unit:
                 todo = range(nb)
             else:
                 todo = range(1)  # bucket 0 is never reduced, only updated
             for b in todo:
                 self._update_only(plan, arena, units, consts, b, stream)
+
+    def _run_update_unit(self, arena: Arena, units: dict, stream: int, g: Any) -> None:
+        """update_unit (phases.py:1148-1193) on the step's unit columns, in the
+        arena's unit order (the program sees the caller's ids)."""
+        from plastax_amd import grow, units as unit_phases
+
+        if self._update_unit is None:
+            self._update_unit = unit_phases.UpdateUnitPhase(self.plan.net, self.static, g)
+        k = grow.Kernels(arena.device, stream)
+        self._update_unit.run(k, units, g, site_ids=arena.uperm32, ids_physical=arena.uinv32)
 
     def _update_only(self, plan: Plan, arena: Arena, units: dict, consts: dict, b: int,
                      stream: int) -> None:

@@ -176,3 +176,99 @@ def test_growing_reservoir_propose_and_prune_bit_exact(oracle) -> None:
 
     _, o, grown = _run(Reservoir, static, state, oracle, inputs, globals_fn, 12, {1, 3, 7, 12})
     assert grown > 0
+
+
+TRACE = px.FieldSpec.float32("trace", 0.5)
+
+
+class DecayTrace(px.UpdateUnit):
+    def update(self, u, i, g):
+        return px.UnitWrite.of((TRACE, u[TRACE, i] * jnp.float32(0.75) + jnp.abs(u[px.ACTIVATION, i])))
+
+
+class PruneSaturated(px.PruneUnit):
+    def predicate(self, u, i, g):
+        return u[TRACE, i] > g["trace_max"]
+
+
+class SpawnCold(px.AddUnit):
+    def spawn(self, u, parent, g):
+        return u[TRACE, parent] < g["trace_min"], jnp.int32(1)
+
+    def init(self, u, child, parent, g):
+        return px.UnitWrite.of((px.ACTIVATION, u[px.ACTIVATION, parent] * jnp.float32(0.5)),
+                               (TRACE, jnp.float32(0.25)))
+
+
+@pytest.mark.parametrize("pipeline", [True, False])
+def test_full_churn_bit_exact(oracle, pipeline: bool) -> None:
+    """update_unit between the backward and the update, prune_unit with its
+    incident-edge kill, add_unit every 3rd step, PruneConn and growth:
+    device vs oracle every step."""
+    rng = np.random.default_rng(6 + pipeline)
+    opt = px.optim.adam(1e-2, nets.GRAD_PRE_ACT)
+    if pipeline:
+        n_alloc, cap = 1500, 2048
+        src = rng.integers(0, n_alloc, 9000).astype(np.int32)
+        dst = rng.integers(0, n_alloc, 9000).astype(np.int32)
+        keep = src != dst
+        src, dst = src[keep], dst[keep]
+        w = (rng.standard_normal(src.size) * 0.3).astype(np.float32)
+        ins, outs = np.arange(32), np.arange(n_alloc - 8, n_alloc)
+        grow_rule = Propose4()
+    else:
+        n_alloc, src, dst, w, ins, outs = _sparse_mlp(rng, [64, 200, 200, 10], 0.15)
+        cap = n_alloc + 200
+        grow_rule = GradGrow()
+
+    class Churn(px.Network):
+        forward_pass = nets.TanhForward()
+        backward_pass = nets.TanhBackward()
+        loss = nets.MSELoss()
+        update_conn = opt.update_conn()
+        update_unit = DecayTrace()
+        prune_unit = PruneSaturated()
+        prune_conn = TauPrune()
+        add_unit = SpawnCold()
+        add_conn = grow_rule
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD, TRACE)
+        extra_conn_fields = tuple(opt.state_fields)
+        unit_capacity = cap
+        structural_interval = 3
+        propagation = px.Propagation.PIPELINE if pipeline else px.Propagation.TOPOLOGICAL
+
+    g0 = {"tau": np.float32(0.0), "trace_max": np.float32(2.6), "trace_min": np.float32(0.3 if pipeline else 0.7)}
+    static, state = px.NetworkBuilder.from_edges(
+        Churn, n_alloc, src, dst, weights=w, input_ids=ins, output_ids=outs, globals_=g0,
+        capacity_headroom=1.0, device="cuda")
+    n_in, n_out = len(ins), len(outs)
+    teacher = rng.standard_normal((n_out, n_in)).astype(np.float32) * np.float32(0.3)
+    xs = rng.standard_normal((14, n_in)).astype(np.float32)
+
+    def inputs(k):
+        x = xs[k - 1]
+        return x, np.tanh(teacher @ x).astype(np.float32)
+
+    def globals_fn(k):
+        return {**g0, "tau": np.float32(0.004 * (k % 2))}
+
+    o = nets.oracle_for(oracle, Churn, static, state)
+    o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
+    step = px.make_step(Churn, static)
+    added = 0
+    for k in range(1, 13):
+        g = globals_fn(k)
+        state.globals_ = g
+        o.globals_ = g
+        x, t = inputs(k)
+        print(f"churn step {k} pipeline={pipeline}", flush=True)
+        res = step(state, px.StepInputs(x, t))
+        state = res.state
+        lo = o.step(x, t)
+        assert (state.units_added, state.unit_overflow, state.grown, state.overflow, state.tail_start) == (
+            o.units_added, o.unit_overflow, o.grown, o.overflow, o.tail_start), f"flags at step {k}"
+        added += state.units_added
+        torch.cuda.synchronize()
+        assert_same_state(static, state, o, f"step {k}")
+        assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at {k}"
+    assert added > 0

@@ -120,8 +120,30 @@ def test_unsupported_phases_fail_at_build() -> None:
     class Net(nets.ReluMlpNet):
         update_unit = object()
 
-    with pytest.raises(UnsupportedPolicyError):
+    with pytest.raises(TypeError):
         compile_plan(Net, _static(Net))
+
+    class Net2(nets.ReluMlpNet):
+        prune_conn = Pr()
+        update_conn = nets.px.optim.sgd(1e-2, nets.GRAD_PRE_ACT).update_conn()
+
+    plan = compile_plan(Net2, _static(Net2))
+    assert plan.prune_conn and not plan.update_unit
+
+    class Normal(px.ProposeAddConn):
+        proposals_per_proposer = 1
+        max_new_per_level = 1
+
+        def propose(self, u, i, j, g, rng):
+            return i, i, rng.normal()
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of()
+
+    from plastax_amd import _site
+
+    with pytest.raises(UnsupportedPolicyError):
+        _site.trace_propose(Normal(), "per_unit", {"activation": np.dtype(np.float32)}, {}, None)
 
 
 def test_register_reuse_keeps_long_programs_in_budget() -> None:
