@@ -84,21 +84,16 @@ class PruneUnitPhase:
         dtypes = {s.name: np.dtype(s.dtype) for s in static.unit_fields}
         self.prog = _site.trace_prune_unit(net.prune_unit, dtypes, globals_)
         self.names = _reset_names(static)
-        self._exempt: dict = {}
+        n = static.num_units
+        m = np.zeros(n, np.uint8)
+        m[np.asarray(tuple(static.input_ids) + tuple(static.output_ids), dtype=np.int64)] = 1
+        self._exempt_host = m
 
     def exempt(self, device: torch.device, order: torch.Tensor | None) -> torch.Tensor:
         """The input/output mask, in the caller's order or through ``order``
         (physical position -> caller's id)."""
-        key = (str(device), None if order is None else order.data_ptr())
-        if key not in self._exempt:
-            n = self.static.num_units
-            m = np.zeros(n, np.uint8)
-            m[np.asarray(tuple(self.static.input_ids) + tuple(self.static.output_ids), dtype=np.int64)] = 1
-            t = torch.from_numpy(m).to(device)
-            if order is not None:
-                t = t[order.long()].contiguous()
-            self._exempt = {key: t}
-        return self._exempt[key]
+        t = torch.from_numpy(self._exempt_host).to(device)
+        return t if order is None else t[order.long()].contiguous()
 
     def run(self, k: Kernels, units: Columns, globals_: Any, *, site_ids: torch.Tensor | None = None,
             ids_physical: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
