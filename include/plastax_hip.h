@@ -537,6 +537,12 @@ typedef struct plx_grow_claim_desc {
   const uint32_t* init_out[PLX_MAX_SOUTS];
   int32_t* flags;
   int32_t* scratch;
+  /* The same-step retry of an overflowing growth (phases.py:5206-5281):
+   * with growable_in set, winner q is growable iff growable_in[q] != 0 (no
+   * threshold or step cap: they were applied by the attempt). dropped_out
+   * (optional) gets 1 for every growable winner that found no slot. */
+  const int32_t* growable_in;
+  int32_t* dropped_out;
 } plx_grow_claim_desc;
 
 PLX_EXPORT int plx_grow_claim(const plx_grow_claim_desc* d, void* stream);
@@ -608,6 +614,25 @@ PLX_EXPORT int plx_unit_place(int64_t n_max, const int32_t* parents, const int32
                               int32_t* level, uint8_t* pruned, int32_t max_level, int32_t ncols,
                               const plx_unit_col* cols, int32_t* child, int32_t* parent, int32_t* flags,
                               void* stream);
+
+/* topo.resort (topo.py:189-452): one Bellman-Ford round of longest-path
+ * levels over the live edges: out = max(in, max over live (u -> v) of
+ * in[u] + 1), then (pin_inputs) every input back to 0; changed[0] = 1 when
+ * any level moved. `out` must start as a copy of `in` (plx_relax_levels
+ * copies it). */
+PLX_EXPORT int plx_relax_levels(int64_t n_units, int64_t n_edges, const int32_t* from_id,
+                                const int32_t* to_id, const uint8_t* dead, const int32_t* level_in,
+                                int32_t* level_out, const uint8_t* is_input, int32_t* changed,
+                                void* stream);
+
+/* Resort keys: key[p] = dead[p] ? sentinel : (pipeline ? 0 : level[from[p]]). */
+PLX_EXPORT int plx_resort_keys(int64_t n, const int32_t* from_id, const uint8_t* dead, const int32_t* level,
+                               int32_t pipeline, int32_t sentinel, int32_t* key, void* stream);
+
+/* Column gather: dst[p] = src[idx[p]] for p < n (count n_dev, optional),
+ * elements of `bytes` (1 or 4) bytes. */
+PLX_EXPORT int plx_gather_col(int64_t n, const int32_t* n_dev, const int32_t* idx, const void* src, void* dst,
+                              int32_t bytes, void* stream);
 
 /* importance masks for the shortlists (phases.py:3683-3746): out[u] = imp[u]
  * where (mode 0: level[u] == b; mode 1: |level[u] - b| <= gap with the

@@ -366,6 +366,7 @@ class GrowthResult:
     tail_start: int
     fired: bool
     winners: list[tuple[int, int]]  # (src, dst) of every committed edge, in claim order
+    remainder: Any = None  # (claims with growable = dropped, levels) for the retry
 
 
 def add_conn(
@@ -543,9 +544,11 @@ def add_conn(
 
     specs = {sp.name: sp for sp in static.conn_fields}
 
-    def values_of(b: int, where: np.ndarray) -> dict[str, np.ndarray]:
-        ts = claims[b]["src"][where].astype(np.int32)
-        td = claims[b]["dst"][where].astype(np.int32)
+    # init of every winner (the reference vmaps it over the whole selection,
+    # phases.py:4981), with field defaults for the columns init leaves alone
+    for c in claims:
+        ts = c["src"].astype(np.int32)
+        td = c["dst"].astype(np.int32)
         outs = site_eval(iprog_init, ts.size, {"src": ts, "dst": td}, units, globals_) if ts.size else [
             np.zeros(0) for _ in init_names
         ]
@@ -561,29 +564,48 @@ def add_conn(
                 vals[name] = outs[init_names.index(name)].astype(spec.dtype)
             else:
                 vals[name] = np.full(ts.size, spec.default, dtype=spec.dtype)
-        return vals
-
-    winners: list[tuple[int, int]] = []
-    if cfg.pipeline:
-        bucket, over, resort, new_tail = claim_pipeline(conns[0], claims[0], levels_of[0], level, tail_start, values_of)
-        new_conns = [bucket]
-        overflow = bool(over.any())
-        reassigning = bool(resort.any())
-        committed = [claims[0]["growable"] & ~over]
-        tail_start = new_tail
-    else:
-        new_conns, overs, resorts = claim_topological(conns, claims, values_of)
-        overflow = any(bool(o.any()) for o in overs)
-        reassigning = any(bool(r.any()) for r in resorts)
-        committed = [c["growable"] & ~o for c, o in zip(claims, overs)]
-    for c, m in zip(claims, committed):
-        winners.extend((int(a), int(b2)) for a, b2 in zip(c["src"][m], c["dst"][m]))
-    if overflow and cfg.on_overflow == "error":
+        c["values"] = vals
+    res = _claim(cfg, conns, claims, levels_of, level, tail_start)
+    if res.overflow and cfg.on_overflow == "error":
         raise RuntimeError(
             "add_conn overflow: selected candidates exceeded the free connection capacity"
         )
+    res.needs_resort = needs_resort or res.needs_resort
+    return res
+
+
+def _claim(cfg: GrowthConfig, conns: list[dict], claims: list[dict], levels_of: list[np.ndarray],
+           level: np.ndarray, tail_start: int) -> GrowthResult:
+    """The claim of every bucket's growable winners; the result keeps the
+    dropped ones as the remainder."""
+
+    def values_of(b: int, where: np.ndarray) -> dict[str, np.ndarray]:
+        return {name: v[where] for name, v in claims[b]["values"].items()}
+
+    if cfg.pipeline:
+        bucket, over, resort, new_tail = claim_pipeline(conns[0], claims[0], levels_of[0], level, tail_start, values_of)
+        new_conns = [bucket]
+        overs = [over]
+        reassigning = bool(resort.any())
+        tail_start = new_tail
+    else:
+        new_conns, overs, resorts = claim_topological(conns, claims, values_of)
+        reassigning = any(bool(r.any()) for r in resorts)
+    overflow = any(bool(o.any()) for o in overs)
+    committed = [c["growable"] & ~o for c, o in zip(claims, overs)]
+    winners: list[tuple[int, int]] = []
+    for c, m in zip(claims, committed):
+        winners.extend((int(a), int(b2)) for a, b2 in zip(c["src"][m], c["dst"][m]))
     grown = int(sum(int(m.sum()) for m in committed))
-    return GrowthResult(new_conns, grown, overflow, needs_resort or reassigning, tail_start, True, winners)
+    remainder = ([{**c, "growable": o} for c, o in zip(claims, overs)], levels_of)
+    return GrowthResult(new_conns, grown, overflow, reassigning, tail_start, True, winners, remainder)
+
+
+def retry(cfg: GrowthConfig, units: dict, conns: list[dict], remainder: Any, tail_start: int) -> GrowthResult:
+    """build_growth_retry (phases.py:5206-5281): the dropped winners claim the
+    (regrown) buckets' free slots with the values the phase computed."""
+    claims, levels_of = remainder
+    return _claim(cfg, conns, claims, levels_of, units["level"].astype(np.int64), tail_start)
 
 
 # ---------------------------------------------------------------------------
@@ -655,3 +677,91 @@ def add_unit(spawn: _site.SiteProgram, init: _site.SiteProgram, init_names: list
         for name, val in zip(init_names, outs):
             new[name][children] = val.astype(new[name].dtype)
     return new, int(placed), bool(parents.size > free_ids.size), children
+
+
+def grow_bucket(static: Any, conns: list[dict], level: int) -> tuple[Any, list[dict]]:
+    """grow_bucket (state.py:238-313) on host arrays."""
+    import dataclasses as _dc
+
+    from plastax_amd.topo import capacity_policy
+
+    old = int(static.level_capacities[level])
+    live = int((~conns[level]["dead"].astype(bool)).sum())
+    policy = capacity_policy(live + 1, headroom=static.capacity_headroom, align=static.capacity_align)
+    floor = old * 2 if static.capacity_align is None else capacity_policy(old + old // 2, align=static.capacity_align)
+    new_cap = max(policy, floor)
+    specs = {s.name: s for s in static.conn_fields}
+    out = [dict(b) for b in conns]
+    out[level] = {
+        name: np.concatenate([col, np.full(new_cap - old, specs[name].default, dtype=col.dtype)])
+        for name, col in conns[level].items()
+    }
+    caps = tuple(new_cap if b == level else c for b, c in enumerate(static.level_capacities))
+    return _dc.replace(static, level_capacities=caps), out
+
+
+# ---------------------------------------------------------------------------
+# topo.resort (topo.py:189-452) on host arrays.
+# ---------------------------------------------------------------------------
+
+
+def relax_levels(static: Any, conns: list[dict], *, pin_inputs: bool, rounds: int) -> tuple[np.ndarray, bool]:
+    """Longest-path relaxation over the live edges from all-zero levels, for
+    at most ``rounds`` Jacobi rounds; returns (levels, converged)."""
+    n = static.num_units
+    frm = np.concatenate([b["from_id"] for b in conns]).astype(np.int64)
+    to = np.concatenate([b["to_id"] for b in conns]).astype(np.int64)
+    live = ~np.concatenate([b["dead"] for b in conns]).astype(bool)
+    frm, to = frm[live], to[live]
+    inputs = np.asarray(static.input_ids, dtype=np.int64)
+    level = np.zeros(n, dtype=np.int64)
+    for _ in range(rounds):
+        new = level.copy()
+        np.maximum.at(new, to, level[frm] + 1)
+        if pin_inputs and inputs.size:
+            new[inputs] = 0
+        if np.array_equal(new, level):
+            return level.astype(np.int32), True
+        level = new
+    return level.astype(np.int32), False
+
+
+def resort(static: Any, units: dict, conns: list[dict]) -> tuple[Any, dict, list[dict], int]:
+    """topo.resort: (static, units, conns, tail_start) after recomputing the
+    levels and regrouping the live edges by source level, old relative order
+    kept, then stably by source."""
+    import dataclasses as _dc
+
+    from plastax_amd.topo import capacity_policy
+
+    n = static.num_units
+    pipeline = static.propagation.value == "pipeline"
+    if not pipeline:
+        _, converged = relax_levels(static, conns, pin_inputs=False, rounds=n)
+        if not converged:
+            raise ValueError("resort: topological propagation requires an acyclic graph; the live connections "
+                             "contain a cycle")
+    depth = static.kahn_max_depth if static.kahn_max_depth is not None else n
+    level, _ = relax_levels(static, conns, pin_inputs=True, rounds=depth)
+    flat = {name: np.concatenate([b[name] for b in conns]) for name in conns[0]}
+    dead = flat["dead"].astype(bool)
+    bucket_of = level[flat["from_id"].astype(np.int64)]
+    nb = 1 if pipeline else max(int(level.max(initial=0)) + (1 if static.deepest_grows else 0), 1)
+    specs = {s.name: s for s in static.conn_fields}
+    caps, out = [], []
+    for b in range(nb):
+        pick = np.flatnonzero(~dead if pipeline else (~dead) & (bucket_of == b))
+        pick = pick[np.argsort(flat["from_id"][pick], kind="stable")]
+        old = static.level_capacities[b] if b < len(static.level_capacities) else 0
+        cap = max(capacity_policy(pick.size, headroom=static.capacity_headroom, align=static.capacity_align), old)
+        caps.append(cap)
+        cols = {}
+        for name, spec in specs.items():
+            col = np.full(cap, spec.default, dtype=flat[name].dtype)
+            col[: pick.size] = flat[name][pick]
+            cols[name] = col
+        out.append(cols)
+    new_units = {k: v.copy() for k, v in units.items()}
+    new_units["level"] = level.astype(units["level"].dtype)
+    tail = int((~dead).sum()) if pipeline else 0
+    return _dc.replace(static, level_capacities=tuple(caps)), new_units, out, tail

@@ -224,6 +224,7 @@ class OracleNet:
         self.overflow = False
         self.units_added = 0
         self.unit_overflow = False
+        self.remainder: Any = None
         self._prune_prog: Any = None
         n = static.num_units
         self.is_input = np.zeros(n, dtype=bool)
@@ -464,6 +465,7 @@ class OracleNet:
                 tail_start=self.tail_start, units_added=self.units_added, needs_resort=self.needs_resort,
             )
             self.grown, self.overflow = res.grown, res.overflow
+            self.remainder = res.remainder
             if res.fired:
                 self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in res.conns]
                 self.needs_resort = res.needs_resort
@@ -490,3 +492,51 @@ def nth_free_slots(dead: np.ndarray, n: int) -> np.ndarray:
     out = np.zeros(n, dtype=np.int64)
     lib.ox_nth_free_slots(d.size, bptr(d), n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)))
     return out
+
+
+class OracleDriver:
+    """The reference Driver's step loop (driver.py:134-168, :319-338) over
+    an OracleNet: complete an overflowing growth (grow every full bucket,
+    retry the dropped winners), then resort a TOPOLOGICAL net whose flag is
+    raised. Every change of the arena's shape lays it out again."""
+
+    def __init__(self, net: OracleNet) -> None:
+        self.o = net
+
+    def _relayout(self) -> None:
+        self.o._bwd_order = {}
+        self.o._phys_index = None
+
+    def _free(self, level: int) -> int:
+        o = self.o
+        cap = int(o.static.level_capacities[level])
+        if o.pipeline:
+            return cap - int(o.tail_start)
+        return cap - int((~o.conns[level]["dead"].astype(bool)).sum())
+
+    def step(self, inputs: Any, targets: Any = None) -> np.float32:
+        from oracle import growth as og
+        from plastax_amd.growth_config import GrowthConfig
+
+        o = self.o
+        loss = o.step(inputs, targets)
+        while o.overflow:
+            for level in range(len(o.static.level_capacities)):
+                if self._free(level) == 0:
+                    o.static, o.conns = og.grow_bucket(o.static, o.conns, level)
+            cfg = GrowthConfig.of(o.plan.net, o.static)
+            res = og.retry(cfg, o.units, o.conns, o.remainder, o.tail_start)
+            o.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in res.conns]
+            o.grown += res.grown
+            o.overflow = res.overflow
+            o.needs_resort = o.needs_resort or res.needs_resort
+            o.tail_start = res.tail_start
+            o.remainder = res.remainder
+            self._relayout()
+        if not o.pipeline and o.needs_resort:
+            o.static, o.units, o.conns, o.tail_start = og.resort(o.static, o.units, o.conns)
+            o.units = {k: np.ascontiguousarray(v) for k, v in o.units.items()}
+            o.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in o.conns]
+            o.needs_resort = False
+            self._relayout()
+        return loss

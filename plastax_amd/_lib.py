@@ -297,6 +297,8 @@ class plx_grow_claim_desc(ctypes.Structure):
         ("init_out", c_vp * PLX_MAX_SOUTS),
         ("flags", c_vp),
         ("scratch", c_vp),
+        ("growable_in", c_vp),
+        ("dropped_out", c_vp),
     ]
 
 
@@ -337,6 +339,9 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_level_counts": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_bucket_free": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_mask_importance": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "plx_relax_levels": (c_i32, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_resort_keys": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp]),
+    "plx_gather_col": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),

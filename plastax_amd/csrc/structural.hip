@@ -638,6 +638,11 @@ __global__ void k_claim_growable(plx_grow_claim_desc d, int32_t* g) {
   const int64_t n = live_count(d.n_max, d.n_dev);
   for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n;
        q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (d.dropped_out) d.dropped_out[q] = 0;
+    if (d.growable_in) {
+      g[q] = d.growable_in[q] != 0;
+      continue;
+    }
     const float f = d.score[d.winners[q]];
     bool ok = (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u;
     if (d.has_threshold) ok = ok && f >= d.threshold;
@@ -704,6 +709,7 @@ __global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int
     }
     if (slot < 0) {
       atomicOr(&d.flags[1], 1);
+      if (d.dropped_out) d.dropped_out[q] = 1;
       continue;
     }
     atomicAdd(&d.flags[0], 1);
@@ -898,6 +904,47 @@ __global__ void k_unit_place(int64_t n_max, const int32_t* parents, const int32_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Resort.
+// ---------------------------------------------------------------------------
+
+__global__ void k_relax_edges(int64_t n, const int32_t* from_id, const int32_t* to_id, const uint8_t* dead,
+                              const int32_t* level_in, int32_t* level_out) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (dead[p]) continue;
+    atomicMax(&level_out[to_id[p]], level_in[from_id[p]] + 1);
+  }
+}
+
+__global__ void k_pin_compare(int64_t n, const int32_t* level_in, int32_t* level_out, const uint8_t* is_input,
+                              int32_t* changed) {
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < n;
+       u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (is_input && is_input[u]) level_out[u] = 0;
+    if (level_out[u] != level_in[u]) atomicOr(changed, 1);
+  }
+}
+
+__global__ void k_resort_keys(int64_t n, const int32_t* from_id, const uint8_t* dead, const int32_t* level,
+                              int32_t pipeline, int32_t sentinel, int32_t* key) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    key[p] = dead[p] ? sentinel : (pipeline ? 0 : level[from_id[p]]);
+}
+
+__global__ void k_gather_col(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const void* src, void* dst,
+                             int32_t bytes) {
+  const int64_t n = live_count(n_max, n_dev);
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (bytes == 1)
+      static_cast<uint8_t*>(dst)[p] = static_cast<const uint8_t*>(src)[idx[p]];
+    else
+      static_cast<uint32_t*>(dst)[p] = static_cast<const uint32_t*>(src)[idx[p]];
+  }
+}
+
 bool unit_cols_ok(int32_t ncols, const plx_unit_col* cols) {
   if (ncols < 0 || ncols > PLX_MAX_UNIT_COLS || (ncols > 0 && !cols)) return false;
   for (int k = 0; k < ncols; ++k)
@@ -1089,7 +1136,7 @@ int plx_grow_claim(const plx_grow_claim_desc* d, void* stream) {
   const int grid = grid_for(n);
   hipLaunchKernelGGL(k_claim_growable, dim3(grid), dim3(kBlock), 0, s, *d, g);
   int32_t* grow = g;
-  if (d->max_new_per_step > 0) {
+  if (d->max_new_per_step > 0 && !d->growable_in) {
     int rc = scan_or_compact(n, d->n_dev, -1, g, scan, nullptr, ss, s, "plx_grow_claim");
     if (rc != PLX_OK) return rc;
     hipLaunchKernelGGL(k_claim_cap, dim3(grid), dim3(kBlock), 0, s, *d, g, scan, g2);
@@ -1216,4 +1263,40 @@ int plx_unit_place(int64_t n_max, const int32_t* parents, const int32_t* nparent
                      static_cast<hipStream_t>(stream), n_max, parents, nparents, free_ids, nfree, offset, level, pruned,
                      max_level, pack_cols(ncols, cols), child, parent, flags);
   return check_launch("plx_unit_place");
+}
+
+int plx_relax_levels(int64_t n_units, int64_t n_edges, const int32_t* from_id, const int32_t* to_id,
+                     const uint8_t* dead, const int32_t* level_in, int32_t* level_out, const uint8_t* is_input,
+                     int32_t* changed, void* stream) {
+  if (n_units < 1 || n_edges < 0) return fail(PLX_ERR_INVALID, "plx_relax_levels: bad sizes");
+  if (!level_in || !level_out || !changed || (n_edges > 0 && (!from_id || !to_id || !dead)))
+    return fail(PLX_ERR_INVALID, "plx_relax_levels: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_copy_i32, dim3(grid_for(n_units)), dim3(kBlock), 0, s, n_units, level_in, level_out);
+  if (n_edges > 0)
+    hipLaunchKernelGGL(k_relax_edges, dim3(grid_for(n_edges)), dim3(kBlock), 0, s, n_edges, from_id, to_id, dead,
+                       level_in, level_out);
+  hipLaunchKernelGGL(k_pin_compare, dim3(grid_for(n_units)), dim3(kBlock), 0, s, n_units, level_in, level_out,
+                     is_input, changed);
+  return check_launch("plx_relax_levels");
+}
+
+int plx_resort_keys(int64_t n, const int32_t* from_id, const uint8_t* dead, const int32_t* level, int32_t pipeline,
+                    int32_t sentinel, int32_t* key, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_resort_keys: negative n");
+  if (n == 0) return PLX_OK;
+  if (!from_id || !dead || !level || !key) return fail(PLX_ERR_INVALID, "plx_resort_keys: null pointer");
+  hipLaunchKernelGGL(k_resort_keys, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, from_id,
+                     dead, level, pipeline, sentinel, key);
+  return check_launch("plx_resort_keys");
+}
+
+int plx_gather_col(int64_t n, const int32_t* n_dev, const int32_t* idx, const void* src, void* dst, int32_t bytes,
+                   void* stream) {
+  if (n < 0 || (bytes != 1 && bytes != 4)) return fail(PLX_ERR_INVALID, "plx_gather_col: bad size");
+  if (n == 0) return PLX_OK;
+  if (!idx || !src || !dst) return fail(PLX_ERR_INVALID, "plx_gather_col: null pointer");
+  hipLaunchKernelGGL(k_gather_col, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, n_dev,
+                     idx, src, dst, bytes);
+  return check_launch("plx_gather_col");
 }

@@ -184,6 +184,24 @@ class Kernels:
 
 
 @dataclasses.dataclass
+class Remainder:
+    """A growth phase's winners on the device, kept for its same-step retry
+    (the reference's GrowthRemainder, phases.py:2776-2816): the winner list
+    (level-major, count in ``nwin``), the candidate columns it indexes, the
+    init values of every winner, and which growable winners found no slot."""
+
+    nc: int
+    winners: torch.Tensor
+    nwin: torch.Tensor
+    src: torch.Tensor
+    dst: torch.Tensor
+    score: torch.Tensor
+    init_outs: list[torch.Tensor]
+    dropped: torch.Tensor
+    nseg: int
+
+
+@dataclasses.dataclass
 class GrowthOutcome:
     conns: tuple[Columns, ...]
     grown: int
@@ -271,6 +289,7 @@ class AddConnPhase:
             self.cand_prog = _site.trace_score(self.ac, unit_dtypes, globals_)
         self.imp_prog = _site.trace_importance(self.ac, unit_dtypes, globals_) if cfg.shortlist else None
         self.init_prog, self.init_names = _site.trace_init(self.ac, unit_dtypes, static.conn_fields, globals_)
+        self.remainder: Remainder | None = None
 
     # -- helpers ---------------------------------------------------------------
     def _top_units(self, k: Kernels, masked: torch.Tensor, m: int, n: int) -> torch.Tensor:
@@ -433,13 +452,39 @@ class AddConnPhase:
                         list_a=wsrc, list_b=wdst, n_dev=nwin, outs=init_outs)
 
         # 6. claim and write
-        c = _lib.plx_grow_claim_desc()
-        c.n_max, c.n_dev, c.winners = nc, nwin.data_ptr(), winners.data_ptr()
-        c.src, c.dst, c.score, c.level = src.data_ptr(), dst.data_ptr(), score.data_ptr(), level.data_ptr()
-        c.pipeline, c.num_buckets, c.num_levels = int(cfg.pipeline), nb, nseg
+        threshold = None
         if cfg.selection == "threshold":
+            threshold = float(np.float32(np.asarray(self.ac.threshold(globals_))))
+        rem = Remainder(nc, winners, nwin, src, dst, score, init_outs, k.mem.i32(nc), nseg)
+        self.remainder = rem
+        return self._claim(k, level, conns, flat, offs, tail_start, rem, threshold=threshold)
+
+    def retry(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], *, tail_start: int) -> GrowthOutcome:
+        """Claim the winners the last phase dropped into ``conns`` (its buckets
+        regrown by the caller), with the values that phase computed, in the
+        total order (build_growth_retry, phases.py:5206-5281). No other
+        stage re-runs; ``grown`` counts only this claim's commits."""
+        rem = self.remainder
+        if rem is None:
+            raise RuntimeError("retry: the last add_conn phase left no remainder")
+        flat, offs = flatten(conns)
+        growable = rem.dropped.clone()
+        return self._claim(k, units["level"], conns, flat, offs, tail_start, rem, growable_in=growable)
+
+    def _claim(self, k: Kernels, level: torch.Tensor, conns: tuple[Columns, ...], flat: Columns, offs: list[int],
+               tail_start: int, rem: "Remainder", *, threshold: float | None = None,
+               growable_in: torch.Tensor | None = None) -> GrowthOutcome:
+        cfg = self.cfg
+        n, nb, nc, nseg = cfg.num_units, cfg.num_buckets, rem.nc, rem.nseg
+        total_slots = offs[-1]
+        dev = level.device
+        c = _lib.plx_grow_claim_desc()
+        c.n_max, c.n_dev, c.winners = nc, rem.nwin.data_ptr(), rem.winners.data_ptr()
+        c.src, c.dst, c.score, c.level = rem.src.data_ptr(), rem.dst.data_ptr(), rem.score.data_ptr(), level.data_ptr()
+        c.pipeline, c.num_buckets, c.num_levels = int(cfg.pipeline), nb, nseg
+        if threshold is not None:
             c.has_threshold = 1
-            c.threshold = float(np.float32(np.asarray(self.ac.threshold(globals_))))
+            c.threshold = threshold
         c.max_new_per_step = int(cfg.max_new_per_step or 0)
         c.capacity, c.tail_start = total_slots, int(tail_start)
         keep: list[torch.Tensor] = []
@@ -482,11 +527,12 @@ class AddConnPhase:
                 gc.default_bits = _default_bits(spec)
             ncols += 1
         c.ncols = ncols
-        for j, o in enumerate(init_outs):
+        for j, o in enumerate(rem.init_outs):
             c.init_out[j] = o.data_ptr()
         flags = torch.zeros(4, dtype=torch.int32, device=dev)
         scratch = k.mem.i32(8 * nc + int(k.lib.plx_scratch_ints(nc)))
         c.flags, c.scratch = flags.data_ptr(), scratch.data_ptr()
+        c.growable_in, c.dropped_out = _ptr(growable_in), rem.dropped.data_ptr()
         _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
         got = flags.cpu().tolist()  # the phase's one host read (synchronises the stream)
         if bool(got[1]) and cfg.on_overflow == "error":

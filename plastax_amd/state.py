@@ -245,3 +245,43 @@ def live_unit_count(state: NetworkState) -> int:
     if live is None:
         return int(next(iter(state.units.values())).shape[0])
     return int(live.sum())
+
+
+def grow_bucket(static: NetworkStatic, state: NetworkState, level: int) -> tuple[NetworkStatic, NetworkState]:
+    """Pad one bucket with never-used (DEAD, default) slots (state.py:238-313).
+
+    The new capacity is ``max(capacity_policy(live + 1), floor)`` with the
+    floor twice the old capacity (1.5x, aligned, under ``capacity_align``),
+    so repeated overflows cost O(log) regrows. In PIPELINE mode the padding
+    extends the never-used tail; ``tail_start`` stays. The state's buffers
+    are handed to the returned state (the old one is retired).
+    """
+    import dataclasses as _dc
+
+    from plastax_amd.topo import capacity_policy
+
+    conns = state.conns  # logical columns, synchronised from the device arena
+    old = int(static.level_capacities[level])
+    live = int((conns[level]["dead"] == 0).sum())
+    policy = capacity_policy(live + 1, headroom=static.capacity_headroom, align=static.capacity_align)
+    if static.capacity_align is None:
+        floor = old * 2
+    else:
+        floor = capacity_policy(old + old // 2, align=static.capacity_align)
+    new_cap = max(policy, floor)
+    pad = new_cap - old
+    specs = {s.name: s for s in static.conn_fields}
+    grown = {}
+    for name, col in conns[level].items():
+        fill = to_column(np.full((pad,), specs[name].default, dtype=specs[name].dtype), specs[name], col.device)
+        grown[name] = torch.cat([col, fill])
+    new_conns = tuple(grown if b == level else dict(c) for b, c in enumerate(conns))
+    caps = tuple(new_cap if b == level else c for b, c in enumerate(static.level_capacities))
+    new_static = _dc.replace(static, level_capacities=caps)
+    units = state.units
+    new_state = NetworkState(
+        dict(units), new_conns, state.globals_, state.needs_resort, state.step, state.grown,
+        state.overflow, state.units_added, state.unit_overflow, state.tail_start,
+    )
+    state._donated = True
+    return new_static, new_state

@@ -15,6 +15,11 @@ import pytest
 
 import growth_cases as gc
 from oracle import growth as og
+from plastax_amd.growth_config import GrowthConfig
+
+
+def whole_grown(doc: dict) -> int:
+    return int(doc["step_growth"]["expect"]["grown"])
 
 
 def _grow(hn: gc.HostNet) -> og.GrowthResult:
@@ -87,6 +92,19 @@ def test_claim_topological_golden(name: str) -> None:
     assert res.needs_resort == expect["needs_resort"]
     full = [b for b, conns in enumerate(res.conns) if not conns["dead"].any()]
     assert full == expect["regrow_levels"]
+
+    # The Driver's regrow and the same-step retry of the dropped winners.
+    static, conns = hn.static, res.conns
+    for lvl in full:
+        static, conns = og.grow_bucket(static, conns, lvl)
+    retry = doc["retry"]
+    conns = gc.pin_free(conns, doc["initial_units"], {int(k): v for k, v in retry["free_per_level"].items()})
+    r2 = og.retry(GrowthConfig.of(hn.net, static), hn.units, conns, res.remainder, hn.tail_start)
+    assert gc.grown_pairs(conns, r2.conns) == gc.want_commits(retry["expect"])
+    assert r2.overflow == retry["expect"]["conn_overflow"]
+    assert not any(c["growable"].any() for c in r2.remainder[0])
+    assert res.grown + r2.grown == whole_grown(doc)
+    assert (res.needs_resort or r2.needs_resort) == (expect["needs_resort"] or retry["expect"]["needs_resort"])
 
     whole = doc["step_growth"]
     step_free = {int(k): v for k, v in whole["free_per_level"].items()}
