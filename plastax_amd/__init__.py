@@ -28,10 +28,13 @@ from plastax_amd._types import (
     UnitIdx,
 )
 from plastax_amd.builder import NetworkBuilder
+from plastax_amd.driver import Driver
+from plastax_amd.growth_config import predicate_add_conn
 from plastax_amd.monoid import Monoid, UnsupportedMonoidError
 from plastax_amd.state import (
     NetworkState,
     NetworkStatic,
+    grow_bucket,
     live_conn_count,
     live_unit_count,
     live_unit_mask,
@@ -68,6 +71,7 @@ __all__ = [
     "AddUnit",
     "BackwardPass",
     "BatchReduction",
+    "Driver",
     "ConnIdx",
     "ConnView",
     "ConnWrite",
@@ -98,6 +102,7 @@ __all__ = [
     "UnsupportedPolicyError",
     "UpdateConn",
     "UpdateUnit",
+    "grow_bucket",
     "live_conn_count",
     "live_unit_count",
     "live_unit_mask",
@@ -107,6 +112,7 @@ __all__ = [
     "nn",
     "numpy",
     "optim",
+    "predicate_add_conn",
     "rng",
     "topo",
 ]

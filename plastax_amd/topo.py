@@ -79,3 +79,11 @@ def capacity_policy(
         return min_bucket
     next_pow2 = 1 << (target - 1).bit_length()
     return max(next_pow2, min_bucket)
+
+
+def resort(static, state):  # noqa: ANN001, ANN201 -- mirrors topo.resort
+    """Recompute levels and lay the buckets out again on the device
+    (topo.py:303-452); see plastax_amd.resort."""
+    from plastax_amd.resort import resort as _resort
+
+    return _resort(static, state)
