@@ -289,7 +289,7 @@ PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
  * b at [off_b, off_b + cap_b)), unit ids in the caller's numbering.
  * ======================================================================== */
 
-#define PLX_MAX_SINSTR 96
+#define PLX_MAX_SINSTR 160
 #define PLX_MAX_SCONST 32
 #define PLX_MAX_SFIELDS 8
 #define PLX_MAX_SOUTS 8

@@ -25,7 +25,7 @@ PLX_MAX_CONST = 32
 PLX_MAX_FIELDS = 8
 PLX_MAX_OUTS = 4
 PLX_MAX_TBL = 8192
-PLX_MAX_SINSTR = 96
+PLX_MAX_SINSTR = 160
 PLX_MAX_SCONST = 32
 PLX_MAX_SFIELDS = 8
 PLX_MAX_SOUTS = 8

@@ -57,7 +57,7 @@ SOP = {
 ROLES = {"i": 0, "j": 1, "src": 2, "dst": 3, "cid": 4}
 KIND_CODE = {"f": 0, "i": 1, "u": 2, "b": 3}
 MAX_SREGS = 32
-MAX_SINSTR = 96
+MAX_SINSTR = 160
 MAX_SCONST = 32
 MAX_SFIELDS = 8
 MAX_SOUTS = 8

@@ -959,6 +959,9 @@ UnitCols pack_cols(int32_t ncols, const plx_unit_col* cols) {
   return u;
 }
 
+// Descriptors travel by value as kernel arguments (4 KB at most).
+static_assert(sizeof(plx_site_desc) <= 3584, "plx_site_desc must fit the kernel-argument segment");
+
 bool prog_ok(const plx_site_prog& p) {
   if (p.ninstr < 0 || p.ninstr > PLX_MAX_SINSTR || p.nout < 0 || p.nout > PLX_MAX_SOUTS) return false;
   for (int k = 0; k < p.ninstr; ++k) {
