@@ -290,78 +290,102 @@ __device__ __forceinline__ void gather_k(const float* tbl, const float* x, int b
 }
 
 // ---------------------------------------------------------------------------
-// Forward: kFwdRows rows (destination units) per workgroup, one row per lane
-// of the first kFwdRows lanes. The rows own a contiguous physical range; the
-// whole workgroup streams it through LDS in windows of kFwdWin terms with
-// 16-byte loads of FROM_ID and WEIGHT (map = weight * x[src]), and each row's
-// lane folds its terms from LDS in slot order, carrying the running value
-// across windows, so the fold order is the slot order for any row length.
-// Row ranges cover live positions only; DEAD is read only when the caller
-// passes it (a bucket with tombstones inside its rows).
+// Forward: rows (destination units) are cut into blocks of kFwdRows, one row
+// per lane of the first kFwdRows lanes. Each workgroup of a persistent grid
+// (kFwdPerCU per CU) takes a contiguous run of blocks, whose positions are
+// contiguous too, and streams them through LDS in windows of kFwdWin terms
+// with 16-byte loads of FROM_ID and WEIGHT (map = weight * x[src], table hits
+// read LDS). Each row's lane folds its terms from LDS in slot order, carrying
+// the running value across windows, so the fold order is the slot order for
+// any row length. The next window's loads (at a block's end, the next
+// block's first window) are issued before the current window is folded, so
+// the fold and the row finalize never leave the memory system idle. Row
+// ranges cover live positions only; DEAD is read only when the caller passes
+// it (a bucket with tombstones inside its rows).
 // ---------------------------------------------------------------------------
-constexpr int kFwdBlock = 256;
+#ifndef PLX_FWD_BLOCK
+#define PLX_FWD_BLOCK 512
+#endif
 #ifndef PLX_FWD_ROWS
-#define PLX_FWD_ROWS 128
+#define PLX_FWD_ROWS 256
 #endif
 #ifndef PLX_FWD_TBL
-#define PLX_FWD_TBL 1024
+#define PLX_FWD_TBL 8192
 #endif
-constexpr int kFwdTbl = PLX_FWD_TBL;  // the forward's workgroups are small: a short table
-constexpr int kFwdRows = PLX_FWD_ROWS;
 #ifndef PLX_FWD_QUADS
-#define PLX_FWD_QUADS 4
+#define PLX_FWD_QUADS 2
 #endif
+#ifndef PLX_FWD_PER_CU
+#define PLX_FWD_PER_CU 2
+#endif
+constexpr int kFwdBlock = PLX_FWD_BLOCK;
+constexpr int kFwdRows = PLX_FWD_ROWS;  // rows per block, one lane each
+static_assert(kFwdRows <= kFwdBlock, "a block's rows need a lane each");
+constexpr int kFwdTbl = PLX_FWD_TBL;
 constexpr int kFwdQuads = PLX_FWD_QUADS;  // 16-byte quads per thread per window
 constexpr int kFwdWin = 4 * kFwdQuads * kFwdBlock;
+constexpr int kFwdPerCU = PLX_FWD_PER_CU;  // workgroups per CU in the persistent grid
 
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   __shared__ __align__(16) float buf[kFwdWin];
   __shared__ float tbl[kFwdTbl > 0 ? kFwdTbl : 1];
+  const int nblk = (d.nrows + kFwdRows - 1) / kFwdRows;
+  const int b0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * nblk / gridDim.x);
+  const int b1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * nblk / gridDim.x);
+  if (b0 >= b1) return;  // uniform over the workgroup
   const int tlen = kFwdTbl > 0 ? min(d.tbl_len, kFwdTbl) : 0;
-  stage_table<kFwdBlock, (kFwdTbl > 0 ? kFwdTbl : 1)>(tbl, d.x, d.tbl_base, tlen);
-  __syncthreads();
-  const int row0 = blockIdx.x * kFwdRows;
-  const int rend = min(row0 + kFwdRows, d.nrows);
-  const int e_begin = d.row_ptr[row0];
-  const int e_end = d.row_ptr[rend];
-  const int r = row0 + static_cast<int>(threadIdx.x);
-  const bool has = threadIdx.x < kFwdRows && r < rend;
-  const int my_b = has ? d.row_ptr[r] : 0;
-  const int my_e = has ? d.row_ptr[r + 1] : 0;
-  RowPre pre;
-  if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
   const float ident = Mono<M>::id();
-  float s = ident;
-  for (int w0 = e_begin & ~3; w0 < e_end; w0 += kFwdWin) {
-    const int wn = min(kFwdWin, e_end - w0);
-    // Issue every load of the window before using any of them.
-    int4 sv[kFwdQuads];
-    float4 wv[kFwdQuads];
-    uint32_t dv[kFwdQuads];
+  auto row_end = [&](int blk) { return d.row_ptr[min((blk + 1) * kFwdRows, d.nrows)]; };
+
+  // The window in flight: positions [cw, cw + kFwdWin) of block cb, whose
+  // rows own [eb, ee); ee_next is the following block's end.
+  int cb = b0;
+  int eb = d.row_ptr[cb * kFwdRows];
+  int ee = row_end(cb);
+  int ee_next = cb + 1 < b1 ? row_end(cb + 1) : ee;
+  int cw = eb & ~3;
+  int4 sv[kFwdQuads];
+  float4 wv[kFwdQuads];
+  uint32_t dv[kFwdQuads];
+  auto load = [&](int w0, int e_end) {
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
       const int q = threadIdx.x + i * kFwdBlock;
       dv[i] = 0;
-      if (4 * q < wn) {
+      if (w0 + 4 * q < e_end) {
         const int e = w0 + 4 * q;
         sv[i] = ld_stream(d.src + e);
         wv[i] = ld_stream(d.weight + e);
         if (d.dead) dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
       }
     }
-    // Only positions of this workgroup's rows contribute; every gather is
+  };
+  load(cw, ee);
+  stage_table<kFwdBlock, (kFwdTbl > 0 ? kFwdTbl : 1)>(tbl, d.x, d.tbl_base, tlen);
+
+  int r = cb * kFwdRows + static_cast<int>(threadIdx.x);
+  bool has = threadIdx.x < kFwdRows && r < d.nrows;
+  int my_b = has ? d.row_ptr[r] : 0;
+  int my_e = has ? d.row_ptr[r + 1] : 0;
+  RowPre pre;
+  if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+  float s = ident;
+  __syncthreads();
+  for (;;) {
+    const int wn = min(kFwdWin, ee - cw);
+    // Only positions of this block's rows contribute; every gather is
     // issued before any is used.
     bool ok[kFwdQuads][4];
     float xv[kFwdQuads][4];
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
-      const int e = w0 + 4 * (threadIdx.x + i * kFwdBlock);
+      const int e = cw + 4 * (threadIdx.x + i * kFwdBlock);
       const bool in = 4 * (threadIdx.x + i * kFwdBlock) < wn;
       const int idx[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        ok[i][k] = in && e + k >= e_begin && e + k < e_end && !((dv[i] >> (8 * k)) & 0xFFu);
+        ok[i][k] = in && e + k >= eb && e + k < ee && !((dv[i] >> (8 * k)) & 0xFFu);
       gather_k<4>(tbl, d.x, d.tbl_base, tlen, idx, ok[i], xv[i]);
     }
 #pragma unroll
@@ -376,10 +400,19 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
         *reinterpret_cast<float4*>(buf + 4 * q) = o;
       }
     }
+    // The next window: the rest of this block, else the next block's first.
+    int nb = cb, nw = cw + kFwdWin, neb = eb, nee = ee;
+    if (nw >= ee) {
+      nb = cb + 1;
+      neb = ee;
+      nee = ee_next;
+      nw = neb & ~3;
+    }
+    if (nb < b1) load(nw, nee);
     __syncthreads();
-    const int lo = max(my_b, w0), hi = min(my_e, w0 + wn);
     {
-      const float* run = buf + (lo - w0);
+      const int lo = max(my_b, cw), hi = min(my_e, cw + wn);
+      const float* run = buf + (lo - cw);
       const int len = hi - lo;
       int j = 0;
       for (; j + 4 <= len; j += 4) {
@@ -391,16 +424,36 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
       }
       for (; j < len; ++j) s = Mono<M>::op(s, run[j]);
     }
+    if (nb != cb) {
+      // The block's rows are complete: combine, finalize, and set up the
+      // next block's rows (their loads land while this window's lanes run
+      // the apply programs).
+      if (has) {
+        const int u = pre.u;
+        const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
+        if (pre.fin) {
+          run_program(d.apply, u, pre.f, a, 0.0f, true);
+          if (d.acc) d.acc[u] = ident;
+        } else if (d.acc) {
+          d.acc[u] = a;
+        }
+      }
+      s = ident;
+      if (nb < b1) {
+        r = nb * kFwdRows + static_cast<int>(threadIdx.x);
+        has = threadIdx.x < kFwdRows && r < d.nrows;
+        my_b = has ? d.row_ptr[r] : 0;
+        my_e = has ? d.row_ptr[r + 1] : 0;
+        if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+        if (nb + 1 < b1) ee_next = row_end(nb + 1);
+      }
+    }
     __syncthreads();
-  }
-  if (!has) return;
-  const int u = pre.u;
-  const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
-  if (pre.fin) {
-    run_program(d.apply, u, pre.f, a, 0.0f, true);
-    if (d.acc) d.acc[u] = ident;
-  } else if (d.acc) {
-    d.acc[u] = a;
+    if (nb >= b1) break;
+    cb = nb;
+    cw = nw;
+    eb = neb;
+    ee = nee;
   }
 }
 
@@ -758,61 +811,70 @@ __device__ __forceinline__ void finish_row(const plx_partials_desc& d, const Row
   }
 }
 
-// Backward finalize of the hot rows (rows [0, nhot) are hot columns 0..nhot-1
-// in order): kHotCols columns per workgroup. The workgroup stages its columns
-// of hot_sb through LDS, kHotSbChunk superblocks at a time, with coalesced
-// loads, and each column's lane folds its superblock sums in order.
-constexpr int kHotCols = 64;
-constexpr int kHotSbChunk = 512;
+// Backward finalize of one level, one launch: the first hot_wgs workgroups
+// take the hot rows, kHotCols columns each, the rest the cold rows.
+//
+// Hot rows (rows [0, nhot) are hot columns 0..nhot-1 in order): the
+// workgroup stages its columns of hot_sb through LDS, kHotSbChunk
+// superblocks at a time, with coalesced loads, and each column's lane folds
+// its superblock sums in order.
+//
+// Cold rows: workgroup k takes rows [part_rows[k], part_rows[k+1]) (at most
+// kPartBlock, one per lane, cut so that their cold runs mostly fit one
+// window). A workgroup's rows own one contiguous range of the source-major
+// cold arrays, which is staged through LDS with coalesced loads; each row
+// folds its run in tile order, closing a superblock sum whenever the
+// superblock id changes.
+#ifndef PLX_HOT_COLS
+#define PLX_HOT_COLS 16
+#endif
+#ifndef PLX_HOT_CHUNK
+#define PLX_HOT_CHUNK 256
+#endif
+constexpr int kFinBlock = 256;
+constexpr int kHotCols = PLX_HOT_COLS;
+constexpr int kHotSbChunk = PLX_HOT_CHUNK;
+constexpr int kPartBlock = kFinBlock;
+constexpr int kPartWin = 2048;
+constexpr size_t kFinLds = (kHotSbChunk * kHotCols * 4 > kPartWin * 6) ? kHotSbChunk * kHotCols * 4
+                                                                       : kPartWin * 6;
 
 template <int M>
-__global__ __launch_bounds__(256) void k_hot_final(plx_partials_desc d) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* stage = reinterpret_cast<float*>(smem);  // [kHotSbChunk][kHotCols]
-  const int c0 = blockIdx.x * kHotCols;
+__device__ __forceinline__ void finalize_hot(const plx_partials_desc& d, float* stage, int wg) {
+  const int c0 = wg * kHotCols;
   const int ncol = min(kHotCols, d.nhot - c0);
   const bool has = static_cast<int>(threadIdx.x) < ncol;
   RowPre pre;
   if (has) pre = prefetch_row(d.row_unit, c0 + threadIdx.x, d.fin, d.apply);
   float s = Mono<M>::id();
-  constexpr int kPer = kHotSbChunk * kHotCols / 256;  // staged values per thread
+  constexpr int kPer = kHotSbChunk * kHotCols / kFinBlock;  // staged values per thread
   for (int sb0 = 0; sb0 < d.nsuper; sb0 += kHotSbChunk) {
     const int nsb = min(kHotSbChunk, d.nsuper - sb0);
     // Issue every load of the chunk before storing any of it.
     float v[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int j = threadIdx.x + i * 256;
+      const int j = threadIdx.x + i * kFinBlock;
       // Clamped into range: every load is unconditional (values past the
       // chunk are staged but never folded).
       const int sb = min(j / kHotCols, nsb - 1), c = min(j % kHotCols, ncol - 1);
       v[i] = d.hot_sb[static_cast<int64_t>(sb0 + sb) * d.nhot + c0 + c];
     }
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) stage[threadIdx.x + i * 256] = v[i];
+    for (int i = 0; i < kPer; ++i) stage[threadIdx.x + i * kFinBlock] = v[i];
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < ncol)
+    if (has)
       for (int sb = 0; sb < nsb; ++sb) s = Mono<M>::op(s, stage[sb * kHotCols + threadIdx.x]);
     __syncthreads();
   }
   if (has) finish_row<M>(d, pre, s);
 }
 
-// Backward finalize of the other rows: workgroup k takes rows
-// [part_rows[k], part_rows[k+1]) (at most kPartBlock, one per lane, cut so
-// that their cold runs mostly fit one window). A workgroup's rows own one
-// contiguous range of the source-major cold arrays, which is staged through
-// LDS with coalesced loads; each row folds its run in tile order, closing a
-// superblock sum whenever the superblock id changes.
-constexpr int kPartBlock = 256;
-constexpr int kPartWin = 2048;
-
 template <int M>
-__global__ __launch_bounds__(kPartBlock) void k_partials(plx_partials_desc d) {
-  __shared__ float cval[kPartWin];
-  __shared__ uint16_t csb[kPartWin];
-  const int row0 = d.part_rows[blockIdx.x];
-  const int rend = d.part_rows[blockIdx.x + 1];
+__device__ __forceinline__ void finalize_cold(const plx_partials_desc& d, float* cval,
+                                              uint16_t* csb, int wg) {
+  const int row0 = d.part_rows[wg];
+  const int rend = d.part_rows[wg + 1];
   const int r = row0 + static_cast<int>(threadIdx.x);
   const bool has = r < rend;
   RowPre pre;
@@ -864,6 +926,19 @@ __global__ __launch_bounds__(kPartBlock) void k_partials(plx_partials_desc d) {
     if (cur >= 0) s = Mono<M>::op(s, q);
   }
   if (has) finish_row<M>(d, pre, s);
+}
+
+template <int M>
+__global__ __launch_bounds__(kFinBlock) void k_finalize(plx_partials_desc d, int hot_wgs) {
+  __shared__ __align__(16) unsigned char smem[kFinLds];
+  const int wg = static_cast<int>(blockIdx.x);
+  if (wg < hot_wgs) {
+    finalize_hot<M>(d, reinterpret_cast<float*>(smem), wg);
+  } else {
+    float* cval = reinterpret_cast<float*>(smem);
+    uint16_t* csb = reinterpret_cast<uint16_t*>(smem + kPartWin * 4);
+    finalize_cold<M>(d, cval, csb, wg - hot_wgs);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1002,6 +1077,20 @@ inline unsigned grid_for(int64_t n, int block) {
   return static_cast<unsigned>((n + block - 1) / block);
 }
 
+// The current device's CU count (queried once per device; 256 on MI355X).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 bool program_ok(const plx_program& p) {
   return p.ninstr >= 0 && p.ninstr <= PLX_MAX_INSTR && p.nout >= 0 && p.nout <= PLX_MAX_OUTS;
 }
@@ -1080,7 +1169,9 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
   if (!d->fin.level || !d->fin.is_input)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: fin.level and fin.is_input are required");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned grid = grid_for(d->nrows, kFwdRows);
+  const unsigned nblk = grid_for(d->nrows, kFwdRows);
+  const unsigned cap = static_cast<unsigned>(cu_count() * kFwdPerCU);
+  const unsigned grid = nblk < cap ? nblk : cap;
   switch (d->monoid) {
     case PLX_MONOID_SUM: k_forward<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
     case PLX_MONOID_PROD: k_forward<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
@@ -1158,39 +1249,15 @@ int plx_backward_partials(const plx_partials_desc* d, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nhot_rows = d->row_hot ? d->nhot : 0;
   if (nhot_rows > d->nrows) return fail(PLX_ERR_INVALID, "plx_backward_partials: nhot > nrows");
-  if (nhot_rows > 0 && d->nsuper > 0) {
-    const unsigned hgrid = grid_for(nhot_rows, kHotCols);
-    const size_t lds = static_cast<size_t>(min(d->nsuper, kHotSbChunk)) * kHotCols * 4;
-    static const hipError_t attr_hot = [] {
-      hipError_t e = hipSuccess;
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_SUM>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_PROD>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_MAX>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_hot_final<PLX_MONOID_MIN>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      return e;
-    }();
-    (void)attr_hot;
-    switch (d->monoid) {
-      case PLX_MONOID_SUM: k_hot_final<PLX_MONOID_SUM><<<hgrid, 256, lds, s>>>(*d); break;
-      case PLX_MONOID_PROD: k_hot_final<PLX_MONOID_PROD><<<hgrid, 256, lds, s>>>(*d); break;
-      case PLX_MONOID_MAX: k_hot_final<PLX_MONOID_MAX><<<hgrid, 256, lds, s>>>(*d); break;
-      case PLX_MONOID_MIN: k_hot_final<PLX_MONOID_MIN><<<hgrid, 256, lds, s>>>(*d); break;
-      default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
-    }
-    const int rc = check_launch("plx_backward_partials");
-    if (rc) return rc;
-  }
-  if (d->nparts <= 0) return PLX_OK;
-  const unsigned grid = static_cast<unsigned>(d->nparts);
+  const int hot_wgs = nhot_rows > 0 && d->nsuper > 0 ? static_cast<int>(grid_for(nhot_rows, kHotCols)) : 0;
+  const int cold_wgs = d->nparts > 0 ? d->nparts : 0;
+  if (hot_wgs + cold_wgs == 0) return PLX_OK;
+  const unsigned grid = static_cast<unsigned>(hot_wgs + cold_wgs);
   switch (d->monoid) {
-    case PLX_MONOID_SUM: k_partials<PLX_MONOID_SUM><<<grid, kPartBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_PROD: k_partials<PLX_MONOID_PROD><<<grid, kPartBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MAX: k_partials<PLX_MONOID_MAX><<<grid, kPartBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MIN: k_partials<PLX_MONOID_MIN><<<grid, kPartBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_SUM: k_finalize<PLX_MONOID_SUM><<<grid, kFinBlock, 0, s>>>(*d, hot_wgs); break;
+    case PLX_MONOID_PROD: k_finalize<PLX_MONOID_PROD><<<grid, kFinBlock, 0, s>>>(*d, hot_wgs); break;
+    case PLX_MONOID_MAX: k_finalize<PLX_MONOID_MAX><<<grid, kFinBlock, 0, s>>>(*d, hot_wgs); break;
+    case PLX_MONOID_MIN: k_finalize<PLX_MONOID_MIN><<<grid, kFinBlock, 0, s>>>(*d, hot_wgs); break;
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_partials: unknown monoid");
   }
   return check_launch("plx_backward_partials");
