@@ -537,12 +537,13 @@ __device__ __forceinline__ uint32_t dead_from_end(int64_t e, int64_t live_end) {
 }
 
 // One 16-byte quad of positions per lane per iteration, the workgroups
-// striding over the bucket (each stages its act table once).
+// striding over the bucket (each stages its act table once). Three quads
+// per lane are in flight at once: while quad e is updated, quad e + stride's
+// gathers and value columns and quad e + 2 stride's addressing columns are
+// loading.
 template <int RULE, bool UNI_T>
 __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
   __shared__ float tbl[kTbl];
-  stage_table<kUpdBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
-  __syncthreads();
   constexpr int nstate =
       RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
   float den1 = 1.0f, den2 = 1.0f;
@@ -552,41 +553,69 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
     den2 = 1.0f - adam_pow(d, d.p[2], step, 1);
   }
   const int64_t stride = 4 * static_cast<int64_t>(gridDim.x) * kUpdBlock;
-  for (int64_t e = 4 * (static_cast<int64_t>(blockIdx.x) * kUpdBlock + threadIdx.x); e < d.n;
-       e += stride) {
-    const int4 sv = ld_stream(d.src + e);
-    const int4 tv = ld_stream(d.dst + e);
-    const uint32_t dv = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
-                               : dead_from_end(e, d.live_end);
-    float4 w = ld_stream(d.weight + e);
-    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0, s2 = s0;
-    if (nstate >= 1) s0 = ld_stream(d.s0 + e);
-    if (nstate >= 2) s1 = ld_stream(d.s1 + e);
-    if (nstate >= 3) s2 = ld_stream(d.s2 + e);
-    // Every gather is issued before any result is used.
-    bool lv[4];
-    float gr[4];
-    {
-      const int di[4] = {tv.x, tv.y, tv.z, tv.w};
-      const int si[4] = {sv.x, sv.y, sv.z, sv.w};
-      float gu[4], ac[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        lv[k] = !((dv >> (8 * k)) & 0xFFu);
-        gu[k] = d.gfield[lv[k] ? di[k] : 0];
-      }
-      gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv, ac);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) gr[k] = gu[k] * ac[k];
+  int64_t e = 4 * (static_cast<int64_t>(blockIdx.x) * kUpdBlock + threadIdx.x);
+  // Addressing columns of quad ea.
+  int64_t ea = e;
+  int4 sv = make_int4(0, 0, 0, 0), tv = sv;
+  uint32_t dv = 0;
+  auto load_addr = [&](int64_t at) {
+    ea = at;
+    if (at < d.n) {
+      sv = ld_stream(d.src + at);
+      tv = ld_stream(d.dst + at);
+      dv = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + at) : dead_from_end(at, d.live_end);
     }
-    if (lv[0]) update_edge<RULE, UNI_T>(d, gr[0], den1, den2, w.x, s0.x, s1.x, s2.x);
-    if (lv[1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, w.y, s0.y, s1.y, s2.y);
-    if (lv[2]) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, w.z, s0.z, s1.z, s2.z);
-    if (lv[3]) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, w.w, s0.w, s1.w, s2.w);
-    st_stream(d.weight + e, w);
-    if (nstate >= 1) st_stream(d.s0 + e, s0);
-    if (nstate >= 2) st_stream(d.s1 + e, s1);
-    if (nstate >= 3) st_stream(d.s2 + e, s2);
+  };
+  // Gathered values and value columns of the current quad.
+  bool lv[4];
+  float gu[4], ac[4];
+  float4 w = make_float4(0.f, 0.f, 0.f, 0.f), s0 = w, s1 = w, s2 = w;
+  auto gather = [&]() {
+    const int di[4] = {tv.x, tv.y, tv.z, tv.w};
+    const int si[4] = {sv.x, sv.y, sv.z, sv.w};
+    const bool in = ea < d.n;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lv[k] = in && !((dv >> (8 * k)) & 0xFFu);
+      gu[k] = d.gfield[lv[k] ? di[k] : 0];
+    }
+    gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv, ac);
+  };
+  auto load_vals = [&](int64_t at) {
+    if (at < d.n) {
+      w = ld_stream(d.weight + at);
+      if (nstate >= 1) s0 = ld_stream(d.s0 + at);
+      if (nstate >= 2) s1 = ld_stream(d.s1 + at);
+      if (nstate >= 3) s2 = ld_stream(d.s2 + at);
+    }
+  };
+  load_addr(e);
+  stage_table<kUpdBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
+  __syncthreads();
+  if (e >= d.n) return;
+  gather();
+  load_vals(e);
+  load_addr(e + stride);
+  for (; e < d.n; e += stride) {
+    float gr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gr[k] = gu[k] * ac[k];
+    const bool l0 = lv[0], l1 = lv[1], l2 = lv[2], l3 = lv[3];
+    float4 a = w, m = s0, v = s1, t = s2;
+    // The next quad's gathers and loads go out before this quad's update.
+    if (e + stride < d.n) {
+      gather();
+      load_vals(e + stride);
+      load_addr(e + 2 * stride);
+    }
+    if (l0) update_edge<RULE, UNI_T>(d, gr[0], den1, den2, a.x, m.x, v.x, t.x);
+    if (l1) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, a.y, m.y, v.y, t.y);
+    if (l2) update_edge<RULE, UNI_T>(d, gr[2], den1, den2, a.z, m.z, v.z, t.z);
+    if (l3) update_edge<RULE, UNI_T>(d, gr[3], den1, den2, a.w, m.w, v.w, t.w);
+    st_stream(d.weight + e, a);
+    if (nstate >= 1) st_stream(d.s0 + e, m);
+    if (nstate >= 2) st_stream(d.s1 + e, v);
+    if (nstate >= 3) st_stream(d.s2 + e, t);
   }
 }
 
@@ -650,13 +679,9 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   float* hot = buf + T;                          // [nhot]
   // [tbl_len] act of the busiest sources (the whole allocation without fold)
   float* tbl = FOLD ? hot + ((d.nhot + 3) & ~3) : reinterpret_cast<float*>(smem);
-  if (RULE >= 0) stage_table<kTileBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
   const int k0 = d.super_tile[blockIdx.x];
   const int k1 = d.super_tile[blockIdx.x + 1];
   const float ident = Mono<M>::id();
-  if (FOLD)
-    for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hot[j] = ident;
-  __syncthreads();
   constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD
                              ? 0
                              : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
@@ -668,31 +693,69 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   }
   constexpr int U = kTileQuads;  // a tile is one pass: at most 4 * U * kTileBlock positions
 
-  // Registers of the tile in flight. A tile's loads (edge columns and its
-  // group descriptors) are issued while the previous tile is folded, so the
-  // fold never leaves the memory system idle.
-  int4 sv[U], tv[U];
+  // The pipeline runs three tiles at once. While tile blk is folded from
+  // LDS, tile blk + 1's gathers (g[dst], act[src]) and value columns
+  // (weight, optimizer state, sorted rank, group descriptors) are in flight,
+  // and so are tile blk + 2's addressing columns (dst, src, dead), which the
+  // gathers of the next iteration need.
+  int4 sv[U], tv[U];  // addressing columns of tile `an` (the next to gather)
   uint32_t dv[U];
+  int64_t ta = 0;
+  int na = 0;
+  auto load_addr = [&](int blk) {
+    ta = d.base + d.tile_pos[blk];
+    na = d.tile_pos[blk + 1] - d.tile_pos[blk];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = threadIdx.x + i * kTileBlock;
+      if (4 * q < na) {
+        const int64_t e = ta + 4 * q;
+        tv[i] = ld_stream(d.dst + e);
+        if (RULE >= 0) sv[i] = ld_stream(d.src + e);
+        dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e) : dead_from_end(e, d.live_end);
+      }
+    }
+  };
+  // Value columns and gathered values of the current tile.
   uint2 rk[U];
   float4 w[U], s0[U], s1[U], s2[U];
+  bool lv[U][4];
+  float gd[U][4], gu[U][4], ac[U][4];
+  int64_t t0 = 0;
+  int n = 0;
   uint32_t gse[kGrpPer];
   int32_t gtg[kGrpPer];
-  int ga = 0, gb = 0, n = 0;
-  int64_t t0 = 0;
-  auto load = [&](int blk) {
-    t0 = d.base + d.tile_pos[blk];
-    n = d.tile_pos[blk + 1] - d.tile_pos[blk];
+  int ga = 0, gb = 0;
+  // Gathers of the tile whose addressing columns are in registers; every one
+  // is issued before any result is used (dead or out-of-tile lanes gather a
+  // harmless unit).
+  auto gather = [&]() {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const bool in = 4 * (threadIdx.x + i * kTileBlock) < na;
+      const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
+      const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
+        const int dk = lv[i][k] ? di[k] : 0;
+        if (FOLD) gd[i][k] = d.g[dk];
+        if (RULE >= 0) gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
+      }
+      if (RULE >= 0) gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ac[i]);
+    }
+    t0 = ta;
+    n = na;
+  };
+  // Value columns and group descriptors of tile blk (positions t0.., n).
+  auto load_vals = [&](int blk) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = threadIdx.x + i * kTileBlock;
       if (4 * q < n) {
         const int64_t e = t0 + 4 * q;
-        tv[i] = ld_stream(d.dst + e);
-        dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e)
-                       : dead_from_end(e, d.live_end);
         w[i] = ld_stream(d.weight + e);
         if (FOLD) rk[i] = ld_stream(d.sorted_rank + (e - d.base));
-        if (RULE >= 0) sv[i] = ld_stream(d.src + e);
         if (nstate >= 1) s0[i] = ld_stream(d.s0 + e);
         if (nstate >= 2) s1[i] = ld_stream(d.s1 + e);
         if (nstate >= 3) s2[i] = ld_stream(d.s2 + e);
@@ -712,26 +775,15 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
     }
   };
 
-  load(k0);
+  load_addr(k0);
+  if (RULE >= 0) stage_table<kTileBlock>(tbl, d.act, d.tbl_base, d.tbl_len);
+  if (FOLD)
+    for (int j = threadIdx.x; j < d.nhot; j += kTileBlock) hot[j] = ident;
+  __syncthreads();
+  gather();
+  load_vals(k0);
+  if (k0 + 1 < k1) load_addr(k0 + 1);
   for (int blk = k0; blk < k1; ++blk) {
-    // Gathers: every one is issued before any result is used (dead or
-    // out-of-tile lanes gather a harmless unit).
-    bool lv[U][4];
-    float gd[U][4], gu[U][4], ac[U][4];
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const bool in = 4 * (threadIdx.x + i * kTileBlock) < n;
-      const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
-      const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
-        const int dk = lv[i][k] ? di[k] : 0;
-        if (FOLD) gd[i][k] = d.g[dk];
-        if (RULE >= 0) gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
-      }
-      if (RULE >= 0) gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ac[i]);
-    }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = threadIdx.x + i * kTileBlock;
@@ -743,7 +795,6 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         // position tombstoned after the layout was built (below live_end)
         // keeps its slot and contributes the identity; every group folds from
         // the identity, so that leaves the fold's bits unchanged.
-        const float idv = Mono<M>::id();
         const int32_t rs[4] = {static_cast<int32_t>(rk[i].x & 0xFFFFu), static_cast<int32_t>(rk[i].x >> 16),
                                static_cast<int32_t>(rk[i].y & 0xFFFFu), static_cast<int32_t>(rk[i].y >> 16)};
         const float wk[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
@@ -752,7 +803,7 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
           if (lv[i][k])
             buf[rs[k]] = wk[k] * gd[i][k];
           else if (e + k < d.live_end)
-            buf[rs[k]] = idv;
+            buf[rs[k]] = ident;
         }
       }
       if (RULE >= 0) {
@@ -779,7 +830,11 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       cse[i] = gse[i];
       ctg[i] = gtg[i];
     }
-    if (blk + 1 < k1) load(blk + 1);
+    if (blk + 1 < k1) {
+      gather();
+      load_vals(blk + 1);
+      if (blk + 2 < k1) load_addr(blk + 2);
+    }
     if (!FOLD) continue;
     __syncthreads();
 #pragma unroll
