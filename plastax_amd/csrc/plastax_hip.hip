@@ -918,8 +918,19 @@ __device__ __forceinline__ void finalize_hot(const plx_partials_desc& d, float* 
 #pragma unroll
     for (int i = 0; i < kPer; ++i) stage[threadIdx.x + i * kFinBlock] = v[i];
     __syncthreads();
-    if (has)
-      for (int sb = 0; sb < nsb; ++sb) s = Mono<M>::op(s, stage[sb * kHotCols + threadIdx.x]);
+    if (has) {
+      // Eight LDS reads in flight per step of the (sequential) fold.
+      const float* col = stage + threadIdx.x;
+      int sb = 0;
+      for (; sb + 8 <= nsb; sb += 8) {
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = col[(sb + k) * kHotCols];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s = Mono<M>::op(s, x[k]);
+      }
+      for (; sb < nsb; ++sb) s = Mono<M>::op(s, col[sb * kHotCols]);
+    }
     __syncthreads();
   }
   if (has) finish_row<M>(d, pre, s);
@@ -967,7 +978,27 @@ __device__ __forceinline__ void finalize_cold(const plx_partials_desc& d, float*
       }
       __syncthreads();
       const int lo = max(j0, w0), hi = min(j1, w0 + wn);
-      for (int j = lo; j < hi; ++j) {
+      // Eight entries' LDS reads in flight per step of the fold.
+      int j = lo;
+      for (; j + 8 <= hi; j += 8) {
+        float x[8];
+        int b[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          x[k] = cval[j + k - w0];
+          b[k] = csb[j + k - w0];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (b[k] != cur) {
+            if (cur >= 0) s = Mono<M>::op(s, q);
+            q = ident;
+            cur = b[k];
+          }
+          q = Mono<M>::op(q, x[k]);
+        }
+      }
+      for (; j < hi; ++j) {
         const int sb = csb[j - w0];
         if (sb != cur) {
           if (cur >= 0) s = Mono<M>::op(s, q);
