@@ -239,6 +239,78 @@ typedef struct plx_update_desc {
 
 PLX_EXPORT int plx_update_conn(const plx_update_desc* d, void* stream);
 
+/* ---- Batched steps (make_step(batch_size=B): step.py:359-468) ----------
+ * Unit columns of a batched step are [num_units][B] (sample b of unit u at
+ * u * B + b); every per-sample fold keeps the streaming step's order.
+ *
+ * Forward of one bucket for B samples (phases.py:812-840 with the per-sample
+ * edge list's order): plx_forward_bucket's descriptor with x, acc and the
+ * apply program's fields and outs batched; tbl_* are ignored. Row r folds
+ * its positions in slot order per sample. */
+PLX_EXPORT int plx_forward_batch(const plx_forward_desc* d, int32_t batch, void* stream);
+
+/* Backward of one bucket for B samples (build_csr_backward, phases.py:843-934,
+ * and the reference's per-sample scatter order): row r is source unit
+ * row_unit[r]; its live out-edges are the physical positions
+ * pos[row_ptr[r] .. row_ptr[r+1]) in logical slot order, each contributing
+ * weight[p] * g[dst[p] * B + b] (pre-update weights), folded in that order
+ * from the identity, combined into acc (null: the identity) and, where the
+ * row finalizes, `apply` runs (fields and outs batched) and acc resets. */
+typedef struct plx_bwd_batch_desc {
+  int32_t nrows;
+  int32_t monoid;
+  int32_t batch;
+  int32_t reserved;
+  const int32_t* row_unit;
+  const int32_t* row_ptr;
+  const int32_t* pos;
+  const int32_t* dst;
+  const float* weight;
+  const uint8_t* dead; /* tombstones set since the lists were built, or null */
+  const float* g;      /* [num_units][B] the map's linear_input field */
+  float* acc;          /* [num_units][B] carried accumulator, or null */
+  plx_finalize fin;
+  plx_program apply;
+} plx_bwd_batch_desc;
+
+PLX_EXPORT int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream);
+
+/* The exact batched connection update (build_batched_update_conn,
+ * phases.py:390-483): per live position, stat_b = gfield[dst * B + b] *
+ * act[src * B + b]; total = stat_0, then total + stat_b for b = 1 .. B-1;
+ * mean = total / B; then the update rule of plx_update_conn with grad =
+ * mean (tbl_* ignored; gfield and act batched). */
+PLX_EXPORT int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream);
+
+/* Batched losses: sample b's outputs at ids[k] * B + b, targets[b * n_out +
+ * k], loss into losses[b]; the per-sample fold is plx_loss_elementwise's /
+ * plx_loss_softmax_ce's. partials: B * ceil(n_out / 256) floats. */
+PLX_EXPORT int plx_loss_elementwise_batch(int32_t n_out, const int32_t* output_ids,
+                                          const float* targets, const plx_program* term,
+                                          float* seed_field, float* partials, float* losses,
+                                          int32_t batch, void* stream);
+PLX_EXPORT int plx_loss_softmax_ce_batch(int32_t n_out, const int32_t* output_ids,
+                                         const float* act, const float* targets,
+                                         float* seed_field, float* losses, int32_t batch,
+                                         void* stream);
+
+/* StepResult.loss of a batched step (step.py:466): (0 + l_0 + ... + l_{B-1}) / B. */
+PLX_EXPORT int plx_batch_mean(int32_t batch, const float* losses, float* out, void* stream);
+
+/* reduce_batch_units (phases.py:298-332) for one column: dst[u] from
+ * src[u * B .. u * B + B): PLX_REDUCE_MEAN (float32: x_0 + x_1 + ... in
+ * sample order, then / B), PLX_REDUCE_SUM (the same sum; int32 wraps),
+ * PLX_REDUCE_FIRST (x_0). kind: PLX_COL_F32, PLX_COL_I32 (MEAN refused) or
+ * PLX_COL_U8 (FIRST only). */
+#define PLX_REDUCE_MEAN 0
+#define PLX_REDUCE_SUM 1
+#define PLX_REDUCE_FIRST 2
+#define PLX_COL_F32 0
+#define PLX_COL_I32 1
+#define PLX_COL_U8 2
+PLX_EXPORT int plx_reduce_batch(int64_t n, int32_t batch, int32_t mode, int32_t kind,
+                                const void* src, void* dst, void* stream);
+
 /* Step input scatter (step.py:598): dst[ids[k]] = values[k]. */
 PLX_EXPORT int plx_scatter_f32(int32_t n, const int32_t* ids, const float* values,
                     float* dst, void* stream);

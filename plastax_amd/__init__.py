@@ -45,6 +45,7 @@ from plastax_amd.traits import (
     AddUnit,
     BackwardPass,
     BatchReduction,
+    FieldReductions,
     ForwardPass,
     Loss,
     MeanFloatFirstRest,
@@ -52,6 +53,7 @@ from plastax_amd.traits import (
     ProposeAddConn,
     PruneConn,
     PruneUnit,
+    Reduction,
     ResetGlobal,
     ScoreAddConn,
     SoftmaxCrossEntropyLoss,
@@ -71,6 +73,8 @@ __all__ = [
     "AddUnit",
     "BackwardPass",
     "BatchReduction",
+    "FieldReductions",
+    "Reduction",
     "Driver",
     "ConnIdx",
     "ConnView",

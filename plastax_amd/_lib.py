@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 6  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 7  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -171,6 +171,25 @@ class plx_update_desc(ctypes.Structure):
     ]
 
 
+class plx_bwd_batch_desc(ctypes.Structure):
+    _fields_ = [
+        ("nrows", c_i32),
+        ("monoid", c_i32),
+        ("batch", c_i32),
+        ("reserved", c_i32),
+        ("row_unit", c_vp),
+        ("row_ptr", c_vp),
+        ("pos", c_vp),
+        ("dst", c_vp),
+        ("weight", c_vp),
+        ("dead", c_vp),
+        ("g", c_vp),
+        ("acc", c_vp),
+        ("fin", plx_finalize),
+        ("apply", plx_program),
+    ]
+
+
 class plx_site_prog(ctypes.Structure):
     _fields_ = [
         ("ninstr", c_i32),
@@ -319,6 +338,16 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "plx_loss_softmax_ce": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_fill_f32": (c_i32, [c_i64, c_f32, c_vp, c_vp]),
+    "plx_forward_batch": (c_i32, [ctypes.POINTER(plx_forward_desc), c_i32, c_vp]),
+    "plx_backward_batch": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
+    "plx_update_batch": (c_i32, [ctypes.POINTER(plx_update_desc), c_i32, c_vp]),
+    "plx_loss_elementwise_batch": (
+        c_i32,
+        [c_i32, c_vp, c_vp, ctypes.POINTER(plx_program), c_vp, c_vp, c_vp, c_i32, c_vp],
+    ),
+    "plx_loss_softmax_ce_batch": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp]),
+    "plx_batch_mean": (c_i32, [c_i32, c_vp, c_vp, c_vp]),
+    "plx_reduce_batch": (c_i32, [c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "plx_philox32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp]),
     "plx_eval_math": (c_i32, [c_i32, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "plx_last_error": (ctypes.c_char_p, []),
@@ -367,6 +396,7 @@ STRUCTS = (
     plx_grow_col,
     plx_grow_claim_desc,
     plx_unit_col,
+    plx_bwd_batch_desc,
 )
 
 _lib: ctypes.CDLL | None = None

@@ -1,0 +1,325 @@
+"""The batched step: ``make_step(net, static, batch_size=B)``.
+
+Mirrors src/plastax/step.py:359-468 and phases.py:217-532. Forward, loss and
+backward run once per sample against the shared connections; the connection
+update is one optimizer step on the batch-mean gradient (the optim bundles'
+exact ``per_sample`` / ``incoming_batched`` pair, phases.py:434-483); the
+per-sample unit columns are reduced by the network's ``batch_reduction``
+(phases.py:298-332); the structural phases then run once on the reduced
+state, and ``StepResult.loss`` is the batch mean.
+
+Device layout: during the step every unit column a per-sample phase reads or
+writes is a ``[num_units, B]`` tensor (sample b of unit u at ``u * B + b``),
+in the arena's physical unit order. A forward row (destination) or a backward
+row (source) is one workgroup whose lanes are the samples: the gathered unit
+row is one coalesced B-wide read and the edge columns are uniform across the
+workgroup. Summation orders, per sample:
+
+- forward: a destination's live in-edges in slot order (the streaming
+  step's, so a batch of one equals the streaming forward bit for bit);
+- backward: a source's live out-edges in logical slot order, from the
+  identity (the reference's per-sample scatter order);
+- update: ``stat_0 + stat_1 + ... + stat_{B-1}`` then ``/ B``
+  (phases.py:462-471);
+- MEAN / SUM reductions: samples in order from sample 0; the loss mean
+  ``(0 + l_0 + ... ) / B``.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import numpy as np
+import torch
+
+from plastax_amd import _lib
+from plastax_amd._expr import UnsupportedPolicyError
+from plastax_amd._layout import Arena
+from plastax_amd._plan import Plan, program_struct
+from plastax_amd._types import ACTIVATION
+from plastax_amd.state import NetworkState, NetworkStatic
+from plastax_amd.step import StepFn, StepInputs, StepResult, _stream
+from plastax_amd.traits import Reduction, batch_written_reduction
+
+_REDUCE = {Reduction.MEAN: 0, Reduction.SUM: 1, Reduction.FIRST: 2}
+
+
+class BatchSources:
+    """Per bucket, its backward rows (sources) and their live out-edge
+    positions in logical slot order (``pos[ptr[r] .. ptr[r+1])``)."""
+
+    def __init__(self, nrows: int, rows: torch.Tensor, ptr: torch.Tensor, pos: torch.Tensor) -> None:
+        self.nrows = nrows
+        self.rows = rows
+        self.ptr = ptr
+        self.pos = pos
+
+
+def batch_sources(arena: Arena, b: int) -> BatchSources:
+    """Bucket b's backward rows: every unit of level b and every live source
+    of the bucket, ascending; each row's live positions sorted by logical slot
+    (cached on the arena, whose structure it follows)."""
+    cache = arena.__dict__.setdefault("_batch_sources", {})
+    if b in cache:
+        return cache[b]
+    base, live = arena.bases[b], arena.lives[b]
+    src = arena.cols["from_id"][base : base + live].cpu().numpy().astype(np.int64)
+    slot = arena.slot[base : base + live].cpu().numpy().astype(np.int64)
+    if b + 1 < arena.lvl_start.size:
+        level_units = np.arange(int(arena.lvl_start[b]), int(arena.lvl_start[b + 1]), dtype=np.int64)
+    else:
+        level_units = np.zeros(0, dtype=np.int64)  # no unit has this level
+    rows = np.union1d(level_units, np.unique(src))
+    order = np.lexsort((slot, src))
+    pos = (order + base).astype(np.int64)
+    ptr = np.searchsorted(src[order], rows, side="left")
+    ptr = np.concatenate([ptr, [live]]).astype(np.int64)
+    dev = arena.device
+    out = BatchSources(
+        int(rows.size),
+        torch.from_numpy(rows.astype(np.int32)).to(dev),
+        torch.from_numpy(ptr.astype(np.int32)).to(dev),
+        torch.from_numpy(np.concatenate([pos, [0]]).astype(np.int32)).to(dev),
+    )
+    cache[b] = out
+    return out
+
+
+def written_columns(plan: Plan, static: NetworkStatic) -> dict[str, str]:
+    """The unit columns a batched step's per-sample phases write, each with
+    the first phase writing it (phases.py:334-387)."""
+    written = {ACTIVATION.name: "the input scatter"}
+    for name in plan.forward.program.out_fields:
+        if name is not None:
+            written.setdefault(name, "forward_pass")
+    if plan.loss is not None:
+        written.setdefault(plan.loss.seed_field, "loss")
+    if plan.backward is not None:
+        for name in plan.backward.program.out_fields:
+            if name is not None:
+                written.setdefault(name, "backward_pass")
+    return written
+
+
+class BatchedStepFn(StepFn):
+    """The callable ``make_step(..., batch_size=B)`` returns."""
+
+    def __init__(self, plan: Plan, static: NetworkStatic, batch_size: int) -> None:
+        super().__init__(plan, static)
+        if plan.update_unit:
+            raise UnsupportedPolicyError("a batched step with update_unit is not in this build yet")
+        self.batch = int(batch_size)
+        self._checked = False
+
+    def _check_policy(self) -> dict[str, Reduction]:
+        """Every column a per-sample phase writes has a MEAN / SUM / FIRST
+        reduction (step.py:429-441); returns them."""
+        net = self.plan.net
+        policy = net.batch_reduction
+        specs = {s.name: s for s in self.static.unit_fields}
+        out = {}
+        for name, where in written_columns(self.plan, self.static).items():
+            try:
+                out[name] = batch_written_reduction(policy, specs[name], where=where)
+            except ValueError as err:
+                raise ValueError(f"{net.__name__}.{err}") from None
+        return out
+
+    def _batched_columns(self, units: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
+        """[num_units, B] copies of every column a per-sample phase reads or
+        writes (each sample starts from the shared state: step.py:421-424)."""
+        plan = self.plan
+        names = {ACTIVATION.name, plan.forward.field}
+        progs = [plan.forward.program]
+        if plan.loss is not None:
+            names.add(plan.loss.seed_field)
+            if plan.loss.program is not None:
+                progs.append(plan.loss.program)
+        if plan.backward is not None:
+            names.add(plan.backward.field)
+            progs.append(plan.backward.program)
+        if plan.update is not None:
+            names.add(plan.update.grad_field.name)
+        for p in progs:
+            names.update(n for n in p.fields)
+            names.update(n for n in p.out_fields if n is not None)
+        B = self.batch
+        return {n: units[n].unsqueeze(1).expand(-1, B).contiguous() for n in sorted(names)}
+
+    def __call__(self, state: NetworkState, inputs: StepInputs) -> StepResult:
+        plan = self.plan
+        B = self.batch
+        dev = state.device
+        if dev.type != "cuda":
+            raise RuntimeError("the plastax_amd step runs on a GPU; the state lives on the CPU")
+        n_in, n_out = len(self.static.input_ids), len(self.static.output_ids)
+        x = torch.as_tensor(inputs.inputs, dtype=torch.float32, device=dev)
+        if tuple(x.shape) != (B, n_in):
+            raise ValueError(f"batched step: inputs must be {(B, n_in)}, got {tuple(x.shape)}")
+        t = None
+        if inputs.targets is not None:
+            t = torch.as_tensor(inputs.targets, dtype=torch.float32, device=dev)
+            if tuple(t.shape) != (B, n_out):
+                raise ValueError(f"batched step: targets must be {(B, n_out)}, got {tuple(t.shape)}")
+            t = t.contiguous()
+        reductions = self._check_policy()
+        lib = _lib.load()
+        state = state._donate()
+        arena = self.arena(state)
+        consts = self._consts(dev, arena)
+        stream = _stream(dev)
+        units = state._physical_units(arena)
+        n_units = self.static.num_units
+        g = state.globals_
+        ub = self._batched_columns(units)
+        if n_in:
+            ub[ACTIVATION.name][consts["input_ids"].long()] = x.t()
+        fin = dict(
+            level=units["level"].data_ptr(),
+            is_input=consts["is_input"].data_ptr(),
+            pruned=units["pruned"].data_ptr() if "pruned" in units else None,
+        )
+
+        # Forward, per sample (phases.py:942-1015; step.py:443-447).
+        fp = plan.forward
+        acc = None
+        if arena.fwd_carry:
+            acc = torch.full((n_units, B), fp.identity, dtype=torch.float32, device=dev)
+        prog = program_struct(fp.program, ub, g)
+        for b in range(arena.num_buckets):
+            rows = arena.fwd[b]
+            d = _lib.plx_forward_desc()
+            d.nrows = rows.nrows
+            d.monoid = fp.monoid
+            d.row_unit = rows.rows.data_ptr()
+            d.row_ptr = rows.ptr.data_ptr()
+            d.src = arena.cols["from_id"].data_ptr()
+            d.weight = arena.cols["weight"].data_ptr()
+            d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
+            d.x = ub[fp.field].data_ptr()
+            d.acc = acc.data_ptr() if acc is not None else None
+            d.fin.level, d.fin.is_input, d.fin.pruned = fin["level"], fin["is_input"], fin["pruned"]
+            d.fin.fin_level = b + 1
+            d.fin.skip_inputs = 1
+            d.apply = prog
+            self._launch("forward", lib.plx_forward_batch, d, B, stream)
+
+        # Loss, per sample, then the batch mean (step.py:448-451, :466).
+        loss = torch.zeros((), dtype=torch.float32, device=dev)
+        if plan.loss is not None:
+            if t is None:
+                raise ValueError("step: this net has a loss, so StepInputs.targets is required")
+            losses = torch.empty(B, dtype=torch.float32, device=dev)
+            lp = plan.loss
+            ids = consts["output_ids"].data_ptr()
+            if lp.kind == "softmax":
+                _lib.check(
+                    lib.plx_loss_softmax_ce_batch(n_out, ids, ub[ACTIVATION.name].data_ptr(), t.data_ptr(),
+                                                  ub[lp.seed_field].data_ptr(), losses.data_ptr(), B, stream),
+                    "plx_loss_softmax_ce_batch",
+                )
+            else:
+                parts = torch.empty(B * (n_out // 256 + 1) + 1, dtype=torch.float32, device=dev)
+                lprog = program_struct(lp.program, ub, g)
+                _lib.check(
+                    lib.plx_loss_elementwise_batch(n_out, ids, t.data_ptr(), lprog, ub[lp.seed_field].data_ptr(),
+                                                   parts.data_ptr(), losses.data_ptr(), B, stream),
+                    "plx_loss_elementwise_batch",
+                )
+            _lib.check(lib.plx_batch_mean(B, losses.data_ptr(), loss.data_ptr(), stream), "plx_batch_mean")
+
+        # Backward, per sample (phases.py:1049-1104): the deepest level from
+        # the identity, then buckets L-1 .. 1 in the reference's slot order.
+        bp = plan.backward
+        if bp is not None:
+            bacc = None
+            if arena.bwd_carry:
+                bacc = torch.full((n_units, B), bp.identity, dtype=torch.float32, device=dev)
+            bprog = program_struct(bp.program, ub, g)
+            empty = torch.zeros(1, dtype=torch.int32, device=dev)
+
+            def run(rows: torch.Tensor, nrows: int, ptr: torch.Tensor, pos: torch.Tensor, level: int) -> None:
+                d = _lib.plx_bwd_batch_desc()
+                d.nrows = nrows
+                d.monoid = bp.monoid
+                d.batch = B
+                d.row_unit = rows.data_ptr()
+                d.row_ptr = ptr.data_ptr()
+                d.pos = pos.data_ptr()
+                d.dst = arena.cols["to_id"].data_ptr()
+                d.weight = arena.cols["weight"].data_ptr()
+                d.dead = arena.cols["dead"].data_ptr()
+                d.g = ub[bp.field].data_ptr()
+                d.acc = bacc.data_ptr() if bacc is not None else None
+                d.fin.level, d.fin.is_input, d.fin.pruned = fin["level"], fin["is_input"], fin["pruned"]
+                d.fin.fin_level = level
+                d.fin.skip_inputs = 1
+                d.apply = bprog
+                self._launch("backward", lib.plx_backward_batch, d, stream)
+
+            nb = arena.num_buckets
+            top = arena.top
+            if top.nrows:
+                zeros = torch.zeros(top.nrows + 1, dtype=torch.int32, device=dev)
+                run(top.rows, top.nrows, zeros, empty, nb)
+            for b in range(nb - 1, 0, -1):
+                src_rows = batch_sources(arena, b)
+                run(src_rows.rows, src_rows.nrows, src_rows.ptr, src_rows.pos, b)
+
+        # The connection update on the batch-mean gradient (phases.py:434-483).
+        up = plan.update
+        if up is not None:
+            for b in range(arena.num_buckets):
+                self._update_batch(plan, arena, ub, consts, b, stream)
+            state._arena_ahead = True
+
+        # reduce_batch_units (phases.py:298-332): the written columns only.
+        for name, red in reductions.items():
+            col = units[name]
+            kind = 0 if col.dtype == torch.float32 else (1 if col.dtype == torch.int32 else 2)
+            _lib.check(
+                lib.plx_reduce_batch(n_units, B, _REDUCE[red], kind, ub[name].data_ptr(), col.data_ptr(), stream),
+                "plx_reduce_batch",
+            )
+
+        # Once per batch: structural phases and reset_global (step.py:455-459).
+        if plan.prune_unit or plan.prune_conn or plan.add_unit or plan.add_conn is not None:
+            self._structural(state, arena, units, stream, g)
+        if plan.reset_global:
+            state.globals_ = plan.net.reset_global.reset(state.globals_)
+        state.step = state.step + 1
+        return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
+
+    def _update_batch(self, plan: Plan, arena: Arena, ub: dict, consts: dict, b: int, stream: int) -> None:
+        lib = _lib.load()
+        up = plan.update
+        base, end = arena.bases[b], arena.ends[b]
+
+        def col(name: str) -> int:
+            t = arena.cols[name]
+            return t.data_ptr() + base * t.element_size()
+
+        d = _lib.plx_update_desc()
+        d.n = end - base
+        d.rule = up.rule_code
+        d.src = col("from_id")
+        d.dst = col("to_id")
+        d.weight = col("weight")
+        for k, name in enumerate(up.state_columns()):
+            setattr(d, f"s{k}", col(name))
+        d.gfield = ub[up.grad_field.name].data_ptr()
+        d.act = ub[ACTIVATION.name].data_ptr()
+        if "pow_table" in consts:
+            d.pow_table = consts["pow_table"].data_ptr()
+            d.pow_table_len = consts["pow_table"].numel() // 2
+        for k, v in enumerate(up.params()):
+            d.p[k] = float(v)
+        self._edge_state(d, arena, b, True)
+        d.live_end -= base
+        d.dead = col("dead") if arena.dead_in_rows else None
+        self._launch("update_conn", lib.plx_update_batch, d, self.batch, stream)
+        self._advance_t(arena, b)
+
+
+def make_batched_step(plan: Plan, static: NetworkStatic, batch_size: int) -> Any:
+    return BatchedStepFn(plan, static, batch_size)

@@ -1028,6 +1028,192 @@ __global__ __launch_bounds__(kFinBlock) void k_finalize(plx_partials_desc d, int
 }
 
 // ---------------------------------------------------------------------------
+// Batched steps. Unit columns are [num_units][B]: a row of the forward or
+// the backward is one workgroup whose lanes are the samples, so the gathered
+// unit row (x[src * B ..] or g[dst * B ..]) is one coalesced B-wide read,
+// while FROM_ID / TO_ID / WEIGHT / DEAD are uniform across the workgroup.
+// Each lane folds its sample's terms in the streaming step's order.
+// ---------------------------------------------------------------------------
+constexpr int kBatchBlock = 256;
+constexpr int kBatchUnroll = 8;  // positions whose loads are in flight together
+
+// Combines a row's sum into acc and finalizes it for sample lane `idx`.
+template <int M>
+__device__ __forceinline__ void finish_batch(float* acc, const plx_program& P, bool fin, int64_t idx,
+                                             float s) {
+  const float a = Mono<M>::op(acc ? acc[idx] : Mono<M>::id(), s);
+  if (fin) {
+    run_program(P, idx, load_fields(P, idx), a, 0.0f, true);
+    if (acc) acc[idx] = Mono<M>::id();
+  } else if (acc) {
+    acc[idx] = a;
+  }
+}
+
+template <int M>
+__global__ __launch_bounds__(kBatchBlock) void k_forward_batch(plx_forward_desc d, int32_t B) {
+  const int r = blockIdx.x;
+  const int u = d.row_unit[r];
+  const int e0 = d.row_ptr[r], e1 = d.row_ptr[r + 1];
+  const bool fin = finalizes(d.fin, u);
+  const float ident = Mono<M>::id();
+  for (int b0 = 0; b0 < B; b0 += blockDim.x) {
+    const int b = b0 + static_cast<int>(threadIdx.x);
+    const int bl = b < B ? b : B - 1;  // every lane's loads stay in its row
+    float s = ident;
+    int e = e0;
+    for (; e + kBatchUnroll <= e1; e += kBatchUnroll) {
+      int sv[kBatchUnroll];
+      float wv[kBatchUnroll], xv[kBatchUnroll];
+      bool live[kBatchUnroll];
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k) {
+        sv[k] = d.src[e + k];
+        wv[k] = d.weight[e + k];
+        live[k] = d.dead ? d.dead[e + k] == 0 : true;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k) xv[k] = d.x[static_cast<int64_t>(sv[k]) * B + bl];
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k)
+        if (live[k]) s = Mono<M>::op(s, wv[k] * xv[k]);
+    }
+    for (; e < e1; ++e) {
+      if (d.dead && d.dead[e]) continue;
+      s = Mono<M>::op(s, d.weight[e] * d.x[static_cast<int64_t>(d.src[e]) * B + bl]);
+    }
+    if (b < B) finish_batch<M>(d.acc, d.apply, fin, static_cast<int64_t>(u) * B + b, s);
+  }
+}
+
+template <int M>
+__global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_desc d) {
+  const int r = blockIdx.x;
+  const int B = d.batch;
+  const int u = d.row_unit[r];
+  const int j0 = d.row_ptr[r], j1 = d.row_ptr[r + 1];
+  const bool fin = finalizes(d.fin, u);
+  const float ident = Mono<M>::id();
+  for (int b0 = 0; b0 < B; b0 += blockDim.x) {
+    const int b = b0 + static_cast<int>(threadIdx.x);
+    const int bl = b < B ? b : B - 1;
+    float s = ident;
+    int j = j0;
+    for (; j + kBatchUnroll <= j1; j += kBatchUnroll) {
+      int pv[kBatchUnroll], tv[kBatchUnroll];
+      float wv[kBatchUnroll], gv[kBatchUnroll];
+      bool live[kBatchUnroll];
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k) pv[k] = d.pos[j + k];
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k) {
+        tv[k] = d.dst[pv[k]];
+        wv[k] = d.weight[pv[k]];
+        live[k] = d.dead ? d.dead[pv[k]] == 0 : true;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k) gv[k] = d.g[static_cast<int64_t>(tv[k]) * B + bl];
+#pragma unroll
+      for (int k = 0; k < kBatchUnroll; ++k)
+        if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
+    }
+    for (; j < j1; ++j) {
+      const int p = d.pos[j];
+      if (d.dead && d.dead[p]) continue;
+      s = Mono<M>::op(s, d.weight[p] * d.g[static_cast<int64_t>(d.dst[p]) * B + bl]);
+    }
+    if (b < B) finish_batch<M>(d.acc, d.apply, fin, static_cast<int64_t>(u) * B + b, s);
+  }
+}
+
+// The batch-mean gradient of one position: stat_0 + stat_1 + ... in sample
+// order, divided by B (phases.py:434-483).
+__device__ __forceinline__ float batch_mean_grad(const float* g, const float* a, int32_t B) {
+  float total = g[0] * a[0];
+  int b = 1;
+  if ((B & 3) == 0) {
+    // 16-byte reads once the rows are aligned (B a multiple of 4).
+    for (; b < 4; ++b) total = total + g[b] * a[b];
+    for (; b + 4 <= B; b += 4) {
+      const float4 gv = *reinterpret_cast<const float4*>(g + b);
+      const float4 av = *reinterpret_cast<const float4*>(a + b);
+      total = total + gv.x * av.x;
+      total = total + gv.y * av.y;
+      total = total + gv.z * av.z;
+      total = total + gv.w * av.w;
+    }
+  }
+  for (; b < B; ++b) total = total + g[b] * a[b];
+  return total / static_cast<float>(B);
+}
+
+template <int RULE, bool UNI_T>
+__global__ __launch_bounds__(kBatchBlock) void k_update_batch(plx_update_desc d, int32_t B) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kBatchBlock + threadIdx.x;
+  if (e >= d.n) return;
+  const bool live = d.dead ? d.dead[e] == 0 : e < d.live_end;
+  if (!live) return;  // dead rows keep their values
+  float den1 = 1.0f, den2 = 1.0f;
+  if (RULE == PLX_RULE_ADAM && UNI_T) {
+    const float step = d.step_t + 1.0f;
+    den1 = 1.0f - adam_pow(d, d.p[1], step, 0);
+    den2 = 1.0f - adam_pow(d, d.p[2], step, 1);
+  }
+  const float grad = batch_mean_grad(d.gfield + static_cast<int64_t>(d.dst[e]) * B,
+                                     d.act + static_cast<int64_t>(d.src[e]) * B, B);
+  constexpr int nstate =
+      RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
+  float w = d.weight[e];
+  float s0 = nstate >= 1 ? d.s0[e] : 0.0f;
+  float s1 = nstate >= 2 ? d.s1[e] : 0.0f;
+  float s2 = nstate >= 3 ? d.s2[e] : 0.0f;
+  update_edge<RULE, UNI_T>(d, grad, den1, den2, w, s0, s1, s2);
+  d.weight[e] = w;
+  if (nstate >= 1) d.s0[e] = s0;
+  if (nstate >= 2) d.s1[e] = s1;
+  if (nstate >= 3) d.s2[e] = s2;
+}
+
+template <typename T>
+__global__ void k_reduce_batch(int64_t n, int32_t B, int32_t mode, const T* src, T* dst) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u >= n) return;
+  const T* x = src + u * B;
+  T s = x[0];
+  if (mode != PLX_REDUCE_FIRST)
+    for (int b = 1; b < B; ++b) s = s + x[b];
+  if (mode == PLX_REDUCE_MEAN) s = s / static_cast<T>(B);
+  dst[u] = s;
+}
+
+template <>
+__global__ void k_reduce_batch<uint8_t>(int64_t n, int32_t B, int32_t mode, const uint8_t* src,
+                                        uint8_t* dst) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u < n) dst[u] = src[u * B];  // FIRST (the entry point refuses the rest)
+}
+
+// int32 sums wrap (two's complement), as numpy's and XLA's do.
+template <>
+__global__ void k_reduce_batch<int32_t>(int64_t n, int32_t B, int32_t mode, const int32_t* src,
+                                        int32_t* dst) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u >= n) return;
+  const int32_t* x = src + u * B;
+  uint32_t s = static_cast<uint32_t>(x[0]);
+  if (mode == PLX_REDUCE_SUM)
+    for (int b = 1; b < B; ++b) s += static_cast<uint32_t>(x[b]);
+  dst[u] = static_cast<int32_t>(s);
+}
+
+__global__ void k_batch_mean(int32_t B, const float* losses, float* out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float s = 0.0f;
+  for (int b = 0; b < B; ++b) s = s + losses[b];
+  *out = s / static_cast<float>(B);
+}
+
+// ---------------------------------------------------------------------------
 // Small kernels: scatter, fill, losses, Philox, math probes.
 // ---------------------------------------------------------------------------
 __global__ void k_scatter(int32_t n, const int32_t* ids, const float* values, float* dst) {
@@ -1045,27 +1231,34 @@ constexpr int kPiece = 256;
 // One 256-output piece per workgroup: each thread runs the loss program for
 // one output (out slot 0, the seed, lands at the output's unit id; slot 1 is
 // the loss term), then one lane folds the piece's terms in order from +0.0.
+// Batched (B > 1): sample b = blockIdx.y reads and writes unit u at u * B + b,
+// its targets at targets[b * n_out ..] and its piece sums at b * gridDim.x.
 __global__ __launch_bounds__(kPiece) void k_loss_pieces(int32_t n_out, const int32_t* ids,
                                                        const float* targets, plx_program P,
-                                                       float* piece_sums) {
+                                                       float* piece_sums, int32_t B) {
   __shared__ float terms[kPiece];
+  const int b = blockIdx.y;
   const int k = blockIdx.x * kPiece + threadIdx.x;
   if (k < n_out) {
-    const int u = ids[k];
-    terms[threadIdx.x] = run_program(P, u, load_fields(P, u), 0.0f, targets[k], true);
+    const int64_t u = static_cast<int64_t>(ids[k]) * B + b;
+    terms[threadIdx.x] =
+        run_program(P, u, load_fields(P, u), 0.0f, targets[static_cast<int64_t>(b) * n_out + k], true);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     const int len = min(kPiece, n_out - static_cast<int>(blockIdx.x) * kPiece);
     float s = 0.0f;
     for (int j = 0; j < len; ++j) s = s + terms[j];
-    piece_sums[blockIdx.x] = s;
+    piece_sums[static_cast<int64_t>(b) * gridDim.x + blockIdx.x] = s;
   }
 }
 
-// Folds n piece sums in order from +0.0 into *out, staging them through LDS.
+// Folds n piece sums in order from +0.0 into *out, staging them through LDS
+// (workgroup b: sums[b * n ..] into out[b]).
 __global__ __launch_bounds__(1024) void k_fold_sums(int32_t n, const float* sums, float* out) {
   __shared__ float buf[1024];
+  sums += static_cast<int64_t>(blockIdx.x) * n;
+  out += blockIdx.x;
   float s = 0.0f;
   for (int base = 0; base < n; base += 1024) {
     const int len = min(1024, n - base);
@@ -1080,17 +1273,24 @@ __global__ __launch_bounds__(1024) void k_fold_sums(int32_t n, const float* sums
 
 constexpr int kSoftmaxMaxPieces = 1024;
 
+// Workgroup b is sample b: unit u at u * B + b, targets[b * n ..], loss_out[b].
 __global__ __launch_bounds__(1024) void k_softmax_ce(int32_t n, const int32_t* ids,
-                                                     const float* act, const float* targets,
-                                                     float* seed_field, float* loss_out) {
+                                                     const float* act_base, const float* targets,
+                                                     float* seed_base, float* loss_out, int32_t B) {
   __shared__ float red[1024];
   __shared__ float piece[kSoftmaxMaxPieces];
   __shared__ float bcast[2];
   const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  targets += static_cast<int64_t>(b) * n;
+  loss_out += b;
+  auto at = [&](int k) { return static_cast<int64_t>(ids[k]) * B + b; };
+  const float* act = act_base;
+  float* seed_field = seed_base;
   // 1. max by a '>' scan from -inf (NaN is never taken), then a tree.
   float m = -__builtin_huge_valf();
   for (int k = tid; k < n; k += blockDim.x) {
-    const float a = act[ids[k]];
+    const float a = act[at(k)];
     if (a > m) m = a;
   }
   red[tid] = m;
@@ -1105,7 +1305,7 @@ __global__ __launch_bounds__(1024) void k_softmax_ce(int32_t n, const int32_t* i
   for (int p = tid; p < npieces; p += blockDim.x) {
     float s = 0.0f;
     const int end = min(n, (p + 1) * kPiece);
-    for (int k = p * kPiece; k < end; ++k) s = s + px::expf_(act[ids[k]] - peak);
+    for (int k = p * kPiece; k < end; ++k) s = s + px::expf_(act[at(k)] - peak);
     piece[p] = s;
   }
   __syncthreads();
@@ -1122,9 +1322,9 @@ __global__ __launch_bounds__(1024) void k_softmax_ce(int32_t n, const int32_t* i
     float s = 0.0f;
     const int end = min(n, (p + 1) * kPiece);
     for (int k = p * kPiece; k < end; ++k) {
-      const float z = act[ids[k]] - peak;
+      const float z = act[at(k)] - peak;
       const float t = targets[k];
-      seed_field[ids[k]] = px::expf_(z) / total - t;
+      seed_field[at(k)] = px::expf_(z) / total - t;
       s = s + t * (log_sum - z);
     }
     piece[p] = s;
@@ -1228,19 +1428,20 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 6; }
+int32_t plx_abi_version(void) { return 7; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[14] = {
+  const int64_t sizes[15] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
       sizeof(plx_partials_desc),    sizeof(plx_update_desc),
       sizeof(plx_site_prog),        sizeof(plx_site_desc),
       sizeof(plx_sort_key),         sizeof(plx_sort_desc),
       sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
-      sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col)};
-  for (int32_t k = 0; k < n && k < 14; ++k) out[k] = sizes[k];
-  return 14;
+      sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col),
+      sizeof(plx_bwd_batch_desc)};
+  for (int32_t k = 0; k < n && k < 15; ++k) out[k] = sizes[k];
+  return 15;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
@@ -1416,7 +1617,7 @@ int plx_loss_elementwise(int32_t n_out, const int32_t* output_ids, const float* 
   if (p.nout < 2) p.nout = 2;
   const int npieces = (n_out + kPiece - 1) / kPiece;
   if (npieces > 0) {
-    k_loss_pieces<<<npieces, kPiece, 0, s>>>(n_out, output_ids, targets, p, partials);
+    k_loss_pieces<<<npieces, kPiece, 0, s>>>(n_out, output_ids, targets, p, partials, 1);
     int rc = check_launch("plx_loss_elementwise");
     if (rc) return rc;
   }
@@ -1433,8 +1634,164 @@ int plx_loss_softmax_ce(int32_t n_out, const int32_t* output_ids, const float* a
   if (!loss_out || (n_out > 0 && (!output_ids || !act || !targets || !seed_field)))
     return fail(PLX_ERR_INVALID, "plx_loss_softmax_ce: null pointer");
   k_softmax_ce<<<1, 1024, 0, static_cast<hipStream_t>(stream)>>>(n_out, output_ids, act,
-                                                                  targets, seed_field, loss_out);
+                                                                  targets, seed_field, loss_out, 1);
   return check_launch("plx_loss_softmax_ce");
+}
+
+// ---- batched steps ---------------------------------------------------------
+int plx_forward_batch(const plx_forward_desc* d, int32_t batch, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_forward_batch: null descriptor");
+  if (batch < 1) return fail(PLX_ERR_INVALID, "plx_forward_batch: batch must be >= 1");
+  if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_forward_batch: negative nrows");
+  if (d->nrows == 0) return PLX_OK;
+  if (!d->row_unit || !d->row_ptr || !d->src || !d->weight || !d->x)
+    return fail(PLX_ERR_INVALID, "plx_forward_batch: null column");
+  if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_forward_batch: bad program");
+  if (!d->fin.level || !d->fin.is_input)
+    return fail(PLX_ERR_INVALID, "plx_forward_batch: fin.level and fin.is_input are required");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned block = batch >= kBatchBlock ? kBatchBlock : static_cast<unsigned>((batch + 63) / 64 * 64);
+  const unsigned grid = static_cast<unsigned>(d->nrows);
+  switch (d->monoid) {
+    case PLX_MONOID_SUM: k_forward_batch<PLX_MONOID_SUM><<<grid, block, 0, s>>>(*d, batch); break;
+    case PLX_MONOID_PROD: k_forward_batch<PLX_MONOID_PROD><<<grid, block, 0, s>>>(*d, batch); break;
+    case PLX_MONOID_MAX: k_forward_batch<PLX_MONOID_MAX><<<grid, block, 0, s>>>(*d, batch); break;
+    case PLX_MONOID_MIN: k_forward_batch<PLX_MONOID_MIN><<<grid, block, 0, s>>>(*d, batch); break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_forward_batch: unknown monoid");
+  }
+  return check_launch("plx_forward_batch");
+}
+
+int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_batch: null descriptor");
+  if (d->batch < 1) return fail(PLX_ERR_INVALID, "plx_backward_batch: batch must be >= 1");
+  if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_batch: negative nrows");
+  if (d->nrows == 0) return PLX_OK;
+  if (!d->row_unit || !d->row_ptr || !d->pos || !d->dst || !d->weight || !d->g)
+    return fail(PLX_ERR_INVALID, "plx_backward_batch: null column");
+  if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_batch: bad program");
+  if (!d->fin.level || !d->fin.is_input)
+    return fail(PLX_ERR_INVALID, "plx_backward_batch: fin.level and fin.is_input are required");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int batch = d->batch;
+  const unsigned block = batch >= kBatchBlock ? kBatchBlock : static_cast<unsigned>((batch + 63) / 64 * 64);
+  const unsigned grid = static_cast<unsigned>(d->nrows);
+  switch (d->monoid) {
+    case PLX_MONOID_SUM: k_backward_batch<PLX_MONOID_SUM><<<grid, block, 0, s>>>(*d); break;
+    case PLX_MONOID_PROD: k_backward_batch<PLX_MONOID_PROD><<<grid, block, 0, s>>>(*d); break;
+    case PLX_MONOID_MAX: k_backward_batch<PLX_MONOID_MAX><<<grid, block, 0, s>>>(*d); break;
+    case PLX_MONOID_MIN: k_backward_batch<PLX_MONOID_MIN><<<grid, block, 0, s>>>(*d); break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_batch: unknown monoid");
+  }
+  return check_launch("plx_backward_batch");
+}
+
+int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_update_batch: null descriptor");
+  if (batch < 1) return fail(PLX_ERR_INVALID, "plx_update_batch: batch must be >= 1");
+  if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_update_batch: negative n");
+  if (d->n == 0) return PLX_OK;
+  if (!d->src || !d->dst || !d->weight || !d->gfield || !d->act)
+    return fail(PLX_ERR_INVALID, "plx_update_batch: null column");
+  if (d->step_mode != 0 && d->step_mode != 1)
+    return fail(PLX_ERR_INVALID, "plx_update_batch: step_mode must be 0 or 1");
+  if ((d->rule == PLX_RULE_MOMENTUM || d->rule == PLX_RULE_RMSPROP) && !d->s0)
+    return fail(PLX_ERR_INVALID, "plx_update_batch: state column missing");
+  if (d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || (d->step_mode == 0 && !d->s2)))
+    return fail(PLX_ERR_INVALID, "plx_update_batch: Adam state columns missing");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(d->n, kBatchBlock);
+  switch (d->rule) {
+    case PLX_RULE_SGD: k_update_batch<PLX_RULE_SGD, false><<<grid, kBatchBlock, 0, s>>>(*d, batch); break;
+    case PLX_RULE_MOMENTUM:
+      k_update_batch<PLX_RULE_MOMENTUM, false><<<grid, kBatchBlock, 0, s>>>(*d, batch);
+      break;
+    case PLX_RULE_ADAM:
+      if (d->step_mode == 1)
+        k_update_batch<PLX_RULE_ADAM, true><<<grid, kBatchBlock, 0, s>>>(*d, batch);
+      else
+        k_update_batch<PLX_RULE_ADAM, false><<<grid, kBatchBlock, 0, s>>>(*d, batch);
+      break;
+    case PLX_RULE_RMSPROP:
+      k_update_batch<PLX_RULE_RMSPROP, false><<<grid, kBatchBlock, 0, s>>>(*d, batch);
+      break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_update_batch: unknown rule");
+  }
+  return check_launch("plx_update_batch");
+}
+
+int plx_loss_elementwise_batch(int32_t n_out, const int32_t* output_ids, const float* targets,
+                               const plx_program* term, float* seed_field, float* partials,
+                               float* losses, int32_t batch, void* stream) {
+  if (n_out < 0 || batch < 1) return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: bad size");
+  if (!term || !losses || !partials)
+    return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: null pointer");
+  if (!program_ok(*term)) return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: bad program");
+  if (n_out > 0 && (!output_ids || !targets || !seed_field))
+    return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  plx_program p = *term;
+  p.outs[0] = seed_field;
+  p.outs[1] = nullptr;
+  if (p.nout < 2) p.nout = 2;
+  const int npieces = (n_out + kPiece - 1) / kPiece;
+  if (npieces > 0) {
+    k_loss_pieces<<<dim3(npieces, batch), kPiece, 0, s>>>(n_out, output_ids, targets, p, partials, batch);
+    int rc = check_launch("plx_loss_elementwise_batch");
+    if (rc) return rc;
+  }
+  k_fold_sums<<<batch, 1024, 0, s>>>(npieces, partials, losses);
+  return check_launch("plx_loss_elementwise_batch");
+}
+
+int plx_loss_softmax_ce_batch(int32_t n_out, const int32_t* output_ids, const float* act,
+                              const float* targets, float* seed_field, float* losses,
+                              int32_t batch, void* stream) {
+  if (n_out < 0 || batch < 1) return fail(PLX_ERR_INVALID, "plx_loss_softmax_ce_batch: bad size");
+  if (n_out > kSoftmaxMaxPieces * kPiece)
+    return fail(PLX_ERR_UNSUPPORTED, "plx_loss_softmax_ce_batch: more than 262144 outputs");
+  if (!losses || (n_out > 0 && (!output_ids || !act || !targets || !seed_field)))
+    return fail(PLX_ERR_INVALID, "plx_loss_softmax_ce_batch: null pointer");
+  k_softmax_ce<<<batch, 1024, 0, static_cast<hipStream_t>(stream)>>>(n_out, output_ids, act, targets,
+                                                                      seed_field, losses, batch);
+  return check_launch("plx_loss_softmax_ce_batch");
+}
+
+int plx_batch_mean(int32_t batch, const float* losses, float* out, void* stream) {
+  if (batch < 1 || !losses || !out) return fail(PLX_ERR_INVALID, "plx_batch_mean: bad argument");
+  k_batch_mean<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(batch, losses, out);
+  return check_launch("plx_batch_mean");
+}
+
+int plx_reduce_batch(int64_t n, int32_t batch, int32_t mode, int32_t kind, const void* src, void* dst,
+                     void* stream) {
+  if (n < 0 || batch < 1) return fail(PLX_ERR_INVALID, "plx_reduce_batch: bad size");
+  if (mode < PLX_REDUCE_MEAN || mode > PLX_REDUCE_FIRST)
+    return fail(PLX_ERR_INVALID, "plx_reduce_batch: unknown mode");
+  if (kind == PLX_COL_I32 && mode == PLX_REDUCE_MEAN)
+    return fail(PLX_ERR_INVALID, "plx_reduce_batch: MEAN needs a float32 column");
+  if (kind == PLX_COL_U8 && mode != PLX_REDUCE_FIRST)
+    return fail(PLX_ERR_INVALID, "plx_reduce_batch: a byte column reduces by FIRST only");
+  if (n == 0) return PLX_OK;
+  if (!src || !dst) return fail(PLX_ERR_INVALID, "plx_reduce_batch: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(n, 256);
+  switch (kind) {
+    case PLX_COL_F32:
+      k_reduce_batch<float><<<grid, 256, 0, s>>>(n, batch, mode, static_cast<const float*>(src),
+                                                static_cast<float*>(dst));
+      break;
+    case PLX_COL_I32:
+      k_reduce_batch<int32_t><<<grid, 256, 0, s>>>(n, batch, mode, static_cast<const int32_t*>(src),
+                                                  static_cast<int32_t*>(dst));
+      break;
+    case PLX_COL_U8:
+      k_reduce_batch<uint8_t><<<grid, 256, 0, s>>>(n, batch, mode, static_cast<const uint8_t*>(src),
+                                                  static_cast<uint8_t*>(dst));
+      break;
+    default: return fail(PLX_ERR_INVALID, "plx_reduce_batch: unknown column kind");
+  }
+  return check_launch("plx_reduce_batch");
 }
 
 int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ctrs, uint32_t* out,

@@ -79,7 +79,9 @@ def make_step(
     if growth not in ("auto", "xla", "triton"):
         raise ValueError(f"make_step: unknown growth engine {growth!r}")
     if batch_size is not None:
-        raise UnsupportedPolicyError("batched steps (batch_size) are not in this build yet")
+        from plastax_amd.batched import BatchedStepFn
+
+        return BatchedStepFn(compile_plan(net, static), static, batch_size)
     return StepFn(compile_plan(net, static), static)
 
 

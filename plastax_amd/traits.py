@@ -11,6 +11,8 @@ device programs, and connection updates must be one of the optim bundles.
 from __future__ import annotations
 
 import dataclasses
+import enum
+from collections.abc import Mapping
 from typing import Any, ClassVar, Generic, TypeVar
 
 import numpy as np
@@ -129,12 +131,85 @@ class ResetGlobal:
         raise NotImplementedError
 
 
+class Reduction(enum.Enum):
+    """How a batched step combines one unit column's per-sample values
+    (traits.py:705-720): MEAN (the sum over the samples in order, then divided
+    by B; floating columns only), SUM (numeric, non-boolean), FIRST (sample
+    0), NOT_BATCHED (no per-sample phase may write the column; it keeps its
+    pre-step value)."""
+
+    MEAN = "mean"
+    SUM = "sum"
+    FIRST = "first"
+    NOT_BATCHED = "not_batched"
+
+
 class BatchReduction:
-    """How a batched step reduces per-sample unit columns (traits.py:705-871)."""
+    """A batch-reduction policy (traits.py:723-754): ``reduction(field)``
+    returns the column's Reduction, or None when it is undeclared. Any object
+    with a callable ``reduction`` satisfies it."""
+
+    def reduction(self, field: FieldSpec) -> "Reduction | None":
+        raise NotImplementedError
+
+    @classmethod
+    def __subclasshook__(cls, other: type) -> bool:
+        return callable(getattr(other, "reduction", None))
+
+
+class FieldReductions(BatchReduction):
+    """Declares unit columns one by one (traits.py:755-808)."""
+
+    def __init__(self, fields: Mapping[FieldSpec, Reduction]) -> None:
+        pairs = tuple(fields.items())
+        names: set[str] = set()
+        for spec, red in pairs:
+            if not isinstance(spec, FieldSpec):
+                raise TypeError(f"FieldReductions: {spec!r} is not a FieldSpec")
+            if not isinstance(red, Reduction):
+                raise TypeError(f"FieldReductions: {spec.name!r} maps to {red!r}, not a Reduction")
+            if spec.name in names:
+                raise ValueError(f"FieldReductions: {spec.name!r} declared twice")
+            names.add(spec.name)
+        self.fields = pairs
+
+    def reduction(self, field: FieldSpec) -> "Reduction | None":
+        for spec, red in self.fields:
+            if spec.name == field.name:
+                return red
+        return None
 
 
 class MeanFloatFirstRest(BatchReduction):
-    """Batch mean of floating columns, sample 0 of the rest."""
+    """MEAN for every floating unit column, FIRST for the others, NOT_BATCHED
+    for LEVEL and PRUNED (traits.py:811-834)."""
+
+    def reduction(self, field: FieldSpec) -> Reduction:
+        if field.name in _STRUCTURAL_UNIT_FIELDS:
+            return Reduction.NOT_BATCHED
+        if np.issubdtype(np.dtype(field.dtype), np.floating):
+            return Reduction.MEAN
+        return Reduction.FIRST
+
+
+# Unit columns only the structural phases write: never reduced over a batch.
+_STRUCTURAL_UNIT_FIELDS = frozenset({"level", "pruned"})
+
+
+def batch_written_reduction(policy: Any, field: FieldSpec, *, where: str) -> Reduction:
+    """The reduction of a column a per-sample phase writes, or ValueError
+    (traits.py:841-871)."""
+    red = policy.reduction(field)
+    if red is None:
+        raise ValueError(
+            f"batch_reduction: unit column {field.name!r} is written per sample ({where}) but the "
+            "batch-reduction policy does not declare it; declare it MEAN, SUM or FIRST (or set "
+            "batch_reduction = MeanFloatFirstRest())")
+    if red is Reduction.NOT_BATCHED:
+        raise ValueError(
+            f"batch_reduction: unit column {field.name!r} is declared NOT_BATCHED but is written "
+            f"per sample ({where})")
+    return red
 
 
 _RESERVED = frozenset(
@@ -201,3 +276,43 @@ def _validate_traits(cls: type) -> None:
         if not isinstance(spec, FieldSpec):
             raise TypeError(f"{cls.__name__}: extra fields must be FieldSpec, got {spec!r}")
         np.dtype(spec.dtype)
+    _validate_batch_reduction(cls)
+
+
+def _validate_batch_reduction(cls: type) -> None:
+    """The policy against the network's unit columns (traits.py:1177-1248)."""
+    policy = getattr(cls, "batch_reduction", None)
+    if policy is None:
+        return
+    if not callable(getattr(policy, "reduction", None)) or isinstance(policy, type):
+        raise TypeError(f"{cls.__name__}.batch_reduction must satisfy BatchReduction (reduction); got {policy!r}")
+    unit_fields = (ACTIVATION, LEVEL, *((PRUNED,) if cls.unit_capacity is not None else ()),
+                   *cls.extra_unit_fields)
+    if isinstance(policy, FieldReductions):
+        known = {spec.name for spec in unit_fields}
+        for spec, _ in policy.fields:
+            if spec.name not in known:
+                raise ValueError(f"{cls.__name__}.batch_reduction declares {spec.name!r}, which is not a unit "
+                                 f"column of the network ({sorted(known)})")
+    for spec in unit_fields:
+        red = policy.reduction(spec)
+        if red is None or red is Reduction.NOT_BATCHED:
+            continue
+        if not isinstance(red, Reduction):
+            raise TypeError(f"{cls.__name__}.batch_reduction.reduction({spec.name!r}) must return a Reduction "
+                            f"or None; got {red!r}")
+        if spec.name in _STRUCTURAL_UNIT_FIELDS:
+            raise ValueError(f"{cls.__name__}.batch_reduction: {spec.name!r} is written only by the structural "
+                             f"phases; declare it NOT_BATCHED or leave it undeclared, not {red.name}")
+        dt = np.dtype(spec.dtype)
+        if red is Reduction.MEAN and not np.issubdtype(dt, np.floating):
+            raise TypeError(f"{cls.__name__}.batch_reduction: MEAN needs a floating column; {spec.name!r} is {dt}")
+        if red is Reduction.SUM and (dt == np.bool_ or not np.issubdtype(dt, np.number)):
+            raise TypeError(f"{cls.__name__}.batch_reduction: SUM needs a numeric, non-boolean column; "
+                            f"{spec.name!r} is {dt}")
+    try:
+        batch_written_reduction(policy, ACTIVATION, where="the input scatter")
+        if cls.loss is not None:
+            batch_written_reduction(policy, cls.loss.seed_field, where="the loss's seed_field")
+    except ValueError as err:
+        raise ValueError(f"{cls.__name__}.{err}") from None

@@ -157,7 +157,7 @@ def build_golden(net, doc: dict[str, Any], device: str = "cpu"):
 
 def host_units(static, state) -> dict[str, np.ndarray]:
     return {
-        s.name: np.ascontiguousarray(column_to_numpy(state.units[s.name], s))
+        s.name: np.array(column_to_numpy(state.units[s.name], s), copy=True, order="C")
         for s in static.unit_fields
     }
 
@@ -165,7 +165,7 @@ def host_units(static, state) -> dict[str, np.ndarray]:
 def host_conns(static, state) -> list[dict[str, np.ndarray]]:
     specs = {s.name: s for s in static.conn_fields}
     return [
-        {n: np.ascontiguousarray(column_to_numpy(b[n], specs[n])) for n in specs}
+        {n: np.array(column_to_numpy(b[n], specs[n]), copy=True, order="C") for n in specs}
         for b in state.conns
     ]
 

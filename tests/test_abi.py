@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_descriptor_layouts_match_the_header(lib) -> None:
     n = len(_lib.STRUCTS)
     out = (ctypes.c_int64 * n)()
-    assert lib.plx_struct_sizes(out, n) == n == 14
+    assert lib.plx_struct_sizes(out, n) == n == 15
     assert list(out) == [ctypes.sizeof(s) for s in _lib.STRUCTS]
     assert lib.plx_abi_version() == _lib.ABI_VERSION
 
@@ -77,3 +77,22 @@ def test_argument_errors_are_reported_not_raised(lib) -> None:
     cd = _lib.plx_grow_claim_desc()
     cd.n_max = 0
     assert lib.plx_grow_claim(cd, None) == 0
+    # batched entry points
+    fd = _lib.plx_forward_desc()
+    fd.nrows = 3
+    assert lib.plx_forward_batch(fd, 0, None) == 1
+    assert b"batch must be >= 1" in lib.plx_last_error()
+    assert lib.plx_forward_batch(fd, 4, None) == 1
+    assert b"null column" in lib.plx_last_error()
+    bd = _lib.plx_bwd_batch_desc()
+    bd.batch, bd.nrows = 2, 0
+    assert lib.plx_backward_batch(bd, None) == 0
+    ud = _lib.plx_update_desc()
+    ud.n = 5
+    assert lib.plx_update_batch(ud, 2, None) == 1
+    assert b"null column" in lib.plx_last_error()
+    assert lib.plx_reduce_batch(4, 2, 0, 1, None, None, None) == 1
+    assert b"MEAN needs a float32" in lib.plx_last_error()
+    assert lib.plx_reduce_batch(4, 2, 1, 2, None, None, None) == 1
+    assert b"FIRST only" in lib.plx_last_error()
+    assert lib.plx_batch_mean(0, None, None, None) == 1

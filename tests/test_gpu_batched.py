@@ -1,0 +1,128 @@
+"""Batched steps on the device (make_step(batch_size=B), step.py:359-468):
+the forward / backward per sample, the exact batch-mean update, the batch
+reductions and the batch-mean loss must equal the batched oracle
+(oracle/batched.py) bit for bit -- every unit column, every connection
+column and the loss, at every step."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import batched_cases as bc
+import nets
+import plastax_amd as px
+from test_gpu_parity import _equal, assert_same_state
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(oracle, net, layers, keep, skip, B, steps, seed=0, onehot=False, headroom=0.0, check=None):
+    from oracle import batched as ob
+
+    static, state = bc.build(net, layers, keep, skip=skip, seed=seed, device="cuda", headroom=headroom)
+    o = nets.oracle_for(oracle, net, static, state)
+    o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
+    orc = ob.OracleBatch(o, B)
+    step = px.make_step(net, static, batch_size=B)
+    xs, ys = bc.data(seed + 1, steps, B, layers[0], layers[-1], onehot=onehot)
+    for k in range(steps):
+        print(f"batched step {k} B={B} layers={layers}", flush=True)
+        res = step(state, px.StepInputs(xs[k], ys[k]))
+        state = res.state
+        lo = orc.step(xs[k], ys[k])
+        if check is not None:
+            check(k, state, o)
+        torch.cuda.synchronize()
+        assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at step {k}: {float(res.loss)} vs {lo}"
+        assert_same_state(static, state, o, f"step {k}")
+    return state, o
+
+
+@pytest.mark.parametrize("B", [1, 3, 16, 70])
+def test_tanh_mse_adam_with_skip_edges(oracle, B: int) -> None:
+    opt = px.optim.adam(1e-2, nets.GRAD_PRE_ACT)
+    _run(oracle, bc.tanh_mse_net(opt), [20, 48, 40, 8], 0.3, 0.05, B, 4)
+
+
+@pytest.mark.parametrize("rule", ["sgd", "momentum", "rmsprop", "adamw"])
+def test_every_rule_on_the_batch_mean(oracle, rule: str) -> None:
+    make = {
+        "sgd": lambda: px.optim.sgd(0.05, nets.GRAD_PRE_ACT),
+        "momentum": lambda: px.optim.momentum(0.05, 0.9, nets.GRAD_PRE_ACT),
+        "rmsprop": lambda: px.optim.rmsprop(1e-3, nets.GRAD_PRE_ACT),
+        "adamw": lambda: px.optim.adamw(1e-3, nets.GRAD_PRE_ACT, weight_decay=1e-2),
+    }[rule]
+    _run(oracle, bc.tanh_mse_net(make()), [16, 32, 8], 0.4, 0.0, 8, 3, seed=2)
+
+
+def test_c3_shaped_softmax_batch(oracle) -> None:
+    """C3's shape scaled down: 784-128-128-10 at 10 % keep, B = 256,
+    softmax cross-entropy, Adam."""
+    opt = px.optim.adam(1e-3, nets.GRAD_PRE_ACT)
+    _run(oracle, bc.softmax_net(opt), [784, 128, 128, 10], 0.1, 0.0, 256, 2, seed=4, onehot=True)
+
+
+def test_structural_phases_run_once_per_batch(oracle) -> None:
+    """tests/test_batched.py:189-229: prune and growth see the reduced state,
+    once per batched step."""
+
+    class TauPrune(px.PruneConn):
+        def predicate(self, u, c, cid, g):
+            return px.numpy.abs(c[px.WEIGHT, cid]) < np.float32(0.02)
+
+    class Grow(px.ScoreAddConn):
+        candidates = "shortlist_per_level"
+        shortlist_size = 8
+        direction = "deeper"
+        dedupe_live = True
+        max_new_per_level = 10
+
+        def score(self, u, src, dst, g):
+            return px.numpy.abs(u[px.ACTIVATION, src] * u[nets.GRAD_PRE_ACT, dst])
+
+        def importance(self, u, i, g):
+            return px.numpy.abs(u[nets.GRAD_PRE_ACT, i]) + px.numpy.abs(u[px.ACTIVATION, i])
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of((px.WEIGHT, np.float32(0.0)))
+
+    opt = px.optim.sgd(0.05, nets.GRAD_PRE_ACT)
+
+    class Net(bc.tanh_mse_net(opt)):
+        prune_conn = TauPrune()
+        add_conn = Grow()
+
+    grown = []
+
+    def check(k, state, o):
+        assert (state.grown, state.overflow) == (o.grown, o.overflow), f"flags at step {k}"
+        grown.append(state.grown)
+
+    _run(oracle, Net, [16, 40, 30, 6], 0.3, 0.0, 5, 4, seed=5, headroom=0.5, check=check)
+    assert sum(grown) > 0
+
+
+def test_policy_and_shape_errors() -> None:
+    opt = px.optim.sgd(0.05, nets.GRAD_PRE_ACT)
+
+    class Partial(px.Network):
+        forward_pass = nets.TanhForward()
+        backward_pass = nets.TanhBackward()
+        loss = nets.MSELoss()
+        update_conn = opt.update_conn()
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD)
+        batch_reduction = px.FieldReductions({px.ACTIVATION: px.Reduction.MEAN,
+                                              nets.LOSS_GRAD: px.Reduction.MEAN})
+
+    static, state = bc.build(Partial, [6, 5, 3], 1.0, device="cuda")
+    step = px.make_step(Partial, static, batch_size=2)
+    xs, ys = bc.data(0, 1, 2, 6, 3)
+    with pytest.raises(ValueError, match=r"'grad_pre_act'.*backward_pass.*not declare"):
+        step(state, px.StepInputs(xs[0], ys[0]))
+    net = bc.tanh_mse_net(opt)
+    static, state = bc.build(net, [6, 5, 3], 1.0, device="cuda")
+    step = px.make_step(net, static, batch_size=4)
+    with pytest.raises(ValueError, match="inputs must be"):
+        step(state, px.StepInputs(xs[0], ys[0]))
