@@ -298,10 +298,180 @@ def run_c5_growth(args) -> int:
     return 0
 
 
+C3_METRIC = "samples/sec per batched step (fwd+bwd+update, B=256) of C3's 784-4096-4096-10 sparse MLP"
+
+
+def build_c3(px):
+    grad = px.FieldSpec.float32("grad_pre_act")
+    lossg = px.FieldSpec.float32("loss_grad")
+    import plastax_amd.numpy as jnp
+
+    class ReluForward(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.maximum(acc, jnp.float32(0.0))))
+
+    class ReluBackward(px.BackwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, src, dst, c, cid, g):
+            return c[px.WEIGHT, cid] * u[grad, dst]
+
+        def apply(self, u, i, g, acc):
+            gate = jnp.where(u[px.ACTIVATION, i] > 0, jnp.float32(1.0), jnp.float32(0.0))
+            return px.UnitWrite.of((grad, (acc + u[lossg, i]) * gate))
+
+    opt = px.optim.adam(1e-3, grad)
+
+    class C3Net(px.Network):
+        forward_pass = ReluForward()
+        backward_pass = ReluBackward()
+        loss = px.SoftmaxCrossEntropyLoss(lossg)
+        update_conn = opt.update_conn()
+        extra_unit_fields = (grad, lossg)
+        extra_conn_fields = tuple(opt.state_fields)
+        batch_reduction = px.MeanFloatFirstRest()
+
+    return C3Net
+
+
+def run_c3(args) -> int:
+    """C3: the batched step (B = 256) of the 784-4096-4096-10 sparse MLP."""
+    import torch
+
+    import plastax_amd as px
+    from plastax_amd import synth
+    from plastax_amd.state import column_to_numpy
+
+    B = 256
+    t_setup = time.perf_counter()
+    net = build_c3(px)
+    e = synth.c3_mlp(args.seed)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, device="cpu")
+    specs = {s.name: s for s in static.conn_fields}
+    host_units = {s.name: column_to_numpy(state.units[s.name], s).copy() for s in static.unit_fields}
+    host_conns = [{n: column_to_numpy(b[n], specs[n]).copy() for n in specs} for b in state.conns]
+    dev = torch.device("cuda", 0)
+    gstate = px.NetworkState(
+        {k: v.to(dev) for k, v in state.units.items()},
+        tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
+        None,
+    )
+    step = px.make_step(net, static, batch_size=B)
+    nsteps = args.warmup + args.steps
+    xs, ys = synth.c3_batches(args.seed, nsteps, B)
+    xs_d, ys_d = torch.from_numpy(xs).to(dev), torch.from_numpy(ys).to(dev)
+    step.arena(gstate)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    progress(f"C3: {e.src.size} edges, B = {B} ({setup_s:.1f} s)")
+    for k in range(args.warmup):
+        gstate = step(gstate, px.StepInputs(xs_d[k], ys_d[k])).state
+    torch.cuda.synchronize()
+    dominant = "update_conn"
+    timer = EventTimer({dominant})
+    step.timer = timer
+    timer.on = True
+    t0 = time.perf_counter()
+    last = None
+    for k in range(args.warmup, nsteps):
+        last = step(gstate, px.StepInputs(xs_d[k], ys_d[k]))
+        gstate = last.state
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.on = False
+    dom = timer.summary()[dominant]
+    breakdown = EventTimer()
+    step.timer = breakdown
+    breakdown.on = True
+    for k in range(min(3, nsteps)):
+        gstate = step(gstate, px.StepInputs(xs_d[k], ys_d[k])).state
+    breakdown.on = False
+    step.timer = None
+    kernels = breakdown.summary()
+    for k in kernels.values():
+        k["total_ms"] = round(k["total_ms"], 3)
+        k["mean_ms"] = round(k["mean_ms"], 4)
+    edges = int(e.src.size)
+    ms = elapsed * 1e3 / args.steps
+    # The batch-mean update reads every edge's columns once (FROM_ID, TO_ID,
+    # DEAD, WEIGHT, m, v, t: 25 B) and writes WEIGHT, m, v, t (16 B), and
+    # gathers two B-wide unit rows per live edge (2 * 4 * B bytes, L2-served).
+    per_launch_hbm = 41 * edges * args.steps / dom["launches"]
+    per_launch_rows = 8 * B * edges * args.steps / dom["launches"]
+    ach = per_launch_hbm / (dom["mean_ms"] * 1e-3) / 1e9
+    roofline = {
+        "kernel": "update_conn (plx_update_batch)",
+        "bound": "hbm",
+        "achieved": round(ach, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "algorithmic_bytes_per_launch": int(per_launch_hbm),
+        "gathered_row_bytes_per_launch": int(per_launch_rows),
+        "mean_launch_ms": round(dom["mean_ms"], 4),
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import batched as ob
+        from oracle import oracle as ox
+        from plastax_amd._plan import compile_plan
+
+        ox.load()
+        o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), None)
+        orc = ob.OracleBatch(o, B)
+        t1 = time.perf_counter()
+        orc.step(xs[0], ys[0])
+        sec = time.perf_counter() - t1
+        cpu = {
+            "value": float(B / sec),
+            "unit": "samples/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"1 batched step of the same workload (B = 256), {sec:.1f} s, the C oracle per sample "
+            "plus numpy batch reductions (oracle/batched.py), one thread",
+        }
+    line = {
+        "metric": C3_METRIC,
+        "value": round(B / (ms * 1e-3), 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3: 784-4096-4096-10 sparse MLP (10 % keep), ReLU, softmax CE, Adam(1e-3), B = 256",
+            "edges": edges,
+            "batch": B,
+            "edge_samples_per_s": round(edges * B / (ms * 1e-3), 1),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "loss_last": float(last.loss),
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=("c2", "c5_growth"), default="c2",
-                    help="c2: the streaming step (the headline metric); c5_growth: the add_conn phase")
+    ap.add_argument("--workload", choices=("c2", "c3", "c5_growth"), default="c2",
+                    help="c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
+                    "c5_growth: the add_conn phase")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
@@ -325,6 +495,8 @@ def main() -> int:
 
     if args.workload == "c5_growth":
         return run_c5_growth(args)
+    if args.workload == "c3":
+        return run_c3(args)
 
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4

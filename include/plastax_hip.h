@@ -251,11 +251,13 @@ PLX_EXPORT int plx_forward_batch(const plx_forward_desc* d, int32_t batch, void*
 
 /* Backward of one bucket for B samples (build_csr_backward, phases.py:843-934,
  * and the reference's per-sample scatter order): row r is source unit
- * row_unit[r]; its live out-edges are the physical positions
- * pos[row_ptr[r] .. row_ptr[r+1]) in logical slot order, each contributing
- * weight[p] * g[dst[p] * B + b] (pre-update weights), folded in that order
- * from the identity, combined into acc (null: the identity) and, where the
- * row finalizes, `apply` runs (fields and outs batched) and acc resets. */
+ * row_unit[r]; its out-edges are the list entries j in [row_ptr[r],
+ * row_ptr[r+1]) in logical slot order, entry j contributing weight[j] *
+ * g[dst[j] * B + b] (pre-update weights) where live[j] is nonzero, folded in
+ * that order from the identity, combined into acc (null: the identity) and,
+ * where the row finalizes, `apply` runs (fields and outs batched) and acc
+ * resets. The lists are slot-ordered copies of the arena's columns
+ * (plx_gather_edges). */
 typedef struct plx_bwd_batch_desc {
   int32_t nrows;
   int32_t monoid;
@@ -263,17 +265,21 @@ typedef struct plx_bwd_batch_desc {
   int32_t reserved;
   const int32_t* row_unit;
   const int32_t* row_ptr;
-  const int32_t* pos;
-  const int32_t* dst;
-  const float* weight;
-  const uint8_t* dead; /* tombstones set since the lists were built, or null */
-  const float* g;      /* [num_units][B] the map's linear_input field */
-  float* acc;          /* [num_units][B] carried accumulator, or null */
+  const int32_t* dst;    /* [entries] TO_ID */
+  const float* weight;   /* [entries] WEIGHT */
+  const uint8_t* live;   /* [entries] 0: skipped (null: every entry live) */
+  const float* g;        /* [num_units][B] the map's linear_input field */
+  float* acc;            /* [num_units][B] carried accumulator, or null */
   plx_finalize fin;
   plx_program apply;
 } plx_bwd_batch_desc;
 
 PLX_EXPORT int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream);
+
+/* out_weight[j] = weight[pos[j]], out_live[j] = !dead[pos[j]] for j < n
+ * (dead null: all live): a bucket's backward lists in slot order. */
+PLX_EXPORT int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,
+                                float* out_weight, uint8_t* out_live, void* stream);
 
 /* The exact batched connection update (build_batched_update_conn,
  * phases.py:390-483): per live position, stat_b = gfield[dst * B + b] *

@@ -179,10 +179,9 @@ class plx_bwd_batch_desc(ctypes.Structure):
         ("reserved", c_i32),
         ("row_unit", c_vp),
         ("row_ptr", c_vp),
-        ("pos", c_vp),
         ("dst", c_vp),
         ("weight", c_vp),
-        ("dead", c_vp),
+        ("live", c_vp),
         ("g", c_vp),
         ("acc", c_vp),
         ("fin", plx_finalize),
@@ -341,6 +340,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_batch": (c_i32, [ctypes.POINTER(plx_forward_desc), c_i32, c_vp]),
     "plx_backward_batch": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
     "plx_update_batch": (c_i32, [ctypes.POINTER(plx_update_desc), c_i32, c_vp]),
+    "plx_gather_edges": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_loss_elementwise_batch": (
         c_i32,
         [c_i32, c_vp, c_vp, ctypes.POINTER(plx_program), c_vp, c_vp, c_vp, c_i32, c_vp],

@@ -45,14 +45,22 @@ _REDUCE = {Reduction.MEAN: 0, Reduction.SUM: 1, Reduction.FIRST: 2}
 
 
 class BatchSources:
-    """Per bucket, its backward rows (sources) and their live out-edge
-    positions in logical slot order (``pos[ptr[r] .. ptr[r+1])``)."""
+    """Per bucket, its backward rows (sources) and their out-edge lists in
+    logical slot order: list entry j (``ptr[r] <= j < ptr[r+1]``) is physical
+    position ``pos[j]``, whose TO_ID ``dst[j]`` is fixed with the layout; the
+    step gathers the entries' weights and liveness into ``weight`` / ``live``
+    (one wide gather), so the backward reads every list sequentially."""
 
-    def __init__(self, nrows: int, rows: torch.Tensor, ptr: torch.Tensor, pos: torch.Tensor) -> None:
+    def __init__(self, nrows: int, rows: torch.Tensor, ptr: torch.Tensor, pos: torch.Tensor,
+                 dst: torch.Tensor) -> None:
         self.nrows = nrows
         self.rows = rows
         self.ptr = ptr
         self.pos = pos
+        self.dst = dst
+        n = int(pos.numel())
+        self.weight = torch.empty(n, dtype=torch.float32, device=pos.device)
+        self.live = torch.empty(n, dtype=torch.uint8, device=pos.device)
 
 
 def batch_sources(arena: Arena, b: int) -> BatchSources:
@@ -64,6 +72,7 @@ def batch_sources(arena: Arena, b: int) -> BatchSources:
         return cache[b]
     base, live = arena.bases[b], arena.lives[b]
     src = arena.cols["from_id"][base : base + live].cpu().numpy().astype(np.int64)
+    dst_all = arena.cols["to_id"][base : base + live].cpu().numpy().astype(np.int64)
     slot = arena.slot[base : base + live].cpu().numpy().astype(np.int64)
     if b + 1 < arena.lvl_start.size:
         level_units = np.arange(int(arena.lvl_start[b]), int(arena.lvl_start[b + 1]), dtype=np.int64)
@@ -79,7 +88,8 @@ def batch_sources(arena: Arena, b: int) -> BatchSources:
         int(rows.size),
         torch.from_numpy(rows.astype(np.int32)).to(dev),
         torch.from_numpy(ptr.astype(np.int32)).to(dev),
-        torch.from_numpy(np.concatenate([pos, [0]]).astype(np.int32)).to(dev),
+        torch.from_numpy(np.concatenate([pos, [base]]).astype(np.int32)).to(dev),
+        torch.from_numpy(np.concatenate([dst_all[order], [0]]).astype(np.int32)).to(dev),
     )
     cache[b] = out
     return out
@@ -238,17 +248,16 @@ class BatchedStepFn(StepFn):
             bprog = program_struct(bp.program, ub, g)
             empty = torch.zeros(1, dtype=torch.int32, device=dev)
 
-            def run(rows: torch.Tensor, nrows: int, ptr: torch.Tensor, pos: torch.Tensor, level: int) -> None:
+            def run(rows: torch.Tensor, nrows: int, ptr: torch.Tensor, lists: Any, level: int) -> None:
                 d = _lib.plx_bwd_batch_desc()
                 d.nrows = nrows
                 d.monoid = bp.monoid
                 d.batch = B
                 d.row_unit = rows.data_ptr()
                 d.row_ptr = ptr.data_ptr()
-                d.pos = pos.data_ptr()
-                d.dst = arena.cols["to_id"].data_ptr()
-                d.weight = arena.cols["weight"].data_ptr()
-                d.dead = arena.cols["dead"].data_ptr()
+                d.dst = lists.dst.data_ptr()
+                d.weight = lists.weight.data_ptr()
+                d.live = lists.live.data_ptr()
                 d.g = ub[bp.field].data_ptr()
                 d.acc = bacc.data_ptr() if bacc is not None else None
                 d.fin.level, d.fin.is_input, d.fin.pruned = fin["level"], fin["is_input"], fin["pruned"]
@@ -261,10 +270,18 @@ class BatchedStepFn(StepFn):
             top = arena.top
             if top.nrows:
                 zeros = torch.zeros(top.nrows + 1, dtype=torch.int32, device=dev)
-                run(top.rows, top.nrows, zeros, empty, nb)
+                none = BatchSources(0, empty, empty, empty, empty)
+                run(top.rows, top.nrows, zeros, none, nb)
             for b in range(nb - 1, 0, -1):
-                src_rows = batch_sources(arena, b)
-                run(src_rows.rows, src_rows.nrows, src_rows.ptr, src_rows.pos, b)
+                lists = batch_sources(arena, b)
+                # This step's (pre-update) weights and tombstones, in slot order.
+                _lib.check(
+                    lib.plx_gather_edges(lists.pos.numel(), lists.pos.data_ptr(), arena.cols["weight"].data_ptr(),
+                                         arena.cols["dead"].data_ptr(), lists.weight.data_ptr(),
+                                         lists.live.data_ptr(), stream),
+                    "plx_gather_edges",
+                )
+                run(lists.rows, lists.nrows, lists.ptr, lists, b)
 
         # The connection update on the batch-mean gradient (phases.py:434-483).
         up = plan.update

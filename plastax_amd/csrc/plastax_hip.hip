@@ -1100,16 +1100,14 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_de
     float s = ident;
     int j = j0;
     for (; j + kBatchUnroll <= j1; j += kBatchUnroll) {
-      int pv[kBatchUnroll], tv[kBatchUnroll];
+      int tv[kBatchUnroll];
       float wv[kBatchUnroll], gv[kBatchUnroll];
       bool live[kBatchUnroll];
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k) pv[k] = d.pos[j + k];
-#pragma unroll
       for (int k = 0; k < kBatchUnroll; ++k) {
-        tv[k] = d.dst[pv[k]];
-        wv[k] = d.weight[pv[k]];
-        live[k] = d.dead ? d.dead[pv[k]] == 0 : true;
+        tv[k] = d.dst[j + k];
+        wv[k] = d.weight[j + k];
+        live[k] = d.live ? d.live[j + k] != 0 : true;
       }
 #pragma unroll
       for (int k = 0; k < kBatchUnroll; ++k) gv[k] = d.g[static_cast<int64_t>(tv[k]) * B + bl];
@@ -1118,22 +1116,48 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_de
         if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
     }
     for (; j < j1; ++j) {
-      const int p = d.pos[j];
-      if (d.dead && d.dead[p]) continue;
-      s = Mono<M>::op(s, d.weight[p] * d.g[static_cast<int64_t>(d.dst[p]) * B + bl]);
+      if (d.live && !d.live[j]) continue;
+      s = Mono<M>::op(s, d.weight[j] * d.g[static_cast<int64_t>(d.dst[j]) * B + bl]);
     }
     if (b < B) finish_batch<M>(d.acc, d.apply, fin, static_cast<int64_t>(u) * B + b, s);
   }
 }
 
-// The batch-mean gradient of one position: stat_0 + stat_1 + ... in sample
-// order, divided by B (phases.py:434-483).
+__global__ void k_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,
+                               float* out_w, uint8_t* out_live) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int p = pos[j];
+  out_w[j] = weight[p];
+  if (out_live) out_live[j] = dead ? (dead[p] == 0) : 1;
+}
+
+// The batched update, one lane per position: its batch-mean gradient is
+// stat_0 + stat_1 + ... in sample order, / B (phases.py:462-471), with
+// stat_b = gfield[dst * B + b] * act[src * B + b], then the update rule.
+// The two B-wide rows are read in 16-byte slices, 32 samples' slices in
+// flight per step of the sequential sum (consecutive positions share their
+// destination row).
 __device__ __forceinline__ float batch_mean_grad(const float* g, const float* a, int32_t B) {
   float total = g[0] * a[0];
   int b = 1;
   if ((B & 3) == 0) {
-    // 16-byte reads once the rows are aligned (B a multiple of 4).
     for (; b < 4; ++b) total = total + g[b] * a[b];
+    for (; b + 32 <= B; b += 32) {
+      float4 gv[8], av[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        gv[k] = *reinterpret_cast<const float4*>(g + b + 4 * k);
+        av[k] = *reinterpret_cast<const float4*>(a + b + 4 * k);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        total = total + gv[k].x * av[k].x;
+        total = total + gv[k].y * av[k].y;
+        total = total + gv[k].z * av[k].z;
+        total = total + gv[k].w * av[k].w;
+      }
+    }
     for (; b + 4 <= B; b += 4) {
       const float4 gv = *reinterpret_cast<const float4*>(g + b);
       const float4 av = *reinterpret_cast<const float4*>(a + b);
@@ -1141,6 +1165,17 @@ __device__ __forceinline__ float batch_mean_grad(const float* g, const float* a,
       total = total + gv.y * av.y;
       total = total + gv.z * av.z;
       total = total + gv.w * av.w;
+    }
+  } else {
+    for (; b + 8 <= B; b += 8) {
+      float gv[8], av[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        gv[k] = g[b + k];
+        av[k] = a[b + k];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) total = total + gv[k] * av[k];
     }
   }
   for (; b < B; ++b) total = total + g[b] * a[b];
@@ -1180,8 +1215,18 @@ __global__ void k_reduce_batch(int64_t n, int32_t B, int32_t mode, const T* src,
   if (u >= n) return;
   const T* x = src + u * B;
   T s = x[0];
-  if (mode != PLX_REDUCE_FIRST)
-    for (int b = 1; b < B; ++b) s = s + x[b];
+  if (mode != PLX_REDUCE_FIRST) {
+    // Eight samples' loads in flight per step of the sequential sum.
+    int b = 1;
+    for (; b + 8 <= B; b += 8) {
+      T v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = x[b + k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s = s + v[k];
+    }
+    for (; b < B; ++b) s = s + x[b];
+  }
   if (mode == PLX_REDUCE_MEAN) s = s / static_cast<T>(B);
   dst[u] = s;
 }
@@ -1667,7 +1712,7 @@ int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream) {
   if (d->batch < 1) return fail(PLX_ERR_INVALID, "plx_backward_batch: batch must be >= 1");
   if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_batch: negative nrows");
   if (d->nrows == 0) return PLX_OK;
-  if (!d->row_unit || !d->row_ptr || !d->pos || !d->dst || !d->weight || !d->g)
+  if (!d->row_unit || !d->row_ptr || !d->dst || !d->weight || !d->g)
     return fail(PLX_ERR_INVALID, "plx_backward_batch: null column");
   if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_batch: bad program");
   if (!d->fin.level || !d->fin.is_input)
@@ -1684,6 +1729,16 @@ int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream) {
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_batch: unknown monoid");
   }
   return check_launch("plx_backward_batch");
+}
+
+int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,
+                     float* out_weight, uint8_t* out_live, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_gather_edges: negative n");
+  if (n == 0) return PLX_OK;
+  if (!pos || !weight || !out_weight) return fail(PLX_ERR_INVALID, "plx_gather_edges: null pointer");
+  k_gather_edges<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(n, pos, weight, dead,
+                                                                                  out_weight, out_live);
+  return check_launch("plx_gather_edges");
 }
 
 int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream) {

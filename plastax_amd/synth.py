@@ -6,6 +6,10 @@ reproducible on any host:
 
 - C1: 1,024 units; 16,384 edges with uniform src/dst and no self-loops;
   PIPELINE tanh; 32 inputs, 8 outputs; weights N(0, 1/fan_in).
+- C3: the batched sparse MLP 784-4096-4096-10 with each layer pair's
+  dense edges kept with probability 0.1 (about 2.0M edges), weights
+  N(0, 1/fan_in); inputs uniform in [0, 1); labels the argmax of a fixed
+  random linear teacher of the inputs.
 - C2: 8 layers x 131,072 units (layer 0 = inputs, layer 7 = outputs);
   2^26 edges between consecutive layers, fan-in 73 plus one more for every
   7th destination; each destination's sources are drawn without replacement
@@ -123,6 +127,35 @@ def c2_topological(seed: int = 0, scale: int = 1, layers: int = 8) -> EdgeList:
         np.arange(width, dtype=np.int32),
         np.arange((layers - 1) * width, layers * width, dtype=np.int32),
     )
+
+
+def c3_mlp(seed: int = 0, layers: tuple[int, ...] = (784, 4096, 4096, 10), keep: float = 0.1) -> EdgeList:
+    """C3's sparse MLP (each dense layer pair's edge kept w.p. ``keep``)."""
+    rng = np.random.default_rng(seed)
+    base = np.concatenate([[0], np.cumsum(layers)])
+    src_all, dst_all = [], []
+    for l in range(len(layers) - 1):
+        m = rng.random((layers[l], layers[l + 1])) < keep
+        ii, jj = np.nonzero(m)
+        src_all.append((base[l] + ii).astype(np.int32))
+        dst_all.append((base[l + 1] + jj).astype(np.int32))
+    src = np.concatenate(src_all)
+    dst = np.concatenate(dst_all)
+    fan = np.bincount(dst, minlength=int(base[-1]))
+    w = (rng.standard_normal(src.size) / np.sqrt(np.maximum(fan[dst], 1))).astype(np.float32)
+    return EdgeList(int(base[-1]), src, dst, w, np.arange(layers[0], dtype=np.int32),
+                    np.arange(base[-2], base[-1], dtype=np.int32))
+
+
+def c3_batches(seed: int, steps: int, batch: int, n_in: int = 784, n_out: int = 10):
+    """C3's synthetic batches: inputs uniform in [0, 1), one-hot labels of a
+    fixed random linear teacher's argmax."""
+    rng = np.random.default_rng(seed + 1)
+    teacher = rng.standard_normal((n_out, n_in)).astype(np.float32)
+    xs = rng.random((steps, batch, n_in)).astype(np.float32)
+    lab = np.argmax(xs @ teacher.T, axis=-1)
+    ys = np.eye(n_out, dtype=np.float32)[lab]
+    return xs, ys
 
 
 def c2_target(seed: int, width: int):

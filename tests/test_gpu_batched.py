@@ -126,3 +126,22 @@ def test_policy_and_shape_errors() -> None:
     step = px.make_step(net, static, batch_size=4)
     with pytest.raises(ValueError, match="inputs must be"):
         step(state, px.StepInputs(xs[0], ys[0]))
+
+
+def test_sum_first_and_mean_reductions(oracle) -> None:
+    """reduce_batch_units (phases.py:298-332) in all three modes: the input
+    scatter's and forward's ACTIVATION summed, the loss seed from sample 0,
+    the backward's grads averaged."""
+    opt = px.optim.sgd(0.05, nets.GRAD_PRE_ACT)
+
+    class Net(px.Network):
+        forward_pass = nets.TanhForward()
+        backward_pass = nets.TanhBackward()
+        loss = nets.MSELoss()
+        update_conn = opt.update_conn()
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD)
+        batch_reduction = px.FieldReductions({px.ACTIVATION: px.Reduction.SUM,
+                                              nets.LOSS_GRAD: px.Reduction.FIRST,
+                                              nets.GRAD_PRE_ACT: px.Reduction.MEAN})
+
+    _run(oracle, Net, [10, 24, 6], 0.5, 0.0, 5, 3, seed=6)
