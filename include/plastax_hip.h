@@ -276,6 +276,12 @@ typedef struct plx_bwd_batch_desc {
 
 PLX_EXPORT int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream);
 
+/* The streaming backward of one bucket over the same slot-ordered lists
+ * (batch must be 1): one lane per row, each folding its list in slot order
+ * (the reference's per-source scatter order, sweep.py:343-399). Used by the
+ * churn layout, which rebuilds on the device after every structural change. */
+PLX_EXPORT int plx_backward_lists(const plx_bwd_batch_desc* d, void* stream);
+
 /* out_weight[j] = weight[pos[j]], out_live[j] = !dead[pos[j]] for j < n
  * (dead null: all live): a bucket's backward lists in slot order. */
 PLX_EXPORT int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,

@@ -341,6 +341,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_backward_batch": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
     "plx_update_batch": (c_i32, [ctypes.POINTER(plx_update_desc), c_i32, c_vp]),
     "plx_gather_edges": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_backward_lists": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
     "plx_loss_elementwise_batch": (
         c_i32,
         [c_i32, c_vp, c_vp, ctypes.POINTER(plx_program), c_vp, c_vp, c_vp, c_i32, c_vp],

@@ -119,7 +119,7 @@ class BatchedStepFn(StepFn):
         if plan.update_unit:
             raise UnsupportedPolicyError("a batched step with update_unit is not in this build yet")
         self.batch = int(batch_size)
-        self._checked = False
+        self.arena_mode = "tiled"  # the batched kernels read the tiled layout's forward rows
 
     def _check_policy(self) -> dict[str, Reduction]:
         """Every column a per-sample phase writes has a MEAN / SUM / FIRST

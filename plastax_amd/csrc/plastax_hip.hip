@@ -1123,6 +1123,46 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_de
   }
 }
 
+// Streaming backward over slot-ordered lists: lane = row (source unit),
+// folding its list in order from the identity, then the finalize.
+template <int M>
+__global__ __launch_bounds__(kBatchBlock) void k_backward_lists(plx_bwd_batch_desc d) {
+  const int r = blockIdx.x * kBatchBlock + threadIdx.x;
+  if (r >= d.nrows) return;
+  const int u = d.row_unit[r];
+  const int j0 = d.row_ptr[r], j1 = d.row_ptr[r + 1];
+  RowPre pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+  float s = Mono<M>::id();
+  int j = j0;
+  for (; j + 4 <= j1; j += 4) {
+    int tv[4];
+    float wv[4], gv[4];
+    bool live[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      tv[k] = d.dst[j + k];
+      wv[k] = d.weight[j + k];
+      live[k] = d.live ? d.live[j + k] != 0 : true;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gv[k] = d.g[tv[k]];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
+  }
+  for (; j < j1; ++j) {
+    if (d.live && !d.live[j]) continue;
+    s = Mono<M>::op(s, d.weight[j] * d.g[d.dst[j]]);
+  }
+  const float a = Mono<M>::op(d.acc ? d.acc[u] : Mono<M>::id(), s);
+  if (pre.fin) {
+    run_program(d.apply, u, pre.f, a, 0.0f, true);
+    if (d.acc) d.acc[u] = Mono<M>::id();
+  } else if (d.acc) {
+    d.acc[u] = a;
+  }
+}
+
 __global__ void k_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,
                                float* out_w, uint8_t* out_live) {
   const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1729,6 +1769,28 @@ int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream) {
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_batch: unknown monoid");
   }
   return check_launch("plx_backward_batch");
+}
+
+int plx_backward_lists(const plx_bwd_batch_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_backward_lists: null descriptor");
+  if (d->batch != 1) return fail(PLX_ERR_INVALID, "plx_backward_lists: batch must be 1");
+  if (d->nrows < 0) return fail(PLX_ERR_INVALID, "plx_backward_lists: negative nrows");
+  if (d->nrows == 0) return PLX_OK;
+  if (!d->row_unit || !d->row_ptr || !d->dst || !d->weight || !d->g)
+    return fail(PLX_ERR_INVALID, "plx_backward_lists: null column");
+  if (!program_ok(d->apply)) return fail(PLX_ERR_INVALID, "plx_backward_lists: bad program");
+  if (!d->fin.level || !d->fin.is_input)
+    return fail(PLX_ERR_INVALID, "plx_backward_lists: fin.level and fin.is_input are required");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(d->nrows, kBatchBlock);
+  switch (d->monoid) {
+    case PLX_MONOID_SUM: k_backward_lists<PLX_MONOID_SUM><<<grid, kBatchBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_PROD: k_backward_lists<PLX_MONOID_PROD><<<grid, kBatchBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MAX: k_backward_lists<PLX_MONOID_MAX><<<grid, kBatchBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_MIN: k_backward_lists<PLX_MONOID_MIN><<<grid, kBatchBlock, 0, s>>>(*d); break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_backward_lists: unknown monoid");
+  }
+  return check_launch("plx_backward_lists");
 }
 
 int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,

@@ -104,6 +104,11 @@ class StepFn:
         # the arenas this step builds.
         self.tile: int = TILE
         self.nsuper: int = NSUPER
+        # The arena layout: "tiled" (host-built tiles: the fast streaming
+        # backward), "churn" (rebuilt on the device after every structural
+        # change; the backward folds each source's edges in slot order), or
+        # "auto": churn when growth fires every step.
+        self.arena_mode: str = "auto"
         # Unit and structural phases, traced on the first step (their
         # programs read the globals' structure).
         self._update_unit: Any = None
@@ -136,13 +141,37 @@ class StepFn:
         c["is_input"] = arena.is_input
         return c
 
+    def churn(self) -> bool:
+        """Whether this step lays its arena out with the churn layout."""
+        if self.arena_mode != "auto":
+            if self.arena_mode not in ("tiled", "churn"):
+                raise ValueError(f"arena_mode must be 'auto', 'tiled' or 'churn', got {self.arena_mode!r}")
+            return self.arena_mode == "churn"
+        cfg = self.plan.add_conn
+        if cfg is None:
+            return False
+        every = cfg.trigger == "every_step" or (isinstance(cfg.trigger, tuple) and int(cfg.trigger[1]) == 1)
+        return every and int(getattr(self.plan.net, "structural_interval", 1)) == 1
+
+    @property
+    def backward_order(self) -> str:
+        """"slot": each source's terms in logical slot order (the churn
+        layout); "tiled": the tiled layout's tile / superblock order."""
+        return "slot" if self.churn() else "tiled"
+
     def arena(self, state: NetworkState) -> Arena:
         """The state's physical arena (built on first use)."""
         if state._arena is None:
-            state._arena = Arena(
-                self.static, state.units, state._conns, state.device, tile=self.tile,
-                nsuper=self.nsuper,
-            )
+            if self.churn():
+                from plastax_amd._churn import ChurnArena
+
+                state._arena = ChurnArena(self.static, state.units, state._conns, state.device,
+                                          _stream(state.device))
+            else:
+                state._arena = Arena(
+                    self.static, state.units, state._conns, state.device, tile=self.tile,
+                    nsuper=self.nsuper,
+                )
             up = self.plan.update
             if up is not None and up.rule_code == 2:
                 state._arena.init_uniform_t(up.state_columns()[2])
@@ -455,10 +484,73 @@ class StepFn:
         d.apply = prog
         self._launch("backward_finalize", lib.plx_backward_partials, d, stream)
 
+    def _backward_lists(self, plan: Plan, arena: Any, units: dict, fin_common: dict, stream: int,
+                        g: Any) -> None:
+        """The churn layout's backward: per bucket, every unit a row folding
+        its live out-edges in slot order (sweep.py:343-449)."""
+        lib = _lib.load()
+        bp = plan.backward
+        dev = arena.device
+        n = self.static.num_units
+        nb = arena.num_buckets
+        swaps = self._shadow(units, bp.program.out_fields) if arena.pipeline else {}
+        acc = torch.empty(n, dtype=torch.float32, device=dev)
+        _lib.call("plx_fill_f32", n, bp.identity, acc.data_ptr(), stream)
+        prog = program_struct(bp.program, units, g, out_override=swaps)
+        rows = arena.fwd[0].rows
+
+        def run(lists: Any, level: int, skip_inputs: int) -> None:
+            d = _lib.plx_bwd_batch_desc()
+            d.nrows = n
+            d.monoid = bp.monoid
+            d.batch = 1
+            d.row_unit = rows.data_ptr()
+            if lists is None:
+                zeros = torch.zeros(n + 1, dtype=torch.int32, device=dev)
+                d.row_ptr = zeros.data_ptr()
+                d.dst = zeros.data_ptr()
+                d.weight = acc.data_ptr()
+                d.live = None
+            else:
+                _lib.check(lib.plx_gather_edges(lists.pos.numel(), lists.pos.data_ptr(),
+                                                arena.cols["weight"].data_ptr(), arena.cols["dead"].data_ptr(),
+                                                lists.weight.data_ptr(), lists.live.data_ptr(), stream),
+                           "plx_gather_edges")
+                d.row_ptr = lists.ptr.data_ptr()
+                d.dst = lists.dst.data_ptr()
+                d.weight = lists.weight.data_ptr()
+                d.live = lists.live.data_ptr()
+            d.g = units[bp.field].data_ptr()
+            d.acc = acc.data_ptr()
+            d.fin.level = fin_common["level"]
+            d.fin.is_input = fin_common["is_input"]
+            d.fin.pruned = fin_common["pruned"]
+            d.fin.fin_level = level
+            d.fin.skip_inputs = skip_inputs
+            d.apply = prog
+            self._launch("backward", lib.plx_backward_lists, d, stream)
+
+        if arena.pipeline:
+            run(arena.lists[0], -1, 0)
+        else:
+            run(None, nb, 1)
+            for b in range(nb - 1, 0, -1):
+                run(arena.lists[b], b, 1)
+        self._unshadow(units, swaps)
+
     def _backward_update(self, plan: Plan, arena: Arena, units: dict, consts: dict,
                          fin_common: dict, stream: int, g: Any) -> None:
         bp, up = plan.backward, plan.update
         nb = arena.num_buckets
+        if getattr(arena, "churn", False):
+            if bp is not None:
+                self._backward_lists(plan, arena, units, fin_common, stream, g)
+            if plan.update_unit:
+                self._run_update_unit(arena, units, stream, g)
+            if up is not None:
+                for b in range(nb):
+                    self._update_only(plan, arena, units, consts, b, stream)
+            return
         if bp is not None:
             dev = arena.device
             n_units = self.static.num_units
@@ -509,15 +601,15 @@ class StepFn:
         quad of positions per lane (phases.py:1196-1242)."""
         lib = _lib.load()
         up = plan.update
-        bt = arena.bwd[b]
+        base, end = arena.bases[b], arena.ends[b]
         d = _lib.plx_update_desc()
-        d.n = bt.end - bt.base
+        d.n = end - base
         d.rule = up.rule_code
         d.tbl_base, d.tbl_len = arena.src_table(b)
 
         def col(name: str) -> int:
             t = arena.cols[name]
-            return t.data_ptr() + bt.base * t.element_size()
+            return t.data_ptr() + base * t.element_size()
 
         d.src = col("from_id")
         d.dst = col("to_id")
@@ -534,7 +626,7 @@ class StepFn:
             d.p[k] = float(v)
         self._edge_state(d, arena, b, True)
         # positions of this descriptor start at the bucket base
-        d.live_end -= bt.base
+        d.live_end -= base
         d.dead = col("dead") if arena.dead_in_rows else None
         self._launch("update_conn", lib.plx_update_conn, d, stream)
         self._advance_t(arena, b)

@@ -140,6 +140,8 @@ def test_driver_regrow_retry_and_resort_bit_exact(oracle, pipeline: bool) -> Non
         capacity_headroom=0.02, device="cuda")
     o = nets.oracle_for(oracle, Net, static, state)
     o.tail_start = int(state.tail_start)
+    if px.make_step(Net, static).backward_order == "slot":
+        o.tile = None  # growth every step: the churn layout's slot-order backward
     od = oracle.OracleDriver(o)
     drv = Driver(Net, static, state)
     xs = rng.standard_normal((12, layers[0])).astype(np.float32)

@@ -73,6 +73,8 @@ def _run(net, static, state, oracle, inputs_fn, globals_fn, steps, check_at):
     o = nets.oracle_for(oracle, net, static, state)
     o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
     step = px.make_step(net, static)
+    if step.backward_order == "slot":
+        o.tile = None  # the churn layout folds each source's edges in slot order
     grown_total = 0
     for k in range(1, steps + 1):
         g = globals_fn(k)
@@ -255,6 +257,8 @@ def test_full_churn_bit_exact(oracle, pipeline: bool) -> None:
     o = nets.oracle_for(oracle, Churn, static, state)
     o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
     step = px.make_step(Churn, static)
+    if step.backward_order == "slot":
+        o.tile = None
     added = 0
     for k in range(1, 13):
         g = globals_fn(k)
