@@ -298,6 +298,102 @@ def run_c5_growth(args) -> int:
     return 0
 
 
+C5_METRIC = "steps/sec of C5's growing reservoir (forward + per-unit proposals + growth + device relayout)"
+
+
+def run_c5(args) -> int:
+    """C5 end to end: every step scatters 256 inputs, runs the PIPELINE
+    forward over the live edges, grows (per-unit proposals, P = 4) and the
+    next step lays the arena out again on the device (the churn layout)."""
+    import torch
+
+    import plastax_amd as px
+    from plastax_amd import synth
+    from plastax_amd.state import column_to_numpy
+
+    t_setup = time.perf_counter()
+    net = build_c5(px)
+    e = synth.c5_reservoir(args.seed)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, capacity_headroom=3.0, device="cpu")
+    uspecs = {s.name: s for s in static.unit_fields}
+    cspecs = {s.name: s for s in static.conn_fields}
+    host_units = {k: column_to_numpy(v, uspecs[k]).copy() for k, v in state.units.items()}
+    host_conns = [{k: column_to_numpy(v, cspecs[k]).copy() for k, v in b.items()} for b in state.conns]
+    dev = torch.device("cuda", 0)
+    gstate = px.NetworkState(
+        {k: v.to(dev) for k, v in state.units.items()},
+        tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
+        None,
+    )
+    step = px.make_step(net, static)
+    nsteps = args.warmup + args.steps
+    rng = np.random.default_rng(args.seed + 3)
+    xs = rng.standard_normal((nsteps, e.input_ids.size)).astype(np.float32)
+    xs_d = torch.from_numpy(xs).to(dev)
+    for k in range(args.warmup):
+        gstate = step(gstate, px.StepInputs(xs_d[k])).state
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    progress(f"C5: {e.src.size} live edges of {static.level_capacities[0]} slots, layout {step.backward_order} "
+             f"({setup_s:.1f} s)")
+    grown = 0
+    t0 = time.perf_counter()
+    for k in range(args.warmup, nsteps):
+        gstate = step(gstate, px.StepInputs(xs_d[k])).state
+        grown += int(gstate.grown)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+    live = int(gstate._arena.lives[0]) if gstate._arena is not None else int(e.src.size)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ox
+        from plastax_amd._plan import compile_plan
+
+        ox.load()
+        o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), None, tile=None)
+        o.tail_start = int(state.tail_start)
+        t1 = time.perf_counter()
+        o.step(xs[0])
+        sec = time.perf_counter() - t1
+        cpu = {
+            "value": float(1.0 / sec),
+            "unit": "steps/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"1 full C5 step (forward + growth) of the same workload, {sec:.2f} s, the C oracle and "
+            "oracle/growth.py, one thread",
+        }
+    line = {
+        "metric": C5_METRIC,
+        "value": round(1e3 / ms, 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C5: 65,536 live of 262,144 unit slots, 4M live of 16M edge slots, PIPELINE tanh, "
+            "per-unit proposals P=4 every step, max_new_per_level 16",
+            "layout": step.backward_order,
+            "live_edges_end": live,
+        },
+        "grown_per_step": grown / args.steps,
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 C3_METRIC = "samples/sec per batched step (fwd+bwd+update, B=256) of C3's 784-4096-4096-10 sparse MLP"
 
 
@@ -469,9 +565,9 @@ def run_c3(args) -> int:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=("c2", "c3", "c5_growth"), default="c2",
+    ap.add_argument("--workload", choices=("c2", "c3", "c5", "c5_growth"), default="c2",
                     help="c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
-                    "c5_growth: the add_conn phase")
+                    "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
@@ -497,6 +593,8 @@ def main() -> int:
         return run_c5_growth(args)
     if args.workload == "c3":
         return run_c3(args)
+    if args.workload == "c5":
+        return run_c5(args)
 
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4

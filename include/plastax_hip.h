@@ -709,6 +709,10 @@ PLX_EXPORT int plx_relax_levels(int64_t n_units, int64_t n_edges, const int32_t*
                                 int32_t* level_out, const uint8_t* is_input, int32_t* changed,
                                 void* stream);
 
+/* CSR offsets from ascending row ids: start[u] = the number of keys[0, n)
+ * below u, for u in [0, nlevels] (keys in [0, nlevels)). */
+PLX_EXPORT int plx_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start, void* stream);
+
 /* Resort keys: key[p] = dead[p] ? sentinel : (pipeline ? 0 : level[from[p]]). */
 PLX_EXPORT int plx_resort_keys(int64_t n, const int32_t* from_id, const uint8_t* dead, const int32_t* level,
                                int32_t pipeline, int32_t sentinel, int32_t* key, void* stream);

@@ -108,51 +108,47 @@ class ChurnArena(Arena):
         self.t_now = []
         nbits = max(1, int(n).bit_length())
         rows = torch.arange(n, dtype=torch.int32, device=device)
-        scratch = k.mem.ints_for(n)
-        count = torch.empty(n, dtype=torch.int32, device=device)
         for b, bucket in enumerate(conns):
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
-            live_list, nlive = k.compact(cap, 0 + 1, dead)  # PLX_FLAG_U8_ZERO: live slots, ascending
-            dead_list, _ = k.compact(cap, 0, dead)  # dead slots, ascending
+            live_list, nlive = k.compact(cap, 1, dead)  # PLX_FLAG_U8_ZERO: live slots, ascending
+            dead_list, _ = k.compact(cap, 0, dead)  # PLX_FLAG_U8: dead slots, ascending
             live = int(nlive.item())
             self.lives.append(live)
+            # Live slots by (destination, slot): a stable sort of the ascending
+            # list. Only the live part moves: the step never writes a slot that
+            # is dead at layout time, so the dead part keeps fill values and
+            # is not written back.
             lv = live_list[:live].clone()
-            # live slots by (destination, slot): a stable sort of the ascending list
             k.sort(lv, live, [(0, nbits, bucket[TO_ID.name], None)], tag="relayout")
-            order = torch.cat([lv, dead_list[: cap - live]])
-            for name, spec in specs.items():
+            for name in specs:
                 col = bucket[name]
-                dst_col = self.cols[name][base : base + cap]
-                _lib.check(k.lib.plx_gather_col(cap, None, order.data_ptr(), col.data_ptr(),
-                                                dst_col.data_ptr(), col.element_size(), k.s), "plx_gather_col")
-            self.slot[base : base + cap] = order
+                _lib.check(k.lib.plx_gather_col(live, None, lv.data_ptr(), col.data_ptr(),
+                                                self.cols[name][base:].data_ptr(), col.element_size(), k.s),
+                           "plx_gather_col")
+            self.slot[base : base + live] = lv
+            self.slot[base + live : base + cap] = dead_list[: cap - live]
             # Forward rows: every unit; row u owns its in-edges' run.
-            start = torch.empty(n + 1, dtype=torch.int32, device=device)
-            _lib.check(k.lib.plx_level_counts(live, None, self.cols[TO_ID.name][base:].data_ptr(), n,
-                                              count.data_ptr(), start.data_ptr(), scratch.data_ptr(), k.s),
-                       "plx_level_counts")
-            start[n] = live
-            self.fwd.append(ForwardRows(n, rows, start + base))
+            fptr = torch.empty(n + 1, dtype=torch.int32, device=device)
+            _lib.check(k.lib.plx_sorted_starts(live, self.cols[TO_ID.name][base:].data_ptr(), n, fptr.data_ptr(),
+                                               k.s), "plx_sorted_starts")
+            self.fwd.append(ForwardRows(n, rows, fptr + base))
             # Backward lists: live slots by (source, slot) -> their positions.
             sl = live_list[:live].clone()
             k.sort(sl, live, [(0, nbits, bucket[FROM_ID.name], None)], tag="relayout")
-            pos_of_slot = torch.empty(cap, dtype=torch.int32, device=device)
-            pos_of_slot[order.long()] = torch.arange(base, base + cap, dtype=torch.int32, device=device)
-            pos = torch.empty(live + 1, dtype=torch.int32, device=device)
-            pos[live] = base
+            pos_of_slot = torch.zeros(cap, dtype=torch.int32, device=device)
+            pos_of_slot[lv.long()] = torch.arange(base, base + live, dtype=torch.int32, device=device)
+            pos = torch.full((live + 1,), base, dtype=torch.int32, device=device)
             _lib.check(k.lib.plx_gather_i32(live, None, sl.data_ptr(), pos_of_slot.data_ptr(), pos.data_ptr(), k.s),
                        "plx_gather_i32")
             ldst = torch.zeros(live + 1, dtype=torch.int32, device=device)
             _lib.check(k.lib.plx_gather_i32(live, None, sl.data_ptr(), bucket[TO_ID.name].data_ptr(),
                                             ldst.data_ptr(), k.s), "plx_gather_i32")
-            lsrc = torch.empty(max(live, 1), dtype=torch.int32, device=device)
+            lsrc = torch.zeros(max(live, 1), dtype=torch.int32, device=device)
             _lib.check(k.lib.plx_gather_i32(live, None, sl.data_ptr(), bucket[FROM_ID.name].data_ptr(),
                                             lsrc.data_ptr(), k.s), "plx_gather_i32")
             lptr = torch.empty(n + 1, dtype=torch.int32, device=device)
-            _lib.check(k.lib.plx_level_counts(live, None, lsrc.data_ptr(), n, count.data_ptr(),
-                                              lptr.data_ptr(), scratch.data_ptr(), k.s), "plx_level_counts")
-            lptr[n] = live
+            _lib.check(k.lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
             self.lists.append(SourceLists(lptr, pos, ldst))
         self.top = None
         self.levels_dev = levels
@@ -160,3 +156,14 @@ class ChurnArena(Arena):
     def src_table(self, b: int) -> tuple[int, int]:
         """No source-value tables: units keep the caller's ids."""
         return 0, 0
+
+    def write_logical(self, conns: tuple[Columns, ...]) -> None:
+        """Scatter the live part of every bucket back into its logical slots
+        (the slots dead at layout time were never written by the step)."""
+        for b, bucket in enumerate(conns):
+            base, live = self.bases[b], self.lives[b]
+            idx = self.slot[base : base + live].long()
+            for name, col in bucket.items():
+                col[idx] = self.cols[name][base : base + live]
+                if name == self.t_name and self.t_now and self.t_now[b] is not None:
+                    col[idx] = self.t_now[b]

@@ -372,6 +372,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_relax_levels": (c_i32, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_resort_keys": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp]),
     "plx_gather_col": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp]),
+    "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),

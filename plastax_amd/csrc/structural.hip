@@ -866,16 +866,33 @@ __global__ void k_unit_prune(int64_t n, const uint32_t* selected, uint8_t* prune
   }
 }
 
+// start[u] = the number of keys below u (lower bound of u in the ascending
+// keys), u in [0, nlevels]: a CSR's offsets from its sorted row ids.
+__global__ void k_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u > nlevels) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (keys[mid] < u)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  start[u] = static_cast<int32_t>(lo);
+}
+
 __global__ void k_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
                                 const uint8_t* doomed, const int32_t* id_map, int32_t* count) {
   for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
        p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (dead[p]) continue;  // already a tombstone: its ids are not read
     int32_t a = from_id[p], b = to_id[p];
     if (id_map) {
       a = id_map[a];
       b = id_map[b];
     }
-    if ((doomed[a] || doomed[b]) && !dead[p]) {
+    if (doomed[a] || doomed[b]) {
       dead[p] = 1;
       if (count) atomicAdd(count, 1);
     }
@@ -1252,6 +1269,14 @@ int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, u
   hipLaunchKernelGGL(k_kill_incident, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n,
                      from_id, to_id, dead, doomed, id_map, kill_count);
   return check_launch("plx_kill_incident");
+}
+
+int plx_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start, void* stream) {
+  if (n < 0 || n >= (int64_t{1} << 31) || nlevels < 0) return fail(PLX_ERR_INVALID, "plx_sorted_starts: bad sizes");
+  if (!start || (n > 0 && !keys)) return fail(PLX_ERR_INVALID, "plx_sorted_starts: null pointer");
+  hipLaunchKernelGGL(k_sorted_starts, dim3(grid_for(static_cast<int64_t>(nlevels) + 1)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), n, keys, nlevels, start);
+  return check_launch("plx_sorted_starts");
 }
 
 int plx_unit_place(int64_t n_max, const int32_t* parents, const int32_t* nparents, const int32_t* free_ids,
