@@ -194,6 +194,9 @@ typedef struct plx_partials_desc {
   float* acc;
   plx_finalize fin;
   plx_program apply;
+  /* optional [nparts][4]: each cold workgroup's first row, end row and first
+   * and end cold entry (row_cold at those rows), read in one load */
+  const int32_t* part_info;
 } plx_partials_desc;
 
 PLX_EXPORT int plx_backward_partials(const plx_partials_desc* d, void* stream);

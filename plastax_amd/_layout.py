@@ -113,6 +113,7 @@ class BackwardTiles:
     row_cold: torch.Tensor | None = None  # int32 [nrows+1]
     nparts: int = 0
     part_rows: torch.Tensor | None = None  # int32 [nparts+1] cold rows per workgroup
+    part_info: torch.Tensor | None = None  # int32 [nparts, 4] (first row, end row, first, end cold entry)
 
 
 def _round_up(n: int, k: int) -> int:
@@ -405,6 +406,8 @@ class Arena:
             row_cold=self._i32(row_cold),
             nparts=parts.size - 1,
             part_rows=self._i32(parts),
+            part_info=self._i32(np.stack([parts[:-1], parts[1:], row_cold[parts[:-1]], row_cold[parts[1:]]],
+                                         axis=1).reshape(-1) if parts.size > 1 else np.zeros(4, np.int64)),
             **tables,
         )
 

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 7  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 8  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -144,6 +144,7 @@ class plx_partials_desc(ctypes.Structure):
         ("acc", c_vp),
         ("fin", plx_finalize),
         ("apply", plx_program),
+        ("part_info", c_vp),
     ]
 
 

@@ -939,8 +939,19 @@ __device__ __forceinline__ void finalize_hot(const plx_partials_desc& d, float* 
 template <int M>
 __device__ __forceinline__ void finalize_cold(const plx_partials_desc& d, float* cval,
                                               uint16_t* csb, int wg) {
-  const int row0 = d.part_rows[wg];
-  const int rend = d.part_rows[wg + 1];
+  int row0, rend, c_first = 0, c_last = 0;
+  if (d.part_info) {
+    // One load gives the rows and their cold range, so the window's loads
+    // need not wait for row_cold.
+    const int4 pi = reinterpret_cast<const int4*>(d.part_info)[wg];
+    row0 = pi.x;
+    rend = pi.y;
+    c_first = pi.z;
+    c_last = pi.w;
+  } else {
+    row0 = d.part_rows[wg];
+    rend = d.part_rows[wg + 1];
+  }
   const int r = row0 + static_cast<int>(threadIdx.x);
   const bool has = r < rend;
   RowPre pre;
@@ -948,7 +959,8 @@ __device__ __forceinline__ void finalize_cold(const plx_partials_desc& d, float*
   const float ident = Mono<M>::id();
   float s = ident;
   if (d.row_cold) {
-    const int c_begin = d.row_cold[row0], c_end = d.row_cold[rend];
+    const int c_begin = d.part_info ? c_first : d.row_cold[row0];
+    const int c_end = d.part_info ? c_last : d.row_cold[rend];
     const int j0 = has ? d.row_cold[r] : 0;
     const int j1 = has ? d.row_cold[r + 1] : 0;
     float q = ident;
@@ -1513,7 +1525,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 7; }
+int32_t plx_abi_version(void) { return 8; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[15] = {

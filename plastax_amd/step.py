@@ -467,6 +467,7 @@ class StepFn:
         d.nhot = bt.nhot
         d.nparts = bt.nparts
         d.part_rows = bt.part_rows.data_ptr() if bt.part_rows is not None else None
+        d.part_info = bt.part_info.data_ptr() if bt.part_info is not None and bt.row_hot is not None else None
         d.row_unit = bt.rows.data_ptr()
         if bt.row_hot is not None:
             d.row_hot = bt.row_hot.data_ptr()
