@@ -40,37 +40,52 @@ METRIC = "edges/sec per streaming step (fwd+bwd+update) at 64M edges; % of HBM p
 class EventTimer:
     """HIP events around kernel launches, on torch's current stream (the
     stream every launch of the step goes to). ``kinds`` limits the recording
-    to those launch kinds (fewer events inside a timed region)."""
+    to those launch kinds; with ``stride`` only every stride-th launch of a
+    kind is bracketed (an event pair costs the stream a few microseconds),
+    and each recorded launch keeps its ordinal among the kind's launches."""
 
-    def __init__(self, kinds: set[str] | None = None) -> None:
+    def __init__(self, kinds: set[str] | None = None, stride: int = 1) -> None:
         import torch
 
         self.torch = torch
         self.on = False
         self.kinds = kinds
+        self.stride = max(1, int(stride))
+        self.count: dict[str, int] = collections.defaultdict(int)
         self.pairs: dict[str, list] = collections.defaultdict(list)
         self._open: tuple | None = None
 
     def begin(self, kind: str) -> None:
         if self.on and (self.kinds is None or kind in self.kinds):
+            c = self.count[kind]
+            self.count[kind] = c + 1
+            if c % self.stride:
+                return
             e = self.torch.cuda.Event(enable_timing=True)
             e.record()
-            self._open = (kind, e)
+            self._open = (kind, e, c)
 
     def end(self, kind: str) -> None:
         if self.on and self._open is not None:
             e = self.torch.cuda.Event(enable_timing=True)
             e.record()
-            self.pairs[kind].append((self._open[1], e))
+            self.pairs[kind].append((self._open[1], e, self._open[2]))
             self._open = None
 
-    def summary(self) -> dict[str, dict[str, float]]:
+    def summary(self) -> dict[str, dict]:
         self.torch.cuda.synchronize()
         out = {}
         for kind, pairs in self.pairs.items():
-            ms = [a.elapsed_time(b) for a, b in pairs]
-            out[kind] = {"launches": len(ms), "total_ms": float(sum(ms)), "mean_ms": float(np.mean(ms))}
+            ms = [a.elapsed_time(b) for a, b, _ in pairs]
+            out[kind] = {"launches": len(ms), "total_ms": float(sum(ms)), "mean_ms": float(np.mean(ms)),
+                         "ms": ms, "ordinals": [c for _, _, c in pairs]}
         return out
+
+
+def kernel_table(kernels: dict[str, dict]) -> dict[str, dict]:
+    """The breakdown as printed: launches, total and mean ms per kind."""
+    return {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 3), "mean_ms": round(v["mean_ms"], 4)}
+            for k, v in kernels.items()}
 
 
 def build_c2(px, seed: int, scale: int):
@@ -491,9 +506,7 @@ def run_c3(args) -> int:
     breakdown.on = False
     step.timer = None
     kernels = breakdown.summary()
-    for k in kernels.values():
-        k["total_ms"] = round(k["total_ms"], 3)
-        k["mean_ms"] = round(k["mean_ms"], 4)
+    kernels = kernel_table(kernels)
     edges = int(e.src.size)
     ms = elapsed * 1e3 / args.steps
     # The batch-mean update reads every edge's columns once (FROM_ID, TO_ID,
@@ -646,11 +659,15 @@ def main() -> int:
         gstate = step(gstate, px.StepInputs(xs_d[k], ts_d[k])).state
     torch.cuda.synchronize()
 
-    # The timed region records HIP events around the dominant kernel's
-    # launches only (the fused backward + update); a short pass afterwards
-    # times every launch kind for the breakdown.
+    # The timed region records HIP events around the dominant kernel (the
+    # fused backward + update) only, one launch in per_step + 1, so that the
+    # sampled launches rotate over the buckets (a step launches it for
+    # buckets nb-1 .. 1, in that order); a short pass afterwards times every
+    # launch kind for the breakdown.
     dominant = "backward_update"
-    timer = EventTimer({dominant})
+    arena = gstate._arena
+    per_step = arena.num_buckets - 1
+    timer = EventTimer({dominant}, stride=per_step + 1)
     step.timer = timer
     timer.on = True
     torch.cuda.synchronize()
@@ -680,8 +697,6 @@ def main() -> int:
     step_bytes = 54 * edges + 16 * n_units
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Algorithmic bytes per launch of each kernel kind (per live edge).
-    arena = gstate._arena
     # Algorithmic bytes per step of each launch kind (the reference column
     # model): the forward reads FROM_ID, TO_ID, DEAD, WEIGHT (13 B/edge) of
     # every bucket; the fused backward+update and the update-only pass read
@@ -695,8 +710,10 @@ def main() -> int:
     }
     roofline = None
     if dominant in bytes_per_step:
-        per_launch = bytes_per_step[dominant] * args.steps / dom["launches"]
-        ach = per_launch / (dom["mean_ms"] * 1e-3) / 1e9
+        # The sampled launches' own buckets: ordinal c is bucket nb-1 - c % per_step.
+        sampled = [41 * lives[arena.num_buckets - 1 - c % per_step] for c in dom["ordinals"]]
+        per_launch = float(np.mean(sampled))
+        ach = sum(sampled) / (dom["total_ms"] * 1e-3) / 1e9
         roofline = {
             "kernel": dominant,
             "bound": "hbm",
@@ -707,6 +724,7 @@ def main() -> int:
             "traffic": None,
             "algorithmic_bytes_per_launch": int(per_launch),
             "mean_launch_ms": round(dom["mean_ms"], 4),
+            "sampled_launches": dom["launches"],
         }
     traffic_file = ROOT / "profiles" / "traffic.json"
     if roofline is not None and traffic_file.exists():
@@ -717,9 +735,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(px, net, static, e, host_units, host_conns, xs, ts, args.cpu_steps)
 
-    for k in kernels.values():
-        k["total_ms"] = round(k["total_ms"], 3)
-        k["mean_ms"] = round(k["mean_ms"], 4)
+    kernels = kernel_table(kernels)
     line = {
         "metric": METRIC,
         "value": round(value, 1),

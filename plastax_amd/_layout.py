@@ -59,6 +59,8 @@ MAX_TBL = 8192  # source values staged in LDS per workgroup (PLX_MAX_TBL)
 PAD = 256  # slack positions after each slab (vector loads may run past the end)
 PART_ROWS = 256  # cold finalize: rows per workgroup at most (one per lane)
 PART_WIN = 2048  # cold finalize: cold partials staged per window
+FIN_HOT_COLS = 16  # hot columns per finalize workgroup (PLX_HOT_COLS)
+XCDS = 8  # MI355X dies: workgroup w of a launch runs on XCD w % 8
 
 
 def cold_row_parts(row_cold: np.ndarray, first: int) -> np.ndarray:
@@ -357,12 +359,6 @@ class Arena:
         g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
         grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
         se = (g_st[g_perm].astype(np.uint64) | (g_len[g_perm].astype(np.uint64) << np.uint64(16)))
-        # Tile-major cold slots: the cold groups in descriptor order.
-        tgt = np.empty(g_start.size, dtype=np.int64)
-        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
-        cold_in_perm = g_perm[~is_hot[g_perm]] if live else g_start
-        tgt[cold_in_perm] = np.arange(cold_in_perm.size)
-        cold_idx = tgt[cold_order]
         # Rows finalized at this bucket: hot sources first (by hot slot, so a
         # wave reads consecutive columns), then every other unit of the level.
         if self.pipeline:
@@ -372,15 +368,32 @@ class Arena:
         others = level_units[hot_idx[level_units] < 0]
         rows = np.concatenate([hot_src, others])
         row_hot = np.concatenate([np.arange(nhot), np.full(others.size, -1)])
-        # Cold slots were numbered in (source, tile) order and `others` is in
-        # source order (hot sources have no cold groups), so each cold row's
-        # run is contiguous and the runs follow the row order.
+        # cold_order is in (source, tile) order and `others` in source order
+        # (hot sources have no cold groups), so each cold row's entries are
+        # one run and the runs follow the row order.
         counts = np.concatenate([np.zeros(nhot, np.int64), cold_count[others]])
         row_cold = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
         assert int(row_cold[-1]) == cold_order.size
         ncold = int(cold_order.size)
         cold_sb = sb_of_tile[g_tile[cold_order]].astype(np.uint16)
         parts = cold_row_parts(row_cold, nhot)
+        # Cold slots: one region per XCD, holding the partials that the
+        # finalize workgroups on that XCD read (finalize workgroup w: hot
+        # workgroups first, then one per row part), so each XCD's L2 fetches
+        # only its region; tile-major inside a region (the cold groups in
+        # descriptor order), so a tile's stores are one run per region.
+        tgt = np.empty(g_start.size, dtype=np.int64)
+        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
+        cold_in_perm = g_perm[~is_hot[g_perm]] if live else g_start
+        if cold_in_perm.size:
+            hot_wgs = -(-nhot // FIN_HOT_COLS) if nhot and nsuper else 0
+            row_of = np.full(n, -1, dtype=np.int64)
+            row_of[rows] = np.arange(rows.size)
+            part_of = np.searchsorted(parts, row_of[g_src[cold_in_perm]], side="right") - 1
+            region = (hot_wgs + part_of) % XCDS
+            cold_in_perm = cold_in_perm[np.argsort(region, kind="stable")]
+        tgt[cold_in_perm] = np.arange(cold_in_perm.size)
+        cold_idx = tgt[cold_order]
         dev = self.device
         return BackwardTiles(
             base,
