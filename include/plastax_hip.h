@@ -110,19 +110,25 @@ PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
  * tile_size, multiples of 4). One workgroup walks each superblock in tile
  * order. With `fold`, every live edge's backward
  * term weight * g[dst] (pre-update weight) is folded per (tile, source)
- * group, in physical order, into a tile partial: a hot source's tile partial
- * is folded, in tile order, into its superblock sum, stored at
- * hot_sb[superblock * nhot + h] (the identity where the source is absent);
- * the other sources' tile partials are stored in their slot of the
- * cold_partial array (group target -1-h or the cold slot; a tile's cold slots
- * are consecutive, in its group order). With
+ * group, in physical order, into a tile partial: a hot source (physical id
+ * hot_base + h, h < nhot) has its tile partial folded, in tile order, into
+ * its superblock sum, stored at hot_sb[superblock * nhot + h] (the identity
+ * where the source is absent); the other sources' tile partials are stored
+ * in their cold_partial slot. With
  * `update`, the same pass applies the update rule (see plx_update_desc for
  * p[] and the state columns) with grad = gfield[dst] * act[src] and stores
  * the new weight and state; dead edges keep theirs. Tile metadata:
- * sorted_rank[p - base] is the rank of live position p in its tile's
- * (source, position) order; grp_off[tile..tile+1] ranges the tile's groups;
- * grp_se packs a group's first rank (low 16 bits) and length (high 16
- * bits); tile_size is at most 4096. */
+ * sorted_rank[p - base] is, in its low 12 bits, the rank of position p
+ * (below live_end) in its tile's (source, position) order, and bit 15 is set
+ * where that rank starts a (tile, source) group; the hot sources' ranks are
+ * [hlo, hhi) of the tile. grp_off[tile..tile+1] ranges the tile's groups in
+ * grp, each packing its first rank (low 12 bits) and its length (high 4
+ * bits; 15 means 15 or more: the group then ends at the next rank that
+ * starts one, or at the tile's last ranked position). tile_info holds 16 int32 per tile: [0] hlo | hhi <<
+ * 16; [1..7] the region bounds b1..b7; [8..15] the region offsets o0..o7.
+ * A cold group starting at rank r stores its partial at o[x] + c, where c is
+ * r, less hhi - hlo when r >= hhi, and x is the number of bounds b1..b7 at or
+ * below c. tile_size is at most 4096; nhot at most 32767. */
 typedef struct plx_tile_desc {
   int64_t base;
   int64_t end;
@@ -137,15 +143,16 @@ typedef struct plx_tile_desc {
   int32_t pow_table_len;
   int32_t tbl_base; /* act[tbl_base, tbl_base + tbl_len) is staged in LDS  */
   int32_t tbl_len;  /* (at most 8192; 0: none)                             */
+  int32_t hot_base; /* hot sources are hot_base .. hot_base + nhot - 1     */
   int64_t live_end; /* with dead == null: positions >= live_end are dead   */
   int32_t step_mode; /* Adam: 0 per-edge step count s2; 1 every live edge  */
   float step_t;      /* has the step count step_t (s2 neither read nor      */
                      /* written; the caller advances step_t after the call) */
   const int32_t* tile_pos;   /* [ntiles+1] tile starts relative to base   */
   const int32_t* super_tile; /* [nsuper+1] first tile of each superblock  */
-  const int32_t* grp_off;
-  const uint32_t* grp_se;
-  const int32_t* grp_tgt;
+  const int32_t* tile_info;    /* [ntiles * 16] (fold)                     */
+  const int32_t* grp_off;      /* [ntiles + 1] (fold)                      */
+  const uint16_t* grp;         /* [groups] (fold)                          */
   const uint16_t* sorted_rank;
   float* hot_sb;
   float* cold_partial;

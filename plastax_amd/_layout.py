@@ -54,13 +54,27 @@ from plastax_amd.state import Columns, NetworkStatic, column_to_numpy, torch_dty
 TILE = 4096  # positions per backward tile (multiple of 4, <= 4096: one device pass)
 NSUPER = 512  # superblocks per bucket at most (device workgroups: 2 per CU)
 HOT_PER_SUPER = 0.25  # hot iff present in more than this many tiles per superblock
-MAX_HOT = 8192  # hot running sums per workgroup (LDS: 4 B each)
+MAX_HOT = 6128  # hot running sums per workgroup (LDS: 4 B each; the fused kernel's LDS stays within 80 KB)
 MAX_TBL = 8192  # source values staged in LDS per workgroup (PLX_MAX_TBL)
 PAD = 256  # slack positions after each slab (vector loads may run past the end)
 PART_ROWS = 256  # cold finalize: rows per workgroup at most (one per lane)
 PART_WIN = 2048  # cold finalize: cold partials staged per window
 FIN_HOT_COLS = 16  # hot columns per finalize workgroup (PLX_HOT_COLS)
 XCDS = 8  # MI355X dies: workgroup w of a launch runs on XCD w % 8
+GROUP_START = 0x8000  # sorted_rank bit: the rank starts a (tile, source) group
+LEN_OPEN = 15  # group descriptor length field: 15 or more
+TILE_INFO = 16  # int32 per tile of tile_info (plx_tile_desc)
+
+
+def xcd_item(first: int, n: int) -> np.ndarray:
+    """The item that each of n consecutive workgroups, the first being
+    workgroup ``first`` of its launch, takes (the device's xcd_item): each
+    XCD's items are one contiguous range, XCD 0's first."""
+    i = np.arange(n, dtype=np.int64)
+    r = (np.arange(XCDS) - first) % XCDS
+    cnt = np.where(r < n, (n - r + XCDS - 1) // XCDS, 0)
+    first_item = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+    return first_item[(first + i) % XCDS] + i // XCDS
 
 
 def cold_row_parts(row_cold: np.ndarray, first: int) -> np.ndarray:
@@ -101,14 +115,15 @@ class BackwardTiles:
     tile_pos: torch.Tensor | None = None  # int32 [ntiles+1] tile starts (relative to base)
     super_tile: torch.Tensor | None = None  # int32 [nsuper+1] first tile of each superblock
     nhot: int = 0
+    hot_base: int = 0  # hot sources are physical ids [hot_base, hot_base + nhot)
+    tile_info: torch.Tensor | None = None  # int32 [ntiles, TILE_INFO] hot ranks, cold regions
     grp_off: torch.Tensor | None = None  # int32 [ntiles+1]
-    grp_se: torch.Tensor | None = None  # int32 (uint32 bits) [groups]
-    grp_tgt: torch.Tensor | None = None  # int32 [groups]
-    sorted_rank: torch.Tensor | None = None  # int16 (uint16 bits) [span] by position
+    grp: torch.Tensor | None = None  # int16 (uint16 bits) [groups] first rank | min(len, 15) << 12
+    sorted_rank: torch.Tensor | None = None  # int16 (uint16 bits) [span]: rank | GROUP_START
     hot_sb: torch.Tensor | None = None  # f32 [nsuper*nhot]
     cold_partial: torch.Tensor | None = None  # f32 [ncold]
     cold_sb: torch.Tensor | None = None  # int16 (uint16 bits) [ncold] superblock ids
-    cold_idx: torch.Tensor | None = None  # int32 [ncold] tile-major slot, source-major order
+    cold_idx: torch.Tensor | None = None  # int32 [ncold groups] slot, source-major order
     nrows: int = 0
     rows: torch.Tensor | None = None  # int32 [nrows] units finalized here
     row_hot: torch.Tensor | None = None  # int32 [nrows]
@@ -320,80 +335,108 @@ class Arena:
         t_sorted = tile_of[o2]
         s_sorted = srcs[o2]
         tile_first = np.searchsorted(t_sorted, np.arange(ntiles + 1), side="left")
-        sorted_rank = np.zeros(int(tile_pos[-1]) + 4, dtype=np.uint16)
         j_in_tile = np.arange(live, dtype=np.int64) - tile_first[t_sorted]
-        sorted_rank[rank[o2]] = j_in_tile.astype(np.uint16)
-        # Groups: runs of one source inside one tile.
+        # Groups: runs of one source inside one tile; sorted_rank carries each
+        # position's rank (low 12 bits) and whether that rank starts a group.
         if live:
             brk = np.flatnonzero((np.diff(t_sorted) != 0) | (np.diff(s_sorted) != 0)) + 1
             g_start = np.concatenate([[0], brk])
         else:
             g_start = np.zeros(0, dtype=np.int64)
-        g_end = np.concatenate([g_start[1:], [live]]).astype(np.int64)
+        starts = np.zeros(live, dtype=np.int64)
+        starts[g_start] = GROUP_START
+        sorted_rank = np.zeros(int(tile_pos[-1]) + 4, dtype=np.uint16)
+        sorted_rank[rank[o2]] = (j_in_tile | starts).astype(np.uint16)
         g_tile = t_sorted[g_start] if live else g_start
         g_src = s_sorted[g_start] if live else g_start
+        g_st = j_in_tile[g_start] if live else g_start
+        g_end = np.concatenate([g_start[1:], [live]]).astype(np.int64)
         g_len = g_end - g_start
-        g_st = g_start - tile_first[g_tile] if live else g_start
-        # Hot sources: a dense superblock row costs 8 B per superblock (write
-        # and read), a cold partial about as much as a scattered 4-byte store
-        # plus its read per tile present: hot iff present in more than
-        # HOT_PER_SUPER tiles per superblock, the most present first.
-        presence = np.bincount(g_src, minlength=n) if live else np.zeros(n, np.int64)
-        cand = np.flatnonzero(presence > max(1.0, HOT_PER_SUPER * nsuper))
-        if cand.size > MAX_HOT:
-            keep = np.argsort(-presence[cand], kind="stable")[:MAX_HOT]
-            cand = np.sort(cand[keep])
-        hot_src = cand
-        hot_idx = np.full(n, -1, dtype=np.int64)
-        hot_idx[hot_src] = np.arange(hot_src.size)
-        nhot = int(hot_src.size)
-        is_hot = hot_idx[g_src] >= 0 if live else np.zeros(0, bool)
-        # Cold groups: each tile writes its cold partials to consecutive
-        # slots (tile-major, in the tile's group order below, so the stores
-        # of a wave are coalesced); cold_idx lists every source's slots in
-        # tile order, source-major, for the finalize.
-        cold = np.flatnonzero(~is_hot)
-        cold_order = cold[np.lexsort((g_tile[cold], g_src[cold]))]
-        cold_count = np.bincount(g_src[cold], minlength=n) if cold.size else np.zeros(n, np.int64)
-        # Within a tile, longest groups first (lanes take them round robin).
+        # Descriptors: within a tile, longest groups first (lanes take them
+        # round robin), each its first rank and min(length, 15).
         g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
         grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
-        se = (g_st[g_perm].astype(np.uint64) | (g_len[g_perm].astype(np.uint64) << np.uint64(16)))
-        # Rows finalized at this bucket: hot sources first (by hot slot, so a
+        grp = (g_st[g_perm] | (np.minimum(g_len[g_perm], LEN_OPEN) << 12)).astype(np.uint16)
+        # Hot sources: a dense superblock row costs 8 B per superblock (write
+        # and read), a cold partial about as much as a scattered 4-byte store
+        # plus its read per tile present: as many hot sources as there are
+        # sources present in more than HOT_PER_SUPER tiles per superblock,
+        # taken as the first ids of the bucket's source range (units are
+        # numbered busiest first), so a source's hot index is its id less
+        # hot_base and the hot ranks of a tile are one range.
+        if self.pipeline:
+            hb, he = 0, n
+        elif b + 1 < self.lvl_start.size:
+            hb, he = int(self.lvl_start[b]), int(self.lvl_start[b + 1])
+        else:
+            hb, he = 0, 0
+        presence = np.bincount(g_src, minlength=n) if live else np.zeros(n, np.int64)
+        nhot = int(min(np.count_nonzero(presence > max(1.0, HOT_PER_SUPER * nsuper)), MAX_HOT, he - hb))
+        hot_src = np.arange(hb, hb + nhot, dtype=np.int64)
+        is_hot = np.zeros(n, dtype=bool)
+        is_hot[hot_src] = True
+        # Rows finalized at this bucket: hot sources first (by hot index, so a
         # wave reads consecutive columns), then every other unit of the level.
         if self.pipeline:
             level_units = np.arange(n, dtype=np.int64)
         else:
             level_units = np.union1d(np.flatnonzero(levels == b), np.unique(srcs)).astype(np.int64)
-        others = level_units[hot_idx[level_units] < 0]
+        others = level_units[~is_hot[level_units]]
         rows = np.concatenate([hot_src, others])
         row_hot = np.concatenate([np.arange(nhot), np.full(others.size, -1)])
-        # cold_order is in (source, tile) order and `others` in source order
+        # Cold groups in (source, tile) order; `others` is in source order
         # (hot sources have no cold groups), so each cold row's entries are
         # one run and the runs follow the row order.
+        cold = np.flatnonzero(~is_hot[g_src]) if live else g_start
+        cold_order = cold[np.lexsort((g_tile[cold], g_src[cold]))]
+        cold_count = np.bincount(g_src[cold], minlength=n) if cold.size else np.zeros(n, np.int64)
         counts = np.concatenate([np.zeros(nhot, np.int64), cold_count[others]])
         row_cold = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
         assert int(row_cold[-1]) == cold_order.size
-        ncold = int(cold_order.size)
         cold_sb = sb_of_tile[g_tile[cold_order]].astype(np.uint16)
         parts = cold_row_parts(row_cold, nhot)
+        # Each tile's hot ranks: [hlo, hhi) (sources below hot_base sort first).
+        hlo = np.bincount(t_sorted[s_sorted < hb], minlength=ntiles)[:ntiles] if live else np.zeros(ntiles, np.int64)
+        hcnt = np.bincount(t_sorted[is_hot[s_sorted]], minlength=ntiles)[:ntiles] if live else np.zeros(ntiles, np.int64)
+        hhi = hlo + hcnt
         # Cold slots: one region per XCD, holding the partials that the
-        # finalize workgroups on that XCD read (finalize workgroup w: hot
-        # workgroups first, then one per row part), so each XCD's L2 fetches
-        # only its region; tile-major inside a region (the cold groups in
-        # descriptor order), so a tile's stores are one run per region.
-        tgt = np.empty(g_start.size, dtype=np.int64)
-        tgt[is_hot] = -1 - hot_idx[g_src[is_hot]]
-        cold_in_perm = g_perm[~is_hot[g_perm]] if live else g_start
-        if cold_in_perm.size:
-            hot_wgs = -(-nhot // FIN_HOT_COLS) if nhot and nsuper else 0
-            row_of = np.full(n, -1, dtype=np.int64)
-            row_of[rows] = np.arange(rows.size)
-            part_of = np.searchsorted(parts, row_of[g_src[cold_in_perm]], side="right") - 1
-            region = (hot_wgs + part_of) % XCDS
-            cold_in_perm = cold_in_perm[np.argsort(region, kind="stable")]
-        tgt[cold_in_perm] = np.arange(cold_in_perm.size)
-        cold_idx = tgt[cold_order]
+        # finalize workgroups on that XCD read, so each XCD's L2 fetches only
+        # its region. The finalize hands the cold parts to its workgroups by
+        # xcd_item, so a part's region grows with the part, hence with the
+        # source id, and within a tile the cold ranks of a region are one
+        # range. A cold group starting at rank r gets the slot o[x] + c, with
+        # c its rank among the tile's cold ranks (hot ranks skipped) and x its
+        # region: inside a region, slots are tile-major and a tile's are one
+        # run (holes where a cold group spans several ranks).
+        nparts = parts.size - 1
+        hot_wgs = -(-nhot // FIN_HOT_COLS) if nhot and nsuper else 0
+        region_of_part = np.zeros(max(nparts, 1), dtype=np.int64)
+        if nparts:
+            region_of_part[xcd_item(hot_wgs, nparts)] = (hot_wgs + np.arange(nparts)) % XCDS
+        row_of = np.full(n, -1, dtype=np.int64)
+        row_of[rows] = np.arange(rows.size)
+        cold_e = np.flatnonzero(~is_hot[s_sorted]) if live else g_start
+        e_tile = t_sorted[cold_e]
+        e_region = region_of_part[np.searchsorted(parts, row_of[s_sorted[cold_e]], side="right") - 1]
+        e_c = j_in_tile[cold_e] - np.where(j_in_tile[cold_e] >= hhi[e_tile], hcnt[e_tile], 0)
+        cnt = np.bincount(e_tile * XCDS + e_region, minlength=ntiles * XCDS).reshape(ntiles, XCDS)
+        bnd = np.concatenate([np.zeros((ntiles, 1), np.int64), np.cumsum(cnt, axis=1)], axis=1)
+        assert ((bnd[e_tile, e_region] <= e_c) & (e_c < bnd[e_tile, e_region + 1])).all()
+        totals = cnt.sum(axis=0)
+        rbase = np.concatenate([[0], np.cumsum(totals)[:-1]])
+        cum = np.cumsum(cnt, axis=0) - cnt
+        off = rbase[None, :] + cum - bnd[:, :XCDS]
+        ncold = int(cnt.sum())
+        g_region = region_of_part[np.searchsorted(parts, row_of[g_src[cold_order]], side="right") - 1]
+        gt = g_tile[cold_order]
+        gst = g_st[cold_order]
+        g_c = gst - np.where(gst >= hhi[gt], hcnt[gt], 0)
+        cold_idx = off[gt, g_region] + g_c
+        info = np.zeros((max(ntiles, 1), TILE_INFO), dtype=np.int64)
+        if ntiles:
+            info[:ntiles, 0] = hlo | (hhi << 16)
+            info[:ntiles, 1:8] = bnd[:, 1:8]
+            info[:ntiles, 8:] = off
         dev = self.device
         return BackwardTiles(
             base,
@@ -401,11 +444,12 @@ class Arena:
             ntiles,
             True,
             nhot=nhot,
+            hot_base=hb,
+            tile_info=torch.from_numpy(info.reshape(-1).astype(np.uint32).view(np.int32)).to(dev),
             grp_off=self._i32(grp_off),
+            grp=torch.from_numpy(np.concatenate([grp, np.zeros(1, np.uint16)]).view(np.int16)).to(dev),
             # (one spare entry each: a bucket without live edges still gets
             # real, if unused, tables)
-            grp_se=torch.from_numpy(np.concatenate([se.astype(np.uint32), np.zeros(1, np.uint32)]).view(np.int32)).to(dev),
-            grp_tgt=self._i32(np.concatenate([tgt[g_perm] if live else tgt, np.zeros(1, np.int64)])),
             cold_idx=self._i32(np.concatenate([cold_idx, np.zeros(1, np.int64)])),
             sorted_rank=torch.from_numpy(sorted_rank.view(np.int16)).to(dev),
             hot_sb=torch.zeros(max(nsuper * nhot, 1), dtype=torch.float32, device=dev),
@@ -417,7 +461,7 @@ class Arena:
             rows=self._i32(rows),
             row_hot=self._i32(row_hot),
             row_cold=self._i32(row_cold),
-            nparts=parts.size - 1,
+            nparts=nparts,
             part_rows=self._i32(parts),
             part_info=self._i32(np.stack([parts[:-1], parts[1:], row_cold[parts[:-1]], row_cold[parts[1:]]],
                                          axis=1).reshape(-1) if parts.size > 1 else np.zeros(4, np.int64)),

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 8  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 9  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -99,14 +99,15 @@ class plx_tile_desc(ctypes.Structure):
         ("pow_table_len", c_i32),
         ("tbl_base", c_i32),
         ("tbl_len", c_i32),
+        ("hot_base", c_i32),
         ("live_end", c_i64),
         ("step_mode", c_i32),
         ("step_t", c_f32),
         ("tile_pos", c_vp),
         ("super_tile", c_vp),
+        ("tile_info", c_vp),
         ("grp_off", c_vp),
-        ("grp_se", c_vp),
-        ("grp_tgt", c_vp),
+        ("grp", c_vp),
         ("sorted_rank", c_vp),
         ("hot_sb", c_vp),
         ("cold_partial", c_vp),

@@ -626,14 +626,18 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
 //
 // For each tile the workgroup streams the edge columns once (16-byte loads):
 // for each live edge it forms the backward term c = weight * g[dst] with the
-// pre-update weight into LDS and, when updating, applies the update rule and
-// stores the new weight and optimizer state. Then the tile's (source) groups
-// are folded from LDS in physical order -- the group lists are precomputed
-// per tile -- and each group sum lands either in the workgroup's LDS running
-// sum of a hot source (sources present in many tiles), folded in tile order,
-// or in its slot of the source-major cold partial array. At the end the
-// running hot sums are the superblock's dense row of hot_sb. No float atomics:
-// every value has exactly one writer and a fixed fold order.
+// pre-update weight and, when updating, applies the update rule and stores
+// the new weight and optimizer state. The term goes to LDS at the edge's rank
+// in the tile's (source, position) order, with a tag: the group-start bit of
+// the rank and, for a hot source, its hot index. Then the tile's (source)
+// groups, listed longest first in 2-byte descriptors (first rank, length),
+// are folded from LDS in order, round robin over the lanes: into the
+// workgroup's LDS running sum of a hot source (hot sources are the id range
+// [hot_base, hot_base + nhot), so their ranks are one range of the tile and
+// the tag gives the index), folded in tile order, or into the group's cold
+// slot, a function of its first rank and the tile's region table. At the
+// end the running hot sums are the superblock's dense row of hot_sb. No
+// float atomics: every value has exactly one writer and a fixed fold order.
 // ---------------------------------------------------------------------------
 constexpr int kTileBlock = 512;
 #ifndef PLX_TILE_QUADS
@@ -641,16 +645,55 @@ constexpr int kTileBlock = 512;
 #endif
 constexpr int kTileQuads = PLX_TILE_QUADS;  // 16-byte quads per thread per streaming pass
 
-constexpr int kGrpPer = 4;  // group descriptors prefetched per thread per tile
+constexpr uint32_t kRankMask = 0x0FFFu;  // sorted_rank: the rank within the tile
+constexpr uint32_t kGroupStart = 0x8000u;  // sorted_rank / tag: the rank starts a group
+constexpr int kTileInfo = 16;             // int32 entries of tile_info per tile
+constexpr int kGrpPer = 4;                // group descriptors prefetched per thread per tile
+constexpr uint32_t kLenOpen = 15;         // descriptor length field: 15 or more (the end is found)
 
-// Folds one (tile, source) group: the contiguous run buf[st, st+len) in
-// order, into its cold partial slot or its hot running sum. A source has one
-// group per tile, so no other lane touches a hot slot within the tile.
+// The cold slot of a cold group starting at rank r of a tile, from the
+// tile's info staged in LDS (tmap: [0] hlo | hhi << 16, the hot ranks;
+// [1..7] the region bounds b1..b7; [8..15] the region offsets o0..o7):
+// c = r less the hot ranks before it, x = the number of bounds at or below
+// c, slot = o[x] + c.
+__device__ __forceinline__ int cold_slot(const int32_t* tmap, int r, int hlo, int hhi) {
+  const int c = r >= hhi ? r - (hhi - hlo) : r;
+  int x = 0;
+#pragma unroll
+  for (int k = 1; k < 8; ++k) x += c >= tmap[k] ? 1 : 0;
+  return tmap[8 + x] + c;
+}
+
+// Folds one (tile, source) group: the run buf[st, st + len) in order, into
+// its hot running sum or its cold slot. The descriptor packs the first rank
+// (low 12 bits) and the length (high 4 bits; kLenOpen: at least that long,
+// the run ends at the next rank whose tag has the group-start bit, or at nr).
+// A source has one group per tile, so no other lane touches a hot slot
+// within the tile.
 template <int M>
-__device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* buf, float* hot,
-                                           uint32_t se, int32_t tgt) {
-  const float* run = buf + (se & 0xFFFFu);
-  const int len = static_cast<int>(se >> 16);
+__device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* buf, const uint16_t* tag,
+                                           float* hot, const int32_t* tmap, int hlo, int hhi, int nr,
+                                           uint16_t desc) {
+  const int st = desc & static_cast<int>(kRankMask);
+  int len = desc >> 12;
+  if (len == static_cast<int>(kLenOpen)) {
+    // Eight tags per 16-byte read, from the aligned group holding st + 15.
+    int j = (st + kLenOpen) & ~7;
+    uint32_t skip = static_cast<uint32_t>((st + kLenOpen) & 7);  // tags of the first read before st + 15
+    for (; j < nr; j += 8) {
+      const uint4 g = *reinterpret_cast<const uint4*>(tag + j);
+      uint32_t bits = ((g.x >> 15) & 1u) | ((g.x >> 30) & 2u) | ((g.y >> 13) & 4u) | ((g.y >> 28) & 8u) |
+                      ((g.z >> 11) & 16u) | ((g.z >> 26) & 32u) | ((g.w >> 9) & 64u) | ((g.w >> 24) & 128u);
+      bits &= ~((1u << skip) - 1u);
+      skip = 0;
+      if (bits) {
+        j += __builtin_ctz(bits);
+        break;
+      }
+    }
+    len = min(j, nr) - st;
+  }
+  const float* run = buf + st;
   float v = Mono<M>::id();
   int j = 0;
   for (; j + 4 <= len; j += 4) {
@@ -661,11 +704,11 @@ __device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* 
     v = Mono<M>::op(v, a3);
   }
   for (; j < len; ++j) v = Mono<M>::op(v, run[j]);
-  if (tgt >= 0) {
-    d.cold_partial[tgt] = v;
-  } else {
-    const int h = -1 - tgt;
+  if (st >= hlo && st < hhi) {
+    const int h = tag[st] & 0x7FFF;
     hot[h] = Mono<M>::op(hot[h], v);
+  } else {
+    d.cold_partial[cold_slot(tmap, st, hlo, hhi)] = v;
   }
 }
 
@@ -676,7 +719,11 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int T = d.tile_size;
   float* buf = reinterpret_cast<float*>(smem);  // [T] terms in source-sorted order
-  float* hot = buf + T;                          // [nhot]
+  // [T] rank tags: group-start bit | hot index (hot sources)
+  uint16_t* tag = reinterpret_cast<uint16_t*>(smem + 4 * T);
+  // [kTileInfo] the folded tile's info
+  int32_t* tmap = reinterpret_cast<int32_t*>(smem + 4 * T + ((2 * T + 15) & ~15));
+  float* hot = reinterpret_cast<float*>(tmap + kTileInfo);  // [nhot]
   // [tbl_len] act of the busiest sources (the whole allocation without fold)
   float* tbl = FOLD ? hot + ((d.nhot + 3) & ~3) : reinterpret_cast<float*>(smem);
   const int k0 = d.super_tile[blockIdx.x];
@@ -695,8 +742,8 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
 
   // The pipeline runs three tiles at once. While tile blk is folded from
   // LDS, tile blk + 1's gathers (g[dst], act[src]) and value columns
-  // (weight, optimizer state, sorted rank, group descriptors) are in flight,
-  // and so are tile blk + 2's addressing columns (dst, src, dead), which the
+  // (weight, optimizer state, sorted rank, tile info) are in flight, and so
+  // are tile blk + 2's addressing columns (dst, src, dead), which the
   // gathers of the next iteration need.
   int4 sv[U], tv[U];  // addressing columns of tile `an` (the next to gather)
   uint32_t dv[U];
@@ -711,7 +758,7 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       if (4 * q < na) {
         const int64_t e = ta + 4 * q;
         tv[i] = ld_stream(d.dst + e);
-        if (RULE >= 0) sv[i] = ld_stream(d.src + e);
+        if (RULE >= 0 || FOLD) sv[i] = ld_stream(d.src + e);
         dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e) : dead_from_end(e, d.live_end);
       }
     }
@@ -723,8 +770,9 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   float gd[U][4], gu[U][4], ac[U][4];
   int64_t t0 = 0;
   int n = 0;
-  uint32_t gse[kGrpPer];
-  int32_t gtg[kGrpPer];
+  uint32_t ht[U][2];  // hot tags of the gathered tile: src - hot_base (hot sources), else 0
+  int32_t tiv = 0;  // lane k < kTileInfo: entry k of the info of the tile whose values are loaded
+  uint16_t gdesc[kGrpPer];  // group descriptors of that tile (this thread's share)
   int ga = 0, gb = 0;
   // Gathers of the tile whose addressing columns are in registers; every one
   // is issued before any result is used (dead or out-of-tile lanes gather a
@@ -743,11 +791,21 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         if (RULE >= 0) gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
       }
       if (RULE >= 0) gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ac[i]);
+      if (FOLD) {
+        uint32_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t o = static_cast<uint32_t>(si[k] - d.hot_base);
+          h[k] = o < static_cast<uint32_t>(d.nhot) ? o : 0u;
+        }
+        ht[i][0] = h[0] | (h[1] << 16);
+        ht[i][1] = h[2] | (h[3] << 16);
+      }
     }
     t0 = ta;
     n = na;
   };
-  // Value columns and group descriptors of tile blk (positions t0.., n).
+  // Value columns and tile info of tile blk (positions t0.., n).
   auto load_vals = [&](int blk) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -762,15 +820,13 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       }
     }
     if (FOLD) {
+      if (threadIdx.x < kTileInfo) tiv = d.tile_info[static_cast<int64_t>(blk) * kTileInfo + threadIdx.x];
       ga = d.grp_off[blk];
       gb = d.grp_off[blk + 1];
 #pragma unroll
       for (int i = 0; i < kGrpPer; ++i) {
         const int gi = ga + threadIdx.x + i * kTileBlock;
-        if (gi < gb) {
-          gse[i] = d.grp_se[gi];
-          gtg[i] = d.grp_tgt[gi];
-        }
+        if (gi < gb) gdesc[i] = d.grp[gi];
       }
     }
   };
@@ -790,20 +846,22 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       if (4 * q >= n) continue;
       const int64_t e = t0 + 4 * q;
       if (FOLD) {
-        // Each live edge's term goes to its slot in the tile's source-sorted
-        // order, so every (tile, source) group is a contiguous run of buf. A
-        // position tombstoned after the layout was built (below live_end)
-        // keeps its slot and contributes the identity; every group folds from
-        // the identity, so that leaves the fold's bits unchanged.
-        const int32_t rs[4] = {static_cast<int32_t>(rk[i].x & 0xFFFFu), static_cast<int32_t>(rk[i].x >> 16),
-                               static_cast<int32_t>(rk[i].y & 0xFFFFu), static_cast<int32_t>(rk[i].y >> 16)};
+        // Each live edge's term goes to its rank in the tile's (source,
+        // position) order, so every (tile, source) group is a contiguous run
+        // of buf, and its tag to the same rank. A position tombstoned after
+        // the layout was built (below live_end) keeps its rank and tag and
+        // contributes the identity; every group folds from the identity, so
+        // that leaves the fold's bits unchanged.
+        const uint32_t rw[4] = {rk[i].x & 0xFFFFu, rk[i].x >> 16, rk[i].y & 0xFFFFu, rk[i].y >> 16};
+        const uint32_t hw[4] = {ht[i][0] & 0xFFFFu, ht[i][0] >> 16, ht[i][1] & 0xFFFFu, ht[i][1] >> 16};
         const float wk[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          if (lv[i][k])
-            buf[rs[k]] = wk[k] * gd[i][k];
-          else if (e + k < d.live_end)
-            buf[rs[k]] = ident;
+          if (lv[i][k] || e + k < d.live_end) {
+            const uint32_t r = rw[k] & kRankMask;
+            buf[r] = lv[i][k] ? wk[k] * gd[i][k] : ident;
+            tag[r] = static_cast<uint16_t>((rw[k] & kGroupStart) | hw[k]);
+          }
         }
       }
       if (RULE >= 0) {
@@ -821,15 +879,13 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         if (nstate >= 3) st_stream(d.s2 + e, t);
       }
     }
-    // This tile's group descriptors, kept while the next tile loads.
-    uint32_t cse[kGrpPer];
-    int32_t ctg[kGrpPer];
+    // This tile's ranked length and info, kept while the next tile loads.
+    const int nr = static_cast<int>(max(static_cast<int64_t>(0), min(static_cast<int64_t>(n), d.live_end - t0)));
+    if (FOLD && threadIdx.x < kTileInfo) tmap[threadIdx.x] = tiv;
+    uint16_t cgd[kGrpPer];
     const int cga = ga, cgb = gb;
 #pragma unroll
-    for (int i = 0; i < kGrpPer; ++i) {
-      cse[i] = gse[i];
-      ctg[i] = gtg[i];
-    }
+    for (int i = 0; i < kGrpPer; ++i) cgd[i] = gdesc[i];
     if (blk + 1 < k1) {
       gather();
       load_vals(blk + 1);
@@ -837,14 +893,15 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
     }
     if (!FOLD) continue;
     __syncthreads();
+    const int hlo = tmap[0] & 0xFFFF, hhi = tmap[0] >> 16;
 #pragma unroll
     for (int i = 0; i < kGrpPer; ++i) {
       const int gi = cga + threadIdx.x + i * kTileBlock;
-      if (gi < cgb) fold_group<M>(d, buf, hot, cse[i], ctg[i]);
+      if (gi < cgb) fold_group<M>(d, buf, tag, hot, tmap, hlo, hhi, nr, cgd[i]);
     }
     // Tiles with more groups than the prefetch covers fold the rest here.
     for (int gi = cga + kGrpPer * kTileBlock + threadIdx.x; gi < cgb; gi += kTileBlock)
-      fold_group<M>(d, buf, hot, d.grp_se[gi], d.grp_tgt[gi]);
+      fold_group<M>(d, buf, tag, hot, tmap, hlo, hhi, nr, d.grp[gi]);
     __syncthreads();
   }
   if (!FOLD) return;
@@ -874,9 +931,10 @@ __device__ __forceinline__ void finish_row(const plx_partials_desc& d, const Row
 // superblocks at a time, with coalesced loads, and each column's lane folds
 // its superblock sums in order.
 //
-// Cold rows: workgroup k takes rows [part_rows[k], part_rows[k+1]) (at most
+// Cold rows: part k is rows [part_rows[k], part_rows[k+1]) (at most
 // kPartBlock, one per lane, cut so that their cold runs mostly fit one
-// window). A workgroup's rows own one contiguous range of the source-major
+// window); hot column blocks and cold parts go to the workgroups by
+// xcd_item, so each XCD takes a contiguous range of each. A workgroup's rows own one contiguous range of the source-major
 // cold arrays, which is staged through LDS with coalesced loads; each row
 // folds its run in tile order, closing a superblock sum whenever the
 // superblock id changes.
@@ -893,6 +951,20 @@ constexpr int kPartBlock = kFinBlock;
 constexpr int kPartWin = 2048;
 constexpr size_t kFinLds = (kHotSbChunk * kHotCols * 4 > kPartWin * 6) ? kHotSbChunk * kHotCols * 4
                                                                        : kPartWin * 6;
+
+// Workgroup w of a launch runs on XCD w % 8. Of the n consecutive
+// workgroups from `first`, the i-th takes item xcd_item(first, i, n): the
+// items of each XCD are one contiguous range, XCD 0's first, so an XCD's
+// workgroups read neighbouring data (one L2 per XCD).
+__device__ __forceinline__ int xcd_item(int first, int i, int n) {
+  const int x = (first + i) & 7;
+  int p = 0;
+  for (int y = 0; y < x; ++y) {
+    const int r = (y - first) & 7;  // the first i with (first + i) % 8 == y
+    p += r < n ? (n - r + 7) >> 3 : 0;
+  }
+  return p + (i >> 3);
+}
 
 template <int M>
 __device__ __forceinline__ void finalize_hot(const plx_partials_desc& d, float* stage, int wg) {
@@ -1031,11 +1103,11 @@ __global__ __launch_bounds__(kFinBlock) void k_finalize(plx_partials_desc d, int
   __shared__ __align__(16) unsigned char smem[kFinLds];
   const int wg = static_cast<int>(blockIdx.x);
   if (wg < hot_wgs) {
-    finalize_hot<M>(d, reinterpret_cast<float*>(smem), wg);
+    finalize_hot<M>(d, reinterpret_cast<float*>(smem), xcd_item(0, wg, hot_wgs));
   } else {
     float* cval = reinterpret_cast<float*>(smem);
     uint16_t* csb = reinterpret_cast<uint16_t*>(smem + kPartWin * 4);
-    finalize_cold<M>(d, cval, csb, wg - hot_wgs);
+    finalize_cold<M>(d, cval, csb, xcd_item(hot_wgs, wg - hot_wgs, d.nparts));
   }
 }
 
@@ -1525,7 +1597,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 8; }
+int32_t plx_abi_version(void) { return 9; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[15] = {
@@ -1580,7 +1652,7 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
   if (d->step_mode != 0 && d->step_mode != 1)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: step_mode must be 0 or 1");
-  if (d->fold && (!d->grp_off || !d->grp_se || !d->grp_tgt || !d->sorted_rank || !d->g ||
+  if (d->fold && (!d->tile_info || !d->grp_off || !d->grp || !d->sorted_rank || !d->g || !d->cold_partial ||
                   (d->nhot > 0 && !d->hot_sb)))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: fold metadata missing");
   if (d->update && (!d->gfield || !d->act))
@@ -1591,11 +1663,13 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
       (!d->s0 || !d->s1 || (d->step_mode == 0 && !d->s2)))
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: Adam state columns missing");
   if (!d->fold && !d->update) return PLX_OK;
-  if (d->fold && d->nhot < 0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: negative nhot");
+  if (d->fold && (d->nhot < 0 || d->nhot > 32767))
+    return fail(PLX_ERR_INVALID, "plx_backward_tiles: nhot must be in [0, 32767]");
   if (d->tbl_len < 0 || d->tbl_len > PLX_MAX_TBL)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: tbl_len must be in [0, PLX_MAX_TBL]");
   const size_t tbl = d->update ? static_cast<size_t>(d->tbl_len) * 4 : 0;
   const size_t lds = (d->fold ? static_cast<size_t>(d->tile_size) * 4 +
+                                    static_cast<size_t>((2 * d->tile_size + 15) & ~15) + kTileInfo * 4 +
                                     static_cast<size_t>((d->nhot + 3) & ~3) * 4
                               : 0) + tbl;
   if (lds > 160 * 1024) return fail(PLX_ERR_UNSUPPORTED, "plx_backward_tiles: tile does not fit in LDS");

@@ -431,9 +431,10 @@ class StepFn:
             bp = plan.backward
             d.monoid = bp.monoid
             d.nhot = bt.nhot
+            d.hot_base = bt.hot_base
+            d.tile_info = bt.tile_info.data_ptr()
             d.grp_off = bt.grp_off.data_ptr()
-            d.grp_se = bt.grp_se.data_ptr()
-            d.grp_tgt = bt.grp_tgt.data_ptr()
+            d.grp = bt.grp.data_ptr()
             d.sorted_rank = bt.sorted_rank.data_ptr()
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()

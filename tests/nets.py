@@ -15,6 +15,7 @@ import numpy as np
 
 import plastax_amd as px
 import plastax_amd.numpy as jnp
+from plastax_amd import synth
 from plastax_amd.state import column_to_numpy
 
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
@@ -176,3 +177,24 @@ def oracle_for(ox, net, static, state, **kw):
     plan = compile_plan(net, static)
     return ox.OracleNet(static, host_units(static, state), host_conns(static, state), plan,
                         state.globals_, **kw)
+
+
+def hub_edges(seed: int, widths: tuple[int, ...] = (64, 256, 512, 16), fan: tuple[int, ...] = (4, 6, 12),
+              hubs: int = 2) -> synth.EdgeList:
+    """A layered net whose first `hubs` units of every layer feed every unit
+    of the next: with short rows a backward tile holds many destinations,
+    so a hub's (tile, source) group runs over many ranks."""
+    rng = np.random.default_rng(seed)
+    base = np.concatenate([[0], np.cumsum(widths)])
+    src, dst = [], []
+    for l in range(len(widths) - 1):
+        for j in range(widths[l + 1]):
+            others = rng.choice(np.arange(hubs, widths[l]), size=fan[l] - hubs, replace=False)
+            for i in np.concatenate([np.arange(hubs), others]):
+                src.append(base[l] + i)
+                dst.append(base[l + 1] + j)
+    src = np.asarray(src, dtype=np.int32)
+    dst = np.asarray(dst, dtype=np.int32)
+    w = (rng.standard_normal(src.size) * 0.3).astype(np.float32)
+    return synth.EdgeList(int(base[-1]), src, dst, w, np.arange(widths[0], dtype=np.int32),
+                          np.arange(base[-2], base[-1], dtype=np.int32))

@@ -252,6 +252,26 @@ def test_many_tiles_and_hot_sources_bit_exact(oracle, tile: int, nsuper: int) ->
     _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile, nsuper=nsuper)
 
 
+@pytest.mark.parametrize("tile,nsuper", [(128, 512), (128, 3)])
+def test_hub_groups_over_many_ranks_bit_exact(oracle, tile: int, nsuper: int) -> None:
+    """Short rows under hub sources: a hub's (tile, source) group spans 15 or
+    more ranks, so its end comes from the rank tags' start bits."""
+    e = nets.hub_edges(5)
+    net = nets.make_trained_net(f"H{nsuper}", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, device="cuda")
+    width, n_out = e.input_ids.size, e.output_ids.size
+    rng = np.random.default_rng(14)
+
+    def inputs(k):
+        x = rng.standard_normal(width).astype(np.float32)
+        return x, np.tanh(x[:n_out]).astype(np.float32)
+
+    _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile, nsuper=nsuper)
+
+
 def test_dead_slots_and_headroom_bit_exact(oracle) -> None:
     """Tombstoned slots inside rows and a capacity tail are skipped by every
     pass and never written."""

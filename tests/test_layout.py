@@ -68,66 +68,99 @@ def _emulate_fold(arena, b, g_logical: np.ndarray):
     T = arena.tile
     w = _np(arena.cols["weight"])
     dst = _np(arena.cols["to_id"])
+    src = _np(arena.cols["from_id"])
     dead = _np(arena.cols["dead"]).astype(bool)
-    rank = _np(bt.sorted_rank).view(np.uint16)
-    off = _np(bt.grp_off)
-    se = _np(bt.grp_se).view(np.uint32)
-    tgt = _np(bt.grp_tgt)
+    rank = _np(bt.sorted_rank).view(np.uint16).astype(np.int64)
+    info = _np(bt.tile_info).reshape(-1, _layout.TILE_INFO).astype(np.int64)
+    goff = _np(bt.grp_off)
+    grp = _np(bt.grp).view(np.uint16).astype(np.int64)
     tile_pos = _np(bt.tile_pos)
     super_tile = _np(bt.super_tile)
-    nhot, nsuper = bt.nhot, bt.nsuper
+    nhot, nsuper, hb = bt.nhot, bt.nsuper, bt.hot_base
     assert tile_pos[0] == 0 and tile_pos[-1] == bt.end - bt.base and (np.diff(tile_pos) > 0).all()
     assert (np.diff(tile_pos) <= T).all() and (tile_pos % 4 == 0).all()
     assert super_tile[0] == 0 and super_tile[-1] == bt.ntiles and (np.diff(super_tile) > 0).all()
+    live_end = bt.base + arena.lives[b]
     hot_sb = np.zeros(nsuper * nhot, np.float32)
     cold = np.zeros(_np(bt.cold_partial).size, np.float32)
+    written = np.zeros(cold.size, bool)
     seen = np.zeros(bt.end - bt.base, np.int64)
     for sb in range(nsuper):
         run = np.zeros(nhot, np.float32)
         for k in range(super_tile[sb], super_tile[sb + 1]):
             t0 = bt.base + tile_pos[k]
             n = tile_pos[k + 1] - tile_pos[k]
-            assert off[k] <= off[k + 1]
-            # the tile's live positions, placed at their source-sorted rank
-            order = np.full(n, -1, np.int64)
-            for p in range(n):
-                if not dead[t0 + p]:
-                    r = int(rank[tile_pos[k] + p])
-                    assert r < n and order[r] == -1
-                    order[r] = p
+            nr = int(min(n, max(0, live_end - t0)))
+            # the ranked positions, placed at their rank with the device's tag
+            at = np.full(nr, -1, np.int64)
+            tag = np.zeros(nr, np.int64)
+            buf = np.zeros(nr, np.float32)
+            for p in range(nr):
+                raw = int(rank[tile_pos[k] + p])
+                r = raw & 0x0FFF
+                assert r < nr and at[r] == -1
+                e = t0 + p
+                at[r] = e
+                h = int(src[e]) - hb
+                tag[r] = (raw & _layout.GROUP_START) | (h if 0 <= h < nhot else 0)
+                buf[r] = np.float32(0.0) if dead[e] else np.float32(w[e] * g_field[dst[e]])
+            # (source, position) order, and the start bits mark source changes
+            for r in range(1, nr):
+                a0, a1 = at[r - 1], at[r]
+                assert (src[a0], a0) < (src[a1], a1)
+                assert bool(tag[r] & _layout.GROUP_START) == (src[a0] != src[a1])
+            assert nr == 0 or tag[0] & _layout.GROUP_START
+            hlo, hhi = int(info[k, 0] & 0xFFFF), int(info[k, 0] >> 16)
+            assert all((hlo <= r < hhi) == (0 <= src[at[r]] - hb < nhot) for r in range(nr))
+            bnd = info[k, 1:8]
+            off = info[k, 8:16]
             touched = set()
-            for gi in range(off[k], off[k + 1]):
-                st, ln = int(se[gi] & 0xFFFF), int(se[gi] >> 16)
-                assert ln >= 1 and st + ln <= n
+            for gi in range(goff[k], goff[k + 1]):
+                st, ln = int(grp[gi] & 0x0FFF), int(grp[gi] >> 12)
+                assert tag[st] & _layout.GROUP_START and 1 <= ln <= _layout.LEN_OPEN
+                if ln == _layout.LEN_OPEN:  # at least 15: the run ends at the next start
+                    ln = next((j for j in range(st + 1, nr) if tag[j] & _layout.GROUP_START), nr) - st
+                    assert ln >= _layout.LEN_OPEN
+                assert st + ln <= nr
+                assert all(not tag[j] & _layout.GROUP_START for j in range(st + 1, st + ln))
+                assert st + ln == nr or tag[st + ln] & _layout.GROUP_START
                 v = np.float32(0.0)
                 for j in range(st, st + ln):
-                    loc = int(order[j])
-                    assert 0 <= loc < n
-                    e = t0 + loc
-                    assert not dead[e]
-                    seen[e - bt.base] += 1
-                    v = np.float32(v + np.float32(w[e] * g_field[dst[e]]))
-                if tgt[gi] >= 0:
-                    cold[tgt[gi]] = v
-                else:
-                    h = -1 - tgt[gi]
-                    assert 0 <= h < nhot and h not in touched  # one writer per tile
+                    seen[at[j] - bt.base] += 1
+                    v = np.float32(v + buf[j])
+                if hlo <= st < hhi:
+                    h = int(tag[st] & 0x7FFF)
+                    assert h == src[at[st]] - hb and h not in touched  # one writer per tile
                     touched.add(h)
                     run[h] = np.float32(run[h] + v)
+                else:
+                    c = st - (hhi - hlo if st >= hhi else 0)
+                    slot = int(off[sum(int(c >= x) for x in bnd)] + c)
+                    assert 0 <= slot < cold.size and not written[slot]
+                    written[slot] = True
+                    cold[slot] = v
+            # longest groups first
+            lens = []
+            for gi in range(goff[k], goff[k + 1]):
+                st = int(grp[gi] & 0x0FFF)
+                lens.append(next((j for j in range(st + 1, nr) if tag[j] & _layout.GROUP_START), nr) - st)
+            assert lens == sorted(lens, reverse=True)
         hot_sb[sb * nhot : (sb + 1) * nhot] = run
     live = arena.lives[b]
     assert (seen[:live] == 1).all() and (seen[live:] == 0).all()
     rows = _np(bt.rows)
     row_hot = _np(bt.row_hot)
     row_cold = _np(bt.row_cold)
-    assert row_cold[0] == 0 and (np.diff(row_cold) >= 0).all() and row_cold[-1] == cold.size or (cold.size == 1 and row_cold[-1] == 0)
+    # one slot per cold rank (groups spanning several ranks leave holes)
+    assert row_cold[0] == 0 and (np.diff(row_cold) >= 0).all() and row_cold[-1] <= cold.size
     cold_sb = _np(bt.cold_sb).view(np.uint16)
     cold_idx = _np(bt.cold_idx)
     ncold = row_cold[-1]
-    assert sorted(cold_idx[:ncold].tolist()) == list(range(ncold))  # a permutation of the slots
+    assert np.unique(cold_idx[:ncold]).size == ncold and written[cold_idx[:ncold]].all()  # every cold group's slot
     # the finalize kernel relies on hot rows coming first, in column order,
     # and on the cold workgroups covering the other rows, 256 at most each
     assert (row_hot[:nhot] == np.arange(nhot)).all() and (row_hot[nhot:] == -1).all()
+    assert (rows[:nhot] == hb + np.arange(nhot)).all()  # hot index = id - hot_base
     parts = _np(bt.part_rows)
     assert bt.nparts == parts.size - 1 and parts[0] == nhot and parts[-1] == rows.size
     assert (np.diff(parts) > 0).all() and (np.diff(parts) <= _layout.PART_ROWS).all()
@@ -152,9 +185,10 @@ def _emulate_fold(arena, b, g_logical: np.ndarray):
     return out
 
 
-@pytest.mark.parametrize("tile,nsuper", [(64, 512), (256, 512), (64, 7), (96, 3)])
-def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int, nsuper: int) -> None:
-    e = synth.c2_topological(seed=2, scale=512, layers=4)
+@pytest.mark.parametrize("tile,nsuper,hub", [(64, 512, False), (256, 512, False), (64, 7, False), (96, 3, False),
+                                              (128, 512, True), (128, 3, True)])
+def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int, nsuper: int, hub: bool) -> None:
+    e = nets.hub_edges(4) if hub else synth.c2_topological(seed=2, scale=512, layers=4)
     net = nets.make_trained_net("L", nets.TanhForward(), nets.TanhBackward(),
                                 px.optim.sgd(0.1, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
     static, state, arena = _arena(net, e, tile, nsuper=nsuper)
@@ -166,6 +200,9 @@ def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int, nsuper: 
     g = rng.standard_normal(static.num_units).astype(np.float32)
     o.units["grad_pre_act"][:] = g
     assert any(arena.bwd[b].nhot > 0 for b in range(1, arena.num_buckets))
+    if hub:  # groups of 15 or more ranks (their end is found from the start bits)
+        assert any(((_np(arena.bwd[b].grp).view(np.uint16) >> 12) == _layout.LEN_OPEN).any()
+                   for b in range(1, arena.num_buckets))
     for b in range(1, arena.num_buckets):
         got = _emulate_fold(arena, b, g)
         want = o._reduce_bwd(b, "grad_pre_act", 0)
