@@ -164,6 +164,11 @@ typedef struct plx_tile_desc {
   float* s1;
   float* s2;
   const float* g;       /* the backward map's linear_input field         */
+  /* Optional (null: TO_ID is read from dst): with positions sorted by
+   * destination, dst8[p - base] + tile_dst0[tile] is TO_ID of every position
+   * p below live_end (one byte per position instead of four). */
+  const uint8_t* dst8;
+  const int32_t* tile_dst0;
   const float* gfield;  /* the update rule's grad field                  */
   const float* act;     /* ACTIVATION                                    */
   const float* pow_table;

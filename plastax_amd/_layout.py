@@ -119,6 +119,8 @@ class BackwardTiles:
     tile_info: torch.Tensor | None = None  # int32 [ntiles, TILE_INFO] hot ranks, cold regions
     grp_off: torch.Tensor | None = None  # int32 [ntiles+1]
     grp: torch.Tensor | None = None  # int16 (uint16 bits) [groups] first rank | min(len, 15) << 12
+    dst8: torch.Tensor | None = None  # uint8 [span] TO_ID - tile_dst0[tile] (None: a tile spans >= 256 ids)
+    tile_dst0: torch.Tensor | None = None  # int32 [ntiles] first destination of each tile
     sorted_rank: torch.Tensor | None = None  # int16 (uint16 bits) [span]: rank | GROUP_START
     hot_sb: torch.Tensor | None = None  # f32 [nsuper*nhot]
     cold_partial: torch.Tensor | None = None  # f32 [ncold]
@@ -291,7 +293,7 @@ class Arena:
             srcs = src[order].astype(np.int64)
             if not self.pipeline and fold and live and not bool((levels[srcs] == b).all()):
                 self.bwd_carry = True
-            self.bwd.append(self._tiles(b, srcs, fold, levels, n))
+            self.bwd.append(self._tiles(b, srcs, dsts, fold, levels, n))
 
         # Rows finalized from the identity before the backward bucket walk:
         # the deepest level (phases.py:1089-1094).
@@ -315,9 +317,10 @@ class Arena:
     def _i32(self, a: np.ndarray) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(np.asarray(a).astype(np.int32))).to(self.device)
 
-    def _tiles(self, b: int, srcs: np.ndarray, fold: bool, levels: np.ndarray, n: int) -> BackwardTiles:
-        """Tile metadata of bucket b; ``srcs`` are the live edges' sources in
-        physical order."""
+    def _tiles(self, b: int, srcs: np.ndarray, dsts: np.ndarray, fold: bool, levels: np.ndarray,
+               n: int) -> BackwardTiles:
+        """Tile metadata of bucket b; ``srcs`` / ``dsts`` are the live edges'
+        sources and destinations in physical order."""
         T = self.tile
         base, end = self.bases[b], self.ends[b]
         tile_pos, super_tile = tile_partition(end - base, T, self.nsuper)
@@ -357,6 +360,18 @@ class Arena:
         g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
         grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
         grp = (g_st[g_perm] | (np.minimum(g_len[g_perm], LEN_OPEN) << 12)).astype(np.uint16)
+        # One-byte destinations: TO_ID = the tile's first destination + a
+        # byte, where every tile's live positions span fewer than 256 ids.
+        dst8 = tile_dst0 = None
+        if live:
+            first = tile_pos[:-1][tile_pos[:-1] < live]
+            d0 = np.zeros(ntiles, dtype=np.int64)
+            d0[: first.size] = dsts[first]
+            delta = dsts - d0[tile_of]
+            if int(delta.max()) < 256:
+                dst8 = np.zeros(int(tile_pos[-1]) + 4, dtype=np.uint8)
+                dst8[:live] = delta
+                tile_dst0 = d0
         # Hot sources: a dense superblock row costs 8 B per superblock (write
         # and read), a cold partial about as much as a scattered 4-byte store
         # plus its read per tile present: as many hot sources as there are
@@ -447,6 +462,8 @@ class Arena:
             hot_base=hb,
             tile_info=torch.from_numpy(info.reshape(-1).astype(np.uint32).view(np.int32)).to(dev),
             grp_off=self._i32(grp_off),
+            dst8=None if dst8 is None else torch.from_numpy(dst8).to(dev),
+            tile_dst0=None if tile_dst0 is None else self._i32(tile_dst0),
             grp=torch.from_numpy(np.concatenate([grp, np.zeros(1, np.uint16)]).view(np.int16)).to(dev),
             # (one spare entry each: a bucket without live edges still gets
             # real, if unused, tables)

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 9  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 10  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -119,6 +119,8 @@ class plx_tile_desc(ctypes.Structure):
         ("s1", c_vp),
         ("s2", c_vp),
         ("g", c_vp),
+        ("dst8", c_vp),
+        ("tile_dst0", c_vp),
         ("gfield", c_vp),
         ("act", c_vp),
         ("pow_table", c_vp),

@@ -62,6 +62,9 @@ __device__ __forceinline__ int4 ld_stream(const int32_t* p) {
   const nt_v4i v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4i*>(p));
   return make_int4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint32_t ld_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
 __device__ __forceinline__ uint2 ld_stream(const uint16_t* p) {
   const nt_v2u v = __builtin_nontemporal_load(reinterpret_cast<const nt_v2u*>(p));
   return make_uint2(v.x, v.y);
@@ -749,15 +752,23 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   uint32_t dv[U];
   int64_t ta = 0;
   int na = 0;
+  // With dst8, a position's TO_ID is its tile's first destination plus a
+  // one-byte delta (positions are destination-sorted): tv[i].x holds the
+  // quad's four deltas and ad0 the tile's base.
+  int ad0 = 0;
   auto load_addr = [&](int blk) {
     ta = d.base + d.tile_pos[blk];
     na = d.tile_pos[blk + 1] - d.tile_pos[blk];
+    if (d.dst8) ad0 = d.tile_dst0[blk];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = threadIdx.x + i * kTileBlock;
       if (4 * q < na) {
         const int64_t e = ta + 4 * q;
-        tv[i] = ld_stream(d.dst + e);
+        if (d.dst8)
+          tv[i].x = static_cast<int>(ld_stream(d.dst8 + (e - d.base)));
+        else
+          tv[i] = ld_stream(d.dst + e);
         if (RULE >= 0 || FOLD) sv[i] = ld_stream(d.src + e);
         dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e) : dead_from_end(e, d.live_end);
       }
@@ -781,7 +792,12 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const bool in = 4 * (threadIdx.x + i * kTileBlock) < na;
-      const int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
+      int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
+      if (d.dst8) {
+        const uint32_t dq = static_cast<uint32_t>(tv[i].x);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) di[k] = ad0 + static_cast<int>((dq >> (8 * k)) & 0xFFu);
+      }
       const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -1597,7 +1613,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 9; }
+int32_t plx_abi_version(void) { return 10; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[15] = {
@@ -1650,6 +1666,7 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile / superblock tables missing");
   if (!d->src || !d->dst || !d->weight)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
+  if (d->dst8 && !d->tile_dst0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: dst8 needs tile_dst0");
   if (d->step_mode != 0 && d->step_mode != 1)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: step_mode must be 0 or 1");
   if (d->fold && (!d->tile_info || !d->grp_off || !d->grp || !d->sorted_rank || !d->g || !d->cold_partial ||

@@ -435,6 +435,9 @@ class StepFn:
             d.tile_info = bt.tile_info.data_ptr()
             d.grp_off = bt.grp_off.data_ptr()
             d.grp = bt.grp.data_ptr()
+            if bt.dst8 is not None:
+                d.dst8 = bt.dst8.data_ptr()
+                d.tile_dst0 = bt.tile_dst0.data_ptr()
             d.sorted_rank = bt.sorted_rank.data_ptr()
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
