@@ -165,10 +165,11 @@ typedef struct plx_tile_desc {
   float* s2;
   const float* g;       /* the backward map's linear_input field         */
   /* Optional (null: TO_ID is read from dst): with positions sorted by
-   * destination, dst8[p - base] + tile_dst0[tile] is TO_ID of every position
-   * p below live_end (one byte per position instead of four). */
+   * destination, blk_dst0[(p - base) >> 12] + dst8[p - base] is TO_ID of
+   * every position p below live_end (one byte per position instead of four;
+   * blocks of 4,096 positions). */
   const uint8_t* dst8;
-  const int32_t* tile_dst0;
+  const int32_t* blk_dst0;
   const float* gfield;  /* the update rule's grad field                  */
   const float* act;     /* ACTIVATION                                    */
   const float* pow_table;
@@ -249,6 +250,10 @@ typedef struct plx_update_desc {
   const float* gfield;
   const float* act;
   const float* pow_table;
+  /* Optional, as plx_tile_desc's (positions here start at 0):
+   * blk_dst0[p >> 12] + dst8[p] is TO_ID below live_end. */
+  const uint8_t* dst8;
+  const int32_t* blk_dst0;
   float p[8];
 } plx_update_desc;
 

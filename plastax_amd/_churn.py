@@ -101,6 +101,8 @@ class ChurnArena(Arena):
         self.fwd = []
         self.bwd = []
         self.lists: list[SourceLists] = []
+        self.dst8 = [None] * nb  # TO_ID is read in full (plx_update_desc.dst8)
+        self.blk_dst0 = [None] * nb
         self.fwd_carry = True
         self.bwd_carry = True
         self.dead_in_rows = False

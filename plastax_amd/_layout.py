@@ -63,6 +63,7 @@ FIN_HOT_COLS = 16  # hot columns per finalize workgroup (PLX_HOT_COLS)
 XCDS = 8  # MI355X dies: workgroup w of a launch runs on XCD w % 8
 GROUP_START = 0x8000  # sorted_rank bit: the rank starts a (tile, source) group
 LEN_OPEN = 15  # group descriptor length field: 15 or more
+DST8_BLOCK = 4096  # positions per one-byte destination block (kDst8Shift)
 TILE_INFO = 16  # int32 per tile of tile_info (plx_tile_desc)
 
 
@@ -75,6 +76,28 @@ def xcd_item(first: int, n: int) -> np.ndarray:
     cnt = np.where(r < n, (n - r + XCDS - 1) // XCDS, 0)
     first_item = np.concatenate([[0], np.cumsum(cnt)[:-1]])
     return first_item[(first + i) % XCDS] + i // XCDS
+
+
+def dst_bytes(dsts: np.ndarray, span: int) -> tuple[np.ndarray | None, np.ndarray | None]:
+    """One-byte destinations of a bucket whose live positions' TO_ID
+    (``dsts``, destination-sorted) are given: block k of DST8_BLOCK positions
+    has base blk_dst0[k] (its first live destination) and position p holds
+    TO_ID - blk_dst0[p // DST8_BLOCK]. None, None where a block spans 256 ids
+    or more, or the bucket has no live edge."""
+    live = int(dsts.size)
+    if not live:
+        return None, None
+    nblk = -(-span // DST8_BLOCK)
+    pos = np.arange(live, dtype=np.int64)
+    d0 = np.zeros(nblk, dtype=np.int64)
+    firsts = np.arange(0, live, DST8_BLOCK)
+    d0[: firsts.size] = dsts[firsts]
+    delta = dsts - d0[pos // DST8_BLOCK]
+    if int(delta.max()) >= 256:
+        return None, None
+    d8 = np.zeros(span + 4, dtype=np.uint8)
+    d8[:live] = delta
+    return d8, d0
 
 
 def cold_row_parts(row_cold: np.ndarray, first: int) -> np.ndarray:
@@ -119,8 +142,6 @@ class BackwardTiles:
     tile_info: torch.Tensor | None = None  # int32 [ntiles, TILE_INFO] hot ranks, cold regions
     grp_off: torch.Tensor | None = None  # int32 [ntiles+1]
     grp: torch.Tensor | None = None  # int16 (uint16 bits) [groups] first rank | min(len, 15) << 12
-    dst8: torch.Tensor | None = None  # uint8 [span] TO_ID - tile_dst0[tile] (None: a tile spans >= 256 ids)
-    tile_dst0: torch.Tensor | None = None  # int32 [ntiles] first destination of each tile
     sorted_rank: torch.Tensor | None = None  # int16 (uint16 bits) [span]: rank | GROUP_START
     hot_sb: torch.Tensor | None = None  # f32 [nsuper*nhot]
     cold_partial: torch.Tensor | None = None  # f32 [ncold]
@@ -245,6 +266,9 @@ class Arena:
         phys = {name: np.full(size, specs[name].default, dtype=specs[name].dtype) for name in specs}
         phys[DEAD.name][:] = True
         self.lives: list[int] = []
+        # One-byte destinations per bucket (None where a block spans >= 256 ids).
+        self.dst8: list[torch.Tensor | None] = []
+        self.blk_dst0: list[torch.Tensor | None] = []
         self.fwd: list[ForwardRows] = []
         self.bwd: list[BackwardTiles] = []
         self.fwd_carry = False
@@ -294,6 +318,9 @@ class Arena:
             if not self.pipeline and fold and live and not bool((levels[srcs] == b).all()):
                 self.bwd_carry = True
             self.bwd.append(self._tiles(b, srcs, dsts, fold, levels, n))
+            d8, d0 = dst_bytes(dsts, self.ends[b] - base)
+            self.dst8.append(None if d8 is None else torch.from_numpy(d8).to(device))
+            self.blk_dst0.append(None if d0 is None else self._i32(d0))
 
         # Rows finalized from the identity before the backward bucket walk:
         # the deepest level (phases.py:1089-1094).
@@ -360,18 +387,6 @@ class Arena:
         g_perm = np.lexsort((-g_len, g_tile)) if live else g_start
         grp_off = np.searchsorted(g_tile[g_perm], np.arange(ntiles + 1), side="left")
         grp = (g_st[g_perm] | (np.minimum(g_len[g_perm], LEN_OPEN) << 12)).astype(np.uint16)
-        # One-byte destinations: TO_ID = the tile's first destination + a
-        # byte, where every tile's live positions span fewer than 256 ids.
-        dst8 = tile_dst0 = None
-        if live:
-            first = tile_pos[:-1][tile_pos[:-1] < live]
-            d0 = np.zeros(ntiles, dtype=np.int64)
-            d0[: first.size] = dsts[first]
-            delta = dsts - d0[tile_of]
-            if int(delta.max()) < 256:
-                dst8 = np.zeros(int(tile_pos[-1]) + 4, dtype=np.uint8)
-                dst8[:live] = delta
-                tile_dst0 = d0
         # Hot sources: a dense superblock row costs 8 B per superblock (write
         # and read), a cold partial about as much as a scattered 4-byte store
         # plus its read per tile present: as many hot sources as there are
@@ -462,8 +477,6 @@ class Arena:
             hot_base=hb,
             tile_info=torch.from_numpy(info.reshape(-1).astype(np.uint32).view(np.int32)).to(dev),
             grp_off=self._i32(grp_off),
-            dst8=None if dst8 is None else torch.from_numpy(dst8).to(dev),
-            tile_dst0=None if tile_dst0 is None else self._i32(tile_dst0),
             grp=torch.from_numpy(np.concatenate([grp, np.zeros(1, np.uint16)]).view(np.int16)).to(dev),
             # (one spare entry each: a bucket without live edges still gets
             # real, if unused, tables)

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 10  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 11  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -120,7 +120,7 @@ class plx_tile_desc(ctypes.Structure):
         ("s2", c_vp),
         ("g", c_vp),
         ("dst8", c_vp),
-        ("tile_dst0", c_vp),
+        ("blk_dst0", c_vp),
         ("gfield", c_vp),
         ("act", c_vp),
         ("pow_table", c_vp),
@@ -171,6 +171,8 @@ class plx_update_desc(ctypes.Structure):
         ("gfield", c_vp),
         ("act", c_vp),
         ("pow_table", c_vp),
+        ("dst8", c_vp),
+        ("blk_dst0", c_vp),
         ("p", c_f32 * 8),
     ]
 

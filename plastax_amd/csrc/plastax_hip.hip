@@ -62,6 +62,10 @@ __device__ __forceinline__ int4 ld_stream(const int32_t* p) {
   const nt_v4i v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4i*>(p));
   return make_int4(v.x, v.y, v.z, v.w);
 }
+// One-byte destinations (dst8): TO_ID = blk_dst0[rel >> kDst8Shift] + dst8[rel]
+// for a bucket-relative position rel.
+constexpr int kDst8Shift = 12;
+
 __device__ __forceinline__ uint32_t ld_stream(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
@@ -561,11 +565,18 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
   int64_t ea = e;
   int4 sv = make_int4(0, 0, 0, 0), tv = sv;
   uint32_t dv = 0;
+  // With dst8: tv.x holds the quad's four one-byte deltas and tv.y the base
+  // of its 4,096-position block.
   auto load_addr = [&](int64_t at) {
     ea = at;
     if (at < d.n) {
       sv = ld_stream(d.src + at);
-      tv = ld_stream(d.dst + at);
+      if (d.dst8) {
+        tv.x = static_cast<int>(ld_stream(d.dst8 + at));
+        tv.y = d.blk_dst0[at >> kDst8Shift];
+      } else {
+        tv = ld_stream(d.dst + at);
+      }
       dv = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + at) : dead_from_end(at, d.live_end);
     }
   };
@@ -574,7 +585,12 @@ __global__ __launch_bounds__(kUpdBlock) void k_update(plx_update_desc d) {
   float gu[4], ac[4];
   float4 w = make_float4(0.f, 0.f, 0.f, 0.f), s0 = w, s1 = w, s2 = w;
   auto gather = [&]() {
-    const int di[4] = {tv.x, tv.y, tv.z, tv.w};
+    int di[4] = {tv.x, tv.y, tv.z, tv.w};
+    if (d.dst8) {
+      const uint32_t dq = static_cast<uint32_t>(tv.x);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) di[k] = tv.y + static_cast<int>((dq >> (8 * k)) & 0xFFu);
+    }
     const int si[4] = {sv.x, sv.y, sv.z, sv.w};
     const bool in = ea < d.n;
 #pragma unroll
@@ -752,14 +768,19 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   uint32_t dv[U];
   int64_t ta = 0;
   int na = 0;
-  // With dst8, a position's TO_ID is its tile's first destination plus a
-  // one-byte delta (positions are destination-sorted): tv[i].x holds the
-  // quad's four deltas and ad0 the tile's base.
-  int ad0 = 0;
+  // With dst8, a position's TO_ID is the first destination of its 4,096-
+  // position block plus a one-byte delta (positions are destination-sorted):
+  // tv[i].x holds the quad's four deltas; a tile spans at most two blocks,
+  // whose bases are ad_lo and ad_hi.
+  int ab_lo = 0, ad_lo = 0, ad_hi = 0;
   auto load_addr = [&](int blk) {
     ta = d.base + d.tile_pos[blk];
     na = d.tile_pos[blk + 1] - d.tile_pos[blk];
-    if (d.dst8) ad0 = d.tile_dst0[blk];
+    if (d.dst8) {
+      ab_lo = d.tile_pos[blk] >> kDst8Shift;
+      ad_lo = d.blk_dst0[ab_lo];
+      ad_hi = d.blk_dst0[(d.tile_pos[blk + 1] - 1) >> kDst8Shift];
+    }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = threadIdx.x + i * kTileBlock;
@@ -795,8 +816,10 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
       if (d.dst8) {
         const uint32_t dq = static_cast<uint32_t>(tv[i].x);
+        const int rel = static_cast<int>(ta - d.base) + 4 * (static_cast<int>(threadIdx.x) + i * kTileBlock);
+        const int d0 = (rel >> kDst8Shift) == ab_lo ? ad_lo : ad_hi;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) di[k] = ad0 + static_cast<int>((dq >> (8 * k)) & 0xFFu);
+        for (int k = 0; k < 4; ++k) di[k] = d0 + static_cast<int>((dq >> (8 * k)) & 0xFFu);
       }
       const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
@@ -1613,7 +1636,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 10; }
+int32_t plx_abi_version(void) { return 11; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[15] = {
@@ -1666,7 +1689,7 @@ int plx_backward_tiles(const plx_tile_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: tile / superblock tables missing");
   if (!d->src || !d->dst || !d->weight)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: null column");
-  if (d->dst8 && !d->tile_dst0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: dst8 needs tile_dst0");
+  if (d->dst8 && !d->blk_dst0) return fail(PLX_ERR_INVALID, "plx_backward_tiles: dst8 needs blk_dst0");
   if (d->step_mode != 0 && d->step_mode != 1)
     return fail(PLX_ERR_INVALID, "plx_backward_tiles: step_mode must be 0 or 1");
   if (d->fold && (!d->tile_info || !d->grp_off || !d->grp || !d->sorted_rank || !d->g || !d->cold_partial ||

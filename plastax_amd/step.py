@@ -435,9 +435,9 @@ class StepFn:
             d.tile_info = bt.tile_info.data_ptr()
             d.grp_off = bt.grp_off.data_ptr()
             d.grp = bt.grp.data_ptr()
-            if bt.dst8 is not None:
-                d.dst8 = bt.dst8.data_ptr()
-                d.tile_dst0 = bt.tile_dst0.data_ptr()
+            if arena.dst8[b] is not None:
+                d.dst8 = arena.dst8[b].data_ptr()
+                d.blk_dst0 = arena.blk_dst0[b].data_ptr()
             d.sorted_rank = bt.sorted_rank.data_ptr()
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
@@ -629,6 +629,9 @@ class StepFn:
             d.pow_table_len = consts["pow_table"].numel() // 2
         for k, v in enumerate(up.params()):
             d.p[k] = float(v)
+        if arena.dst8[b] is not None:
+            d.dst8 = arena.dst8[b].data_ptr()
+            d.blk_dst0 = arena.blk_dst0[b].data_ptr()
         self._edge_state(d, arena, b, True)
         # positions of this descriptor start at the bucket base
         d.live_end -= base
