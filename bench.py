@@ -142,14 +142,15 @@ def cpu_baseline(px, net, static, e, host_units, host_conns, inputs, targets, st
     from plastax_amd._plan import compile_plan
 
     o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static))
-    o.step(inputs[0], targets[0])  # warm-up
+    losses = [np.float32(o.step(inputs[0], targets[0]))]  # warm-up
     times = []
     for k in range(steps):
         t0 = time.perf_counter()
-        o.step(inputs[(k + 1) % len(inputs)], targets[(k + 1) % len(targets)])
+        losses.append(np.float32(o.step(inputs[(k + 1) % len(inputs)], targets[(k + 1) % len(targets)])))
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     return {
+        "losses": losses,
         "value": float(e.src.size / med),
         "unit": "edges/s",
         "cores": 1,
@@ -482,8 +483,12 @@ def run_c3(args) -> int:
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
     progress(f"C3: {e.src.size} edges, B = {B} ({setup_s:.1f} s)")
+    first_loss = None
     for k in range(args.warmup):
-        gstate = step(gstate, px.StepInputs(xs_d[k], ys_d[k])).state
+        res = step(gstate, px.StepInputs(xs_d[k], ys_d[k]))
+        gstate = res.state
+        if k == 0:
+            first_loss = res.loss
     torch.cuda.synchronize()
     dominant = "update_conn"
     timer = EventTimer({dominant})
@@ -528,6 +533,7 @@ def run_c3(args) -> int:
         "mean_launch_ms": round(dom["mean_ms"], 4),
     }
     cpu = None
+    parity = None
     if not args.no_cpu_baseline:
         from oracle import batched as ob
         from oracle import oracle as ox
@@ -537,8 +543,12 @@ def run_c3(args) -> int:
         o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), None)
         orc = ob.OracleBatch(o, B)
         t1 = time.perf_counter()
-        orc.step(xs[0], ys[0])
+        ref_loss = np.float32(orc.step(xs[0], ys[0]))
         sec = time.perf_counter() - t1
+        if first_loss is not None:
+            # Full-size parity: the first batched step's loss, bit for bit.
+            got = np.float32(float(first_loss))
+            parity = {"steps": 1, "loss_bit_exact": bool(got.view(np.uint32) == ref_loss.view(np.uint32))}
         cpu = {
             "value": float(B / sec),
             "unit": "samples/s",
@@ -568,6 +578,7 @@ def run_c3(args) -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "full_size_parity": parity,
         "kernels": kernels,
         "loss_last": float(last.loss),
         "setup_s": round(setup_s, 1),
@@ -647,7 +658,8 @@ def main() -> int:
     nsteps = args.warmup + args.steps
     rng = np.random.default_rng(args.seed + 2)
     xs = rng.standard_normal((nsteps, width)).astype(np.float32)
-    ts = (sign[None, :] * xs[:, perm]).astype(np.float32)
+    # (dense rows: numpy's fancy indexing returns a column-major array)
+    ts = np.ascontiguousarray((sign[None, :] * xs[:, perm]).astype(np.float32))
     xs_d = torch.from_numpy(xs).to(dev)
     ts_d = torch.from_numpy(ts).to(dev)
     step.arena(gstate)  # physical layout build (host, once)
@@ -655,8 +667,14 @@ def main() -> int:
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
 
+    # The losses of the first steps (warm-up and timed) are kept, on the
+    # device, for the full-size parity check against the CPU oracle's steps.
+    dev_losses = []
     for k in range(args.warmup):
-        gstate = step(gstate, px.StepInputs(xs_d[k], ts_d[k])).state
+        res = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+        gstate = res.state
+        if k <= args.cpu_steps:
+            dev_losses.append(res.loss)
     torch.cuda.synchronize()
 
     # The timed region records HIP events around the dominant kernel (the
@@ -676,6 +694,8 @@ def main() -> int:
     for k in range(args.warmup, nsteps):
         last = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
         gstate = last.state
+        if k <= args.cpu_steps:
+            dev_losses.append(last.loss)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     timer.on = False
@@ -731,9 +751,20 @@ def main() -> int:
         roofline["traffic"] = json.loads(traffic_file.read_text()).get(dominant)
 
     cpu = None
+    parity = None
     progress(f"timed {args.steps} steps: {elapsed * 1e3 / args.steps:.3f} ms/step")
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(px, net, static, e, host_units, host_conns, xs, ts, args.cpu_steps)
+        # Full-size parity: the device's loss of each of the first steps, bit
+        # for bit against the oracle's on the same inputs (the loss of step k
+        # reads every weight after k updates).
+        ref = cpu.pop("losses")
+        got = [np.float32(float(x)) for x in dev_losses]
+        m = min(len(ref), len(got))
+        same = [bool(np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)) for a, b in zip(got[:m], ref[:m])]
+        parity = {"steps": m, "loss_bit_exact": all(same),
+                  "first_mismatch": None if all(same) else same.index(False)}
+        progress(f"full-size parity over {m} steps: {'bit-exact' if all(same) else 'MISMATCH'}")
 
     kernels = kernel_table(kernels)
     line = {
@@ -761,6 +792,7 @@ def main() -> int:
         "step_algorithmic_gbs": round(step_gbs, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "full_size_parity": parity,
         "kernels": kernels,
         "loss_last": loss,
         "setup_s": round(setup_s, 1),

@@ -209,7 +209,8 @@ class StepFn:
         # Input scatter (step.py:598).
         n_in = len(self.static.input_ids)
         if n_in:
-            x_in = torch.as_tensor(inputs.inputs, dtype=torch.float32, device=dev).reshape(-1)
+            # (the kernels read dense arrays: a strided view is copied)
+            x_in = torch.as_tensor(inputs.inputs, dtype=torch.float32, device=dev).reshape(-1).contiguous()
             if x_in.numel() != n_in:
                 raise ValueError(f"step: expected {n_in} inputs, got {x_in.numel()}")
             _lib.check(
@@ -372,7 +373,7 @@ class StepFn:
         n_out = len(self.static.output_ids)
         if inputs.targets is None:
             raise ValueError("step: this net has a loss, so StepInputs.targets is required")
-        t = torch.as_tensor(inputs.targets, dtype=torch.float32, device=dev).reshape(-1)
+        t = torch.as_tensor(inputs.targets, dtype=torch.float32, device=dev).reshape(-1).contiguous()
         if t.numel() != n_out:
             raise ValueError(f"step: expected {n_out} targets, got {t.numel()}")
         lp = plan.loss

@@ -272,6 +272,40 @@ def test_hub_groups_over_many_ranks_bit_exact(oracle, tile: int, nsuper: int) ->
     _run_both(net, static, state, oracle, inputs, 6, {1, 6}, tile=tile, nsuper=nsuper)
 
 
+def test_strided_inputs_and_targets(oracle) -> None:
+    """Inputs and targets given as strided views (rows of column-major
+    arrays, as numpy's fancy indexing returns) step exactly like dense
+    copies: the kernels read dense arrays, so the step copies such views."""
+    e = synth.c2_topological(seed=12, scale=256)
+    net = nets.make_trained_net("SV", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    width = e.input_ids.size
+    rng = np.random.default_rng(15)
+    xs = np.asfortranarray(rng.standard_normal((3, width)).astype(np.float32))
+    ts = np.asfortranarray(np.tanh(xs[:, ::-1]).astype(np.float32))
+    xs_d, ts_d = torch.from_numpy(xs).to("cuda"), torch.from_numpy(ts).to("cuda")
+    assert not xs_d[1].is_contiguous() and not ts_d[1].is_contiguous()
+    losses = []
+    for strided in (True, False):
+        static, state = px.NetworkBuilder.from_edges(
+            net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+            output_ids=e.output_ids, globals_=None, device="cuda")
+        step = px.make_step(net, static)
+        got = []
+        for k in range(3):
+            x, t = (xs_d[k], ts_d[k]) if strided else (xs_d[k].contiguous(), ts_d[k].contiguous())
+            res = step(state, px.StepInputs(x, t))
+            state = res.state
+            got.append(float(res.loss))
+        losses.append(got)
+    assert losses[0] == losses[1]
+    o = nets.oracle_for(oracle, net, static, px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, device="cpu")[1])
+    want = [float(o.step(np.ascontiguousarray(xs[k]), np.ascontiguousarray(ts[k]))) for k in range(3)]
+    assert losses[0] == want
+
+
 def test_dead_slots_and_headroom_bit_exact(oracle) -> None:
     """Tombstoned slots inside rows and a capacity tail are skipped by every
     pass and never written."""
