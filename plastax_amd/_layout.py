@@ -22,15 +22,20 @@ bucket's positions are cut into at most ``NSUPER`` superblocks of near-equal
 length (one device workgroup each) and each superblock into tiles of at most
 ``tile`` positions (``tile_partition``). Within a tile, the live edges of each
 source form one group (``sorted_rank`` gives every live position its rank in
-the tile's (source, position) order, so a group is a run of ranks), folded on
-the device in physical order into one partial per (tile, source). Sources present in many tiles (the Zipf head) are hot:
-the workgroup keeps their running sums in LDS and writes one dense row per
-superblock (``nhot`` wide); the others get source-major runs of cold
-partials. A source's sum is therefore the fold, in superblock order, of its
-superblock sums, each the fold in tile order of its tile partials, each tile
-partial the fold of its terms in (dst, slot) order. Cold partials are stored
-tile-major (each tile's in consecutive slots) and listed source-major by
-``cold_idx``.
+the tile's (source, position) order, so a group is a run of ranks, and marks
+the rank that starts each group), folded on the device in physical order
+into one partial per (tile, source); 2-byte descriptors (first rank, length)
+list a tile's groups longest first. Sources present in many tiles (the Zipf
+head) are hot: taken as the first ids of the bucket's source range, the
+workgroup keeps their running sums in LDS and writes one dense row per
+superblock (``nhot`` wide); the others get cold partials. A source's sum is
+therefore the fold, in superblock order, of its superblock sums, each the
+fold in tile order of its tile partials, each tile partial the fold of its
+terms in (dst, slot) order. Cold partials are stored in one region per XCD
+(the finalize workgroups on XCD x read region x), tile-major inside a region,
+each slot a function of the group's first rank and the tile's region table
+(``tile_info``), and listed source-major by ``cold_idx``. TO_ID is also kept
+as one byte per position over a base per 4,096 positions (``dst_bytes``).
 
 Units are renumbered: the arena fixes a physical unit order (``unit_order``:
 by level, then out-degree descending, then unit id), the edge columns and
