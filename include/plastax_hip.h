@@ -314,6 +314,29 @@ PLX_EXPORT int plx_gather_edges(int64_t n, const int32_t* pos, const float* weig
  * mean (tbl_* ignored; gfield and act batched). */
 PLX_EXPORT int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream);
 
+/* The same update with the edges grouped into tiles of at most 64
+ * destination x 64 source units (tile k: entries tile_off[k] ..
+ * tile_off[k+1], at most 2,048; destination ids tile_base[2k] + 0..63,
+ * source ids tile_base[2k+1] + 0..63), so a workgroup stages its tile's
+ * unit rows through LDS, 64 samples at a time, and each edge reads them from
+ * there. Entry j is the edge at position pos[j] (relative to d's columns),
+ * loc[j] = (dst - dst base) | (src - src base) << 8. Every live edge of
+ * [0, d->n) appears once; the sum over the samples keeps the order of
+ * plx_update_batch (stat_0 + stat_1 + ...), so the results are the same
+ * bits. num_units bounds the staged rows. No counterpart in the reference:
+ * a layout of plx_update_batch's work. */
+typedef struct plx_batch_tiles {
+  int32_t ntiles;
+  int32_t num_units;
+  const int32_t* tile_off;  /* [ntiles + 1] */
+  const int32_t* tile_base; /* [2 * ntiles] */
+  const int32_t* pos;       /* [entries] */
+  const uint16_t* loc;      /* [entries] */
+} plx_batch_tiles;
+
+PLX_EXPORT int plx_update_batch_tiles(const plx_update_desc* d, const plx_batch_tiles* t, int32_t batch,
+                                      void* stream);
+
 /* Batched losses: sample b's outputs at ids[k] * B + b, targets[b * n_out +
  * k], loss into losses[b]; the per-sample fold is plx_loss_elementwise's /
  * plx_loss_softmax_ce's. partials: B * ceil(n_out / 256) floats. */

@@ -105,6 +105,32 @@ def dst_bytes(dsts: np.ndarray, span: int) -> tuple[np.ndarray | None, np.ndarra
     return d8, d0
 
 
+BATCH_TILE_UNITS = 64  # destination / source units per batched-update tile (kTileRows)
+BATCH_TILE_EDGES = 2048  # edges per batched-update tile at most (kTileEdges)
+
+
+def batch_tiles(src: np.ndarray, dst: np.ndarray) -> dict[str, np.ndarray]:
+    """The batched update's tiles of a bucket whose live positions 0.. have
+    sources ``src`` and destinations ``dst`` (physical ids): positions
+    grouped by (dst // 64, src // 64), in position order within a group,
+    groups of more than BATCH_TILE_EDGES cut into several tiles."""
+    u = BATCH_TILE_UNITS
+    n = int(src.size)
+    src = src.astype(np.int64)
+    dst = dst.astype(np.int64)
+    key = (dst // u) * (int(src.max(initial=0)) // u + 1) + src // u
+    order = np.argsort(key, kind="stable")
+    ks = key[order]
+    starts = np.flatnonzero(np.diff(ks)) + 1 if n else np.zeros(0, np.int64)
+    bounds = np.concatenate([[0], starts, [n]]).astype(np.int64) if n else np.zeros(1, np.int64)
+    cuts = [np.arange(lo, hi, BATCH_TILE_EDGES) for lo, hi in zip(bounds[:-1], bounds[1:])]
+    tile_off = np.concatenate(cuts + [[n]]).astype(np.int64) if n else np.zeros(1, np.int64)
+    first = order[tile_off[:-1]]
+    tile_base = np.stack([(dst[first] // u) * u, (src[first] // u) * u], axis=1).reshape(-1)
+    loc = ((dst[order] % u) | ((src[order] % u) << 8)).astype(np.uint16)
+    return {"tile_off": tile_off, "tile_base": tile_base, "pos": order.astype(np.int64), "loc": loc}
+
+
 def cold_row_parts(row_cold: np.ndarray, first: int) -> np.ndarray:
     """Split rows [first, nrows) into workgroups of at most PART_ROWS rows
     and, where rows allow, at most PART_WIN cold partials (one LDS window),

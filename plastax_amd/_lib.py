@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 11  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 12  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -195,6 +195,17 @@ class plx_bwd_batch_desc(ctypes.Structure):
     ]
 
 
+class plx_batch_tiles(ctypes.Structure):
+    _fields_ = [
+        ("ntiles", c_i32),
+        ("num_units", c_i32),
+        ("tile_off", c_vp),
+        ("tile_base", c_vp),
+        ("pos", c_vp),
+        ("loc", c_vp),
+    ]
+
+
 class plx_site_prog(ctypes.Structure):
     _fields_ = [
         ("ninstr", c_i32),
@@ -346,6 +357,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_batch": (c_i32, [ctypes.POINTER(plx_forward_desc), c_i32, c_vp]),
     "plx_backward_batch": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
     "plx_update_batch": (c_i32, [ctypes.POINTER(plx_update_desc), c_i32, c_vp]),
+    "plx_update_batch_tiles": (c_i32, [ctypes.POINTER(plx_update_desc), ctypes.POINTER(plx_batch_tiles), c_i32, c_vp]),
     "plx_gather_edges": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_backward_lists": (c_i32, [ctypes.POINTER(plx_bwd_batch_desc), c_vp]),
     "plx_loss_elementwise_batch": (
@@ -405,6 +417,7 @@ STRUCTS = (
     plx_grow_claim_desc,
     plx_unit_col,
     plx_bwd_batch_desc,
+    plx_batch_tiles,
 )
 
 _lib: ctypes.CDLL | None = None

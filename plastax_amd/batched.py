@@ -32,7 +32,7 @@ from typing import Any
 import numpy as np
 import torch
 
-from plastax_amd import _lib
+from plastax_amd import _layout, _lib
 from plastax_amd._expr import UnsupportedPolicyError
 from plastax_amd._layout import Arena
 from plastax_amd._plan import Plan, program_struct
@@ -307,6 +307,29 @@ class BatchedStepFn(StepFn):
         state.step = state.step + 1
         return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
 
+    def _update_tiles(self, arena: Arena, b: int) -> tuple[Any, tuple]:
+        """Bucket b's batched-update tiles (built once per arena): the edges
+        grouped by 64 destination x 64 source units, so a workgroup stages
+        their unit rows in LDS."""
+        cache = arena.__dict__.setdefault("_batch_tiles", {})
+        if b not in cache:
+            base, live = arena.bases[b], arena.lives[b]
+            src = arena.cols["from_id"][base : base + live].cpu().numpy()
+            dst = arena.cols["to_id"][base : base + live].cpu().numpy()
+            tb = _layout.batch_tiles(src, dst)
+            dev = arena.device
+            cache[b] = {k: torch.from_numpy(v.astype(np.uint16).view(np.int16) if k == "loc" else v.astype(np.int32)).to(dev)
+                        for k, v in tb.items()}
+        c = cache[b]
+        t = _lib.plx_batch_tiles()
+        t.ntiles = int(c["tile_off"].numel()) - 1
+        t.num_units = self.static.num_units
+        t.tile_off = c["tile_off"].data_ptr()
+        t.tile_base = c["tile_base"].data_ptr()
+        t.pos = c["pos"].data_ptr()
+        t.loc = c["loc"].data_ptr()
+        return t, (c,)
+
     def _update_batch(self, plan: Plan, arena: Arena, ub: dict, consts: dict, b: int, stream: int) -> None:
         lib = _lib.load()
         up = plan.update
@@ -334,7 +357,9 @@ class BatchedStepFn(StepFn):
         self._edge_state(d, arena, b, True)
         d.live_end -= base
         d.dead = col("dead") if arena.dead_in_rows else None
-        self._launch("update_conn", lib.plx_update_batch, d, self.batch, stream)
+        t, keep = self._update_tiles(arena, b)
+        self._launch("update_conn", lib.plx_update_batch_tiles, d, t, self.batch, stream)
+        del keep
         self._advance_t(arena, b)
 
 

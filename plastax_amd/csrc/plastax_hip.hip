@@ -1372,6 +1372,119 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch(plx_update_desc d,
   if (nstate >= 3) d.s2[e] = s2;
 }
 
+// The batch-mean update over tiles of <= 64 destination x 64 source units:
+// the tile's gfield and act rows are staged in LDS 64 samples at a time
+// (rows padded to 65 floats: lanes reading different rows at one sample hit
+// different banks), and each edge (up to kTileEdges / kBatchBlock per lane)
+// carries its running sum over the chunks, in sample order.
+constexpr int kTileRows = 64;
+constexpr int kTileChunk = 64;
+constexpr int kTileStride = kTileChunk + 1;
+constexpr int kTileEdgesPer = 8;
+constexpr int kTileEdges = kTileEdgesPer * kBatchBlock;
+
+template <int RULE, bool UNI_T>
+__global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_desc d, plx_batch_tiles t,
+                                                                    int32_t B) {
+  __shared__ float gs[kTileRows * kTileStride];
+  __shared__ float as[kTileRows * kTileStride];
+  const int k = blockIdx.x;
+  const int j0 = t.tile_off[k], j1 = t.tile_off[k + 1];
+  const int dbase = t.tile_base[2 * k], sbase = t.tile_base[2 * k + 1];
+  int64_t pe[kTileEdgesPer];
+  int ld[kTileEdgesPer], ls[kTileEdgesPer];
+  bool use[kTileEdgesPer];
+  float total[kTileEdgesPer];
+#pragma unroll
+  for (int i = 0; i < kTileEdgesPer; ++i) {
+    const int j = j0 + static_cast<int>(threadIdx.x) + i * kBatchBlock;
+    use[i] = j < j1;
+    pe[i] = 0;
+    ld[i] = ls[i] = 0;
+    total[i] = 0.0f;
+    if (use[i]) {
+      pe[i] = t.pos[j];
+      const uint32_t l = t.loc[j];
+      ld[i] = static_cast<int>(l & 0xFFu);
+      ls[i] = static_cast<int>(l >> 8);
+      use[i] = d.dead ? d.dead[pe[i]] == 0 : pe[i] < d.live_end;
+    }
+  }
+  for (int c0 = 0; c0 < B; c0 += kTileChunk) {
+    const int cn = min(kTileChunk, B - c0);
+    // Stage rows [base, base + 64) x samples [c0, c0 + cn) of both fields
+    // (rows past the last unit are not read), every load issued before any
+    // LDS store.
+    constexpr int kStage = kTileRows * kTileChunk / kBatchBlock;
+    float vg[kStage], va[kStage];
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+      const int q = static_cast<int>(threadIdx.x) + i * kBatchBlock;
+      const int r = q / kTileChunk, c = q % kTileChunk;
+      const bool inc = c < cn;
+      vg[i] = inc && dbase + r < t.num_units ? d.gfield[static_cast<int64_t>(dbase + r) * B + c0 + c] : 0.0f;
+      va[i] = inc && sbase + r < t.num_units ? d.act[static_cast<int64_t>(sbase + r) * B + c0 + c] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+      const int q = static_cast<int>(threadIdx.x) + i * kBatchBlock;
+      const int r = q / kTileChunk, c = q % kTileChunk;
+      gs[r * kTileStride + c] = vg[i];
+      as[r * kTileStride + c] = va[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTileEdgesPer; ++i) {
+      if (!use[i]) continue;
+      const float* g = gs + ld[i] * kTileStride;
+      const float* a = as + ls[i] * kTileStride;
+      float s = total[i];
+      int c = 0;
+      if (c0 == 0) {
+        s = g[0] * a[0];  // the sum starts from sample 0's term, not from +0.0
+        c = 1;
+      }
+      // Eight samples' LDS reads in flight per step of the sequential sum.
+      for (; c + 8 <= cn; c += 8) {
+        float x[8], y[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          x[k] = g[c + k];
+          y[k] = a[c + k];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s = s + x[k] * y[k];
+      }
+      for (; c < cn; ++c) s = s + g[c] * a[c];
+      total[i] = s;
+    }
+    __syncthreads();
+  }
+  float den1 = 1.0f, den2 = 1.0f;
+  if (RULE == PLX_RULE_ADAM && UNI_T) {
+    const float step = d.step_t + 1.0f;
+    den1 = 1.0f - adam_pow(d, d.p[1], step, 0);
+    den2 = 1.0f - adam_pow(d, d.p[2], step, 1);
+  }
+  constexpr int nstate =
+      RULE == PLX_RULE_SGD ? 0 : (RULE == PLX_RULE_ADAM ? (UNI_T ? 2 : 3) : 1);
+#pragma unroll
+  for (int i = 0; i < kTileEdgesPer; ++i) {
+    if (!use[i]) continue;
+    const int64_t e = pe[i];
+    const float grad = total[i] / static_cast<float>(B);
+    float w = d.weight[e];
+    float s0 = nstate >= 1 ? d.s0[e] : 0.0f;
+    float s1 = nstate >= 2 ? d.s1[e] : 0.0f;
+    float s2 = nstate >= 3 ? d.s2[e] : 0.0f;
+    update_edge<RULE, UNI_T>(d, grad, den1, den2, w, s0, s1, s2);
+    d.weight[e] = w;
+    if (nstate >= 1) d.s0[e] = s0;
+    if (nstate >= 2) d.s1[e] = s1;
+    if (nstate >= 3) d.s2[e] = s2;
+  }
+}
+
 template <typename T>
 __global__ void k_reduce_batch(int64_t n, int32_t B, int32_t mode, const T* src, T* dst) {
   const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1636,10 +1749,10 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 11; }
+int32_t plx_abi_version(void) { return 12; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[15] = {
+  const int64_t sizes[16] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
       sizeof(plx_partials_desc),    sizeof(plx_update_desc),
@@ -1647,9 +1760,9 @@ int plx_struct_sizes(int64_t* out, int32_t n) {
       sizeof(plx_sort_key),         sizeof(plx_sort_desc),
       sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
       sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col),
-      sizeof(plx_bwd_batch_desc)};
-  for (int32_t k = 0; k < n && k < 15; ++k) out[k] = sizes[k];
-  return 15;
+      sizeof(plx_bwd_batch_desc),   sizeof(plx_batch_tiles)};
+  for (int32_t k = 0; k < n && k < 16; ++k) out[k] = sizes[k];
+  return 16;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
@@ -1961,6 +2074,42 @@ int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream) {
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_update_batch: unknown rule");
   }
   return check_launch("plx_update_batch");
+}
+
+int plx_update_batch_tiles(const plx_update_desc* d, const plx_batch_tiles* t, int32_t batch,
+                           void* stream) {
+  if (!d || !t) return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: null descriptor");
+  if (batch < 1) return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: batch must be >= 1");
+  if (t->ntiles < 0 || t->num_units < 0) return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: negative size");
+  if (t->ntiles == 0 || d->n == 0) return PLX_OK;
+  if (!t->tile_off || !t->tile_base || !t->pos || !t->loc)
+    return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: null tile table");
+  if (!d->weight || !d->gfield || !d->act) return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: null column");
+  if (d->step_mode != 0 && d->step_mode != 1)
+    return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: step_mode must be 0 or 1");
+  if ((d->rule == PLX_RULE_MOMENTUM || d->rule == PLX_RULE_RMSPROP) && !d->s0)
+    return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: state column missing");
+  if (d->rule == PLX_RULE_ADAM && (!d->s0 || !d->s1 || (d->step_mode == 0 && !d->s2)))
+    return fail(PLX_ERR_INVALID, "plx_update_batch_tiles: Adam state columns missing");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>(t->ntiles);
+  switch (d->rule) {
+    case PLX_RULE_SGD: k_update_batch_tiles<PLX_RULE_SGD, false><<<grid, kBatchBlock, 0, s>>>(*d, *t, batch); break;
+    case PLX_RULE_MOMENTUM:
+      k_update_batch_tiles<PLX_RULE_MOMENTUM, false><<<grid, kBatchBlock, 0, s>>>(*d, *t, batch);
+      break;
+    case PLX_RULE_ADAM:
+      if (d->step_mode == 1)
+        k_update_batch_tiles<PLX_RULE_ADAM, true><<<grid, kBatchBlock, 0, s>>>(*d, *t, batch);
+      else
+        k_update_batch_tiles<PLX_RULE_ADAM, false><<<grid, kBatchBlock, 0, s>>>(*d, *t, batch);
+      break;
+    case PLX_RULE_RMSPROP:
+      k_update_batch_tiles<PLX_RULE_RMSPROP, false><<<grid, kBatchBlock, 0, s>>>(*d, *t, batch);
+      break;
+    default: return fail(PLX_ERR_UNSUPPORTED, "plx_update_batch_tiles: unknown rule");
+  }
+  return check_launch("plx_update_batch_tiles");
 }
 
 int plx_loss_elementwise_batch(int32_t n_out, const int32_t* output_ids, const float* targets,

@@ -345,3 +345,29 @@ def test_one_byte_destinations_fall_back_on_wide_blocks() -> None:
     d8, d0 = _layout.dst_bytes(np.repeat(np.arange(300), 16), 4800)
     assert d8 is not None and d0.tolist() == [0, 256] and int(d8[4096]) == 0 and int(d8[4095]) == 255
     assert _layout.dst_bytes(np.arange(300), 300) == (None, None)
+
+
+def test_batch_tiles_cover_every_live_edge_once() -> None:
+    """The batched update's tiles: every live position once, grouped by 64
+    destination x 64 source units (positions ascending inside a group), at
+    most BATCH_TILE_EDGES per tile, and loc / tile_base recover each edge's
+    ids."""
+    rng = np.random.default_rng(3)
+    n = 20000
+    dst = np.sort(rng.integers(0, 5000, n))
+    src = rng.integers(0, 3000, n)
+    src[:3000] = 7  # one dense block: a group cut into several tiles
+    dst[:3000] = 100
+    order = np.lexsort((src, dst))
+    src, dst = src[order], dst[order]
+    tb = _layout.batch_tiles(src, dst)
+    off, base, pos, loc = tb["tile_off"], tb["tile_base"].reshape(-1, 2), tb["pos"], tb["loc"].astype(np.int64)
+    assert sorted(pos.tolist()) == list(range(n))
+    assert off[0] == 0 and off[-1] == n and (np.diff(off) > 0).all()
+    assert (np.diff(off) <= _layout.BATCH_TILE_EDGES).all() and (np.diff(off) == _layout.BATCH_TILE_EDGES).any()
+    assert (base % _layout.BATCH_TILE_UNITS == 0).all()
+    for k in range(off.size - 1):
+        p = pos[off[k] : off[k + 1]]
+        assert (np.diff(p) > 0).all()
+        assert (base[k, 0] + (loc[off[k] : off[k + 1]] & 0xFF) == dst[p]).all()
+        assert (base[k, 1] + (loc[off[k] : off[k + 1]] >> 8) == src[p]).all()
