@@ -316,7 +316,7 @@ PLX_EXPORT int plx_update_batch(const plx_update_desc* d, int32_t batch, void* s
 
 /* The same update with the edges grouped into tiles of at most 64
  * destination x 64 source units (tile k: entries tile_off[k] ..
- * tile_off[k+1], at most 2,048; destination ids tile_base[2k] + 0..63,
+ * tile_off[k+1], at most 1,024; destination ids tile_base[2k] + 0..63,
  * source ids tile_base[2k+1] + 0..63), so a workgroup stages its tile's
  * unit rows through LDS, 64 samples at a time, and each edge reads them from
  * there. Entry j is the edge at position pos[j] (relative to d's columns),

@@ -106,7 +106,7 @@ def dst_bytes(dsts: np.ndarray, span: int) -> tuple[np.ndarray | None, np.ndarra
 
 
 BATCH_TILE_UNITS = 64  # destination / source units per batched-update tile (kTileRows)
-BATCH_TILE_EDGES = 2048  # edges per batched-update tile at most (kTileEdges)
+BATCH_TILE_EDGES = 1024  # edges per batched-update tile at most (kTileEdges)
 
 
 def batch_tiles(src: np.ndarray, dst: np.ndarray) -> dict[str, np.ndarray]:

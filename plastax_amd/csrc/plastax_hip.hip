@@ -1377,10 +1377,13 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch(plx_update_desc d,
 // (rows padded to 65 floats: lanes reading different rows at one sample hit
 // different banks), and each edge (up to kTileEdges / kBatchBlock per lane)
 // carries its running sum over the chunks, in sample order.
-constexpr int kTileRows = 64;
+#ifndef PLX_BATCH_TILE_ROWS
+#define PLX_BATCH_TILE_ROWS 64
+#endif
+constexpr int kTileRows = PLX_BATCH_TILE_ROWS;
 constexpr int kTileChunk = 64;
 constexpr int kTileStride = kTileChunk + 1;
-constexpr int kTileEdgesPer = 8;
+constexpr int kTileEdgesPer = 4;
 constexpr int kTileEdges = kTileEdgesPer * kBatchBlock;
 
 template <int RULE, bool UNI_T>
@@ -1410,21 +1413,25 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_d
       use[i] = d.dead ? d.dead[pe[i]] == 0 : pe[i] < d.live_end;
     }
   }
-  for (int c0 = 0; c0 < B; c0 += kTileChunk) {
-    const int cn = min(kTileChunk, B - c0);
-    // Stage rows [base, base + 64) x samples [c0, c0 + cn) of both fields
-    // (rows past the last unit are not read), every load issued before any
-    // LDS store.
-    constexpr int kStage = kTileRows * kTileChunk / kBatchBlock;
-    float vg[kStage], va[kStage];
+  // Rows [base, base + 64) x samples [c0, c0 + 64) of both fields (rows
+  // past the last unit and samples past B are not read) go to registers, every
+  // load issued before any is used; the next chunk's loads are in flight while
+  // this chunk is summed from LDS.
+  constexpr int kStage = kTileRows * kTileChunk / kBatchBlock;
+  float vg[kStage], va[kStage];
+  auto stage_load = [&](int c0) {
 #pragma unroll
     for (int i = 0; i < kStage; ++i) {
       const int q = static_cast<int>(threadIdx.x) + i * kBatchBlock;
       const int r = q / kTileChunk, c = q % kTileChunk;
-      const bool inc = c < cn;
+      const bool inc = c0 + c < B;
       vg[i] = inc && dbase + r < t.num_units ? d.gfield[static_cast<int64_t>(dbase + r) * B + c0 + c] : 0.0f;
       va[i] = inc && sbase + r < t.num_units ? d.act[static_cast<int64_t>(sbase + r) * B + c0 + c] : 0.0f;
     }
+  };
+  stage_load(0);
+  for (int c0 = 0; c0 < B; c0 += kTileChunk) {
+    const int cn = min(kTileChunk, B - c0);
 #pragma unroll
     for (int i = 0; i < kStage; ++i) {
       const int q = static_cast<int>(threadIdx.x) + i * kBatchBlock;
@@ -1433,6 +1440,7 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_d
       as[r * kTileStride + c] = va[i];
     }
     __syncthreads();
+    if (c0 + kTileChunk < B) stage_load(c0 + kTileChunk);
 #pragma unroll
     for (int i = 0; i < kTileEdgesPer; ++i) {
       if (!use[i]) continue;
