@@ -57,6 +57,14 @@ def test_every_rule_on_the_batch_mean(oracle, rule: str) -> None:
     _run(oracle, bc.tanh_mse_net(make()), [16, 32, 8], 0.4, 0.0, 8, 3, seed=2)
 
 
+def test_dense_tiles_are_split(oracle) -> None:
+    """90 % keep: a 64 x 64-unit tile of the batched update holds ~3,700
+    edges, so it is cut into several tiles of at most 1,024 edges (samples
+    in two chunks of 64, the last one short)."""
+    opt = px.optim.adam(1e-2, nets.GRAD_PRE_ACT)
+    _run(oracle, bc.tanh_mse_net(opt), [64, 128, 64, 8], 0.9, 0.0, 100, 2, seed=6)
+
+
 def test_c3_shaped_softmax_batch(oracle) -> None:
     """C3's shape scaled down: 784-128-128-10 at 10 % keep, B = 256,
     softmax cross-entropy, Adam."""
