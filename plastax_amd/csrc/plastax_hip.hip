@@ -2090,8 +2090,10 @@ int plx_forward_batch(const plx_forward_desc* d, int32_t batch, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned block = batch >= kBatchBlock ? kBatchBlock : static_cast<unsigned>((batch + 63) / 64 * 64);
   const unsigned grid = static_cast<unsigned>(d->nrows);
-  if (batch % 4 == 0 && batch >= 128) {
+  if (batch % 4 == 0 && batch >= 128 && d->nrows >= 256) {
     // 16-byte row loads: x rows are 16-byte aligned when B is a multiple of 4.
+    // (A level of few rows keeps a 256-lane workgroup per row: with one wave
+    // per row it would leave the GPU idle.)
     switch (d->monoid) {
       case PLX_MONOID_SUM: k_forward_batch4<PLX_MONOID_SUM><<<grid, 64, 0, s>>>(*d, batch); break;
       case PLX_MONOID_PROD: k_forward_batch4<PLX_MONOID_PROD><<<grid, 64, 0, s>>>(*d, batch); break;
@@ -2125,8 +2127,9 @@ int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream) {
   const int batch = d->batch;
   const unsigned block = batch >= kBatchBlock ? kBatchBlock : static_cast<unsigned>((batch + 63) / 64 * 64);
   const unsigned grid = static_cast<unsigned>(d->nrows);
-  if (batch % 4 == 0 && batch >= 128) {
-    // 16-byte row loads: g rows are 16-byte aligned when B is a multiple of 4.
+  if (batch % 4 == 0 && batch >= 128 && d->nrows >= 256) {
+    // 16-byte row loads: g rows are 16-byte aligned when B is a multiple of 4
+    // (few rows: the 256-lane form, as for the forward).
     switch (d->monoid) {
       case PLX_MONOID_SUM: k_backward_batch4<PLX_MONOID_SUM><<<grid, 64, 0, s>>>(*d); break;
       case PLX_MONOID_PROD: k_backward_batch4<PLX_MONOID_PROD><<<grid, 64, 0, s>>>(*d); break;
