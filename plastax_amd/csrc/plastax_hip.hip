@@ -1488,15 +1488,15 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch(plx_update_desc d,
 #endif
 constexpr int kTileRows = PLX_BATCH_TILE_ROWS;
 constexpr int kTileChunk = 64;
-constexpr int kTileStride = kTileChunk + 1;
+constexpr int kTileStride = kTileChunk + 4;  // 16-byte aligned rows, offset by 4 banks each
 constexpr int kTileEdgesPer = 4;
 constexpr int kTileEdges = kTileEdgesPer * kBatchBlock;
 
 template <int RULE, bool UNI_T>
 __global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_desc d, plx_batch_tiles t,
                                                                     int32_t B) {
-  __shared__ float gs[kTileRows * kTileStride];
-  __shared__ float as[kTileRows * kTileStride];
+  __shared__ __align__(16) float gs[kTileRows * kTileStride];
+  __shared__ __align__(16) float as[kTileRows * kTileStride];
   const int k = blockIdx.x;
   const int j0 = t.tile_off[k], j1 = t.tile_off[k + 1];
   const int dbase = t.tile_base[2 * k], sbase = t.tile_base[2 * k + 1];
@@ -1558,16 +1558,22 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_d
         s = g[0] * a[0];  // the sum starts from sample 0's term, not from +0.0
         c = 1;
       }
-      // Eight samples' LDS reads in flight per step of the sequential sum.
+      // Up to the next multiple of 4 one sample at a time, then eight
+      // samples per step from 16-byte LDS reads.
+      for (; c < cn && (c & 3); ++c) s = s + g[c] * a[c];
       for (; c + 8 <= cn; c += 8) {
-        float x[8], y[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          x[k] = g[c + k];
-          y[k] = a[c + k];
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s = s + x[k] * y[k];
+        const float4 x0 = *reinterpret_cast<const float4*>(g + c);
+        const float4 x1 = *reinterpret_cast<const float4*>(g + c + 4);
+        const float4 y0 = *reinterpret_cast<const float4*>(a + c);
+        const float4 y1 = *reinterpret_cast<const float4*>(a + c + 4);
+        s = s + x0.x * y0.x;
+        s = s + x0.y * y0.y;
+        s = s + x0.z * y0.z;
+        s = s + x0.w * y0.w;
+        s = s + x1.x * y1.x;
+        s = s + x1.y * y1.y;
+        s = s + x1.z * y1.z;
+        s = s + x1.w * y1.w;
       }
       for (; c < cn; ++c) s = s + g[c] * a[c];
       total[i] = s;
