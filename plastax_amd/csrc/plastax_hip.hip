@@ -1158,7 +1158,8 @@ __global__ __launch_bounds__(kFinBlock) void k_finalize(plx_partials_desc d, int
 // Each lane folds its sample's terms in the streaming step's order.
 // ---------------------------------------------------------------------------
 constexpr int kBatchBlock = 256;
-constexpr int kBatchUnroll = 8;  // positions whose loads are in flight together
+constexpr int kBatchUnroll = 8;       // positions whose loads are in flight together (one wave per row)
+constexpr int kBatchUnrollWide = 16;  // the same for a 256-lane workgroup per row (levels of few, long rows)
 
 // Combines a row's sum into acc and finalizes it for sample lane `idx`.
 template <int M>
@@ -1185,20 +1186,20 @@ __global__ __launch_bounds__(kBatchBlock) void k_forward_batch(plx_forward_desc 
     const int bl = b < B ? b : B - 1;  // every lane's loads stay in its row
     float s = ident;
     int e = e0;
-    for (; e + kBatchUnroll <= e1; e += kBatchUnroll) {
-      int sv[kBatchUnroll];
-      float wv[kBatchUnroll], xv[kBatchUnroll];
-      bool live[kBatchUnroll];
+    for (; e + kBatchUnrollWide <= e1; e += kBatchUnrollWide) {
+      int sv[kBatchUnrollWide];
+      float wv[kBatchUnrollWide], xv[kBatchUnrollWide];
+      bool live[kBatchUnrollWide];
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k) {
+      for (int k = 0; k < kBatchUnrollWide; ++k) {
         sv[k] = d.src[e + k];
         wv[k] = d.weight[e + k];
         live[k] = d.dead ? d.dead[e + k] == 0 : true;
       }
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k) xv[k] = d.x[static_cast<int64_t>(sv[k]) * B + bl];
+      for (int k = 0; k < kBatchUnrollWide; ++k) xv[k] = d.x[static_cast<int64_t>(sv[k]) * B + bl];
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k)
+      for (int k = 0; k < kBatchUnrollWide; ++k)
         if (live[k]) s = Mono<M>::op(s, wv[k] * xv[k]);
     }
     for (; e < e1; ++e) {
@@ -1275,20 +1276,20 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_de
     const int bl = b < B ? b : B - 1;
     float s = ident;
     int j = j0;
-    for (; j + kBatchUnroll <= j1; j += kBatchUnroll) {
-      int tv[kBatchUnroll];
-      float wv[kBatchUnroll], gv[kBatchUnroll];
-      bool live[kBatchUnroll];
+    for (; j + kBatchUnrollWide <= j1; j += kBatchUnrollWide) {
+      int tv[kBatchUnrollWide];
+      float wv[kBatchUnrollWide], gv[kBatchUnrollWide];
+      bool live[kBatchUnrollWide];
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k) {
+      for (int k = 0; k < kBatchUnrollWide; ++k) {
         tv[k] = d.dst[j + k];
         wv[k] = d.weight[j + k];
         live[k] = d.live ? d.live[j + k] != 0 : true;
       }
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k) gv[k] = d.g[static_cast<int64_t>(tv[k]) * B + bl];
+      for (int k = 0; k < kBatchUnrollWide; ++k) gv[k] = d.g[static_cast<int64_t>(tv[k]) * B + bl];
 #pragma unroll
-      for (int k = 0; k < kBatchUnroll; ++k)
+      for (int k = 0; k < kBatchUnrollWide; ++k)
         if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
     }
     for (; j < j1; ++j) {
