@@ -52,16 +52,37 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> pathlib.Path:
-    """Compile every HIP source into the in-tree shared library."""
-    sources = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
+    """Compile every HIP source (in parallel, one object each) and link the
+    in-tree shared library."""
+    sources = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    procs = []
+    objs = []
+    for src in sources:
+        obj = objdir / (src.stem + ".o")
+        objs.append(obj)
+        cmd = [hipcc(), *compile_flags, "-c", "-I", str(ROOT / "include"), str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = []
+    for cmd, proc in procs:
+        out, _ = proc.communicate()
+        if proc.returncode != 0:
+            sys.stderr.write(out)
+            failed.append(proc.returncode)
+    if failed:
+        raise RuntimeError(f"hipcc failed with exit code {failed[0]}")
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), *sources, "-o", str(tmp)]
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+        raise RuntimeError(f"hipcc link failed with exit code {proc.returncode}")
     os.replace(tmp, LIB)
     return LIB
 

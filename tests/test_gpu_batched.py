@@ -72,6 +72,35 @@ def test_c3_shaped_softmax_batch(oracle) -> None:
     _run(oracle, bc.softmax_net(opt), [784, 128, 128, 10], 0.1, 0.0, 256, 2, seed=4, onehot=True)
 
 
+@pytest.mark.parametrize("B", [256, 132])
+def test_wide_levels_run_the_one_wave_row_kernels(oracle, B: int) -> None:
+    """Levels of 512 rows at a batch that is a multiple of 4 and >= 128: the
+    forward of both hidden levels and the backward of both reduced buckets
+    take the one-wave-per-row kernels (k_forward_batch4, k_backward_batch4;
+    plx_forward_batch / plx_backward_batch dispatch them for B % 4 == 0,
+    B >= 128 and >= 256 rows). B = 132 leaves 31 lanes of each wave without
+    samples. Softmax cross-entropy and Adam, as at C3."""
+    opt = px.optim.adam(1e-3, nets.GRAD_PRE_ACT)
+    _run(oracle, bc.softmax_net(opt), [784, 512, 512, 10], 0.1, 0.0, B, 2, seed=7, onehot=True)
+
+
+def test_wide_levels_with_the_max_monoid(oracle) -> None:
+    """The same one-wave-per-row kernels folding with the max monoid in the
+    forward (skip edges carry accumulators across levels)."""
+    opt = px.optim.adam(1e-3, nets.GRAD_PRE_ACT)
+
+    class Net(px.Network):
+        forward_pass = nets.MaxForward()
+        backward_pass = nets.TanhBackward()
+        loss = nets.MSELoss()
+        update_conn = opt.update_conn()
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD)
+        extra_conn_fields = tuple(opt.state_fields)
+        batch_reduction = px.MeanFloatFirstRest()
+
+    _run(oracle, Net, [64, 384, 320, 8], 0.2, 0.02, 256, 2, seed=8)
+
+
 def test_structural_phases_run_once_per_batch(oracle) -> None:
     """tests/test_batched.py:189-229: prune and growth see the reduced state,
     once per batched step."""

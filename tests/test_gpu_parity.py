@@ -330,6 +330,44 @@ def test_dead_slots_and_headroom_bit_exact(oracle) -> None:
     _run_both(net, static, state, oracle, inputs, 4, {1, 4}, tile=512)
 
 
+@pytest.mark.parametrize("dead", [False, True])
+def test_forward_blocks_beyond_the_persistent_grid(oracle, dead: bool) -> None:
+    """A level of more rows than the forward's persistent grid covers in one
+    pass (cu_count x 2 workgroups x 256 rows): workgroups take two row blocks
+    each, so the next block's prefetch and row set-up run. With `dead`,
+    tombstones inside the rows make the forward read the DEAD column."""
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    wide = cu * 2 * 256 * 3 // 2 + 77
+    widths = (1024, wide, 24)
+    rng = np.random.default_rng(21)
+    base = np.cumsum([0, *widths])
+    src = [base[0] + rng.integers(0, widths[0], (wide, 3)).ravel()]
+    dst = [np.repeat(np.arange(base[1], base[2]), 3)]
+    src.append(base[1] + rng.integers(0, wide, (widths[2], 400)).ravel())
+    dst.append(np.repeat(np.arange(base[2], base[3]), 400))
+    src = np.concatenate(src).astype(np.int32)
+    dst = np.concatenate(dst).astype(np.int32)
+    fan = np.bincount(dst, minlength=int(base[-1]))
+    w = (rng.standard_normal(src.size) / np.sqrt(fan[dst])).astype(np.float32)
+    net = nets.make_trained_net(f"Wide{int(dead)}", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, int(base[-1]), src, dst, weights=w, input_ids=np.arange(widths[0]),
+        output_ids=np.arange(base[2], base[3]), globals_=None, device="cuda")
+    if dead:
+        for bucket in state.conns:
+            live = torch.nonzero(bucket["dead"] == 0).flatten()
+            bucket["dead"][live[::7]] = 1
+    rng_x = np.random.default_rng(22)
+
+    def inputs(k):
+        x = rng_x.standard_normal(widths[0]).astype(np.float32)
+        return x, np.tanh(x[: widths[2]]).astype(np.float32)
+
+    print(f"wide forward: {wide} rows in bucket 0, {src.size} edges, dead={dead}", flush=True)
+    _run_both(net, static, state, oracle, inputs, 3, {1, 3})
+
+
 @pytest.mark.parametrize("fwd,bwd", [
     (nets.SigmoidForward(), nets.SigmoidBackward()),
     (nets.ReluForward(), nets.ReluBackward()),
