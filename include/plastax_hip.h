@@ -509,6 +509,18 @@ PLX_EXPORT int plx_scan_i32(int64_t n, const int32_t* n_dev, const int32_t* in, 
 /* Scratch ints plx_compact / plx_scan_i32 / plx_sort need for n elements. */
 PLX_EXPORT int64_t plx_scratch_ints(int64_t n);
 
+/* plx_compact without a workspace: its chunk sums live in a file-scope
+ * device array of PLX_COMPACT_NOALLOC_MAX_N / 2048 ints (128 KiB per GPU,
+ * held until the process ends), so the call allocates nothing. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code under stream capture, serving loops, harnesses that forbid
+ * hipMalloc). n > PLX_COMPACT_NOALLOC_MAX_N returns PLX_ERR_UNSUPPORTED.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or threads) race. */
+#define PLX_COMPACT_NOALLOC_MAX_N (1LL << 26)
+PLX_EXPORT int plx_compact_noalloc(int64_t n, const int32_t* n_dev, int32_t mode, const void* flags,
+                                   int32_t* out, int32_t* count, void* stream);
+
 /* Sort keys, least significant first; each is derived from the index being
  * sorted (idx) and ordered ascending over its low `bits` bits:
  *   I32      a[idx] (int32 read as unsigned; callers keep it >= 0)

@@ -376,6 +376,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_compact": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_scan_i32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_scratch_ints": (c_i64, [c_i64]),
+    "plx_compact_noalloc": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_sort": (c_i32, [ctypes.POINTER(plx_sort_desc), c_vp]),
     "plx_grow_filter": (c_i32, [ctypes.POINTER(plx_grow_filter_desc), c_vp]),
     "plx_grow_mark_repeats": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),

@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/plastax_hip.h"
 #include "px_common.h"
@@ -1327,4 +1328,60 @@ int plx_gather_col(int64_t n, const int32_t* n_dev, const int32_t* idx, const vo
   hipLaunchKernelGGL(k_gather_col, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, n_dev,
                      idx, src, dst, bytes);
   return check_launch("plx_gather_col");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free ordered compaction. plx_compact_noalloc runs plx_compact's
+// kernels with their chunk sums in `scratch`, a file-scope device array, so a
+// caller that cannot allocate (code under stream capture, a serving loop)
+// needs no workspace. Each GPU holds its own copy of the array; its address
+// on a device comes from hipGetSymbolAddress, looked up once per device (the
+// array's name is only a host-side handle and must never reach a kernel).
+// k_chunk_sums overwrites every chunk sum a call reads, so nothing is
+// cleared between calls; calls that overlap on one GPU share the array and
+// race.
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kNoAllocMaxN = PLX_COMPACT_NOALLOC_MAX_N;
+constexpr int64_t kNoAllocInts = (kNoAllocMaxN + kChunk - 1) / kChunk;
+static_assert(kNoAllocInts * kChunk >= kNoAllocMaxN, "scratch holds every chunk sum");
+
+static __device__ __align__(256) int32_t scratch[kNoAllocInts];
+
+namespace {
+
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+int32_t* g_noalloc_ptr[kNoAllocDevices] = {};
+
+// The current device's address of `scratch` (looked up on its first use).
+int noalloc_scratch(int32_t** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(PLX_ERR_HIP, "plx_compact_noalloc: hipGetDevice failed");
+  if (dev < 0 || dev >= kNoAllocDevices) return fail(PLX_ERR_UNSUPPORTED, "plx_compact_noalloc: device ordinal >= 64");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) return fail(PLX_ERR_HIP, "plx_compact_noalloc: hipGetSymbolAddress(scratch) failed");
+    g_noalloc_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_noalloc_ptr[dev];
+  return PLX_OK;
+}
+
+}  // namespace
+
+int plx_compact_noalloc(int64_t n, const int32_t* n_dev, int32_t mode, const void* flags, int32_t* out,
+                        int32_t* count, void* stream) {
+  if (n < 0 || mode < 0 || mode > PLX_FLAG_I32) return fail(PLX_ERR_INVALID, "plx_compact_noalloc: bad n or mode");
+  if (n > kNoAllocMaxN)
+    return fail(PLX_ERR_UNSUPPORTED, "plx_compact_noalloc: n exceeds PLX_COMPACT_NOALLOC_MAX_N (2^26)");
+  if ((n > 0 && (!flags || !out)) || !count) return fail(PLX_ERR_INVALID, "plx_compact_noalloc: null pointer");
+  int32_t* sums = nullptr;
+  const int rc = noalloc_scratch(&sums);
+  if (rc != PLX_OK) return rc;
+  return scan_or_compact(n, n_dev, mode, flags, out, count, sums, static_cast<hipStream_t>(stream),
+                         "plx_compact_noalloc");
 }
