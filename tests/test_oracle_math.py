@@ -151,3 +151,71 @@ def test_initial_levels_longest_path() -> None:
     # inputs stay at level 0 even with an edge into them
     lv = px.topo.initial_levels(3, np.asarray([[1, 0], [0, 2]]), input_ids=(0,))
     assert lv[0] == 0 and lv[2] == 1
+
+
+def _levels_by_definition(n: int, edges: np.ndarray, inputs: tuple[int, ...]) -> tuple[np.ndarray, bool]:
+    """Brute force on a tiny graph: the transitive closure by repeated
+    squaring; a unit on a cycle reaches itself; tainted = on a cycle or
+    reachable from one; an untainted unit's level is its longest incoming
+    path (recursion over predecessors); a tainted one's is one more than its
+    highest untainted predecessor (0 without one). Edges into inputs are
+    dropped for the levels, kept for the cycle flag."""
+    def closure(es):
+        r = np.zeros((n, n), dtype=bool)
+        for a, b in es:
+            r[a, b] = True
+        for _ in range(n.bit_length() + 1):
+            r = r | ((r.astype(np.int64) @ r.astype(np.int64)) > 0)
+        return r
+
+    any_cycle = bool(np.diag(closure(edges)).any()) if len(edges) else False
+    es = [(a, b) for a, b in edges.tolist() if b not in inputs]
+    r = closure(es)
+    cyc = np.diag(r).copy()
+    tainted = cyc | (r[cyc].any(axis=0) if cyc.any() else np.zeros(n, bool))
+    preds = {v: [a for a, b in es if b == v] for v in range(n)}
+    memo: dict[int, int] = {}
+
+    def longest(v):
+        if v not in memo:
+            memo[v] = max((longest(p) + 1 for p in preds[v]), default=0)
+        return memo[v]
+
+    lv = np.zeros(n, dtype=np.int32)
+    for v in range(n):
+        if not tainted[v]:
+            lv[v] = longest(v)
+        else:
+            lv[v] = max((longest(p) + 1 for p in preds[v] if not tainted[p]), default=0)
+    return lv, any_cycle
+
+
+def test_initial_levels_match_the_definition_on_random_graphs() -> None:
+    rng = np.random.default_rng(3)
+    for _ in range(400):
+        n = int(rng.integers(1, 12))
+        m = int(rng.integers(0, 25))
+        edges = np.stack([rng.integers(0, n, m), rng.integers(0, n, m)], 1)
+        if rng.random() < 0.5:
+            edges = edges[edges[:, 0] < edges[:, 1]]
+        inputs = tuple(sorted(set(rng.integers(0, n, int(rng.integers(0, 3))).tolist())))
+        want, cyclic = _levels_by_definition(n, edges, inputs)
+        got = px.topo.initial_levels(n, edges, allow_cycles=True, input_ids=inputs)
+        assert got.tolist() == want.tolist(), (n, edges.tolist(), inputs)
+        if cyclic:
+            with pytest.raises(ValueError, match="cycle"):
+                px.topo.initial_levels(n, edges, input_ids=inputs)
+        else:
+            assert px.topo.initial_levels(n, edges, input_ids=inputs).tolist() == want.tolist()
+
+
+def test_initial_levels_of_a_chain_deeper_than_the_quick_rounds() -> None:
+    n = 200
+    chain = np.stack([np.arange(n - 1), np.arange(1, n)], 1)
+    assert px.topo.initial_levels(n, chain).tolist() == list(range(n))
+    ring = np.concatenate([chain, [[n - 1, 150]]])
+    with pytest.raises(ValueError, match="cycle"):
+        px.topo.initial_levels(n, ring)
+    lv = px.topo.initial_levels(n, ring, allow_cycles=True)
+    # 150 enters the cycle from 149; the rest of the cycle has no untainted predecessor
+    assert lv[:151].tolist() == list(range(151)) and not lv[151:].any()
