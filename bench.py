@@ -136,27 +136,61 @@ def build_c2(px, seed: int, scale: int):
     return C2Net, e
 
 
+def host_cpu() -> dict:
+    """The host's CPU model and counts (the CPU baseline runs on these cores)."""
+    model = None
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def cpu_baseline(px, net, static, e, host_units, host_conns, inputs, targets, steps: int) -> dict:
-    """The oracle (a scalar C port, one thread) on the same workload."""
+    """The oracle (the C restatement, -O3, OpenMP) on the same workload, timed
+    twice from the same initial state: one thread in its sequential form, and
+    all the threads OpenMP is given in its parallel form (the same folds, so
+    the same bits: both legs' losses are returned for the parity check)."""
     from oracle import oracle as ox
     from plastax_amd._plan import compile_plan
 
-    o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static))
-    losses = [np.float32(o.step(inputs[0], targets[0]))]  # warm-up
-    times = []
-    for k in range(steps):
-        t0 = time.perf_counter()
-        losses.append(np.float32(o.step(inputs[(k + 1) % len(inputs)], targets[(k + 1) % len(targets)])))
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    plan = compile_plan(net, static)
+    legs = {}
+    for name, parallel in (("single_thread", False), ("all_cores", True)):
+        o = ox.OracleNet(static, {k: v.copy() for k, v in host_units.items()},
+                         [{k: v.copy() for k, v in b.items()} for b in host_conns], plan, parallel=parallel)
+        threads = o.lib.ox_set_threads(1 if not parallel else max(1, len(os.sched_getaffinity(0))))
+        if parallel and os.environ.get("OMP_NUM_THREADS"):
+            threads = o.lib.ox_set_threads(int(os.environ["OMP_NUM_THREADS"]))
+        losses = [np.float32(o.step(inputs[0], targets[0]))]  # warm-up
+        times = []
+        for k in range(steps):
+            t0 = time.perf_counter()
+            losses.append(np.float32(o.step(inputs[(k + 1) % len(inputs)], targets[(k + 1) % len(targets)])))
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        legs[name] = {"value": float(e.src.size / med), "cores": int(threads), "median_step_ms": round(med * 1e3, 1),
+                      "losses": losses}
+        del o
+        o = None
+        progress(f"CPU baseline ({name}, {threads} thread(s)): {med * 1e3:.1f} ms per C2 step")
+    one, allc = legs["single_thread"], legs["all_cores"]
     return {
-        "losses": losses,
-        "value": float(e.src.size / med),
+        "losses": {k: v.pop("losses") for k, v in legs.items()},
+        "value": allc["value"],
         "unit": "edges/s",
-        "cores": 1,
+        "cores": allc["cores"],
         "kind": "port",
-        "sample": f"{steps} full C2 steps ({e.src.size} edges) after 1 warm-up, median step {med * 1e3:.1f} ms, "
-        "single-threaded C oracle (oracle/plastax_oracle.c)",
+        "sample": f"{steps} full C2 steps ({e.src.size} edges) after 1 warm-up, median step "
+        f"{allc['median_step_ms']} ms on {allc['cores']} threads; the C oracle (oracle/plastax_oracle.c, "
+        "gcc -O3 -march=x86-64-v3 -fopenmp, no contraction), its parallel form",
+        "single_thread": {"value": one["value"], "cores": 1, "median_step_ms": one["median_step_ms"],
+                          "form": "sequential (slot-order loops)"},
+        "host": host_cpu(),
     }
 
 
@@ -514,14 +548,23 @@ def run_c3(args) -> int:
     kernels = kernel_table(kernels)
     edges = int(e.src.size)
     ms = elapsed * 1e3 / args.steps
-    # The batch-mean update reads every edge's columns once (FROM_ID, TO_ID,
-    # DEAD, WEIGHT, m, v, t: 25 B) and writes WEIGHT, m, v, t (16 B), and
-    # gathers two B-wide unit rows per live edge (2 * 4 * B bytes, L2-served).
-    per_launch_hbm = 41 * edges * args.steps / dom["launches"]
+    # The tiled batch-mean update (plx_update_batch_tiles) reads, per live
+    # edge, its position (4 B) and packed tile-local ids (2 B), WEIGHT and the
+    # optimizer state it keeps per edge, and writes WEIGHT and that state
+    # back: Adam with the step count uniform over the bucket keeps m and v
+    # (t is one number), so 4 + 2 + 12 read + 12 written = 30 B; DEAD is read
+    # only when tombstones sit inside the live range. It also gathers two
+    # B-wide unit rows per tile (L2-served, counted apart).
+    arena = gstate._arena
+    uniform_t = all(t is not None for t in arena.t_now)
+    state_cols = 2 if uniform_t else 3
+    per_edge = 4 + 2 + 4 * (1 + state_cols) * 2 + (1 if arena.dead_in_rows else 0)
+    per_launch_hbm = per_edge * edges * args.steps / dom["launches"]
     per_launch_rows = 8 * B * edges * args.steps / dom["launches"]
     ach = per_launch_hbm / (dom["mean_ms"] * 1e-3) / 1e9
     roofline = {
-        "kernel": "update_conn (plx_update_batch)",
+        "kernel": "update_conn (plx_update_batch_tiles)",
+        "bytes_per_edge": per_edge,
         "bound": "hbm",
         "achieved": round(ach, 1),
         "peak": HBM_PEAK_GBS,
@@ -746,9 +789,14 @@ def main() -> int:
             "mean_launch_ms": round(dom["mean_ms"], 4),
             "sampled_launches": dom["launches"],
         }
+    # HBM traffic per launch is a profile figure (rocprofv3 FETCH_SIZE and
+    # WRITE_SIZE of the dominant kernel, scaled by a plain copy), measured at
+    # the commit the file names, not in this run.
     traffic_file = ROOT / "profiles" / "traffic.json"
     if roofline is not None and traffic_file.exists():
-        roofline["traffic"] = json.loads(traffic_file.read_text()).get(dominant)
+        tf = json.loads(traffic_file.read_text())
+        roofline["traffic"] = tf.get(dominant)
+        roofline["traffic_source"] = {k: tf.get(k) for k in ("measured_at", "kernel", "method") if k in tf}
 
     cpu = None
     parity = None
@@ -758,13 +806,19 @@ def main() -> int:
         # Full-size parity: the device's loss of each of the first steps, bit
         # for bit against the oracle's on the same inputs (the loss of step k
         # reads every weight after k updates).
-        ref = cpu.pop("losses")
+        refs = cpu.pop("losses")
         got = [np.float32(float(x)) for x in dev_losses]
-        m = min(len(ref), len(got))
-        same = [bool(np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)) for a, b in zip(got[:m], ref[:m])]
-        parity = {"steps": m, "loss_bit_exact": all(same),
-                  "first_mismatch": None if all(same) else same.index(False)}
-        progress(f"full-size parity over {m} steps: {'bit-exact' if all(same) else 'MISMATCH'}")
+        parity = {}
+        for leg, ref in refs.items():
+            m = min(len(ref), len(got))
+            same = [bool(np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32))
+                    for a, b in zip(got[:m], ref[:m])]
+            parity[leg] = {"steps": m, "loss_bit_exact": all(same),
+                           "first_mismatch": None if all(same) else same.index(False)}
+            progress(f"full-size parity over {m} steps vs the {leg} oracle: "
+                     f"{'bit-exact' if all(same) else 'MISMATCH'}")
+        parity = {"steps": min(p["steps"] for p in parity.values()),
+                  "loss_bit_exact": all(p["loss_bit_exact"] for p in parity.values()), "legs": parity}
 
     kernels = kernel_table(kernels)
     line = {

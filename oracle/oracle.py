@@ -123,6 +123,15 @@ def load() -> ctypes.CDLL:
             _i32p, _i32p, ctypes.c_int32, _f32p,
         ]
         lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
+        _i64p = ctypes.POINTER(ctypes.c_int64)
+        lib.ox_bucket_reduce_fwd_rows.argtypes = [
+            ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, ctypes.c_int32, _f32p,
+        ]
+        lib.ox_bucket_reduce_bwd_tiled_runs.argtypes = [
+            ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, _i32p, _i32p, ctypes.c_int32, _f32p,
+        ]
+        lib.ox_set_threads.restype = ctypes.c_int32
+        lib.ox_set_threads.argtypes = [ctypes.c_int32]
         lib.ox_apply.argtypes = [
             _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
             ctypes.c_int64, _f32p, _u8p, ctypes.c_int32, _f32p,
@@ -205,8 +214,14 @@ class OracleNet:
         piece: int = PIECE,
         tile: int | None = TILE,
         nsuper: int = NSUPER,
+        parallel: bool = False,
     ) -> None:
         self.static = static
+        # parallel: the forward folds by destination rows and the tiled
+        # backward by source runs (the same folds, so the same bits), which
+        # lets the C loops run on the OpenMP team (ox_set_threads).
+        self.parallel = parallel
+        self._fwd_rows: dict = {}
         self.units = {k: np.ascontiguousarray(v) for k, v in units.items()}
         self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in conns]
         self.plan = plan
@@ -251,10 +266,34 @@ class OracleNet:
             nout, n, fptr(acc), bptr(m), pp.monoid, fptr(scratch),
         )
 
+    def _rows(self, b: int) -> tuple[np.ndarray, ...]:
+        """(row_ptr, row_slots, row_unit) of bucket b: its live slots
+        grouped by destination, ascending slot order inside a destination.
+        Cached with the structure (the structural phases drop the cache)."""
+        hit = self._fwd_rows.get(b)
+        if hit is not None:
+            return hit
+        c = self.conns[b]
+        live = np.flatnonzero(~c["dead"].astype(bool))
+        slots = live[np.argsort(c["to_id"][live], kind="stable")].astype(np.int64)
+        dst = c["to_id"][slots]
+        starts = np.concatenate([[0], np.flatnonzero(np.diff(dst)) + 1, [slots.size]]).astype(np.int64)
+        units = np.ascontiguousarray(dst[starts[:-1]].astype(np.int32))
+        self._fwd_rows[b] = (starts, np.ascontiguousarray(slots), units)
+        return self._fwd_rows[b]
+
     def _reduce_fwd(self, b: int, field: str, monoid: int) -> np.ndarray:
         c = self.conns[b]
         n = self.static.num_units
         out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
+        if self.parallel:
+            starts, slots, units = self._rows(b)
+            self.lib.ox_bucket_reduce_fwd_rows(
+                units.size, starts.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                slots.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), iptr(units),
+                iptr(c["from_id"]), fptr(c["weight"]), fptr(self.units[field]), monoid, fptr(out),
+            )
+            return out
         self.lib.ox_bucket_reduce_fwd(
             c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
             fptr(c["weight"]), fptr(self.units[field]), monoid, fptr(out),
@@ -307,6 +346,20 @@ class OracleNet:
         dead_now = c["dead"].astype(bool)[order]
         if dead_now.any():
             order = np.ascontiguousarray(order[~dead_now])
+        if self.parallel:
+            run_off = self._fwd_rows.get(("runs", b)) if not dead_now.any() else None
+            if run_off is None:
+                fr = c["from_id"][order]
+                run_off = np.concatenate([[0], np.flatnonzero(np.diff(fr)) + 1, [order.size]]).astype(np.int64)
+                if not dead_now.any():
+                    self._fwd_rows[("runs", b)] = run_off
+            self.lib.ox_bucket_reduce_bwd_tiled_runs(
+                run_off.size - 1, run_off.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
+                fptr(self.units[field]), iptr(tile), iptr(sb), monoid, fptr(out),
+            )
+            return out
         self.lib.ox_bucket_reduce_bwd_tiled(
             order.size, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
             iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
@@ -456,6 +509,7 @@ class OracleNet:
                 if self.units_added:
                     # new units get rows when the arena is laid out again
                     self._bwd_order = {}
+                    self._fwd_rows = {}
                     self._phys_index = None
             else:
                 self.units_added, self.unit_overflow = 0, False
@@ -471,6 +525,7 @@ class OracleNet:
                 self.needs_resort = res.needs_resort
                 self.tail_start = res.tail_start
                 self._bwd_order = {}
+                self._fwd_rows = {}
                 self._phys_index = None
 
 
@@ -505,6 +560,7 @@ class OracleDriver:
 
     def _relayout(self) -> None:
         self.o._bwd_order = {}
+        self.o._fwd_rows = {}
         self.o._phys_index = None
 
     def _free(self, level: int) -> int:

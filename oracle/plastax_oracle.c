@@ -20,8 +20,11 @@
  * reduce). ox_bucket_reduce_bwd keeps the plain slot-order fold (optionally in
  * pieces) for comparisons against the reference's literal order.
  *
- * Build: see Makefile (gcc -O2 -ffp-contract=off: no contraction, so every
+ * Build: see Makefile (gcc -O3 -ffp-contract=off: no contraction, so every
  * product and sum rounds to float32 exactly as the reference's jnp ops do).
+ * The per-edge and per-unit loops run under OpenMP when it is on: every
+ * iteration writes its own slot and every fold keeps its order inside one
+ * iteration, so the results do not depend on the thread count.
  */
 #include <math.h>
 #include <stdint.h>
@@ -29,6 +32,25 @@
 #include <string.h>
 
 #define OX_API __attribute__((visibility("default")))
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Loops of at least this many iterations run on the OpenMP team. */
+#define OX_PAR_MIN 65536
+
+/* The OpenMP team size for later calls (1: sequential); returns the size
+ * in force, 1 when built without OpenMP. */
+OX_API int32_t ox_set_threads(int32_t n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+  return omp_get_max_threads();
+#else
+  (void)n;
+  return 1;
+#endif
+}
 
 /* ------------------------------------------------------------------------ */
 /* Philox-4x32-10: rng.py:109-141, scripts/parity/reference.py:153-184.      */
@@ -355,8 +377,68 @@ OX_API void ox_bucket_reduce_bwd_tiled(int64_t n, const int64_t* order,
   }
 }
 
+/* ox_bucket_reduce_fwd by destination rows: row r folds, into
+ * out[row_unit[r]] (pre-filled with the identity), the terms of the live
+ * slots row_slots[row_ptr[r] .. row_ptr[r+1]) -- that destination's live
+ * slots in ascending slot order -- so every destination sees the same fold
+ * as the slot-order loop, and the rows run in parallel. */
+OX_API void ox_bucket_reduce_fwd_rows(int64_t nrows, const int64_t* row_ptr,
+                                      const int64_t* row_slots,
+                                      const int32_t* row_unit,
+                                      const int32_t* from, const float* weight,
+                                      const float* x, int32_t monoid,
+                                      float* out) {
+#pragma omp parallel for schedule(dynamic, 256) if (nrows >= 1024)
+  for (int64_t r = 0; r < nrows; ++r) {
+    float v = out[row_unit[r]];
+    for (int64_t k = row_ptr[r]; k < row_ptr[r + 1]; ++k) {
+      int64_t e = row_slots[k];
+      v = ox_combine1(monoid, v, weight[e] * x[from[e]]);
+    }
+    out[row_unit[r]] = v;
+  }
+}
+
+/* ox_bucket_reduce_bwd_tiled by source runs: `order` as there, cut into
+ * nruns runs of one source each (run_off[k] .. run_off[k+1]); each run is
+ * that source's whole fold, so the runs are independent and run in
+ * parallel. */
+OX_API void ox_bucket_reduce_bwd_tiled_runs(int64_t nruns, const int64_t* run_off,
+                                            const int64_t* order,
+                                            const int32_t* from, const int32_t* to,
+                                            const float* weight, const float* g,
+                                            const int32_t* tile, const int32_t* sb,
+                                            int32_t monoid, float* out) {
+  float id = ox_identity(monoid);
+#pragma omp parallel for schedule(dynamic, 256) if (nruns >= 1024)
+  for (int64_t q = 0; q < nruns; ++q) {
+    int64_t k = run_off[q];
+    const int64_t end = run_off[q + 1];
+    if (k >= end) continue;
+    int32_t s = from[order[k]];
+    float total = out[s];
+    while (k < end) {
+      int32_t b = sb[order[k]];
+      float sbsum = id;
+      while (k < end && sb[order[k]] == b) {
+        int32_t t = tile[order[k]];
+        float part = id;
+        while (k < end && tile[order[k]] == t) {
+          int64_t e = order[k];
+          part = ox_combine1(monoid, part, weight[e] * g[to[e]]);
+          ++k;
+        }
+        sbsum = ox_combine1(monoid, sbsum, part);
+      }
+      total = ox_combine1(monoid, total, sbsum);
+    }
+    out[s] = total;
+  }
+}
+
 /* combine_pairwise (monoid.py:124-152): acc = acc op b, elementwise. */
 OX_API void ox_combine(int64_t n, int32_t monoid, float* acc, const float* b) {
+#pragma omp parallel for schedule(static) if (n >= OX_PAR_MIN)
   for (int64_t i = 0; i < n; ++i) acc[i] = ox_combine1(monoid, acc[i], b[i]);
 }
 
@@ -457,13 +539,15 @@ OX_API void ox_apply(const int32_t* prog, int32_t ninstr, const float* consts,
                      float* const* fields, const int32_t* out_field,
                      int32_t nout, int64_t num_units, float* acc,
                      const uint8_t* mask, int32_t monoid, float* scratch) {
-  float outs[OX_NOUT];
+#pragma omp parallel for schedule(static) if (num_units >= OX_PAR_MIN)
   for (int64_t i = 0; i < num_units; ++i) {
+    float outs[OX_NOUT];
     if (!mask[i]) continue;
     ox_run_program(prog, ninstr, consts, fields, i, acc[i], NULL, 0, outs);
     for (int32_t k = 0; k < nout; ++k) scratch[k * num_units + i] = outs[k];
   }
   float id = ox_identity(monoid);
+#pragma omp parallel for schedule(static) if (num_units >= OX_PAR_MIN)
   for (int64_t i = 0; i < num_units; ++i) {
     if (!mask[i]) continue;
     for (int32_t k = 0; k < nout; ++k)
@@ -541,6 +625,7 @@ OX_API float ox_loss_softmax_ce(const float* act, const int32_t* output_ids,
 OX_API void ox_update_sgd(int64_t cap, const int32_t* from, const int32_t* to,
                           const uint8_t* dead, float* w, const float* gfield,
                           const float* act, float lr) {
+  #pragma omp parallel for schedule(static) if (cap >= OX_PAR_MIN)
   for (int64_t e = 0; e < cap; ++e) {
     if (dead[e]) continue;
     float grad = gfield[to[e]] * act[from[e]];
@@ -553,6 +638,7 @@ OX_API void ox_update_momentum(int64_t cap, const int32_t* from,
                                const int32_t* to, const uint8_t* dead, float* w,
                                float* vel, const float* gfield,
                                const float* act, float lr, float mu) {
+  #pragma omp parallel for schedule(static) if (cap >= OX_PAR_MIN)
   for (int64_t e = 0; e < cap; ++e) {
     if (dead[e]) continue;
     float grad = gfield[to[e]] * act[from[e]];
@@ -569,6 +655,7 @@ OX_API void ox_update_adam(int64_t cap, const int32_t* from, const int32_t* to,
                            float* t, const float* gfield, const float* act,
                            float lr, float b1, float b2, float eps, float wd,
                            float omb1, float omb2) {
+  #pragma omp parallel for schedule(static) if (cap >= OX_PAR_MIN)
   for (int64_t e = 0; e < cap; ++e) {
     if (dead[e]) continue;
     float grad = gfield[to[e]] * act[from[e]];
@@ -592,6 +679,7 @@ OX_API void ox_update_rmsprop(int64_t cap, const int32_t* from,
                               const int32_t* to, const uint8_t* dead, float* w,
                               float* ms, const float* gfield, const float* act,
                               float lr, float decay, float omd, float eps) {
+  #pragma omp parallel for schedule(static) if (cap >= OX_PAR_MIN)
   for (int64_t e = 0; e < cap; ++e) {
     if (dead[e]) continue;
     float grad = gfield[to[e]] * act[from[e]];

@@ -333,9 +333,21 @@ constexpr int kFwdQuads = PLX_FWD_QUADS;  // 16-byte quads per thread per window
 constexpr int kFwdWin = 4 * kFwdQuads * kFwdBlock;
 constexpr int kFwdPerCU = PLX_FWD_PER_CU;  // workgroups per CU in the persistent grid
 
+// A window's raw columns: FROM_ID and WEIGHT quads, DEAD bytes.
+struct FwdRaw {
+  int4 sv[kFwdQuads];
+  float4 wv[kFwdQuads];
+  uint32_t dv[kFwdQuads];
+};
+
+// A window: positions [w0, w0 + kFwdWin) of block b, whose rows own [eb, ee).
+struct FwdWin {
+  int b, w0, eb, ee;
+};
+
 template <int M>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
-  __shared__ __align__(16) float buf[kFwdWin];
+  __shared__ __align__(16) float buf[2][kFwdWin];
   __shared__ float tbl[kFwdTbl > 0 ? kFwdTbl : 1];
   const int nblk = (d.nrows + kFwdRows - 1) / kFwdRows;
   const int b0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * nblk / gridDim.x);
@@ -345,96 +357,141 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   const float ident = Mono<M>::id();
   auto row_end = [&](int blk) { return d.row_ptr[min((blk + 1) * kFwdRows, d.nrows)]; };
 
-  // The window in flight: positions [cw, cw + kFwdWin) of block cb, whose
-  // rows own [eb, ee); ee_next is the following block's end.
-  int cb = b0;
-  int eb = d.row_ptr[cb * kFwdRows];
-  int ee = row_end(cb);
-  int ee_next = cb + 1 < b1 ? row_end(cb + 1) : ee;
-  int cw = eb & ~3;
-  int4 sv[kFwdQuads];
-  float4 wv[kFwdQuads];
-  uint32_t dv[kFwdQuads];
-  auto load = [&](int w0, int e_end) {
+  // Windows in order: every block has at least one (an empty block's
+  // window holds nothing). ee_next is the end of the block after the last
+  // window handed out.
+  int ee_next = b0 + 1 < b1 ? row_end(b0 + 1) : 0;
+  auto next_win = [&](const FwdWin& w) {
+    FwdWin n = w;
+    n.w0 = w.w0 + kFwdWin;
+    if (n.w0 >= w.ee) {
+      n.b = w.b + 1;
+      n.eb = w.ee;
+      n.ee = ee_next;
+      n.w0 = n.eb & ~3;
+      if (n.b + 1 < b1) ee_next = row_end(n.b + 1);
+    }
+    return n;
+  };
+  auto load = [&](FwdRaw& R, const FwdWin& w) {
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
       const int q = threadIdx.x + i * kFwdBlock;
-      dv[i] = 0;
-      if (w0 + 4 * q < e_end) {
-        const int e = w0 + 4 * q;
-        sv[i] = ld_stream(d.src + e);
-        wv[i] = ld_stream(d.weight + e);
-        if (d.dead) dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+      R.dv[i] = 0;
+      if (w.w0 + 4 * q < w.ee) {
+        const int e = w.w0 + 4 * q;
+        R.sv[i] = ld_stream(d.src + e);
+        R.wv[i] = ld_stream(d.weight + e);
+        if (d.dead) R.dv[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
       }
     }
   };
-  load(cw, ee);
-  stage_table<kFwdBlock, (kFwdTbl > 0 ? kFwdTbl : 1)>(tbl, d.x, d.tbl_base, tlen);
-
-  int r = cb * kFwdRows + static_cast<int>(threadIdx.x);
-  bool has = threadIdx.x < kFwdRows && r < d.nrows;
-  int my_b = has ? d.row_ptr[r] : 0;
-  int my_e = has ? d.row_ptr[r + 1] : 0;
-  RowPre pre;
-  if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
-  float s = ident;
-  __syncthreads();
-  for (;;) {
-    const int wn = min(kFwdWin, ee - cw);
-    // Only positions of this block's rows contribute; every gather is
-    // issued before any is used.
+  // Terms of window w from its raw columns into out; the loads of window
+  // `ahead` into `spare` go out between the gathers and their use. Only
+  // positions of the window's block rows contribute.
+  auto terms = [&](const FwdRaw& cur, const FwdWin& w, float* out, FwdRaw& spare, const FwdWin& ahead,
+                   bool load_ahead) {
+    const int wn = min(kFwdWin, w.ee - w.w0);
     bool ok[kFwdQuads][4];
     float xv[kFwdQuads][4];
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
-      const int e = cw + 4 * (threadIdx.x + i * kFwdBlock);
+      const int e = w.w0 + 4 * (threadIdx.x + i * kFwdBlock);
       const bool in = 4 * (threadIdx.x + i * kFwdBlock) < wn;
-      const int idx[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+      const int idx[4] = {cur.sv[i].x, cur.sv[i].y, cur.sv[i].z, cur.sv[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        ok[i][k] = in && e + k >= eb && e + k < ee && !((dv[i] >> (8 * k)) & 0xFFu);
+        ok[i][k] = in && e + k >= w.eb && e + k < w.ee && !((cur.dv[i] >> (8 * k)) & 0xFFu);
       gather_k<4>(tbl, d.x, d.tbl_base, tlen, idx, ok[i], xv[i]);
     }
+    if (load_ahead) load(spare, ahead);
 #pragma unroll
     for (int i = 0; i < kFwdQuads; ++i) {
       const int q = threadIdx.x + i * kFwdBlock;
       if (4 * q < wn) {
         float4 o;
-        o.x = ok[i][0] ? wv[i].x * xv[i][0] : ident;
-        o.y = ok[i][1] ? wv[i].y * xv[i][1] : ident;
-        o.z = ok[i][2] ? wv[i].z * xv[i][2] : ident;
-        o.w = ok[i][3] ? wv[i].w * xv[i][3] : ident;
-        *reinterpret_cast<float4*>(buf + 4 * q) = o;
+        o.x = ok[i][0] ? cur.wv[i].x * xv[i][0] : ident;
+        o.y = ok[i][1] ? cur.wv[i].y * xv[i][1] : ident;
+        o.z = ok[i][2] ? cur.wv[i].z * xv[i][2] : ident;
+        o.w = ok[i][3] ? cur.wv[i].w * xv[i][3] : ident;
+        *reinterpret_cast<float4*>(out + 4 * q) = o;
       }
     }
-    // The next window: the rest of this block, else the next block's first.
-    int nb = cb, nw = cw + kFwdWin, neb = eb, nee = ee;
-    if (nw >= ee) {
-      nb = cb + 1;
-      neb = ee;
-      nee = ee_next;
-      nw = neb & ~3;
+  };
+
+  // The rows being folded (block fb): lane's row r, its positions [my_b, my_e).
+  int fb = b0;
+  int r = 0, my_b = 0, my_e = 0;
+  bool has = false;
+  RowPre pre;
+  auto setup_rows = [&]() {
+    r = fb * kFwdRows + static_cast<int>(threadIdx.x);
+    has = threadIdx.x < kFwdRows && r < d.nrows;
+    my_b = has ? d.row_ptr[r] : 0;
+    my_e = has ? d.row_ptr[r + 1] : 0;
+    if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+  };
+  float s = ident;
+  // The lane's row over window w held in `in`: the unaligned head one term
+  // at a time, then aligned 16-byte runs, the last one padded with the
+  // identity past the row's end (for every monoid that leaves the running
+  // value's bits unchanged: a sum that starts at +0 never holds -0).
+  auto fold = [&](const float* in, const FwdWin& w) {
+    const int wn = min(kFwdWin, w.ee - w.w0);
+    const int lo = max(my_b, w.w0) - w.w0;
+    const int hi = min(my_e, w.w0 + wn) - w.w0;
+    if (lo >= hi) return;
+    int j = lo;
+    const int a = min((lo + 3) & ~3, hi);
+    for (; j < a; ++j) s = Mono<M>::op(s, in[j]);
+    for (; j + 8 <= hi; j += 8) {
+      const float4 x0 = *reinterpret_cast<const float4*>(in + j);
+      const float4 x1 = *reinterpret_cast<const float4*>(in + j + 4);
+      s = Mono<M>::op(s, x0.x);
+      s = Mono<M>::op(s, x0.y);
+      s = Mono<M>::op(s, x0.z);
+      s = Mono<M>::op(s, x0.w);
+      s = Mono<M>::op(s, x1.x);
+      s = Mono<M>::op(s, x1.y);
+      s = Mono<M>::op(s, x1.z);
+      s = Mono<M>::op(s, x1.w);
     }
-    if (nb < b1) load(nw, nee);
-    __syncthreads();
-    {
-      const int lo = max(my_b, cw), hi = min(my_e, cw + wn);
-      const float* run = buf + (lo - cw);
-      const int len = hi - lo;
-      int j = 0;
-      for (; j + 4 <= len; j += 4) {
-        const float a0 = run[j], a1 = run[j + 1], a2 = run[j + 2], a3 = run[j + 3];
-        s = Mono<M>::op(s, a0);
-        s = Mono<M>::op(s, a1);
-        s = Mono<M>::op(s, a2);
-        s = Mono<M>::op(s, a3);
-      }
-      for (; j < len; ++j) s = Mono<M>::op(s, run[j]);
+    for (; j < hi; j += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(in + j);
+      s = Mono<M>::op(s, x.x);
+      s = Mono<M>::op(s, j + 1 < hi ? x.y : ident);
+      s = Mono<M>::op(s, j + 2 < hi ? x.z : ident);
+      s = Mono<M>::op(s, j + 3 < hi ? x.w : ident);
     }
-    if (nb != cb) {
-      // The block's rows are complete: combine, finalize, and set up the
-      // next block's rows (their loads land while this window's lanes run
-      // the apply programs).
+  };
+
+  // Prologue: window 0's loads, the table, the first rows, window 0's
+  // terms (window 1's loads go out meanwhile).
+  FwdWin wc{b0, 0, d.row_ptr[b0 * kFwdRows], row_end(b0)};
+  wc.w0 = wc.eb & ~3;
+  FwdRaw A, B;
+  load(A, wc);
+  stage_table<kFwdBlock, (kFwdTbl > 0 ? kFwdTbl : 1)>(tbl, d.x, d.tbl_base, tlen);
+  setup_rows();
+  __syncthreads();
+  FwdWin wn1 = next_win(wc);
+  terms(A, wc, buf[0], B, wn1, wn1.b < b1);
+  __syncthreads();
+  // Step k: window k+1's terms (window k+2's loads go out meanwhile) and
+  // window k's fold in the same phase, one barrier each. `cur` holds window
+  // k+1's loads and `spare` receives window k+2's.
+  int par = 0;
+  auto step = [&](FwdRaw& cur, FwdRaw& spare) -> bool {
+    const bool more = wn1.b < b1;
+    FwdWin wn2 = wn1;
+    if (more) {
+      wn2 = next_win(wn1);
+      terms(cur, wn1, buf[par ^ 1], spare, wn2, wn2.b < b1);
+    }
+    fold(buf[par], wc);
+    if (!more || wn1.b != wc.b) {
+      // Window k closes its block: combine, finalize, and take the next
+      // block's rows.
       if (has) {
         const int u = pre.u;
         const float a = Mono<M>::op(d.acc ? d.acc[u] : ident, s);
@@ -446,21 +503,21 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
         }
       }
       s = ident;
-      if (nb < b1) {
-        r = nb * kFwdRows + static_cast<int>(threadIdx.x);
-        has = threadIdx.x < kFwdRows && r < d.nrows;
-        my_b = has ? d.row_ptr[r] : 0;
-        my_e = has ? d.row_ptr[r + 1] : 0;
-        if (has) pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
-        if (nb + 1 < b1) ee_next = row_end(nb + 1);
+      if (more) {
+        fb = wn1.b;
+        setup_rows();
       }
     }
     __syncthreads();
-    if (nb >= b1) break;
-    cb = nb;
-    cw = nw;
-    eb = neb;
-    ee = nee;
+    if (!more) return true;
+    wc = wn1;
+    wn1 = wn2;
+    par ^= 1;
+    return false;
+  };
+  for (;;) {
+    if (step(B, A)) break;
+    if (step(A, B)) break;
   }
 }
 
