@@ -78,6 +78,23 @@ typedef struct plx_finalize {
   int32_t skip_inputs;
 } plx_finalize;
 
+/* A pass's map, of the product form (connection factor) * (unit factor at
+ * the edge's other end): the reference's linear_input contract
+ * c[WEIGHT, cid] * u[F, other] (phases.py:535-556) and its variants with a
+ * constant factor (a constant map counts live edges: the in- or out-degree
+ * under sum_). With PLX_MAP_W_CONST the connection factor of every edge is
+ * `w` instead of WEIGHT; with PLX_MAP_X_CONST the unit factor is `x`
+ * instead of the gathered field, whose pointer must still name a readable
+ * unit column. flags 0 (a zeroed struct) is the linear map. */
+#define PLX_MAP_W_CONST 1
+#define PLX_MAP_X_CONST 2
+typedef struct plx_map {
+  int32_t flags;
+  float w;
+  float x;
+  int32_t reserved;
+} plx_map;
+
 /* One bucket of the forward pass: _accumulate_into + _apply_masked
  * (sweep.py:113-230, phases.py:972-1015) for a linear map
  * weight * x[from] (phases.py:535-556). Rows are destination units in a CSR
@@ -98,6 +115,7 @@ typedef struct plx_forward_desc {
   float* acc;              /* [num_units] carried accumulator, or null     */
   plx_finalize fin;
   plx_program apply;
+  plx_map map;             /* the map's factors (zeroed: weight * x[from]) */
 } plx_forward_desc;
 
 PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
@@ -174,6 +192,7 @@ typedef struct plx_tile_desc {
   const float* act;     /* ACTIVATION                                    */
   const float* pow_table;
   float p[8];
+  plx_map map;          /* the backward map's factors (zeroed: weight * g[to]) */
 } plx_tile_desc;
 
 PLX_EXPORT int plx_backward_tiles(const plx_tile_desc* d, void* stream);
@@ -292,6 +311,7 @@ typedef struct plx_bwd_batch_desc {
   float* acc;            /* [num_units][B] carried accumulator, or null */
   plx_finalize fin;
   plx_program apply;
+  plx_map map;           /* the map's factors (zeroed: weight * g[dst]) */
 } plx_bwd_batch_desc;
 
 PLX_EXPORT int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream);

@@ -84,77 +84,90 @@ def build() -> pathlib.Path:
 
 
 def load() -> ctypes.CDLL:
+    """The C restatement (built on first use), its signatures declared."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        lib = ctypes.CDLL(str(LIB_PATH))
-        for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf"):
-            getattr(lib, name).restype = ctypes.c_float
-            getattr(lib, name).argtypes = [ctypes.c_float]
-        lib.ox_pow_step.restype = ctypes.c_float
-        lib.ox_pow_step.argtypes = [ctypes.c_float, ctypes.c_float]
-        lib.ox_philox32.restype = ctypes.c_uint32
-        lib.ox_philox32.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
-        lib.ox_philox4x32_10.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 3
-        lib.ox_site_seed.restype = ctypes.c_uint64
-        lib.ox_site_seed.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
-        lib.ox_conn_key.restype = ctypes.c_uint32
-        lib.ox_conn_key.argtypes = [ctypes.c_uint32] * 3
-        lib.ox_site_draw.restype = ctypes.c_uint32
-        lib.ox_site_draw.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32]
-        lib.ox_uniform_int.restype = ctypes.c_uint32
-        lib.ox_uniform_int.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
-        lib.ox_unit_float.restype = ctypes.c_float
-        lib.ox_unit_float.argtypes = [ctypes.c_uint32]
-        lib.ox_loss_elementwise.restype = ctypes.c_float
-        lib.ox_loss_softmax_ce.restype = ctypes.c_float
-        lib.ox_identity.restype = ctypes.c_float
-        lib.ox_identity.argtypes = [ctypes.c_int32]
-        lib.ox_bucket_reduce_fwd.argtypes = [
-            ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32, _f32p
-        ]
-        lib.ox_bucket_reduce_bwd.argtypes = [
-            ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32,
-            ctypes.c_int32, ctypes.c_int32, _f32p, _f32p, _i32p,
-        ]
-        lib.ox_bucket_reduce_bwd_tiled.argtypes = [
-            ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _i32p, _i32p, _f32p, _f32p,
-            _i32p, _i32p, ctypes.c_int32, _f32p,
-        ]
-        lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
-        _i64p = ctypes.POINTER(ctypes.c_int64)
-        lib.ox_bucket_reduce_fwd_rows.argtypes = [
-            ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, ctypes.c_int32, _f32p,
-        ]
-        lib.ox_bucket_reduce_bwd_tiled_runs.argtypes = [
-            ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, _i32p, _i32p, ctypes.c_int32, _f32p,
-        ]
-        lib.ox_set_threads.restype = ctypes.c_int32
-        lib.ox_set_threads.argtypes = [ctypes.c_int32]
-        lib.ox_apply.argtypes = [
-            _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
-            ctypes.c_int64, _f32p, _u8p, ctypes.c_int32, _f32p,
-        ]
-        lib.ox_loss_elementwise.argtypes = [
-            _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
-            _f32p, _f32p, _f32p, ctypes.c_int32,
-        ]
-        lib.ox_loss_softmax_ce.argtypes = [
-            _f32p, _i32p, ctypes.c_int32, _f32p, _f32p, _f32p, ctypes.c_int32
-        ]
-        upd = [ctypes.c_int64, _i32p, _i32p, _u8p, _f32p]
-        lib.ox_update_sgd.argtypes = upd + [_f32p, _f32p, ctypes.c_float]
-        lib.ox_update_momentum.argtypes = upd + [_f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_float]
-        lib.ox_update_adam.argtypes = upd + [_f32p, _f32p, _f32p, _f32p, _f32p] + [ctypes.c_float] * 7
-        lib.ox_update_rmsprop.argtypes = upd + [_f32p, _f32p, _f32p] + [ctypes.c_float] * 4
-        lib.ox_free_block_counts.argtypes = [ctypes.c_int64, _u8p, ctypes.c_int32, _i32p]
-        lib.ox_nth_free_slots.restype = ctypes.c_int64
-        lib.ox_nth_free_slots.argtypes = [
-            ctypes.c_int64, _u8p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)
-        ]
-        _lib = lib
+        _lib = _declare(ctypes.CDLL(str(LIB_PATH)))
     return _lib
+
+
+def load_variant(path: pathlib.Path) -> ctypes.CDLL:
+    """Another build of the same source (e.g. the perturbation build),
+    its signatures declared; not cached."""
+    if not path.exists():
+        build()
+    return _declare(ctypes.CDLL(str(path)))
+
+
+def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
+    for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf"):
+        getattr(lib, name).restype = ctypes.c_float
+        getattr(lib, name).argtypes = [ctypes.c_float]
+    lib.ox_pow_step.restype = ctypes.c_float
+    lib.ox_pow_step.argtypes = [ctypes.c_float, ctypes.c_float]
+    lib.ox_philox32.restype = ctypes.c_uint32
+    lib.ox_philox32.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+    lib.ox_philox4x32_10.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 3
+    lib.ox_site_seed.restype = ctypes.c_uint64
+    lib.ox_site_seed.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+    lib.ox_conn_key.restype = ctypes.c_uint32
+    lib.ox_conn_key.argtypes = [ctypes.c_uint32] * 3
+    lib.ox_site_draw.restype = ctypes.c_uint32
+    lib.ox_site_draw.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32]
+    lib.ox_uniform_int.restype = ctypes.c_uint32
+    lib.ox_uniform_int.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    lib.ox_unit_float.restype = ctypes.c_float
+    lib.ox_unit_float.argtypes = [ctypes.c_uint32]
+    lib.ox_loss_elementwise.restype = ctypes.c_float
+    lib.ox_loss_softmax_ce.restype = ctypes.c_float
+    lib.ox_identity.restype = ctypes.c_float
+    lib.ox_identity.argtypes = [ctypes.c_int32]
+    lib.ox_bucket_reduce_fwd.argtypes = [
+        ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32, _f32p
+    ]
+    lib.ox_bucket_reduce_bwd.argtypes = [
+        ctypes.c_int64, _i32p, _i32p, _u8p, _f32p, _f32p, ctypes.c_int32,
+        ctypes.c_int32, ctypes.c_int32, _f32p, _f32p, _i32p,
+    ]
+    lib.ox_bucket_reduce_bwd_tiled.argtypes = [
+        ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _i32p, _i32p, _f32p, _f32p,
+        _i32p, _i32p, ctypes.c_int32, _f32p,
+    ]
+    lib.ox_combine.argtypes = [ctypes.c_int64, ctypes.c_int32, _f32p, _f32p]
+    _i64p = ctypes.POINTER(ctypes.c_int64)
+    lib.ox_bucket_reduce_fwd_rows.argtypes = [
+        ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, ctypes.c_int32, _f32p,
+    ]
+    lib.ox_bucket_reduce_bwd_tiled_runs.argtypes = [
+        ctypes.c_int64, _i64p, _i64p, _i32p, _i32p, _f32p, _f32p, _i32p, _i32p, ctypes.c_int32, _f32p,
+    ]
+    lib.ox_set_threads.restype = ctypes.c_int32
+    lib.ox_set_threads.argtypes = [ctypes.c_int32]
+    lib.ox_apply.argtypes = [
+        _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
+        ctypes.c_int64, _f32p, _u8p, ctypes.c_int32, _f32p,
+    ]
+    lib.ox_loss_elementwise.argtypes = [
+        _i32p, ctypes.c_int32, _f32p, ctypes.POINTER(_f32p), _i32p, ctypes.c_int32,
+        _f32p, _f32p, _f32p, ctypes.c_int32,
+    ]
+    lib.ox_loss_softmax_ce.argtypes = [
+        _f32p, _i32p, ctypes.c_int32, _f32p, _f32p, _f32p, ctypes.c_int32
+    ]
+    upd = [ctypes.c_int64, _i32p, _i32p, _u8p, _f32p]
+    lib.ox_update_sgd.argtypes = upd + [_f32p, _f32p, ctypes.c_float]
+    lib.ox_update_momentum.argtypes = upd + [_f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_float]
+    lib.ox_update_adam.argtypes = upd + [_f32p, _f32p, _f32p, _f32p, _f32p] + [ctypes.c_float] * 7
+    lib.ox_update_rmsprop.argtypes = upd + [_f32p, _f32p, _f32p] + [ctypes.c_float] * 4
+    lib.ox_free_block_counts.argtypes = [ctypes.c_int64, _u8p, ctypes.c_int32, _i32p]
+    lib.ox_nth_free_slots.restype = ctypes.c_int64
+    lib.ox_nth_free_slots.argtypes = [
+        ctypes.c_int64, _u8p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)
+    ]
+    return lib
+
 
 
 def ptr(a: np.ndarray, ctype: Any) -> Any:
@@ -282,21 +295,34 @@ class OracleNet:
         self._fwd_rows[b] = (starts, np.ascontiguousarray(slots), units)
         return self._fwd_rows[b]
 
-    def _reduce_fwd(self, b: int, field: str, monoid: int) -> np.ndarray:
+    def _factors(self, b: int, pp: Any) -> tuple[np.ndarray, np.ndarray]:
+        """(connection factor per slot, unit factor per unit) of a pass's
+        product map: WEIGHT and the gathered field, or the map's constants
+        spread over the bucket's slots / the units (the term is their float32
+        product either way)."""
+        c = self.conns[b]
+        w = c["weight"] if pp.w_const is None else np.full(c["dead"].size, pp.w_const, np.float32)
+        x = (self.units[pp.field] if pp.field is not None
+             else np.full(self.static.num_units, pp.x_const, np.float32))
+        return w, x
+
+    def _reduce_fwd(self, b: int, pp: Any) -> np.ndarray:
         c = self.conns[b]
         n = self.static.num_units
+        monoid = pp.monoid
+        weight, x = self._factors(b, pp)
         out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
         if self.parallel:
             starts, slots, units = self._rows(b)
             self.lib.ox_bucket_reduce_fwd_rows(
                 units.size, starts.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                 slots.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), iptr(units),
-                iptr(c["from_id"]), fptr(c["weight"]), fptr(self.units[field]), monoid, fptr(out),
+                iptr(c["from_id"]), fptr(weight), fptr(x), monoid, fptr(out),
             )
             return out
         self.lib.ox_bucket_reduce_fwd(
             c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
-            fptr(c["weight"]), fptr(self.units[field]), monoid, fptr(out),
+            fptr(weight), fptr(x), monoid, fptr(out),
         )
         return out
 
@@ -326,9 +352,11 @@ class OracleNet:
             self._bwd_order[b] = (order, tile, sb)
         return self._bwd_order[b]
 
-    def _reduce_bwd(self, b: int, field: str, monoid: int) -> np.ndarray:
+    def _reduce_bwd(self, b: int, pp: Any) -> np.ndarray:
         c = self.conns[b]
         n = self.static.num_units
+        monoid = pp.monoid
+        weight, gx = self._factors(b, pp)
         out = np.full(n, self.lib.ox_identity(monoid), dtype=np.float32)
         if self.tile is None:
             # the reference's literal slot-order fold
@@ -336,7 +364,7 @@ class OracleNet:
             pn = np.zeros(n, dtype=np.int32)
             self.lib.ox_bucket_reduce_bwd(
                 c["dead"].size, iptr(c["from_id"]), iptr(c["to_id"]), bptr(c["dead"]),
-                fptr(c["weight"]), fptr(self.units[field]), n, monoid, 1 << 30,
+                fptr(weight), fptr(gx), n, monoid, 1 << 30,
                 fptr(out), fptr(pc), iptr(pn),
             )
             return out
@@ -356,14 +384,14 @@ class OracleNet:
             self.lib.ox_bucket_reduce_bwd_tiled_runs(
                 run_off.size - 1, run_off.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                 order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
-                iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
-                fptr(self.units[field]), iptr(tile), iptr(sb), monoid, fptr(out),
+                iptr(c["from_id"]), iptr(c["to_id"]), fptr(weight),
+                fptr(gx), iptr(tile), iptr(sb), monoid, fptr(out),
             )
             return out
         self.lib.ox_bucket_reduce_bwd_tiled(
             order.size, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
-            iptr(c["from_id"]), iptr(c["to_id"]), fptr(c["weight"]),
-            fptr(self.units[field]), iptr(tile), iptr(sb), monoid, fptr(out),
+            iptr(c["from_id"]), iptr(c["to_id"]), fptr(weight),
+            fptr(gx), iptr(tile), iptr(sb), monoid, fptr(out),
         )
         return out
 
@@ -376,11 +404,11 @@ class OracleNet:
         acc = np.full(n, fp.identity, dtype=np.float32)
         nb = len(self.conns)
         if self.pipeline:
-            self.lib.ox_combine(n, fp.monoid, fptr(acc), fptr(self._reduce_fwd(0, fp.field, fp.monoid)))
+            self.lib.ox_combine(n, fp.monoid, fptr(acc), fptr(self._reduce_fwd(0, fp)))
             self._apply(fp, acc, ~self.is_input & live)
             return
         for lv in range(nb):
-            out = self._reduce_fwd(lv, fp.field, fp.monoid)
+            out = self._reduce_fwd(lv, fp)
             self.lib.ox_combine(n, fp.monoid, fptr(acc), fptr(out))
             self._apply(fp, acc, (levels == lv + 1) & ~self.is_input & live)
 
@@ -412,12 +440,12 @@ class OracleNet:
         acc = np.full(n, bp.identity, dtype=np.float32)
         nb = len(self.conns)
         if self.pipeline:
-            self.lib.ox_combine(n, bp.monoid, fptr(acc), fptr(self._reduce_bwd(0, bp.field, bp.monoid)))
+            self.lib.ox_combine(n, bp.monoid, fptr(acc), fptr(self._reduce_bwd(0, bp)))
             self._apply(bp, acc, live)
             return
         self._apply(bp, acc, (levels == nb) & ~self.is_input & live)
         for lv in range(nb - 1, 0, -1):
-            out = self._reduce_bwd(lv, bp.field, bp.monoid)
+            out = self._reduce_bwd(lv, bp)
             self.lib.ox_combine(n, bp.monoid, fptr(acc), fptr(out))
             self._apply(bp, acc, (levels == lv) & ~self.is_input & live)
 

@@ -22,6 +22,9 @@
  *
  * Build: see Makefile (gcc -O3 -ffp-contract=off: no contraction, so every
  * product and sum rounds to float32 exactly as the reference's jnp ops do).
+ * Built with -DOX_LIBM_ELEMENTARY (libplastax_oracle_libm.so), exp, log and
+ * tanh come from the C library instead: that build only serves the
+ * perturbation study of oracle/perturb.py and is never a parity oracle.
  * The per-edge and per-unit loops run under OpenMP when it is on: every
  * iteration writes its own slot and every fold keeps its order inside one
  * iteration, so the results do not depend on the thread count.
@@ -154,6 +157,9 @@ static inline float ox_pow2i(int n) {
 }
 
 OX_API float ox_expf(float x) {
+#ifdef OX_LIBM_ELEMENTARY
+  return expf(x); /* perturbation build (oracle/perturb.py) */
+#endif
   if (x != x) return x;
   if (x > 88.72283935546875f) return INFINITY;
   if (x < -103.97208404541015625f) return 0.0f;
@@ -176,6 +182,9 @@ OX_API float ox_expf(float x) {
 }
 
 OX_API float ox_logf(float x) {
+#ifdef OX_LIBM_ELEMENTARY
+  return logf(x); /* perturbation build (oracle/perturb.py) */
+#endif
   if (x != x) return x;
   if (x < 0.0f) return NAN;
   if (x == 0.0f) return -INFINITY;
@@ -216,6 +225,9 @@ OX_API float ox_logf(float x) {
 }
 
 OX_API float ox_tanhf(float x) {
+#ifdef OX_LIBM_ELEMENTARY
+  return tanhf(x); /* perturbation build (oracle/perturb.py) */
+#endif
   float z = fabsf(x);
   if (z > 44.36141967773437500f) return x > 0.0f ? 1.0f : -1.0f;
   if (z >= 0.625f) {

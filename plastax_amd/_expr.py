@@ -423,26 +423,67 @@ class TraceGlobals:
 # ---------------------------------------------------------------------------
 
 
-def linear_map_field(expr: Any, other_role: str) -> str:
-    """The unit field a map multiplies the edge weight by.
+@dataclasses.dataclass(frozen=True)
+class ProductMap:
+    """A traced map of the product form (connection factor) * (unit factor
+    at the edge's other end). ``field`` is the unit field gathered at the
+    other end (None: the constant ``x_const``); the connection factor is
+    WEIGHT unless ``w_const`` is set. A lone factor is its product with 1.0,
+    which leaves every float32 bit unchanged."""
 
-    The device runs maps of the form ``c[WEIGHT, cid] * u[F, other]`` (either
-    operand order; float multiplication commutes bit for bit), the reference's
-    ``linear_input`` contract (phases.py:535-556).
-    """
+    field: str | None
+    w_const: np.float32 | None = None
+    x_const: np.float32 | None = None
+
+
+def _float_const(x: Any) -> np.float32 | None:
+    if isinstance(x, Expr) and x.op == "const" and x.dtype in ("f", "wf", "wi"):
+        return np.float32(x.value)
+    return None
+
+
+def product_map(expr: Any, other_role: str) -> ProductMap:
+    """The factors of a map the device runs: ``c[WEIGHT, cid] * u[F, other]``
+    (the reference's ``linear_input`` contract, phases.py:535-556; either
+    operand order, as float multiplication commutes bit for bit), either
+    factor replaced by a float constant, or a lone factor (``c[WEIGHT, cid]``,
+    ``u[F, other]`` or a constant, e.g. 1.0 to count the live edges)."""
+
+    def factor(x: Any) -> tuple[str, Any] | None:
+        if isinstance(x, Expr) and x.op == "ldc" and x.field == "weight":
+            return ("w", None)
+        if isinstance(x, Expr) and x.op == "ldu" and x.role == other_role and x.dtype == "f":
+            return ("x", str(x.field))
+        k = _float_const(x)
+        return None if k is None else ("k", k)
+
+    expr = lift(expr)
     if isinstance(expr, Expr) and expr.op == "mul":
-        a, b = expr.args
-        for w, x in ((a, b), (b, a)):
-            if (
-                w.op == "ldc"
-                and w.field == "weight"
-                and x.op == "ldu"
-                and x.role == other_role
-            ):
-                return str(x.field)
+        parts = [factor(x) for x in expr.args]
+    else:
+        parts = [factor(expr), ("k", np.float32(1.0))]
+    if all(p is not None for p in parts):
+        ws = [v for k, v in parts if k == "w"]
+        xs = [v for k, v in parts if k == "x"]
+        ks = [v for k, v in parts if k == "k"]
+        if len(ws) <= 1 and len(xs) <= 1:
+            w_const = None if ws else ks.pop(0)
+            return ProductMap(xs[0] if xs else None, w_const, None if xs else ks.pop(0))
     raise UnsupportedPolicyError(
-        f"map must be c[WEIGHT, cid] * u[FIELD, {other_role}] to run on the device, got {expr!r}"
+        f"map must be c[WEIGHT, cid] * u[FIELD, {other_role}] (either factor may be a float "
+        f"constant, or stand alone) to run on the device, got {expr!r}"
     )
+
+
+def linear_map_field(expr: Any, other_role: str) -> str:
+    """The unit field a map multiplies the edge weight by (the linear form
+    ``c[WEIGHT, cid] * u[F, other]``; see product_map for the general one)."""
+    pm = product_map(expr, other_role)
+    if pm.field is None or pm.w_const is not None or pm.x_const is not None:
+        raise UnsupportedPolicyError(
+            f"map must be c[WEIGHT, cid] * u[FIELD, {other_role}] here, got {expr!r}"
+        )
+    return pm.field
 
 
 # ---------------------------------------------------------------------------

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 12  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 13  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -66,6 +66,14 @@ class plx_finalize(ctypes.Structure):
     ]
 
 
+PLX_MAP_W_CONST = 1
+PLX_MAP_X_CONST = 2
+
+
+class plx_map(ctypes.Structure):
+    _fields_ = [("flags", c_i32), ("w", c_f32), ("x", c_f32), ("reserved", c_i32)]
+
+
 class plx_forward_desc(ctypes.Structure):
     _fields_ = [
         ("nrows", c_i32),
@@ -81,6 +89,7 @@ class plx_forward_desc(ctypes.Structure):
         ("acc", c_vp),
         ("fin", plx_finalize),
         ("apply", plx_program),
+        ("map", plx_map),
     ]
 
 
@@ -125,6 +134,7 @@ class plx_tile_desc(ctypes.Structure):
         ("act", c_vp),
         ("pow_table", c_vp),
         ("p", c_f32 * 8),
+        ("map", plx_map),
     ]
 
 
@@ -192,6 +202,7 @@ class plx_bwd_batch_desc(ctypes.Structure):
         ("acc", c_vp),
         ("fin", plx_finalize),
         ("apply", plx_program),
+        ("map", plx_map),
     ]
 
 

@@ -4,9 +4,11 @@
 trace time; ``compile_plan`` makes the same decisions for the device and
 checks that every present policy has a device lowering:
 
-- forward / backward: the map must be linear (``WEIGHT * field[other]``,
-  the ``linear_input`` contract of phases.py:535-556), the combine a named
-  monoid, and ``apply`` is compiled to a unit program;
+- forward / backward: the map must be of the product form
+  ``WEIGHT * field[other]`` (the ``linear_input`` contract of
+  phases.py:535-556), either factor possibly a float constant or absent
+  (``_expr.product_map``: a constant map counts live edges), the combine a
+  named monoid, and ``apply`` is compiled to a unit program;
 - loss: ``SoftmaxCrossEntropyLoss`` runs its own kernel; any other loss must
   return ``(jnp.sum(term), seed)`` with ``term`` and ``seed`` elementwise in
   the output's prediction and target, and is compiled to a program;
@@ -32,7 +34,7 @@ from plastax_amd._expr import (
     TraceUnitView,
     UnsupportedPolicyError,
     compile_program,
-    linear_map_field,
+    product_map,
 )
 from plastax_amd.growth_config import GrowthConfig
 from plastax_amd.monoid import Monoid
@@ -48,10 +50,28 @@ POW_TABLE_LEN = 1 << 16
 class PassPlan:
     """A traced forward or backward pass."""
 
-    field: str  # the linear_input unit field the map gathers
+    field: str | None  # the unit field the map gathers at the other end (None: x_const)
     monoid: int
     identity: float
     program: Program  # the apply
+    w_const: np.float32 | None = None  # the map's connection factor, when not WEIGHT
+    x_const: np.float32 | None = None  # the map's unit factor, when not a field
+
+    def map_struct(self) -> "_lib.plx_map":
+        """The plx_map of this pass's map."""
+        m = _lib.plx_map()
+        if self.w_const is not None:
+            m.flags |= _lib.PLX_MAP_W_CONST
+            m.w = float(self.w_const)
+        if self.x_const is not None:
+            m.flags |= _lib.PLX_MAP_X_CONST
+            m.x = float(self.x_const)
+        return m
+
+    def gathered(self, units: dict, fallback: str) -> Any:
+        """The unit column the kernels gather for the map: the field, or
+        (for a constant unit factor, never read for the term) ``fallback``."""
+        return units[self.field if self.field is not None else fallback]
 
 
 @dataclasses.dataclass
@@ -121,17 +141,19 @@ def _trace_pass(policy: Any, static: NetworkStatic, *, backward: bool) -> PassPl
         raise UnsupportedPolicyError(f"{name}.combine must be a single named monoid")
     if backward:
         expr = policy.map(u, Index("src"), Index("dst"), c, Index("cid"), g)
-        field = linear_map_field(expr, "dst")
+        pm = product_map(expr, "dst")
     else:
         expr = policy.map(u, Index("dst"), Index("src"), c, Index("cid"), g)
-        field = linear_map_field(expr, "src")
+        pm = product_map(expr, "src")
+    field = pm.field
     write = policy.apply(u, Index("self"), g, Expr("acc"))
     if not isinstance(write, UnitWrite):
         raise UnsupportedPolicyError(f"{name}.apply must return a UnitWrite")
     outs = list(write.fields.keys())
     prog = compile_program(list(write.fields.values()), outs, allow={"acc", "self"})
     _check_float_fields(outs + prog.fields + [field], dtypes, f"{name}")
-    return PassPlan(field=field, monoid=combine.code, identity=combine.identity_for(), program=prog)
+    return PassPlan(field=field, monoid=combine.code, identity=combine.identity_for(), program=prog,
+                    w_const=pm.w_const, x_const=pm.x_const)
 
 
 def _trace_loss(loss: Any, static: NetworkStatic) -> LossPlan:

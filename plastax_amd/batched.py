@@ -139,14 +139,15 @@ class BatchedStepFn(StepFn):
         """[num_units, B] copies of every column a per-sample phase reads or
         writes (each sample starts from the shared state: step.py:421-424)."""
         plan = self.plan
-        names = {ACTIVATION.name, plan.forward.field}
+        names = {ACTIVATION.name} | ({plan.forward.field} - {None})
         progs = [plan.forward.program]
         if plan.loss is not None:
             names.add(plan.loss.seed_field)
             if plan.loss.program is not None:
                 progs.append(plan.loss.program)
         if plan.backward is not None:
-            names.add(plan.backward.field)
+            if plan.backward.field is not None:
+                names.add(plan.backward.field)
             progs.append(plan.backward.program)
         if plan.update is not None:
             names.add(plan.update.grad_field.name)
@@ -206,7 +207,8 @@ class BatchedStepFn(StepFn):
             d.src = arena.cols["from_id"].data_ptr()
             d.weight = arena.cols["weight"].data_ptr()
             d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
-            d.x = ub[fp.field].data_ptr()
+            d.x = fp.gathered(ub, ACTIVATION.name).data_ptr()
+            d.map = fp.map_struct()
             d.acc = acc.data_ptr() if acc is not None else None
             d.fin.level, d.fin.is_input, d.fin.pruned = fin["level"], fin["is_input"], fin["pruned"]
             d.fin.fin_level = b + 1
@@ -258,7 +260,8 @@ class BatchedStepFn(StepFn):
                 d.dst = lists.dst.data_ptr()
                 d.weight = lists.weight.data_ptr()
                 d.live = lists.live.data_ptr()
-                d.g = ub[bp.field].data_ptr()
+                d.g = bp.gathered(ub, ACTIVATION.name).data_ptr()
+                d.map = bp.map_struct()
                 d.acc = bacc.data_ptr() if bacc is not None else None
                 d.fin.level, d.fin.is_input, d.fin.pruned = fin["level"], fin["is_input"], fin["pruned"]
                 d.fin.fin_level = level

@@ -105,6 +105,13 @@ struct Mono<PLX_MONOID_MIN> {
   static __device__ __forceinline__ float op(float a, float b) { return px::fmin_nan(a, b); }
 };
 
+// A map's term: (connection factor) * (unit factor), each the loaded value
+// or the map's constant (plx_map; the flags are uniform, so these are
+// scalar selects).
+__device__ __forceinline__ float map_term(const plx_map& m, float w, float x) {
+  return ((m.flags & PLX_MAP_W_CONST) ? m.w : w) * ((m.flags & PLX_MAP_X_CONST) ? m.x : x);
+}
+
 // ---------------------------------------------------------------------------
 // Unit-program interpreter. The program is uniform across the grid (it sits
 // in the kernel argument segment), so every dispatch below is a scalar branch.
@@ -410,10 +417,10 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
       const int q = threadIdx.x + i * kFwdBlock;
       if (4 * q < wn) {
         float4 o;
-        o.x = ok[i][0] ? cur.wv[i].x * xv[i][0] : ident;
-        o.y = ok[i][1] ? cur.wv[i].y * xv[i][1] : ident;
-        o.z = ok[i][2] ? cur.wv[i].z * xv[i][2] : ident;
-        o.w = ok[i][3] ? cur.wv[i].w * xv[i][3] : ident;
+        o.x = ok[i][0] ? map_term(d.map, cur.wv[i].x, xv[i][0]) : ident;
+        o.y = ok[i][1] ? map_term(d.map, cur.wv[i].y, xv[i][1]) : ident;
+        o.z = ok[i][2] ? map_term(d.map, cur.wv[i].z, xv[i][2]) : ident;
+        o.w = ok[i][3] ? map_term(d.map, cur.wv[i].w, xv[i][3]) : ident;
         *reinterpret_cast<float4*>(out + 4 * q) = o;
       }
     }
@@ -955,7 +962,7 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         for (int k = 0; k < 4; ++k) {
           if (lv[i][k] || e + k < d.live_end) {
             const uint32_t r = rw[k] & kRankMask;
-            buf[r] = lv[i][k] ? wk[k] * gd[i][k] : ident;
+            buf[r] = lv[i][k] ? map_term(d.map, wk[k], gd[i][k]) : ident;
             tag[r] = static_cast<uint16_t>((rw[k] & kGroupStart) | hw[k]);
           }
         }
@@ -1257,11 +1264,11 @@ __global__ __launch_bounds__(kBatchBlock) void k_forward_batch(plx_forward_desc 
       for (int k = 0; k < kBatchUnrollWide; ++k) xv[k] = d.x[static_cast<int64_t>(sv[k]) * B + bl];
 #pragma unroll
       for (int k = 0; k < kBatchUnrollWide; ++k)
-        if (live[k]) s = Mono<M>::op(s, wv[k] * xv[k]);
+        if (live[k]) s = Mono<M>::op(s, map_term(d.map, wv[k], xv[k]));
     }
     for (; e < e1; ++e) {
       if (d.dead && d.dead[e]) continue;
-      s = Mono<M>::op(s, d.weight[e] * d.x[static_cast<int64_t>(d.src[e]) * B + bl]);
+      s = Mono<M>::op(s, map_term(d.map, d.weight[e], d.x[static_cast<int64_t>(d.src[e]) * B + bl]));
     }
     if (b < B) finish_batch<M>(d.acc, d.apply, fin, static_cast<int64_t>(u) * B + b, s);
   }
@@ -1299,20 +1306,20 @@ __global__ __launch_bounds__(64) void k_forward_batch4(plx_forward_desc d, int32
 #pragma unroll
       for (int k = 0; k < kBatchUnroll; ++k) {
         if (!live[k]) continue;
-        s[0] = Mono<M>::op(s[0], wv[k] * xv[k].x);
-        s[1] = Mono<M>::op(s[1], wv[k] * xv[k].y);
-        s[2] = Mono<M>::op(s[2], wv[k] * xv[k].z);
-        s[3] = Mono<M>::op(s[3], wv[k] * xv[k].w);
+        s[0] = Mono<M>::op(s[0], map_term(d.map, wv[k], xv[k].x));
+        s[1] = Mono<M>::op(s[1], map_term(d.map, wv[k], xv[k].y));
+        s[2] = Mono<M>::op(s[2], map_term(d.map, wv[k], xv[k].z));
+        s[3] = Mono<M>::op(s[3], map_term(d.map, wv[k], xv[k].w));
       }
     }
     for (; e < e1; ++e) {
       if (d.dead && d.dead[e]) continue;
       const float w = d.weight[e];
       const float4 x = *reinterpret_cast<const float4*>(d.x + static_cast<int64_t>(d.src[e]) * B + bl);
-      s[0] = Mono<M>::op(s[0], w * x.x);
-      s[1] = Mono<M>::op(s[1], w * x.y);
-      s[2] = Mono<M>::op(s[2], w * x.z);
-      s[3] = Mono<M>::op(s[3], w * x.w);
+      s[0] = Mono<M>::op(s[0], map_term(d.map, w, x.x));
+      s[1] = Mono<M>::op(s[1], map_term(d.map, w, x.y));
+      s[2] = Mono<M>::op(s[2], map_term(d.map, w, x.z));
+      s[3] = Mono<M>::op(s[3], map_term(d.map, w, x.w));
     }
     if (b < B)
 #pragma unroll
@@ -1347,11 +1354,11 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_batch(plx_bwd_batch_de
       for (int k = 0; k < kBatchUnrollWide; ++k) gv[k] = d.g[static_cast<int64_t>(tv[k]) * B + bl];
 #pragma unroll
       for (int k = 0; k < kBatchUnrollWide; ++k)
-        if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
+        if (live[k]) s = Mono<M>::op(s, map_term(d.map, wv[k], gv[k]));
     }
     for (; j < j1; ++j) {
       if (d.live && !d.live[j]) continue;
-      s = Mono<M>::op(s, d.weight[j] * d.g[static_cast<int64_t>(d.dst[j]) * B + bl]);
+      s = Mono<M>::op(s, map_term(d.map, d.weight[j], d.g[static_cast<int64_t>(d.dst[j]) * B + bl]));
     }
     if (b < B) finish_batch<M>(d.acc, d.apply, fin, static_cast<int64_t>(u) * B + b, s);
   }
@@ -1389,20 +1396,20 @@ __global__ __launch_bounds__(64) void k_backward_batch4(plx_bwd_batch_desc d) {
 #pragma unroll
       for (int k = 0; k < kBatchUnroll; ++k) {
         if (!live[k]) continue;
-        s[0] = Mono<M>::op(s[0], wv[k] * gv[k].x);
-        s[1] = Mono<M>::op(s[1], wv[k] * gv[k].y);
-        s[2] = Mono<M>::op(s[2], wv[k] * gv[k].z);
-        s[3] = Mono<M>::op(s[3], wv[k] * gv[k].w);
+        s[0] = Mono<M>::op(s[0], map_term(d.map, wv[k], gv[k].x));
+        s[1] = Mono<M>::op(s[1], map_term(d.map, wv[k], gv[k].y));
+        s[2] = Mono<M>::op(s[2], map_term(d.map, wv[k], gv[k].z));
+        s[3] = Mono<M>::op(s[3], map_term(d.map, wv[k], gv[k].w));
       }
     }
     for (; j < j1; ++j) {
       if (d.live && !d.live[j]) continue;
       const float w = d.weight[j];
       const float4 g = *reinterpret_cast<const float4*>(d.g + static_cast<int64_t>(d.dst[j]) * B + bl);
-      s[0] = Mono<M>::op(s[0], w * g.x);
-      s[1] = Mono<M>::op(s[1], w * g.y);
-      s[2] = Mono<M>::op(s[2], w * g.z);
-      s[3] = Mono<M>::op(s[3], w * g.w);
+      s[0] = Mono<M>::op(s[0], map_term(d.map, w, g.x));
+      s[1] = Mono<M>::op(s[1], map_term(d.map, w, g.y));
+      s[2] = Mono<M>::op(s[2], map_term(d.map, w, g.z));
+      s[3] = Mono<M>::op(s[3], map_term(d.map, w, g.w));
     }
     if (b < B)
 #pragma unroll
@@ -1435,11 +1442,11 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_lists(plx_bwd_batch_de
     for (int k = 0; k < 4; ++k) gv[k] = d.g[tv[k]];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if (live[k]) s = Mono<M>::op(s, wv[k] * gv[k]);
+      if (live[k]) s = Mono<M>::op(s, map_term(d.map, wv[k], gv[k]));
   }
   for (; j < j1; ++j) {
     if (d.live && !d.live[j]) continue;
-    s = Mono<M>::op(s, d.weight[j] * d.g[d.dst[j]]);
+    s = Mono<M>::op(s, map_term(d.map, d.weight[j], d.g[d.dst[j]]));
   }
   const float a = Mono<M>::op(d.acc ? d.acc[u] : Mono<M>::id(), s);
   if (pre.fin) {
@@ -1927,7 +1934,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 12; }
+int32_t plx_abi_version(void) { return 13; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[16] = {

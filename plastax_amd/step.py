@@ -252,7 +252,8 @@ class StepFn:
             # Row ranges hold live positions only unless tombstones were set
             # inside them after the layout was built.
             d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
-            d.x = units[fp.field].data_ptr()
+            d.x = fp.gathered(units, ACTIVATION.name).data_ptr()
+            d.map = fp.map_struct()
             d.acc = acc.data_ptr() if acc is not None else None
             d.fin.level = fin_common["level"]
             d.fin.is_input = fin_common["is_input"]
@@ -442,7 +443,8 @@ class StepFn:
             d.sorted_rank = bt.sorted_rank.data_ptr()
             d.hot_sb = bt.hot_sb.data_ptr()
             d.cold_partial = bt.cold_partial.data_ptr()
-            d.g = units[bp.field].data_ptr()
+            d.g = bp.gathered(units, ACTIVATION.name).data_ptr()
+            d.map = bp.map_struct()
         if update:
             up = plan.update
             d.rule = up.rule_code
@@ -526,7 +528,8 @@ class StepFn:
                 d.dst = lists.dst.data_ptr()
                 d.weight = lists.weight.data_ptr()
                 d.live = lists.live.data_ptr()
-            d.g = units[bp.field].data_ptr()
+            d.g = bp.gathered(units, ACTIVATION.name).data_ptr()
+            d.map = bp.map_struct()
             d.acc = acc.data_ptr()
             d.fin.level = fin_common["level"]
             d.fin.is_input = fin_common["is_input"]

@@ -10,6 +10,8 @@ tolerance is written in the test.
 
 from __future__ import annotations
 
+import os
+
 import ctypes
 
 import numpy as np
@@ -164,11 +166,14 @@ def test_softmax_ce_golden_on_device(name: str) -> None:
 # ---------------------------------------------------------------------------
 
 
-def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None, nsuper=None):
+def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None, nsuper=None,
+              parallel=False):
     kw = {} if tile is None else {"tile": tile}
     if nsuper is not None:
         kw["nsuper"] = nsuper
-    o = nets.oracle_for(oracle, net, static, state, **kw)
+    o = nets.oracle_for(oracle, net, static, state, parallel=parallel, **kw)
+    if parallel:
+        o.lib.ox_set_threads(min(16, len(os.sched_getaffinity(0))))
     step = px.make_step(net, static)
     if tile is not None:
         step.tile = tile
@@ -183,6 +188,9 @@ def _run_both(net, static, state, oracle, inputs_fn, steps, check_at, tile=None,
             torch.cuda.synchronize()
             assert_same_state(static, state, o, f"step {k}")
             assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at {k}"
+            print(f"step {k}: every column bit-exact", flush=True)
+    if parallel:
+        o.lib.ox_set_threads(1)
     return state, o
 
 
@@ -230,6 +238,29 @@ def test_topological_zipf_net_bit_exact(oracle, opt_name: str) -> None:
         return x, (sign * x[perm]).astype(np.float32)
 
     _run_both(net, static, state, oracle, inputs, 12, {1, 12})
+
+
+def test_c2_generator_adam_1000_steps_bit_exact(oracle) -> None:
+    """C2's generator at 1/64 width (8 layers x 2,048 tanh units, ~1M Zipf
+    edges), MSE, Adam(1e-3), 1,000 streaming steps: every unit and
+    connection column and the loss equal the oracle's at steps 1, 10, 100
+    and 1,000."""
+    e = synth.c2_topological(seed=5, scale=64)
+    net = nets.make_trained_net("Z1000", nets.TanhForward(), nets.TanhBackward(),
+                                px.optim.adam(1e-3, nets.GRAD_PRE_ACT), px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+        output_ids=e.output_ids, globals_=None, capacity_align=256, device="cuda")
+    width = e.input_ids.size
+    sign, perm = synth.c2_target(5, width)
+    rng = np.random.default_rng(13)
+    xs = rng.standard_normal((1000, width)).astype(np.float32)
+
+    def inputs(k):
+        x = xs[k - 1]
+        return x, (sign * x[perm]).astype(np.float32)
+
+    _run_both(net, static, state, oracle, inputs, 1000, {1, 10, 100, 1000}, parallel=True)
 
 
 @pytest.mark.parametrize("tile,nsuper", [(64, 512), (1024, 512), (64, 5), (256, 37)])

@@ -17,6 +17,13 @@ import plastax_amd as px
 from plastax_amd import _layout, synth
 
 
+def _sum_map(field: str):
+    """The linear sum_ map over ``field`` as the oracle's pass plans state it."""
+    import types
+
+    return types.SimpleNamespace(field=field, monoid=0, w_const=None, x_const=None)
+
+
 def _arena(net, e, tile, nsuper=_layout.NSUPER, **kw):
     static, state = px.NetworkBuilder.from_edges(
         net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
@@ -212,7 +219,7 @@ def test_tiled_fold_emulation_matches_oracle_exactly(oracle, tile: int, nsuper: 
                    for b in range(1, arena.num_buckets))
     for b in range(1, arena.num_buckets):
         got = _emulate_fold(arena, b, g)
-        want = o._reduce_bwd(b, "grad_pre_act", 0)
+        want = o._reduce_bwd(b, _sum_map("grad_pre_act"))
         for u, v in got.items():
             assert np.float32(v).view(np.uint32) == want[u].view(np.uint32), (b, u, v, want[u])
 
@@ -227,7 +234,7 @@ def test_pipeline_arena_and_fold(oracle) -> None:
     g = np.random.default_rng(1).standard_normal(static.num_units).astype(np.float32)
     o.units["grad_pre_act"][:] = g
     got = _emulate_fold(arena, 0, g)
-    want = o._reduce_bwd(0, "grad_pre_act", 0)
+    want = o._reduce_bwd(0, _sum_map("grad_pre_act"))
     assert len(got) == static.num_units  # every unit is a PIPELINE backward row
     for u, v in got.items():
         assert np.float32(v).view(np.uint32) == want[u].view(np.uint32)

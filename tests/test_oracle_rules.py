@@ -18,6 +18,13 @@ import nets
 import plastax_amd as px
 
 
+def _sum_map(field: str):
+    """The linear sum_ map over ``field`` as the oracle's pass plans state it."""
+    import types
+
+    return types.SimpleNamespace(field=field, monoid=0, w_const=None, x_const=None)
+
+
 def _single_edge_net(opt):
     return nets.make_trained_net(
         "One_" + type(opt).__name__, nets.LinearForward(), nets.TanhBackward(), opt,
@@ -202,7 +209,7 @@ def test_backward_pieces_only_regroup_the_slot_order_fold(oracle) -> None:
         o.units["grad_pre_act"][2:] = rng.standard_normal(n_dst).astype(np.float32)
         o.units["level"][:] = 1
         o.units["level"][0] = 1
-        out = o._reduce_bwd(0, "grad_pre_act", 0)
+        out = o._reduce_bwd(0, _sum_map("grad_pre_act"))
         res[piece] = out[0]
         rng = np.random.default_rng(3)
         rng.standard_normal(n_dst)
