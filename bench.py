@@ -348,13 +348,86 @@ def run_c5_growth(args) -> int:
     return 0
 
 
-C5_METRIC = "steps/sec of C5's growing reservoir (forward + per-unit proposals + growth + device relayout)"
+C5_METRIC = ("steps/sec of C5's growing reservoir (forward + out-degree count + PruneUnit + AddUnit + "
+             "per-unit proposals + growth + device relayout)")
+
+
+def build_c5_recipe(px, num_units: int, unit_capacity: int, spawn_lo: int, spawn_n: int):
+    """C5's recipe: the PIPELINE tanh reservoir, a backward pass that counts
+    every unit's live out-edges (a constant map under sum_), PruneUnit of the
+    units whose out-degree is zero, AddUnit spawning the parents with ids in
+    [spawn_lo, spawn_lo + spawn_n) when the global ``spawn`` is set (the bench
+    sets it every 100 steps), and per-unit proposals (P = 4, counter-based
+    rng) every step."""
+    import plastax_amd.numpy as jnp
+
+    outdeg = px.FieldSpec.float32("out_degree")
+
+    class Tanh(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(acc)))
+
+    class CountOut(px.BackwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, src, dst, c, cid, g):
+            return jnp.float32(1.0)
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((outdeg, acc))
+
+    class PruneSilent(px.PruneUnit):
+        def predicate(self, u, i, g):
+            return u[outdeg, i] == jnp.float32(0.0)
+
+    class SpawnBand(px.AddUnit):
+        def spawn(self, u, parent, g):
+            band = (parent >= spawn_lo) & (parent < spawn_lo + spawn_n)
+            return band & (g["spawn"] > jnp.float32(0.0)), jnp.int32(0)
+
+        def init(self, u, child, parent, g):
+            return px.UnitWrite.of((px.ACTIVATION, u[px.ACTIVATION, parent] * jnp.float32(0.5)))
+
+    class Propose(px.ProposeAddConn):
+        proposer = "per_unit"
+        proposals_per_proposer = 4
+        max_new_per_level = 16
+        max_level_gap = 1 << 20
+
+        def propose(self, u, i, j, g, rng):
+            dst = rng.uniform_int(num_units).astype(jnp.int32)
+            return jnp.asarray(i, jnp.int32), dst, rng.uniform()
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of((px.WEIGHT, jnp.float32(0.01)))
+
+    class C5(px.Network):
+        unit_capacity = 262144
+        forward_pass = Tanh()
+        backward_pass = CountOut()
+        prune_unit = PruneSilent()
+        add_unit = SpawnBand()
+        add_conn = Propose()
+        extra_unit_fields = (outdeg,)
+        propagation = px.Propagation.PIPELINE
+
+    C5.unit_capacity = unit_capacity
+    return C5
 
 
 def run_c5(args) -> int:
-    """C5 end to end: every step scatters 256 inputs, runs the PIPELINE
-    forward over the live edges, grows (per-unit proposals, P = 4) and the
-    next step lays the arena out again on the device (the churn layout)."""
+    """C5 end to end, its whole recipe: every step scatters 256 inputs, runs
+    the PIPELINE forward and the out-degree count over the live edges, prunes
+    the units left without out-edges, spawns 16 units every 100 steps, grows
+    (per-unit proposals, P = 4), and the next step lays the arena out again on
+    the device (the churn layout). The first steps are checked against the
+    oracle from the same initial state: flags every step and, after them,
+    every unit and connection column bit for bit."""
     import torch
 
     import plastax_amd as px
@@ -362,11 +435,12 @@ def run_c5(args) -> int:
     from plastax_amd.state import column_to_numpy
 
     t_setup = time.perf_counter()
-    net = build_c5(px)
     e = synth.c5_reservoir(args.seed)
+    net = build_c5_recipe(px, e.num_units, 262144, 1024, 16)
+    g_of = lambda k: {"spawn": np.float32(1.0 if k % 100 == 0 else 0.0)}  # noqa: E731
     static, state = px.NetworkBuilder.from_edges(
         net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
-        output_ids=e.output_ids, globals_=None, capacity_headroom=3.0, device="cpu")
+        output_ids=e.output_ids, globals_=g_of(0), capacity_headroom=3.0, device="cpu")
     uspecs = {s.name: s for s in static.unit_fields}
     cspecs = {s.name: s for s in static.conn_fields}
     host_units = {k: column_to_numpy(v, uspecs[k]).copy() for k, v in state.units.items()}
@@ -375,46 +449,81 @@ def run_c5(args) -> int:
     gstate = px.NetworkState(
         {k: v.to(dev) for k, v in state.units.items()},
         tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
-        None,
+        g_of(0),
     )
+    gstate.tail_start = state.tail_start
     step = px.make_step(net, static)
-    nsteps = args.warmup + args.steps
+    npar = 0 if args.no_cpu_baseline else 2
+    nsteps = npar + args.warmup + args.steps
     rng = np.random.default_rng(args.seed + 3)
     xs = rng.standard_normal((nsteps, e.input_ids.size)).astype(np.float32)
     xs_d = torch.from_numpy(xs).to(dev)
-    for k in range(args.warmup):
+    flags = []
+    k = 0
+    for _ in range(npar):
+        gstate.globals_ = g_of(k)
         gstate = step(gstate, px.StepInputs(xs_d[k])).state
+        flags.append((int(gstate.units_added), bool(gstate.unit_overflow), int(gstate.grown),
+                      bool(gstate.overflow), int(gstate.tail_start)))
+        k += 1
+    snap = None
+    if npar:
+        torch.cuda.synchronize()
+        snap = ({n: column_to_numpy(gstate.units[n], uspecs[n]).copy() for n in uspecs},
+                [{n: column_to_numpy(b[n], cspecs[n]).copy() for n in cspecs} for b in gstate.conns])
+    for _ in range(args.warmup):
+        gstate.globals_ = g_of(k)
+        gstate = step(gstate, px.StepInputs(xs_d[k])).state
+        k += 1
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
     progress(f"C5: {e.src.size} live edges of {static.level_capacities[0]} slots, layout {step.backward_order} "
              f"({setup_s:.1f} s)")
-    grown = 0
+    grown = added = 0
     t0 = time.perf_counter()
-    for k in range(args.warmup, nsteps):
+    for _ in range(args.steps):
+        gstate.globals_ = g_of(k)
         gstate = step(gstate, px.StepInputs(xs_d[k])).state
         grown += int(gstate.grown)
+        added += int(gstate.units_added)
+        k += 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
-    live = int(gstate._arena.lives[0]) if gstate._arena is not None else int(e.src.size)
+    live = int(sum(int((b["dead"] == 0).sum().item()) for b in gstate.conns))
+    live_units = int((gstate.units["pruned"] == 0).sum().item())
     cpu = None
-    if not args.no_cpu_baseline:
+    parity = None
+    if npar:
         from oracle import oracle as ox
         from plastax_amd._plan import compile_plan
 
         ox.load()
-        o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), None, tile=None)
-        o.tail_start = int(state.tail_start)
-        t1 = time.perf_counter()
-        o.step(xs[0])
-        sec = time.perf_counter() - t1
+        o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), g_of(0), tile=None)
+        o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
+        times = []
+        same_flags = True
+        for q in range(npar):
+            o.globals_ = g_of(q)
+            t1 = time.perf_counter()
+            o.step(xs[q])
+            times.append(time.perf_counter() - t1)
+            same_flags &= flags[q] == (o.units_added, o.unit_overflow, o.grown, o.overflow, o.tail_start)
+        units_d, conns_d = snap
+        same_units = all(np.array_equal(units_d[n].view(np.uint8), o.units[n].view(np.uint8)) for n in uspecs)
+        same_conns = all(np.array_equal(conns_d[b][n].view(np.uint8), o.conns[b][n].view(np.uint8))
+                         for b in range(len(conns_d)) for n in cspecs)
+        parity = {"steps": npar, "flags_equal": bool(same_flags), "units_bit_exact": bool(same_units),
+                  "conns_bit_exact": bool(same_conns), "spawn_step_included": True}
+        progress(f"C5 parity over {npar} steps: flags {same_flags}, units {same_units}, conns {same_conns}")
+        sec = float(np.median(times))
         cpu = {
             "value": float(1.0 / sec),
             "unit": "steps/s",
             "cores": 1,
             "kind": "port",
-            "sample": f"1 full C5 step (forward + growth) of the same workload, {sec:.2f} s, the C oracle and "
-            "oracle/growth.py, one thread",
+            "sample": f"{npar} full C5 recipe steps of the same workload (the first spawns 16 units), median "
+            f"{sec:.2f} s, the C oracle and oracle/growth.py, one thread",
         }
     line = {
         "metric": C5_METRIC,
@@ -431,13 +540,17 @@ def run_c5(args) -> int:
         "data": "synthetic",
         "config": {
             "workload": "C5: 65,536 live of 262,144 unit slots, 4M live of 16M edge slots, PIPELINE tanh, "
-            "per-unit proposals P=4 every step, max_new_per_level 16",
+            "out-degree count, PruneUnit (zero out-degree), AddUnit 16 per 100 steps, per-unit proposals "
+            "P=4 every step, max_new_per_level 16",
             "layout": step.backward_order,
             "live_edges_end": live,
+            "live_units_end": live_units,
         },
         "grown_per_step": grown / args.steps,
+        "units_added": added,
         "roofline": None,
         "cpu_baseline": cpu,
+        "full_size_parity": parity,
         "setup_s": round(setup_s, 1),
     }
     print(json.dumps(line), flush=True)
