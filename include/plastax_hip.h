@@ -417,7 +417,8 @@ PLX_EXPORT int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ct
                  uint32_t* out, void* stream);
 
 /* Elementary functions exactly as the kernels evaluate them (op 0 exp,
- * 1 log, 2 tanh, 3 sigmoid, 4 sqrt, 5 Adam power b^t with b=x[i], t=y[i]). */
+ * 1 log, 2 tanh, 3 sigmoid, 4 sqrt, 5 Adam power b^t with b=x[i], t=y[i],
+ * 6 cos, 7 sin). */
 PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float* y,
                   float* out, void* stream);
 

@@ -102,7 +102,7 @@ def load_variant(path: pathlib.Path) -> ctypes.CDLL:
 
 
 def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
-    for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf"):
+    for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf", "ox_cosf", "ox_sinf"):
         getattr(lib, name).restype = ctypes.c_float
         getattr(lib, name).argtypes = [ctypes.c_float]
     lib.ox_pow_step.restype = ctypes.c_float

@@ -249,6 +249,81 @@ OX_API float ox_tanhf(float x) {
 
 OX_API float ox_sigmoidf(float x) { return 1.0f / (1.0f + ox_expf(-x)); }
 
+/* sin and cos follow Cephes sinf.c / cosf.c (Moshier): |x| is reduced */
+/* modulo pi/4 by the octant j = trunc(|x| * 4/pi), rounded up to even, and */
+/* r = |x| - j * pi/4 with pi/4 split in three (DP1 and DP2 have few */
+/* significant bits, so j * DP1 and j * DP2 are exact while |x| <= 8192); */
+/* the sine or cosine minimax polynomial of r on [-pi/4, pi/4] is chosen by */
+/* octant. Past 8192 the reduction loses precision (Cephes' PLOSS), past */
+/* 2^24 - 1 the result is 0 (TLOSS); infinities and NaN give NaN. */
+static float ox_sincos_reduce(float x, int j) {
+  if (x > 8192.0f)
+    x = x - (float)j * 0.7853981633974483096f;
+  else
+    x = ((x - (float)j * 0.78515625f) - (float)j * 2.4187564849853515625e-4f) -
+        (float)j * 3.77489497744594108e-8f;
+  return x;
+}
+
+static float ox_sin_poly(float x, float z) {
+  float r = ((-1.9515295891e-4f * z + 8.3321608736e-3f) * z - 1.6666654611e-1f) * z * x;
+  return r + x;
+}
+
+static float ox_cos_poly(float z) {
+  float r = ((2.443315711809948e-5f * z - 1.388731625493765e-3f) * z + 4.166664568298827e-2f) * z * z;
+  r = r - 0.5f * z;
+  return r + 1.0f;
+}
+
+OX_API float ox_cosf(float xx) {
+  if (xx != xx) return xx;
+  const float x = fabsf(xx);
+  if (x == INFINITY) return NAN;
+  if (x > 16777215.0f) return 0.0f;
+  int j = (int)(1.27323954473516f * x);
+  int y = j;
+  if (j & 1) {
+    j += 1;
+    y += 1;
+  }
+  j &= 7;
+  int neg = 0;
+  if (j > 3) {
+    j -= 4;
+    neg = 1;
+  }
+  if (j > 1) neg = !neg;
+  const float r = ox_sincos_reduce(x, y);
+  const float z = r * r;
+  const float v = (j == 1 || j == 2) ? ox_sin_poly(r, z) : ox_cos_poly(z);
+  return neg ? -v : v;
+}
+
+OX_API float ox_sinf(float xx) {
+  if (xx != xx) return xx;
+  int neg = signbit(xx) != 0; /* sin(-0) = -0 */
+  const float x = fabsf(xx);
+  if (x == INFINITY) return NAN;
+  if (x > 16777215.0f) return 0.0f;
+  int j = (int)(1.27323954473516f * x);
+  int y = j;
+  if (j & 1) {
+    j += 1;
+    y += 1;
+  }
+  j &= 7;
+  if (j > 3) {
+    neg = !neg;
+    j -= 4;
+  }
+  const float r = ox_sincos_reduce(x, y);
+  const float z = r * r;
+  const float v = (j == 1 || j == 2) ? ox_cos_poly(z) : ox_sin_poly(r, z);
+  return neg ? -v : v;
+}
+
+
 /* NaN-propagating max/min, as jnp.maximum / jnp.minimum (monoid.py:46-51). */
 static inline float ox_fmax_nan(float a, float b) {
   if (a != a) return a;
@@ -492,7 +567,9 @@ enum {
   OP_SIGN = 29,
   OP_LOG1P = 30,
   OP_EXPM1 = 31,
-  OP_POW = 32
+  OP_POW = 32,
+  OP_COS = 33,
+  OP_SIN = 34
 };
 
 #define OX_NREG 32
@@ -527,6 +604,8 @@ static float ox_run_program(const int32_t* prog, int32_t ninstr,
       case OP_LOG: r[d] = ox_logf(r[a]); break;
       case OP_SQRT: r[d] = sqrtf(r[a]); break;
       case OP_SIGMOID: r[d] = ox_sigmoidf(r[a]); break;
+      case OP_COS: r[d] = ox_cosf(r[a]); break;
+      case OP_SIN: r[d] = ox_sinf(r[a]); break;
       case OP_SIGN:
         r[d] = r[a] > 0.0f ? 1.0f : (r[a] < 0.0f ? -1.0f : r[a]);
         break;
@@ -742,6 +821,7 @@ enum {
   S_OUT = 8,
   S_FADD = 10, S_FSUB, S_FMUL, S_FDIV, S_FNEG, S_FABS, S_FMAX, S_FMIN, S_FTANH,
   S_FEXP, S_FLOG, S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR,
+  S_FCOS, S_FSIN,
   S_FGT = 30, S_FGE, S_FLT, S_FLE, S_FEQ, S_FNE,
   S_IADD = 40, S_ISUB, S_IMUL, S_INEG, S_IABS, S_IMAX, S_IMIN, S_IFLOORDIV,
   S_IMOD, S_ISIGN,
@@ -838,6 +918,8 @@ OX_API void ox_site_eval(const int32_t* prog, int32_t ninstr, const uint32_t* co
         case S_FLOG: r[d] = ox_u(ox_logf(ox_f(x))); break;
         case S_FSQRT: r[d] = ox_u(sqrtf(ox_f(x))); break;
         case S_FSIGMOID: r[d] = ox_u(ox_sigmoidf(ox_f(x))); break;
+        case S_FCOS: r[d] = ox_u(ox_cosf(ox_f(x))); break;
+        case S_FSIN: r[d] = ox_u(ox_sinf(ox_f(x))); break;
         case S_FSQUARE: r[d] = ox_u(ox_f(x) * ox_f(x)); break;
         case S_FRELU: r[d] = ox_u(ox_fmax_nan(ox_f(x), 0.0f)); break;
         case S_FSIGN: {

@@ -65,8 +65,10 @@ OPCODES = {
     "square": 27,
     "relu": 28,
     "sign": 29,
+    "cos": 33,
+    "sin": 34,
 }
-_UNARY = {"neg", "abs", "tanh", "exp", "log", "sqrt", "sigmoid", "square", "relu", "sign"}
+_UNARY = {"neg", "abs", "tanh", "exp", "log", "sqrt", "sigmoid", "square", "relu", "sign", "cos", "sin"}
 _BINARY = {"add", "sub", "mul", "div", "max", "min", "gt", "ge", "lt", "le", "eq", "ne"}
 MAX_REGS = 16
 MAX_INSTR = 48
@@ -83,7 +85,7 @@ def _f32(x: Any) -> np.float32:
 # ("u"), bool ("b"), and the weakly typed Python scalars ("wi", "wf") that
 # take the other operand's type, as jnp's weak typing does.
 _WEAK = {"wi", "wf"}
-_FLOAT_ONLY = {"tanh", "exp", "log", "sqrt", "sigmoid", "floor"}
+_FLOAT_ONLY = {"tanh", "exp", "log", "sqrt", "sigmoid", "floor", "cos", "sin"}
 _INT_ONLY = {"mod", "floordiv", "shl", "shr"}
 _LOGIC = {"and", "or", "xor"}
 

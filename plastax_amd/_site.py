@@ -36,6 +36,7 @@ from plastax_amd._expr import (
     cast,
     kind_of_dtype,
     lift,
+    unary,
 )
 
 # Site opcodes: keep in sync with plastax_amd/csrc/structural.hip and the
@@ -44,7 +45,7 @@ SOP = {
     "const": 1, "idx": 2, "ldu": 3, "ldc": 4, "rng": 5, "mov": 6, "sel": 7, "out": 8,
     "fadd": 10, "fsub": 11, "fmul": 12, "fdiv": 13, "fneg": 14, "fabs": 15, "fmax": 16,
     "fmin": 17, "ftanh": 18, "fexp": 19, "flog": 20, "fsqrt": 21, "fsigmoid": 22,
-    "fsquare": 23, "frelu": 24, "fsign": 25, "ffloor": 26,
+    "fsquare": 23, "frelu": 24, "fsign": 25, "ffloor": 26, "fcos": 27, "fsin": 28,
     "fgt": 30, "fge": 31, "flt": 32, "fle": 33, "feq": 34, "fne": 35,
     "iadd": 40, "isub": 41, "imul": 42, "ineg": 43, "iabs": 44, "imax": 45, "imin": 46,
     "ifloordiv": 47, "imod": 48, "isign": 49,
@@ -174,9 +175,14 @@ class SiteRng:
         return binary("lt", self.uniform(), cast(lift(p), np.float32))
 
     def normal(self) -> Expr:
-        raise UnsupportedPolicyError(
-            "Rng.normal needs cos, which the device programs do not provide"
-        )
+        """Box-Muller on the next two uniforms (rng.py:289-299):
+        sqrt(-2 log(1 - u1)) * cos(2 pi u2), float32 throughout; log and cos
+        are the framework's Cephes functions (within 2 ulp of the exact ones
+        on Box-Muller's range), the same on the device and in the oracle."""
+        u1 = self.uniform()
+        u2 = self.uniform()
+        r = unary("sqrt", binary("mul", np.float32(-2.0), unary("log", binary("sub", np.float32(1.0), u1))))
+        return binary("mul", r, unary("cos", binary("mul", np.float32(6.28318530717958648), u2)))
 
 
 # ---------------------------------------------------------------------------
@@ -244,7 +250,7 @@ def _opcode(node: Expr) -> str:
         name = {"add": "fadd", "sub": "fsub", "mul": "fmul", "div": "fdiv", "neg": "fneg",
                 "abs": "fabs", "max": "fmax", "min": "fmin", "tanh": "ftanh", "exp": "fexp",
                 "log": "flog", "sqrt": "fsqrt", "sigmoid": "fsigmoid", "square": "fsquare",
-                "relu": "frelu", "sign": "fsign", "floor": "ffloor"}.get(op)
+                "relu": "frelu", "sign": "fsign", "floor": "ffloor", "cos": "fcos", "sin": "fsin"}.get(op)
     elif k == "i":
         name = {"add": "iadd", "sub": "isub", "mul": "imul", "neg": "ineg", "abs": "iabs",
                 "max": "imax", "min": "imin", "floordiv": "ifloordiv", "mod": "imod",

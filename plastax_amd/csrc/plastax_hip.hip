@@ -122,7 +122,7 @@ enum : int32_t {
   OP_EXP = 13, OP_LOG = 14, OP_SQRT = 15, OP_SIGMOID = 16, OP_GT = 17,
   OP_GE = 18, OP_LT = 19, OP_LE = 20, OP_EQ = 21, OP_NE = 22, OP_SEL = 23,
   OP_OUT = 24, OP_LDX = 25, OP_MOV = 26, OP_SQUARE = 27, OP_RELU = 28,
-  OP_SIGN = 29
+  OP_SIGN = 29, OP_COS = 33, OP_SIN = 34
 };
 
 constexpr int kRegs = 16;
@@ -211,6 +211,8 @@ __device__ float run_program(const plx_program& P, int64_t u, const UnitFields& 
       case OP_SQRT: v = sqrtf(ra); break;
       case OP_SIGMOID: v = px::sigmoidf_(ra); break;
       case OP_SIGN: v = ra > 0.0f ? 1.0f : (ra < 0.0f ? -1.0f : ra); break;
+      case OP_COS: v = px::cosf_(ra); break;
+      case OP_SIN: v = px::sinf_(ra); break;
       case OP_GT: v = ra > rb ? 1.0f : 0.0f; break;
       case OP_GE: v = ra >= rb ? 1.0f : 0.0f; break;
       case OP_LT: v = ra < rb ? 1.0f : 0.0f; break;
@@ -1860,6 +1862,8 @@ __global__ void k_math(int32_t op, int64_t n, const float* x, const float* y, fl
     case 2: r = px::tanhf_(v); break;
     case 3: r = px::sigmoidf_(v); break;
     case 4: r = sqrtf(v); break;
+    case 6: r = px::cosf_(v); break;
+    case 7: r = px::sinf_(v); break;
     default: r = px::pow_step(v, y[i]); break;
   }
   out[i] = r;
@@ -2407,7 +2411,7 @@ int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ctrs, uint32_
 
 int plx_eval_math(int32_t op, int64_t n, const float* x, const float* y, float* out,
                   void* stream) {
-  if (n < 0 || op < 0 || op > 5) return fail(PLX_ERR_INVALID, "plx_eval_math: bad argument");
+  if (n < 0 || op < 0 || op > 7) return fail(PLX_ERR_INVALID, "plx_eval_math: bad argument");
   if (n == 0) return PLX_OK;
   if (!x || !out || (op == 5 && !y)) return fail(PLX_ERR_INVALID, "plx_eval_math: null pointer");
   k_math<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(op, n, x, y, out);

@@ -1,7 +1,7 @@
 // px_math.h -- the framework's float32 elementary functions on the device.
 //
-// exp, log and tanh follow the Cephes single-precision algorithms
-// (S. L. Moshier, Cephes Math Library: expf.c, logf.c, tanhf.c): Cody-Waite
+// exp, log, tanh, sin and cos follow the Cephes single-precision algorithms
+// (S. L. Moshier, Cephes Math Library: expf.c, logf.c, tanhf.c, sinf.c): Cody-Waite
 // range reduction and the published minimax polynomials. They are evaluated
 // with plain float32 +, -, *, / (the library is built with
 // -ffp-contract=off), so every result is a fixed sequence of correctly
@@ -103,6 +103,80 @@ __device__ __forceinline__ float tanhf_(float x) {
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf_(-x)); }
+
+// sin and cos follow Cephes sinf.c / cosf.c (Moshier): |x| is reduced
+// modulo pi/4 by the octant j = trunc(|x| * 4/pi), rounded up to even, and
+// r = |x| - j * pi/4 with pi/4 split in three (DP1 and DP2 have few
+// significant bits, so j * DP1 and j * DP2 are exact while |x| <= 8192);
+// the sine or cosine minimax polynomial of r on [-pi/4, pi/4] is chosen by
+// octant. Past 8192 the reduction loses precision (Cephes' PLOSS), past
+// 2^24 - 1 the result is 0 (TLOSS); infinities and NaN give NaN.
+__device__ __forceinline__ float sincos_reduce_(float x, int j) {
+  if (x > 8192.0f)
+    x = x - static_cast<float>(j) * 0.7853981633974483096f;
+  else
+    x = ((x - static_cast<float>(j) * 0.78515625f) - static_cast<float>(j) * 2.4187564849853515625e-4f) -
+        static_cast<float>(j) * 3.77489497744594108e-8f;
+  return x;
+}
+
+__device__ __forceinline__ float sin_poly_(float x, float z) {
+  float r = ((-1.9515295891e-4f * z + 8.3321608736e-3f) * z - 1.6666654611e-1f) * z * x;
+  return r + x;
+}
+
+__device__ __forceinline__ float cos_poly_(float z) {
+  float r = ((2.443315711809948e-5f * z - 1.388731625493765e-3f) * z + 4.166664568298827e-2f) * z * z;
+  r = r - 0.5f * z;
+  return r + 1.0f;
+}
+
+__device__ __forceinline__ float cosf_(float xx) {
+  if (xx != xx) return xx;
+  const float x = fabsf(xx);
+  if (x == __builtin_huge_valf()) return __builtin_nanf("");
+  if (x > 16777215.0f) return 0.0f;
+  int j = static_cast<int>(1.27323954473516f * x);
+  int y = j;
+  if (j & 1) {
+    j += 1;
+    y += 1;
+  }
+  j &= 7;
+  bool neg = false;
+  if (j > 3) {
+    j -= 4;
+    neg = true;
+  }
+  if (j > 1) neg = !neg;
+  const float r = sincos_reduce_(x, y);
+  const float z = r * r;
+  const float v = (j == 1 || j == 2) ? sin_poly_(r, z) : cos_poly_(z);
+  return neg ? -v : v;
+}
+
+__device__ __forceinline__ float sinf_(float xx) {
+  if (xx != xx) return xx;
+  bool neg = (__float_as_uint(xx) >> 31) != 0u;  // sin(-0) = -0
+  const float x = fabsf(xx);
+  if (x == __builtin_huge_valf()) return __builtin_nanf("");
+  if (x > 16777215.0f) return 0.0f;
+  int j = static_cast<int>(1.27323954473516f * x);
+  int y = j;
+  if (j & 1) {
+    j += 1;
+    y += 1;
+  }
+  j &= 7;
+  if (j > 3) {
+    neg = !neg;
+    j -= 4;
+  }
+  const float r = sincos_reduce_(x, y);
+  const float z = r * r;
+  const float v = (j == 1 || j == 2) ? cos_poly_(z) : sin_poly_(r, z);
+  return neg ? -v : v;
+}
 
 // jnp.maximum / jnp.minimum: NaN in either operand propagates.
 __device__ __forceinline__ float fmax_nan(float a, float b) {

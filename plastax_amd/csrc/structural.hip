@@ -318,7 +318,7 @@ int grid_for(int64_t n) {
 enum : int32_t {
   S_CONST = 1, S_IDX = 2, S_LDU = 3, S_LDC = 4, S_RNG = 5, S_MOV = 6, S_SEL = 7, S_OUT = 8,
   S_FADD = 10, S_FSUB, S_FMUL, S_FDIV, S_FNEG, S_FABS, S_FMAX, S_FMIN, S_FTANH, S_FEXP, S_FLOG,
-  S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR,
+  S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR, S_FCOS, S_FSIN,
   S_FGT = 30, S_FGE, S_FLT, S_FLE, S_FEQ, S_FNE,
   S_IADD = 40, S_ISUB, S_IMUL, S_INEG, S_IABS, S_IMAX, S_IMIN, S_IFLOORDIV, S_IMOD, S_ISIGN,
   S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
@@ -420,6 +420,8 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
       case S_FLOG: v = __float_as_uint(px::logf_(xf)); break;
       case S_FSQRT: v = __float_as_uint(__builtin_sqrtf(xf)); break;
       case S_FSIGMOID: v = __float_as_uint(px::sigmoidf_(xf)); break;
+      case S_FCOS: v = __float_as_uint(px::cosf_(xf)); break;
+      case S_FSIN: v = __float_as_uint(px::sinf_(xf)); break;
       case S_FSQUARE: v = __float_as_uint(xf * xf); break;
       case S_FRELU: v = __float_as_uint(fmax_nan(xf, 0.0f)); break;
       case S_FSIGN: v = xf > 0.0f ? 0x3F800000u : (xf < 0.0f ? 0xBF800000u : x); break;

@@ -40,6 +40,8 @@ tanh = _unary("tanh", np.tanh)
 exp = _unary("exp", np.exp)
 log = _unary("log", np.log)
 sqrt = _unary("sqrt", np.sqrt)
+cos = _unary("cos", np.cos)
+sin = _unary("sin", np.sin)
 abs = _unary("abs", np.abs)  # noqa: A001 -- mirrors jnp.abs
 absolute = abs
 negative = _unary("neg", np.negative)

@@ -269,6 +269,34 @@ def test_random_propose_matches_oracle(seed: int, kind: str, pipeline: bool) -> 
     assert out.grown > 0
 
 
+def test_normal_draws_in_proposals_match_oracle() -> None:
+    """Per-unit proposals scored by Rng.normal (Box-Muller on two uniforms,
+    rng.py:289-299: Cephes log and cos on both sides) and a normal draw mixed
+    into the destination: the commits and every column, bit for bit."""
+    n = 3000
+
+    class NormalRule(px.ProposeAddConn):
+        proposer = "per_unit"
+        proposals_per_proposer = 4
+        max_new_per_level = 40
+        max_level_gap = 3
+        direction = "any"
+        dedupe_step = True
+
+        def propose(self, u, i, j, g, rng):
+            z = rng.normal()
+            dst = (jnp.abs(z) * jnp.float32(700.0)).astype(jnp.int32) % n
+            return jnp.asarray(i, jnp.int32), dst, rng.normal() + jnp.cos(u[px.ACTIVATION, i])
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of((px.WEIGHT, jnp.sin(u[px.ACTIVATION, src]) * jnp.float32(0.5)))
+
+    hn = _random_net(NormalRule(), seed=5, n=n, levels=4, edges=12000, pipeline=True, dead_frac=0.05,
+                     with_capacity=False)
+    out, _ = _check(hn)
+    assert out.grown > 0
+
+
 def _score_rule(cands: str, *, k: int | None, M: int, **knobs):
     class Rule(px.ScoreAddConn):
         candidates = cands

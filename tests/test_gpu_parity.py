@@ -76,12 +76,13 @@ def test_device_math_is_bit_exact_with_the_oracle(oracle) -> None:
     lib = oracle.load()
     rng = np.random.default_rng(0)
     specials = np.asarray([0.0, -0.0, 1.0, -1.0, 0.625, -0.625, 88.7, -103.9, 1e-40, -1e-40,
-                           np.inf, -np.inf, np.nan, 44.4, -44.4, 1e-30], dtype=np.float32)
+                           np.inf, -np.inf, np.nan, 44.4, -44.4, 1e-30, 8192.5, -3e7, 16777215.0,
+                           np.pi, np.pi / 2], dtype=np.float32)
     xs = np.concatenate([
         rng.uniform(-90, 90, 20000), rng.uniform(-2, 2, 20000), rng.standard_normal(20000),
         np.exp(rng.uniform(-80, 80, 20000)), specials,
     ]).astype(np.float32)
-    for op, fn in ((0, lib.ox_expf), (2, lib.ox_tanhf), (3, lib.ox_sigmoidf)):
+    for op, fn in ((0, lib.ox_expf), (2, lib.ox_tanhf), (3, lib.ox_sigmoidf), (6, lib.ox_cosf), (7, lib.ox_sinf)):
         dev = _device_math(op, xs)
         ref = np.asarray([fn(float(v)) for v in xs], dtype=np.float32)
         assert _equal(dev, ref), f"op {op}: {_first_diff(dev, ref)}"

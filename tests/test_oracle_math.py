@@ -93,6 +93,23 @@ def test_elementary_functions_within_two_ulp(oracle, name, ref, lo, hi) -> None:
     assert worst <= 2.0, worst
 
 
+@pytest.mark.parametrize("name,ref", [("ox_cosf", math.cos), ("ox_sinf", math.sin)])
+def test_cos_sin_accuracy(oracle, name, ref) -> None:
+    """Cephes' float32 sin / cos: within 2 ulp of the exact function on
+    |x| <= 64 (Box-Muller's argument is in [0, 2 pi)), and within 1e-7
+    absolute up to the reduction's limit 8192, where a result near a zero of
+    the function has few significant bits left (Cephes' PLOSS range)."""
+    fn = getattr(oracle.load(), name)
+    rng = np.random.default_rng(3)
+    near = np.concatenate([rng.uniform(-64, 64, 20000), rng.uniform(0, 2 * math.pi, 20000),
+                           np.float32([0.0, -0.0, 1e-38, math.pi, math.pi / 2, math.pi / 4, 2 * math.pi])])
+    near = near.astype(np.float32)
+    worst = max(_ulps(fn(float(x)), ref(float(x))) for x in near)
+    assert worst <= 2.0, worst
+    far = rng.uniform(-8192, 8192, 20000).astype(np.float32)
+    assert max(abs(fn(float(x)) - ref(float(x))) for x in far) <= 1e-7
+
+
 def test_log_within_two_ulp(oracle) -> None:
     fn = oracle.load().ox_logf
     rng = np.random.default_rng(2)
@@ -118,6 +135,11 @@ def test_special_values(oracle) -> None:
     assert lib.ox_tanhf(50.0) == 1.0 and lib.ox_tanhf(-50.0) == -1.0
     assert lib.ox_tanhf(math.inf) == 1.0
     assert lib.ox_sigmoidf(0.0) == 0.5
+    assert lib.ox_cosf(0.0) == 1.0 and lib.ox_cosf(-0.0) == 1.0
+    assert lib.ox_sinf(0.0) == 0.0 and math.copysign(1, lib.ox_sinf(-0.0)) < 0
+    for fn in (lib.ox_cosf, lib.ox_sinf):
+        assert math.isnan(fn(math.inf)) and math.isnan(fn(-math.inf)) and math.isnan(fn(math.nan))
+        assert fn(3e7) == 0.0  # past 2^24 - 1: no significant bits left
 
 
 def test_adam_power_is_the_correctly_rounded_power(oracle) -> None:

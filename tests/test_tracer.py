@@ -142,8 +142,13 @@ def test_unsupported_phases_fail_at_build() -> None:
 
     from plastax_amd import _site
 
-    with pytest.raises(UnsupportedPolicyError):
-        _site.trace_propose(Normal(), "per_unit", {"activation": np.dtype(np.float32)}, {}, None)
+    # Rng.normal is Box-Muller on two draws (rng.py:289-299): two rng reads,
+    # then log, sqrt and cos, in the reference's float32 op order.
+    prog = _site.trace_propose(Normal(), "per_unit", {"activation": np.dtype(np.float32)}, {}, None)
+    ops = [c[0] for c in prog.code]
+    assert ops.count(_site.SOP["rng"]) == 2
+    for name in ("flog", "fsqrt", "fcos"):
+        assert _site.SOP[name] in ops
 
 
 def test_register_reuse_keeps_long_programs_in_budget() -> None:
