@@ -468,7 +468,8 @@ typedef struct plx_site_prog {
 #define PLX_SITES_GRID 3   /* g = s / per^2: src = list_a[g per + a], dst = list_b[g per + b],
                               with s % per^2 = a per + b (candidate grids) */
 #define PLX_SITES_PAIRS 4  /* src = list_a[s], dst = list_b[s] (init of the winners) */
-#define PLX_SITES_EDGE 5   /* cid = s (PruneConn) */
+#define PLX_SITES_EDGE 5   /* cid = s; src = from_id[s], dst = to_id[s] when given (through
+                              ids_logical when set): PruneConn, UpdateConn */
 
 /* One evaluation of a site program over n sites (replaces the jax.vmap of a
  * growth / pruning callback). The rng of a site is philox32(((keyed << 32)

@@ -169,6 +169,26 @@ def prune_conn(prog: _site.SiteProgram, units: dict, conns: list[dict], globals_
     return out
 
 
+def update_conn(passes: list, units: dict, conns: list[dict], globals_: Any) -> list[dict]:
+    """A user UpdateConn (phases.py:1196-1242): the incoming program over
+    every slot of every bucket, merged, then the outgoing program over the
+    result (sweep.py:488-532). Each program already keeps a dead row's old
+    value (where(dead, old, new)); cid is the bucket-local slot."""
+    out = [dict(b) for b in conns]
+    for prog, names in passes:
+        if not names:
+            continue
+        for b, bucket in enumerate(out):
+            cap = bucket["dead"].shape[0]
+            roles = {"cid": np.arange(cap, dtype=np.int32), "src": bucket["from_id"], "dst": bucket["to_id"]}
+            vals = site_eval(prog, cap, roles, units, globals_, conns=bucket)
+            nb = dict(bucket)
+            for name, v in zip(names, vals):
+                nb[name] = np.ascontiguousarray(v.astype(bucket[name].dtype, copy=False))
+            out[b] = nb
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Candidates, validity, dedupe, order, selection.
 # ---------------------------------------------------------------------------

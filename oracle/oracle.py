@@ -450,6 +450,17 @@ class OracleNet:
             self._apply(bp, acc, (levels == lv) & ~self.is_input & live)
 
     def update(self) -> None:
+        if getattr(self.plan, "update_generic", False):
+            from oracle import growth as og
+            from plastax_amd import _site
+
+            if getattr(self, "_ucp", None) is None:
+                udt = {s.name: np.dtype(s.dtype) for s in self.static.unit_fields}
+                uc = self.plan.net.update_conn
+                self._ucp = [_site.trace_conn_update(getattr(uc, d), d, udt, self.static.conn_fields,
+                                                     self.globals_) for d in ("incoming", "outgoing")]
+            self.conns = og.update_conn(self._ucp, self.units, self.conns, self.globals_)
+            return
         up = self.plan.update
         p = [float(v) for v in up.params()]
         g = self.units[up.grad_field.name]
@@ -480,7 +491,7 @@ class OracleNet:
             self.backward()
         if getattr(self.plan, "update_unit", False):
             self.update_unit()
-        if self.plan.update is not None:
+        if self.plan.update is not None or getattr(self.plan, "update_generic", False):
             self.update()
         if (getattr(self.plan, "prune_unit", False) or getattr(self.plan, "prune_conn", False)
                 or getattr(self.plan, "add_unit", False) or getattr(self.plan, "add_conn", None) is not None):

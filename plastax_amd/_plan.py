@@ -12,7 +12,9 @@ checks that every present policy has a device lowering:
 - loss: ``SoftmaxCrossEntropyLoss`` runs its own kernel; any other loss must
   return ``(jnp.sum(term), seed)`` with ``term`` and ``seed`` elementwise in
   the output's prediction and target, and is compiled to a program;
-- update_conn: one of the optim bundles (fused update kernel).
+- update_conn: one of the optim bundles (fused update kernel), or any other
+  UpdateConn, whose ``incoming`` / ``outgoing`` run as edge site programs
+  (``update_generic``; traced when the step first runs, against its globals).
 
 Policies outside these forms raise UnsupportedPolicyError.
 """
@@ -94,6 +96,7 @@ class Plan:
     add_unit: bool = False
     add_conn: Any = None  # the validated GrowthConfig, or None
     reset_global: bool = False
+    update_generic: bool = False  # update_conn is a user UpdateConn (edge programs)
 
     def pow_table(self) -> np.ndarray:
         """float32(b1^t), float32(b2^t) for t < POW_TABLE_LEN, by binary
@@ -201,10 +204,13 @@ def compile_plan(net: type, static: NetworkStatic) -> Plan:
     if net.update_conn is not None:
         uc = net.update_conn
         if not isinstance(uc, _RuleBase):
-            raise UnsupportedPolicyError(
-                f"{net.__name__}.update_conn must be an optim bundle's update_conn() to run "
-                "on the device"
-            )
+            for method in ("incoming", "outgoing"):
+                if not callable(getattr(uc, method, None)):
+                    raise TypeError(f"{net.__name__}.update_conn needs an {method} method")
+            return Plan(forward, loss, backward, None, net=net, update_unit=net.update_unit is not None,
+                        prune_unit=net.prune_unit is not None, prune_conn=net.prune_conn is not None,
+                        add_unit=net.add_unit is not None, add_conn=growth,
+                        reset_global=net.reset_global is not None, update_generic=True)
         dtypes = _float_unit_fields(static)
         _check_float_fields([uc.grad_field.name], dtypes, "update_conn")
         conn_names = {s.name for s in static.conn_fields}

@@ -486,6 +486,51 @@ def trace_init(rule: Any, unit_dtypes: dict, conn_specs: Sequence[Any], g: Any) 
     return compile_site_program(outs, roles=("src", "dst")), names
 
 
+def trace_conn_update(fn: Any, direction: str, unit_dtypes: dict, conn_specs: Sequence[Any],
+                      g: Any) -> tuple[SiteProgram, list[str]]:
+    """One pass of a user UpdateConn (sweep.py:488-532) as an edge program:
+    ``incoming(u, dst, src, c, cid, g)`` or ``outgoing(u, src, dst, c, cid,
+    g)`` -> ConnWrite, each written column merged keep-old on dead rows
+    (``where(dead, old, new)``, sweep.py:527-529). Returns the program and the
+    column each output writes. Writes of FROM_ID / TO_ID / DEAD (structure)
+    and of columns narrower than 32 bits are refused."""
+    specs = {s.name: s for s in conn_specs}
+    conn_dtypes = {n: np.dtype(s.dtype) for n, s in specs.items()}
+    u, c, gv = SiteUnitView(unit_dtypes), SiteConnView(conn_dtypes), SiteGlobals(g)
+    cid = idx("cid")
+    if direction == "incoming":
+        write = fn(u, idx("dst"), idx("src"), c, cid, gv)
+    else:
+        write = fn(u, idx("src"), idx("dst"), c, cid, gv)
+    fields = dict(getattr(write, "fields", write))
+    dead = c[_Field("dead"), cid]
+    outs, names = [], []
+    for name, value in fields.items():
+        if name not in specs:
+            raise UnsupportedPolicyError(f"update_conn writes {name!r}, which is not a conn column")
+        if name in ("from_id", "to_id", "dead"):
+            raise UnsupportedPolicyError(f"update_conn may not write {name!r} (the arena's structure)")
+        if conn_dtypes[name].itemsize != 4:
+            raise UnsupportedPolicyError(f"update_conn writes {name!r}, a {conn_dtypes[name]} column: "
+                                         "the device writes 32-bit connection columns")
+        kind = kind_of_dtype(conn_dtypes[name])
+        outs.append((_select(dead, c[_Field(name), cid], value, kind), kind))
+        names.append(name)
+    return compile_site_program(outs, roles=("cid", "src", "dst")), names
+
+
+class _Field:
+    """A column name in the shape of a FieldSpec (for the views)."""
+
+    def __init__(self, name: str) -> None:
+        self.name = name
+
+
+def _select(cond: Expr, a: Any, b: Any, kind: str) -> Expr:
+    ty = {"f": np.float32, "i": np.int32, "u": np.uint32, "b": np.bool_}[kind]
+    return Expr("sel", (cast(cond, np.bool_), cast(lift(a), ty), cast(lift(b), ty)), dtype=kind)
+
+
 def trace_predicate(rule: Any, unit_dtypes: dict, conn_dtypes: dict, g: Any) -> SiteProgram:
     """PruneConn.predicate(u, c, cid, g) -> bool (phases.py:1444-1498)."""
     out = rule.predicate(SiteUnitView(unit_dtypes), SiteConnView(conn_dtypes), idx("cid"), SiteGlobals(g))

@@ -118,6 +118,8 @@ class BatchedStepFn(StepFn):
         super().__init__(plan, static)
         if plan.update_unit:
             raise UnsupportedPolicyError("a batched step with update_unit is not in this build yet")
+        if plan.update_generic:
+            raise UnsupportedPolicyError("a batched step with a user UpdateConn is not in this build yet")
         self.batch = int(batch_size)
         self.arena_mode = "tiled"  # the batched kernels read the tiled layout's forward rows
 

@@ -515,7 +515,13 @@ __global__ void k_site_eval(plx_site_desc d) {
         c.role[2] = d.list_a[s];
         c.role[3] = d.list_b[s];
         break;
-      default: c.role[4] = static_cast<int32_t>(s); break;  // EDGE
+      default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
+        c.role[4] = static_cast<int32_t>(s);
+        const int32_t* lg = d.ids_logical;
+        if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
+        if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
+        break;
+      }
     }
     c.cid_value = c.role[4];
     if (d.site_ids) {

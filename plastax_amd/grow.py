@@ -267,6 +267,39 @@ class PruneConnPhase:
                         ids_physical=arena.uinv32)
 
 
+class ConnUpdatePhase:
+    """A user UpdateConn (phases.py:1196-1242, sweep.py:488-532): every
+    bucket's incoming pass, then every bucket's outgoing pass, each an edge
+    program whose writes land on the edge's own row (dead rows keep theirs)."""
+
+    def __init__(self, net: Any, static: Any, globals_: Any) -> None:
+        unit_dtypes = {s.name: np.dtype(s.dtype) for s in static.unit_fields}
+        uc = net.update_conn
+        self.passes = [_site.trace_conn_update(getattr(uc, d), d, unit_dtypes, static.conn_fields, globals_)
+                       for d in ("incoming", "outgoing")]
+
+    def run_physical(self, k: Kernels, arena: Any, units: Columns, globals_: Any) -> None:
+        """On the step's physical arena, over each bucket's positions that
+        held live edges when it was laid out ([base, base + live); a slot
+        dead then is not laid out with its values and keeps them, and one
+        tombstoned since reads its DEAD and keeps its row). The programs see
+        the caller's ids and each edge's logical slot."""
+        n_units = int(next(iter(units.values())).shape[0])
+        for prog, names in self.passes:
+            if not names:
+                continue
+            for b in range(arena.num_buckets):
+                base, live = arena.bases[b], arena.lives[b]
+                if live == 0:
+                    continue
+                view = {name: col[base : base + live] for name, col in arena.cols.items()}
+                k.site_eval(prog, units, globals_, n=live, kind=_lib_sites("EDGE"), num_units=n_units,
+                            conns=view, outs=[view[name] for name in names],
+                            from_id=view["from_id"], to_id=view["to_id"],
+                            site_ids=arena.slot[base : base + live], ids_logical=arena.uperm32,
+                            ids_physical=arena.uinv32)
+
+
 def _lib_sites(name: str) -> int:
     return {"UNIT": 0, "GLOBAL": 1, "CONN": 2, "GRID": 3, "PAIRS": 4, "EDGE": 5}[name]
 

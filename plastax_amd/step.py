@@ -112,6 +112,7 @@ class StepFn:
         # Unit and structural phases, traced on the first step (their
         # programs read the globals' structure).
         self._update_unit: Any = None
+        self._update_generic: Any = None
         self._prune_unit: Any = None
         self._prune: Any = None
         self._add_unit: Any = None
@@ -277,7 +278,7 @@ class StepFn:
         # bucket b's backward terms use its pre-update weights, and bucket b's
         # update needs only finalized grads (levels > b) and activations.
         self._backward_update(plan, arena, units, consts, fin_common, stream, g)
-        if plan.update is not None:
+        if plan.update is not None or plan.update_generic:
             state._arena_ahead = True
 
         # Structural phases (phases.py:1245-1498, :4490-5203).
@@ -559,6 +560,8 @@ class StepFn:
             if up is not None:
                 for b in range(nb):
                     self._update_only(plan, arena, units, consts, b, stream)
+            if plan.update_generic:
+                self._run_update_generic(arena, units, stream, g)
             return
         if bp is not None:
             dev = arena.device
@@ -593,6 +596,17 @@ class StepFn:
                 todo = range(1)  # bucket 0 is never reduced, only updated
             for b in todo:
                 self._update_only(plan, arena, units, consts, b, stream)
+        if plan.update_generic:
+            self._run_update_generic(arena, units, stream, g)
+
+    def _run_update_generic(self, arena: Arena, units: dict, stream: int, g: Any) -> None:
+        """A user UpdateConn (phases.py:1196-1242): incoming over every bucket,
+        then outgoing, as edge programs on the physical arena."""
+        from plastax_amd import grow
+
+        if self._update_generic is None:
+            self._update_generic = grow.ConnUpdatePhase(self.plan.net, self.static, g)
+        self._update_generic.run_physical(grow.Kernels(arena.device, stream), arena, units, g)
 
     def _run_update_unit(self, arena: Arena, units: dict, stream: int, g: Any) -> None:
         """update_unit (phases.py:1148-1193) on the step's unit columns, in the
