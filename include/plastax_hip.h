@@ -507,9 +507,26 @@ typedef struct plx_site_desc {
   const int32_t* site_ids;
   const int32_t* ids_logical;
   const int32_t* ids_physical;
+  /* batch > 1: the unit columns are [num_units][batch] (a batched step's
+   * per-sample columns) and a unit read at unit u reads u * batch + b, b the
+   * site's sample: for PLX_SITES_UNIT the n = num_units * batch sites are
+   * (unit s / batch, sample s % batch) and out slot k of site s lands at
+   * outs[k][s]; for the other kinds b is `sample`. */
+  int32_t batch;
+  int32_t sample;
 } plx_site_desc;
 
 PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
+
+/* The mean-of-writes connection update of a batched step with a user
+ * UpdateConn (phases.py:484-533), one float32 column at a time over n
+ * slots: mode 0 total = next - old; mode 1 total = total + (next - old)
+ * (samples in order); mode 2 old = old + total / batch. */
+#define PLX_MOW_FIRST 0
+#define PLX_MOW_ADD 1
+#define PLX_MOW_APPLY 2
+PLX_EXPORT int plx_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* old, const float* next,
+                                  float* total, void* stream);
 
 /* Ordered stream compaction (the free-slot accounting of phases.py:2573-2754
  * and every "which candidates survive" list): out[k] = the k-th position p

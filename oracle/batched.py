@@ -33,8 +33,9 @@ import numpy as np
 from oracle import oracle as ox
 
 
-def written_columns(plan: Any) -> dict[str, str]:
-    """The unit columns the per-sample phases write (phases.py:334-387)."""
+def written_columns(plan: Any, update_unit: list[str] = ()) -> dict[str, str]:
+    """The unit columns the per-sample phases write (phases.py:334-387);
+    ``update_unit`` names the columns the traced update_unit writes."""
     written = {"activation": "the input scatter"}
     for name in plan.forward.program.out_fields:
         if name is not None:
@@ -45,6 +46,8 @@ def written_columns(plan: Any) -> dict[str, str]:
         for name in plan.backward.program.out_fields:
             if name is not None:
                 written.setdefault(name, "backward_pass")
+    for name in update_unit:
+        written.setdefault(name, "update_unit")
     return written
 
 
@@ -98,6 +101,44 @@ class OracleBatch:
             else:
                 lib.ox_update_rmsprop(*base, *cols, ox.fptr(mean), ox.fptr(ones), p[0], p[1], p[2], p[3])
 
+    def _mean_of_writes(self, per: list[dict[str, np.ndarray]]) -> None:
+        """A user UpdateConn under a batched step (phases.py:484-533): per
+        sample, incoming then outgoing against the unchanged connections;
+        every float32 column (written or not) takes old + (sum of the
+        per-sample changes, in sample order) / B, a non-float written column
+        sample 0's write."""
+        from oracle import growth as og
+        from plastax_amd import _site
+
+        o = self.o
+        B = self.batch
+        if getattr(o, "_ucp", None) is None:
+            udt = {s.name: np.dtype(s.dtype) for s in o.static.unit_fields}
+            uc = o.plan.net.update_conn
+            o._ucp = [_site.trace_conn_update(getattr(uc, d), d, udt, o.static.conn_fields, o.globals_)
+                      for d in ("incoming", "outgoing")]
+        old = o.conns
+        totals = None
+        first = None
+        for b in range(B):
+            new = og.update_conn(o._ucp, per[b], old, o.globals_)
+            deltas = [{k: (nb[k] - ob[k]).astype(np.float32) for k in ob if ob[k].dtype == np.float32}
+                      for nb, ob in zip(new, old)]
+            if b == 0:
+                totals, first = deltas, new
+            else:
+                totals = [{k: (t[k] + d[k]).astype(np.float32) for k in t} for t, d in zip(totals, deltas)]
+        out = []
+        for ob, nb0, tot in zip(old, first, totals):
+            bucket = dict(ob)
+            for k, v in ob.items():
+                if v.dtype == np.float32:
+                    bucket[k] = np.ascontiguousarray((v + tot[k] / np.float32(B)).astype(np.float32))
+                else:
+                    bucket[k] = np.ascontiguousarray(nb0[k])
+            out.append(bucket)
+        o.conns = out
+
     def step(self, inputs: Any, targets: Any = None) -> np.float32:
         """One batched step (step.py:402-468); returns the batch-mean loss."""
         o = self.o
@@ -118,14 +159,19 @@ class OracleBatch:
                 losses[b] = np.float32(np.float32(0.0) + o.loss(tg[b]))
             if plan.backward is not None:
                 o.backward()
+            if getattr(plan, "update_unit", False):
+                o.update_unit()
             per.append(o.units)
         o.units = shared
         if plan.update is not None:
             self._update(per)
+        if getattr(plan, "update_generic", False):
+            self._mean_of_writes(per)
         policy = plan.net.batch_reduction
         specs = {s.name: s for s in o.static.unit_fields}
         reduced = dict(shared)
-        for name in written_columns(plan):
+        uu = list(getattr(o, "_uu", (None, []))[1]) if getattr(plan, "update_unit", False) else []
+        for name in written_columns(plan, uu):
             red = policy.reduction(specs[name])
             reduced[name] = np.ascontiguousarray(reduce_column(red.value, [u[name] for u in per], B))
         o.units = reduced

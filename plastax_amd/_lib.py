@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 13  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 14  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -65,6 +65,10 @@ class plx_finalize(ctypes.Structure):
         ("skip_inputs", c_i32),
     ]
 
+
+PLX_MOW_FIRST = 0
+PLX_MOW_ADD = 1
+PLX_MOW_APPLY = 2
 
 PLX_MAP_W_CONST = 1
 PLX_MAP_X_CONST = 2
@@ -252,6 +256,8 @@ class plx_site_desc(ctypes.Structure):
         ("site_ids", c_vp),
         ("ids_logical", c_vp),
         ("ids_physical", c_vp),
+        ("batch", c_i32),
+        ("sample", c_i32),
     ]
 
 
@@ -384,6 +390,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_abi_version": (c_i32, []),
     "plx_struct_sizes": (c_i32, [ctypes.POINTER(c_i64), c_i32]),
     "plx_site_eval": (c_i32, [ctypes.POINTER(plx_site_desc), c_vp]),
+    "plx_mean_of_writes": (c_i32, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_compact": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_scan_i32": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_scratch_ints": (c_i64, [c_i64]),

@@ -95,9 +95,10 @@ def batch_sources(arena: Arena, b: int) -> BatchSources:
     return out
 
 
-def written_columns(plan: Plan, static: NetworkStatic) -> dict[str, str]:
+def written_columns(plan: Plan, static: NetworkStatic, update_unit: list[str] = ()) -> dict[str, str]:
     """The unit columns a batched step's per-sample phases write, each with
-    the first phase writing it (phases.py:334-387)."""
+    the first phase writing it (phases.py:334-387); ``update_unit`` names the
+    columns the traced update_unit writes."""
     written = {ACTIVATION.name: "the input scatter"}
     for name in plan.forward.program.out_fields:
         if name is not None:
@@ -108,6 +109,8 @@ def written_columns(plan: Plan, static: NetworkStatic) -> dict[str, str]:
         for name in plan.backward.program.out_fields:
             if name is not None:
                 written.setdefault(name, "backward_pass")
+    for name in update_unit:
+        written.setdefault(name, "update_unit")
     return written
 
 
@@ -116,10 +119,6 @@ class BatchedStepFn(StepFn):
 
     def __init__(self, plan: Plan, static: NetworkStatic, batch_size: int) -> None:
         super().__init__(plan, static)
-        if plan.update_unit:
-            raise UnsupportedPolicyError("a batched step with update_unit is not in this build yet")
-        if plan.update_generic:
-            raise UnsupportedPolicyError("a batched step with a user UpdateConn is not in this build yet")
         self.batch = int(batch_size)
         self.arena_mode = "tiled"  # the batched kernels read the tiled layout's forward rows
 
@@ -130,7 +129,8 @@ class BatchedStepFn(StepFn):
         policy = net.batch_reduction
         specs = {s.name: s for s in self.static.unit_fields}
         out = {}
-        for name, where in written_columns(self.plan, self.static).items():
+        uu = self._update_unit.names if self._update_unit is not None else []
+        for name, where in written_columns(self.plan, self.static, uu).items():
             try:
                 out[name] = batch_written_reduction(policy, specs[name], where=where)
             except ValueError as err:
@@ -153,6 +153,13 @@ class BatchedStepFn(StepFn):
             progs.append(plan.backward.program)
         if plan.update is not None:
             names.add(plan.update.grad_field.name)
+        if self._update_unit is not None:
+            names.update(self._update_unit.prog.unit_fields)
+            names.update(self._update_unit.names)
+        if self._update_generic is not None:
+            for prog, _ in self._update_generic.passes:
+                names.update(prog.unit_fields)
+        names.discard("pruned")
         for p in progs:
             names.update(n for n in p.fields)
             names.update(n for n in p.out_fields if n is not None)
@@ -175,6 +182,14 @@ class BatchedStepFn(StepFn):
             if tuple(t.shape) != (B, n_out):
                 raise ValueError(f"batched step: targets must be {(B, n_out)}, got {tuple(t.shape)}")
             t = t.contiguous()
+        if plan.update_unit and self._update_unit is None:
+            from plastax_amd import units as unit_phases
+
+            self._update_unit = unit_phases.UpdateUnitPhase(plan.net, self.static, state.globals_)
+        if plan.update_generic and self._update_generic is None:
+            from plastax_amd import grow
+
+            self._update_generic = grow.ConnUpdatePhase(plan.net, self.static, state.globals_)
         reductions = self._check_policy()
         lib = _lib.load()
         state = state._donate()
@@ -288,11 +303,24 @@ class BatchedStepFn(StepFn):
                 )
                 run(lists.rows, lists.nrows, lists.ptr, lists, b)
 
+        # update_unit, per sample (step.py:435-436), on the live units.
+        if plan.update_unit:
+            from plastax_amd import grow
+
+            skip = None
+            if "pruned" in units:
+                skip = units["pruned"].unsqueeze(1).expand(-1, B).contiguous()
+            self._update_unit.run(grow.Kernels(dev, stream), ub, g, site_ids=arena.uperm32,
+                                  ids_physical=arena.uinv32, batch=B, skip=skip)
+
         # The connection update on the batch-mean gradient (phases.py:434-483).
         up = plan.update
         if up is not None:
             for b in range(arena.num_buckets):
                 self._update_batch(plan, arena, ub, consts, b, stream)
+            state._arena_ahead = True
+        if plan.update_generic:
+            self._mean_of_writes(arena, ub, g, stream)
             state._arena_ahead = True
 
         # reduce_batch_units (phases.py:298-332): the written columns only.
@@ -311,6 +339,55 @@ class BatchedStepFn(StepFn):
             state.globals_ = plan.net.reset_global.reset(state.globals_)
         state.step = state.step + 1
         return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
+
+    def _mean_of_writes(self, arena: Arena, ub: dict, g: Any, stream: int) -> None:
+        """A user UpdateConn under a batched step (phases.py:484-533): each
+        sample's incoming then outgoing pass against the unchanged
+        connections; every float32 column's per-sample changes are summed in
+        sample order and old + total / B is kept, a non-float column takes
+        sample 0's write. A float column neither pass writes has the change
+        old - old for every sample (+0, or NaN where old is not finite), so
+        its total is the first one and one APPLY gives the result."""
+        from plastax_amd import grow
+
+        lib = _lib.load()
+        B = self.batch
+        k = grow.Kernels(arena.device, stream)
+        passes = self._update_generic.passes
+        written = sorted({n for _, names in passes for n in names})
+        n_units = int(next(iter(ub.values())).shape[0])
+        for b in range(arena.num_buckets):
+            base, cap, live = arena.bases[b], arena.caps[b], arena.lives[b]
+            if cap == 0:
+                continue
+            old = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            floats = [n for n, c in old.items() if c.dtype == torch.float32]
+            total = {n: torch.empty_like(old[n]) for n in floats}
+            first = {}
+            for s in range(B):
+                work = {n: old[n].clone() for n in written}
+                view = {n: work.get(n, old[n]) for n in old}
+                for prog, names in passes:
+                    if names and live:
+                        k.site_eval(prog, ub, g, n=live, kind=grow._lib_sites("EDGE"), num_units=n_units,
+                                    conns={n: c[:live] for n, c in view.items()},
+                                    outs=[view[n][:live] for n in names],
+                                    from_id=view["from_id"][:live], to_id=view["to_id"][:live],
+                                    site_ids=arena.slot[base : base + live], ids_logical=arena.uperm32,
+                                    ids_physical=arena.uinv32, batch=B, sample=s)
+                for n in floats:
+                    if n not in written and s > 0:
+                        continue
+                    mode = _lib.PLX_MOW_FIRST if s == 0 else _lib.PLX_MOW_ADD
+                    _lib.check(lib.plx_mean_of_writes(cap, mode, B, old[n].data_ptr(), view[n].data_ptr(),
+                                                      total[n].data_ptr(), stream), "plx_mean_of_writes")
+                if s == 0:
+                    first = {n: work[n] for n in written if old[n].dtype != torch.float32}
+            for n in floats:
+                _lib.check(lib.plx_mean_of_writes(cap, _lib.PLX_MOW_APPLY, B, old[n].data_ptr(), None,
+                                                  total[n].data_ptr(), stream), "plx_mean_of_writes")
+            for n, w in first.items():
+                old[n].copy_(w)
 
     def _update_tiles(self, arena: Arena, b: int) -> tuple[Any, tuple]:
         """Bucket b's batched-update tiles (built once per arena): the edges

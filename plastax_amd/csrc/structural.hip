@@ -373,7 +373,25 @@ struct Site {
   uint64_t seed;      // (keyed << 32) | key
   const int32_t* ids_logical;
   const int32_t* ids_physical;
+  int32_t batch;      // unit columns are [num_units][batch] when > 1
+  int32_t sample;     // the site's sample
 };
+
+// One step of a batched mean-of-writes update over a float32 column
+// (phases.py:497-531: total of the per-sample changes in sample order, then
+// old + total / batch).
+__global__ void k_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* old, const float* next,
+                                 float* total) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (mode == PLX_MOW_FIRST)
+      total[i] = next[i] - old[i];
+    else if (mode == PLX_MOW_ADD)
+      total[i] = total[i] + (next[i] - old[i]);
+    else
+      old[i] = old[i] + total[i] / static_cast<float>(batch);
+  }
+}
 
 __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units, uint32_t* outv) {
   uint32_t r[32];
@@ -390,6 +408,7 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
         int64_t at = yi;
         at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
         if (c.ids_physical) at = c.ids_physical[at];
+        if (c.batch > 1) at = at * c.batch + c.sample;
         v = load32(p.ufields[a], p.ubytes[a], at);
         break;
       }
@@ -486,8 +505,16 @@ __global__ void k_site_eval(plx_site_desc d) {
     Site c;
     c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
     uint32_t key = 0;
+    c.batch = d.batch > 1 ? d.batch : 1;
+    c.sample = d.sample;
     switch (d.kind) {
       case PLX_SITES_UNIT:
+        if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
+          c.role[0] = static_cast<int32_t>(s / c.batch);
+          c.sample = static_cast<int32_t>(s % c.batch);
+          key = static_cast<uint32_t>(c.role[0]);
+          break;
+        }
         c.role[0] = static_cast<int32_t>(s / per);
         c.role[1] = static_cast<int32_t>(s % per);
         key = static_cast<uint32_t>(c.role[0]);
@@ -526,7 +553,7 @@ __global__ void k_site_eval(plx_site_desc d) {
     c.cid_value = c.role[4];
     if (d.site_ids) {
       if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
-      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[s / per];
+      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
     }
     c.ids_logical = d.ids_logical;
     c.ids_physical = d.ids_physical;
@@ -1026,6 +1053,10 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
   if (d->num_units < 1) return fail(PLX_ERR_INVALID, "plx_site_eval: num_units must be positive");
   if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE)
     return fail(PLX_ERR_INVALID, "plx_site_eval: unknown site kind");
+  if (d->batch > 1 && (d->sample < 0 || d->sample >= d->batch))
+    return fail(PLX_ERR_INVALID, "plx_site_eval: sample outside the batch");
+  if (d->batch > 1 && d->kind == PLX_SITES_UNIT && d->n != static_cast<int64_t>(d->num_units) * d->batch)
+    return fail(PLX_ERR_INVALID, "plx_site_eval: batched unit sites are num_units * batch");
   if ((d->kind == PLX_SITES_CONN && (!d->list_a || !d->from_id || !d->to_id || !d->occ)) ||
       ((d->kind == PLX_SITES_GRID || d->kind == PLX_SITES_PAIRS) && (!d->list_a || !d->list_b)))
     return fail(PLX_ERR_INVALID, "plx_site_eval: site lists missing");
@@ -1035,6 +1066,18 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_site_eval, dim3(grid_for(d->n)), dim3(kBlock), 0, s, *d);
   return check_launch("plx_site_eval");
+}
+
+int plx_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* old, const float* next, float* total,
+                       void* stream) {
+  if (n < 0 || mode < PLX_MOW_FIRST || mode > PLX_MOW_APPLY || batch < 1)
+    return fail(PLX_ERR_INVALID, "plx_mean_of_writes: bad n, mode or batch");
+  if (n == 0) return PLX_OK;
+  if (!old || !total || (mode != PLX_MOW_APPLY && !next))
+    return fail(PLX_ERR_INVALID, "plx_mean_of_writes: null column");
+  hipLaunchKernelGGL(k_mean_of_writes, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n,
+                     mode, batch, old, next, total);
+  return check_launch("plx_mean_of_writes");
 }
 
 int plx_compact(int64_t n, const int32_t* n_dev, int32_t mode, const void* flags, int32_t* out,

@@ -126,8 +126,9 @@ class Kernels:
                   outs: list[torch.Tensor] | None = None, conns: Columns | None = None,
                   or_into: torch.Tensor | None = None, kill_count: torch.Tensor | None = None,
                   site_ids: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
-                  ids_physical: torch.Tensor | None = None) -> None:
+                  ids_physical: torch.Tensor | None = None, batch: int = 1, sample: int = 0) -> None:
         d = _lib.plx_site_desc()
+        d.batch, d.sample = int(batch), int(sample)
         d.prog = fill_prog(sp, units, conns, globals_, physical_ids=ids_logical is not None)
         d.n, d.kind, d.per, d.num_units = int(n), int(kind), int(per), int(num_units)
         d.step = int(np.array(int(step) & 0xFFFFFFFF, dtype=np.uint32).view(np.int32))

@@ -62,16 +62,21 @@ class UpdateUnitPhase:
         self.prog, self.names = _site.trace_update_unit(net.update_unit, dtypes, globals_)
 
     def run(self, k: Kernels, units: Columns, globals_: Any, *, site_ids: torch.Tensor | None = None,
-            ids_physical: torch.Tensor | None = None) -> None:
-        n = int(units["level"].shape[0])
+            ids_physical: torch.Tensor | None = None, batch: int = 1, skip: torch.Tensor | None = None) -> None:
+        """With batch > 1 the unit columns are a batched step's [num_units][B]
+        per-sample columns (every sample updated against its own values) and
+        ``skip`` is the matching [num_units][B] PRUNED mask."""
+        n_units = int(units["level"].shape[0]) if batch == 1 else int(next(iter(units.values())).shape[0])
+        n = n_units * batch
         if not self.names:
             return
         outs = [k.mem.i32(n) for _ in self.names]
-        k.site_eval(self.prog, units, globals_, n=n, kind=0, per=1, num_units=n, outs=outs,
-                    site_ids=site_ids, ids_physical=ids_physical)
+        k.site_eval(self.prog, units, globals_, n=n, kind=0, per=1, num_units=n_units, outs=outs,
+                    site_ids=site_ids, ids_physical=ids_physical, batch=batch)
         cols = _unit_cols(units, self.specs, self.names)
         ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
-        _lib.check(k.lib.plx_unit_write(n, None, None, _ptr(units.get("pruned")), len(self.names),
+        mask = units.get("pruned") if batch == 1 else skip
+        _lib.check(k.lib.plx_unit_write(n, None, None, _ptr(mask), len(self.names),
                                         ctypes.addressof(cols), ctypes.addressof(ptrs), k.s), "plx_unit_write")
 
 

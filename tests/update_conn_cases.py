@@ -124,3 +124,19 @@ def random_hebb_net(seed: int, device: str, pipeline: bool):
         N, n, src, dst, weights=w, input_ids=np.arange(40), output_ids=np.arange(n - 8, n),
         globals_={"lr": np.float32(0.05)}, capacity_headroom=0.5, device=device)
     return N, static, state
+
+
+class PlainSGD(px.UpdateConn):
+    """SGD without the exact batch pair: a batched step takes the mean of
+    its per-sample writes (the reference's tests/test_batched.py _PlainSGD)."""
+
+    def __init__(self, lr: float, grad_field) -> None:
+        self.lr = np.float32(lr)
+        self.grad_field = grad_field
+
+    def incoming(self, u, dst, src, c, cid, g):
+        grad = u[self.grad_field, dst] * u[px.ACTIVATION, src]
+        return px.ConnWrite.of((px.WEIGHT, c[px.WEIGHT, cid] - self.lr * grad))
+
+    def outgoing(self, u, src, dst, c, cid, g):
+        return px.ConnWrite.of()
