@@ -514,6 +514,10 @@ typedef struct plx_site_desc {
    * outs[k][s]; for the other kinds b is `sample`. */
   int32_t batch;
   int32_t sample;
+  /* With or_into: stamp (optional) gets stamp_value at every site whose
+   * byte turns to 1 (see plx_kill_incident). */
+  float* stamp;
+  float stamp_value;
 } plx_site_desc;
 
 PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
@@ -776,10 +780,12 @@ PLX_EXPORT int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* prun
 
 /* The incident-edge kill of prune_unit: dead[p] |= doomed[from[p]] |
  * doomed[to[p]] over n positions (ids mapped through id_map when set);
- * kill_count (optional) counts the bytes turned to 1. */
+ * kill_count (optional) counts the bytes turned to 1, and stamp (optional)
+ * gets stamp_value at each of them (a column the caller keeps implicit while
+ * an edge lives, such as a uniform Adam step count, frozen at the kill). */
 PLX_EXPORT int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
                                  const uint8_t* doomed, const int32_t* id_map, int32_t* kill_count,
-                                 void* stream);
+                                 float* stamp, float stamp_value, void* stream);
 
 /* add_unit's placement (phases.py:1376-1405): the r-th parent (parents:
  * ascending live spawning ids, *nparents) takes the r-th free slot (free:

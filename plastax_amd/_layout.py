@@ -541,7 +541,11 @@ class Arena:
                     vals = self.uperm_t[vals.long()].to(col.dtype)
                 col[idx] = vals
                 if name == self.t_name and self.t_now and self.t_now[b] is not None:
-                    col[idx[: self.lives[b]]] = self.t_now[b]
+                    # Live edges hold the bucket's count; an edge tombstoned
+                    # since the layout keeps the count stamped at its kill.
+                    live = slice(base, base + self.lives[b])
+                    col[idx[: self.lives[b]]] = torch.where(self.cols[DEAD.name][live] != 0, self.cols[name][live],
+                                                            self.t_now[b])
 
     def init_uniform_t(self, t_name: str) -> None:
         """Adam's per-edge step count: where every live edge of a bucket holds
@@ -560,17 +564,14 @@ class Arena:
                     t = lo
             self.t_now.append(t)
 
-    def materialize_t(self) -> None:
-        """Write every uniform Adam step count back into the per-edge column
-        (live positions) and return to per-edge counts: once tombstones are
-        set in place, dead edges keep the count they died with."""
-        if not self.t_name:
-            return
-        col = self.cols[self.t_name]
-        for b, t in enumerate(self.t_now):
-            if t is not None:
-                col[self.bases[b] : self.bases[b] + self.lives[b]] = t
-                self.t_now[b] = None
+    def stamp_target(self, b: int) -> tuple[torch.Tensor | None, float]:
+        """(column from bucket b's base, value) that a kill in bucket b
+        stamps: Adam's step-count column and the bucket's count while every
+        live edge shares it (the column is not kept for live edges then), so
+        a tombstoned edge keeps the count it died with; (None, 0) otherwise."""
+        if self.t_name and self.t_now and self.t_now[b] is not None:
+            return self.cols[self.t_name][self.bases[b] :], float(self.t_now[b])
+        return None, 0.0
 
     def live_end(self, b: int) -> int:
         """End of bucket b's live positions (live edges come first)."""

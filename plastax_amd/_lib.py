@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 14  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 15  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -258,6 +258,8 @@ class plx_site_desc(ctypes.Structure):
         ("ids_physical", c_vp),
         ("batch", c_i32),
         ("sample", c_i32),
+        ("stamp", c_vp),
+        ("stamp_value", ctypes.c_float),
     ]
 
 
@@ -412,7 +414,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
-    "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
                                c_vp]),
 }

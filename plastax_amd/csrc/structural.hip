@@ -563,6 +563,7 @@ __global__ void k_site_eval(plx_site_desc d) {
     if (d.or_into) {
       if (out[0] && !d.or_into[s]) {
         d.or_into[s] = 1;
+        if (d.stamp) d.stamp[s] = d.stamp_value;
         if (d.kill_count) atomicAdd(d.kill_count, 1);
       }
     } else {
@@ -919,7 +920,8 @@ __global__ void k_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels,
 }
 
 __global__ void k_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
-                                const uint8_t* doomed, const int32_t* id_map, int32_t* count) {
+                                const uint8_t* doomed, const int32_t* id_map, int32_t* count, float* stamp,
+                                float stamp_value) {
   for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
        p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     if (dead[p]) continue;  // already a tombstone: its ids are not read
@@ -930,6 +932,7 @@ __global__ void k_kill_incident(int64_t n, const int32_t* from_id, const int32_t
     }
     if (doomed[a] || doomed[b]) {
       dead[p] = 1;
+      if (stamp) stamp[p] = stamp_value;
       if (count) atomicAdd(count, 1);
     }
   }
@@ -1314,12 +1317,12 @@ int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const u
 }
 
 int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead, const uint8_t* doomed,
-                      const int32_t* id_map, int32_t* kill_count, void* stream) {
+                      const int32_t* id_map, int32_t* kill_count, float* stamp, float stamp_value, void* stream) {
   if (n < 0) return fail(PLX_ERR_INVALID, "plx_kill_incident: negative n");
   if (n == 0) return PLX_OK;
   if (!from_id || !to_id || !dead || !doomed) return fail(PLX_ERR_INVALID, "plx_kill_incident: null pointer");
   hipLaunchKernelGGL(k_kill_incident, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n,
-                     from_id, to_id, dead, doomed, id_map, kill_count);
+                     from_id, to_id, dead, doomed, id_map, kill_count, stamp, stamp_value);
   return check_launch("plx_kill_incident");
 }
 

@@ -126,9 +126,11 @@ class Kernels:
                   outs: list[torch.Tensor] | None = None, conns: Columns | None = None,
                   or_into: torch.Tensor | None = None, kill_count: torch.Tensor | None = None,
                   site_ids: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
-                  ids_physical: torch.Tensor | None = None, batch: int = 1, sample: int = 0) -> None:
+                  ids_physical: torch.Tensor | None = None, batch: int = 1, sample: int = 0,
+                  stamp: torch.Tensor | None = None, stamp_value: float = 0.0) -> None:
         d = _lib.plx_site_desc()
         d.batch, d.sample = int(batch), int(sample)
+        d.stamp, d.stamp_value = _ptr(stamp), float(stamp_value)
         d.prog = fill_prog(sp, units, conns, globals_, physical_ids=ids_logical is not None)
         d.n, d.kind, d.per, d.num_units = int(n), int(kind), int(per), int(num_units)
         d.step = int(np.array(int(step) & 0xFFFFFFFF, dtype=np.uint32).view(np.int32))
@@ -251,21 +253,24 @@ class PruneConnPhase:
                         conns=bucket, or_into=bucket["dead"], kill_count=kill_count)
 
     def run_physical(self, k: Kernels, arena: Any, units: Columns, globals_: Any,
-                     kill_count: torch.Tensor) -> None:
+                     kill_count: torch.Tensor | None = None) -> None:
         """On the step's physical arena: positions of bucket b are
         [base_b, base_b + cap_b), unit columns and the id columns are in the
         arena's unit order; the program still sees the caller's ids and each
-        edge's logical slot (arena.slot)."""
+        edge's logical slot (arena.slot). An edge killed in a bucket whose
+        Adam step count is kept as one number gets that number in its own
+        column (arena.stamp_target), so no host read follows the pass."""
         n_units = int(next(iter(units.values())).shape[0])
         for b in range(arena.num_buckets):
             base, cap = arena.bases[b], arena.caps[b]
             if cap == 0:
                 continue
             view = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            stamp, value = arena.stamp_target(b)
             k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
                         conns=view, or_into=view["dead"], kill_count=kill_count,
                         site_ids=arena.slot[base : base + cap], ids_logical=arena.uperm32,
-                        ids_physical=arena.uinv32)
+                        ids_physical=arena.uinv32, stamp=stamp, stamp_value=value)
 
 
 class ConnUpdatePhase:

@@ -305,27 +305,22 @@ class StepFn:
             if self._prune_unit is None:
                 self._prune_unit = unit_phases.PruneUnitPhase(plan.net, self.static, g)
             doomed, _ = self._prune_unit.run(k, units, g, site_ids=arena.uperm32, ids_physical=arena.uinv32)
-            kills = torch.zeros(1, dtype=torch.int32, device=state.device)
-            self._prune_unit.kill(k, arena.n_positions, arena.cols["from_id"], arena.cols["to_id"],
-                                  arena.cols["dead"], doomed, kills)
-            if int(kills.item()):
-                arena.materialize_t()
-                arena.dead_in_rows = True
-                state._arena_ahead = True
+            self._prune_unit.kill(k, arena, doomed)
+            # Whether anything died stays on the device: from here on the
+            # kernels read DEAD inside the live ranges.
+            arena.dead_in_rows = True
+            state._arena_ahead = True
         if plan.prune_conn:
             if self._prune is None:
                 self._prune = grow.PruneConnPhase(plan.net, self.static, g)
-            kills = torch.zeros(1, dtype=torch.int32, device=state.device)
             timer = self.timer
             if timer is not None:
                 timer.begin("prune_conn")
-            self._prune.run_physical(k, arena, units, g, kills)
+            self._prune.run_physical(k, arena, units, g)
             if timer is not None:
                 timer.end("prune_conn")
-            if int(kills.item()):
-                arena.materialize_t()
-                arena.dead_in_rows = True
-                state._arena_ahead = True
+            arena.dead_in_rows = True
+            state._arena_ahead = True
         if plan.add_unit:
             if self._add_unit is None:
                 self._add_unit = unit_phases.AddUnitPhase(plan.net, self.static, g)

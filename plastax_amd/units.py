@@ -118,10 +118,31 @@ class PruneUnitPhase:
         return doomed, count
 
     @staticmethod
-    def kill(k: Kernels, n: int, from_id: torch.Tensor, to_id: torch.Tensor, dead: torch.Tensor,
-             doomed: torch.Tensor, kills: torch.Tensor) -> None:
+    def kill_columns(k: Kernels, n: int, from_id: torch.Tensor, to_id: torch.Tensor, dead: torch.Tensor,
+                     doomed: torch.Tensor, kills: torch.Tensor | None = None) -> None:
+        """The incident-edge kill over n slots of one bucket's columns (unit
+        ids in the numbering of ``doomed``)."""
         _lib.check(k.lib.plx_kill_incident(n, from_id.data_ptr(), to_id.data_ptr(), dead.data_ptr(),
-                                           doomed.data_ptr(), None, kills.data_ptr(), k.s), "plx_kill_incident")
+                                           doomed.data_ptr(), None, None if kills is None else kills.data_ptr(),
+                                           None, 0.0, k.s), "plx_kill_incident")
+
+    @staticmethod
+    def kill(k: Kernels, arena: Any, doomed: torch.Tensor, kills: torch.Tensor | None = None) -> None:
+        """The incident-edge kill on the physical arena, bucket by bucket
+        (physical unit ids on both sides); an edge killed in a bucket whose
+        Adam step count is kept as one number gets that number in its own
+        column (arena.stamp_target)."""
+        cols = arena.cols
+        for b in range(arena.num_buckets):
+            base, span = arena.bases[b], arena.ends[b] - arena.bases[b]
+            if span == 0:
+                continue
+            stamp, value = arena.stamp_target(b)
+            _lib.check(k.lib.plx_kill_incident(span, cols["from_id"][base:].data_ptr(), cols["to_id"][base:].data_ptr(),
+                                               cols["dead"][base:].data_ptr(), doomed.data_ptr(), None,
+                                               None if kills is None else kills.data_ptr(),
+                                               None if stamp is None else stamp.data_ptr(), float(value), k.s),
+                       "plx_kill_incident")
 
 
 class AddUnitPhase:

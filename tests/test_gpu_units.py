@@ -34,7 +34,7 @@ def _run_device(net, static, hu, hc):
         doomed, count = ph.run(k, units, None)
         kills = torch.zeros(1, dtype=torch.int32, device=DEV)
         for b in conns:
-            ph.kill(k, int(b["dead"].shape[0]), b["from_id"], b["to_id"], b["dead"], doomed, kills)
+            ph.kill_columns(k, int(b["dead"].shape[0]), b["from_id"], b["to_id"], b["dead"], doomed, kills)
         pruned_by_phase = np.flatnonzero(doomed.cpu().numpy()).tolist()
         assert int(count.item()) == len(pruned_by_phase)
     if net.add_unit is not None:
