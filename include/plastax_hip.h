@@ -101,6 +101,8 @@ typedef struct plx_map {
  * over the physical (destination-sorted) positions; each row is folded in slot
  * order, combined into acc, and finalized rows apply `apply` and reset acc.
  * `dead` may be null when no row range holds a tombstone. */
+struct plx_site_prog;
+
 typedef struct plx_forward_desc {
   int32_t nrows;
   int32_t monoid;
@@ -116,6 +118,23 @@ typedef struct plx_forward_desc {
   plx_finalize fin;
   plx_program apply;
   plx_map map;             /* the map's factors (zeroed: weight * x[from]) */
+  /* Optional (null prune_prog: none): a PruneConn predicate evaluated in the
+   * same sweep (the fused forward + prune of phases.py:2322-2444). For every
+   * position p of the rows' ranges, prune_sink[p] = 1 where the predicate
+   * holds and p is not a tombstone (dead, when given), else 0; the predicate
+   * is the site program at *prune_prog (device memory) evaluated as the
+   * PLX_SITES_EDGE site s = p - prune_base with cid prune_slot[s] and unit
+   * ids mapped through ids_logical / ids_physical (see plx_site_desc). The
+   * state's DEAD is not written: the caller commits the sink at its prune
+   * slot (plx_merge_kills). */
+  const struct plx_site_prog* prune_prog;
+  uint8_t* prune_sink;
+  const int32_t* prune_slot;
+  const int32_t* ids_logical;
+  const int32_t* ids_physical;
+  int64_t prune_base;
+  int32_t num_units;
+  int32_t reserved;
 } plx_forward_desc;
 
 PLX_EXPORT int plx_forward_bucket(const plx_forward_desc* d, void* stream);
@@ -777,6 +796,13 @@ PLX_EXPORT int plx_unit_write(int64_t n, const int32_t* n_dev, const int32_t* id
 PLX_EXPORT int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const uint8_t* exempt,
                               int32_t ncols, const plx_unit_col* cols, uint8_t* doomed, int32_t* doomed_count,
                               void* stream);
+
+/* Commits the fused forward's tombstones (build_prune_merge_phase,
+ * phases.py:2447-2469) over n positions: where sink[p] is set and dead[p]
+ * is not, dead[p] = 1 and stamp (optional) gets stamp_value (see
+ * plx_kill_incident). */
+PLX_EXPORT int plx_merge_kills(int64_t n, const uint8_t* sink, uint8_t* dead, float* stamp, float stamp_value,
+                               void* stream);
 
 /* The incident-edge kill of prune_unit: dead[p] |= doomed[from[p]] |
  * doomed[to[p]] over n positions (ids mapped through id_map when set);

@@ -106,6 +106,7 @@ class ChurnArena(Arena):
         self.fwd_carry = True
         self.bwd_carry = True
         self.dead_in_rows = False
+        self.prune_sink = None
         self.t_name = None
         self.t_now = []
         nbits = max(1, int(n).bit_length())

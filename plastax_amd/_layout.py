@@ -307,6 +307,7 @@ class Arena:
         # Live positions come first in every bucket, so no forward row range
         # holds a tombstone until one is set in place after this build.
         self.dead_in_rows = False
+        self.prune_sink: torch.Tensor | None = None  # the fused forward's tombstones (plastax_amd.fusion)
         # Adam's step count when every live edge of a bucket holds the same
         # one (per bucket; None: the per-edge column is authoritative).
         self.t_name: str | None = None

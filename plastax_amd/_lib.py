@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 15  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 16  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -94,6 +94,14 @@ class plx_forward_desc(ctypes.Structure):
         ("fin", plx_finalize),
         ("apply", plx_program),
         ("map", plx_map),
+        ("prune_prog", c_vp),
+        ("prune_sink", c_vp),
+        ("prune_slot", c_vp),
+        ("ids_logical", c_vp),
+        ("ids_physical", c_vp),
+        ("prune_base", c_i64),
+        ("num_units", c_i32),
+        ("reserved", c_i32),
     ]
 
 
@@ -414,6 +422,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
                                c_vp]),

@@ -22,6 +22,7 @@
 #include "../../include/plastax_hip.h"
 #include "px_common.h"
 #include "px_math.h"
+#include "px_site.h"
 
 namespace plx_detail {
 
@@ -354,7 +355,28 @@ struct FwdWin {
   int b, w0, eb, ee;
 };
 
-template <int M>
+// The fused forward's PruneConn predicate at position p (an EDGE site of
+// the bucket's positions, as plx_site_eval runs it on the physical arena).
+__device__ __forceinline__ uint8_t prune_at(const plx_forward_desc& d, int64_t p, uint32_t keyed) {
+  Site c;
+  c.role[0] = c.role[1] = c.role[2] = c.role[3] = 0;
+  const int32_t s = static_cast<int32_t>(p - d.prune_base);
+  c.role[4] = s;
+  c.cid_value = d.prune_slot ? d.prune_slot[s] : s;
+  c.seed = static_cast<uint64_t>(keyed) << 32;
+  c.ids_logical = d.ids_logical;
+  c.ids_physical = d.ids_physical;
+  c.batch = 1;
+  c.sample = 0;
+  uint32_t out[PLX_MAX_SOUTS];
+  out[0] = 0;
+  site_run(*d.prune_prog, c, d.num_units, out);
+  return out[0] != 0u;
+}
+
+// PRUNE: the PruneConn predicate of every visited position goes to
+// prune_sink (see plx_forward_desc).
+template <int M, bool PRUNE>
 __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
   __shared__ __align__(16) float buf[2][kFwdWin];
   __shared__ float tbl[kFwdTbl > 0 ? kFwdTbl : 1];
@@ -424,6 +446,23 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
         o.z = ok[i][2] ? map_term(d.map, cur.wv[i].z, xv[i][2]) : ident;
         o.w = ok[i][3] ? map_term(d.map, cur.wv[i].w, xv[i][3]) : ident;
         *reinterpret_cast<float4*>(out + 4 * q) = o;
+      }
+    }
+    if (PRUNE) {
+      // Each position of the rows' ranges is in exactly one window's
+      // [eb, ee), so every sink byte has one writer.
+      const uint32_t keyed = px::philox32(0, 1);  // the rng key of an unseeded step-0 site
+#pragma unroll
+      for (int i = 0; i < kFwdQuads; ++i) {
+        const int q = threadIdx.x + i * kFwdBlock;
+        const int e = w.w0 + 4 * q;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int p = e + k;
+          if (4 * q >= wn || p < w.eb || p >= w.ee) continue;
+          const bool tomb = (cur.dv[i] >> (8 * k)) & 0xFFu;
+          d.prune_sink[p] = tomb ? 0 : prune_at(d, p, keyed);
+        }
       }
     }
   };
@@ -1938,7 +1977,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 15; }
+int32_t plx_abi_version(void) { return 16; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[16] = {
@@ -1965,15 +2004,38 @@ int plx_forward_bucket(const plx_forward_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: tbl_len must be in [0, PLX_MAX_TBL]");
   if (!d->fin.level || !d->fin.is_input)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket: fin.level and fin.is_input are required");
+  const bool prune = d->prune_prog != nullptr;
+  if (prune && (!d->prune_sink || d->num_units <= 0))
+    return fail(PLX_ERR_INVALID, "plx_forward_bucket: prune_prog needs prune_sink and num_units");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned nblk = grid_for(d->nrows, kFwdRows);
   const unsigned cap = static_cast<unsigned>(cu_count() * kFwdPerCU);
   const unsigned grid = nblk < cap ? nblk : cap;
   switch (d->monoid) {
-    case PLX_MONOID_SUM: k_forward<PLX_MONOID_SUM><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_PROD: k_forward<PLX_MONOID_PROD><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MAX: k_forward<PLX_MONOID_MAX><<<grid, kFwdBlock, 0, s>>>(*d); break;
-    case PLX_MONOID_MIN: k_forward<PLX_MONOID_MIN><<<grid, kFwdBlock, 0, s>>>(*d); break;
+    case PLX_MONOID_SUM:
+      if (prune)
+        k_forward<PLX_MONOID_SUM, true><<<grid, kFwdBlock, 0, s>>>(*d);
+      else
+        k_forward<PLX_MONOID_SUM, false><<<grid, kFwdBlock, 0, s>>>(*d);
+      break;
+    case PLX_MONOID_PROD:
+      if (prune)
+        k_forward<PLX_MONOID_PROD, true><<<grid, kFwdBlock, 0, s>>>(*d);
+      else
+        k_forward<PLX_MONOID_PROD, false><<<grid, kFwdBlock, 0, s>>>(*d);
+      break;
+    case PLX_MONOID_MAX:
+      if (prune)
+        k_forward<PLX_MONOID_MAX, true><<<grid, kFwdBlock, 0, s>>>(*d);
+      else
+        k_forward<PLX_MONOID_MAX, false><<<grid, kFwdBlock, 0, s>>>(*d);
+      break;
+    case PLX_MONOID_MIN:
+      if (prune)
+        k_forward<PLX_MONOID_MIN, true><<<grid, kFwdBlock, 0, s>>>(*d);
+      else
+        k_forward<PLX_MONOID_MIN, false><<<grid, kFwdBlock, 0, s>>>(*d);
+      break;
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_forward_bucket: unknown monoid");
   }
   return check_launch("plx_forward_bucket");

@@ -27,6 +27,7 @@
 #include "../../include/plastax_hip.h"
 #include "px_common.h"
 #include "px_math.h"
+#include "px_site.h"
 
 using plx_detail::check_launch;
 using plx_detail::fail;
@@ -312,70 +313,8 @@ int grid_for(int64_t n) {
 }
 
 // ---------------------------------------------------------------------------
-// Site programs.
+// Site programs (the interpreter is in px_site.h).
 // ---------------------------------------------------------------------------
-
-enum : int32_t {
-  S_CONST = 1, S_IDX = 2, S_LDU = 3, S_LDC = 4, S_RNG = 5, S_MOV = 6, S_SEL = 7, S_OUT = 8,
-  S_FADD = 10, S_FSUB, S_FMUL, S_FDIV, S_FNEG, S_FABS, S_FMAX, S_FMIN, S_FTANH, S_FEXP, S_FLOG,
-  S_FSQRT, S_FSIGMOID, S_FSQUARE, S_FRELU, S_FSIGN, S_FFLOOR, S_FCOS, S_FSIN,
-  S_FGT = 30, S_FGE, S_FLT, S_FLE, S_FEQ, S_FNE,
-  S_IADD = 40, S_ISUB, S_IMUL, S_INEG, S_IABS, S_IMAX, S_IMIN, S_IFLOORDIV, S_IMOD, S_ISIGN,
-  S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
-  S_UMAX = 60, S_UMIN, S_UFLOORDIV, S_UMOD, S_UGT, S_UGE, S_ULT, S_ULE,
-  S_AND = 70, S_OR, S_XOR, S_NOT, S_SHL, S_SHRU, S_SHRI, S_BNOT,
-  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B
-};
-
-__device__ __forceinline__ float fmax_nan(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return a > b ? a : b;
-}
-__device__ __forceinline__ float fmin_nan(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return a < b ? a : b;
-}
-__device__ __forceinline__ int32_t floordiv_i32(int32_t a, int32_t b) {
-  if (b == 0) return a == 0 ? -1 : -2;
-  if (a == INT32_MIN && b == -1) return INT32_MIN;
-  int32_t q = a / b;
-  if ((a % b != 0) && ((a < 0) != (b < 0))) q -= 1;
-  return q;
-}
-__device__ __forceinline__ int32_t mod_i32(int32_t a, int32_t b) {
-  if (b == 0) return a;
-  if (b == -1) return 0;
-  int32_t r = a % b;
-  if (r != 0 && ((r < 0) != (b < 0))) r += b;
-  return r;
-}
-__device__ __forceinline__ int32_t f2i(float x) {
-  if (x != x) return 0;
-  if (x >= 2147483648.0f) return INT32_MAX;
-  if (x <= -2147483648.0f) return INT32_MIN;
-  return static_cast<int32_t>(x);
-}
-__device__ __forceinline__ uint32_t f2u(float x) {
-  if (x != x || x <= 0.0f) return 0u;
-  if (x >= 4294967296.0f) return UINT32_MAX;
-  return static_cast<uint32_t>(x);
-}
-__device__ __forceinline__ uint32_t load32(const void* base, int32_t bytes, int64_t at) {
-  if (bytes == 1) return static_cast<const uint8_t*>(base)[at] != 0;
-  return static_cast<const uint32_t*>(base)[at];
-}
-
-struct Site {
-  int32_t role[5];    // i, j, src, dst, cid (the position conn fields are read at)
-  int32_t cid_value;  // the cid the program sees
-  uint64_t seed;      // (keyed << 32) | key
-  const int32_t* ids_logical;
-  const int32_t* ids_physical;
-  int32_t batch;      // unit columns are [num_units][batch] when > 1
-  int32_t sample;     // the site's sample
-};
 
 // One step of a batched mean-of-writes update over a float32 column
 // (phases.py:497-531: total of the per-sample changes in sample order, then
@@ -390,108 +329,6 @@ __global__ void k_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* 
       total[i] = total[i] + (next[i] - old[i]);
     else
       old[i] = old[i] + total[i] / static_cast<float>(batch);
-  }
-}
-
-__device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units, uint32_t* outv) {
-  uint32_t r[32];
-  for (int k = 0; k < p.ninstr; ++k) {
-    const int op = p.code[4 * k], d = p.code[4 * k + 1], a = p.code[4 * k + 2], b = p.code[4 * k + 3];
-    const uint32_t x = r[a & 31], y = r[b & 31];
-    const int32_t xi = static_cast<int32_t>(x), yi = static_cast<int32_t>(y);
-    const float xf = __uint_as_float(x), yf = __uint_as_float(y);
-    uint32_t v = 0;
-    switch (op) {
-      case S_CONST: v = p.consts[a]; break;
-      case S_IDX: v = static_cast<uint32_t>(a == 4 ? c.cid_value : c.role[a]); break;
-      case S_LDU: {
-        int64_t at = yi;
-        at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
-        if (c.ids_physical) at = c.ids_physical[at];
-        if (c.batch > 1) at = at * c.batch + c.sample;
-        v = load32(p.ufields[a], p.ubytes[a], at);
-        break;
-      }
-      case S_LDC:
-        v = load32(p.cfields[a], p.cbytes[a] & 0xFF, c.role[4]);
-        if ((p.cbytes[a] & PLX_SITE_ID_COLUMN) && c.ids_logical) {
-          const int32_t id = static_cast<int32_t>(v);
-          v = static_cast<uint32_t>(c.ids_logical[id < 0 ? 0 : (id > num_units - 1 ? num_units - 1 : id)]);
-        }
-        break;
-      case S_RNG:
-        v = px::philox32(c.seed, (static_cast<uint64_t>(static_cast<uint32_t>(c.role[1])) << 16) |
-                                     static_cast<uint32_t>(a));
-        break;
-      case S_MOV: v = x; break;
-      case S_SEL: v = x ? r[b & 31] : r[(b + 1) & 31]; break;
-      case S_OUT: outv[d] = x; continue;
-      case S_FADD: v = __float_as_uint(xf + yf); break;
-      case S_FSUB: v = __float_as_uint(xf - yf); break;
-      case S_FMUL: v = __float_as_uint(xf * yf); break;
-      case S_FDIV: v = __float_as_uint(xf / yf); break;
-      case S_FNEG: v = x ^ 0x80000000u; break;
-      case S_FABS: v = x & 0x7FFFFFFFu; break;
-      case S_FMAX: v = __float_as_uint(fmax_nan(xf, yf)); break;
-      case S_FMIN: v = __float_as_uint(fmin_nan(xf, yf)); break;
-      case S_FTANH: v = __float_as_uint(px::tanhf_(xf)); break;
-      case S_FEXP: v = __float_as_uint(px::expf_(xf)); break;
-      case S_FLOG: v = __float_as_uint(px::logf_(xf)); break;
-      case S_FSQRT: v = __float_as_uint(__builtin_sqrtf(xf)); break;
-      case S_FSIGMOID: v = __float_as_uint(px::sigmoidf_(xf)); break;
-      case S_FCOS: v = __float_as_uint(px::cosf_(xf)); break;
-      case S_FSIN: v = __float_as_uint(px::sinf_(xf)); break;
-      case S_FSQUARE: v = __float_as_uint(xf * xf); break;
-      case S_FRELU: v = __float_as_uint(fmax_nan(xf, 0.0f)); break;
-      case S_FSIGN: v = xf > 0.0f ? 0x3F800000u : (xf < 0.0f ? 0xBF800000u : x); break;
-      case S_FFLOOR: v = __float_as_uint(floorf(xf)); break;
-      case S_FGT: v = xf > yf; break;
-      case S_FGE: v = xf >= yf; break;
-      case S_FLT: v = xf < yf; break;
-      case S_FLE: v = xf <= yf; break;
-      case S_FEQ: v = xf == yf; break;
-      case S_FNE: v = xf != yf; break;
-      case S_IADD: v = x + y; break;
-      case S_ISUB: v = x - y; break;
-      case S_IMUL: v = x * y; break;
-      case S_INEG: v = 0u - x; break;
-      case S_IABS: v = xi < 0 ? 0u - x : x; break;
-      case S_IMAX: v = xi > yi ? x : y; break;
-      case S_IMIN: v = xi < yi ? x : y; break;
-      case S_IFLOORDIV: v = static_cast<uint32_t>(floordiv_i32(xi, yi)); break;
-      case S_IMOD: v = static_cast<uint32_t>(mod_i32(xi, yi)); break;
-      case S_ISIGN: v = static_cast<uint32_t>(xi > 0 ? 1 : (xi < 0 ? -1 : 0)); break;
-      case S_IGT: v = xi > yi; break;
-      case S_IGE: v = xi >= yi; break;
-      case S_ILT: v = xi < yi; break;
-      case S_ILE: v = xi <= yi; break;
-      case S_IEQ: v = x == y; break;
-      case S_INE: v = x != y; break;
-      case S_UMAX: v = x > y ? x : y; break;
-      case S_UMIN: v = x < y ? x : y; break;
-      case S_UFLOORDIV: v = y ? x / y : UINT32_MAX; break;
-      case S_UMOD: v = y ? x % y : x; break;
-      case S_UGT: v = x > y; break;
-      case S_UGE: v = x >= y; break;
-      case S_ULT: v = x < y; break;
-      case S_ULE: v = x <= y; break;
-      case S_AND: v = x & y; break;
-      case S_OR: v = x | y; break;
-      case S_XOR: v = x ^ y; break;
-      case S_NOT: v = ~x; break;
-      case S_BNOT: v = x == 0u; break;
-      case S_SHL: v = y >= 32u ? 0u : x << y; break;
-      case S_SHRU: v = y >= 32u ? 0u : x >> y; break;
-      case S_SHRI: v = y >= 32u ? (xi < 0 ? UINT32_MAX : 0u) : static_cast<uint32_t>(xi >> y); break;
-      case S_I2F: v = __float_as_uint(static_cast<float>(xi)); break;
-      case S_U2F: v = __float_as_uint(static_cast<float>(x)); break;
-      case S_F2I: v = static_cast<uint32_t>(f2i(xf)); break;
-      case S_F2U: v = f2u(xf); break;
-      case S_F2B: v = xf != 0.0f; break;
-      case S_I2B: v = x != 0u; break;
-      default: break;
-    }
-    r[d & 31] = v;
   }
 }
 
@@ -919,6 +756,16 @@ __global__ void k_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels,
   start[u] = static_cast<int32_t>(lo);
 }
 
+__global__ void k_merge_kills(int64_t n, const uint8_t* sink, uint8_t* dead, float* stamp, float stamp_value) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (sink[p] && !dead[p]) {
+      dead[p] = 1;
+      if (stamp) stamp[p] = stamp_value;
+    }
+  }
+}
+
 __global__ void k_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead,
                                 const uint8_t* doomed, const int32_t* id_map, int32_t* count, float* stamp,
                                 float stamp_value) {
@@ -1314,6 +1161,15 @@ int plx_unit_prune(int64_t n, const uint32_t* selected, uint8_t* pruned, const u
   hipLaunchKernelGGL(k_unit_prune, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, selected,
                      pruned, exempt, pack_cols(ncols, cols), doomed, doomed_count);
   return check_launch("plx_unit_prune");
+}
+
+int plx_merge_kills(int64_t n, const uint8_t* sink, uint8_t* dead, float* stamp, float stamp_value, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_merge_kills: negative n");
+  if (n == 0) return PLX_OK;
+  if (!sink || !dead) return fail(PLX_ERR_INVALID, "plx_merge_kills: null pointer");
+  hipLaunchKernelGGL(k_merge_kills, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, sink,
+                     dead, stamp, stamp_value);
+  return check_launch("plx_merge_kills");
 }
 
 int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead, const uint8_t* doomed,

@@ -23,6 +23,7 @@ from plastax_amd._expr import UnsupportedPolicyError
 from plastax_amd._layout import NSUPER, TILE, Arena
 from plastax_amd._plan import Plan, compile_plan, program_struct
 from plastax_amd._types import ACTIVATION, Propagation
+from plastax_amd.fusion import PruneFusionPlan, PruneFusionRecord, plan_prune_fusion
 from plastax_amd.state import NetworkState, NetworkStatic
 
 
@@ -81,8 +82,11 @@ def make_step(
     if batch_size is not None:
         from plastax_amd.batched import BatchedStepFn
 
-        return BatchedStepFn(compile_plan(net, static), static, batch_size)
-    return StepFn(compile_plan(net, static), static)
+        step = BatchedStepFn(compile_plan(net, static), static, batch_size)
+    else:
+        step = StepFn(compile_plan(net, static), static)
+    step.prune_fusion = PruneFusionRecord(fuse_prune)
+    return step
 
 
 def _stream(device: torch.device) -> int:
@@ -117,6 +121,9 @@ class StepFn:
         self._prune: Any = None
         self._add_unit: Any = None
         self._grow: Any = None
+        # prune_conn inside the forward sweep (phases.py:1629-1848), planned
+        # on the first call.
+        self.prune_fusion = PruneFusionRecord("auto")
 
     def _launch(self, kind: str, fn: Any, *args: Any) -> None:
         timer = self.timer
@@ -240,6 +247,8 @@ class StepFn:
             acc = torch.empty(n_units, dtype=torch.float32, device=dev)
             _lib.call("plx_fill_f32", n_units, fp.identity, acc.data_ptr(), stream)
         prog = program_struct(fp.program, units, g, out_override=swaps)
+        fusion = self._fusion_plan(g)
+        fused = self._fused_prune_progs(arena, units, fin_common, g, stream) if fusion.fused else None
         for b in range(arena.num_buckets):
             rows = arena.fwd[b]
             d = _lib.plx_forward_desc()
@@ -262,8 +271,17 @@ class StepFn:
             d.fin.fin_level = -1 if arena.pipeline else b + 1
             d.fin.skip_inputs = 1
             d.apply = prog
+            if fused is not None and fusion.engine == "hip":
+                d.prune_prog = fused[b].data_ptr()
+                d.prune_sink = arena.prune_sink.data_ptr()
+                d.prune_slot = arena.slot[arena.bases[b]:].data_ptr()
+                d.ids_logical, d.ids_physical = arena.uperm32.data_ptr(), arena.uinv32.data_ptr()
+                d.prune_base = arena.bases[b]
+                d.num_units = n_units
             self._launch("forward", lib.plx_forward_bucket, d, stream)
         self._unshadow(units, swaps)
+        if fused is not None and fusion.engine == "xla":
+            self._xla_prune(arena, g, stream)
 
         # Loss (phases.py:1107-1131).
         if plan.loss is not None:
@@ -316,7 +334,10 @@ class StepFn:
             timer = self.timer
             if timer is not None:
                 timer.begin("prune_conn")
-            self._prune.run_physical(k, arena, units, g)
+            if self.prune_fusion.plan is not None and self.prune_fusion.plan.fused:
+                self._merge_prune(arena, stream)  # build_prune_merge_phase (phases.py:2447-2469)
+            else:
+                self._prune.run_physical(k, arena, units, g)
             if timer is not None:
                 timer.end("prune_conn")
             arena.dead_in_rows = True
@@ -350,6 +371,103 @@ class StepFn:
             state.grown, state.overflow = out.grown, out.overflow
             state.needs_resort = bool(state.needs_resort) or out.needs_resort
             state.tail_start = out.tail_start
+
+    # -- fused forward + prune (phases.py:1629-1848, :2322-2469) ---------------
+    def _fusion_plan(self, g: Any) -> PruneFusionPlan:
+        rec = self.prune_fusion
+        if rec.plan is None:
+            if self.plan.net.prune_conn is None:
+                rec.plan = PruneFusionPlan(False, "no prune_conn")
+            elif rec.requested == "off":
+                rec.plan = PruneFusionPlan(False, "fuse_prune='off'")
+            else:
+                rec.plan = plan_prune_fusion(self.plan.net, self.static, g, engine=rec.requested)
+        return rec.plan
+
+    def _fused_prune_progs(self, arena: Arena, units: dict, fin_common: dict, g: Any,
+                           stream: int) -> list[torch.Tensor]:
+        """The predicate's site program per bucket, in device memory, over
+        the units the predicate sees (forwarded fields at their post-forward
+        values); allocates the arena's sink column on first use."""
+        from plastax_amd import grow
+
+        if self._prune is None:
+            self._prune = grow.PruneConnPhase(self.plan.net, self.static, g)
+        if getattr(arena, "prune_sink", None) is None:
+            arena.prune_sink = torch.zeros(arena.cols["dead"].numel(), dtype=torch.uint8, device=arena.device)
+        pred_units = dict(units)
+        names = self.prune_fusion.plan.forwarded
+        if names:
+            pred_units.update(self._forwarded(arena, units, fin_common, names, g, stream))
+        self._pred_units = pred_units
+        progs = []
+        for b in range(arena.num_buckets):
+            base, cap = arena.bases[b], arena.caps[b]
+            view = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            p = grow.fill_prog(self._prune.prog, pred_units, view, g, physical_ids=True)
+            raw = bytes(memoryview(p).cast("B"))
+            progs.append(torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(arena.device, non_blocking=False))
+        return progs
+
+    def _forwarded(self, arena: Arena, units: dict, fin_common: dict, names: tuple[str, ...], g: Any,
+                   stream: int) -> dict[str, torch.Tensor]:
+        """Post-forward values of the forwarded unit fields: the forward's
+        apply from the identity accumulator on every unit the forward
+        finalizes, the column's value elsewhere (phases.py:2367-2388)."""
+        lib = _lib.load()
+        fp = self.plan.forward
+        n = self.static.num_units
+        outs = {name: units[name].clone() for name in fp.program.out_fields if name is not None}
+        prog = program_struct(fp.program, units, g, out_override=outs)
+        if arena.pipeline:
+            passes = [(torch.arange(n, dtype=torch.int32, device=arena.device), n, -1)]
+        else:
+            passes = [(arena.fwd[b].rows, arena.fwd[b].nrows, b + 1) for b in range(arena.num_buckets)]
+        for rows, nrows, level in passes:
+            if nrows == 0:
+                continue
+            parts = torch.arange(0, nrows + 256, 256, dtype=torch.int32, device=arena.device).clamp_(max=nrows)
+            d = _lib.plx_partials_desc()
+            d.nrows, d.monoid = nrows, fp.monoid
+            d.nparts = -(-nrows // 256)
+            d.part_rows = parts.data_ptr()
+            d.row_unit = rows.data_ptr()
+            d.fin.level, d.fin.is_input, d.fin.pruned = fin_common["level"], fin_common["is_input"], \
+                fin_common["pruned"]
+            d.fin.fin_level, d.fin.skip_inputs = level, 1
+            d.apply = prog
+            _lib.check(lib.plx_backward_partials(d, stream), "plx_backward_partials")
+        return {name: outs[name] for name in names}
+
+    def _xla_prune(self, arena: Arena, g: Any, stream: int) -> None:
+        """The "xla" engine: the predicate pass at the forward's slot, into
+        the sink (two reads of the edge columns, one phase)."""
+        from plastax_amd import grow
+
+        k = grow.Kernels(arena.device, stream)
+        arena.prune_sink.zero_()
+        n_units = self.static.num_units
+        for b in range(arena.num_buckets):
+            base, cap = arena.bases[b], arena.caps[b]
+            if cap == 0:
+                continue
+            view = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            k.site_eval(self._prune.prog, self._pred_units, g, n=cap, kind=5, num_units=n_units, conns=view,
+                        or_into=arena.prune_sink[base : base + cap], site_ids=arena.slot[base : base + cap],
+                        ids_logical=arena.uperm32, ids_physical=arena.uinv32)
+
+    def _merge_prune(self, arena: Arena, stream: int) -> None:
+        """Commit the fused forward's tombstones (phases.py:2447-2469)."""
+        lib = _lib.load()
+        sink, dead = arena.prune_sink, arena.cols["dead"]
+        for b in range(arena.num_buckets):
+            base, cap = arena.bases[b], arena.caps[b]
+            if cap == 0:
+                continue
+            stamp, value = arena.stamp_target(b)
+            _lib.check(lib.plx_merge_kills(cap, sink[base:].data_ptr(), dead[base:].data_ptr(),
+                                           None if stamp is None else stamp.data_ptr(), float(value), stream),
+                       "plx_merge_kills")
 
     # -- phases -----------------------------------------------------------------
     @staticmethod
