@@ -444,9 +444,9 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
 /* sizeof of the descriptor structs, in the order plx_program, plx_finalize,
  * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc,
  * plx_site_prog, plx_site_desc, plx_sort_key, plx_sort_desc,
- * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc, plx_unit_col (for
- * binding layers to check their mirrors). Writes min(n, 14) values and
- * returns 14. */
+ * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc, plx_unit_col,
+ * plx_bwd_batch_desc, plx_batch_tiles, plx_tile_build_desc (for binding
+ * layers to check their mirrors). Writes min(n, 17) values and returns 17. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
 
 /* ========================================================================
@@ -856,6 +856,61 @@ PLX_EXPORT int plx_mask_importance(int32_t n, const float* imp, const int32_t* l
                                    int32_t gap, int32_t direction, float* out, void* stream);
 
 PLX_EXPORT const char* plx_last_error(void);
+/* The tiled arena's backward tables on the device (the host build is
+ * plastax_amd/_layout.py; the reference's arena has no transpose tables, its
+ * resort being topo.py:303-452). One workgroup per tile sorts the tile's live
+ * positions by (physical source, position) in LDS. Positions are relative to
+ * the bucket; the first `live` hold its live edges, destination-sorted, with
+ * physical FROM_ID src[p]; tile t is [tile_pos[t], tile_pos[t+1]).
+ *   pass 0: ngroups[t] = the tile's (tile, source) groups; presence[u] +=
+ *           the tiles holding source u (presence zeroed by the caller).
+ *   pass 1: sorted_rank[p] = rank of p in its tile's order | 0x8000 where the
+ *           rank starts a group (positions past `live` are not written);
+ *           per group, in (tile, source) order from grp_off[t]: g_src, g_st
+ *           (first rank), g_tile; grp[grp_off[t]..] the tile's descriptors
+ *           (first rank | min(length, 15) << 12), longest first, ties in
+ *           source order; hl[2t] / hl[2t+1] the ranks of sources below
+ *           hot_base / in [hot_base, hot_base + nhot); cnt[8t + x] the tile's
+ *           other ranks whose source's finalize row is in region x
+ *           (region[u], 0..7). */
+typedef struct plx_tile_build_desc {
+  int32_t ntiles;
+  int32_t live;
+  int32_t pass;
+  int32_t hot_base;
+  int32_t nhot;
+  int32_t reserved;
+  const int32_t* tile_pos;
+  const int32_t* src;
+  int32_t* ngroups;
+  int32_t* presence;
+  const int32_t* grp_off;
+  const int8_t* region;
+  uint16_t* sorted_rank;
+  uint16_t* grp;
+  int32_t* g_src;
+  int32_t* g_st;
+  int32_t* g_tile;
+  int32_t* hl;
+  int32_t* cnt;
+} plx_tile_build_desc;
+
+PLX_EXPORT int plx_tile_build(const plx_tile_build_desc* d, void* stream);
+
+/* The cold slots of the tiled backward, for the cold groups cold[k] (group
+ * indices of plx_tile_build's lists, ordered by (source, tile); count n_dev
+ * or n): cold_idx[k] = off[8 t + region[src]] + c, c the group's first rank
+ * less the tile's hot ranks before it; cold_sb[k] = sb_of_tile[t]. */
+PLX_EXPORT int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const int32_t* g_src,
+                              const int32_t* g_st, const int32_t* g_tile, const int32_t* hl, const int32_t* off,
+                              const int8_t* region, const int32_t* sb_of_tile, int32_t* cold_idx,
+                              uint16_t* cold_sb, void* stream);
+
+/* counts[ids[p]] += 1 over n positions, skipping p where skip[p] (optional)
+ * and ids outside [0, nbins) (integer atomics: the counts are exact). */
+PLX_EXPORT int plx_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts,
+                             void* stream);
+
 PLX_EXPORT int32_t plx_abi_version(void);
 
 #ifdef __cplusplus

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 16  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 17  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -271,6 +271,30 @@ class plx_site_desc(ctypes.Structure):
     ]
 
 
+class plx_tile_build_desc(ctypes.Structure):
+    _fields_ = [
+        ("ntiles", c_i32),
+        ("live", c_i32),
+        ("pass_", c_i32),
+        ("hot_base", c_i32),
+        ("nhot", c_i32),
+        ("reserved", c_i32),
+        ("tile_pos", c_vp),
+        ("src", c_vp),
+        ("ngroups", c_vp),
+        ("presence", c_vp),
+        ("grp_off", c_vp),
+        ("region", c_vp),
+        ("sorted_rank", c_vp),
+        ("grp", c_vp),
+        ("g_src", c_vp),
+        ("g_st", c_vp),
+        ("g_tile", c_vp),
+        ("hl", c_vp),
+        ("cnt", c_vp),
+    ]
+
+
 class plx_sort_key(ctypes.Structure):
     _fields_ = [("kind", c_i32), ("bits", c_i32), ("bound", c_i32), ("reserved", c_i32), ("a", c_vp), ("b", c_vp)]
 
@@ -422,6 +446,9 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "plx_tile_build": (c_i32, [ctypes.POINTER(plx_tile_build_desc), c_vp]),
+    "plx_cold_slots": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "plx_count_ids": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
@@ -448,6 +475,7 @@ STRUCTS = (
     plx_unit_col,
     plx_bwd_batch_desc,
     plx_batch_tiles,
+    plx_tile_build_desc,
 )
 
 _lib: ctypes.CDLL | None = None

@@ -24,7 +24,7 @@ PKG = pathlib.Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libplastax_hip.so"
-SOURCES = ("plastax_hip.hip", "structural.hip")
+SOURCES = ("plastax_hip.hip", "structural.hip", "layout.hip")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -1,0 +1,252 @@
+// layout.hip -- the tiled arena's backward tables built on the device.
+//
+// The physical arena (dst-sorted slabs, units renumbered busiest source
+// first) is laid out with the structural entry points (compaction, stable
+// radix sort, gathers); these kernels add what the tiled backward needs per
+// bucket: every tile's (source, position) order, its (tile, source) groups
+// and their descriptors, the hot ranks and the cold slots' region counts.
+// One workgroup per tile sorts the tile's keys in LDS, so the whole
+// transpose costs two passes over FROM_ID instead of a global sort by
+// (tile, source). The tables equal the host build's (plastax_amd/_layout.py)
+// entry for entry.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/plastax_hip.h"
+#include "px_common.h"
+
+using plx_detail::check_launch;
+using plx_detail::fail;
+
+namespace {
+
+constexpr int kTB = 512;          // threads per tile workgroup
+constexpr int kTileMax = 4096;    // positions per tile at most
+constexpr int kPerT = kTileMax / kTB;
+constexpr uint32_t kStart = 0x8000u;
+
+// Sorts keys[0, kTileMax) ascending (bitonic; every thread takes part).
+__device__ void bitonic4096(uint32_t* keys) {
+  for (int k = 2; k <= kTileMax; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < kTileMax; i += kTB) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint32_t a = keys[i], b = keys[ixj];
+          const bool up = (i & k) == 0;
+          if ((a > b) == up) {
+            keys[i] = b;
+            keys[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Exclusive scan of one int per thread over the workgroup (wave prefix
+// sums, then the waves' totals); *total gets the sum.
+__device__ int block_scan(int v, int* lds, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) lds[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < kTB / 64; ++w) {
+      const int t = lds[w];
+      lds[w] = run;
+      run += t;
+    }
+    lds[kTB / 64] = run;
+  }
+  __syncthreads();
+  const int out = lds[wave] + x - v;
+  *total = lds[kTB / 64];
+  __syncthreads();
+  return out;
+}
+
+// The tile's live positions' keys (source << 12 | position in the tile),
+// sorted; n = their number.
+__device__ int load_sorted(const plx_tile_build_desc& d, int t, uint32_t* keys) {
+  const int p0 = d.tile_pos[t];
+  const int n = max(0, min(d.tile_pos[t + 1], d.live) - p0);
+  for (int i = threadIdx.x; i < kTileMax; i += kTB)
+    keys[i] = i < n ? (static_cast<uint32_t>(d.src[p0 + i]) << 12) | static_cast<uint32_t>(i) : 0xFFFFFFFFu;
+  __syncthreads();
+  bitonic4096(keys);
+  return n;
+}
+
+// Pass 0: groups per tile, and every group's source counted in presence.
+__global__ __launch_bounds__(kTB) void k_tile_count(plx_tile_build_desc d) {
+  __shared__ uint32_t keys[kTileMax];
+  __shared__ int scan_lds[kTB / 64 + 1];
+  const int t = blockIdx.x;
+  const int n = load_sorted(d, t, keys);
+  int mine = 0;
+  for (int k = 0; k < kPerT; ++k) {
+    const int i = threadIdx.x * kPerT + k;
+    if (i < n && (i == 0 || (keys[i] >> 12) != (keys[i - 1] >> 12))) {
+      ++mine;
+      atomicAdd(d.presence + (keys[i] >> 12), 1);
+    }
+  }
+  int total = 0;
+  block_scan(mine, scan_lds, &total);
+  if (threadIdx.x == 0) d.ngroups[t] = total;
+}
+
+// Pass 1: the tile's tables.
+__global__ __launch_bounds__(kTB) void k_tile_tables(plx_tile_build_desc d) {
+  __shared__ uint32_t keys[kTileMax];
+  __shared__ uint32_t gkey[kTileMax];
+  __shared__ int gstart[kTileMax + 1];
+  __shared__ int scan_lds[kTB / 64 + 1];
+  __shared__ int counts[2 + 8];
+  const int t = blockIdx.x;
+  const int p0 = d.tile_pos[t];
+  const int n = load_sorted(d, t, keys);
+  const uint32_t hb = static_cast<uint32_t>(d.hot_base), he = hb + static_cast<uint32_t>(d.nhot);
+  if (threadIdx.x < 10) counts[threadIdx.x] = 0;
+  // Group starts of this thread's consecutive ranks, then their indices.
+  bool st[kPerT];
+  int mine = 0;
+  for (int k = 0; k < kPerT; ++k) {
+    const int i = threadIdx.x * kPerT + k;
+    st[k] = i < n && (i == 0 || (keys[i] >> 12) != (keys[i - 1] >> 12));
+    mine += st[k];
+  }
+  int ng = 0;
+  int g = block_scan(mine, scan_lds, &ng);
+  int hlo = 0, hcnt = 0;
+  int rc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int k = 0; k < kPerT; ++k) {
+    const int i = threadIdx.x * kPerT + k;
+    if (i >= n) break;
+    const uint32_t src = keys[i] >> 12;
+    const int pos = p0 + static_cast<int>(keys[i] & 0xFFFu);
+    d.sorted_rank[pos] = static_cast<uint16_t>(static_cast<uint32_t>(i) | (st[k] ? kStart : 0u));
+    if (st[k]) gstart[g++] = i;
+    if (src < hb)
+      ++hlo;
+    else if (src < he)
+      ++hcnt;
+    if (src < hb || src >= he) ++rc[d.region[src] & 7];
+  }
+  if (threadIdx.x == 0) gstart[ng] = n;
+  atomicAdd(&counts[0], hlo);
+  atomicAdd(&counts[1], hcnt);
+  for (int x = 0; x < 8; ++x)
+    if (rc[x]) atomicAdd(&counts[2 + x], rc[x]);
+  __syncthreads();
+  // Groups in source order: their source, first rank and tile; and the
+  // descriptor keys (longest first, then source order).
+  const int g0 = d.grp_off[t];
+  for (int q = threadIdx.x; q < kTileMax; q += kTB) {
+    if (q < ng) {
+      const int s0 = gstart[q], len = gstart[q + 1] - s0;
+      d.g_src[g0 + q] = static_cast<int32_t>(keys[s0] >> 12);
+      d.g_st[g0 + q] = s0;
+      d.g_tile[g0 + q] = t;
+      gkey[q] = (static_cast<uint32_t>(kTileMax - len) << 12) | static_cast<uint32_t>(q);
+    } else {
+      gkey[q] = 0xFFFFFFFFu;
+    }
+  }
+  __syncthreads();
+  bitonic4096(gkey);
+  for (int q = threadIdx.x; q < ng; q += kTB) {
+    const int gi = static_cast<int>(gkey[q] & 0xFFFu);
+    const int s0 = gstart[gi], len = gstart[gi + 1] - s0;
+    d.grp[g0 + q] = static_cast<uint16_t>(static_cast<uint32_t>(s0) | (static_cast<uint32_t>(min(len, 15)) << 12));
+  }
+  if (threadIdx.x < 2) d.hl[2 * t + threadIdx.x] = counts[threadIdx.x];
+  if (threadIdx.x < 8) d.cnt[8 * t + threadIdx.x] = counts[2 + threadIdx.x];
+}
+
+__global__ void k_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const int32_t* g_src,
+                             const int32_t* g_st, const int32_t* g_tile, const int32_t* hl, const int32_t* off,
+                             const int8_t* region, const int32_t* sb_of_tile, int32_t* cold_idx,
+                             uint16_t* cold_sb) {
+  const int64_t m = n_dev ? *n_dev : n;
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k < m;
+       k += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t g = cold[k];
+    const int32_t t = g_tile[g], s0 = g_st[g];
+    const int32_t hlo = hl[2 * t], hcnt = hl[2 * t + 1];
+    const int32_t c = s0 >= hlo + hcnt ? s0 - hcnt : s0;
+    cold_idx[k] = off[8 * t + (region[g_src[g]] & 7)] + c;
+    cold_sb[k] = static_cast<uint16_t>(sb_of_tile[t]);
+  }
+}
+
+__global__ void k_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (skip && skip[p]) continue;
+    const int32_t u = ids[p];
+    if (u >= 0 && u < nbins) atomicAdd(counts + u, 1);
+  }
+}
+
+unsigned grid_of(int64_t n, int block) {
+  const int64_t g = (n + block - 1) / block;
+  return static_cast<unsigned>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+}  // namespace
+
+extern "C" {
+
+int plx_tile_build(const plx_tile_build_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_tile_build: null descriptor");
+  if (d->ntiles < 0 || d->live < 0) return fail(PLX_ERR_INVALID, "plx_tile_build: negative sizes");
+  if (d->ntiles == 0) return PLX_OK;
+  if (!d->tile_pos || (d->live > 0 && !d->src)) return fail(PLX_ERR_INVALID, "plx_tile_build: null column");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->pass == 0) {
+    if (!d->ngroups || !d->presence) return fail(PLX_ERR_INVALID, "plx_tile_build: pass 0 outputs missing");
+    hipLaunchKernelGGL(k_tile_count, dim3(d->ntiles), dim3(kTB), 0, s, *d);
+  } else if (d->pass == 1) {
+    if (!d->grp_off || !d->region || !d->sorted_rank || !d->grp || !d->g_src || !d->g_st || !d->g_tile || !d->hl ||
+        !d->cnt)
+      return fail(PLX_ERR_INVALID, "plx_tile_build: pass 1 tables missing");
+    if (d->nhot < 0 || d->hot_base < 0) return fail(PLX_ERR_INVALID, "plx_tile_build: bad hot range");
+    hipLaunchKernelGGL(k_tile_tables, dim3(d->ntiles), dim3(kTB), 0, s, *d);
+  } else {
+    return fail(PLX_ERR_INVALID, "plx_tile_build: pass must be 0 or 1");
+  }
+  return check_launch("plx_tile_build");
+}
+
+int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const int32_t* g_src, const int32_t* g_st,
+                   const int32_t* g_tile, const int32_t* hl, const int32_t* off, const int8_t* region,
+                   const int32_t* sb_of_tile, int32_t* cold_idx, uint16_t* cold_sb, void* stream) {
+  if (n < 0) return fail(PLX_ERR_INVALID, "plx_cold_slots: negative n");
+  if (n == 0) return PLX_OK;
+  if (!cold || !g_src || !g_st || !g_tile || !hl || !off || !region || !sb_of_tile || !cold_idx || !cold_sb)
+    return fail(PLX_ERR_INVALID, "plx_cold_slots: null pointer");
+  hipLaunchKernelGGL(k_cold_slots, dim3(grid_of(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream), n, n_dev,
+                     cold, g_src, g_st, g_tile, hl, off, region, sb_of_tile, cold_idx, cold_sb);
+  return check_launch("plx_cold_slots");
+}
+
+int plx_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts, void* stream) {
+  if (n < 0 || nbins < 0) return fail(PLX_ERR_INVALID, "plx_count_ids: negative size");
+  if (n == 0) return PLX_OK;
+  if (!ids || !counts) return fail(PLX_ERR_INVALID, "plx_count_ids: null pointer");
+  hipLaunchKernelGGL(k_count_ids, dim3(grid_of(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream), n, ids, skip,
+                     nbins, counts);
+  return check_launch("plx_count_ids");
+}
+
+}  // extern "C"

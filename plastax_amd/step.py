@@ -113,6 +113,9 @@ class StepFn:
         # change; the backward folds each source's edges in slot order), or
         # "auto": churn when growth fires every step.
         self.arena_mode: str = "auto"
+        # Where the tiled layout is built: "device" (plastax_amd._layout_dev)
+        # or "host" (plastax_amd._layout, numpy); the tables are equal.
+        self.layout_build: str = "device"
         # Unit and structural phases, traced on the first step (their
         # programs read the globals' structure).
         self._update_unit: Any = None
@@ -175,11 +178,18 @@ class StepFn:
 
                 state._arena = ChurnArena(self.static, state.units, state._conns, state.device,
                                           _stream(state.device))
-            else:
+            elif self.layout_build == "device":
+                from plastax_amd._layout_dev import DeviceArena
+
+                state._arena = DeviceArena(self.static, state.units, state._conns, state.device,
+                                           _stream(state.device), tile=self.tile, nsuper=self.nsuper)
+            elif self.layout_build == "host":
                 state._arena = Arena(
                     self.static, state.units, state._conns, state.device, tile=self.tile,
                     nsuper=self.nsuper,
                 )
+            else:
+                raise ValueError(f"layout_build must be 'device' or 'host', got {self.layout_build!r}")
             up = self.plan.update
             if up is not None and up.rule_code == 2:
                 state._arena.init_uniform_t(up.state_columns()[2])
