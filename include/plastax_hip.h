@@ -373,6 +373,11 @@ typedef struct plx_batch_tiles {
   const uint16_t* loc;      /* [entries] */
 } plx_batch_tiles;
 
+/* The tile limits plx_update_batch_tiles is built with: units per tile side
+ * (loc's fields index [0, *rows)) and edges per tile (entries beyond are not
+ * updated). Table builders check theirs against these. */
+PLX_EXPORT int plx_batch_tile_limits(int32_t* rows, int32_t* edges);
+
 PLX_EXPORT int plx_update_batch_tiles(const plx_update_desc* d, const plx_batch_tiles* t, int32_t batch,
                                       void* stream);
 

@@ -128,6 +128,11 @@ def batch_tiles(src: np.ndarray, dst: np.ndarray) -> dict[str, np.ndarray]:
     first = order[tile_off[:-1]]
     tile_base = np.stack([(dst[first] // u) * u, (src[first] // u) * u], axis=1).reshape(-1)
     loc = ((dst[order] % u) | ((src[order] % u) << 8)).astype(np.uint16)
+    sizes = np.diff(tile_off)
+    if sizes.size and int(sizes.max()) > BATCH_TILE_EDGES:
+        raise ValueError("batch_tiles: a tile holds more than BATCH_TILE_EDGES edges")
+    if n and (int((loc & 0xFF).max()) >= u or int((loc >> 8).max()) >= u):
+        raise ValueError("batch_tiles: a unit offset falls outside its tile")
     return {"tile_off": tile_off, "tile_base": tile_base, "pos": order.astype(np.int64), "loc": loc}
 
 

@@ -449,6 +449,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_tile_build": (c_i32, [ctypes.POINTER(plx_tile_build_desc), c_vp]),
     "plx_cold_slots": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_count_ids": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "plx_batch_tile_limits": (c_i32, [c_vp, c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,

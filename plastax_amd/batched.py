@@ -27,6 +27,7 @@ workgroup. Summation orders, per sample:
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any
 
 import numpy as np
@@ -394,6 +395,14 @@ class BatchedStepFn(StepFn):
         grouped by 64 destination x 64 source units, so a workgroup stages
         their unit rows in LDS."""
         cache = arena.__dict__.setdefault("_batch_tiles", {})
+        if not cache:
+            rows, edges = ctypes.c_int32(), ctypes.c_int32()
+            _lib.check(_lib.load().plx_batch_tile_limits(ctypes.byref(rows), ctypes.byref(edges)),
+                       "plx_batch_tile_limits")
+            if (rows.value, edges.value) != (_layout.BATCH_TILE_UNITS, _layout.BATCH_TILE_EDGES):
+                raise RuntimeError(
+                    f"the library's batched-update tiles are {rows.value} units / {edges.value} edges, "
+                    f"the layout builds {_layout.BATCH_TILE_UNITS} / {_layout.BATCH_TILE_EDGES}: rebuild it")
         if b not in cache:
             base, live = arena.bases[b], arena.lives[b]
             src = arena.cols["from_id"][base : base + live].cpu().numpy()

@@ -1593,6 +1593,8 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch(plx_update_desc d,
 #define PLX_BATCH_TILE_ROWS 64
 #endif
 constexpr int kTileRows = PLX_BATCH_TILE_ROWS;
+static_assert(kTileRows > 0 && kTileRows <= 256 && (kTileRows & (kTileRows - 1)) == 0,
+              "batched-update tile rows: a power of two that fits loc's 8-bit fields");
 constexpr int kTileChunk = 64;
 constexpr int kTileStride = kTileChunk + 4;  // 16-byte aligned rows, offset by 4 banks each
 constexpr int kTileEdgesPer = 4;
@@ -1620,8 +1622,9 @@ __global__ __launch_bounds__(kBatchBlock) void k_update_batch_tiles(plx_update_d
     if (use[i]) {
       pe[i] = t.pos[j];
       const uint32_t l = t.loc[j];
-      ld[i] = static_cast<int>(l & 0xFFu);
-      ls[i] = static_cast<int>(l >> 8);
+      // (masked to the tile: an entry outside it cannot reach past the LDS rows)
+      ld[i] = static_cast<int>(l & 0xFFu) & (kTileRows - 1);
+      ls[i] = static_cast<int>(l >> 8) & (kTileRows - 1);
       use[i] = d.dead ? d.dead[pe[i]] == 0 : pe[i] < d.live_end;
     }
   }
@@ -2351,6 +2354,13 @@ int plx_update_batch(const plx_update_desc* d, int32_t batch, void* stream) {
     default: return fail(PLX_ERR_UNSUPPORTED, "plx_update_batch: unknown rule");
   }
   return check_launch("plx_update_batch");
+}
+
+int plx_batch_tile_limits(int32_t* rows, int32_t* edges) {
+  if (!rows || !edges) return fail(PLX_ERR_INVALID, "plx_batch_tile_limits: null pointer");
+  *rows = kTileRows;
+  *edges = kTileEdges;
+  return PLX_OK;
 }
 
 int plx_update_batch_tiles(const plx_update_desc* d, const plx_batch_tiles* t, int32_t batch,

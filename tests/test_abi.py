@@ -96,3 +96,14 @@ def test_argument_errors_are_reported_not_raised(lib) -> None:
     assert lib.plx_reduce_batch(4, 2, 1, 2, None, None, None) == 1
     assert b"FIRST only" in lib.plx_last_error()
     assert lib.plx_batch_mean(0, None, None, None) == 1
+
+
+def test_batch_tile_limits_match_the_layout(lib) -> None:
+    """The batched-update kernel's tile limits, queried through the ABI,
+    are the ones plastax_amd._layout.batch_tiles builds for."""
+    from plastax_amd import _layout
+
+    rows, edges = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.plx_batch_tile_limits(ctypes.byref(rows), ctypes.byref(edges)) == 0
+    assert (rows.value, edges.value) == (_layout.BATCH_TILE_UNITS, _layout.BATCH_TILE_EDGES)
+    assert lib.plx_batch_tile_limits(None, None) != 0

@@ -378,3 +378,20 @@ def test_batch_tiles_cover_every_live_edge_once() -> None:
         assert (np.diff(p) > 0).all()
         assert (base[k, 0] + (loc[off[k] : off[k + 1]] & 0xFF) == dst[p]).all()
         assert (base[k, 1] + (loc[off[k] : off[k + 1]] >> 8) == src[p]).all()
+
+
+def test_batch_tiles_reject_tables_the_kernel_cannot_take() -> None:
+    """batch_tiles validates its own output against the kernel's limits
+    (plx_batch_tile_limits); a forged oversize tile is refused."""
+    from plastax_amd import _layout
+
+    rng = np.random.default_rng(1)
+    src = rng.integers(0, 300, 5000)
+    dst = rng.integers(300, 600, 5000)
+    tb = _layout.batch_tiles(src, dst)
+    assert int(np.diff(tb["tile_off"]).max()) <= _layout.BATCH_TILE_EDGES
+    assert int((tb["loc"] & 0xFF).max()) < _layout.BATCH_TILE_UNITS
+    # every edge of one (dst block, src block) pair: more than one tile's worth
+    many = np.zeros(3 * _layout.BATCH_TILE_EDGES, np.int64)
+    tb = _layout.batch_tiles(many, many + 1)
+    assert np.diff(tb["tile_off"]).tolist() == [_layout.BATCH_TILE_EDGES] * 3
