@@ -72,6 +72,17 @@ def test_c3_shaped_softmax_batch(oracle) -> None:
     _run(oracle, bc.softmax_net(opt), [784, 128, 128, 10], 0.1, 0.0, 256, 2, seed=4, onehot=True)
 
 
+@pytest.mark.parametrize("B", [64, 256])
+def test_long_rows_cross_the_staged_chunks(oracle, B: int) -> None:
+    """Few rows with thousands of in- and out-edges (3,000 -> 6 -> 4 at 60 %
+    keep: ~1,800 in-edges per hidden row, ~3,600 edges per output's backward
+    row set): the workgroup-per-row kernels stage a row's positions in LDS
+    1,024 at a time, so each row's fold crosses chunk boundaries; with
+    skip edges and dead slots from the builder's headroom."""
+    opt = px.optim.adam(1e-2, nets.GRAD_PRE_ACT)
+    _run(oracle, bc.tanh_mse_net(opt), [3000, 6, 4], 0.6, 0.05, B, 2, seed=9, headroom=0.25)
+
+
 @pytest.mark.parametrize("B", [256, 132])
 def test_wide_levels_run_the_one_wave_row_kernels(oracle, B: int) -> None:
     """Levels of 512 rows at a batch that is a multiple of 4 and >= 128: the
