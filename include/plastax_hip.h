@@ -450,8 +450,9 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
  * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc,
  * plx_site_prog, plx_site_desc, plx_sort_key, plx_sort_desc,
  * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc, plx_unit_col,
- * plx_bwd_batch_desc, plx_batch_tiles, plx_tile_build_desc (for binding
- * layers to check their mirrors). Writes min(n, 17) values and returns 17. */
+ * plx_bwd_batch_desc, plx_batch_tiles, plx_tile_build_desc, plx_gen_fold_desc
+ * (for binding layers to check their mirrors). Writes min(n, 18) values and
+ * returns 18. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
 
 /* ========================================================================
@@ -545,6 +546,41 @@ typedef struct plx_site_desc {
 } plx_site_desc;
 
 PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
+
+/* One bucket of a generic pass (a map outside the product form, one float32
+ * component or a tuple with a tuple of monoids: sweep.py:113-180 / :343-399
+ * with any `map` and `combine`): for every row r (one thread each), unit u =
+ * row_unit[r], its entries j in [row_ptr[r], row_ptr[r+1]) in order, each at
+ * physical position p = entry_pos ? entry_pos[j] : j, skipped where dead[p]
+ * (dead optional): the map program (`prog`, ncomp float32 outputs) runs as
+ * the PLX_SITES_EDGE site s = p - base (its connection columns start at
+ * base) with cid slot[s] and the unit ids seen through ids_logical (unit
+ * reads through ids_physical); a forward row binds dst = u and src =
+ * from_id[p], a backward row (backward != 0) src = u and dst = to_id[p].
+ * Component k folds in entry order from identity[k] with monoid[k]
+ * (PLX_MONOID_*), then acc[k][u] = monoid[k](acc[k][u], fold). */
+typedef struct plx_gen_fold_desc {
+  plx_site_prog prog;
+  int32_t nrows;
+  int32_t ncomp;
+  int32_t backward;
+  int32_t num_units;
+  int32_t monoid[8];
+  float identity[8];
+  const int32_t* row_unit;
+  const int32_t* row_ptr;
+  const int32_t* entry_pos;
+  const int32_t* from_id;
+  const int32_t* to_id;
+  const uint8_t* dead;
+  int64_t base;
+  const int32_t* slot;
+  const int32_t* ids_logical;
+  const int32_t* ids_physical;
+  float* acc[8];
+} plx_gen_fold_desc;
+
+PLX_EXPORT int plx_gen_fold(const plx_gen_fold_desc* d, void* stream);
 
 /* The mean-of-writes connection update of a batched step with a user
  * UpdateConn (phases.py:484-533), one float32 column at a time over n

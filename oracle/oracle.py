@@ -396,8 +396,117 @@ class OracleNet:
         return out
 
     # -- phases ---------------------------------------------------------------
+    # -- generic passes (plastax_amd/generic.py) -----------------------------
+    def _gen(self, which: str) -> tuple:
+        """(GenericPass, map program, apply program, apply's written fields)."""
+        key = "_gen_" + which
+        if getattr(self, key, None) is None:
+            from plastax_amd import _site
+
+            pp = self.plan.forward if which == "fwd" else self.plan.backward
+            gp = pp.generic
+            udt = {s.name: np.dtype(s.dtype) for s in self.static.unit_fields}
+            cdt = {s.name: np.dtype(s.dtype) for s in self.static.conn_fields}
+            mprog = _site.trace_pass_map(gp.policy, gp.backward, udt, cdt, self.globals_)
+            aprog, names = _site.trace_pass_apply(gp.policy, len(gp.monoids), gp.tuple_acc, udt, self.globals_)
+            setattr(self, key, (gp, mprog, aprog, names))
+        return getattr(self, key)
+
+    @staticmethod
+    def _gen_op(m: int, a: Any, b: Any) -> Any:
+        """A named monoid on float32 arrays, with the device's NaN and
+        tie rules (max / min keep the first operand only when it compares
+        strictly greater / less)."""
+        a = np.asarray(a, dtype=np.float32)
+        b = np.asarray(b, dtype=np.float32)
+        if m == 0:
+            return (a + b).astype(np.float32)
+        if m == 1:
+            return (a * b).astype(np.float32)
+        pick = (a > b) if m == 2 else (a < b)
+        return np.where(np.isnan(a), a, np.where(np.isnan(b), b, np.where(pick, a, b))).astype(np.float32)
+
+    def _gen_reduce(self, which: str, b: int) -> list[np.ndarray]:
+        """Per-unit folds of bucket b's live edges, each row's edges in slot
+        order from the identity (rows: destinations forward, sources
+        backward); the identity where a unit has none."""
+        from oracle import growth as og
+
+        gp, mprog, _, _ = self._gen(which)
+        n = self.static.num_units
+        c = self.conns[b]
+        cap = c["dead"].size
+        roles = {"cid": np.arange(cap, dtype=np.int32), "src": c["from_id"], "dst": c["to_id"]}
+        terms = og.site_eval(mprog, cap, roles, self.units, self.globals_, conns=c)
+        live = np.flatnonzero(~c["dead"].astype(bool))
+        key = c["from_id"] if gp.backward else c["to_id"]
+        order = live[np.argsort(key[live], kind="stable")]
+        rows = key[order]
+        outs = [np.full(n, v, dtype=np.float32) for v in gp.identities]
+        bounds = np.concatenate([[0], np.flatnonzero(np.diff(rows)) + 1, [rows.size]]) if rows.size else [0]
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            u = int(rows[lo])
+            for k, (m, ident) in enumerate(zip(gp.monoids, gp.identities)):
+                s = np.float32(ident)
+                for v in terms[k][order[lo:hi]]:
+                    s = self._gen_op(m, s, v)
+                outs[k][u] = s
+        return outs
+
+    def _gen_apply(self, which: str, acc: list[np.ndarray], mask: np.ndarray) -> None:
+        from oracle import growth as og
+        from plastax_amd import _site
+
+        gp, _, aprog, names = self._gen(which)
+        fin = np.flatnonzero(mask).astype(np.int32)
+        if fin.size and names:
+            units = dict(self.units)
+            units.update(dict(zip(_site.acc_field_names(len(acc)), acc)))
+            vals = og.site_eval(aprog, fin.size, {"i": fin}, units, self.globals_)
+            live = self._live()[fin]
+            for name, v in zip(names, vals):
+                col = self.units[name]
+                col[fin[live]] = np.asarray(v, dtype=col.dtype)[live]
+        for a, v in zip(acc, gp.identities):
+            a[fin] = np.float32(v)
+
+    def _gen_forward(self) -> None:
+        gp = self.plan.forward.generic
+        n = self.static.num_units
+        levels = self.units["level"]
+        live = np.ones(n, dtype=bool)  # pruned units are skipped by the apply's writes
+        acc = [np.full(n, v, dtype=np.float32) for v in gp.identities]
+        nb = len(self.conns)
+        for lv in range(nb):
+            out = self._gen_reduce("fwd", lv)
+            acc = [self._gen_op(m, a, o) for m, a, o in zip(gp.monoids, acc, out)]
+            if not self.pipeline:
+                self._gen_apply("fwd", acc, (levels == lv + 1) & ~self.is_input & live)
+        if self.pipeline:
+            self._gen_apply("fwd", acc, ~self.is_input & live)
+
+    def _gen_backward(self) -> None:
+        gp = self.plan.backward.generic
+        n = self.static.num_units
+        levels = self.units["level"]
+        acc = [np.full(n, v, dtype=np.float32) for v in gp.identities]
+        nb = len(self.conns)
+        if self.pipeline:
+            out = self._gen_reduce("bwd", 0)
+            acc = [self._gen_op(m, a, o) for m, a, o in zip(gp.monoids, acc, out)]
+            self._gen_apply("bwd", acc, np.ones(n, dtype=bool))
+            return
+        self._gen_apply("bwd", acc, (levels == nb) & ~self.is_input)
+        for lv in range(nb - 1, 0, -1):
+            out = self._gen_reduce("bwd", lv)
+            acc = [self._gen_op(m, a, o) for m, a, o in zip(gp.monoids, acc, out)]
+            self._gen_apply("bwd", acc, (levels == lv) & ~self.is_input)
+
     def forward(self) -> None:
         fp = self.plan.forward
+        if fp.generic is not None:
+            self._gen_forward()
+            return
         n = self.static.num_units
         levels = self.units["level"]
         live = self._live()
@@ -434,6 +543,9 @@ class OracleNet:
 
     def backward(self) -> None:
         bp = self.plan.backward
+        if bp.generic is not None:
+            self._gen_backward()
+            return
         n = self.static.num_units
         levels = self.units["level"]
         live = self._live()

@@ -72,6 +72,7 @@ class ChurnArena(Arena):
         self.uperm32 = self.uperm_t.to(torch.int32)
         self.uinv32 = self.uperm32
         levels = units["level"]
+        self.unit_levels = levels.cpu().numpy().astype(np.int64)
         self.lvl_start = np.zeros(1, np.int64)
         self.input_ids = self._i32(np.asarray(static.input_ids, dtype=np.int64))
         self.output_ids = self._i32(np.asarray(static.output_ids, dtype=np.int64))

@@ -275,6 +275,7 @@ class Arena:
         for name in (FROM_ID.name, TO_ID.name):
             host[name] = [self.uinv[np.clip(h, 0, n - 1)].astype(np.int32) for h in host[name]]
         levels = levels_l[self.uperm]
+        self.unit_levels = levels  # levels in the physical unit order
         is_input = np.zeros(n, dtype=bool)
         if static.input_ids:
             is_input[self.uinv[np.asarray(static.input_ids)]] = True

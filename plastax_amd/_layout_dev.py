@@ -97,6 +97,7 @@ class DeviceArena(Arena):
         self.uperm32 = self.uperm_t.to(torch.int32)
         self.uinv32 = self.uinv_t.to(torch.int32)
         levels = levels_l[self.uperm]
+        self.unit_levels = levels
         is_input = np.zeros(n, dtype=bool)
         if static.input_ids:
             is_input[self.uinv[np.asarray(static.input_ids)]] = True

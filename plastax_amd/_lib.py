@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 17  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 18  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -295,6 +295,29 @@ class plx_tile_build_desc(ctypes.Structure):
     ]
 
 
+class plx_gen_fold_desc(ctypes.Structure):
+    _fields_ = [
+        ("prog", plx_site_prog),
+        ("nrows", c_i32),
+        ("ncomp", c_i32),
+        ("backward", c_i32),
+        ("num_units", c_i32),
+        ("monoid", c_i32 * 8),
+        ("identity", ctypes.c_float * 8),
+        ("row_unit", c_vp),
+        ("row_ptr", c_vp),
+        ("entry_pos", c_vp),
+        ("from_id", c_vp),
+        ("to_id", c_vp),
+        ("dead", c_vp),
+        ("base", c_i64),
+        ("slot", c_vp),
+        ("ids_logical", c_vp),
+        ("ids_physical", c_vp),
+        ("acc", c_vp * 8),
+    ]
+
+
 class plx_sort_key(ctypes.Structure):
     _fields_ = [("kind", c_i32), ("bits", c_i32), ("bound", c_i32), ("reserved", c_i32), ("a", c_vp), ("b", c_vp)]
 
@@ -450,6 +473,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_cold_slots": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_count_ids": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_batch_tile_limits": (c_i32, [c_vp, c_vp]),
+    "plx_gen_fold": (c_i32, [ctypes.POINTER(plx_gen_fold_desc), c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
@@ -477,6 +501,7 @@ STRUCTS = (
     plx_bwd_batch_desc,
     plx_batch_tiles,
     plx_tile_build_desc,
+    plx_gen_fold_desc,
 )
 
 _lib: ctypes.CDLL | None = None

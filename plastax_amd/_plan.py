@@ -49,6 +49,21 @@ POW_TABLE_LEN = 1 << 16
 
 
 @dataclasses.dataclass
+class GenericPass:
+    """A pass outside the product form: any map (one float32 component, or a
+    tuple with a tuple of monoids), folded per row by the map's edge program
+    and applied by a unit program (traced on the step's first call, against
+    its globals)."""
+
+    policy: Any
+    backward: bool
+    monoids: tuple[int, ...]  # PLX_MONOID_* per component
+    identities: tuple[float, ...]
+    tuple_acc: bool
+    why: str  # why the product form did not apply
+
+
+@dataclasses.dataclass
 class PassPlan:
     """A traced forward or backward pass."""
 
@@ -58,6 +73,7 @@ class PassPlan:
     program: Program  # the apply
     w_const: np.float32 | None = None  # the map's connection factor, when not WEIGHT
     x_const: np.float32 | None = None  # the map's unit factor, when not a field
+    generic: GenericPass | None = None  # set: the pass runs as edge / unit programs
 
     def map_struct(self) -> "_lib.plx_map":
         """The plx_map of this pass's map."""
@@ -132,7 +148,37 @@ def _check_float_fields(names: list[str | None], dtypes: dict[str, np.dtype], wh
             raise UnsupportedPolicyError(f"{what} touches {name!r}, which is not float32")
 
 
+def _generic_pass(policy: Any, *, backward: bool, why: str) -> PassPlan:
+    """The plan of a pass whose map is not of the product form."""
+    name = type(policy).__name__
+    combine = policy.combine
+    monoids = combine if isinstance(combine, tuple) else (combine,)
+    if not monoids or not all(isinstance(m, Monoid) for m in monoids):
+        raise UnsupportedPolicyError(f"{name}.combine must be a named monoid or a tuple of them")
+    if len(monoids) > 8:
+        raise UnsupportedPolicyError(f"{name}: at most 8 accumulator components")
+    codes = tuple(m.code for m in monoids)
+    idents = tuple(float(m.identity_for()) for m in monoids)
+    gp = GenericPass(policy, backward, codes, idents, isinstance(combine, tuple), why)
+    empty = Program([], [], [], [], {})
+    return PassPlan(field=None, monoid=codes[0], identity=idents[0], program=empty, generic=gp)
+
+
 def _trace_pass(policy: Any, static: NetworkStatic, *, backward: bool) -> PassPlan:
+    if isinstance(policy.combine, tuple):
+        return _generic_pass(policy, backward=backward, why="a tuple accumulator")
+    try:
+        return _trace_product_pass(policy, static, backward=backward)
+    except _NotProductForm as exc:
+        return _generic_pass(policy, backward=backward, why=str(exc))
+
+
+class _NotProductForm(UnsupportedPolicyError):
+    """The map is outside the product form (the pass runs generic); other
+    refusals -- an apply the tracer cannot follow -- stand."""
+
+
+def _trace_product_pass(policy: Any, static: NetworkStatic, *, backward: bool) -> PassPlan:
     dtypes = _float_unit_fields(static)
     conn_dtypes = {s.name: np.dtype(s.dtype) for s in static.conn_fields}
     u = TraceUnitView(dtypes)
@@ -142,12 +188,15 @@ def _trace_pass(policy: Any, static: NetworkStatic, *, backward: bool) -> PassPl
     combine = policy.combine
     if not isinstance(combine, Monoid):
         raise UnsupportedPolicyError(f"{name}.combine must be a single named monoid")
-    if backward:
-        expr = policy.map(u, Index("src"), Index("dst"), c, Index("cid"), g)
-        pm = product_map(expr, "dst")
-    else:
-        expr = policy.map(u, Index("dst"), Index("src"), c, Index("cid"), g)
-        pm = product_map(expr, "src")
+    try:
+        if backward:
+            expr = policy.map(u, Index("src"), Index("dst"), c, Index("cid"), g)
+            pm = product_map(expr, "dst")
+        else:
+            expr = policy.map(u, Index("dst"), Index("src"), c, Index("cid"), g)
+            pm = product_map(expr, "src")
+    except UnsupportedPolicyError as exc:
+        raise _NotProductForm(str(exc)) from exc
     field = pm.field
     write = policy.apply(u, Index("self"), g, Expr("acc"))
     if not isinstance(write, UnitWrite):

@@ -585,3 +585,45 @@ def trace_unit_init(rule: Any, unit_dtypes: dict, g: Any) -> tuple[SiteProgram, 
     write = rule.init(SiteUnitView(unit_dtypes), idx("src"), idx("dst"), SiteGlobals(g))
     outs, names = _unit_outputs(write, unit_dtypes)
     return compile_site_program(outs, roles=("src", "dst")), names
+
+
+def trace_pass_map(policy: Any, backward: bool, unit_dtypes: dict, conn_dtypes: dict,
+                   g: Any) -> SiteProgram:
+    """A forward or backward pass's ``map`` outside the product form, as an
+    edge program with one float32 output per accumulator component
+    (sweep.py:113-180 / :343-399): forward ``map(u, dst, src, c, cid, g)``,
+    backward ``map(u, src, dst, c, cid, g)``; a tuple map is one output per
+    element."""
+    u, c, gv = SiteUnitView(unit_dtypes), SiteConnView(conn_dtypes), SiteGlobals(g)
+    if backward:
+        out = policy.map(u, idx("src"), idx("dst"), c, idx("cid"), gv)
+    else:
+        out = policy.map(u, idx("dst"), idx("src"), c, idx("cid"), gv)
+    comps = list(out) if isinstance(out, tuple) else [out]
+    outs = []
+    for k, e in enumerate(comps):
+        e = lift(e)
+        if e.dtype not in ("f", "wf"):
+            raise UnsupportedPolicyError(
+                f"{type(policy).__name__}.map: component {k} is not float32 (generic passes accumulate float32)")
+        outs.append((e, "f"))
+    return compile_site_program(outs, roles=("cid", "src", "dst"))
+
+
+def acc_field_names(k: int) -> list[str]:
+    """The unit columns a generic pass's apply reads its accumulator from."""
+    return [f"__acc{j}" for j in range(k)]
+
+
+def trace_pass_apply(policy: Any, ncomp: int, tuple_acc: bool, unit_dtypes: dict,
+                     g: Any) -> tuple[SiteProgram, list[str]]:
+    """A generic pass's ``apply(u, i, g, acc)`` -> UnitWrite as a unit
+    program; the accumulator (a tuple when ``tuple_acc``) is read from the
+    unit columns ``acc_field_names(ncomp)``."""
+    names = acc_field_names(ncomp)
+    acc_view = SiteUnitView({n: np.dtype(np.float32) for n in names})
+    comps = [acc_view[_Field(n), idx("i")] for n in names]
+    acc = tuple(comps) if tuple_acc else comps[0]
+    write = policy.apply(SiteUnitView(unit_dtypes), idx("i"), SiteGlobals(g), acc)
+    outs, written = _unit_outputs(write, unit_dtypes)
+    return compile_site_program(outs, roles=("i",)), written

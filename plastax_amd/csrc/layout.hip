@@ -189,12 +189,28 @@ __global__ void k_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* col
   }
 }
 
+// Runs of equal ids among a wave's consecutive lanes add once, from their
+// first lane (the logical buckets are source-major and the slabs
+// destination-sorted, so most ids repeat across neighbouring positions and
+// a plain per-position atomic would serialise on them).
 __global__ void k_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts) {
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
-       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    if (skip && skip[p]) continue;
-    const int32_t u = ids[p];
-    if (u >= 0 && u < nbins) atomicAdd(counts + u, 1);
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x; base < n; base += stride) {
+    const int64_t p = base + threadIdx.x;
+    int32_t u = -1;
+    if (p < n && !(skip && skip[p])) {
+      u = ids[p];
+      if (u < 0 || u >= nbins) u = -1;
+    }
+    const int32_t prev = __shfl_up(u, 1, 64);
+    const bool head = lane == 0 || prev != u;
+    const uint64_t heads = __ballot(head);
+    if (head && u >= 0) {
+      const uint64_t after = lane == 63 ? 0ull : (heads >> (lane + 1));
+      const int len = after ? __builtin_ctzll(after) + 1 : 64 - lane;
+      atomicAdd(counts + u, len);
+    }
   }
 }
 

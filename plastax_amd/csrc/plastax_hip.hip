@@ -1980,10 +1980,10 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 17; }
+int32_t plx_abi_version(void) { return 18; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[17] = {
+  const int64_t sizes[18] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
       sizeof(plx_partials_desc),    sizeof(plx_update_desc),
@@ -1992,9 +1992,9 @@ int plx_struct_sizes(int64_t* out, int32_t n) {
       sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
       sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col),
       sizeof(plx_bwd_batch_desc),   sizeof(plx_batch_tiles),
-      sizeof(plx_tile_build_desc)};
-  for (int32_t k = 0; k < n && k < 17; ++k) out[k] = sizes[k];
-  return 17;
+      sizeof(plx_tile_build_desc),  sizeof(plx_gen_fold_desc)};
+  for (int32_t k = 0; k < n && k < 18; ++k) out[k] = sizes[k];
+  return 18;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {

@@ -332,6 +332,53 @@ __global__ void k_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* 
   }
 }
 
+__device__ __forceinline__ float gen_op(int32_t m, float a, float b) {
+  switch (m) {
+    case PLX_MONOID_PROD: return a * b;
+    case PLX_MONOID_MAX: return fmax_nan(a, b);
+    case PLX_MONOID_MIN: return fmin_nan(a, b);
+    default: return a + b;
+  }
+}
+
+__global__ void k_gen_fold(plx_gen_fold_desc d) {
+  const uint32_t keyed = px::philox32(0, 1);  // the rng key of an unseeded step-0 site
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < d.nrows;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t u = d.row_unit[r];
+    float s[8];
+    for (int k = 0; k < 8; ++k) s[k] = d.identity[k];
+    const int32_t* lg = d.ids_logical;
+    const int32_t uu = lg ? lg[u] : u;
+    for (int32_t j = d.row_ptr[r]; j < d.row_ptr[r + 1]; ++j) {
+      const int64_t p = d.entry_pos ? d.entry_pos[j] : j;
+      if (d.dead && d.dead[p]) continue;
+      Site c;
+      c.role[0] = c.role[1] = 0;
+      if (d.backward) {
+        c.role[2] = uu;
+        c.role[3] = lg ? lg[d.to_id[p]] : d.to_id[p];
+      } else {
+        c.role[2] = lg ? lg[d.from_id[p]] : d.from_id[p];
+        c.role[3] = uu;
+      }
+      const int32_t site = static_cast<int32_t>(p - d.base);
+      c.role[4] = site;
+      c.cid_value = d.slot ? d.slot[site] : site;
+      c.seed = static_cast<uint64_t>(keyed) << 32;
+      c.ids_logical = d.ids_logical;
+      c.ids_physical = d.ids_physical;
+      c.batch = 1;
+      c.sample = 0;
+      uint32_t out[PLX_MAX_SOUTS];
+      for (int k = 0; k < PLX_MAX_SOUTS; ++k) out[k] = 0;
+      site_run(d.prog, c, d.num_units, out);
+      for (int k = 0; k < d.ncomp; ++k) s[k] = gen_op(d.monoid[k], s[k], __uint_as_float(out[k]));
+    }
+    for (int k = 0; k < d.ncomp; ++k) d.acc[k][u] = gen_op(d.monoid[k], d.acc[k][u], s[k]);
+  }
+}
+
 __global__ void k_site_eval(plx_site_desc d) {
   const int64_t n = live_count(d.n, d.n_dev);
   const uint32_t keyed =
@@ -1170,6 +1217,22 @@ int plx_merge_kills(int64_t n, const uint8_t* sink, uint8_t* dead, float* stamp,
   hipLaunchKernelGGL(k_merge_kills, dim3(grid_for(n)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), n, sink,
                      dead, stamp, stamp_value);
   return check_launch("plx_merge_kills");
+}
+
+int plx_gen_fold(const plx_gen_fold_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_gen_fold: null descriptor");
+  if (d->nrows < 0 || d->ncomp < 1 || d->ncomp > 8 || d->num_units <= 0)
+    return fail(PLX_ERR_INVALID, "plx_gen_fold: bad sizes (1 <= ncomp <= 8)");
+  if (d->nrows == 0) return PLX_OK;
+  if (!d->row_unit || !d->row_ptr || (d->backward ? !d->to_id : !d->from_id))
+    return fail(PLX_ERR_INVALID, "plx_gen_fold: null row table or id column");
+  if (d->prog.ninstr < 0 || d->prog.ninstr > PLX_MAX_SINSTR || d->prog.nout < d->ncomp)
+    return fail(PLX_ERR_INVALID, "plx_gen_fold: the program has fewer outputs than components");
+  for (int k = 0; k < d->ncomp; ++k)
+    if (!d->acc[k] || d->monoid[k] < PLX_MONOID_SUM || d->monoid[k] > PLX_MONOID_MIN)
+      return fail(PLX_ERR_INVALID, "plx_gen_fold: bad accumulator column or monoid");
+  hipLaunchKernelGGL(k_gen_fold, dim3(grid_for(d->nrows)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), *d);
+  return check_launch("plx_gen_fold");
 }
 
 int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, uint8_t* dead, const uint8_t* doomed,

@@ -82,7 +82,12 @@ def make_step(
     if batch_size is not None:
         from plastax_amd.batched import BatchedStepFn
 
-        step = BatchedStepFn(compile_plan(net, static), static, batch_size)
+        plan = compile_plan(net, static)
+        if plan.forward.generic is not None or (plan.backward is not None and plan.backward.generic is not None):
+            raise UnsupportedPolicyError(
+                "make_step: a batched step runs passes of the product form only (a generic map or a tuple "
+                "accumulator runs in the streaming step)")
+        step = BatchedStepFn(plan, static, batch_size)
     else:
         step = StepFn(compile_plan(net, static), static)
     step.prune_fusion = PruneFusionRecord(fuse_prune)
@@ -157,7 +162,12 @@ class StepFn:
         if self.arena_mode != "auto":
             if self.arena_mode not in ("tiled", "churn"):
                 raise ValueError(f"arena_mode must be 'auto', 'tiled' or 'churn', got {self.arena_mode!r}")
+            if (self.arena_mode == "tiled" and self.plan.backward is not None
+                    and self.plan.backward.generic is not None):
+                raise UnsupportedPolicyError("a generic backward pass runs on the churn layout, not the tiled one")
             return self.arena_mode == "churn"
+        if self.plan.backward is not None and self.plan.backward.generic is not None:
+            return True  # a generic backward folds each source's out-edges from the churn lists
         cfg = self.plan.add_conn
         if cfg is None:
             return False
@@ -250,48 +260,51 @@ class StepFn:
         g = state.globals_
 
         # Forward (phases.py:942-1015).
-        fp = plan.forward
-        swaps = self._shadow(units, fp.program.out_fields) if arena.pipeline else {}
-        acc = None
-        if arena.fwd_carry:
-            acc = torch.empty(n_units, dtype=torch.float32, device=dev)
-            _lib.call("plx_fill_f32", n_units, fp.identity, acc.data_ptr(), stream)
-        prog = program_struct(fp.program, units, g, out_override=swaps)
-        fusion = self._fusion_plan(g)
-        fused = self._fused_prune_progs(arena, units, fin_common, g, stream) if fusion.fused else None
-        for b in range(arena.num_buckets):
-            rows = arena.fwd[b]
-            d = _lib.plx_forward_desc()
-            d.nrows = rows.nrows
-            d.monoid = fp.monoid
-            d.tbl_base, d.tbl_len = arena.src_table(b)
-            d.row_unit = rows.rows.data_ptr()
-            d.row_ptr = rows.ptr.data_ptr()
-            d.src = arena.cols["from_id"].data_ptr()
-            d.weight = arena.cols["weight"].data_ptr()
-            # Row ranges hold live positions only unless tombstones were set
-            # inside them after the layout was built.
-            d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
-            d.x = fp.gathered(units, ACTIVATION.name).data_ptr()
-            d.map = fp.map_struct()
-            d.acc = acc.data_ptr() if acc is not None else None
-            d.fin.level = fin_common["level"]
-            d.fin.is_input = fin_common["is_input"]
-            d.fin.pruned = fin_common["pruned"]
-            d.fin.fin_level = -1 if arena.pipeline else b + 1
-            d.fin.skip_inputs = 1
-            d.apply = prog
-            if fused is not None and fusion.engine == "hip":
-                d.prune_prog = fused[b].data_ptr()
-                d.prune_sink = arena.prune_sink.data_ptr()
-                d.prune_slot = arena.slot[arena.bases[b]:].data_ptr()
-                d.ids_logical, d.ids_physical = arena.uperm32.data_ptr(), arena.uinv32.data_ptr()
-                d.prune_base = arena.bases[b]
-                d.num_units = n_units
-            self._launch("forward", lib.plx_forward_bucket, d, stream)
-        self._unshadow(units, swaps)
-        if fused is not None and fusion.engine == "xla":
-            self._xla_prune(arena, g, stream)
+        if plan.forward.generic is not None:
+            self._forward_generic(arena, units, g, stream)
+        else:
+            fp = plan.forward
+            swaps = self._shadow(units, fp.program.out_fields) if arena.pipeline else {}
+            acc = None
+            if arena.fwd_carry:
+                acc = torch.empty(n_units, dtype=torch.float32, device=dev)
+                _lib.call("plx_fill_f32", n_units, fp.identity, acc.data_ptr(), stream)
+            prog = program_struct(fp.program, units, g, out_override=swaps)
+            fusion = self._fusion_plan(g)
+            fused = self._fused_prune_progs(arena, units, fin_common, g, stream) if fusion.fused else None
+            for b in range(arena.num_buckets):
+                rows = arena.fwd[b]
+                d = _lib.plx_forward_desc()
+                d.nrows = rows.nrows
+                d.monoid = fp.monoid
+                d.tbl_base, d.tbl_len = arena.src_table(b)
+                d.row_unit = rows.rows.data_ptr()
+                d.row_ptr = rows.ptr.data_ptr()
+                d.src = arena.cols["from_id"].data_ptr()
+                d.weight = arena.cols["weight"].data_ptr()
+                # Row ranges hold live positions only unless tombstones were set
+                # inside them after the layout was built.
+                d.dead = arena.cols["dead"].data_ptr() if arena.dead_in_rows else None
+                d.x = fp.gathered(units, ACTIVATION.name).data_ptr()
+                d.map = fp.map_struct()
+                d.acc = acc.data_ptr() if acc is not None else None
+                d.fin.level = fin_common["level"]
+                d.fin.is_input = fin_common["is_input"]
+                d.fin.pruned = fin_common["pruned"]
+                d.fin.fin_level = -1 if arena.pipeline else b + 1
+                d.fin.skip_inputs = 1
+                d.apply = prog
+                if fused is not None and fusion.engine == "hip":
+                    d.prune_prog = fused[b].data_ptr()
+                    d.prune_sink = arena.prune_sink.data_ptr()
+                    d.prune_slot = arena.slot[arena.bases[b]:].data_ptr()
+                    d.ids_logical, d.ids_physical = arena.uperm32.data_ptr(), arena.uinv32.data_ptr()
+                    d.prune_base = arena.bases[b]
+                    d.num_units = n_units
+                self._launch("forward", lib.plx_forward_bucket, d, stream)
+            self._unshadow(units, swaps)
+            if fused is not None and fusion.engine == "xla":
+                self._xla_prune(arena, g, stream)
 
         # Loss (phases.py:1107-1131).
         if plan.loss is not None:
@@ -382,12 +395,62 @@ class StepFn:
             state.needs_resort = bool(state.needs_resort) or out.needs_resort
             state.tail_start = out.tail_start
 
+    # -- generic passes (plastax_amd/generic.py) ---------------------------------
+    def _generic_runner(self, which: str, g: Any) -> Any:
+        from plastax_amd.generic import GenericPassRunner
+
+        key = "_gen_" + which
+        if getattr(self, key, None) is None:
+            pp = self.plan.forward if which == "fwd" else self.plan.backward
+            setattr(self, key, GenericPassRunner(pp.generic, self.static, g))
+        return getattr(self, key)
+
+    def _forward_generic(self, arena: Arena, units: dict, g: Any, stream: int) -> None:
+        from plastax_amd import grow
+        from plastax_amd.generic import finalize_lists
+
+        run = self._generic_runner("fwd", g)
+        k = grow.Kernels(arena.device, stream)
+        fin = finalize_lists(arena, self.static)["fwd"]
+        acc = run.new_acc(self.static.num_units, arena.device)
+        for b in range(arena.num_buckets):
+            rows = arena.fwd[b]
+            run.fold(k, arena, b, units, acc, g, rows=rows.rows, nrows=rows.nrows, ptr=rows.ptr, entry_pos=None)
+            if not arena.pipeline:
+                run.apply(k, arena, units, acc, g, fin[b])
+        if arena.pipeline:
+            run.apply(k, arena, units, acc, g, fin[0])
+
+    def _backward_generic(self, arena: Arena, units: dict, stream: int, g: Any) -> None:
+        from plastax_amd import grow
+        from plastax_amd.generic import finalize_lists
+
+        run = self._generic_runner("bwd", g)
+        k = grow.Kernels(arena.device, stream)
+        fin = finalize_lists(arena, self.static)["bwd"]
+        n = self.static.num_units
+        acc = run.new_acc(n, arena.device)
+        rows = torch.arange(n, dtype=torch.int32, device=arena.device)
+        nb = arena.num_buckets
+        if arena.pipeline:
+            lists = arena.lists[0]
+            run.fold(k, arena, 0, units, acc, g, rows=rows, nrows=n, ptr=lists.ptr, entry_pos=lists.pos)
+            run.apply(k, arena, units, acc, g, fin[0])
+            return
+        run.apply(k, arena, units, acc, g, fin[nb])
+        for b in range(nb - 1, 0, -1):
+            lists = arena.lists[b]
+            run.fold(k, arena, b, units, acc, g, rows=rows, nrows=n, ptr=lists.ptr, entry_pos=lists.pos)
+            run.apply(k, arena, units, acc, g, fin[b])
+
     # -- fused forward + prune (phases.py:1629-1848, :2322-2469) ---------------
     def _fusion_plan(self, g: Any) -> PruneFusionPlan:
         rec = self.prune_fusion
         if rec.plan is None:
             if self.plan.net.prune_conn is None:
                 rec.plan = PruneFusionPlan(False, "no prune_conn")
+            elif self.plan.forward.generic is not None:
+                rec.plan = PruneFusionPlan(False, "the forward is a generic pass (no single-pass kernel)")
             elif rec.requested == "off":
                 rec.plan = PruneFusionPlan(False, "fuse_prune='off'")
             else:
@@ -676,7 +739,9 @@ class StepFn:
         bp, up = plan.backward, plan.update
         nb = arena.num_buckets
         if getattr(arena, "churn", False):
-            if bp is not None:
+            if bp is not None and bp.generic is not None:
+                self._backward_generic(arena, units, stream, g)
+            elif bp is not None:
                 self._backward_lists(plan, arena, units, fin_common, stream, g)
             if plan.update_unit:
                 self._run_update_unit(arena, units, stream, g)

@@ -1,0 +1,73 @@
+"""Generic passes on the device (plastax_amd/generic.py, plx_gen_fold):
+bit-exact with the oracle's generic path over training steps.
+
+Cases: a nonlinear forward map with the product backward (tiled layout);
+a tuple forward accumulator under (sum, max, sum) with a three-factor
+backward map (both generic: the churn layout's source lists), TOPOLOGICAL
+and PIPELINE; and a product map written as a one-element tuple, whose device
+run must equal the product kernels' bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import generic_cases as gc
+import nets
+import plastax_amd as px
+from test_gpu_parity import _equal, assert_same_state
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(oracle, net, pipeline: bool, steps: int, seed: int):
+    static, state = gc.build(net, pipeline=pipeline, seed=seed, device="cuda")
+    o = nets.oracle_for(oracle, net, static, state)
+    step = px.make_step(net, static)
+    if step.backward_order == "slot":
+        o.tile = None
+    xs, ts = gc.data(seed + 1, steps, len(static.input_ids), len(static.output_ids))
+    losses = []
+    for k in range(steps):
+        print(f"generic step {k} {net.forward_pass.__class__.__name__} pipeline={pipeline}", flush=True)
+        res = step(state, px.StepInputs(xs[k], ts[k]))
+        state = res.state
+        lo = o.step(xs[k], ts[k])
+        torch.cuda.synchronize()
+        assert_same_state(static, state, o, f"step {k}")
+        assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at step {k}"
+        losses.append(float(res.loss))
+    return static, state, losses
+
+
+@pytest.mark.parametrize(
+    ("forward", "backward", "pipeline"),
+    [
+        (gc.TanhSrcForward(), nets.TanhBackward(), False),
+        (gc.TupleForward(), gc.ThreeFactorBackward(), False),
+        (gc.TupleForward(), gc.ThreeFactorBackward(), True),
+    ],
+)
+def test_generic_passes_match_the_oracle(oracle, forward, backward, pipeline: bool) -> None:
+    net = gc.make_net(forward, backward, pipeline=pipeline, optimizer=px.optim.adam(1e-2, nets.GRAD_PRE_ACT))
+    _run(oracle, net, pipeline, 6, 11)
+
+
+def test_product_map_as_a_tuple_matches_the_product_kernels(oracle) -> None:
+    prod = gc.make_net(nets.TanhForward(), nets.TanhBackward())
+    gen = gc.make_net(gc.ProductAsTupleForward(), gc.ProductAsTupleBackward())
+    sp, st_p = gc.build(prod, pipeline=False, seed=5, device="cuda")
+    step_p = px.make_step(prod, sp)
+    step_p.arena_mode = "churn"  # the generic backward's slot order
+    xs, ts = gc.data(6, 5, len(sp.input_ids), len(sp.output_ids))
+    for k in range(5):
+        st_p = step_p(st_p, px.StepInputs(xs[k], ts[k])).state
+    _, st_g, _ = _run(oracle, gen, False, 5, 5)
+    hp, hg = nets.host_units(sp, st_p), nets.host_units(sp, st_g)
+    for name in hp:
+        assert np.array_equal(hp[name].view(np.uint8), hg[name].view(np.uint8)), name
+    for a, b in zip(nets.host_conns(sp, st_p), nets.host_conns(sp, st_g)):
+        for name in a:
+            assert np.array_equal(np.asarray(a[name]).view(np.uint8), np.asarray(b[name]).view(np.uint8)), name

@@ -47,7 +47,7 @@ def test_softmax_loss_is_its_own_kernel() -> None:
     assert plan.loss.kind == "softmax" and plan.loss.program is None
 
 
-def test_nonlinear_map_is_refused() -> None:
+def test_nonlinear_map_runs_as_a_generic_pass() -> None:
     class SquareMap(px.ForwardPass):
         def map(self, u, dst, src, c, cid, g):
             return c[px.WEIGHT, cid] * u[px.ACTIVATION, src] * u[px.ACTIVATION, src]
@@ -58,8 +58,8 @@ def test_nonlinear_map_is_refused() -> None:
     class Net(px.Network):
         forward_pass = SquareMap()
 
-    with pytest.raises(UnsupportedPolicyError, match="map must be"):
-        compile_plan(Net, _static(Net))
+    plan = compile_plan(Net, _static(Net))
+    assert plan.forward.generic is not None and "map must be" in plan.forward.generic.why
 
 
 def test_generic_monoid_is_refused() -> None:
