@@ -54,12 +54,16 @@ extern "C" {
  * term of an elementwise Loss (phases.py:1107-1131). Opcodes are listed in
  * plastax_amd/_expr.py; each instruction is {op, dst, a, b}. LDU operand a
  * indexes `fields`; OUT slot d writes `outs[d]` at the unit. Passed by value
- * (it travels in the kernel argument segment). */
+ * (it travels in the kernel argument segment).
+ * fixed_mask (loss programs only; 0 elsewhere): bit k set means fields[k]
+ * already points at one fixed unit's row (a loss reading u[F, UnitIdx(k)],
+ * as the reference's examples/swifttd.py:381-392 does) and is read at the
+ * sample index (0 in a streaming step), not at the output's unit. */
 typedef struct plx_program {
   int32_t ninstr;
   int32_t nout;
   int32_t nfields;
-  int32_t reserved;
+  int32_t fixed_mask;
   int32_t code[4 * PLX_MAX_INSTR];
   float consts[PLX_MAX_CONST];
   const float* fields[PLX_MAX_FIELDS];
@@ -442,7 +446,7 @@ PLX_EXPORT int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ct
 
 /* Elementary functions exactly as the kernels evaluate them (op 0 exp,
  * 1 log, 2 tanh, 3 sigmoid, 4 sqrt, 5 Adam power b^t with b=x[i], t=y[i],
- * 6 cos, 7 sin). */
+ * 6 cos, 7 sin, 8 log1p, 9 expm1). */
 PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float* y,
                   float* out, void* stream);
 

@@ -102,7 +102,7 @@ def load_variant(path: pathlib.Path) -> ctypes.CDLL:
 
 
 def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
-    for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf", "ox_cosf", "ox_sinf"):
+    for name in ("ox_expf", "ox_logf", "ox_tanhf", "ox_sigmoidf", "ox_cosf", "ox_sinf", "ox_log1pf", "ox_expm1f"):
         getattr(lib, name).restype = ctypes.c_float
         getattr(lib, name).argtypes = [ctypes.c_float]
     lib.ox_pow_step.restype = ctypes.c_float
@@ -199,16 +199,25 @@ class _ProgramArgs:
         if self.consts.size == 0:
             self.consts = np.zeros(1, np.float32)
         names = list(prog.fields)
+        fixed = dict(getattr(prog, "fixed_at", {}))
+        # A field read at one fixed unit (a loss's u[F, UnitIdx(k)]) is handed
+        # over as a column holding that unit's value at every index.
+        cols = [np.full(units[n].shape, units[n][fixed[k]], dtype=units[n].dtype) if k in fixed else units[n]
+                for k, n in enumerate(names)]
         out_idx = []
         for name in prog.out_fields:
             if name is None:
                 out_idx.append(-1)
                 continue
-            if name not in names:
+            own = [k for k, n in enumerate(names) if n == name and k not in fixed]
+            if not own:
                 names.append(name)
-            out_idx.append(names.index(name))
+                cols.append(units[name])
+                own = [len(names) - 1]
+            out_idx.append(own[0])
         self.names = names
-        self.table = (_f32p * max(len(names), 1))(*[fptr(units[n]) for n in names])
+        self._cols = cols  # kept alive: the table points into them
+        self.table = (_f32p * max(len(names), 1))(*[fptr(c) for c in cols])
         self.out_idx = np.asarray(out_idx, dtype=np.int32)
         self.ninstr = prog.ninstr
 

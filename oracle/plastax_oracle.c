@@ -249,6 +249,26 @@ OX_API float ox_tanhf(float x) {
 
 OX_API float ox_sigmoidf(float x) { return 1.0f / (1.0f + ox_expf(-x)); }
 
+/* log1p and expm1 by Kahan's method (Goldberg, "What Every Computer
+ * Scientist Should Know About Floating-Point Arithmetic", 1991, Theorem 4):
+ * u = fl(1 + x), log1p = x * (log(u) / (u - 1)); u = exp(x),
+ * expm1 = (u - 1) * (x / log(u)); exact where u == 1, infinities pass. */
+OX_API float ox_log1pf(float x) {
+  const float u = 1.0f + x;
+  if (u == 1.0f) return x;
+  if (u == INFINITY) return u;
+  return x * (ox_logf(u) / (u - 1.0f));
+}
+
+OX_API float ox_expm1f(float x) {
+  const float u = ox_expf(x);
+  if (u == 1.0f) return x;
+  if (u == INFINITY) return u;
+  const float um1 = u - 1.0f;
+  if (um1 == -1.0f) return -1.0f;
+  return um1 * (x / ox_logf(u));
+}
+
 /* sin and cos follow Cephes sinf.c / cosf.c (Moshier): |x| is reduced */
 /* modulo pi/4 by the octant j = trunc(|x| * 4/pi), rounded up to even, and */
 /* r = |x| - j * pi/4 with pi/4 split in three (DP1 and DP2 have few */
@@ -606,6 +626,8 @@ static float ox_run_program(const int32_t* prog, int32_t ninstr,
       case OP_SIGMOID: r[d] = ox_sigmoidf(r[a]); break;
       case OP_COS: r[d] = ox_cosf(r[a]); break;
       case OP_SIN: r[d] = ox_sinf(r[a]); break;
+      case OP_LOG1P: r[d] = ox_log1pf(r[a]); break;
+      case OP_EXPM1: r[d] = ox_expm1f(r[a]); break;
       case OP_SIGN:
         r[d] = r[a] > 0.0f ? 1.0f : (r[a] < 0.0f ? -1.0f : r[a]);
         break;
@@ -828,7 +850,8 @@ enum {
   S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
   S_UMAX = 60, S_UMIN, S_UFLOORDIV, S_UMOD, S_UGT, S_UGE, S_ULT, S_ULE,
   S_AND = 70, S_OR, S_XOR, S_NOT, S_SHL, S_SHRU, S_SHRI, S_BNOT,
-  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B
+  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B,
+  S_FLOG1P = 90, S_FEXPM1 = 91
 };
 
 #define OX_SREGS 32
@@ -920,6 +943,8 @@ OX_API void ox_site_eval(const int32_t* prog, int32_t ninstr, const uint32_t* co
         case S_FSIGMOID: r[d] = ox_u(ox_sigmoidf(ox_f(x))); break;
         case S_FCOS: r[d] = ox_u(ox_cosf(ox_f(x))); break;
         case S_FSIN: r[d] = ox_u(ox_sinf(ox_f(x))); break;
+        case S_FLOG1P: r[d] = ox_u(ox_log1pf(ox_f(x))); break;
+        case S_FEXPM1: r[d] = ox_u(ox_expm1f(ox_f(x))); break;
         case S_FSQUARE: r[d] = ox_u(ox_f(x) * ox_f(x)); break;
         case S_FRELU: r[d] = ox_u(ox_fmax_nan(ox_f(x), 0.0f)); break;
         case S_FSIGN: {

@@ -65,10 +65,13 @@ OPCODES = {
     "square": 27,
     "relu": 28,
     "sign": 29,
+    "log1p": 30,
+    "expm1": 31,
     "cos": 33,
     "sin": 34,
 }
-_UNARY = {"neg", "abs", "tanh", "exp", "log", "sqrt", "sigmoid", "square", "relu", "sign", "cos", "sin"}
+_UNARY = {"neg", "abs", "tanh", "exp", "log", "sqrt", "sigmoid", "square", "relu", "sign", "cos", "sin", "log1p",
+          "expm1"}
 _BINARY = {"add", "sub", "mul", "div", "max", "min", "gt", "ge", "lt", "le", "eq", "ne"}
 MAX_REGS = 16
 MAX_INSTR = 48
@@ -85,7 +88,7 @@ def _f32(x: Any) -> np.float32:
 # ("u"), bool ("b"), and the weakly typed Python scalars ("wi", "wf") that
 # take the other operand's type, as jnp's weak typing does.
 _WEAK = {"wi", "wf"}
-_FLOAT_ONLY = {"tanh", "exp", "log", "sqrt", "sigmoid", "floor", "cos", "sin"}
+_FLOAT_ONLY = {"tanh", "exp", "log", "sqrt", "sigmoid", "floor", "cos", "sin", "log1p", "expm1"}
 _INT_ONLY = {"mod", "floordiv", "shl", "shr"}
 _LOGIC = {"and", "or", "xor"}
 
@@ -382,12 +385,28 @@ class TraceUnitView:
             return self._load(spec, idx.role)
         if isinstance(idx, Expr) and idx.op == "ldc" and idx.field in ("from_id", "to_id"):
             return self._load(spec, "src" if idx.field == "from_id" else "dst")
+        fixed = _fixed_index(idx)
+        if fixed is not None:
+            e = self._load(spec, "fixed")
+            e.value = fixed
+            return e
         raise UnsupportedPolicyError(f"unit field read at an untraceable index {idx!r}")
 
     def gather(self, spec: FieldSpec, ids: Any) -> Expr:
         if isinstance(ids, Index):
             return self._load(spec, ids.role)
         raise UnsupportedPolicyError("UnitView.gather is traced only over the output ids")
+
+
+def _fixed_index(idx: Any) -> int | None:
+    """A unit index known at trace time (``UnitIdx(jnp.int32(k))``), or None."""
+    if isinstance(idx, (bool, np.bool_)):
+        return None
+    if isinstance(idx, (int, np.integer)):
+        return int(idx)
+    if isinstance(idx, np.ndarray) and idx.shape == () and np.issubdtype(idx.dtype, np.integer):
+        return int(idx)
+    return None
 
 
 class TraceConnView:
@@ -502,6 +521,10 @@ class Program:
     fields: list[str]  # LDU operand table (unit field names)
     out_fields: list[str | None]  # OUT slot -> unit field written (None: returned)
     globals_at: dict[int, str]  # const slot -> global name, refreshed per call
+    # LDU operand slot -> the one unit it is read at (a loss reading a unit
+    # fixed at trace time, e.g. u[F, UnitIdx(k)]); other slots read the
+    # program's own unit.
+    fixed_at: dict[int, int] = dataclasses.field(default_factory=dict)
 
     @property
     def ninstr(self) -> int:
@@ -534,7 +557,8 @@ def compile_program(
     """Compile expression outputs to a register program.
 
     ``allow`` names the leaf kinds the context permits: "acc" (apply),
-    "target" (loss), and the unit-field roles ("self" or "out").
+    "target" (loss), and the unit-field roles ("self" or "out", and "fixed":
+    a unit index known at trace time).
     """
     allowed = set(allow)
     outs = [lift(o) for o in outputs]
@@ -574,6 +598,8 @@ def compile_program(
     const_slot: dict[Any, int] = {}
     globals_at: dict[int, str] = {}
     fields: list[str] = []
+    field_slot: dict[tuple[str, int | None], int] = {}
+    fixed_at: dict[int, int] = {}
     reg: dict[int, int] = {}
     free = list(range(MAX_REGS - 1, -1, -1))
     code: list[tuple[int, int, int, int]] = []
@@ -615,15 +641,22 @@ def compile_program(
             instr = ("target", 0, 0)
         elif op == "ldu":
             if node.role not in allowed:
+                where = "a fixed unit" if node.role == "fixed" else repr(node.role)
                 raise UnsupportedPolicyError(
-                    f"unit field {node.field!r} read at {node.role!r}: only the unit's own "
+                    f"unit field {node.field!r} read at {where}: only the unit's own "
                     "fields are visible here"
                 )
-            if node.field not in fields:
+            key = (str(node.field), int(node.value) if node.role == "fixed" else None)
+            if key not in field_slot:
                 if len(fields) >= MAX_FIELDS:
                     raise UnsupportedPolicyError("a policy reads too many unit fields")
-                fields.append(str(node.field))
-            instr = ("ldu", fields.index(str(node.field)), 0)
+                field_slot[key] = len(fields)
+                fields.append(key[0])
+                if key[1] is not None:
+                    if key[1] < 0:
+                        raise UnsupportedPolicyError(f"unit index {key[1]} is negative")
+                    fixed_at[field_slot[key]] = key[1]
+            instr = ("ldu", field_slot[key], 0)
         elif op in _UNARY:
             instr = (op, reg[id(node.args[0])], 0)
         elif op in _BINARY:
@@ -657,7 +690,7 @@ def compile_program(
         code.append((OPCODES["out"], slot, reg[id(o)], 0))
     if len(code) > MAX_INSTR:
         raise UnsupportedPolicyError(f"a policy compiles to {len(code)} instructions; at most {MAX_INSTR}")
-    return Program(code, consts, fields, list(out_fields), globals_at)
+    return Program(code, consts, fields, list(out_fields), globals_at, fixed_at)
 
 
 def _take_pair(free: list[int]) -> int:

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 18  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 19  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -48,7 +48,7 @@ class plx_program(ctypes.Structure):
         ("ninstr", c_i32),
         ("nout", c_i32),
         ("nfields", c_i32),
-        ("reserved", c_i32),
+        ("fixed_mask", c_i32),
         ("code", c_i32 * (4 * PLX_MAX_INSTR)),
         ("consts", c_f32 * PLX_MAX_CONST),
         ("fields", c_vp * PLX_MAX_FIELDS),

@@ -224,7 +224,10 @@ def _trace_loss(loss: Any, static: NetworkStatic) -> LossPlan:
             "an elementwise loss must return jnp.sum(term) over the outputs as its value"
         )
     term = value.args[0]
-    prog = compile_program([seed, term], [seed_field, None], allow={"target", "out"})
+    prog = compile_program([seed, term], [seed_field, None], allow={"target", "out", "fixed"})
+    for k in prog.fixed_at.values():
+        if k >= static.num_units:
+            raise UnsupportedPolicyError(f"{type(loss).__name__} reads unit {k}; the net has {static.num_units}")
     _check_float_fields(prog.fields, dtypes, type(loss).__name__)
     return LossPlan("elementwise", seed_field, prog)
 
@@ -281,8 +284,12 @@ def program_struct(
     globals_: Any,
     *,
     out_override: dict | None = None,
+    batch: int = 1,
+    unit_map: np.ndarray | None = None,
 ) -> "_lib.plx_program":
-    """The plx_program of ``prog`` over the given unit tensors."""
+    """The plx_program of ``prog`` over the given unit tensors (``batch`` > 1:
+    columns of ``[num_units][batch]``; ``unit_map``: a fixed unit's logical
+    id -> its row in renumbered columns)."""
     p = _lib.plx_program()
     p.ninstr = prog.ninstr
     p.nout = len(prog.out_fields)
@@ -292,8 +299,19 @@ def program_struct(
         p.code[k] = int(v)
     for k, v in enumerate(prog.const_values(globals_)):
         p.consts[k] = float(v)
+    mask = 0
     for k, name in enumerate(prog.fields):
-        p.fields[k] = units[name].data_ptr()
+        col = units[name]
+        p.fields[k] = col.data_ptr()
+        at = prog.fixed_at.get(k)
+        if at is not None and unit_map is not None:
+            at = int(unit_map[at])
+        if at is not None:
+            if (at + 1) * batch > col.numel():
+                raise ValueError(f"unit {at} is outside the {name!r} column")
+            p.fields[k] = col.data_ptr() + at * batch * col.element_size()
+            mask |= 1 << k
+    p.fixed_mask = mask
     over = out_override or {}
     for k, name in enumerate(prog.out_fields):
         if name is None:

@@ -54,6 +54,7 @@ SOP = {
     "ule": 67,
     "and": 70, "or": 71, "xor": 72, "not": 73, "shl": 74, "shru": 75, "shri": 76, "bnot": 77,
     "i2f": 80, "u2f": 81, "f2i": 82, "f2u": 83, "f2b": 84, "i2b": 85,
+    "flog1p": 90, "fexpm1": 91,
 }
 ROLES = {"i": 0, "j": 1, "src": 2, "dst": 3, "cid": 4}
 KIND_CODE = {"f": 0, "i": 1, "u": 2, "b": 3}
@@ -250,7 +251,8 @@ def _opcode(node: Expr) -> str:
         name = {"add": "fadd", "sub": "fsub", "mul": "fmul", "div": "fdiv", "neg": "fneg",
                 "abs": "fabs", "max": "fmax", "min": "fmin", "tanh": "ftanh", "exp": "fexp",
                 "log": "flog", "sqrt": "fsqrt", "sigmoid": "fsigmoid", "square": "fsquare",
-                "relu": "frelu", "sign": "fsign", "floor": "ffloor", "cos": "fcos", "sin": "fsin"}.get(op)
+                "relu": "frelu", "sign": "fsign", "floor": "ffloor", "cos": "fcos", "sin": "fsin",
+                "log1p": "flog1p", "expm1": "fexpm1"}.get(op)
     elif k == "i":
         name = {"add": "iadd", "sub": "isub", "mul": "imul", "neg": "ineg", "abs": "iabs",
                 "max": "imax", "min": "imin", "floordiv": "ifloordiv", "mod": "imod",

@@ -250,7 +250,7 @@ class BatchedStepFn(StepFn):
                 )
             else:
                 parts = torch.empty(B * (n_out // 256 + 1) + 1, dtype=torch.float32, device=dev)
-                lprog = program_struct(lp.program, ub, g)
+                lprog = program_struct(lp.program, ub, g, batch=B, unit_map=consts["unit_map"])
                 _lib.check(
                     lib.plx_loss_elementwise_batch(n_out, ids, t.data_ptr(), lprog, ub[lp.seed_field].data_ptr(),
                                                    parts.data_ptr(), losses.data_ptr(), B, stream),

@@ -123,7 +123,7 @@ enum : int32_t {
   OP_EXP = 13, OP_LOG = 14, OP_SQRT = 15, OP_SIGMOID = 16, OP_GT = 17,
   OP_GE = 18, OP_LT = 19, OP_LE = 20, OP_EQ = 21, OP_NE = 22, OP_SEL = 23,
   OP_OUT = 24, OP_LDX = 25, OP_MOV = 26, OP_SQUARE = 27, OP_RELU = 28,
-  OP_SIGN = 29, OP_COS = 33, OP_SIN = 34
+  OP_SIGN = 29, OP_LOG1P = 30, OP_EXPM1 = 31, OP_COS = 33, OP_SIN = 34
 };
 
 constexpr int kRegs = 16;
@@ -167,6 +167,16 @@ __device__ __forceinline__ UnitFields load_fields(const plx_program& P, int64_t 
     case 1: f.v[0] = P.fields[0][u]; [[fallthrough]];
     default: break;
   }
+  return f;
+}
+
+// A loss program's fields at output row u of sample b: a field whose
+// fixed_mask bit is set points at one fixed unit's row and is read at b.
+__device__ __forceinline__ UnitFields load_loss_fields(const plx_program& P, int64_t u, int b) {
+  UnitFields f;
+#pragma unroll
+  for (int k = 0; k < PLX_MAX_FIELDS; ++k)
+    f.v[k] = k < P.nfields ? P.fields[k][(P.fixed_mask >> k) & 1 ? static_cast<int64_t>(b) : u] : 0.0f;
   return f;
 }
 
@@ -214,6 +224,8 @@ __device__ float run_program(const plx_program& P, int64_t u, const UnitFields& 
       case OP_SIGN: v = ra > 0.0f ? 1.0f : (ra < 0.0f ? -1.0f : ra); break;
       case OP_COS: v = px::cosf_(ra); break;
       case OP_SIN: v = px::sinf_(ra); break;
+      case OP_LOG1P: v = px::log1pf_(ra); break;
+      case OP_EXPM1: v = px::expm1f_(ra); break;
       case OP_GT: v = ra > rb ? 1.0f : 0.0f; break;
       case OP_GE: v = ra >= rb ? 1.0f : 0.0f; break;
       case OP_LT: v = ra < rb ? 1.0f : 0.0f; break;
@@ -1792,7 +1804,7 @@ __global__ __launch_bounds__(kPiece) void k_loss_pieces(int32_t n_out, const int
   if (k < n_out) {
     const int64_t u = static_cast<int64_t>(ids[k]) * B + b;
     terms[threadIdx.x] =
-        run_program(P, u, load_fields(P, u), 0.0f, targets[static_cast<int64_t>(b) * n_out + k], true);
+        run_program(P, u, load_loss_fields(P, u, b), 0.0f, targets[static_cast<int64_t>(b) * n_out + k], true);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1906,6 +1918,8 @@ __global__ void k_math(int32_t op, int64_t n, const float* x, const float* y, fl
     case 4: r = sqrtf(v); break;
     case 6: r = px::cosf_(v); break;
     case 7: r = px::sinf_(v); break;
+    case 8: r = px::log1pf_(v); break;
+    case 9: r = px::expm1f_(v); break;
     default: r = px::pow_step(v, y[i]); break;
   }
   out[i] = r;
@@ -1929,8 +1943,13 @@ int cu_count() {
   return cached[dev];
 }
 
-bool program_ok(const plx_program& p) {
-  return p.ninstr >= 0 && p.ninstr <= PLX_MAX_INSTR && p.nout >= 0 && p.nout <= PLX_MAX_OUTS;
+// A program's sizes are in range; fields read at a fixed unit only where
+// the kernel honours them (the loss) and only among the program's fields.
+bool program_ok(const plx_program& p, bool fixed_ok = false) {
+  if (p.ninstr < 0 || p.ninstr > PLX_MAX_INSTR || p.nout < 0 || p.nout > PLX_MAX_OUTS) return false;
+  if (p.nfields < 0 || p.nfields > PLX_MAX_FIELDS) return false;
+  if (p.fixed_mask == 0) return true;
+  return fixed_ok && (static_cast<uint32_t>(p.fixed_mask) >> p.nfields) == 0u;
 }
 
 template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
@@ -1980,7 +1999,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 18; }
+int32_t plx_abi_version(void) { return 19; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[18] = {
@@ -2186,7 +2205,7 @@ int plx_loss_elementwise(int32_t n_out, const int32_t* output_ids, const float* 
   if (n_out < 0) return fail(PLX_ERR_INVALID, "plx_loss_elementwise: negative n_out");
   if (!term || !loss_out || !partials)
     return fail(PLX_ERR_INVALID, "plx_loss_elementwise: null pointer");
-  if (!program_ok(*term)) return fail(PLX_ERR_INVALID, "plx_loss_elementwise: bad program");
+  if (!program_ok(*term, true)) return fail(PLX_ERR_INVALID, "plx_loss_elementwise: bad program");
   if (n_out > 0 && (!output_ids || !targets || !seed_field))
     return fail(PLX_ERR_INVALID, "plx_loss_elementwise: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2405,7 +2424,7 @@ int plx_loss_elementwise_batch(int32_t n_out, const int32_t* output_ids, const f
   if (n_out < 0 || batch < 1) return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: bad size");
   if (!term || !losses || !partials)
     return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: null pointer");
-  if (!program_ok(*term)) return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: bad program");
+  if (!program_ok(*term, true)) return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: bad program");
   if (n_out > 0 && (!output_ids || !targets || !seed_field))
     return fail(PLX_ERR_INVALID, "plx_loss_elementwise_batch: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2484,7 +2503,7 @@ int plx_philox32(int64_t n, const uint64_t* seeds, const uint64_t* ctrs, uint32_
 
 int plx_eval_math(int32_t op, int64_t n, const float* x, const float* y, float* out,
                   void* stream) {
-  if (n < 0 || op < 0 || op > 7) return fail(PLX_ERR_INVALID, "plx_eval_math: bad argument");
+  if (n < 0 || op < 0 || op > 9) return fail(PLX_ERR_INVALID, "plx_eval_math: bad argument");
   if (n == 0) return PLX_OK;
   if (!x || !out || (op == 5 && !y)) return fail(PLX_ERR_INVALID, "plx_eval_math: null pointer");
   k_math<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(op, n, x, y, out);

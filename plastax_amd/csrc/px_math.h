@@ -104,6 +104,27 @@ __device__ __forceinline__ float tanhf_(float x) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf_(-x)); }
 
+// log1p and expm1 by Kahan's method (D. Goldberg, "What Every Computer
+// Scientist Should Know About Floating-Point Arithmetic", ACM Computing
+// Surveys 23(1), 1991, Theorem 4): with u = fl(1 + x), the rounding error of
+// the sum cancels in x * (log(u) / (u - 1)); likewise expm1 from u = exp(x)
+// as (u - 1) * (x / log(u)). Exact for u == 1; infinities pass through.
+__device__ __forceinline__ float log1pf_(float x) {
+  const float u = 1.0f + x;
+  if (u == 1.0f) return x;
+  if (u == __builtin_huge_valf()) return u;
+  return x * (logf_(u) / (u - 1.0f));
+}
+
+__device__ __forceinline__ float expm1f_(float x) {
+  const float u = expf_(x);
+  if (u == 1.0f) return x;
+  if (u == __builtin_huge_valf()) return u;
+  const float um1 = u - 1.0f;
+  if (um1 == -1.0f) return -1.0f;
+  return um1 * (x / logf_(u));
+}
+
 // sin and cos follow Cephes sinf.c / cosf.c (Moshier): |x| is reduced
 // modulo pi/4 by the octant j = trunc(|x| * 4/pi), rounded up to even, and
 // r = |x| - j * pi/4 with pi/4 split in three (DP1 and DP2 have few

@@ -22,7 +22,8 @@ enum : int32_t {
   S_IGT = 50, S_IGE, S_ILT, S_ILE, S_IEQ, S_INE,
   S_UMAX = 60, S_UMIN, S_UFLOORDIV, S_UMOD, S_UGT, S_UGE, S_ULT, S_ULE,
   S_AND = 70, S_OR, S_XOR, S_NOT, S_SHL, S_SHRU, S_SHRI, S_BNOT,
-  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B
+  S_I2F = 80, S_U2F, S_F2I, S_F2U, S_F2B, S_I2B,
+  S_FLOG1P = 90, S_FEXPM1 = 91
 };
 
 __device__ __forceinline__ float fmax_nan(float a, float b) {
@@ -123,6 +124,8 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
       case S_FSIGMOID: v = __float_as_uint(px::sigmoidf_(xf)); break;
       case S_FCOS: v = __float_as_uint(px::cosf_(xf)); break;
       case S_FSIN: v = __float_as_uint(px::sinf_(xf)); break;
+      case S_FLOG1P: v = __float_as_uint(px::log1pf_(xf)); break;
+      case S_FEXPM1: v = __float_as_uint(px::expm1f_(xf)); break;
       case S_FSQUARE: v = __float_as_uint(xf * xf); break;
       case S_FRELU: v = __float_as_uint(fmax_nan(xf, 0.0f)); break;
       case S_FSIGN: v = xf > 0.0f ? 0x3F800000u : (xf < 0.0f ? 0xBF800000u : x); break;

@@ -42,6 +42,8 @@ log = _unary("log", np.log)
 sqrt = _unary("sqrt", np.sqrt)
 cos = _unary("cos", np.cos)
 sin = _unary("sin", np.sin)
+log1p = _unary("log1p", np.log1p)
+expm1 = _unary("expm1", np.expm1)
 abs = _unary("abs", np.abs)  # noqa: A001 -- mirrors jnp.abs
 absolute = abs
 negative = _unary("neg", np.negative)

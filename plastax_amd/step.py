@@ -155,6 +155,7 @@ class StepFn:
         c["input_ids"] = arena.input_ids
         c["output_ids"] = arena.output_ids
         c["is_input"] = arena.is_input
+        c["unit_map"] = arena.uinv  # logical unit id -> its row in the laid-out columns (host)
         return c
 
     def churn(self) -> bool:
@@ -581,7 +582,7 @@ class StepFn:
             )
             return
         scratch = torch.empty(n_out // 256 + 2, dtype=torch.float32, device=dev)
-        prog = program_struct(lp.program, units, g)
+        prog = program_struct(lp.program, units, g, unit_map=consts["unit_map"])
         _lib.check(
             lib.plx_loss_elementwise(
                 n_out,

@@ -82,7 +82,8 @@ def test_device_math_is_bit_exact_with_the_oracle(oracle) -> None:
         rng.uniform(-90, 90, 20000), rng.uniform(-2, 2, 20000), rng.standard_normal(20000),
         np.exp(rng.uniform(-80, 80, 20000)), specials,
     ]).astype(np.float32)
-    for op, fn in ((0, lib.ox_expf), (2, lib.ox_tanhf), (3, lib.ox_sigmoidf), (6, lib.ox_cosf), (7, lib.ox_sinf)):
+    for op, fn in ((0, lib.ox_expf), (2, lib.ox_tanhf), (3, lib.ox_sigmoidf), (6, lib.ox_cosf), (7, lib.ox_sinf),
+                   (8, lib.ox_log1pf), (9, lib.ox_expm1f)):
         dev = _device_math(op, xs)
         ref = np.asarray([fn(float(v)) for v in xs], dtype=np.float32)
         assert _equal(dev, ref), f"op {op}: {_first_diff(dev, ref)}"
