@@ -631,11 +631,16 @@ def run_c3(args) -> int:
     setup_s = time.perf_counter() - t_setup
     progress(f"C3: {e.src.size} edges, B = {B} ({setup_s:.1f} s)")
     first_loss = None
+    first_units = first_conns = None
     for k in range(args.warmup):
         res = step(gstate, px.StepInputs(xs_d[k], ys_d[k]))
         gstate = res.state
         if k == 0:
             first_loss = res.loss
+            if not args.no_cpu_baseline:
+                # every column after the first step, for the full-size parity check
+                first_units = {s.name: column_to_numpy(gstate.units[s.name], s).copy() for s in static.unit_fields}
+                first_conns = [{n: column_to_numpy(b[n], specs[n]).copy() for n in specs} for b in gstate.conns]
     torch.cuda.synchronize()
     dominant = "update_conn"
     timer = EventTimer({dominant})
@@ -702,9 +707,21 @@ def run_c3(args) -> int:
         ref_loss = np.float32(orc.step(xs[0], ys[0]))
         sec = time.perf_counter() - t1
         if first_loss is not None:
-            # Full-size parity: the first batched step's loss, bit for bit.
+            # Full-size parity: the first batched step's loss and every unit
+            # and connection column after it, bit for bit.
             got = np.float32(float(first_loss))
-            parity = {"steps": 1, "loss_bit_exact": bool(got.view(np.uint32) == ref_loss.view(np.uint32))}
+
+            def same(a, b):  # bitwise for float32 (NaN == NaN, -0.0 != +0.0), by value otherwise
+                a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+                if a.dtype == np.float32:
+                    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+                return bool(np.array_equal(a, b))
+
+            units_ok = all(same(first_units[n], o.units[n]) for n in first_units)
+            conns_ok = all(same(c[n], oc[n]) for c, oc in zip(first_conns, o.conns) for n in c)
+            parity = {"steps": 1, "loss_bit_exact": bool(got.view(np.uint32) == ref_loss.view(np.uint32)),
+                      "units_bit_exact": bool(units_ok), "conns_bit_exact": bool(conns_ok)}
+            progress(f"C3 parity after step 1: loss {parity['loss_bit_exact']}, units {units_ok}, conns {conns_ok}")
         cpu = {
             "value": float(B / sec),
             "unit": "samples/s",
