@@ -453,6 +453,7 @@ def run_c5(args) -> int:
     )
     gstate.tail_start = state.tail_start
     step = px.make_step(net, static)
+    step.relayout = args.relayout
     npar = 0 if args.no_cpu_baseline else 2
     nsteps = npar + args.warmup + args.steps
     rng = np.random.default_rng(args.seed + 3)
@@ -772,6 +773,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--relayout", choices=("merge", "full"), default="merge",
+                    help="c5: the churn layout after a growth step: merged from the previous one, or built again")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain elementwise copy of MIB MiB (read MIB, write MIB) "
                     "five times: the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")

@@ -454,9 +454,9 @@ PLX_EXPORT int plx_eval_math(int32_t op, int64_t n, const float* x, const float*
  * plx_forward_desc, plx_tile_desc, plx_partials_desc, plx_update_desc,
  * plx_site_prog, plx_site_desc, plx_sort_key, plx_sort_desc,
  * plx_grow_filter_desc, plx_grow_col, plx_grow_claim_desc, plx_unit_col,
- * plx_bwd_batch_desc, plx_batch_tiles, plx_tile_build_desc, plx_gen_fold_desc
- * (for binding layers to check their mirrors). Writes min(n, 18) values and
- * returns 18. */
+ * plx_bwd_batch_desc, plx_batch_tiles, plx_tile_build_desc, plx_gen_fold_desc,
+ * plx_merge_desc, plx_merge_gather_desc (for binding layers to check their
+ * mirrors). Writes min(n, 20) values and returns 20. */
 PLX_EXPORT int plx_struct_sizes(int64_t* out, int32_t n);
 
 /* ========================================================================
@@ -950,6 +950,76 @@ PLX_EXPORT int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* co
                               const int32_t* g_st, const int32_t* g_tile, const int32_t* hl, const int32_t* off,
                               const int8_t* region, const int32_t* sb_of_tile, int32_t* cold_idx,
                               uint16_t* cold_sb, void* stream);
+
+/* The churn layout's incremental rebuild (plastax_amd/_churn.py
+ * ChurnArena.merged): after a growth step the live edges are the previous
+ * layout's survivors, still in (destination, slot) order, plus the slots the
+ * claim filled; merging the two sorted lists gives the order a full rebuild
+ * (the reference's resort, topo.py:303-452, a stable sort of every live
+ * slot) would give, for the cost of one pass over the columns. */
+
+/* out[t] = 1 for t = via ? via[idx[i]] : idx[i], i < n (count n_dev,
+ * optional; via, when given, has via_len entries and idx values outside it
+ * are skipped), t in [0, m). */
+PLX_EXPORT int plx_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via,
+                           int64_t via_len, int64_t m, uint8_t* out, void* stream);
+
+/* One side of a merge: n elements whose ids (in [0, id_limit)) are listed
+ * in ascending (key1[id], key2[id]) order, keys compared as uint32; key2
+ * null means the id itself. map (optional, id_limit entries) receives each
+ * element's merged rank plus the merge's offset. */
+typedef struct plx_merge_side {
+  int64_t n;
+  int64_t id_limit;
+  const int32_t* ids;
+  const int32_t* key1;
+  const int32_t* key2;
+  int32_t* map;
+} plx_merge_side;
+
+/* Merges a and b (a first where keys are equal): order[r] (optional,
+ * a.n + b.n entries) is a's id at merged rank r, or -1 - j for b's j-th
+ * element. */
+typedef struct plx_merge_desc {
+  plx_merge_side a;
+  plx_merge_side b;
+  int64_t offset;
+  int32_t* order;
+} plx_merge_desc;
+
+PLX_EXPORT int plx_merge_index(const plx_merge_desc* d, void* stream);
+
+/* out[r] = a[order[r]] where order[r] >= 0, else b[b_ids[j]] (b null: the
+ * id b_ids[j] itself) for j = -1 - order[r], r < n; elements of `bytes`
+ * (1 or 4) bytes; a has a_limit entries, b b_limit, b_ids nb. */
+typedef struct plx_merge_col {
+  const void* a;
+  const void* b;
+  void* out;
+  int32_t bytes;
+  int32_t reserved;
+} plx_merge_col;
+
+#define PLX_MERGE_MAX_COLS 12
+
+typedef struct plx_merge_gather_desc {
+  int64_t n;
+  const int32_t* order;
+  const int32_t* b_ids;
+  int64_t nb;
+  int64_t a_limit;
+  int64_t b_limit;
+  int32_t ncols;
+  int32_t reserved;
+  plx_merge_col cols[PLX_MERGE_MAX_COLS];
+} plx_merge_gather_desc;
+
+PLX_EXPORT int plx_merge_gather(const plx_merge_gather_desc* d, void* stream);
+
+/* out[j] = map[idx[j] - off] (-1 where idx[j] - off is outside
+ * [0, map_len)), live[j] = out[j] >= 0, for j < n. */
+PLX_EXPORT int plx_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
+                             int32_t* out, uint8_t* live, void* stream);
 
 /* counts[ids[p]] += 1 over n positions, skipping p where skip[p] (optional)
  * and ids outside [0, nbins) (integer atomics: the counts are exact). */

@@ -19,6 +19,16 @@ stable radix sorts and gathers, all on the device:
   the reference's own scatter order (sweep.py:343-399) -- from copies of
   TO_ID (fixed by the build) and of WEIGHT / liveness (gathered each step
   before the update).
+
+After a growth step the arena is rebuilt from the previous one (``prev``)
+instead: its live edges that are still live keep their (destination, slot)
+and (source, slot) orders, so the new orders are those lists merged with
+the slots the claim filled, sorted by the same keys (``plx_merge_index``, a
+binary search per element) -- one pass over the columns
+(``plx_merge_gather``) instead of two radix sorts of every live edge and a
+gather per column. The result equals the full build's entry for entry. The
+columns alternate between two buffers, so the positions past the live range
+keep the fill values with a write of only the range that stopped being live.
 """
 
 from __future__ import annotations
@@ -37,10 +47,13 @@ class SourceLists:
     ``[ptr[r], ptr[r+1])``, entry j being physical position ``pos[j]`` with
     TO_ID ``dst[j]``; ``weight`` / ``live`` are refreshed each step."""
 
-    def __init__(self, ptr: torch.Tensor, pos: torch.Tensor, dst: torch.Tensor) -> None:
+    def __init__(self, ptr: torch.Tensor, pos: torch.Tensor, dst: torch.Tensor, src: torch.Tensor,
+                 slot: torch.Tensor) -> None:
         self.ptr = ptr
         self.pos = pos
         self.dst = dst
+        self.src = src  # entry j's FROM_ID (the list key)
+        self.slot = slot  # entry j's logical slot (the tiebreak)
         n = int(pos.numel())
         self.weight = torch.empty(n, dtype=torch.float32, device=pos.device)
         self.live = torch.empty(n, dtype=torch.uint8, device=pos.device)
@@ -52,7 +65,7 @@ class ChurnArena(Arena):
     churn = True
 
     def __init__(self, static: NetworkStatic, units: Columns, conns: tuple[Columns, ...],
-                 device: torch.device, stream: int) -> None:
+                 device: torch.device, stream: int, prev: "ChurnArena | None" = None) -> None:
         from plastax_amd.grow import Kernels
 
         self.static = static
@@ -92,12 +105,20 @@ class ChurnArena(Arena):
         self.ends = [int(b) for b in bases[1:]]
         size = total + PAD
         specs = {s.name: s for s in static.conn_fields}
-        self.cols = {}
-        for name, spec in specs.items():
-            dt = torch_dtype(spec.dtype)
-            fill = 1 if name == DEAD.name else spec.default
-            self.cols[name] = torch.full((size,), fill, dtype=dt, device=device)
-        self.slot = torch.full((size,), -1, dtype=torch.int32, device=device)
+        self._fills = {name: (1 if name == DEAD.name else spec.default) for name, spec in specs.items()}
+        if prev is not None and not self.can_follow(prev, static, caps):
+            prev = None
+        if prev is not None and prev._spare is not None:
+            # the other buffer: fill values past `extent` in every bucket
+            self.cols, self.slot, extent = prev._spare
+        else:
+            self.cols = {}
+            for name, spec in specs.items():
+                self.cols[name] = torch.full((size,), self._fills[name], dtype=torch_dtype(spec.dtype), device=device)
+            self.slot = torch.full((size,), -1, dtype=torch.int32, device=device)
+            extent = [0] * nb
+        self._spare = None if prev is None else (prev.cols, prev.slot, prev._extent)
+        self.merged = prev is not None
         self.lives = []
         self.fwd = []
         self.bwd = []
@@ -113,6 +134,9 @@ class ChurnArena(Arena):
         nbits = max(1, int(n).bit_length())
         rows = torch.arange(n, dtype=torch.int32, device=device)
         for b, bucket in enumerate(conns):
+            if prev is not None:
+                self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b])
+                continue
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
             live_list, nlive = k.compact(cap, 1, dead)  # PLX_FLAG_U8_ZERO: live slots, ascending
@@ -138,7 +162,7 @@ class ChurnArena(Arena):
                                                k.s), "plx_sorted_starts")
             self.fwd.append(ForwardRows(n, rows, fptr + base))
             # Backward lists: live slots by (source, slot) -> their positions.
-            sl = live_list[:live].clone()
+            sl = live_list[: max(live, 1)].clone()
             k.sort(sl, live, [(0, nbits, bucket[FROM_ID.name], None)], tag="relayout")
             pos_of_slot = torch.zeros(cap, dtype=torch.int32, device=device)
             pos_of_slot[lv.long()] = torch.arange(base, base + live, dtype=torch.int32, device=device)
@@ -153,9 +177,107 @@ class ChurnArena(Arena):
                                             lsrc.data_ptr(), k.s), "plx_gather_i32")
             lptr = torch.empty(n + 1, dtype=torch.int32, device=device)
             _lib.check(k.lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
-            self.lists.append(SourceLists(lptr, pos, ldst))
+            self.lists.append(SourceLists(lptr, pos, ldst, lsrc, sl))
+        self._extent = list(self.lives)
         self.top = None
         self.levels_dev = levels
+        if prev is not None:
+            prev._retire()
+
+    @staticmethod
+    def can_follow(prev: "ChurnArena", static: NetworkStatic, caps: list[int]) -> bool:
+        """Whether a merged rebuild from ``prev`` applies: the same net and
+        bucket capacities, ``prev`` still holding its buffers, and columns of
+        1- or 4-byte elements (what plx_merge_gather moves)."""
+        return (isinstance(prev, ChurnArena) and prev.static is static and prev.caps == caps
+                and prev.cols is not None
+                and all(np.dtype(s.dtype).itemsize in (1, 4) for s in static.conn_fields))
+
+    def _retire(self) -> None:
+        """This arena's buffers now belong to its successor."""
+        self.cols = None
+        self.slot = None
+        self._spare = None
+
+    def _merge_bucket(self, k, b: int, prev: "ChurnArena", bucket: Columns, specs: dict, nbits: int,
+                      rows: torch.Tensor, extent: int) -> None:
+        """Bucket b laid out from ``prev``'s layout of it (see the module
+        docstring): the survivors (prev's live positions whose DEAD is still
+        0) merged with the live slots that no survivor holds."""
+        dev = self.device
+        n = self.static.num_units
+        base, cap = self.bases[b], self.caps[b]
+        old_live = prev.lives[b]
+        lib = k.lib
+        if prev.t_name and prev.t_now and prev.t_now[b] is not None and old_live:
+            # Adam's count is one number for prev's live edges (its column
+            # was not kept for them): materialise it for the survivors.
+            t_col = prev.cols[prev.t_name][base : base + old_live]
+            t_col.masked_fill_(prev.cols[DEAD.name][base : base + old_live] == 0, float(prev.t_now[b]))
+        # Survivors: prev's live positions still live, in (destination, slot) order.
+        surv, nsurv_d = k.compact(old_live, 1, prev.cols[DEAD.name][base:])  # PLX_FLAG_U8_ZERO
+        # New: the slots live in the logical bucket that no survivor holds
+        # (claimed this step, possibly a slot that died and was claimed again).
+        mark = bucket[DEAD.name].clone()
+        _lib.check(lib.plx_mark_u8(old_live, nsurv_d.data_ptr(), surv.data_ptr(), prev.slot[base:].data_ptr(),
+                                   old_live, cap, mark.data_ptr(), k.s), "plx_mark_u8")
+        fresh, nnew_d = k.compact(cap, 1, mark)  # PLX_FLAG_U8_ZERO: ascending slots
+        counts = torch.cat([nsurv_d, nnew_d]).cpu().tolist()  # the rebuild's host read (as the full build's)
+        nsurv, nnew = int(counts[0]), int(counts[1])
+        live = nsurv + nnew
+        self.lives.append(live)
+        by_dst = fresh[:max(nnew, 1)].clone()
+        by_src = fresh[:max(nnew, 1)].clone()
+        k.sort(by_dst, nnew, [(0, nbits, bucket[TO_ID.name], None)], tag="relayout")
+        k.sort(by_src, nnew, [(0, nbits, bucket[FROM_ID.name], None)], tag="relayout")
+        # Positions: merge by (TO_ID, slot); maps old position / new slot -> new position.
+        order = torch.empty(max(live, 1), dtype=torch.int32, device=dev)
+        old_to_new = torch.full((max(old_live, 1),), -1, dtype=torch.int32, device=dev)
+        new_pos = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+        m = _lib.plx_merge_desc()
+        _side(m.a, nsurv, old_live, surv, prev.cols[TO_ID.name][base:], prev.slot[base:], old_to_new)
+        _side(m.b, nnew, cap, by_dst, bucket[TO_ID.name], None, new_pos)
+        m.offset, m.order = base, order.data_ptr()
+        _lib.check(lib.plx_merge_index(m, k.s), "plx_merge_index")
+        cols = [(prev.cols[name][base:], bucket[name], self.cols[name][base:], bucket[name].element_size())
+                for name in specs]
+        cols.append((prev.slot[base:], None, self.slot[base:], 4))
+        _gather(lib, k.s, live, order, by_dst, nnew, old_live, cap, cols)
+        # Past the live range: dead slots in slot order; the columns' fill values.
+        dead_list, _ = k.compact(cap, 0, bucket[DEAD.name])  # PLX_FLAG_U8: dead slots, ascending
+        self.slot[base + live : base + cap] = dead_list[: cap - live]
+        if extent > live:
+            for name, col in self.cols.items():
+                col[base + live : base + extent].fill_(self._fills[name])
+        # Forward rows: every unit; row u owns its in-edges' run.
+        fptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+        _lib.check(lib.plx_sorted_starts(live, self.cols[TO_ID.name][base:].data_ptr(), n, fptr.data_ptr(), k.s),
+                   "plx_sorted_starts")
+        self.fwd.append(ForwardRows(n, rows, fptr + base))
+        # Backward lists: the surviving entries (their positions remapped)
+        # merged with the new slots by (FROM_ID, slot).
+        old = prev.lists[b]
+        moved = torch.empty(max(old_live, 1), dtype=torch.int32, device=dev)
+        keep = torch.empty(max(old_live, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.plx_remap_i32(old_live, old.pos.data_ptr(), base, old_live, old_to_new.data_ptr(),
+                                     moved.data_ptr(), keep.data_ptr(), k.s), "plx_remap_i32")
+        lsurv, _ = k.compact(old_live, 0, keep)  # PLX_FLAG_U8: surviving entries, in list order
+        lorder = torch.empty(max(live, 1), dtype=torch.int32, device=dev)
+        m2 = _lib.plx_merge_desc()
+        _side(m2.a, nsurv, old_live, lsurv, old.src, old.slot, None)
+        _side(m2.b, nnew, cap, by_src, bucket[FROM_ID.name], None, None)
+        m2.offset, m2.order = 0, lorder.data_ptr()
+        _lib.check(lib.plx_merge_index(m2, k.s), "plx_merge_index")
+        pos = torch.full((live + 1,), base, dtype=torch.int32, device=dev)
+        ldst = torch.zeros(live + 1, dtype=torch.int32, device=dev)
+        lsrc = torch.zeros(max(live, 1), dtype=torch.int32, device=dev)
+        lslot = torch.zeros(max(live, 1), dtype=torch.int32, device=dev)
+        _gather(lib, k.s, live, lorder, by_src, nnew, old_live, cap,
+                [(moved, new_pos, pos, 4), (old.dst, bucket[TO_ID.name], ldst, 4),
+                 (old.src, bucket[FROM_ID.name], lsrc, 4), (old.slot, None, lslot, 4)])
+        lptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+        _lib.check(lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
+        self.lists.append(SourceLists(lptr, pos, ldst, lsrc, lslot))
 
     def src_table(self, b: int) -> tuple[int, int]:
         """No source-value tables: units keep the caller's ids."""
@@ -168,6 +290,39 @@ class ChurnArena(Arena):
             base, live = self.bases[b], self.lives[b]
             idx = self.slot[base : base + live].long()
             for name, col in bucket.items():
-                col[idx] = self.cols[name][base : base + live]
+                vals = self.cols[name][base : base + live]
                 if name == self.t_name and self.t_now and self.t_now[b] is not None:
-                    col[idx] = self.t_now[b]
+                    # Live edges hold the bucket's count; an edge tombstoned
+                    # since the layout keeps the count stamped at its kill.
+                    vals = torch.where(self.cols[DEAD.name][base : base + live] != 0, vals,
+                                       torch.tensor(self.t_now[b], dtype=vals.dtype, device=vals.device))
+                col[idx] = vals
+
+
+def _side(side, n: int, limit: int, ids: torch.Tensor, key1: torch.Tensor, key2: torch.Tensor | None,
+          out_map: torch.Tensor | None) -> None:
+    side.n, side.id_limit = int(n), int(limit)
+    side.ids, side.key1 = ids.data_ptr(), key1.data_ptr()
+    side.key2 = None if key2 is None else key2.data_ptr()
+    side.map = None if out_map is None else out_map.data_ptr()
+
+
+def _gather(lib, stream: int, n: int, order: torch.Tensor, b_ids: torch.Tensor, nb: int, a_limit: int,
+            b_limit: int, cols: list[tuple]) -> None:
+    """out[r] = a[order[r]] or b[b_ids[j]] per column (plx_merge_gather), in
+    launches of at most PLX_MERGE_MAX_COLS columns."""
+    if n == 0:
+        return
+    step = _lib.PLX_MERGE_MAX_COLS
+    for c0 in range(0, len(cols), step):
+        g = _lib.plx_merge_gather_desc()
+        g.n, g.order, g.b_ids, g.nb = int(n), order.data_ptr(), b_ids.data_ptr(), int(nb)
+        g.a_limit, g.b_limit = max(int(a_limit), 1), max(int(b_limit), 1)
+        part = cols[c0 : c0 + step]
+        g.ncols = len(part)
+        for j, (a, b, out, nbytes) in enumerate(part):
+            g.cols[j].a = a.data_ptr()
+            g.cols[j].b = None if b is None else b.data_ptr()
+            g.cols[j].out = out.data_ptr()
+            g.cols[j].bytes = int(nbytes)
+        _lib.check(lib.plx_merge_gather(g, stream), "plx_merge_gather")

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 19  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 20  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -295,6 +295,53 @@ class plx_tile_build_desc(ctypes.Structure):
     ]
 
 
+class plx_merge_side(ctypes.Structure):
+    _fields_ = [
+        ("n", c_i64),
+        ("id_limit", c_i64),
+        ("ids", c_vp),
+        ("key1", c_vp),
+        ("key2", c_vp),
+        ("map", c_vp),
+    ]
+
+
+class plx_merge_desc(ctypes.Structure):
+    _fields_ = [
+        ("a", plx_merge_side),
+        ("b", plx_merge_side),
+        ("offset", c_i64),
+        ("order", c_vp),
+    ]
+
+
+PLX_MERGE_MAX_COLS = 12
+
+
+class plx_merge_col(ctypes.Structure):
+    _fields_ = [
+        ("a", c_vp),
+        ("b", c_vp),
+        ("out", c_vp),
+        ("bytes", c_i32),
+        ("reserved", c_i32),
+    ]
+
+
+class plx_merge_gather_desc(ctypes.Structure):
+    _fields_ = [
+        ("n", c_i64),
+        ("order", c_vp),
+        ("b_ids", c_vp),
+        ("nb", c_i64),
+        ("a_limit", c_i64),
+        ("b_limit", c_i64),
+        ("ncols", c_i32),
+        ("reserved", c_i32),
+        ("cols", plx_merge_col * PLX_MERGE_MAX_COLS),
+    ]
+
+
 class plx_gen_fold_desc(ctypes.Structure):
     _fields_ = [
         ("prog", plx_site_prog),
@@ -474,6 +521,10 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_count_ids": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_batch_tile_limits": (c_i32, [c_vp, c_vp]),
     "plx_gen_fold": (c_i32, [ctypes.POINTER(plx_gen_fold_desc), c_vp]),
+    "plx_mark_u8": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "plx_merge_index": (c_i32, [ctypes.POINTER(plx_merge_desc), c_vp]),
+    "plx_merge_gather": (c_i32, [ctypes.POINTER(plx_merge_gather_desc), c_vp]),
+    "plx_remap_i32": (c_i32, [c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
@@ -502,6 +553,8 @@ STRUCTS = (
     plx_batch_tiles,
     plx_tile_build_desc,
     plx_gen_fold_desc,
+    plx_merge_desc,
+    plx_merge_gather_desc,
 )
 
 _lib: ctypes.CDLL | None = None

@@ -214,6 +214,99 @@ __global__ void k_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, 
   }
 }
 
+__global__ void k_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via,
+                          int64_t via_len, int64_t m, uint8_t* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n || (n_dev && i >= *n_dev)) return;
+  int64_t t = idx[i];
+  if (via) {
+    if (t < 0 || t >= via_len) return;
+    t = via[t];
+  }
+  if (t >= 0 && t < m) out[t] = 1;
+}
+
+// The (key1, key2) of id `id` of a merge side, as one 64-bit unsigned key;
+// ids are clamped into [0, id_limit) for the reads.
+__device__ __forceinline__ uint64_t merge_key(const plx_merge_side& s, int64_t id) {
+  id = id < 0 ? 0 : (id >= s.id_limit ? s.id_limit - 1 : id);
+  const uint32_t k1 = static_cast<uint32_t>(s.key1[id]);
+  const uint32_t k2 = s.key2 ? static_cast<uint32_t>(s.key2[id]) : static_cast<uint32_t>(id);
+  return (static_cast<uint64_t>(k1) << 32) | k2;
+}
+
+// The number of elements of `s` whose key is below `key` (or_equal: at most
+// `key`): a binary search over the side's sorted ids.
+__device__ __forceinline__ int64_t merge_count(const plx_merge_side& s, uint64_t key, bool or_equal) {
+  int64_t lo = 0, hi = s.n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    const uint64_t k = merge_key(s, s.ids[mid]);
+    if (k < key || (or_equal && k == key)) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// One thread per element of a, then of b: its merged rank is its rank in its
+// own side plus the other side's elements before it (a first on ties).
+__global__ void k_merge_index(plx_merge_desc d) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= d.a.n + d.b.n) return;
+  const bool in_a = t < d.a.n;
+  const plx_merge_side& own = in_a ? d.a : d.b;
+  const int64_t j = in_a ? t : t - d.a.n;
+  const int64_t id = own.ids[j];
+  const int64_t r = j + merge_count(in_a ? d.b : d.a, merge_key(own, id), !in_a);
+  if (d.order) d.order[r] = in_a ? static_cast<int32_t>(id) : static_cast<int32_t>(-1 - j);
+  if (own.map && id >= 0 && id < own.id_limit) own.map[id] = static_cast<int32_t>(r + d.offset);
+}
+
+__device__ __forceinline__ void merge_copy(const plx_merge_col& c, int64_t r, bool from_a, int64_t at,
+                                           int32_t id) {
+  if (c.bytes == 1) {
+    const uint8_t v = from_a ? static_cast<const uint8_t*>(c.a)[at]
+                             : (c.b ? static_cast<const uint8_t*>(c.b)[at] : static_cast<uint8_t>(id));
+    static_cast<uint8_t*>(c.out)[r] = v;
+  } else {
+    const uint32_t v = from_a ? static_cast<const uint32_t*>(c.a)[at]
+                              : (c.b ? static_cast<const uint32_t*>(c.b)[at] : static_cast<uint32_t>(id));
+    static_cast<uint32_t*>(c.out)[r] = v;
+  }
+}
+
+// One thread per merged rank; each column's element comes from a (by the
+// id in `order`) or from b (by the id in b_ids).
+__global__ void k_merge_gather(plx_merge_gather_desc d) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= d.n) return;
+  const int32_t o = d.order[r];
+  // Every index is clamped into its array (a malformed order reads a wrong
+  // element rather than outside the buffers).
+  const bool from_a = o >= 0 || d.nb == 0;
+  int64_t at;
+  int32_t id = 0;
+  if (from_a) {
+    at = o < 0 ? 0 : (o < d.a_limit ? o : d.a_limit - 1);
+  } else {
+    int64_t j = -1 - static_cast<int64_t>(o);
+    j = j < d.nb ? j : d.nb - 1;
+    id = d.b_ids[j];
+    at = id < 0 ? 0 : (id >= d.b_limit ? d.b_limit - 1 : id);
+  }
+  for (int k = 0; k < d.ncols; ++k) merge_copy(d.cols[k], r, from_a, at, id);
+}
+
+__global__ void k_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
+                            int32_t* out, uint8_t* live) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int64_t p = static_cast<int64_t>(idx[j]) - off;
+  const int32_t m = (p >= 0 && p < map_len) ? map[p] : -1;
+  out[j] = m;
+  live[j] = m >= 0;
+}
+
 unsigned grid_of(int64_t n, int block) {
   const int64_t g = (n + block - 1) / block;
   return static_cast<unsigned>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -254,6 +347,61 @@ int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const i
   hipLaunchKernelGGL(k_cold_slots, dim3(grid_of(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream), n, n_dev,
                      cold, g_src, g_st, g_tile, hl, off, region, sb_of_tile, cold_idx, cold_sb);
   return check_launch("plx_cold_slots");
+}
+
+int plx_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via, int64_t via_len,
+                int64_t m, uint8_t* out, void* stream) {
+  if (n < 0 || m < 0 || via_len < 0) return fail(PLX_ERR_INVALID, "plx_mark_u8: negative size");
+  if (n == 0) return PLX_OK;
+  if (!idx || !out) return fail(PLX_ERR_INVALID, "plx_mark_u8: null pointer");
+  hipLaunchKernelGGL(k_mark_u8, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n, n_dev, idx, via, via_len, m, out);
+  return check_launch("plx_mark_u8");
+}
+
+static bool merge_side_ok(const plx_merge_side& s) {
+  if (s.n < 0 || s.id_limit < 0) return false;
+  if (s.n == 0) return true;
+  return s.ids && s.key1 && s.id_limit > 0;
+}
+
+int plx_merge_index(const plx_merge_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_merge_index: null descriptor");
+  if (!merge_side_ok(d->a) || !merge_side_ok(d->b)) return fail(PLX_ERR_INVALID, "plx_merge_index: bad side");
+  const int64_t n = d->a.n + d->b.n;
+  if (n > INT32_MAX || d->offset < 0 || d->offset + n > INT32_MAX)
+    return fail(PLX_ERR_INVALID, "plx_merge_index: ranks exceed int32");
+  if (n == 0) return PLX_OK;
+  hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *d);
+  return check_launch("plx_merge_index");
+}
+
+int plx_merge_gather(const plx_merge_gather_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_merge_gather: null descriptor");
+  if (d->n < 0 || d->nb < 0 || d->ncols < 0 || d->ncols > PLX_MERGE_MAX_COLS)
+    return fail(PLX_ERR_INVALID, "plx_merge_gather: bad sizes");
+  if (d->n == 0 || d->ncols == 0) return PLX_OK;
+  if (!d->order || d->a_limit <= 0 || (d->nb > 0 && (!d->b_ids || d->b_limit <= 0)))
+    return fail(PLX_ERR_INVALID, "plx_merge_gather: null order or empty side");
+  for (int k = 0; k < d->ncols; ++k) {
+    const plx_merge_col& c = d->cols[k];
+    if (!c.a || !c.out || (c.bytes != 1 && c.bytes != 4))
+      return fail(PLX_ERR_INVALID, "plx_merge_gather: bad column");
+  }
+  hipLaunchKernelGGL(k_merge_gather, dim3(static_cast<unsigned>((d->n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *d);
+  return check_launch("plx_merge_gather");
+}
+
+int plx_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map, int32_t* out,
+                  uint8_t* live, void* stream) {
+  if (n < 0 || map_len < 0) return fail(PLX_ERR_INVALID, "plx_remap_i32: negative size");
+  if (n == 0) return PLX_OK;
+  if (!idx || !map || !out || !live) return fail(PLX_ERR_INVALID, "plx_remap_i32: null pointer");
+  hipLaunchKernelGGL(k_remap_i32, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n, idx, off, map_len, map, out, live);
+  return check_launch("plx_remap_i32");
 }
 
 int plx_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts, void* stream) {

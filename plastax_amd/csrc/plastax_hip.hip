@@ -1999,10 +1999,10 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 19; }
+int32_t plx_abi_version(void) { return 20; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
-  const int64_t sizes[18] = {
+  const int64_t sizes[20] = {
       sizeof(plx_program),          sizeof(plx_finalize),
       sizeof(plx_forward_desc),     sizeof(plx_tile_desc),
       sizeof(plx_partials_desc),    sizeof(plx_update_desc),
@@ -2011,9 +2011,10 @@ int plx_struct_sizes(int64_t* out, int32_t n) {
       sizeof(plx_grow_filter_desc), sizeof(plx_grow_col),
       sizeof(plx_grow_claim_desc),  sizeof(plx_unit_col),
       sizeof(plx_bwd_batch_desc),   sizeof(plx_batch_tiles),
-      sizeof(plx_tile_build_desc),  sizeof(plx_gen_fold_desc)};
-  for (int32_t k = 0; k < n && k < 18; ++k) out[k] = sizes[k];
-  return 18;
+      sizeof(plx_tile_build_desc),  sizeof(plx_gen_fold_desc),
+      sizeof(plx_merge_desc),       sizeof(plx_merge_gather_desc)};
+  for (int32_t k = 0; k < n && k < 20; ++k) out[k] = sizes[k];
+  return 20;
 }
 
 int plx_forward_bucket(const plx_forward_desc* d, void* stream) {

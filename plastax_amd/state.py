@@ -121,6 +121,9 @@ class NetworkState:
         self.tail_start = tail_start
         self._arena: Any = None  # plastax_amd._layout.Arena once a step ran
         self._arena_ahead = False  # the arena holds newer conn values
+        # The churn layout a growth step replaced: the next layout is merged
+        # from it (plastax_amd/_churn.py) instead of built from scratch.
+        self._arena_prev: Any = None
         self._units_phys = False  # _units are in the arena's unit order
         self._units_view: Columns | None = None  # cached caller-order view
         self._donated = False
@@ -149,6 +152,7 @@ class NetworkState:
         )
         new._arena = self._arena
         new._arena_ahead = self._arena_ahead
+        new._arena_prev = self._arena_prev
         new._units_phys = self._units_phys
         self._donated = True
         return new
@@ -202,6 +206,7 @@ class NetworkState:
         self._conns = tuple(dict(b) for b in value)
         self._arena = None  # structure or values changed on the host side
         self._arena_ahead = False
+        self._arena_prev = None
 
     @property
     def device(self) -> torch.device:

@@ -121,6 +121,10 @@ class StepFn:
         # Where the tiled layout is built: "device" (plastax_amd._layout_dev)
         # or "host" (plastax_amd._layout, numpy); the tables are equal.
         self.layout_build: str = "device"
+        # How the churn layout follows a growth step: "merge" (the claimed
+        # slots merged into the previous layout) or "full" (built again from
+        # the logical buckets); the layouts are equal.
+        self.relayout: str = "merge"
         # Unit and structural phases, traced on the first step (their
         # programs read the globals' structure).
         self._update_unit: Any = None
@@ -187,8 +191,11 @@ class StepFn:
             if self.churn():
                 from plastax_amd._churn import ChurnArena
 
+                prev, state._arena_prev = state._arena_prev, None
+                if self.relayout not in ("merge", "full"):
+                    raise ValueError(f"relayout must be 'merge' or 'full', got {self.relayout!r}")
                 state._arena = ChurnArena(self.static, state.units, state._conns, state.device,
-                                          _stream(state.device))
+                                          _stream(state.device), prev=prev if self.relayout == "merge" else None)
             elif self.layout_build == "device":
                 from plastax_amd._layout_dev import DeviceArena
 
@@ -391,7 +398,10 @@ class StepFn:
                 return
             out = phase.run(k, state.units, state.conns, step=int(state.step), globals_=g,
                             tail_start=int(state.tail_start), units_added=int(state.units_added))
+            prev = state._arena
             state.conns = out.conns
+            if getattr(prev, "churn", False):
+                state._arena_prev = prev  # the next layout merges the claimed slots into prev's
             state.grown, state.overflow = out.grown, out.overflow
             state.needs_resort = bool(state.needs_resort) or out.needs_resort
             state.tail_start = out.tail_start

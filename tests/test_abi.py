@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_descriptor_layouts_match_the_header(lib) -> None:
     n = len(_lib.STRUCTS)
     out = (ctypes.c_int64 * n)()
-    assert lib.plx_struct_sizes(out, n) == n == 18
+    assert lib.plx_struct_sizes(out, n) == n == 20
     assert list(out) == [ctypes.sizeof(s) for s in _lib.STRUCTS]
     assert lib.plx_abi_version() == _lib.ABI_VERSION
 
