@@ -319,7 +319,8 @@ PLX_EXPORT int plx_forward_batch(const plx_forward_desc* d, int32_t batch, void*
  * that order from the identity, combined into acc (null: the identity) and,
  * where the row finalizes, `apply` runs (fields and outs batched) and acc
  * resets. The lists are slot-ordered copies of the arena's columns
- * (plx_gather_edges). */
+ * (plx_gather_edges); a factor the map holds constant (plx_map flags) is
+ * not loaded, so its copy need not exist. */
 typedef struct plx_bwd_batch_desc {
   int32_t nrows;
   int32_t monoid;
@@ -345,8 +346,9 @@ PLX_EXPORT int plx_backward_batch(const plx_bwd_batch_desc* d, void* stream);
  * churn layout, which rebuilds on the device after every structural change. */
 PLX_EXPORT int plx_backward_lists(const plx_bwd_batch_desc* d, void* stream);
 
-/* out_weight[j] = weight[pos[j]], out_live[j] = !dead[pos[j]] for j < n
- * (dead null: all live): a bucket's backward lists in slot order. */
+/* out_weight[j] = weight[pos[j]] (out_weight optional), out_live[j] =
+ * !dead[pos[j]] (out_live optional; dead null: all live) for j < n: a
+ * bucket's backward lists in slot order. */
 PLX_EXPORT int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const uint8_t* dead,
                                 float* out_weight, uint8_t* out_live, void* stream);
 
@@ -958,12 +960,6 @@ PLX_EXPORT int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* co
  * (the reference's resort, topo.py:303-452, a stable sort of every live
  * slot) would give, for the cost of one pass over the columns. */
 
-/* out[t] = 1 for t = via ? via[idx[i]] : idx[i], i < n (count n_dev,
- * optional; via, when given, has via_len entries and idx values outside it
- * are skipped), t in [0, m). */
-PLX_EXPORT int plx_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via,
-                           int64_t via_len, int64_t m, uint8_t* out, void* stream);
-
 /* One side of a merge: n elements whose ids (in [0, id_limit)) are listed
  * in ascending (key1[id], key2[id]) order, keys compared as uint32; key2
  * null means the id itself. map (optional, id_limit entries) receives each
@@ -979,7 +975,9 @@ typedef struct plx_merge_side {
 
 /* Merges a and b (a first where keys are equal): order[r] (optional,
  * a.n + b.n entries) is a's id at merged rank r, or -1 - j for b's j-th
- * element. */
+ * element. One thread per element of a searches b; b is meant to be the
+ * short side (the claimed slots), each of its elements written by the
+ * thread of the a element it precedes. */
 typedef struct plx_merge_desc {
   plx_merge_side a;
   plx_merge_side b;

@@ -65,7 +65,8 @@ class ChurnArena(Arena):
     churn = True
 
     def __init__(self, static: NetworkStatic, units: Columns, conns: tuple[Columns, ...],
-                 device: torch.device, stream: int, prev: "ChurnArena | None" = None) -> None:
+                 device: torch.device, stream: int, prev: "ChurnArena | None" = None,
+                 dead_before: list[torch.Tensor] | None = None) -> None:
         from plastax_amd.grow import Kernels
 
         self.static = static
@@ -106,7 +107,7 @@ class ChurnArena(Arena):
         size = total + PAD
         specs = {s.name: s for s in static.conn_fields}
         self._fills = {name: (1 if name == DEAD.name else spec.default) for name, spec in specs.items()}
-        if prev is not None and not self.can_follow(prev, static, caps):
+        if prev is not None and (dead_before is None or not self.can_follow(prev, static, caps)):
             prev = None
         if prev is not None and prev._spare is not None:
             # the other buffer: fill values past `extent` in every bucket
@@ -119,6 +120,8 @@ class ChurnArena(Arena):
             extent = [0] * nb
         self._spare = None if prev is None else (prev.cols, prev.slot, prev._extent)
         self.merged = prev is not None
+        # Columns written since the logical view was last in step (None: any).
+        self._written: set | None = set()
         self.lives = []
         self.fwd = []
         self.bwd = []
@@ -135,7 +138,8 @@ class ChurnArena(Arena):
         rows = torch.arange(n, dtype=torch.int32, device=device)
         for b, bucket in enumerate(conns):
             if prev is not None:
-                self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b])
+                self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b],
+                                   None if dead_before is None else dead_before[b])
                 continue
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
@@ -200,10 +204,13 @@ class ChurnArena(Arena):
         self._spare = None
 
     def _merge_bucket(self, k, b: int, prev: "ChurnArena", bucket: Columns, specs: dict, nbits: int,
-                      rows: torch.Tensor, extent: int) -> None:
+                      rows: torch.Tensor, extent: int, dead_before: torch.Tensor) -> None:
         """Bucket b laid out from ``prev``'s layout of it (see the module
         docstring): the survivors (prev's live positions whose DEAD is still
-        0) merged with the live slots that no survivor holds."""
+        0) merged with the slots the claim turned live (``dead_before``: DEAD
+        just before the claim, after the step's prunes were copied back).
+        Nothing else changes the logical bucket in between, so these are all
+        of its live slots."""
         dev = self.device
         n = self.static.num_units
         base, cap = self.bases[b], self.caps[b]
@@ -216,12 +223,10 @@ class ChurnArena(Arena):
             t_col.masked_fill_(prev.cols[DEAD.name][base : base + old_live] == 0, float(prev.t_now[b]))
         # Survivors: prev's live positions still live, in (destination, slot) order.
         surv, nsurv_d = k.compact(old_live, 1, prev.cols[DEAD.name][base:])  # PLX_FLAG_U8_ZERO
-        # New: the slots live in the logical bucket that no survivor holds
-        # (claimed this step, possibly a slot that died and was claimed again).
-        mark = bucket[DEAD.name].clone()
-        _lib.check(lib.plx_mark_u8(old_live, nsurv_d.data_ptr(), surv.data_ptr(), prev.slot[base:].data_ptr(),
-                                   old_live, cap, mark.data_ptr(), k.s), "plx_mark_u8")
-        fresh, nnew_d = k.compact(cap, 1, mark)  # PLX_FLAG_U8_ZERO: ascending slots
+        # New: the slots the claim filled (a slot that died this step may be
+        # among them: its old position is not a survivor).
+        claimed = (dead_before != 0) & (bucket[DEAD.name] == 0)
+        fresh, nnew_d = k.compact(cap, 0, claimed)  # PLX_FLAG_U8: ascending slots
         counts = torch.cat([nsurv_d, nnew_d]).cpu().tolist()  # the rebuild's host read (as the full build's)
         nsurv, nnew = int(counts[0]), int(counts[1])
         live = nsurv + nnew
@@ -283,13 +288,24 @@ class ChurnArena(Arena):
         """No source-value tables: units keep the caller's ids."""
         return 0, 0
 
+    def wrote(self, columns=None) -> None:
+        if columns is None or self._written is None:
+            self._written = None
+        else:
+            self._written |= {c for c in columns if c is not None}
+
     def write_logical(self, conns: tuple[Columns, ...]) -> None:
         """Scatter the live part of every bucket back into its logical slots
-        (the slots dead at layout time were never written by the step)."""
+        (the slots dead at layout time were never written by the step): the
+        columns a step wrote since the last such copy (a prune: DEAD and the
+        step count it stamps), or all of them."""
+        written, self._written = self._written, set()
         for b, bucket in enumerate(conns):
             base, live = self.bases[b], self.lives[b]
             idx = self.slot[base : base + live].long()
             for name, col in bucket.items():
+                if written is not None and name not in written:
+                    continue
                 vals = self.cols[name][base : base + live]
                 if name == self.t_name and self.t_now and self.t_now[b] is not None:
                     # Live edges hold the bucket's count; an edge tombstoned

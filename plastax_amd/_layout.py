@@ -554,6 +554,10 @@ class Arena:
                     col[idx[: self.lives[b]]] = torch.where(self.cols[DEAD.name][live] != 0, self.cols[name][live],
                                                             self.t_now[b])
 
+    def wrote(self, columns: Any = None) -> None:
+        """A step wrote ``columns`` (None: any) of this arena; write_logical
+        copies every column back regardless."""
+
     def init_uniform_t(self, t_name: str) -> None:
         """Adam's per-edge step count: where every live edge of a bucket holds
         the same integer count below 2^23 (each step adds exactly 1.0 to

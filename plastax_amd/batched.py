@@ -319,10 +319,10 @@ class BatchedStepFn(StepFn):
         if up is not None:
             for b in range(arena.num_buckets):
                 self._update_batch(plan, arena, ub, consts, b, stream)
-            state._arena_ahead = True
+            state._mark_ahead()
         if plan.update_generic:
             self._mean_of_writes(arena, ub, g, stream)
-            state._arena_ahead = True
+            state._mark_ahead()
 
         # reduce_batch_units (phases.py:298-332): the written columns only.
         for name, red in reductions.items():

@@ -214,18 +214,6 @@ __global__ void k_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, 
   }
 }
 
-__global__ void k_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via,
-                          int64_t via_len, int64_t m, uint8_t* out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n || (n_dev && i >= *n_dev)) return;
-  int64_t t = idx[i];
-  if (via) {
-    if (t < 0 || t >= via_len) return;
-    t = via[t];
-  }
-  if (t >= 0 && t < m) out[t] = 1;
-}
-
 // The (key1, key2) of id `id` of a merge side, as one 64-bit unsigned key;
 // ids are clamped into [0, id_limit) for the reads.
 __device__ __forceinline__ uint64_t merge_key(const plx_merge_side& s, int64_t id) {
@@ -248,18 +236,65 @@ __device__ __forceinline__ int64_t merge_count(const plx_merge_side& s, uint64_t
   return lo;
 }
 
-// One thread per element of a, then of b: its merged rank is its rank in its
-// own side plus the other side's elements before it (a first on ties).
-__global__ void k_merge_index(plx_merge_desc d) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= d.a.n + d.b.n) return;
-  const bool in_a = t < d.a.n;
-  const plx_merge_side& own = in_a ? d.a : d.b;
-  const int64_t j = in_a ? t : t - d.a.n;
-  const int64_t id = own.ids[j];
-  const int64_t r = j + merge_count(in_a ? d.b : d.a, merge_key(own, id), !in_a);
-  if (d.order) d.order[r] = in_a ? static_cast<int32_t>(id) : static_cast<int32_t>(-1 - j);
-  if (own.map && id >= 0 && id < own.id_limit) own.map[id] = static_cast<int32_t>(r + d.offset);
+__device__ __forceinline__ void merge_put(const plx_merge_desc& d, const plx_merge_side& s, int64_t r,
+                                          int32_t code, int64_t id) {
+  if (d.order) d.order[r] = code;
+  if (s.map && id >= 0 && id < s.id_limit) s.map[id] = static_cast<int32_t>(r + d.offset);
+}
+
+constexpr int kMergeBlock = 256;
+constexpr int kMergeStaged = 2048;  // b keys staged in LDS (16 KiB); a longer b is searched in global memory
+
+// The number of the n keys of `keys` (ascending, in LDS) below `key`.
+__device__ __forceinline__ int64_t lds_count(const uint64_t* keys, int64_t n, uint64_t key) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// One thread per element i of a (a is the long side: the survivors). With
+// c(i) the number of b elements below a's i-th key (a first on ties), a_i
+// lands at i + c(i), and b_j for c(i-1) <= j < c(i) lands just before it,
+// at j + i; the last thread places the b elements after every a. Each
+// thread searches only b (its keys staged in LDS), and takes c(i-1) from
+// its neighbour lane. With a empty, b_j lands at j.
+__global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
+  __shared__ uint64_t bkey[kMergeStaged];
+  __shared__ int64_t cnt[kMergeBlock];
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kMergeBlock + threadIdx.x;
+  if (d.a.n == 0) {  // uniform over the grid
+    if (t < d.b.n) merge_put(d, d.b, t, static_cast<int32_t>(-1 - t), d.b.ids[t]);
+    return;
+  }
+  const bool staged = d.b.n <= kMergeStaged;
+  if (staged)
+    for (int64_t j = threadIdx.x; j < d.b.n; j += kMergeBlock) bkey[j] = merge_key(d.b, d.b.ids[j]);
+  __syncthreads();
+  const bool valid = t < d.a.n;
+  const int64_t id = valid ? d.a.ids[t] : 0;
+  int64_t c = 0;
+  if (valid) {
+    const uint64_t key = merge_key(d.a, id);
+    c = staged ? lds_count(bkey, d.b.n, key) : merge_count(d.b, key, false);
+  }
+  cnt[threadIdx.x] = c;
+  __syncthreads();
+  if (!valid) return;
+  merge_put(d, d.a, t + c, static_cast<int32_t>(id), id);
+  int64_t c0 = 0;
+  if (threadIdx.x > 0) {
+    c0 = cnt[threadIdx.x - 1];
+  } else if (t > 0) {
+    const uint64_t key = merge_key(d.a, d.a.ids[t - 1]);
+    c0 = staged ? lds_count(bkey, d.b.n, key) : merge_count(d.b, key, false);
+  }
+  for (int64_t j = c0; j < c; ++j) merge_put(d, d.b, j + t, static_cast<int32_t>(-1 - j), d.b.ids[j]);
+  if (t == d.a.n - 1)
+    for (int64_t j = c; j < d.b.n; ++j) merge_put(d, d.b, j + d.a.n, static_cast<int32_t>(-1 - j), d.b.ids[j]);
 }
 
 __device__ __forceinline__ void merge_copy(const plx_merge_col& c, int64_t r, bool from_a, int64_t at,
@@ -349,16 +384,6 @@ int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const i
   return check_launch("plx_cold_slots");
 }
 
-int plx_mark_u8(int64_t n, const int32_t* n_dev, const int32_t* idx, const int32_t* via, int64_t via_len,
-                int64_t m, uint8_t* out, void* stream) {
-  if (n < 0 || m < 0 || via_len < 0) return fail(PLX_ERR_INVALID, "plx_mark_u8: negative size");
-  if (n == 0) return PLX_OK;
-  if (!idx || !out) return fail(PLX_ERR_INVALID, "plx_mark_u8: null pointer");
-  hipLaunchKernelGGL(k_mark_u8, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), n, n_dev, idx, via, via_len, m, out);
-  return check_launch("plx_mark_u8");
-}
-
 static bool merge_side_ok(const plx_merge_side& s) {
   if (s.n < 0 || s.id_limit < 0) return false;
   if (s.n == 0) return true;
@@ -372,8 +397,9 @@ int plx_merge_index(const plx_merge_desc* d, void* stream) {
   if (n > INT32_MAX || d->offset < 0 || d->offset + n > INT32_MAX)
     return fail(PLX_ERR_INVALID, "plx_merge_index: ranks exceed int32");
   if (n == 0) return PLX_OK;
-  hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), *d);
+  const int64_t threads = d->a.n > 0 ? d->a.n : d->b.n;
+  hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((threads + kMergeBlock - 1) / kMergeBlock)),
+                     dim3(kMergeBlock), 0, static_cast<hipStream_t>(stream), *d);
   return check_launch("plx_merge_index");
 }
 

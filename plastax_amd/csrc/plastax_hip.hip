@@ -1479,6 +1479,10 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_lists(plx_bwd_batch_de
   const int u = d.row_unit[r];
   const int j0 = d.row_ptr[r], j1 = d.row_ptr[r + 1];
   RowPre pre = prefetch_row(d.row_unit, r, d.fin, d.apply);
+  // A constant factor of the map is not loaded (uniform branches): a count
+  // pass (both factors constant) reads only liveness, or nothing.
+  const bool need_w = !(d.map.flags & PLX_MAP_W_CONST);
+  const bool need_x = !(d.map.flags & PLX_MAP_X_CONST);
   float s = Mono<M>::id();
   int j = j0;
   for (; j + 4 <= j1; j += 4) {
@@ -1487,19 +1491,19 @@ __global__ __launch_bounds__(kBatchBlock) void k_backward_lists(plx_bwd_batch_de
     bool live[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      tv[k] = d.dst[j + k];
-      wv[k] = d.weight[j + k];
+      tv[k] = need_x ? d.dst[j + k] : 0;
+      wv[k] = need_w ? d.weight[j + k] : 0.0f;
       live[k] = d.live ? d.live[j + k] != 0 : true;
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) gv[k] = d.g[tv[k]];
+    for (int k = 0; k < 4; ++k) gv[k] = need_x ? d.g[tv[k]] : 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       if (live[k]) s = Mono<M>::op(s, map_term(d.map, wv[k], gv[k]));
   }
   for (; j < j1; ++j) {
     if (d.live && !d.live[j]) continue;
-    s = Mono<M>::op(s, map_term(d.map, d.weight[j], d.g[d.dst[j]]));
+    s = Mono<M>::op(s, map_term(d.map, need_w ? d.weight[j] : 0.0f, need_x ? d.g[d.dst[j]] : 0.0f));
   }
   const float a = Mono<M>::op(d.acc ? d.acc[u] : Mono<M>::id(), s);
   if (pre.fin) {
@@ -1515,7 +1519,7 @@ __global__ void k_gather_edges(int64_t n, const int32_t* pos, const float* weigh
   const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (j >= n) return;
   const int p = pos[j];
-  out_w[j] = weight[p];
+  if (out_w) out_w[j] = weight[p];
   if (out_live) out_live[j] = dead ? (dead[p] == 0) : 1;
 }
 
@@ -2336,7 +2340,7 @@ int plx_gather_edges(int64_t n, const int32_t* pos, const float* weight, const u
                      float* out_weight, uint8_t* out_live, void* stream) {
   if (n < 0) return fail(PLX_ERR_INVALID, "plx_gather_edges: negative n");
   if (n == 0) return PLX_OK;
-  if (!pos || !weight || !out_weight) return fail(PLX_ERR_INVALID, "plx_gather_edges: null pointer");
+  if (!pos || (out_weight && !weight)) return fail(PLX_ERR_INVALID, "plx_gather_edges: null pointer");
   k_gather_edges<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(n, pos, weight, dead,
                                                                                   out_weight, out_live);
   return check_launch("plx_gather_edges");

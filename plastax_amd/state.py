@@ -157,6 +157,14 @@ class NetworkState:
         self._donated = True
         return new
 
+    def _mark_ahead(self, columns: Any = None) -> None:
+        """The step wrote connection values into the arena: ``columns`` (a
+        set of column names) or every column (None). The logical view is
+        synchronised from the arena on its next access."""
+        self._arena_ahead = True
+        if self._arena is not None:
+            self._arena.wrote(columns)
+
     def _physical_units(self, arena: Any) -> Columns:
         """The unit columns in ``arena``'s unit order (converted once); the
         step updates them in place, so the caller-order view is dropped."""

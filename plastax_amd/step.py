@@ -22,7 +22,7 @@ from plastax_amd import _lib
 from plastax_amd._expr import UnsupportedPolicyError
 from plastax_amd._layout import NSUPER, TILE, Arena
 from plastax_amd._plan import Plan, compile_plan, program_struct
-from plastax_amd._types import ACTIVATION, Propagation
+from plastax_amd._types import ACTIVATION, DEAD, Propagation
 from plastax_amd.fusion import PruneFusionPlan, PruneFusionRecord, plan_prune_fusion
 from plastax_amd.state import NetworkState, NetworkStatic
 
@@ -194,8 +194,10 @@ class StepFn:
                 prev, state._arena_prev = state._arena_prev, None
                 if self.relayout not in ("merge", "full"):
                     raise ValueError(f"relayout must be 'merge' or 'full', got {self.relayout!r}")
+                if prev is None or self.relayout == "full":
+                    prev = (None, None)
                 state._arena = ChurnArena(self.static, state.units, state._conns, state.device,
-                                          _stream(state.device), prev=prev if self.relayout == "merge" else None)
+                                          _stream(state.device), prev=prev[0], dead_before=prev[1])
             elif self.layout_build == "device":
                 from plastax_amd._layout_dev import DeviceArena
 
@@ -328,7 +330,7 @@ class StepFn:
         # update needs only finalized grads (levels > b) and activations.
         self._backward_update(plan, arena, units, consts, fin_common, stream, g)
         if plan.update is not None or plan.update_generic:
-            state._arena_ahead = True
+            state._mark_ahead()
 
         # Structural phases (phases.py:1245-1498, :4490-5203).
         if plan.prune_unit or plan.prune_conn or plan.add_unit or plan.add_conn is not None:
@@ -358,7 +360,7 @@ class StepFn:
             # Whether anything died stays on the device: from here on the
             # kernels read DEAD inside the live ranges.
             arena.dead_in_rows = True
-            state._arena_ahead = True
+            state._mark_ahead({DEAD.name, arena.t_name})  # tombstones and their stamped step counts
         if plan.prune_conn:
             if self._prune is None:
                 self._prune = grow.PruneConnPhase(plan.net, self.static, g)
@@ -372,7 +374,7 @@ class StepFn:
             if timer is not None:
                 timer.end("prune_conn")
             arena.dead_in_rows = True
-            state._arena_ahead = True
+            state._mark_ahead({DEAD.name, arena.t_name})
         if plan.add_unit:
             if self._add_unit is None:
                 self._add_unit = unit_phases.AddUnitPhase(plan.net, self.static, g)
@@ -396,12 +398,17 @@ class StepFn:
             if not fires:
                 state.grown, state.overflow = 0, False
                 return
-            out = phase.run(k, state.units, state.conns, step=int(state.step), globals_=g,
-                            tail_start=int(state.tail_start), units_added=int(state.units_added))
+            conns = state.conns  # the logical view, in step with the arena
             prev = state._arena
-            state.conns = out.conns
+            before = None
             if getattr(prev, "churn", False):
-                state._arena_prev = prev  # the next layout merges the claimed slots into prev's
+                # DEAD before the claim: the claimed slots are the ones it turns live
+                before = [bucket[DEAD.name].clone() for bucket in conns]
+            out = phase.run(k, state.units, conns, step=int(state.step), globals_=g,
+                            tail_start=int(state.tail_start), units_added=int(state.units_added))
+            state.conns = out.conns
+            if before is not None:
+                state._arena_prev = (prev, before)  # the next layout merges the claimed slots into prev's
             state.grown, state.overflow = out.grown, out.overflow
             state.needs_resort = bool(state.needs_resort) or out.needs_resort
             state.tail_start = out.tail_start
@@ -718,14 +725,19 @@ class StepFn:
                 d.weight = acc.data_ptr()
                 d.live = None
             else:
-                _lib.check(lib.plx_gather_edges(lists.pos.numel(), lists.pos.data_ptr(),
-                                                arena.cols["weight"].data_ptr(), arena.cols["dead"].data_ptr(),
-                                                lists.weight.data_ptr(), lists.live.data_ptr(), stream),
-                           "plx_gather_edges")
+                # Only what the pass reads: the weights unless the map holds
+                # them constant, liveness while tombstones sit in the lists.
+                need_w = bp.w_const is None
+                need_live = arena.dead_in_rows
+                if need_w or need_live:
+                    _lib.check(lib.plx_gather_edges(
+                        lists.pos.numel(), lists.pos.data_ptr(), arena.cols["weight"].data_ptr(),
+                        arena.cols["dead"].data_ptr(), lists.weight.data_ptr() if need_w else None,
+                        lists.live.data_ptr() if need_live else None, stream), "plx_gather_edges")
                 d.row_ptr = lists.ptr.data_ptr()
                 d.dst = lists.dst.data_ptr()
                 d.weight = lists.weight.data_ptr()
-                d.live = lists.live.data_ptr()
+                d.live = lists.live.data_ptr() if need_live else None
             d.g = bp.gathered(units, ACTIVATION.name).data_ptr()
             d.map = bp.map_struct()
             d.acc = acc.data_ptr()

@@ -1,0 +1,119 @@
+"""plx_merge_index / plx_merge_gather / plx_remap_i32 through the C ABI
+against numpy: two sorted id lists merged by (key1, key2) (a first on equal
+keys), the order and both maps; a multi-column gather from the two sides;
+short b (keys staged in LDS) and long b (searched in global memory), empty
+sides, ties across the sides."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from plastax_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def _t(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _side(side, ids, k1, k2, out_map, limit):
+    side.n, side.id_limit = int(ids.numel()), int(limit)
+    side.ids, side.key1 = ids.data_ptr(), k1.data_ptr()
+    side.key2 = None if k2 is None else k2.data_ptr()
+    side.map = None if out_map is None else out_map.data_ptr()
+
+
+def _case(rng, na: int, nb: int, limit: int, nkeys: int, ties: bool):
+    """Ids sorted by (key1, key2 = slot-like unique values)."""
+    key1 = rng.integers(0, nkeys, limit).astype(np.int32)
+    key2 = rng.permutation(limit).astype(np.int32)
+    ids = rng.permutation(limit)
+    a_ids = np.sort(ids[:na])
+    b_ids = np.sort(ids[na : na + nb])
+    a_ids = a_ids[np.lexsort((key2[a_ids], key1[a_ids]))].astype(np.int32)
+    b_key2 = key2.copy()
+    if ties and na and nb:  # b's first element takes a's first element's key
+        b_key2[b_ids[0]] = key2[a_ids[0]]
+        key1_b = key1.copy()
+        key1_b[b_ids[0]] = key1[a_ids[0]]
+    else:
+        key1_b = key1
+    b_ids = b_ids[np.lexsort((b_key2[b_ids], key1_b[b_ids]))].astype(np.int32)
+    return key1, key2, key1_b, b_key2, a_ids, b_ids
+
+
+@pytest.mark.parametrize(("na", "nb"), [(5000, 37), (5000, 3000), (0, 100), (4000, 0), (1, 1), (300, 2048),
+                                        (257, 2049)])
+@pytest.mark.parametrize("ties", [False, True])
+def test_merge_index_and_gather(na: int, nb: int, ties: bool) -> None:
+    lib = _lib.load()
+    rng = np.random.default_rng(na * 7 + nb + ties)
+    limit = na + nb + 64
+    k1, k2, k1b, k2b, a_ids, b_ids = _case(rng, na, nb, limit, max(4, limit // 9), ties)
+    # expected: a first where keys are equal
+    keys = [((int(k1[i]) & 0xFFFFFFFF) << 32 | (int(k2[i]) & 0xFFFFFFFF), 0, r, int(i)) for r, i in enumerate(a_ids)]
+    keys += [((int(k1b[i]) & 0xFFFFFFFF) << 32 | (int(k2b[i]) & 0xFFFFFFFF), 1, r, int(i))
+             for r, i in enumerate(b_ids)]
+    keys.sort()
+    want_order = np.asarray([i if side == 0 else -1 - r for _, side, r, i in keys], dtype=np.int32)
+    n = na + nb
+    order = torch.full((max(n, 1),), 7777, dtype=torch.int32, device=DEV)
+    map_a = torch.full((limit,), -1, dtype=torch.int32, device=DEV)
+    map_b = torch.full((limit,), -1, dtype=torch.int32, device=DEV)
+    ta, tb = _t(a_ids), _t(b_ids)
+    m = _lib.plx_merge_desc()
+    _side(m.a, ta, _t(k1), _t(k2), map_a, limit)
+    _side(m.b, tb, _t(k1b), _t(k2b), map_b, limit)
+    m.offset, m.order = 100, order.data_ptr()
+    assert lib.plx_merge_index(m, None) == 0, lib.plx_last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(order.cpu().numpy()[:n], want_order)
+    ma, mb = map_a.cpu().numpy(), map_b.cpu().numpy()
+    for r, (_, side, _, i) in enumerate(keys):
+        assert (ma if side == 0 else mb)[i] == r + 100
+    # gather: a 4-byte column, a 1-byte column, b's id itself
+    if n == 0:
+        return
+    col_a = rng.standard_normal(limit).astype(np.float32)
+    col_b = rng.standard_normal(limit).astype(np.float32)
+    u8_a = rng.integers(0, 255, limit).astype(np.uint8)
+    u8_b = rng.integers(0, 255, limit).astype(np.uint8)
+    outs = [torch.empty(n, dtype=torch.float32, device=DEV), torch.empty(n, dtype=torch.uint8, device=DEV),
+            torch.empty(n, dtype=torch.int32, device=DEV)]
+    ins = [(_t(col_a), _t(col_b), 4), (_t(u8_a), _t(u8_b), 1), (_t(np.arange(limit, dtype=np.int32)), None, 4)]
+    g = _lib.plx_merge_gather_desc()
+    g.n, g.order, g.b_ids, g.nb, g.a_limit, g.b_limit = n, order.data_ptr(), tb.data_ptr(), nb, limit, limit
+    g.ncols = 3
+    for j, ((a, b, nbytes), out) in enumerate(zip(ins, outs)):
+        g.cols[j].a, g.cols[j].b = a.data_ptr(), (None if b is None else b.data_ptr())
+        g.cols[j].out, g.cols[j].bytes = out.data_ptr(), nbytes
+    assert lib.plx_merge_gather(g, None) == 0, lib.plx_last_error()
+    torch.cuda.synchronize()
+    src_a = want_order >= 0
+    ids_all = np.where(src_a, want_order, b_ids[np.where(src_a, 0, -1 - want_order)] if nb else 0)
+    assert np.array_equal(outs[0].cpu().numpy(), np.where(src_a, col_a[ids_all], col_b[ids_all]))
+    assert np.array_equal(outs[1].cpu().numpy(), np.where(src_a, u8_a[ids_all], u8_b[ids_all]))
+    assert np.array_equal(outs[2].cpu().numpy(), ids_all.astype(np.int32))
+
+
+def test_remap() -> None:
+    lib = _lib.load()
+    rng = np.random.default_rng(9)
+    base, n_map = 1000, 5000
+    mp = np.where(rng.random(n_map) < 0.3, -1, rng.integers(0, 10**6, n_map)).astype(np.int32)
+    idx = (base + rng.integers(-5, n_map + 5, 20000)).astype(np.int32)
+    out = torch.empty(idx.size, dtype=torch.int32, device=DEV)
+    live = torch.empty(idx.size, dtype=torch.uint8, device=DEV)
+    tm = _t(mp)
+    assert lib.plx_remap_i32(idx.size, _t(idx).data_ptr(), base, n_map, tm.data_ptr(), out.data_ptr(),
+                             live.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    p = idx.astype(np.int64) - base
+    want = np.where((p >= 0) & (p < n_map), mp[np.clip(p, 0, n_map - 1)], -1)
+    assert np.array_equal(out.cpu().numpy(), want)
+    assert np.array_equal(live.cpu().numpy(), (want >= 0).astype(np.uint8))
