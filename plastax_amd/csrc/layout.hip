@@ -256,90 +256,150 @@ __device__ __forceinline__ int64_t lds_count(const uint64_t* keys, int64_t n, ui
   return lo;
 }
 
-// One thread per element i of a (a is the long side: the survivors). With
-// c(i) the number of b elements below a's i-th key (a first on ties), a_i
-// lands at i + c(i), and b_j for c(i-1) <= j < c(i) lands just before it,
-// at j + i; the last thread places the b elements after every a. Each
-// thread searches only b (its keys staged in LDS), and takes c(i-1) from
-// its neighbour lane. With a empty, b_j lands at j.
+constexpr int kMergePer = 4;  // elements per thread: their loads are in flight together
+
+// One thread per element i of a (a is the long side: the survivors), four
+// per thread (element i = block * 1024 + k * 256 + lane). With c(i) the
+// number of b elements below a's i-th key (a first on ties), a_i lands at
+// i + c(i), and b_j for c(i-1) <= j < c(i) lands just before it, at j + i;
+// the last element's thread places the b elements after every a. Each
+// thread searches only b (its keys staged in LDS) and takes c(i-1) from the
+// block's table. With a empty, b_j lands at j.
 __global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
   __shared__ uint64_t bkey[kMergeStaged];
-  __shared__ int64_t cnt[kMergeBlock];
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kMergeBlock + threadIdx.x;
+  __shared__ int64_t cnt[kMergeBlock * kMergePer];
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kMergeBlock * kMergePer;
   if (d.a.n == 0) {  // uniform over the grid
-    if (t < d.b.n) merge_put(d, d.b, t, static_cast<int32_t>(-1 - t), d.b.ids[t]);
+    for (int k = 0; k < kMergePer; ++k) {
+      const int64_t t = first + k * kMergeBlock + threadIdx.x;
+      if (t < d.b.n) merge_put(d, d.b, t, static_cast<int32_t>(-1 - t), d.b.ids[t]);
+    }
     return;
   }
   const bool staged = d.b.n <= kMergeStaged;
   if (staged)
     for (int64_t j = threadIdx.x; j < d.b.n; j += kMergeBlock) bkey[j] = merge_key(d.b, d.b.ids[j]);
+  int64_t id[kMergePer];
+  uint64_t key[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t t = first + k * kMergeBlock + threadIdx.x;
+    id[k] = t < d.a.n ? d.a.ids[t] : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) key[k] = merge_key(d.a, id[k]);
   __syncthreads();
-  const bool valid = t < d.a.n;
-  const int64_t id = valid ? d.a.ids[t] : 0;
-  int64_t c = 0;
-  if (valid) {
-    const uint64_t key = merge_key(d.a, id);
-    c = staged ? lds_count(bkey, d.b.n, key) : merge_count(d.b, key, false);
+  int64_t c[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    c[k] = staged ? lds_count(bkey, d.b.n, key[k]) : merge_count(d.b, key[k], false);
+    cnt[k * kMergeBlock + threadIdx.x] = c[k];
   }
-  cnt[threadIdx.x] = c;
   __syncthreads();
-  if (!valid) return;
-  merge_put(d, d.a, t + c, static_cast<int32_t>(id), id);
-  int64_t c0 = 0;
-  if (threadIdx.x > 0) {
-    c0 = cnt[threadIdx.x - 1];
-  } else if (t > 0) {
-    const uint64_t key = merge_key(d.a, d.a.ids[t - 1]);
-    c0 = staged ? lds_count(bkey, d.b.n, key) : merge_count(d.b, key, false);
-  }
-  for (int64_t j = c0; j < c; ++j) merge_put(d, d.b, j + t, static_cast<int32_t>(-1 - j), d.b.ids[j]);
-  if (t == d.a.n - 1)
-    for (int64_t j = c; j < d.b.n; ++j) merge_put(d, d.b, j + d.a.n, static_cast<int32_t>(-1 - j), d.b.ids[j]);
-}
-
-__device__ __forceinline__ void merge_copy(const plx_merge_col& c, int64_t r, bool from_a, int64_t at,
-                                           int32_t id) {
-  if (c.bytes == 1) {
-    const uint8_t v = from_a ? static_cast<const uint8_t*>(c.a)[at]
-                             : (c.b ? static_cast<const uint8_t*>(c.b)[at] : static_cast<uint8_t>(id));
-    static_cast<uint8_t*>(c.out)[r] = v;
-  } else {
-    const uint32_t v = from_a ? static_cast<const uint32_t*>(c.a)[at]
-                              : (c.b ? static_cast<const uint32_t*>(c.b)[at] : static_cast<uint32_t>(id));
-    static_cast<uint32_t*>(c.out)[r] = v;
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int e = k * kMergeBlock + threadIdx.x;  // the element's index in the block
+    const int64_t t = first + e;
+    if (t >= d.a.n) break;
+    merge_put(d, d.a, t + c[k], static_cast<int32_t>(id[k]), id[k]);
+    int64_t c0 = 0;
+    if (e > 0) {
+      c0 = cnt[e - 1];
+    } else if (t > 0) {
+      const uint64_t kp = merge_key(d.a, d.a.ids[t - 1]);
+      c0 = staged ? lds_count(bkey, d.b.n, kp) : merge_count(d.b, kp, false);
+    }
+    for (int64_t j = c0; j < c[k]; ++j) merge_put(d, d.b, j + t, static_cast<int32_t>(-1 - j), d.b.ids[j]);
+    if (t == d.a.n - 1)
+      for (int64_t j = c[k]; j < d.b.n; ++j)
+        merge_put(d, d.b, j + d.a.n, static_cast<int32_t>(-1 - j), d.b.ids[j]);
   }
 }
 
-// One thread per merged rank; each column's element comes from a (by the
-// id in `order`) or from b (by the id in b_ids).
-__global__ void k_merge_gather(plx_merge_gather_desc d) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= d.n) return;
-  const int32_t o = d.order[r];
-  // Every index is clamped into its array (a malformed order reads a wrong
-  // element rather than outside the buffers).
-  const bool from_a = o >= 0 || d.nb == 0;
-  int64_t at;
-  int32_t id = 0;
-  if (from_a) {
-    at = o < 0 ? 0 : (o < d.a_limit ? o : d.a_limit - 1);
-  } else {
-    int64_t j = -1 - static_cast<int64_t>(o);
-    j = j < d.nb ? j : d.nb - 1;
-    id = d.b_ids[j];
-    at = id < 0 ? 0 : (id >= d.b_limit ? d.b_limit - 1 : id);
+// Four ranks per thread (rank = block * 1024 + k * 256 + lane); each
+// column's element comes from a (by the id in `order`) or from b (by the id
+// in b_ids). NC columns, a compile-time count, so the values stay in
+// registers and every load is issued before any store.
+template <int NC>
+__global__ __launch_bounds__(256) void k_merge_gather(plx_merge_gather_desc d) {
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 * kMergePer;
+  bool ok[kMergePer], from_a[kMergePer];
+  int64_t at[kMergePer];
+  int32_t id[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t r = first + k * 256 + threadIdx.x;
+    ok[k] = r < d.n;
+    const int32_t o = ok[k] ? d.order[r] : 0;
+    // Every index is clamped into its array (a malformed order reads a
+    // wrong element rather than outside the buffers).
+    from_a[k] = o >= 0 || d.nb == 0;
+    id[k] = 0;
+    if (from_a[k]) {
+      at[k] = o < 0 ? 0 : (o < d.a_limit ? o : d.a_limit - 1);
+    } else {
+      int64_t j = -1 - static_cast<int64_t>(o);
+      j = j < d.nb ? j : d.nb - 1;
+      id[k] = d.b_ids[j];
+      at[k] = id[k] < 0 ? 0 : (id[k] >= d.b_limit ? d.b_limit - 1 : id[k]);
+    }
   }
-  for (int k = 0; k < d.ncols; ++k) merge_copy(d.cols[k], r, from_a, at, id);
+  uint32_t v[NC][kMergePer];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const plx_merge_col& col = d.cols[c];
+#pragma unroll
+    for (int k = 0; k < kMergePer; ++k) {
+      const void* src = from_a[k] ? col.a : col.b;
+      v[c][k] = !ok[k] ? 0u
+                : !src    ? static_cast<uint32_t>(id[k])
+                : col.bytes == 1 ? static_cast<uint32_t>(static_cast<const uint8_t*>(src)[at[k]])
+                                 : static_cast<const uint32_t*>(src)[at[k]];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const plx_merge_col& col = d.cols[c];
+#pragma unroll
+    for (int k = 0; k < kMergePer; ++k) {
+      if (!ok[k]) continue;
+      const int64_t r = first + k * 256 + threadIdx.x;
+      if (col.bytes == 1) static_cast<uint8_t*>(col.out)[r] = static_cast<uint8_t>(v[c][k]);
+      else static_cast<uint32_t*>(col.out)[r] = v[c][k];
+    }
+  }
 }
 
-__global__ void k_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
-                            int32_t* out, uint8_t* live) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const int64_t p = static_cast<int64_t>(idx[j]) - off;
-  const int32_t m = (p >= 0 && p < map_len) ? map[p] : -1;
-  out[j] = m;
-  live[j] = m >= 0;
+template <int NC>
+void launch_merge_gather(const plx_merge_gather_desc& d, hipStream_t s) {
+  if (d.ncols == NC) {
+    hipLaunchKernelGGL(k_merge_gather<NC>, dim3(static_cast<unsigned>((d.n + 256 * kMergePer - 1) / (256 * kMergePer))),
+                       dim3(256), 0, s, d);
+    return;
+  }
+  if constexpr (NC < PLX_MERGE_MAX_COLS) launch_merge_gather<NC + 1>(d, s);
+}
+
+// Four entries per thread, their loads in flight together.
+__global__ __launch_bounds__(256) void k_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len,
+                                                   const int32_t* map, int32_t* out, uint8_t* live) {
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 * kMergePer;
+  int64_t p[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t j = first + k * 256 + threadIdx.x;
+    p[k] = j < n ? static_cast<int64_t>(idx[j]) - off : -1;
+  }
+  int32_t m[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) m[k] = (p[k] >= 0 && p[k] < map_len) ? map[p[k]] : -1;
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t j = first + k * 256 + threadIdx.x;
+    if (j >= n) break;
+    out[j] = m[k];
+    live[j] = m[k] >= 0;
+  }
 }
 
 unsigned grid_of(int64_t n, int block) {
@@ -397,8 +457,9 @@ int plx_merge_index(const plx_merge_desc* d, void* stream) {
   if (n > INT32_MAX || d->offset < 0 || d->offset + n > INT32_MAX)
     return fail(PLX_ERR_INVALID, "plx_merge_index: ranks exceed int32");
   if (n == 0) return PLX_OK;
-  const int64_t threads = d->a.n > 0 ? d->a.n : d->b.n;
-  hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((threads + kMergeBlock - 1) / kMergeBlock)),
+  const int64_t elems = d->a.n > 0 ? d->a.n : d->b.n;
+  const int64_t per_block = static_cast<int64_t>(kMergeBlock) * kMergePer;
+  hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((elems + per_block - 1) / per_block)),
                      dim3(kMergeBlock), 0, static_cast<hipStream_t>(stream), *d);
   return check_launch("plx_merge_index");
 }
@@ -415,8 +476,7 @@ int plx_merge_gather(const plx_merge_gather_desc* d, void* stream) {
     if (!c.a || !c.out || (c.bytes != 1 && c.bytes != 4))
       return fail(PLX_ERR_INVALID, "plx_merge_gather: bad column");
   }
-  hipLaunchKernelGGL(k_merge_gather, dim3(static_cast<unsigned>((d->n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), *d);
+  launch_merge_gather<1>(*d, static_cast<hipStream_t>(stream));
   return check_launch("plx_merge_gather");
 }
 
@@ -425,7 +485,8 @@ int plx_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, c
   if (n < 0 || map_len < 0) return fail(PLX_ERR_INVALID, "plx_remap_i32: negative size");
   if (n == 0) return PLX_OK;
   if (!idx || !map || !out || !live) return fail(PLX_ERR_INVALID, "plx_remap_i32: null pointer");
-  hipLaunchKernelGGL(k_remap_i32, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+  hipLaunchKernelGGL(k_remap_i32, dim3(static_cast<unsigned>((n + 256 * kMergePer - 1) / (256 * kMergePer))),
+                     dim3(256), 0,
                      static_cast<hipStream_t>(stream), n, idx, off, map_len, map, out, live);
   return check_launch("plx_remap_i32");
 }
