@@ -960,6 +960,13 @@ PLX_EXPORT int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* co
  * (the reference's resort, topo.py:303-452, a stable sort of every live
  * slot) would give, for the cost of one pass over the columns. */
 
+/* dst[slot[pos[i]]] = src[pos[i]] for i < n (count n_dev, optional),
+ * elements of `bytes` (1 or 4) bytes; slot values outside [0, dst_len) are
+ * skipped: copies the positions listed in pos (the edges killed since the
+ * layout) back into their logical slots. */
+PLX_EXPORT int plx_copy_to_slots(int64_t n, const int32_t* n_dev, const int32_t* pos, const int32_t* slot,
+                                 const void* src, void* dst, int64_t dst_len, int32_t bytes, void* stream);
+
 /* One side of a merge: n elements whose ids (in [0, id_limit)) are listed
  * in ascending (key1[id], key2[id]) order, keys compared as uint32; key2
  * null means the id itself. map (optional, id_limit entries) receives each

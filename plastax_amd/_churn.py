@@ -284,6 +284,27 @@ class ChurnArena(Arena):
         _lib.check(lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
         self.lists.append(SourceLists(lptr, pos, ldst, lsrc, lslot))
 
+    def _write_kills(self, conns: tuple[Columns, ...], written: set) -> None:
+        """Only prunes wrote since the logical view was in step: DEAD went
+        from 0 to 1 at the killed edges (every position of the live range
+        was live at layout time) and the step count was stamped there, so
+        only those positions are copied back."""
+        from plastax_amd.grow import Kernels
+
+        k = Kernels(self.device, int(torch.cuda.current_stream(self.device).cuda_stream))
+        for b, bucket in enumerate(conns):
+            base, live, cap = self.bases[b], self.lives[b], self.caps[b]
+            if live == 0:
+                continue
+            killed, nk = k.compact(live, 0, self.cols[DEAD.name][base:])  # PLX_FLAG_U8: positions now dead
+            for name in written:
+                if name not in bucket:
+                    continue
+                col = bucket[name]
+                _lib.check(k.lib.plx_copy_to_slots(live, nk.data_ptr(), killed.data_ptr(), self.slot[base:].data_ptr(),
+                                                   self.cols[name][base:].data_ptr(), col.data_ptr(), cap,
+                                                   col.element_size(), k.s), "plx_copy_to_slots")
+
     def src_table(self, b: int) -> tuple[int, int]:
         """No source-value tables: units keep the caller's ids."""
         return 0, 0
@@ -300,6 +321,9 @@ class ChurnArena(Arena):
         columns a step wrote since the last such copy (a prune: DEAD and the
         step count it stamps), or all of them."""
         written, self._written = self._written, set()
+        if written is not None and written <= {DEAD.name, self.t_name}:
+            self._write_kills(conns, written)
+            return
         for b, bucket in enumerate(conns):
             base, live = self.bases[b], self.lives[b]
             idx = self.slot[base : base + live].long()

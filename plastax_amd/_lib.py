@@ -521,6 +521,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_count_ids": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_batch_tile_limits": (c_i32, [c_vp, c_vp]),
     "plx_gen_fold": (c_i32, [ctypes.POINTER(plx_gen_fold_desc), c_vp]),
+    "plx_copy_to_slots": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp]),
     "plx_merge_index": (c_i32, [ctypes.POINTER(plx_merge_desc), c_vp]),
     "plx_merge_gather": (c_i32, [ctypes.POINTER(plx_merge_gather_desc), c_vp]),
     "plx_remap_i32": (c_i32, [c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),

@@ -214,6 +214,17 @@ __global__ void k_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, 
   }
 }
 
+__global__ void k_copy_to_slots(int64_t n, const int32_t* n_dev, const int32_t* pos, const int32_t* slot,
+                                const void* src, void* dst, int64_t dst_len, int32_t bytes) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n || (n_dev && i >= *n_dev)) return;
+  const int32_t p = pos[i];
+  const int64_t s = slot[p];
+  if (s < 0 || s >= dst_len) return;
+  if (bytes == 1) static_cast<uint8_t*>(dst)[s] = static_cast<const uint8_t*>(src)[p];
+  else static_cast<uint32_t*>(dst)[s] = static_cast<const uint32_t*>(src)[p];
+}
+
 // The (key1, key2) of id `id` of a merge side, as one 64-bit unsigned key;
 // ids are clamped into [0, id_limit) for the reads.
 __device__ __forceinline__ uint64_t merge_key(const plx_merge_side& s, int64_t id) {
@@ -442,6 +453,17 @@ int plx_cold_slots(int64_t n, const int32_t* n_dev, const int32_t* cold, const i
   hipLaunchKernelGGL(k_cold_slots, dim3(grid_of(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream), n, n_dev,
                      cold, g_src, g_st, g_tile, hl, off, region, sb_of_tile, cold_idx, cold_sb);
   return check_launch("plx_cold_slots");
+}
+
+int plx_copy_to_slots(int64_t n, const int32_t* n_dev, const int32_t* pos, const int32_t* slot, const void* src,
+                      void* dst, int64_t dst_len, int32_t bytes, void* stream) {
+  if (n < 0 || dst_len < 0) return fail(PLX_ERR_INVALID, "plx_copy_to_slots: negative size");
+  if (bytes != 1 && bytes != 4) return fail(PLX_ERR_INVALID, "plx_copy_to_slots: bytes must be 1 or 4");
+  if (n == 0) return PLX_OK;
+  if (!pos || !slot || !src || !dst) return fail(PLX_ERR_INVALID, "plx_copy_to_slots: null pointer");
+  hipLaunchKernelGGL(k_copy_to_slots, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n, n_dev, pos, slot, src, dst, dst_len, bytes);
+  return check_launch("plx_copy_to_slots");
 }
 
 static bool merge_side_ok(const plx_merge_side& s) {

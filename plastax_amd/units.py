@@ -134,7 +134,8 @@ class PruneUnitPhase:
         column (arena.stamp_target)."""
         cols = arena.cols
         for b in range(arena.num_buckets):
-            base, span = arena.bases[b], arena.ends[b] - arena.bases[b]
+            # Positions past the live range are dead slots: nothing to kill there.
+            base, span = arena.bases[b], arena.lives[b]
             if span == 0:
                 continue
             stamp, value = arena.stamp_target(b)
