@@ -599,6 +599,132 @@ def build_c3(px):
     return C3Net
 
 
+def run_c1(args) -> int:
+    """C1: the streaming PIPELINE net (1,024 units, 16,384 edges, SGD) run in
+    chunks by Driver.scan: as captured HIP graphs (each chunk's first step
+    eager, the rest one replay) and step by step, same chunks."""
+    import torch
+
+    import plastax_amd as px
+    import plastax_amd.numpy as jnp
+    from plastax_amd import synth
+    from plastax_amd.driver import Driver
+    from plastax_amd.state import column_to_numpy
+
+    grad = px.FieldSpec.float32("grad_pre_act")
+    lossg = px.FieldSpec.float32("loss_grad")
+
+    class TanhForward(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(acc)))
+
+    class TanhBackward(px.BackwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, src, dst, c, cid, g):
+            return c[px.WEIGHT, cid] * u[grad, dst]
+
+        def apply(self, u, i, g, acc):
+            a = u[px.ACTIVATION, i]
+            return px.UnitWrite.of((grad, (acc + u[lossg, i]) * (jnp.float32(1.0) - a * a)))
+
+    class MSELoss(px.Loss):
+        seed_field = lossg
+
+        def calculate_loss(self, u, outputs, targets, g):
+            d = u.gather(px.ACTIVATION, outputs) - targets
+            return jnp.sum(jnp.float32(0.5) * d * d), d
+
+    opt = px.optim.sgd(1e-2, grad)
+
+    class C1Net(px.Network):
+        forward_pass = TanhForward()
+        backward_pass = TanhBackward()
+        loss = MSELoss()
+        update_conn = opt.update_conn()
+        extra_unit_fields = (grad, lossg)
+        extra_conn_fields = opt.state_fields
+        propagation = px.Propagation.PIPELINE
+
+    e = synth.c1_pipeline(args.seed)
+    a = synth.c1_target(args.seed)
+    K = args.chunk
+    nchunks = max(1, args.steps // K)
+    rng = np.random.default_rng(args.seed + 7)
+    xs = rng.standard_normal(((nchunks + 1) * K, e.input_ids.size)).astype(np.float32)
+    ts = (xs @ a.T).astype(np.float32)
+    dev = torch.device("cuda", 0)
+    xs_d, ts_d = torch.from_numpy(xs).to(dev), torch.from_numpy(ts).to(dev)
+    rates, first_records = {}, {}
+    host = None
+    for mode in ("graph", "step_by_step"):
+        static, state = px.NetworkBuilder.from_edges(
+            C1Net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+            output_ids=e.output_ids, globals_=None, device="cpu")
+        if host is None:
+            specs = {s.name: s for s in static.conn_fields}
+            host = ({s.name: column_to_numpy(state.units[s.name], s).copy() for s in static.unit_fields},
+                    [{n: column_to_numpy(b[n], specs[n]).copy() for n in specs} for b in state.conns], static)
+        gstate = px.NetworkState({k: v.to(dev) for k, v in state.units.items()},
+                                 tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns), None)
+        drv = Driver(C1Net, static, gstate)
+        use_graph = mode == "graph"
+        # warm-up chunk (captures the graph)
+        first_records[mode] = drv.scan(px.StepInputs(xs_d[:K], ts_d[:K]), graph=use_graph).cpu().numpy()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for c in range(1, nchunks + 1):
+            drv.scan(px.StepInputs(xs_d[c * K : (c + 1) * K], ts_d[c * K : (c + 1) * K]), graph=use_graph)
+        torch.cuda.synchronize()
+        rates[mode] = nchunks * K / (time.perf_counter() - t0)
+        progress(f"C1 {mode}: {rates[mode]:.0f} steps/s")
+    cpu = parity = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ox
+        from plastax_amd._plan import compile_plan
+
+        ox.load()
+        units, conns, static = host
+        o = ox.OracleNet(static, {k: v.copy() for k, v in units.items()}, [{k: v.copy() for k, v in b.items()}
+                                                                            for b in conns],
+                         compile_plan(C1Net, static), None)
+        t1 = time.perf_counter()
+        ref = np.asarray([o.step(xs[i], ts[i]) for i in range(K)], dtype=np.float32)
+        sec = time.perf_counter() - t1
+        parity = {"steps": K, "graph_records_bit_exact": bool(np.array_equal(
+            first_records["graph"].astype(np.float32).view(np.uint32), ref.view(np.uint32))),
+                  "step_by_step_records_bit_exact": bool(np.array_equal(
+            first_records["step_by_step"].astype(np.float32).view(np.uint32), ref.view(np.uint32)))}
+        cpu = {"value": float(K / sec), "unit": "steps/s", "cores": 1, "kind": "port",
+               "sample": f"{K} steps of the same workload, the C oracle (oracle/plastax_oracle.c), one thread"}
+        progress(f"C1 parity over the first chunk: {parity}")
+    line = {
+        "metric": "steps/sec of C1's streaming pipeline net, Driver.scan in chunks (captured HIP graph)",
+        "value": round(rates["graph"], 1),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": nchunks * K,
+        "warmup": K,
+        "ms_per_step": round(1e3 / rates["graph"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C1: 1,024 tanh units, 16,384 edges, PIPELINE, MSE to a linear target, SGD(1e-2)",
+                   "chunk": K, "step_by_step_steps_per_s": round(rates["step_by_step"], 1)},
+        "cpu_baseline": cpu,
+        "full_size_parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def run_c3(args) -> int:
     """C3: the batched step (B = 256) of the 784-4096-4096-10 sparse MLP."""
     import torch
@@ -763,8 +889,9 @@ def run_c3(args) -> int:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=("c2", "c3", "c5", "c5_growth"), default="c2",
-                    help="c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c5", "c5_growth"), default="c2",
+                    help="c1: the small streaming PIPELINE net run by Driver.scan (graph vs step by step); "
+                    "c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
                     "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -773,6 +900,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--chunk", type=int, default=100, help="c1: steps per Driver.scan chunk")
     ap.add_argument("--relayout", choices=("merge", "full"), default="merge",
                     help="c5: the churn layout after a growth step: merged from the previous one, or built again")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -791,6 +919,8 @@ def main() -> int:
 
     if args.workload == "c5_growth":
         return run_c5_growth(args)
+    if args.workload == "c1":
+        return run_c1(args)
     if args.workload == "c3":
         return run_c3(args)
     if args.workload == "c5":

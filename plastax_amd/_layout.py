@@ -575,6 +575,21 @@ class Arena:
                     t = lo
             self.t_now.append(t)
 
+    def drop_uniform_t(self) -> None:
+        """Keep Adam's step count per edge from here on: write the bucket's
+        count into the column of its live edges (a tombstone keeps the count
+        stamped at its kill) and let the kernels read and advance the column
+        (a captured graph cannot carry a count the host advances)."""
+        if not (self.t_name and self.t_now):
+            return
+        col = self.cols[self.t_name]
+        for b, t in enumerate(self.t_now):
+            if t is None:
+                continue
+            live = slice(self.bases[b], self.bases[b] + self.lives[b])
+            col[live].masked_fill_(self.cols[DEAD.name][live] == 0, float(t))
+            self.t_now[b] = None
+
     def stamp_target(self, b: int) -> tuple[torch.Tensor | None, float]:
         """(column from bucket b's base, value) that a kill in bucket b
         stamps: Adam's step-count column and the bucket's count while every

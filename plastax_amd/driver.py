@@ -53,6 +53,7 @@ class Driver:
         self._overflowed = False
         self.regrows = 0
         self.resorts = 0
+        self._graphs: dict = {}  # scan's captured chunks
 
     @property
     def state(self) -> NetworkState:
@@ -77,11 +78,22 @@ class Driver:
         return StepResult(state=self._state, overflow=self._state.overflow, loss=result.loss)
 
     def scan(self, inputs: StepInputs, *, record: Callable[[StepResult], Any] | None = None,
-             steps: int | None = None) -> Any:
+             steps: int | None = None, graph: bool | None = None) -> Any:
         """Run a chunk of steps (inputs and targets with a leading chunk axis)
         with `step`'s semantics; returns the per-step records stacked along
         a leading axis (the loss by default), entries at or beyond ``steps``
-        zero (driver.py:170-270)."""
+        zero (driver.py:170-270).
+
+        The reference runs the chunk as one device-side loop. Here, for a
+        streaming step without structural phases or reset_global (nothing
+        the host must decide between steps), the chunk's first step runs as
+        usual and the other steps are captured once into a HIP graph and
+        replayed -- one launch for the chunk, no dispatch per step -- with
+        the inputs copied into the graph's buffers; the results are step for
+        step those of `step`. ``graph``: None uses the graph where it
+        applies and ``record`` is the default; True requires it (``record``
+        must then return device tensors); False runs the steps one by one.
+        """
         rec = _loss_record if record is None else record
         xs = inputs.inputs
         if getattr(xs, "ndim", 0) < 2:
@@ -92,6 +104,11 @@ class Driver:
         count = length if steps is None else int(steps)
         if not 0 <= count <= length:
             raise ValueError(f"Driver.scan: steps must be in [0, {length}], got {steps}")
+        why = self._graph_refusal()
+        if graph is True and why:
+            raise ValueError(f"Driver.scan(graph=True): {why}")
+        if count >= 2 and not why and (graph is True or (graph is None and record is None)):
+            return self._scan_graph(inputs, rec, count, length)
         out = []
         for i in range(count):
             t = None if inputs.targets is None else inputs.targets[i]
@@ -103,6 +120,87 @@ class Driver:
             pad = [torch.zeros_like(first)] * (length - count)
             return torch.stack([o.reshape(first.shape) for o in out] + pad)
         return np.concatenate([np.asarray(out), np.zeros((length - count,) + np.shape(first))])
+
+    def _graph_refusal(self) -> str:
+        """Why a chunk cannot run as a captured graph ('' when it can)."""
+        step = self._step
+        if not isinstance(step, StepFn) or self._kw.get("batch_size") is not None:
+            return "batched steps run step by step"
+        if self._check_every != 1:
+            return "check_every > 1 reads flags between steps"
+        plan = step.plan
+        if plan.prune_unit or plan.prune_conn or plan.add_unit or plan.add_conn is not None:
+            return "structural phases decide on the host between steps"
+        if plan.reset_global:
+            return "reset_global changes the globals on the host every step"
+        if plan.forward.generic is not None or (plan.backward is not None and plan.backward.generic is not None):
+            return "generic passes run step by step"
+        if self._state.device.type != "cuda":
+            return "the state is not on a GPU"
+        return ""
+
+    def _scan_graph(self, inputs: StepInputs, rec: Callable[[StepResult], Any], count: int, length: int) -> Any:
+        """The chunk's first step eagerly (every first-use build and host
+        read happens there), then steps 1.. as one replay of a captured
+        graph (captured on first use for this arena, buffers and shapes)."""
+        dev = self._state.device
+        xs = torch.as_tensor(inputs.inputs, dtype=torch.float32, device=dev)
+        ts = None if inputs.targets is None else torch.as_tensor(inputs.targets, dtype=torch.float32, device=dev)
+        first = rec(self.step(StepInputs(xs[0], None if ts is None else ts[0])))
+        state = self._state
+        arena = self._step.arena(state)
+        n = count - 1
+        key = (n, rec, id(self._step), id(arena), tuple(xs.shape[1:]), None if ts is None else tuple(ts.shape[1:]),
+               tuple(state._units), _globals_key(state.globals_))
+        entry = self._graphs.get(key)
+        if entry is not None:
+            # The graph reads and writes the unit buffers it was captured on;
+            # an eager PIPELINE step since then left the values in copies.
+            for name, col in entry[4].items():
+                if state._units[name] is not col:
+                    col.copy_(state._units[name])
+                    state._units[name] = col
+        if entry is None:
+            self._graphs.clear()  # one captured chunk at a time: its buffers stay allocated
+            arena.drop_uniform_t()
+            xin = torch.empty((n,) + tuple(xs.shape[1:]), dtype=torch.float32, device=dev)
+            tin = None if ts is None else torch.empty((n,) + tuple(ts.shape[1:]), dtype=torch.float32, device=dev)
+            xin.copy_(xs[1:count])
+            if tin is not None:
+                tin.copy_(ts[1:count])
+            units = state._units
+            orig = dict(units)
+            g = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize(dev)
+            with torch.cuda.graph(g):
+                recs = []
+                for i in range(n):
+                    res = self._step(state, StepInputs(xin[i], None if tin is None else tin[i]))
+                    state = res.state
+                    recs.append(rec(res))
+                out = torch.stack(recs)
+                # Swapped unit buffers (a PIPELINE apply writes copies) go back
+                # into the state's own, so every replay starts from them.
+                for name, col in orig.items():
+                    if state._units[name] is not col:
+                        col.copy_(state._units[name])
+            for name, col in orig.items():
+                state._units[name] = col
+            self._state = state
+            entry = self._graphs[key] = (g, xin, tin, out, orig)
+            g.replay()
+        else:
+            g, xin, tin, out, _ = entry
+            xin.copy_(xs[1:count])
+            if tin is not None:
+                tin.copy_(ts[1:count])
+            g.replay()
+            state.step = int(state.step) + n
+        result = torch.cat([torch.as_tensor(first, device=dev).reshape((1,) + tuple(out.shape[1:])), out.clone()])
+        if count < length:
+            pad = torch.zeros((length - count,) + tuple(result.shape[1:]), dtype=result.dtype, device=dev)
+            result = torch.cat([result, pad])
+        return result
 
     # -- recoveries ---------------------------------------------------------------
     def _free_slots(self, state: NetworkState, level: int) -> int:
@@ -165,3 +263,11 @@ class Driver:
                 self._step = self._make_step()
             self._state = self._resort_if_due(self._state)
         return StepResult(state=self._state, overflow=self._state.overflow, loss=result.loss)
+
+
+def _globals_key(g: Any) -> Any:
+    """The globals' values (they are traced into the captured programs)."""
+    if g is None:
+        return None
+    items = g.items() if isinstance(g, dict) else vars(g).items()
+    return tuple(sorted((str(k), np.asarray(v).tobytes()) for k, v in items))
