@@ -183,7 +183,7 @@ __device__ __forceinline__ UnitFields load_loss_fields(const plx_program& P, int
 // Runs `P` for unit `u`, reading its fields from `f`; out slot k is stored to
 // P.outs[k][u] when `store`. Returns out slot 1 (the loss term of a loss
 // program).
-__device__ float run_program(const plx_program& P, int64_t u, const UnitFields& f, float acc,
+__device__ __forceinline__ float run_program(const plx_program& P, int64_t u, const UnitFields& f, float acc,
                              float aux, bool store) {
   float r[kRegs];
   float outs[PLX_MAX_OUTS];
