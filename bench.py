@@ -599,6 +599,95 @@ def build_c3(px):
     return C3Net
 
 
+def run_c2_prune(args) -> int:
+    """C2 with a PruneConn every step, fused into the forward's edge pass
+    (fuse_prune="auto") against a separate predicate pass at the prune slot
+    ("off"): same steps, same kills; both losses and DEAD columns must agree."""
+    import torch
+
+    import plastax_amd as px
+    import plastax_amd.numpy as jnp
+    from plastax_amd import synth
+
+    class HashPrune(px.PruneConn):
+        """About one edge in 2^20 per step, from its ids and the step."""
+
+        def predicate(self, u, c, cid, g):
+            h = c[px.FROM_ID, cid] * jnp.int32(7) + c[px.TO_ID, cid] * jnp.int32(13) + g["step"]
+            return (h % jnp.int32(1048573)) == jnp.int32(0)
+
+    net0, e = build_c2(px, args.seed, args.scale)
+
+    class C2Prune(net0):
+        prune_conn = HashPrune()
+
+    width = e.input_ids.size
+    sign, perm = synth.c2_target(args.seed, width)
+    nsteps = args.warmup + args.steps
+    rng = np.random.default_rng(args.seed + 2)
+    xs = rng.standard_normal((nsteps, width)).astype(np.float32)
+    ts = np.ascontiguousarray((sign[None, :] * xs[:, perm]).astype(np.float32))
+    dev = torch.device("cuda", 0)
+    xs_d, ts_d = torch.from_numpy(xs).to(dev), torch.from_numpy(ts).to(dev)
+    res = {}
+    for mode in ("auto", "off"):
+        static, state = px.NetworkBuilder.from_edges(
+            C2Prune, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids,
+            output_ids=e.output_ids, globals_={"step": np.int32(0)}, capacity_align=256, device="cpu")
+        gstate = px.NetworkState({k: v.to(dev) for k, v in state.units.items()},
+                                 tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
+                                 {"step": np.int32(0)})
+        del state
+        dead0 = sum(int(b["dead"].to(torch.int64).sum()) for b in gstate.conns)
+        step = px.make_step(C2Prune, static, fuse_prune=mode)
+        step.arena(gstate)
+        losses = []
+        for k in range(args.warmup):
+            gstate.globals_ = {"step": np.int32(k)}
+            r = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+            gstate = r.state
+            losses.append(r.loss)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(args.warmup, nsteps):
+            gstate.globals_ = {"step": np.int32(k)}
+            r = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+            gstate = r.state
+            losses.append(r.loss)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        dead = torch.cat([b["dead"].to(torch.int64) for b in gstate.conns])
+        res[mode] = {"ms_per_step": ms, "fused": bool(step.prune_fusion.plan.fused),
+                     "losses": torch.stack(losses).cpu().numpy(), "killed": int(dead.sum()) - dead0,
+                     "dead": dead.cpu()}
+        progress(f"C2 + PruneConn, fuse_prune={mode}: {ms:.4f} ms per step (fused: {res[mode]['fused']})")
+        del gstate, step
+        torch.cuda.empty_cache()
+    same_loss = bool(np.array_equal(res["auto"]["losses"].view(np.uint32), res["off"]["losses"].view(np.uint32)))
+    same_dead = bool(torch.equal(res["auto"]["dead"], res["off"]["dead"]))
+    edges = int(e.src.size)
+    line = {
+        "metric": "ms per C2 streaming step with a PruneConn every step, fused into the forward's edge pass",
+        "value": round(res["auto"]["ms_per_step"], 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["auto"]["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C2 + PruneConn (edge-id hash, ~1 in 2^20 per step), Adam", "edges": edges,
+                   "separate_pass_ms_per_step": round(res["off"]["ms_per_step"], 4),
+                   "fused": res["auto"]["fused"], "separate_fused": res["off"]["fused"]},
+        "parity": {"losses_bit_exact": same_loss, "dead_equal": same_dead, "killed": res["auto"]["killed"]},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def run_c1(args) -> int:
     """C1: the streaming PIPELINE net (1,024 units, 16,384 edges, SGD) run in
     chunks by Driver.scan: as captured HIP graphs (each chunk's first step
@@ -889,7 +978,7 @@ def run_c3(args) -> int:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c5", "c5_growth"), default="c2",
+    ap.add_argument("--workload", choices=("c1", "c2", "c2_prune", "c3", "c5", "c5_growth"), default="c2",
                     help="c1: the small streaming PIPELINE net run by Driver.scan (graph vs step by step); "
                     "c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
                     "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
@@ -921,6 +1010,8 @@ def main() -> int:
         return run_c5_growth(args)
     if args.workload == "c1":
         return run_c1(args)
+    if args.workload == "c2_prune":
+        return run_c2_prune(args)
     if args.workload == "c3":
         return run_c3(args)
     if args.workload == "c5":
