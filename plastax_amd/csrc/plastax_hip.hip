@@ -464,17 +464,20 @@ __global__ __launch_bounds__(kFwdBlock) void k_forward(plx_forward_desc d) {
       // Each position of the rows' ranges is in exactly one window's
       // [eb, ee), so every sink byte has one writer.
       const uint32_t keyed = px::philox32(0, 1);  // the rng key of an unseeded step-0 site
-#pragma unroll
-      for (int i = 0; i < kFwdQuads; ++i) {
+      // One rolled loop over the thread's positions: a single inlined copy
+      // of the site interpreter (unrolled, each copy adds its registers).
+#pragma unroll 1
+      for (int t = 0; t < 4 * kFwdQuads; ++t) {
+        const int i = t >> 2, k = t & 3;
         const int q = threadIdx.x + i * kFwdBlock;
-        const int e = w.w0 + 4 * q;
+        const int p = w.w0 + 4 * q + k;
+        if (4 * q >= wn || p < w.eb || p >= w.ee) continue;
+        uint32_t dv = static_cast<uint32_t>(cur.dv[0]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int p = e + k;
-          if (4 * q >= wn || p < w.eb || p >= w.ee) continue;
-          const bool tomb = (cur.dv[i] >> (8 * k)) & 0xFFu;
-          d.prune_sink[p] = tomb ? 0 : prune_at(d, p, keyed);
-        }
+        for (int ii = 1; ii < kFwdQuads; ++ii)
+          if (i == ii) dv = static_cast<uint32_t>(cur.dv[ii]);
+        const bool tomb = (dv >> (8 * k)) & 0xFFu;
+        d.prune_sink[p] = tomb ? 0 : prune_at(d, p, keyed);
       }
     }
   };

@@ -76,17 +76,126 @@ struct Site {
   int32_t sample;     // the site's sample
 };
 
-__device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units, uint32_t* outv) {
+// The interpreter's 32 registers. Every operand index comes from the
+// program in the kernel arguments, so it is uniform across the wave; each
+// access is a switch on it (a scalar branch) whose cases name one register,
+// so the file stays in VGPRs instead of scratch memory.
+struct SiteRegs {
   uint32_t r[32];
+  __device__ __forceinline__ uint32_t get(int i) const {
+    switch (i & 31) {
+      case 0: return r[0];
+      case 1: return r[1];
+      case 2: return r[2];
+      case 3: return r[3];
+      case 4: return r[4];
+      case 5: return r[5];
+      case 6: return r[6];
+      case 7: return r[7];
+      case 8: return r[8];
+      case 9: return r[9];
+      case 10: return r[10];
+      case 11: return r[11];
+      case 12: return r[12];
+      case 13: return r[13];
+      case 14: return r[14];
+      case 15: return r[15];
+      case 16: return r[16];
+      case 17: return r[17];
+      case 18: return r[18];
+      case 19: return r[19];
+      case 20: return r[20];
+      case 21: return r[21];
+      case 22: return r[22];
+      case 23: return r[23];
+      case 24: return r[24];
+      case 25: return r[25];
+      case 26: return r[26];
+      case 27: return r[27];
+      case 28: return r[28];
+      case 29: return r[29];
+      case 30: return r[30];
+      case 31: return r[31];
+      default: return 0u;
+    }
+  }
+  __device__ __forceinline__ void set(int i, uint32_t v) {
+    switch (i & 31) {
+      case 0: r[0] = v; return;
+      case 1: r[1] = v; return;
+      case 2: r[2] = v; return;
+      case 3: r[3] = v; return;
+      case 4: r[4] = v; return;
+      case 5: r[5] = v; return;
+      case 6: r[6] = v; return;
+      case 7: r[7] = v; return;
+      case 8: r[8] = v; return;
+      case 9: r[9] = v; return;
+      case 10: r[10] = v; return;
+      case 11: r[11] = v; return;
+      case 12: r[12] = v; return;
+      case 13: r[13] = v; return;
+      case 14: r[14] = v; return;
+      case 15: r[15] = v; return;
+      case 16: r[16] = v; return;
+      case 17: r[17] = v; return;
+      case 18: r[18] = v; return;
+      case 19: r[19] = v; return;
+      case 20: r[20] = v; return;
+      case 21: r[21] = v; return;
+      case 22: r[22] = v; return;
+      case 23: r[23] = v; return;
+      case 24: r[24] = v; return;
+      case 25: r[25] = v; return;
+      case 26: r[26] = v; return;
+      case 27: r[27] = v; return;
+      case 28: r[28] = v; return;
+      case 29: r[29] = v; return;
+      case 30: r[30] = v; return;
+      case 31: r[31] = v; return;
+      default: return;
+    }
+  }
+};
+
+static_assert(PLX_MAX_SOUTS == 8, "site_out names eight outputs");
+__device__ __forceinline__ void site_out(uint32_t (&o)[PLX_MAX_SOUTS], int i, uint32_t v) {
+  switch (i & 7) {
+    case 0: o[0] = v; return;
+    case 1: o[1] = v; return;
+    case 2: o[2] = v; return;
+    case 3: o[3] = v; return;
+    case 4: o[4] = v; return;
+    case 5: o[5] = v; return;
+    case 6: o[6] = v; return;
+    case 7: o[7] = v; return;
+    default: return;
+  }
+}
+
+__device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units,
+                                         uint32_t (&outv)[PLX_MAX_SOUTS]) {
+  SiteRegs r;
   for (int k = 0; k < p.ninstr; ++k) {
     const int op = p.code[4 * k], d = p.code[4 * k + 1], a = p.code[4 * k + 2], b = p.code[4 * k + 3];
-    const uint32_t x = r[a & 31], y = r[b & 31];
+    const uint32_t x = r.get(a), y = r.get(b);
     const int32_t xi = static_cast<int32_t>(x), yi = static_cast<int32_t>(y);
     const float xf = __uint_as_float(x), yf = __uint_as_float(y);
     uint32_t v = 0;
     switch (op) {
       case S_CONST: v = p.consts[a]; break;
-      case S_IDX: v = static_cast<uint32_t>(a == 4 ? c.cid_value : c.role[a]); break;
+      case S_IDX: {  // a is uniform: a switch keeps c.role in registers
+        int32_t w = c.cid_value;
+        switch (a) {
+          case 0: w = c.role[0]; break;
+          case 1: w = c.role[1]; break;
+          case 2: w = c.role[2]; break;
+          case 3: w = c.role[3]; break;
+          default: break;
+        }
+        v = static_cast<uint32_t>(w);
+        break;
+      }
       case S_LDU: {
         int64_t at = yi;
         at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
@@ -107,8 +216,8 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
                                      static_cast<uint32_t>(a));
         break;
       case S_MOV: v = x; break;
-      case S_SEL: v = x ? r[b & 31] : r[(b + 1) & 31]; break;
-      case S_OUT: outv[d] = x; continue;
+      case S_SEL: v = x ? r.get(b) : r.get(b + 1); break;
+      case S_OUT: site_out(outv, d, x); continue;
       case S_FADD: v = __float_as_uint(xf + yf); break;
       case S_FSUB: v = __float_as_uint(xf - yf); break;
       case S_FMUL: v = __float_as_uint(xf * yf); break;
@@ -176,7 +285,7 @@ __device__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_unit
       case S_I2B: v = x != 0u; break;
       default: break;
     }
-    r[d & 31] = v;
+    r.set(d, v);
   }
 }
 

@@ -373,9 +373,14 @@ __global__ void k_gen_fold(plx_gen_fold_desc d) {
       uint32_t out[PLX_MAX_SOUTS];
       for (int k = 0; k < PLX_MAX_SOUTS; ++k) out[k] = 0;
       site_run(d.prog, c, d.num_units, out);
-      for (int k = 0; k < d.ncomp; ++k) s[k] = gen_op(d.monoid[k], s[k], __uint_as_float(out[k]));
+      // (unrolled with a guard: constant indices keep out and s in registers)
+#pragma unroll
+      for (int k = 0; k < PLX_MAX_SOUTS; ++k)
+        if (k < d.ncomp) s[k] = gen_op(d.monoid[k], s[k], __uint_as_float(out[k]));
     }
-    for (int k = 0; k < d.ncomp; ++k) d.acc[k][u] = gen_op(d.monoid[k], d.acc[k][u], s[k]);
+#pragma unroll
+    for (int k = 0; k < PLX_MAX_SOUTS; ++k)
+      if (k < d.ncomp) d.acc[k][u] = gen_op(d.monoid[k], d.acc[k][u], s[k]);
   }
 }
 
@@ -451,7 +456,9 @@ __global__ void k_site_eval(plx_site_desc d) {
         if (d.kill_count) atomicAdd(d.kill_count, 1);
       }
     } else {
-      for (int k = 0; k < d.prog.nout; ++k) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
+#pragma unroll
+      for (int k = 0; k < PLX_MAX_SOUTS; ++k)
+        if (k < d.prog.nout) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
     }
   }
 }

@@ -115,15 +115,17 @@ def _static(net):
 @pytest.mark.parametrize("train", [False, True])
 def test_edge_column_predicate_is_fused(train: bool) -> None:
     net = _net(HashPrune(), train=train)
-    plan = plan_prune_fusion(net, _static(net), G)
+    plan = plan_prune_fusion(net, _static(net), G, engine="triton")
     assert plan.fused and plan.engine == "hip" and plan.forwarded == (), plan
     xla = plan_prune_fusion(net, _static(net), G, engine="xla")
     assert xla.fused and xla.engine == "xla", xla
+    auto = plan_prune_fusion(net, _static(net), G)
+    assert not auto.fused and "legal" in auto.reason, auto
 
 
 def test_marked_predicate_forwards_the_field() -> None:
     net = _net(MarkedPrune(), train=True)
-    plan = plan_prune_fusion(net, _static(net), G)
+    plan = plan_prune_fusion(net, _static(net), G, engine="triton")
     assert plan.fused and plan.forwarded == (MARK.name,), plan
 
 
@@ -146,7 +148,8 @@ def test_predicate_reading_a_written_field_is_not_fused(prune, forward, train, w
 
 def test_weight_prune_without_update_conn_is_fused() -> None:
     net = _net(WeightPrune())
-    assert plan_prune_fusion(net, _static(net), G).fused
+    assert plan_prune_fusion(net, _static(net), G, engine="triton").fused
+    assert "legal" in plan_prune_fusion(net, _static(net), G).reason
 
 
 def test_prune_unit_and_missing_prune_conn_are_not_fused() -> None:

@@ -1,10 +1,11 @@
 """Fused forward + prune on the device (phases.py:2322-2469): bit-identical
 to the two-pass step, and to the oracle, over churn steps.
 
-Each net runs three ways from the same state: ``fuse_prune="off"`` (the
-predicate pass at the prune slot), ``"auto"`` (the predicate evaluated inside
-plx_forward_bucket's sweep, tombstones committed at the prune slot) and
-``"xla"`` (the predicate pass at the forward's slot). Every unit column, every
+Each net runs four ways from the same state: ``fuse_prune="off"`` (the
+predicate pass at the prune slot), ``"triton"`` (the predicate evaluated
+inside plx_forward_bucket's sweep, tombstones committed at the prune slot),
+``"xla"`` (the predicate pass at the forward's slot) and ``"auto"`` (which
+does not fuse: the prune slot's pass is the fastest here). Every unit column, every
 logical connection column, the loss and the structural flags must agree bit
 for bit at every step, and the fused run must match the oracle (whose prune
 runs at its own slot). Cases, after the reference's tests/test_prune_fusion.py:
@@ -101,7 +102,7 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
     ts = np.tanh(rng.standard_normal((8, n_out))).astype(np.float32)
     o = nets.oracle_for(oracle, net, static, state0)
     o.tail_start, o.needs_resort = int(state0.tail_start), bool(state0.needs_resort)
-    for mode in ("off", "auto", "xla"):
+    for mode in ("off", "triton", "xla", "auto"):
         state = _clone(state0)
         step = px.make_step(net, static, fuse_prune=mode)
         if step.backward_order == "slot":
@@ -114,7 +115,7 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
             res = step(state, px.StepInputs(xs[k], ts[k] if net.loss is not None else None))
             state = res.state
             trace.append((float(res.loss), state.grown, state.overflow, state.tail_start))
-            if mode == "auto":
+            if mode == "triton":
                 o.globals_ = g
                 lo = o.step(xs[k], ts[k] if net.loss is not None else None)
                 assert (state.grown, state.overflow, state.tail_start) == (o.grown, o.overflow, o.tail_start)
@@ -122,12 +123,12 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
                 assert_same_state(static, state, o, f"{case} step {k}")
                 assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at {k}"
         plan = step.prune_fusion.plan
-        if mode == "off":
+        if mode in ("off", "auto"):
             assert plan is not None and not plan.fused
         else:
-            assert plan.fused and plan.engine == ("xla" if mode == "xla" else "hip"), plan
+            assert plan.fused and plan.engine == ("hip" if mode == "triton" else "xla"), plan
         runs[mode] = (trace, _host(static, state))
-    for mode in ("auto", "xla"):
+    for mode in ("triton", "xla", "auto"):
         assert runs[mode][0] == runs["off"][0], mode
         (ua, ca), (ub, cb) = runs[mode][1], runs["off"][1]
         for name in ua:
@@ -136,6 +137,6 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
             for name in a:
                 assert np.array_equal(np.asarray(a[name]).view(np.uint8), np.asarray(b[name]).view(np.uint8)), \
                     (mode, name)
-    dead = np.concatenate([c["dead"] for c in runs["auto"][1][1]])
+    dead = np.concatenate([c["dead"] for c in runs["triton"][1][1]])
     dead0 = np.concatenate([np.asarray(c["dead"].cpu()) for c in state0.conns])
     assert int(dead.sum()) > int(dead0.sum()), "nothing was pruned"
