@@ -542,7 +542,8 @@ typedef struct plx_site_desc {
    * per-sample columns) and a unit read at unit u reads u * batch + b, b the
    * site's sample: for PLX_SITES_UNIT the n = num_units * batch sites are
    * (unit s / batch, sample s % batch) and out slot k of site s lands at
-   * outs[k][s]; for the other kinds b is `sample`. */
+   * outs[k][s] (with site_ids: n is a multiple of batch and the unit is
+   * site_ids[s / batch]); for the other kinds b is `sample`. */
   int32_t batch;
   int32_t sample;
   /* With or_into: stamp (optional) gets stamp_value at every site whose
@@ -584,6 +585,10 @@ typedef struct plx_gen_fold_desc {
   const int32_t* ids_logical;
   const int32_t* ids_physical;
   float* acc[8];
+  /* samples (>= 1): unit columns and acc are [num_units][batch]; each
+   * (row, sample) folds its entries with the unit reads at that sample */
+  int32_t batch;
+  int32_t reserved;
 } plx_gen_fold_desc;
 
 PLX_EXPORT int plx_gen_fold(const plx_gen_fold_desc* d, void* stream);

@@ -33,17 +33,20 @@ import numpy as np
 from oracle import oracle as ox
 
 
-def written_columns(plan: Any, update_unit: list[str] = ()) -> dict[str, str]:
+def written_columns(plan: Any, update_unit: list[str] = (), forward_generic: list[str] = (),
+                    backward_generic: list[str] = ()) -> dict[str, str]:
     """The unit columns the per-sample phases write (phases.py:334-387);
-    ``update_unit`` names the columns the traced update_unit writes."""
+    ``update_unit`` names the columns the traced update_unit writes,
+    ``forward_generic`` / ``backward_generic`` those a generic pass's apply
+    writes."""
     written = {"activation": "the input scatter"}
-    for name in plan.forward.program.out_fields:
+    for name in list(plan.forward.program.out_fields) + list(forward_generic):
         if name is not None:
             written.setdefault(name, "forward_pass")
     if plan.loss is not None:
         written.setdefault(plan.loss.seed_field, "loss")
     if plan.backward is not None:
-        for name in plan.backward.program.out_fields:
+        for name in list(plan.backward.program.out_fields) + list(backward_generic):
             if name is not None:
                 written.setdefault(name, "backward_pass")
     for name in update_unit:
@@ -171,7 +174,9 @@ class OracleBatch:
         specs = {s.name: s for s in o.static.unit_fields}
         reduced = dict(shared)
         uu = list(getattr(o, "_uu", (None, []))[1]) if getattr(plan, "update_unit", False) else []
-        for name in written_columns(plan, uu):
+        gen = [list(o._gen(w)[3]) if pp is not None and pp.generic is not None else []
+               for w, pp in (("fwd", plan.forward), ("bwd", plan.backward))]
+        for name in written_columns(plan, uu, *gen):
             red = policy.reduction(specs[name])
             reduced[name] = np.ascontiguousarray(reduce_column(red.value, [u[name] for u in per], B))
         o.units = reduced

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 20  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 21  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -362,6 +362,8 @@ class plx_gen_fold_desc(ctypes.Structure):
         ("ids_logical", c_vp),
         ("ids_physical", c_vp),
         ("acc", c_vp * 8),
+        ("batch", c_i32),
+        ("reserved", c_i32),
     ]
 
 

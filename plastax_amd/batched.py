@@ -96,18 +96,20 @@ def batch_sources(arena: Arena, b: int) -> BatchSources:
     return out
 
 
-def written_columns(plan: Plan, static: NetworkStatic, update_unit: list[str] = ()) -> dict[str, str]:
+def written_columns(plan: Plan, static: NetworkStatic, update_unit: list[str] = (),
+                    forward_generic: list[str] = (), backward_generic: list[str] = ()) -> dict[str, str]:
     """The unit columns a batched step's per-sample phases write, each with
     the first phase writing it (phases.py:334-387); ``update_unit`` names the
-    columns the traced update_unit writes."""
+    columns the traced update_unit writes, ``forward_generic`` /
+    ``backward_generic`` those a generic pass's apply writes."""
     written = {ACTIVATION.name: "the input scatter"}
-    for name in plan.forward.program.out_fields:
+    for name in list(plan.forward.program.out_fields) + list(forward_generic):
         if name is not None:
             written.setdefault(name, "forward_pass")
     if plan.loss is not None:
         written.setdefault(plan.loss.seed_field, "loss")
     if plan.backward is not None:
-        for name in plan.backward.program.out_fields:
+        for name in list(plan.backward.program.out_fields) + list(backward_generic):
             if name is not None:
                 written.setdefault(name, "backward_pass")
     for name in update_unit:
@@ -121,7 +123,19 @@ class BatchedStepFn(StepFn):
     def __init__(self, plan: Plan, static: NetworkStatic, batch_size: int) -> None:
         super().__init__(plan, static)
         self.batch = int(batch_size)
+        self._globals: Any = None
         self.arena_mode = "tiled"  # the batched kernels read the tiled layout's forward rows
+
+    def churn(self) -> bool:
+        return False  # a generic backward reads batch_sources' lists, which the tiled layout has
+
+    def _generic_runners(self) -> list[Any]:
+        """The traced generic passes (forward, backward), None where the pass
+        has the product form."""
+        out = []
+        for which, pp in (("fwd", self.plan.forward), ("bwd", self.plan.backward)):
+            out.append(self._generic_runner(which, self._globals) if pp is not None and pp.generic else None)
+        return out
 
     def _check_policy(self) -> dict[str, Reduction]:
         """Every column a per-sample phase writes has a MEAN / SUM / FIRST
@@ -131,7 +145,9 @@ class BatchedStepFn(StepFn):
         specs = {s.name: s for s in self.static.unit_fields}
         out = {}
         uu = self._update_unit.names if self._update_unit is not None else []
-        for name, where in written_columns(self.plan, self.static, uu).items():
+        gf, gb = self._generic_runners()
+        gen = [list(r.names) if r is not None else [] for r in (gf, gb)]
+        for name, where in written_columns(self.plan, self.static, uu, *gen).items():
             try:
                 out[name] = batch_written_reduction(policy, specs[name], where=where)
             except ValueError as err:
@@ -160,6 +176,11 @@ class BatchedStepFn(StepFn):
         if self._update_generic is not None:
             for prog, _ in self._update_generic.passes:
                 names.update(prog.unit_fields)
+        for run in self._generic_runners():
+            if run is not None:
+                names.update(run.map_prog.unit_fields)
+                names.update(n for n in run.apply_prog.unit_fields if n not in run.acc_names)
+                names.update(run.names)
         names.discard("pruned")
         for p in progs:
             names.update(n for n in p.fields)
@@ -168,6 +189,9 @@ class BatchedStepFn(StepFn):
         return {n: units[n].unsqueeze(1).expand(-1, B).contiguous() for n in sorted(names)}
 
     def __call__(self, state: NetworkState, inputs: StepInputs) -> StepResult:
+        from plastax_amd import grow
+        from plastax_amd.generic import finalize_lists
+
         plan = self.plan
         B = self.batch
         dev = state.device
@@ -191,6 +215,7 @@ class BatchedStepFn(StepFn):
             from plastax_amd import grow
 
             self._update_generic = grow.ConnUpdatePhase(plan.net, self.static, state.globals_)
+        self._globals = state.globals_
         reductions = self._check_policy()
         lib = _lib.load()
         state = state._donate()
@@ -209,13 +234,28 @@ class BatchedStepFn(StepFn):
             pruned=units["pruned"].data_ptr() if "pruned" in units else None,
         )
 
+        gf, gb = self._generic_runners()
+        if (gf is not None or gb is not None) and arena.pipeline:
+            raise UnsupportedPolicyError("a batched step runs generic passes on level-synchronous nets only")
+        pruned = units.get("pruned")
+
         # Forward, per sample (phases.py:942-1015; step.py:443-447).
         fp = plan.forward
         acc = None
-        if arena.fwd_carry:
+        if gf is not None:
+            gf.check_columns(ub, B)
+            k = grow.Kernels(dev, stream)
+            fin_lists = finalize_lists(arena, self.static)["fwd"]
+            gacc = gf.new_acc(n_units, dev, B)
+            for b in range(arena.num_buckets):
+                rows = arena.fwd[b]
+                gf.fold(k, arena, b, ub, gacc, g, rows=rows.rows, nrows=rows.nrows, ptr=rows.ptr, entry_pos=None,
+                        batch=B)
+                gf.apply(k, arena, ub, gacc, g, fin_lists[b], batch=B, pruned=pruned)
+        elif arena.fwd_carry:
             acc = torch.full((n_units, B), fp.identity, dtype=torch.float32, device=dev)
         prog = program_struct(fp.program, ub, g)
-        for b in range(arena.num_buckets):
+        for b in range(arena.num_buckets if gf is None else 0):
             rows = arena.fwd[b]
             d = _lib.plx_forward_desc()
             d.nrows = rows.nrows
@@ -261,7 +301,19 @@ class BatchedStepFn(StepFn):
         # Backward, per sample (phases.py:1049-1104): the deepest level from
         # the identity, then buckets L-1 .. 1 in the reference's slot order.
         bp = plan.backward
-        if bp is not None:
+        if gb is not None:
+            gb.check_columns(ub, B)
+            k = grow.Kernels(dev, stream)
+            fin_lists = finalize_lists(arena, self.static)["bwd"]
+            gacc = gb.new_acc(n_units, dev, B)
+            nb = arena.num_buckets
+            gb.apply(k, arena, ub, gacc, g, fin_lists[nb], batch=B, pruned=pruned)
+            for b in range(nb - 1, 0, -1):
+                lists = batch_sources(arena, b)
+                gb.fold(k, arena, b, ub, gacc, g, rows=lists.rows, nrows=lists.nrows, ptr=lists.ptr,
+                        entry_pos=lists.pos, batch=B)
+                gb.apply(k, arena, ub, gacc, g, fin_lists[b], batch=B, pruned=pruned)
+        elif bp is not None:
             bacc = None
             if arena.bwd_carry:
                 bacc = torch.full((n_units, B), bp.identity, dtype=torch.float32, device=dev)
@@ -306,8 +358,6 @@ class BatchedStepFn(StepFn):
 
         # update_unit, per sample (step.py:435-436), on the live units.
         if plan.update_unit:
-            from plastax_amd import grow
-
             skip = None
             if "pruned" in units:
                 skip = units["pruned"].unsqueeze(1).expand(-1, B).contiguous()

@@ -343,8 +343,11 @@ __device__ __forceinline__ float gen_op(int32_t m, float a, float b) {
 
 __global__ void k_gen_fold(plx_gen_fold_desc d) {
   const uint32_t keyed = px::philox32(0, 1);  // the rng key of an unseeded step-0 site
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < d.nrows;
-       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+  const int64_t B = d.batch > 1 ? d.batch : 1;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < d.nrows * B;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = t / B;
+    const int32_t smp = static_cast<int32_t>(t - r * B);
     const int32_t u = d.row_unit[r];
     float s[8];
     for (int k = 0; k < 8; ++k) s[k] = d.identity[k];
@@ -368,8 +371,8 @@ __global__ void k_gen_fold(plx_gen_fold_desc d) {
       c.seed = static_cast<uint64_t>(keyed) << 32;
       c.ids_logical = d.ids_logical;
       c.ids_physical = d.ids_physical;
-      c.batch = 1;
-      c.sample = 0;
+      c.batch = static_cast<int32_t>(B);
+      c.sample = smp;
       uint32_t out[PLX_MAX_SOUTS];
       for (int k = 0; k < PLX_MAX_SOUTS; ++k) out[k] = 0;
       site_run(d.prog, c, d.num_units, out);
@@ -378,9 +381,10 @@ __global__ void k_gen_fold(plx_gen_fold_desc d) {
       for (int k = 0; k < PLX_MAX_SOUTS; ++k)
         if (k < d.ncomp) s[k] = gen_op(d.monoid[k], s[k], __uint_as_float(out[k]));
     }
+    const int64_t at = static_cast<int64_t>(u) * B + smp;
 #pragma unroll
     for (int k = 0; k < PLX_MAX_SOUTS; ++k)
-      if (k < d.ncomp) d.acc[k][u] = gen_op(d.monoid[k], d.acc[k][u], s[k]);
+      if (k < d.ncomp) d.acc[k][at] = gen_op(d.monoid[k], d.acc[k][at], s[k]);
   }
 }
 
@@ -959,8 +963,10 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_site_eval: unknown site kind");
   if (d->batch > 1 && (d->sample < 0 || d->sample >= d->batch))
     return fail(PLX_ERR_INVALID, "plx_site_eval: sample outside the batch");
-  if (d->batch > 1 && d->kind == PLX_SITES_UNIT && d->n != static_cast<int64_t>(d->num_units) * d->batch)
-    return fail(PLX_ERR_INVALID, "plx_site_eval: batched unit sites are num_units * batch");
+  if (d->batch > 1 && d->kind == PLX_SITES_UNIT &&
+      (d->site_ids ? d->n % d->batch != 0 : d->n != static_cast<int64_t>(d->num_units) * d->batch))
+    return fail(PLX_ERR_INVALID,
+                "plx_site_eval: batched unit sites are num_units * batch (site_ids: a multiple of batch)");
   if ((d->kind == PLX_SITES_CONN && (!d->list_a || !d->from_id || !d->to_id || !d->occ)) ||
       ((d->kind == PLX_SITES_GRID || d->kind == PLX_SITES_PAIRS) && (!d->list_a || !d->list_b)))
     return fail(PLX_ERR_INVALID, "plx_site_eval: site lists missing");
@@ -1228,8 +1234,8 @@ int plx_merge_kills(int64_t n, const uint8_t* sink, uint8_t* dead, float* stamp,
 
 int plx_gen_fold(const plx_gen_fold_desc* d, void* stream) {
   if (!d) return fail(PLX_ERR_INVALID, "plx_gen_fold: null descriptor");
-  if (d->nrows < 0 || d->ncomp < 1 || d->ncomp > 8 || d->num_units <= 0)
-    return fail(PLX_ERR_INVALID, "plx_gen_fold: bad sizes (1 <= ncomp <= 8)");
+  if (d->nrows < 0 || d->ncomp < 1 || d->ncomp > 8 || d->num_units <= 0 || d->batch < 1)
+    return fail(PLX_ERR_INVALID, "plx_gen_fold: bad sizes (1 <= ncomp <= 8, batch >= 1)");
   if (d->nrows == 0) return PLX_OK;
   if (!d->row_unit || !d->row_ptr || (d->backward ? !d->to_id : !d->from_id))
     return fail(PLX_ERR_INVALID, "plx_gen_fold: null row table or id column");
@@ -1238,7 +1244,8 @@ int plx_gen_fold(const plx_gen_fold_desc* d, void* stream) {
   for (int k = 0; k < d->ncomp; ++k)
     if (!d->acc[k] || d->monoid[k] < PLX_MONOID_SUM || d->monoid[k] > PLX_MONOID_MIN)
       return fail(PLX_ERR_INVALID, "plx_gen_fold: bad accumulator column or monoid");
-  hipLaunchKernelGGL(k_gen_fold, dim3(grid_for(d->nrows)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), *d);
+  hipLaunchKernelGGL(k_gen_fold, dim3(grid_for(d->nrows * d->batch)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), *d);
   return check_launch("plx_gen_fold");
 }
 

@@ -82,12 +82,7 @@ def make_step(
     if batch_size is not None:
         from plastax_amd.batched import BatchedStepFn
 
-        plan = compile_plan(net, static)
-        if plan.forward.generic is not None or (plan.backward is not None and plan.backward.generic is not None):
-            raise UnsupportedPolicyError(
-                "make_step: a batched step runs passes of the product form only (a generic map or a tuple "
-                "accumulator runs in the streaming step)")
-        step = BatchedStepFn(plan, static, batch_size)
+        step = BatchedStepFn(compile_plan(net, static), static, batch_size)
     else:
         step = StepFn(compile_plan(net, static), static)
     step.prune_fusion = PruneFusionRecord(fuse_prune)

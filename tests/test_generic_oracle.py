@@ -75,7 +75,7 @@ def test_tuple_accumulator_components_match_closed_forms(oracle) -> None:
     assert np.array_equal(np.isneginf(mx[fin]), deg[fin] == 0)
 
 
-def test_plan_marks_generic_passes_and_batched_steps_refuse_them() -> None:
+def test_plan_marks_generic_passes_and_batched_steps_reduce_their_writes() -> None:
     net = gc.make_net(gc.TanhSrcForward(), nets.TanhBackward())
     static, _ = gc.build(net, pipeline=False, seed=4)
     plan = compile_plan(net, static)
@@ -90,10 +90,62 @@ def test_plan_marks_generic_passes_and_batched_steps_refuse_them() -> None:
     class Batched(tup):
         batch_reduction = px.MeanFloatFirstRest()
 
-    with pytest.raises(UnsupportedPolicyError, match="product form"):
-        px.make_step(Batched, static2, batch_size=4)
+    bstep = px.make_step(Batched, static2, batch_size=4)
+    assert not bstep.churn()  # the batched backward reads batch_sources' lists on the tiled layout
+    bstep._globals = gc.build(Batched, pipeline=False, seed=4)[1].globals_
+    red = bstep._check_policy()
+    # the generic applies' writes are batch-reduced: ACTIVATION and DEG
+    # (forward), GRAD_PRE_ACT (backward), with MeanFloatFirstRest's MEAN
+    assert red[gc.DEG.name] is px.Reduction.MEAN and red[nets.GRAD_PRE_ACT.name] is px.Reduction.MEAN
     step = px.make_step(tup, static2)
     assert step.churn()  # a generic backward folds each source's out-edges from the churn lists
     step.arena_mode = "tiled"
     with pytest.raises(UnsupportedPolicyError, match="churn"):
         step.churn()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_batched_generic_oracle_gives_the_product_paths_bits(oracle, B: int) -> None:
+    """The batched oracle on a generic net whose maps have the product form
+    gives the batched product path's bits (every unit column, every
+    connection column, the loss), so the batched generic writes are reduced
+    exactly as the product outputs are; at B = 1 both are the streaming step
+    (tests/test_batched.py:117-140)."""
+    from oracle import batched as ob
+
+    runs = []
+    for fwd, bwd in ((nets.TanhForward(), nets.TanhBackward()),
+                     (gc.ProductAsTupleForward(), gc.ProductAsTupleBackward())):
+        base = gc.make_net(fwd, bwd)
+
+        class Batched(base):
+            batch_reduction = px.MeanFloatFirstRest()
+
+        static, state = gc.build(Batched, pipeline=False, seed=2)
+        orc = ob.OracleBatch(_oracle(oracle, Batched, static, state), B)
+        rng = np.random.default_rng(3)
+        n_in, n_out = len(static.input_ids), len(static.output_ids)
+        losses = []
+        for _ in range(3):
+            x = rng.standard_normal((B, n_in)).astype(np.float32)
+            t = rng.standard_normal((B, n_out)).astype(np.float32)
+            losses.append(orc.step(x, t))
+        runs.append((losses, orc.o.units, orc.o.conns))
+    if B == 1:  # and the streaming oracle on the same inputs
+        static, state = gc.build(gc.make_net(nets.TanhForward(), nets.TanhBackward()), pipeline=False, seed=2)
+        o = _oracle(oracle, gc.make_net(nets.TanhForward(), nets.TanhBackward()), static, state)
+        rng = np.random.default_rng(3)
+        losses = []
+        for _ in range(3):
+            x = rng.standard_normal((1, len(static.input_ids))).astype(np.float32)
+            t = rng.standard_normal((1, len(static.output_ids))).astype(np.float32)
+            losses.append(o.step(x[0], t[0]))
+        runs.append((losses, o.units, o.conns))
+    (la, ua, ca) = runs[0]
+    for lb, ub, cb in runs[1:]:
+        assert np.array_equal(np.float32(la).view(np.uint32), np.float32(lb).view(np.uint32))
+        for name in ua:
+            assert np.array_equal(np.asarray(ua[name]).view(np.uint8), np.asarray(ub[name]).view(np.uint8)), name
+        for a, b in zip(ca, cb):
+            for name in a:
+                assert np.array_equal(np.asarray(a[name]).view(np.uint8), np.asarray(b[name]).view(np.uint8)), name

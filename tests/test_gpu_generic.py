@@ -71,3 +71,41 @@ def test_product_map_as_a_tuple_matches_the_product_kernels(oracle) -> None:
     for a, b in zip(nets.host_conns(sp, st_p), nets.host_conns(sp, st_g)):
         for name in a:
             assert np.array_equal(np.asarray(a[name]).view(np.uint8), np.asarray(b[name]).view(np.uint8)), name
+
+
+@pytest.mark.parametrize(
+    ("forward", "backward", "B"),
+    [
+        (gc.TanhSrcForward(), nets.TanhBackward(), 3),
+        (gc.TupleForward(), gc.ThreeFactorBackward(), 4),
+        (gc.TupleForward(), gc.ThreeFactorBackward(), 1),
+    ],
+)
+def test_batched_generic_passes_match_the_batched_oracle(oracle, forward, backward, B: int) -> None:
+    """A generic forward / backward per sample (step.py:443-447): the fold
+    per (row, sample), the apply per (finalized unit, sample), the apply's
+    written columns batch-reduced (phases.py:298-387) -- against the batched
+    oracle bit for bit."""
+    from oracle import batched as ob
+
+    base = gc.make_net(forward, backward, optimizer=px.optim.adam(1e-2, nets.GRAD_PRE_ACT))
+
+    class Batched(base):
+        batch_reduction = px.MeanFloatFirstRest()
+
+    static, state = gc.build(Batched, pipeline=False, seed=7, device="cuda")
+    o = nets.oracle_for(oracle, Batched, static, state)
+    orc = ob.OracleBatch(o, B)
+    step = px.make_step(Batched, static, batch_size=B)
+    rng = np.random.default_rng(8)
+    n_in, n_out = len(static.input_ids), len(static.output_ids)
+    for k in range(4):
+        x = rng.standard_normal((B, n_in)).astype(np.float32)
+        t = rng.standard_normal((B, n_out)).astype(np.float32)
+        print(f"batched generic pass step {k} B={B} {forward.__class__.__name__}", flush=True)
+        res = step(state, px.StepInputs(x, t))
+        state = res.state
+        lo = orc.step(x, t)
+        torch.cuda.synchronize()
+        assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at step {k}"
+        assert_same_state(static, state, o, f"step {k}")
