@@ -12,9 +12,9 @@ reference's examples xmc.py, upgd.py, cbp.py) -- runs here:
 - ``plx_gen_fold`` folds each row's entries in order, one thread per row:
   a forward row is a destination, its entries the slab range of its
   in-edges (slot order); a backward row a source, its entries its out-edges
-  in slot order (the churn layout's lists, so a generic backward lays the
-  arena out with that layout); each component from its monoid's identity,
-  then combined into the carried accumulator columns;
+  in slot order (the churn layout's lists, or on a tiled arena the
+  per-source lists of ``batched.batch_sources``); each component from its
+  monoid's identity, then combined into the carried accumulator columns;
 - the apply is traced into a unit program reading the accumulator from
   those columns (``_site.trace_pass_apply``), evaluated for the units the
   bucket finalizes against the pre-apply columns, its writes committed with

@@ -162,9 +162,6 @@ class StepFn:
         if self.arena_mode != "auto":
             if self.arena_mode not in ("tiled", "churn"):
                 raise ValueError(f"arena_mode must be 'auto', 'tiled' or 'churn', got {self.arena_mode!r}")
-            if (self.arena_mode == "tiled" and self.plan.backward is not None
-                    and self.plan.backward.generic is not None):
-                raise UnsupportedPolicyError("a generic backward pass runs on the churn layout, not the tiled one")
             return self.arena_mode == "churn"
         if self.plan.backward is not None and self.plan.backward.generic is not None:
             return True  # a generic backward folds each source's out-edges from the churn lists
@@ -445,15 +442,24 @@ class StepFn:
         acc = run.new_acc(n, arena.device)
         rows = torch.arange(n, dtype=torch.int32, device=arena.device)
         nb = arena.num_buckets
+        churn = hasattr(arena, "lists")
         if arena.pipeline:
+            if not churn:
+                raise UnsupportedPolicyError("a generic backward on a PIPELINE net runs on the churn layout")
             lists = arena.lists[0]
             run.fold(k, arena, 0, units, acc, g, rows=rows, nrows=n, ptr=lists.ptr, entry_pos=lists.pos)
             run.apply(k, arena, units, acc, g, fin[0])
             return
         run.apply(k, arena, units, acc, g, fin[nb])
         for b in range(nb - 1, 0, -1):
-            lists = arena.lists[b]
-            run.fold(k, arena, b, units, acc, g, rows=rows, nrows=n, ptr=lists.ptr, entry_pos=lists.pos)
+            if churn:
+                lists = arena.lists[b]
+                run.fold(k, arena, b, units, acc, g, rows=rows, nrows=n, ptr=lists.ptr, entry_pos=lists.pos)
+            else:  # the tiled layout: each source's out-edges in slot order from batch_sources
+                from plastax_amd.batched import batch_sources
+
+                bs = batch_sources(arena, b)
+                run.fold(k, arena, b, units, acc, g, rows=bs.rows, nrows=bs.nrows, ptr=bs.ptr, entry_pos=bs.pos)
             run.apply(k, arena, units, acc, g, fin[b])
 
     # -- fused forward + prune (phases.py:1629-1848, :2322-2469) ---------------
@@ -756,7 +762,9 @@ class StepFn:
                          fin_common: dict, stream: int, g: Any) -> None:
         bp, up = plan.backward, plan.update
         nb = arena.num_buckets
-        if getattr(arena, "churn", False):
+        # (a generic backward is its own pass on either layout; the update
+        # then runs bucket by bucket on its own)
+        if getattr(arena, "churn", False) or (bp is not None and bp.generic is not None):
             if bp is not None and bp.generic is not None:
                 self._backward_generic(arena, units, stream, g)
             elif bp is not None:

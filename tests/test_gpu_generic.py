@@ -22,10 +22,11 @@ from test_gpu_parity import _equal, assert_same_state
 pytestmark = pytest.mark.gpu
 
 
-def _run(oracle, net, pipeline: bool, steps: int, seed: int):
+def _run(oracle, net, pipeline: bool, steps: int, seed: int, arena_mode: str = "auto"):
     static, state = gc.build(net, pipeline=pipeline, seed=seed, device="cuda")
     o = nets.oracle_for(oracle, net, static, state)
     step = px.make_step(net, static)
+    step.arena_mode = arena_mode
     if step.backward_order == "slot":
         o.tile = None
     xs, ts = gc.data(seed + 1, steps, len(static.input_ids), len(static.output_ids))
@@ -53,6 +54,13 @@ def _run(oracle, net, pipeline: bool, steps: int, seed: int):
 def test_generic_passes_match_the_oracle(oracle, forward, backward, pipeline: bool) -> None:
     net = gc.make_net(forward, backward, pipeline=pipeline, optimizer=px.optim.adam(1e-2, nets.GRAD_PRE_ACT))
     _run(oracle, net, pipeline, 6, 11)
+
+
+def test_generic_backward_on_the_tiled_layout(oracle) -> None:
+    """arena_mode="tiled": the generic backward folds each source's
+    out-edges in slot order from the tiled arena's batch_sources lists."""
+    net = gc.make_net(gc.TupleForward(), gc.ThreeFactorBackward(), optimizer=px.optim.adam(1e-2, nets.GRAD_PRE_ACT))
+    _run(oracle, net, False, 5, 13, arena_mode="tiled")
 
 
 def test_product_map_as_a_tuple_matches_the_product_kernels(oracle) -> None:
