@@ -117,3 +117,69 @@ def test_batched_generic_passes_match_the_batched_oracle(oracle, forward, backwa
         torch.cuda.synchronize()
         assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at step {k}"
         assert_same_state(static, state, o, f"step {k}")
+
+
+class _TauPrune(px.PruneConn):
+    def predicate(self, u, c, cid, g):
+        return px.numpy.abs(c[px.WEIGHT, cid]) < np.float32(0.03)
+
+
+class _Grow(px.ScoreAddConn):
+    candidates = "shortlist_per_level"
+    shortlist_size = 8
+    direction = "deeper"
+    dedupe_live = True
+    max_new_per_level = 10
+
+    def score(self, u, src, dst, g):
+        return px.numpy.abs(u[px.ACTIVATION, src] * u[nets.GRAD_PRE_ACT, dst])
+
+    def importance(self, u, i, g):
+        return px.numpy.abs(u[nets.GRAD_PRE_ACT, i]) + px.numpy.abs(u[px.ACTIVATION, i])
+
+    def init(self, u, src, dst, g):
+        return px.ConnWrite.of((px.WEIGHT, np.float32(0.0)))
+
+
+@pytest.mark.parametrize("B", [None, 3])
+def test_generic_passes_with_pruning_and_growth(oracle, B) -> None:
+    """Tombstones inside the backward's per-source lists (PruneConn each
+    step) and a new layout after every growth, under a generic forward and
+    backward: the streaming step on the tiled layout (B None) and a batched
+    step (B = 3), against the oracle bit for bit."""
+    from oracle import batched as ob
+
+    base = gc.make_net(gc.TupleForward(), gc.ThreeFactorBackward(), optimizer=px.optim.adam(1e-2, nets.GRAD_PRE_ACT))
+
+    class Net(base):
+        prune_conn = _TauPrune()
+        add_conn = _Grow()
+        batch_reduction = px.MeanFloatFirstRest()
+
+    static, state = gc.build(Net, pipeline=False, seed=7, device="cuda")
+    o = nets.oracle_for(oracle, Net, static, state)
+    if B is None:
+        step = px.make_step(Net, static)
+        step.arena_mode = "tiled"
+    else:
+        step = px.make_step(Net, static, batch_size=B)
+        orc = ob.OracleBatch(o, B)
+    rng = np.random.default_rng(8)
+    n_in, n_out = len(static.input_ids), len(static.output_ids)
+    for k in range(4):
+        nb = B or 1
+        x = rng.standard_normal((nb, n_in)).astype(np.float32)
+        t = rng.standard_normal((nb, n_out)).astype(np.float32)
+        print(f"generic prune+growth step {k} B={B}", flush=True)
+        if B is None:
+            res = step(state, px.StepInputs(x[0], t[0]))
+            lo = o.step(x[0], t[0])
+        else:
+            res = step(state, px.StepInputs(x, t))
+            lo = orc.step(x, t)
+        state = res.state
+        torch.cuda.synchronize()
+        assert (state.grown, state.overflow) == (o.grown, o.overflow), f"flags at step {k}"
+        assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at step {k}"
+        assert_same_state(static, state, o, f"step {k}")
+    assert o.grown > 0 and sum(int(c["dead"].sum()) for c in o.conns) > 0
