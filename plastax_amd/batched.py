@@ -123,21 +123,20 @@ class BatchedStepFn(StepFn):
     def __init__(self, plan: Plan, static: NetworkStatic, batch_size: int) -> None:
         super().__init__(plan, static)
         self.batch = int(batch_size)
-        self._globals: Any = None
         self.arena_mode = "tiled"  # the batched kernels read the tiled layout's forward rows
 
     def churn(self) -> bool:
         return False  # a generic backward reads batch_sources' lists, which the tiled layout has
 
-    def _generic_runners(self) -> list[Any]:
+    def _generic_runners(self, g: Any) -> list[Any]:
         """The traced generic passes (forward, backward), None where the pass
-        has the product form."""
+        has the product form (traced on the first call, against ``g``)."""
         out = []
         for which, pp in (("fwd", self.plan.forward), ("bwd", self.plan.backward)):
-            out.append(self._generic_runner(which, self._globals) if pp is not None and pp.generic else None)
+            out.append(self._generic_runner(which, g) if pp is not None and pp.generic else None)
         return out
 
-    def _check_policy(self) -> dict[str, Reduction]:
+    def _check_policy(self, g: Any) -> dict[str, Reduction]:
         """Every column a per-sample phase writes has a MEAN / SUM / FIRST
         reduction (step.py:429-441); returns them."""
         net = self.plan.net
@@ -145,7 +144,7 @@ class BatchedStepFn(StepFn):
         specs = {s.name: s for s in self.static.unit_fields}
         out = {}
         uu = self._update_unit.names if self._update_unit is not None else []
-        gf, gb = self._generic_runners()
+        gf, gb = self._generic_runners(g)
         gen = [list(r.names) if r is not None else [] for r in (gf, gb)]
         for name, where in written_columns(self.plan, self.static, uu, *gen).items():
             try:
@@ -154,7 +153,7 @@ class BatchedStepFn(StepFn):
                 raise ValueError(f"{net.__name__}.{err}") from None
         return out
 
-    def _batched_columns(self, units: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
+    def _batched_columns(self, units: dict[str, torch.Tensor], g: Any) -> dict[str, torch.Tensor]:
         """[num_units, B] copies of every column a per-sample phase reads or
         writes (each sample starts from the shared state: step.py:421-424)."""
         plan = self.plan
@@ -176,7 +175,7 @@ class BatchedStepFn(StepFn):
         if self._update_generic is not None:
             for prog, _ in self._update_generic.passes:
                 names.update(prog.unit_fields)
-        for run in self._generic_runners():
+        for run in self._generic_runners(g):
             if run is not None:
                 names.update(run.map_prog.unit_fields)
                 names.update(n for n in run.apply_prog.unit_fields if n not in run.acc_names)
@@ -215,8 +214,7 @@ class BatchedStepFn(StepFn):
             from plastax_amd import grow
 
             self._update_generic = grow.ConnUpdatePhase(plan.net, self.static, state.globals_)
-        self._globals = state.globals_
-        reductions = self._check_policy()
+        reductions = self._check_policy(state.globals_)
         lib = _lib.load()
         state = state._donate()
         arena = self.arena(state)
@@ -225,7 +223,7 @@ class BatchedStepFn(StepFn):
         units = state._physical_units(arena)
         n_units = self.static.num_units
         g = state.globals_
-        ub = self._batched_columns(units)
+        ub = self._batched_columns(units, g)
         if n_in:
             ub[ACTIVATION.name][consts["input_ids"].long()] = x.t()
         fin = dict(
@@ -234,7 +232,7 @@ class BatchedStepFn(StepFn):
             pruned=units["pruned"].data_ptr() if "pruned" in units else None,
         )
 
-        gf, gb = self._generic_runners()
+        gf, gb = self._generic_runners(g)
         if (gf is not None or gb is not None) and arena.pipeline:
             raise UnsupportedPolicyError("a batched step runs generic passes on level-synchronous nets only")
         pruned = units.get("pruned")

@@ -91,8 +91,7 @@ def test_plan_marks_generic_passes_and_batched_steps_reduce_their_writes() -> No
 
     bstep = px.make_step(Batched, static2, batch_size=4)
     assert not bstep.churn()  # the batched backward reads batch_sources' lists on the tiled layout
-    bstep._globals = gc.build(Batched, pipeline=False, seed=4)[1].globals_
-    red = bstep._check_policy()
+    red = bstep._check_policy(gc.build(Batched, pipeline=False, seed=4)[1].globals_)
     # the generic applies' writes are batch-reduced: ACTIVATION and DEG
     # (forward), GRAD_PRE_ACT (backward), with MeanFloatFirstRest's MEAN
     assert red[gc.DEG.name] is px.Reduction.MEAN and red[nets.GRAD_PRE_ACT.name] is px.Reduction.MEAN
