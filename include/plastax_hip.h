@@ -913,9 +913,14 @@ PLX_EXPORT const char* plx_last_error(void);
  * resort being topo.py:303-452). One workgroup per tile sorts the tile's live
  * positions by (physical source, position) in LDS. Positions are relative to
  * the bucket; the first `live` hold its live edges, destination-sorted, with
- * physical FROM_ID src[p]; tile t is [tile_pos[t], tile_pos[t+1]).
- *   pass 0: ngroups[t] = the tile's (tile, source) groups; presence[u] +=
- *           the tiles holding source u (presence zeroed by the caller).
+ * physical FROM_ID src[p] (any non-negative int32 id: the sort keys are 64
+ * bits); tile t is [tile_pos[t], tile_pos[t+1]) and spans at most 4096
+ * positions.
+ *   pass 0: ngroups[t] = the tile's (tile, source) groups, or -1 where the
+ *           tile spans more than 4096 positions (its tables are then
+ *           unusable; the caller reads the counts and refuses them);
+ *           presence[u] += the tiles holding source u (presence zeroed by
+ *           the caller).
  *   pass 1: sorted_rank[p] = rank of p in its tile's order | 0x8000 where the
  *           rank starts a group (positions past `live` are not written);
  *           per group, in (tile, source) order from grp_off[t]: g_src, g_st

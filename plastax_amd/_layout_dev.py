@@ -240,6 +240,9 @@ class DeviceArena(Arena):
         _lib.check(lib.plx_tile_build(d, k.s), "plx_tile_build")
         pres = presence.cpu().numpy().astype(np.int64)
         ng = ngroups.cpu().numpy().astype(np.int64)[:ntiles]
+        if (ng < 0).any():
+            raise ValueError(f"plx_tile_build: tile {int(np.flatnonzero(ng < 0)[0])} spans more than "
+                             "4096 positions")
         grp_off = np.concatenate([[0], np.cumsum(ng)]).astype(np.int64)
         total_groups = int(grp_off[-1])
 

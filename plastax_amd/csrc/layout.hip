@@ -28,13 +28,14 @@ constexpr int kPerT = kTileMax / kTB;
 constexpr uint32_t kStart = 0x8000u;
 
 // Sorts keys[0, kTileMax) ascending (bitonic; every thread takes part).
-__device__ void bitonic4096(uint32_t* keys) {
+template <typename K>
+__device__ void bitonic4096(K* keys) {
   for (int k = 2; k <= kTileMax; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = threadIdx.x; i < kTileMax; i += kTB) {
         const int ixj = i ^ j;
         if (ixj > i) {
-          const uint32_t a = keys[i], b = keys[ixj];
+          const K a = keys[i], b = keys[ixj];
           const bool up = (i & k) == 0;
           if ((a > b) == up) {
             keys[i] = b;
@@ -74,47 +75,59 @@ __device__ int block_scan(int v, int* lds, int* total) {
   return out;
 }
 
-// The tile's live positions' keys (source << 12 | position in the tile),
-// sorted; n = their number.
-__device__ int load_sorted(const plx_tile_build_desc& d, int t, uint32_t* keys) {
+// The tile's live positions' keys (source << 12 | position in the tile, in
+// 64 bits, so any int32 source id fits), sorted; n = their number. A tile
+// spanning more than kTileMax positions breaks the caller's contract: its
+// first kTileMax positions are sorted (every LDS access stays in bounds) and
+// *over is set.
+__device__ int load_sorted(const plx_tile_build_desc& d, int t, uint64_t* keys, bool* over) {
   const int p0 = d.tile_pos[t];
-  const int n = max(0, min(d.tile_pos[t + 1], d.live) - p0);
+  const int span = max(0, min(d.tile_pos[t + 1], d.live) - p0);
+  *over = span > kTileMax;
+  const int n = min(span, kTileMax);
   for (int i = threadIdx.x; i < kTileMax; i += kTB)
-    keys[i] = i < n ? (static_cast<uint32_t>(d.src[p0 + i]) << 12) | static_cast<uint32_t>(i) : 0xFFFFFFFFu;
+    keys[i] = i < n ? (static_cast<uint64_t>(static_cast<uint32_t>(d.src[p0 + i])) << 12) | static_cast<uint64_t>(i)
+                    : ~0ull;
   __syncthreads();
   bitonic4096(keys);
   return n;
 }
 
+__device__ __forceinline__ uint32_t key_src(uint64_t k) { return static_cast<uint32_t>(k >> 12); }
+
 // Pass 0: groups per tile, and every group's source counted in presence.
+// A tile longer than kTileMax positions reports -1 groups (the host reads
+// the counts and refuses the layout).
 __global__ __launch_bounds__(kTB) void k_tile_count(plx_tile_build_desc d) {
-  __shared__ uint32_t keys[kTileMax];
+  __shared__ uint64_t keys[kTileMax];
   __shared__ int scan_lds[kTB / 64 + 1];
   const int t = blockIdx.x;
-  const int n = load_sorted(d, t, keys);
+  bool over = false;
+  const int n = load_sorted(d, t, keys, &over);
   int mine = 0;
   for (int k = 0; k < kPerT; ++k) {
     const int i = threadIdx.x * kPerT + k;
-    if (i < n && (i == 0 || (keys[i] >> 12) != (keys[i - 1] >> 12))) {
+    if (i < n && (i == 0 || key_src(keys[i]) != key_src(keys[i - 1]))) {
       ++mine;
-      atomicAdd(d.presence + (keys[i] >> 12), 1);
+      atomicAdd(d.presence + key_src(keys[i]), 1);
     }
   }
   int total = 0;
   block_scan(mine, scan_lds, &total);
-  if (threadIdx.x == 0) d.ngroups[t] = total;
+  if (threadIdx.x == 0) d.ngroups[t] = over ? -1 : total;
 }
 
 // Pass 1: the tile's tables.
 __global__ __launch_bounds__(kTB) void k_tile_tables(plx_tile_build_desc d) {
-  __shared__ uint32_t keys[kTileMax];
+  __shared__ uint64_t keys[kTileMax];
   __shared__ uint32_t gkey[kTileMax];
-  __shared__ int gstart[kTileMax + 1];
+  __shared__ uint16_t gstart[kTileMax + 1];  // ranks 0..kTileMax; the workgroup stays within 64 KiB of LDS
   __shared__ int scan_lds[kTB / 64 + 1];
   __shared__ int counts[2 + 8];
   const int t = blockIdx.x;
   const int p0 = d.tile_pos[t];
-  const int n = load_sorted(d, t, keys);
+  bool over = false;
+  const int n = load_sorted(d, t, keys, &over);
   const uint32_t hb = static_cast<uint32_t>(d.hot_base), he = hb + static_cast<uint32_t>(d.nhot);
   if (threadIdx.x < 10) counts[threadIdx.x] = 0;
   // Group starts of this thread's consecutive ranks, then their indices.
@@ -122,7 +135,7 @@ __global__ __launch_bounds__(kTB) void k_tile_tables(plx_tile_build_desc d) {
   int mine = 0;
   for (int k = 0; k < kPerT; ++k) {
     const int i = threadIdx.x * kPerT + k;
-    st[k] = i < n && (i == 0 || (keys[i] >> 12) != (keys[i - 1] >> 12));
+    st[k] = i < n && (i == 0 || key_src(keys[i]) != key_src(keys[i - 1]));
     mine += st[k];
   }
   int ng = 0;
@@ -132,17 +145,17 @@ __global__ __launch_bounds__(kTB) void k_tile_tables(plx_tile_build_desc d) {
   for (int k = 0; k < kPerT; ++k) {
     const int i = threadIdx.x * kPerT + k;
     if (i >= n) break;
-    const uint32_t src = keys[i] >> 12;
+    const uint32_t src = key_src(keys[i]);
     const int pos = p0 + static_cast<int>(keys[i] & 0xFFFu);
     d.sorted_rank[pos] = static_cast<uint16_t>(static_cast<uint32_t>(i) | (st[k] ? kStart : 0u));
-    if (st[k]) gstart[g++] = i;
+    if (st[k]) gstart[g++] = static_cast<uint16_t>(i);
     if (src < hb)
       ++hlo;
     else if (src < he)
       ++hcnt;
     if (src < hb || src >= he) ++rc[d.region[src] & 7];
   }
-  if (threadIdx.x == 0) gstart[ng] = n;
+  if (threadIdx.x == 0) gstart[ng] = static_cast<uint16_t>(n);
   atomicAdd(&counts[0], hlo);
   atomicAdd(&counts[1], hcnt);
   for (int x = 0; x < 8; ++x)
@@ -154,7 +167,7 @@ __global__ __launch_bounds__(kTB) void k_tile_tables(plx_tile_build_desc d) {
   for (int q = threadIdx.x; q < kTileMax; q += kTB) {
     if (q < ng) {
       const int s0 = gstart[q], len = gstart[q + 1] - s0;
-      d.g_src[g0 + q] = static_cast<int32_t>(keys[s0] >> 12);
+      d.g_src[g0 + q] = static_cast<int32_t>(key_src(keys[s0]));
       d.g_st[g0 + q] = s0;
       d.g_tile[g0 + q] = t;
       gkey[q] = (static_cast<uint32_t>(kTileMax - len) << 12) | static_cast<uint32_t>(q);

@@ -14,6 +14,9 @@ import plastax_amd.numpy as jnp
 
 UTIL = px.FieldSpec.float32("test/util", 0.5)
 DEG = px.FieldSpec.float32("test/deg")
+MX = px.FieldSpec.float32("test/mx")
+MN = px.FieldSpec.float32("test/mn")
+PR = px.FieldSpec.float32("test/pr")
 
 
 class TanhSrcForward(px.ForwardPass):
@@ -39,7 +42,23 @@ class TupleForward(px.ForwardPass):
 
     def apply(self, u, i, g, acc):
         s, m, n = acc
-        return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(s) + m * jnp.float32(0.01)), (DEG, n))
+        return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(s) + m * jnp.float32(0.01)), (DEG, n), (MX, m))
+
+
+class MinProdMaxForward(px.ForwardPass):
+    """(min util, product of util, max |w| * util) under (min, prod, max):
+    every named monoid but sum in one tuple; each component is also written
+    to its own unit column."""
+
+    combine = (px.monoid.min_, px.monoid.prod, px.monoid.max_)
+
+    def map(self, u, dst, src, c, cid, g):
+        return (c[UTIL, cid], c[UTIL, cid], jnp.abs(c[px.WEIGHT, cid]) * c[UTIL, cid])
+
+    def apply(self, u, i, g, acc):
+        mn, pr, mx = acc
+        return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(mn + pr * jnp.float32(0.01))), (MN, mn), (PR, pr),
+                               (MX, mx))
 
 
 class ProductAsTupleForward(px.ForwardPass):
@@ -88,7 +107,7 @@ def make_net(forward, backward, *, pipeline: bool = False, optimizer=None):
         backward_pass = backward
         loss = nets.MSELoss()
         update_conn = opt.update_conn()
-        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD, DEG)
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD, DEG, MX, MN, PR)
         extra_conn_fields = (UTIL, *tuple(opt.state_fields))
         propagation = px.Propagation.PIPELINE if pipeline else px.Propagation.TOPOLOGICAL
 

@@ -4,9 +4,11 @@ plan and in the oracle, on the host.
 The oracle's generic path is pinned two ways: a product map written as a
 one-element tuple runs through it and must give the product path's bits
 (same fold order: each row's live edges in slot order); and a tuple
-accumulator's count component must equal the in-degree (a closed form),
-its max component the largest |w| * util of each destination's live
-in-edges.
+accumulator's components must equal their closed forms: the count
+component the in-degree, the max component (written to its own column) the
+numpy scatter-max of |w| * util over each destination's live in-edges,
+-inf where a row has none. The min and prod components are pinned the same
+way in test_monoid_oracle.py.
 """
 
 from __future__ import annotations
@@ -54,6 +56,9 @@ def test_tuple_accumulator_components_match_closed_forms(oracle) -> None:
     rng = np.random.default_rng(0)
     for c in o.conns:  # a varied UTIL column
         c[gc.UTIL.name] = rng.random(c["dead"].size).astype(np.float32)
+        live = np.flatnonzero(c["dead"] == 0)
+        c["dead"][live[::9]] = 1  # tombstones inside the rows
+        c["dead"][c["to_id"] == 30] = 1  # a level-1 row with no live in-edge
     x = rng.standard_normal(len(static.input_ids)).astype(np.float32)
     o.units["activation"][np.asarray(static.input_ids)] = x
     o.forward()
@@ -68,10 +73,10 @@ def test_tuple_accumulator_components_match_closed_forms(oracle) -> None:
     is_in[np.asarray(static.input_ids)] = True
     fin = ~is_in & (o.units["level"] >= 1)
     assert np.array_equal(o.units[gc.DEG.name][fin], deg[fin].astype(np.float32))
-    # ACTIVATION = tanh(sum) + 0.01 * max: the max term recovered exactly where sum's tanh is known
-    a = o.units["activation"][fin]
-    assert np.all(np.isfinite(a))
-    assert np.array_equal(np.isneginf(mx[fin]), deg[fin] == 0)
+    got = o.units[gc.MX.name][fin]
+    assert np.array_equal(got.view(np.uint32), mx[fin].view(np.uint32))
+    assert deg[30] == 0 and o.units[gc.MX.name][30] == -np.inf
+    assert np.array_equal(np.isneginf(got), deg[fin] == 0)
 
 
 def test_plan_marks_generic_passes_and_batched_steps_reduce_their_writes() -> None:

@@ -163,3 +163,29 @@ def test_layout_after_device_growth_and_prune(oracle) -> None:
     state.conns  # write the arena back to the logical buckets
     print("layout: after growth", flush=True)
     _compare(static, state)
+
+
+def test_sources_above_2_to_the_20() -> None:
+    """Physical source ids past 2^20 (2^20 + 64 input units, each feeding one
+    of 96 hidden units, which feed 8 outputs): the tile build's sort keys
+    hold (source << 12 | position) in 64 bits, so bucket 1's sources, whose
+    physical ids all lie above 2^20, keep their ids, and the arena equals
+    the host build."""
+    n_in, n_hid, n_out = (1 << 20) + 64, 96, 8
+    rng = np.random.default_rng(5)
+    src0 = np.arange(n_in, dtype=np.int32)
+    dst0 = (n_in + rng.integers(0, n_hid, n_in)).astype(np.int32)
+    src1 = np.repeat(np.arange(n_in, n_in + n_hid, dtype=np.int32), 4)
+    dst1 = (n_in + n_hid + rng.integers(0, n_out, src1.size)).astype(np.int32)
+    src = np.concatenate([src0, src1])
+    dst = np.concatenate([dst0, dst1])
+    w = (rng.standard_normal(src.size) * 0.1).astype(np.float32)
+    opt = px.optim.adam(1e-3, nets.GRAD_PRE_ACT)
+    net = nets.make_trained_net("Wide20", nets.TanhForward(), nets.TanhBackward(), opt,
+                                px.Propagation.TOPOLOGICAL)
+    static, state = px.NetworkBuilder.from_edges(
+        net, n_in + n_hid + n_out, src, dst, weights=w, input_ids=np.arange(n_in),
+        output_ids=np.arange(n_in + n_hid, n_in + n_hid + n_out), globals_=None, device="cuda")
+    print("layout: sources above 2^20", flush=True)
+    host = _compare(static, state, tile=128, nsuper=8)
+    assert int(host.lvl_start[1]) >= 1 << 20
