@@ -29,7 +29,12 @@ from plastax_amd._types import (
 )
 from plastax_amd.builder import NetworkBuilder
 from plastax_amd.driver import Driver
-from plastax_amd.growth_config import predicate_add_conn
+from plastax_amd.growth_config import (
+    ShortlistCoverage,
+    predicate_add_conn,
+    recommended_shortlist,
+    shortlist_coverage,
+)
 from plastax_amd.monoid import Monoid, UnsupportedMonoidError
 from plastax_amd.state import (
     NetworkState,
@@ -50,6 +55,7 @@ from plastax_amd.traits import (
     Loss,
     MeanFloatFirstRest,
     Network,
+    Proposal,
     ProposeAddConn,
     PruneConn,
     PruneUnit,
@@ -90,12 +96,14 @@ __all__ = [
     "NetworkState",
     "NetworkStatic",
     "Propagation",
+    "Proposal",
     "ProposeAddConn",
     "PruneConn",
     "PruneUnit",
     "ResetGlobal",
     "ScoreAddConn",
     "ShardSpec",
+    "ShortlistCoverage",
     "SoftmaxCrossEntropyLoss",
     "StepInputs",
     "StepResult",
@@ -117,6 +125,8 @@ __all__ = [
     "numpy",
     "optim",
     "predicate_add_conn",
+    "recommended_shortlist",
     "rng",
+    "shortlist_coverage",
     "topo",
 ]

@@ -141,8 +141,78 @@ def _as_kind(x: "Expr", kind: str) -> "Expr":
     return Expr("cvt", (x,), dtype=kind)
 
 
+def _is_vector(x: Any) -> bool:
+    return isinstance(x, np.ndarray) and x.ndim == 1
+
+
+def _elements(x: Any, n: int) -> list:
+    if _is_vector(x):
+        if x.size != n:
+            raise UnsupportedPolicyError(f"constant arrays of lengths {x.size} and {n} do not broadcast")
+        return [x[k] for k in range(n)]
+    return [x] * n
+
+
+def vector_binary(op: str, a: Any, b: Any) -> np.ndarray:
+    """An elementwise op where an operand is a 1-D constant array (or an
+    array of traced values): an object array of traced scalars, one per
+    element (jnp broadcasting of a scalar against a vector)."""
+    n = a.size if _is_vector(a) else b.size
+    out = np.empty(n, dtype=object)
+    for k, (x, y) in enumerate(zip(_elements(a, n), _elements(b, n))):
+        out[k] = binary(op, x, y)
+    return out
+
+
+def const_gather(values: np.ndarray, key: Any) -> "Expr":
+    """``values[key]`` for a 1-D constant array and a traced integer, with
+    jnp's gather semantics: a negative index counts from the end, then the
+    index is clamped into the array (an out-of-range read returns the
+    nearest end). Compiled as a chain of selects."""
+    values = np.asarray(values)
+    if values.ndim != 1 or values.size == 0:
+        raise UnsupportedPolicyError("a traced index reads a non-empty 1-D constant array")
+    k = lift(key)
+    if k.dtype in ("f", "wf", "b"):
+        raise UnsupportedPolicyError("an array index must be an integer")
+    n = values.size
+    k = select(binary("lt", k, 0), binary("add", k, n), k)
+    out: Any = values[n - 1]
+    for j in range(n - 2, -1, -1):
+        out = select(binary("le", k, j), values[j], out)
+    return lift(out)
+
+
+def vector_sum(x: np.ndarray) -> "Expr":
+    """jnp.sum of a vector of traced scalars: booleans count as int32; the
+    elements fold left to right (a float sum over a constant-length vector
+    rounds in that order)."""
+    items = [lift(v) for v in x]
+    if not items:
+        return Expr("const", value=0, dtype="wi")
+    items = [_as_kind(v, "i") if v.dtype == "b" else v for v in items]
+    out = items[0]
+    for v in items[1:]:
+        out = binary("add", out, v)
+    return out
+
+
+class ConstArray(np.ndarray):
+    """A constant array a traced policy may index with a traced integer
+    (``table[layer]``, see const_gather) or compare and combine with traced
+    scalars elementwise; on concrete indices it is a plain numpy array.
+    ``plastax_amd.numpy.asarray`` returns one for non-traced input."""
+
+    def __getitem__(self, key: Any) -> Any:
+        if isinstance(key, Expr):
+            return const_gather(self.view(np.ndarray), key)
+        return super().__getitem__(key)
+
+
 def binary(op: str, a: Any, b: Any) -> "Expr":
     """A typed binary node: arithmetic, comparison or logical."""
+    if _is_vector(a) or _is_vector(b):
+        return vector_binary(op, a, b)  # type: ignore[return-value]
     a, b = lift(a), lift(b)
     if op == "div":
         t = "f"  # true division: ints go to float32, as jnp's / does

@@ -11,7 +11,7 @@ computes the static sizes the phase needs (candidate pool, per-level budget
 from __future__ import annotations
 
 import dataclasses
-from typing import Any, Callable
+from typing import Any, Callable, NamedTuple
 
 import numpy as np
 
@@ -190,3 +190,58 @@ def predicate_add_conn(should_add: Callable[..., Any], init: Callable[..., Any],
     for key, value in params.items():
         setattr(PredicateAddConn, key, value)
     return PredicateAddConn()
+
+
+class ShortlistCoverage(NamedTuple):
+    """Whether one bucket's growth shortlist reaches every eligible
+    destination (phases.py:3560-3575).
+
+    bucket: the bucket (its source level); candidate_units: the shortlist
+    size M; source_units / destination_units: the units at the bucket's level
+    / in its growth window (deeper, within ``max_level_gap``); covered:
+    M >= destination_units.
+    """
+
+    bucket: int
+    candidate_units: int
+    source_units: int
+    destination_units: int
+    covered: bool
+
+
+def shortlist_coverage(net: Any, static: Any, state: Any) -> tuple[ShortlistCoverage, ...]:
+    """Per bucket, whether a shortlisted ``add_conn`` can reach every
+    eligible destination (phases.py:3578-3628).
+
+    A shortlist draws candidates from the M most important sources of a
+    bucket's level crossed with the M most important eligible destinations,
+    so at most M distinct units of a wider destination window can ever gain
+    an edge. The check reads the state's LEVEL column on the host (levels are
+    runtime data). Empty when the net declares no shortlist."""
+    from plastax_amd._types import LEVEL
+
+    ac = getattr(net, "add_conn", None)
+    if ac is None:
+        return ()
+    kind = str(getattr(ac, "candidates", "exhaustive"))
+    m = getattr(ac, "shortlist_size", None) if kind != "exhaustive" else None
+    if m is None:
+        return ()
+    col = state.units[LEVEL.name]
+    levels = np.asarray(col.cpu().numpy() if hasattr(col, "cpu") else col)
+    gap = int(getattr(ac, "max_level_gap", 1))
+    out = []
+    for b in range(len(static.level_capacities)):
+        dests = int(np.count_nonzero((levels > b) & (levels <= b + gap)))
+        out.append(ShortlistCoverage(bucket=b, candidate_units=int(m),
+                                     source_units=int(np.count_nonzero(levels == b)),
+                                     destination_units=dests, covered=int(m) >= dests))
+    return tuple(out)
+
+
+def recommended_shortlist(net: Any, static: Any, state: Any) -> int:
+    """The smallest shortlist size that reaches every eligible destination
+    of every bucket (phases.py:3631-3650): the largest destination window,
+    or 0 without a shortlist. A floor only: the candidate volume rule (M
+    above sqrt(churn * E)) still applies."""
+    return max((c.destination_units for c in shortlist_coverage(net, static, state)), default=0)

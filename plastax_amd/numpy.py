@@ -11,7 +11,17 @@ from typing import Any
 
 import numpy as np
 
-from plastax_amd._expr import Expr, UnsupportedPolicyError, binary, cast, lift, select, unary
+from plastax_amd._expr import (
+    ConstArray,
+    Expr,
+    UnsupportedPolicyError,
+    binary,
+    cast,
+    lift,
+    select,
+    unary,
+    vector_sum,
+)
 
 float32 = np.float32
 int32 = np.int32
@@ -23,7 +33,9 @@ pi = np.pi
 
 
 def _traced(*xs: Any) -> bool:
-    return any(isinstance(x, Expr) for x in xs)
+    """Any operand traced: an expression, or an array holding expressions
+    (a traced scalar broadcast against a constant array)."""
+    return any(isinstance(x, Expr) or (isinstance(x, np.ndarray) and x.dtype == object) for x in xs)
 
 
 def _unary(name: str, fn: Any) -> Any:
@@ -131,7 +143,13 @@ def where(cond: Any, a: Any, b: Any) -> Any:
 
 
 def sum(x: Any, axis: Any = None) -> Any:  # noqa: A001 -- mirrors jnp.sum
-    """Sum over the traced output axis (a loss's reduction)."""
+    """Sum over the traced output axis (a loss's reduction), or of a vector
+    of traced scalars (e.g. ``jnp.sum(i >= starts)``: booleans count as
+    int32)."""
+    if isinstance(x, np.ndarray) and x.dtype == object:
+        if axis not in (None, 0, -1):
+            raise UnsupportedPolicyError("a traced vector sums over its one axis")
+        return vector_sum(x)
     if _traced(x):
         if axis not in (None, 0, -1):
             raise UnsupportedPolicyError("traced sums reduce over the output axis only")
@@ -140,9 +158,12 @@ def sum(x: Any, axis: Any = None) -> Any:  # noqa: A001 -- mirrors jnp.sum
 
 
 def asarray(x: Any, dtype: Any = None) -> Any:
+    """A traced value as is (cast to dtype); a constant as a ConstArray,
+    which a traced policy may index with a traced integer."""
     if _traced(x):
         return x if dtype is None else cast(x, dtype)
-    return np.asarray(x, dtype=dtype)
+    a = np.asarray(x, dtype=dtype)
+    return a.view(ConstArray) if a.ndim >= 1 else a
 
 
 def clip(x: Any, lo: Any, hi: Any) -> Any:

@@ -13,7 +13,7 @@ from __future__ import annotations
 import dataclasses
 import enum
 from collections.abc import Mapping
-from typing import Any, ClassVar, Generic, TypeVar
+from typing import Any, ClassVar, Generic, NamedTuple, TypeVar
 
 import numpy as np
 
@@ -118,6 +118,16 @@ class AddUnit:
 
 class ScoreAddConn:
     """Scored connection growth (traits.py:466-551)."""
+
+
+class Proposal(NamedTuple):
+    """One growth proposal (traits.py:554-566): a directed candidate edge and
+    its priority. ``propose`` may return one (or a plain ``(src, dst,
+    score)`` tuple); a ``-inf`` score vetoes the candidate."""
+
+    src: Any
+    dst: Any
+    score: Any
 
 
 class ProposeAddConn:

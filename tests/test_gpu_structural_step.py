@@ -276,3 +276,71 @@ def test_full_churn_bit_exact(oracle, pipeline: bool) -> None:
         assert_same_state(static, state, o, f"step {k}")
         assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at {k}"
     assert added > 0
+
+
+class SetProposeGrow(px.ProposeAddConn):
+    """The proposer of examples/dst_sparse.py:296-337 (SET with proposals):
+    each unit proposes P edges into a random unit of the next layer with a
+    random priority, read from constant layer tables at the traced layer
+    index, and returns a px.Proposal."""
+
+    proposer = "per_unit"
+
+    def __init__(self, max_new_per_level, grow_scale, layer_sizes, proposals_per_unit=16):
+        self.max_new_per_level = max_new_per_level
+        self.proposals_per_proposer = proposals_per_unit
+        self.direction = "deeper"
+        self.dedupe_live = True
+        self.dedupe_step = True
+        self.grow_scale = grow_scale
+        sizes = np.asarray(layer_sizes, dtype=np.int32)
+        starts = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+        self._next_start = jnp.asarray(starts[1:])
+        self._next_width = jnp.asarray(np.append(sizes[1:], 0).astype(np.int32))
+
+    def propose(self, u, i, j, g, rng):
+        layer = jnp.sum(i >= self._next_start)
+        width = self._next_width[layer]
+        offset = (rng.uniform() * width.astype(jnp.float32)).astype(jnp.int32)
+        dst = self._next_start[layer] + jnp.minimum(offset, width - 1)
+        score = jnp.where(width > 0, rng.uniform(), -jnp.inf)
+        return px.Proposal(src=i, dst=dst, score=score)
+
+    def init(self, u, src, dst, g):
+        return px.ConnWrite.of((px.WEIGHT, jnp.float32(self.grow_scale)))
+
+
+def test_set_proposer_returning_proposals_bit_exact(oracle) -> None:
+    """A sparse MLP pruned by |w| < tau and regrown every step by the SET
+    proposer (P = 4, 24 per level, live and step dedupe): flags every step,
+    every column at the checked steps, bit for bit with the oracle."""
+    rng = np.random.default_rng(6)
+    layers = [96, 256, 256, 10]
+    n, src, dst, w, ins, outs = _sparse_mlp(rng, layers, 0.1)
+    opt = px.optim.adam(1e-2, nets.GRAD_PRE_ACT)
+
+    class SET(px.Network):
+        forward_pass = nets.TanhForward()
+        backward_pass = nets.TanhBackward()
+        loss = nets.MSELoss()
+        update_conn = opt.update_conn()
+        prune_conn = TauPrune()
+        add_conn = SetProposeGrow(24, 0.01, tuple(layers), proposals_per_unit=4)
+        extra_unit_fields = (nets.GRAD_PRE_ACT, nets.LOSS_GRAD)
+        extra_conn_fields = tuple(opt.state_fields)
+
+    static, state = px.NetworkBuilder.from_edges(
+        SET, n, src, dst, weights=w, input_ids=ins, output_ids=outs,
+        globals_={"tau": np.float32(0.0)}, capacity_headroom=0.25, device="cuda")
+    teacher = rng.standard_normal((10, 96)).astype(np.float32) * np.float32(0.1)
+    xs = rng.random((12, 96)).astype(np.float32)
+
+    def inputs(k):
+        x = xs[k - 1]
+        return x, np.tanh(teacher @ x).astype(np.float32)
+
+    def globals_fn(k):
+        return {"tau": np.float32(0.01 if k % 3 == 1 else 0.0)}
+
+    _, o, grown = _run(SET, static, state, oracle, inputs, globals_fn, 8, {1, 2, 4, 8})
+    assert grown > 0
