@@ -16,7 +16,9 @@
 #ifndef PLASTAX_HIP_H_
 #define PLASTAX_HIP_H_
 
+#ifndef __HIPCC_RTC__
 #include <stdint.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -553,6 +555,22 @@ typedef struct plx_site_desc {
 } plx_site_desc;
 
 PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
+
+/* A site program compiled to its own kernel: the same evaluation as
+ * plx_site_eval (its instructions are the interpreter's, with literal
+ * operands, so the results are the same bits), without interpreting the
+ * program per site. The reference lowers the PruneConn predicate's jaxpr to
+ * the fused kernel's source the same way (phases.py:1910-2147, template
+ * :2174-2203). plx_site_compile generates the kernel's source and compiles it
+ * with hipRTC for `arch` (null: the current device's), with the library's
+ * floating-point flags, headers from `csrc_dir` (the library's csrc
+ * directory); the module is loaded and *handle set, one compile per
+ * (device, program code) for the process. With handle null it only compiles
+ * (a check that needs no device). plx_site_eval_compiled runs a handle on a
+ * descriptor whose program has the same code (checked; the constants and
+ * field pointers are the descriptor's). */
+PLX_EXPORT int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* arch, void** handle);
+PLX_EXPORT int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream);
 
 /* One bucket of a generic pass (a map outside the product form, one float32
  * component or a tuple with a tuple of monoids: sweep.py:113-180 / :343-399

@@ -76,7 +76,10 @@ def build(verbose: bool = False) -> pathlib.Path:
     if failed:
         raise RuntimeError(f"hipcc failed with exit code {failed[0]}")
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # hipRTC compiles the site programs at run time (plx_site_compile)
+    rocm_lib = pathlib.Path(hipcc()).resolve().parent.parent / "lib"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
+           f"-L{rocm_lib}", "-lhiprtc", f"-Wl,-rpath,{rocm_lib}"]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

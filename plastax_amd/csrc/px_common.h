@@ -2,6 +2,7 @@
 // per-thread error text behind plx_last_error() and the device Philox.
 #pragma once
 
+#ifndef __HIPCC_RTC__  // (hipRTC compiles of site programs bring their own runtime header)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -12,6 +13,7 @@ extern thread_local std::string g_last_error;
 int fail(int code, const char* what);
 int check_launch(const char* what);
 }  // namespace plx_detail
+#endif
 
 namespace px {
 

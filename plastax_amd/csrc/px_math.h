@@ -10,8 +10,10 @@
 // function over the float32 range.
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#endif
 
 namespace px {
 

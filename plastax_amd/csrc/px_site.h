@@ -4,8 +4,10 @@
 // pass that evaluates a PruneConn predicate in its sweep.
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#endif
 
 #include "../../include/plastax_hip.h"
 #include "px_common.h"
@@ -173,11 +175,13 @@ __device__ __forceinline__ void site_out(uint32_t (&o)[PLX_MAX_SOUTS], int i, ui
   }
 }
 
-__device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units,
-                                         uint32_t (&outv)[PLX_MAX_SOUTS]) {
-  SiteRegs r;
-  for (int k = 0; k < p.ninstr; ++k) {
-    const int op = p.code[4 * k], d = p.code[4 * k + 1], a = p.code[4 * k + 2], b = p.code[4 * k + 3];
+// One instruction (op, d, a, b) of a site program. The interpreter calls it
+// with the operands it reads from the program; a compiled program (the source
+// plx_site_compile generates) calls it with literal operands, and the switch
+// and the register selects fold away.
+__device__ __forceinline__ void site_step(int op, int d, int a, int b, SiteRegs& r, const plx_site_prog& p,
+                                          const Site& c, int32_t num_units, uint32_t (&outv)[PLX_MAX_SOUTS]) {
+  {
     const uint32_t x = r.get(a), y = r.get(b);
     const int32_t xi = static_cast<int32_t>(x), yi = static_cast<int32_t>(y);
     const float xf = __uint_as_float(x), yf = __uint_as_float(y);
@@ -217,7 +221,7 @@ __device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, 
         break;
       case S_MOV: v = x; break;
       case S_SEL: v = x ? r.get(b) : r.get(b + 1); break;
-      case S_OUT: site_out(outv, d, x); continue;
+      case S_OUT: site_out(outv, d, x); return;
       case S_FADD: v = __float_as_uint(xf + yf); break;
       case S_FSUB: v = __float_as_uint(xf - yf); break;
       case S_FMUL: v = __float_as_uint(xf * yf); break;
@@ -286,6 +290,110 @@ __device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, 
       default: break;
     }
     r.set(d, v);
+  }
+}
+
+// The interpreter: the program's instructions in order.
+__device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, int32_t num_units,
+                                         uint32_t (&outv)[PLX_MAX_SOUTS]) {
+  SiteRegs r;
+  for (int k = 0; k < p.ninstr; ++k)
+    site_step(p.code[4 * k], p.code[4 * k + 1], p.code[4 * k + 2], p.code[4 * k + 3], r, p, c, num_units, outv);
+}
+
+struct SiteInterp {
+  __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t num_units,
+                                             uint32_t (&outv)[PLX_MAX_SOUTS]) {
+    site_run(p, c, num_units, outv);
+  }
+};
+
+__device__ __forceinline__ int64_t live_count(int64_t n_max, const int32_t* n_dev) {
+  if (!n_dev) return n_max;
+  const int64_t c = *n_dev;
+  return c < n_max ? (c < 0 ? 0 : c) : n_max;
+}
+
+// plx_site_eval's sites (grid-strided): each site's roles and rng seed, the
+// program (Prog::run: the interpreter, or a compiled program), then its
+// outputs -- one column per output, or a kill ORed into or_into.
+template <class Prog>
+__device__ __forceinline__ void site_eval_body(const plx_site_desc& d) {
+  const int64_t n = live_count(d.n, d.n_dev);
+  const uint32_t keyed =
+      px::philox32(d.net_seed, (static_cast<uint64_t>(static_cast<uint32_t>(d.step)) << 8) | 1u);
+  const int64_t per = d.per > 0 ? d.per : 1;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < n;
+       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    Site c;
+    c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
+    uint32_t key = 0;
+    c.batch = d.batch > 1 ? d.batch : 1;
+    c.sample = d.sample;
+    switch (d.kind) {
+      case PLX_SITES_UNIT:
+        if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
+          c.role[0] = static_cast<int32_t>(s / c.batch);
+          c.sample = static_cast<int32_t>(s % c.batch);
+          key = static_cast<uint32_t>(c.role[0]);
+          break;
+        }
+        c.role[0] = static_cast<int32_t>(s / per);
+        c.role[1] = static_cast<int32_t>(s % per);
+        key = static_cast<uint32_t>(c.role[0]);
+        break;
+      case PLX_SITES_GLOBAL: c.role[1] = static_cast<int32_t>(s); break;
+      case PLX_SITES_CONN: {
+        const int32_t cid = d.list_a[s / per];
+        c.role[1] = static_cast<int32_t>(s % per);
+        c.role[2] = d.from_id[cid];
+        c.role[3] = d.to_id[cid];
+        c.role[4] = cid;
+        const uint64_t pair = (static_cast<uint64_t>(static_cast<uint32_t>(c.role[2])) << 32) |
+                              static_cast<uint32_t>(c.role[3]);
+        key = px::philox32(pair, static_cast<uint32_t>(d.occ[cid]));
+        break;
+      }
+      case PLX_SITES_GRID: {
+        const int64_t m2 = per * per;
+        const int64_t g = s / m2, rem = s - g * m2;
+        c.role[2] = d.list_a[g * per + rem / per];
+        c.role[3] = d.list_b[g * per + rem % per];
+        break;
+      }
+      case PLX_SITES_PAIRS:
+        c.role[2] = d.list_a[s];
+        c.role[3] = d.list_b[s];
+        break;
+      default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
+        c.role[4] = static_cast<int32_t>(s);
+        const int32_t* lg = d.ids_logical;
+        if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
+        if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
+        break;
+      }
+    }
+    c.cid_value = c.role[4];
+    if (d.site_ids) {
+      if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
+      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
+    }
+    c.ids_logical = d.ids_logical;
+    c.ids_physical = d.ids_physical;
+    c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
+    uint32_t out[PLX_MAX_SOUTS];
+    Prog::run(d.prog, c, d.num_units, out);
+    if (d.or_into) {
+      if (out[0] && !d.or_into[s]) {
+        d.or_into[s] = 1;
+        if (d.stamp) d.stamp[s] = d.stamp_value;
+        if (d.kill_count) atomicAdd(d.kill_count, 1);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < PLX_MAX_SOUTS; ++k)
+        if (k < d.prog.nout) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
+    }
   }
 }
 

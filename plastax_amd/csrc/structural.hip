@@ -21,8 +21,14 @@
 //    per-wave LDS counts.
 #include <hip/hip_runtime.h>
 
+#include <hip/hiprtc.h>
+
 #include <cstdint>
+#include <cstring>
+#include <map>
 #include <mutex>
+#include <string>
+#include <vector>
 
 #include "../../include/plastax_hip.h"
 #include "px_common.h"
@@ -39,12 +45,6 @@ constexpr int kWaves = kBlock / 64;
 constexpr int kChunk = kBlock * 8;   // elements per scan / compaction chunk
 constexpr int kTile = kBlock * 16;   // elements per radix tile
 constexpr int kScanLanes = 1024;     // the single-workgroup scan
-
-__device__ __forceinline__ int64_t live_count(int64_t n_max, const int32_t* n_dev) {
-  if (!n_dev) return n_max;
-  const int64_t c = *n_dev;
-  return c < n_max ? (c < 0 ? 0 : c) : n_max;
-}
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int lane = threadIdx.x & 63;
@@ -388,84 +388,7 @@ __global__ void k_gen_fold(plx_gen_fold_desc d) {
   }
 }
 
-__global__ void k_site_eval(plx_site_desc d) {
-  const int64_t n = live_count(d.n, d.n_dev);
-  const uint32_t keyed =
-      px::philox32(d.net_seed, (static_cast<uint64_t>(static_cast<uint32_t>(d.step)) << 8) | 1u);
-  const int64_t per = d.per > 0 ? d.per : 1;
-  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < n;
-       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    Site c;
-    c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
-    uint32_t key = 0;
-    c.batch = d.batch > 1 ? d.batch : 1;
-    c.sample = d.sample;
-    switch (d.kind) {
-      case PLX_SITES_UNIT:
-        if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
-          c.role[0] = static_cast<int32_t>(s / c.batch);
-          c.sample = static_cast<int32_t>(s % c.batch);
-          key = static_cast<uint32_t>(c.role[0]);
-          break;
-        }
-        c.role[0] = static_cast<int32_t>(s / per);
-        c.role[1] = static_cast<int32_t>(s % per);
-        key = static_cast<uint32_t>(c.role[0]);
-        break;
-      case PLX_SITES_GLOBAL: c.role[1] = static_cast<int32_t>(s); break;
-      case PLX_SITES_CONN: {
-        const int32_t cid = d.list_a[s / per];
-        c.role[1] = static_cast<int32_t>(s % per);
-        c.role[2] = d.from_id[cid];
-        c.role[3] = d.to_id[cid];
-        c.role[4] = cid;
-        const uint64_t pair = (static_cast<uint64_t>(static_cast<uint32_t>(c.role[2])) << 32) |
-                              static_cast<uint32_t>(c.role[3]);
-        key = px::philox32(pair, static_cast<uint32_t>(d.occ[cid]));
-        break;
-      }
-      case PLX_SITES_GRID: {
-        const int64_t m2 = per * per;
-        const int64_t g = s / m2, rem = s - g * m2;
-        c.role[2] = d.list_a[g * per + rem / per];
-        c.role[3] = d.list_b[g * per + rem % per];
-        break;
-      }
-      case PLX_SITES_PAIRS:
-        c.role[2] = d.list_a[s];
-        c.role[3] = d.list_b[s];
-        break;
-      default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
-        c.role[4] = static_cast<int32_t>(s);
-        const int32_t* lg = d.ids_logical;
-        if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
-        if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
-        break;
-      }
-    }
-    c.cid_value = c.role[4];
-    if (d.site_ids) {
-      if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
-      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
-    }
-    c.ids_logical = d.ids_logical;
-    c.ids_physical = d.ids_physical;
-    c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
-    uint32_t out[PLX_MAX_SOUTS];
-    site_run(d.prog, c, d.num_units, out);
-    if (d.or_into) {
-      if (out[0] && !d.or_into[s]) {
-        d.or_into[s] = 1;
-        if (d.stamp) d.stamp[s] = d.stamp_value;
-        if (d.kill_count) atomicAdd(d.kill_count, 1);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < PLX_MAX_SOUTS; ++k)
-        if (k < d.prog.nout) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
-    }
-  }
-}
+__global__ void k_site_eval(plx_site_desc d) { site_eval_body<SiteInterp>(d); }
 
 // ---------------------------------------------------------------------------
 // Growth: validity, dedupe, selection, claim.
@@ -941,6 +864,75 @@ bool prog_ok(const plx_site_prog& p) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Compiled site programs: a program's own kernel, generated as source (the
+// shared site_eval_body with a runner that calls site_step once per
+// instruction, operands as literals) and compiled with hipRTC for the
+// current device, with the library's floating-point flags. One compile per
+// (device, program code); the modules stay loaded for the process.
+// ---------------------------------------------------------------------------
+struct CompiledSite {
+  hipModule_t mod = nullptr;
+  hipFunction_t fn = nullptr;
+  int dev = -1;
+  int32_t ninstr = 0, nout = 0;
+  std::vector<int32_t> code;
+};
+
+std::mutex g_site_mu;
+std::map<std::string, CompiledSite*> g_site_cache;
+
+std::string site_source(const plx_site_prog& p) {
+  std::string s =
+      "// generated by plx_site_compile: one site program, its instructions as site_step calls\n"
+      "using __hip_internal::int8_t;\nusing __hip_internal::uint8_t;\nusing __hip_internal::int16_t;\n"
+      "using __hip_internal::uint16_t;\nusing __hip_internal::int32_t;\nusing __hip_internal::uint32_t;\n"
+      "using __hip_internal::int64_t;\nusing __hip_internal::uint64_t;\n"
+      "#ifndef INT32_MIN\n#define INT32_MIN (-2147483647 - 1)\n#endif\n"
+      "#ifndef INT32_MAX\n#define INT32_MAX 2147483647\n#endif\n"
+      "#ifndef UINT32_MAX\n#define UINT32_MAX 4294967295u\n#endif\n"
+      "#include \"px_site.h\"\n"
+      "namespace {\n"
+      "struct SiteGen {\n"
+      "  __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t nu,\n"
+      "                                             uint32_t (&o)[PLX_MAX_SOUTS]) {\n"
+      "    SiteRegs r;\n";
+  for (int k = 0; k < p.ninstr; ++k) {
+    s += "    site_step(" + std::to_string(p.code[4 * k]) + ", " + std::to_string(p.code[4 * k + 1]) + ", " +
+         std::to_string(p.code[4 * k + 2]) + ", " + std::to_string(p.code[4 * k + 3]) + ", r, p, c, nu, o);\n";
+  }
+  s += "  }\n};\n}  // namespace\n"
+       "extern \"C\" __global__ void plx_site_kernel(plx_site_desc d) { site_eval_body<SiteGen>(d); }\n";
+  return s;
+}
+
+int site_rtc_compile(const plx_site_prog& p, const char* csrc_dir, const std::string& arch, std::vector<char>* code) {
+  const std::string src = site_source(p);
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "plx_site.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    return fail(PLX_ERR_HIP, "plx_site_compile: hiprtcCreateProgram failed");
+  const std::string inc = std::string("-I") + csrc_dir;
+  const std::string off = "--offload-arch=" + arch;
+  const char* opts[] = {off.c_str(), "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", inc.c_str()};
+  const hiprtcResult rc = hiprtcCompileProgram(prog, static_cast<int>(sizeof(opts) / sizeof(opts[0])), opts);
+  if (rc != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    plx_detail::g_last_error = "plx_site_compile: " + std::string(hiprtcGetErrorString(rc)) + ": " + log.substr(0, 4000);
+    return PLX_ERR_HIP;
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  code->assign(n, 0);
+  hiprtcGetCode(prog, code->data());
+  hiprtcDestroyProgram(&prog);
+  return PLX_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -953,10 +945,8 @@ int64_t plx_scratch_ints(int64_t n) {
   return h + chunks_of(h) + chunks_of(n) + 64;
 }
 
-int plx_site_eval(const plx_site_desc* d, void* stream) {
-  if (!d) return fail(PLX_ERR_INVALID, "plx_site_eval: null descriptor");
-  if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_site_eval: negative n");
-  if (d->n == 0) return PLX_OK;
+// The checks of plx_site_eval for n > 0.
+static int site_desc_check(const plx_site_desc* d) {
   if (!prog_ok(d->prog)) return fail(PLX_ERR_INVALID, "plx_site_eval: bad program");
   if (d->num_units < 1) return fail(PLX_ERR_INVALID, "plx_site_eval: num_units must be positive");
   if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE)
@@ -973,9 +963,83 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
   if (!d->or_into)
     for (int k = 0; k < d->prog.nout; ++k)
       if (!d->outs[k]) return fail(PLX_ERR_INVALID, "plx_site_eval: null output");
+  return PLX_OK;
+}
+
+int plx_site_eval(const plx_site_desc* d, void* stream) {
+  if (!d) return fail(PLX_ERR_INVALID, "plx_site_eval: null descriptor");
+  if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_site_eval: negative n");
+  if (d->n == 0) return PLX_OK;
+  const int rc = site_desc_check(d);
+  if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_site_eval, dim3(grid_for(d->n)), dim3(kBlock), 0, s, *d);
   return check_launch("plx_site_eval");
+}
+
+
+
+int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* arch, void** handle) {
+  if (!p || !csrc_dir) return fail(PLX_ERR_INVALID, "plx_site_compile: null argument");
+  if (p->ninstr < 0 || p->ninstr > PLX_MAX_SINSTR || p->nout < 0 || p->nout > PLX_MAX_SOUTS)
+    return fail(PLX_ERR_INVALID, "plx_site_compile: bad program");
+  std::string target = arch ? arch : "";
+  int dev = -1;
+  if (handle) {
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+      return fail(PLX_ERR_HIP, "plx_site_compile: no current device");
+    if (target.empty()) target = prop.gcnArchName;
+  }
+  if (target.empty()) return fail(PLX_ERR_INVALID, "plx_site_compile: no target architecture");
+  std::string key = std::to_string(dev) + "|" + target + "|" + std::to_string(p->ninstr) + "|" +
+                    std::to_string(p->nout) + "|";
+  key.append(reinterpret_cast<const char*>(p->code), sizeof(int32_t) * 4 * static_cast<size_t>(p->ninstr));
+  std::lock_guard<std::mutex> lock(g_site_mu);
+  if (handle) {
+    const auto it = g_site_cache.find(key);
+    if (it != g_site_cache.end()) {
+      *handle = it->second;
+      return PLX_OK;
+    }
+  }
+  std::vector<char> code;
+  const int rc = site_rtc_compile(*p, csrc_dir, target, &code);
+  if (rc || !handle) return rc;
+  auto* cs = new CompiledSite;
+  if (hipModuleLoadData(&cs->mod, code.data()) != hipSuccess ||
+      hipModuleGetFunction(&cs->fn, cs->mod, "plx_site_kernel") != hipSuccess) {
+    delete cs;
+    (void)hipGetLastError();
+    return fail(PLX_ERR_HIP, "plx_site_compile: loading the compiled program failed");
+  }
+  cs->dev = dev;
+  cs->ninstr = p->ninstr;
+  cs->nout = p->nout;
+  cs->code.assign(p->code, p->code + 4 * p->ninstr);
+  g_site_cache[key] = cs;
+  *handle = cs;
+  return PLX_OK;
+}
+
+int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream) {
+  if (!handle || !d) return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: null argument");
+  if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_site_eval: negative n");
+  if (d->n == 0) return PLX_OK;
+  const int rc = site_desc_check(d);
+  if (rc) return rc;
+  const auto* cs = static_cast<const CompiledSite*>(handle);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != cs->dev)
+    return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: the program was compiled for another device");
+  if (cs->ninstr != d->prog.ninstr || cs->nout != d->prog.nout ||
+      std::memcmp(cs->code.data(), d->prog.code, sizeof(int32_t) * 4 * static_cast<size_t>(cs->ninstr)) != 0)
+    return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: the descriptor's program is not the compiled one");
+  void* args[] = {const_cast<plx_site_desc*>(d)};
+  if (hipModuleLaunchKernel(cs->fn, grid_for(d->n), 1, 1, kBlock, 1, 1, 0, static_cast<hipStream_t>(stream), args,
+                            nullptr) != hipSuccess)
+    return fail(PLX_ERR_HIP, "plx_site_eval_compiled: launch failed");
+  return check_launch("plx_site_eval_compiled");
 }
 
 int plx_mean_of_writes(int64_t n, int32_t mode, int32_t batch, float* old, const float* next, float* total,

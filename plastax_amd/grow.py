@@ -29,7 +29,10 @@ order, concatenated into flat device columns (bucket ``b`` at
 
 from __future__ import annotations
 
+import ctypes
 import dataclasses
+import pathlib
+import warnings
 from typing import Any
 
 import numpy as np
@@ -99,6 +102,32 @@ class Scratch:
         return self.i32(int(_lib.load().plx_scratch_ints(int(n))))
 
 
+# Site programs evaluated over at least this many sites run as their own
+# compiled kernel (plx_site_compile; compiled once per program and device);
+# smaller launches interpret the program (plx_site_eval). Both give the same
+# bits. "always" / "never" force either (tests).
+COMPILE_SITES: str | int = 1 << 18
+_CSRC = (pathlib.Path(__file__).resolve().parent / "csrc").as_posix().encode()
+_compile_failed: set[bytes] = set()
+
+
+def compiled_site_handle(prog: _lib.plx_site_prog) -> int | None:
+    """The compiled kernel of a filled plx_site_prog (None if hipRTC could
+    not build it: the caller interprets the program instead, with a warning
+    the first time)."""
+    key = np.asarray(prog.code[: 4 * prog.ninstr] + [prog.ninstr, prog.nout], dtype=np.int32).tobytes()
+    if key in _compile_failed:
+        return None
+    lib = _lib.load()
+    handle = ctypes.c_void_p()
+    rc = lib.plx_site_compile(ctypes.byref(prog), _CSRC, None, ctypes.byref(handle))
+    if rc != 0:
+        _compile_failed.add(key)
+        warnings.warn(f"site program not compiled, interpreted instead: {lib.plx_last_error().decode()[:500]}")
+        return None
+    return handle.value
+
+
 class Kernels:
     """Thin wrappers of the structural entry points on one stream."""
 
@@ -142,8 +171,14 @@ class Kernels:
         d.or_into = _ptr(or_into)
         d.kill_count, d.site_ids = _ptr(kill_count), _ptr(site_ids)
         d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
+        policy = COMPILE_SITES
+        compiled = policy == "always" or (policy != "never" and int(n) >= int(policy))
+        handle = compiled_site_handle(d.prog) if compiled else None
         self._begin("site_eval")
-        _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
+        if handle is not None:
+            _lib.check(self.lib.plx_site_eval_compiled(handle, d, self.s), "plx_site_eval_compiled")
+        else:
+            _lib.check(self.lib.plx_site_eval(d, self.s), "plx_site_eval")
         self._end("site_eval")
 
     def compact(self, n: int, mode: int, flags: torch.Tensor, n_dev: torch.Tensor | None = None

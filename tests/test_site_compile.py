@@ -1,0 +1,99 @@
+"""Compiled site programs (plx_site_compile): the generated kernel source
+compiles with hipRTC for gfx950 under the library's floating-point flags,
+for a program holding every opcode of the site machine and for traced
+policies (a PruneConn hash predicate, a Box-Muller proposer, the SET
+proposer's table reads). Compile only -- no device is needed; the device
+runs of compiled programs against the oracle are in
+test_gpu_site_compiled.py."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import numpy as np
+import pytest
+
+import plastax_amd as px
+import plastax_amd.numpy as jnp
+from plastax_amd import _lib, _site
+
+CSRC = (pathlib.Path(_lib.__file__).resolve().parent / "csrc").as_posix().encode()
+
+
+def _prog(code: list[tuple[int, int, int, int]], nout: int) -> _lib.plx_site_prog:
+    p = _lib.plx_site_prog()
+    p.ninstr = len(code)
+    p.nout = nout
+    for k, ins in enumerate(code):
+        for j in range(4):
+            p.code[4 * k + j] = int(ins[j])
+    return p
+
+
+def _compile(p: _lib.plx_site_prog) -> None:
+    lib = _lib.load()
+    rc = lib.plx_site_compile(ctypes.byref(p), CSRC, b"gfx950", None)
+    assert rc == 0, lib.plx_last_error().decode()[:3000]
+
+
+def _traced(sp: _site.SiteProgram) -> _lib.plx_site_prog:
+    code = sp.flat_code().reshape(-1, 4)
+    return _prog([tuple(int(v) for v in row) for row in code], len(sp.out_kinds))
+
+
+def test_every_opcode_compiles() -> None:
+    ops = sorted(set(_site.SOP.values()) - {_site.SOP["out"]})
+    code = [(op, k % 32, 1 + k % 4, 2 + k % 8) for k, op in enumerate(ops)]
+    code += [(_site.SOP["out"], 0, 3, 0), (_site.SOP["out"], 1, 5, 0)]
+    assert len(code) <= _site.MAX_SINSTR
+    _compile(_prog(code, 2))
+
+
+def test_traced_policies_compile() -> None:
+    class HashPrune(px.PruneConn):
+        def predicate(self, u, c, cid, g):
+            h = c[px.FROM_ID, cid] * jnp.int32(7) + c[px.TO_ID, cid] * jnp.int32(13) + g["step"]
+            return (h % jnp.int32(1048573)) == jnp.int32(0)
+
+    class NormalRule(px.ProposeAddConn):
+        proposer = "per_unit"
+        proposals_per_proposer = 4
+
+        def propose(self, u, i, j, g, rng):
+            z = rng.normal()
+            dst = (jnp.abs(z) * jnp.float32(700.0)).astype(jnp.int32) % 3000
+            return px.Proposal(i, dst, rng.normal() + jnp.cos(u[px.ACTIVATION, i]))
+
+    class Tables(px.ProposeAddConn):
+        proposer = "per_unit"
+        proposals_per_proposer = 4
+
+        def __init__(self):
+            self.start = jnp.asarray(np.int32([4, 10, 16]))
+            self.width = jnp.asarray(np.int32([6, 6, 0]))
+
+        def propose(self, u, i, j, g, rng):
+            layer = jnp.sum(i >= self.start)
+            w = self.width[layer]
+            dst = self.start[layer] + jnp.minimum((rng.uniform() * w.astype(jnp.float32)).astype(jnp.int32), w - 1)
+            return px.Proposal(i, dst, jnp.where(w > 0, rng.uniform(), -jnp.inf))
+
+    udt = {"activation": np.dtype(np.float32), "level": np.dtype(np.int32)}
+    cdt = {"from_id": np.dtype(np.int32), "to_id": np.dtype(np.int32), "weight": np.dtype(np.float32)}
+    progs = [
+        _site.trace_predicate(HashPrune(), udt, cdt, {"step": np.int32(0)}),
+        _site.trace_propose(NormalRule(), "per_unit", udt, cdt, None),
+        _site.trace_propose(Tables(), "per_unit", udt, cdt, None),
+    ]
+    for sp in progs:
+        _compile(_traced(sp))
+
+
+def test_compile_rejects_a_bad_program() -> None:
+    lib = _lib.load()
+    p = _prog([(1, 0, 0, 0)], 1)
+    p.ninstr = _site.MAX_SINSTR + 1
+    assert lib.plx_site_compile(ctypes.byref(p), CSRC, b"gfx950", None) != 0
+    with pytest.raises(Exception):
+        _lib.check(lib.plx_site_compile(None, CSRC, b"gfx950", None), "plx_site_compile")
