@@ -590,6 +590,20 @@ class Arena:
             col[live].masked_fill_(self.cols[DEAD.name][live] == 0, float(t))
             self.t_now[b] = None
 
+    def logical_ids(self) -> dict[str, torch.Tensor]:
+        """FROM_ID and TO_ID of every position in the caller's numbering (the
+        slab holds arena unit ids), for site programs that read them: built
+        on first use (4 bytes per position each) and kept with the arena,
+        whose ids never change in place. Ids outside [0, num_units) are
+        clamped first, as the kernels' own id translation does."""
+        cached = getattr(self, "_logical_ids", None)
+        if cached is None:
+            n = self.static.num_units
+            cached = {name: self.uperm32[self.cols[name].clamp(0, n - 1).long()]
+                      for name in (FROM_ID.name, TO_ID.name)}
+            self._logical_ids = cached
+        return cached
+
     def stamp_target(self, b: int) -> tuple[torch.Tensor | None, float]:
         """(column from bucket b's base, value) that a kill in bucket b
         stamps: Adam's step-count column and the bucket's count while every

@@ -302,6 +302,7 @@ __device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, 
 }
 
 struct SiteInterp {
+  static constexpr int kSites = 1;  // sites per lane per pass of the kernel's loop
   __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t num_units,
                                              uint32_t (&outv)[PLX_MAX_SOUTS]) {
     site_run(p, c, num_units, outv);
@@ -316,83 +317,102 @@ __device__ __forceinline__ int64_t live_count(int64_t n_max, const int32_t* n_de
 
 // plx_site_eval's sites (grid-strided): each site's roles and rng seed, the
 // program (Prog::run: the interpreter, or a compiled program), then its
-// outputs -- one column per output, or a kill ORed into or_into.
+// outputs -- one column per output, or a kill ORed into or_into. Each lane
+// takes Prog::kSites sites per pass (a stride apart): their programs run
+// before any output is stored, so a compiled program's loads for all of them
+// are in flight together.
+__device__ __forceinline__ void site_setup(const plx_site_desc& d, int64_t s, int64_t per, uint32_t keyed, Site& c) {
+  c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
+  uint32_t key = 0;
+  c.batch = d.batch > 1 ? d.batch : 1;
+  c.sample = d.sample;
+  switch (d.kind) {
+    case PLX_SITES_UNIT:
+      if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
+        c.role[0] = static_cast<int32_t>(s / c.batch);
+        c.sample = static_cast<int32_t>(s % c.batch);
+        key = static_cast<uint32_t>(c.role[0]);
+        break;
+      }
+      c.role[0] = static_cast<int32_t>(s / per);
+      c.role[1] = static_cast<int32_t>(s % per);
+      key = static_cast<uint32_t>(c.role[0]);
+      break;
+    case PLX_SITES_GLOBAL: c.role[1] = static_cast<int32_t>(s); break;
+    case PLX_SITES_CONN: {
+      const int32_t cid = d.list_a[s / per];
+      c.role[1] = static_cast<int32_t>(s % per);
+      c.role[2] = d.from_id[cid];
+      c.role[3] = d.to_id[cid];
+      c.role[4] = cid;
+      const uint64_t pair = (static_cast<uint64_t>(static_cast<uint32_t>(c.role[2])) << 32) |
+                            static_cast<uint32_t>(c.role[3]);
+      key = px::philox32(pair, static_cast<uint32_t>(d.occ[cid]));
+      break;
+    }
+    case PLX_SITES_GRID: {
+      const int64_t m2 = per * per;
+      const int64_t g = s / m2, rem = s - g * m2;
+      c.role[2] = d.list_a[g * per + rem / per];
+      c.role[3] = d.list_b[g * per + rem % per];
+      break;
+    }
+    case PLX_SITES_PAIRS:
+      c.role[2] = d.list_a[s];
+      c.role[3] = d.list_b[s];
+      break;
+    default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
+      c.role[4] = static_cast<int32_t>(s);
+      const int32_t* lg = d.ids_logical;
+      if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
+      if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
+      break;
+    }
+  }
+  c.cid_value = c.role[4];
+  if (d.site_ids) {
+    if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
+    if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
+  }
+  c.ids_logical = d.ids_logical;
+  c.ids_physical = d.ids_physical;
+  c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
+}
+
 template <class Prog>
 __device__ __forceinline__ void site_eval_body(const plx_site_desc& d) {
+  constexpr int K = Prog::kSites;
   const int64_t n = live_count(d.n, d.n_dev);
   const uint32_t keyed =
       px::philox32(d.net_seed, (static_cast<uint64_t>(static_cast<uint32_t>(d.step)) << 8) | 1u);
   const int64_t per = d.per > 0 ? d.per : 1;
-  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < n;
-       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    Site c;
-    c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
-    uint32_t key = 0;
-    c.batch = d.batch > 1 ? d.batch : 1;
-    c.sample = d.sample;
-    switch (d.kind) {
-      case PLX_SITES_UNIT:
-        if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
-          c.role[0] = static_cast<int32_t>(s / c.batch);
-          c.sample = static_cast<int32_t>(s % c.batch);
-          key = static_cast<uint32_t>(c.role[0]);
-          break;
-        }
-        c.role[0] = static_cast<int32_t>(s / per);
-        c.role[1] = static_cast<int32_t>(s % per);
-        key = static_cast<uint32_t>(c.role[0]);
-        break;
-      case PLX_SITES_GLOBAL: c.role[1] = static_cast<int32_t>(s); break;
-      case PLX_SITES_CONN: {
-        const int32_t cid = d.list_a[s / per];
-        c.role[1] = static_cast<int32_t>(s % per);
-        c.role[2] = d.from_id[cid];
-        c.role[3] = d.to_id[cid];
-        c.role[4] = cid;
-        const uint64_t pair = (static_cast<uint64_t>(static_cast<uint32_t>(c.role[2])) << 32) |
-                              static_cast<uint32_t>(c.role[3]);
-        key = px::philox32(pair, static_cast<uint32_t>(d.occ[cid]));
-        break;
-      }
-      case PLX_SITES_GRID: {
-        const int64_t m2 = per * per;
-        const int64_t g = s / m2, rem = s - g * m2;
-        c.role[2] = d.list_a[g * per + rem / per];
-        c.role[3] = d.list_b[g * per + rem % per];
-        break;
-      }
-      case PLX_SITES_PAIRS:
-        c.role[2] = d.list_a[s];
-        c.role[3] = d.list_b[s];
-        break;
-      default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
-        c.role[4] = static_cast<int32_t>(s);
-        const int32_t* lg = d.ids_logical;
-        if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
-        if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
-        break;
-      }
-    }
-    c.cid_value = c.role[4];
-    if (d.site_ids) {
-      if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
-      if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
-    }
-    c.ids_logical = d.ids_logical;
-    c.ids_physical = d.ids_physical;
-    c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
-    uint32_t out[PLX_MAX_SOUTS];
-    Prog::run(d.prog, c, d.num_units, out);
-    if (d.or_into) {
-      if (out[0] && !d.or_into[s]) {
-        d.or_into[s] = 1;
-        if (d.stamp) d.stamp[s] = d.stamp_value;
-        if (d.kill_count) atomicAdd(d.kill_count, 1);
-      }
-    } else {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s0 < n; s0 += K * stride) {
+    uint32_t out[K][PLX_MAX_SOUTS];
 #pragma unroll
-      for (int k = 0; k < PLX_MAX_SOUTS; ++k)
-        if (k < d.prog.nout) static_cast<uint32_t*>(d.outs[k])[s] = out[k];
+    for (int k = 0; k < K; ++k) {
+      const int64_t s = s0 + k * stride;
+      if (s < n) {
+        Site c;
+        site_setup(d, s, per, keyed, c);
+        Prog::run(d.prog, c, d.num_units, out[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t s = s0 + k * stride;
+      if (s >= n) continue;
+      if (d.or_into) {
+        if (out[k][0] && !d.or_into[s]) {
+          d.or_into[s] = 1;
+          if (d.stamp) d.stamp[s] = d.stamp_value;
+          if (d.kill_count) atomicAdd(d.kill_count, 1);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < PLX_MAX_SOUTS; ++j)
+          if (j < d.prog.nout) static_cast<uint32_t*>(d.outs[j])[s] = out[k][j];
+      }
     }
   }
 }

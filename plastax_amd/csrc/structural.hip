@@ -894,6 +894,7 @@ std::string site_source(const plx_site_prog& p) {
       "#include \"px_site.h\"\n"
       "namespace {\n"
       "struct SiteGen {\n"
+      "  static constexpr int kSites = 4;\n"
       "  __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t nu,\n"
       "                                             uint32_t (&o)[PLX_MAX_SOUTS]) {\n"
       "    SiteRegs r;\n";
@@ -1036,8 +1037,9 @@ int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream) {
       std::memcmp(cs->code.data(), d->prog.code, sizeof(int32_t) * 4 * static_cast<size_t>(cs->ninstr)) != 0)
     return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: the descriptor's program is not the compiled one");
   void* args[] = {const_cast<plx_site_desc*>(d)};
-  if (hipModuleLaunchKernel(cs->fn, grid_for(d->n), 1, 1, kBlock, 1, 1, 0, static_cast<hipStream_t>(stream), args,
-                            nullptr) != hipSuccess)
+  // (four sites per lane per pass: SiteGen::kSites)
+  if (hipModuleLaunchKernel(cs->fn, grid_for((d->n + 3) / 4), 1, 1, kBlock, 1, 1, 0,
+                            static_cast<hipStream_t>(stream), args, nullptr) != hipSuccess)
     return fail(PLX_ERR_HIP, "plx_site_eval_compiled: launch failed");
   return check_launch("plx_site_eval_compiled");
 }

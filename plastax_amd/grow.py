@@ -39,7 +39,7 @@ import numpy as np
 import torch
 
 from plastax_amd import _lib, _site
-from plastax_amd._types import Propagation
+from plastax_amd._types import FROM_ID, TO_ID, Propagation
 from plastax_amd.growth_config import GrowthConfig
 
 Columns = dict[str, torch.Tensor]
@@ -156,11 +156,18 @@ class Kernels:
                   or_into: torch.Tensor | None = None, kill_count: torch.Tensor | None = None,
                   site_ids: torch.Tensor | None = None, ids_logical: torch.Tensor | None = None,
                   ids_physical: torch.Tensor | None = None, batch: int = 1, sample: int = 0,
-                  stamp: torch.Tensor | None = None, stamp_value: float = 0.0) -> None:
+                  stamp: torch.Tensor | None = None, stamp_value: float = 0.0,
+                  id_columns_logical: bool = False) -> None:
+        """One site-program launch (plx_site_eval, or its compiled kernel).
+        With ids_logical the unit columns and the id columns of `conns` are
+        in the arena's numbering and translated to the caller's, unless
+        `id_columns_logical`: the id columns passed already hold the
+        caller's ids."""
         d = _lib.plx_site_desc()
         d.batch, d.sample = int(batch), int(sample)
         d.stamp, d.stamp_value = _ptr(stamp), float(stamp_value)
-        d.prog = fill_prog(sp, units, conns, globals_, physical_ids=ids_logical is not None)
+        d.prog = fill_prog(sp, units, conns, globals_,
+                           physical_ids=ids_logical is not None and not id_columns_logical)
         d.n, d.kind, d.per, d.num_units = int(n), int(kind), int(per), int(num_units)
         d.step = int(np.array(int(step) & 0xFFFFFFFF, dtype=np.uint32).view(np.int32))
         d.net_seed = int(net_seed) & 0xFFFFFFFFFFFFFFFF
@@ -296,16 +303,28 @@ class PruneConnPhase:
         Adam step count is kept as one number gets that number in its own
         column (arena.stamp_target), so no host read follows the pass."""
         n_units = int(next(iter(units.values())).shape[0])
+        # A program that reads FROM_ID / TO_ID reads them in the caller's
+        # numbering: a churn arena keeps the caller's ids (no translation at
+        # all), a tiled one keeps translated copies (Arena.logical_ids) so
+        # that no edge pays two id gathers.
+        churn = bool(getattr(arena, "churn", False))
+        reads_ids = bool({FROM_ID.name, TO_ID.name} & set(self.prog.conn_fields))
+        logical = arena.logical_ids() if reads_ids and not churn else None
         for b in range(arena.num_buckets):
             base, cap = arena.bases[b], arena.caps[b]
             if cap == 0:
                 continue
             view = {name: col[base : base + cap] for name, col in arena.cols.items()}
+            if logical is not None:
+                view.update({name: col[base : base + cap] for name, col in logical.items()})
             stamp, value = arena.stamp_target(b)
             k.site_eval(self.prog, units, globals_, n=cap, kind=_lib_sites("EDGE"), num_units=n_units,
                         conns=view, or_into=view["dead"], kill_count=kill_count,
-                        site_ids=arena.slot[base : base + cap], ids_logical=arena.uperm32,
-                        ids_physical=arena.uinv32, stamp=stamp, stamp_value=value)
+                        # (the logical slot only where the program reads cid's value)
+                        site_ids=arena.slot[base : base + cap] if self.prog.uses_role("cid") else None,
+                        ids_logical=None if churn else arena.uperm32,
+                        ids_physical=None if churn else arena.uinv32, stamp=stamp, stamp_value=value,
+                        id_columns_logical=logical is not None)
 
 
 class ConnUpdatePhase:
