@@ -987,10 +987,20 @@ int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* a
   std::string target = arch ? arch : "";
   int dev = -1;
   if (handle) {
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
-      return fail(PLX_ERR_HIP, "plx_site_compile: no current device");
-    if (target.empty()) target = prop.gcnArchName;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PLX_ERR_HIP, "plx_site_compile: no current device");
+    if (target.empty()) {
+      static std::mutex arch_mu;
+      static std::map<int, std::string> arch_of;  // (device properties are slow to query)
+      std::lock_guard<std::mutex> lock(arch_mu);
+      auto it = arch_of.find(dev);
+      if (it == arch_of.end()) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+          return fail(PLX_ERR_HIP, "plx_site_compile: device properties unavailable");
+        it = arch_of.emplace(dev, std::string(prop.gcnArchName)).first;
+      }
+      target = it->second;
+    }
   }
   if (target.empty()) return fail(PLX_ERR_INVALID, "plx_site_compile: no target architecture");
   std::string key = std::to_string(dev) + "|" + target + "|" + std::to_string(p->ninstr) + "|" +

@@ -62,9 +62,11 @@ def fill_prog(sp: _site.SiteProgram, units: Columns, conns: Columns | None, glob
     p = _lib.plx_site_prog()
     p.ninstr = sp.ninstr
     p.nout = len(sp.out_kinds)
-    code = sp.flat_code()
-    for k, v in enumerate(code):
-        p.code[k] = int(v)
+    code = sp.__dict__.get("_code_bytes")
+    if code is None:  # (the code is fixed at trace time: packed once per program)
+        code = np.ascontiguousarray(sp.flat_code(), dtype=np.int32).tobytes()
+        sp.__dict__["_code_bytes"] = code
+    ctypes.memmove(ctypes.addressof(p.code), code, len(code))
     for k, v in enumerate(sp.const_bits(globals_)):
         p.consts[k] = int(v)
     for f, name in enumerate(sp.unit_fields):
@@ -108,23 +110,25 @@ class Scratch:
 # bits. "always" / "never" force either (tests).
 COMPILE_SITES: str | int = 1 << 18
 _CSRC = (pathlib.Path(__file__).resolve().parent / "csrc").as_posix().encode()
-_compile_failed: set[bytes] = set()
 
 
-def compiled_site_handle(prog: _lib.plx_site_prog) -> int | None:
-    """The compiled kernel of a filled plx_site_prog (None if hipRTC could
-    not build it: the caller interprets the program instead, with a warning
-    the first time)."""
-    key = np.asarray(prog.code[: 4 * prog.ninstr] + [prog.ninstr, prog.nout], dtype=np.int32).tobytes()
-    if key in _compile_failed:
-        return None
+def compiled_site_handle(sp: _site.SiteProgram, prog: _lib.plx_site_prog, device: torch.device) -> int | None:
+    """The compiled kernel of a traced program (``prog`` its filled
+    plx_site_prog), kept on the program per device; None if hipRTC could not
+    build it (the caller interprets the program instead, with a warning the
+    first time)."""
+    cache = sp.__dict__.setdefault("_compiled", {})
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    if dev in cache:
+        return cache[dev]
     lib = _lib.load()
     handle = ctypes.c_void_p()
     rc = lib.plx_site_compile(ctypes.byref(prog), _CSRC, None, ctypes.byref(handle))
     if rc != 0:
-        _compile_failed.add(key)
         warnings.warn(f"site program not compiled, interpreted instead: {lib.plx_last_error().decode()[:500]}")
+        cache[dev] = None
         return None
+    cache[dev] = handle.value
     return handle.value
 
 
@@ -180,7 +184,7 @@ class Kernels:
         d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
         policy = COMPILE_SITES
         compiled = policy == "always" or (policy != "never" and int(n) >= int(policy))
-        handle = compiled_site_handle(d.prog) if compiled else None
+        handle = compiled_site_handle(sp, d.prog, self.mem.device) if compiled else None
         self._begin("site_eval")
         if handle is not None:
             _lib.check(self.lib.plx_site_eval_compiled(handle, d, self.s), "plx_site_eval_compiled")
