@@ -561,15 +561,18 @@ PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
  * operands, so the results are the same bits), without interpreting the
  * program per site. The reference lowers the PruneConn predicate's jaxpr to
  * the fused kernel's source the same way (phases.py:1910-2147, template
- * :2174-2203). plx_site_compile generates the kernel's source and compiles it
- * with hipRTC for `arch` (null: the current device's), with the library's
- * floating-point flags, headers from `csrc_dir` (the library's csrc
- * directory); the module is loaded and *handle set, one compile per
- * (device, program code) for the process. With handle null it only compiles
- * (a check that needs no device). plx_site_eval_compiled runs a handle on a
- * descriptor whose program has the same code (checked; the constants and
- * field pointers are the descriptor's). */
-PLX_EXPORT int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* arch, void** handle);
+ * :2174-2203). plx_site_compile generates the kernel's source for the
+ * program of `d` and its launch shape (site kind, batched or not, which of
+ * from_id / to_id / site_ids / ids_logical / ids_physical are set, the
+ * fields' widths: fixed in the kernel, so its loads need no branch) and
+ * compiles it with hipRTC for `arch` (null: the current device's), with the
+ * library's floating-point flags, headers from `csrc_dir` (the library's csrc
+ * directory); the module is loaded and *handle set, one compile per (device,
+ * program code, shape) for the process. With handle null it only compiles (a
+ * check that needs no device). plx_site_eval_compiled runs a handle on a
+ * descriptor with the same code and shape (checked; the constants, counts and
+ * pointers are the descriptor's). */
+PLX_EXPORT int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* arch, void** handle);
 PLX_EXPORT int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream);
 
 /* One bucket of a generic pass (a map outside the product form, one float32

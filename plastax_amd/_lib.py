@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 22  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 23  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -469,7 +469,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_forward_bucket": (c_i32, [ctypes.POINTER(plx_forward_desc), c_vp]),
     "plx_backward_tiles": (c_i32, [ctypes.POINTER(plx_tile_desc), c_vp]),
     "plx_backward_partials": (c_i32, [ctypes.POINTER(plx_partials_desc), c_vp]),
-    "plx_site_compile": (c_i32, [ctypes.POINTER(plx_site_prog), ctypes.c_char_p, ctypes.c_char_p,
+    "plx_site_compile": (c_i32, [ctypes.POINTER(plx_site_desc), ctypes.c_char_p, ctypes.c_char_p,
                                  ctypes.POINTER(c_vp)]),
     "plx_site_eval_compiled": (c_i32, [c_vp, ctypes.POINTER(plx_site_desc), c_vp]),
     "plx_update_conn": (c_i32, [ctypes.POINTER(plx_update_desc), c_vp]),

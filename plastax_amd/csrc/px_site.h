@@ -38,6 +38,8 @@ __device__ __forceinline__ float fmin_nan(float a, float b) {
   if (b != b) return b;
   return a < b ? a : b;
 }
+// Floor division and modulo of int32 (b == 0: -1 for a == 0 else -2, and a;
+// INT32_MIN / -1 wraps).
 __device__ __forceinline__ int32_t floordiv_i32(int32_t a, int32_t b) {
   if (b == 0) return a == 0 ? -1 : -2;
   if (a == INT32_MIN && b == -1) return INT32_MIN;
@@ -51,6 +53,25 @@ __device__ __forceinline__ int32_t mod_i32(int32_t a, int32_t b) {
   int32_t r = a % b;
   if (r != 0 && ((r < 0) != (b < 0))) r += b;
   return r;
+}
+// The same values with selects only, for compiled programs: the divisor is
+// often a program constant, uniform over the wave, and a branch on it would
+// split the program into blocks the loads of the lane's next site cannot
+// move above. (The interpreter keeps the branches: in its one big switch
+// the selects' extra live values spill.)
+__device__ __forceinline__ int32_t floordiv_i32_sel(int32_t a, int32_t b) {
+  const bool zero = b == 0, wrap = a == INT32_MIN && b == -1;
+  const int32_t bb = (zero || wrap) ? 1 : b;
+  int32_t q = a / bb;
+  const int32_t r = a - q * bb;  // the remainder, with a's sign (|q * bb| <= |a|)
+  q -= (r != 0 && ((r < 0) != (bb < 0))) ? 1 : 0;
+  return zero ? (a == 0 ? -1 : -2) : (wrap ? INT32_MIN : q);
+}
+__device__ __forceinline__ int32_t mod_i32_sel(int32_t a, int32_t b) {
+  const int32_t bb = (b == 0 || b == -1) ? 1 : b;
+  int32_t r = a % bb;
+  r += (r != 0 && ((r < 0) != (bb < 0))) ? bb : 0;
+  return b == 0 ? a : (b == -1 ? 0 : r);
 }
 __device__ __forceinline__ int32_t f2i(float x) {
   if (x != x) return 0;
@@ -175,10 +196,29 @@ __device__ __forceinline__ void site_out(uint32_t (&o)[PLX_MAX_SOUTS], int i, ui
   }
 }
 
+// A launch's shape as the interpreter sees it: read from the descriptor,
+// the site and the program at run time. A compiled program gets a shape
+// whose answers are constants (the generated source's SiteShape), so its
+// loads are straight-line code with no branch between them.
+struct ShapeRT {
+  static constexpr bool kSelects = false;  // integer division and modulo with branches
+  __device__ __forceinline__ static int kind(const plx_site_desc& d) { return d.kind; }
+  __device__ __forceinline__ static int32_t batch(const plx_site_desc& d) { return d.batch > 1 ? d.batch : 1; }
+  __device__ __forceinline__ static bool from(const plx_site_desc& d) { return d.from_id != nullptr; }
+  __device__ __forceinline__ static bool to(const plx_site_desc& d) { return d.to_id != nullptr; }
+  __device__ __forceinline__ static bool site_ids(const plx_site_desc& d) { return d.site_ids != nullptr; }
+  __device__ __forceinline__ static bool logical(const Site& c) { return c.ids_logical != nullptr; }
+  __device__ __forceinline__ static bool physical(const Site& c) { return c.ids_physical != nullptr; }
+  __device__ __forceinline__ static bool batched(const Site& c) { return c.batch > 1; }
+  __device__ __forceinline__ static int32_t ubytes(const plx_site_prog& p, int a) { return p.ubytes[a]; }
+  __device__ __forceinline__ static int32_t cbytes(const plx_site_prog& p, int a) { return p.cbytes[a]; }
+};
+
 // One instruction (op, d, a, b) of a site program. The interpreter calls it
 // with the operands it reads from the program; a compiled program (the source
 // plx_site_compile generates) calls it with literal operands, and the switch
 // and the register selects fold away.
+template <class Sh>
 __device__ __forceinline__ void site_step(int op, int d, int a, int b, SiteRegs& r, const plx_site_prog& p,
                                           const Site& c, int32_t num_units, uint32_t (&outv)[PLX_MAX_SOUTS]) {
   {
@@ -203,14 +243,14 @@ __device__ __forceinline__ void site_step(int op, int d, int a, int b, SiteRegs&
       case S_LDU: {
         int64_t at = yi;
         at = at < 0 ? 0 : (at > num_units - 1 ? num_units - 1 : at);
-        if (c.ids_physical) at = c.ids_physical[at];
-        if (c.batch > 1) at = at * c.batch + c.sample;
-        v = load32(p.ufields[a], p.ubytes[a], at);
+        if (Sh::physical(c)) at = c.ids_physical[at];
+        if (Sh::batched(c)) at = at * c.batch + c.sample;
+        v = load32(p.ufields[a], Sh::ubytes(p, a), at);
         break;
       }
       case S_LDC:
-        v = load32(p.cfields[a], p.cbytes[a] & 0xFF, c.role[4]);
-        if ((p.cbytes[a] & PLX_SITE_ID_COLUMN) && c.ids_logical) {
+        v = load32(p.cfields[a], Sh::cbytes(p, a) & 0xFF, c.role[4]);
+        if ((Sh::cbytes(p, a) & PLX_SITE_ID_COLUMN) && Sh::logical(c)) {
           const int32_t id = static_cast<int32_t>(v);
           v = static_cast<uint32_t>(c.ids_logical[id < 0 ? 0 : (id > num_units - 1 ? num_units - 1 : id)]);
         }
@@ -256,8 +296,10 @@ __device__ __forceinline__ void site_step(int op, int d, int a, int b, SiteRegs&
       case S_IABS: v = xi < 0 ? 0u - x : x; break;
       case S_IMAX: v = xi > yi ? x : y; break;
       case S_IMIN: v = xi < yi ? x : y; break;
-      case S_IFLOORDIV: v = static_cast<uint32_t>(floordiv_i32(xi, yi)); break;
-      case S_IMOD: v = static_cast<uint32_t>(mod_i32(xi, yi)); break;
+      case S_IFLOORDIV:
+        v = static_cast<uint32_t>(Sh::kSelects ? floordiv_i32_sel(xi, yi) : floordiv_i32(xi, yi));
+        break;
+      case S_IMOD: v = static_cast<uint32_t>(Sh::kSelects ? mod_i32_sel(xi, yi) : mod_i32(xi, yi)); break;
       case S_ISIGN: v = static_cast<uint32_t>(xi > 0 ? 1 : (xi < 0 ? -1 : 0)); break;
       case S_IGT: v = xi > yi; break;
       case S_IGE: v = xi >= yi; break;
@@ -298,10 +340,12 @@ __device__ __forceinline__ void site_run(const plx_site_prog& p, const Site& c, 
                                          uint32_t (&outv)[PLX_MAX_SOUTS]) {
   SiteRegs r;
   for (int k = 0; k < p.ninstr; ++k)
-    site_step(p.code[4 * k], p.code[4 * k + 1], p.code[4 * k + 2], p.code[4 * k + 3], r, p, c, num_units, outv);
+    site_step<ShapeRT>(p.code[4 * k], p.code[4 * k + 1], p.code[4 * k + 2], p.code[4 * k + 3], r, p, c, num_units,
+                       outv);
 }
 
 struct SiteInterp {
+  using Shape = ShapeRT;
   static constexpr int kSites = 1;  // sites per lane per pass of the kernel's loop
   __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t num_units,
                                              uint32_t (&outv)[PLX_MAX_SOUTS]) {
@@ -321,12 +365,15 @@ __device__ __forceinline__ int64_t live_count(int64_t n_max, const int32_t* n_de
 // takes Prog::kSites sites per pass (a stride apart): their programs run
 // before any output is stored, so a compiled program's loads for all of them
 // are in flight together.
+template <class Sh>
 __device__ __forceinline__ void site_setup(const plx_site_desc& d, int64_t s, int64_t per, uint32_t keyed, Site& c) {
   c.role[0] = c.role[1] = c.role[2] = c.role[3] = c.role[4] = 0;
   uint32_t key = 0;
-  c.batch = d.batch > 1 ? d.batch : 1;
+  c.batch = Sh::batch(d);
   c.sample = d.sample;
-  switch (d.kind) {
+  c.ids_logical = d.ids_logical;
+  c.ids_physical = d.ids_physical;
+  switch (Sh::kind(d)) {
     case PLX_SITES_UNIT:
       if (c.batch > 1) {  // (unit, sample) sites over [num_units][batch] columns
         c.role[0] = static_cast<int32_t>(s / c.batch);
@@ -364,20 +411,22 @@ __device__ __forceinline__ void site_setup(const plx_site_desc& d, int64_t s, in
     default: {  // EDGE: the edge's own slot; its endpoints when the ids are passed
       c.role[4] = static_cast<int32_t>(s);
       const int32_t* lg = d.ids_logical;
-      if (d.from_id) c.role[2] = lg ? lg[d.from_id[s]] : d.from_id[s];
-      if (d.to_id) c.role[3] = lg ? lg[d.to_id[s]] : d.to_id[s];
+      if (Sh::from(d)) c.role[2] = Sh::logical(c) ? lg[d.from_id[s]] : d.from_id[s];
+      if (Sh::to(d)) c.role[3] = Sh::logical(c) ? lg[d.to_id[s]] : d.to_id[s];
       break;
     }
   }
   c.cid_value = c.role[4];
-  if (d.site_ids) {
-    if (d.kind == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
-    if (d.kind == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
+  if (Sh::site_ids(d)) {
+    if (Sh::kind(d) == PLX_SITES_EDGE) c.cid_value = d.site_ids[s];
+    if (Sh::kind(d) == PLX_SITES_UNIT) c.role[0] = d.site_ids[c.batch > 1 ? s / c.batch : s / per];
   }
-  c.ids_logical = d.ids_logical;
-  c.ids_physical = d.ids_physical;
   c.seed = (static_cast<uint64_t>(keyed) << 32) | key;
 }
+
+// Lanes per workgroup of every site-program launch (a constant, so the
+// kernel reads no launch size from memory).
+constexpr int kSiteBlock = 256;
 
 template <class Prog>
 __device__ __forceinline__ void site_eval_body(const plx_site_desc& d) {
@@ -386,17 +435,18 @@ __device__ __forceinline__ void site_eval_body(const plx_site_desc& d) {
   const uint32_t keyed =
       px::philox32(d.net_seed, (static_cast<uint64_t>(static_cast<uint32_t>(d.step)) << 8) | 1u);
   const int64_t per = d.per > 0 ? d.per : 1;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s0 < n; s0 += K * stride) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSiteBlock;
+  for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * kSiteBlock + threadIdx.x; s0 < n; s0 += K * stride) {
     uint32_t out[K][PLX_MAX_SOUTS];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const int64_t s = s0 + k * stride;
-      if (s < n) {
-        Site c;
-        site_setup(d, s, per, keyed, c);
-        Prog::run(d.prog, c, d.num_units, out[k]);
-      }
+      // A site past the end evaluates the last site again (s0 < n) and
+      // stores nothing: no branch around the program, so the loads of the
+      // lane's sites can all be issued before the first is used.
+      const int64_t s = K > 1 ? min(s0 + k * stride, n - 1) : s0;
+      Site c;
+      site_setup<typename Prog::Shape>(d, s, per, keyed, c);
+      Prog::run(d.prog, c, d.num_units, out[k]);
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {

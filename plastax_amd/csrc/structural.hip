@@ -41,6 +41,7 @@ using plx_detail::fail;
 namespace {
 
 constexpr int kBlock = 256;          // lanes per workgroup (4 waves of 64)
+static_assert(kBlock == kSiteBlock, "site programs are launched with kSiteBlock lanes");
 constexpr int kWaves = kBlock / 64;
 constexpr int kChunk = kBlock * 8;   // elements per scan / compaction chunk
 constexpr int kTile = kBlock * 16;   // elements per radix tile
@@ -869,7 +870,8 @@ bool prog_ok(const plx_site_prog& p) {
 // shared site_eval_body with a runner that calls site_step once per
 // instruction, operands as literals) and compiled with hipRTC for the
 // current device, with the library's floating-point flags. One compile per
-// (device, program code); the modules stay loaded for the process.
+// (device, program code, launch shape); the modules stay loaded for the
+// process.
 // ---------------------------------------------------------------------------
 struct CompiledSite {
   hipModule_t mod = nullptr;
@@ -877,12 +879,38 @@ struct CompiledSite {
   int dev = -1;
   int32_t ninstr = 0, nout = 0;
   std::vector<int32_t> code;
+  std::vector<int32_t> shape;  // site_shape of the descriptors it runs
 };
+
+// What a compiled kernel fixes besides the code: the site kind, whether the
+// unit columns are batched, which optional id arrays are passed, and every
+// field's width (and id-column flag). A descriptor runs on the kernel only
+// with the same values.
+std::vector<int32_t> site_shape(const plx_site_desc& d) {
+  std::vector<int32_t> v = {d.kind,
+                            d.batch > 1,
+                            d.from_id != nullptr,
+                            d.to_id != nullptr,
+                            d.site_ids != nullptr,
+                            d.ids_logical != nullptr,
+                            d.ids_physical != nullptr};
+  v.insert(v.end(), d.prog.ubytes, d.prog.ubytes + PLX_MAX_SFIELDS);
+  v.insert(v.end(), d.prog.cbytes, d.prog.cbytes + PLX_MAX_SFIELDS);
+  return v;
+}
 
 std::mutex g_site_mu;
 std::map<std::string, CompiledSite*> g_site_cache;
 
-std::string site_source(const plx_site_prog& p) {
+std::string site_source(const plx_site_desc& d) {
+  const plx_site_prog& p = d.prog;
+  const std::vector<int32_t> sh = site_shape(d);
+  auto b = [](bool v) { return std::string(v ? "true" : "false"); };
+  auto widths = [](const int32_t* w) {
+    std::string t = "switch (a) {";
+    for (int f = 0; f < PLX_MAX_SFIELDS; ++f) t += " case " + std::to_string(f) + ": return " + std::to_string(w[f]) + ";";
+    return t + " default: return 4; }";
+  };
   std::string s =
       "// generated by plx_site_compile: one site program, its instructions as site_step calls\n"
       "using __hip_internal::int8_t;\nusing __hip_internal::uint8_t;\nusing __hip_internal::int16_t;\n"
@@ -893,13 +921,28 @@ std::string site_source(const plx_site_prog& p) {
       "#ifndef UINT32_MAX\n#define UINT32_MAX 4294967295u\n#endif\n"
       "#include \"px_site.h\"\n"
       "namespace {\n"
+      "struct SiteShape {\n"
+      "  static constexpr bool kSelects = true;\n"
+      "  __device__ __forceinline__ static int kind(const plx_site_desc&) { return " + std::to_string(sh[0]) + "; }\n"
+      "  __device__ __forceinline__ static int32_t batch(const plx_site_desc& d) { return " +
+      std::string(sh[1] ? "d.batch" : "1") + "; }\n"
+      "  __device__ __forceinline__ static bool from(const plx_site_desc&) { return " + b(sh[2]) + "; }\n"
+      "  __device__ __forceinline__ static bool to(const plx_site_desc&) { return " + b(sh[3]) + "; }\n"
+      "  __device__ __forceinline__ static bool site_ids(const plx_site_desc&) { return " + b(sh[4]) + "; }\n"
+      "  __device__ __forceinline__ static bool logical(const Site&) { return " + b(sh[5]) + "; }\n"
+      "  __device__ __forceinline__ static bool physical(const Site&) { return " + b(sh[6]) + "; }\n"
+      "  __device__ __forceinline__ static bool batched(const Site&) { return " + b(sh[1]) + "; }\n"
+      "  __device__ __forceinline__ static int32_t ubytes(const plx_site_prog&, int a) { " + widths(p.ubytes) + " }\n"
+      "  __device__ __forceinline__ static int32_t cbytes(const plx_site_prog&, int a) { " + widths(p.cbytes) + " }\n"
+      "};\n"
       "struct SiteGen {\n"
+      "  using Shape = SiteShape;\n"
       "  static constexpr int kSites = 4;\n"
       "  __device__ __forceinline__ static void run(const plx_site_prog& p, const Site& c, int32_t nu,\n"
       "                                             uint32_t (&o)[PLX_MAX_SOUTS]) {\n"
       "    SiteRegs r;\n";
   for (int k = 0; k < p.ninstr; ++k) {
-    s += "    site_step(" + std::to_string(p.code[4 * k]) + ", " + std::to_string(p.code[4 * k + 1]) + ", " +
+    s += "    site_step<SiteShape>(" + std::to_string(p.code[4 * k]) + ", " + std::to_string(p.code[4 * k + 1]) + ", " +
          std::to_string(p.code[4 * k + 2]) + ", " + std::to_string(p.code[4 * k + 3]) + ", r, p, c, nu, o);\n";
   }
   s += "  }\n};\n}  // namespace\n"
@@ -907,8 +950,8 @@ std::string site_source(const plx_site_prog& p) {
   return s;
 }
 
-int site_rtc_compile(const plx_site_prog& p, const char* csrc_dir, const std::string& arch, std::vector<char>* code) {
-  const std::string src = site_source(p);
+int site_rtc_compile(const plx_site_desc& d, const char* csrc_dir, const std::string& arch, std::vector<char>* code) {
+  const std::string src = site_source(d);
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, src.c_str(), "plx_site.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
     return fail(PLX_ERR_HIP, "plx_site_compile: hiprtcCreateProgram failed");
@@ -980,8 +1023,11 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
 
 
 
-int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* arch, void** handle) {
-  if (!p || !csrc_dir) return fail(PLX_ERR_INVALID, "plx_site_compile: null argument");
+int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* arch, void** handle) {
+  if (!d || !csrc_dir) return fail(PLX_ERR_INVALID, "plx_site_compile: null argument");
+  const plx_site_prog* p = &d->prog;
+  if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE)
+    return fail(PLX_ERR_INVALID, "plx_site_compile: bad site kind");
   if (p->ninstr < 0 || p->ninstr > PLX_MAX_SINSTR || p->nout < 0 || p->nout > PLX_MAX_SOUTS)
     return fail(PLX_ERR_INVALID, "plx_site_compile: bad program");
   std::string target = arch ? arch : "";
@@ -1006,6 +1052,8 @@ int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* a
   std::string key = std::to_string(dev) + "|" + target + "|" + std::to_string(p->ninstr) + "|" +
                     std::to_string(p->nout) + "|";
   key.append(reinterpret_cast<const char*>(p->code), sizeof(int32_t) * 4 * static_cast<size_t>(p->ninstr));
+  const std::vector<int32_t> shape = site_shape(*d);
+  key.append(reinterpret_cast<const char*>(shape.data()), sizeof(int32_t) * shape.size());
   std::lock_guard<std::mutex> lock(g_site_mu);
   if (handle) {
     const auto it = g_site_cache.find(key);
@@ -1015,7 +1063,7 @@ int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* a
     }
   }
   std::vector<char> code;
-  const int rc = site_rtc_compile(*p, csrc_dir, target, &code);
+  const int rc = site_rtc_compile(*d, csrc_dir, target, &code);
   if (rc || !handle) return rc;
   auto* cs = new CompiledSite;
   if (hipModuleLoadData(&cs->mod, code.data()) != hipSuccess ||
@@ -1028,6 +1076,7 @@ int plx_site_compile(const plx_site_prog* p, const char* csrc_dir, const char* a
   cs->ninstr = p->ninstr;
   cs->nout = p->nout;
   cs->code.assign(p->code, p->code + 4 * p->ninstr);
+  cs->shape = shape;
   g_site_cache[key] = cs;
   *handle = cs;
   return PLX_OK;
@@ -1046,6 +1095,10 @@ int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream) {
   if (cs->ninstr != d->prog.ninstr || cs->nout != d->prog.nout ||
       std::memcmp(cs->code.data(), d->prog.code, sizeof(int32_t) * 4 * static_cast<size_t>(cs->ninstr)) != 0)
     return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: the descriptor's program is not the compiled one");
+  if (site_shape(*d) != cs->shape)
+    return fail(PLX_ERR_INVALID,
+                "plx_site_eval_compiled: the descriptor's site kind, batch, id arrays or field widths are not the "
+                "compiled ones");
   void* args[] = {const_cast<plx_site_desc*>(d)};
   // (four sites per lane per pass: SiteGen::kSites)
   if (hipModuleLaunchKernel(cs->fn, grid_for((d->n + 3) / 4), 1, 1, kBlock, 1, 1, 0,

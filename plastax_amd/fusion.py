@@ -90,11 +90,12 @@ def plan_prune_fusion(net: type, static: Any, globals_: Any, *, engine: str = "a
     position it folds), "xla" (the predicate as its own pass at the
     forward's slot, its kills staged in a sink and merged at the prune
     slot), or "auto": not fused -- on this device the predicate pass at the
-    prune slot, one site per thread ORing straight into DEAD, is the fastest
-    (C2 with a PruneConn every step: 3.37 ms per step, against 3.70 for
-    "xla" and 4.48 for "triton", where each forward thread interprets the
-    predicate for its window's positions in turn); the results are the same
-    bits every way."""
+    prune slot, the predicate compiled to its own kernel (four sites per
+    lane, ORing straight into DEAD), is the fastest (C2 with a PruneConn
+    every step: 1.03 ms per step, against 4.39 for "triton", where each
+    forward thread interprets the predicate for its window's positions in
+    turn, and a sink to merge for "xla"); the results are the same bits
+    every way."""
     if engine not in ENGINES:
         raise ValueError(f"plan_prune_fusion: unknown engine {engine!r}")
     from plastax_amd import _site

@@ -105,30 +105,38 @@ class Scratch:
 
 
 # Site programs evaluated over at least this many sites run as their own
-# compiled kernel (plx_site_compile; compiled once per program and device);
-# smaller launches interpret the program (plx_site_eval). Both give the same
-# bits. "always" / "never" force either (tests).
+# compiled kernel (plx_site_compile; compiled once per program, device and
+# launch shape); smaller launches interpret the program (plx_site_eval). Both
+# give the same bits. "always" / "never" force either (tests).
 COMPILE_SITES: str | int = 1 << 18
 _CSRC = (pathlib.Path(__file__).resolve().parent / "csrc").as_posix().encode()
 
 
-def compiled_site_handle(sp: _site.SiteProgram, prog: _lib.plx_site_prog, device: torch.device) -> int | None:
-    """The compiled kernel of a traced program (``prog`` its filled
-    plx_site_prog), kept on the program per device; None if hipRTC could not
+def _launch_shape(d: _lib.plx_site_desc) -> tuple:
+    """What a compiled kernel fixes besides the code (plx_site_compile): the
+    site kind, batched unit columns, which id arrays are set, the widths."""
+    return (d.kind, d.batch > 1, bool(d.from_id), bool(d.to_id), bool(d.site_ids), bool(d.ids_logical),
+            bool(d.ids_physical), tuple(d.prog.ubytes), tuple(d.prog.cbytes))
+
+
+def compiled_site_handle(sp: _site.SiteProgram, d: _lib.plx_site_desc, device: torch.device) -> int | None:
+    """The compiled kernel of a traced program for descriptor ``d``'s launch
+    shape, kept on the program per (device, shape); None if hipRTC could not
     build it (the caller interprets the program instead, with a warning the
     first time)."""
     cache = sp.__dict__.setdefault("_compiled", {})
     dev = device.index if device.index is not None else torch.cuda.current_device()
-    if dev in cache:
-        return cache[dev]
+    key = (dev, _launch_shape(d))
+    if key in cache:
+        return cache[key]
     lib = _lib.load()
     handle = ctypes.c_void_p()
-    rc = lib.plx_site_compile(ctypes.byref(prog), _CSRC, None, ctypes.byref(handle))
+    rc = lib.plx_site_compile(ctypes.byref(d), _CSRC, None, ctypes.byref(handle))
     if rc != 0:
         warnings.warn(f"site program not compiled, interpreted instead: {lib.plx_last_error().decode()[:500]}")
-        cache[dev] = None
+        cache[key] = None
         return None
-    cache[dev] = handle.value
+    cache[key] = handle.value
     return handle.value
 
 
@@ -184,7 +192,7 @@ class Kernels:
         d.ids_logical, d.ids_physical = _ptr(ids_logical), _ptr(ids_physical)
         policy = COMPILE_SITES
         compiled = policy == "always" or (policy != "never" and int(n) >= int(policy))
-        handle = compiled_site_handle(sp, d.prog, self.mem.device) if compiled else None
+        handle = compiled_site_handle(sp, d, self.mem.device) if compiled else None
         self._begin("site_eval")
         if handle is not None:
             _lib.check(self.lib.plx_site_eval_compiled(handle, d, self.s), "plx_site_eval_compiled")

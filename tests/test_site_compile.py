@@ -2,7 +2,8 @@
 compiles with hipRTC for gfx950 under the library's floating-point flags,
 for a program holding every opcode of the site machine and for traced
 policies (a PruneConn hash predicate, a Box-Muller proposer, the SET
-proposer's table reads). Compile only -- no device is needed; the device
+proposer's table reads), under each launch shape the kernel fixes (site
+kind, batched unit columns, id arrays, byte-wide fields). Compile only -- no device is needed; the device
 runs of compiled programs against the oracle are in
 test_gpu_site_compiled.py."""
 
@@ -31,9 +32,27 @@ def _prog(code: list[tuple[int, int, int, int]], nout: int) -> _lib.plx_site_pro
     return p
 
 
-def _compile(p: _lib.plx_site_prog) -> None:
+_DUMMY = (ctypes.c_int32 * 1)()
+
+
+def _desc(p: _lib.plx_site_prog, kind: int = 5, batch: int = 1, ids: bool = False,
+          ends: bool = False) -> _lib.plx_site_desc:
+    """A descriptor of program p for compiling only: the pointers that fix
+    the shape are set to a dummy host address (nothing is launched)."""
+    d = _lib.plx_site_desc()
+    d.prog = p
+    d.kind, d.batch, d.n, d.per = kind, batch, 1, 1
+    addr = ctypes.addressof(_DUMMY)
+    if ids:
+        d.ids_logical = d.ids_physical = d.site_ids = addr
+    if ends:
+        d.from_id = d.to_id = addr
+    return d
+
+
+def _compile(p: _lib.plx_site_prog, **shape) -> None:
     lib = _lib.load()
-    rc = lib.plx_site_compile(ctypes.byref(p), CSRC, b"gfx950", None)
+    rc = lib.plx_site_compile(ctypes.byref(_desc(p, **shape)), CSRC, b"gfx950", None)
     assert rc == 0, lib.plx_last_error().decode()[:3000]
 
 
@@ -47,7 +66,13 @@ def test_every_opcode_compiles() -> None:
     code = [(op, k % 32, 1 + k % 4, 2 + k % 8) for k, op in enumerate(ops)]
     code += [(_site.SOP["out"], 0, 3, 0), (_site.SOP["out"], 1, 5, 0)]
     assert len(code) <= _site.MAX_SINSTR
-    _compile(_prog(code, 2))
+    p = _prog(code, 2)
+    _compile(p)
+    for f in range(3):  # byte-wide (bool) columns and id columns
+        p.ubytes[f], p.cbytes[f] = 1, 4 | _lib.PLX_SITE_ID_COLUMN
+    for shape in (dict(kind=0, batch=8, ids=True), dict(kind=5, ids=True, ends=True), dict(kind=2),
+                  dict(kind=3), dict(kind=4), dict(kind=1)):
+        _compile(p, **shape)
 
 
 def test_traced_policies_compile() -> None:
@@ -86,14 +111,17 @@ def test_traced_policies_compile() -> None:
         _site.trace_propose(NormalRule(), "per_unit", udt, cdt, None),
         _site.trace_propose(Tables(), "per_unit", udt, cdt, None),
     ]
-    for sp in progs:
-        _compile(_traced(sp))
+    _compile(_traced(progs[0]), kind=5, ends=True)
+    for sp in progs[1:]:
+        _compile(_traced(sp), kind=0)
 
 
 def test_compile_rejects_a_bad_program() -> None:
     lib = _lib.load()
     p = _prog([(1, 0, 0, 0)], 1)
     p.ninstr = _site.MAX_SINSTR + 1
-    assert lib.plx_site_compile(ctypes.byref(p), CSRC, b"gfx950", None) != 0
+    assert lib.plx_site_compile(ctypes.byref(_desc(p)), CSRC, b"gfx950", None) != 0
+    p.ninstr = 1
+    assert lib.plx_site_compile(ctypes.byref(_desc(p, kind=9)), CSRC, b"gfx950", None) != 0
     with pytest.raises(Exception):
         _lib.check(lib.plx_site_compile(None, CSRC, b"gfx950", None), "plx_site_compile")
