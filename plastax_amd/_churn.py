@@ -78,23 +78,33 @@ class ChurnArena(Arena):
         self.num_buckets = nb
         self.pipeline = static.propagation is Propagation.PIPELINE
         k = Kernels(device, stream)
-        ident = np.arange(n, dtype=np.int64)
-        self.uperm = ident
-        self.uinv = ident
-        self.uperm_t = torch.arange(n, dtype=torch.int64, device=device)
-        self.uinv_t = self.uperm_t
-        self.uperm32 = self.uperm_t.to(torch.int32)
-        self.uinv32 = self.uperm32
         levels = units["level"]
-        self.unit_levels = levels.cpu().numpy().astype(np.int64)
+        self._unit_levels: np.ndarray | None = None  # read from levels_dev on first use
         self.lvl_start = np.zeros(1, np.int64)
-        self.input_ids = self._i32(np.asarray(static.input_ids, dtype=np.int64))
-        self.output_ids = self._i32(np.asarray(static.output_ids, dtype=np.int64))
-        is_input = np.zeros(n, dtype=np.uint8)
-        if static.input_ids:
-            is_input[np.asarray(static.input_ids)] = 1
-        self.is_input = torch.from_numpy(is_input).to(device)
         caps = [int(b[DEAD.name].numel()) for b in conns]
+        if prev is not None and getattr(prev, "_consts", None) is not None and prev.static is static \
+                and prev.device == device:
+            # The identity numbering and the id tables depend only on the net:
+            # a rebuild keeps its predecessor's.
+            (self.uperm, self.uinv, self.uperm_t, self.uinv_t, self.uperm32, self.uinv32, self.input_ids,
+             self.output_ids, self.is_input, rows) = prev._consts
+        else:
+            ident = np.arange(n, dtype=np.int64)
+            self.uperm = ident
+            self.uinv = ident
+            self.uperm_t = torch.arange(n, dtype=torch.int64, device=device)
+            self.uinv_t = self.uperm_t
+            self.uperm32 = self.uperm_t.to(torch.int32)
+            self.uinv32 = self.uperm32
+            self.input_ids = self._i32(np.asarray(static.input_ids, dtype=np.int64))
+            self.output_ids = self._i32(np.asarray(static.output_ids, dtype=np.int64))
+            is_input = np.zeros(n, dtype=np.uint8)
+            if static.input_ids:
+                is_input[np.asarray(static.input_ids)] = 1
+            self.is_input = torch.from_numpy(is_input).to(device)
+            rows = torch.arange(n, dtype=torch.int32, device=device)
+        self._consts = (self.uperm, self.uinv, self.uperm_t, self.uinv_t, self.uperm32, self.uinv32,
+                        self.input_ids, self.output_ids, self.is_input, rows)
         spans = [_round_up(c, 4) for c in caps]
         bases = np.concatenate([[0], np.cumsum(spans)]).astype(np.int64)
         total = int(bases[-1])
@@ -135,7 +145,6 @@ class ChurnArena(Arena):
         self.t_name = None
         self.t_now = []
         nbits = max(1, int(n).bit_length())
-        rows = torch.arange(n, dtype=torch.int32, device=device)
         for b, bucket in enumerate(conns):
             if prev is not None:
                 self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b],
@@ -187,6 +196,14 @@ class ChurnArena(Arena):
         self.levels_dev = levels
         if prev is not None:
             prev._retire()
+
+    @property
+    def unit_levels(self) -> np.ndarray:
+        """The units' levels on the host, read from the device on first use
+        (only the generic passes' finalize lists need them)."""
+        if self._unit_levels is None:
+            self._unit_levels = self.levels_dev.cpu().numpy().astype(np.int64)
+        return self._unit_levels
 
     @staticmethod
     def can_follow(prev: "ChurnArena", static: NetworkStatic, caps: list[int]) -> bool:

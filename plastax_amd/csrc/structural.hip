@@ -103,6 +103,10 @@ __global__ void k_chunk_sums(int64_t n_max, const int32_t* n_dev, int32_t mode, 
   __shared__ int lds[kWaves + 1];
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  if (base >= n) {  // a chunk past the count sums to 0 (uniform over the workgroup)
+    if (threadIdx.x == 0) sums[blockIdx.x] = 0;
+    return;
+  }
   int acc = 0;
   for (int r = 0; r < kChunk / kBlock; ++r) {
     const int64_t p = base + r * kBlock + threadIdx.x;
@@ -137,6 +141,7 @@ __global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t*
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
   int run = sums[blockIdx.x];
   for (int r = 0; r < kChunk / kBlock; ++r) {
+    if (base + r * kBlock >= n) break;  // uniform: the rest of the chunk is past the count
     const int64_t p = base + r * kBlock + threadIdx.x;
     const int v = p < n ? in[p] : 0;
     int total;
@@ -154,6 +159,7 @@ __global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mod
   int run = sums[blockIdx.x];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int r = 0; r < kChunk / kBlock; ++r) {
+    if (base + r * kBlock >= n) break;  // uniform: the rest of the chunk is past the count
     const int64_t p = base + r * kBlock + threadIdx.x;
     const int f = p < n ? flag_of(mode, flags, p) : 0;
     const uint64_t m = __ballot(f);
@@ -168,6 +174,75 @@ __global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mod
     if (f) out[before + __popcll(m & lanemask_lt())] = static_cast<int32_t>(p);
     run += total;
     __syncthreads();
+  }
+}
+
+// A radix pass's digit-by-tile counts, tile-major (t[tile * 256 + d]),
+// turned in place into each (tile, digit)'s first output position: the
+// count of smaller digits plus the count of digit d in earlier tiles. One
+// workgroup of kScanTilesWaves waves; wave w keeps tiles [w kScanTilesPer,
+// (w + 1) kScanTilesPer) in registers, lane l digits [4 l, 4 l + 4), so
+// every load and store moves 1 KB per wave. (Up to kScanTilesMax tiles:
+// the sort's table scan in one launch; larger tables take the chunked scan
+// of a digit-major table.)
+constexpr int kScanTilesWaves = kScanLanes / 64;
+constexpr int kScanTilesPer = 16;
+constexpr int64_t kScanTilesMax = int64_t(kScanTilesWaves) * kScanTilesPer;
+__global__ __launch_bounds__(kScanLanes) void k_scan_tiles(int64_t ntiles, int32_t* t) {
+  __shared__ __align__(16) int part[kScanTilesWaves][256];
+  __shared__ __align__(16) int base[256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t t0 = static_cast<int64_t>(wave) * kScanTilesPer;
+  int4 c[kScanTilesPer];
+  int4 sum = make_int4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < kScanTilesPer; ++i) {
+    c[i] = t0 + i < ntiles ? *reinterpret_cast<const int4*>(t + (t0 + i) * 256 + 4 * lane) : make_int4(0, 0, 0, 0);
+    sum.x += c[i].x;
+    sum.y += c[i].y;
+    sum.z += c[i].z;
+    sum.w += c[i].w;
+  }
+  *reinterpret_cast<int4*>(&part[wave][4 * lane]) = sum;
+  __syncthreads();
+  if (threadIdx.x < 256) {  // per digit: the waves' exclusive prefix, then the digit's total
+    const int d = threadIdx.x;
+    int run = 0;
+    for (int w = 0; w < kScanTilesWaves; ++w) {
+      const int x = part[w][d];
+      part[w][d] = run;
+      run += x;
+    }
+    base[d] = run;
+  }
+  __syncthreads();
+  if (wave == 0) {  // the digit totals' exclusive scan: digit d starts after every smaller digit
+    const int4 v = *reinterpret_cast<const int4*>(&base[4 * lane]);
+    const int own = v.x + v.y + v.z + v.w;
+    int x = own;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    int4 e;
+    e.x = x - own;
+    e.y = e.x + v.x;
+    e.z = e.y + v.y;
+    e.w = e.z + v.z;
+    *reinterpret_cast<int4*>(&base[4 * lane]) = e;
+  }
+  __syncthreads();
+  const int4 b = *reinterpret_cast<const int4*>(&base[4 * lane]);
+  const int4 w0 = *reinterpret_cast<const int4*>(&part[wave][4 * lane]);
+  int4 run = make_int4(b.x + w0.x, b.y + w0.y, b.z + w0.z, b.w + w0.w);
+#pragma unroll
+  for (int i = 0; i < kScanTilesPer; ++i) {
+    if (t0 + i < ntiles) *reinterpret_cast<int4*>(t + (t0 + i) * 256 + 4 * lane) = run;
+    run.x += c[i].x;
+    run.y += c[i].y;
+    run.z += c[i].z;
+    run.w += c[i].w;
   }
 }
 
@@ -210,61 +285,84 @@ __device__ __forceinline__ uint32_t score_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__global__ void k_gather_key(int64_t n_max, const int32_t* n_dev, plx_sort_key key,
-                             const uint32_t* vals, uint32_t* keys) {
-  const int64_t n = live_count(n_max, n_dev);
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
-       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t idx = vals[p];
-    uint32_t k;
-    switch (key.kind) {
-      case PLX_KEY_SCORE: k = score_key(static_cast<const float*>(key.a)[idx]); break;
-      case PLX_KEY_LEVEL_OF: {
-        int32_t id = static_cast<const int32_t*>(key.a)[idx];
-        if (key.bound > 0) id = id < 0 ? 0 : (id >= key.bound ? key.bound - 1 : id);
-        k = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id]);
-        break;
-      }
-      case PLX_KEY_PAIR16:
-        k = (static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]) << 16) |
-            (static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[idx]) & 0xFFFFu);
-        break;
-      case PLX_KEY_DEADMAX:
-        k = static_cast<const uint8_t*>(key.b)[idx]
-                ? (key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u))
-                : static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]);
-        break;
-      default: k = static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]); break;
+// Key `key` of element idx (the value being sorted).
+__device__ __forceinline__ uint32_t sort_key_of(const plx_sort_key& key, uint32_t idx) {
+  uint32_t k;
+  switch (key.kind) {
+    case PLX_KEY_SCORE: k = score_key(static_cast<const float*>(key.a)[idx]); break;
+    case PLX_KEY_LEVEL_OF: {
+      int32_t id = static_cast<const int32_t*>(key.a)[idx];
+      if (key.bound > 0) id = id < 0 ? 0 : (id >= key.bound ? key.bound - 1 : id);
+      k = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id]);
+      break;
     }
-    keys[p] = k;
+    case PLX_KEY_PAIR16:
+      k = (static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]) << 16) |
+          (static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[idx]) & 0xFFFFu);
+      break;
+    case PLX_KEY_DEADMAX:
+      k = static_cast<const uint8_t*>(key.b)[idx]
+              ? (key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u))
+              : static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]);
+      break;
+    default: k = static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]); break;
   }
+  return k;
 }
 
-__global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, const uint32_t* keys, int shift,
-                             int64_t ntiles, int32_t* hist) {
+// Per-tile digit counts at `shift`, digit-major (hist[d * ntiles + tile]).
+// With GATHER the keys are computed from the values (sort_key_of) and
+// written to keys; vals_copy (optional) receives a copy of the values.
+// The table's entry of (digit d, tile): tile-major when the table is
+// scanned by k_scan_tiles, else digit-major (the chunked scan's flat order).
+__device__ __forceinline__ int64_t hist_at(bool tile_major, int d, int64_t tile, int64_t ntiles) {
+  return tile_major ? tile * 256 + d : static_cast<int64_t>(d) * ntiles + tile;
+}
+
+template <bool GATHER>
+__global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key key, const uint32_t* vals,
+                             uint32_t* keys, uint32_t* vals_copy, int shift, int64_t ntiles, bool tile_major,
+                             int32_t* hist) {
   __shared__ int h[256];
   const int64_t n = live_count(n_max, n_dev);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  if (base >= n) {  // a tile past the count has no element (uniform over the workgroup)
+    hist[hist_at(tile_major, threadIdx.x, blockIdx.x, ntiles)] = 0;
+    return;
+  }
   h[threadIdx.x] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   for (int r = 0; r < kTile / kBlock; ++r) {
     const int64_t p = base + r * kBlock + threadIdx.x;
-    if (p < n) atomicAdd(&h[(keys[p] >> shift) & 255u], 1);
+    if (p < n) {
+      uint32_t k;
+      if (GATHER) {
+        const uint32_t idx = vals[p];
+        k = sort_key_of(key, idx);
+        keys[p] = k;
+        if (vals_copy) vals_copy[p] = idx;
+      } else {
+        k = keys[p];
+      }
+      atomicAdd(&h[(k >> shift) & 255u], 1);
+    }
   }
   __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x] = h[threadIdx.x];
+  hist[hist_at(tile_major, threadIdx.x, blockIdx.x, ntiles)] = h[threadIdx.x];
 }
 
 __global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint32_t* keys_in,
                                 const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
-                                int shift, int64_t ntiles, const int32_t* hist) {
+                                int shift, int64_t ntiles, bool tile_major, const int32_t* hist) {
   __shared__ int s_off[256];
   __shared__ int s_wcnt[kWaves][256];
   const int64_t n = live_count(n_max, n_dev);
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  s_off[t] = hist[static_cast<int64_t>(t) * ntiles + blockIdx.x];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  if (base >= n) return;  // uniform over the workgroup
+  s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
   for (int r = 0; r < kTile / kBlock; ++r) {
+    if (base + r * kBlock >= n) break;  // uniform: the rest of the tile is past the count
     for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
     __syncthreads();
     const int64_t p = base + r * kBlock + t;
@@ -299,13 +397,6 @@ __global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint3
     }
     __syncthreads();
   }
-}
-
-__global__ void k_copy_u32(int64_t n_max, const int32_t* n_dev, const uint32_t* in, uint32_t* out) {
-  const int64_t n = live_count(n_max, n_dev);
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n;
-       p += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    out[p] = in[p];
 }
 
 int grid_for(int64_t n) {
@@ -1146,26 +1237,36 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
   const int64_t ntiles = (d->n_max + kTile - 1) / kTile;
   int32_t* hist = d->hist;
   int32_t* scan_scratch = d->hist + 256 * ntiles;
+  const bool tile_major = ntiles <= kScanTilesMax;  // the table scan in one launch
   for (int k = 0; k < d->nkeys; ++k) {
     const plx_sort_key& key = d->keys[k];
     if (key.bits < 1 || key.bits > 32 || !key.a) return fail(PLX_ERR_INVALID, "plx_sort: bad key");
     if ((key.kind == PLX_KEY_LEVEL_OF || key.kind == PLX_KEY_PAIR16 || key.kind == PLX_KEY_DEADMAX) && !key.b)
       return fail(PLX_ERR_INVALID, "plx_sort: key needs its second column");
-    hipLaunchKernelGGL(k_gather_key, dim3(grid_for(d->n_max)), dim3(kBlock), 0, s, d->n_max, d->n_dev, key,
-                       d->vals, d->keys_buf);
-    uint32_t* kin = d->keys_buf;
-    uint32_t* vin = d->vals;
-    uint32_t* kout = d->keys_alt;
-    uint32_t* vout = d->vals_alt;
+    // Pass 0's histogram computes the keys from the values. With an odd
+    // number of passes it also copies the values to vals_alt and pass 0
+    // reads them there, so the last pass writes its order into vals.
     const int passes = (key.bits + 7) / 8;
+    const bool odd = passes & 1;
+    hipLaunchKernelGGL(k_radix_hist<true>, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, key, d->vals,
+                       d->keys_buf, odd ? d->vals_alt : nullptr, 0, ntiles, tile_major, hist);
+    uint32_t* kin = d->keys_buf;
+    uint32_t* vin = odd ? d->vals_alt : d->vals;
+    uint32_t* kout = d->keys_alt;
+    uint32_t* vout = odd ? d->vals : d->vals_alt;
     for (int pass = 0; pass < passes; ++pass) {
       const int shift = 8 * pass;
-      hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, kin, shift,
-                         ntiles, hist);
-      const int rc = scan_or_compact(256 * ntiles, nullptr, -1, hist, hist, nullptr, scan_scratch, s, "plx_sort");
-      if (rc != PLX_OK) return rc;
+      if (pass > 0)
+        hipLaunchKernelGGL(k_radix_hist<false>, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, key,
+                           nullptr, kin, nullptr, shift, ntiles, tile_major, hist);
+      if (tile_major) {
+        hipLaunchKernelGGL(k_scan_tiles, dim3(1), dim3(kScanLanes), 0, s, ntiles, hist);
+      } else {
+        const int rc = scan_or_compact(256 * ntiles, nullptr, -1, hist, hist, nullptr, scan_scratch, s, "plx_sort");
+        if (rc != PLX_OK) return rc;
+      }
       hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, kin, vin, kout,
-                         vout, shift, ntiles, hist);
+                         vout, shift, ntiles, tile_major, hist);
       uint32_t* t = kin;
       kin = kout;
       kout = t;
@@ -1173,9 +1274,6 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
       vin = vout;
       vout = t;
     }
-    if (vin != d->vals)
-      hipLaunchKernelGGL(k_copy_u32, dim3(grid_for(d->n_max)), dim3(kBlock), 0, s, d->n_max, d->n_dev, vin,
-                         d->vals);
   }
   return check_launch("plx_sort");
 }

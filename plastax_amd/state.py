@@ -116,8 +116,11 @@ class NetworkState:
         self.step = step
         self.grown = grown
         self.overflow = overflow
-        self.units_added = units_added
-        self.unit_overflow = unit_overflow
+        self._units_added = units_added
+        self._unit_overflow = unit_overflow
+        # add_unit's (units_added, unit_overflow) while they are still on the
+        # device: read on first access, so a step need not wait for them.
+        self._unit_flags_dev: Any = None
         self.tail_start = tail_start
         self._arena: Any = None  # plastax_amd._layout.Arena once a step ran
         self._arena_ahead = False  # the arena holds newer conn values
@@ -146,16 +149,50 @@ class NetworkState:
             self.step,
             self.grown,
             self.overflow,
-            self.units_added,
-            self.unit_overflow,
+            self._units_added,
+            self._unit_overflow,
             self.tail_start,
         )
+        new._unit_flags_dev = self._unit_flags_dev
         new._arena = self._arena
         new._arena_ahead = self._arena_ahead
         new._arena_prev = self._arena_prev
         new._units_phys = self._units_phys
         self._donated = True
         return new
+
+    # -- add_unit's flags ---------------------------------------------------------
+    @property
+    def units_added(self) -> int:
+        self._resolve_unit_flags()
+        return self._units_added
+
+    @units_added.setter
+    def units_added(self, value: int) -> None:
+        self._resolve_unit_flags()
+        self._units_added = value
+
+    @property
+    def unit_overflow(self) -> bool:
+        self._resolve_unit_flags()
+        return self._unit_overflow
+
+    @unit_overflow.setter
+    def unit_overflow(self, value: bool) -> None:
+        self._resolve_unit_flags()
+        self._unit_overflow = value
+
+    def _resolve_unit_flags(self) -> None:
+        flags, self._unit_flags_dev = self._unit_flags_dev, None
+        if flags is not None:
+            got = flags.cpu().tolist()
+            self._units_added, self._unit_overflow = int(got[0]), bool(got[1])
+
+    def _set_unit_flags(self, added: int, overflow: bool, flags_dev: Any = None) -> None:
+        """Both flags at once (no read of a pending pair), or, with
+        ``flags_dev``, the device pair (units_added, unit_overflow) to read
+        on first access."""
+        self._units_added, self._unit_overflow, self._unit_flags_dev = added, overflow, flags_dev
 
     def _mark_ahead(self, columns: Any = None) -> None:
         """The step wrote connection values into the arena: ``columns`` (a

@@ -367,28 +367,38 @@ class StepFn:
                 timer.end("prune_conn")
             arena.dead_in_rows = True
             state._mark_ahead({DEAD.name, arena.t_name})
+        spawned = False  # add_unit ran: its flags stay on the device until read
         if plan.add_unit:
             if self._add_unit is None:
                 self._add_unit = unit_phases.AddUnitPhase(plan.net, self.static, g)
             phase_u = self._add_unit
             if phase_u.fires(int(state.step)):
                 ulog = {name: col.clone() for name, col in state.units.items()}
-                added, unit_overflow = phase_u.run(k, ulog, g)
-                state.units_added, state.unit_overflow = added, unit_overflow
-                if added:
-                    # New units need rows in the layout: the arena is laid out again.
-                    state.conns = state.conns
+                state._set_unit_flags(0, False, phase_u.run_device(k, ulog, g))
                 state.units = ulog
+                spawned = True
             else:
-                state.units_added, state.unit_overflow = 0, False
-        if plan.add_conn is not None:
+                state._set_unit_flags(0, False)
+
+        def relayout_for_new_units() -> None:
+            # New units need rows in the layout: the arena is laid out again
+            # (a growth that fires replaces the buckets and does it anyway).
+            if spawned and state.units_added:
+                state.conns = state.conns
+
+        if plan.add_conn is None:
+            relayout_for_new_units()
+        else:
             if self._grow is None:
                 self._grow = grow.AddConnPhase(plan.net, self.static, g)
             phase = self._grow
+            # (units_added is read only for a growth triggered by it)
+            added = int(state.units_added) if phase.cfg.trigger == "on_units_added" else 0
             fires = phase.cfg.fires(phase.ac, step=int(state.step), interval=phase.interval,
-                                    units_added=int(state.units_added), globals_=g)
+                                    units_added=added, globals_=g)
             if not fires:
                 state.grown, state.overflow = 0, False
+                relayout_for_new_units()
                 return
             conns = state.conns  # the logical view, in step with the arena
             prev = state._arena
@@ -397,7 +407,7 @@ class StepFn:
                 # DEAD before the claim: the claimed slots are the ones it turns live
                 before = [bucket[DEAD.name].clone() for bucket in conns]
             out = phase.run(k, state.units, conns, step=int(state.step), globals_=g,
-                            tail_start=int(state.tail_start), units_added=int(state.units_added))
+                            tail_start=int(state.tail_start), units_added=added)
             state.conns = out.conns
             if before is not None:
                 state._arena_prev = (prev, before)  # the next layout merges the claimed slots into prev's

@@ -96,9 +96,15 @@ class PruneUnitPhase:
 
     def exempt(self, device: torch.device, order: torch.Tensor | None) -> torch.Tensor:
         """The input/output mask, in the caller's order or through ``order``
-        (physical position -> caller's id)."""
+        (physical position -> caller's id); the last one is kept while the
+        same ``order`` tensor comes back (an arena's numbering)."""
+        last = self.__dict__.get("_exempt_last")
+        if last is not None and last[0] == device and last[1] is order:
+            return last[2]
         t = torch.from_numpy(self._exempt_host).to(device)
-        return t if order is None else t[order.long()].contiguous()
+        t = t if order is None else t[order.long()].contiguous()
+        self._exempt_last = (device, order, t)
+        return t
 
     def run(self, k: Kernels, units: Columns, globals_: Any, *, site_ids: torch.Tensor | None = None,
             ids_physical: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -164,7 +170,13 @@ class AddUnitPhase:
 
     def run(self, k: Kernels, units: Columns, globals_: Any) -> tuple[int, bool]:
         """On the caller's unit numbering; returns (units_added,
-        unit_overflow) (the phase's one host read)."""
+        unit_overflow) (a host read)."""
+        got = self.run_device(k, units, globals_).cpu().tolist()
+        return int(got[0]), bool(got[1])
+
+    def run_device(self, k: Kernels, units: Columns, globals_: Any) -> torch.Tensor:
+        """run() without the host read: returns the device flags
+        (units_added, unit_overflow) as two int32."""
         n = int(units["level"].shape[0])
         wants, offset = k.mem.i32(n), k.mem.i32(n)
         k.site_eval(self.spawn, units, globals_, n=n, kind=0, per=1, num_units=n, outs=[wants, offset])
@@ -185,6 +197,5 @@ class AddUnitPhase:
             ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
             _lib.check(k.lib.plx_unit_write(n, flags.data_ptr(), child.data_ptr(), None, len(self.init_names),
                                             ctypes.addressof(icols), ctypes.addressof(ptrs), k.s), "plx_unit_write")
-        got = flags.cpu().tolist()
-        return int(got[0]), bool(got[1])
+        return flags
 
