@@ -386,6 +386,17 @@ typedef struct plx_batch_tiles {
  * updated). Table builders check theirs against these. */
 PLX_EXPORT int plx_batch_tile_limits(int32_t* rows, int32_t* edges);
 
+/* Roof probes (no counterpart in the reference: a measurement helper for
+ * the benchmark's rooflines). Times one launch of a read loop and returns
+ * the bytes it read and its duration (the call synchronises `stream`):
+ * PLX_PROBE_LDS, conflict-free 16-byte LDS reads (buf unused); PLX_PROBE_L2,
+ * coalesced 16-byte reads of buf (buf_bytes / 16 a power of two; a few MB
+ * stay L2-resident). out: 2048 * 256 uint32 of device memory. */
+#define PLX_PROBE_LDS 0
+#define PLX_PROBE_L2 1
+PLX_EXPORT int plx_roof_probe(int32_t kind, int32_t iters, const void* buf, int64_t buf_bytes, uint32_t* out,
+                              double* bytes, float* ms, void* stream);
+
 PLX_EXPORT int plx_update_batch_tiles(const plx_update_desc* d, const plx_batch_tiles* t, int32_t batch,
                                       void* stream);
 

@@ -31,6 +31,8 @@ PLX_MAX_SFIELDS = 8
 PLX_MAX_SOUTS = 8
 PLX_MAX_GROW_COLS = 16
 PLX_SITE_ID_COLUMN = 0x100
+PLX_PROBE_LDS = 0
+PLX_PROBE_L2 = 1
 PLX_MAX_UNIT_COLS = 16
 
 c_i32 = ctypes.c_int32
@@ -472,6 +474,8 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_site_compile": (c_i32, [ctypes.POINTER(plx_site_desc), ctypes.c_char_p, ctypes.c_char_p,
                                  ctypes.POINTER(c_vp)]),
     "plx_site_eval_compiled": (c_i32, [c_vp, ctypes.POINTER(plx_site_desc), c_vp]),
+    "plx_roof_probe": (c_i32, [c_i32, c_i32, c_vp, c_i64, c_vp, ctypes.POINTER(ctypes.c_double),
+                               ctypes.POINTER(ctypes.c_float), c_vp]),
     "plx_update_conn": (c_i32, [ctypes.POINTER(plx_update_desc), c_vp]),
     "plx_scatter_f32": (c_i32, [c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_loss_elementwise": (

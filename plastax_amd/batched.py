@@ -67,10 +67,18 @@ class BatchSources:
 def batch_sources(arena: Arena, b: int) -> BatchSources:
     """Bucket b's backward rows: every unit of level b and every live source
     of the bucket, ascending; each row's live positions sorted by logical slot
-    (cached on the arena, whose structure it follows)."""
+    (built on the device, cached on the arena, whose structure it follows)."""
+    from plastax_amd._batch_dev import batch_sources_dev
+
     cache = arena.__dict__.setdefault("_batch_sources", {})
-    if b in cache:
-        return cache[b]
+    if b not in cache:
+        cache[b] = batch_sources_dev(arena, b)
+    return cache[b]
+
+
+def batch_sources_host(arena: Arena, b: int) -> BatchSources:
+    """batch_sources built on the host with numpy (the restatement the
+    device build is tested against)."""
     base, live = arena.bases[b], arena.lives[b]
     src = arena.cols["from_id"][base : base + live].cpu().numpy().astype(np.int64)
     dst_all = arena.cols["to_id"][base : base + live].cpu().numpy().astype(np.int64)
@@ -92,7 +100,6 @@ def batch_sources(arena: Arena, b: int) -> BatchSources:
         torch.from_numpy(np.concatenate([pos, [base]]).astype(np.int32)).to(dev),
         torch.from_numpy(np.concatenate([dst_all[order], [0]]).astype(np.int32)).to(dev),
     )
-    cache[b] = out
     return out
 
 
@@ -452,13 +459,9 @@ class BatchedStepFn(StepFn):
                     f"the library's batched-update tiles are {rows.value} units / {edges.value} edges, "
                     f"the layout builds {_layout.BATCH_TILE_UNITS} / {_layout.BATCH_TILE_EDGES}: rebuild it")
         if b not in cache:
-            base, live = arena.bases[b], arena.lives[b]
-            src = arena.cols["from_id"][base : base + live].cpu().numpy()
-            dst = arena.cols["to_id"][base : base + live].cpu().numpy()
-            tb = _layout.batch_tiles(src, dst)
-            dev = arena.device
-            cache[b] = {k: torch.from_numpy(v.astype(np.uint16).view(np.int16) if k == "loc" else v.astype(np.int32)).to(dev)
-                        for k, v in tb.items()}
+            from plastax_amd._batch_dev import batch_tiles_dev
+
+            cache[b] = batch_tiles_dev(arena, b)
         c = cache[b]
         t = _lib.plx_batch_tiles()
         t.ntiles = int(c["tile_off"].numel()) - 1

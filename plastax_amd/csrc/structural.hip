@@ -1278,6 +1278,47 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
   return check_launch("plx_sort");
 }
 
+// ---------------------------------------------------------------------------
+// Roof probes: the read bandwidth of LDS (conflict-free 16-byte reads, each
+// wave reading 1 KB per instruction) and of an L2-resident buffer (16-byte
+// coalesced reads of `words` uint4, a power of two, read over and over).
+// Every index is masked into its buffer.
+// ---------------------------------------------------------------------------
+constexpr int kProbeLdsWords = 4096;  // uint4 = 64 KB
+constexpr int kProbeBlocks = 2048;
+
+__global__ __launch_bounds__(256) void k_probe_lds(uint32_t* out, int32_t iters) {
+  __shared__ uint4 buf[kProbeLdsWords];
+  for (int i = threadIdx.x; i < kProbeLdsWords; i += 256) buf[i] = make_uint4(i, i * 3u, i * 5u, i * 7u);
+  __syncthreads();
+  uint32_t acc = 0;
+  int idx = threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint4 v = buf[(idx + k * 256) & (kProbeLdsWords - 1)];
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    idx = (idx + 64) & (kProbeLdsWords - 1);
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(256) void k_probe_l2(const uint4* buf, int64_t words, uint32_t* out, int32_t iters) {
+  uint32_t acc = 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint4 v = buf[(idx + k * stride) & (words - 1)];
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    idx = (idx + 8 * stride) & (words - 1);
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
 int plx_grow_filter(const plx_grow_filter_desc* d, void* stream) {
   if (!d) return fail(PLX_ERR_INVALID, "plx_grow_filter: null descriptor");
   if (d->n < 0 || d->num_units < 1) return fail(PLX_ERR_INVALID, "plx_grow_filter: bad sizes");
@@ -1598,4 +1639,38 @@ int plx_compact_noalloc(int64_t n, const int32_t* n_dev, int32_t mode, const voi
   if (rc != PLX_OK) return rc;
   return scan_or_compact(n, n_dev, mode, flags, out, count, sums, static_cast<hipStream_t>(stream),
                          "plx_compact_noalloc");
+}
+
+int plx_roof_probe(int32_t kind, int32_t iters, const void* buf, int64_t buf_bytes, uint32_t* out, double* bytes,
+                   float* ms, void* stream) {
+  if (kind != PLX_PROBE_LDS && kind != PLX_PROBE_L2) return fail(PLX_ERR_INVALID, "plx_roof_probe: unknown kind");
+  if (iters < 1 || !out || !bytes || !ms) return fail(PLX_ERR_INVALID, "plx_roof_probe: bad arguments");
+  const int64_t words = buf_bytes / 16;
+  if (kind == PLX_PROBE_L2 && (!buf || words < 1 || (words & (words - 1)) != 0))
+    return fail(PLX_ERR_INVALID, "plx_roof_probe: the L2 buffer must hold a power-of-two count of 16 bytes");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return fail(PLX_ERR_HIP, "plx_roof_probe: event");
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return fail(PLX_ERR_HIP, "plx_roof_probe: event");
+  }
+  (void)hipEventRecord(a, s);
+  if (kind == PLX_PROBE_LDS) {
+    hipLaunchKernelGGL(k_probe_lds, dim3(kProbeBlocks), dim3(256), 0, s, out, iters);
+    *bytes = double(kProbeBlocks) * 256 * iters * 16 * 16;
+  } else {
+    hipLaunchKernelGGL(k_probe_l2, dim3(kProbeBlocks), dim3(256), 0, s, static_cast<const uint4*>(buf), words, out,
+                       iters);
+    *bytes = double(kProbeBlocks) * 256 * iters * 8 * 16;
+  }
+  (void)hipEventRecord(b, s);
+  const hipError_t e = hipEventSynchronize(b);
+  float t = 0.0f;
+  if (e == hipSuccess) (void)hipEventElapsedTime(&t, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  if (e != hipSuccess) return fail(PLX_ERR_HIP, "plx_roof_probe: launch failed");
+  *ms = t;
+  return check_launch("plx_roof_probe");
 }
