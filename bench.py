@@ -480,16 +480,20 @@ def run_c5(args) -> int:
     setup_s = time.perf_counter() - t_setup
     progress(f"C5: {e.src.size} live edges of {static.level_capacities[0]} slots, layout {step.backward_order} "
              f"({setup_s:.1f} s)")
-    grown = added = 0
+    # Each step's flags stay on the device; they are read after the timed
+    # region (a driver checking them every step would add a host read per
+    # step on top of the step itself).
+    readers = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
         gstate.globals_ = g_of(k)
         gstate = step(gstate, px.StepInputs(xs_d[k])).state
-        grown += int(gstate.grown)
-        added += int(gstate.units_added)
+        readers.append((gstate._flag_reader("grown"), gstate._flag_reader("units_added")))
         k += 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    grown = sum(int(r()) for r, _ in readers)
+    added = sum(int(r()) for _, r in readers)
     ms = elapsed * 1e3 / args.steps
     live = int(sum(int((b["dead"] == 0).sum().item()) for b in gstate.conns))
     live_units = int((gstate.units["pruned"] == 0).sum().item())

@@ -781,8 +781,8 @@ PLX_EXPORT int plx_grow_select(int64_t n_max, const int32_t* n_dev, const int32_
  * Committed winners write from_id, to_id, dead = 0 and every column in
  * cols: from init output slot (init_out[q] for winner q) or the column's
  * default bits. flags[0] += committed, flags[1] |= overflow, flags[2] |=
- * committed with level[dst] <= level[src], flags[3] += tail slots used.
- * scratch: 8 n_max + plx_scratch_ints(n_max) ints. */
+ * committed with level[dst] <= level[src], flags[3] += tail slots used
+ * (flags[4]: see tail_dev). scratch: 8 n_max + plx_scratch_ints(n_max) ints. */
 #define PLX_MAX_GROW_COLS 16
 typedef struct plx_grow_col {
   void* ptr;
@@ -828,6 +828,11 @@ typedef struct plx_grow_claim_desc {
    * (optional) gets 1 for every growable winner that found no slot. */
   const int32_t* growable_in;
   int32_t* dropped_out;
+  /* PIPELINE, optional: the tail start read from the device (int32)
+   * instead of tail_start; flags then holds five ints and flags[4] gets the
+   * new tail start, *tail_dev + flags[3], so a caller can pass &flags[4] as
+   * the next claim's tail_dev without reading anything on the host. */
+  const int32_t* tail_dev;
 } plx_grow_claim_desc;
 
 PLX_EXPORT int plx_grow_claim(const plx_grow_claim_desc* d, void* stream);

@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 23  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 24  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -459,6 +459,7 @@ class plx_grow_claim_desc(ctypes.Structure):
         ("scratch", c_vp),
         ("growable_in", c_vp),
         ("dropped_out", c_vp),
+        ("tail_dev", c_vp),
     ]
 
 

@@ -394,7 +394,7 @@ class BatchedStepFn(StepFn):
         if plan.reset_global:
             state.globals_ = plan.net.reset_global.reset(state.globals_)
         state.step = state.step + 1
-        return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
+        return StepResult(state=state, overflow=state._flag_reader("overflow"), loss=loss, growth_remainder=None)
 
     def _mean_of_writes(self, arena: Arena, ub: dict, g: Any, stream: int) -> None:
         """A user UpdateConn under a batched step (phases.py:484-533): each

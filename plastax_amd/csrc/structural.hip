@@ -648,7 +648,7 @@ __global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int
       const int32_t l = lvl < d.num_levels ? lvl : d.num_levels - 1;
       slot = d.own_slots[d.own_start[l] + rank[q]];
     } else {
-      const int64_t t = d.tail_start + spill_rank[q];
+      const int64_t t = (d.tail_dev ? static_cast<int64_t>(*d.tail_dev) : d.tail_start) + spill_rank[q];
       if (t < d.capacity) {
         slot = t;
         atomicAdd(&d.flags[3], 1);
@@ -673,6 +673,12 @@ __global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int
         static_cast<uint32_t*>(col.ptr)[slot] = v;
     }
   }
+}
+
+// The new tail start after a PIPELINE claim: the old one plus the tail slots
+// it used.
+__global__ void k_claim_tail(const int32_t* tail_dev, int32_t* flags) {
+  if (threadIdx.x == 0) flags[4] = *tail_dev + flags[3];
 }
 
 __global__ void k_gather_level(int64_t n_max, const int32_t* n_dev, const int32_t* idx, const int32_t* ids,
@@ -1360,7 +1366,15 @@ int plx_grow_claim(const plx_grow_claim_desc* d, void* stream) {
   if (!d) return fail(PLX_ERR_INVALID, "plx_grow_claim: null descriptor");
   if (d->n_max < 0 || d->ncols < 0 || d->ncols > PLX_MAX_GROW_COLS)
     return fail(PLX_ERR_INVALID, "plx_grow_claim: bad sizes");
-  if (d->n_max == 0) return PLX_OK;
+  if (d->tail_dev && (!d->pipeline || !d->flags))
+    return fail(PLX_ERR_INVALID, "plx_grow_claim: tail_dev without a PIPELINE claim's flags");
+  if (d->n_max == 0) {
+    if (d->tail_dev) {
+      hipLaunchKernelGGL(k_claim_tail, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), d->tail_dev, d->flags);
+      return check_launch("plx_grow_claim");
+    }
+    return PLX_OK;
+  }
   if (!d->winners || !d->src || !d->dst || !d->score || !d->level || !d->from_id || !d->to_id || !d->dead ||
       !d->flags || !d->scratch)
     return fail(PLX_ERR_INVALID, "plx_grow_claim: null pointer");
@@ -1400,6 +1414,7 @@ int plx_grow_claim(const plx_grow_claim_desc* d, void* stream) {
     if (rc != PLX_OK) return rc;
   }
   hipLaunchKernelGGL(k_claim_write, dim3(grid), dim3(kBlock), 0, s, *d, grow, rank, spill, spill_rank);
+  if (d->tail_dev) hipLaunchKernelGGL(k_claim_tail, dim3(1), dim3(64), 0, s, d->tail_dev, d->flags);
   return check_launch("plx_grow_claim");
 }
 

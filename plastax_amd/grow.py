@@ -258,14 +258,33 @@ class Remainder:
     nseg: int
 
 
-@dataclasses.dataclass
 class GrowthOutcome:
-    conns: tuple[Columns, ...]
-    grown: int
-    overflow: bool
-    needs_resort: bool
-    tail_start: int
-    fired: bool
+    """A growth phase's result: the new buckets, whether it ran, and its
+    flags. A claim leaves the flags on the device (``flags``: int32 grown,
+    overflow, needs_resort, tail slots used and, for PIPELINE, the new tail
+    start), read on first access of ``grown`` / ``overflow`` /
+    ``needs_resort`` / ``tail_start``; a step passes them on unread."""
+
+    def __init__(self, conns: tuple[Columns, ...], grown: int = 0, overflow: bool = False,
+                 needs_resort: bool = False, tail_start: Any = 0, fired: bool = False, *,
+                 flags: torch.Tensor | None = None) -> None:
+        self.conns = conns
+        self.fired = fired
+        self.flags = flags
+        self._tail_in = tail_start  # host int or a device int32[1] (PIPELINE)
+        self._host = None if flags is not None else (int(grown), bool(overflow), bool(needs_resort), tail_start)
+
+    def _values(self) -> tuple[int, bool, bool, int]:
+        if self._host is None:
+            got = self.flags.cpu().tolist()
+            tail = got[4] if len(got) > 4 else self._tail_in
+            self._host = (int(got[0]), bool(got[1]), bool(got[2]), int(tail))
+        return self._host
+
+    grown = property(lambda self: self._values()[0])
+    overflow = property(lambda self: self._values()[1])
+    needs_resort = property(lambda self: self._values()[2])
+    tail_start = property(lambda self: int(self._values()[3]))
 
 
 def flatten(conns: tuple[Columns, ...]) -> tuple[Columns, list[int]]:
@@ -395,6 +414,9 @@ class AddConnPhase:
         self.imp_prog = _site.trace_importance(self.ac, unit_dtypes, globals_) if cfg.shortlist else None
         self.init_prog, self.init_names = _site.trace_init(self.ac, unit_dtypes, static.conn_fields, globals_)
         self.remainder: Remainder | None = None
+        # (flags of the last PIPELINE claim, a host bound on the tail start
+        # it wrote into flags[4])
+        self._tail_hint: tuple[torch.Tensor, int] | None = None
 
     # -- helpers ---------------------------------------------------------------
     def _top_units(self, k: Kernels, masked: torch.Tensor, m: int, n: int) -> torch.Tensor:
@@ -420,7 +442,11 @@ class AddConnPhase:
 
     # -- the phase --------------------------------------------------------------
     def run(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], *, step: int, globals_: Any,
-            tail_start: int = 0, units_added: int = 0) -> GrowthOutcome:
+            tail_start: Any = 0, units_added: int = 0, needs_resort: Any = False) -> GrowthOutcome:
+        """One growth phase. ``tail_start``: an int, or (PIPELINE) a device
+        int32[1] such as the last outcome's ``flags[4:5]``. ``needs_resort``:
+        the flag before the phase (a bool, or a pending (device tensor,
+        index)); the outcome's needs_resort is it OR the claim's."""
         cfg = self.cfg
         if not cfg.fires(self.ac, step=step, interval=self.interval, units_added=units_added, globals_=globals_):
             return GrowthOutcome(conns, 0, False, False, tail_start, False)
@@ -562,9 +588,10 @@ class AddConnPhase:
             threshold = float(np.float32(np.asarray(self.ac.threshold(globals_))))
         rem = Remainder(nc, winners, nwin, src, dst, score, init_outs, k.mem.i32(nc), nseg)
         self.remainder = rem
-        return self._claim(k, level, conns, flat, offs, tail_start, rem, threshold=threshold)
+        return self._claim(k, level, conns, flat, offs, tail_start, rem, threshold=threshold,
+                           needs_resort=needs_resort)
 
-    def retry(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], *, tail_start: int) -> GrowthOutcome:
+    def retry(self, k: Kernels, units: Columns, conns: tuple[Columns, ...], *, tail_start: Any) -> GrowthOutcome:
         """Claim the winners the last phase dropped into ``conns`` (its buckets
         regrown by the caller), with the values that phase computed, in the
         total order (build_growth_retry, phases.py:5206-5281). No other
@@ -577,8 +604,8 @@ class AddConnPhase:
         return self._claim(k, units["level"], conns, flat, offs, tail_start, rem, growable_in=growable)
 
     def _claim(self, k: Kernels, level: torch.Tensor, conns: tuple[Columns, ...], flat: Columns, offs: list[int],
-               tail_start: int, rem: "Remainder", *, threshold: float | None = None,
-               growable_in: torch.Tensor | None = None) -> GrowthOutcome:
+               tail_start: Any, rem: "Remainder", *, threshold: float | None = None,
+               growable_in: torch.Tensor | None = None, needs_resort: Any = False) -> GrowthOutcome:
         cfg = self.cfg
         n, nb, nc, nseg = cfg.num_units, cfg.num_buckets, rem.nc, rem.nseg
         total_slots = offs[-1]
@@ -591,24 +618,44 @@ class AddConnPhase:
             c.has_threshold = 1
             c.threshold = threshold
         c.max_new_per_step = int(cfg.max_new_per_step or 0)
-        c.capacity, c.tail_start = total_slots, int(tail_start)
+        c.capacity = total_slots
         keep: list[torch.Tensor] = []
+        tail_dev = None
         if cfg.pipeline:
             # Each level's own dead slots (below the tail, by the level of
-            # their former source), in slot order, level after level.
-            tail = int(tail_start)
-            own, nown = k.compact(tail, 0, flat["dead"])  # PLX_FLAG_U8 over [0, tail)
-            k.sort(own, tail, [(2, _bits_for(nseg - 1), flat["from_id"], level, n)], n_dev=nown)
-            domain = k.mem.i32(tail)
-            _lib.check(k.lib.plx_gather_level(tail, nown.data_ptr(), own.data_ptr(), flat["from_id"].data_ptr(),
+            # their former source), in slot order, level after level. The
+            # tail start is a device int32 (the last claim's result, or the
+            # caller's value), so the lists are sized by the arena's slots
+            # and counted on the device.
+            # The lists are sized by a host bound on the tail: exact for a host
+            # value; for the last claim's device tail, that claim's bound
+            # plus its winner budget (tail slots used <= winners); else the
+            # arena's slots.
+            if isinstance(tail_start, torch.Tensor):
+                tail_dev = tail_start
+                hint = self._tail_hint
+                span = total_slots
+                if hint is not None and tail_dev.data_ptr() == hint[0].data_ptr() + 16:
+                    span = hint[1]
+            else:
+                span = int(tail_start)
+                tail_dev = torch.tensor([span], dtype=torch.int32, device=dev)
+            span = max(0, min(total_slots, span))
+            c.tail_dev = tail_dev.data_ptr()
+            own, nown = k.compact(span, 0, flat["dead"], n_dev=tail_dev)  # PLX_FLAG_U8 over [0, tail)
+            k.sort(own, span, [(2, _bits_for(nseg - 1), flat["from_id"], level, n)], n_dev=nown)
+            domain = k.mem.i32(span)
+            _lib.check(k.lib.plx_gather_level(span, nown.data_ptr(), own.data_ptr(), flat["from_id"].data_ptr(),
                                               level.data_ptr(), n, domain.data_ptr(), k.s), "plx_gather_level")
             count, start = k.mem.i32(nseg), k.mem.i32(nseg)
             lscratch = k.mem.ints_for(nseg)
-            _lib.check(k.lib.plx_level_counts(tail, nown.data_ptr(), domain.data_ptr(), nseg, count.data_ptr(),
-                                              start.data_ptr(), lscratch.data_ptr(), k.s), "plx_level_counts")
+            _lib.check(k.lib.plx_level_counts(span, nown.data_ptr(), domain.data_ptr(), nseg,
+                                              count.data_ptr(), start.data_ptr(), lscratch.data_ptr(), k.s),
+                       "plx_level_counts")
             c.own_slots, c.own_start, c.own_count = own.data_ptr(), start.data_ptr(), count.data_ptr()
-            keep += [domain, own, nown, count, start, lscratch]
+            keep += [domain, own, nown, count, start, lscratch, tail_dev]
         else:
+            c.tail_start = int(tail_start)
             free, nfree = k.compact(total_slots, 0, flat["dead"])
             off = torch.tensor(offs, dtype=torch.int64, device=dev)
             info = k.mem.i32(2 * nb)
@@ -634,16 +681,25 @@ class AddConnPhase:
         c.ncols = ncols
         for j, o in enumerate(rem.init_outs):
             c.init_out[j] = o.data_ptr()
-        flags = torch.zeros(4, dtype=torch.int32, device=dev)
+        # grown, overflow, needs_resort, tail slots used (+ the new tail start)
+        flags = torch.zeros(5 if tail_dev is not None else 4, dtype=torch.int32, device=dev)
+        if isinstance(needs_resort, tuple):  # the claim ORs into the flag it starts from
+            t, i = needs_resort
+            flags[2:3].copy_(t[i : i + 1])
+        elif needs_resort:
+            flags[2:3].fill_(1)
         scratch = k.mem.i32(8 * nc + int(k.lib.plx_scratch_ints(nc)))
         c.flags, c.scratch = flags.data_ptr(), scratch.data_ptr()
         c.growable_in, c.dropped_out = _ptr(growable_in), rem.dropped.data_ptr()
         _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
-        got = flags.cpu().tolist()  # the phase's one host read (synchronises the stream)
-        if bool(got[1]) and cfg.on_overflow == "error":
+        if tail_dev is not None:
+            # the new tail (flags[4]) is at most the old bound plus the winners
+            winners_max = nseg * int(cfg.k) if not cfg.step_scope else int(cfg.k)
+            self._tail_hint = (flags, span + max(0, winners_max))
+        out = GrowthOutcome(unflatten(flat, offs), tail_start=tail_start, fired=True, flags=flags)
+        if cfg.on_overflow == "error" and out.overflow:  # (this policy reads the flags here)
             raise RuntimeError("add_conn overflow: selected candidates exceeded the free connection capacity")
-        return GrowthOutcome(unflatten(flat, offs), int(got[0]), bool(got[1]), bool(got[2]),
-                             int(tail_start) + int(got[3]), True)
+        return out
 
     @staticmethod
     def _pair_keys(src: torch.Tensor, dst: torch.Tensor, n: int) -> list[tuple[int, int, torch.Tensor, Any]]:

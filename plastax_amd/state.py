@@ -86,6 +86,9 @@ def column_to_numpy(col: torch.Tensor, spec: FieldSpec) -> np.ndarray:
     return arr
 
 
+_BOOL_FLAGS = frozenset({"needs_resort", "overflow", "unit_overflow"})
+
+
 class NetworkState:
     """Mutable arena state (state.py:83-135).
 
@@ -112,16 +115,14 @@ class NetworkState:
         self._units = dict(units)
         self._conns: tuple[Columns, ...] = tuple(dict(b) for b in conns)
         self.globals_ = globals_
-        self.needs_resort = needs_resort
         self.step = step
-        self.grown = grown
-        self.overflow = overflow
-        self._units_added = units_added
-        self._unit_overflow = unit_overflow
-        # add_unit's (units_added, unit_overflow) while they are still on the
-        # device: read on first access, so a step need not wait for them.
-        self._unit_flags_dev: Any = None
-        self.tail_start = tail_start
+        # The structural flags. A step leaves the ones its phases computed on
+        # the device (_flag_dev: name -> (int32 device tensor, index)); the
+        # first access reads that tensor once, so no step waits for them.
+        self._flag_val: dict[str, Any] = {
+            "needs_resort": needs_resort, "grown": grown, "overflow": overflow, "units_added": units_added,
+            "unit_overflow": unit_overflow, "tail_start": tail_start}
+        self._flag_dev: dict[str, tuple[Any, int]] = {}
         self._arena: Any = None  # plastax_amd._layout.Arena once a step ran
         self._arena_ahead = False  # the arena holds newer conn values
         # The churn layout a growth step replaced: the next layout is merged
@@ -141,19 +142,9 @@ class NetworkState:
     def _donate(self) -> "NetworkState":
         """Hand every buffer to a fresh state object and retire this one."""
         self._check()
-        new = NetworkState(
-            self._units,
-            self._conns,
-            self.globals_,
-            self.needs_resort,
-            self.step,
-            self.grown,
-            self.overflow,
-            self._units_added,
-            self._unit_overflow,
-            self.tail_start,
-        )
-        new._unit_flags_dev = self._unit_flags_dev
+        new = NetworkState(self._units, self._conns, self.globals_, step=self.step)
+        new._flag_val = dict(self._flag_val)
+        new._flag_dev = dict(self._flag_dev)
         new._arena = self._arena
         new._arena_ahead = self._arena_ahead
         new._arena_prev = self._arena_prev
@@ -161,38 +152,57 @@ class NetworkState:
         self._donated = True
         return new
 
-    # -- add_unit's flags ---------------------------------------------------------
-    @property
-    def units_added(self) -> int:
-        self._resolve_unit_flags()
-        return self._units_added
+    # -- structural flags ---------------------------------------------------------
+    def _flag(self, name: str) -> Any:
+        src = self._flag_dev.get(name)
+        if src is not None:
+            self._read_flags(src[0])
+        return self._flag_val[name]
 
-    @units_added.setter
-    def units_added(self, value: int) -> None:
-        self._resolve_unit_flags()
-        self._units_added = value
+    def _set_flag(self, name: str, value: Any) -> None:
+        """A host value (any pending device value of the flag is dropped)."""
+        self._flag_dev.pop(name, None)
+        self._flag_val[name] = value
 
-    @property
-    def unit_overflow(self) -> bool:
-        self._resolve_unit_flags()
-        return self._unit_overflow
-
-    @unit_overflow.setter
-    def unit_overflow(self, value: bool) -> None:
-        self._resolve_unit_flags()
-        self._unit_overflow = value
-
-    def _resolve_unit_flags(self) -> None:
-        flags, self._unit_flags_dev = self._unit_flags_dev, None
-        if flags is not None:
-            got = flags.cpu().tolist()
-            self._units_added, self._unit_overflow = int(got[0]), bool(got[1])
-
-    def _set_unit_flags(self, added: int, overflow: bool, flags_dev: Any = None) -> None:
-        """Both flags at once (no read of a pending pair), or, with
-        ``flags_dev``, the device pair (units_added, unit_overflow) to read
+    def _defer_flag(self, name: str, tensor: Any, index: int) -> None:
+        """The flag is element ``index`` of the int32 device ``tensor``, read
         on first access."""
-        self._units_added, self._unit_overflow, self._unit_flags_dev = added, overflow, flags_dev
+        self._flag_dev[name] = (tensor, int(index))
+
+    def _flag_source(self, name: str) -> Any:
+        """The flag's pending (device tensor, index), or None when its value
+        is on the host."""
+        return self._flag_dev.get(name)
+
+    def _read_flags(self, tensor: Any) -> None:
+        """One read of ``tensor`` resolves every flag pending on it."""
+        vals = tensor.cpu().tolist()
+        for name, (t, i) in list(self._flag_dev.items()):
+            if t is tensor:
+                v = vals[i]
+                self._flag_val[name] = bool(v) if name in _BOOL_FLAGS else int(v)
+                del self._flag_dev[name]
+
+    def _flag_reader(self, name: str) -> Any:
+        """A zero-argument callable giving the flag's value as of now, read
+        from the device only when called (it holds no reference to the
+        state, which a later step may donate)."""
+        src = self._flag_dev.get(name)
+        if src is None:
+            value = self._flag_val[name]
+            return lambda: value
+        t, i = src
+        kind = bool if name in _BOOL_FLAGS else int
+        return lambda: kind(t[i].item())
+
+    needs_resort = property(lambda self: self._flag("needs_resort"),
+                            lambda self, v: self._set_flag("needs_resort", v))
+    grown = property(lambda self: self._flag("grown"), lambda self, v: self._set_flag("grown", v))
+    overflow = property(lambda self: self._flag("overflow"), lambda self, v: self._set_flag("overflow", v))
+    units_added = property(lambda self: self._flag("units_added"), lambda self, v: self._set_flag("units_added", v))
+    unit_overflow = property(lambda self: self._flag("unit_overflow"),
+                             lambda self, v: self._set_flag("unit_overflow", v))
+    tail_start = property(lambda self: self._flag("tail_start"), lambda self, v: self._set_flag("tail_start", v))
 
     def _mark_ahead(self, columns: Any = None) -> None:
         """The step wrote connection values into the arena: ``columns`` (a

@@ -35,16 +35,29 @@ class StepInputs:
     targets: Any = None
 
 
-@dataclasses.dataclass(frozen=True)
 class StepResult:
     """A step's output (step.py:45-67): the new state, the growth overflow
     flag, the loss (a 0-d float32 device tensor) and the dropped growth
-    candidates (None without growth)."""
+    candidates (None without growth). ``overflow`` may be given as a
+    zero-argument callable: it is then read (from the device) on first
+    access, so returning the result waits for nothing."""
 
-    state: NetworkState
-    overflow: Any
-    loss: Any
-    growth_remainder: Any = None
+    __slots__ = ("state", "loss", "growth_remainder", "_overflow")
+
+    def __init__(self, state: NetworkState, overflow: Any, loss: Any, growth_remainder: Any = None) -> None:
+        self.state = state
+        self.loss = loss
+        self.growth_remainder = growth_remainder
+        self._overflow = overflow
+
+    @property
+    def overflow(self) -> Any:
+        if callable(self._overflow):
+            self._overflow = self._overflow()
+        return self._overflow
+
+    def __repr__(self) -> str:
+        return f"StepResult(state={self.state!r}, loss={self.loss!r})"
 
 
 def make_step(
@@ -332,7 +345,7 @@ class StepFn:
             state.globals_ = plan.net.reset_global.reset(state.globals_)
 
         state.step = state.step + 1
-        return StepResult(state=state, overflow=state.overflow, loss=loss, growth_remainder=None)
+        return StepResult(state=state, overflow=state._flag_reader("overflow"), loss=loss, growth_remainder=None)
 
     def _structural(self, state: NetworkState, arena: Arena, units: dict, stream: int, g: Any) -> None:
         """prune_unit and PruneConn on the physical arena (tombstones set in
@@ -374,11 +387,13 @@ class StepFn:
             phase_u = self._add_unit
             if phase_u.fires(int(state.step)):
                 ulog = {name: col.clone() for name, col in state.units.items()}
-                state._set_unit_flags(0, False, phase_u.run_device(k, ulog, g))
+                flags = phase_u.run_device(k, ulog, g)
+                state._defer_flag("units_added", flags, 0)
+                state._defer_flag("unit_overflow", flags, 1)
                 state.units = ulog
                 spawned = True
             else:
-                state._set_unit_flags(0, False)
+                state.units_added, state.unit_overflow = 0, False
 
         def relayout_for_new_units() -> None:
             # New units need rows in the layout: the arena is laid out again
@@ -406,14 +421,23 @@ class StepFn:
             if getattr(prev, "churn", False):
                 # DEAD before the claim: the claimed slots are the ones it turns live
                 before = [bucket[DEAD.name].clone() for bucket in conns]
-            out = phase.run(k, state.units, conns, step=int(state.step), globals_=g,
-                            tail_start=int(state.tail_start), units_added=added)
+            # The flags stay on the device from step to step: the tail start
+            # (PIPELINE) and needs_resort go in as the last claim's device
+            # values, and this claim's flags are read only when the caller
+            # asks (as the reference's Driver reads them after its step).
+            tail_src = state._flag_source("tail_start")
+            tail = tail_src[0][tail_src[1] : tail_src[1] + 1] if tail_src is not None else int(state.tail_start)
+            resort_src = state._flag_source("needs_resort")
+            out = phase.run(k, state.units, conns, step=int(state.step), globals_=g, tail_start=tail,
+                            units_added=added,
+                            needs_resort=resort_src if resort_src is not None else bool(state.needs_resort))
             state.conns = out.conns
             if before is not None:
                 state._arena_prev = (prev, before)  # the next layout merges the claimed slots into prev's
-            state.grown, state.overflow = out.grown, out.overflow
-            state.needs_resort = bool(state.needs_resort) or out.needs_resort
-            state.tail_start = out.tail_start
+            for name, i in (("grown", 0), ("overflow", 1), ("needs_resort", 2)):
+                state._defer_flag(name, out.flags, i)
+            if out.flags.numel() > 4:
+                state._defer_flag("tail_start", out.flags, 4)
 
     # -- generic passes (plastax_amd/generic.py) ---------------------------------
     def _generic_runner(self, which: str, g: Any) -> Any:
