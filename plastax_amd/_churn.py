@@ -197,6 +197,13 @@ class ChurnArena(Arena):
         if prev is not None:
             prev._retire()
 
+    def units_to_physical(self, units: Columns) -> Columns:
+        """Units keep the caller's ids: the same columns."""
+        return dict(units)
+
+    def units_to_logical(self, units: Columns) -> Columns:
+        return dict(units)
+
     @property
     def unit_levels(self) -> np.ndarray:
         """The units' levels on the host, read from the device on first use

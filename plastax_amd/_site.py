@@ -219,6 +219,29 @@ class SiteProgram:
     def uses_role(self, role: str) -> bool:
         return any(op == SOP["idx"] and a == ROLES[role] for op, _, a, _ in self.code)
 
+    def const_output(self, k: int) -> int | None:
+        """The int32 value of output k when the program writes a traced
+        constant there (not a global, not a computed value); else None."""
+        regs: dict[int, int] = {}  # register -> const slot it holds
+        out: int | None = None
+        written = False
+        for op, d, a, _ in self.code:
+            if op == SOP["out"]:
+                if d == k:  # (the last write of the slot wins)
+                    slot = regs.get(a)
+                    written = True
+                    out = None if slot is None or slot in self.globals_at else slot
+                continue
+            if op == SOP["const"]:
+                regs[d] = a
+            elif op == SOP["mov"] and a in regs:
+                regs[d] = regs[a]
+            else:
+                regs.pop(d, None)
+        if not written or out is None:
+            return None
+        return int(np.uint32(self.consts[out]).view(np.int32))
+
 
 def _bits(value: Any, kind: str) -> int:
     if kind == "f":

@@ -417,6 +417,27 @@ class AddConnPhase:
         # (flags of the last PIPELINE claim, a host bound on the tail start
         # it wrote into flags[4])
         self._tail_hint: tuple[torch.Tensor, int] | None = None
+        # (a level column, a bound on its deepest level): read once, then
+        # carried through the add_unit phases that derive new columns
+        self._level_hint: tuple[torch.Tensor, int] | None = None
+
+    def level_bound(self, level: torch.Tensor) -> int:
+        """A bound on the deepest level of ``level``: the carried one when
+        this is the column it was carried to, else one host read."""
+        hint = self._level_hint
+        if hint is not None and hint[0] is level:
+            return hint[1]
+        bound = int(level.max().item()) if level.numel() else 0
+        self._level_hint = (level, bound)
+        return bound
+
+    def carry_level_bound(self, old: torch.Tensor, new: torch.Tensor, bound_after: Any) -> None:
+        """add_unit derived the column ``new`` from ``old``:
+        ``bound_after(b)`` bounds its deepest level given ``old``'s bound b
+        (nothing carried when ``old``'s bound is not known)."""
+        hint = self._level_hint
+        if hint is not None and hint[0] is old:
+            self._level_hint = (new, int(bound_after(hint[1])))
 
     # -- helpers ---------------------------------------------------------------
     def _top_units(self, k: Kernels, masked: torch.Tensor, m: int, n: int) -> torch.Tensor:
@@ -458,9 +479,11 @@ class AddConnPhase:
         pruned = units.get("pruned")
         seed, dev = int(self.static.seed), level.device
         INT_MAX = 0x7FFFFFFF
-        # Levels bound the per-level segments (PIPELINE levels run up to the
-        # unit count): one read of the deepest level sizes them.
-        max_level = int(level.max().item()) if level.numel() else 0
+        # PIPELINE: the levels bound the per-level segments (they run up to
+        # the unit count). A bound on the deepest level sizes them: read once,
+        # then carried (level_bound); a bound above the deepest level only
+        # adds empty segments.
+        max_level = self.level_bound(level) if cfg.pipeline else 0
 
         # 1. candidates
         grid_sq = 0

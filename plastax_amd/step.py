@@ -386,8 +386,11 @@ class StepFn:
                 self._add_unit = unit_phases.AddUnitPhase(plan.net, self.static, g)
             phase_u = self._add_unit
             if phase_u.fires(int(state.step)):
-                ulog = {name: col.clone() for name, col in state.units.items()}
+                before_units = state.units
+                ulog = {name: col.clone() for name, col in before_units.items()}
                 flags = phase_u.run_device(k, ulog, g)
+                if self._grow is not None:
+                    self._grow.carry_level_bound(before_units["level"], ulog["level"], phase_u.level_bound)
                 state._defer_flag("units_added", flags, 0)
                 state._defer_flag("unit_overflow", flags, 1)
                 state.units = ulog

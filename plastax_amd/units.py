@@ -164,6 +164,16 @@ class AddUnitPhase:
         self.names = _reset_names(static)
         self.max_level = int(getattr(net, "max_levels", 1024)) - 1
         self.interval = int(getattr(net, "structural_interval", 1))
+        # the level offset a spawn gives its children, when the policy
+        # returns a traced constant (None: computed per parent)
+        self.offset_const = self.spawn.const_output(1)
+
+    def level_bound(self, bound: int) -> int:
+        """A bound on the deepest level after this phase, given one before:
+        a child's level is clamp(parent + offset, 1, max_level)."""
+        c = self.offset_const
+        child = self.max_level if c is None else min(self.max_level, max(bound + c, 1))
+        return max(bound, child)
 
     def fires(self, step: int) -> bool:
         return self.interval <= 1 or step % self.interval == 0
