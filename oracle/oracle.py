@@ -299,7 +299,10 @@ class OracleNet:
         live = np.flatnonzero(~c["dead"].astype(bool))
         slots = live[np.argsort(c["to_id"][live], kind="stable")].astype(np.int64)
         dst = c["to_id"][slots]
-        starts = np.concatenate([[0], np.flatnonzero(np.diff(dst)) + 1, [slots.size]]).astype(np.int64)
+        if slots.size == 0:  # no live edge: no row
+            starts = np.zeros(1, dtype=np.int64)
+        else:
+            starts = np.concatenate([[0], np.flatnonzero(np.diff(dst)) + 1, [slots.size]]).astype(np.int64)
         units = np.ascontiguousarray(dst[starts[:-1]].astype(np.int32))
         self._fwd_rows[b] = (starts, np.ascontiguousarray(slots), units)
         return self._fwd_rows[b]
@@ -651,12 +654,14 @@ class OracleNet:
             if not hasattr(self, "_pu"):
                 self._pu = _site.trace_prune_unit(net.prune_unit, unit_dtypes, self.globals_)
             self.units, self.conns, _ = og.prune_unit(self._pu, self.static, self.units, self.conns, self.globals_)
+            self._fwd_rows = {}  # (its incident kills: rows hold live slots only)
             self.units = {k: np.ascontiguousarray(v) for k, v in self.units.items()}
             self.conns = [{k: np.ascontiguousarray(v) for k, v in b.items()} for b in self.conns]
         if self.plan.prune_conn:
             if self._prune_prog is None:
                 self._prune_prog = _site.trace_predicate(net.prune_conn, unit_dtypes, conn_dtypes, self.globals_)
             self.conns = og.prune_conn(self._prune_prog, self.units, self.conns, self.globals_)
+            self._fwd_rows = {}  # the parallel forward's rows hold live slots only
         if getattr(self.plan, "add_unit", False):
             interval = int(getattr(net, "structural_interval", 1))
             if interval <= 1 or self.step_count % interval == 0:
