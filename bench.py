@@ -562,6 +562,197 @@ def run_c5(args) -> int:
     return 0
 
 
+C4_METRIC = "steps/sec of C4's dynamic sparse training (C3's sparse MLP at batch 1, prune + regrow every 100 steps)"
+
+
+def build_c4(px):
+    """C4: C3's sparse MLP at batch 1 with tanh units (their gradients stay
+    alive, so regrowth scores are not all zero), softmax cross-entropy,
+    Adam(1e-3); every 100 steps a PruneConn drops the live edges with |w|
+    below the global tau (the driver sets it to the 10th percentile of the
+    live |w|) and a ScoreAddConn regrows up to 1,024 edges per level from a
+    32 x 32 shortlist scored by |act[src] * grad[dst]|."""
+    import plastax_amd.numpy as jnp
+
+    grad = px.FieldSpec.float32("grad_pre_act")
+    lossg = px.FieldSpec.float32("loss_grad")
+
+    class Tanh(px.ForwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, dst, src, c, cid, g):
+            return c[px.WEIGHT, cid] * u[px.ACTIVATION, src]
+
+        def apply(self, u, i, g, acc):
+            return px.UnitWrite.of((px.ACTIVATION, jnp.tanh(acc)))
+
+    class TanhBack(px.BackwardPass):
+        combine = px.monoid.sum_
+
+        def map(self, u, src, dst, c, cid, g):
+            return c[px.WEIGHT, cid] * u[grad, dst]
+
+        def apply(self, u, i, g, acc):
+            a = u[px.ACTIVATION, i]
+            return px.UnitWrite.of((grad, (acc + u[lossg, i]) * (jnp.float32(1.0) - a * a)))
+
+    class MagnitudePrune(px.PruneConn):
+        def predicate(self, u, c, cid, g):
+            return jnp.abs(c[px.WEIGHT, cid]) < g["tau"]
+
+    class GradGrow(px.ScoreAddConn):
+        candidates = "shortlist_per_level"
+        shortlist_size = 32
+        direction = "deeper"
+        max_level_gap = 1
+        dedupe_live = True
+        max_new_per_level = 1024
+        trigger = ("every", 100)
+
+        def score(self, u, src, dst, g):
+            return jnp.abs(u[px.ACTIVATION, src] * u[grad, dst])
+
+        def importance(self, u, i, g):
+            return jnp.abs(u[grad, i]) + jnp.abs(u[px.ACTIVATION, i])
+
+        def init(self, u, src, dst, g):
+            return px.ConnWrite.of((px.WEIGHT, jnp.float32(0.0)))
+
+    opt = px.optim.adam(1e-3, grad)
+
+    class C4Net(px.Network):
+        forward_pass = Tanh()
+        backward_pass = TanhBack()
+        loss = px.SoftmaxCrossEntropyLoss(lossg)
+        update_conn = opt.update_conn()
+        prune_conn = MagnitudePrune()
+        add_conn = GradGrow()
+        extra_unit_fields = (grad, lossg)
+        extra_conn_fields = tuple(opt.state_fields)
+
+    return C4Net
+
+
+def run_c4(args) -> int:
+    """C4 end to end: all 5,000 batch-1 steps (--c4-steps) from the built
+    state, a prune + regrow event every 100 steps (steps 1, 101, ...). The
+    driver sets tau, the 10th percentile of the live |w|, before each event
+    step (one host read per 100 steps, outside the step). The first two
+    steps (an event step and a plain one) run again from the same state
+    against the oracle: flags, loss and every unit and connection column,
+    bit for bit; their oracle time is the CPU leg."""
+    import torch
+
+    import plastax_amd as px
+    from plastax_amd import synth
+    from plastax_amd.state import column_to_numpy
+
+    t_setup = time.perf_counter()
+    net = build_c4(px)
+    e = synth.c3_mlp(args.seed)
+    static, state = px.NetworkBuilder.from_edges(
+        net, e.num_units, e.src, e.dst, weights=e.weight, input_ids=e.input_ids, output_ids=e.output_ids,
+        globals_={"tau": np.float32(0.0)}, capacity_headroom=0.1, device="cpu")
+    uspecs = {s.name: s for s in static.unit_fields}
+    cspecs = {s.name: s for s in static.conn_fields}
+    host_units = {k: column_to_numpy(v, uspecs[k]).copy() for k, v in state.units.items()}
+    host_conns = [{k: column_to_numpy(v, cspecs[k]).copy() for k, v in b.items()} for b in state.conns]
+    dev = torch.device("cuda", 0)
+
+    def fresh():
+        return px.NetworkState({k: v.to(dev) for k, v in state.units.items()},
+                               tuple({k: v.to(dev) for k, v in b.items()} for b in state.conns),
+                               {"tau": np.float32(0.0)})
+
+    def live_tau(st) -> np.float32:
+        w = torch.cat([b["weight"][b["dead"] == 0].abs() for b in st.conns])
+        return np.float32(torch.quantile(w, 0.1).item())
+
+    nsteps = args.c4_steps
+    xs, ys = synth.c3_batches(args.seed + 1, nsteps, 1)
+    xs_d, ys_d = torch.from_numpy(xs[:, 0]).contiguous().to(dev), torch.from_numpy(ys[:, 0]).contiguous().to(dev)
+    step = px.make_step(net, static)
+    gstate = fresh()
+    step.arena(gstate)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    progress(f"C4: {e.src.size} edges, {nsteps} steps ({setup_s:.1f} s)")
+    readers = []
+    t0 = time.perf_counter()
+    for k in range(nsteps):
+        if k % 100 == 0:
+            gstate.globals_ = {"tau": live_tau(gstate)}
+        elif k % 100 == 1:
+            gstate.globals_ = {"tau": np.float32(0.0)}
+        gstate = step(gstate, px.StepInputs(xs_d[k], ys_d[k])).state
+        readers.append(gstate._flag_reader("grown"))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    grown = sum(int(r()) for r in readers)
+    live = int(sum(int((b["dead"] == 0).sum().item()) for b in gstate.conns))
+    progress(f"C4: {nsteps} steps in {elapsed:.2f} s, {grown} edges regrown, {live} live at the end")
+    cpu = parity = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ox
+        from plastax_amd._plan import compile_plan
+
+        ox.load()
+        o = ox.OracleNet(static, host_units, host_conns, compile_plan(net, static), {"tau": np.float32(0.0)})
+        o.tail_start, o.needs_resort = int(state.tail_start), bool(state.needs_resort)
+        pstate = fresh()
+        pstep = px.make_step(net, static)
+        times, same = [], True
+        for k in range(2):
+            tau = live_tau(pstate) if k == 0 else np.float32(0.0)
+            pstate.globals_ = {"tau": tau}
+            o.globals_ = {"tau": tau}
+            res = pstep(pstate, px.StepInputs(xs_d[k], ys_d[k]))
+            pstate = res.state
+            t1 = time.perf_counter()
+            lo = o.step(xs[k, 0], ys[k, 0])
+            times.append(time.perf_counter() - t1)
+            got = (int(pstate.grown), bool(pstate.overflow), bool(pstate.needs_resort), int(pstate.tail_start))
+            same &= got == (o.grown, o.overflow, o.needs_resort, o.tail_start)
+            same &= bool(np.float32(float(res.loss)).view(np.uint32) == np.float32(lo).view(np.uint32))
+        units_ok = all(np.array_equal(column_to_numpy(pstate.units[n], uspecs[n]).view(np.uint8),
+                                      o.units[n].view(np.uint8)) for n in uspecs)
+        conns_ok = all(np.array_equal(column_to_numpy(b[n], cspecs[n]).view(np.uint8), o.conns[i][n].view(np.uint8))
+                       for i, b in enumerate(pstate.conns) for n in cspecs)
+        parity = {"steps": 2, "event_step_included": True, "flags_and_loss_equal": bool(same),
+                  "units_bit_exact": bool(units_ok), "conns_bit_exact": bool(conns_ok)}
+        progress(f"C4 parity over 2 steps: flags and loss {same}, units {units_ok}, conns {conns_ok}")
+        sec = float(sum(times)) / 2
+        cpu = {"value": 1.0 / sec, "unit": "steps/s", "cores": 1, "kind": "port",
+               "sample": f"the first 2 steps of the same workload (a prune + regrow step and a plain one), "
+                         f"{sec:.2f} s per step on average, the C oracle and oracle/growth.py, one thread"}
+    ms = elapsed * 1e3 / nsteps
+    line = {
+        "metric": C4_METRIC,
+        "value": round(1e3 / ms, 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": nsteps,
+        "warmup": 0,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C4: C3's 784-4096-4096-10 sparse MLP (10 % keep) at batch 1, tanh, softmax CE, "
+                               "Adam(1e-3); every 100 steps PruneConn |w| < 10th percentile and ScoreAddConn "
+                               "(32 x 32 shortlist per level, up to 1,024 new per level)",
+                   "edges_start": int(e.src.size), "live_edges_end": live, "regrown_total": grown,
+                   "events": (nsteps + 99) // 100},
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "full_size_parity": parity,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 C3_METRIC = "samples/sec per batched step (fwd+bwd+update, B=256) of C3's 784-4096-4096-10 sparse MLP"
 
 
@@ -1020,7 +1211,7 @@ def run_c3(args) -> int:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=("c1", "c2", "c2_prune", "c3", "c5", "c5_growth"), default="c2",
+    ap.add_argument("--workload", choices=("c1", "c2", "c2_prune", "c3", "c4", "c5", "c5_growth"), default="c2",
                     help="c1: the small streaming PIPELINE net run by Driver.scan (graph vs step by step); "
                     "c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
                     "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
@@ -1032,6 +1223,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--chunk", type=int, default=100, help="c1: steps per Driver.scan chunk")
+    ap.add_argument("--c4-steps", type=int, default=5000, help="c4: steps of the run (events every 100)")
     ap.add_argument("--relayout", choices=("merge", "full"), default="merge",
                     help="c5: the churn layout after a growth step: merged from the previous one, or built again")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -1056,6 +1248,8 @@ def main() -> int:
         return run_c2_prune(args)
     if args.workload == "c3":
         return run_c3(args)
+    if args.workload == "c4":
+        return run_c4(args)
     if args.workload == "c5":
         return run_c5(args)
 
