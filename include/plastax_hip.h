@@ -925,8 +925,10 @@ PLX_EXPORT int plx_relax_levels(int64_t n_units, int64_t n_edges, const int32_t*
                                 void* stream);
 
 /* CSR offsets from ascending row ids: start[u] = the number of keys[0, n)
- * below u, for u in [0, nlevels] (keys in [0, nlevels)). */
-PLX_EXPORT int plx_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start, void* stream);
+ * below u, for u in [0, nlevels] (keys in [0, nlevels)); n_dev (optional)
+ * holds the key count (at most n) on the device. */
+PLX_EXPORT int plx_sorted_starts(int64_t n, const int32_t* n_dev, const int32_t* keys, int32_t nlevels, int32_t* start,
+                                 void* stream);
 
 /* Resort keys: key[p] = dead[p] ? sentinel : (pipeline ? 0 : level[from[p]]). */
 PLX_EXPORT int plx_resort_keys(int64_t n, const int32_t* from_id, const uint8_t* dead, const int32_t* level,
@@ -1025,6 +1027,7 @@ typedef struct plx_merge_side {
   const int32_t* key1;
   const int32_t* key2;
   int32_t* map;
+  const int32_t* n_dev; /* optional: the element count (at most n) on the device */
 } plx_merge_side;
 
 /* Merges a and b (a first where keys are equal): order[r] (optional,
@@ -1043,13 +1046,15 @@ PLX_EXPORT int plx_merge_index(const plx_merge_desc* d, void* stream);
 
 /* out[r] = a[order[r]] where order[r] >= 0, else b[b_ids[j]] (b null: the
  * id b_ids[j] itself) for j = -1 - order[r], r < n; elements of `bytes`
- * (1 or 4) bytes; a has a_limit entries, b b_limit, b_ids nb. */
+ * (1 or 4) bytes; a has a_limit entries, b b_limit, b_ids nb. With n_dev
+ * (optional) only the first *n_dev ranks are gathered (at most n) and ranks
+ * [*n_dev, n) get each column's `fill` bits. */
 typedef struct plx_merge_col {
   const void* a;
   const void* b;
   void* out;
   int32_t bytes;
-  int32_t reserved;
+  uint32_t fill;
 } plx_merge_col;
 
 #define PLX_MERGE_MAX_COLS 12
@@ -1064,6 +1069,7 @@ typedef struct plx_merge_gather_desc {
   int32_t ncols;
   int32_t reserved;
   plx_merge_col cols[PLX_MERGE_MAX_COLS];
+  const int32_t* n_dev;
 } plx_merge_gather_desc;
 
 PLX_EXPORT int plx_merge_gather(const plx_merge_gather_desc* d, void* stream);

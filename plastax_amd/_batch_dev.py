@@ -69,7 +69,7 @@ def batch_sources_dev(arena: Any, b: int) -> Any:
     nrows = int(nrows_d.item())  # sizes the backward's launches
     start = torch.zeros(n + 1, dtype=torch.int32, device=dev)
     if live:
-        _lib.check(k.lib.plx_sorted_starts(live, src_sorted.data_ptr(), n, start.data_ptr(), k.s),
+        _lib.check(k.lib.plx_sorted_starts(live, None, src_sorted.data_ptr(), n, start.data_ptr(), k.s),
                    "plx_sorted_starts")
     ptr = torch.empty(nrows + 1, dtype=torch.int32, device=dev)
     ptr[:nrows] = start[rows[:nrows].long()]

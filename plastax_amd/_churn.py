@@ -33,6 +33,8 @@ keep the fill values with a write of only the range that stopped being live.
 
 from __future__ import annotations
 
+from typing import Any
+
 import numpy as np
 import torch
 
@@ -66,7 +68,7 @@ class ChurnArena(Arena):
 
     def __init__(self, static: NetworkStatic, units: Columns, conns: tuple[Columns, ...],
                  device: torch.device, stream: int, prev: "ChurnArena | None" = None,
-                 dead_before: list[torch.Tensor] | None = None) -> None:
+                 dead_before: list[torch.Tensor] | None = None, claim_bound: int | None = None) -> None:
         from plastax_amd.grow import Kernels
 
         self.static = static
@@ -132,7 +134,13 @@ class ChurnArena(Arena):
         self.merged = prev is not None
         # Columns written since the logical view was last in step (None: any).
         self._written: set | None = set()
+        # Per bucket: lives[b], a host bound on its live count that sizes
+        # the launches (the count itself after a full build), and
+        # live_dev[b], the count on the device (int32[1]). Positions
+        # [live, lives[b]) hold fill values (DEAD 1), so the step reads DEAD
+        # in the rows of a merged arena.
         self.lives = []
+        self.live_dev: list[torch.Tensor] = []
         self.fwd = []
         self.bwd = []
         self.lists: list[SourceLists] = []
@@ -148,7 +156,7 @@ class ChurnArena(Arena):
         for b, bucket in enumerate(conns):
             if prev is not None:
                 self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b],
-                                   None if dead_before is None else dead_before[b])
+                                   None if dead_before is None else dead_before[b], claim_bound)
                 continue
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
@@ -156,6 +164,7 @@ class ChurnArena(Arena):
             dead_list, _ = k.compact(cap, 0, dead)  # PLX_FLAG_U8: dead slots, ascending
             live = int(nlive.item())
             self.lives.append(live)
+            self.live_dev.append(nlive)
             # Live slots by (destination, slot): a stable sort of the ascending
             # list. Only the live part moves: the step never writes a slot that
             # is dead at layout time, so the dead part keeps fill values and
@@ -171,8 +180,8 @@ class ChurnArena(Arena):
             self.slot[base + live : base + cap] = dead_list[: cap - live]
             # Forward rows: every unit; row u owns its in-edges' run.
             fptr = torch.empty(n + 1, dtype=torch.int32, device=device)
-            _lib.check(k.lib.plx_sorted_starts(live, self.cols[TO_ID.name][base:].data_ptr(), n, fptr.data_ptr(),
-                                               k.s), "plx_sorted_starts")
+            _lib.check(k.lib.plx_sorted_starts(live, None, self.cols[TO_ID.name][base:].data_ptr(), n,
+                                               fptr.data_ptr(), k.s), "plx_sorted_starts")
             self.fwd.append(ForwardRows(n, rows, fptr + base))
             # Backward lists: live slots by (source, slot) -> their positions.
             sl = live_list[: max(live, 1)].clone()
@@ -189,11 +198,14 @@ class ChurnArena(Arena):
             _lib.check(k.lib.plx_gather_i32(live, None, sl.data_ptr(), bucket[FROM_ID.name].data_ptr(),
                                             lsrc.data_ptr(), k.s), "plx_gather_i32")
             lptr = torch.empty(n + 1, dtype=torch.int32, device=device)
-            _lib.check(k.lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
+            _lib.check(k.lib.plx_sorted_starts(live, None, lsrc.data_ptr(), n, lptr.data_ptr(), k.s),
+                       "plx_sorted_starts")
             self.lists.append(SourceLists(lptr, pos, ldst, lsrc, sl))
         self._extent = list(self.lives)
         self.top = None
         self.levels_dev = levels
+        if self.merged:
+            self.dead_in_rows = True  # the fill positions up to each bound are dead
         if prev is not None:
             prev._retire()
 
@@ -228,85 +240,101 @@ class ChurnArena(Arena):
         self._spare = None
 
     def _merge_bucket(self, k, b: int, prev: "ChurnArena", bucket: Columns, specs: dict, nbits: int,
-                      rows: torch.Tensor, extent: int, dead_before: torch.Tensor) -> None:
+                      rows: torch.Tensor, extent: int, dead_before: torch.Tensor, claim_bound: int | None) -> None:
         """Bucket b laid out from ``prev``'s layout of it (see the module
         docstring): the survivors (prev's live positions whose DEAD is still
         0) merged with the slots the claim turned live (``dead_before``: DEAD
         just before the claim, after the step's prunes were copied back).
         Nothing else changes the logical bucket in between, so these are all
-        of its live slots."""
+        of its live slots.
+
+        The counts stay on the device. The launches are sized by host bounds:
+        prev's bound on its live count and ``claim_bound``, a bound on the
+        claimed slots (the growth's winner budget; the bucket's capacity
+        when not given). Ranks past the live count get fill values (slot -1),
+        so every array up to the bound is defined."""
         dev = self.device
         n = self.static.num_units
         base, cap = self.bases[b], self.caps[b]
-        old_live = prev.lives[b]
+        old_bound, old_live_d = prev.lives[b], prev.live_dev[b]
+        new_bound = cap if claim_bound is None else max(0, min(cap, int(claim_bound)))
+        bound = min(cap, old_bound + new_bound)
         lib = k.lib
-        if prev.t_name and prev.t_now and prev.t_now[b] is not None and old_live:
+        if prev.t_name and prev.t_now and prev.t_now[b] is not None and old_bound:
             # Adam's count is one number for prev's live edges (its column
             # was not kept for them): materialise it for the survivors.
-            t_col = prev.cols[prev.t_name][base : base + old_live]
-            t_col.masked_fill_(prev.cols[DEAD.name][base : base + old_live] == 0, float(prev.t_now[b]))
+            t_col = prev.cols[prev.t_name][base : base + old_bound]
+            t_col.masked_fill_(prev.cols[DEAD.name][base : base + old_bound] == 0, float(prev.t_now[b]))
         # Survivors: prev's live positions still live, in (destination, slot) order.
-        surv, nsurv_d = k.compact(old_live, 1, prev.cols[DEAD.name][base:])  # PLX_FLAG_U8_ZERO
+        surv, nsurv_d = k.compact(old_bound, 1, prev.cols[DEAD.name][base:], n_dev=old_live_d)  # PLX_FLAG_U8_ZERO
         # New: the slots the claim filled (a slot that died this step may be
         # among them: its old position is not a survivor).
         claimed = (dead_before != 0) & (bucket[DEAD.name] == 0)
         fresh, nnew_d = k.compact(cap, 0, claimed)  # PLX_FLAG_U8: ascending slots
-        counts = torch.cat([nsurv_d, nnew_d]).cpu().tolist()  # the rebuild's host read (as the full build's)
-        nsurv, nnew = int(counts[0]), int(counts[1])
-        live = nsurv + nnew
-        self.lives.append(live)
-        by_dst = fresh[:max(nnew, 1)].clone()
-        by_src = fresh[:max(nnew, 1)].clone()
-        k.sort(by_dst, nnew, [(0, nbits, bucket[TO_ID.name], None)], tag="relayout")
-        k.sort(by_src, nnew, [(0, nbits, bucket[FROM_ID.name], None)], tag="relayout")
+        live_d = nsurv_d + nnew_d
+        self.lives.append(bound)
+        self.live_dev.append(live_d)
+        by_dst = fresh[: max(new_bound, 1)].clone()
+        by_src = fresh[: max(new_bound, 1)].clone()
+        k.sort(by_dst, new_bound, [(0, nbits, bucket[TO_ID.name], None)], n_dev=nnew_d, tag="relayout")
+        k.sort(by_src, new_bound, [(0, nbits, bucket[FROM_ID.name], None)], n_dev=nnew_d, tag="relayout")
         # Positions: merge by (TO_ID, slot); maps old position / new slot -> new position.
-        order = torch.empty(max(live, 1), dtype=torch.int32, device=dev)
-        old_to_new = torch.full((max(old_live, 1),), -1, dtype=torch.int32, device=dev)
+        order = torch.empty(max(bound, 1), dtype=torch.int32, device=dev)
+        old_to_new = torch.full((max(old_bound, 1),), -1, dtype=torch.int32, device=dev)
         new_pos = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
         m = _lib.plx_merge_desc()
-        _side(m.a, nsurv, old_live, surv, prev.cols[TO_ID.name][base:], prev.slot[base:], old_to_new)
-        _side(m.b, nnew, cap, by_dst, bucket[TO_ID.name], None, new_pos)
+        _side(m.a, old_bound, old_bound, surv, prev.cols[TO_ID.name][base:], prev.slot[base:], old_to_new, nsurv_d)
+        _side(m.b, new_bound, cap, by_dst, bucket[TO_ID.name], None, new_pos, nnew_d)
         m.offset, m.order = base, order.data_ptr()
         _lib.check(lib.plx_merge_index(m, k.s), "plx_merge_index")
-        cols = [(prev.cols[name][base:], bucket[name], self.cols[name][base:], bucket[name].element_size())
-                for name in specs]
-        cols.append((prev.slot[base:], None, self.slot[base:], 4))
-        _gather(lib, k.s, live, order, by_dst, nnew, old_live, cap, cols)
-        # Past the live range: dead slots in slot order; the columns' fill values.
-        dead_list, _ = k.compact(cap, 0, bucket[DEAD.name])  # PLX_FLAG_U8: dead slots, ascending
-        self.slot[base + live : base + cap] = dead_list[: cap - live]
-        if extent > live:
+        cols = [(prev.cols[name][base:], bucket[name], self.cols[name][base:], bucket[name].element_size(),
+                 _fill_bits(self._fills[name], bucket[name])) for name in specs]
+        cols.append((prev.slot[base:], None, self.slot[base:], 4, _fill_bits(-1, self.slot)))
+        _gather(lib, k.s, bound, order, by_dst, new_bound, old_bound, cap, cols, n_dev=live_d)
+        # Past the bound: the columns' fill values where the other buffer had more.
+        if extent > bound:
             for name, col in self.cols.items():
-                col[base + live : base + extent].fill_(self._fills[name])
+                col[base + bound : base + extent].fill_(self._fills[name])
+            self.slot[base + bound : base + extent].fill_(-1)
         # Forward rows: every unit; row u owns its in-edges' run.
         fptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
-        _lib.check(lib.plx_sorted_starts(live, self.cols[TO_ID.name][base:].data_ptr(), n, fptr.data_ptr(), k.s),
-                   "plx_sorted_starts")
+        _lib.check(lib.plx_sorted_starts(bound, live_d.data_ptr(), self.cols[TO_ID.name][base:].data_ptr(), n,
+                                         fptr.data_ptr(), k.s), "plx_sorted_starts")
         self.fwd.append(ForwardRows(n, rows, fptr + base))
         # Backward lists: the surviving entries (their positions remapped)
-        # merged with the new slots by (FROM_ID, slot).
+        # merged with the new slots by (FROM_ID, slot). Entries of prev's
+        # lists past its live count hold position base; the compaction counts
+        # only the first old_live_d entries.
         old = prev.lists[b]
-        moved = torch.empty(max(old_live, 1), dtype=torch.int32, device=dev)
-        keep = torch.empty(max(old_live, 1), dtype=torch.uint8, device=dev)
-        _lib.check(lib.plx_remap_i32(old_live, old.pos.data_ptr(), base, old_live, old_to_new.data_ptr(),
+        moved = torch.empty(max(old_bound, 1), dtype=torch.int32, device=dev)
+        keep = torch.empty(max(old_bound, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.plx_remap_i32(old_bound, old.pos.data_ptr(), base, old_bound, old_to_new.data_ptr(),
                                      moved.data_ptr(), keep.data_ptr(), k.s), "plx_remap_i32")
-        lsurv, _ = k.compact(old_live, 0, keep)  # PLX_FLAG_U8: surviving entries, in list order
-        lorder = torch.empty(max(live, 1), dtype=torch.int32, device=dev)
+        lsurv, nlsurv_d = k.compact(old_bound, 0, keep, n_dev=old_live_d)  # PLX_FLAG_U8: surviving entries
+        lorder = torch.empty(max(bound, 1), dtype=torch.int32, device=dev)
         m2 = _lib.plx_merge_desc()
-        _side(m2.a, nsurv, old_live, lsurv, old.src, old.slot, None)
-        _side(m2.b, nnew, cap, by_src, bucket[FROM_ID.name], None, None)
+        _side(m2.a, old_bound, old_bound, lsurv, old.src, old.slot, None, nlsurv_d)
+        _side(m2.b, new_bound, cap, by_src, bucket[FROM_ID.name], None, None, nnew_d)
         m2.offset, m2.order = 0, lorder.data_ptr()
         _lib.check(lib.plx_merge_index(m2, k.s), "plx_merge_index")
-        pos = torch.full((live + 1,), base, dtype=torch.int32, device=dev)
-        ldst = torch.zeros(live + 1, dtype=torch.int32, device=dev)
-        lsrc = torch.zeros(max(live, 1), dtype=torch.int32, device=dev)
-        lslot = torch.zeros(max(live, 1), dtype=torch.int32, device=dev)
-        _gather(lib, k.s, live, lorder, by_src, nnew, old_live, cap,
-                [(moved, new_pos, pos, 4), (old.dst, bucket[TO_ID.name], ldst, 4),
-                 (old.src, bucket[FROM_ID.name], lsrc, 4), (old.slot, None, lslot, 4)])
+        pos = torch.full((bound + 1,), base, dtype=torch.int32, device=dev)
+        ldst = torch.zeros(bound + 1, dtype=torch.int32, device=dev)
+        lsrc = torch.zeros(max(bound, 1), dtype=torch.int32, device=dev)
+        lslot = torch.zeros(max(bound, 1), dtype=torch.int32, device=dev)
+        _gather(lib, k.s, bound, lorder, by_src, new_bound, old_bound, cap,
+                [(moved, new_pos, pos, 4, base), (old.dst, bucket[TO_ID.name], ldst, 4, 0),
+                 (old.src, bucket[FROM_ID.name], lsrc, 4, 0), (old.slot, None, lslot, 4, 0)], n_dev=live_d)
+        # (pos past the count keeps base: a valid position for the per-step
+        # gather of the list's weights, which runs over the whole bound)
         lptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
-        _lib.check(lib.plx_sorted_starts(live, lsrc.data_ptr(), n, lptr.data_ptr(), k.s), "plx_sorted_starts")
+        _lib.check(lib.plx_sorted_starts(bound, live_d.data_ptr(), lsrc.data_ptr(), n, lptr.data_ptr(), k.s),
+                   "plx_sorted_starts")
         self.lists.append(SourceLists(lptr, pos, ldst, lsrc, lslot))
+
+    def live_counts(self) -> list[int]:
+        """Each bucket's live count (a host read; the step itself never
+        needs it)."""
+        return [int(t.item()) for t in self.live_dev]
 
     def _write_kills(self, conns: tuple[Columns, ...], written: set) -> None:
         """Only prunes wrote since the logical view was in step: DEAD went
@@ -320,7 +348,8 @@ class ChurnArena(Arena):
             base, live, cap = self.bases[b], self.lives[b], self.caps[b]
             if live == 0:
                 continue
-            killed, nk = k.compact(live, 0, self.cols[DEAD.name][base:])  # PLX_FLAG_U8: positions now dead
+            # positions now dead among the live count's (past it: fill values)
+            killed, nk = k.compact(live, 0, self.cols[DEAD.name][base:], n_dev=self.live_dev[b])  # PLX_FLAG_U8
             for name in written:
                 if name not in bucket:
                     continue
@@ -348,9 +377,15 @@ class ChurnArena(Arena):
         if written is not None and written <= {DEAD.name, self.t_name}:
             self._write_kills(conns, written)
             return
+        from plastax_amd.grow import Kernels
+
+        k = Kernels(self.device, int(torch.cuda.current_stream(self.device).cuda_stream))
         for b, bucket in enumerate(conns):
-            base, live = self.bases[b], self.lives[b]
-            idx = self.slot[base : base + live].long()
+            base, live, cap = self.bases[b], self.lives[b], self.caps[b]
+            if live == 0:
+                continue
+            # positions [0, live count) to their logical slots (the count on the device)
+            every = k.iota(live)
             for name, col in bucket.items():
                 if written is not None and name not in written:
                     continue
@@ -360,21 +395,36 @@ class ChurnArena(Arena):
                     # since the layout keeps the count stamped at its kill.
                     vals = torch.where(self.cols[DEAD.name][base : base + live] != 0, vals,
                                        torch.tensor(self.t_now[b], dtype=vals.dtype, device=vals.device))
-                col[idx] = vals
+                vals = vals.contiguous()
+                _lib.check(k.lib.plx_copy_to_slots(live, self.live_dev[b].data_ptr(), every.data_ptr(),
+                                                   self.slot[base:].data_ptr(), vals.data_ptr(), col.data_ptr(), cap,
+                                                   col.element_size(), k.s), "plx_copy_to_slots")
 
 
 def _side(side, n: int, limit: int, ids: torch.Tensor, key1: torch.Tensor, key2: torch.Tensor | None,
-          out_map: torch.Tensor | None) -> None:
+          out_map: torch.Tensor | None, n_dev: torch.Tensor | None = None) -> None:
     side.n, side.id_limit = int(n), int(limit)
     side.ids, side.key1 = ids.data_ptr(), key1.data_ptr()
     side.key2 = None if key2 is None else key2.data_ptr()
     side.map = None if out_map is None else out_map.data_ptr()
+    side.n_dev = None if n_dev is None else n_dev.data_ptr()
+
+
+def _fill_bits(value: Any, like: torch.Tensor) -> int:
+    """The bits of ``value`` in the element type of ``like`` (what
+    plx_merge_col.fill holds)."""
+    if like.dtype == torch.float32:
+        return int(np.float32(value).view(np.uint32))
+    if like.element_size() == 1:
+        return int(bool(value)) if like.dtype == torch.bool else int(np.asarray(value).astype(np.int64)) & 0xFF
+    return int(np.asarray(value).astype(np.int64)) & 0xFFFFFFFF
 
 
 def _gather(lib, stream: int, n: int, order: torch.Tensor, b_ids: torch.Tensor, nb: int, a_limit: int,
-            b_limit: int, cols: list[tuple]) -> None:
+            b_limit: int, cols: list[tuple], n_dev: torch.Tensor | None = None) -> None:
     """out[r] = a[order[r]] or b[b_ids[j]] per column (plx_merge_gather), in
-    launches of at most PLX_MERGE_MAX_COLS columns."""
+    launches of at most PLX_MERGE_MAX_COLS columns; with ``n_dev`` the ranks
+    past the device count get each column's fill value (its fifth entry)."""
     if n == 0:
         return
     step = _lib.PLX_MERGE_MAX_COLS
@@ -382,11 +432,13 @@ def _gather(lib, stream: int, n: int, order: torch.Tensor, b_ids: torch.Tensor, 
         g = _lib.plx_merge_gather_desc()
         g.n, g.order, g.b_ids, g.nb = int(n), order.data_ptr(), b_ids.data_ptr(), int(nb)
         g.a_limit, g.b_limit = max(int(a_limit), 1), max(int(b_limit), 1)
+        g.n_dev = None if n_dev is None else n_dev.data_ptr()
         part = cols[c0 : c0 + step]
         g.ncols = len(part)
-        for j, (a, b, out, nbytes) in enumerate(part):
+        for j, (a, b, out, nbytes, fill) in enumerate(part):
             g.cols[j].a = a.data_ptr()
             g.cols[j].b = None if b is None else b.data_ptr()
             g.cols[j].out = out.data_ptr()
             g.cols[j].bytes = int(nbytes)
+            g.cols[j].fill = int(fill)
         _lib.check(lib.plx_merge_gather(g, stream), "plx_merge_gather")

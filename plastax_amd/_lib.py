@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 24  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 25  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -305,6 +305,7 @@ class plx_merge_side(ctypes.Structure):
         ("key1", c_vp),
         ("key2", c_vp),
         ("map", c_vp),
+        ("n_dev", c_vp),
     ]
 
 
@@ -326,7 +327,7 @@ class plx_merge_col(ctypes.Structure):
         ("b", c_vp),
         ("out", c_vp),
         ("bytes", c_i32),
-        ("reserved", c_i32),
+        ("fill", ctypes.c_uint32),
     ]
 
 
@@ -341,6 +342,7 @@ class plx_merge_gather_desc(ctypes.Structure):
         ("ncols", c_i32),
         ("reserved", c_i32),
         ("cols", plx_merge_col * PLX_MERGE_MAX_COLS),
+        ("n_dev", c_vp),
     ]
 
 
@@ -523,7 +525,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_relax_levels": (c_i32, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "plx_resort_keys": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp]),
     "plx_gather_col": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp]),
-    "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_i32, c_vp, c_vp]),
+    "plx_sorted_starts": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "plx_unit_write": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "plx_unit_prune": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "plx_tile_build": (c_i32, [ctypes.POINTER(plx_tile_build_desc), c_vp]),

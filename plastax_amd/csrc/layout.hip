@@ -247,10 +247,18 @@ __device__ __forceinline__ uint64_t merge_key(const plx_merge_side& s, int64_t i
   return (static_cast<uint64_t>(k1) << 32) | k2;
 }
 
-// The number of elements of `s` whose key is below `key` (or_equal: at most
-// `key`): a binary search over the side's sorted ids.
-__device__ __forceinline__ int64_t merge_count(const plx_merge_side& s, uint64_t key, bool or_equal) {
-  int64_t lo = 0, hi = s.n;
+// A side's element count: n, or *n_dev (at most n) when the count is on the
+// device.
+__device__ __forceinline__ int64_t side_count(const plx_merge_side& s) {
+  if (!s.n_dev) return s.n;
+  const int64_t c = *s.n_dev;
+  return c < 0 ? 0 : (c < s.n ? c : s.n);
+}
+
+// The number of the first n elements of `s` whose key is below `key`
+// (or_equal: at most `key`): a binary search over the side's sorted ids.
+__device__ __forceinline__ int64_t merge_count(const plx_merge_side& s, int64_t n, uint64_t key, bool or_equal) {
+  int64_t lo = 0, hi = n;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
     const uint64_t k = merge_key(s, s.ids[mid]);
@@ -292,23 +300,25 @@ constexpr int kMergePer = 4;  // elements per thread: their loads are in flight 
 __global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
   __shared__ uint64_t bkey[kMergeStaged];
   __shared__ int64_t cnt[kMergeBlock * kMergePer];
+  const int64_t na = side_count(d.a), nb = side_count(d.b);
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kMergeBlock * kMergePer;
-  if (d.a.n == 0) {  // uniform over the grid
+  if (na == 0) {  // uniform over the grid
     for (int k = 0; k < kMergePer; ++k) {
       const int64_t t = first + k * kMergeBlock + threadIdx.x;
-      if (t < d.b.n) merge_put(d, d.b, t, static_cast<int32_t>(-1 - t), d.b.ids[t]);
+      if (t < nb) merge_put(d, d.b, t, static_cast<int32_t>(-1 - t), d.b.ids[t]);
     }
     return;
   }
-  const bool staged = d.b.n <= kMergeStaged;
+  if (first >= na) return;  // uniform over the workgroup: the grid is sized for the sides' maxima
+  const bool staged = nb <= kMergeStaged;
   if (staged)
-    for (int64_t j = threadIdx.x; j < d.b.n; j += kMergeBlock) bkey[j] = merge_key(d.b, d.b.ids[j]);
+    for (int64_t j = threadIdx.x; j < nb; j += kMergeBlock) bkey[j] = merge_key(d.b, d.b.ids[j]);
   int64_t id[kMergePer];
   uint64_t key[kMergePer];
 #pragma unroll
   for (int k = 0; k < kMergePer; ++k) {
     const int64_t t = first + k * kMergeBlock + threadIdx.x;
-    id[k] = t < d.a.n ? d.a.ids[t] : 0;
+    id[k] = t < na ? d.a.ids[t] : 0;
   }
 #pragma unroll
   for (int k = 0; k < kMergePer; ++k) key[k] = merge_key(d.a, id[k]);
@@ -316,7 +326,7 @@ __global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
   int64_t c[kMergePer];
 #pragma unroll
   for (int k = 0; k < kMergePer; ++k) {
-    c[k] = staged ? lds_count(bkey, d.b.n, key[k]) : merge_count(d.b, key[k], false);
+    c[k] = staged ? lds_count(bkey, nb, key[k]) : merge_count(d.b, nb, key[k], false);
     cnt[k * kMergeBlock + threadIdx.x] = c[k];
   }
   __syncthreads();
@@ -324,19 +334,18 @@ __global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
   for (int k = 0; k < kMergePer; ++k) {
     const int e = k * kMergeBlock + threadIdx.x;  // the element's index in the block
     const int64_t t = first + e;
-    if (t >= d.a.n) break;
+    if (t >= na) break;
     merge_put(d, d.a, t + c[k], static_cast<int32_t>(id[k]), id[k]);
     int64_t c0 = 0;
     if (e > 0) {
       c0 = cnt[e - 1];
     } else if (t > 0) {
       const uint64_t kp = merge_key(d.a, d.a.ids[t - 1]);
-      c0 = staged ? lds_count(bkey, d.b.n, kp) : merge_count(d.b, kp, false);
+      c0 = staged ? lds_count(bkey, nb, kp) : merge_count(d.b, nb, kp, false);
     }
     for (int64_t j = c0; j < c[k]; ++j) merge_put(d, d.b, j + t, static_cast<int32_t>(-1 - j), d.b.ids[j]);
-    if (t == d.a.n - 1)
-      for (int64_t j = c[k]; j < d.b.n; ++j)
-        merge_put(d, d.b, j + d.a.n, static_cast<int32_t>(-1 - j), d.b.ids[j]);
+    if (t == na - 1)
+      for (int64_t j = c[k]; j < nb; ++j) merge_put(d, d.b, j + na, static_cast<int32_t>(-1 - j), d.b.ids[j]);
   }
 }
 
@@ -347,13 +356,20 @@ __global__ __launch_bounds__(kMergeBlock) void k_merge_index(plx_merge_desc d) {
 template <int NC>
 __global__ __launch_bounds__(256) void k_merge_gather(plx_merge_gather_desc d) {
   const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 * kMergePer;
+  // ranks below cnt are gathered; with n_dev, ranks [cnt, n) get the
+  // columns' fill values
+  int64_t cnt = d.n;
+  if (d.n_dev) {
+    const int64_t c = *d.n_dev;
+    cnt = c < 0 ? 0 : (c < d.n ? c : d.n);
+  }
   bool ok[kMergePer], from_a[kMergePer];
   int64_t at[kMergePer];
   int32_t id[kMergePer];
 #pragma unroll
   for (int k = 0; k < kMergePer; ++k) {
     const int64_t r = first + k * 256 + threadIdx.x;
-    ok[k] = r < d.n;
+    ok[k] = r < cnt;
     const int32_t o = ok[k] ? d.order[r] : 0;
     // Every index is clamped into its array (a malformed order reads a
     // wrong element rather than outside the buffers).
@@ -386,10 +402,11 @@ __global__ __launch_bounds__(256) void k_merge_gather(plx_merge_gather_desc d) {
     const plx_merge_col& col = d.cols[c];
 #pragma unroll
     for (int k = 0; k < kMergePer; ++k) {
-      if (!ok[k]) continue;
       const int64_t r = first + k * 256 + threadIdx.x;
-      if (col.bytes == 1) static_cast<uint8_t*>(col.out)[r] = static_cast<uint8_t>(v[c][k]);
-      else static_cast<uint32_t*>(col.out)[r] = v[c][k];
+      if (r >= d.n) continue;
+      const uint32_t x = ok[k] ? v[c][k] : col.fill;
+      if (col.bytes == 1) static_cast<uint8_t*>(col.out)[r] = static_cast<uint8_t>(x);
+      else static_cast<uint32_t*>(col.out)[r] = x;
     }
   }
 }
@@ -492,7 +509,9 @@ int plx_merge_index(const plx_merge_desc* d, void* stream) {
   if (n > INT32_MAX || d->offset < 0 || d->offset + n > INT32_MAX)
     return fail(PLX_ERR_INVALID, "plx_merge_index: ranks exceed int32");
   if (n == 0) return PLX_OK;
-  const int64_t elems = d->a.n > 0 ? d->a.n : d->b.n;
+  // one thread per element of a, or of b when a is empty (counts on the
+  // device: sized for the larger maximum, the rest of the grid exits)
+  const int64_t elems = d->a.n > d->b.n ? d->a.n : d->b.n;
   const int64_t per_block = static_cast<int64_t>(kMergeBlock) * kMergePer;
   hipLaunchKernelGGL(k_merge_index, dim3(static_cast<unsigned>((elems + per_block - 1) / per_block)),
                      dim3(kMergeBlock), 0, static_cast<hipStream_t>(stream), *d);

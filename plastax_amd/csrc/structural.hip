@@ -821,9 +821,11 @@ __global__ void k_unit_prune(int64_t n, const uint32_t* selected, uint8_t* prune
 
 // start[u] = the number of keys below u (lower bound of u in the ascending
 // keys), u in [0, nlevels]: a CSR's offsets from its sorted row ids.
-__global__ void k_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start) {
+__global__ void k_sorted_starts(int64_t n_max, const int32_t* n_dev, const int32_t* keys, int32_t nlevels,
+                                int32_t* start) {
   const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (u > nlevels) return;
+  const int64_t n = live_count(n_max, n_dev);
   int64_t lo = 0, hi = n;
   while (lo < hi) {
     const int64_t mid = lo + (hi - lo) / 2;
@@ -1542,11 +1544,12 @@ int plx_kill_incident(int64_t n, const int32_t* from_id, const int32_t* to_id, u
   return check_launch("plx_kill_incident");
 }
 
-int plx_sorted_starts(int64_t n, const int32_t* keys, int32_t nlevels, int32_t* start, void* stream) {
+int plx_sorted_starts(int64_t n, const int32_t* n_dev, const int32_t* keys, int32_t nlevels, int32_t* start,
+                      void* stream) {
   if (n < 0 || n >= (int64_t{1} << 31) || nlevels < 0) return fail(PLX_ERR_INVALID, "plx_sorted_starts: bad sizes");
   if (!start || (n > 0 && !keys)) return fail(PLX_ERR_INVALID, "plx_sorted_starts: null pointer");
   hipLaunchKernelGGL(k_sorted_starts, dim3(grid_for(static_cast<int64_t>(nlevels) + 1)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), n, keys, nlevels, start);
+                     static_cast<hipStream_t>(stream), n, n_dev, keys, nlevels, start);
   return check_launch("plx_sorted_starts");
 }
 

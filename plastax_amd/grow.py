@@ -417,6 +417,8 @@ class AddConnPhase:
         # (flags of the last PIPELINE claim, a host bound on the tail start
         # it wrote into flags[4])
         self._tail_hint: tuple[torch.Tensor, int] | None = None
+        # a bound on the slots the last claim filled (sizes the next relayout)
+        self.claim_bound: int | None = None
         # (a level column, a bound on its deepest level): read once, then
         # carried through the add_unit phases that derive new columns
         self._level_hint: tuple[torch.Tensor, int] | None = None
@@ -715,10 +717,14 @@ class AddConnPhase:
         c.flags, c.scratch = flags.data_ptr(), scratch.data_ptr()
         c.growable_in, c.dropped_out = _ptr(growable_in), rem.dropped.data_ptr()
         _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
+        # claims are winners: a bound on the slots this claim can fill
+        winners_max = max(0, nseg * int(cfg.k) if not cfg.step_scope else int(cfg.k))
+        if cfg.max_new_per_step:
+            winners_max = min(winners_max, int(cfg.max_new_per_step))
+        self.claim_bound = min(winners_max, nc)
         if tail_dev is not None:
             # the new tail (flags[4]) is at most the old bound plus the winners
-            winners_max = nseg * int(cfg.k) if not cfg.step_scope else int(cfg.k)
-            self._tail_hint = (flags, span + max(0, winners_max))
+            self._tail_hint = (flags, span + self.claim_bound)
         out = GrowthOutcome(unflatten(flat, offs), tail_start=tail_start, fired=True, flags=flags)
         if cfg.on_overflow == "error" and out.overflow:  # (this policy reads the flags here)
             raise RuntimeError("add_conn overflow: selected candidates exceeded the free connection capacity")

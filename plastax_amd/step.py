@@ -200,9 +200,10 @@ class StepFn:
                 if self.relayout not in ("merge", "full"):
                     raise ValueError(f"relayout must be 'merge' or 'full', got {self.relayout!r}")
                 if prev is None or self.relayout == "full":
-                    prev = (None, None)
+                    prev = (None, None, None)
                 state._arena = ChurnArena(self.static, state.units, state._conns, state.device,
-                                          _stream(state.device), prev=prev[0], dead_before=prev[1])
+                                          _stream(state.device), prev=prev[0], dead_before=prev[1],
+                                          claim_bound=prev[2])
             elif self.layout_build == "device":
                 from plastax_amd._layout_dev import DeviceArena
 
@@ -436,7 +437,9 @@ class StepFn:
                             needs_resort=resort_src if resort_src is not None else bool(state.needs_resort))
             state.conns = out.conns
             if before is not None:
-                state._arena_prev = (prev, before)  # the next layout merges the claimed slots into prev's
+                # the next layout merges the claimed slots into prev's, sized
+                # by the claim's bound on them (its winner budget)
+                state._arena_prev = (prev, before, phase.claim_bound)
             for name, i in (("grown", 0), ("overflow", 1), ("needs_resort", 2)):
                 state._defer_flag(name, out.flags, i)
             if out.flags.numel() > 4:

@@ -1,8 +1,9 @@
 """The churn layout's merged rebuild (ChurnArena with ``prev``: survivors
 merged with the claimed slots by plx_merge_index / plx_merge_gather) must
 give the full rebuild's arena entry for entry: every column over the whole
-buffer (live range and the fill values past it), the slot map, the live
-counts, the forward rows and the backward lists, after every growth step,
+buffer (live range and the fill values past it), the live counts and, over
+the live range, the slot map, the forward rows and the backward lists,
+after every growth step,
 with prunes that free slots the growth then claims again. Two identical
 states step side by side, one per mode; both also match the oracle."""
 
@@ -22,11 +23,18 @@ pytestmark = pytest.mark.gpu
 
 
 def _arrays(arena) -> dict[str, np.ndarray]:
+    """Every column over the whole buffer; per bucket the live count, the
+    slot map and the lists over the live range (a merged arena sizes its
+    launches by a bound: past the count its lists and slot map hold fill
+    values, the full build's slot map the dead slots)."""
     out = {f"col/{name}": col.cpu().numpy() for name, col in arena.cols.items()}
-    out["slot"] = arena.slot.cpu().numpy()
-    out["lives"] = np.asarray(arena.lives)
+    lives = arena.live_counts()
+    out["lives"] = np.asarray(lives)
+    slot = arena.slot.cpu().numpy()
     for b, (f, lst) in enumerate(zip(arena.fwd, arena.lists)):
-        live = arena.lives[b]
+        live = lives[b]
+        assert live <= arena.lives[b]
+        out[f"slot{b}"] = slot[arena.bases[b] : arena.bases[b] + live]
         out[f"fwd{b}/ptr"] = f.ptr.cpu().numpy()
         out[f"list{b}/ptr"] = lst.ptr.cpu().numpy()
         out[f"list{b}/pos"] = lst.pos[: live + 1].cpu().numpy()

@@ -117,3 +117,70 @@ def test_remap() -> None:
     want = np.where((p >= 0) & (p < n_map), mp[np.clip(p, 0, n_map - 1)], -1)
     assert np.array_equal(out.cpu().numpy(), want)
     assert np.array_equal(live.cpu().numpy(), (want >= 0).astype(np.uint8))
+
+
+@pytest.mark.parametrize(("na", "nb", "pad_a", "pad_b"), [(5000, 37, 800, 60), (0, 100, 300, 20), (4000, 0, 5, 9),
+                                                          (300, 2048, 1000, 100), (257, 2049, 3, 3000)])
+def test_merge_with_device_counts(na: int, nb: int, pad_a: int, pad_b: int) -> None:
+    """The sides' counts on the device (n_dev) below their host bounds, the
+    id lists holding garbage past the counts: the merge sees only the counted
+    elements; the gather with a device output count writes each column's
+    fill bits at the ranks from the count to its bound, and the sorted starts
+    count only the first n_dev keys."""
+    lib = _lib.load()
+    rng = np.random.default_rng(na + 3 * nb + pad_a)
+    limit = na + nb + 64
+    k1, k2, k1b, k2b, a_ids, b_ids = _case(rng, na, nb, limit, max(4, limit // 9), False)
+    keys = [((int(k1[i]) & 0xFFFFFFFF) << 32 | (int(k2[i]) & 0xFFFFFFFF), 0, r, int(i)) for r, i in enumerate(a_ids)]
+    keys += [((int(k1b[i]) & 0xFFFFFFFF) << 32 | (int(k2b[i]) & 0xFFFFFFFF), 1, r, int(i))
+             for r, i in enumerate(b_ids)]
+    keys.sort()
+    want_order = np.asarray([i if side == 0 else -1 - r for _, side, r, i in keys], dtype=np.int32)
+    # garbage ids past the counts (in range, so any read stays in bounds)
+    ga = np.concatenate([a_ids, rng.integers(0, limit, pad_a)]).astype(np.int32)
+    gb = np.concatenate([b_ids, rng.integers(0, limit, pad_b)]).astype(np.int32)
+    bound = ga.size + gb.size
+    order = torch.full((max(bound, 1),), 7777, dtype=torch.int32, device=DEV)
+    ta, tb = _t(ga), _t(gb)
+    na_d, nb_d = _t(np.int32([na])), _t(np.int32([nb]))
+    m = _lib.plx_merge_desc()
+    _side(m.a, ta, _t(k1), _t(k2), None, limit)
+    _side(m.b, tb, _t(k1b), _t(k2b), None, limit)
+    m.a.n_dev, m.b.n_dev = na_d.data_ptr(), nb_d.data_ptr()
+    m.offset, m.order = 0, order.data_ptr()
+    assert lib.plx_merge_index(m, None) == 0, lib.plx_last_error()
+    torch.cuda.synchronize()
+    n = na + nb
+    assert np.array_equal(order.cpu().numpy()[:n], want_order)
+    if n:
+        col_a = rng.standard_normal(limit).astype(np.float32)
+        col_b = rng.standard_normal(limit).astype(np.float32)
+        out_f = torch.empty(bound, dtype=torch.float32, device=DEV)
+        out_u = torch.empty(bound, dtype=torch.uint8, device=DEV)
+        u8 = _t(rng.integers(0, 255, limit).astype(np.uint8))
+        g = _lib.plx_merge_gather_desc()
+        g.n, g.order, g.b_ids, g.nb, g.a_limit, g.b_limit = bound, order.data_ptr(), tb.data_ptr(), gb.size, limit, limit
+        n_d = _t(np.int32([n]))
+        g.n_dev = n_d.data_ptr()
+        g.ncols = 2
+        ta_f, tb_f = _t(col_a), _t(col_b)
+        g.cols[0].a, g.cols[0].b, g.cols[0].out, g.cols[0].bytes = ta_f.data_ptr(), tb_f.data_ptr(), out_f.data_ptr(), 4
+        g.cols[0].fill = int(np.float32(-2.5).view(np.uint32))
+        g.cols[1].a, g.cols[1].b, g.cols[1].out, g.cols[1].bytes = u8.data_ptr(), u8.data_ptr(), out_u.data_ptr(), 1
+        g.cols[1].fill = 1
+        assert lib.plx_merge_gather(g, None) == 0, lib.plx_last_error()
+        torch.cuda.synchronize()
+        src_a = want_order >= 0
+        ids_all = np.where(src_a, want_order, b_ids[np.where(src_a, 0, -1 - want_order)] if nb else 0)
+        got = out_f.cpu().numpy()
+        assert np.array_equal(got[:n], np.where(src_a, col_a[ids_all], col_b[ids_all]))
+        assert np.all(got[n:] == np.float32(-2.5)) and np.all(out_u.cpu().numpy()[n:] == 1)
+    # sorted starts over the first n_dev keys of a list with garbage after them
+    keys_s = np.sort(rng.integers(0, 50, max(n, 1))).astype(np.int32)[: max(n, 1)]
+    cnt = int(min(n, keys_s.size))
+    padded = np.concatenate([keys_s[:cnt], rng.integers(0, 3, 40)]).astype(np.int32)
+    start = torch.empty(51, dtype=torch.int32, device=DEV)
+    assert lib.plx_sorted_starts(padded.size, _t(np.int32([cnt])).data_ptr(), _t(padded).data_ptr(), 50,
+                                 start.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(start.cpu().numpy(), np.searchsorted(keys_s[:cnt], np.arange(51), side="left"))
