@@ -153,18 +153,10 @@ class ChurnArena(Arena):
         self.t_name = None
         self.t_now = []
         nbits = max(1, int(n).bit_length())
-        # The live counts, copied to pinned host memory without waiting: a
-        # later merge that finds the copy done (an event query, no wait)
-        # sizes its launches by the counts instead of the drifting bounds.
-        anchor = prev._anchor if prev is not None and dead_before is not None else None
-        exact = None
-        if anchor is not None and anchor[1].query():
-            exact = [int(v) for v in anchor[0].tolist()]
         for b, bucket in enumerate(conns):
             if prev is not None:
                 self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b],
-                                   None if dead_before is None else dead_before[b], claim_bound,
-                                   None if exact is None else exact[b])
+                                   None if dead_before is None else dead_before[b], claim_bound)
                 continue
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
@@ -214,12 +206,6 @@ class ChurnArena(Arena):
         self.levels_dev = levels
         if self.merged:
             self.dead_in_rows = True  # the fill positions up to each bound are dead
-        pinned = anchor[0] if anchor is not None else torch.zeros(nb, dtype=torch.int32, pin_memory=True)
-        for b, t in enumerate(self.live_dev):
-            pinned[b : b + 1].copy_(t.reshape(1), non_blocking=True)
-        event = torch.cuda.Event()
-        event.record(torch.cuda.ExternalStream(stream, device=device))
-        self._anchor = (pinned, event)
         if prev is not None:
             prev._retire()
 
@@ -254,8 +240,7 @@ class ChurnArena(Arena):
         self._spare = None
 
     def _merge_bucket(self, k, b: int, prev: "ChurnArena", bucket: Columns, specs: dict, nbits: int,
-                      rows: torch.Tensor, extent: int, dead_before: torch.Tensor, claim_bound: int | None,
-                      prev_live: int | None = None) -> None:
+                      rows: torch.Tensor, extent: int, dead_before: torch.Tensor, claim_bound: int | None) -> None:
         """Bucket b laid out from ``prev``'s layout of it (see the module
         docstring): the survivors (prev's live positions whose DEAD is still
         0) merged with the slots the claim turned live (``dead_before``: DEAD
@@ -266,16 +251,12 @@ class ChurnArena(Arena):
         The counts stay on the device. The launches are sized by host bounds:
         prev's bound on its live count and ``claim_bound``, a bound on the
         claimed slots (the growth's winner budget; the bucket's capacity
-        when not given), or by prev's count itself when its copy to the host
-        (started by prev's build) is already done (``prev_live``). Ranks past
-        the live count get fill values (slot -1), so every array up to the
-        bound is defined."""
+        when not given). Ranks past the live count get fill values (slot -1),
+        so every array up to the bound is defined."""
         dev = self.device
         n = self.static.num_units
         base, cap = self.bases[b], self.caps[b]
         old_bound, old_live_d = prev.lives[b], prev.live_dev[b]
-        if prev_live is not None:  # prev's count, already on the host
-            old_bound = min(old_bound, prev_live)
         new_bound = cap if claim_bound is None else max(0, min(cap, int(claim_bound)))
         bound = min(cap, old_bound + new_bound)
         lib = k.lib
