@@ -336,6 +336,15 @@ class ChurnArena(Arena):
         needs it)."""
         return [int(t.item()) for t in self.live_dev]
 
+    def reanchor(self) -> None:
+        """Tighten the host bounds to the live counts. The bounds grow by
+        the claim's budget at every merge; a caller that waits on the device
+        anyway (reading the flags) calls this, one small read more, so a long
+        run's launches stay sized by its counts."""
+        if self.live_dev:
+            counts = torch.cat([t.reshape(1) for t in self.live_dev]).tolist()
+            self.lives = [min(bound, int(c)) for bound, c in zip(self.lives, counts)]
+
     def _write_kills(self, conns: tuple[Columns, ...], written: set) -> None:
         """Only prunes wrote since the logical view was in step: DEAD went
         from 0 to 1 at the killed edges (every position of the live range

@@ -175,13 +175,18 @@ class NetworkState:
         return self._flag_dev.get(name)
 
     def _read_flags(self, tensor: Any) -> None:
-        """One read of ``tensor`` resolves every flag pending on it."""
+        """One read of ``tensor`` resolves every flag pending on it. The
+        caller waits on the device here anyway, so a churn arena's bounds
+        are tightened to its counts at the same time (ChurnArena.reanchor)."""
         vals = tensor.cpu().tolist()
         for name, (t, i) in list(self._flag_dev.items()):
             if t is tensor:
                 v = vals[i]
                 self._flag_val[name] = bool(v) if name in _BOOL_FLAGS else int(v)
                 del self._flag_dev[name]
+        arena = self._arena_prev[0] if self._arena_prev else self._arena
+        if hasattr(arena, "reanchor") and getattr(arena, "cols", None) is not None:
+            arena.reanchor()
 
     def _flag_reader(self, name: str) -> Any:
         """A zero-argument callable giving the flag's value as of now, read
