@@ -301,6 +301,9 @@ __device__ __forceinline__ void stage_table(float* tbl, const float* x, int base
 // Gathers K values x[idx[k]] (lanes with use[k] false read the table's first
 // entry, or x[0] without a table, and their value is ignored): table hits
 // read LDS, the rest issue one global load each, all before any is used.
+// A hit and a miss share out[k], so the table read waits for the global
+// loads in flight (the memory counter retires in order); gather_split
+// keeps them apart.
 template <int K>
 __device__ __forceinline__ void gather_k(const float* tbl, const float* x, int base, int len,
                                          const int* idx, const bool* use, float* out) {
@@ -316,6 +319,41 @@ __device__ __forceinline__ void gather_k(const float* tbl, const float* x, int b
 #pragma unroll
   for (int k = 0; k < K; ++k)
     if (in[k]) out[k] = tbl[o[k]];
+}
+
+// As gather_k, with table hits read into hit[k] and misses into miss[k]
+// (the register of the other kind holds 0): the value is
+// gather_join(hit[k], miss[k]), taken where it is used, so nothing here
+// waits for the global loads.
+template <int K>
+__device__ __forceinline__ void gather_split(const float* tbl, const float* x, int base, int len,
+                                             const int* idx, const bool* use, uint32_t* hit, uint32_t* miss) {
+  int o[K];
+  bool in[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = use[k] ? idx[k] : (len > 0 ? base : 0);
+    o[k] = i - base;
+    in[k] = static_cast<unsigned>(o[k]) < static_cast<unsigned>(len);
+    miss[k] = 0u;
+    if (!in[k]) miss[k] = __float_as_uint(x[i]);
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    hit[k] = 0u;
+    if (in[k]) hit[k] = __float_as_uint(tbl[o[k]]);
+  }
+}
+
+__device__ __forceinline__ float gather_join(uint32_t hit, uint32_t miss) { return __uint_as_float(hit | miss); }
+
+// A launch-uniform read of a layout table through the scalar cache (the
+// constant address space: the tables are written by earlier launches and
+// only read by the kernels that use this). Waiting for a scalar load does
+// not wait for the vector loads and stores in flight, which retire in order.
+typedef const __attribute__((address_space(4))) int32_t const_i32;
+__device__ __forceinline__ int32_t ld_uniform(const int32_t* p, int64_t i) {
+  return ((const_i32*)p)[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -789,6 +827,9 @@ constexpr uint32_t kGroupStart = 0x8000u;  // sorted_rank / tag: the rank starts
 constexpr int kTileInfo = 16;             // int32 entries of tile_info per tile
 constexpr int kGrpPer = 4;                // group descriptors prefetched per thread per tile
 constexpr uint32_t kLenOpen = 15;         // descriptor length field: 15 or more (the end is found)
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // The cold slot of a cold group starting at rank r of a tile, from the
 // tile's info staged in LDS (tmap: [0] hlo | hhi << 16, the hot ranks;
@@ -853,8 +894,15 @@ __device__ __forceinline__ void fold_group(const plx_tile_desc& d, const float* 
 
 // SAME_G: the backward field and the update's grad field are one column, so
 // one gather serves both.
-template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
+// SAME_G: the backward field and the update's grad field are one column, so
+// one gather serves both. FAST: the layout has one-byte destinations and the
+// caller passes no DEAD column (the common case), so neither is a branch at
+// run time.
+template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T, bool FAST>
 __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
+  // Known at compile time on the FAST path: one-byte destinations, no DEAD.
+  const bool dst8 = FAST || d.dst8 != nullptr;
+  const bool dead = !FAST && d.dead != nullptr;
   extern __shared__ __align__(16) unsigned char smem[];
   const int T = d.tile_size;
   float* buf = reinterpret_cast<float*>(smem);  // [T] terms in source-sorted order
@@ -865,8 +913,8 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   float* hot = reinterpret_cast<float*>(tmap + kTileInfo);  // [nhot]
   // [tbl_len] act of the busiest sources (the whole allocation without fold)
   float* tbl = FOLD ? hot + ((d.nhot + 3) & ~3) : reinterpret_cast<float*>(smem);
-  const int k0 = d.super_tile[blockIdx.x];
-  const int k1 = d.super_tile[blockIdx.x + 1];
+  const int k0 = ld_uniform(d.super_tile, blockIdx.x);
+  const int k1 = ld_uniform(d.super_tile, blockIdx.x + 1);
   const float ident = Mono<M>::id();
   constexpr int nstate = RULE < 0 || RULE == PLX_RULE_SGD
                              ? 0
@@ -885,41 +933,57 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   // are tile blk + 2's addressing columns (dst, src, dead), which the
   // gathers of the next iteration need.
   int4 sv[U], tv[U];  // addressing columns of tile `an` (the next to gather)
-  uint32_t dv[U];
+  // Dead bytes of those quads: dl from DEAD, de from live_end (the other
+  // one 0). Loaded columns and computed values never share a register (nor
+  // do the two TO_ID forms, tv and t8): a register written on one path and
+  // loaded on the other would make every path wait for all memory
+  // operations in flight.
+  uint32_t dl[U], de[U], t8[U];
   int64_t ta = 0;
   int na = 0;
   // With dst8, a position's TO_ID is the first destination of its 4,096-
   // position block plus a one-byte delta (positions are destination-sorted):
-  // tv[i].x holds the quad's four deltas; a tile spans at most two blocks,
+  // t8[i] holds the quad's four deltas; a tile spans at most two blocks,
   // whose bases are ad_lo and ad_hi.
   int ab_lo = 0, ad_lo = 0, ad_hi = 0;
   auto load_addr = [&](int blk) {
-    ta = d.base + d.tile_pos[blk];
-    na = d.tile_pos[blk + 1] - d.tile_pos[blk];
-    if (d.dst8) {
-      ab_lo = d.tile_pos[blk] >> kDst8Shift;
-      ad_lo = d.blk_dst0[ab_lo];
-      ad_hi = d.blk_dst0[(d.tile_pos[blk + 1] - 1) >> kDst8Shift];
+    const int p0 = ld_uniform(d.tile_pos, blk), p1 = ld_uniform(d.tile_pos, blk + 1);
+    ta = d.base + p0;
+    na = p1 - p0;
+    if (dst8) {
+      ab_lo = p0 >> kDst8Shift;
+      ad_lo = ld_uniform(d.blk_dst0, ab_lo);
+      ad_hi = ld_uniform(d.blk_dst0, (p1 - 1) >> kDst8Shift);
     }
+    if (na <= 0) return;  // (tiles are never empty; uniform)
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      const int q = threadIdx.x + i * kTileBlock;
-      if (4 * q < na) {
-        const int64_t e = ta + 4 * q;
-        if (d.dst8)
-          tv[i].x = static_cast<int>(ld_stream(d.dst8 + (e - d.base)));
-        else
-          tv[i] = ld_stream(d.dst + e);
-        if (RULE >= 0 || FOLD) sv[i] = ld_stream(d.src + e);
-        dv[i] = d.dead ? *reinterpret_cast<const uint32_t*>(d.dead + e) : dead_from_end(e, d.live_end);
-      }
+      // Lanes past the tile's end load its last quad again (one more
+      // request to a line already read; gather() marks them out of the
+      // tile), so no load is under a lane-dependent branch, and each
+      // register is cleared before the uniform branches that may load it:
+      // merging a loaded register with an older value would wait for every
+      // memory operation in flight.
+      const int q = min(static_cast<int>(threadIdx.x) + i * kTileBlock, (na >> 2) - 1);
+      const int64_t e = ta + 4 * q;
+      t8[i] = 0u;
+      tv[i] = make_int4(0, 0, 0, 0);
+      dl[i] = 0u;
+      if (dst8)
+        t8[i] = ld_stream(d.dst8 + (e - d.base));
+      else
+        tv[i] = ld_stream(d.dst + e);
+      if (RULE >= 0 || FOLD) sv[i] = ld_stream(d.src + e);
+      if (dead) dl[i] = *reinterpret_cast<const uint32_t*>(d.dead + e);
+      de[i] = dead ? 0u : dead_from_end(e, d.live_end);
     }
   };
   // Value columns and gathered values of the current tile.
   uint2 rk[U];
   float4 w[U], s0[U], s1[U], s2[U];
   bool lv[U][4];
-  float gd[U][4], gu[U][4], ac[U][4];
+  float gd[U][4], gu[U][4];
+  uint32_t ah[U][4], am[U][4];  // act gathers: table hits, misses (gather_join)
   int64_t t0 = 0;
   int n = 0;
   uint32_t ht[U][2];  // hot tags of the gathered tile: src - hot_base (hot sources), else 0
@@ -934,8 +998,8 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
     for (int i = 0; i < U; ++i) {
       const bool in = 4 * (threadIdx.x + i * kTileBlock) < na;
       int di[4] = {tv[i].x, tv[i].y, tv[i].z, tv[i].w};
-      if (d.dst8) {
-        const uint32_t dq = static_cast<uint32_t>(tv[i].x);
+      if (dst8) {
+        const uint32_t dq = t8[i];
         const int rel = static_cast<int>(ta - d.base) + 4 * (static_cast<int>(threadIdx.x) + i * kTileBlock);
         const int d0 = (rel >> kDst8Shift) == ab_lo ? ad_lo : ad_hi;
 #pragma unroll
@@ -944,12 +1008,12 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       const int si[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        lv[i][k] = in && !((dv[i] >> (8 * k)) & 0xFFu);
+        lv[i][k] = in && !(((dl[i] | de[i]) >> (8 * k)) & 0xFFu);
         const int dk = lv[i][k] ? di[k] : 0;
         if (FOLD) gd[i][k] = d.g[dk];
         if (RULE >= 0) gu[i][k] = SAME_G && FOLD ? 0.0f : d.gfield[dk];
       }
-      if (RULE >= 0) gather_k<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ac[i]);
+      if (RULE >= 0) gather_split<4>(tbl, d.act, d.tbl_base, d.tbl_len, si, lv[i], ah[i], am[i]);
       if (FOLD) {
         uint32_t h[4];
 #pragma unroll
@@ -968,20 +1032,22 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   auto load_vals = [&](int blk) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      const int q = threadIdx.x + i * kTileBlock;
-      if (4 * q < n) {
-        const int64_t e = t0 + 4 * q;
-        w[i] = ld_stream(d.weight + e);
-        if (FOLD) rk[i] = ld_stream(d.sorted_rank + (e - d.base));
-        if (nstate >= 1) s0[i] = ld_stream(d.s0 + e);
-        if (nstate >= 2) s1[i] = ld_stream(d.s1 + e);
-        if (nstate >= 3) s2[i] = ld_stream(d.s2 + e);
-      }
+      // As in load_addr: lanes past the tile's end load its last quad (the
+      // update loop skips them; tiles are never empty).
+      const int q = max(min(static_cast<int>(threadIdx.x) + i * kTileBlock, (n >> 2) - 1), 0);
+      const int64_t e = t0 + 4 * q;
+      w[i] = ld_stream(d.weight + e);
+      if (FOLD) rk[i] = ld_stream(d.sorted_rank + (e - d.base));
+      if (nstate >= 1) s0[i] = ld_stream(d.s0 + e);
+      if (nstate >= 2) s1[i] = ld_stream(d.s1 + e);
+      if (nstate >= 3) s2[i] = ld_stream(d.s2 + e);
     }
     if (FOLD) {
-      if (threadIdx.x < kTileInfo) tiv = d.tile_info[static_cast<int64_t>(blk) * kTileInfo + threadIdx.x];
-      ga = d.grp_off[blk];
-      gb = d.grp_off[blk + 1];
+      // Every lane loads an entry (lanes past kTileInfo repeat the first
+      // ones: one cache line), so the load is not under a branch.
+      tiv = d.tile_info[static_cast<int64_t>(blk) * kTileInfo + (threadIdx.x & (kTileInfo - 1))];
+      ga = ld_uniform(d.grp_off, blk);
+      gb = ld_uniform(d.grp_off, blk + 1);
 #pragma unroll
       for (int i = 0; i < kGrpPer; ++i) {
         const int gi = ga + threadIdx.x + i * kTileBlock;
@@ -999,6 +1065,18 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
   load_vals(k0);
   if (k0 + 1 < k1) load_addr(k0 + 1);
   for (int blk = k0; blk < k1; ++blk) {
+    // Every load issued for this tile and the next tile's addressing columns
+    // is waited for here, before this tile's stores: the memory counter
+    // retires in order, so a wait for the addressing columns after the
+    // stores would wait for the stores too. This tile's info and group
+    // descriptors are taken here for the same reason. (The previous tile's
+    // fold, which read tmap, ended at a barrier.)
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    if (FOLD && threadIdx.x < kTileInfo) tmap[threadIdx.x] = tiv;
+    uint16_t cgd[kGrpPer];
+    const int cga = ga, cgb = gb;
+#pragma unroll
+    for (int i = 0; i < kGrpPer; ++i) cgd[i] = gdesc[i];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = threadIdx.x + i * kTileBlock;
@@ -1026,7 +1104,8 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
       if (RULE >= 0) {
         float gr[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) gr[k] = (SAME_G && FOLD ? gd[i][k] : gu[i][k]) * ac[i][k];
+        for (int k = 0; k < 4; ++k)
+          gr[k] = (SAME_G && FOLD ? gd[i][k] : gu[i][k]) * gather_join(ah[i][k], am[i][k]);
         float4 a = w[i], m = s0[i], v = s1[i], t = s2[i];
         if (lv[i][0]) update_edge<RULE, UNI_T>(d, gr[0], den1, den2, a.x, m.x, v.x, t.x);
         if (lv[i][1]) update_edge<RULE, UNI_T>(d, gr[1], den1, den2, a.y, m.y, v.y, t.y);
@@ -1038,13 +1117,8 @@ __global__ __launch_bounds__(kTileBlock, 2) void k_tile(plx_tile_desc d) {
         if (nstate >= 3) st_stream(d.s2 + e, t);
       }
     }
-    // This tile's ranked length and info, kept while the next tile loads.
+    // This tile's ranked length, kept while the next tile loads.
     const int nr = static_cast<int>(max(static_cast<int64_t>(0), min(static_cast<int64_t>(n), d.live_end - t0)));
-    if (FOLD && threadIdx.x < kTileInfo) tmap[threadIdx.x] = tiv;
-    uint16_t cgd[kGrpPer];
-    const int cga = ga, cgb = gb;
-#pragma unroll
-    for (int i = 0; i < kGrpPer; ++i) cgd[i] = gdesc[i];
     if (blk + 1 < k1) {
       gather();
       load_vals(blk + 1);
@@ -1959,38 +2033,50 @@ bool program_ok(const plx_program& p, bool fixed_ok = false) {
   return fixed_ok && (static_cast<uint32_t>(p.fixed_mask) >> p.nfields) == 0u;
 }
 
-template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
-void launch_tile_g(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T, bool FAST>
+void launch_tile_k(const plx_tile_desc& d, size_t lds, hipStream_t s) {
   // LDS beyond 64 KiB needs an explicit per-kernel opt-in.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD, SAME_G, UNI_T>),
+      reinterpret_cast<const void*>(&k_tile<RULE, M, FOLD, SAME_G, UNI_T, FAST>),
       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   (void)attr;
   // One workgroup per superblock of tiles.
-  k_tile<RULE, M, FOLD, SAME_G, UNI_T>
+  k_tile<RULE, M, FOLD, SAME_G, UNI_T, FAST>
       <<<static_cast<unsigned>(d.nsuper), kTileBlock, lds, s>>>(d);
 }
-
+template <int RULE, int M, bool FOLD, bool SAME_G, bool UNI_T>
+void launch_tile_g(const plx_tile_desc& d, size_t lds, hipStream_t s) {
+  if (d.dst8 && !d.dead)
+    launch_tile_k<RULE, M, FOLD, SAME_G, UNI_T, true>(d, lds, s);
+  else
+    launch_tile_k<RULE, M, FOLD, SAME_G, UNI_T, false>(d, lds, s);
+}
+// Instantiates only the meaningful variants: SAME_G needs a fold and an
+// update, UNI_T is Adam's.
 template <int RULE, int M, bool FOLD>
 void launch_tile(const plx_tile_desc& d, size_t lds, hipStream_t s) {
-  const bool same = FOLD && RULE >= 0 && d.g == d.gfield;
-  if (RULE == PLX_RULE_ADAM && d.step_mode == 1) {
-    if (same)
-      launch_tile_g<RULE, M, FOLD, true, true>(d, lds, s);
-    else
-      launch_tile_g<RULE, M, FOLD, false, true>(d, lds, s);
-  } else {
-    if (same)
-      launch_tile_g<RULE, M, FOLD, true, false>(d, lds, s);
-    else
-      launch_tile_g<RULE, M, FOLD, false, false>(d, lds, s);
+  constexpr bool kSame = FOLD && RULE >= 0;
+  const bool same = kSame && d.g == d.gfield;
+  if constexpr (RULE == PLX_RULE_ADAM) {
+    if (d.step_mode == 1) {
+      if constexpr (kSame) {
+        if (same) return launch_tile_g<RULE, M, FOLD, kSame, true>(d, lds, s);
+      }
+      return launch_tile_g<RULE, M, FOLD, false, true>(d, lds, s);
+    }
   }
+  if constexpr (kSame) {
+    if (same) return launch_tile_g<RULE, M, FOLD, kSame, false>(d, lds, s);
+  }
+  launch_tile_g<RULE, M, FOLD, false, false>(d, lds, s);
 }
-
 template <int M, bool FOLD>
 int dispatch_rule(const plx_tile_desc& d, size_t lds, hipStream_t s) {
   switch (d.update ? d.rule : -1) {
-    case -1: launch_tile<-1, M, FOLD>(d, lds, s); break;
+    case -1:
+      // (no update: only a fold launches; the caller returns before otherwise)
+      if constexpr (FOLD) launch_tile<-1, M, FOLD>(d, lds, s);
+      break;
     case PLX_RULE_SGD: launch_tile<PLX_RULE_SGD, M, FOLD>(d, lds, s); break;
     case PLX_RULE_MOMENTUM: launch_tile<PLX_RULE_MOMENTUM, M, FOLD>(d, lds, s); break;
     case PLX_RULE_ADAM: launch_tile<PLX_RULE_ADAM, M, FOLD>(d, lds, s); break;
