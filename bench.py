@@ -1216,8 +1216,8 @@ def main() -> int:
                     "c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
                     "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--scale", type=int, default=1, help="shrink C2's layer width (tests only)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=12)
