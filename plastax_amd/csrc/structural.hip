@@ -285,33 +285,73 @@ __device__ __forceinline__ uint32_t score_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Key `key` of element idx (the value being sorted).
-__device__ __forceinline__ uint32_t sort_key_of(const plx_sort_key& key, uint32_t idx) {
-  uint32_t k;
+// Keys of R elements (the values being sorted, idx[r]; every idx[r] a valid
+// index), with every load of a stage issued before any is used: the kind is
+// uniform, so each case is straight-line code. Elements with ok[r] false get
+// key 0 (their loads still go out, at a valid index).
+template <int R>
+__device__ __forceinline__ void sort_keys_of(const plx_sort_key& key, const uint32_t* idx, const bool* ok,
+                                             uint32_t* k) {
+  const int32_t* a = static_cast<const int32_t*>(key.a);
   switch (key.kind) {
-    case PLX_KEY_SCORE: k = score_key(static_cast<const float*>(key.a)[idx]); break;
-    case PLX_KEY_LEVEL_OF: {
-      int32_t id = static_cast<const int32_t*>(key.a)[idx];
-      if (key.bound > 0) id = id < 0 ? 0 : (id >= key.bound ? key.bound - 1 : id);
-      k = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id]);
+    case PLX_KEY_SCORE: {
+      float f[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) f[r] = static_cast<const float*>(key.a)[idx[r]];
+#pragma unroll
+      for (int r = 0; r < R; ++r) k[r] = ok[r] ? score_key(f[r]) : 0u;
       break;
     }
-    case PLX_KEY_PAIR16:
-      k = (static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]) << 16) |
-          (static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[idx]) & 0xFFFFu);
+    case PLX_KEY_LEVEL_OF: {
+      int32_t id[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        id[r] = a[idx[r]];
+        if (key.bound > 0) id[r] = id[r] < 0 ? 0 : (id[r] >= key.bound ? key.bound - 1 : id[r]);
+      }
+      uint32_t lv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) lv[r] = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[id[r]]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) k[r] = ok[r] ? lv[r] : 0u;
       break;
-    case PLX_KEY_DEADMAX:
-      k = static_cast<const uint8_t*>(key.b)[idx]
-              ? (key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u))
-              : static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]);
+    }
+    case PLX_KEY_PAIR16: {
+      uint32_t hi[R], lo[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        hi[r] = static_cast<uint32_t>(a[idx[r]]);
+        lo[r] = static_cast<uint32_t>(static_cast<const int32_t*>(key.b)[idx[r]]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) k[r] = ok[r] ? (hi[r] << 16) | (lo[r] & 0xFFFFu) : 0u;
       break;
-    default: k = static_cast<uint32_t>(static_cast<const int32_t*>(key.a)[idx]); break;
+    }
+    case PLX_KEY_DEADMAX: {
+      const uint32_t top = key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u);
+      uint32_t dv[R], av[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        dv[r] = static_cast<const uint8_t*>(key.b)[idx[r]];
+        av[r] = static_cast<uint32_t>(a[idx[r]]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) k[r] = ok[r] ? (dv[r] ? top : av[r]) : 0u;
+      break;
+    }
+    default: {
+      uint32_t av[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) av[r] = static_cast<uint32_t>(a[idx[r]]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) k[r] = ok[r] ? av[r] : 0u;
+      break;
+    }
   }
-  return k;
 }
 
 // Per-tile digit counts at `shift`, digit-major (hist[d * ntiles + tile]).
-// With GATHER the keys are computed from the values (sort_key_of) and
+// With GATHER the keys are computed from the values (sort_keys_of) and
 // written to keys; vals_copy (optional) receives a copy of the values.
 // The table's entry of (digit d, tile): tile-major when the table is
 // scanned by k_scan_tiles, else digit-major (the chunked scan's flat order).
@@ -319,10 +359,13 @@ __device__ __forceinline__ int64_t hist_at(bool tile_major, int d, int64_t tile,
   return tile_major ? tile * 256 + d : static_cast<int64_t>(d) * ntiles + tile;
 }
 
+// Each thread issues every load of its kTile / kBlock elements before using
+// any (one memory latency per tile, not one per round).
 template <bool GATHER>
 __global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key key, const uint32_t* vals,
                              uint32_t* keys, uint32_t* vals_copy, int shift, int64_t ntiles, bool tile_major,
                              int32_t* hist) {
+  constexpr int R = kTile / kBlock;
   __shared__ int h[256];
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
@@ -331,22 +374,40 @@ __global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key k
     return;
   }
   h[threadIdx.x] = 0;
-  __syncthreads();
-  for (int r = 0; r < kTile / kBlock; ++r) {
-    const int64_t p = base + r * kBlock + threadIdx.x;
-    if (p < n) {
-      uint32_t k;
-      if (GATHER) {
-        const uint32_t idx = vals[p];
-        k = sort_key_of(key, idx);
-        keys[p] = k;
-        if (vals_copy) vals_copy[p] = idx;
-      } else {
-        k = keys[p];
-      }
-      atomicAdd(&h[(k >> shift) & 255u], 1);
+  uint32_t k[R];
+  if (GATHER) {
+    uint32_t idx[R];
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      // (positions past the count read the last element: a valid index)
+      const int64_t p = base + r * kBlock + threadIdx.x;
+      ok[r] = p < n;
+      idx[r] = vals[ok[r] ? p : n - 1];
     }
+    sort_keys_of<R>(key, idx, ok, k);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t p = base + r * kBlock + threadIdx.x;
+      if (ok[r]) {
+        keys[p] = k[r];
+        if (vals_copy) vals_copy[p] = idx[r];
+      }
+    }
+  } else {
+    uint32_t kv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t p = base + r * kBlock + threadIdx.x;
+      kv[r] = keys[p < n ? p : n - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) k[r] = base + r * kBlock + threadIdx.x < n ? kv[r] : 0u;
   }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (base + r * kBlock + threadIdx.x < n) atomicAdd(&h[(k[r] >> shift) & 255u], 1);
   __syncthreads();
   hist[hist_at(tile_major, threadIdx.x, blockIdx.x, ntiles)] = h[threadIdx.x];
 }
@@ -361,14 +422,25 @@ __global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint3
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   if (base >= n) return;  // uniform over the workgroup
   s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
-  for (int r = 0; r < kTile / kBlock; ++r) {
+  // Every key and value of the thread's rounds is loaded before the first
+  // round (one memory latency per tile, not one per round).
+  constexpr int R = kTile / kBlock;
+  uint32_t kr[R], vr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t p = base + r * kBlock + t;
+    kr[r] = keys_in[p < n ? p : n - 1];  // (past the count: read but unused)
+    vr[r] = vals_in[p < n ? p : n - 1];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
     if (base + r * kBlock >= n) break;  // uniform: the rest of the tile is past the count
     for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
     __syncthreads();
     const int64_t p = base + r * kBlock + t;
     const bool valid = p < n;
-    const uint32_t key = valid ? keys_in[p] : 0u;
-    const uint32_t val = valid ? vals_in[p] : 0u;
+    const uint32_t key = kr[r];
+    const uint32_t val = vr[r];
     const uint32_t d = (key >> shift) & 255u;
     uint64_t peers = __ballot(valid);
 #pragma unroll
