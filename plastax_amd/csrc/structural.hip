@@ -85,15 +85,41 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total)
 // Flags, chunk sums and the scans.
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ int flag_of(int32_t mode, const void* flags, int64_t p) {
-  switch (mode) {
-    case PLX_FLAG_U8: return static_cast<const uint8_t*>(flags)[p] != 0;
-    case PLX_FLAG_U8_ZERO: return static_cast<const uint8_t*>(flags)[p] == 0;
-    case PLX_FLAG_FINITE: {
-      const float f = static_cast<const float*>(flags)[p];
-      return (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u;
-    }
-    default: return static_cast<const int32_t*>(flags)[p] != 0;
+// The R values a thread reads of the chunk at `base` (positions base + r *
+// kBlock + threadIdx.x; base < n): mode < 0 the int32 values of `in`, else
+// the flags of the compaction mode (0 or 1); positions at or past n give 0.
+// The mode is uniform, so each case is straight-line code: every load is
+// issued (past n at the last position) before any is used, one memory
+// latency per chunk instead of one per round.
+template <int R>
+__device__ __forceinline__ void chunk_values(int32_t mode, const void* in, int64_t base, int64_t n, int* v) {
+  int64_t q[R];
+  bool ok[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t p = base + r * kBlock + threadIdx.x;
+    ok[r] = p < n;
+    q[r] = ok[r] ? p : n - 1;
+  }
+  if (mode == PLX_FLAG_U8 || mode == PLX_FLAG_U8_ZERO) {
+    uint32_t b[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) b[r] = static_cast<const uint8_t*>(in)[q[r]];
+    const bool want = mode == PLX_FLAG_U8;
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = ok[r] && ((b[r] != 0u) == want);
+  } else if (mode == PLX_FLAG_FINITE) {
+    uint32_t b[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) b[r] = static_cast<const uint32_t*>(in)[q[r]];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = ok[r] && (b[r] & 0x7F800000u) != 0x7F800000u;
+  } else {
+    int b[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) b[r] = static_cast<const int32_t*>(in)[q[r]];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = !ok[r] ? 0 : (mode < 0 ? b[r] : (b[r] != 0));
   }
 }
 
@@ -107,11 +133,12 @@ __global__ void k_chunk_sums(int64_t n_max, const int32_t* n_dev, int32_t mode, 
     if (threadIdx.x == 0) sums[blockIdx.x] = 0;
     return;
   }
+  constexpr int R = kChunk / kBlock;
+  int v[R];
+  chunk_values<R>(mode, in, base, n, v);
   int acc = 0;
-  for (int r = 0; r < kChunk / kBlock; ++r) {
-    const int64_t p = base + r * kBlock + threadIdx.x;
-    if (p < n) acc += mode < 0 ? static_cast<const int32_t*>(in)[p] : flag_of(mode, in, p);
-  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc += v[r];
   int total;
   block_exclusive_scan<kBlock>(acc, lds, &total);
   if (threadIdx.x == 0) sums[blockIdx.x] = total;
@@ -139,11 +166,16 @@ __global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t*
   __shared__ int lds[kWaves + 1];
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  if (base >= n) return;  // uniform over the workgroup: the chunk is past the count
   int run = sums[blockIdx.x];
-  for (int r = 0; r < kChunk / kBlock; ++r) {
+  constexpr int R = kChunk / kBlock;
+  int vals[R];
+  chunk_values<R>(-1, in, base, n, vals);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
     if (base + r * kBlock >= n) break;  // uniform: the rest of the chunk is past the count
     const int64_t p = base + r * kBlock + threadIdx.x;
-    const int v = p < n ? in[p] : 0;
+    const int v = vals[r];
     int total;
     const int ex = block_exclusive_scan<kBlock>(v, lds, &total);
     if (p < n) out[p] = run + ex;
@@ -156,12 +188,17 @@ __global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mod
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
   __shared__ int wcnt[kWaves];
+  if (base >= n) return;  // uniform over the workgroup: the chunk is past the count
   int run = sums[blockIdx.x];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int r = 0; r < kChunk / kBlock; ++r) {
+  constexpr int R = kChunk / kBlock;
+  int fv[R];
+  chunk_values<R>(mode, flags, base, n, fv);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
     if (base + r * kBlock >= n) break;  // uniform: the rest of the chunk is past the count
     const int64_t p = base + r * kBlock + threadIdx.x;
-    const int f = p < n ? flag_of(mode, flags, p) : 0;
+    const int f = fv[r];
     const uint64_t m = __ballot(f);
     if (lane == 0) wcnt[wave] = __popcll(m);
     __syncthreads();
