@@ -214,74 +214,10 @@ __global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mod
   }
 }
 
-// A radix pass's digit-by-tile counts, tile-major (t[tile * 256 + d]),
-// turned in place into each (tile, digit)'s first output position: the
-// count of smaller digits plus the count of digit d in earlier tiles. One
-// workgroup of kScanTilesWaves waves; wave w keeps tiles [w kScanTilesPer,
-// (w + 1) kScanTilesPer) in registers, lane l digits [4 l, 4 l + 4), so
-// every load and store moves 1 KB per wave. (Up to kScanTilesMax tiles:
-// the sort's table scan in one launch; larger tables take the chunked scan
-// of a digit-major table.)
-constexpr int kScanTilesWaves = kScanLanes / 64;
-constexpr int kScanTilesPer = 16;
-constexpr int64_t kScanTilesMax = int64_t(kScanTilesWaves) * kScanTilesPer;
-__global__ __launch_bounds__(kScanLanes) void k_scan_tiles(int64_t ntiles, int32_t* t) {
-  __shared__ __align__(16) int part[kScanTilesWaves][256];
-  __shared__ __align__(16) int base[256];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t t0 = static_cast<int64_t>(wave) * kScanTilesPer;
-  int4 c[kScanTilesPer];
-  int4 sum = make_int4(0, 0, 0, 0);
-#pragma unroll
-  for (int i = 0; i < kScanTilesPer; ++i) {
-    c[i] = t0 + i < ntiles ? *reinterpret_cast<const int4*>(t + (t0 + i) * 256 + 4 * lane) : make_int4(0, 0, 0, 0);
-    sum.x += c[i].x;
-    sum.y += c[i].y;
-    sum.z += c[i].z;
-    sum.w += c[i].w;
-  }
-  *reinterpret_cast<int4*>(&part[wave][4 * lane]) = sum;
-  __syncthreads();
-  if (threadIdx.x < 256) {  // per digit: the waves' exclusive prefix, then the digit's total
-    const int d = threadIdx.x;
-    int run = 0;
-    for (int w = 0; w < kScanTilesWaves; ++w) {
-      const int x = part[w][d];
-      part[w][d] = run;
-      run += x;
-    }
-    base[d] = run;
-  }
-  __syncthreads();
-  if (wave == 0) {  // the digit totals' exclusive scan: digit d starts after every smaller digit
-    const int4 v = *reinterpret_cast<const int4*>(&base[4 * lane]);
-    const int own = v.x + v.y + v.z + v.w;
-    int x = own;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    int4 e;
-    e.x = x - own;
-    e.y = e.x + v.x;
-    e.z = e.y + v.y;
-    e.w = e.z + v.z;
-    *reinterpret_cast<int4*>(&base[4 * lane]) = e;
-  }
-  __syncthreads();
-  const int4 b = *reinterpret_cast<const int4*>(&base[4 * lane]);
-  const int4 w0 = *reinterpret_cast<const int4*>(&part[wave][4 * lane]);
-  int4 run = make_int4(b.x + w0.x, b.y + w0.y, b.z + w0.z, b.w + w0.w);
-#pragma unroll
-  for (int i = 0; i < kScanTilesPer; ++i) {
-    if (t0 + i < ntiles) *reinterpret_cast<int4*>(t + (t0 + i) * 256 + 4 * lane) = run;
-    run.x += c[i].x;
-    run.y += c[i].y;
-    run.z += c[i].z;
-    run.w += c[i].w;
-  }
-}
+// A radix pass's digit-by-tile counts are kept tile-major (t[tile * 256 + d])
+// for up to kScanTilesMax tiles, and each scatter workgroup scans the table
+// itself; larger tables are scanned digit-major by the chunked scan first.
+constexpr int64_t kScanTilesMax = 256;
 
 int64_t chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
 
@@ -390,8 +326,8 @@ __device__ __forceinline__ void sort_keys_of(const plx_sort_key& key, const uint
 // Per-tile digit counts at `shift`, digit-major (hist[d * ntiles + tile]).
 // With GATHER the keys are computed from the values (sort_keys_of) and
 // written to keys; vals_copy (optional) receives a copy of the values.
-// The table's entry of (digit d, tile): tile-major when the table is
-// scanned by k_scan_tiles, else digit-major (the chunked scan's flat order).
+// The table's entry of (digit d, tile): tile-major when the scatter scans
+// the table itself, else digit-major (the chunked scan's flat order).
 __device__ __forceinline__ int64_t hist_at(bool tile_major, int d, int64_t tile, int64_t ntiles) {
   return tile_major ? tile * 256 + d : static_cast<int64_t>(d) * ntiles + tile;
 }
@@ -458,7 +394,32 @@ __global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint3
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   if (base >= n) return;  // uniform over the workgroup
-  s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
+  if (tile_major) {
+    // The raw digit-by-tile counts (tile-major, at most kScanTilesMax
+    // tiles): thread t takes digit t. Its first output position is the
+    // count of smaller digits over all tiles plus the count of digit t in
+    // earlier tiles; every workgroup reads the whole table (one launch
+    // fewer per pass than scanning it in its own kernel).
+    constexpr int kBatch = 16;
+    int total = 0, before = 0;
+    for (int64_t j0 = 0; j0 < ntiles; j0 += kBatch) {
+      int c[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) c[j] = hist[min(j0 + j, ntiles - 1) * 256 + t];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int64_t tile = j0 + j;
+        const int v = tile < ntiles ? c[j] : 0;
+        total += v;
+        before += tile < static_cast<int64_t>(blockIdx.x) ? v : 0;
+      }
+    }
+    __shared__ int scan_lds[kWaves + 1];
+    int all;
+    s_off[t] = block_exclusive_scan<kBlock>(total, scan_lds, &all) + before;
+  } else {
+    s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
+  }
   // Every key and value of the thread's rounds is loaded before the first
   // round (one memory latency per tile, not one per round).
   constexpr int R = kTile / kBlock;
@@ -1354,7 +1315,7 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
   const int64_t ntiles = (d->n_max + kTile - 1) / kTile;
   int32_t* hist = d->hist;
   int32_t* scan_scratch = d->hist + 256 * ntiles;
-  const bool tile_major = ntiles <= kScanTilesMax;  // the table scan in one launch
+  const bool tile_major = ntiles <= kScanTilesMax;  // each scatter scans the table itself
   for (int k = 0; k < d->nkeys; ++k) {
     const plx_sort_key& key = d->keys[k];
     if (key.bits < 1 || key.bits > 32 || !key.a) return fail(PLX_ERR_INVALID, "plx_sort: bad key");
@@ -1376,9 +1337,8 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
       if (pass > 0)
         hipLaunchKernelGGL(k_radix_hist<false>, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, key,
                            nullptr, kin, nullptr, shift, ntiles, tile_major, hist);
-      if (tile_major) {
-        hipLaunchKernelGGL(k_scan_tiles, dim3(1), dim3(kScanLanes), 0, s, ntiles, hist);
-      } else {
+      // (a tile-major table is scanned by the scatter itself)
+      if (!tile_major) {
         const int rc = scan_or_compact(256 * ntiles, nullptr, -1, hist, hist, nullptr, scan_scratch, s, "plx_sort");
         if (rc != PLX_OK) return rc;
       }
