@@ -833,9 +833,31 @@ typedef struct plx_grow_claim_desc {
    * new tail start, *tail_dev + flags[3], so a caller can pass &flags[4] as
    * the next claim's tail_dev without reading anything on the host. */
   const int32_t* tail_dev;
+  /* Optional (null: none): every slot the claim fills is appended to
+   * claimed_out (in no particular order) at index atomicAdd(claimed_n, 1);
+   * the caller zeroes *claimed_n first. Appends at or past claimed_cap are
+   * not written, so the caller sizes it by a bound on the claims (the
+   * winners' budget). plx_claimed_split turns the list into each bucket's
+   * claimed slots in ascending order. */
+  int32_t* claimed_out;
+  int32_t* claimed_n;
+  int64_t claimed_cap;
 } plx_grow_claim_desc;
 
 PLX_EXPORT int plx_grow_claim(const plx_grow_claim_desc* d, void* stream);
+
+/* The claimed slots of plx_grow_claim's list, split by bucket and sorted:
+ * for bucket b (flat slots [offs[b], offs[b+1]); offs: nb + 1 int64 on the
+ * device), out[b * region + i] for i < counts[b] are its claimed slots less
+ * offs[b], ascending; counts[b] their number (at most region are written).
+ * The list holds min(*n_dev, cap) entries; cap <= PLX_CLAIMED_SPLIT_MAX.
+ * No counterpart in the reference, whose claim writes the bucket in place:
+ * it lets the merged relayout find the claimed slots without comparing DEAD
+ * before and after the claim over the whole bucket. */
+#define PLX_CLAIMED_SPLIT_MAX 4096
+PLX_EXPORT int plx_claimed_split(int64_t cap, const int32_t* n_dev, const int32_t* list, int32_t nb,
+                                 const int64_t* offs, int64_t region, int32_t* out, int32_t* counts,
+                                 void* stream);
 
 /* PIPELINE claim domains (phases.py:3040-3049): for the listed slots,
  * out[p] = level[clamp(ids[idx[p]], 0, bound - 1)], the level of each dead

@@ -153,10 +153,16 @@ class ChurnArena(Arena):
         self.t_name = None
         self.t_now = []
         nbits = max(1, int(n).bit_length())
+        claimed = None
+        if prev is not None and not isinstance(dead_before, (list, tuple)):
+            # the claim's list of the slots it filled (grow.ClaimedSlots):
+            # each bucket's, ascending, in one launch
+            out, counts = dead_before.split(k.lib, k.s)
+            claimed = [(out[b], counts[b : b + 1]) for b in range(nb)]
         for b, bucket in enumerate(conns):
             if prev is not None:
-                self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b],
-                                   None if dead_before is None else dead_before[b], claim_bound)
+                fresh = claimed[b] if claimed is not None else dead_before[b]
+                self._merge_bucket(k, b, prev, bucket, specs, nbits, rows, extent[b], fresh, claim_bound)
                 continue
             base, cap = self.bases[b], caps[b]
             dead = bucket[DEAD.name]
@@ -246,7 +252,8 @@ class ChurnArena(Arena):
         0) merged with the slots the claim turned live (``dead_before``: DEAD
         just before the claim, after the step's prunes were copied back).
         Nothing else changes the logical bucket in between, so these are all
-        of its live slots.
+        of its live slots. ``dead_before`` may instead be the claim's own list
+        of them: (ascending slots, device count), at most ``claim_bound``.
 
         The counts stay on the device. The launches are sized by host bounds:
         prev's bound on its live count and ``claim_bound``, a bound on the
@@ -268,9 +275,14 @@ class ChurnArena(Arena):
         # Survivors: prev's live positions still live, in (destination, slot) order.
         surv, nsurv_d = k.compact(old_bound, 1, prev.cols[DEAD.name][base:], n_dev=old_live_d)  # PLX_FLAG_U8_ZERO
         # New: the slots the claim filled (a slot that died this step may be
-        # among them: its old position is not a survivor).
-        claimed = (dead_before != 0) & (bucket[DEAD.name] == 0)
-        fresh, nnew_d = k.compact(cap, 0, claimed)  # PLX_FLAG_U8: ascending slots
+        # among them: its old position is not a survivor), ascending: listed
+        # by the claim (a (slots, count) pair), or the slots DEAD shows
+        # turned live.
+        if isinstance(dead_before, tuple):
+            fresh, nnew_d = dead_before
+        else:
+            claimed = (dead_before != 0) & (bucket[DEAD.name] == 0)
+            fresh, nnew_d = k.compact(cap, 0, claimed)  # PLX_FLAG_U8: ascending slots
         live_d = nsurv_d + nnew_d
         self.lives.append(bound)
         self.live_dev.append(live_d)
@@ -317,10 +329,14 @@ class ChurnArena(Arena):
         _side(m2.b, new_bound, cap, by_src, bucket[FROM_ID.name], None, None, nnew_d)
         m2.offset, m2.order = 0, lorder.data_ptr()
         _lib.check(lib.plx_merge_index(m2, k.s), "plx_merge_index")
-        pos = torch.full((bound + 1,), base, dtype=torch.int32, device=dev)
-        ldst = torch.zeros(bound + 1, dtype=torch.int32, device=dev)
-        lsrc = torch.zeros(max(bound, 1), dtype=torch.int32, device=dev)
-        lslot = torch.zeros(max(bound, 1), dtype=torch.int32, device=dev)
+        # The gather writes every rank below the bound (fill values past the
+        # count), so only the trailing entries (pos base, dst 0) are set here.
+        pos = torch.empty(bound + 1, dtype=torch.int32, device=dev)
+        ldst = torch.empty(bound + 1, dtype=torch.int32, device=dev)
+        pos[bound:].fill_(base)
+        ldst[bound:].fill_(0)
+        lsrc = torch.empty(bound, dtype=torch.int32, device=dev) if bound else torch.zeros(1, dtype=torch.int32, device=dev)
+        lslot = torch.empty(bound, dtype=torch.int32, device=dev) if bound else torch.zeros(1, dtype=torch.int32, device=dev)
         _gather(lib, k.s, bound, lorder, by_src, new_bound, old_bound, cap,
                 [(moved, new_pos, pos, 4, base), (old.dst, bucket[TO_ID.name], ldst, 4, 0),
                  (old.src, bucket[FROM_ID.name], lsrc, 4, 0), (old.slot, None, lslot, 4, 0)], n_dev=live_d)

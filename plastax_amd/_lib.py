@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 25  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 26  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -319,6 +319,7 @@ class plx_merge_desc(ctypes.Structure):
 
 
 PLX_MERGE_MAX_COLS = 12
+PLX_CLAIMED_SPLIT_MAX = 4096
 
 
 class plx_merge_col(ctypes.Structure):
@@ -462,6 +463,9 @@ class plx_grow_claim_desc(ctypes.Structure):
         ("growable_in", c_vp),
         ("dropped_out", c_vp),
         ("tail_dev", c_vp),
+        ("claimed_out", c_vp),
+        ("claimed_n", c_vp),
+        ("claimed_cap", c_i64),
     ]
 
 
@@ -537,6 +541,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_merge_index": (c_i32, [ctypes.POINTER(plx_merge_desc), c_vp]),
     "plx_merge_gather": (c_i32, [ctypes.POINTER(plx_merge_gather_desc), c_vp]),
     "plx_remap_i32": (c_i32, [c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "plx_claimed_split": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,

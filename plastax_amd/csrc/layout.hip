@@ -448,6 +448,40 @@ unsigned grid_of(int64_t n, int block) {
   return static_cast<unsigned>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
 }
 
+// plx_claimed_split: one workgroup per bucket keeps the listed slots in its
+// range (less its start), sorts them in LDS (absent entries sort last) and
+// writes the first min(count, region).
+static_assert(PLX_CLAIMED_SPLIT_MAX == kTileMax, "the split sorts one LDS tile");
+__global__ __launch_bounds__(kTB) void k_claimed_split(int64_t cap, const int32_t* n_dev, const int32_t* list,
+                                                      const int64_t* offs, int64_t region, int32_t* out,
+                                                      int32_t* counts) {
+  __shared__ uint32_t keys[kTileMax];
+  __shared__ int kept;
+  const int b = static_cast<int>(blockIdx.x);
+  const int64_t lo = offs[b], hi = offs[b + 1];
+  int64_t n = *n_dev;
+  n = n < 0 ? 0 : (n < cap ? n : cap);
+  if (threadIdx.x == 0) kept = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < kTileMax; i += kTB) {
+    uint32_t k = 0xFFFFFFFFu;
+    if (i < n) {
+      const int64_t v = list[i];
+      if (v >= lo && v < hi) {
+        k = static_cast<uint32_t>(v - lo);
+        atomicAdd(&kept, 1);
+      }
+    }
+    keys[i] = k;
+  }
+  __syncthreads();
+  bitonic4096(keys);
+  __syncthreads();
+  const int c = kept;
+  for (int64_t i = threadIdx.x; i < c && i < region; i += kTB) out[b * region + i] = static_cast<int32_t>(keys[i]);
+  if (threadIdx.x == 0) counts[b] = c;
+}
+
 }  // namespace
 
 extern "C" {
@@ -552,6 +586,18 @@ int plx_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nb
   hipLaunchKernelGGL(k_count_ids, dim3(grid_of(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream), n, ids, skip,
                      nbins, counts);
   return check_launch("plx_count_ids");
+}
+
+int plx_claimed_split(int64_t cap, const int32_t* n_dev, const int32_t* list, int32_t nb, const int64_t* offs,
+                      int64_t region, int32_t* out, int32_t* counts, void* stream) {
+  if (cap < 0 || nb < 0 || region < 0) return fail(PLX_ERR_INVALID, "plx_claimed_split: negative size");
+  if (cap > PLX_CLAIMED_SPLIT_MAX) return fail(PLX_ERR_UNSUPPORTED, "plx_claimed_split: cap above PLX_CLAIMED_SPLIT_MAX");
+  if (nb == 0) return PLX_OK;
+  if (!n_dev || !offs || !counts || (cap > 0 && !list) || (region > 0 && !out))
+    return fail(PLX_ERR_INVALID, "plx_claimed_split: null pointer");
+  hipLaunchKernelGGL(k_claimed_split, dim3(static_cast<unsigned>(nb)), dim3(kTB), 0, static_cast<hipStream_t>(stream),
+                     cap, n_dev, list, offs, region, out, counts);
+  return check_launch("plx_claimed_split");
 }
 
 }  // extern "C"

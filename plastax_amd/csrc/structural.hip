@@ -731,6 +731,10 @@ __global__ void k_claim_write(plx_grow_claim_desc d, const int32_t* g, const int
     }
     atomicAdd(&d.flags[0], 1);
     if (d.level[b] <= lvl) atomicOr(&d.flags[2], 1);
+    if (d.claimed_out) {
+      const int i = atomicAdd(d.claimed_n, 1);
+      if (i < d.claimed_cap) d.claimed_out[i] = static_cast<int32_t>(slot);
+    }
     d.from_id[slot] = a;
     d.to_id[slot] = b;
     d.dead[slot] = 0;

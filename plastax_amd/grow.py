@@ -258,6 +258,36 @@ class Remainder:
     nseg: int
 
 
+_OFFS_CACHE: dict[tuple, torch.Tensor] = {}
+
+
+class ClaimedSlots:
+    """The flat slots a claim filled, appended in no particular order
+    (``plx_grow_claim``'s claimed_out): ``count`` (device int32) of them in
+    ``slots``, at most ``bound``; ``offs`` are the buckets' flat starts.
+    ``split`` sorts them into each bucket's ascending relative slots."""
+
+    def __init__(self, slots: torch.Tensor, count: torch.Tensor, bound: int, offs: list[int]) -> None:
+        self.slots, self.count, self.bound, self.offs = slots, count, int(bound), list(offs)
+
+    def split(self, lib: Any, stream: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """(out [nb, max(bound, 1)], counts [nb]): bucket b's claimed slots
+        less its start, ascending, in out[b, :counts[b]]."""
+        dev = self.slots.device
+        nb = len(self.offs) - 1
+        region = max(self.bound, 1)
+        out = torch.empty((nb, region), dtype=torch.int32, device=dev)
+        counts = torch.empty(nb, dtype=torch.int32, device=dev)
+        key = (tuple(self.offs), dev)
+        offs = _OFFS_CACHE.get(key)
+        if offs is None:  # (one host-to-device copy per arena shape, not per step)
+            offs = _OFFS_CACHE[key] = torch.tensor(self.offs, dtype=torch.int64, device=dev)
+        _lib.check(lib.plx_claimed_split(self.bound, self.count.data_ptr(), self.slots.data_ptr(), nb,
+                                         offs.data_ptr(), region, out.data_ptr(), counts.data_ptr(), stream),
+                   "plx_claimed_split")
+        return out, counts
+
+
 class GrowthOutcome:
     """A growth phase's result: the new buckets, whether it ran, and its
     flags. A claim leaves the flags on the device (``flags``: int32 grown,
@@ -419,9 +449,23 @@ class AddConnPhase:
         self._tail_hint: tuple[torch.Tensor, int] | None = None
         # a bound on the slots the last claim filled (sizes the next relayout)
         self.claim_bound: int | None = None
+        # set by the caller: the claim also lists the slots it fills
+        # (ClaimedSlots, for a merged relayout; None when the bound is too
+        # large for plx_claimed_split or the list was not asked for)
+        self.want_claimed = False
+        self.claimed: ClaimedSlots | None = None
         # (a level column, a bound on its deepest level): read once, then
         # carried through the add_unit phases that derive new columns
         self._level_hint: tuple[torch.Tensor, int] | None = None
+
+    def claims_listable(self) -> bool:
+        """Whether the claim's filled slots can be listed for a merged
+        relayout: a bound on them known before the phase runs fits
+        plx_claimed_split (the step cap, or k for a step-scope selection)."""
+        cfg = self.cfg
+        cap = _lib.PLX_CLAIMED_SPLIT_MAX
+        return bool(cfg.max_new_per_step and int(cfg.max_new_per_step) <= cap) or \
+            bool(cfg.step_scope and int(cfg.k) <= cap)
 
     def level_bound(self, level: torch.Tensor) -> int:
         """A bound on the deepest level of ``level``: the carried one when
@@ -716,12 +760,19 @@ class AddConnPhase:
         scratch = k.mem.i32(8 * nc + int(k.lib.plx_scratch_ints(nc)))
         c.flags, c.scratch = flags.data_ptr(), scratch.data_ptr()
         c.growable_in, c.dropped_out = _ptr(growable_in), rem.dropped.data_ptr()
-        _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
         # claims are winners: a bound on the slots this claim can fill
         winners_max = max(0, nseg * int(cfg.k) if not cfg.step_scope else int(cfg.k))
         if cfg.max_new_per_step:
             winners_max = min(winners_max, int(cfg.max_new_per_step))
         self.claim_bound = min(winners_max, nc)
+        self.claimed = None
+        if self.want_claimed and self.claim_bound <= _lib.PLX_CLAIMED_SPLIT_MAX:
+            # the filled slots, appended by the claim (for a merged relayout)
+            lst = k.mem.i32(max(self.claim_bound, 1))
+            cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+            c.claimed_out, c.claimed_n, c.claimed_cap = lst.data_ptr(), cnt.data_ptr(), self.claim_bound
+            self.claimed = ClaimedSlots(lst, cnt, self.claim_bound, offs)
+        _lib.check(k.lib.plx_grow_claim(c, k.s), "plx_grow_claim")
         if tail_dev is not None:
             # the new tail (flags[4]) is at most the old bound plus the winners
             self._tail_hint = (flags, span + self.claim_bound)

@@ -421,10 +421,16 @@ class StepFn:
                 return
             conns = state.conns  # the logical view, in step with the arena
             prev = state._arena
-            before = None
+            before: Any = None
+            listed = False
             if getattr(prev, "churn", False):
-                # DEAD before the claim: the claimed slots are the ones it turns live
-                before = [bucket[DEAD.name].clone() for bucket in conns]
+                if phase.claims_listable():
+                    # the claim lists the slots it fills (grow.ClaimedSlots)
+                    listed = phase.want_claimed = True
+                else:
+                    # DEAD before the claim: the claimed slots are the ones it turns live
+                    before = [bucket[DEAD.name].clone() for bucket in conns]
+            phase.claimed = None
             # The flags stay on the device from step to step: the tail start
             # (PIPELINE) and needs_resort go in as the last claim's device
             # values, and this claim's flags are read only when the caller
@@ -435,7 +441,10 @@ class StepFn:
             out = phase.run(k, state.units, conns, step=int(state.step), globals_=g, tail_start=tail,
                             units_added=added,
                             needs_resort=resort_src if resort_src is not None else bool(state.needs_resort))
+            phase.want_claimed = False
             state.conns = out.conns
+            if listed:
+                before = phase.claimed  # (None: not listed; the next layout is built afresh)
             if before is not None:
                 # the next layout merges the claimed slots into prev's, sized
                 # by the claim's bound on them (its winner budget)

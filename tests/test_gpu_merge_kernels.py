@@ -1,8 +1,8 @@
-"""plx_merge_index / plx_merge_gather / plx_remap_i32 through the C ABI
-against numpy: two sorted id lists merged by (key1, key2) (a first on equal
-keys), the order and both maps; a multi-column gather from the two sides;
+"""plx_merge_index / plx_merge_gather / plx_remap_i32 / plx_claimed_split
+through the C ABI against numpy: two sorted id lists merged by (key1, key2)
+(a first on equal keys), the order and both maps; a multi-column gather from the two sides;
 short b (keys staged in LDS) and long b (searched in global memory), empty
-sides, ties across the sides."""
+sides, ties across the sides; a claim's slot list split by bucket."""
 
 from __future__ import annotations
 
@@ -184,3 +184,42 @@ def test_merge_with_device_counts(na: int, nb: int, pad_a: int, pad_b: int) -> N
                                  start.data_ptr(), None) == 0
     torch.cuda.synchronize()
     assert np.array_equal(start.cpu().numpy(), np.searchsorted(keys_s[:cnt], np.arange(51), side="left"))
+
+
+@pytest.mark.parametrize("caps,nlisted,cap,region", [
+    ([100, 0, 37, 513], 40, 64, 64),        # an empty bucket, a short list
+    ([4096], 4096, 4096, 4096),             # one bucket, the largest list
+    ([50, 50, 50], 20, 32, 8),              # a region shorter than a bucket's count
+    ([10, 20], 0, 16, 16),                  # nothing claimed
+    ([3000, 5000], 100, 128, 128),          # the device count past cap
+])
+def test_claimed_split(caps, nlisted, cap, region) -> None:
+    """plx_claimed_split against numpy: each bucket's listed slots less its
+    start, ascending, the first `region` of them, and their count."""
+    rng = np.random.default_rng(sum(caps) + nlisted)
+    offs = np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
+    total = int(offs[-1])
+    listed = rng.choice(total, size=min(nlisted, total), replace=False).astype(np.int32)
+    buf = np.full(max(cap, 1), -7, np.int32)
+    n_dev = min(nlisted, len(listed))
+    buf[: min(n_dev, cap)] = listed[: min(n_dev, cap)]
+    if caps == [3000, 5000]:
+        n_dev = cap + 50  # appends past cap were never written: only cap entries count
+    nb = len(caps)
+    out = torch.full((nb, max(region, 1)), -1, dtype=torch.int32, device=DEV)
+    counts = torch.full((nb,), -1, dtype=torch.int32, device=DEV)
+    lst, nd, offs_t = _t(buf), _t(np.array([n_dev], np.int32)), _t(offs)
+    _lib.call("plx_claimed_split", cap, nd.data_ptr(), lst.data_ptr(), nb, offs_t.data_ptr(), region,
+              out.data_ptr(), counts.data_ptr(), None)
+    torch.cuda.synchronize()
+    got_out, got_counts = out.cpu().numpy(), counts.cpu().numpy()
+    seen = buf[: min(n_dev, cap)]
+    for b in range(nb):
+        want = np.sort(seen[(seen >= offs[b]) & (seen < offs[b + 1])] - offs[b])
+        assert got_counts[b] == want.size, f"bucket {b}: count"
+        k = min(want.size, region)
+        assert np.array_equal(got_out[b, :k], want[:k]), f"bucket {b}: slots"
+        assert np.all(got_out[b, k:] == -1), f"bucket {b}: wrote past its slots"
+    with pytest.raises(_lib.PlxError):
+        _lib.call("plx_claimed_split", 4097, nd.data_ptr(), lst.data_ptr(), nb, offs_t.data_ptr(), region,
+                  out.data_ptr(), counts.data_ptr(), None)
