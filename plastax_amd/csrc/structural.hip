@@ -161,13 +161,45 @@ __global__ void k_scan_single(int64_t m, int32_t* sums, int32_t* total) {
   if (threadIdx.x == 0 && total) *total = run;
 }
 
+// With `fused`, sums[0, nc) are the raw chunk totals (not scanned): the
+// workgroup of chunk c adds up those before c itself (nc <= kFusedChunks:
+// at most 8 loads per thread), and chunk 0's workgroup writes the grand
+// total. This saves the scan launch between the two passes.
+constexpr int64_t kFusedChunks = 2048;
+__device__ __forceinline__ int chunk_base(const int32_t* sums, int64_t nc, bool fused, int* lds,
+                                          int32_t* total) {
+  if (!fused) return sums[blockIdx.x];
+  constexpr int kPer = static_cast<int>(kFusedChunks / kBlock);
+  int v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t j = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+    v[i] = j < nc ? sums[j] : 0;
+  }
+  int before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t j = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+    all += v[i];
+    before += j < static_cast<int64_t>(blockIdx.x) ? v[i] : 0;
+  }
+  int sum_before, sum_all;
+  block_exclusive_scan<kBlock>(before, lds, &sum_before);
+  block_exclusive_scan<kBlock>(all, lds, &sum_all);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && total) *total = sum_all;
+  return sum_before;
+}
+
 __global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t* in, int32_t* out,
-                             const int32_t* sums) {
+                             const int32_t* sums, bool fused, int64_t nc, int32_t* total) {
   __shared__ int lds[kWaves + 1];
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
-  if (base >= n) return;  // uniform over the workgroup: the chunk is past the count
-  int run = sums[blockIdx.x];
+  if (base >= n) {  // uniform over the workgroup: the chunk is past the count
+    if (fused && blockIdx.x == 0 && threadIdx.x == 0 && total) *total = 0;  // (n == 0)
+    return;
+  }
+  int run = chunk_base(sums, nc, fused, lds, total);
   constexpr int R = kChunk / kBlock;
   int vals[R];
   chunk_values<R>(-1, in, base, n, vals);
@@ -184,12 +216,16 @@ __global__ void k_chunk_scan(int64_t n_max, const int32_t* n_dev, const int32_t*
 }
 
 __global__ void k_chunk_compact(int64_t n_max, const int32_t* n_dev, int32_t mode, const void* flags,
-                                int32_t* out, const int32_t* sums) {
+                                int32_t* out, const int32_t* sums, bool fused, int64_t nc, int32_t* total) {
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
   __shared__ int wcnt[kWaves];
-  if (base >= n) return;  // uniform over the workgroup: the chunk is past the count
-  int run = sums[blockIdx.x];
+  __shared__ int lds[kWaves + 1];
+  if (base >= n) {  // uniform over the workgroup: the chunk is past the count
+    if (fused && blockIdx.x == 0 && threadIdx.x == 0 && total) *total = 0;  // (n == 0)
+    return;
+  }
+  int run = chunk_base(sums, nc, fused, lds, total);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   constexpr int R = kChunk / kBlock;
   int fv[R];
@@ -237,13 +273,16 @@ int scan_or_compact(int64_t n_max, const int32_t* n_dev, int32_t mode, const voi
     return check_launch(what);
   }
   hipLaunchKernelGGL(k_chunk_sums, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev, mode, in, scratch);
-  hipLaunchKernelGGL(k_scan_single, dim3(1), dim3(kScanLanes), 0, s, nc, scratch, total);
+  // Up to kFusedChunks chunks the second pass adds up the chunk totals
+  // itself; beyond, one workgroup scans them in between.
+  const bool fused = nc <= kFusedChunks;
+  if (!fused) hipLaunchKernelGGL(k_scan_single, dim3(1), dim3(kScanLanes), 0, s, nc, scratch, total);
   if (mode < 0)
     hipLaunchKernelGGL(k_chunk_scan, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev,
-                       static_cast<const int32_t*>(in), out, scratch);
+                       static_cast<const int32_t*>(in), out, scratch, fused, nc, total);
   else
     hipLaunchKernelGGL(k_chunk_compact, dim3(nc), dim3(kBlock), 0, s, n_max, n_dev, mode, in, out,
-                       scratch);
+                       scratch, fused, nc, total);
   return check_launch(what);
 }
 
