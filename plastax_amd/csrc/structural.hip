@@ -371,21 +371,30 @@ __device__ __forceinline__ int64_t hist_at(bool tile_major, int d, int64_t tile,
   return tile_major ? tile * 256 + d : static_cast<int64_t>(d) * ntiles + tile;
 }
 
-// Each thread issues every load of its kTile / kBlock elements before using
-// any (one memory latency per tile, not one per round).
+// The radix kernels run kSortBlock threads per tile of kTile elements: R =
+// 4 rounds of one element per thread. Each thread issues every load of its
+// R elements before using any (one memory latency per tile, not one per
+// round); the per-digit work (counters, the tile's digit offsets, the scan
+// across the waves of a round) takes the first 256 threads.
+constexpr int kSortBlock = 1024;
+constexpr int kSortWaves = kSortBlock / 64;
+static_assert(kTile % kSortBlock == 0, "a radix tile is whole rounds");
+
 template <bool GATHER>
-__global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key key, const uint32_t* vals,
-                             uint32_t* keys, uint32_t* vals_copy, int shift, int64_t ntiles, bool tile_major,
-                             int32_t* hist) {
-  constexpr int R = kTile / kBlock;
+__global__ __launch_bounds__(kSortBlock) void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key key,
+                                                           const uint32_t* vals, uint32_t* keys,
+                                                           uint32_t* vals_copy, int shift, int64_t ntiles,
+                                                           bool tile_major, int32_t* hist) {
+  constexpr int R = kTile / kSortBlock;
   __shared__ int h[256];
+  const int t = threadIdx.x;
   const int64_t n = live_count(n_max, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   if (base >= n) {  // a tile past the count has no element (uniform over the workgroup)
-    hist[hist_at(tile_major, threadIdx.x, blockIdx.x, ntiles)] = 0;
+    if (t < 256) hist[hist_at(tile_major, t, blockIdx.x, ntiles)] = 0;
     return;
   }
-  h[threadIdx.x] = 0;
+  if (t < 256) h[t] = 0;
   uint32_t k[R];
   if (GATHER) {
     uint32_t idx[R];
@@ -393,14 +402,14 @@ __global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key k
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       // (positions past the count read the last element: a valid index)
-      const int64_t p = base + r * kBlock + threadIdx.x;
+      const int64_t p = base + r * kSortBlock + t;
       ok[r] = p < n;
       idx[r] = vals[ok[r] ? p : n - 1];
     }
     sort_keys_of<R>(key, idx, ok, k);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t p = base + r * kBlock + threadIdx.x;
+      const int64_t p = base + r * kSortBlock + t;
       if (ok[r]) {
         keys[p] = k[r];
         if (vals_copy) vals_copy[p] = idx[r];
@@ -410,71 +419,75 @@ __global__ void k_radix_hist(int64_t n_max, const int32_t* n_dev, plx_sort_key k
     uint32_t kv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t p = base + r * kBlock + threadIdx.x;
+      const int64_t p = base + r * kSortBlock + t;
       kv[r] = keys[p < n ? p : n - 1];
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) k[r] = base + r * kBlock + threadIdx.x < n ? kv[r] : 0u;
+    for (int r = 0; r < R; ++r) k[r] = base + r * kSortBlock + t < n ? kv[r] : 0u;
   }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    if (base + r * kBlock + threadIdx.x < n) atomicAdd(&h[(k[r] >> shift) & 255u], 1);
+    if (base + r * kSortBlock + t < n) atomicAdd(&h[(k[r] >> shift) & 255u], 1);
   __syncthreads();
-  hist[hist_at(tile_major, threadIdx.x, blockIdx.x, ntiles)] = h[threadIdx.x];
+  if (t < 256) hist[hist_at(tile_major, t, blockIdx.x, ntiles)] = h[t];
 }
 
-__global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint32_t* keys_in,
-                                const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
-                                int shift, int64_t ntiles, bool tile_major, const int32_t* hist) {
+__global__ __launch_bounds__(kSortBlock) void k_radix_scatter(int64_t n_max, const int32_t* n_dev,
+                                                              const uint32_t* keys_in, const uint32_t* vals_in,
+                                                              uint32_t* keys_out, uint32_t* vals_out, int shift,
+                                                              int64_t ntiles, bool tile_major,
+                                                              const int32_t* hist) {
   __shared__ int s_off[256];
-  __shared__ int s_wcnt[kWaves][256];
+  __shared__ int s_wcnt[kSortWaves][256];
+  __shared__ int scan_lds[kSortWaves + 1];
   const int64_t n = live_count(n_max, n_dev);
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   if (base >= n) return;  // uniform over the workgroup
-  if (tile_major) {
-    // The raw digit-by-tile counts (tile-major, at most kScanTilesMax
-    // tiles): thread t takes digit t. Its first output position is the
-    // count of smaller digits over all tiles plus the count of digit t in
-    // earlier tiles; every workgroup reads the whole table (one launch
-    // fewer per pass than scanning it in its own kernel).
-    constexpr int kBatch = 16;
-    int total = 0, before = 0;
-    for (int64_t j0 = 0; j0 < ntiles; j0 += kBatch) {
-      int c[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) c[j] = hist[min(j0 + j, ntiles - 1) * 256 + t];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int64_t tile = j0 + j;
-        const int v = tile < ntiles ? c[j] : 0;
-        total += v;
-        before += tile < static_cast<int64_t>(blockIdx.x) ? v : 0;
-      }
-    }
-    __shared__ int scan_lds[kWaves + 1];
-    int all;
-    s_off[t] = block_exclusive_scan<kBlock>(total, scan_lds, &all) + before;
-  } else {
-    s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
-  }
-  // Every key and value of the thread's rounds is loaded before the first
-  // round (one memory latency per tile, not one per round).
-  constexpr int R = kTile / kBlock;
+  // Every key and value of the thread's rounds is loaded first.
+  constexpr int R = kTile / kSortBlock;
   uint32_t kr[R], vr[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t p = base + r * kBlock + t;
+    const int64_t p = base + r * kSortBlock + t;
     kr[r] = keys_in[p < n ? p : n - 1];  // (past the count: read but unused)
     vr[r] = vals_in[p < n ? p : n - 1];
   }
+  if (tile_major) {
+    // The raw digit-by-tile counts (tile-major, at most kScanTilesMax
+    // tiles): thread t < 256 takes digit t. Its first output position is
+    // the count of smaller digits over all tiles plus the count of digit t
+    // in earlier tiles; every workgroup reads the whole table (one launch
+    // fewer per pass than scanning it in its own kernel).
+    constexpr int kBatch = 16;
+    int total = 0, before = 0;
+    if (t < 256) {
+      for (int64_t j0 = 0; j0 < ntiles; j0 += kBatch) {
+        int c[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) c[j] = hist[min(j0 + j, ntiles - 1) * 256 + t];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int64_t tile = j0 + j;
+          const int v = tile < ntiles ? c[j] : 0;
+          total += v;
+          before += tile < static_cast<int64_t>(blockIdx.x) ? v : 0;
+        }
+      }
+    }
+    int all;
+    const int ex = block_exclusive_scan<kSortBlock>(total, scan_lds, &all);
+    if (t < 256) s_off[t] = ex + before;
+  } else if (t < 256) {
+    s_off[t] = hist[hist_at(tile_major, t, blockIdx.x, ntiles)];
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if (base + r * kBlock >= n) break;  // uniform: the rest of the tile is past the count
-    for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
+    if (base + r * kSortBlock >= n) break;  // uniform: the rest of the tile is past the count
+    for (int i = t; i < kSortWaves * 256; i += kSortBlock) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
-    const int64_t p = base + r * kBlock + t;
+    const int64_t p = base + r * kSortBlock + t;
     const bool valid = p < n;
     const uint32_t key = kr[r];
     const uint32_t val = vr[r];
@@ -489,9 +502,9 @@ __global__ void k_radix_scatter(int64_t n_max, const int32_t* n_dev, const uint3
     const int lrank = __popcll(peers & lanemask_lt());
     if (valid && lane == __ffsll(static_cast<long long>(peers)) - 1) s_wcnt[wave][d] = __popcll(peers);
     __syncthreads();
-    {
+    if (t < 256) {
       int run = s_off[t];
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < kSortWaves; ++w) {
         const int c = s_wcnt[w][t];
         s_wcnt[w][t] = run;
         run += c;
@@ -1369,7 +1382,7 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
     // reads them there, so the last pass writes its order into vals.
     const int passes = (key.bits + 7) / 8;
     const bool odd = passes & 1;
-    hipLaunchKernelGGL(k_radix_hist<true>, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, key, d->vals,
+    hipLaunchKernelGGL(k_radix_hist<true>, dim3(ntiles), dim3(kSortBlock), 0, s, d->n_max, d->n_dev, key, d->vals,
                        d->keys_buf, odd ? d->vals_alt : nullptr, 0, ntiles, tile_major, hist);
     uint32_t* kin = d->keys_buf;
     uint32_t* vin = odd ? d->vals_alt : d->vals;
@@ -1378,14 +1391,14 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
     for (int pass = 0; pass < passes; ++pass) {
       const int shift = 8 * pass;
       if (pass > 0)
-        hipLaunchKernelGGL(k_radix_hist<false>, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, key,
+        hipLaunchKernelGGL(k_radix_hist<false>, dim3(ntiles), dim3(kSortBlock), 0, s, d->n_max, d->n_dev, key,
                            nullptr, kin, nullptr, shift, ntiles, tile_major, hist);
       // (a tile-major table is scanned by the scatter itself)
       if (!tile_major) {
         const int rc = scan_or_compact(256 * ntiles, nullptr, -1, hist, hist, nullptr, scan_scratch, s, "plx_sort");
         if (rc != PLX_OK) return rc;
       }
-      hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kBlock), 0, s, d->n_max, d->n_dev, kin, vin, kout,
+      hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kSortBlock), 0, s, d->n_max, d->n_dev, kin, vin, kout,
                          vout, shift, ntiles, tile_major, hist);
       uint32_t* t = kin;
       kin = kout;
