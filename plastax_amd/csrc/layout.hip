@@ -449,9 +449,13 @@ unsigned grid_of(int64_t n, int block) {
 }
 
 // plx_claimed_split: one workgroup per bucket keeps the listed slots in its
-// range (less its start), sorts them in LDS (absent entries sort last) and
-// writes the first min(count, region).
+// range (less its start) and writes the first min(count, region) of them in
+// ascending order. The slots are distinct, so up to kSplitRank listed
+// entries each one's rank is the number of smaller ones (a broadcast LDS
+// loop); longer lists sort in LDS (bitonic over the next power of two;
+// absent entries sort last).
 static_assert(PLX_CLAIMED_SPLIT_MAX == kTileMax, "the split sorts one LDS tile");
+constexpr int kSplitRank = 1024;
 __global__ __launch_bounds__(kTB) void k_claimed_split(int64_t cap, const int32_t* n_dev, const int32_t* list,
                                                       const int64_t* offs, int64_t region, int32_t* out,
                                                       int32_t* counts) {
@@ -459,11 +463,13 @@ __global__ __launch_bounds__(kTB) void k_claimed_split(int64_t cap, const int32_
   __shared__ int kept;
   const int b = static_cast<int>(blockIdx.x);
   const int64_t lo = offs[b], hi = offs[b + 1];
-  int64_t n = *n_dev;
-  n = n < 0 ? 0 : (n < cap ? n : cap);
+  int64_t nl = *n_dev;
+  const int n = static_cast<int>(nl < 0 ? 0 : (nl < cap ? nl : cap));
+  int p2 = 1;
+  while (p2 < n) p2 <<= 1;
   if (threadIdx.x == 0) kept = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < kTileMax; i += kTB) {
+  for (int i = threadIdx.x; i < p2; i += kTB) {
     uint32_t k = 0xFFFFFFFFu;
     if (i < n) {
       const int64_t v = list[i];
@@ -475,10 +481,35 @@ __global__ __launch_bounds__(kTB) void k_claimed_split(int64_t cap, const int32_
     keys[i] = k;
   }
   __syncthreads();
-  bitonic4096(keys);
-  __syncthreads();
   const int c = kept;
-  for (int64_t i = threadIdx.x; i < c && i < region; i += kTB) out[b * region + i] = static_cast<int32_t>(keys[i]);
+  int32_t* o = out + static_cast<int64_t>(b) * region;
+  if (n <= kSplitRank) {
+    for (int i = threadIdx.x; i < n; i += kTB) {
+      const uint32_t k = keys[i];
+      if (k == 0xFFFFFFFFu) continue;
+      int r = 0;
+      for (int j = 0; j < n; ++j) r += keys[j] < k ? 1 : 0;
+      if (r < region) o[r] = static_cast<int32_t>(k);
+    }
+  } else {
+    for (int k = 2; k <= p2; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = threadIdx.x; i < p2; i += kTB) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint32_t x = keys[i], y = keys[ixj];
+            const bool up = (i & k) == 0;
+            if ((x > y) == up) {
+              keys[i] = y;
+              keys[ixj] = x;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int64_t i = threadIdx.x; i < c && i < region; i += kTB) o[i] = static_cast<int32_t>(keys[i]);
+  }
   if (threadIdx.x == 0) counts[b] = c;
 }
 

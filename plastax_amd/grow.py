@@ -458,14 +458,25 @@ class AddConnPhase:
         # carried through the add_unit phases that derive new columns
         self._level_hint: tuple[torch.Tensor, int] | None = None
 
-    def claims_listable(self) -> bool:
+    def claims_listable(self, level: torch.Tensor) -> bool:
         """Whether the claim's filled slots can be listed for a merged
-        relayout: a bound on them known before the phase runs fits
-        plx_claimed_split (the step cap, or k for a step-scope selection)."""
+        relayout: the bound on them the claim will use (its winners' budget,
+        ``claim_bound``), known now without a host read, fits
+        plx_claimed_split. ``level``: the level column the phase will run
+        with (PIPELINE: its carried bound gives the segments)."""
         cfg = self.cfg
-        cap = _lib.PLX_CLAIMED_SPLIT_MAX
-        return bool(cfg.max_new_per_step and int(cfg.max_new_per_step) <= cap) or \
-            bool(cfg.step_scope and int(cfg.k) <= cap)
+        if cfg.step_scope:
+            bound = int(cfg.k)
+        elif cfg.pipeline:
+            hint = self._level_hint
+            if hint is None or hint[0] is not level:
+                return False
+            bound = (int(hint[1]) + 1) * int(cfg.k)
+        else:
+            bound = int(cfg.num_buckets) * int(cfg.k)
+        if cfg.max_new_per_step:
+            bound = min(bound, int(cfg.max_new_per_step))
+        return max(0, bound) <= _lib.PLX_CLAIMED_SPLIT_MAX
 
     def level_bound(self, level: torch.Tensor) -> int:
         """A bound on the deepest level of ``level``: the carried one when

@@ -424,7 +424,7 @@ class StepFn:
             before: Any = None
             listed = False
             if getattr(prev, "churn", False):
-                if phase.claims_listable():
+                if phase.claims_listable(state.units["level"]):
                     # the claim lists the slots it fills (grow.ClaimedSlots)
                     listed = phase.want_claimed = True
                 else:
