@@ -521,6 +521,48 @@ __global__ __launch_bounds__(kSortBlock) void k_radix_scatter(int64_t n_max, con
   }
 }
 
+// A sort of at most kSortSmall elements in one workgroup and one launch:
+// each element's key tuple (every key masked to its bits) goes to LDS, and
+// its rank is the number of elements before it in the order the LSD passes
+// give (the last key most significant; equal tuples keep their positions).
+constexpr int kSortSmall = 1024;
+__global__ __launch_bounds__(kSortSmall) void k_sort_small(int64_t n_max, const int32_t* n_dev,
+                                                           plx_sort_desc d) {
+  __shared__ uint32_t kt[6][kSortSmall];
+  const int t = threadIdx.x;
+  const int n = static_cast<int>(live_count(n_max, n_dev));
+  // Nothing to sort (uniform). Below, threads past the count compute their
+  // keys at vals[0], a listed element, so every key load stays in bounds:
+  // with no element, vals[0] is not one.
+  if (n == 0) return;
+  const bool ok = t < n;
+  const uint32_t v = ok ? d.vals[t] : 0u;
+  for (int q = 0; q < d.nkeys; ++q) {
+    const plx_sort_key& key = d.keys[q];
+    uint32_t k;
+    const uint32_t idx[1] = {ok ? v : d.vals[0]};
+    const bool okk[1] = {ok};
+    sort_keys_of<1>(key, idx, okk, &k);
+    const uint32_t mask = key.bits >= 32 ? 0xFFFFFFFFu : ((1u << key.bits) - 1u);
+    kt[q][t] = k & mask;
+  }
+  __syncthreads();
+  int rank = 0;
+  if (ok) {
+    for (int j = 0; j < n; ++j) {
+      if (j == t) continue;
+      int cmp = 0;  // -1: j before t, 1: t before j
+      for (int q = d.nkeys - 1; q >= 0 && cmp == 0; --q) {
+        const uint32_t a = kt[q][j], b = kt[q][t];
+        cmp = a < b ? -1 : (a > b ? 1 : 0);
+      }
+      rank += (cmp < 0 || (cmp == 0 && j < t)) ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  if (ok) d.vals[rank] = v;
+}
+
 int grid_for(int64_t n) {
   const int64_t g = (n + kBlock - 1) / kBlock;
   return static_cast<int>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -1368,6 +1410,16 @@ int plx_sort(const plx_sort_desc* d, void* stream) {
     return fail(PLX_ERR_INVALID, "plx_sort: null buffer");
   if (d->n_max > (int64_t(1) << 31) - 1) return fail(PLX_ERR_UNSUPPORTED, "plx_sort: more than 2^31 - 1 elements");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->n_max <= kSortSmall) {
+    for (int k = 0; k < d->nkeys; ++k) {
+      const plx_sort_key& key = d->keys[k];
+      if (key.bits < 1 || key.bits > 32 || !key.a) return fail(PLX_ERR_INVALID, "plx_sort: bad key");
+      if ((key.kind == PLX_KEY_LEVEL_OF || key.kind == PLX_KEY_PAIR16 || key.kind == PLX_KEY_DEADMAX) && !key.b)
+        return fail(PLX_ERR_INVALID, "plx_sort: key needs its second column");
+    }
+    if (d->nkeys > 0) hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(kSortSmall), 0, s, d->n_max, d->n_dev, *d);
+    return check_launch("plx_sort");
+  }
   const int64_t ntiles = (d->n_max + kTile - 1) / kTile;
   int32_t* hist = d->hist;
   int32_t* scan_scratch = d->hist + 256 * ntiles;

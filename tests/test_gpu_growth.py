@@ -108,10 +108,11 @@ def test_compact_and_scan(n: int) -> None:
     assert int(total.item()) == int(v.sum())
 
 
-@pytest.mark.parametrize("n", [1, 4095, 4097, 100000])
+@pytest.mark.parametrize("n", [1, 700, 1024, 1025, 4095, 4097, 100000])
 def test_radix_sort_is_the_total_order(n: int) -> None:
     """(-score, src, dst, index) with ties, NaN, +-0 and +-inf, against
-    numpy's lexsort (the oracle's total_order)."""
+    numpy's lexsort (the oracle's total_order); up to 1,024 elements the
+    one-workgroup sort, beyond it the radix passes."""
     rng = np.random.default_rng(n + 7)
     k = _kernels()
     score = rng.choice(np.array([0.5, -0.0, 0.0, np.inf, -np.inf, np.nan, 1.25, -3.0], np.float32), n)
@@ -122,6 +123,29 @@ def test_radix_sort_is_the_total_order(n: int) -> None:
     order = k.iota(n)
     k.sort(order, n, [(0, 17, dst_t, None), (0, 9, src_t, None), (1, 32, s_t, None)])
     assert np.array_equal(order[:n].cpu().numpy(), og.total_order(score, src, dst))
+
+
+def test_small_sort_with_device_counts() -> None:
+    """The one-workgroup sort (at most 1,024 elements) with a device count:
+    the first count elements are sorted stably, the rest of the list is left
+    as it was; with a count of 0 nothing is read (the entries past the count
+    here are far outside the key column)."""
+    k = _kernels()
+    rng = np.random.default_rng(3)
+    n_max = 900
+    keys_np = rng.integers(0, 50, 5000).astype(np.int32)
+    keys = torch.from_numpy(keys_np).to(DEV)
+    base = rng.permutation(5000)[:n_max].astype(np.int32)
+    for cnt in (0, 1, 517, n_max):
+        v = base.copy()
+        v[cnt:] = 2_000_000_000
+        vt = torch.from_numpy(v).to(DEV)
+        nd = torch.tensor([cnt], dtype=torch.int32, device=DEV)
+        k.sort(vt, n_max, [(0, 6, keys, None)], n_dev=nd)
+        got = vt.cpu().numpy()
+        head = v[:cnt]
+        assert np.array_equal(got[:cnt], head[np.argsort(keys_np[head], kind="stable")]), f"count {cnt}"
+        assert np.array_equal(got[cnt:], v[cnt:]), f"count {cnt}: past the count"
 
 
 # ---------------------------------------------------------------------------
