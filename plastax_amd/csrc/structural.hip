@@ -460,20 +460,36 @@ __global__ __launch_bounds__(kSortBlock) void k_radix_scatter(int64_t n_max, con
     // the count of smaller digits over all tiles plus the count of digit t
     // in earlier tiles; every workgroup reads the whole table (one launch
     // fewer per pass than scanning it in its own kernel).
+    // Four threads per digit (quarter q takes tiles q, q + 4, ...), each
+    // issuing its loads in batches of 16: one memory round trip for up to
+    // 64 tiles.
     constexpr int kBatch = 16;
+    constexpr int kQuarters = kSortBlock / 256;
+    __shared__ int part_total[kQuarters][256], part_before[kQuarters][256];
+    const int dg = t & 255, q = t >> 8;
     int total = 0, before = 0;
+    for (int64_t j0 = q; j0 < ntiles; j0 += kBatch * kQuarters) {
+      int c[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) c[j] = hist[min(j0 + j * kQuarters, ntiles - 1) * 256 + dg];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int64_t tile = j0 + j * kQuarters;
+        const int v = tile < ntiles ? c[j] : 0;
+        total += v;
+        before += tile < static_cast<int64_t>(blockIdx.x) ? v : 0;
+      }
+    }
+    part_total[q][dg] = total;
+    part_before[q][dg] = before;
+    __syncthreads();
+    total = 0;
+    before = 0;
     if (t < 256) {
-      for (int64_t j0 = 0; j0 < ntiles; j0 += kBatch) {
-        int c[kBatch];
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) c[j] = hist[min(j0 + j, ntiles - 1) * 256 + t];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-          const int64_t tile = j0 + j;
-          const int v = tile < ntiles ? c[j] : 0;
-          total += v;
-          before += tile < static_cast<int64_t>(blockIdx.x) ? v : 0;
-        }
+      for (int i = 0; i < kQuarters; ++i) {
+        total += part_total[i][t];
+        before += part_before[i][t];
       }
     }
     int all;
