@@ -1101,6 +1101,24 @@ PLX_EXPORT int plx_merge_gather(const plx_merge_gather_desc* d, void* stream);
 PLX_EXPORT int plx_remap_i32(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
                              int32_t* out, uint8_t* live, void* stream);
 
+/* plx_remap_i32 for a merge's old-to-new positions, without reading the map
+ * at random when the merge moved few elements: for p = idx[j] - off in
+ * [0, map_len), out[j] = -1 where p is one of the dropped positions, else
+ * s + c + off, with s = p less the dropped positions below it (its rank
+ * among the survivors) and c the inserted elements placed before survivor
+ * s; live[j] = out[j] >= 0; -1 outside [0, map_len). dropped: the dropped
+ * positions (ascending, *ndropped of them, at most map_len); ins: the
+ * inserted elements in merge order (*nins of them, at most ins_len),
+ * new_pos[ins[i]] - off their merged ranks.
+ * With more than PLX_REMAP_LDS_MAX of either, out[j] = map[p] (the map
+ * plx_merge_index wrote). No counterpart in the reference, whose layout is
+ * rebuilt in full. */
+#define PLX_REMAP_LDS_MAX 4096
+PLX_EXPORT int plx_remap_merged(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
+                                const int32_t* dropped, const int32_t* ndropped, const int32_t* ins,
+                                const int32_t* nins, int64_t ins_len, const int32_t* new_pos, int32_t* out,
+                                uint8_t* live, void* stream);
+
 /* counts[ids[p]] += 1 over n positions, skipping p where skip[p] (optional)
  * and ids outside [0, nbins) (integer atomics: the counts are exact). */
 PLX_EXPORT int plx_count_ids(int64_t n, const int32_t* ids, const uint8_t* skip, int32_t nbins, int32_t* counts,

@@ -320,8 +320,14 @@ class ChurnArena(Arena):
         old = prev.lists[b]
         moved = torch.empty(max(old_bound, 1), dtype=torch.int32, device=dev)
         keep = torch.empty(max(old_bound, 1), dtype=torch.uint8, device=dev)
-        _lib.check(lib.plx_remap_i32(old_bound, old.pos.data_ptr(), base, old_bound, old_to_new.data_ptr(),
-                                     moved.data_ptr(), keep.data_ptr(), k.s), "plx_remap_i32")
+        # New positions of the list entries: from the few dropped positions
+        # and inserted slots (old_to_new read at random only past
+        # PLX_REMAP_LDS_MAX of either).
+        dropped, ndropped_d = k.compact(old_bound, 0, prev.cols[DEAD.name][base:], n_dev=old_live_d)  # PLX_FLAG_U8
+        _lib.check(lib.plx_remap_merged(old_bound, old.pos.data_ptr(), base, old_bound, old_to_new.data_ptr(),
+                                        dropped.data_ptr(), ndropped_d.data_ptr(), by_dst.data_ptr(),
+                                        nnew_d.data_ptr(), max(new_bound, 1), new_pos.data_ptr(), moved.data_ptr(),
+                                        keep.data_ptr(), k.s), "plx_remap_merged")
         lsurv, nlsurv_d = k.compact(old_bound, 0, keep, n_dev=old_live_d)  # PLX_FLAG_U8: surviving entries
         lorder = torch.empty(max(bound, 1), dtype=torch.int32, device=dev)
         m2 = _lib.plx_merge_desc()

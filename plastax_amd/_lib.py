@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 26  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 27  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -320,6 +320,7 @@ class plx_merge_desc(ctypes.Structure):
 
 PLX_MERGE_MAX_COLS = 12
 PLX_CLAIMED_SPLIT_MAX = 4096
+PLX_REMAP_LDS_MAX = 4096
 
 
 class plx_merge_col(ctypes.Structure):
@@ -542,6 +543,8 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_merge_gather": (c_i32, [ctypes.POINTER(plx_merge_gather_desc), c_vp]),
     "plx_remap_i32": (c_i32, [c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "plx_claimed_split": (c_i32, [c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),
+    "plx_remap_merged": (c_i32, [c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                 c_vp]),
     "plx_merge_kills": (c_i32, [c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_kill_incident": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
     "plx_unit_place": (c_i32, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,

@@ -443,6 +443,69 @@ __global__ __launch_bounds__(256) void k_remap_i32(int64_t n, const int32_t* idx
   }
 }
 
+// plx_remap_merged: the dropped positions and the inserted elements' ranks
+// among the survivors staged in LDS (both at most PLX_REMAP_LDS_MAX, else
+// the map is read), then two binary searches per entry.
+__global__ __launch_bounds__(256) void k_remap_merged(int64_t n, const int32_t* idx, int64_t off, int64_t map_len,
+                                                     const int32_t* map, const int32_t* dropped,
+                                                     const int32_t* ndropped, const int32_t* ins,
+                                                     const int32_t* nins, int64_t ins_len,
+                                                     const int32_t* new_pos, int32_t* out, uint8_t* live) {
+  __shared__ int32_t sk[PLX_REMAP_LDS_MAX], sr[PLX_REMAP_LDS_MAX];
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 * kMergePer;
+  // (the counts clamped to their lists' lengths)
+  const int nk = static_cast<int>(min(static_cast<int64_t>(max(*ndropped, 0)), map_len));
+  const int ni = static_cast<int>(min(static_cast<int64_t>(max(*nins, 0)), ins_len));
+  const bool staged = nk <= PLX_REMAP_LDS_MAX && ni <= PLX_REMAP_LDS_MAX;  // uniform
+  if (staged) {
+    for (int i = threadIdx.x; i < nk; i += 256) sk[i] = dropped[i];
+    // the number of survivors placed before inserted element i
+    for (int i = threadIdx.x; i < ni; i += 256) sr[i] = static_cast<int32_t>(new_pos[ins[i]] - off - i);
+  }
+  __syncthreads();
+  int64_t p[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t j = first + k * 256 + threadIdx.x;
+    p[k] = j < n ? static_cast<int64_t>(idx[j]) - off : -1;
+  }
+  int32_t m[kMergePer];
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const bool in = p[k] >= 0 && p[k] < map_len;
+    if (!in) {
+      m[k] = -1;
+    } else if (!staged) {
+      m[k] = map[p[k]];
+    } else {
+      const int32_t q = static_cast<int32_t>(p[k]);
+      int lo = 0, hi = nk;  // the dropped positions below q
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sk[mid] < q) lo = mid + 1; else hi = mid;
+      }
+      if (lo < nk && sk[lo] == q) {
+        m[k] = -1;
+      } else {
+        const int32_t sv = q - lo;  // the survivor's rank
+        int a = 0, b = ni;          // the inserted elements with sr <= sv
+        while (a < b) {
+          const int mid = (a + b) >> 1;
+          if (sr[mid] <= sv) a = mid + 1; else b = mid;
+        }
+        m[k] = static_cast<int32_t>(sv + a + off);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMergePer; ++k) {
+    const int64_t j = first + k * 256 + threadIdx.x;
+    if (j >= n) break;
+    out[j] = m[k];
+    live[j] = m[k] >= 0;
+  }
+}
+
 unsigned grid_of(int64_t n, int block) {
   const int64_t g = (n + block - 1) / block;
   return static_cast<unsigned>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -629,6 +692,19 @@ int plx_claimed_split(int64_t cap, const int32_t* n_dev, const int32_t* list, in
   hipLaunchKernelGGL(k_claimed_split, dim3(static_cast<unsigned>(nb)), dim3(kTB), 0, static_cast<hipStream_t>(stream),
                      cap, n_dev, list, offs, region, out, counts);
   return check_launch("plx_claimed_split");
+}
+
+int plx_remap_merged(int64_t n, const int32_t* idx, int64_t off, int64_t map_len, const int32_t* map,
+                     const int32_t* dropped, const int32_t* ndropped, const int32_t* ins, const int32_t* nins,
+                     int64_t ins_len, const int32_t* new_pos, int32_t* out, uint8_t* live, void* stream) {
+  if (n < 0 || map_len < 0 || ins_len < 0) return fail(PLX_ERR_INVALID, "plx_remap_merged: negative size");
+  if (n == 0) return PLX_OK;
+  if (!idx || !map || !dropped || !ndropped || !ins || !nins || !new_pos || !out || !live)
+    return fail(PLX_ERR_INVALID, "plx_remap_merged: null pointer");
+  hipLaunchKernelGGL(k_remap_merged, dim3(static_cast<unsigned>((n + 256 * kMergePer - 1) / (256 * kMergePer))),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), n, idx, off, map_len, map, dropped, ndropped,
+                     ins, nins, ins_len, new_pos, out, live);
+  return check_launch("plx_remap_merged");
 }
 
 }  // extern "C"

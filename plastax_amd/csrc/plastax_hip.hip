@@ -2092,7 +2092,7 @@ extern "C" {
 
 const char* plx_last_error(void) { return plx_detail::g_last_error.c_str(); }
 
-int32_t plx_abi_version(void) { return 26; }
+int32_t plx_abi_version(void) { return 27; }
 
 int plx_struct_sizes(int64_t* out, int32_t n) {
   const int64_t sizes[20] = {

@@ -388,7 +388,10 @@ class StepFn:
             phase_u = self._add_unit
             if phase_u.fires(int(state.step)):
                 before_units = state.units
-                ulog = {name: col.clone() for name, col in before_units.items()}
+                # The phase writes the new units into free slots of these
+                # columns in place (the state was donated to the step, and
+                # the spawned units read only their parents' values).
+                ulog = dict(before_units)
                 flags = phase_u.run_device(k, ulog, g)
                 if self._grow is not None:
                     self._grow.carry_level_bound(before_units["level"], ulog["level"], phase_u.level_bound)

@@ -1,5 +1,5 @@
-"""plx_merge_index / plx_merge_gather / plx_remap_i32 / plx_claimed_split
-through the C ABI against numpy: two sorted id lists merged by (key1, key2)
+"""plx_merge_index / plx_merge_gather / plx_remap_i32 / plx_remap_merged /
+plx_claimed_split through the C ABI against numpy: two sorted id lists merged by (key1, key2)
 (a first on equal keys), the order and both maps; a multi-column gather from the two sides;
 short b (keys staged in LDS) and long b (searched in global memory), empty
 sides, ties across the sides; a claim's slot list split by bucket."""
@@ -223,3 +223,37 @@ def test_claimed_split(caps, nlisted, cap, region) -> None:
     with pytest.raises(_lib.PlxError):
         _lib.call("plx_claimed_split", 4097, nd.data_ptr(), lst.data_ptr(), nb, offs_t.data_ptr(), region,
                   out.data_ptr(), counts.data_ptr(), None)
+
+
+@pytest.mark.parametrize("m,ndrop,nins", [(5000, 40, 32), (20000, 0, 0), (20000, 3000, 4096), (30000, 5000, 10)])
+def test_remap_merged(m: int, ndrop: int, nins: int) -> None:
+    """plx_remap_merged against the old-to-new map of the same merge (numpy):
+    m old positions, `ndrop` of them dropped, `nins` elements inserted at
+    random survivor ranks; list entries at random positions (some outside
+    the map). More than PLX_REMAP_LDS_MAX dropped positions take the map."""
+    rng = np.random.default_rng(m + ndrop + nins)
+    off = 1000
+    dropped = np.sort(rng.choice(m, ndrop, replace=False)).astype(np.int32)
+    surv = np.setdiff1d(np.arange(m), dropped)
+    ranks = np.sort(rng.integers(0, surv.size + 1, nins))  # survivors before each inserted element
+    # merged order: survivor s at s + #(ranks <= s); inserted i at ranks[i] + i
+    old_to_new = np.full(m, -1, np.int32)
+    old_to_new[surv] = np.arange(surv.size) + np.searchsorted(ranks, np.arange(surv.size), side="right") + off
+    ins = rng.permutation(max(nins, 1)).astype(np.int32)[:nins]  # slot ids of the inserted elements
+    new_pos = np.full(max(nins, 1) + 5, -7, np.int32)
+    new_pos[ins] = ranks + np.arange(nins) + off
+    n = 70000
+    idx = (rng.integers(-50, m + 50, n) + off).astype(np.int32)
+    want = np.full(n, -1, np.int32)
+    inside = (idx - off >= 0) & (idx - off < m)
+    want[inside] = old_to_new[idx[inside] - off]
+    out = torch.empty(n, dtype=torch.int32, device=DEV)
+    live = torch.empty(n, dtype=torch.uint8, device=DEV)
+    t_idx, t_map, t_drop = _t(idx), _t(old_to_new), _t(dropped if ndrop else np.zeros(1, np.int32))
+    t_ins, t_new = _t(ins if nins else np.zeros(1, np.int32)), _t(new_pos)
+    nd, ni = _t(np.array([ndrop], np.int32)), _t(np.array([nins], np.int32))
+    _lib.call("plx_remap_merged", n, t_idx.data_ptr(), off, m, t_map.data_ptr(), t_drop.data_ptr(), nd.data_ptr(),
+              t_ins.data_ptr(), ni.data_ptr(), max(nins, 1), t_new.data_ptr(), out.data_ptr(), live.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+    assert np.array_equal(live.cpu().numpy(), (want >= 0).astype(np.uint8))
