@@ -586,6 +586,22 @@ PLX_EXPORT int plx_site_eval(const plx_site_desc* d, void* stream);
 PLX_EXPORT int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* arch, void** handle);
 PLX_EXPORT int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream);
 
+/* The fused forward + PruneConn sweep with the predicate compiled in: the
+ * reference translates the predicate's jaxpr into the fused forward kernel's
+ * source (phases.py:1910-2147, template :2174-2203, launch :2240-2319).
+ * plx_forward_prune_compile generates plx_forward_bucket's kernel for monoid
+ * `monoid` (PLX_MONOID_*) with the program of `d` (an unbatched
+ * PLX_SITES_EDGE program; d's ids_logical / ids_physical set as the forward
+ * descriptor's will be, and its fields' widths) in place of the site
+ * interpreter, compiled and cached as plx_site_compile does.
+ * plx_forward_bucket_compiled runs a bucket on it: the same descriptor,
+ * checks and results as plx_forward_bucket with that prune_prog, which must
+ * hold the compiled program (its fields and constants are read from it; its
+ * instructions are the compiled ones). */
+PLX_EXPORT int plx_forward_prune_compile(const plx_site_desc* d, int32_t monoid, const char* csrc_dir,
+                                         const char* arch, void** handle);
+PLX_EXPORT int plx_forward_bucket_compiled(void* handle, const plx_forward_desc* d, void* stream);
+
 /* One bucket of a generic pass (a map outside the product form, one float32
  * component or a tuple with a tuple of monoids: sweep.py:113-180 / :343-399
  * with any `map` and `combine`): for every row r (one thread each), unit u =

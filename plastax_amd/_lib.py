@@ -18,7 +18,7 @@ LIB_PATH = pathlib.Path(
     or pathlib.Path(__file__).resolve().parent / "libplastax_hip.so"
 )
 
-ABI_VERSION = 27  # plx_abi_version() of the library these mirrors describe
+ABI_VERSION = 28  # plx_abi_version() of the library these mirrors describe
 
 PLX_MAX_INSTR = 48
 PLX_MAX_CONST = 32
@@ -482,6 +482,9 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "plx_site_compile": (c_i32, [ctypes.POINTER(plx_site_desc), ctypes.c_char_p, ctypes.c_char_p,
                                  ctypes.POINTER(c_vp)]),
     "plx_site_eval_compiled": (c_i32, [c_vp, ctypes.POINTER(plx_site_desc), c_vp]),
+    "plx_forward_prune_compile": (c_i32, [ctypes.POINTER(plx_site_desc), c_i32, ctypes.c_char_p, ctypes.c_char_p,
+                                          ctypes.POINTER(c_vp)]),
+    "plx_forward_bucket_compiled": (c_i32, [c_vp, ctypes.POINTER(plx_forward_desc), c_vp]),
     "plx_roof_probe": (c_i32, [c_i32, c_i32, c_vp, c_i64, c_vp, ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(ctypes.c_float), c_vp]),
     "plx_update_conn": (c_i32, [ctypes.POINTER(plx_update_desc), c_vp]),

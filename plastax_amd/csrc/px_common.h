@@ -8,10 +8,15 @@
 
 #include <string>
 
+struct plx_forward_desc;
+
 namespace plx_detail {
 extern thread_local std::string g_last_error;
 int fail(int code, const char* what);
 int check_launch(const char* what);
+// plx_forward_bucket's checks of d and its launch: *grid workgroups (0: no
+// rows, nothing to launch) of *block lanes.
+int forward_launch_shape(const plx_forward_desc* d, const char* who, unsigned* grid, unsigned* block);
 }  // namespace plx_detail
 #endif
 

@@ -1160,6 +1160,7 @@ struct CompiledSite {
   hipModule_t mod = nullptr;
   hipFunction_t fn = nullptr;
   int dev = -1;
+  int32_t monoid = -1;  // < 0: plx_site_eval's kernel; else the forward + prune kernel for this monoid
   int32_t ninstr = 0, nout = 0;
   std::vector<int32_t> code;
   std::vector<int32_t> shape;  // site_shape of the descriptors it runs
@@ -1185,7 +1186,9 @@ std::vector<int32_t> site_shape(const plx_site_desc& d) {
 std::mutex g_site_mu;
 std::map<std::string, CompiledSite*> g_site_cache;
 
-std::string site_source(const plx_site_desc& d) {
+// The generated program after `header`: its launch shape (SiteShape) and
+// instructions (SiteGen), in an anonymous namespace.
+std::string site_gen_source(const plx_site_desc& d, const char* header) {
   const plx_site_prog& p = d.prog;
   const std::vector<int32_t> sh = site_shape(d);
   auto b = [](bool v) { return std::string(v ? "true" : "false"); };
@@ -1202,7 +1205,7 @@ std::string site_source(const plx_site_desc& d) {
       "#ifndef INT32_MIN\n#define INT32_MIN (-2147483647 - 1)\n#endif\n"
       "#ifndef INT32_MAX\n#define INT32_MAX 2147483647\n#endif\n"
       "#ifndef UINT32_MAX\n#define UINT32_MAX 4294967295u\n#endif\n"
-      "#include \"px_site.h\"\n"
+      "#include \"" + std::string(header) + "\"\n"
       "namespace {\n"
       "struct SiteShape {\n"
       "  static constexpr bool kSelects = true;\n"
@@ -1228,13 +1231,25 @@ std::string site_source(const plx_site_desc& d) {
     s += "    site_step<SiteShape>(" + std::to_string(p.code[4 * k]) + ", " + std::to_string(p.code[4 * k + 1]) + ", " +
          std::to_string(p.code[4 * k + 2]) + ", " + std::to_string(p.code[4 * k + 3]) + ", r, p, c, nu, o);\n";
   }
-  s += "  }\n};\n}  // namespace\n"
-       "extern \"C\" __global__ void plx_site_kernel(plx_site_desc d) { site_eval_body<SiteGen>(d); }\n";
+  s += "  }\n};\n}  // namespace\n";
   return s;
 }
 
-int site_rtc_compile(const plx_site_desc& d, const char* csrc_dir, const std::string& arch, std::vector<char>* code) {
-  const std::string src = site_source(d);
+// plx_site_eval's kernel for the program of d.
+std::string site_source(const plx_site_desc& d) {
+  return site_gen_source(d, "px_site.h") +
+         "extern \"C\" __global__ void plx_site_kernel(plx_site_desc d) { site_eval_body<SiteGen>(d); }\n";
+}
+
+// The forward sweep with the PruneConn program of d compiled in
+// (px_forward.h's forward_body), for monoid m.
+std::string forward_prune_source(const plx_site_desc& d, int32_t m) {
+  return site_gen_source(d, "px_forward.h") +
+         "extern \"C\" __global__ __launch_bounds__(kFwdBlock) void plx_fwd_prune_kernel(plx_forward_desc d) {\n"
+         "  forward_body<" + std::to_string(m) + ", true, SiteGen>(d);\n}\n";
+}
+
+int site_rtc_compile(const std::string& src, const char* csrc_dir, const std::string& arch, std::vector<char>* code) {
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, src.c_str(), "plx_site.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
     return fail(PLX_ERR_HIP, "plx_site_compile: hiprtcCreateProgram failed");
@@ -1306,17 +1321,22 @@ int plx_site_eval(const plx_site_desc* d, void* stream) {
 
 
 
-int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* arch, void** handle) {
-  if (!d || !csrc_dir) return fail(PLX_ERR_INVALID, "plx_site_compile: null argument");
+// plx_site_compile and plx_forward_prune_compile: the program of d compiled
+// as plx_site_eval's kernel (monoid < 0) or inside the forward sweep for
+// monoid m, loaded on the current device, once per (device, target, kernel,
+// program code, launch shape) for the process.
+static int compile_kernel(const plx_site_desc* d, int32_t monoid, const char* csrc_dir, const char* arch,
+                          void** handle, const char* who) {
+  const std::string w(who);
+  if (!d || !csrc_dir) return fail(PLX_ERR_INVALID, (w + ": null argument").c_str());
   const plx_site_prog* p = &d->prog;
-  if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE)
-    return fail(PLX_ERR_INVALID, "plx_site_compile: bad site kind");
+  if (d->kind < PLX_SITES_UNIT || d->kind > PLX_SITES_EDGE) return fail(PLX_ERR_INVALID, (w + ": bad site kind").c_str());
   if (p->ninstr < 0 || p->ninstr > PLX_MAX_SINSTR || p->nout < 0 || p->nout > PLX_MAX_SOUTS)
-    return fail(PLX_ERR_INVALID, "plx_site_compile: bad program");
+    return fail(PLX_ERR_INVALID, (w + ": bad program").c_str());
   std::string target = arch ? arch : "";
   int dev = -1;
   if (handle) {
-    if (hipGetDevice(&dev) != hipSuccess) return fail(PLX_ERR_HIP, "plx_site_compile: no current device");
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PLX_ERR_HIP, (w + ": no current device").c_str());
     if (target.empty()) {
       static std::mutex arch_mu;
       static std::map<int, std::string> arch_of;  // (device properties are slow to query)
@@ -1325,15 +1345,15 @@ int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* a
       if (it == arch_of.end()) {
         hipDeviceProp_t prop;
         if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
-          return fail(PLX_ERR_HIP, "plx_site_compile: device properties unavailable");
+          return fail(PLX_ERR_HIP, (w + ": device properties unavailable").c_str());
         it = arch_of.emplace(dev, std::string(prop.gcnArchName)).first;
       }
       target = it->second;
     }
   }
-  if (target.empty()) return fail(PLX_ERR_INVALID, "plx_site_compile: no target architecture");
-  std::string key = std::to_string(dev) + "|" + target + "|" + std::to_string(p->ninstr) + "|" +
-                    std::to_string(p->nout) + "|";
+  if (target.empty()) return fail(PLX_ERR_INVALID, (w + ": no target architecture").c_str());
+  std::string key = std::to_string(dev) + "|" + target + "|" + std::to_string(monoid) + "|" +
+                    std::to_string(p->ninstr) + "|" + std::to_string(p->nout) + "|";
   key.append(reinterpret_cast<const char*>(p->code), sizeof(int32_t) * 4 * static_cast<size_t>(p->ninstr));
   const std::vector<int32_t> shape = site_shape(*d);
   key.append(reinterpret_cast<const char*>(shape.data()), sizeof(int32_t) * shape.size());
@@ -1346,16 +1366,19 @@ int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* a
     }
   }
   std::vector<char> code;
-  const int rc = site_rtc_compile(*d, csrc_dir, target, &code);
+  const int rc = site_rtc_compile(monoid < 0 ? site_source(*d) : forward_prune_source(*d, monoid), csrc_dir, target,
+                                  &code);
   if (rc || !handle) return rc;
   auto* cs = new CompiledSite;
+  const char* name = monoid < 0 ? "plx_site_kernel" : "plx_fwd_prune_kernel";
   if (hipModuleLoadData(&cs->mod, code.data()) != hipSuccess ||
-      hipModuleGetFunction(&cs->fn, cs->mod, "plx_site_kernel") != hipSuccess) {
+      hipModuleGetFunction(&cs->fn, cs->mod, name) != hipSuccess) {
     delete cs;
     (void)hipGetLastError();
-    return fail(PLX_ERR_HIP, "plx_site_compile: loading the compiled program failed");
+    return fail(PLX_ERR_HIP, (w + ": loading the compiled program failed").c_str());
   }
   cs->dev = dev;
+  cs->monoid = monoid;
   cs->ninstr = p->ninstr;
   cs->nout = p->nout;
   cs->code.assign(p->code, p->code + 4 * p->ninstr);
@@ -1365,8 +1388,44 @@ int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* a
   return PLX_OK;
 }
 
+int plx_site_compile(const plx_site_desc* d, const char* csrc_dir, const char* arch, void** handle) {
+  return compile_kernel(d, -1, csrc_dir, arch, handle, "plx_site_compile");
+}
+
+int plx_forward_prune_compile(const plx_site_desc* d, int32_t monoid, const char* csrc_dir, const char* arch,
+                              void** handle) {
+  if (monoid < PLX_MONOID_SUM || monoid > PLX_MONOID_MIN)
+    return fail(PLX_ERR_UNSUPPORTED, "plx_forward_prune_compile: unknown monoid");
+  if (d && (d->kind != PLX_SITES_EDGE || d->batch > 1 || d->prog.nout < 1))
+    return fail(PLX_ERR_INVALID, "plx_forward_prune_compile: the predicate is an unbatched EDGE site program "
+                                 "with an output");
+  return compile_kernel(d, monoid, csrc_dir, arch, handle, "plx_forward_prune_compile");
+}
+
+int plx_forward_bucket_compiled(void* handle, const plx_forward_desc* d, void* stream) {
+  if (!handle || !d) return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: null argument");
+  const auto* cs = static_cast<const CompiledSite*>(handle);
+  if (cs->monoid < 0) return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: not a forward + prune kernel");
+  if (d->monoid != cs->monoid)
+    return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: the descriptor's monoid is not the compiled one");
+  if (!d->prune_prog) return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: prune_prog is required");
+  unsigned grid = 0, block = 0;
+  const int rc = plx_detail::forward_launch_shape(d, "plx_forward_bucket_compiled", &grid, &block);
+  if (rc || grid == 0) return rc;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != cs->dev)
+    return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: the kernel was compiled for another device");
+  void* args[] = {const_cast<plx_forward_desc*>(d)};
+  if (hipModuleLaunchKernel(cs->fn, grid, 1, 1, block, 1, 1, 0, static_cast<hipStream_t>(stream), args, nullptr) !=
+      hipSuccess)
+    return fail(PLX_ERR_HIP, "plx_forward_bucket_compiled: launch failed");
+  return check_launch("plx_forward_bucket_compiled");
+}
+
 int plx_site_eval_compiled(void* handle, const plx_site_desc* d, void* stream) {
   if (!handle || !d) return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: null argument");
+  if (static_cast<const CompiledSite*>(handle)->monoid >= 0)
+    return fail(PLX_ERR_INVALID, "plx_site_eval_compiled: a forward + prune kernel, not a site kernel");
   if (d->n < 0) return fail(PLX_ERR_INVALID, "plx_site_eval: negative n");
   if (d->n == 0) return PLX_OK;
   const int rc = site_desc_check(d);

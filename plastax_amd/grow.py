@@ -140,6 +140,37 @@ def compiled_site_handle(sp: _site.SiteProgram, d: _lib.plx_site_desc, device: t
     return handle.value
 
 
+def compiled_forward_prune_handle(sp: _site.SiteProgram, prog: _lib.plx_site_prog, monoid: int,
+                                  device: torch.device) -> int | None:
+    """The fused forward + PruneConn kernel (plx_forward_prune_compile) of a
+    traced predicate whose filled program is ``prog``, for ``monoid``, with
+    the unit id arrays the fused forward passes; kept on the program per
+    (device, monoid, field widths); None if hipRTC could not build it (the
+    forward then interprets the predicate, with a warning the first time)."""
+    cache = sp.__dict__.setdefault("_compiled_fwd", {})
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    key = (dev, int(monoid), tuple(prog.ubytes), tuple(prog.cbytes))
+    if key in cache:
+        return cache[key]
+    d = _lib.plx_site_desc()
+    d.prog = prog
+    d.kind, d.batch, d.n, d.per = _lib_sites("EDGE"), 1, 1, 1
+    d.ids_logical = d.ids_physical = ctypes.addressof(_ID_SHAPE)  # (only whether they are set)
+    lib = _lib.load()
+    handle = ctypes.c_void_p()
+    rc = lib.plx_forward_prune_compile(ctypes.byref(d), int(monoid), _CSRC, None, ctypes.byref(handle))
+    if rc != 0:
+        warnings.warn(f"fused prune predicate not compiled, interpreted instead: "
+                      f"{lib.plx_last_error().decode()[:500]}")
+        cache[key] = None
+        return None
+    cache[key] = handle.value
+    return handle.value
+
+
+_ID_SHAPE = (ctypes.c_int32 * 1)()
+
+
 class Kernels:
     """Thin wrappers of the structural entry points on one stream."""
 

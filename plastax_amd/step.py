@@ -26,6 +26,12 @@ from plastax_amd._types import ACTIVATION, DEAD, Propagation
 from plastax_amd.fusion import PruneFusionPlan, PruneFusionRecord, plan_prune_fusion
 from plastax_amd.state import NetworkState, NetworkStatic
 
+# The fused forward + PruneConn sweep ("hip" engine): "compiled" runs the
+# predicate compiled into the forward kernel (plx_forward_prune_compile);
+# "interpreted" evaluates it with the site interpreter inside the library's
+# forward kernel (tests). Both give the same bits.
+FUSED_PREDICATE: str = "compiled"
+
 
 @dataclasses.dataclass(frozen=True)
 class StepInputs:
@@ -310,6 +316,7 @@ class StepFn:
                 d.fin.fin_level = -1 if arena.pipeline else b + 1
                 d.fin.skip_inputs = 1
                 d.apply = prog
+                handle = None
                 if fused is not None and fusion.engine == "hip":
                     d.prune_prog = fused[b].data_ptr()
                     d.prune_sink = arena.prune_sink.data_ptr()
@@ -317,7 +324,11 @@ class StepFn:
                     d.ids_logical, d.ids_physical = arena.uperm32.data_ptr(), arena.uinv32.data_ptr()
                     d.prune_base = arena.bases[b]
                     d.num_units = n_units
-                self._launch("forward", lib.plx_forward_bucket, d, stream)
+                    handle = self._fused_handle
+                if handle is not None:
+                    self._launch("forward", lib.plx_forward_bucket_compiled, handle, d, stream)
+                else:
+                    self._launch("forward", lib.plx_forward_bucket, d, stream)
             self._unshadow(units, swaps)
             if fused is not None and fusion.engine == "xla":
                 self._xla_prune(arena, g, stream)
@@ -544,14 +555,27 @@ class StepFn:
         if names:
             pred_units.update(self._forwarded(arena, units, fin_common, names, g, stream))
         self._pred_units = pred_units
-        progs = []
+        raws = []
+        self._fused_handle = None
         for b in range(arena.num_buckets):
             base, cap = arena.bases[b], arena.caps[b]
             view = {name: col[base : base + cap] for name, col in arena.cols.items()}
             p = grow.fill_prog(self._prune.prog, pred_units, view, g, physical_ids=True)
-            raw = bytes(memoryview(p).cast("B"))
-            progs.append(torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(arena.device, non_blocking=False))
-        return progs
+            if b == 0 and FUSED_PREDICATE == "compiled":
+                # (every bucket's program has the same code and field widths)
+                self._fused_handle = grow.compiled_forward_prune_handle(self._prune.prog, p,
+                                                                        self.plan.forward.monoid, arena.device)
+            raws.append(bytes(memoryview(p).cast("B")))
+        # One upload for every bucket's program, from pinned memory and
+        # asynchronous on the step's stream (the programs hold this step's
+        # globals, so they change every step; a synchronous copy would make
+        # the host wait for the previous step's kernels).
+        size = -(-len(raws[0]) // 256) * 256
+        host = torch.zeros(size * len(raws), dtype=torch.uint8, pin_memory=True)
+        for b, raw in enumerate(raws):
+            host[b * size : b * size + len(raw)] = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+        dev_all = host.to(arena.device, non_blocking=True)  # (the current stream is the step's)
+        return [dev_all[b * size : (b + 1) * size] for b in range(len(raws))]
 
     def _forwarded(self, arena: Arena, units: dict, fin_common: dict, names: tuple[str, ...], g: Any,
                    stream: int) -> dict[str, torch.Tensor]:

@@ -4,8 +4,9 @@ to the two-pass step, and to the oracle, over churn steps.
 Each net runs four ways from the same state: ``fuse_prune="off"`` (the
 predicate pass at the prune slot), ``"triton"`` (the predicate evaluated
 inside plx_forward_bucket's sweep, tombstones committed at the prune slot),
-``"xla"`` (the predicate pass at the forward's slot) and ``"auto"`` (which
-does not fuse: the prune slot's pass is the fastest here). Every unit column, every
+``"xla"`` (the predicate pass at the forward's slot) and ``"auto"``; the
+"triton" run takes the predicate compiled into the forward kernel and is
+repeated with the predicate interpreted there. Every unit column, every
 logical connection column, the loss and the structural flags must agree bit
 for bit at every step, and the fused run must match the oracle (whose prune
 runs at its own slot). Cases, after the reference's tests/test_prune_fusion.py:
@@ -85,7 +86,7 @@ def _host(static, state):
     "case",
     ["hash+train+grow", "hash+pipeline+propose", "weight, no update", "marked (forwarded)"],
 )
-def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
+def test_fused_step_matches_two_pass_and_oracle(oracle, case: str, monkeypatch) -> None:
     pipeline = case == "hash+pipeline+propose"
     if case == "hash+train+grow":
         net = _net(HashPrune(), grow=GradGrow())
@@ -102,9 +103,13 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
     ts = np.tanh(rng.standard_normal((8, n_out))).astype(np.float32)
     o = nets.oracle_for(oracle, net, static, state0)
     o.tail_start, o.needs_resort = int(state0.tail_start), bool(state0.needs_resort)
-    for mode in ("off", "triton", "xla", "auto"):
+    from plastax_amd import step as step_mod
+
+    for mode in ("off", "triton", "triton/interpreted", "xla", "auto"):
         state = _clone(state0)
-        step = px.make_step(net, static, fuse_prune=mode)
+        engine = mode.split("/")[0]
+        monkeypatch.setattr(step_mod, "FUSED_PREDICATE", "interpreted" if mode.endswith("interpreted") else "compiled")
+        step = px.make_step(net, static, fuse_prune=engine)
         if step.backward_order == "slot":
             o.tile = None
         trace = []
@@ -123,12 +128,17 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str) -> None:
                 assert_same_state(static, state, o, f"{case} step {k}")
                 assert _equal(np.float32([float(res.loss)]), np.float32([lo])), f"loss at {k}"
         plan = step.prune_fusion.plan
-        if mode in ("off", "auto"):
+        if engine == "off":
             assert plan is not None and not plan.fused
+        elif engine == "auto":
+            assert plan is not None and plan.fused == (plan.engine == "hip"), plan
         else:
-            assert plan.fused and plan.engine == ("hip" if mode == "triton" else "xla"), plan
+            assert plan.fused and plan.engine == ("hip" if engine == "triton" else "xla"), plan
+        if plan.fused and plan.engine == "hip":
+            # the predicate compiled into the forward kernel, or interpreted there
+            assert (step._fused_handle is not None) == (mode != "triton/interpreted"), mode
         runs[mode] = (trace, _host(static, state))
-    for mode in ("triton", "xla", "auto"):
+    for mode in ("triton", "triton/interpreted", "xla", "auto"):
         assert runs[mode][0] == runs["off"][0], mode
         (ua, ca), (ub, cb) = runs[mode][1], runs["off"][1]
         for name in ua:

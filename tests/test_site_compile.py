@@ -125,3 +125,26 @@ def test_compile_rejects_a_bad_program() -> None:
     assert lib.plx_site_compile(ctypes.byref(_desc(p, kind=9)), CSRC, b"gfx950", None) != 0
     with pytest.raises(Exception):
         _lib.check(lib.plx_site_compile(None, CSRC, b"gfx950", None), "plx_site_compile")
+
+
+def test_forward_prune_compiles() -> None:
+    """The fused forward + PruneConn kernel (plx_forward_prune_compile) for a
+    traced hash predicate, under every monoid, with the id arrays the fused
+    forward passes; a batched or non-EDGE program and an unknown monoid are
+    refused."""
+
+    class HashPrune(px.PruneConn):
+        def predicate(self, u, c, cid, g):
+            h = c[px.FROM_ID, cid] * jnp.int32(7) + c[px.TO_ID, cid] * jnp.int32(13) + g["step"]
+            return (h % jnp.int32(1048573)) == jnp.int32(0)
+
+    udt = {"activation": np.dtype(np.float32), "level": np.dtype(np.int32)}
+    cdt = {"from_id": np.dtype(np.int32), "to_id": np.dtype(np.int32), "weight": np.dtype(np.float32)}
+    p = _traced(_site.trace_predicate(HashPrune(), udt, cdt, {"step": np.int32(0)}))
+    lib = _lib.load()
+    for m in (0, 1, 2, 3):  # PLX_MONOID_SUM, _PROD, _MAX, _MIN
+        rc = lib.plx_forward_prune_compile(ctypes.byref(_desc(p, ids=True)), m, CSRC, b"gfx950", None)
+        assert rc == 0, lib.plx_last_error().decode()[:3000]
+    assert lib.plx_forward_prune_compile(ctypes.byref(_desc(p, ids=True)), 9, CSRC, b"gfx950", None) != 0
+    assert lib.plx_forward_prune_compile(ctypes.byref(_desc(p, kind=0)), 0, CSRC, b"gfx950", None) != 0
+    assert lib.plx_forward_prune_compile(ctypes.byref(_desc(p, batch=4)), 0, CSRC, b"gfx950", None) != 0
