@@ -1409,6 +1409,10 @@ int plx_forward_bucket_compiled(void* handle, const plx_forward_desc* d, void* s
   if (d->monoid != cs->monoid)
     return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: the descriptor's monoid is not the compiled one");
   if (!d->prune_prog) return fail(PLX_ERR_INVALID, "plx_forward_bucket_compiled: prune_prog is required");
+  // (the kernel reads the id arrays the compiled shape names, unconditionally)
+  if ((d->ids_logical != nullptr) != (cs->shape[5] != 0) || (d->ids_physical != nullptr) != (cs->shape[6] != 0))
+    return fail(PLX_ERR_INVALID,
+                "plx_forward_bucket_compiled: ids_logical / ids_physical are not set as in the compiled shape");
   unsigned grid = 0, block = 0;
   const int rc = plx_detail::forward_launch_shape(d, "plx_forward_bucket_compiled", &grid, &block);
   if (rc || grid == 0) return rc;

@@ -150,3 +150,34 @@ def test_fused_step_matches_two_pass_and_oracle(oracle, case: str, monkeypatch) 
     dead = np.concatenate([c["dead"] for c in runs["triton"][1][1]])
     dead0 = np.concatenate([np.asarray(c["dead"].cpu()) for c in state0.conns])
     assert int(dead.sum()) > int(dead0.sum()), "nothing was pruned"
+
+
+def test_compiled_forward_refuses_a_mismatched_descriptor() -> None:
+    """plx_forward_bucket_compiled checks the descriptor against what the
+    kernel was compiled for (monoid, the id arrays its shape reads) and
+    launches nothing when they differ."""
+    import ctypes
+
+    from plastax_amd import _lib, _site, grow
+
+    udt = {"activation": np.dtype(np.float32), "level": np.dtype(np.int32)}
+    cdt = {"from_id": np.dtype(np.int32), "to_id": np.dtype(np.int32), "weight": np.dtype(np.float32)}
+    sp = _site.trace_predicate(HashPrune(), udt, cdt, {"step": np.int32(0)})
+    prog = _lib.plx_site_prog()
+    code = sp.flat_code().reshape(-1, 4)
+    prog.ninstr, prog.nout = len(code), len(sp.out_kinds)
+    for k, row in enumerate(code):
+        for j in range(4):
+            prog.code[4 * k + j] = int(row[j])
+    dev = torch.device("cuda", 0)
+    handle = grow.compiled_forward_prune_handle(sp, prog, 0, dev)
+    assert handle is not None
+    lib = _lib.load()
+    d = _lib.plx_forward_desc()
+    d.nrows, d.monoid = 1, 0
+    d.prune_prog = 16  # (never dereferenced: every check below fails first)
+    assert lib.plx_forward_bucket_compiled(ctypes.c_void_p(handle), ctypes.byref(d), None) != 0  # no id arrays
+    assert "compiled shape" in lib.plx_last_error().decode()
+    d.monoid = 2
+    assert lib.plx_forward_bucket_compiled(ctypes.c_void_p(handle), ctypes.byref(d), None) != 0
+    assert "monoid" in lib.plx_last_error().decode()
