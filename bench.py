@@ -27,6 +27,10 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# C2: the default timed steps, and the pool of synthetic samples the steps
+# cycle through (step k streams sample k % pool)
+C2_DEFAULT_STEPS = 6000
+C2_INPUT_POOL = 1000
 
 
 def progress(msg: str) -> None:
@@ -1216,7 +1220,9 @@ def main() -> int:
                     "c2: the streaming step (the headline metric); c3: the batched step (B = 256); "
                     "c5: the growing reservoir end to end; c5_growth: its add_conn phase alone")
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None,
+                    help=f"timed steps (default: {C2_DEFAULT_STEPS} for c2, about five seconds of GPU work; "
+                    "200 for the other workloads)")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--scale", type=int, default=1, help="shrink C2's layer width (tests only)")
     ap.add_argument("--seed", type=int, default=0)
@@ -1230,6 +1236,8 @@ def main() -> int:
                     help="only run a plain elementwise copy of MIB MiB (read MIB, write MIB) "
                     "five times: the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = C2_DEFAULT_STEPS if args.workload == "c2" else 200
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures the step on one "
@@ -1290,7 +1298,10 @@ def main() -> int:
     sign, perm = synth.c2_target(args.seed, width)
     nsteps = args.warmup + args.steps
     rng = np.random.default_rng(args.seed + 2)
-    xs = rng.standard_normal((nsteps, width)).astype(np.float32)
+    # Step k streams sample k % pool of a pool of synthetic samples (a long
+    # run needs no more host or device memory for its inputs).
+    pool = min(nsteps, C2_INPUT_POOL)
+    xs = rng.standard_normal((pool, width)).astype(np.float32)
     # (dense rows: numpy's fancy indexing returns a column-major array)
     ts = np.ascontiguousarray((sign[None, :] * xs[:, perm]).astype(np.float32))
     xs_d = torch.from_numpy(xs).to(dev)
@@ -1304,7 +1315,7 @@ def main() -> int:
     # device, for the full-size parity check against the CPU oracle's steps.
     dev_losses = []
     for k in range(args.warmup):
-        res = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+        res = step(gstate, px.StepInputs(xs_d[k % pool], ts_d[k % pool]))
         gstate = res.state
         if k <= args.cpu_steps:
             dev_losses.append(res.loss)
@@ -1325,7 +1336,7 @@ def main() -> int:
     t0 = time.perf_counter()
     last = None
     for k in range(args.warmup, nsteps):
-        last = step(gstate, px.StepInputs(xs_d[k], ts_d[k]))
+        last = step(gstate, px.StepInputs(xs_d[k % pool], ts_d[k % pool]))
         gstate = last.state
         if k <= args.cpu_steps:
             dev_losses.append(last.loss)
@@ -1431,6 +1442,7 @@ def main() -> int:
             "layers": 8,
             "optimizer": "adam(1e-3)",
             "scale": args.scale,
+            "input_pool": pool,
         },
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "step_algorithmic_gbs": round(step_gbs, 1),
