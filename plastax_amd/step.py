@@ -570,6 +570,8 @@ class StepFn:
         # asynchronous on the step's stream (the programs hold this step's
         # globals, so they change every step; a synchronous copy would make
         # the host wait for the previous step's kernels).
+        if not raws:
+            return []
         size = -(-len(raws[0]) // 256) * 256
         host = torch.zeros(size * len(raws), dtype=torch.uint8, pin_memory=True)
         for b, raw in enumerate(raws):
