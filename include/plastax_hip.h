@@ -11,7 +11,8 @@
  * (thread-local). No C++ exception crosses this boundary.
  *
  * Callers: plastax_amd/_lib.py (ctypes over torch-allocated device memory);
- * INTEGRATION.md shows the jax.ffi / XLA custom-call binding.
+ * a jax.ffi / XLA custom-call handler would pass its buffers' device pointers
+ * and its stream to the same entry points.
  */
 #ifndef PLASTAX_HIP_H_
 #define PLASTAX_HIP_H_
